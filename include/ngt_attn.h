@@ -1,0 +1,218 @@
+/*
+ * ngt_attn.h -- C ABI of libngt_attn.so, the MI355X (gfx950) kernels behind
+ * NeutronGT's window attention core.
+ *
+ * Every entry point takes device pointers, sizes and a hipStream_t (passed as
+ * void*), launches asynchronously on that stream, never synchronises and never
+ * allocates: scratch memory comes from the caller through a workspace pointer
+ * whose size is given by the matching *_workspace_bytes() query.
+ * Return value: NGT_OK (0) or an NGT_ERR_* code; ngt_last_error() returns the
+ * message of the last failure on the calling thread.
+ *
+ * Tensor layouts (row-major, contiguous, 16-byte aligned base pointers):
+ *   q   [n_q, H, d]    queries            (reference: q.view(-1, H, d))
+ *   k,v [n_k, H, d]    keys / values
+ *   out [n_q, H, d]    attention output   (reference returns x.view(1, N, H*d))
+ * Element type is selected by `dtype` (NGT_F32 or NGT_BF16); all arithmetic is
+ * fp32.
+ */
+#ifndef NGT_ATTN_H
+#define NGT_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NGT_ABI_VERSION 1
+
+#define NGT_F32 0
+#define NGT_BF16 1
+
+#define NGT_OK 0
+#define NGT_ERR_ARG 1         /* bad argument (shape, null pointer, range) */
+#define NGT_ERR_UNSUPPORTED 2 /* shape the library has no kernel for */
+#define NGT_ERR_HIP 3         /* HIP runtime error */
+#define NGT_ERR_WORKSPACE 4   /* workspace smaller than the query said */
+
+/* Indices into ngt_window_csr.info (device int32[NGT_INFO_LEN]). */
+#define NGT_INFO_ITEMS_Q 0   /* work items, query-major */
+#define NGT_INFO_PARTS_Q 1   /* partial slots, query-major */
+#define NGT_INFO_SPLITS_Q 2  /* rows split over several items, query-major */
+#define NGT_INFO_ITEMS_K 3
+#define NGT_INFO_PARTS_K 4
+#define NGT_INFO_SPLITS_K 5
+#define NGT_INFO_DST_END 6   /* max(dst) + 1, or 0 without edges */
+#define NGT_INFO_SRC_END 7   /* max(src) + 1, or 0 without edges */
+#define NGT_INFO_BAD_EDGES 8 /* edges whose src/dst fell outside [0,n_k)/[0,n_q) */
+#define NGT_INFO_MAX_DEG_Q 9
+#define NGT_INFO_MAX_DEG_K 10
+#define NGT_INFO_LEN 16
+
+/*
+ * Window adjacency in both orientations plus the degree-binned work lists the
+ * kernels are scheduled from.  All pointers are device memory owned by the
+ * caller; sizes are fixed by ngt_csr_sizes().
+ *
+ * Query-major ("CSR"): row i lists the edges e = (j -> i) with dst == i, sorted
+ *   by (dst, src, edge id) -- duplicates kept, stable.  col = src, perm = edge id.
+ * Key-major ("transposed CSR"): row j lists the edges with src == j, sorted by
+ *   (src, dst, edge id).  t_col = dst, t_perm = edge id.
+ * q2t[p] = key-major position of the query-major edge at position p.
+ * Work items are int32x4 {row, edge_begin, edge_end, part}: part = -1 means the
+ *   item covers the whole row; part >= 0 is the partial slot of one chunk of a
+ *   row longer than chunk_{q,k} edges.  Chunks of split rows come first.
+ * Splits are int32x4 {row, part_begin, n_parts, 0}.
+ */
+typedef struct ngt_window_csr {
+  int32_t n_q;
+  int32_t n_k;
+  int64_t n_edges;
+  int32_t chunk_q;
+  int32_t chunk_k;
+  int32_t* rowptr;   /* [n_q + 1] */
+  int32_t* col;      /* [E] */
+  int32_t* perm;     /* [E] */
+  int32_t* t_rowptr; /* [n_k + 1] */
+  int32_t* t_col;    /* [E] */
+  int32_t* t_perm;   /* [E] */
+  int32_t* q2t;      /* [E] */
+  int32_t* items_q;  /* [max_items_q * 4] */
+  int32_t* splits_q; /* [max_splits_q * 4] */
+  int32_t* items_k;  /* [max_items_k * 4] */
+  int32_t* splits_k; /* [max_splits_k * 4] */
+  int32_t* info;     /* [NGT_INFO_LEN] */
+  int32_t max_items_q;
+  int32_t max_splits_q;
+  int32_t max_items_k;
+  int32_t max_splits_k;
+  /* Host copies of info[] that the launch functions size their grids and
+   * partial buffers from; the caller fills them after ngt_csr_build (one
+   * device-to-host copy of info). */
+  int32_t n_items_q;
+  int32_t n_parts_q;
+  int32_t n_splits_q;
+  int32_t n_items_k;
+  int32_t n_parts_k;
+  int32_t n_splits_k;
+} ngt_window_csr;
+
+int ngt_abi_version(void);
+const char* ngt_last_error(void);
+
+/* Sizes of the ngt_window_csr arrays for a window (host-only arithmetic). */
+int ngt_csr_sizes(int64_t n_edges, int32_t n_q, int32_t n_k, int32_t chunk_q, int32_t chunk_k,
+                  int32_t* max_items_q, int32_t* max_splits_q, int32_t* max_items_k,
+                  int32_t* max_splits_k);
+
+/* Scratch bytes ngt_csr_build needs (queries the device's sort configuration). */
+int ngt_csr_workspace_bytes(int64_t n_edges, int32_t n_q, int32_t n_k, size_t* bytes);
+
+/*
+ * Builds both orientations of the window adjacency from a COO edge_index.
+ * Replaces the COO consumption in
+ *   NeutronGT/models/graphormer_dist_node_level.py:75-97 (gathers by
+ *   edge_index[0]/[1] and torch_scatter by edge_index[1]), with the edge list
+ *   produced by NeutronGT/core/node_level_pipeline/window_state.py:122-140.
+ * edge_index: int64 [2, n_edges] (row 0 = src/key, row 1 = dst/query).
+ * Out-of-range edges are counted in info[NGT_INFO_BAD_EDGES] and dropped; the
+ * caller must check that counter and reject the window (the reference raises a
+ * device-side index error).
+ */
+int ngt_csr_build(const int64_t* edge_index, ngt_window_csr* csr, void* workspace,
+                  size_t workspace_bytes, void* stream);
+
+/*
+ * Sparse (topology-masked) attention forward.
+ * Replaces CoreAttention.sparse_attention_bias, forward half:
+ *   NeutronGT/models/graphormer_dist_node_level.py:67-98
+ *   NeutronGT/models/gt_dist_node_level_single_window.py:112-179
+ * For edge e = (j -> i) and head h:
+ *   a = sum_c k[j,h,c] q[i,h,c] / scale;  p = exp(clamp(a, lo, hi))
+ *   out[i,h,:] = sum_e p v[j,h,:] / (sum_e p + eps)
+ * rinv[i,h] = 1 / (sum_e p + eps) (fp32, saved for the backward).
+ * node_score[i] = mean_h sum_e p for i < node_score_len (may be NULL).
+ * Requires n_heads <= 64; head_dim <= 64.
+ */
+int ngt_sparse_workspace_bytes(const ngt_window_csr* csr, int32_t n_heads, int32_t head_dim,
+                               size_t* fwd_bytes, size_t* bwd_bytes);
+int ngt_sparse_fwd(int dtype, const void* q, const void* k, const void* v,
+                   const ngt_window_csr* csr, int32_t n_heads, int32_t head_dim, float scale,
+                   float clamp_lo, float clamp_hi, float eps, void* out, float* rinv,
+                   float* node_score, int32_t node_score_len, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+/*
+ * Sparse attention backward (what autograd derives from the same lines).
+ * With G = grad_out, r = rinv, D_i = sum_c G[i,h,c] out[i,h,c]:
+ *   dp_e = r_i (G_i . v_j - D_i);  da_e = dp_e p_e [lo <= a_e <= hi]
+ *   grad_q[i] = sum_e da_e k_j / scale      (query-major pass)
+ *   grad_k[j] = sum_e da_e q_i / scale      (key-major pass, no atomics)
+ *   grad_v[j] = sum_e p_e r_i G_i           (key-major pass, no atomics)
+ */
+int ngt_sparse_bwd(int dtype, const void* q, const void* k, const void* v, const void* out,
+                   const void* grad_out, const float* rinv, const ngt_window_csr* csr,
+                   int32_t n_heads, int32_t head_dim, float scale, float clamp_lo, float clamp_hi,
+                   void* grad_q, void* grad_k, void* grad_v, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+/*
+ * Dense full-window attention (all pairs, no mask/bias, dropout p = 0).
+ * Replaces CoreAttention.full_attention:
+ *   NeutronGT/models/graphormer_dist_node_level.py:42-65
+ *   NeutronGT/models/gt_dist_node_level_single_window.py:56-109
+ *   S = (q * scale) k^T per head (the reference multiplies by sqrt(d));
+ *   out = softmax(S) v;  lse[h,i] = logsumexp_j S[h,i,j] (fp32, for backward);
+ *   node_score[j] = sum_i mean_h |S[h,i,j]| (may be NULL).
+ */
+int ngt_dense_workspace_bytes(int32_t n_q, int32_t n_k, int32_t n_heads, int32_t head_dim,
+                              size_t* fwd_bytes, size_t* bwd_bytes);
+int ngt_dense_fwd(int dtype, const void* q, const void* k, const void* v, int32_t n_q,
+                  int32_t n_k, int32_t n_heads, int32_t head_dim, float scale, void* out,
+                  float* lse, float* node_score, void* workspace, size_t workspace_bytes,
+                  void* stream);
+int ngt_dense_bwd(int dtype, const void* q, const void* k, const void* v, const void* out,
+                  const void* grad_out, const float* lse, int32_t n_q, int32_t n_k,
+                  int32_t n_heads, int32_t head_dim, float scale, void* grad_q, void* grad_k,
+                  void* grad_v, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Related-node selection for one window.
+ * Replaces weightMetis_keepParent._merge_related_nodes,
+ *   NeutronGT/core/metisPartition.py:397-425.
+ * xadj/adjncy/eweights: int32 symmetric weighted CSR of the global graph
+ *   (as built by NeutronGT/core/ppr_preprocess.py:30-71).
+ * partition: int64 [n_part] global node ids (distinct).
+ * For every neighbour nb outside the partition, w[nb] = sum of the weights of
+ * the edges (u, nb) with u in the partition; ranking is by w descending, ties
+ * by first appearance in (partition order, adjacency order); the top
+ * len(w) * topk_percent // 100 are kept.  out (int64, capacity n_nodes) gets
+ * sorted(partition U selected); out_len (device int32[3]) gets
+ * {output length, number of external neighbours, number of invalid entries
+ * (node ids out of range, negative weights, weight sums >= 2^33)}; the caller
+ * must reject the result when the third is non-zero.
+ */
+int ngt_related_workspace_bytes(int32_t n_nodes, int32_t n_part, size_t* bytes);
+int ngt_merge_related_nodes(const int32_t* xadj, const int32_t* adjncy, const int32_t* eweights,
+                            int32_t n_nodes, const int64_t* partition, int32_t n_part,
+                            int32_t topk_percent, int64_t* out, int32_t* out_len,
+                            void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Row gather dst[r, :] = src[idx[r], :] for r < n_rows (row_bytes a multiple
+ * of 4).  Assembles a window's feature block from the feature table and the
+ * duplicate-node cache, as in
+ *   NeutronGT/core/node_level_pipeline/train_eval.py:234-242.
+ * Indices outside [0, n_src) are counted in *bad (device int32) and their row
+ * is zero-filled.
+ */
+int ngt_gather_rows(const void* src, int64_t n_src, const int64_t* idx, int64_t n_rows,
+                    int64_t row_bytes, void* dst, int32_t* bad, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NGT_ATTN_H */

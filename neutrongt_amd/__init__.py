@@ -1,0 +1,26 @@
+"""neutrongt_amd -- MI355X (gfx950) window attention for NeutronGT.
+
+Public API
+----------
+CoreAttention            drop-in for NeutronGT's CoreAttention (sparse + full)
+install(model)           swap a model's local_attn modules for CoreAttention
+sparse_attention(...)    functional masked attention over a window edge_index
+dense_attention(...)     functional full-window attention
+WindowAdjacency          device CSR/transposed CSR/work lists of one window
+"""
+from .attention import (CoreAttention, DenseAttentionFunction, SparseAttentionFunction,
+                        dense_attention, install, sparse_attention)
+from .csr import AdjacencyCache, WindowAdjacency, chunk_for_heads, default_cache
+
+__all__ = [
+    "CoreAttention",
+    "install",
+    "sparse_attention",
+    "dense_attention",
+    "SparseAttentionFunction",
+    "DenseAttentionFunction",
+    "WindowAdjacency",
+    "AdjacencyCache",
+    "chunk_for_heads",
+    "default_cache",
+]

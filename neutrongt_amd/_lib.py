@@ -1,0 +1,134 @@
+"""ctypes binding of libngt_attn.so (declared in include/ngt_attn.h).
+
+The library is loaded lazily on first use; a missing or stale build raises
+``RuntimeError`` -- there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libngt_attn.so"
+ABI_VERSION = 1
+
+NGT_F32 = 0
+NGT_BF16 = 1
+
+INFO_ITEMS_Q = 0
+INFO_PARTS_Q = 1
+INFO_SPLITS_Q = 2
+INFO_ITEMS_K = 3
+INFO_PARTS_K = 4
+INFO_SPLITS_K = 5
+INFO_DST_END = 6
+INFO_SRC_END = 7
+INFO_BAD_EDGES = 8
+INFO_MAX_DEG_Q = 9
+INFO_MAX_DEG_K = 10
+INFO_LEN = 16
+
+
+class WindowCSR(C.Structure):
+    """Mirror of ``ngt_window_csr``."""
+
+    _fields_ = [
+        ("n_q", C.c_int32),
+        ("n_k", C.c_int32),
+        ("n_edges", C.c_int64),
+        ("chunk_q", C.c_int32),
+        ("chunk_k", C.c_int32),
+        ("rowptr", C.c_void_p),
+        ("col", C.c_void_p),
+        ("perm", C.c_void_p),
+        ("t_rowptr", C.c_void_p),
+        ("t_col", C.c_void_p),
+        ("t_perm", C.c_void_p),
+        ("q2t", C.c_void_p),
+        ("items_q", C.c_void_p),
+        ("splits_q", C.c_void_p),
+        ("items_k", C.c_void_p),
+        ("splits_k", C.c_void_p),
+        ("info", C.c_void_p),
+        ("max_items_q", C.c_int32),
+        ("max_splits_q", C.c_int32),
+        ("max_items_k", C.c_int32),
+        ("max_splits_k", C.c_int32),
+        ("n_items_q", C.c_int32),
+        ("n_parts_q", C.c_int32),
+        ("n_splits_q", C.c_int32),
+        ("n_items_k", C.c_int32),
+        ("n_parts_k", C.c_int32),
+        ("n_splits_k", C.c_int32),
+    ]
+
+
+_i32, _i64, _f32, _vp, _sz = C.c_int32, C.c_int64, C.c_float, C.c_void_p, C.c_size_t
+_pi32 = C.POINTER(C.c_int32)
+_psz = C.POINTER(C.c_size_t)
+_pcsr = C.POINTER(WindowCSR)
+
+# name -> argtypes (restype is int unless listed in _RESTYPES)
+SIGNATURES = {
+    "ngt_abi_version": [],
+    "ngt_last_error": [],
+    "ngt_csr_sizes": [_i64, _i32, _i32, _i32, _i32, _pi32, _pi32, _pi32, _pi32],
+    "ngt_csr_workspace_bytes": [_i64, _i32, _i32, _psz],
+    "ngt_csr_build": [_vp, _pcsr, _vp, _sz, _vp],
+    "ngt_sparse_workspace_bytes": [_pcsr, _i32, _i32, _psz, _psz],
+    "ngt_sparse_fwd": [_i32, _vp, _vp, _vp, _pcsr, _i32, _i32, _f32, _f32, _f32, _f32, _vp, _vp,
+                       _vp, _i32, _vp, _sz, _vp],
+    "ngt_sparse_bwd": [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _pcsr, _i32, _i32, _f32, _f32, _f32,
+                       _vp, _vp, _vp, _vp, _sz, _vp],
+    "ngt_dense_workspace_bytes": [_i32, _i32, _i32, _i32, _psz, _psz],
+    "ngt_dense_fwd": [_i32, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _vp, _vp, _vp, _vp, _sz,
+                      _vp],
+    "ngt_dense_bwd": [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _vp, _vp,
+                      _vp, _vp, _sz, _vp],
+    "ngt_related_workspace_bytes": [_i32, _i32, _psz],
+    "ngt_merge_related_nodes": [_vp, _vp, _vp, _i32, _vp, _i32, _i32, _vp, _vp, _vp, _sz, _vp],
+    "ngt_gather_rows": [_vp, _i64, _vp, _i64, _i64, _vp, _vp, _vp],
+}
+_RESTYPES = {"ngt_last_error": C.c_char_p}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class NGTError(RuntimeError):
+    pass
+
+
+def load(path: str | os.PathLike | None = None):
+    """Returns the loaded library (loads it on first call)."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        p = Path(path) if path else LIB_PATH
+        if not p.exists():
+            raise RuntimeError(
+                f"{p.name} is not built ({p}); run `python -m neutrongt_amd.build` "
+                "(hipcc, gfx950). There is no CPU fallback.")
+        lib = C.CDLL(str(p))
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = argtypes
+            fn.restype = _RESTYPES.get(name, C.c_int)
+        ver = lib.ngt_abi_version()
+        if ver != ABI_VERSION:
+            raise RuntimeError(f"{p.name} ABI version {ver} != expected {ABI_VERSION}; rebuild it")
+        _lib = lib
+        return lib
+
+
+def check(rc: int) -> None:
+    """Raises NGTError with the library's message when rc != 0."""
+    if rc != 0:
+        msg = load().ngt_last_error()
+        raise NGTError((msg or b"").decode(errors="replace") or f"ngt error {rc}")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(load(), name)(*args))

@@ -1,0 +1,262 @@
+"""Drop-in replacement of NeutronGT's attention core backed by HIP kernels.
+
+``CoreAttention`` keeps the reference class's constructor, attributes and
+methods (NeutronGT/models/graphormer_dist_node_level.py:33-127; twin
+NeutronGT/models/gt_dist_node_level_single_window.py:30-227) so it can be
+installed as ``MultiHeadAttention.local_attn`` (graphormer_dist_node_level.py:138,
+call at :170; gt_dist_node_level_single_window.py:243-244, call at :292) or as
+``DistributedAttentionNodeLevel.local_attn`` (NeutronGT/gt_sp/gt_layer.py:276-286).
+
+Every compute call goes through libngt_attn.so; there is no PyTorch/CPU
+fallback (CPU tensors raise).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+
+import torch
+import torch.nn as nn
+
+from . import _lib
+from .csr import AdjacencyCache, chunk_for_heads, default_cache
+
+CLAMP_LO = -5.0
+CLAMP_HI = 5.0
+EPS = 1e-6
+
+_DTYPES = {torch.float32: _lib.NGT_F32, torch.bfloat16: _lib.NGT_BF16}
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    code = _DTYPES.get(t.dtype)
+    if code is None:
+        raise TypeError(f"unsupported dtype {t.dtype} (float32 or bfloat16)")
+    return code
+
+
+def _prep(t: torch.Tensor, name: str) -> torch.Tensor:
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor (the attention core has no CPU path)")
+    if not t.is_contiguous() or t.data_ptr() % 16:
+        t = t.contiguous() if not t.is_contiguous() else t.clone()
+    return t
+
+
+def _stream(dev) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _workspace(nbytes: int, dev) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
+
+
+# ------------------------------------------------------------------- sparse
+class SparseAttentionFunction(torch.autograd.Function):
+    """out, node_score = masked attention over a WindowAdjacency.
+
+    q [N_q, H, d], k/v [N_k, H, d] (same dtype, fp32 or bf16).  node_score is
+    returned without gradient (the reference's caller detaches it,
+    graphormer_dist_node_level.py:345).
+    """
+
+    @staticmethod
+    def forward(ctx, q, k, v, adj, scale, lo, hi, eps):
+        lib = _lib.load()
+        n_q, H, d = q.shape
+        dev = q.device
+        out = torch.empty_like(q)
+        rinv = torch.empty(n_q, H, dtype=torch.float32, device=dev)
+        ns = torch.empty(adj.dst_end, dtype=torch.float32, device=dev)
+        fb, bb = C.c_size_t(), C.c_size_t()
+        _lib.check(lib.ngt_sparse_workspace_bytes(adj.ptr(), H, d, C.byref(fb), C.byref(bb)))
+        ws = _workspace(fb.value, dev)
+        _lib.check(lib.ngt_sparse_fwd(_dtype_code(q), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                      adj.ptr(), H, d, scale, lo, hi, eps, out.data_ptr(),
+                                      rinv.data_ptr(), ns.data_ptr() if ns.numel() else None,
+                                      int(ns.numel()), ws.data_ptr(), fb.value, _stream(dev)))
+        ctx.save_for_backward(q, k, v, out, rinv)
+        ctx.adj, ctx.scale, ctx.lo, ctx.hi, ctx.bwd_bytes = adj, scale, lo, hi, bb.value
+        ctx.mark_non_differentiable(ns)
+        return out, ns
+
+    @staticmethod
+    def backward(ctx, g_out, g_ns):
+        q, k, v, out, rinv = ctx.saved_tensors
+        lib = _lib.load()
+        n_q, H, d = q.shape
+        dev = q.device
+        g = g_out.to(q.dtype)
+        if not g.is_contiguous() or g.data_ptr() % 16:
+            g = g.contiguous() if not g.is_contiguous() else g.clone()
+        gq = torch.empty_like(q)
+        gk = torch.empty_like(k)
+        gv = torch.empty_like(v)
+        ws = _workspace(ctx.bwd_bytes, dev)
+        _lib.check(lib.ngt_sparse_bwd(_dtype_code(q), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                      out.data_ptr(), g.data_ptr(), rinv.data_ptr(),
+                                      ctx.adj.ptr(), H, d, ctx.scale, ctx.lo, ctx.hi,
+                                      gq.data_ptr(), gk.data_ptr(), gv.data_ptr(), ws.data_ptr(),
+                                      ctx.bwd_bytes, _stream(dev)))
+        return gq, gk, gv, None, None, None, None, None
+
+
+def sparse_attention(q, k, v, edge_index, num_heads=None, scale=None, cache: AdjacencyCache = None,
+                     lo=CLAMP_LO, hi=CLAMP_HI, eps=EPS):
+    """Functional form.  q [.., N_q, H, d] -> (x [N_q, H, d], node_scores [max(dst)+1]).
+
+    ``edge_index`` [2, E]: row 0 = key (src) index < N_k, row 1 = query (dst)
+    index < N_q.  The reference requires N_q == N_k; N_q < N_k (extra key rows,
+    e.g. related nodes served from the cache) is also accepted.
+    """
+    H, d = q.shape[-2], q.shape[-1]
+    if num_heads is not None and num_heads != H:
+        raise ValueError(f"q has {H} heads, expected {num_heads}")
+    q = _prep(q.reshape(-1, H, d), "q")
+    k = _prep(k.reshape(-1, H, d), "k")
+    v = _prep(v.reshape(-1, H, d), "v")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError("q, k, v must share a dtype")
+    _dtype_code(q)
+    if k.shape != v.shape or k.shape[1:] != q.shape[1:]:
+        raise ValueError(f"shape mismatch q {tuple(q.shape)} k {tuple(k.shape)} v {tuple(v.shape)}")
+    if q.shape[0] > k.shape[0]:
+        raise ValueError(f"N_q={q.shape[0]} exceeds N_k={k.shape[0]}")
+    if scale is None:
+        scale = math.sqrt(d)
+    cache = cache or default_cache
+    adj = cache.get(edge_index, q.shape[0], k.shape[0], chunk_for_heads(H))
+    return SparseAttentionFunction.apply(q, k, v, adj, float(scale), float(lo), float(hi),
+                                         float(eps))
+
+
+# -------------------------------------------------------------------- dense
+class DenseAttentionFunction(torch.autograd.Function):
+    """out = softmax((q*scale) k^T) v per head, node_score[j] = sum_i mean_h |S|."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, scale, want_scores):
+        lib = _lib.load()
+        n_q, H, d = q.shape
+        n_k = k.shape[0]
+        dev = q.device
+        out = torch.empty_like(q)
+        lse = torch.empty(H, n_q, dtype=torch.float32, device=dev)
+        ns = torch.empty(n_k if want_scores else 0, dtype=torch.float32, device=dev)
+        fb, bb = C.c_size_t(), C.c_size_t()
+        _lib.check(lib.ngt_dense_workspace_bytes(n_q, n_k, H, d, C.byref(fb), C.byref(bb)))
+        ws = _workspace(fb.value, dev)
+        _lib.check(lib.ngt_dense_fwd(_dtype_code(q), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                     n_q, n_k, H, d, scale, out.data_ptr(), lse.data_ptr(),
+                                     ns.data_ptr() if want_scores and n_k else None,
+                                     ws.data_ptr(), fb.value, _stream(dev)))
+        ctx.save_for_backward(q, k, v, out, lse)
+        ctx.scale, ctx.bwd_bytes = scale, bb.value
+        ctx.mark_non_differentiable(ns)
+        return out, ns
+
+    @staticmethod
+    def backward(ctx, g_out, g_ns):
+        q, k, v, out, lse = ctx.saved_tensors
+        lib = _lib.load()
+        n_q, H, d = q.shape
+        n_k = k.shape[0]
+        dev = q.device
+        g = g_out.to(q.dtype)
+        if not g.is_contiguous() or g.data_ptr() % 16:
+            g = g.contiguous() if not g.is_contiguous() else g.clone()
+        gq = torch.empty_like(q)
+        gk = torch.empty_like(k)
+        gv = torch.empty_like(v)
+        ws = _workspace(ctx.bwd_bytes, dev)
+        _lib.check(lib.ngt_dense_bwd(_dtype_code(q), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                     out.data_ptr(), g.data_ptr(), lse.data_ptr(), n_q, n_k, H, d,
+                                     ctx.scale, gq.data_ptr(), gk.data_ptr(), gv.data_ptr(),
+                                     ws.data_ptr(), ctx.bwd_bytes, _stream(dev)))
+        return gq, gk, gv, None, None
+
+
+def dense_attention(q, k, v, scale=None, node_scores=True):
+    """Functional form of full_attention: q [.., N_q, H, d], k/v [.., N_k, H, d]
+    -> (x [N_q, H, d], node_scores [N_k] or empty)."""
+    H, d = q.shape[-2], q.shape[-1]
+    q = _prep(q.reshape(-1, H, d), "q")
+    k = _prep(k.reshape(-1, H, d), "k")
+    v = _prep(v.reshape(-1, H, d), "v")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError("q, k, v must share a dtype")
+    _dtype_code(q)
+    if k.shape != v.shape or k.shape[1:] != q.shape[1:]:
+        raise ValueError(f"shape mismatch q {tuple(q.shape)} k {tuple(k.shape)} v {tuple(v.shape)}")
+    if scale is None:
+        scale = math.sqrt(d)
+    return DenseAttentionFunction.apply(q, k, v, float(scale), bool(node_scores))
+
+
+# ---------------------------------------------------------------- the module
+class CoreAttention(nn.Module):
+    """Same constructor/attributes/forward as the reference's CoreAttention."""
+
+    def __init__(self, hidden_size, attention_dropout_rate, num_heads, cache: AdjacencyCache = None):
+        super().__init__()
+        self.hidden_size_per_attention_head = hidden_size // num_heads
+        self.scale = math.sqrt(self.hidden_size_per_attention_head)
+        self.num_heads = num_heads
+        self.att_dropout = nn.Dropout(attention_dropout_rate)
+        self.attention_dropout_rate = attention_dropout_rate
+        self.adjacency_cache = cache or default_cache
+
+    def full_attention(self, k, q, v, attn_bias, mask=None, pruning_mask=None):
+        """graphormer_dist_node_level.py:42-65.  Returns (x [b, N, H, d], node_scores [N_k])."""
+        if attn_bias is not None or mask is not None or pruning_mask is not None:
+            raise NotImplementedError(
+                "full attention with attn_bias/mask/pruning_mask is not implemented by the "
+                "dense kernel (all are None on NeutronGT's training path)")
+        if self.training and self.att_dropout.p > 0:
+            raise NotImplementedError(
+                "dropout on full-attention probabilities is not implemented by the dense kernel; "
+                "use attention_dropout_rate=0 or eval mode")
+        if q.size(0) != 1:
+            raise NotImplementedError("batch size must be 1 (as in NeutronGT's window step)")
+        x, ns = dense_attention(q, k, v, scale=self.scale)
+        return x.unsqueeze(0), ns
+
+    def sparse_attention_bias(self, q, k, v, edge_index, attn_bias):
+        """graphormer_dist_node_level.py:67-98.  Returns (x [N_q, H, d], node_scores)."""
+        if attn_bias is not None:
+            raise NotImplementedError(
+                "sparse attention with a dense attn_bias is not implemented (struct_enc is "
+                "False on NeutronGT's training path)")
+        return sparse_attention(q, k, v, edge_index, num_heads=self.num_heads, scale=self.scale,
+                                cache=self.adjacency_cache)
+
+    def forward(self, q, k, v, attn_bias=None, edge_index=None, attn_type=None, mask=None,
+                pruning_mask=None):
+        batch_size, s_len = q.size(0), q.size(1)
+        if attn_type == "sparse":
+            x, score = self.sparse_attention_bias(q, k, v, edge_index, attn_bias)
+        elif attn_type == "flash":
+            raise NotImplementedError(
+                "attn_type='flash' (the reference's fp16 naive attention with dropout always on) "
+                "is not provided; use 'sparse' or 'full'")
+        else:
+            x, score = self.full_attention(k, q, v, attn_bias, mask=mask, pruning_mask=pruning_mask)
+        x = x.view(batch_size, s_len, -1)
+        return x, score
+
+
+def install(model: nn.Module, cache: AdjacencyCache = None) -> int:
+    """Replaces every ``local_attn`` CoreAttention-like submodule of ``model``
+    (NeutronGT's MultiHeadAttention / DistributedAttentionNodeLevel) with this
+    module, keeping hidden size, heads and dropout.  Returns the count."""
+    n = 0
+    for mod in list(model.modules()):
+        old = getattr(mod, "local_attn", None)
+        if isinstance(old, nn.Module) and hasattr(old, "hidden_size_per_attention_head") \
+                and not isinstance(old, CoreAttention):
+            new = CoreAttention(old.hidden_size_per_attention_head * old.num_heads,
+                                old.attention_dropout_rate, old.num_heads, cache=cache)
+            new.train(old.training)
+            mod.local_attn = new
+            n += 1
+    return n

@@ -1,0 +1,127 @@
+"""Device-resident window adjacency (CSR + transposed CSR + work lists).
+
+The reference hands the attention core a COO ``edge_index`` [2, E] (row 0 =
+key/src, row 1 = query/dst; NeutronGT/core/node_level_pipeline/
+window_state.py:122-140) and re-derives the grouping with gathers and scatter
+adds on every call (NeutronGT/models/graphormer_dist_node_level.py:75-97).
+Here the window's edge_index is converted once on the GPU
+(``ngt_csr_build``) and cached: the same edge_index object is reused by every
+layer of a window step and across epochs.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from collections import OrderedDict
+
+import torch
+
+from . import _lib
+
+# Work items cover at most this many "rounds" of a wave's edge slots before a
+# row is split into chunks whose partial sums are added by a finalize pass.
+ITEM_ROUNDS = 32
+
+
+def lanes_for_heads(n_heads: int) -> int:
+    lanes = 1
+    while lanes < n_heads:
+        lanes <<= 1
+    return lanes
+
+
+def chunk_for_heads(n_heads: int) -> int:
+    """Edges per work item: (64 / lanes-per-edge) slots x ITEM_ROUNDS."""
+    return max(1, 64 // lanes_for_heads(n_heads)) * ITEM_ROUNDS
+
+
+class WindowAdjacency:
+    """Both CSR orientations of one window plus its work lists (int32, on device)."""
+
+    def __init__(self, edge_index: torch.Tensor, n_q: int, n_k: int, chunk: int):
+        if edge_index.dim() != 2 or edge_index.shape[0] != 2:
+            raise ValueError(f"edge_index must be [2, E], got {tuple(edge_index.shape)}")
+        if not edge_index.is_cuda:
+            raise ValueError("edge_index must be on the GPU")
+        lib = _lib.load()
+        dev = edge_index.device
+        ei = edge_index.to(torch.int64).contiguous()
+        E = int(ei.shape[1])
+        self.edge_index = edge_index  # pins the cache key's storage
+        self.n_q, self.n_k, self.n_edges, self.chunk = int(n_q), int(n_k), E, int(chunk)
+        miq, msq, mik, msk = (C.c_int32() for _ in range(4))
+        _lib.check(lib.ngt_csr_sizes(E, n_q, n_k, chunk, chunk, C.byref(miq), C.byref(msq),
+                                     C.byref(mik), C.byref(msk)))
+        i32 = dict(dtype=torch.int32, device=dev)
+        self.rowptr = torch.empty(n_q + 1, **i32)
+        self.col = torch.empty(max(E, 1), **i32)
+        self.perm = torch.empty(max(E, 1), **i32)
+        self.t_rowptr = torch.empty(n_k + 1, **i32)
+        self.t_col = torch.empty(max(E, 1), **i32)
+        self.t_perm = torch.empty(max(E, 1), **i32)
+        self.q2t = torch.empty(max(E, 1), **i32)
+        self.items_q = torch.empty(miq.value, 4, **i32)
+        self.splits_q = torch.empty(msq.value, 4, **i32)
+        self.items_k = torch.empty(mik.value, 4, **i32)
+        self.splits_k = torch.empty(msk.value, 4, **i32)
+        self.info_dev = torch.zeros(_lib.INFO_LEN, **i32)
+        s = _lib.WindowCSR()
+        s.n_q, s.n_k, s.n_edges, s.chunk_q, s.chunk_k = n_q, n_k, E, chunk, chunk
+        for name in ("rowptr", "col", "perm", "t_rowptr", "t_col", "t_perm", "q2t", "items_q",
+                     "splits_q", "items_k", "splits_k"):
+            setattr(s, name, getattr(self, name).data_ptr())
+        s.info = self.info_dev.data_ptr()
+        s.max_items_q, s.max_splits_q = miq.value, msq.value
+        s.max_items_k, s.max_splits_k = mik.value, msk.value
+        ws_bytes = C.c_size_t()
+        with torch.cuda.device(dev):
+            _lib.check(lib.ngt_csr_workspace_bytes(E, n_q, n_k, C.byref(ws_bytes)))
+            ws = torch.empty(max(ws_bytes.value, 1), dtype=torch.uint8, device=dev)
+            stream = torch.cuda.current_stream(dev).cuda_stream
+            _lib.check(lib.ngt_csr_build(ei.data_ptr() if E else None, C.byref(s), ws.data_ptr(),
+                                         ws_bytes.value, stream))
+            info = self.info_dev.cpu()  # one sync per window build
+        del ws
+        self.info = [int(x) for x in info.tolist()]
+        if self.info[_lib.INFO_BAD_EDGES]:
+            raise IndexError(f"edge_index has {self.info[_lib.INFO_BAD_EDGES]} entries outside "
+                             f"[0, {n_k}) x [0, {n_q}) (src x dst)")
+        s.n_items_q = self.info[_lib.INFO_ITEMS_Q]
+        s.n_parts_q = self.info[_lib.INFO_PARTS_Q]
+        s.n_splits_q = self.info[_lib.INFO_SPLITS_Q]
+        s.n_items_k = self.info[_lib.INFO_ITEMS_K]
+        s.n_parts_k = self.info[_lib.INFO_PARTS_K]
+        s.n_splits_k = self.info[_lib.INFO_SPLITS_K]
+        self.struct = s
+        self.dst_end = self.info[_lib.INFO_DST_END]
+        self.max_deg_q = self.info[_lib.INFO_MAX_DEG_Q]
+        self.max_deg_k = self.info[_lib.INFO_MAX_DEG_K]
+
+    def ptr(self):
+        return C.byref(self.struct)
+
+
+class AdjacencyCache:
+    """LRU of WindowAdjacency keyed by the edge_index tensor's storage/version."""
+
+    def __init__(self, capacity: int = 64):
+        self.capacity = capacity
+        self._d: OrderedDict = OrderedDict()
+
+    def get(self, edge_index: torch.Tensor, n_q: int, n_k: int, chunk: int) -> WindowAdjacency:
+        key = (edge_index.data_ptr(), edge_index._version, tuple(edge_index.shape),
+               str(edge_index.device), edge_index.dtype, n_q, n_k, chunk)
+        adj = self._d.get(key)
+        if adj is not None and adj.edge_index is edge_index:
+            self._d.move_to_end(key)
+            return adj
+        adj = WindowAdjacency(edge_index, n_q, n_k, chunk)
+        self._d[key] = adj
+        while len(self._d) > self.capacity:
+            self._d.popitem(last=False)
+        return adj
+
+    def clear(self):
+        self._d.clear()
+
+
+default_cache = AdjacencyCache()

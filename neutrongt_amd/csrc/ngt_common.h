@@ -1,0 +1,200 @@
+// Shared device helpers for the window attention kernels (gfx950, wave64).
+//
+// Element types: the kernels read q/k/v and write outputs in either fp32 or
+// bf16 (stored as raw uint16).  All arithmetic is fp32.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/ngt_attn.h"
+
+namespace ngt {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- bf16 <-> f32
+struct bf16_t {
+  uint16_t x;
+};
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// Round-to-nearest-even (the rule torch uses for float -> bfloat16); NaN stays
+// a quiet NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+template <typename T>
+struct elem;
+template <>
+struct elem<float> {
+  static __device__ __forceinline__ float load(const float* p) { return *p; }
+  static __device__ __forceinline__ void store(float* p, float v) { *p = v; }
+};
+template <>
+struct elem<bf16_t> {
+  static __device__ __forceinline__ float load(const bf16_t* p) { return bf16_to_f32(p->x); }
+  static __device__ __forceinline__ void store(bf16_t* p, float v) { p->x = f32_to_bf16(v); }
+};
+
+// ------------------------------------------------------- vector row load/store
+// Load DH consecutive elements starting at p into fp32 registers.  The widest
+// access that divides the row is used (16 B when the row is a multiple of 16 B;
+// callers guarantee 16-byte aligned base pointers and row strides).
+template <typename T, int DH>
+__device__ __forceinline__ void load_row(const T* __restrict__ p, float (&out)[DH]) {
+  constexpr int bytes = DH * static_cast<int>(sizeof(T));
+  if constexpr (bytes % 16 == 0) {
+    const uint4* v = reinterpret_cast<const uint4*>(p);
+#pragma unroll
+    for (int i = 0; i < bytes / 16; ++i) {
+      const uint4 w = v[i];
+      if constexpr (sizeof(T) == 4) {
+        out[4 * i + 0] = __uint_as_float(w.x);
+        out[4 * i + 1] = __uint_as_float(w.y);
+        out[4 * i + 2] = __uint_as_float(w.z);
+        out[4 * i + 3] = __uint_as_float(w.w);
+      } else {
+        out[8 * i + 0] = __uint_as_float(w.x << 16);
+        out[8 * i + 1] = __uint_as_float(w.x & 0xffff0000u);
+        out[8 * i + 2] = __uint_as_float(w.y << 16);
+        out[8 * i + 3] = __uint_as_float(w.y & 0xffff0000u);
+        out[8 * i + 4] = __uint_as_float(w.z << 16);
+        out[8 * i + 5] = __uint_as_float(w.z & 0xffff0000u);
+        out[8 * i + 6] = __uint_as_float(w.w << 16);
+        out[8 * i + 7] = __uint_as_float(w.w & 0xffff0000u);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < DH; ++c) out[c] = elem<T>::load(p + c);
+  }
+}
+
+template <typename T, int DH>
+__device__ __forceinline__ void store_row(T* __restrict__ p, const float (&in)[DH]) {
+  constexpr int bytes = DH * static_cast<int>(sizeof(T));
+  if constexpr (bytes % 16 == 0) {
+    uint4* v = reinterpret_cast<uint4*>(p);
+#pragma unroll
+    for (int i = 0; i < bytes / 16; ++i) {
+      uint4 w;
+      if constexpr (sizeof(T) == 4) {
+        w.x = __float_as_uint(in[4 * i + 0]);
+        w.y = __float_as_uint(in[4 * i + 1]);
+        w.z = __float_as_uint(in[4 * i + 2]);
+        w.w = __float_as_uint(in[4 * i + 3]);
+      } else {
+        w.x = uint32_t(f32_to_bf16(in[8 * i + 0])) | (uint32_t(f32_to_bf16(in[8 * i + 1])) << 16);
+        w.y = uint32_t(f32_to_bf16(in[8 * i + 2])) | (uint32_t(f32_to_bf16(in[8 * i + 3])) << 16);
+        w.z = uint32_t(f32_to_bf16(in[8 * i + 4])) | (uint32_t(f32_to_bf16(in[8 * i + 5])) << 16);
+        w.w = uint32_t(f32_to_bf16(in[8 * i + 6])) | (uint32_t(f32_to_bf16(in[8 * i + 7])) << 16);
+      }
+      v[i] = w;
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < DH; ++c) elem<T>::store(p + c, in[c]);
+  }
+}
+
+// fp32 rows (partials, statistics) with 16-byte accesses when DH % 4 == 0.
+template <int DH>
+__device__ __forceinline__ void load_f32(const float* __restrict__ p, float (&out)[DH]) {
+  if constexpr (DH % 4 == 0) {
+    const float4* v = reinterpret_cast<const float4*>(p);
+#pragma unroll
+    for (int i = 0; i < DH / 4; ++i) {
+      float4 w = v[i];
+      out[4 * i + 0] = w.x;
+      out[4 * i + 1] = w.y;
+      out[4 * i + 2] = w.z;
+      out[4 * i + 3] = w.w;
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < DH; ++c) out[c] = p[c];
+  }
+}
+
+template <int DH>
+__device__ __forceinline__ void store_f32(float* __restrict__ p, const float (&in)[DH]) {
+  if constexpr (DH % 4 == 0) {
+    float4* v = reinterpret_cast<float4*>(p);
+#pragma unroll
+    for (int i = 0; i < DH / 4; ++i) v[i] = make_float4(in[4 * i], in[4 * i + 1], in[4 * i + 2], in[4 * i + 3]);
+  } else {
+#pragma unroll
+    for (int c = 0; c < DH; ++c) p[c] = in[c];
+  }
+}
+
+// ------------------------------------------------------------ wave reductions
+__device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor(v, mask, kWave); }
+
+// Sum over the lanes that share (lane % L) -- i.e. across the 64/L edge slots
+// of a wave whose lanes are laid out as (slot, head).
+template <int DH>
+__device__ __forceinline__ void reduce_slots(float (&acc)[DH], float& z, int L) {
+  for (int off = L; off < kWave; off <<= 1) {
+    z += shfl_xor(z, off);
+#pragma unroll
+    for (int c = 0; c < DH; ++c) acc[c] += shfl_xor(acc[c], off);
+  }
+}
+
+template <int DH>
+__device__ __forceinline__ void reduce_slots2(float (&a)[DH], float (&b)[DH], int L) {
+  for (int off = L; off < kWave; off <<= 1) {
+#pragma unroll
+    for (int c = 0; c < DH; ++c) {
+      a[c] += shfl_xor(a[c], off);
+      b[c] += shfl_xor(b[c], off);
+    }
+  }
+}
+
+template <int DH>
+__device__ __forceinline__ void reduce_slots1(float (&a)[DH], int L) {
+  for (int off = L; off < kWave; off <<= 1) {
+#pragma unroll
+    for (int c = 0; c < DH; ++c) a[c] += shfl_xor(a[c], off);
+  }
+}
+
+// Sum over the low log2(L) lane bits (the heads of one slot).
+__device__ __forceinline__ float reduce_heads(float v, int L) {
+  for (int off = 1; off < L; off <<= 1) v += shfl_xor(v, off);
+  return v;
+}
+
+template <typename T>
+struct dtype_of;
+template <>
+struct dtype_of<float> {
+  static constexpr int value = NGT_F32;
+};
+template <>
+struct dtype_of<bf16_t> {
+  static constexpr int value = NGT_BF16;
+};
+
+// Records a message for ngt_last_error() (thread-local) and returns the code.
+int set_error(int code, const char* fmt, ...);
+
+}  // namespace ngt
+
+#define NGT_HIP_CHECK(expr)                                                              \
+  do {                                                                                   \
+    hipError_t _e = (expr);                                                              \
+    if (_e != hipSuccess)                                                                \
+      return ::ngt::set_error(NGT_ERR_HIP, "%s:%d %s: %s", __FILE__, __LINE__, #expr,    \
+                              hipGetErrorString(_e));                                    \
+  } while (0)

@@ -1,0 +1,174 @@
+"""Window preparation that feeds the attention core (integer work, bit-exact).
+
+  merge_related_nodes       GPU (ngt_merge_related_nodes); mirrors
+                            weightMetis_keepParent._merge_related_nodes,
+                            NeutronGT/core/metisPartition.py:397-425
+  duplicate_rerange         NeutronGT/core/node_level_pipeline/window_state.py:52-73
+  dup_cache_metadata        NeutronGT/core/node_level_pipeline/window_state.py:181-205
+  assemble_window_features  GPU row gather (ngt_gather_rows); mirrors
+                            NeutronGT/core/node_level_pipeline/train_eval.py:234-242
+  adj_weights               NeutronGT/core/ppr_preprocess.py:30-71 weight rule,
+                            with a stable neighbour order (the reference's
+                            argsort at :53 is unstable)
+
+The duplicate bookkeeping is host logic in the reference (torch unique/isin on
+CPU tensors) and stays torch code here; the per-element work (related-node
+ranking, feature gathers) runs as HIP kernels.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import torch
+
+from . import _lib
+
+
+def merge_related_nodes(xadj: torch.Tensor, adjncy: torch.Tensor, eweights: torch.Tensor,
+                        partition: torch.Tensor, topk_percent: int) -> torch.Tensor:
+    """Partition expanded by its top ``topk_percent`` % external neighbours.
+
+    xadj/adjncy/eweights: int32 symmetric CSR of the global graph on the GPU
+    (METIS adjacency + edge weights); partition: int64 global ids.  Returns a
+    sorted int64 tensor on the GPU (one device->host sync for its length).
+    """
+    lib = _lib.load()
+    dev = partition.device
+    if not (xadj.is_cuda and adjncy.is_cuda and eweights.is_cuda and partition.is_cuda):
+        raise ValueError("merge_related_nodes: all tensors must be on the GPU")
+    xadj = xadj.to(torch.int32).contiguous()
+    adjncy = adjncy.to(torch.int32).contiguous()
+    eweights = eweights.to(torch.int32).contiguous()
+    part = partition.to(torch.int64).contiguous()
+    n_nodes = int(xadj.numel()) - 1
+    if adjncy.numel() != eweights.numel():
+        raise ValueError("adjncy and eweights differ in length")
+    # The kernels index adjncy through xadj: reject a malformed CSR up front.
+    if n_nodes < 0 or int(xadj[0].item()) != 0 or int(xadj[-1].item()) != adjncy.numel() or \
+            bool((xadj[1:] < xadj[:-1]).any().item()):
+        raise ValueError("merge_related_nodes: xadj is not a valid CSR row pointer for adjncy")
+    out = torch.empty(max(n_nodes, 1), dtype=torch.int64, device=dev)
+    status = torch.zeros(3, dtype=torch.int32, device=dev)
+    nb = C.c_size_t()
+    _lib.check(lib.ngt_related_workspace_bytes(n_nodes, int(part.numel()), C.byref(nb)))
+    ws = torch.empty(max(nb.value, 1), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    _lib.check(lib.ngt_merge_related_nodes(xadj.data_ptr(), adjncy.data_ptr(),
+                                           eweights.data_ptr(), n_nodes, part.data_ptr(),
+                                           int(part.numel()), int(topk_percent), out.data_ptr(),
+                                           status.data_ptr(), ws.data_ptr(), nb.value, stream))
+    length, _n_ext, bad = (int(x) for x in status.cpu().tolist())
+    if bad:
+        raise ValueError(f"merge_related_nodes: {bad} invalid node ids / weights")
+    return out[:length]
+
+
+def duplicate_rerange(local_partitions):
+    """Nodes present in >= 2 of a rank's windows move to the front of each
+    window (original order kept).  Returns (reranged, dup_nodes_per_partition)."""
+    if not local_partitions:
+        return [], []
+    all_nodes = torch.cat([p.to(torch.long).cpu() for p in local_partitions])
+    if all_nodes.numel() == 0:
+        return ([p.clone() for p in local_partitions],
+                [torch.empty((0,), dtype=torch.long) for _ in local_partitions])
+    uniq, counts = torch.unique(all_nodes, return_counts=True, sorted=True)
+    dups = uniq[counts >= 2]
+    if dups.numel() == 0:
+        return ([p.clone() for p in local_partitions],
+                [torch.empty((0,), dtype=torch.long) for _ in local_partitions])
+    reranged, dup_lists = [], []
+    for p in local_partitions:
+        pc = p.to(torch.long).cpu()
+        m = torch.isin(pc, dups)
+        reranged.append(torch.cat([pc[m], pc[~m]]))
+        dup_lists.append(pc[m])
+    return reranged, dup_lists
+
+
+def dup_cache_metadata(dup_lists, device=None):
+    """(cache_ids sorted unique, per-window indices into the cache)."""
+    non_empty = [d.to(torch.long).cpu() for d in dup_lists if d.numel() > 0]
+    if not non_empty:
+        return (torch.empty((0,), dtype=torch.long),
+                [torch.empty((0,), dtype=torch.long, device=device) for _ in dup_lists])
+    uniq = torch.unique(torch.cat(non_empty), sorted=True)
+    idx = []
+    for d in dup_lists:
+        dc = d.to(torch.long).cpu()
+        t = torch.searchsorted(uniq, dc) if dc.numel() else torch.empty((0,), dtype=torch.long)
+        idx.append(t.to(device=device, dtype=torch.long) if device is not None else t)
+    return uniq, idx
+
+
+def gather_rows(src: torch.Tensor, idx: torch.Tensor, out: torch.Tensor | None = None):
+    """out[r] = src[idx[r]] on the GPU (bit copy).  Raises IndexError on a bad index."""
+    lib = _lib.load()
+    if not (src.is_cuda and idx.is_cuda):
+        raise ValueError("gather_rows: tensors must be on the GPU")
+    src = src.contiguous()
+    idx = idx.to(torch.int64).contiguous()
+    row_bytes = src[0].numel() * src.element_size() if src.dim() > 1 else src.element_size()
+    if out is None:
+        out = torch.empty((idx.numel(),) + tuple(src.shape[1:]), dtype=src.dtype, device=src.device)
+    bad = torch.zeros(1, dtype=torch.int32, device=src.device)
+    if row_bytes % 4:
+        raise ValueError("gather_rows: row size must be a multiple of 4 bytes")
+    stream = torch.cuda.current_stream(src.device).cuda_stream
+    _lib.check(lib.ngt_gather_rows(src.data_ptr(), int(src.shape[0]), idx.data_ptr(),
+                                   int(idx.numel()), int(row_bytes), out.data_ptr(),
+                                   bad.data_ptr(), stream))
+    return out, bad
+
+
+def assemble_window_features(feature: torch.Tensor, cache: torch.Tensor, dup_index: torch.Tensor,
+                             partition: torch.Tensor, check: bool = True) -> torch.Tensor:
+    """x_i = cat(cache[dup_index], feature[partition[n_dup:]]) as two GPU
+    gathers into one buffer (feature and cache resident in HBM)."""
+    n_dup = int(dup_index.numel())
+    part = partition.to(feature.device)
+    n = int(part.numel())
+    out = torch.empty((n,) + tuple(feature.shape[1:]), dtype=feature.dtype, device=feature.device)
+    bads = []
+    if n_dup:
+        _, b = gather_rows(cache, dup_index.to(feature.device), out[:n_dup])
+        bads.append(b)
+    if n - n_dup:
+        _, b = gather_rows(feature, part[n_dup:], out[n_dup:])
+        bads.append(b)
+    if check and bads and int(sum(b for b in bads).item()):
+        raise IndexError("assemble_window_features: index out of range")
+    return out
+
+
+def adj_weights(edge_index: torch.Tensor, ppr_val: torch.Tensor):
+    """Symmetric int32 METIS adjacency + weights from a PPR edge list.
+
+    w = int32(clamp_min(fp32 sum of the PPR values of {u,v} * 1000, 1)); rows in
+    ascending node order; inside row u the (u, v>u) keys come first in ascending
+    v, then the (v<u, u) keys in ascending v (stable order).  Returns
+    (xadj, adjncy, eweights) int32 on edge_index's device.
+    """
+    dev = edge_index.device
+    if edge_index.numel() == 0:
+        z = torch.zeros(0, dtype=torch.int32, device=dev)
+        return torch.zeros(1, dtype=torch.int32, device=dev), z, z
+    n = int(edge_index.max().item()) + 1
+    src, dst = edge_index[0].long(), edge_index[1].long()
+    u = torch.minimum(src, dst)
+    v = torch.maximum(src, dst)
+    key = u * n + v
+    uniq, inv = torch.unique(key, sorted=True, return_inverse=True)
+    summed = torch.zeros(uniq.numel(), dtype=torch.float32, device=dev)
+    summed.scatter_add_(0, inv, ppr_val.to(torch.float32))
+    uu = torch.div(uniq, n, rounding_mode="floor")
+    vv = uniq % n
+    w = (summed * 1000).clamp_min(1).to(torch.int32)
+    u_all = torch.cat([uu, vv])
+    v_all = torch.cat([vv, uu])
+    w_all = torch.cat([w, w])
+    order = torch.sort(u_all, stable=True).indices
+    deg = torch.bincount(u_all, minlength=n)
+    xadj = torch.zeros(n + 1, dtype=torch.int64, device=dev)
+    xadj[1:] = torch.cumsum(deg, 0)
+    return xadj.to(torch.int32), v_all[order].to(torch.int32), w_all[order]

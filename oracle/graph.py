@@ -1,0 +1,181 @@
+"""numpy restatements of the integer window preparation (test oracle only).
+
+Every function returns plain numpy arrays and is bit-exact by construction
+(integer arithmetic, stable sorts).
+
+  csr_from_coo              the canonical CSR the kernels consume, built from the
+                            window COO of NeutronGT/core/node_level_pipeline/
+                            window_state.py:122-140 (rows sorted by (dst, src,
+                            edge id); transposed by (src, dst, edge id))
+  work_items                degree-binned work list (chunked long rows first)
+  merge_related_nodes       NeutronGT/core/metisPartition.py:397-425
+  duplicate_rerange         NeutronGT/core/node_level_pipeline/window_state.py:52-73
+  dup_cache_metadata        NeutronGT/core/node_level_pipeline/window_state.py:181-205
+  assemble_window_features  NeutronGT/core/node_level_pipeline/train_eval.py:234-242
+  adj_weights               NeutronGT/core/ppr_preprocess.py:30-71 (weight rule;
+                            neighbour order fixed stable, see the docstring)
+  subgraph_coo              torch_geometric.utils.subgraph(relabel_nodes=True)
+                            semantics as used at window_state.py:127
+"""
+from __future__ import annotations
+
+import numpy as np
+
+
+def csr_from_coo(src, dst, n_q: int, n_k: int):
+    """Query-major + key-major CSR of a window COO.  Returns a dict of int32
+    arrays: rowptr, col, perm, t_rowptr, t_col, t_perm, q2t."""
+    src = np.asarray(src, dtype=np.int64)
+    dst = np.asarray(dst, dtype=np.int64)
+    assert src.shape == dst.shape
+    assert (src >= 0).all() and (src < n_k).all() and (dst >= 0).all() and (dst < n_q).all()
+    perm = np.lexsort((src, dst))  # stable: ties keep edge-id order
+    t_perm = np.lexsort((dst, src))
+    rowptr = np.zeros(n_q + 1, dtype=np.int64)
+    rowptr[1:] = np.cumsum(np.bincount(dst, minlength=n_q))
+    t_rowptr = np.zeros(n_k + 1, dtype=np.int64)
+    t_rowptr[1:] = np.cumsum(np.bincount(src, minlength=n_k))
+    tpos = np.empty(src.shape[0], dtype=np.int64)
+    tpos[t_perm] = np.arange(src.shape[0])
+    return {
+        "rowptr": rowptr.astype(np.int32),
+        "col": src[perm].astype(np.int32),
+        "perm": perm.astype(np.int32),
+        "t_rowptr": t_rowptr.astype(np.int32),
+        "t_col": dst[t_perm].astype(np.int32),
+        "t_perm": t_perm.astype(np.int32),
+        "q2t": tpos[perm].astype(np.int32),
+    }
+
+
+def work_items(rowptr, chunk: int):
+    """Work list for one orientation: rows longer than ``chunk`` are cut into
+    chunks (listed first, in row order, part slot = item index); every other row
+    is one item with part -1.  Returns (items [n,4], splits [m,4])."""
+    rowptr = np.asarray(rowptr, dtype=np.int64)
+    split_items, plain_items, splits = [], [], []
+    for r in range(rowptr.shape[0] - 1):
+        b, e = int(rowptr[r]), int(rowptr[r + 1])
+        if e - b > chunk:
+            n = (e - b + chunk - 1) // chunk
+            splits.append((r, len(split_items), n, 0))
+            for c in range(n):
+                s = len(split_items)
+                split_items.append((r, b + c * chunk, min(e, b + (c + 1) * chunk), s))
+        else:
+            plain_items.append((r, b, e, -1))
+    items = np.array(split_items + plain_items, dtype=np.int32).reshape(-1, 4)
+    return items, np.array(splits, dtype=np.int32).reshape(-1, 4)
+
+
+def merge_related_nodes(xadj, adjncy, eweights, partition, topk_percent: int):
+    """weightMetis_keepParent._merge_related_nodes (metisPartition.py:397-425),
+    restated with the same Python containers (dict insertion order, stable
+    ``sorted``)."""
+    xadj = [int(x) for x in xadj]
+    adjncy = [int(x) for x in adjncy]
+    eweights = [int(x) for x in eweights]
+    part = [int(x) for x in partition]
+    partition_set = set(part)
+    external = {}
+    for node in part:
+        start, end = xadj[node], xadj[node + 1]
+        if end - start == 0:
+            continue
+        for nb, w in zip(adjncy[start:end], eweights[start:end]):
+            if nb not in partition_set:
+                external[nb] = external.get(nb, 0) + w
+    ranked = sorted(external.items(), key=lambda x: x[1], reverse=True)
+    n_select = len(ranked) * topk_percent // 100 if topk_percent > 0 else 0
+    selected = {node for node, _ in ranked[:n_select]}
+    out = sorted(partition_set | selected)
+    return np.array(out, dtype=np.int64), len(external)
+
+
+def duplicate_rerange(local_partitions):
+    """_compute_local_duplicate_nodes (window_state.py:52-73): nodes present in
+    >= 2 of the rank's windows go first in each window (original order kept)."""
+    parts = [np.asarray(p, dtype=np.int64) for p in local_partitions]
+    if not parts:
+        return [], []
+    all_nodes = np.concatenate(parts) if parts else np.zeros(0, np.int64)
+    if all_nodes.size == 0:
+        return [p.copy() for p in parts], [np.zeros(0, np.int64) for _ in parts]
+    uniq, counts = np.unique(all_nodes, return_counts=True)
+    dups = uniq[counts >= 2]
+    if dups.size == 0:
+        return [p.copy() for p in parts], [np.zeros(0, np.int64) for _ in parts]
+    reranged, dup_lists = [], []
+    for p in parts:
+        m = np.isin(p, dups)
+        reranged.append(np.concatenate([p[m], p[~m]]))
+        dup_lists.append(p[m])
+    return reranged, dup_lists
+
+
+def dup_cache_metadata(dup_lists):
+    """build_dup_cache_metadata (window_state.py:181-205): the cache holds the
+    sorted unique duplicate ids; each window indexes it by searchsorted."""
+    non_empty = [np.asarray(d, np.int64) for d in dup_lists if len(d) > 0]
+    if not non_empty:
+        return np.zeros(0, np.int64), [np.zeros(0, np.int64) for _ in dup_lists]
+    uniq = np.unique(np.concatenate(non_empty))
+    idx = [np.searchsorted(uniq, np.asarray(d, np.int64)) if len(d) else np.zeros(0, np.int64)
+           for d in dup_lists]
+    return uniq, idx
+
+
+def assemble_window_features(feature, cache_ids, dup_index, partition):
+    """x_i = cat(cache[dup_index], feature[partition[n_dup:]]) (train_eval.py:234-242)."""
+    feature = np.asarray(feature)
+    cache = feature[np.asarray(cache_ids, np.int64)]
+    n_dup = len(dup_index)
+    rest = feature[np.asarray(partition, np.int64)[n_dup:]]
+    if n_dup == 0:
+        return rest
+    return np.concatenate([cache[np.asarray(dup_index, np.int64)], rest], axis=0)
+
+
+def adj_weights(edge_index, ppr_val):
+    """build_adj_fromat's weight rule (ppr_preprocess.py:30-71).
+
+    Undirected key min*N+max, unique (sorted), fp32 sum of the PPR values per
+    key, w = int32(clamp_min(sum * 1000, 1)) (truncation), both directions.
+    The reference orders rows with an unstable argsort; this restatement (and
+    the product) fixes the order stable: within row u, the entries coming from
+    (u, v>u) keys in ascending v, then the (v<u, u) keys in ascending v.
+    Returns (xadj int32 [N+1], adjncy int32, eweights int32).
+    """
+    ei = np.asarray(edge_index, dtype=np.int64)
+    val = np.asarray(ppr_val, dtype=np.float32)
+    if ei.size == 0:
+        return np.zeros(1, np.int32), np.zeros(0, np.int32), np.zeros(0, np.int32)
+    n = int(ei.max()) + 1
+    u = np.minimum(ei[0], ei[1])
+    v = np.maximum(ei[0], ei[1])
+    key = u * n + v
+    uniq, inv = np.unique(key, return_inverse=True)
+    summed = np.zeros(uniq.shape[0], dtype=np.float32)
+    np.add.at(summed, inv, val)
+    uu = uniq // n
+    vv = uniq % n
+    w = np.maximum(summed * np.float32(1000.0), np.float32(1.0)).astype(np.int32)
+    u_all = np.concatenate([uu, vv])
+    v_all = np.concatenate([vv, uu])
+    w_all = np.concatenate([w, w])
+    order = np.argsort(u_all, kind="stable")
+    deg = np.bincount(u_all, minlength=n)
+    xadj = np.zeros(n + 1, dtype=np.int64)
+    xadj[1:] = np.cumsum(deg)
+    return xadj.astype(np.int32), v_all[order].astype(np.int32), w_all[order].astype(np.int32)
+
+
+def subgraph_coo(partition, edge_index, num_nodes: int):
+    """Induced subgraph with relabelling by position in ``partition``, edges in
+    global edge order (torch_geometric subgraph(relabel_nodes=True))."""
+    part = np.asarray(partition, np.int64)
+    ei = np.asarray(edge_index, np.int64)
+    pos = np.full(num_nodes, -1, dtype=np.int64)
+    pos[part] = np.arange(part.shape[0])
+    keep = (pos[ei[0]] >= 0) & (pos[ei[1]] >= 0)
+    return np.stack([pos[ei[0][keep]], pos[ei[1][keep]]])

@@ -1,0 +1,51 @@
+"""Shared helpers for the test-suite."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+# Tolerances of the attention path (normwise relative error ||a-b|| / ||b||).
+TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2}
+
+
+def relerr(a, b) -> float:
+    a = torch.as_tensor(a).double().cpu()
+    b = torch.as_tensor(b).double().cpu()
+    nb = b.norm().item()
+    d = (a - b).norm().item()
+    return d / nb if nb > 0 else d
+
+
+def assert_close(a, b, dtype, what=""):
+    tol = TOL[dtype]
+    e = relerr(a, b)
+    assert e <= tol, f"{what}: relative error {e:.3e} > {tol:.0e}"
+    # elementwise guard scaled to the reference's magnitude
+    a = torch.as_tensor(a).double().cpu()
+    b = torch.as_tensor(b).double().cpu()
+    if b.numel():
+        atol = 10 * tol * max(b.abs().max().item(), 1e-30)
+        worst = (a - b).abs().max().item()
+        assert worst <= atol, f"{what}: max abs diff {worst:.3e} > {atol:.3e}"
+
+
+def random_coo(n_q: int, n_k: int, n_edges: int, seed: int = 0, self_loops: bool = True):
+    """Random window COO (duplicates allowed) with some empty rows."""
+    rng = np.random.default_rng(seed)
+    src = rng.integers(0, n_k, n_edges)
+    dst = rng.integers(0, max(1, n_q - n_q // 5), n_edges)  # last ~20% of rows stay empty
+    if self_loops:
+        m = min(n_q, n_k) - n_q // 5
+        src = np.concatenate([src, np.arange(max(m, 0))])
+        dst = np.concatenate([dst, np.arange(max(m, 0))])
+    return np.stack([src, dst]).astype(np.int64)
+
+
+def hub_coo(n_q: int, n_k: int, hub_deg: int, seed: int = 0):
+    """COO with one query hub row of degree hub_deg and one key hub."""
+    rng = np.random.default_rng(seed)
+    src = np.concatenate([rng.integers(0, n_k, hub_deg), np.full(hub_deg // 2, 1),
+                          rng.integers(0, n_k, 4 * n_q)])
+    dst = np.concatenate([np.zeros(hub_deg, np.int64), rng.integers(0, n_q, hub_deg // 2),
+                          rng.integers(0, n_q, 4 * n_q)])
+    return np.stack([src, dst]).astype(np.int64)

@@ -1,0 +1,82 @@
+"""The C-ABI library loads, exports every declared symbol and validates its
+arguments -- no GPU needed (no compute call is made)."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+from neutrongt_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "ngt_attn.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ngt_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_is_built_and_loads():
+    assert _lib.LIB_PATH.exists(), "run python -m neutrongt_amd.build"
+    lib = _lib.load()
+    assert lib.ngt_abi_version() == _lib.ABI_VERSION
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    lib = _lib.load()
+    names = _declared()
+    assert len(names) >= 14
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in ngt_attn.h but not exported"
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+
+
+def test_struct_layout_matches_header():
+    # int32 n_q, n_k; int64 n_edges; int32 chunk_q, chunk_k; 12 pointers; 10 int32
+    assert C.sizeof(_lib.WindowCSR) == 8 + 8 + 8 + 12 * 8 + 10 * 4
+    assert _lib.WindowCSR.rowptr.offset == 24
+    assert _lib.WindowCSR.max_items_q.offset == 24 + 12 * 8
+
+
+def test_csr_sizes_arithmetic():
+    lib = _lib.load()
+    a, b, c, d = (C.c_int32() for _ in range(4))
+    assert lib.ngt_csr_sizes(1000, 100, 300, 64, 32, C.byref(a), C.byref(b), C.byref(c),
+                             C.byref(d)) == 0
+    assert a.value == 100 + 2 * 16 + 1 and c.value == 300 + 2 * 32 + 1
+    assert b.value == 16 + 1 and d.value == 32 + 1
+    assert lib.ngt_csr_sizes(-1, 1, 1, 1, 1, None, None, None, None) == 1
+
+
+def test_argument_errors_are_reported_without_touching_the_gpu():
+    lib = _lib.load()
+    rc = lib.ngt_sparse_fwd(0, None, None, None, None, 8, 8, 1.0, -5.0, 5.0, 1e-6, None, None,
+                            None, 0, None, 0, None)
+    assert rc == 1
+    assert b"null csr" in lib.ngt_last_error()
+    s = _lib.WindowCSR()
+    rc = lib.ngt_sparse_fwd(0, None, None, None, C.byref(s), 8, 12, 1.0, -5.0, 5.0, 1e-6, None,
+                            None, None, 0, None, 0, None)
+    assert rc == 2 and b"head_dim" in lib.ngt_last_error()
+    rc = lib.ngt_dense_fwd(7, None, None, None, 1, 1, 1, 8, 1.0, None, None, None, None, 0, None)
+    assert rc == 1
+    with pytest.raises(_lib.NGTError):
+        _lib.check(1)
+
+
+def test_product_never_imports_the_oracle():
+    pkg = ROOT / "neutrongt_amd"
+    for f in list(pkg.rglob("*.py")) + list(pkg.rglob("*.hip")):
+        text = f.read_text()
+        assert not re.search(r"^\s*(from|import)\s+oracle\b", text, flags=re.M), f
+        assert "oracle/" not in text, f
+
+
+def test_build_entry_compiles(tmp_path):
+    """The build script's flags keep packed-fp32 VALU ops disabled."""
+    from neutrongt_amd import build
+
+    flags = " ".join(build.HIPCC_FLAGS)
+    assert "-packed-fp32-ops" in flags and "--offload-arch=gfx950" in flags

@@ -1,0 +1,223 @@
+"""GPU parity of the sparse attention path (CSR build, forward, backward)
+against the CPU oracle on identical seeded inputs."""
+import numpy as np
+import pytest
+import torch
+
+from neutrongt_amd import CoreAttention, SparseAttentionFunction, WindowAdjacency, sparse_attention
+from neutrongt_amd import synthetic as S
+from oracle import attention as OA
+from oracle import graph as OG
+from tests._util import TOL, assert_close, hub_coo, random_coo, relerr
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _run_kernel(q, k, v, ei, go, chunk=None):
+    """fwd + bwd through the HIP path; returns dict of CPU tensors."""
+    qd, kd, vd = (t.cuda().requires_grad_(True) for t in (q, k, v))
+    eid = torch.from_numpy(ei).cuda()
+    if chunk is None:
+        x, ns = sparse_attention(qd, kd, vd, eid)
+    else:
+        adj = WindowAdjacency(eid, q.shape[0], k.shape[0], chunk)
+        x, ns = SparseAttentionFunction.apply(qd, kd, vd, adj, float(q.shape[-1]) ** 0.5, -5.0,
+                                              5.0, 1e-6)
+    x.backward(go.cuda())
+    torch.cuda.synchronize()
+    return {"x": x.detach().cpu(), "node_scores": ns.cpu(), "dq": qd.grad.cpu(),
+            "dk": kd.grad.cpu(), "dv": vd.grad.cpu()}
+
+
+def _oracle(q, k, v, ei, go, H):
+    return OA.sparse_fwd_bwd(q.float(), k.float(), v.float(), torch.from_numpy(ei), go.float(), H,
+                             dtype=torch.float32)
+
+
+def _check(res, ref, dtype, what):
+    for name in ("x", "node_scores", "dq", "dk", "dv"):
+        assert res[name].shape == ref[name].shape, (what, name, res[name].shape, ref[name].shape)
+        assert_close(res[name].float(), ref[name].float(), dtype, f"{what}:{name}")
+
+
+def _qkv(n_q, n_k, H, d, dtype, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    q = (torch.randn(n_q, H, d, generator=g) * scale).to(dtype)
+    k = torch.randn(n_k, H, d, generator=g).to(dtype)
+    v = torch.randn(n_k, H, d, generator=g).to(dtype)
+    go = torch.randn(n_q, H, d, generator=g).to(dtype)
+    return q, k, v, go
+
+
+CASES = [
+    # n_q, n_k, H, d, E, dtype
+    (200, 200, 8, 8, 2000, torch.float32),
+    (150, 260, 8, 16, 1500, torch.float32),
+    (180, 180, 32, 24, 1200, torch.float32),
+    (100, 130, 4, 32, 900, torch.float32),
+    (90, 90, 2, 64, 700, torch.float32),
+    (120, 120, 3, 8, 800, torch.float32),  # non-power-of-two heads
+    (200, 200, 8, 8, 2000, torch.bfloat16),
+    (180, 240, 32, 24, 1500, torch.bfloat16),
+    (160, 160, 8, 16, 1800, torch.bfloat16),
+    (64, 64, 64, 8, 500, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("n_q,n_k,H,d,E,dtype", CASES)
+def test_sparse_parity_random(n_q, n_k, H, d, E, dtype):
+    _say(f"case random n_q={n_q} n_k={n_k} H={H} d={d} E={E} {dtype}")
+    ei = random_coo(n_q, n_k, E, seed=E + H)
+    q, k, v, go = _qkv(n_q, n_k, H, d, dtype, seed=H * 100 + d, scale=2.0)
+    _check(_run_kernel(q, k, v, ei, go), _oracle(q, k, v, ei, go, H), dtype, "random")
+
+
+@pytest.mark.parametrize("H,d,dtype,chunk", [(8, 8, torch.float32, 16), (32, 24, torch.bfloat16, 8),
+                                             (4, 16, torch.float32, 40)])
+def test_sparse_parity_hub_rows_split(H, d, dtype, chunk):
+    """A query hub and a key hub far longer than the chunk: split items +
+    finalize passes in both orientations."""
+    _say(f"case hub H={H} d={d} {dtype} chunk={chunk}")
+    n = 150
+    ei = hub_coo(n, n, 700, seed=H)
+    q, k, v, go = _qkv(n, n, H, d, dtype, seed=7)
+    res = _run_kernel(q, k, v, ei, go, chunk=chunk)
+    _check(res, _oracle(q, k, v, ei, go, H), dtype, "hub")
+
+
+def test_sparse_golden_fixtures():
+    from pathlib import Path
+
+    for f in sorted((Path(__file__).parent / "golden").glob("attn_sparse_*.npz")):
+        _say(f"case golden {f.name}")
+        z = np.load(f)
+        q, k, v, go = (torch.from_numpy(z[n]) for n in ("q", "k", "v", "go"))
+        res = _run_kernel(q, k, v, z["edge_index"], go)
+        for name in ("x", "node_scores", "dq", "dk", "dv"):
+            assert_close(res[name], torch.from_numpy(z[name]), torch.float32, f"{f.name}:{name}")
+
+
+def test_sparse_clamp_boundary_and_empty():
+    """a = +-5 exactly (inclusive clamp gradient), an empty query row, a row
+    whose only edge is a duplicate pair."""
+    _say("case clamp-boundary")
+    H, d = 1, 16
+    q = torch.zeros(4, H, d)
+    k = torch.zeros(4, H, d)
+    q[0, 0, 0] = 4.0
+    k[1, 0, 0] = 5.0
+    k[2, 0, 0] = -5.0
+    q[3, 0, 1] = 1.0
+    k[3, 0, 1] = 2.0
+    g = torch.Generator().manual_seed(3)
+    v = torch.randn(4, H, d, generator=g)
+    go = torch.randn(4, H, d, generator=g)
+    ei = np.array([[1, 2, 3, 3], [0, 0, 3, 3]], np.int64)  # row 1, 2 empty
+    res = _run_kernel(q, k, v, ei, go)
+    ref = _oracle(q, k, v, ei, go, H)
+    _check(res, ref, torch.float32, "boundary")
+    assert res["dq"][0].abs().sum() > 0
+    assert torch.all(res["x"][1] == 0) and torch.all(res["x"][2] == 0)
+
+
+def test_sparse_no_edges():
+    _say("case no-edges")
+    q, k, v, go = _qkv(10, 10, 2, 8, torch.float32, seed=1)
+    res = _run_kernel(q, k, v, np.zeros((2, 0), np.int64), go)
+    assert torch.all(res["x"] == 0) and res["node_scores"].numel() == 0
+    assert torch.all(res["dq"] == 0) and torch.all(res["dk"] == 0) and torch.all(res["dv"] == 0)
+
+
+@pytest.mark.parametrize("n_q,n_k,E,chunk", [(300, 300, 4000, 64), (120, 500, 3000, 7),
+                                             (1, 1, 5, 1), (50, 20, 0, 8)])
+def test_csr_bit_exact(n_q, n_k, E, chunk):
+    _say(f"case csr n_q={n_q} n_k={n_k} E={E} chunk={chunk}")
+    if E:
+        rng = np.random.default_rng(E)
+        ei = np.stack([rng.integers(0, n_k, E), rng.integers(0, n_q, E)]).astype(np.int64)
+    else:
+        ei = np.zeros((2, 0), np.int64)
+    adj = WindowAdjacency(torch.from_numpy(ei).cuda(), n_q, n_k, chunk)
+    ref = OG.csr_from_coo(ei[0], ei[1], n_q, n_k)
+    got = {n: getattr(adj, n).cpu().numpy() for n in ref}
+    for n in ref:
+        np.testing.assert_array_equal(got[n][: ref[n].shape[0]], ref[n], err_msg=n)
+    for side, rp in (("q", ref["rowptr"]), ("k", ref["t_rowptr"])):
+        items, splits = OG.work_items(rp, chunk)
+        gi = getattr(adj, "items_" + side).cpu().numpy()[: items.shape[0]]
+        gs = getattr(adj, "splits_" + side).cpu().numpy()[: splits.shape[0]]
+        np.testing.assert_array_equal(gi, items, err_msg="items_" + side)
+        np.testing.assert_array_equal(gs, splits, err_msg="splits_" + side)
+        assert adj.info[0 if side == "q" else 3] == items.shape[0]
+    assert adj.dst_end == (int(ei[1].max()) + 1 if E else 0)
+
+
+def test_csr_rejects_out_of_range():
+    _say("case csr-bad-index")
+    ei = torch.tensor([[0, 5], [1, 1]]).cuda()
+    with pytest.raises(IndexError):
+        WindowAdjacency(ei, 3, 3, 8)
+
+
+def test_core_attention_module_drop_in():
+    """The module keeps the reference call signature and output shapes."""
+    _say("case module")
+    H, d, n = 4, 8, 64
+    mod = CoreAttention(H * d, 0.5, H).cuda()
+    ei = random_coo(n, n, 400, seed=2)
+    q, k, v, go = _qkv(n, n, H, d, torch.float32, seed=2)
+    x, score = mod(q[None].cuda(), k[None].cuda(), v[None].cuda(), None,
+                   torch.from_numpy(ei).cuda(), "sparse")
+    assert x.shape == (1, n, H * d)
+    ref = _oracle(q, k, v, ei, go, H)
+    assert_close(x[0].view(n, H, d).cpu(), ref["x"], torch.float32, "module")
+    assert_close(score.cpu(), ref["node_scores"], torch.float32, "module score")
+
+
+# ----------------------------------------------------- full-size windows
+def _sampled_rows_oracle(q, k, v, ei, go, rows, H):
+    """Restatement restricted to the edges of sampled query rows (exact: a
+    query row depends only on its own edges)."""
+    m = np.isin(ei[1], rows)
+    sub = ei[:, m]
+    remap = -np.ones(q.shape[0], np.int64)
+    remap[rows] = np.arange(len(rows))
+    keys, kinv = np.unique(sub[0], return_inverse=True)
+    sub_ei = np.stack([kinv, remap[sub[1]]])
+    qs = q[torch.from_numpy(rows)]
+    ks, vs = k[torch.from_numpy(keys)], v[torch.from_numpy(keys)]
+    gs = go[torch.from_numpy(rows)]
+    # pad queries to the key count (square window as in the reference)
+    return OA.sparse_fwd_bwd(qs.float(), ks.float(), vs.float(), torch.from_numpy(sub_ei),
+                             gs.float(), H, dtype=torch.float32)
+
+
+@pytest.mark.parametrize("name", ["gph_slim", "gt_arxiv", "gph_large", "gt_highdeg"])
+def test_full_size_window_sampled_rows_and_invariants(name):
+    cfg = S.CONFIGS[name]
+    ei, n_k = S.make_window_edges(cfg)
+    _say(f"case full-size {name} E={ei.shape[1]} n_k={n_k}")
+    q, k, v, go = S.make_qkv(cfg, n_k)
+    res = _run_kernel(q, k, v, ei, go)
+    rng = np.random.default_rng(0)
+    deg = np.bincount(ei[1], minlength=cfg.n_q)
+    rows = np.unique(np.concatenate([rng.choice(cfg.n_q, 96, replace=False),
+                                     [int(deg.argmax())]]))
+    ref = _sampled_rows_oracle(q, k, v, ei, go, rows, cfg.n_heads)
+    assert_close(res["x"][rows].float(), ref["x"], cfg.dtype, f"{name}:x rows")
+    assert_close(res["dq"][rows].float(), ref["dq"], cfg.dtype, f"{name}:dq rows")
+    assert_close(res["node_scores"][rows].float(), ref["node_scores"], cfg.dtype, f"{name}:ns")
+    # <dQ, Q> = <dK, K> = sum_e da_e a_e  (a is bilinear in q and k)
+    lhs = (res["dq"].double() * q.double()).sum().item()
+    rhs = (res["dk"].double() * k.double()).sum().item()
+    scale = max(abs(lhs), abs(rhs), 1e-30)
+    assert abs(lhs - rhs) / scale < 10 * TOL[cfg.dtype], (lhs, rhs)
+    # sum_j dV_j = sum_i Z_i/(Z_i+eps) G_i  ~= sum over rows with edges of G_i
+    has = torch.from_numpy(deg > 0)
+    sv = res["dv"].double().sum(0)
+    sg = go.double()[has].sum(0)
+    assert relerr(sv, sg) < max(1e-3, 10 * TOL[cfg.dtype])

@@ -1,0 +1,175 @@
+"""Pins the CPU oracle of the attention core (no GPU).
+
+The restatement in oracle/attention.py is checked against forms that do not
+share its op sequence: a float64 dense masked-matrix formula, hand-derived
+gradients, torch.autograd.gradcheck, closed-form special cases and the
+committed golden fixtures.
+"""
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as OA
+from tests._util import random_coo, relerr
+
+GOLDEN = Path(__file__).parent / "golden"
+
+
+def _inputs(n_q, n_k, H, d, seed, dtype=torch.float64):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(n_q, H, d, generator=g, dtype=dtype)
+    k = torch.randn(n_k, H, d, generator=g, dtype=dtype)
+    v = torch.randn(n_k, H, d, generator=g, dtype=dtype)
+    go = torch.randn(n_q, H, d, generator=g, dtype=dtype)
+    return q, k, v, go
+
+
+@pytest.mark.parametrize("n_q,n_k,H,d,E", [(40, 40, 4, 8, 300), (30, 55, 2, 16, 200),
+                                           (64, 64, 8, 8, 1500)])
+def test_sparse_forward_matches_bruteforce_fp64(n_q, n_k, H, d, E):
+    ei = torch.from_numpy(random_coo(n_q, n_k, E, seed=n_q + E))
+    q, k, v, _ = _inputs(n_q, n_k, H, d, seed=1)
+    qf = torch.zeros(n_k, H, d, dtype=torch.float64)
+    qf[:n_q] = q
+    x, ns = OA.sparse_attention_bias(qf[None], k[None], v[None], ei, H)
+    xb, zb = OA.sparse_bruteforce_fp64(q, k, v, ei)
+    assert relerr(x[:n_q], xb) < 1e-12
+    # node_scores = mean over heads of Z, length max(dst) + 1
+    dst_end = int(ei[1].max()) + 1
+    assert ns.shape == (dst_end,)
+    assert relerr(ns, zb.mean(1)[:dst_end]) < 1e-12
+
+
+def test_sparse_backward_autograd_matches_closed_form():
+    n_q, n_k, H, d = 35, 50, 4, 8
+    ei = torch.from_numpy(random_coo(n_q, n_k, 260, seed=7))
+    q, k, v, go = _inputs(n_q, n_k, H, d, seed=3)
+    # push some scores past the clamp so the mask matters
+    q = q * 3.0
+    res = OA.sparse_fwd_bwd(q, k, v, ei, go, H, dtype=torch.float64)
+    dq, dk, dv = OA.sparse_backward_closed_form(q, k, v, ei, go)
+    assert relerr(res["dq"], dq) < 1e-12
+    assert relerr(res["dk"], dk) < 1e-12
+    assert relerr(res["dv"], dv) < 1e-12
+
+
+def test_sparse_gradcheck_fp64():
+    n, H, d = 9, 2, 4
+    ei = torch.from_numpy(random_coo(n, n, 30, seed=11))
+    q, k, v, _ = _inputs(n, n, H, d, seed=5)
+    q.requires_grad_(True)
+    k.requires_grad_(True)
+    v.requires_grad_(True)
+    f = lambda a, b, c: OA.sparse_attention_bias(a[None], b[None], c[None], ei, H)[0]
+    assert torch.autograd.gradcheck(f, (q, k, v), eps=1e-6, atol=1e-7)
+
+
+def test_sparse_special_cases():
+    H, d = 2, 4
+    n = 5
+    q, k, v, _ = _inputs(n, n, H, d, seed=9)
+    # row 0: single edge 3->0; row 1: empty; row 2: two edges with q = 0 (p = 1 each)
+    ei = torch.tensor([[3, 1, 4], [0, 2, 2]])
+    q2 = q.clone()
+    q2[2] = 0
+    x, ns = OA.sparse_attention_bias(q2[None], k[None], v[None], ei, H)
+    a = (k[3] * q2[0]).sum(-1) / math.sqrt(d)
+    p = torch.exp(a.clamp(-5, 5))
+    torch.testing.assert_close(x[0], v[3] * (p / (p + 1e-6)).unsqueeze(-1), rtol=1e-12, atol=0)
+    assert torch.all(x[1] == 0)
+    torch.testing.assert_close(x[2], (v[1] + v[4]) / (2 + 1e-6), rtol=1e-12, atol=0)
+    assert ns.shape == (3,) and ns[1] == 0 and abs(ns[2].item() - 2.0) < 1e-12
+    # duplicate edges count twice
+    ei_dup = torch.tensor([[3, 3], [0, 0]])
+    xd, nsd = OA.sparse_attention_bias(q[None], k[None], v[None], ei_dup, H)
+    torch.testing.assert_close(nsd[0], 2 * p.mean(), rtol=1e-12, atol=0)
+    torch.testing.assert_close(xd[0], v[3] * (2 * p / (2 * p + 1e-6)).unsqueeze(-1), rtol=1e-12,
+                               atol=0)
+
+
+def test_clamp_boundary_gradient_is_inclusive():
+    """a = +-5 exactly: torch.clamp's backward passes the gradient (mask is
+    lo <= a <= hi); a planted exclusive mask must differ."""
+    H, d = 1, 16  # scale = 4, exact in binary
+    q = torch.zeros(3, H, d, dtype=torch.float64)
+    k = torch.zeros(3, H, d, dtype=torch.float64)
+    v = torch.randn(3, H, d, dtype=torch.float64, generator=torch.Generator().manual_seed(1))
+    q[0, 0, 0] = 4.0
+    k[1, 0, 0] = 5.0  # a = 20/4 = +5
+    k[2, 0, 0] = -5.0  # a = -5
+    ei = torch.tensor([[1, 2], [0, 0]])
+    go = torch.randn(3, H, d, dtype=torch.float64, generator=torch.Generator().manual_seed(2))
+    res = OA.sparse_fwd_bwd(q, k, v, ei, go, H, dtype=torch.float64)
+    dq, dk, dv = OA.sparse_backward_closed_form(q, k, v, ei, go)
+    assert relerr(res["dq"], dq) < 1e-10 and relerr(res["dk"], dk) < 1e-10
+    assert res["dq"].abs().sum() > 0  # gradient flows at the boundary
+    dq_excl, _, _ = OA.sparse_backward_closed_form(q, k, v, ei, go, lo=-5 + 1e-9, hi=5 - 1e-9)
+    assert relerr(dq_excl, res["dq"]) > 1e-3
+
+
+def test_max_subtraction_would_break_parity():
+    """The reference has no max subtraction: eps sits outside a sum that is not
+    rescaled, so a max-subtracted softmax changes low-degree rows."""
+    H, d = 1, 4
+    q = torch.full((1, H, d), -3.0, dtype=torch.float64)
+    k = torch.full((2, H, d), 2.0, dtype=torch.float64)
+    v = torch.randn(2, H, d, dtype=torch.float64)
+    ei = torch.tensor([[0], [0]])
+    qf = torch.zeros(2, H, d, dtype=torch.float64)
+    qf[:1] = q
+    x, _ = OA.sparse_attention_bias(qf[None], k[None], v[None], ei, H)
+    p = math.exp(-5.0)  # clamped
+    assert abs(x[0, 0, 0].item() - v[0, 0, 0].item() * p / (p + 1e-6)) < 1e-12
+    # max-subtracted form gives p' = 1 -> v / (1 + 1e-6): relative change ~1.5e-4
+    alt = v[0, 0, 0].item() / (1 + 1e-6)
+    assert abs(alt - x[0, 0, 0].item()) / abs(x[0, 0, 0].item()) > 1e-4
+
+
+@pytest.mark.parametrize("n_q,n_k,H,d", [(20, 20, 2, 8), (17, 33, 3, 4)])
+def test_full_attention_matches_fp64(n_q, n_k, H, d):
+    q, k, v, go = _inputs(n_q, n_k, H, d, seed=4)
+    x, ns = OA.full_attention(q[None], k[None], v[None])
+    xb, nsb = OA.full_attention_fp64(q, k, v)
+    assert relerr(x[0], xb) < 1e-12 and relerr(ns, nsb) < 1e-12
+    # x = softmax(sqrt(d) q k^T) v: check one row by hand
+    for h in range(H):
+        srow = (q[0, h] * math.sqrt(d)) @ k[:, h].T
+        w = torch.softmax(srow, 0)
+        torch.testing.assert_close(x[0, 0, h], w @ v[:, h], rtol=1e-12, atol=1e-14)
+
+
+def test_full_attention_gradcheck_fp64():
+    q, k, v, _ = _inputs(6, 7, 2, 4, seed=8)
+    for t in (q, k, v):
+        t.requires_grad_(True)
+    f = lambda a, b, c: OA.full_attention(a[None], b[None], c[None])[0]
+    assert torch.autograd.gradcheck(f, (q, k, v), eps=1e-6, atol=1e-7)
+
+
+def test_golden_fixtures_reproduce():
+    files = sorted(GOLDEN.glob("attn_*.npz"))
+    assert files, "golden fixtures missing (tests/golden/make_golden.py)"
+    for f in files:
+        z = np.load(f)
+        kind = str(z["kind"])
+        q, k, v, go = (torch.from_numpy(z[n]) for n in ("q", "k", "v", "go"))
+        if kind == "sparse":
+            ei = torch.from_numpy(z["edge_index"])
+            res = OA.sparse_fwd_bwd(q, k, v, ei, go, q.shape[1], dtype=torch.float32)
+        else:
+            res = OA.full_fwd_bwd(q, k, v, go, dtype=torch.float32)
+        for name in ("x", "node_scores", "dq", "dk", "dv"):
+            assert relerr(res[name], torch.from_numpy(z[name])) < 1e-6, (f.name, name)
+        # and against float64 forms that share none of the op sequence
+        if kind == "sparse":
+            xb, _ = OA.sparse_bruteforce_fp64(q, k, v, ei)
+            dq, dk, dv = OA.sparse_backward_closed_form(q, k, v, ei, go)
+            assert relerr(torch.from_numpy(z["dq"]), dq) < 1e-5
+            assert relerr(torch.from_numpy(z["dk"]), dk) < 1e-5
+            assert relerr(torch.from_numpy(z["dv"]), dv) < 1e-5
+        else:
+            xb, _ = OA.full_attention_fp64(q, k, v)
+        assert relerr(torch.from_numpy(z["x"]), xb) < 1e-5

@@ -1,0 +1,184 @@
+"""Pins the integer window-preparation oracle (no GPU) and checks the torch
+host logic of neutrongt_amd.window against it."""
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import graph as OG
+from tests._util import random_coo
+
+GOLDEN = Path(__file__).parent / "golden"
+
+
+# ------------------------------------------------------------------ CSR
+def _brute_csr(src, dst, n_q):
+    rows = [[] for _ in range(n_q)]
+    for e, (s, d) in enumerate(zip(src.tolist(), dst.tolist())):
+        rows[d].append((s, e))
+    col, perm, rowptr = [], [], [0]
+    for r in rows:
+        for s, e in sorted(r):
+            col.append(s)
+            perm.append(e)
+        rowptr.append(len(col))
+    return np.array(rowptr), np.array(col), np.array(perm)
+
+
+@pytest.mark.parametrize("n_q,n_k,E,seed", [(30, 30, 200, 0), (25, 60, 300, 1), (5, 5, 0, 2),
+                                             (1, 1, 7, 3)])
+def test_csr_matches_bruteforce(n_q, n_k, E, seed):
+    ei = random_coo(n_q, n_k, E, seed=seed) if E else np.zeros((2, 0), np.int64)
+    c = OG.csr_from_coo(ei[0], ei[1], n_q, n_k)
+    rp, col, perm = _brute_csr(ei[0], ei[1], n_q)
+    np.testing.assert_array_equal(c["rowptr"], rp)
+    np.testing.assert_array_equal(c["col"], col)
+    np.testing.assert_array_equal(c["perm"], perm)
+    trp, tcol, tperm = _brute_csr(ei[1], ei[0], n_k)
+    np.testing.assert_array_equal(c["t_rowptr"], trp)
+    np.testing.assert_array_equal(c["t_col"], tcol)
+    np.testing.assert_array_equal(c["t_perm"], tperm)
+    # q2t maps each query-major edge to the same edge id in key-major order
+    if E:
+        np.testing.assert_array_equal(c["t_perm"][c["q2t"]], c["perm"])
+
+
+def test_csr_matches_torch_sparse_on_duplicate_free_input():
+    """Convention of NeutronGT/utils/trans2csr.py:23-35 (sparse_coo -> csr)."""
+    rng = np.random.default_rng(5)
+    n = 40
+    key = np.unique(rng.integers(0, n * n, 300))
+    dst, src = key // n, key % n
+    perm = rng.permutation(key.shape[0])
+    src, dst = src[perm], dst[perm]
+    c = OG.csr_from_coo(src, dst, n, n)
+    t = torch.sparse_coo_tensor(torch.from_numpy(np.stack([dst, src])), torch.ones(len(src)),
+                                (n, n)).coalesce().to_sparse_csr()
+    np.testing.assert_array_equal(c["rowptr"], t.crow_indices().numpy())
+    np.testing.assert_array_equal(c["col"], t.col_indices().numpy())
+
+
+def test_work_items_cover_each_row_once():
+    ei = random_coo(50, 50, 900, seed=3)
+    ei = np.concatenate([ei, np.stack([np.arange(300) % 50, np.zeros(300, np.int64)])], axis=1)
+    c = OG.csr_from_coo(ei[0], ei[1], 50, 50)
+    items, splits = OG.work_items(c["rowptr"], chunk=16)
+    cover = np.zeros(ei.shape[1], np.int64)
+    for r, b, e, p in items.tolist():
+        assert c["rowptr"][r] <= b <= e <= c["rowptr"][r + 1] and e - b <= 16
+        cover[b:e] += 1
+    assert (cover == 1).all()
+    assert len({r for r, *_ in items.tolist()}) == 50
+    n_split = sum(int(n) for _, _, n, _ in splits.tolist())
+    assert (items[:n_split, 3] == np.arange(n_split)).all() and (items[n_split:, 3] == -1).all()
+
+
+# ------------------------------------------------------- related nodes
+def test_merge_related_nodes_hand_derived():
+    """Partition [2, 0, 1] of an 8-node weighted graph.  External neighbours in
+    first-seen order: 6 (w 2), 7 (1), 3 (5), 4 (2+3=5), 5 (2).  Stable ranking by
+    weight: 3, 4, 6, 5, 7 -- 6 precedes 5 (tie, seen first)."""
+    z = np.load(GOLDEN / "related_small.npz")
+    expect = {0: [0, 1, 2], 25: [0, 1, 2, 3], 50: [0, 1, 2, 3, 4], 60: [0, 1, 2, 3, 4, 6],
+              100: [0, 1, 2, 3, 4, 5, 6, 7]}
+    for pct, want in expect.items():
+        out, n_ext = OG.merge_related_nodes(z["xadj"], z["adjncy"], z["eweights"], z["partition"],
+                                            pct)
+        assert out.tolist() == want and n_ext == 5
+        assert z[f"out_{pct}"].tolist() == want
+
+
+def _related_alt(xadj, adjncy, ew, part, pct):
+    """Independent formulation: per external node, weight sum and first
+    traversal index; rank by (-weight, first index)."""
+    inpart = np.zeros(len(xadj) - 1, bool)
+    inpart[part] = True
+    w, first = {}, {}
+    t = 0
+    for u in part:
+        for a in range(xadj[u], xadj[u + 1]):
+            nb = adjncy[a]
+            if not inpart[nb]:
+                w[nb] = w.get(nb, 0) + ew[a]
+                first.setdefault(nb, t)
+            t += 1
+    order = sorted(w, key=lambda x: (-w[x], first[x]))
+    n_sel = len(order) * pct // 100 if pct > 0 else 0
+    return np.array(sorted(set(part.tolist()) | set(order[:n_sel])), np.int64)
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_merge_related_nodes_matches_alternative(seed):
+    rng = np.random.default_rng(seed)
+    n = 200
+    ei = rng.integers(0, n, (2, 1500))
+    val = rng.integers(1, 4, 1500).astype(np.float32) / 1000  # many weight ties
+    xadj, adjncy, ew = OG.adj_weights(ei, val)
+    part = rng.permutation(n)[:40]
+    for pct in (0, 7, 33, 50, 100):
+        out, _ = OG.merge_related_nodes(xadj, adjncy, ew, part, pct)
+        np.testing.assert_array_equal(out, _related_alt(xadj, adjncy, ew, part, pct))
+
+
+# ------------------------------------------------------------- dup / cache
+def test_duplicate_rerange_and_cache_hand_derived():
+    parts = [np.array([5, 1, 9, 3]), np.array([3, 7, 5]), np.array([8, 2])]
+    rer, dups = OG.duplicate_rerange(parts)
+    assert [r.tolist() for r in rer] == [[5, 3, 1, 9], [3, 5, 7], [8, 2]]
+    assert [d.tolist() for d in dups] == [[5, 3], [3, 5], []]
+    cache_ids, idx = OG.dup_cache_metadata(dups)
+    assert cache_ids.tolist() == [3, 5]
+    assert [i.tolist() for i in idx] == [[1, 0], [0, 1], []]
+    feat = np.arange(20, dtype=np.float32).reshape(10, 2)
+    for r, i in zip(rer, idx):
+        np.testing.assert_array_equal(OG.assemble_window_features(feat, cache_ids, i, r), feat[r])
+
+
+def test_host_dup_logic_matches_oracle():
+    from neutrongt_amd import window as W
+
+    rng = np.random.default_rng(2)
+    parts = [rng.choice(100, 30, replace=False) for _ in range(4)]
+    rer, dups = W.duplicate_rerange([torch.from_numpy(p) for p in parts])
+    rer_o, dups_o = OG.duplicate_rerange(parts)
+    for a, b in zip(rer, rer_o):
+        np.testing.assert_array_equal(a.numpy(), b)
+    for a, b in zip(dups, dups_o):
+        np.testing.assert_array_equal(a.numpy(), b)
+    cache_ids, idx = W.dup_cache_metadata(dups)
+    cache_o, idx_o = OG.dup_cache_metadata(dups_o)
+    np.testing.assert_array_equal(cache_ids.numpy(), cache_o)
+    for a, b in zip(idx, idx_o):
+        np.testing.assert_array_equal(a.numpy(), b)
+
+
+# -------------------------------------------------------------- adj weights
+def test_adj_weights_hand_derived():
+    # PPR pairs: (0,1) 0.0026 + (1,0) 0.0010 -> 0.0036*1000 = 3.6 -> 3; (2,0) 0.0004 -> 1 (clamp)
+    ei = np.array([[0, 1, 2], [1, 0, 0]])
+    val = np.array([0.0026, 0.0010, 0.0004], np.float32)
+    xadj, adjncy, ew = OG.adj_weights(ei, val)
+    assert xadj.tolist() == [0, 2, 3, 4]
+    assert adjncy.tolist() == [1, 2, 0, 0]
+    assert ew.tolist() == [3, 1, 3, 1]
+
+
+def test_host_adj_weights_matches_oracle():
+    from neutrongt_amd import window as W
+
+    rng = np.random.default_rng(9)
+    ei = rng.integers(0, 60, (2, 400))
+    val = rng.random(400).astype(np.float32) / 100
+    x, a, w = W.adj_weights(torch.from_numpy(ei), torch.from_numpy(val))
+    xo, ao, wo = OG.adj_weights(ei, val)
+    np.testing.assert_array_equal(x.numpy(), xo)
+    np.testing.assert_array_equal(a.numpy(), ao)
+    np.testing.assert_array_equal(w.numpy(), wo)
+
+
+def test_subgraph_relabel_by_position():
+    ei = np.array([[0, 3, 4, 3, 9], [3, 0, 3, 9, 4]])
+    sub = OG.subgraph_coo(np.array([4, 3, 0]), ei, 10)
+    # kept edges in global order: (0,3), (3,0), (4,3) -> positions (2,1), (1,2), (0,1)
+    assert sub.tolist() == [[2, 1, 0], [1, 2, 1]]
