@@ -1,0 +1,312 @@
+#!/usr/bin/env python3
+"""Window sparse-attention benchmark on one MI355X.
+
+A step is one pass of the attention path over one synthetic window: for the
+default workload (GPH_Large: 32,768-query window + 4 related keys per query,
+H=32, d=24, bf16, 12 layers) the forward of all 12 attention layers followed by
+their backward, each layer with its own q/k/v, through the drop-in autograd
+path (SparseAttentionFunction -> libngt_attn.so).  Inputs and the window CSR
+are resident in HBM before timing starts (the CSR is built once per window and
+reused by every layer and step, as in the training loop).
+
+Prints ONE JSON line: value = masked edges/s (layers x E / step time), the
+roofline of the dominant kernel (algorithmic bytes / its mean launch time,
+from hipEvents recorded around each launch on its own stream) and the CPU
+baseline: the reference's op sequence (the CPU oracle, fp32 torch) timed on a
+bounded sample of the same window.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "masked attn edges/sec fwd+bwd per GPU (GPH_Slim, GPH_Large); % HBM peak"
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+MFMA_BF16_TFLOPS = 2500.0
+
+
+def _log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def _elem_bytes(dtype) -> int:
+    import torch
+
+    return 4 if dtype == torch.float32 else 2
+
+
+def sparse_kernel_bytes(name: str, cfg, n_k: int, E: int, adj) -> float:
+    """Algorithmic (compulsory) HBM bytes of one launch of a sparse kernel:
+    every tensor the kernel must touch, counted once."""
+    b = _elem_bytes(cfg.dtype)
+    H = cfg.n_heads
+    D = H * cfg.head_dim
+    n_q = cfg.n_q
+    iq, ik = adj.struct.n_items_q, adj.struct.n_items_k
+    if name == "sparse_fwd":  # Q, K, V, O, col, items, rinv, node_score
+        return b * D * (2 * n_q + 2 * n_k) + 4 * E + 16 * iq + 4 * n_q * H + 4 * adj.dst_end
+    if name == "sparse_bwd_kv":  # Q, G, K, V, dK, dV, {r, rD}, t_col, items, dS (write)
+        return b * D * (2 * n_q + 4 * n_k) + 8 * n_q * H + 4 * E + 16 * ik + 4 * E * H
+    if name == "sparse_bwd_q":  # K, dQ, col, q2t, dS (read), items
+        return b * D * (n_k + n_q) + 8 * E + 4 * E * H + 16 * iq
+    if name == "sparse_rowstat":  # O, G, rinv, {r, rD}
+        return b * D * 2 * n_q + 12 * n_q * H
+    return float("nan")
+
+
+def path_bytes(cfg, n_k: int, E: int) -> float:
+    """Compulsory bytes of one layer's forward + backward (each tensor once):
+    fwd Q,O,K,V + CSR + Zinv + node_score; bwd Q,O,dO,K,V + {Zinv,D} + both CSRs
+    + perm + dQ,dK,dV."""
+    b = _elem_bytes(cfg.dtype)
+    H = cfg.n_heads
+    D = H * cfg.head_dim
+    n_q = cfg.n_q
+    fwd = b * D * (2 * n_q + 2 * n_k) + 4 * (n_q + 1) + 4 * E + 4 * n_q * H + 4 * n_q
+    bwd = (b * D * (3 * n_q + 2 * n_k) + 8 * n_q * H + 4 * (n_q + 1) + 4 * E + 4 * (n_k + 1)
+           + 8 * E + b * D * (n_q + 2 * n_k))
+    return float(fwd + bwd)
+
+
+def cpu_baseline(cfg, ei_np, n_k, target_s: float = 3.0):
+    """The reference's op sequence (CPU oracle, fp32) on the in-edges of a
+    seeded random subset of the window's query rows, sized so one fwd+bwd takes
+    ~target_s.
+    1 warm-up + median of 3.  Returns the cpu_baseline JSON object."""
+    import numpy as np
+    import torch
+
+    from neutrongt_amd import synthetic as S
+    from oracle import attention as OA
+
+    threads = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit():
+        threads = min(threads, int(env))
+    torch.set_num_threads(max(1, threads))
+    H = cfg.n_heads
+    q, k, v, go = S.make_qkv(cfg, n_k, layer=0, device="cpu")
+    # query rows in a seeded random order, so any prefix has the window's
+    # degree distribution
+    rank = np.empty(cfg.n_q, np.int64)
+    rank[np.random.default_rng(S.SEED).permutation(cfg.n_q)] = np.arange(cfg.n_q)
+    dst_rank = rank[ei_np[1]]
+
+    def sample(n_rows):
+        sub = ei_np[:, dst_rank < n_rows]
+        keys, kinv = np.unique(sub[0], return_inverse=True)
+        rows = np.argsort(rank)[:n_rows]
+        sub_ei = torch.from_numpy(np.stack([kinv, rank[sub[1]]]))
+        rows_t = torch.from_numpy(rows)
+        return (q[rows_t].float(), k[torch.from_numpy(keys)].float(),
+                v[torch.from_numpy(keys)].float(), go[rows_t].float(), sub_ei)
+
+    def run(args):
+        t = time.perf_counter()
+        OA.sparse_fwd_bwd(args[0], args[1], args[2], args[4], args[3], H, dtype=torch.float32)
+        return time.perf_counter() - t
+
+    n_rows = min(cfg.n_q, 64)
+    args = sample(n_rows)
+    t = run(args)
+    while t < target_s / 3 and n_rows < cfg.n_q:
+        n_rows = min(cfg.n_q, int(n_rows * min(8.0, max(1.5, target_s / max(t, 1e-3)))))
+        args = sample(n_rows)
+        t = run(args)  # doubles as the warm-up of the final size
+    times = [run(args) for _ in range(3)]
+    t_med = statistics.median(times)
+    e_s = int(args[4].shape[1])
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": e_s / t_med,
+        "unit": "edges/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"one layer fwd+bwd of the reference op sequence (fp32 torch CPU oracle, "
+                   f"bf16-rounded inputs) on the in-edges of {n_rows} of {cfg.n_q} query rows "
+                   f"(seeded random choice): {e_s} edges, all {H} heads; median of 3 after 1 warm-up, "
+                   f"{t_med:.2f} s each; cpu: {model}"),
+    }
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="gph_large",
+                    help="gph_large (default), gph_slim, gt_arxiv, gt_highdeg, dense_slim")
+    ap.add_argument("--layers", type=int, default=None, help="override the layer count")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="run one 512 MiB device copy first (calibrates HBM byte counters)")
+    args = ap.parse_args(argv)
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this build runs the attention path on a single "
+              "MI355X (window sharding across GPUs is not part of it); use --gpus 1.",
+              file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from neutrongt_amd import _lib, chunk_for_heads
+    from neutrongt_amd import synthetic as S
+    from neutrongt_amd.attention import DenseAttentionFunction, SparseAttentionFunction
+    from neutrongt_amd.csr import WindowAdjacency
+
+    cfg = S.CONFIGS[args.config]
+    layers = args.layers or cfg.layers
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    H, d = cfg.n_heads, cfg.head_dim
+    scale = math.sqrt(d)
+
+    t0 = time.perf_counter()
+    if cfg.dense:
+        ei_np, n_k, E = None, cfg.n_q, cfg.n_q * cfg.n_q
+    else:
+        ei_np, n_k = S.make_window_edges(cfg)
+        E = int(ei_np.shape[1])
+    _log(f"[bench] workload {cfg.name}: n_q={cfg.n_q} n_k={n_k} E={E} H={H} d={d} "
+         f"layers={layers} ({time.perf_counter() - t0:.1f}s)")
+    tensors = []
+    for layer in range(layers):
+        q, k, v, go = S.make_qkv(cfg, n_k, layer=layer, device=dev)
+        tensors.append([t.requires_grad_(True) for t in (q, k, v)] + [go])
+    adj = None
+    csr_ms = None
+    if not cfg.dense:
+        ei = torch.from_numpy(ei_np).to(dev)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        adj = WindowAdjacency(ei, cfg.n_q, n_k, chunk_for_heads(H))
+        csr_ms = (time.perf_counter() - t1) * 1e3
+        _log(f"[bench] csr built in {csr_ms:.2f} ms (incl. one info sync); items q/k "
+             f"{adj.struct.n_items_q}/{adj.struct.n_items_k}, splits q/k "
+             f"{adj.struct.n_splits_q}/{adj.struct.n_splits_k}, max deg q/k "
+             f"{adj.max_deg_q}/{adj.max_deg_k}")
+
+    def step():
+        outs, grads = [], []
+        for q, k, v, go in tensors:
+            q.grad = k.grad = v.grad = None
+            if cfg.dense:
+                x, _ = DenseAttentionFunction.apply(q, k, v, scale, True)
+            else:
+                x, _ = SparseAttentionFunction.apply(q, k, v, adj, scale, -5.0, 5.0, 1e-6)
+            outs.append(x)
+            grads.append(go)
+        torch.autograd.backward(outs, grads)
+
+    if args.calib_copy:
+        src = torch.empty(256 << 20, dtype=torch.int16, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)  # 512 MiB read + 512 MiB written
+        torch.cuda.synchronize()
+        del src, dst
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for i in range(args.steps):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    ms_step = ev0.elapsed_time(ev1) / args.steps
+    value = layers * E / (ms_step * 1e-3)
+    _log(f"[bench] {args.steps} steps: {ms_step:.3f} ms/step, {value / 1e9:.3f} G edges/s")
+
+    # Kernel-level timing (separate pass of the same steps; hipEvents around
+    # every launch of the library, on the launch stream).
+    _lib.timing_enable(True)
+    _lib.timing_summary()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    summ = _lib.timing_summary()
+    _lib.timing_enable(False)
+    kernels = {n: {"launches": c, "avg_us": 1e3 * ms / c, "total_ms_per_step": ms / args.steps}
+               for n, (c, ms) in summ.items()}
+    dom = max(summ, key=lambda n: summ[n][1])
+    dom_avg_s = summ[dom][1] / summ[dom][0] * 1e-3
+    if cfg.dense:
+        flops = 4.0 * cfg.n_q * n_k * d * H  # PV-class: P V (fwd) ~ 2 N^2 d H per GEMM-like op
+        roof = {"bound": "mfma", "achieved": flops / dom_avg_s / 1e12, "peak": MFMA_BF16_TFLOPS,
+                "unit": "TFLOP/s", "frac": flops / dom_avg_s / 1e12 / MFMA_BF16_TFLOPS,
+                "traffic": None, "kernel": dom}
+        path = None
+    else:
+        kb = sparse_kernel_bytes(dom, cfg, n_k, E, adj)
+        ach = kb / dom_avg_s / 1e9
+        roof = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": ach / HBM_PEAK_GBS, "traffic": None, "kernel": dom,
+                "bytes_per_launch": kb, "avg_launch_us": dom_avg_s * 1e6}
+        pb = path_bytes(cfg, n_k, E)
+        path = {"algorithmic_bytes_per_layer": pb,
+                "achieved_GBs": pb * layers / (ms_step * 1e-3) / 1e9,
+                "frac": pb * layers / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    _log(f"[bench] kernels: " + ", ".join(f"{n} {v['avg_us']:.1f}us x{v['launches']}"
+                                          for n, v in sorted(kernels.items())))
+
+    cpu = None
+    if not args.no_cpu and not cfg.dense:
+        _log("[bench] timing the CPU baseline ...")
+        cpu = cpu_baseline(cfg, ei_np, n_k)
+        _log(f"[bench] cpu baseline {cpu['value'] / 1e6:.3f} M edges/s on {cpu['cores']} threads")
+
+    dtype = "f32" if cfg.dtype == torch.float32 else "bf16"
+    out = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "edges/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dtype,
+        "data": "synthetic",
+        "config": {
+            "workload": (f"{cfg.name}: {layers}-layer {'dense' if cfg.dense else 'sparse'} "
+                         f"attention fwd+bwd, window n_q={cfg.n_q}, n_k={n_k}, E={E}, H={H}, "
+                         f"d={d}, {dtype}"),
+            "n_q": cfg.n_q, "n_k": n_k, "edges": E, "heads": H, "head_dim": d,
+            "layers": layers, "csr_build_ms": csr_ms,
+        },
+        "roofline": roof,
+        "path_roofline": path,
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -211,6 +211,16 @@ int ngt_merge_related_nodes(const int32_t* xadj, const int32_t* adjncy, const in
 int ngt_gather_rows(const void* src, int64_t n_src, const int64_t* idx, int64_t n_rows,
                     int64_t row_bytes, void* dst, int32_t* bad, void* stream);
 
+/*
+ * Per-kernel timing (no counterpart in the reference: instrumentation for the
+ * benchmark's roofline figure).  While enabled, every kernel launch of this
+ * library is bracketed by a hipEvent pair on its stream.  ngt_timing_summary
+ * waits for the recorded events and writes one "name count total_ms" line per
+ * kernel into buf (NUL-terminated), then forgets the records.
+ */
+int ngt_timing_enable(int on);
+int ngt_timing_summary(char* buf, size_t len);
+
 #ifdef __cplusplus
 }
 #endif

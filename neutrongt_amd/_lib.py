@@ -89,6 +89,8 @@ SIGNATURES = {
     "ngt_related_workspace_bytes": [_i32, _i32, _psz],
     "ngt_merge_related_nodes": [_vp, _vp, _vp, _i32, _vp, _i32, _i32, _vp, _vp, _vp, _sz, _vp],
     "ngt_gather_rows": [_vp, _i64, _vp, _i64, _i64, _vp, _vp, _vp],
+    "ngt_timing_enable": [_i32],
+    "ngt_timing_summary": [C.c_char_p, _sz],
 }
 _RESTYPES = {"ngt_last_error": C.c_char_p}
 
@@ -132,3 +134,18 @@ def check(rc: int) -> None:
 
 def call(name: str, *args) -> None:
     check(getattr(load(), name)(*args))
+
+
+def timing_enable(on: bool) -> None:
+    check(load().ngt_timing_enable(1 if on else 0))
+
+
+def timing_summary() -> dict:
+    """{kernel name: (launches, total ms)} since the last summary (waits for the GPU)."""
+    buf = C.create_string_buffer(1 << 16)
+    check(load().ngt_timing_summary(buf, len(buf)))
+    out = {}
+    for line in buf.value.decode().splitlines():
+        name, cnt, ms = line.split()
+        out[name] = (int(cnt), float(ms))
+    return out

@@ -17,21 +17,17 @@ import torch
 
 from . import _lib
 
-# Work items cover at most this many "rounds" of a wave's edge slots before a
-# row is split into chunks whose partial sums are added by a finalize pass.
-ITEM_ROUNDS = 32
-
-
-def lanes_for_heads(n_heads: int) -> int:
-    lanes = 1
-    while lanes < n_heads:
-        lanes <<= 1
-    return lanes
+# A work item covers at most this many edges of one row; longer rows are cut
+# into chunks whose partial sums a finalize pass adds.  With the kernels'
+# 8 edge slots per wave (8 heads per pass) a chunk is 32 rounds of a wave.
+CHUNK_EDGES = 256
 
 
 def chunk_for_heads(n_heads: int) -> int:
-    """Edges per work item: (64 / lanes-per-edge) slots x ITEM_ROUNDS."""
-    return max(1, 64 // lanes_for_heads(n_heads)) * ITEM_ROUNDS
+    """Edges per work item (the same for every head count; the argument is
+    kept so callers can pass the layer's head count)."""
+    del n_heads
+    return CHUNK_EDGES
 
 
 class WindowAdjacency:

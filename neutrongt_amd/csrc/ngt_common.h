@@ -105,6 +105,50 @@ __device__ __forceinline__ void store_row(T* __restrict__ p, const float (&in)[D
   }
 }
 
+// Raw 16-byte row chunks: a row slice of DH elements of T is NV = DH*sizeof(T)/16
+// uint4 words (every supported head size is a multiple of 16 bytes).  Loading raw
+// words first and converting at use keeps bf16 rows packed in registers while
+// the loads of several edges are in flight.
+template <typename T, int DH>
+struct RowWords {
+  static_assert((DH * sizeof(T)) % 16 == 0, "row slice must be a multiple of 16 bytes");
+  static constexpr int NV = DH * static_cast<int>(sizeof(T)) / 16;
+  uint4 w[NV];
+};
+
+template <typename T, int DH>
+__device__ __forceinline__ void load_words(const T* __restrict__ p, RowWords<T, DH>& r) {
+  const uint4* v = reinterpret_cast<const uint4*>(p);
+#pragma unroll
+  for (int i = 0; i < RowWords<T, DH>::NV; ++i) r.w[i] = v[i];
+}
+
+template <typename T, int DH>
+__device__ __forceinline__ void zero_words(RowWords<T, DH>& r) {
+#pragma unroll
+  for (int i = 0; i < RowWords<T, DH>::NV; ++i) r.w[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+template <typename T, int DH>
+__device__ __forceinline__ float word_elem(const RowWords<T, DH>& r, int c) {
+  if constexpr (sizeof(T) == 4) {
+    const uint4 w = r.w[c / 4];
+    const uint32_t x = (c % 4 == 0) ? w.x : (c % 4 == 1) ? w.y : (c % 4 == 2) ? w.z : w.w;
+    return __uint_as_float(x);
+  } else {
+    const uint4 w = r.w[c / 8];
+    const int k = (c % 8) / 2;
+    const uint32_t x = (k == 0) ? w.x : (k == 1) ? w.y : (k == 2) ? w.z : w.w;
+    return (c % 2 == 0) ? __uint_as_float(x << 16) : __uint_as_float(x & 0xffff0000u);
+  }
+}
+
+template <typename T, int DH>
+__device__ __forceinline__ void words_to_f32(const RowWords<T, DH>& r, float (&out)[DH]) {
+#pragma unroll
+  for (int c = 0; c < DH; ++c) out[c] = word_elem<T, DH>(r, c);
+}
+
 // fp32 rows (partials, statistics) with 16-byte accesses when DH % 4 == 0.
 template <int DH>
 __device__ __forceinline__ void load_f32(const float* __restrict__ p, float (&out)[DH]) {
@@ -188,6 +232,24 @@ struct dtype_of<bf16_t> {
 
 // Records a message for ngt_last_error() (thread-local) and returns the code.
 int set_error(int code, const char* fmt, ...);
+
+// Optional per-kernel timing (ngt_timing_enable): when on, a KernelTimer
+// placed around a launch records a start/stop hipEvent pair on the launch
+// stream; ngt_timing_summary() aggregates them per kernel name.
+bool timing_enabled();
+void timing_record(const char* name, hipStream_t st, bool start);
+
+struct KernelTimer {
+  const char* name;
+  hipStream_t st;
+  bool on;
+  KernelTimer(const char* n, hipStream_t s) : name(n), st(s), on(timing_enabled()) {
+    if (on) timing_record(name, st, true);
+  }
+  ~KernelTimer() {
+    if (on) timing_record(name, st, false);
+  }
+};
 
 }  // namespace ngt
 

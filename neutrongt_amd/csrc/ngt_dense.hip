@@ -313,10 +313,13 @@ int launch_fwd(const void* q, const void* k, const void* v, int n_q, int n_k, in
   if (n_q == 0) return NGT_OK;
   float* part = ns ? reinterpret_cast<float*>(ws) : nullptr;
   dim3 grid(static_cast<unsigned>(qblocks(n_q)), static_cast<unsigned>(H));
-  hipLaunchKernelGGL((k_dense_fwd<T, DH>), grid, dim3(kBlock), 0, st, static_cast<const T*>(q),
-                     static_cast<const T*>(k), static_cast<const T*>(v), n_q, n_k, H, scale,
-                     static_cast<T*>(out), lse, part);
-  NGT_HIP_CHECK(hipGetLastError());
+  {
+    KernelTimer timer_("dense_fwd", st);
+    hipLaunchKernelGGL((k_dense_fwd<T, DH>), grid, dim3(kBlock), 0, st, static_cast<const T*>(q),
+                       static_cast<const T*>(k), static_cast<const T*>(v), n_q, n_k, H, scale,
+                       static_cast<T*>(out), lse, part);
+    NGT_HIP_CHECK(hipGetLastError());
+  }
   if (ns && n_k > 0) {
     const int rows = static_cast<int>(qblocks(n_q) * H);
     hipLaunchKernelGGL(k_dense_scores, dim3((n_k + kBlock - 1) / kBlock), dim3(kBlock), 0, st,
@@ -334,25 +337,34 @@ int launch_bwd(const void* q, const void* k, const void* v, const void* out, con
   if (n_q > 0) {
     int64_t blocks = (int64_t(n_q) * H + kBlock - 1) / kBlock;
     if (blocks > 65536) blocks = 65536;
-    hipLaunchKernelGGL((k_dense_rowstat<T, DH>), dim3(int(blocks)), dim3(kBlock), 0, st,
-                       static_cast<const T*>(out), static_cast<const T*>(g), n_q, H, dsum);
-    NGT_HIP_CHECK(hipGetLastError());
+    {
+      KernelTimer timer_("dense_rowstat", st);
+      hipLaunchKernelGGL((k_dense_rowstat<T, DH>), dim3(int(blocks)), dim3(kBlock), 0, st,
+                         static_cast<const T*>(out), static_cast<const T*>(g), n_q, H, dsum);
+      NGT_HIP_CHECK(hipGetLastError());
+    }
   }
   if (n_k > 0) {
     dim3 grid(static_cast<unsigned>(qblocks(n_k)), static_cast<unsigned>(H));
-    hipLaunchKernelGGL((k_dense_bwd_kv<T, DH>), grid, dim3(kBlock), 0, st,
-                       static_cast<const T*>(q), static_cast<const T*>(k),
-                       static_cast<const T*>(v), static_cast<const T*>(g), lse, dsum, n_q, n_k, H,
-                       scale, static_cast<T*>(gk), static_cast<T*>(gv));
-    NGT_HIP_CHECK(hipGetLastError());
+    {
+      KernelTimer timer_("dense_bwd_kv", st);
+      hipLaunchKernelGGL((k_dense_bwd_kv<T, DH>), grid, dim3(kBlock), 0, st,
+                         static_cast<const T*>(q), static_cast<const T*>(k),
+                         static_cast<const T*>(v), static_cast<const T*>(g), lse, dsum, n_q, n_k, H,
+                         scale, static_cast<T*>(gk), static_cast<T*>(gv));
+      NGT_HIP_CHECK(hipGetLastError());
+    }
   }
   if (n_q > 0) {
     dim3 grid(static_cast<unsigned>(qblocks(n_q)), static_cast<unsigned>(H));
-    hipLaunchKernelGGL((k_dense_bwd_q<T, DH>), grid, dim3(kBlock), 0, st,
-                       static_cast<const T*>(q), static_cast<const T*>(k),
-                       static_cast<const T*>(v), static_cast<const T*>(g), lse, dsum, n_q, n_k, H,
-                       scale, static_cast<T*>(gq));
-    NGT_HIP_CHECK(hipGetLastError());
+    {
+      KernelTimer timer_("dense_bwd_q", st);
+      hipLaunchKernelGGL((k_dense_bwd_q<T, DH>), grid, dim3(kBlock), 0, st,
+                         static_cast<const T*>(q), static_cast<const T*>(k),
+                         static_cast<const T*>(v), static_cast<const T*>(g), lse, dsum, n_q, n_k, H,
+                         scale, static_cast<T*>(gq));
+      NGT_HIP_CHECK(hipGetLastError());
+    }
   }
   return NGT_OK;
 }

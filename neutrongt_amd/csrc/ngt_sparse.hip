@@ -8,13 +8,20 @@
 //   score_i = sum_e mean_h p_e
 // Because no running maximum is subtracted, partial sums over disjoint edge
 // subsets combine by plain addition; long rows are therefore split into
-// fixed-size chunks whose partials a finalize kernel adds in chunk order.
+// fixed-size chunks whose partials a finalize kernel adds.
 //
-// Wave layout: lane = slot * L + h with L = next_pow2(H) lanes per edge and
-// S = 64 / L edge slots per wave.  Each lane owns one head of one edge and the
-// d-element head slice of every gathered row, so one slot reads a full
-// contiguous K/V row (H*d elements) per edge: coalesced row-segment gathers.
+// Wave layout: lane = slot * L + hl with L = next_pow2(heads per pass) lanes
+// per edge and S = 64 / L edge slots per wave.  Each lane owns one head of one
+// edge and the d-element head slice of every gathered row, so the L lanes of a
+// slot read one contiguous segment of a K/V row per edge.
+//
+// Head groups: a launch can walk the work list once per group of `hg` heads
+// (all items of group 0, then group 1, ...), so that one pass gathers only
+// hg*d-element row slices.  The default is one group of all heads (see
+// heads_per_pass for the measurement behind that choice).
 #include "ngt_common.h"
+
+#include <stdlib.h>
 
 #include <utility>
 
@@ -23,6 +30,7 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kWavesPerBlock = kBlock / kWave;
+constexpr int kColTile = kWave;  // finalize: columns per block
 
 template <int DH>
 __device__ __forceinline__ float dot(const float (&a)[DH], const float (&b)[DH]) {
@@ -39,125 +47,167 @@ __device__ __forceinline__ float clampf(float a, float lo, float hi) {
   return fminf(fmaxf(a, lo), hi);
 }
 
+// Edges per slot whose row loads are issued together before any is used:
+// as many as fit a budget of 16 raw 16-byte words per lane (at most 4).
+constexpr int unroll_for(int words_per_edge) {
+  return words_per_edge >= 16 ? 1 : (16 / words_per_edge >= 4 ? 4 : 16 / words_per_edge);
+}
+
+// Work decomposition shared by the edge kernels.
+struct Lane {
+  int slot;     // edge slot of this lane
+  int S;        // edge slots per wave
+  int h;        // head of this lane
+  bool active;  // lane maps to a real head
+};
+
+__device__ __forceinline__ bool wave_work(int n_items, int n_groups, int hg, int L, int H,
+                                          int& item, Lane& ln) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t gw = int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+  const int64_t group = gw / n_items;
+  if (group >= n_groups) return false;
+  item = static_cast<int>(gw - group * n_items);
+  const int hl = lane & (L - 1);
+  ln.slot = lane / L;
+  ln.S = kWave / L;
+  ln.h = static_cast<int>(group) * hg + hl;
+  ln.active = hl < hg && ln.h < H;
+  return true;
+}
+
 // ------------------------------------------------------------------ forward
 template <typename T, int DH>
 __global__ __launch_bounds__(kBlock) void k_fwd(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
-    const int32_t* __restrict__ col, const int4* __restrict__ items, int32_t n_items, int32_t H,
-    int32_t L, float inv_scale, float lo, float hi, float eps, T* __restrict__ out,
-    float* __restrict__ rinv, float* __restrict__ node_score, int32_t ns_len,
+    const int32_t* __restrict__ col, const int4* __restrict__ items, int32_t n_items,
+    int32_t n_groups, int32_t hg, int32_t H, int32_t L, float inv_scale, float lo, float hi,
+    float eps, T* __restrict__ out, float* __restrict__ rinv, float* __restrict__ zbuf,
     float* __restrict__ part_acc, float* __restrict__ part_z) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int item = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
-  if (item >= n_items) return;
+  int item;
+  Lane ln;
+  if (!wave_work(n_items, n_groups, hg, L, H, item, ln)) return;
   const int4 it = items[item];
-  const int h = lane & (L - 1);
-  const int slot = lane / L;
-  const int S = kWave / L;
-  const bool active = h < H;
   const int64_t row = it.x;
+  const int h = ln.h;
+  const int S = ln.S;
 
   float qr[DH], acc[DH];
   float z = 0.f;
 #pragma unroll
   for (int c = 0; c < DH; ++c) acc[c] = 0.f;
-  if (active) {
+  if (ln.active) {
     load_row<T, DH>(q + (row * H + h) * DH, qr);
   } else {
 #pragma unroll
     for (int c = 0; c < DH; ++c) qr[c] = 0.f;
   }
 
-  int e = it.y + slot;
-  const int end = it.z;
-  for (; e + S < end; e += 2 * S) {
-    const int64_t j0 = col[e];
-    const int64_t j1 = col[e + S];
-    if (active) {
-      float k0[DH], v0[DH], k1[DH], v1[DH];
-      load_row<T, DH>(k + (j0 * H + h) * DH, k0);
-      load_row<T, DH>(k + (j1 * H + h) * DH, k1);
-      load_row<T, DH>(v + (j0 * H + h) * DH, v0);
-      load_row<T, DH>(v + (j1 * H + h) * DH, v1);
-      const float p0 = __expf(clampf(dot<DH>(qr, k0) * inv_scale, lo, hi));
-      const float p1 = __expf(clampf(dot<DH>(qr, k1) * inv_scale, lo, hi));
-      z += p0;
-      z += p1;
-#pragma unroll
-      for (int c = 0; c < DH; ++c) acc[c] = fmaf(p1, v1[c], fmaf(p0, v0[c], acc[c]));
-    }
-  }
-  if (e < end) {
-    const int64_t j0 = col[e];
-    if (active) {
-      float k0[DH], v0[DH];
-      load_row<T, DH>(k + (j0 * H + h) * DH, k0);
-      load_row<T, DH>(v + (j0 * H + h) * DH, v0);
-      const float p0 = __expf(clampf(dot<DH>(qr, k0) * inv_scale, lo, hi));
-      z += p0;
-#pragma unroll
-      for (int c = 0; c < DH; ++c) acc[c] = fmaf(p0, v0[c], acc[c]);
-    }
-  }
-
-  reduce_slots<DH>(acc, z, L);
-  if (it.w < 0) {
-    const float zs = reduce_heads(z, L);  // inactive lanes hold z = 0
-    if (slot == 0 && active) {
-      const float den = z + eps;
-      float o[DH];
-#pragma unroll
-      for (int c = 0; c < DH; ++c) o[c] = acc[c] / den;
-      store_row<T, DH>(out + (row * H + h) * DH, o);
-      rinv[row * H + h] = 1.0f / den;
-    }
-    if (lane == 0 && node_score != nullptr && row < ns_len) node_score[row] = zs / float(H);
-  } else if (slot == 0 && active) {
-    const int64_t p = int64_t(it.w) * H + h;
-    store_f32<DH>(part_acc + p * DH, acc);
-    part_z[p] = z;
-  }
-}
-
-template <typename T, int DH>
-__global__ __launch_bounds__(kBlock) void k_fwd_finalize(
-    const int4* __restrict__ splits, int32_t n_splits, int32_t H, int32_t L, float eps,
-    const float* __restrict__ part_acc, const float* __restrict__ part_z, T* __restrict__ out,
-    float* __restrict__ rinv, float* __restrict__ node_score, int32_t ns_len) {
+  // Column indices of 64 edges are loaded at once (one coalesced access) and
+  // handed to the slots with ds_bpermute; then the K/V rows of U edges per
+  // slot are requested before any of them is used.
+  constexpr int NV = RowWords<T, DH>::NV;
+  constexpr int U = unroll_for(2 * NV);
   const int lane = threadIdx.x & (kWave - 1);
-  const int w = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
-  if (w >= n_splits) return;
-  const int4 sp = splits[w];
-  const int h = lane & (L - 1);
-  const int slot = lane / L;
-  const int S = kWave / L;
-  const bool active = h < H;
-  const int64_t row = sp.x;
-  float acc[DH];
-  float z = 0.f;
+  for (int blk = it.y; blk < it.z; blk += kWave) {
+    const int nb = min(kWave, it.z - blk);
+    const int my_j = lane < nb ? col[blk + lane] : 0;
+    for (int t0 = 0; t0 < nb; t0 += S * U) {
+      RowWords<T, DH> kw[U], vw[U];
+      bool ok[U];
 #pragma unroll
-  for (int c = 0; c < DH; ++c) acc[c] = 0.f;
-  if (active) {
-    for (int p = slot; p < sp.z; p += S) {
-      const int64_t at = int64_t(sp.y + p) * H + h;
-      float t[DH];
-      load_f32<DH>(part_acc + at * DH, t);
+      for (int u = 0; u < U; ++u) {
+        const int t = t0 + u * S + ln.slot;
+        ok[u] = t < nb && ln.active;
+        const int64_t j = __shfl(my_j, t < nb ? t : 0, kWave);
+        if (ok[u]) {
+          load_words<T, DH>(k + (j * H + h) * DH, kw[u]);
+          load_words<T, DH>(v + (j * H + h) * DH, vw[u]);
+        }
+      }
 #pragma unroll
-      for (int c = 0; c < DH; ++c) acc[c] += t[c];
-      z += part_z[at];
+      for (int u = 0; u < U; ++u) {
+        if (ok[u]) {
+          float kk[DH];
+          words_to_f32<T, DH>(kw[u], kk);
+          const float p = __expf(clampf(dot<DH>(qr, kk) * inv_scale, lo, hi));
+          z += p;
+#pragma unroll
+          for (int c = 0; c < DH; ++c) acc[c] = fmaf(p, word_elem<T, DH>(vw[u], c), acc[c]);
+        }
+      }
     }
   }
+
   reduce_slots<DH>(acc, z, L);
-  const float zs = reduce_heads(z, L);
-  if (slot == 0 && active) {
+  if (ln.slot != 0 || !ln.active) return;
+  if (it.w < 0) {
     const float den = z + eps;
     float o[DH];
 #pragma unroll
     for (int c = 0; c < DH; ++c) o[c] = acc[c] / den;
     store_row<T, DH>(out + (row * H + h) * DH, o);
     rinv[row * H + h] = 1.0f / den;
+    zbuf[row * H + h] = z;
+  } else {
+    const int64_t p = int64_t(it.w) * H + h;
+    store_f32<DH>(part_acc + p * DH, acc);
+    part_z[p] = z;
   }
-  if (lane == 0 && node_score != nullptr && row < ns_len) node_score[row] = zs / float(H);
+}
+
+// Split rows: column c of the H*DH output columns of row sp.x is the sum of
+// that column over the row's partial slots.  grid = (n_splits, col tiles);
+// the 4 waves of a block take every 4th part and meet in LDS.
+template <typename T, int DH>
+__global__ __launch_bounds__(kBlock) void k_fwd_finalize(
+    const int4* __restrict__ splits, int32_t H, float eps, const float* __restrict__ part_acc,
+    const float* __restrict__ part_z, T* __restrict__ out, float* __restrict__ rinv,
+    float* __restrict__ zbuf) {
+  __shared__ float red[2][kWavesPerBlock][kColTile];
+  const int4 sp = splits[blockIdx.x];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x >> 6;
+  const int ncols = H * DH;
+  const int col = blockIdx.y * kColTile + lane;
+  const bool ok = col < ncols;
+  const int h = ok ? col / DH : 0;
+  float a = 0.f, z = 0.f;
+  if (ok) {
+    for (int p = wave; p < sp.z; p += kWavesPerBlock) {
+      const int64_t base = int64_t(sp.y + p);
+      a += part_acc[base * ncols + col];
+      z += part_z[base * H + h];
+    }
+  }
+  red[0][wave][lane] = a;
+  red[1][wave][lane] = z;
+  __syncthreads();
+  if (wave != 0 || !ok) return;
+#pragma unroll
+  for (int w = 1; w < kWavesPerBlock; ++w) {
+    a += red[0][w][lane];
+    z += red[1][w][lane];
+  }
+  const int64_t row = sp.x;
+  const float den = z + eps;
+  elem<T>::store(out + row * ncols + col, a / den);
+  if (col % DH == 0) {
+    rinv[row * H + h] = 1.0f / den;
+    zbuf[row * H + h] = z;
+  }
+}
+
+// node_score[i] = sum_h Z[i,h] / H  (the reference: per-edge mean over heads,
+// summed over the row's edges).
+__global__ void k_node_score(const float* __restrict__ zbuf, int32_t ns_len, int32_t H,
+                             float* __restrict__ ns) {
+  for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < ns_len;
+       i += int64_t(gridDim.x) * blockDim.x) {
+    float s = 0.f;
+    for (int h = 0; h < H; ++h) s += zbuf[i * H + h];
+    ns[i] = s / float(H);
+  }
 }
 
 // ----------------------------------------------------------------- backward
@@ -184,18 +234,16 @@ template <typename T, int DH>
 __global__ __launch_bounds__(kBlock) void k_bwd_kv(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const T* __restrict__ g, const float2* __restrict__ rd, const int32_t* __restrict__ t_col,
-    const int4* __restrict__ items, int32_t n_items, int32_t H, int32_t L, float inv_scale,
-    float lo, float hi, T* __restrict__ grad_k, T* __restrict__ grad_v, float* __restrict__ ds,
-    float* __restrict__ part_kv) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int item = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
-  if (item >= n_items) return;
+    const int4* __restrict__ items, int32_t n_items, int32_t n_groups, int32_t hg, int32_t H,
+    int32_t L, float inv_scale, float lo, float hi, T* __restrict__ grad_k,
+    T* __restrict__ grad_v, float* __restrict__ ds, float* __restrict__ part_kv) {
+  int item;
+  Lane ln;
+  if (!wave_work(n_items, n_groups, hg, L, H, item, ln)) return;
   const int4 it = items[item];
-  const int h = lane & (L - 1);
-  const int slot = lane / L;
-  const int S = kWave / L;
-  const bool active = h < H;
   const int64_t row = it.x;
+  const int h = ln.h;
+  const int S = ln.S;
 
   float kr[DH], vr[DH], dk[DH], dv[DH];
 #pragma unroll
@@ -203,7 +251,7 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
     dk[c] = 0.f;
     dv[c] = 0.f;
   }
-  if (active) {
+  if (ln.active) {
     load_row<T, DH>(k + (row * H + h) * DH, kr);
     load_row<T, DH>(v + (row * H + h) * DH, vr);
   } else {
@@ -213,178 +261,198 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
       vr[c] = 0.f;
     }
   }
-  for (int e = it.y + slot; e < it.z; e += S) {
-    const int64_t i = t_col[e];
-    if (active) {
-      float qi[DH], gi[DH];
-      load_row<T, DH>(q + (i * H + h) * DH, qi);
-      load_row<T, DH>(g + (i * H + h) * DH, gi);
-      const float2 r = rd[i * H + h];
-      const float a = dot<DH>(qi, kr) * inv_scale;
-      const float p = __expf(clampf(a, lo, hi));
-      const float dp = r.x * dot<DH>(gi, vr) - r.y;
-      const float da = (a >= lo && a <= hi) ? dp * p : 0.f;
-      const float pr = p * r.x;
+  constexpr int NV = RowWords<T, DH>::NV;
+  constexpr int U = unroll_for(2 * NV);
+  const int lane = threadIdx.x & (kWave - 1);
+  for (int blk = it.y; blk < it.z; blk += kWave) {
+    const int nb = min(kWave, it.z - blk);
+    const int my_i = lane < nb ? t_col[blk + lane] : 0;
+    for (int t0 = 0; t0 < nb; t0 += S * U) {
+      RowWords<T, DH> qw[U], gw[U];
+      float2 r[U];
+      bool ok[U];
 #pragma unroll
-      for (int c = 0; c < DH; ++c) {
-        dk[c] = fmaf(da, qi[c], dk[c]);
-        dv[c] = fmaf(pr, gi[c], dv[c]);
+      for (int u = 0; u < U; ++u) {
+        const int t = t0 + u * S + ln.slot;
+        ok[u] = t < nb && ln.active;
+        const int64_t i = __shfl(my_i, t < nb ? t : 0, kWave);
+        if (ok[u]) {
+          load_words<T, DH>(q + (i * H + h) * DH, qw[u]);
+          load_words<T, DH>(g + (i * H + h) * DH, gw[u]);
+          r[u] = rd[i * H + h];
+        }
       }
-      ds[int64_t(e) * H + h] = da;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (ok[u]) {
+          float qi[DH], gi[DH];
+          words_to_f32<T, DH>(qw[u], qi);
+          words_to_f32<T, DH>(gw[u], gi);
+          const float a = dot<DH>(qi, kr) * inv_scale;
+          const float p = __expf(clampf(a, lo, hi));
+          const float dp = r[u].x * dot<DH>(gi, vr) - r[u].y;
+          const float da = (a >= lo && a <= hi) ? dp * p : 0.f;
+          const float pr = p * r[u].x;
+#pragma unroll
+          for (int c = 0; c < DH; ++c) {
+            dk[c] = fmaf(da, qi[c], dk[c]);
+            dv[c] = fmaf(pr, gi[c], dv[c]);
+          }
+          ds[int64_t(blk + t0 + u * S + ln.slot) * H + h] = da;
+        }
+      }
     }
   }
   reduce_slots2<DH>(dk, dv, L);
-  if (slot == 0 && active) {
+  if (ln.slot != 0 || !ln.active) return;
 #pragma unroll
-    for (int c = 0; c < DH; ++c) dk[c] *= inv_scale;
-    if (it.w < 0) {
-      store_row<T, DH>(grad_k + (row * H + h) * DH, dk);
-      store_row<T, DH>(grad_v + (row * H + h) * DH, dv);
-    } else {
-      float* p = part_kv + (int64_t(it.w) * H + h) * (2 * DH);
-      store_f32<DH>(p, dk);
-      store_f32<DH>(p + DH, dv);
-    }
+  for (int c = 0; c < DH; ++c) dk[c] *= inv_scale;
+  if (it.w < 0) {
+    store_row<T, DH>(grad_k + (row * H + h) * DH, dk);
+    store_row<T, DH>(grad_v + (row * H + h) * DH, dv);
+  } else {
+    float* p = part_kv + (int64_t(it.w) * H + h) * (2 * DH);
+    store_f32<DH>(p, dk);
+    store_f32<DH>(p + DH, dv);
   }
 }
 
+// Split key rows: columns are (h, [dk | dv]) = 2*H*DH per part.
 template <typename T, int DH>
-__global__ __launch_bounds__(kBlock) void k_bwd_kv_finalize(
-    const int4* __restrict__ splits, int32_t n_splits, int32_t H, int32_t L,
-    const float* __restrict__ part_kv, T* __restrict__ grad_k, T* __restrict__ grad_v) {
+__global__ __launch_bounds__(kBlock) void k_bwd_kv_finalize(const int4* __restrict__ splits,
+                                                            int32_t H,
+                                                            const float* __restrict__ part_kv,
+                                                            T* __restrict__ grad_k,
+                                                            T* __restrict__ grad_v) {
+  __shared__ float red[kWavesPerBlock][kColTile];
+  const int4 sp = splits[blockIdx.x];
   const int lane = threadIdx.x & (kWave - 1);
-  const int w = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
-  if (w >= n_splits) return;
-  const int4 sp = splits[w];
-  const int h = lane & (L - 1);
-  const int slot = lane / L;
-  const int S = kWave / L;
-  const bool active = h < H;
-  const int64_t row = sp.x;
-  float dk[DH], dv[DH];
+  const int wave = threadIdx.x >> 6;
+  const int ncols = 2 * H * DH;
+  const int col = blockIdx.y * kColTile + lane;
+  const bool ok = col < ncols;
+  float a = 0.f;
+  if (ok)
+    for (int p = wave; p < sp.z; p += kWavesPerBlock) a += part_kv[int64_t(sp.y + p) * ncols + col];
+  red[wave][lane] = a;
+  __syncthreads();
+  if (wave != 0 || !ok) return;
 #pragma unroll
-  for (int c = 0; c < DH; ++c) {
-    dk[c] = 0.f;
-    dv[c] = 0.f;
-  }
-  if (active) {
-    for (int p = slot; p < sp.z; p += S) {
-      const float* src = part_kv + (int64_t(sp.y + p) * H + h) * (2 * DH);
-      float a[DH], b[DH];
-      load_f32<DH>(src, a);
-      load_f32<DH>(src + DH, b);
-#pragma unroll
-      for (int c = 0; c < DH; ++c) {
-        dk[c] += a[c];
-        dv[c] += b[c];
-      }
-    }
-  }
-  reduce_slots2<DH>(dk, dv, L);
-  if (slot == 0 && active) {
-    store_row<T, DH>(grad_k + (row * H + h) * DH, dk);
-    store_row<T, DH>(grad_v + (row * H + h) * DH, dv);
-  }
+  for (int w = 1; w < kWavesPerBlock; ++w) a += red[w][lane];
+  const int h = col / (2 * DH);
+  const int c = col - h * 2 * DH;
+  const int64_t at = (int64_t(sp.x) * H + h) * DH;
+  if (c < DH)
+    elem<T>::store(grad_k + at + c, a);
+  else
+    elem<T>::store(grad_v + at + (c - DH), a);
 }
 
 // Query-major pass: grad_q[i] = sum_e da_e k_j / scale.
 template <typename T, int DH>
 __global__ __launch_bounds__(kBlock) void k_bwd_q(
     const T* __restrict__ k, const int32_t* __restrict__ col, const int32_t* __restrict__ q2t,
-    const float* __restrict__ ds, const int4* __restrict__ items, int32_t n_items, int32_t H,
-    int32_t L, float inv_scale, T* __restrict__ grad_q, float* __restrict__ part_q) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int item = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
-  if (item >= n_items) return;
+    const float* __restrict__ ds, const int4* __restrict__ items, int32_t n_items,
+    int32_t n_groups, int32_t hg, int32_t H, int32_t L, float inv_scale, T* __restrict__ grad_q,
+    float* __restrict__ part_q) {
+  int item;
+  Lane ln;
+  if (!wave_work(n_items, n_groups, hg, L, H, item, ln)) return;
   const int4 it = items[item];
-  const int h = lane & (L - 1);
-  const int slot = lane / L;
-  const int S = kWave / L;
-  const bool active = h < H;
   const int64_t row = it.x;
+  const int h = ln.h;
+  const int S = ln.S;
   float dq[DH];
 #pragma unroll
   for (int c = 0; c < DH; ++c) dq[c] = 0.f;
-  int e = it.y + slot;
-  for (; e + S < it.z; e += 2 * S) {
-    const int64_t j0 = col[e], j1 = col[e + S];
-    const int64_t t0 = q2t[e], t1 = q2t[e + S];
-    if (active) {
-      float k0[DH], k1[DH];
-      load_row<T, DH>(k + (j0 * H + h) * DH, k0);
-      load_row<T, DH>(k + (j1 * H + h) * DH, k1);
-      const float d0 = ds[t0 * H + h];
-      const float d1 = ds[t1 * H + h];
+  constexpr int NV = RowWords<T, DH>::NV;
+  constexpr int U = unroll_for(NV);
+  const int lane = threadIdx.x & (kWave - 1);
+  for (int blk = it.y; blk < it.z; blk += kWave) {
+    const int nb = min(kWave, it.z - blk);
+    const int my_j = lane < nb ? col[blk + lane] : 0;
+    const int my_t = lane < nb ? q2t[blk + lane] : 0;
+    for (int t0 = 0; t0 < nb; t0 += S * U) {
+      RowWords<T, DH> kw[U];
+      float dsv[U];
+      bool ok[U];
 #pragma unroll
-      for (int c = 0; c < DH; ++c) dq[c] = fmaf(d1, k1[c], fmaf(d0, k0[c], dq[c]));
-    }
-  }
-  if (e < it.z) {
-    const int64_t j0 = col[e];
-    const int64_t t0 = q2t[e];
-    if (active) {
-      float k0[DH];
-      load_row<T, DH>(k + (j0 * H + h) * DH, k0);
-      const float d0 = ds[t0 * H + h];
+      for (int u = 0; u < U; ++u) {
+        const int t = t0 + u * S + ln.slot;
+        ok[u] = t < nb && ln.active;
+        const int src = t < nb ? t : 0;
+        const int64_t j = __shfl(my_j, src, kWave);
+        const int64_t tp = __shfl(my_t, src, kWave);
+        if (ok[u]) {
+          load_words<T, DH>(k + (j * H + h) * DH, kw[u]);
+          dsv[u] = ds[tp * H + h];
+        }
+      }
 #pragma unroll
-      for (int c = 0; c < DH; ++c) dq[c] = fmaf(d0, k0[c], dq[c]);
+      for (int u = 0; u < U; ++u) {
+        if (ok[u]) {
+#pragma unroll
+          for (int c = 0; c < DH; ++c) dq[c] = fmaf(dsv[u], word_elem<T, DH>(kw[u], c), dq[c]);
+        }
+      }
     }
   }
   reduce_slots1<DH>(dq, L);
-  if (slot == 0 && active) {
+  if (ln.slot != 0 || !ln.active) return;
 #pragma unroll
-    for (int c = 0; c < DH; ++c) dq[c] *= inv_scale;
-    if (it.w < 0)
-      store_row<T, DH>(grad_q + (row * H + h) * DH, dq);
-    else
-      store_f32<DH>(part_q + (int64_t(it.w) * H + h) * DH, dq);
-  }
+  for (int c = 0; c < DH; ++c) dq[c] *= inv_scale;
+  if (it.w < 0)
+    store_row<T, DH>(grad_q + (row * H + h) * DH, dq);
+  else
+    store_f32<DH>(part_q + (int64_t(it.w) * H + h) * DH, dq);
 }
 
 template <typename T, int DH>
 __global__ __launch_bounds__(kBlock) void k_bwd_q_finalize(const int4* __restrict__ splits,
-                                                           int32_t n_splits, int32_t H, int32_t L,
+                                                           int32_t H,
                                                            const float* __restrict__ part_q,
                                                            T* __restrict__ grad_q) {
+  __shared__ float red[kWavesPerBlock][kColTile];
+  const int4 sp = splits[blockIdx.x];
   const int lane = threadIdx.x & (kWave - 1);
-  const int w = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
-  if (w >= n_splits) return;
-  const int4 sp = splits[w];
-  const int h = lane & (L - 1);
-  const int slot = lane / L;
-  const int S = kWave / L;
-  const bool active = h < H;
-  const int64_t row = sp.x;
-  float dq[DH];
+  const int wave = threadIdx.x >> 6;
+  const int ncols = H * DH;
+  const int col = blockIdx.y * kColTile + lane;
+  const bool ok = col < ncols;
+  float a = 0.f;
+  if (ok)
+    for (int p = wave; p < sp.z; p += kWavesPerBlock) a += part_q[int64_t(sp.y + p) * ncols + col];
+  red[wave][lane] = a;
+  __syncthreads();
+  if (wave != 0 || !ok) return;
 #pragma unroll
-  for (int c = 0; c < DH; ++c) dq[c] = 0.f;
-  if (active) {
-    for (int p = slot; p < sp.z; p += S) {
-      float a[DH];
-      load_f32<DH>(part_q + (int64_t(sp.y + p) * H + h) * DH, a);
-#pragma unroll
-      for (int c = 0; c < DH; ++c) dq[c] += a[c];
-    }
-  }
-  reduce_slots1<DH>(dq, L);
-  if (slot == 0 && active) store_row<T, DH>(grad_q + (row * H + h) * DH, dq);
+  for (int w = 1; w < kWavesPerBlock; ++w) a += red[w][lane];
+  elem<T>::store(grad_q + int64_t(sp.x) * ncols + col, a);
 }
 
 // ------------------------------------------------------------------ host side
-inline int blocks_for_waves(int64_t waves) {
-  return static_cast<int>((waves + kWavesPerBlock - 1) / kWavesPerBlock);
-}
-
-inline int lanes_for_heads(int H) {
+inline int lanes_for(int n) {
   int L = 1;
-  while (L < H) L <<= 1;
+  while (L < n) L <<= 1;
   return L;
 }
 
 inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
+// Heads per pass.  All heads in one pass (hg = H) measured fastest on the
+// 32,768-query / 105K-key window: splitting H=32 into 8-head groups costs more
+// in per-edge index/loop overhead than the smaller gathered working set saves
+// (bwd_kv 738 -> 1284 us).  NGT_HEAD_GROUP overrides for experiments.
+int heads_per_pass(int H) {
+  if (const char* env = getenv("NGT_HEAD_GROUP")) {
+    const int v = atoi(env);
+    if (v >= 1) return v < H ? v : H;
+  }
+  return H;
+}
+
 struct FwdLayout {
-  size_t part_acc, part_z, total;
+  size_t part_acc, part_z, zbuf, total;
 };
 struct BwdLayout {
   size_t rd, ds, part_kv, part_q, total;
@@ -397,6 +465,8 @@ FwdLayout fwd_layout(const ngt_window_csr* c, int H, int d) {
   off += align256(size_t(c->n_parts_q) * H * d * 4);
   L.part_z = off;
   off += align256(size_t(c->n_parts_q) * H * 4);
+  L.zbuf = off;
+  off += align256(size_t(c->n_q) * H * 4);
   L.total = off;
   return L;
 }
@@ -426,32 +496,48 @@ int check_common(const char* fn, int dtype, const ngt_window_csr* csr, int H, in
     return set_error(NGT_ERR_UNSUPPORTED, "%s: head_dim=%d (supported 8,16,24,32,64)", fn, d);
   if (csr->n_items_q < 0 || csr->n_items_k < 0 || csr->n_items_q > csr->max_items_q ||
       csr->n_items_k > csr->max_items_k || csr->n_splits_q > csr->max_splits_q ||
-      csr->n_splits_k > csr->max_splits_k)
+      csr->n_splits_k > csr->max_splits_k || csr->n_parts_q > csr->n_items_q ||
+      csr->n_parts_k > csr->n_items_k)
     return set_error(NGT_ERR_ARG, "%s: csr counters not filled from info[]", fn);
   return NGT_OK;
+}
+
+inline unsigned blocks_for(int64_t waves) {
+  return static_cast<unsigned>((waves + kWavesPerBlock - 1) / kWavesPerBlock);
 }
 
 template <typename T, int DH>
 int launch_fwd(const ngt_window_csr* c, const void* q, const void* k, const void* v, int H,
                float inv_scale, float lo, float hi, float eps, void* out, float* rinv, float* ns,
                int ns_len, char* ws, hipStream_t st) {
-  const int L = lanes_for_heads(H);
+  const int hg = heads_per_pass(H);
+  const int groups = (H + hg - 1) / hg;
+  const int L = lanes_for(hg);
   const FwdLayout lay = fwd_layout(c, H, DH);
   float* part_acc = reinterpret_cast<float*>(ws + lay.part_acc);
   float* part_z = reinterpret_cast<float*>(ws + lay.part_z);
+  float* zbuf = reinterpret_cast<float*>(ws + lay.zbuf);
   if (c->n_items_q > 0) {
-    hipLaunchKernelGGL((k_fwd<T, DH>), dim3(blocks_for_waves(c->n_items_q)), dim3(kBlock), 0, st,
-                       static_cast<const T*>(q), static_cast<const T*>(k),
+    KernelTimer timer_("sparse_fwd", st);
+    hipLaunchKernelGGL((k_fwd<T, DH>), dim3(blocks_for(int64_t(c->n_items_q) * groups)),
+                       dim3(kBlock), 0, st, static_cast<const T*>(q), static_cast<const T*>(k),
                        static_cast<const T*>(v), c->col, reinterpret_cast<const int4*>(c->items_q),
-                       c->n_items_q, H, L, inv_scale, lo, hi, eps, static_cast<T*>(out), rinv, ns,
-                       ns_len, part_acc, part_z);
+                       c->n_items_q, groups, hg, H, L, inv_scale, lo, hi, eps,
+                       static_cast<T*>(out), rinv, zbuf, part_acc, part_z);
     NGT_HIP_CHECK(hipGetLastError());
   }
   if (c->n_splits_q > 0) {
-    hipLaunchKernelGGL((k_fwd_finalize<T, DH>), dim3(blocks_for_waves(c->n_splits_q)),
-                       dim3(kBlock), 0, st, reinterpret_cast<const int4*>(c->splits_q),
-                       c->n_splits_q, H, L, eps, part_acc, part_z, static_cast<T*>(out), rinv, ns,
-                       ns_len);
+    KernelTimer timer_("sparse_fwd_finalize", st);
+    dim3 grid(c->n_splits_q, (H * DH + kColTile - 1) / kColTile);
+    hipLaunchKernelGGL((k_fwd_finalize<T, DH>), grid, dim3(kBlock), 0, st,
+                       reinterpret_cast<const int4*>(c->splits_q), H, eps, part_acc, part_z,
+                       static_cast<T*>(out), rinv, zbuf);
+    NGT_HIP_CHECK(hipGetLastError());
+  }
+  if (ns && ns_len > 0) {
+    KernelTimer timer_("sparse_node_score", st);
+    hipLaunchKernelGGL(k_node_score, dim3((ns_len + kBlock - 1) / kBlock), dim3(kBlock), 0, st,
+                       zbuf, ns_len, H, ns);
     NGT_HIP_CHECK(hipGetLastError());
   }
   return NGT_OK;
@@ -461,7 +547,9 @@ template <typename T, int DH>
 int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void* v,
                const void* out, const void* g, const float* rinv, int H, float inv_scale,
                float lo, float hi, void* gq, void* gk, void* gv, char* ws, hipStream_t st) {
-  const int L = lanes_for_heads(H);
+  const int hg = heads_per_pass(H);
+  const int groups = (H + hg - 1) / hg;
+  const int L = lanes_for(hg);
   const BwdLayout lay = bwd_layout(c, H, DH);
   float2* rd = reinterpret_cast<float2*>(ws + lay.rd);
   float* ds = reinterpret_cast<float*>(ws + lay.ds);
@@ -471,35 +559,42 @@ int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void
   if (nrh > 0) {
     int64_t blocks = (nrh + kBlock - 1) / kBlock;
     if (blocks > 65536) blocks = 65536;
+    KernelTimer timer_("sparse_rowstat", st);
     hipLaunchKernelGGL((k_rowstat<T, DH>), dim3(int(blocks)), dim3(kBlock), 0, st,
                        static_cast<const T*>(out), static_cast<const T*>(g), rinv, nrh, rd);
     NGT_HIP_CHECK(hipGetLastError());
   }
   if (c->n_items_k > 0) {
-    hipLaunchKernelGGL((k_bwd_kv<T, DH>), dim3(blocks_for_waves(c->n_items_k)), dim3(kBlock), 0,
-                       st, static_cast<const T*>(q), static_cast<const T*>(k),
+    KernelTimer timer_("sparse_bwd_kv", st);
+    hipLaunchKernelGGL((k_bwd_kv<T, DH>), dim3(blocks_for(int64_t(c->n_items_k) * groups)),
+                       dim3(kBlock), 0, st, static_cast<const T*>(q), static_cast<const T*>(k),
                        static_cast<const T*>(v), static_cast<const T*>(g), rd, c->t_col,
-                       reinterpret_cast<const int4*>(c->items_k), c->n_items_k, H, L, inv_scale,
-                       lo, hi, static_cast<T*>(gk), static_cast<T*>(gv), ds, part_kv);
+                       reinterpret_cast<const int4*>(c->items_k), c->n_items_k, groups, hg, H, L,
+                       inv_scale, lo, hi, static_cast<T*>(gk), static_cast<T*>(gv), ds, part_kv);
     NGT_HIP_CHECK(hipGetLastError());
   }
   if (c->n_splits_k > 0) {
-    hipLaunchKernelGGL((k_bwd_kv_finalize<T, DH>), dim3(blocks_for_waves(c->n_splits_k)),
-                       dim3(kBlock), 0, st, reinterpret_cast<const int4*>(c->splits_k),
-                       c->n_splits_k, H, L, part_kv, static_cast<T*>(gk), static_cast<T*>(gv));
+    KernelTimer timer_("sparse_bwd_kv_finalize", st);
+    dim3 grid(c->n_splits_k, (2 * H * DH + kColTile - 1) / kColTile);
+    hipLaunchKernelGGL((k_bwd_kv_finalize<T, DH>), grid, dim3(kBlock), 0, st,
+                       reinterpret_cast<const int4*>(c->splits_k), H, part_kv,
+                       static_cast<T*>(gk), static_cast<T*>(gv));
     NGT_HIP_CHECK(hipGetLastError());
   }
   if (c->n_items_q > 0) {
-    hipLaunchKernelGGL((k_bwd_q<T, DH>), dim3(blocks_for_waves(c->n_items_q)), dim3(kBlock), 0,
-                       st, static_cast<const T*>(k), c->col, c->q2t, ds,
-                       reinterpret_cast<const int4*>(c->items_q), c->n_items_q, H, L, inv_scale,
-                       static_cast<T*>(gq), part_q);
+    KernelTimer timer_("sparse_bwd_q", st);
+    hipLaunchKernelGGL((k_bwd_q<T, DH>), dim3(blocks_for(int64_t(c->n_items_q) * groups)),
+                       dim3(kBlock), 0, st, static_cast<const T*>(k), c->col, c->q2t, ds,
+                       reinterpret_cast<const int4*>(c->items_q), c->n_items_q, groups, hg, H, L,
+                       inv_scale, static_cast<T*>(gq), part_q);
     NGT_HIP_CHECK(hipGetLastError());
   }
   if (c->n_splits_q > 0) {
-    hipLaunchKernelGGL((k_bwd_q_finalize<T, DH>), dim3(blocks_for_waves(c->n_splits_q)),
-                       dim3(kBlock), 0, st, reinterpret_cast<const int4*>(c->splits_q),
-                       c->n_splits_q, H, L, part_q, static_cast<T*>(gq));
+    KernelTimer timer_("sparse_bwd_q_finalize", st);
+    dim3 grid(c->n_splits_q, (H * DH + kColTile - 1) / kColTile);
+    hipLaunchKernelGGL((k_bwd_q_finalize<T, DH>), grid, dim3(kBlock), 0, st,
+                       reinterpret_cast<const int4*>(c->splits_q), H, part_q,
+                       static_cast<T*>(gq));
     NGT_HIP_CHECK(hipGetLastError());
   }
   return NGT_OK;
@@ -507,8 +602,8 @@ int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void
 
 template <template <typename, int> class F, typename... Args>
 int dispatch(int dtype, int d, Args&&... args) {
-#define NGT_CASE(DH)                                                       \
-  case DH:                                                                 \
+#define NGT_CASE(DH)                                                         \
+  case DH:                                                                   \
     return dtype == NGT_F32 ? F<float, DH>::run(std::forward<Args>(args)...) \
                             : F<bf16_t, DH>::run(std::forward<Args>(args)...);
   switch (d) {

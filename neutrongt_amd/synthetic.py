@@ -138,14 +138,18 @@ def make_window_edges(cfg: WindowConfig, seed: int = SEED):
 
 
 def make_qkv(cfg: WindowConfig, n_k: int, seed: int = SEED, layer: int = 0, device="cpu"):
-    """q [N_q,H,d], k/v [N_k,H,d] in cfg.dtype, plus grad_out [N_q,H,d]."""
+    """q [N_q,H,d], k/v [N_k,H,d] in cfg.dtype, plus grad_out [N_q,H,d].
+
+    Random draws are made on the CPU (seeded); the feature projection runs on
+    ``device`` (fp32), so the values depend on that device's matmul rounding."""
     g = torch.Generator(device="cpu").manual_seed(seed * 1000 + layer)
     H, d = cfg.n_heads, cfg.head_dim
     D = H * d
     if cfg.feat_dim > 0:
-        x = torch.randn(n_k, cfg.feat_dim, generator=g)
+        x = torch.randn(n_k, cfg.feat_dim, generator=g).to(device)
         bound = math.sqrt(6.0 / (cfg.feat_dim + D))
-        ws = [(torch.rand(cfg.feat_dim, D, generator=g) * 2 - 1) * bound for _ in range(3)]
+        ws = [((torch.rand(cfg.feat_dim, D, generator=g) * 2 - 1) * bound).to(device)
+              for _ in range(3)]
         q = (x[: cfg.n_q] @ ws[0]).view(cfg.n_q, H, d)
         k = (x @ ws[1]).view(n_k, H, d)
         v = (x @ ws[2]).view(n_k, H, d)

@@ -102,26 +102,38 @@ def test_sparse_golden_fixtures():
 
 
 def test_sparse_clamp_boundary_and_empty():
-    """a = +-5 exactly (inclusive clamp gradient), an empty query row, a row
-    whose only edge is a duplicate pair."""
+    """a = +5 and a = -5 exactly (the clamp gradient is inclusive: it flows),
+    two empty query rows, a duplicated edge.  Scores are chosen so that no row
+    is dominated by one edge (which would make the fp32 backward cancel)."""
     _say("case clamp-boundary")
-    H, d = 1, 16
-    q = torch.zeros(4, H, d)
-    k = torch.zeros(4, H, d)
+    H, d = 1, 16  # scale = 4: every product below is exact
+    n = 7
+    q = torch.zeros(n, H, d)
+    k = torch.zeros(n, H, d)
     q[0, 0, 0] = 4.0
-    k[1, 0, 0] = 5.0
-    k[2, 0, 0] = -5.0
-    q[3, 0, 1] = 1.0
-    k[3, 0, 1] = 2.0
+    k[1, 0, 0] = 5.0  # a(1->0) = +5
+    k[2, 0, 0] = 5.0  # a(2->0) = +5
+    k[2, 0, 5] = 3.0  # orthogonal to q[0] and q[3]: a unchanged, keys not parallel (a
+    k[1, 0, 7] = -2.0  # parallel pair would make dq a pure cancellation of equal scores)
+    q[3, 0, 0] = -4.0  # a(1->3) = a(2->3) = -5
+    q[4, 0, 1] = 1.0
+    k[4, 0, 1] = 2.0
     g = torch.Generator().manual_seed(3)
-    v = torch.randn(4, H, d, generator=g)
-    go = torch.randn(4, H, d, generator=g)
-    ei = np.array([[1, 2, 3, 3], [0, 0, 3, 3]], np.int64)  # row 1, 2 empty
+    v = torch.randn(n, H, d, generator=g)
+    go = torch.randn(n, H, d, generator=g)
+    ei = np.array([[1, 2, 1, 2, 4, 4], [0, 0, 3, 3, 4, 4]], np.int64)  # rows 1, 2 empty
     res = _run_kernel(q, k, v, ei, go)
     ref = _oracle(q, k, v, ei, go, H)
     _check(res, ref, torch.float32, "boundary")
-    assert res["dq"][0].abs().sum() > 0
+    dq, dk, dv = OA.sparse_backward_closed_form(q, k, v, torch.from_numpy(ei), go)
+    assert_close(res["dq"], dq[:n], torch.float32, "dq vs closed form")
+    assert_close(res["dk"], dk, torch.float32, "dk vs closed form")
+    assert res["dq"][0].abs().sum() > 0 and res["dq"][3].abs().sum() > 0  # flows at +-5
     assert torch.all(res["x"][1] == 0) and torch.all(res["x"][2] == 0)
+    # a planted exclusive clamp mask (on the CPU closed form) would zero those rows
+    dq_x, _, _ = OA.sparse_backward_closed_form(q, k, v, torch.from_numpy(ei), go, lo=-5 + 1e-6,
+                                                hi=5 - 1e-6)
+    assert dq_x[0].abs().sum() == 0 and relerr(res["dq"], dq_x) > 0.1
 
 
 def test_sparse_no_edges():
