@@ -77,6 +77,20 @@ def path_bytes(cfg, n_k: int, E: int) -> float:
     return float(fwd + bwd)
 
 
+def measured_traffic(config: str, kernel: str):
+    """HBM bytes per launch of `kernel` measured with rocprofv3 counters
+    (profiles/traffic.json, calibrated against a plain device copy), or None."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f).get(f"{config}:{kernel}")
+    except (OSError, ValueError):
+        return None
+    if not rec:
+        return None
+    return float(rec["read_bytes"]) + float(rec["write_bytes"])
+
+
 def cpu_baseline(cfg, ei_np, n_k, target_s: float = 3.0):
     """The reference's op sequence (CPU oracle, fp32) on the in-edges of a
     seeded random subset of the window's query rows, sized so one fwd+bwd takes
@@ -139,8 +153,9 @@ def cpu_baseline(cfg, ei_np, n_k, target_s: float = 3.0):
         "unit": "edges/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"one layer fwd+bwd of the reference op sequence (fp32 torch CPU oracle, "
-                   f"bf16-rounded inputs) on the in-edges of {n_rows} of {cfg.n_q} query rows "
+        "sample": (f"one layer fwd+bwd of the reference op sequence (torch CPU oracle in fp32 on "
+                   f"{'bf16-rounded' if cfg.dtype != torch.float32 else 'fp32'} inputs) on the "
+                   f"in-edges of {n_rows} of {cfg.n_q} query rows "
                    f"(seeded random choice): {e_s} edges, all {H} heads; median of 3 after 1 warm-up, "
                    f"{t_med:.2f} s each; cpu: {model}"),
     }
@@ -262,8 +277,9 @@ def main(argv=None) -> int:
     else:
         kb = sparse_kernel_bytes(dom, cfg, n_k, E, adj)
         ach = kb / dom_avg_s / 1e9
+        traffic = measured_traffic(cfg.name, dom) if layers == cfg.layers else None
         roof = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": ach / HBM_PEAK_GBS, "traffic": None, "kernel": dom,
+                "frac": ach / HBM_PEAK_GBS, "traffic": traffic, "kernel": dom,
                 "bytes_per_launch": kb, "avg_launch_us": dom_avg_s * 1e6}
         pb = path_bytes(cfg, n_k, E)
         path = {"algorithmic_bytes_per_layer": pb,

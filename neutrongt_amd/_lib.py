@@ -108,7 +108,7 @@ def load(path: str | os.PathLike | None = None):
     with _lock:
         if _lib is not None:
             return _lib
-        p = Path(path) if path else LIB_PATH
+        p = Path(path or os.environ.get("NGT_LIB") or LIB_PATH)
         if not p.exists():
             raise RuntimeError(
                 f"{p.name} is not built ({p}); run `python -m neutrongt_amd.build` "

@@ -40,8 +40,8 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
 
 
-def _compile(src: Path, obj: Path, verbose: bool) -> None:
-    cmd = [_hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+def _compile(src: Path, obj: Path, verbose: bool, extra: list[str]) -> None:
+    cmd = [_hipcc(), *HIPCC_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -54,20 +54,25 @@ def _compile(src: Path, obj: Path, verbose: bool) -> None:
         print(msg, file=sys.stderr)
 
 
-def build_library(verbose: bool = False, jobs: int | None = None) -> Path:
-    """Compiles every ``csrc/*.hip`` and links ``libngt_attn.so``; returns its path."""
-    BUILD.mkdir(exist_ok=True)
+def build_library(verbose: bool = False, jobs: int | None = None, out: Path | None = None,
+                  extra_flags: list[str] | None = None) -> Path:
+    """Compiles every ``csrc/*.hip`` and links ``libngt_attn.so`` (or ``out``);
+    returns its path.  ``extra_flags`` (or NGT_HIPCC_EXTRA) are added to every
+    compile, e.g. -D tuning macros for an experimental build."""
+    extra = list(extra_flags or os.environ.get("NGT_HIPCC_EXTRA", "").split())
+    build_dir = BUILD if not extra else BUILD / ("x" + str(abs(hash(tuple(extra))) % 10**8))
+    build_dir.mkdir(parents=True, exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
-    objs = [BUILD / (s.stem + ".o") for s in sources]
+    objs = [build_dir / (s.stem + ".o") for s in sources]
     jobs = jobs or min(len(sources), max(1, min(8, os.cpu_count() or 1)))
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        futs = [ex.submit(_compile, s, o, verbose) for s, o in zip(sources, objs)]
+        futs = [ex.submit(_compile, s, o, verbose, extra) for s, o in zip(sources, objs)]
         for f in futs:
             f.result()
-    out = PKG / LIB_NAME
-    tmp = PKG / (LIB_NAME + ".tmp")
+    out = Path(out) if out else PKG / LIB_NAME
+    tmp = out.with_name(out.name + ".tmp")
     cmd = [_hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objs), "-o", str(tmp)]
     if verbose:
         print(" ".join(cmd), flush=True)

@@ -48,9 +48,19 @@ __device__ __forceinline__ float clampf(float a, float lo, float hi) {
 }
 
 // Edges per slot whose row loads are issued together before any is used:
-// as many as fit a budget of 16 raw 16-byte words per lane (at most 4).
-constexpr int unroll_for(int words_per_edge) {
-  return words_per_edge >= 16 ? 1 : (16 / words_per_edge >= 4 ? 4 : 16 / words_per_edge);
+// as many as fit a budget of raw 16-byte words per lane (at most 4).
+#ifndef NGT_FWD_WORDS
+#define NGT_FWD_WORDS 16
+#endif
+#ifndef NGT_BWD_KV_WORDS
+#define NGT_BWD_KV_WORDS 16
+#endif
+#ifndef NGT_BWD_Q_WORDS
+#define NGT_BWD_Q_WORDS 16
+#endif
+constexpr int unroll_for(int words_per_edge, int budget) {
+  return words_per_edge >= budget ? 1
+                                  : (budget / words_per_edge >= 4 ? 4 : budget / words_per_edge);
 }
 
 // Work decomposition shared by the edge kernels.
@@ -107,7 +117,7 @@ __global__ __launch_bounds__(kBlock) void k_fwd(
   // handed to the slots with ds_bpermute; then the K/V rows of U edges per
   // slot are requested before any of them is used.
   constexpr int NV = RowWords<T, DH>::NV;
-  constexpr int U = unroll_for(2 * NV);
+  constexpr int U = unroll_for(2 * NV, NGT_FWD_WORDS);
   const int lane = threadIdx.x & (kWave - 1);
   for (int blk = it.y; blk < it.z; blk += kWave) {
     const int nb = min(kWave, it.z - blk);
@@ -262,7 +272,7 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
     }
   }
   constexpr int NV = RowWords<T, DH>::NV;
-  constexpr int U = unroll_for(2 * NV);
+  constexpr int U = unroll_for(2 * NV, NGT_BWD_KV_WORDS);
   const int lane = threadIdx.x & (kWave - 1);
   for (int blk = it.y; blk < it.z; blk += kWave) {
     const int nb = min(kWave, it.z - blk);
@@ -285,18 +295,24 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         if (ok[u]) {
-          float qi[DH], gi[DH];
-          words_to_f32<T, DH>(qw[u], qi);
-          words_to_f32<T, DH>(gw[u], gi);
-          const float a = dot<DH>(qi, kr) * inv_scale;
+          // rows stay packed; elements are unpacked at each use
+          float sa0 = 0.f, sa1 = 0.f, sg0 = 0.f, sg1 = 0.f;
+#pragma unroll
+          for (int c = 0; c < DH; c += 2) {
+            sa0 = fmaf(word_elem<T, DH>(qw[u], c), kr[c], sa0);
+            sa1 = fmaf(word_elem<T, DH>(qw[u], c + 1), kr[c + 1], sa1);
+            sg0 = fmaf(word_elem<T, DH>(gw[u], c), vr[c], sg0);
+            sg1 = fmaf(word_elem<T, DH>(gw[u], c + 1), vr[c + 1], sg1);
+          }
+          const float a = (sa0 + sa1) * inv_scale;
           const float p = __expf(clampf(a, lo, hi));
-          const float dp = r[u].x * dot<DH>(gi, vr) - r[u].y;
+          const float dp = r[u].x * (sg0 + sg1) - r[u].y;
           const float da = (a >= lo && a <= hi) ? dp * p : 0.f;
           const float pr = p * r[u].x;
 #pragma unroll
           for (int c = 0; c < DH; ++c) {
-            dk[c] = fmaf(da, qi[c], dk[c]);
-            dv[c] = fmaf(pr, gi[c], dv[c]);
+            dk[c] = fmaf(da, word_elem<T, DH>(qw[u], c), dk[c]);
+            dv[c] = fmaf(pr, word_elem<T, DH>(gw[u], c), dv[c]);
           }
           ds[int64_t(blk + t0 + u * S + ln.slot) * H + h] = da;
         }
@@ -366,7 +382,7 @@ __global__ __launch_bounds__(kBlock) void k_bwd_q(
 #pragma unroll
   for (int c = 0; c < DH; ++c) dq[c] = 0.f;
   constexpr int NV = RowWords<T, DH>::NV;
-  constexpr int U = unroll_for(NV);
+  constexpr int U = unroll_for(NV, NGT_BWD_Q_WORDS);
   const int lane = threadIdx.x & (kWave - 1);
   for (int blk = it.y; blk < it.z; blk += kWave) {
     const int nb = min(kWave, it.z - blk);
