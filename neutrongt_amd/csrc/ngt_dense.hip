@@ -17,9 +17,20 @@
 #include "ngt_common.h"
 
 #include <math.h>
+#include <stdlib.h>
+
 #include <utility>
 
 namespace ngt {
+
+// Matrix-core kernels (ngt_dense_mfma.hip).
+bool mfma_dense_supported(int d);
+int mfma_dense_fwd(int d, const void* q, const void* k, const void* v, int n_q, int n_k, int H,
+                   float scale, void* out, float* lse, float* part, hipStream_t st);
+int mfma_dense_bwd(int d, const void* q, const void* k, const void* v, const void* g,
+                   const float* lse, const float* dsum, int n_q, int n_k, int H, float scale,
+                   void* gq, void* gk, void* gv, hipStream_t st);
+
 namespace {
 
 constexpr int kBlock = 256;
@@ -412,6 +423,37 @@ int check_args(const char* fn, int dtype, int n_q, int n_k, int H, int d) {
   return NGT_OK;
 }
 
+// The bf16 path runs on the matrix cores (ngt_dense_mfma.hip) for d <= 32;
+// NGT_DENSE_VALU=1 selects the vector-ALU kernels instead (for comparison).
+bool use_mfma(int dtype, int d) {
+  static const bool valu = getenv("NGT_DENSE_VALU") != nullptr;
+  return dtype == NGT_BF16 && mfma_dense_supported(d) && !valu;
+}
+
+int rowstat_bf16(int d, const void* out, const void* g, int n_q, int H, float* dsum,
+                 hipStream_t st) {
+  int64_t blocks = (int64_t(n_q) * H + kBlock - 1) / kBlock;
+  if (blocks > 65536) blocks = 65536;
+  KernelTimer timer_("dense_rowstat", st);
+#define NGT_RS(DH)                                                                              \
+  case DH:                                                                                      \
+    hipLaunchKernelGGL((k_dense_rowstat<bf16_t, DH>), dim3(int(blocks)), dim3(kBlock), 0, st,  \
+                       static_cast<const bf16_t*>(out), static_cast<const bf16_t*>(g), n_q, H,  \
+                       dsum);                                                                   \
+    break;
+  switch (d) {
+    NGT_RS(8)
+    NGT_RS(16)
+    NGT_RS(24)
+    NGT_RS(32)
+    default:
+      return set_error(NGT_ERR_UNSUPPORTED, "rowstat: head_dim %d", d);
+  }
+#undef NGT_RS
+  NGT_HIP_CHECK(hipGetLastError());
+  return NGT_OK;
+}
+
 }  // namespace
 }  // namespace ngt
 
@@ -442,9 +484,19 @@ extern "C" int ngt_dense_fwd(int dtype, const void* q, const void* k, const void
   }
   if (node_score && n_q == 0 && n_k > 0)
     NGT_HIP_CHECK(hipMemsetAsync(node_score, 0, size_t(n_k) * 4, static_cast<hipStream_t>(stream)));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (use_mfma(dtype, head_dim)) {
+    if (n_q == 0) return NGT_OK;
+    float* part = node_score ? static_cast<float*>(workspace) : nullptr;
+    rc = mfma_dense_fwd(head_dim, q, k, v, n_q, n_k, n_heads, scale, out, lse, part, st);
+    if (rc != NGT_OK || !node_score || n_k == 0) return rc;
+    hipLaunchKernelGGL(k_dense_scores, dim3((n_k + kBlock - 1) / kBlock), dim3(kBlock), 0, st,
+                       part, n_heads, n_k, n_heads, node_score);
+    NGT_HIP_CHECK(hipGetLastError());
+    return NGT_OK;
+  }
   return dispatch<FwdOp>(dtype, head_dim, q, k, v, int(n_q), int(n_k), int(n_heads), scale, out,
-                         lse, node_score, static_cast<char*>(workspace),
-                         static_cast<hipStream_t>(stream));
+                         lse, node_score, static_cast<char*>(workspace), st);
 }
 
 extern "C" int ngt_dense_bwd(int dtype, const void* q, const void* k, const void* v,
@@ -462,7 +514,17 @@ extern "C" int ngt_dense_bwd(int dtype, const void* q, const void* k, const void
   if (need > 0 && (!workspace || workspace_bytes < need))
     return set_error(NGT_ERR_WORKSPACE, "ngt_dense_bwd: workspace %zu < %zu", workspace_bytes,
                      need);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (use_mfma(dtype, head_dim)) {
+    float* dsum = static_cast<float*>(workspace);
+    if (n_q > 0) {
+      rc = rowstat_bf16(head_dim, out, grad_out, n_q, n_heads, dsum, st);
+      if (rc != NGT_OK) return rc;
+    }
+    return mfma_dense_bwd(head_dim, q, k, v, grad_out, lse, dsum, n_q, n_k, n_heads, scale,
+                          grad_q, grad_k, grad_v, st);
+  }
   return dispatch<BwdOp>(dtype, head_dim, q, k, v, out, grad_out, lse, int(n_q), int(n_k),
                          int(n_heads), scale, grad_q, grad_k, grad_v,
-                         static_cast<char*>(workspace), static_cast<hipStream_t>(stream));
+                         static_cast<char*>(workspace), st);
 }

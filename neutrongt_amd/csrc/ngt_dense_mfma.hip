@@ -1,0 +1,433 @@
+// Dense full-window attention on the matrix cores (bf16 inputs, fp32
+// accumulation), head_dim d in {8, 16, 24, 32}.
+//
+// Every product runs on v_mfma_f32_32x32x8_bf16: its K = 8 equals the smallest
+// head dim, so the QK^T and dP = G V^T contractions over d have no padding,
+// and the PV-class contractions over keys/queries take 8-row K steps.  Lane
+// layouts of the 32x32x8 instruction (checked on gfx950):
+//   A (32 x 8):  lane l holds A[l % 32][4*(l/32) + i], i < 4
+//   B (8 x 32):  lane l holds B[4*(l/32) + i][l % 32], i < 4
+//   D (32 x 32): lane l holds D[8*(i/4) + 4*(l/32) + i%4][l % 32], i < 16
+// The D rows a lane holds for i = 4j..4j+3 are exactly the B rows it must
+// supply for K step j, so a score tile computed with the contraction index in
+// its rows feeds the next MFMA as B without any data movement.
+//
+// Forward, per (head, 32 queries): S^T = K Q^T (rows = keys, cols = queries),
+// online softmax per query column (in-lane over 16 keys + one lane^32 swap),
+// O^T += V^T P^T with V^T staged in LDS.  Backward: key-major dK/dV (S and dP
+// recomputed as D[q][key], dV += P^T G and dK += dS^T Q with Q/G tiles staged
+// in LDS) and query-major dQ (dQ += dS K with K staged in LDS).  Column scores
+// sum_i |S| come from a separate key-major pass (S tiles again on MFMA).
+#include "ngt_common.h"
+
+#include <math.h>
+
+namespace ngt {
+namespace {
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kBlock = 256;
+constexpr int kWaves = kBlock / kWave;
+constexpr int kT = 32;                  // tile edge (rows/cols of one MFMA)
+constexpr int kRowsPerBlock = kWaves * kT;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ f32x16 mfma(s16x4 a, s16x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+// 4 consecutive bf16 of a row (8-byte aligned: d is a multiple of 8).
+__device__ __forceinline__ s16x4 load4(const bf16_t* p) {
+  const uint2 w = *reinterpret_cast<const uint2*>(p);
+  s16x4 r;
+  r[0] = static_cast<short>(w.x & 0xffffu);
+  r[1] = static_cast<short>(w.x >> 16);
+  r[2] = static_cast<short>(w.y & 0xffffu);
+  r[3] = static_cast<short>(w.y >> 16);
+  return r;
+}
+
+__device__ __forceinline__ s16x4 zero4() {
+  s16x4 r;
+  r[0] = r[1] = r[2] = r[3] = 0;
+  return r;
+}
+
+__device__ __forceinline__ short bf(float f) { return static_cast<short>(f32_to_bf16(f)); }
+__device__ __forceinline__ float fb(short s) { return bf16_to_f32(static_cast<uint16_t>(s)); }
+
+// ------------------------------------------------------------------ forward
+// grid = (ceil(n_q / 128), H); wave w owns queries q0 .. q0+31.
+template <int DH>
+__global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
+                                                   const bf16_t* __restrict__ k,
+                                                   const bf16_t* __restrict__ v, int32_t n_q,
+                                                   int32_t n_k, int32_t H, float scale,
+                                                   bf16_t* __restrict__ out,
+                                                   float* __restrict__ lse) {
+  constexpr int NC = DH / 8;  // K chunks of the QK^T contraction
+  __shared__ short vt[DH][kT + 4];  // V^T tile: [c][key]
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x >> 6;
+  const int half = lane >> 5;
+  const int l32 = lane & 31;
+  const int h = blockIdx.y;
+  const int64_t qi = int64_t(blockIdx.x) * kRowsPerBlock + wave * kT + l32;
+  const bool q_ok = qi < n_q;
+
+  // Q^T as the B operand of S^T = K Q^T: lane holds Q[qi][8j + 4*half .. +4].
+  s16x4 qb[NC];
+#pragma unroll
+  for (int j = 0; j < NC; ++j)
+    qb[j] = q_ok ? load4(q + (qi * H + h) * DH + 8 * j + 4 * half) : zero4();
+
+  const float s2 = scale * kLog2e;  // scores in log2 units
+  float m = -INFINITY, l = 0.f;
+  f32x16 acc = zero16();  // O^T[c][q]: c = 8*(i/4) + 4*half + i%4
+
+  for (int kb = 0; kb < n_k; kb += kT) {
+    __syncthreads();
+    for (int e = threadIdx.x; e < kT * DH; e += kBlock) {
+      const int key = e / DH, c = e - key * DH;
+      vt[c][key] = (kb + key < n_k) ? static_cast<short>(v[(int64_t(kb + key) * H + h) * DH + c].x)
+                                    : short(0);
+    }
+    __syncthreads();
+    // S^T tile: rows = keys kb + (8*(i/4) + 4*half + i%4), cols = this lane's query.
+    const int64_t kr = kb + l32;
+    f32x16 st = zero16();
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      const s16x4 ka = kr < n_k ? load4(k + (kr * H + h) * DH + 8 * j + 4 * half) : zero4();
+      st = mfma(ka, qb[j], st);
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int key = kb + 8 * (i / 4) + 4 * half + (i % 4);
+      st[i] = key < n_k ? st[i] * s2 : -INFINITY;
+      mx = fmaxf(mx, st[i]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    const float m_new = fmaxf(m, mx);
+    const float alpha = exp2f(m - m_new);
+    l *= alpha;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] *= alpha;
+    s16x4 pb[4];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const short pbits = bf(exp2f(st[i] - m_new));
+      pb[i / 4][i % 4] = pbits;
+      l += fb(pbits);
+    }
+    m = m_new;
+    // O^T += V^T P^T, K steps of 8 keys.
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      s16x4 va;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) va[t] = l32 < DH ? vt[l32][8 * j + 4 * half + t] : short(0);
+      acc = mfma(va, pb[j], acc);
+    }
+  }
+  l += __shfl_xor(l, 32, kWave);
+  if (!q_ok) return;
+  const float inv = n_k > 0 ? 1.0f / l : 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int c = 8 * (i / 4) + 4 * half + (i % 4);
+    if (c < DH) out[(qi * H + h) * DH + c].x = f32_to_bf16(acc[i] * inv);
+  }
+  if (half == 0) lse[int64_t(h) * n_q + qi] = n_k > 0 ? (m + __log2f(l)) * kLn2 : -INFINITY;
+}
+
+// Column scores: part[h][j] = sum_i |S[h, i, j]|.  grid = (ceil(n_k/128), H);
+// wave w owns keys k0 .. k0+31; S = Q K^T tiles with rows = queries.
+template <int DH>
+__global__ __launch_bounds__(kBlock) void k_mf_scores(const bf16_t* __restrict__ q,
+                                                      const bf16_t* __restrict__ k, int32_t n_q,
+                                                      int32_t n_k, int32_t H, float scale,
+                                                      float* __restrict__ part) {
+  constexpr int NC = DH / 8;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x >> 6;
+  const int half = lane >> 5;
+  const int l32 = lane & 31;
+  const int h = blockIdx.y;
+  const int64_t kj = int64_t(blockIdx.x) * kRowsPerBlock + wave * kT + l32;
+  const bool k_ok = kj < n_k;
+  s16x4 kbv[NC];  // K^T as B: lane holds K[kj][8j + 4*half .. +4]
+#pragma unroll
+  for (int j = 0; j < NC; ++j)
+    kbv[j] = k_ok ? load4(k + (kj * H + h) * DH + 8 * j + 4 * half) : zero4();
+  float s = 0.f;
+  for (int qb = 0; qb < n_q; qb += kT) {
+    const int64_t qr = qb + l32;
+    f32x16 st = zero16();
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      const s16x4 qa = qr < n_q ? load4(q + (qr * H + h) * DH + 8 * j + 4 * half) : zero4();
+      st = mfma(qa, kbv[j], st);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s += fabsf(st[i]);  // padded query rows are zero
+  }
+  s += __shfl_xor(s, 32, kWave);
+  if (k_ok && half == 0) part[int64_t(h) * n_k + kj] = s * scale;
+}
+
+// ----------------------------------------------------------------- backward
+// Key-major: dK, dV for keys k0 .. k0+31 of one head.  S, dP recomputed as
+// D[q][key]; Q, G tiles of 32 queries staged row-major in LDS (shared by the
+// block's 4 waves, which walk the same query tiles).
+template <int DH>
+__global__ __launch_bounds__(kBlock) void k_mf_bwd_kv(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
+    const bf16_t* __restrict__ g, const float* __restrict__ lse, const float* __restrict__ dsum,
+    int32_t n_q, int32_t n_k, int32_t H, float scale, bf16_t* __restrict__ grad_k,
+    bf16_t* __restrict__ grad_v) {
+  constexpr int NC = DH / 8;
+  __shared__ short qs[kT][DH + 4];
+  __shared__ short gs[kT][DH + 4];
+  __shared__ float ls[kT];
+  __shared__ float dd[kT];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x >> 6;
+  const int half = lane >> 5;
+  const int l32 = lane & 31;
+  const int h = blockIdx.y;
+  const int64_t kj = int64_t(blockIdx.x) * kRowsPerBlock + wave * kT + l32;
+  const bool k_ok = kj < n_k;
+  s16x4 kbv[NC], vbv[NC];  // K^T, V^T as B operands
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    kbv[j] = k_ok ? load4(k + (kj * H + h) * DH + 8 * j + 4 * half) : zero4();
+    vbv[j] = k_ok ? load4(v + (kj * H + h) * DH + 8 * j + 4 * half) : zero4();
+  }
+  const float s2 = scale * kLog2e;
+  f32x16 dk = zero16(), dv = zero16();  // D[key][c]: key = 8*(i/4)+4*half+i%4, c = l32
+  for (int qb = 0; qb < n_q; qb += kT) {
+    __syncthreads();
+    for (int e = threadIdx.x; e < kT * DH; e += kBlock) {
+      const int r = e / DH, c = e - r * DH;
+      const bool ok = qb + r < n_q;
+      const int64_t at = (int64_t(qb + r) * H + h) * DH + c;
+      qs[r][c] = ok ? static_cast<short>(q[at].x) : short(0);
+      gs[r][c] = ok ? static_cast<short>(g[at].x) : short(0);
+    }
+    if (threadIdx.x < kT) {
+      const int r = threadIdx.x;
+      const bool ok = qb + r < n_q;
+      ls[r] = ok ? lse[int64_t(h) * n_q + qb + r] * kLog2e : INFINITY;
+      dd[r] = ok ? dsum[int64_t(h) * n_q + qb + r] : 0.f;
+    }
+    __syncthreads();
+    // S and dP tiles, rows = queries qb + 8*(i/4) + 4*half + i%4, col = this lane's key.
+    f32x16 st = zero16(), dp = zero16();
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      s16x4 qa, ga;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        qa[t] = qs[l32][8 * j + 4 * half + t];
+        ga[t] = gs[l32][8 * j + 4 * half + t];
+      }
+      st = mfma(qa, kbv[j], st);
+      dp = mfma(ga, vbv[j], dp);
+    }
+    s16x4 pa[4], dsa[4];  // P^T and dS^T as A operands: A[key][q-step row]
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = 8 * (i / 4) + 4 * half + (i % 4);
+      const float p = exp2f(st[i] * s2 - ls[r]);  // padded rows: exp2(-inf) = 0
+      pa[i / 4][i % 4] = bf(p);
+      dsa[i / 4][i % 4] = bf(p * (dp[i] - dd[r]));
+    }
+    // dV += P^T G, dK += dS^T Q: K steps of 8 queries; B = G/Q rows from LDS.
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      s16x4 gb, qbv;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        gb[t] = l32 < DH ? gs[8 * j + 4 * half + t][l32] : short(0);
+        qbv[t] = l32 < DH ? qs[8 * j + 4 * half + t][l32] : short(0);
+      }
+      dv = mfma(pa[j], gb, dv);
+      dk = mfma(dsa[j], qbv, dk);
+    }
+  }
+  // D[key][c] -> grad rows; lane holds column c = l32 of 16 key rows.
+  if (l32 >= DH) return;
+  const int64_t k0 = int64_t(blockIdx.x) * kRowsPerBlock + wave * kT;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t key = k0 + 8 * (i / 4) + 4 * half + (i % 4);
+    if (key < n_k) {
+      grad_k[(key * H + h) * DH + l32].x = f32_to_bf16(dk[i] * scale);
+      grad_v[(key * H + h) * DH + l32].x = f32_to_bf16(dv[i]);
+    }
+  }
+}
+
+// Query-major: dQ for queries q0 .. q0+31.  S^T, dP^T as D[key][q]; K, V tiles
+// of 32 keys staged row-major in LDS.
+template <int DH>
+__global__ __launch_bounds__(kBlock) void k_mf_bwd_q(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
+    const bf16_t* __restrict__ g, const float* __restrict__ lse, const float* __restrict__ dsum,
+    int32_t n_q, int32_t n_k, int32_t H, float scale, bf16_t* __restrict__ grad_q) {
+  constexpr int NC = DH / 8;
+  __shared__ short ks[kT][DH + 4];
+  __shared__ short vs[kT][DH + 4];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x >> 6;
+  const int half = lane >> 5;
+  const int l32 = lane & 31;
+  const int h = blockIdx.y;
+  const int64_t qi = int64_t(blockIdx.x) * kRowsPerBlock + wave * kT + l32;
+  const bool q_ok = qi < n_q;
+  s16x4 qbv[NC], gbv[NC];  // Q^T, G^T as B operands
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    qbv[j] = q_ok ? load4(q + (qi * H + h) * DH + 8 * j + 4 * half) : zero4();
+    gbv[j] = q_ok ? load4(g + (qi * H + h) * DH + 8 * j + 4 * half) : zero4();
+  }
+  const float L2 = q_ok ? lse[int64_t(h) * n_q + qi] * kLog2e : INFINITY;
+  const float Dq = q_ok ? dsum[int64_t(h) * n_q + qi] : 0.f;
+  const float s2 = scale * kLog2e;
+  f32x16 dq = zero16();  // D[q][c]: q = 8*(i/4)+4*half+i%4 (tile row), c = l32
+  for (int kb = 0; kb < n_k; kb += kT) {
+    __syncthreads();
+    for (int e = threadIdx.x; e < kT * DH; e += kBlock) {
+      const int r = e / DH, c = e - r * DH;
+      const bool ok = kb + r < n_k;
+      const int64_t at = (int64_t(kb + r) * H + h) * DH + c;
+      ks[r][c] = ok ? static_cast<short>(k[at].x) : short(0);
+      vs[r][c] = ok ? static_cast<short>(v[at].x) : short(0);
+    }
+    __syncthreads();
+    // S^T and dP^T tiles: rows = keys kb + 8*(i/4)+4*half+i%4, col = this lane's query.
+    f32x16 st = zero16(), dp = zero16();
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      s16x4 ka, va;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        ka[t] = ks[l32][8 * j + 4 * half + t];
+        va[t] = vs[l32][8 * j + 4 * half + t];
+      }
+      st = mfma(ka, qbv[j], st);
+      dp = mfma(va, gbv[j], dp);
+    }
+    s16x4 dsa[4];  // dS as A operand: A[q][key step row] from the D[key][q] layout
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int key = kb + 8 * (i / 4) + 4 * half + (i % 4);
+      const float p = key < n_k ? exp2f(st[i] * s2 - L2) : 0.f;
+      dsa[i / 4][i % 4] = bf(p * (dp[i] - Dq));
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      s16x4 kbk;  // B = K rows of this K step: B[key][c = l32]
+#pragma unroll
+      for (int t = 0; t < 4; ++t) kbk[t] = l32 < DH ? ks[8 * j + 4 * half + t][l32] : short(0);
+      dq = mfma(dsa[j], kbk, dq);
+    }
+  }
+  if (l32 >= DH) return;
+  const int64_t q0 = int64_t(blockIdx.x) * kRowsPerBlock + wave * kT;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t qq = q0 + 8 * (i / 4) + 4 * half + (i % 4);
+    if (qq < n_q) grad_q[(qq * H + h) * DH + l32].x = f32_to_bf16(dq[i] * scale);
+  }
+}
+
+}  // namespace
+
+// Launchers used by ngt_dense.hip for bf16 and d in {8, 16, 24, 32}.
+bool mfma_dense_supported(int d) { return d == 8 || d == 16 || d == 24 || d == 32; }
+
+template <int DH>
+static int mf_fwd(const void* q, const void* k, const void* v, int n_q, int n_k, int H,
+                  float scale, void* out, float* lse, float* part, hipStream_t st) {
+  const dim3 grid((n_q + kRowsPerBlock - 1) / kRowsPerBlock, H);
+  {
+    KernelTimer timer_("dense_fwd", st);
+    hipLaunchKernelGGL((k_mf_fwd<DH>), grid, dim3(kBlock), 0, st,
+                       static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
+                       static_cast<const bf16_t*>(v), n_q, n_k, H, scale,
+                       static_cast<bf16_t*>(out), lse);
+    NGT_HIP_CHECK(hipGetLastError());
+  }
+  if (part && n_k > 0) {
+    KernelTimer timer_("dense_scores", st);
+    const dim3 g2((n_k + kRowsPerBlock - 1) / kRowsPerBlock, H);
+    hipLaunchKernelGGL((k_mf_scores<DH>), g2, dim3(kBlock), 0, st,
+                       static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k), n_q, n_k, H,
+                       scale, part);
+    NGT_HIP_CHECK(hipGetLastError());
+  }
+  return NGT_OK;
+}
+
+template <int DH>
+static int mf_bwd(const void* q, const void* k, const void* v, const void* g, const float* lse,
+                  const float* dsum, int n_q, int n_k, int H, float scale, void* gq, void* gk,
+                  void* gv, hipStream_t st) {
+  if (n_k > 0) {
+    KernelTimer timer_("dense_bwd_kv", st);
+    const dim3 grid((n_k + kRowsPerBlock - 1) / kRowsPerBlock, H);
+    hipLaunchKernelGGL((k_mf_bwd_kv<DH>), grid, dim3(kBlock), 0, st,
+                       static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
+                       static_cast<const bf16_t*>(v), static_cast<const bf16_t*>(g), lse, dsum,
+                       n_q, n_k, H, scale, static_cast<bf16_t*>(gk), static_cast<bf16_t*>(gv));
+    NGT_HIP_CHECK(hipGetLastError());
+  }
+  if (n_q > 0) {
+    KernelTimer timer_("dense_bwd_q", st);
+    const dim3 grid((n_q + kRowsPerBlock - 1) / kRowsPerBlock, H);
+    hipLaunchKernelGGL((k_mf_bwd_q<DH>), grid, dim3(kBlock), 0, st,
+                       static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
+                       static_cast<const bf16_t*>(v), static_cast<const bf16_t*>(g), lse, dsum,
+                       n_q, n_k, H, scale, static_cast<bf16_t*>(gq));
+    NGT_HIP_CHECK(hipGetLastError());
+  }
+  return NGT_OK;
+}
+
+int mfma_dense_fwd(int d, const void* q, const void* k, const void* v, int n_q, int n_k, int H,
+                   float scale, void* out, float* lse, float* part, hipStream_t st) {
+  switch (d) {
+    case 8: return mf_fwd<8>(q, k, v, n_q, n_k, H, scale, out, lse, part, st);
+    case 16: return mf_fwd<16>(q, k, v, n_q, n_k, H, scale, out, lse, part, st);
+    case 24: return mf_fwd<24>(q, k, v, n_q, n_k, H, scale, out, lse, part, st);
+    case 32: return mf_fwd<32>(q, k, v, n_q, n_k, H, scale, out, lse, part, st);
+    default: return set_error(NGT_ERR_UNSUPPORTED, "mfma dense: head_dim %d", d);
+  }
+}
+
+int mfma_dense_bwd(int d, const void* q, const void* k, const void* v, const void* g,
+                   const float* lse, const float* dsum, int n_q, int n_k, int H, float scale,
+                   void* gq, void* gk, void* gv, hipStream_t st) {
+  switch (d) {
+    case 8: return mf_bwd<8>(q, k, v, g, lse, dsum, n_q, n_k, H, scale, gq, gk, gv, st);
+    case 16: return mf_bwd<16>(q, k, v, g, lse, dsum, n_q, n_k, H, scale, gq, gk, gv, st);
+    case 24: return mf_bwd<24>(q, k, v, g, lse, dsum, n_q, n_k, H, scale, gq, gk, gv, st);
+    case 32: return mf_bwd<32>(q, k, v, g, lse, dsum, n_q, n_k, H, scale, gq, gk, gv, st);
+    default: return set_error(NGT_ERR_UNSUPPORTED, "mfma dense: head_dim %d", d);
+  }
+}
+
+}  // namespace ngt

@@ -36,7 +36,8 @@ def _qkv(n_q, n_k, H, d, dtype, seed):
     (70, 70, 2, 8, torch.float32), (130, 90, 3, 16, torch.float32), (64, 200, 2, 24, torch.float32),
     (50, 77, 1, 32, torch.float32), (40, 40, 2, 64, torch.float32),
     (100, 100, 8, 8, torch.bfloat16), (96, 150, 4, 16, torch.bfloat16),
-    (60, 61, 2, 24, torch.bfloat16), (33, 47, 2, 64, torch.bfloat16)])
+    (60, 61, 2, 24, torch.bfloat16), (70, 45, 3, 32, torch.bfloat16),
+    (33, 47, 2, 64, torch.bfloat16), (1, 1, 1, 8, torch.bfloat16), (130, 33, 2, 8, torch.bfloat16)])
 def test_dense_parity(n_q, n_k, H, d, dtype):
     _say(f"case dense n_q={n_q} n_k={n_k} H={H} d={d} {dtype}")
     q, k, v, go = _qkv(n_q, n_k, H, d, dtype, seed=n_q + d)
