@@ -31,6 +31,15 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   return static_cast<uint16_t>(u >> 16);
 }
 
+// Two floats -> packed bf16 pair with the hardware round-to-nearest-even
+// conversion (v_cvt_pk_bf16_f32); low half = a.
+typedef float ngt_f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 ngt_bf16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
+  const ngt_f32x2 v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, ngt_bf16x2));
+}
+
 template <typename T>
 struct elem;
 template <>
@@ -92,10 +101,10 @@ __device__ __forceinline__ void store_row(T* __restrict__ p, const float (&in)[D
         w.z = __float_as_uint(in[4 * i + 2]);
         w.w = __float_as_uint(in[4 * i + 3]);
       } else {
-        w.x = uint32_t(f32_to_bf16(in[8 * i + 0])) | (uint32_t(f32_to_bf16(in[8 * i + 1])) << 16);
-        w.y = uint32_t(f32_to_bf16(in[8 * i + 2])) | (uint32_t(f32_to_bf16(in[8 * i + 3])) << 16);
-        w.z = uint32_t(f32_to_bf16(in[8 * i + 4])) | (uint32_t(f32_to_bf16(in[8 * i + 5])) << 16);
-        w.w = uint32_t(f32_to_bf16(in[8 * i + 6])) | (uint32_t(f32_to_bf16(in[8 * i + 7])) << 16);
+        w.x = pack2_bf16(in[8 * i + 0], in[8 * i + 1]);
+        w.y = pack2_bf16(in[8 * i + 2], in[8 * i + 3]);
+        w.z = pack2_bf16(in[8 * i + 4], in[8 * i + 5]);
+        w.w = pack2_bf16(in[8 * i + 6], in[8 * i + 7]);
       }
       v[i] = w;
     }

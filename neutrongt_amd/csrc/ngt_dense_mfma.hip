@@ -63,8 +63,83 @@ __device__ __forceinline__ s16x4 zero4() {
   return r;
 }
 
-__device__ __forceinline__ short bf(float f) { return static_cast<short>(f32_to_bf16(f)); }
-__device__ __forceinline__ float fb(short s) { return bf16_to_f32(static_cast<uint16_t>(s)); }
+// Four floats -> MFMA operand of packed bf16 (hardware RNE conversion).
+__device__ __forceinline__ s16x4 pack4(float a, float b, float c, float d) {
+  const uint2 w = make_uint2(pack2_bf16(a, b), pack2_bf16(c, d));
+  return __builtin_bit_cast(s16x4, w);
+}
+
+__device__ __forceinline__ float sum4(s16x4 x) {
+  return (bf16_to_f32(static_cast<uint16_t>(x[0])) + bf16_to_f32(static_cast<uint16_t>(x[1]))) +
+         (bf16_to_f32(static_cast<uint16_t>(x[2])) + bf16_to_f32(static_cast<uint16_t>(x[3])));
+}
+
+__device__ __forceinline__ s16x4 ones4() {
+  s16x4 r;
+  r[0] = r[1] = r[2] = r[3] = static_cast<short>(0x3f80);  // bf16 1.0
+  return r;
+}
+
+// ------------------------------------------------------------- LDS staging
+// A block stages kSB rows (keys or queries) of one head at a time: each thread
+// prefetches its 16-byte pieces of the next stage into registers while the
+// block computes on the current one, then writes them to LDS either row-major
+// ([row][c], read as A operands) or transposed ([c][row], read as B operands).
+constexpr int kSB = 128;
+
+template <int DH>
+struct Stage {
+  static constexpr int VPR = DH / 8;                          // 16-byte pieces per row
+  static constexpr int NV = (kSB * VPR + kBlock - 1) / kBlock;  // pieces per thread
+  uint4 w[NV];
+
+  __device__ __forceinline__ void load(const bf16_t* __restrict__ base, int64_t row0, int n_rows,
+                                       int H, int h) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int e = threadIdx.x + i * kBlock;
+      const int r = e / VPR, cv = e - r * VPR;
+      w[i] = make_uint4(0u, 0u, 0u, 0u);
+      if (e < kSB * VPR && row0 + r < n_rows)
+        w[i] = *reinterpret_cast<const uint4*>(base + ((row0 + r) * H + h) * DH + 8 * cv);
+    }
+  }
+  __device__ __forceinline__ void store_rows(short (*lds)[DH + 8]) const {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int e = threadIdx.x + i * kBlock;
+      if (e < kSB * VPR) {
+        const int r = e / VPR, cv = e - r * VPR;
+        *reinterpret_cast<uint4*>(&lds[r][8 * cv]) = w[i];
+      }
+    }
+  }
+  __device__ __forceinline__ void store_trans(short (*lds)[kSB + 8]) const {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int e = threadIdx.x + i * kBlock;
+      if (e < kSB * VPR) {
+        const int r = e / VPR, cv = e - r * VPR;
+        const uint32_t u[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          lds[8 * cv + 2 * t][r] = static_cast<short>(u[t] & 0xffffu);
+          lds[8 * cv + 2 * t + 1][r] = static_cast<short>(u[t] >> 16);
+        }
+      }
+    }
+  }
+};
+
+__device__ __forceinline__ s16x4 lds4(const short* p) {
+  const uint2 w = *reinterpret_cast<const uint2*>(p);
+  s16x4 r;
+  r[0] = static_cast<short>(w.x & 0xffffu);
+  r[1] = static_cast<short>(w.x >> 16);
+  r[2] = static_cast<short>(w.y & 0xffffu);
+  r[3] = static_cast<short>(w.y >> 16);
+  return r;
+}
 
 // ------------------------------------------------------------------ forward
 // grid = (ceil(n_q / 128), H); wave w owns queries q0 .. q0+31.
@@ -76,7 +151,8 @@ __global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
                                                    bf16_t* __restrict__ out,
                                                    float* __restrict__ lse) {
   constexpr int NC = DH / 8;  // K chunks of the QK^T contraction
-  __shared__ short vt[DH][kT + 4];  // V^T tile: [c][key]
+  __shared__ __align__(16) short ks[kSB][DH + 8];  // K rows
+  __shared__ __align__(16) short vt[DH][kSB + 8];  // V^T: [c][key]
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
   const int half = lane >> 5;
@@ -95,53 +171,69 @@ __global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
   float m = -INFINITY, l = 0.f;
   f32x16 acc = zero16();  // O^T[c][q]: c = 8*(i/4) + 4*half + i%4
 
-  for (int kb = 0; kb < n_k; kb += kT) {
+  Stage<DH> pk, pv;
+  pk.load(k, 0, n_k, H, h);
+  pv.load(v, 0, n_k, H, h);
+  for (int kb = 0; kb < n_k; kb += kSB) {
     __syncthreads();
-    for (int e = threadIdx.x; e < kT * DH; e += kBlock) {
-      const int key = e / DH, c = e - key * DH;
-      vt[c][key] = (kb + key < n_k) ? static_cast<short>(v[(int64_t(kb + key) * H + h) * DH + c].x)
-                                    : short(0);
-    }
+    pk.store_rows(ks);
+    pv.store_trans(vt);
     __syncthreads();
-    // S^T tile: rows = keys kb + (8*(i/4) + 4*half + i%4), cols = this lane's query.
-    const int64_t kr = kb + l32;
-    f32x16 st = zero16();
-#pragma unroll
-    for (int j = 0; j < NC; ++j) {
-      const s16x4 ka = kr < n_k ? load4(k + (kr * H + h) * DH + 8 * j + 4 * half) : zero4();
-      st = mfma(ka, qb[j], st);
+    if (kb + kSB < n_k) {
+      pk.load(k, kb + kSB, n_k, H, h);
+      pv.load(v, kb + kSB, n_k, H, h);
     }
-    float mx = -INFINITY;
+    for (int sub = 0; sub < kSB / kT && kb + sub * kT < n_k; ++sub) {
+      const int r0 = sub * kT;
+      // S^T tile: rows = keys kb + r0 + (8*(i/4) + 4*half + i%4), col = this lane's query.
+      f32x16 st = zero16();
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int key = kb + 8 * (i / 4) + 4 * half + (i % 4);
-      st[i] = key < n_k ? st[i] * s2 : -INFINITY;
-      mx = fmaxf(mx, st[i]);
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-    const float m_new = fmaxf(m, mx);
-    const float alpha = exp2f(m - m_new);
-    l *= alpha;
+      for (int j = 0; j < NC; ++j) st = mfma(lds4(&ks[r0 + l32][8 * j + 4 * half]), qb[j], st);
+      float mx = -INFINITY;
+      if (kb + r0 + kT <= n_k) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) acc[i] *= alpha;
-    s16x4 pb[4];
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, st[i]);
+      } else {  // tail tile: keys past n_k drop out
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const short pbits = bf(exp2f(st[i] - m_new));
-      pb[i / 4][i % 4] = pbits;
-      l += fb(pbits);
-    }
-    m = m_new;
-    // O^T += V^T P^T, K steps of 8 keys.
+        for (int i = 0; i < 16; ++i) {
+          if (kb + r0 + 8 * (i / 4) + 4 * half + (i % 4) >= n_k) st[i] = -INFINITY;
+          mx = fmaxf(mx, st[i]);
+        }
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+      const float m_new = fmaxf(m, mx * s2);  // scale > 0: max commutes with scaling
+      const float alpha = exp2f(m - m_new);
+      if (__any(alpha != 1.f)) {
+        l *= alpha;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      s16x4 va;
+        for (int i = 0; i < 16; ++i) acc[i] *= alpha;
+      }
+      m = m_new;
+      s16x4 pb[4];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) va[t] = l32 < DH ? vt[l32][8 * j + 4 * half + t] : short(0);
-      acc = mfma(va, pb[j], acc);
+      for (int j = 0; j < 4; ++j)
+        pb[j] = pack4(exp2f(fmaf(st[4 * j], s2, -m_new)), exp2f(fmaf(st[4 * j + 1], s2, -m_new)),
+                      exp2f(fmaf(st[4 * j + 2], s2, -m_new)), exp2f(fmaf(st[4 * j + 3], s2, -m_new)));
+      if constexpr (DH == 32) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) l += sum4(pb[j]);
+      }
+      // O^T += V^T P^T, K steps of 8 keys.  For d < 32 row c = d of V^T is all
+      // ones, so O^T row d accumulates the row sum of the (rounded) P.
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const s16x4 va = l32 < DH ? lds4(&vt[l32][r0 + 8 * j + 4 * half])
+                                  : (l32 == DH ? ones4() : zero4());
+        acc = mfma(va, pb[j], acc);
+      }
     }
   }
-  l += __shfl_xor(l, 32, kWave);
+  if constexpr (DH < 32) {
+    // O^T row d sits in acc[d/2] of the half-0 lanes (d is a multiple of 8).
+    l = __shfl(acc[DH / 2], l32, kWave);
+  } else {
+    l += __shfl_xor(l, 32, kWave);
+  }
   if (!q_ok) return;
   const float inv = n_k > 0 ? 1.0f / l : 0.f;
 #pragma unroll
@@ -189,8 +281,8 @@ __global__ __launch_bounds__(kBlock) void k_mf_scores(const bf16_t* __restrict__
 
 // ----------------------------------------------------------------- backward
 // Key-major: dK, dV for keys k0 .. k0+31 of one head.  S, dP recomputed as
-// D[q][key]; Q, G tiles of 32 queries staged row-major in LDS (shared by the
-// block's 4 waves, which walk the same query tiles).
+// D[q][key]; Q and G stages of 128 queries in LDS, row-major (A operands of S
+// and dP) and transposed (B operands of dV += P^T G and dK += dS^T Q).
 template <int DH>
 __global__ __launch_bounds__(kBlock) void k_mf_bwd_kv(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
@@ -198,10 +290,12 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_kv(
     int32_t n_q, int32_t n_k, int32_t H, float scale, bf16_t* __restrict__ grad_k,
     bf16_t* __restrict__ grad_v) {
   constexpr int NC = DH / 8;
-  __shared__ short qs[kT][DH + 4];
-  __shared__ short gs[kT][DH + 4];
-  __shared__ float ls[kT];
-  __shared__ float dd[kT];
+  __shared__ __align__(16) short qs[kSB][DH + 8];
+  __shared__ __align__(16) short gs[kSB][DH + 8];
+  __shared__ __align__(16) short qt[DH][kSB + 8];
+  __shared__ __align__(16) short gt[DH][kSB + 8];
+  __shared__ __align__(16) float ls[kSB];
+  __shared__ __align__(16) float dd[kSB];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
   const int half = lane >> 5;
@@ -217,54 +311,62 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_kv(
   }
   const float s2 = scale * kLog2e;
   f32x16 dk = zero16(), dv = zero16();  // D[key][c]: key = 8*(i/4)+4*half+i%4, c = l32
-  for (int qb = 0; qb < n_q; qb += kT) {
+  Stage<DH> pq, pg;
+  float pl = 0.f, pd = 0.f;
+  auto prefetch = [&](int qb) {
+    pq.load(q, qb, n_q, H, h);
+    pg.load(g, qb, n_q, H, h);
+    if (threadIdx.x < kSB) {
+      const bool ok = qb + int(threadIdx.x) < n_q;
+      pl = ok ? lse[int64_t(h) * n_q + qb + threadIdx.x] * kLog2e : INFINITY;
+      pd = ok ? dsum[int64_t(h) * n_q + qb + threadIdx.x] : 0.f;
+    }
+  };
+  prefetch(0);
+  for (int qb = 0; qb < n_q; qb += kSB) {
     __syncthreads();
-    for (int e = threadIdx.x; e < kT * DH; e += kBlock) {
-      const int r = e / DH, c = e - r * DH;
-      const bool ok = qb + r < n_q;
-      const int64_t at = (int64_t(qb + r) * H + h) * DH + c;
-      qs[r][c] = ok ? static_cast<short>(q[at].x) : short(0);
-      gs[r][c] = ok ? static_cast<short>(g[at].x) : short(0);
-    }
-    if (threadIdx.x < kT) {
-      const int r = threadIdx.x;
-      const bool ok = qb + r < n_q;
-      ls[r] = ok ? lse[int64_t(h) * n_q + qb + r] * kLog2e : INFINITY;
-      dd[r] = ok ? dsum[int64_t(h) * n_q + qb + r] : 0.f;
+    pq.store_rows(qs);
+    pg.store_rows(gs);
+    pq.store_trans(qt);
+    pg.store_trans(gt);
+    if (threadIdx.x < kSB) {
+      ls[threadIdx.x] = pl;
+      dd[threadIdx.x] = pd;
     }
     __syncthreads();
-    // S and dP tiles, rows = queries qb + 8*(i/4) + 4*half + i%4, col = this lane's key.
-    f32x16 st = zero16(), dp = zero16();
+    if (qb + kSB < n_q) prefetch(qb + kSB);
+    for (int sub = 0; sub < kSB / kT && qb + sub * kT < n_q; ++sub) {
+      const int r0 = sub * kT;
+      // S and dP tiles, rows = queries qb + r0 + 8*(i/4) + 4*half + i%4, col = this lane's key.
+      f32x16 st = zero16(), dp = zero16();
 #pragma unroll
-    for (int j = 0; j < NC; ++j) {
-      s16x4 qa, ga;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        qa[t] = qs[l32][8 * j + 4 * half + t];
-        ga[t] = gs[l32][8 * j + 4 * half + t];
+      for (int j = 0; j < NC; ++j) {
+        st = mfma(lds4(&qs[r0 + l32][8 * j + 4 * half]), kbv[j], st);
+        dp = mfma(lds4(&gs[r0 + l32][8 * j + 4 * half]), vbv[j], dp);
       }
-      st = mfma(qa, kbv[j], st);
-      dp = mfma(ga, vbv[j], dp);
-    }
-    s16x4 pa[4], dsa[4];  // P^T and dS^T as A operands: A[key][q-step row]
+      s16x4 pa[4], dsa[4];  // P^T and dS^T as A operands: A[key][query step row]
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int r = 8 * (i / 4) + 4 * half + (i % 4);
-      const float p = exp2f(st[i] * s2 - ls[r]);  // padded rows: exp2(-inf) = 0
-      pa[i / 4][i % 4] = bf(p);
-      dsa[i / 4][i % 4] = bf(p * (dp[i] - dd[r]));
-    }
-    // dV += P^T G, dK += dS^T Q: K steps of 8 queries; B = G/Q rows from LDS.
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      s16x4 gb, qbv;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        gb[t] = l32 < DH ? gs[8 * j + 4 * half + t][l32] : short(0);
-        qbv[t] = l32 < DH ? qs[8 * j + 4 * half + t][l32] : short(0);
+      for (int j = 0; j < 4; ++j) {
+        const int r = r0 + 8 * j + 4 * half;  // rows r .. r+3 of this K step
+        const float4 lv = *reinterpret_cast<const float4*>(&ls[r]);
+        const float4 dv4 = *reinterpret_cast<const float4*>(&dd[r]);
+        // padded rows carry ls = +inf: exp2(-inf) = 0
+        const float p0 = exp2f(fmaf(st[4 * j], s2, -lv.x));
+        const float p1 = exp2f(fmaf(st[4 * j + 1], s2, -lv.y));
+        const float p2 = exp2f(fmaf(st[4 * j + 2], s2, -lv.z));
+        const float p3 = exp2f(fmaf(st[4 * j + 3], s2, -lv.w));
+        pa[j] = pack4(p0, p1, p2, p3);
+        dsa[j] = pack4(p0 * (dp[4 * j] - dv4.x), p1 * (dp[4 * j + 1] - dv4.y),
+                       p2 * (dp[4 * j + 2] - dv4.z), p3 * (dp[4 * j + 3] - dv4.w));
       }
-      dv = mfma(pa[j], gb, dv);
-      dk = mfma(dsa[j], qbv, dk);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int c0 = r0 + 8 * j + 4 * half;
+        const s16x4 gb = l32 < DH ? lds4(&gt[l32][c0]) : zero4();
+        const s16x4 qbq = l32 < DH ? lds4(&qt[l32][c0]) : zero4();
+        dv = mfma(pa[j], gb, dv);
+        dk = mfma(dsa[j], qbq, dk);
+      }
     }
   }
   // D[key][c] -> grad rows; lane holds column c = l32 of 16 key rows.
@@ -280,16 +382,17 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_kv(
   }
 }
 
-// Query-major: dQ for queries q0 .. q0+31.  S^T, dP^T as D[key][q]; K, V tiles
-// of 32 keys staged row-major in LDS.
+// Query-major: dQ for queries q0 .. q0+31.  S^T, dP^T as D[key][q]; K and V
+// stages of 128 keys in LDS (row-major for the A operands, K^T for dQ += dS K).
 template <int DH>
 __global__ __launch_bounds__(kBlock) void k_mf_bwd_q(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
     const bf16_t* __restrict__ g, const float* __restrict__ lse, const float* __restrict__ dsum,
     int32_t n_q, int32_t n_k, int32_t H, float scale, bf16_t* __restrict__ grad_q) {
   constexpr int NC = DH / 8;
-  __shared__ short ks[kT][DH + 4];
-  __shared__ short vs[kT][DH + 4];
+  __shared__ __align__(16) short ks[kSB][DH + 8];
+  __shared__ __align__(16) short vs[kSB][DH + 8];
+  __shared__ __align__(16) short kt[DH][kSB + 8];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
   const int half = lane >> 5;
@@ -307,42 +410,46 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_q(
   const float Dq = q_ok ? dsum[int64_t(h) * n_q + qi] : 0.f;
   const float s2 = scale * kLog2e;
   f32x16 dq = zero16();  // D[q][c]: q = 8*(i/4)+4*half+i%4 (tile row), c = l32
-  for (int kb = 0; kb < n_k; kb += kT) {
+  Stage<DH> pk, pv;
+  pk.load(k, 0, n_k, H, h);
+  pv.load(v, 0, n_k, H, h);
+  for (int kb = 0; kb < n_k; kb += kSB) {
     __syncthreads();
-    for (int e = threadIdx.x; e < kT * DH; e += kBlock) {
-      const int r = e / DH, c = e - r * DH;
-      const bool ok = kb + r < n_k;
-      const int64_t at = (int64_t(kb + r) * H + h) * DH + c;
-      ks[r][c] = ok ? static_cast<short>(k[at].x) : short(0);
-      vs[r][c] = ok ? static_cast<short>(v[at].x) : short(0);
+    pk.store_rows(ks);
+    pv.store_rows(vs);
+    pk.store_trans(kt);
+    __syncthreads();
+    if (kb + kSB < n_k) {
+      pk.load(k, kb + kSB, n_k, H, h);
+      pv.load(v, kb + kSB, n_k, H, h);
     }
-    __syncthreads();
-    // S^T and dP^T tiles: rows = keys kb + 8*(i/4)+4*half+i%4, col = this lane's query.
-    f32x16 st = zero16(), dp = zero16();
+    for (int sub = 0; sub < kSB / kT && kb + sub * kT < n_k; ++sub) {
+      const int r0 = sub * kT;
+      f32x16 st = zero16(), dp = zero16();
 #pragma unroll
-    for (int j = 0; j < NC; ++j) {
-      s16x4 ka, va;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        ka[t] = ks[l32][8 * j + 4 * half + t];
-        va[t] = vs[l32][8 * j + 4 * half + t];
+      for (int j = 0; j < NC; ++j) {
+        st = mfma(lds4(&ks[r0 + l32][8 * j + 4 * half]), qbv[j], st);
+        dp = mfma(lds4(&vs[r0 + l32][8 * j + 4 * half]), gbv[j], dp);
       }
-      st = mfma(ka, qbv[j], st);
-      dp = mfma(va, gbv[j], dp);
-    }
-    s16x4 dsa[4];  // dS as A operand: A[q][key step row] from the D[key][q] layout
+      float ds[16];
+      if (kb + r0 + kT <= n_k) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int key = kb + 8 * (i / 4) + 4 * half + (i % 4);
-      const float p = key < n_k ? exp2f(st[i] * s2 - L2) : 0.f;
-      dsa[i / 4][i % 4] = bf(p * (dp[i] - Dq));
-    }
+        for (int i = 0; i < 16; ++i) ds[i] = exp2f(fmaf(st[i], s2, -L2)) * (dp[i] - Dq);
+      } else {  // tail tile: keys past n_k drop out
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      s16x4 kbk;  // B = K rows of this K step: B[key][c = l32]
+        for (int i = 0; i < 16; ++i) {
+          const int key = kb + r0 + 8 * (i / 4) + 4 * half + (i % 4);
+          ds[i] = key < n_k ? exp2f(fmaf(st[i], s2, -L2)) * (dp[i] - Dq) : 0.f;
+        }
+      }
+      s16x4 dsa[4];  // dS as A operand: A[q][key step row] from the D[key][q] layout
 #pragma unroll
-      for (int t = 0; t < 4; ++t) kbk[t] = l32 < DH ? ks[8 * j + 4 * half + t][l32] : short(0);
-      dq = mfma(dsa[j], kbk, dq);
+      for (int j = 0; j < 4; ++j) dsa[j] = pack4(ds[4 * j], ds[4 * j + 1], ds[4 * j + 2], ds[4 * j + 3]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const s16x4 kbk = l32 < DH ? lds4(&kt[l32][r0 + 8 * j + 4 * half]) : zero4();
+        dq = mfma(dsa[j], kbk, dq);
+      }
     }
   }
   if (l32 >= DH) return;
