@@ -184,7 +184,7 @@ def main(argv=None) -> int:
     import numpy as np
     import torch
 
-    from neutrongt_amd import _lib, chunk_for_heads
+    from neutrongt_amd import _lib, chunk_for_heads, small_for_heads
     from neutrongt_amd import synthetic as S
     from neutrongt_amd.attention import DenseAttentionFunction, SparseAttentionFunction
     from neutrongt_amd.csr import WindowAdjacency
@@ -214,10 +214,11 @@ def main(argv=None) -> int:
         ei = torch.from_numpy(ei_np).to(dev)
         torch.cuda.synchronize()
         t1 = time.perf_counter()
-        adj = WindowAdjacency(ei, cfg.n_q, n_k, chunk_for_heads(H))
+        adj = WindowAdjacency(ei, cfg.n_q, n_k, chunk_for_heads(H), small_for_heads(H))
         csr_ms = (time.perf_counter() - t1) * 1e3
         _log(f"[bench] csr built in {csr_ms:.2f} ms (incl. one info sync); items q/k "
-             f"{adj.struct.n_items_q}/{adj.struct.n_items_k}, splits q/k "
+             f"{adj.struct.n_items_q}/{adj.struct.n_items_k}, packed q/k "
+             f"{adj.struct.n_packed_q}/{adj.struct.n_packed_k}, splits q/k "
              f"{adj.struct.n_splits_q}/{adj.struct.n_splits_k}, max deg q/k "
              f"{adj.max_deg_q}/{adj.max_deg_k}")
 

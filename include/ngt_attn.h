@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define NGT_ABI_VERSION 1
+#define NGT_ABI_VERSION 2
 
 #define NGT_F32 0
 #define NGT_BF16 1
@@ -49,6 +49,8 @@ extern "C" {
 #define NGT_INFO_BAD_EDGES 8 /* edges whose src/dst fell outside [0,n_k)/[0,n_q) */
 #define NGT_INFO_MAX_DEG_Q 9
 #define NGT_INFO_MAX_DEG_K 10
+#define NGT_INFO_PACKED_Q 11  /* rows in the packed small-row list, query-major */
+#define NGT_INFO_PACKED_K 12
 #define NGT_INFO_LEN 16
 
 /*
@@ -61,17 +63,24 @@ extern "C" {
  * Key-major ("transposed CSR"): row j lists the edges with src == j, sorted by
  *   (src, dst, edge id).  t_col = dst, t_perm = edge id.
  * q2t[p] = key-major position of the query-major edge at position p.
+ * Degree-binned schedule, per orientation:
+ *   rows with more than chunk edges: cut into chunk-edge work items (listed
+ *     first); each writes fp32 partials into its partial slot;
+ *   rows with small < degree <= chunk: one work item per row, longest first;
+ *   rows with degree <= small: the packed list (row ids, longest first); the
+ *     kernels give each packed row one edge slot, several rows per wave.
  * Work items are int32x4 {row, edge_begin, edge_end, part}: part = -1 means the
- *   item covers the whole row; part >= 0 is the partial slot of one chunk of a
- *   row longer than chunk_{q,k} edges.  Chunks of split rows come first.
+ *   item covers the whole row; part >= 0 is the partial slot of one chunk.
  * Splits are int32x4 {row, part_begin, n_parts, 0}.
  */
 typedef struct ngt_window_csr {
   int32_t n_q;
   int32_t n_k;
   int64_t n_edges;
-  int32_t chunk_q;
+  int32_t chunk_q;   /* max edges per work item */
   int32_t chunk_k;
+  int32_t small_q;   /* rows with <= small edges go to the packed list (0 <= small < chunk) */
+  int32_t small_k;
   int32_t* rowptr;   /* [n_q + 1] */
   int32_t* col;      /* [E] */
   int32_t* perm;     /* [E] */
@@ -81,8 +90,10 @@ typedef struct ngt_window_csr {
   int32_t* q2t;      /* [E] */
   int32_t* items_q;  /* [max_items_q * 4] */
   int32_t* splits_q; /* [max_splits_q * 4] */
+  int32_t* packed_q; /* [n_q] */
   int32_t* items_k;  /* [max_items_k * 4] */
   int32_t* splits_k; /* [max_splits_k * 4] */
+  int32_t* packed_k; /* [n_k] */
   int32_t* info;     /* [NGT_INFO_LEN] */
   int32_t max_items_q;
   int32_t max_splits_q;
@@ -94,9 +105,11 @@ typedef struct ngt_window_csr {
   int32_t n_items_q;
   int32_t n_parts_q;
   int32_t n_splits_q;
+  int32_t n_packed_q;
   int32_t n_items_k;
   int32_t n_parts_k;
   int32_t n_splits_k;
+  int32_t n_packed_k;
 } ngt_window_csr;
 
 int ngt_abi_version(void);

@@ -10,7 +10,7 @@ WindowAdjacency          device CSR/transposed CSR/work lists of one window
 """
 from .attention import (CoreAttention, DenseAttentionFunction, SparseAttentionFunction,
                         dense_attention, install, sparse_attention)
-from .csr import AdjacencyCache, WindowAdjacency, chunk_for_heads, default_cache
+from .csr import AdjacencyCache, WindowAdjacency, chunk_for_heads, default_cache, small_for_heads
 
 __all__ = [
     "CoreAttention",
@@ -22,5 +22,6 @@ __all__ = [
     "WindowAdjacency",
     "AdjacencyCache",
     "chunk_for_heads",
+    "small_for_heads",
     "default_cache",
 ]

@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libngt_attn.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 NGT_F32 = 0
 NGT_BF16 = 1
@@ -27,6 +27,8 @@ INFO_SRC_END = 7
 INFO_BAD_EDGES = 8
 INFO_MAX_DEG_Q = 9
 INFO_MAX_DEG_K = 10
+INFO_PACKED_Q = 11
+INFO_PACKED_K = 12
 INFO_LEN = 16
 
 
@@ -39,6 +41,8 @@ class WindowCSR(C.Structure):
         ("n_edges", C.c_int64),
         ("chunk_q", C.c_int32),
         ("chunk_k", C.c_int32),
+        ("small_q", C.c_int32),
+        ("small_k", C.c_int32),
         ("rowptr", C.c_void_p),
         ("col", C.c_void_p),
         ("perm", C.c_void_p),
@@ -48,8 +52,10 @@ class WindowCSR(C.Structure):
         ("q2t", C.c_void_p),
         ("items_q", C.c_void_p),
         ("splits_q", C.c_void_p),
+        ("packed_q", C.c_void_p),
         ("items_k", C.c_void_p),
         ("splits_k", C.c_void_p),
+        ("packed_k", C.c_void_p),
         ("info", C.c_void_p),
         ("max_items_q", C.c_int32),
         ("max_splits_q", C.c_int32),
@@ -58,9 +64,11 @@ class WindowCSR(C.Structure):
         ("n_items_q", C.c_int32),
         ("n_parts_q", C.c_int32),
         ("n_splits_q", C.c_int32),
+        ("n_packed_q", C.c_int32),
         ("n_items_k", C.c_int32),
         ("n_parts_k", C.c_int32),
         ("n_splits_k", C.c_int32),
+        ("n_packed_k", C.c_int32),
     ]
 
 

@@ -19,7 +19,7 @@ import torch
 import torch.nn as nn
 
 from . import _lib
-from .csr import AdjacencyCache, chunk_for_heads, default_cache
+from .csr import AdjacencyCache, chunk_for_heads, default_cache, small_for_heads
 
 CLAMP_LO = -5.0
 CLAMP_HI = 5.0
@@ -125,7 +125,7 @@ def sparse_attention(q, k, v, edge_index, num_heads=None, scale=None, cache: Adj
     if scale is None:
         scale = math.sqrt(d)
     cache = cache or default_cache
-    adj = cache.get(edge_index, q.shape[0], k.shape[0], chunk_for_heads(H))
+    adj = cache.get(edge_index, q.shape[0], k.shape[0], chunk_for_heads(H), small_for_heads(H))
     return SparseAttentionFunction.apply(q, k, v, adj, float(scale), float(lo), float(hi),
                                          float(eps))
 

@@ -30,10 +30,19 @@ def chunk_for_heads(n_heads: int) -> int:
     return CHUNK_EDGES
 
 
+def small_for_heads(n_heads: int) -> int:
+    """Rows with at most this many edges are packed one row per edge slot:
+    the kernels' slots per wave, 64 / next_pow2(H)."""
+    lanes = 1
+    while lanes < n_heads:
+        lanes <<= 1
+    return max(1, 64 // lanes)
+
+
 class WindowAdjacency:
     """Both CSR orientations of one window plus its work lists (int32, on device)."""
 
-    def __init__(self, edge_index: torch.Tensor, n_q: int, n_k: int, chunk: int):
+    def __init__(self, edge_index: torch.Tensor, n_q: int, n_k: int, chunk: int, small: int = 0):
         if edge_index.dim() != 2 or edge_index.shape[0] != 2:
             raise ValueError(f"edge_index must be [2, E], got {tuple(edge_index.shape)}")
         if not edge_index.is_cuda:
@@ -44,6 +53,8 @@ class WindowAdjacency:
         E = int(ei.shape[1])
         self.edge_index = edge_index  # pins the cache key's storage
         self.n_q, self.n_k, self.n_edges, self.chunk = int(n_q), int(n_k), E, int(chunk)
+        small = int(min(max(small, 0), chunk - 1))
+        self.small = small
         miq, msq, mik, msk = (C.c_int32() for _ in range(4))
         _lib.check(lib.ngt_csr_sizes(E, n_q, n_k, chunk, chunk, C.byref(miq), C.byref(msq),
                                      C.byref(mik), C.byref(msk)))
@@ -59,11 +70,14 @@ class WindowAdjacency:
         self.splits_q = torch.empty(msq.value, 4, **i32)
         self.items_k = torch.empty(mik.value, 4, **i32)
         self.splits_k = torch.empty(msk.value, 4, **i32)
+        self.packed_q = torch.empty(max(n_q, 1), **i32)
+        self.packed_k = torch.empty(max(n_k, 1), **i32)
         self.info_dev = torch.zeros(_lib.INFO_LEN, **i32)
         s = _lib.WindowCSR()
         s.n_q, s.n_k, s.n_edges, s.chunk_q, s.chunk_k = n_q, n_k, E, chunk, chunk
+        s.small_q = s.small_k = small
         for name in ("rowptr", "col", "perm", "t_rowptr", "t_col", "t_perm", "q2t", "items_q",
-                     "splits_q", "items_k", "splits_k"):
+                     "splits_q", "packed_q", "items_k", "splits_k", "packed_k"):
             setattr(s, name, getattr(self, name).data_ptr())
         s.info = self.info_dev.data_ptr()
         s.max_items_q, s.max_splits_q = miq.value, msq.value
@@ -87,6 +101,8 @@ class WindowAdjacency:
         s.n_items_k = self.info[_lib.INFO_ITEMS_K]
         s.n_parts_k = self.info[_lib.INFO_PARTS_K]
         s.n_splits_k = self.info[_lib.INFO_SPLITS_K]
+        s.n_packed_q = self.info[_lib.INFO_PACKED_Q]
+        s.n_packed_k = self.info[_lib.INFO_PACKED_K]
         self.struct = s
         self.dst_end = self.info[_lib.INFO_DST_END]
         self.max_deg_q = self.info[_lib.INFO_MAX_DEG_Q]
@@ -103,14 +119,15 @@ class AdjacencyCache:
         self.capacity = capacity
         self._d: OrderedDict = OrderedDict()
 
-    def get(self, edge_index: torch.Tensor, n_q: int, n_k: int, chunk: int) -> WindowAdjacency:
+    def get(self, edge_index: torch.Tensor, n_q: int, n_k: int, chunk: int,
+            small: int = 0) -> WindowAdjacency:
         key = (edge_index.data_ptr(), edge_index._version, tuple(edge_index.shape),
-               str(edge_index.device), edge_index.dtype, n_q, n_k, chunk)
+               str(edge_index.device), edge_index.dtype, n_q, n_k, chunk, small)
         adj = self._d.get(key)
         if adj is not None and adj.edge_index is edge_index:
             self._d.move_to_end(key)
             return adj
-        adj = WindowAdjacency(edge_index, n_q, n_k, chunk)
+        adj = WindowAdjacency(edge_index, n_q, n_k, chunk, small)
         self._d[key] = adj
         while len(self._d) > self.capacity:
             self._d.popitem(last=False)
@@ -120,4 +137,4 @@ class AdjacencyCache:
         self._d.clear()
 
 
-default_cache = AdjacencyCache()
+default_cache = AdjacencyCache(capacity=16)

@@ -1,6 +1,11 @@
 // Window adjacency construction: COO edge_index -> query-major CSR,
 // key-major (transposed) CSR, the position map between them and the
-// degree-binned work lists the attention kernels are scheduled from.
+// degree-binned work lists the attention kernels are scheduled from:
+//   rows with more than `chunk` edges -> chunks of `chunk` edges (listed first),
+//   rows with small < degree <= chunk -> one work item per row, longest first,
+//   rows with degree <= small         -> packed list, longest first; the
+//                                        kernels give each such row one edge
+//                                        slot (several rows per wave).
 //
 // The reference keeps the window mask as a COO edge_index
 // (NeutronGT/core/node_level_pipeline/window_state.py:122-140) and consumes it
@@ -105,21 +110,63 @@ __device__ __forceinline__ Count3 row_counts(int32_t deg, int32_t chunk) {
   return Count3{0, 1, 0};
 }
 
+// Per row: chunk counts for the scan, and (degree, row) pairs for the sort.
 __global__ void k_count(const int32_t* __restrict__ rowptr, int32_t n_rows, int32_t chunk,
-                        Count3* __restrict__ cnt, int32_t* __restrict__ info, int max_deg_slot) {
+                        Count3* __restrict__ cnt, uint32_t* __restrict__ deg_key,
+                        int32_t* __restrict__ row_val, int32_t* __restrict__ info,
+                        int max_deg_slot) {
   int32_t local_max = 0;
   for (int32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < n_rows; r += gridDim.x * blockDim.x) {
     const int32_t deg = rowptr[r + 1] - rowptr[r];
     cnt[r] = row_counts(deg, chunk);
+    deg_key[r] = static_cast<uint32_t>(deg);
+    row_val[r] = r;
     local_max = max(local_max, deg);
   }
   if (local_max > 0) atomicMax(info + max_deg_slot, local_max);
 }
 
-__global__ void k_emit(const int32_t* __restrict__ rowptr, int32_t n_rows, int32_t chunk,
-                       const Count3* __restrict__ scan, int4* __restrict__ items,
-                       int4* __restrict__ splits, int32_t* __restrict__ info, int info_base) {
-  // Totals = exclusive prefix of the last row + that row's own counts.
+// Chunks of the rows longer than `chunk` (row order) and the split table.
+__global__ void k_emit_split(const int32_t* __restrict__ rowptr, int32_t n_rows, int32_t chunk,
+                             const Count3* __restrict__ scan, int4* __restrict__ items,
+                             int4* __restrict__ splits) {
+  for (int32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < n_rows; r += gridDim.x * blockDim.x) {
+    const int32_t beg = rowptr[r];
+    const int32_t end = rowptr[r + 1];
+    if (end - beg <= chunk) continue;
+    const Count3 pre = scan[r];
+    const int32_t n = (end - beg + chunk - 1) / chunk;
+    for (int32_t c = 0; c < n; ++c) {
+      const int32_t b = beg + c * chunk;
+      const int32_t slot = pre.split_items + c;
+      items[slot] = make_int4(r, b, min(end, b + chunk), slot);
+    }
+    splits[pre.split_rows] = make_int4(r, pre.split_items, n, 0);
+  }
+}
+
+// First index in sorted[0, n) whose value exceeds x.
+__device__ __forceinline__ int32_t upper_bound_u32(const uint32_t* __restrict__ sorted, int32_t n,
+                                                   uint32_t x) {
+  int32_t lo = 0, hi = n;
+  while (lo < hi) {
+    const int32_t mid = (lo + hi) >> 1;
+    if (sorted[mid] <= x) lo = mid + 1;
+    else hi = mid;
+  }
+  return lo;
+}
+
+// From the rows sorted by ascending degree: the packed small rows and the
+// single-item medium rows, both longest first.  info gets the totals.
+__global__ void k_emit_sorted(const int32_t* __restrict__ rowptr, int32_t n_rows, int32_t chunk,
+                              int32_t small, const uint32_t* __restrict__ sdeg,
+                              const int32_t* __restrict__ srow, const Count3* __restrict__ scan,
+                              int4* __restrict__ items, int32_t* __restrict__ packed,
+                              int32_t* __restrict__ info, int info_base, int packed_slot) {
+  const int32_t n_small = upper_bound_u32(sdeg, n_rows, static_cast<uint32_t>(small));
+  const int32_t n_le_chunk = upper_bound_u32(sdeg, n_rows, static_cast<uint32_t>(chunk));
+  const int32_t n_medium = n_le_chunk - n_small;
   Count3 tot{0, 0, 0};
   if (n_rows > 0) {
     const Count3 last = scan[n_rows - 1];
@@ -128,24 +175,18 @@ __global__ void k_emit(const int32_t* __restrict__ rowptr, int32_t n_rows, int32
                  last.split_rows + own.split_rows};
   }
   if (blockIdx.x == 0 && threadIdx.x == 0) {
-    info[info_base + 0] = tot.split_items + tot.plain_items;  // items
-    info[info_base + 1] = tot.split_items;                    // partial slots
-    info[info_base + 2] = tot.split_rows;                     // split rows
+    info[info_base + 0] = tot.split_items + n_medium;  // work items
+    info[info_base + 1] = tot.split_items;             // partial slots
+    info[info_base + 2] = tot.split_rows;              // split rows
+    info[packed_slot] = n_small;                       // packed rows
   }
-  for (int32_t r = blockIdx.x * blockDim.x + threadIdx.x; r < n_rows; r += gridDim.x * blockDim.x) {
-    const int32_t beg = rowptr[r];
-    const int32_t end = rowptr[r + 1];
-    const Count3 pre = scan[r];
-    if (end - beg > chunk) {
-      const int32_t n = (end - beg + chunk - 1) / chunk;
-      for (int32_t c = 0; c < n; ++c) {
-        const int32_t b = beg + c * chunk;
-        const int32_t slot = pre.split_items + c;
-        items[slot] = make_int4(r, b, min(end, b + chunk), slot);
-      }
-      splits[pre.split_rows] = make_int4(r, pre.split_items, n, 0);
+  for (int32_t p = blockIdx.x * blockDim.x + threadIdx.x; p < n_le_chunk;
+       p += gridDim.x * blockDim.x) {
+    const int32_t r = srow[p];
+    if (p < n_small) {
+      packed[n_small - 1 - p] = r;
     } else {
-      items[tot.split_items + pre.plain_items] = make_int4(r, beg, end, -1);
+      items[tot.split_items + (n_le_chunk - 1 - p)] = make_int4(r, rowptr[r], rowptr[r + 1], -1);
     }
   }
 }
@@ -172,7 +213,7 @@ inline int grid_for(int64_t n) {
 }
 
 struct CsrLayout {
-  size_t key_a, key_b, key_c, eid, tpos, cnt, cnt_scan, temp, total;
+  size_t key_a, key_b, key_c, eid, tpos, cnt, cnt_scan, deg_a, deg_b, row_a, row_b, temp, total;
   size_t temp_bytes;
 };
 
@@ -199,31 +240,53 @@ int csr_layout(int64_t E, int32_t n_q, int32_t n_k, CsrLayout* L) {
   L->tpos = take(n * 4);
   L->cnt = take(size_t(n_rows + 1) * sizeof(Count3));
   L->cnt_scan = take(size_t(n_rows + 1) * sizeof(Count3));
+  L->deg_a = take(size_t(n_rows + 1) * 4);
+  L->deg_b = take(size_t(n_rows + 1) * 4);
+  L->row_a = take(size_t(n_rows + 1) * 4);
+  L->row_b = take(size_t(n_rows + 1) * 4);
+  size_t deg_sort_bytes = 0;
+  NGT_HIP_CHECK(rocprim::radix_sort_pairs(nullptr, deg_sort_bytes, (uint32_t*)nullptr,
+                                          (uint32_t*)nullptr, (int32_t*)nullptr,
+                                          (int32_t*)nullptr, size_t(n_rows > 0 ? n_rows : 1),
+                                          0u, 32u, hipStream_t(0)));
   L->temp_bytes = sort_bytes > scan_bytes ? sort_bytes : scan_bytes;
+  if (deg_sort_bytes > L->temp_bytes) L->temp_bytes = deg_sort_bytes;
   L->temp = take(L->temp_bytes);
   L->total = off;
   return NGT_OK;
 }
 
-int build_worklist(const int32_t* rowptr, int32_t n_rows, int32_t chunk, int4* items,
-                   int4* splits, int32_t* info, int info_base, int max_deg_slot, char* ws,
-                   const CsrLayout& L, hipStream_t st) {
+int build_worklist(const int32_t* rowptr, int32_t n_rows, int32_t chunk, int32_t small,
+                   int4* items, int4* splits, int32_t* packed, int32_t* info, int info_base,
+                   int packed_slot, int max_deg_slot, char* ws, const CsrLayout& L,
+                   hipStream_t st) {
   Count3* cnt = reinterpret_cast<Count3*>(ws + L.cnt);
   Count3* scan = reinterpret_cast<Count3*>(ws + L.cnt_scan);
+  uint32_t* deg_a = reinterpret_cast<uint32_t*>(ws + L.deg_a);
+  uint32_t* deg_b = reinterpret_cast<uint32_t*>(ws + L.deg_b);
+  int32_t* row_a = reinterpret_cast<int32_t*>(ws + L.row_a);
+  int32_t* row_b = reinterpret_cast<int32_t*>(ws + L.row_b);
   if (n_rows == 0) {
-    hipLaunchKernelGGL(k_emit, dim3(1), dim3(kBlock), 0, st, rowptr, n_rows, chunk, scan, items,
-                       splits, info, info_base);
+    hipLaunchKernelGGL(k_emit_sorted, dim3(1), dim3(kBlock), 0, st, rowptr, n_rows, chunk, small,
+                       deg_b, row_b, scan, items, packed, info, info_base, packed_slot);
     NGT_HIP_CHECK(hipGetLastError());
     return NGT_OK;
   }
   hipLaunchKernelGGL(k_count, dim3(grid_for(n_rows)), dim3(kBlock), 0, st, rowptr, n_rows, chunk,
-                     cnt, info, max_deg_slot);
+                     cnt, deg_a, row_a, info, max_deg_slot);
   NGT_HIP_CHECK(hipGetLastError());
   size_t temp_bytes = L.temp_bytes;
   NGT_HIP_CHECK(rocprim::exclusive_scan(ws + L.temp, temp_bytes, cnt, scan, Count3{0, 0, 0},
                                         size_t(n_rows), Count3Plus(), st));
-  hipLaunchKernelGGL(k_emit, dim3(grid_for(n_rows)), dim3(kBlock), 0, st, rowptr, n_rows, chunk,
-                     scan, items, splits, info, info_base);
+  hipLaunchKernelGGL(k_emit_split, dim3(grid_for(n_rows)), dim3(kBlock), 0, st, rowptr, n_rows,
+                     chunk, scan, items, splits);
+  NGT_HIP_CHECK(hipGetLastError());
+  temp_bytes = L.temp_bytes;
+  NGT_HIP_CHECK(rocprim::radix_sort_pairs(ws + L.temp, temp_bytes, deg_a, deg_b, row_a, row_b,
+                                          size_t(n_rows), 0u, 32u, st));
+  hipLaunchKernelGGL(k_emit_sorted, dim3(grid_for(n_rows)), dim3(kBlock), 0, st, rowptr, n_rows,
+                     chunk, small, deg_b, row_b, scan, items, packed, info, info_base,
+                     packed_slot);
   NGT_HIP_CHECK(hipGetLastError());
   return NGT_OK;
 }
@@ -268,12 +331,15 @@ extern "C" int ngt_csr_build(const int64_t* edge_index, ngt_window_csr* csr, voi
   if (!csr) return set_error(NGT_ERR_ARG, "ngt_csr_build: null csr");
   const int64_t E = csr->n_edges;
   const int32_t n_q = csr->n_q, n_k = csr->n_k;
-  if (E < 0 || n_q < 0 || n_k < 0 || csr->chunk_q <= 0 || csr->chunk_k <= 0)
-    return set_error(NGT_ERR_ARG, "ngt_csr_build: bad sizes");
+  if (E < 0 || n_q < 0 || n_k < 0 || csr->chunk_q <= 0 || csr->chunk_k <= 0 ||
+      csr->small_q < 0 || csr->small_k < 0 || csr->small_q >= csr->chunk_q ||
+      csr->small_k >= csr->chunk_k)
+    return set_error(NGT_ERR_ARG, "ngt_csr_build: bad sizes (need 0 <= small < chunk)");
   if (E > 0 && (!edge_index || n_q == 0 || n_k == 0))
     return set_error(NGT_ERR_ARG, "ngt_csr_build: edges given for an empty window");
   if (!csr->rowptr || !csr->t_rowptr || !csr->info || !csr->items_q || !csr->items_k ||
-      !csr->splits_q || !csr->splits_k || (E > 0 && (!csr->col || !csr->perm || !csr->t_col ||
+      !csr->splits_q || !csr->splits_k || (n_q > 0 && !csr->packed_q) ||
+      (n_k > 0 && !csr->packed_k) || (E > 0 && (!csr->col || !csr->perm || !csr->t_col ||
                                                      !csr->t_perm || !csr->q2t)))
     return set_error(NGT_ERR_ARG, "ngt_csr_build: null output array");
   int32_t miq, msq, mik, msk;
@@ -331,12 +397,14 @@ extern "C" int ngt_csr_build(const int64_t* edge_index, ngt_window_csr* csr, voi
                        csr->info);
     NGT_HIP_CHECK(hipGetLastError());
   }
-  rc = build_worklist(csr->rowptr, n_q, csr->chunk_q, reinterpret_cast<int4*>(csr->items_q),
-                      reinterpret_cast<int4*>(csr->splits_q), csr->info, NGT_INFO_ITEMS_Q,
+  rc = build_worklist(csr->rowptr, n_q, csr->chunk_q, csr->small_q,
+                      reinterpret_cast<int4*>(csr->items_q), reinterpret_cast<int4*>(csr->splits_q),
+                      csr->packed_q, csr->info, NGT_INFO_ITEMS_Q, NGT_INFO_PACKED_Q,
                       NGT_INFO_MAX_DEG_Q, ws, L, st);
   if (rc != NGT_OK) return rc;
-  rc = build_worklist(csr->t_rowptr, n_k, csr->chunk_k, reinterpret_cast<int4*>(csr->items_k),
-                      reinterpret_cast<int4*>(csr->splits_k), csr->info, NGT_INFO_ITEMS_K,
+  rc = build_worklist(csr->t_rowptr, n_k, csr->chunk_k, csr->small_k,
+                      reinterpret_cast<int4*>(csr->items_k), reinterpret_cast<int4*>(csr->splits_k),
+                      csr->packed_k, csr->info, NGT_INFO_ITEMS_K, NGT_INFO_PACKED_K,
                       NGT_INFO_MAX_DEG_K, ws, L, st);
   return rc;
 }

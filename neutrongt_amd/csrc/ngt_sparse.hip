@@ -75,6 +75,7 @@ __device__ __forceinline__ bool wave_work(int n_items, int n_groups, int hg, int
                                           int& item, Lane& ln) {
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t gw = int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+  if (n_items <= 0) return false;
   const int64_t group = gw / n_items;
   if (group >= n_groups) return false;
   item = static_cast<int>(gw - group * n_items);
@@ -86,6 +87,58 @@ __device__ __forceinline__ bool wave_work(int n_items, int n_groups, int hg, int
   return true;
 }
 
+// Packed small rows: each edge slot of a wave owns one whole row.  Returns
+// false for lanes without a row (they leave; packed mode uses no shuffles).
+__device__ __forceinline__ bool packed_work(int64_t pw, int n_pwaves, int n_groups, int hg,
+                                            int L, int H, const int32_t* __restrict__ packed,
+                                            int n_packed, int64_t& row, int& h) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t group = pw / n_pwaves;
+  if (group >= n_groups) return false;
+  const int64_t idx = pw - group * n_pwaves;
+  const int hl = lane & (L - 1);
+  const int64_t r_idx = idx * (kWave / L) + lane / L;
+  h = static_cast<int>(group) * hg + hl;
+  if (hl >= hg || h >= H || r_idx >= n_packed) return false;
+  row = packed[r_idx];
+  return true;
+}
+
+template <typename T, int DH>
+__device__ __forceinline__ void fwd_packed(const T* __restrict__ q, const T* __restrict__ k,
+                                           const T* __restrict__ v,
+                                           const int32_t* __restrict__ rowptr,
+                                           const int32_t* __restrict__ col, int64_t row, int h,
+                                           int H, float inv_scale, float lo, float hi, float eps,
+                                           T* __restrict__ out, float* __restrict__ rinv,
+                                           float* __restrict__ zbuf) {
+  float qr[DH], acc[DH];
+  float z = 0.f;
+  load_row<T, DH>(q + (row * H + h) * DH, qr);
+#pragma unroll
+  for (int c = 0; c < DH; ++c) acc[c] = 0.f;
+  const int beg = rowptr[row], end = rowptr[row + 1];
+  for (int e = beg; e < end; ++e) {
+    const int64_t j = col[e];
+    RowWords<T, DH> kw, vw;
+    load_words<T, DH>(k + (j * H + h) * DH, kw);
+    load_words<T, DH>(v + (j * H + h) * DH, vw);
+    float kk[DH];
+    words_to_f32<T, DH>(kw, kk);
+    const float p = __expf(clampf(dot<DH>(qr, kk) * inv_scale, lo, hi));
+    z += p;
+#pragma unroll
+    for (int c = 0; c < DH; ++c) acc[c] = fmaf(p, word_elem<T, DH>(vw, c), acc[c]);
+  }
+  const float den = z + eps;
+  float o[DH];
+#pragma unroll
+  for (int c = 0; c < DH; ++c) o[c] = acc[c] / den;
+  store_row<T, DH>(out + (row * H + h) * DH, o);
+  rinv[row * H + h] = 1.0f / den;
+  zbuf[row * H + h] = z;
+}
+
 // ------------------------------------------------------------------ forward
 template <typename T, int DH>
 __global__ __launch_bounds__(kBlock) void k_fwd(
@@ -93,7 +146,18 @@ __global__ __launch_bounds__(kBlock) void k_fwd(
     const int32_t* __restrict__ col, const int4* __restrict__ items, int32_t n_items,
     int32_t n_groups, int32_t hg, int32_t H, int32_t L, float inv_scale, float lo, float hi,
     float eps, T* __restrict__ out, float* __restrict__ rinv, float* __restrict__ zbuf,
-    float* __restrict__ part_acc, float* __restrict__ part_z) {
+    float* __restrict__ part_acc, float* __restrict__ part_z, const int32_t* __restrict__ rowptr,
+    const int32_t* __restrict__ packed, int32_t n_packed, int32_t n_pwaves) {
+  const int64_t gw = int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+  if (gw >= int64_t(n_items) * n_groups) {
+    int64_t prow;
+    int ph;
+    if (packed_work(gw - int64_t(n_items) * n_groups, n_pwaves, n_groups, hg, L, H, packed,
+                    n_packed, prow, ph))
+      fwd_packed<T, DH>(q, k, v, rowptr, col, prow, ph, H, inv_scale, lo, hi, eps, out, rinv,
+                        zbuf);
+    return;
+  }
   int item;
   Lane ln;
   if (!wave_work(n_items, n_groups, hg, L, H, item, ln)) return;
@@ -238,6 +302,53 @@ __global__ __launch_bounds__(kBlock) void k_rowstat(const T* __restrict__ out,
   }
 }
 
+template <typename T, int DH>
+__device__ __forceinline__ void bwd_kv_packed(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    const T* __restrict__ g, const float2* __restrict__ rd, const int32_t* __restrict__ t_rowptr,
+    const int32_t* __restrict__ t_col, int64_t row, int h, int H, float inv_scale, float lo,
+    float hi, T* __restrict__ grad_k, T* __restrict__ grad_v, float* __restrict__ ds) {
+  float kr[DH], vr[DH], dk[DH], dv[DH];
+  load_row<T, DH>(k + (row * H + h) * DH, kr);
+  load_row<T, DH>(v + (row * H + h) * DH, vr);
+#pragma unroll
+  for (int c = 0; c < DH; ++c) {
+    dk[c] = 0.f;
+    dv[c] = 0.f;
+  }
+  const int beg = t_rowptr[row], end = t_rowptr[row + 1];
+  for (int e = beg; e < end; ++e) {
+    const int64_t i = t_col[e];
+    RowWords<T, DH> qw, gw;
+    load_words<T, DH>(q + (i * H + h) * DH, qw);
+    load_words<T, DH>(g + (i * H + h) * DH, gw);
+    const float2 r = rd[i * H + h];
+    float sa0 = 0.f, sa1 = 0.f, sg0 = 0.f, sg1 = 0.f;
+#pragma unroll
+    for (int c = 0; c < DH; c += 2) {
+      sa0 = fmaf(word_elem<T, DH>(qw, c), kr[c], sa0);
+      sa1 = fmaf(word_elem<T, DH>(qw, c + 1), kr[c + 1], sa1);
+      sg0 = fmaf(word_elem<T, DH>(gw, c), vr[c], sg0);
+      sg1 = fmaf(word_elem<T, DH>(gw, c + 1), vr[c + 1], sg1);
+    }
+    const float a = (sa0 + sa1) * inv_scale;
+    const float p = __expf(clampf(a, lo, hi));
+    const float dp = r.x * (sg0 + sg1) - r.y;
+    const float da = (a >= lo && a <= hi) ? dp * p : 0.f;
+    const float pr = p * r.x;
+#pragma unroll
+    for (int c = 0; c < DH; ++c) {
+      dk[c] = fmaf(da, word_elem<T, DH>(qw, c), dk[c]);
+      dv[c] = fmaf(pr, word_elem<T, DH>(gw, c), dv[c]);
+    }
+    ds[int64_t(e) * H + h] = da;
+  }
+#pragma unroll
+  for (int c = 0; c < DH; ++c) dk[c] *= inv_scale;
+  store_row<T, DH>(grad_k + (row * H + h) * DH, dk);
+  store_row<T, DH>(grad_v + (row * H + h) * DH, dv);
+}
+
 // Key-major pass: grad_k, grad_v of key row j and da_e for every edge of j
 // (stored at the key-major edge position for the query-major pass).
 template <typename T, int DH>
@@ -246,7 +357,19 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
     const T* __restrict__ g, const float2* __restrict__ rd, const int32_t* __restrict__ t_col,
     const int4* __restrict__ items, int32_t n_items, int32_t n_groups, int32_t hg, int32_t H,
     int32_t L, float inv_scale, float lo, float hi, T* __restrict__ grad_k,
-    T* __restrict__ grad_v, float* __restrict__ ds, float* __restrict__ part_kv) {
+    T* __restrict__ grad_v, float* __restrict__ ds, float* __restrict__ part_kv,
+    const int32_t* __restrict__ t_rowptr, const int32_t* __restrict__ packed, int32_t n_packed,
+    int32_t n_pwaves) {
+  const int64_t gw0 = int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+  if (gw0 >= int64_t(n_items) * n_groups) {
+    int64_t prow;
+    int ph;
+    if (packed_work(gw0 - int64_t(n_items) * n_groups, n_pwaves, n_groups, hg, L, H, packed,
+                    n_packed, prow, ph))
+      bwd_kv_packed<T, DH>(q, k, v, g, rd, t_rowptr, t_col, prow, ph, H, inv_scale, lo, hi,
+                           grad_k, grad_v, ds);
+    return;
+  }
   int item;
   Lane ln;
   if (!wave_work(n_items, n_groups, hg, L, H, item, ln)) return;
@@ -364,13 +487,48 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv_finalize(const int4* __restri
     elem<T>::store(grad_v + at + (c - DH), a);
 }
 
+template <typename T, int DH>
+__device__ __forceinline__ void bwd_q_packed(const T* __restrict__ k,
+                                             const int32_t* __restrict__ rowptr,
+                                             const int32_t* __restrict__ col,
+                                             const int32_t* __restrict__ q2t,
+                                             const float* __restrict__ ds, int64_t row, int h,
+                                             int H, float inv_scale, T* __restrict__ grad_q) {
+  float dq[DH];
+#pragma unroll
+  for (int c = 0; c < DH; ++c) dq[c] = 0.f;
+  const int beg = rowptr[row], end = rowptr[row + 1];
+  for (int e = beg; e < end; ++e) {
+    const int64_t j = col[e];
+    const int64_t t = q2t[e];
+    RowWords<T, DH> kw;
+    load_words<T, DH>(k + (j * H + h) * DH, kw);
+    const float d = ds[t * H + h];
+#pragma unroll
+    for (int c = 0; c < DH; ++c) dq[c] = fmaf(d, word_elem<T, DH>(kw, c), dq[c]);
+  }
+#pragma unroll
+  for (int c = 0; c < DH; ++c) dq[c] *= inv_scale;
+  store_row<T, DH>(grad_q + (row * H + h) * DH, dq);
+}
+
 // Query-major pass: grad_q[i] = sum_e da_e k_j / scale.
 template <typename T, int DH>
 __global__ __launch_bounds__(kBlock) void k_bwd_q(
     const T* __restrict__ k, const int32_t* __restrict__ col, const int32_t* __restrict__ q2t,
     const float* __restrict__ ds, const int4* __restrict__ items, int32_t n_items,
     int32_t n_groups, int32_t hg, int32_t H, int32_t L, float inv_scale, T* __restrict__ grad_q,
-    float* __restrict__ part_q) {
+    float* __restrict__ part_q, const int32_t* __restrict__ rowptr,
+    const int32_t* __restrict__ packed, int32_t n_packed, int32_t n_pwaves) {
+  const int64_t gw0 = int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+  if (gw0 >= int64_t(n_items) * n_groups) {
+    int64_t prow;
+    int ph;
+    if (packed_work(gw0 - int64_t(n_items) * n_groups, n_pwaves, n_groups, hg, L, H, packed,
+                    n_packed, prow, ph))
+      bwd_q_packed<T, DH>(k, rowptr, col, q2t, ds, prow, ph, H, inv_scale, grad_q);
+    return;
+  }
   int item;
   Lane ln;
   if (!wave_work(n_items, n_groups, hg, L, H, item, ln)) return;
@@ -513,9 +671,18 @@ int check_common(const char* fn, int dtype, const ngt_window_csr* csr, int H, in
   if (csr->n_items_q < 0 || csr->n_items_k < 0 || csr->n_items_q > csr->max_items_q ||
       csr->n_items_k > csr->max_items_k || csr->n_splits_q > csr->max_splits_q ||
       csr->n_splits_k > csr->max_splits_k || csr->n_parts_q > csr->n_items_q ||
-      csr->n_parts_k > csr->n_items_k)
+      csr->n_parts_k > csr->n_items_k || csr->n_packed_q < 0 || csr->n_packed_q > csr->n_q ||
+      csr->n_packed_k < 0 || csr->n_packed_k > csr->n_k ||
+      csr->n_items_q + csr->n_packed_q < csr->n_q - csr->n_splits_q ||
+      csr->n_items_k + csr->n_packed_k < csr->n_k - csr->n_splits_k)
     return set_error(NGT_ERR_ARG, "%s: csr counters not filled from info[]", fn);
   return NGT_OK;
+}
+
+// Waves for the packed list: 64 / L rows (one per edge slot) per wave.
+inline int packed_waves(int n_packed, int L) {
+  const int per = kWave / L;
+  return (n_packed + per - 1) / per;
 }
 
 inline unsigned blocks_for(int64_t waves) {
@@ -533,13 +700,16 @@ int launch_fwd(const ngt_window_csr* c, const void* q, const void* k, const void
   float* part_acc = reinterpret_cast<float*>(ws + lay.part_acc);
   float* part_z = reinterpret_cast<float*>(ws + lay.part_z);
   float* zbuf = reinterpret_cast<float*>(ws + lay.zbuf);
-  if (c->n_items_q > 0) {
+  const int pw_q = packed_waves(c->n_packed_q, L);
+  const int64_t waves_q = (int64_t(c->n_items_q) + pw_q) * groups;
+  if (waves_q > 0) {
     KernelTimer timer_("sparse_fwd", st);
-    hipLaunchKernelGGL((k_fwd<T, DH>), dim3(blocks_for(int64_t(c->n_items_q) * groups)),
-                       dim3(kBlock), 0, st, static_cast<const T*>(q), static_cast<const T*>(k),
+    hipLaunchKernelGGL((k_fwd<T, DH>), dim3(blocks_for(waves_q)), dim3(kBlock), 0, st,
+                       static_cast<const T*>(q), static_cast<const T*>(k),
                        static_cast<const T*>(v), c->col, reinterpret_cast<const int4*>(c->items_q),
                        c->n_items_q, groups, hg, H, L, inv_scale, lo, hi, eps,
-                       static_cast<T*>(out), rinv, zbuf, part_acc, part_z);
+                       static_cast<T*>(out), rinv, zbuf, part_acc, part_z, c->rowptr, c->packed_q,
+                       c->n_packed_q, pw_q);
     NGT_HIP_CHECK(hipGetLastError());
   }
   if (c->n_splits_q > 0) {
@@ -580,13 +750,16 @@ int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void
                        static_cast<const T*>(out), static_cast<const T*>(g), rinv, nrh, rd);
     NGT_HIP_CHECK(hipGetLastError());
   }
-  if (c->n_items_k > 0) {
+  const int pw_k = packed_waves(c->n_packed_k, L);
+  const int64_t waves_k = (int64_t(c->n_items_k) + pw_k) * groups;
+  if (waves_k > 0) {
     KernelTimer timer_("sparse_bwd_kv", st);
-    hipLaunchKernelGGL((k_bwd_kv<T, DH>), dim3(blocks_for(int64_t(c->n_items_k) * groups)),
-                       dim3(kBlock), 0, st, static_cast<const T*>(q), static_cast<const T*>(k),
+    hipLaunchKernelGGL((k_bwd_kv<T, DH>), dim3(blocks_for(waves_k)), dim3(kBlock), 0, st,
+                       static_cast<const T*>(q), static_cast<const T*>(k),
                        static_cast<const T*>(v), static_cast<const T*>(g), rd, c->t_col,
                        reinterpret_cast<const int4*>(c->items_k), c->n_items_k, groups, hg, H, L,
-                       inv_scale, lo, hi, static_cast<T*>(gk), static_cast<T*>(gv), ds, part_kv);
+                       inv_scale, lo, hi, static_cast<T*>(gk), static_cast<T*>(gv), ds, part_kv,
+                       c->t_rowptr, c->packed_k, c->n_packed_k, pw_k);
     NGT_HIP_CHECK(hipGetLastError());
   }
   if (c->n_splits_k > 0) {
@@ -597,12 +770,15 @@ int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void
                        static_cast<T*>(gk), static_cast<T*>(gv));
     NGT_HIP_CHECK(hipGetLastError());
   }
-  if (c->n_items_q > 0) {
+  const int pw_q = packed_waves(c->n_packed_q, L);
+  const int64_t waves_q = (int64_t(c->n_items_q) + pw_q) * groups;
+  if (waves_q > 0) {
     KernelTimer timer_("sparse_bwd_q", st);
-    hipLaunchKernelGGL((k_bwd_q<T, DH>), dim3(blocks_for(int64_t(c->n_items_q) * groups)),
-                       dim3(kBlock), 0, st, static_cast<const T*>(k), c->col, c->q2t, ds,
+    hipLaunchKernelGGL((k_bwd_q<T, DH>), dim3(blocks_for(waves_q)), dim3(kBlock), 0, st,
+                       static_cast<const T*>(k), c->col, c->q2t, ds,
                        reinterpret_cast<const int4*>(c->items_q), c->n_items_q, groups, hg, H, L,
-                       inv_scale, static_cast<T*>(gq), part_q);
+                       inv_scale, static_cast<T*>(gq), part_q, c->rowptr, c->packed_q,
+                       c->n_packed_q, pw_q);
     NGT_HIP_CHECK(hipGetLastError());
   }
   if (c->n_splits_q > 0) {

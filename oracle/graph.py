@@ -48,12 +48,18 @@ def csr_from_coo(src, dst, n_q: int, n_k: int):
     }
 
 
-def work_items(rowptr, chunk: int):
-    """Work list for one orientation: rows longer than ``chunk`` are cut into
-    chunks (listed first, in row order, part slot = item index); every other row
-    is one item with part -1.  Returns (items [n,4], splits [m,4])."""
+def work_items(rowptr, chunk: int, small: int = 0):
+    """Degree-binned work list for one orientation.
+
+    Rows longer than ``chunk`` are cut into chunks (listed first, in row
+    order, part slot = item index).  Rows with small < degree <= chunk are one
+    item each (part -1) and rows with degree <= small go to the packed list;
+    both follow the order of a stable ascending sort by degree, reversed
+    (longest first; equal degrees by descending row id).
+    Returns (items [n,4], splits [m,4], packed [p])."""
     rowptr = np.asarray(rowptr, dtype=np.int64)
-    split_items, plain_items, splits = [], [], []
+    deg = np.diff(rowptr)
+    split_items, splits = [], []
     for r in range(rowptr.shape[0] - 1):
         b, e = int(rowptr[r]), int(rowptr[r + 1])
         if e - b > chunk:
@@ -62,10 +68,14 @@ def work_items(rowptr, chunk: int):
             for c in range(n):
                 s = len(split_items)
                 split_items.append((r, b + c * chunk, min(e, b + (c + 1) * chunk), s))
-        else:
-            plain_items.append((r, b, e, -1))
-    items = np.array(split_items + plain_items, dtype=np.int32).reshape(-1, 4)
-    return items, np.array(splits, dtype=np.int32).reshape(-1, 4)
+    order = np.argsort(deg, kind="stable")
+    d_sorted = deg[order]
+    packed = order[d_sorted <= small][::-1]
+    medium = order[(d_sorted > small) & (d_sorted <= chunk)][::-1]
+    plain = [(int(r), int(rowptr[r]), int(rowptr[r + 1]), -1) for r in medium]
+    items = np.array(split_items + plain, dtype=np.int32).reshape(-1, 4)
+    return (items, np.array(splits, dtype=np.int32).reshape(-1, 4),
+            np.asarray(packed, dtype=np.int32))
 
 
 def merge_related_nodes(xadj, adjncy, eweights, partition, topk_percent: int):

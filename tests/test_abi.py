@@ -34,10 +34,11 @@ def test_every_declared_symbol_is_exported_and_bound():
 
 
 def test_struct_layout_matches_header():
-    # int32 n_q, n_k; int64 n_edges; int32 chunk_q, chunk_k; 12 pointers; 10 int32
-    assert C.sizeof(_lib.WindowCSR) == 8 + 8 + 8 + 12 * 8 + 10 * 4
-    assert _lib.WindowCSR.rowptr.offset == 24
-    assert _lib.WindowCSR.max_items_q.offset == 24 + 12 * 8
+    # int32 n_q, n_k; int64 n_edges; int32 chunk_q, chunk_k, small_q, small_k;
+    # 14 pointers; 12 int32
+    assert C.sizeof(_lib.WindowCSR) == 8 + 8 + 16 + 14 * 8 + 12 * 4
+    assert _lib.WindowCSR.rowptr.offset == 32
+    assert _lib.WindowCSR.max_items_q.offset == 32 + 14 * 8
 
 
 def test_csr_sizes_arithmetic():

@@ -17,14 +17,14 @@ def _say(*a):
     print(*a, flush=True)
 
 
-def _run_kernel(q, k, v, ei, go, chunk=None):
+def _run_kernel(q, k, v, ei, go, chunk=None, small=0):
     """fwd + bwd through the HIP path; returns dict of CPU tensors."""
     qd, kd, vd = (t.cuda().requires_grad_(True) for t in (q, k, v))
     eid = torch.from_numpy(ei).cuda()
     if chunk is None:
         x, ns = sparse_attention(qd, kd, vd, eid)
     else:
-        adj = WindowAdjacency(eid, q.shape[0], k.shape[0], chunk)
+        adj = WindowAdjacency(eid, q.shape[0], k.shape[0], chunk, small)
         x, ns = SparseAttentionFunction.apply(qd, kd, vd, adj, float(q.shape[-1]) ** 0.5, -5.0,
                                               5.0, 1e-6)
     x.backward(go.cuda())
@@ -76,16 +76,18 @@ def test_sparse_parity_random(n_q, n_k, H, d, E, dtype):
     _check(_run_kernel(q, k, v, ei, go), _oracle(q, k, v, ei, go, H), dtype, "random")
 
 
-@pytest.mark.parametrize("H,d,dtype,chunk", [(8, 8, torch.float32, 16), (32, 24, torch.bfloat16, 8),
-                                             (4, 16, torch.float32, 40)])
-def test_sparse_parity_hub_rows_split(H, d, dtype, chunk):
+@pytest.mark.parametrize("H,d,dtype,chunk,small", [(8, 8, torch.float32, 16, 8),
+                                                   (32, 24, torch.bfloat16, 8, 2),
+                                                   (4, 16, torch.float32, 40, 0),
+                                                   (8, 16, torch.bfloat16, 64, 12)])
+def test_sparse_parity_hub_rows_split(H, d, dtype, chunk, small):
     """A query hub and a key hub far longer than the chunk: split items +
-    finalize passes in both orientations."""
-    _say(f"case hub H={H} d={d} {dtype} chunk={chunk}")
+    finalize passes in both orientations, plus packed small rows."""
+    _say(f"case hub H={H} d={d} {dtype} chunk={chunk} small={small}")
     n = 150
     ei = hub_coo(n, n, 700, seed=H)
     q, k, v, go = _qkv(n, n, H, d, dtype, seed=7)
-    res = _run_kernel(q, k, v, ei, go, chunk=chunk)
+    res = _run_kernel(q, k, v, ei, go, chunk=chunk, small=small)
     _check(res, _oracle(q, k, v, ei, go, H), dtype, "hub")
 
 
@@ -144,27 +146,31 @@ def test_sparse_no_edges():
     assert torch.all(res["dq"] == 0) and torch.all(res["dk"] == 0) and torch.all(res["dv"] == 0)
 
 
-@pytest.mark.parametrize("n_q,n_k,E,chunk", [(300, 300, 4000, 64), (120, 500, 3000, 7),
-                                             (1, 1, 5, 1), (50, 20, 0, 8)])
-def test_csr_bit_exact(n_q, n_k, E, chunk):
-    _say(f"case csr n_q={n_q} n_k={n_k} E={E} chunk={chunk}")
+@pytest.mark.parametrize("n_q,n_k,E,chunk,small", [(300, 300, 4000, 64, 8), (120, 500, 3000, 7, 2),
+                                                   (1, 1, 5, 1, 0), (50, 20, 0, 8, 4),
+                                                   (400, 400, 2500, 256, 0)])
+def test_csr_bit_exact(n_q, n_k, E, chunk, small):
+    _say(f"case csr n_q={n_q} n_k={n_k} E={E} chunk={chunk} small={small}")
     if E:
         rng = np.random.default_rng(E)
         ei = np.stack([rng.integers(0, n_k, E), rng.integers(0, n_q, E)]).astype(np.int64)
     else:
         ei = np.zeros((2, 0), np.int64)
-    adj = WindowAdjacency(torch.from_numpy(ei).cuda(), n_q, n_k, chunk)
+    adj = WindowAdjacency(torch.from_numpy(ei).cuda(), n_q, n_k, chunk, small)
     ref = OG.csr_from_coo(ei[0], ei[1], n_q, n_k)
     got = {n: getattr(adj, n).cpu().numpy() for n in ref}
     for n in ref:
         np.testing.assert_array_equal(got[n][: ref[n].shape[0]], ref[n], err_msg=n)
     for side, rp in (("q", ref["rowptr"]), ("k", ref["t_rowptr"])):
-        items, splits = OG.work_items(rp, chunk)
+        items, splits, packed = OG.work_items(rp, chunk, small)
         gi = getattr(adj, "items_" + side).cpu().numpy()[: items.shape[0]]
         gs = getattr(adj, "splits_" + side).cpu().numpy()[: splits.shape[0]]
+        gp = getattr(adj, "packed_" + side).cpu().numpy()[: packed.shape[0]]
         np.testing.assert_array_equal(gi, items, err_msg="items_" + side)
         np.testing.assert_array_equal(gs, splits, err_msg="splits_" + side)
+        np.testing.assert_array_equal(gp, packed, err_msg="packed_" + side)
         assert adj.info[0 if side == "q" else 3] == items.shape[0]
+        assert adj.info[11 if side == "q" else 12] == packed.shape[0]
     assert adj.dst_end == (int(ei[1].max()) + 1 if E else 0)
 
 

@@ -63,15 +63,22 @@ def test_work_items_cover_each_row_once():
     ei = random_coo(50, 50, 900, seed=3)
     ei = np.concatenate([ei, np.stack([np.arange(300) % 50, np.zeros(300, np.int64)])], axis=1)
     c = OG.csr_from_coo(ei[0], ei[1], 50, 50)
-    items, splits = OG.work_items(c["rowptr"], chunk=16)
+    items, splits, packed = OG.work_items(c["rowptr"], chunk=16, small=4)
     cover = np.zeros(ei.shape[1], np.int64)
     for r, b, e, p in items.tolist():
         assert c["rowptr"][r] <= b <= e <= c["rowptr"][r + 1] and e - b <= 16
         cover[b:e] += 1
+    deg = np.diff(c["rowptr"])
+    for r in packed.tolist():
+        assert deg[r] <= 4
+        cover[c["rowptr"][r]:c["rowptr"][r + 1]] += 1
     assert (cover == 1).all()
-    assert len({r for r, *_ in items.tolist()}) == 50
+    assert len({r for r, *_ in items.tolist()} | set(packed.tolist())) == 50
     n_split = sum(int(n) for _, _, n, _ in splits.tolist())
     assert (items[:n_split, 3] == np.arange(n_split)).all() and (items[n_split:, 3] == -1).all()
+    # longest first among the single-item rows and the packed rows
+    single = deg[items[n_split:, 0]]
+    assert (np.diff(single) <= 0).all() and (np.diff(deg[packed]) <= 0).all()
 
 
 # ------------------------------------------------------- related nodes
