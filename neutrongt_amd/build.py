@@ -29,6 +29,9 @@ HIPCC_FLAGS = [
     "-Wno-unused-function",
     # Packed FP32 VALU ops stay disabled in every kernel.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in ordinary VGPRs (gfx950 has one register file), so
+    # the softmax VALU work on score tiles needs no accvgpr copies.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     f"-I{INCLUDE}",
 ]
 

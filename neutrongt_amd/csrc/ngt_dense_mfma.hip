@@ -202,7 +202,7 @@ __global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
       }
       mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
       const float m_new = fmaxf(m, mx * s2);  // scale > 0: max commutes with scaling
-      const float alpha = exp2f(m - m_new);
+      const float alpha = __builtin_amdgcn_exp2f(m - m_new);
       if (__any(alpha != 1.f)) {
         l *= alpha;
 #pragma unroll
@@ -212,8 +212,8 @@ __global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
       s16x4 pb[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        pb[j] = pack4(exp2f(fmaf(st[4 * j], s2, -m_new)), exp2f(fmaf(st[4 * j + 1], s2, -m_new)),
-                      exp2f(fmaf(st[4 * j + 2], s2, -m_new)), exp2f(fmaf(st[4 * j + 3], s2, -m_new)));
+        pb[j] = pack4(__builtin_amdgcn_exp2f(fmaf(st[4 * j], s2, -m_new)), __builtin_amdgcn_exp2f(fmaf(st[4 * j + 1], s2, -m_new)),
+                      __builtin_amdgcn_exp2f(fmaf(st[4 * j + 2], s2, -m_new)), __builtin_amdgcn_exp2f(fmaf(st[4 * j + 3], s2, -m_new)));
       if constexpr (DH == 32) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) l += sum4(pb[j]);
@@ -245,13 +245,15 @@ __global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
 }
 
 // Column scores: part[h][j] = sum_i |S[h, i, j]|.  grid = (ceil(n_k/128), H);
-// wave w owns keys k0 .. k0+31; S = Q K^T tiles with rows = queries.
+// wave w owns keys k0 .. k0+31; S = Q K^T tiles with rows = queries, Q staged
+// 128 rows at a time in LDS (prefetched while the previous stage computes).
 template <int DH>
 __global__ __launch_bounds__(kBlock) void k_mf_scores(const bf16_t* __restrict__ q,
                                                       const bf16_t* __restrict__ k, int32_t n_q,
                                                       int32_t n_k, int32_t H, float scale,
                                                       float* __restrict__ part) {
   constexpr int NC = DH / 8;
+  __shared__ __align__(16) short qs[kSB][DH + 8];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
   const int half = lane >> 5;
@@ -264,16 +266,21 @@ __global__ __launch_bounds__(kBlock) void k_mf_scores(const bf16_t* __restrict__
   for (int j = 0; j < NC; ++j)
     kbv[j] = k_ok ? load4(k + (kj * H + h) * DH + 8 * j + 4 * half) : zero4();
   float s = 0.f;
-  for (int qb = 0; qb < n_q; qb += kT) {
-    const int64_t qr = qb + l32;
-    f32x16 st = zero16();
+  Stage<DH> pq;
+  pq.load(q, 0, n_q, H, h);
+  for (int qb = 0; qb < n_q; qb += kSB) {
+    __syncthreads();
+    pq.store_rows(qs);
+    __syncthreads();
+    if (qb + kSB < n_q) pq.load(q, qb + kSB, n_q, H, h);
+    for (int sub = 0; sub < kSB / kT && qb + sub * kT < n_q; ++sub) {
+      f32x16 st = zero16();
 #pragma unroll
-    for (int j = 0; j < NC; ++j) {
-      const s16x4 qa = qr < n_q ? load4(q + (qr * H + h) * DH + 8 * j + 4 * half) : zero4();
-      st = mfma(qa, kbv[j], st);
+      for (int j = 0; j < NC; ++j)
+        st = mfma(lds4(&qs[sub * kT + l32][8 * j + 4 * half]), kbv[j], st);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s += fabsf(st[i]);  // padded query rows are zero
     }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) s += fabsf(st[i]);  // padded query rows are zero
   }
   s += __shfl_xor(s, 32, kWave);
   if (k_ok && half == 0) part[int64_t(h) * n_k + kj] = s * scale;
@@ -351,10 +358,10 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_kv(
         const float4 lv = *reinterpret_cast<const float4*>(&ls[r]);
         const float4 dv4 = *reinterpret_cast<const float4*>(&dd[r]);
         // padded rows carry ls = +inf: exp2(-inf) = 0
-        const float p0 = exp2f(fmaf(st[4 * j], s2, -lv.x));
-        const float p1 = exp2f(fmaf(st[4 * j + 1], s2, -lv.y));
-        const float p2 = exp2f(fmaf(st[4 * j + 2], s2, -lv.z));
-        const float p3 = exp2f(fmaf(st[4 * j + 3], s2, -lv.w));
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(st[4 * j], s2, -lv.x));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(st[4 * j + 1], s2, -lv.y));
+        const float p2 = __builtin_amdgcn_exp2f(fmaf(st[4 * j + 2], s2, -lv.z));
+        const float p3 = __builtin_amdgcn_exp2f(fmaf(st[4 * j + 3], s2, -lv.w));
         pa[j] = pack4(p0, p1, p2, p3);
         dsa[j] = pack4(p0 * (dp[4 * j] - dv4.x), p1 * (dp[4 * j + 1] - dv4.y),
                        p2 * (dp[4 * j + 2] - dv4.z), p3 * (dp[4 * j + 3] - dv4.w));
@@ -434,12 +441,12 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_q(
       float ds[16];
       if (kb + r0 + kT <= n_k) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) ds[i] = exp2f(fmaf(st[i], s2, -L2)) * (dp[i] - Dq);
+        for (int i = 0; i < 16; ++i) ds[i] = __builtin_amdgcn_exp2f(fmaf(st[i], s2, -L2)) * (dp[i] - Dq);
       } else {  // tail tile: keys past n_k drop out
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int key = kb + r0 + 8 * (i / 4) + 4 * half + (i % 4);
-          ds[i] = key < n_k ? exp2f(fmaf(st[i], s2, -L2)) * (dp[i] - Dq) : 0.f;
+          ds[i] = key < n_k ? __builtin_amdgcn_exp2f(fmaf(st[i], s2, -L2)) * (dp[i] - Dq) : 0.f;
         }
       }
       s16x4 dsa[4];  // dS as A operand: A[q][key step row] from the D[key][q] layout
