@@ -172,6 +172,8 @@ def main(argv=None) -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--calib-copy", action="store_true",
                     help="run one 512 MiB device copy first (calibrates HBM byte counters)")
+    ap.add_argument("--graph", action="store_true",
+                    help="capture one step (all layers, fwd+bwd) in a HIP graph and time replays")
     args = ap.parse_args(argv)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -244,12 +246,28 @@ def main(argv=None) -> int:
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    run = step
+    if args.graph:
+        # Same kernels, launched from one captured graph (no per-launch host work).
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                step()
+        torch.cuda.current_stream(dev).wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        run = graph.replay
+        for _ in range(2):
+            run()
+        torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     ev0.record(stream)
     for i in range(args.steps):
-        step()
+        run()
     ev1.record(stream)
     torch.cuda.synchronize()
     ms_step = ev0.elapsed_time(ev1) / args.steps
@@ -314,7 +332,7 @@ def main(argv=None) -> int:
                          f"attention fwd+bwd, window n_q={cfg.n_q}, n_k={n_k}, E={E}, H={H}, "
                          f"d={d}, {dtype}"),
             "n_q": cfg.n_q, "n_k": n_k, "edges": E, "heads": H, "head_dim": d,
-            "layers": layers, "csr_build_ms": csr_ms,
+            "layers": layers, "csr_build_ms": csr_ms, "hip_graph": bool(args.graph),
         },
         "roofline": roof,
         "path_roofline": path,
