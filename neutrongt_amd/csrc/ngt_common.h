@@ -158,6 +158,43 @@ __device__ __forceinline__ void words_to_f32(const RowWords<T, DH>& r, float (&o
   for (int c = 0; c < DH; ++c) out[c] = word_elem<T, DH>(r, c);
 }
 
+template <typename T, int DH>
+__device__ __forceinline__ uint32_t row_word(const RowWords<T, DH>& r, int p) {
+  const uint4 w = r.w[p / 4];
+  return (p % 4 == 0) ? w.x : (p % 4 == 1) ? w.y : (p % 4 == 2) ? w.z : w.w;
+}
+
+// Dot product of two head slices held as raw words.  Every score of the sparse
+// path goes through this one function (operands in the same order), so the
+// backward recomputes bit-identical scores.  bf16: v_dot2c_f32_bf16 over
+// element pairs (products exact in fp32); fp32: fma chains.  Two interleaved
+// accumulators either way.
+typedef __bf16 ngt_bf16x2v __attribute__((ext_vector_type(2)));
+template <typename T, int DH>
+__device__ __forceinline__ float edge_dot(const RowWords<T, DH>& a, const RowWords<T, DH>& b) {
+  float s0 = 0.f, s1 = 0.f;
+  if constexpr (sizeof(T) == 2) {
+    constexpr int NW = DH / 2;
+#pragma unroll
+    for (int p = 0; p < NW; p += 2) {
+      s0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(ngt_bf16x2v, row_word<T, DH>(a, p)),
+                                           __builtin_bit_cast(ngt_bf16x2v, row_word<T, DH>(b, p)),
+                                           s0, false);
+      if (p + 1 < NW)
+        s1 = __builtin_amdgcn_fdot2_f32_bf16(
+            __builtin_bit_cast(ngt_bf16x2v, row_word<T, DH>(a, p + 1)),
+            __builtin_bit_cast(ngt_bf16x2v, row_word<T, DH>(b, p + 1)), s1, false);
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < DH; c += 2) {
+      s0 = fmaf(word_elem<T, DH>(a, c), word_elem<T, DH>(b, c), s0);
+      if (c + 1 < DH) s1 = fmaf(word_elem<T, DH>(a, c + 1), word_elem<T, DH>(b, c + 1), s1);
+    }
+  }
+  return s0 + s1;
+}
+
 // fp32 rows (partials, statistics) with 16-byte accesses when DH % 4 == 0.
 template <int DH>
 __device__ __forceinline__ void load_f32(const float* __restrict__ p, float (&out)[DH]) {

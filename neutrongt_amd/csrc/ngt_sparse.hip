@@ -112,9 +112,10 @@ __device__ __forceinline__ void fwd_packed(const T* __restrict__ q, const T* __r
                                            int H, float inv_scale, float lo, float hi, float eps,
                                            T* __restrict__ out, float* __restrict__ rinv,
                                            float* __restrict__ zbuf) {
-  float qr[DH], acc[DH];
+  RowWords<T, DH> qw;
+  float acc[DH];
   float z = 0.f;
-  load_row<T, DH>(q + (row * H + h) * DH, qr);
+  load_words<T, DH>(q + (row * H + h) * DH, qw);
 #pragma unroll
   for (int c = 0; c < DH; ++c) acc[c] = 0.f;
   const int beg = rowptr[row], end = rowptr[row + 1];
@@ -123,9 +124,7 @@ __device__ __forceinline__ void fwd_packed(const T* __restrict__ q, const T* __r
     RowWords<T, DH> kw, vw;
     load_words<T, DH>(k + (j * H + h) * DH, kw);
     load_words<T, DH>(v + (j * H + h) * DH, vw);
-    float kk[DH];
-    words_to_f32<T, DH>(kw, kk);
-    const float p = __expf(clampf(dot<DH>(qr, kk) * inv_scale, lo, hi));
+    const float p = __expf(clampf(edge_dot<T, DH>(qw, kw) * inv_scale, lo, hi));
     z += p;
 #pragma unroll
     for (int c = 0; c < DH; ++c) acc[c] = fmaf(p, word_elem<T, DH>(vw, c), acc[c]);
@@ -166,16 +165,15 @@ __global__ __launch_bounds__(kBlock) void k_fwd(
   const int h = ln.h;
   const int S = ln.S;
 
-  float qr[DH], acc[DH];
+  RowWords<T, DH> qw;
+  float acc[DH];
   float z = 0.f;
 #pragma unroll
   for (int c = 0; c < DH; ++c) acc[c] = 0.f;
-  if (ln.active) {
-    load_row<T, DH>(q + (row * H + h) * DH, qr);
-  } else {
-#pragma unroll
-    for (int c = 0; c < DH; ++c) qr[c] = 0.f;
-  }
+  if (ln.active)
+    load_words<T, DH>(q + (row * H + h) * DH, qw);
+  else
+    zero_words<T, DH>(qw);
 
   // Column indices of 64 edges are loaded at once (one coalesced access) and
   // handed to the slots with ds_bpermute; then the K/V rows of U edges per
@@ -202,9 +200,7 @@ __global__ __launch_bounds__(kBlock) void k_fwd(
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         if (ok[u]) {
-          float kk[DH];
-          words_to_f32<T, DH>(kw[u], kk);
-          const float p = __expf(clampf(dot<DH>(qr, kk) * inv_scale, lo, hi));
+          const float p = __expf(clampf(edge_dot<T, DH>(qw, kw[u]) * inv_scale, lo, hi));
           z += p;
 #pragma unroll
           for (int c = 0; c < DH; ++c) acc[c] = fmaf(p, word_elem<T, DH>(vw[u], c), acc[c]);
@@ -308,9 +304,10 @@ __device__ __forceinline__ void bwd_kv_packed(
     const T* __restrict__ g, const float2* __restrict__ rd, const int32_t* __restrict__ t_rowptr,
     const int32_t* __restrict__ t_col, int64_t row, int h, int H, float inv_scale, float lo,
     float hi, T* __restrict__ grad_k, T* __restrict__ grad_v, float* __restrict__ ds) {
-  float kr[DH], vr[DH], dk[DH], dv[DH];
-  load_row<T, DH>(k + (row * H + h) * DH, kr);
-  load_row<T, DH>(v + (row * H + h) * DH, vr);
+  RowWords<T, DH> krw, vrw;
+  float dk[DH], dv[DH];
+  load_words<T, DH>(k + (row * H + h) * DH, krw);
+  load_words<T, DH>(v + (row * H + h) * DH, vrw);
 #pragma unroll
   for (int c = 0; c < DH; ++c) {
     dk[c] = 0.f;
@@ -323,17 +320,9 @@ __device__ __forceinline__ void bwd_kv_packed(
     load_words<T, DH>(q + (i * H + h) * DH, qw);
     load_words<T, DH>(g + (i * H + h) * DH, gw);
     const float2 r = rd[i * H + h];
-    float sa0 = 0.f, sa1 = 0.f, sg0 = 0.f, sg1 = 0.f;
-#pragma unroll
-    for (int c = 0; c < DH; c += 2) {
-      sa0 = fmaf(word_elem<T, DH>(qw, c), kr[c], sa0);
-      sa1 = fmaf(word_elem<T, DH>(qw, c + 1), kr[c + 1], sa1);
-      sg0 = fmaf(word_elem<T, DH>(gw, c), vr[c], sg0);
-      sg1 = fmaf(word_elem<T, DH>(gw, c + 1), vr[c + 1], sg1);
-    }
-    const float a = (sa0 + sa1) * inv_scale;
+    const float a = edge_dot<T, DH>(qw, krw) * inv_scale;
     const float p = __expf(clampf(a, lo, hi));
-    const float dp = r.x * (sg0 + sg1) - r.y;
+    const float dp = r.x * edge_dot<T, DH>(gw, vrw) - r.y;
     const float da = (a >= lo && a <= hi) ? dp * p : 0.f;
     const float pr = p * r.x;
 #pragma unroll
@@ -378,21 +367,19 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
   const int h = ln.h;
   const int S = ln.S;
 
-  float kr[DH], vr[DH], dk[DH], dv[DH];
+  RowWords<T, DH> krw, vrw;
+  float dk[DH], dv[DH];
 #pragma unroll
   for (int c = 0; c < DH; ++c) {
     dk[c] = 0.f;
     dv[c] = 0.f;
   }
   if (ln.active) {
-    load_row<T, DH>(k + (row * H + h) * DH, kr);
-    load_row<T, DH>(v + (row * H + h) * DH, vr);
+    load_words<T, DH>(k + (row * H + h) * DH, krw);
+    load_words<T, DH>(v + (row * H + h) * DH, vrw);
   } else {
-#pragma unroll
-    for (int c = 0; c < DH; ++c) {
-      kr[c] = 0.f;
-      vr[c] = 0.f;
-    }
+    zero_words<T, DH>(krw);
+    zero_words<T, DH>(vrw);
   }
   constexpr int NV = RowWords<T, DH>::NV;
   constexpr int U = unroll_for(2 * NV, NGT_BWD_KV_WORDS);
@@ -419,17 +406,9 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
       for (int u = 0; u < U; ++u) {
         if (ok[u]) {
           // rows stay packed; elements are unpacked at each use
-          float sa0 = 0.f, sa1 = 0.f, sg0 = 0.f, sg1 = 0.f;
-#pragma unroll
-          for (int c = 0; c < DH; c += 2) {
-            sa0 = fmaf(word_elem<T, DH>(qw[u], c), kr[c], sa0);
-            sa1 = fmaf(word_elem<T, DH>(qw[u], c + 1), kr[c + 1], sa1);
-            sg0 = fmaf(word_elem<T, DH>(gw[u], c), vr[c], sg0);
-            sg1 = fmaf(word_elem<T, DH>(gw[u], c + 1), vr[c + 1], sg1);
-          }
-          const float a = (sa0 + sa1) * inv_scale;
+          const float a = edge_dot<T, DH>(qw[u], krw) * inv_scale;
           const float p = __expf(clampf(a, lo, hi));
-          const float dp = r[u].x * (sg0 + sg1) - r[u].y;
+          const float dp = r[u].x * edge_dot<T, DH>(gw[u], vrw) - r[u].y;
           const float da = (a >= lo && a <= hi) ? dp * p : 0.f;
           const float pr = p * r[u].x;
 #pragma unroll
