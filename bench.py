@@ -63,6 +63,16 @@ def sparse_kernel_bytes(name: str, cfg, n_k: int, E: int, adj) -> float:
     return float("nan")
 
 
+def dense_kernel_flops(name: str, n_q: int, n_k: int, H: int, d: int) -> float:
+    """Matrix-product flops one launch of a dense kernel has to do (2 per
+    multiply-add; each N_q x N_k x d product is 2 N_q N_k d per head):
+    fwd S = Q K^T, O = P V; scores recomputes S; bwd_kv S, dP^T = V G^T,
+    dV = P^T G, dK = dS^T Q; bwd_q S, dP, dQ = dS K."""
+    one = 2.0 * n_q * n_k * d * H
+    return one * {"dense_fwd": 2, "dense_scores": 1, "dense_bwd_kv": 4,
+                  "dense_bwd_q": 3}.get(name, float("nan"))
+
+
 def path_bytes(cfg, n_k: int, E: int) -> float:
     """Compulsory bytes of one layer's forward + backward (each tensor once):
     fwd Q,O,K,V + CSR + Zinv + node_score; bwd Q,O,dO,K,V + {Zinv,D} + both CSRs
@@ -161,6 +171,83 @@ def cpu_baseline(cfg, ei_np, n_k, target_s: float = 3.0):
     }
 
 
+def model_step_bench(args, cfg, layers: int, dev) -> dict:
+    """The window training step of train_eval.py:255-300 on one GPU: the
+    node-level Graphormer (cfg's hidden size, heads and layers; FFN width =
+    hidden as in the GPH presets) over one synthetic window, bf16 autocast,
+    NLL over the window's training nodes, backward, AdamW.  Related keys' K/V
+    come from a per-layer cache.  The loss is read back every step, as the
+    reference's loop does (loss.item())."""
+    import numpy as np
+    import torch
+
+    from neutrongt_amd import _lib
+    from neutrongt_amd import synthetic as S
+    from neutrongt_amd.encoder import WindowGraphormer, window_step
+
+    H, d = cfg.n_heads, cfg.head_dim
+    hidden = H * d
+    n_classes = 47
+    feat = cfg.feat_dim or hidden
+    ei_np, n_k = S.make_window_edges(cfg)
+    E = int(ei_np.shape[1])
+    R = n_k - cfg.n_q
+    g = torch.Generator(device="cpu").manual_seed(S.SEED)
+    x = torch.randn(cfg.n_q, feat, generator=g).to(dev)
+    labels = torch.randint(0, n_classes, (cfg.n_q,), generator=g).to(dev)
+    train_mask = (torch.rand(cfg.n_q, generator=g) < 0.5).to(dev)
+    cache = [tuple((0.05 * torch.randn(R, H, d, generator=g)).to(torch.bfloat16).to(dev)
+                   for _ in range(2)) for _ in range(layers)] if R else None
+    ei = torch.from_numpy(ei_np).to(dev)
+    torch.manual_seed(S.SEED)
+    model = WindowGraphormer(layers, H, feat, hidden, n_classes, dropout_rate=0.3,
+                             input_dropout_rate=0.1, attention_dropout_rate=0.5,
+                             ffn_dim=hidden).to(dev).train()
+    n_params = sum(p.numel() for p in model.parameters())
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, weight_decay=0.01)
+    _log(f"[bench] window step: {layers} layers, hidden {hidden}, {n_params} parameters, "
+         f"n_q={cfg.n_q} n_k={n_k} E={E}")
+
+    def step():
+        loss, _ = window_step(model, opt, x, ei, labels, train_mask, cache, torch.bfloat16)
+        return loss.item()
+
+    for _ in range(max(args.warmup, 1)):
+        step()
+    torch.cuda.synchronize()
+    times, losses = [], []
+    for _ in range(args.steps):
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        losses.append(step())
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t)
+    ms = 1e3 * statistics.median(times)
+    _lib.timing_enable(True)
+    _lib.timing_summary()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    summ = _lib.timing_summary()
+    _lib.timing_enable(False)
+    attn_ms = sum(v[1] for v in summ.values()) / args.steps
+    _log(f"[bench] window step {ms:.2f} ms (median of {args.steps}), attention kernels "
+         f"{attn_ms:.2f} ms/step, loss {losses[0]:.4f} -> {losses[-1]:.4f}")
+    return {
+        "metric": "window training step time (encoder fwd + NLL + bwd + AdamW)",
+        "value": ms, "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": (f"{cfg.name} window step: {layers}-layer Graphormer, hidden "
+                                f"{hidden}, {H} heads, ffn {hidden}, {n_params} parameters, "
+                                f"n_q={cfg.n_q}, n_k={n_k}, E={E}, bf16 autocast, AdamW"),
+                   "layers": layers, "parameters": n_params, "edges": E},
+        "attention_ms_per_step": attn_ms,
+        "edges_per_s_in_step": layers * E / (ms * 1e-3),
+        "losses": [losses[0], losses[-1]],
+    }
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -174,6 +261,9 @@ def main(argv=None) -> int:
                     help="run one 512 MiB device copy first (calibrates HBM byte counters)")
     ap.add_argument("--graph", action="store_true",
                     help="capture one step (all layers, fwd+bwd) in a HIP graph and time replays")
+    ap.add_argument("--model", action="store_true",
+                    help="time the whole window training step instead (encoder projections, "
+                         "LayerNorm, FFN and attention, NLL, backward, AdamW) in bf16 autocast")
     args = ap.parse_args(argv)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -195,6 +285,12 @@ def main(argv=None) -> int:
     layers = args.layers or cfg.layers
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.model:
+        if cfg.dense:
+            print("--model runs the sparse window encoder; pick a sparse --config", file=sys.stderr)
+            return 2
+        print(json.dumps(model_step_bench(args, cfg, layers, dev)), flush=True)
+        return 0
     H, d = cfg.n_heads, cfg.head_dim
     scale = math.sqrt(d)
 
@@ -288,10 +384,11 @@ def main(argv=None) -> int:
     dom = max(summ, key=lambda n: summ[n][1])
     dom_avg_s = summ[dom][1] / summ[dom][0] * 1e-3
     if cfg.dense:
-        flops = 4.0 * cfg.n_q * n_k * d * H  # PV-class: P V (fwd) ~ 2 N^2 d H per GEMM-like op
+        flops = dense_kernel_flops(dom, cfg.n_q, n_k, H, d)
         roof = {"bound": "mfma", "achieved": flops / dom_avg_s / 1e12, "peak": MFMA_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": flops / dom_avg_s / 1e12 / MFMA_BF16_TFLOPS,
-                "traffic": None, "kernel": dom}
+                "traffic": None, "kernel": dom, "flops_per_launch": flops,
+                "avg_launch_us": dom_avg_s * 1e6}
         path = None
     else:
         kb = sparse_kernel_bytes(dom, cfg, n_k, E, adj)

@@ -2,8 +2,13 @@
 
     python -m neutrongt_amd.profsum trace <dir>/run_kernel_stats.csv
     python -m neutrongt_amd.profsum pmc <fetch_dir> <write_dir> [<tcc_dir>]
+    python -m neutrongt_amd.profsum counters <dir>
+    python -m neutrongt_amd.profsum traffic <config> <fetch_dir> <write_dir>
 
-``trace`` prints per-kernel call count and mean/min/max duration.  ``pmc``
+``trace`` prints per-kernel call count and mean/min/max duration.  ``counters``
+prints the mean per dispatch of every counter of one ``--pmc`` run for the
+library's kernels.  ``traffic`` prints the calibrated read/write bytes per
+dispatch as the JSON records bench.py reads (keyed ``config:timer name``).  ``pmc``
 prints per-kernel FETCH_SIZE / WRITE_SIZE (KiB per dispatch, mean over the
 dispatches of that kernel) and their values scaled by the calibration factor
 read from the largest plain device copy in the same run (a 512 MiB
@@ -81,11 +86,60 @@ def pmc_table(fetch_dir: str, write_dir: str, tcc_dir: str | None = None) -> str
     return "\n".join(out)
 
 
+# kernel symbol -> the timer name the library records for its launches
+TIMER_NAMES = {"k_fwd": "sparse_fwd", "k_bwd_kv": "sparse_bwd_kv", "k_bwd_q": "sparse_bwd_q",
+               "k_rowstat": "sparse_rowstat", "k_mf_fwd": "dense_fwd",
+               "k_mf_bwd_kv": "dense_bwd_kv", "k_mf_bwd_q": "dense_bwd_q"}
+
+
+def _calibration(fe, wr):
+    copy = [k for k in fe if "copyBuffer" in k]
+    if not copy:
+        raise SystemExit("no calibration copy in the run (bench.py --calib-copy)")
+    f_max = max(max(fe[k]["FETCH_SIZE"]) for k in copy)
+    w_max = max(max(wr[k]["WRITE_SIZE"]) for k in copy if k in wr)
+    return 512 * 1024.0 / f_max, 512 * 1024.0 / w_max
+
+
+def counters_table(d: str) -> str:
+    vals = _counters(d)
+    names = sorted({c for k in vals for c in vals[k]})
+    out = ["| kernel | dispatches | " + " | ".join(names) + " |",
+           "|---|---|" + "---|" * len(names)]
+    for k, c in vals.items():
+        if "ngt::" not in k:
+            continue
+        n = max(len(v) for v in c.values())
+        cells = [f"{sum(c[m]) / len(c[m]):.4g}" if c.get(m) else "" for m in names]
+        out.append(f"| {short_name(k)} | {n} | " + " | ".join(cells) + " |")
+    return "\n".join(out)
+
+
+def traffic_json(config: str, fetch_dir: str, write_dir: str) -> str:
+    import json
+
+    fe, wr = _counters(fetch_dir), _counters(write_dir)
+    cf, cw = _calibration(fe, wr)
+    rec = {}
+    for k, c in fe.items():
+        base = short_name(k).split("<")[0]
+        if base not in TIMER_NAMES or k not in wr:
+            continue
+        f = sum(c["FETCH_SIZE"]) / len(c["FETCH_SIZE"]) * 1024 * cf
+        w = sum(wr[k]["WRITE_SIZE"]) / len(wr[k]["WRITE_SIZE"]) * 1024 * cw
+        rec[f"{config}:{TIMER_NAMES[base]}"] = {"read_bytes": round(f), "write_bytes": round(w)}
+    return json.dumps(rec, indent=1)
+
+
 def main(argv):
     if len(argv) >= 2 and argv[0] == "trace":
         print(trace_table(argv[1]))
     elif len(argv) >= 3 and argv[0] == "pmc":
         print(pmc_table(argv[1], argv[2], argv[3] if len(argv) > 3 else None))
+    elif len(argv) >= 2 and argv[0] == "counters":
+        print(counters_table(argv[1]))
+    elif len(argv) >= 4 and argv[0] == "traffic":
+        print(traffic_json(argv[1], argv[2], argv[3]))
     else:
         print(__doc__)
         return 2

@@ -1,0 +1,148 @@
+"""The window encoder (projections, LayerNorm, FFN and the HIP attention core)
+against the same encoder on the CPU whose attention is the oracle: log-probs,
+per-layer node scores and every parameter gradient."""
+import pytest
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from oracle import attention as OA
+from tests._util import TOL, assert_close, assert_parity, random_coo, relerr
+
+pytestmark = pytest.mark.gpu
+
+N_Q, R, H, D_HEAD, FEAT, CLASSES = 160, 40, 4, 8, 24, 5
+
+
+class OracleCore(nn.Module):
+    """local_attn stand-in that runs the oracle's restatement of the
+    reference's sparse attention.  bf16 inputs are computed in fp32 and the
+    output rounded back to bf16 (what the HIP core does)."""
+
+    def __init__(self, num_heads):
+        super().__init__()
+        self.num_heads = num_heads
+
+    def forward(self, q, k, v, attn_bias=None, edge_index=None, attn_type=None, mask=None,
+                pruning_mask=None):
+        n_q, n_k = q.shape[1], k.shape[1]
+        out_dtype = q.dtype
+        if out_dtype == torch.bfloat16:
+            q, k, v = q.float(), k.float(), v.float()
+        if n_k > n_q:  # the restatement is square: queries are the first n_q rows
+            q = torch.cat([q, q.new_zeros(1, n_k - n_q, *q.shape[2:])], dim=1)
+        x, score = OA.sparse_attention_bias(q, k, v, edge_index, self.num_heads)
+        return x[:n_q].reshape(1, n_q, -1).to(out_dtype), score
+
+
+def _build(dtype=torch.float32, seed=0):
+    from neutrongt_amd.encoder import WindowGraphormer
+
+    torch.manual_seed(seed)
+    model = WindowGraphormer(2, H, FEAT, H * D_HEAD, CLASSES, ffn_dim=48)
+    # weights large enough that scores span the clamp range (the default init
+    # is 0.02/sqrt(layers), which makes every score ~0)
+    for m in model.modules():
+        if isinstance(m, nn.Linear):
+            nn.init.normal_(m.weight, std=1.5 / m.in_features ** 0.5)
+            nn.init.normal_(m.bias, std=0.1)
+    g = torch.Generator().manual_seed(seed + 1)
+    x = torch.randn(N_Q, FEAT, generator=g)
+    ei = torch.from_numpy(random_coo(N_Q, N_Q + R, 900, seed=seed))
+    cache = [tuple(torch.randn(R, H, D_HEAD, generator=g) for _ in range(2)) for _ in range(2)]
+    labels = torch.randint(0, CLASSES, (N_Q,), generator=g)
+    mask = torch.rand(N_Q, generator=g) < 0.6
+    ref = WindowGraphormer(2, H, FEAT, H * D_HEAD, CLASSES, ffn_dim=48).to(dtype)
+    ref.load_state_dict({k: v.to(dtype) for k, v in model.state_dict().items()})
+    for layer in ref.layers:
+        layer.self_attention.local_attn = OracleCore(H)
+    return model, ref, x, ei, cache, labels, mask
+
+
+def _run(model, x, ei, cache, labels, mask, autocast=None):
+    model.zero_grad(set_to_none=True)
+    if autocast is not None:
+        with torch.autocast("cuda", dtype=autocast):
+            out, scores = model(x, ei, "sparse", cache)
+    else:
+        out, scores = model(x, ei, "sparse", cache)
+    loss = F.nll_loss(out[mask], labels[mask])
+    loss.backward()
+    grads = {n: p.grad.detach().double().cpu() for n, p in model.named_parameters()}
+    return out.detach(), [s.cpu() for s in scores], loss.detach(), grads
+
+
+def test_encoder_fp32_matches_oracle_encoder():
+    model, ref32, x, ei, cache, labels, mask = _build()
+    _, ref64, *_ = _build(torch.float64)
+    dev = torch.device("cuda")
+    model = model.to(dev)
+    gpu = _run(model, x.to(dev), ei.to(dev), [tuple(t.to(dev) for t in c) for c in cache],
+               labels.to(dev), mask.to(dev))
+    c32 = _run(ref32, x, ei, cache, labels, mask)
+    c64 = _run(ref64, x.double(), ei, [tuple(t.double() for t in c) for c in cache], labels, mask)
+    assert_parity(gpu[0], c32[0], c64[0], torch.float32, "log_probs")
+    for i, (a, b, c) in enumerate(zip(gpu[1], c32[1], c64[1])):
+        assert a.shape == b.shape
+        assert_parity(a, b, c, torch.float32, f"node_score layer {i}")
+    assert_parity(gpu[2], c32[2], c64[2], torch.float32, "loss")
+    for n in gpu[3]:
+        assert_parity(gpu[3][n], c32[3][n], c64[3][n], torch.float32, f"grad {n}")
+
+
+def test_encoder_bf16_autocast_matches_oracle_encoder():
+    """bf16 autocast: the encoder with the HIP core against the same encoder,
+    same GEMMs (bf16 autocast on the GPU), with the oracle as its attention
+    core, at the bf16 tolerance.  Against the fp32 encoder on the CPU the
+    difference is dominated by the bf16 GEMMs themselves (measured ~2.5e-2 on
+    LayerNorm-weight gradients), so that comparison is a 6e-2 sanity bound."""
+    model, ref32, x, ei, cache, labels, mask = _build(seed=3)
+    dev = torch.device("cuda")
+    orc = _build(seed=3)[1].to(dev)  # fp32 weights, oracle core, on the GPU
+    model = model.to(dev)
+    cache_bf = [tuple(t.to(torch.bfloat16) for t in c) for c in cache]
+    args = (x.to(dev), ei.to(dev), [tuple(t.to(dev) for t in c) for c in cache_bf],
+            labels.to(dev), mask.to(dev))
+    gpu = _run(model, *args, autocast=torch.bfloat16)
+    ref = _run(orc, *args, autocast=torch.bfloat16)
+    assert_close(gpu[0], ref[0], torch.bfloat16, "log_probs")
+    assert_close(gpu[2], ref[2], torch.bfloat16, "loss")
+    for n in gpu[3]:
+        assert_close(gpu[3][n], ref[3][n], torch.bfloat16, f"grad {n}")
+    cpu = _run(ref32, x, ei, [tuple(t.float() for t in c) for c in cache_bf], labels, mask)
+    assert relerr(gpu[0], cpu[0]) <= 6e-2
+    for n in gpu[3]:
+        assert relerr(gpu[3][n], cpu[3][n]) <= 6e-2, n
+
+
+def test_window_step_trains_and_matches_the_first_loss():
+    from neutrongt_amd.encoder import window_step
+
+    model, ref32, x, ei, cache, labels, mask = _build(seed=5)
+    dev = torch.device("cuda")
+    model = model.to(dev)
+    opt = torch.optim.AdamW(model.parameters(), lr=3e-3, weight_decay=0.01)
+    xs, eis = x.to(dev), ei.to(dev)
+    cs = [tuple(t.to(dev) for t in c) for c in cache]
+    ls, ms = labels.to(dev), mask.to(dev)
+    want = _run(ref32, x, ei, cache, labels, mask)[2]
+    losses = []
+    for _ in range(20):
+        loss, score = window_step(model, opt, xs, eis, ls, ms, cs)
+        losses.append(loss.item())
+    assert abs(losses[0] - want.item()) <= TOL[torch.float32] * abs(want.item())
+    assert losses[-1] < 0.7 * losses[0]
+    assert score.shape[0] == int(ei[1].max()) + 1
+
+
+def test_kv_cache_shape_is_checked():
+    from neutrongt_amd.encoder import WindowGraphormer
+
+    model = WindowGraphormer(1, H, FEAT, H * D_HEAD, CLASSES).cuda()
+    x = torch.randn(10, FEAT, device="cuda")
+    ei = torch.tensor([[0, 1], [1, 0]], device="cuda")
+    bad = [(torch.zeros(3, H, D_HEAD + 1, device="cuda"),) * 2]
+    with pytest.raises(ValueError):
+        model(x, ei, "sparse", bad)
+    with pytest.raises(ValueError):
+        model(x, ei, "sparse", bad * 2)
