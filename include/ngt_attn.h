@@ -225,6 +225,38 @@ int ngt_gather_rows(const void* src, int64_t n_src, const int64_t* idx, int64_t 
                     int64_t row_bytes, void* dst, int32_t* bad, void* stream);
 
 /*
+ * Induced window subgraph with relabelling, on the GPU.
+ *
+ * ngt_subgraph_coo replaces torch_geometric.utils.subgraph(subset, edge_index,
+ *   relabel_nodes=True, num_nodes) as called at
+ *   NeutronGT/core/node_level_pipeline/window_state.py:82,127 and
+ *   NeutronGT/core/metisPartition.py:280,290: edge e of edge_index (int64
+ *   [2, n_edges], row 0 at edge_index, row 1 at edge_index + n_edges) is kept
+ *   iff both endpoints are in subset; kept edges keep their order; node ids
+ *   become positions in subset.
+ * ngt_subgraph_csr replaces _subgraph_from_csr,
+ *   NeutronGT/core/node_level_pipeline/window_state.py:92-119: for each node of
+ *   node_set in order, its neighbours col[rowptr[g] .. rowptr[g+1]) (n_col
+ *   entries in col) that are in node_set, in CSR order; out row 0 = the row
+ *   node's position, row 1 = the neighbour's position.
+ *
+ * out: int64 [2, cap] (row 1 at out + cap), may be NULL to only count.
+ * result: device int64[2] = {number of kept edges, error bits}; error bits:
+ *   1 set node out of range, 2 duplicate set node, 4 edge endpoint out of
+ *   range, 8 CSR row outside col.  Entries past cap are not written; call once
+ *   with out = NULL, read result, then again with cap = result[0].
+ * Workspace from ngt_subgraph_workspace_bytes(n_nodes, n_edges (COO form, else
+ * 0), n_set, ...); the map it holds is rebuilt by every call.
+ */
+int ngt_subgraph_workspace_bytes(int64_t n_nodes, int64_t n_edges, int32_t n_set, size_t* bytes);
+int ngt_subgraph_coo(const int64_t* edge_index, int64_t n_edges, int64_t n_nodes,
+                     const int64_t* subset, int32_t n_subset, int64_t* out, int64_t cap,
+                     int64_t* result, void* workspace, size_t workspace_bytes, void* stream);
+int ngt_subgraph_csr(const int64_t* rowptr, const int64_t* col, int64_t n_col, int64_t n_nodes,
+                     const int64_t* node_set, int32_t n_set, int64_t* out, int64_t cap,
+                     int64_t* result, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Per-kernel timing (no counterpart in the reference: instrumentation for the
  * benchmark's roofline figure).  While enabled, every kernel launch of this
  * library is bracketed by a hipEvent pair on its stream.  ngt_timing_summary

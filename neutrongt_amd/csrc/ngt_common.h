@@ -299,6 +299,12 @@ struct KernelTimer {
 
 }  // namespace ngt
 
+#define NGT_CHECK_OK(expr)                                                               \
+  do {                                                                                   \
+    const int _rc = (expr);                                                              \
+    if (_rc != NGT_OK) return _rc;                                                       \
+  } while (0)
+
 #define NGT_HIP_CHECK(expr)                                                              \
   do {                                                                                   \
     hipError_t _e = (expr);                                                              \

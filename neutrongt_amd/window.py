@@ -10,10 +10,14 @@
   adj_weights               NeutronGT/core/ppr_preprocess.py:30-71 weight rule,
                             with a stable neighbour order (the reference's
                             argsort at :53 is unstable)
+  subgraph                  GPU (ngt_subgraph_coo); torch_geometric subgraph with
+                            relabel_nodes=True as called at window_state.py:82,127
+                            and metisPartition.py:280,290
+  subgraph_from_csr         GPU (ngt_subgraph_csr); window_state.py:92-119
 
 The duplicate bookkeeping is host logic in the reference (torch unique/isin on
 CPU tensors) and stays torch code here; the per-element work (related-node
-ranking, feature gathers) runs as HIP kernels.
+ranking, induced subgraphs, feature gathers) runs as HIP kernels.
 """
 from __future__ import annotations
 
@@ -119,6 +123,69 @@ def gather_rows(src: torch.Tensor, idx: torch.Tensor, out: torch.Tensor | None =
                                    int(idx.numel()), int(row_bytes), out.data_ptr(),
                                    bad.data_ptr(), stream))
     return out, bad
+
+
+_SUBGRAPH_ERRORS = {1: "node id out of range in the node set", 2: "duplicate node in the node set",
+                    4: "edge endpoint out of range", 8: "CSR row outside col"}
+
+
+def _run_subgraph(call, n_nodes: int, n_edges: int, n_set: int, device):
+    """Count pass, one read-back, then the emit pass into an exact [2, n] tensor."""
+    lib = _lib.load()
+    nb = C.c_size_t()
+    _lib.check(lib.ngt_subgraph_workspace_bytes(n_nodes, n_edges, n_set, C.byref(nb)))
+    ws = torch.empty(max(nb.value, 1), dtype=torch.uint8, device=device)
+    result = torch.zeros(2, dtype=torch.int64, device=device)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    _lib.check(call(None, 0, result.data_ptr(), ws.data_ptr(), nb.value, stream))
+    n, err = (int(v) for v in result.tolist())
+    if err:
+        why = ", ".join(m for b, m in _SUBGRAPH_ERRORS.items() if err & b)
+        raise IndexError(f"subgraph: {why}")
+    out = torch.empty(2, n, dtype=torch.int64, device=device)
+    if n:
+        _lib.check(call(out.data_ptr(), n, result.data_ptr(), ws.data_ptr(), nb.value, stream))
+    return out
+
+
+def subgraph(subset: torch.Tensor, edge_index: torch.Tensor, num_nodes: int) -> torch.Tensor:
+    """torch_geometric.utils.subgraph(subset, edge_index, relabel_nodes=True,
+    num_nodes)[0] on the GPU (window_state.py:82,127; metisPartition.py:280,290):
+    the edges with both endpoints in ``subset``, in their original order, each
+    node renamed to its position in ``subset``.  int64 [2, E_sub].  Raises
+    IndexError on ids outside [0, num_nodes) or a repeated subset node."""
+    lib = _lib.load()
+    if not (subset.is_cuda and edge_index.is_cuda):
+        raise ValueError("subgraph: tensors must be on the GPU")
+    if edge_index.dim() != 2 or edge_index.shape[0] != 2:
+        raise ValueError(f"subgraph: edge_index must be [2, E], got {tuple(edge_index.shape)}")
+    subset = subset.to(torch.int64).contiguous()
+    ei = edge_index.to(torch.int64).contiguous()
+    E, n_set = int(ei.shape[1]), int(subset.numel())
+    return _run_subgraph(
+        lambda out, cap, res, ws, wb, st: lib.ngt_subgraph_coo(
+            ei.data_ptr(), E, int(num_nodes), subset.data_ptr(), n_set, out, cap, res, ws, wb, st),
+        int(num_nodes), E, n_set, subset.device)
+
+
+def subgraph_from_csr(node_set: torch.Tensor, rowptr: torch.Tensor, col: torch.Tensor) -> torch.Tensor:
+    """_subgraph_from_csr (window_state.py:92-119) on the GPU: for each node of
+    ``node_set`` in order, its CSR neighbours (CSR order) inside the set, as
+    (position of the row node, position of the neighbour).  int64 [2, E_sub]."""
+    lib = _lib.load()
+    if not (node_set.is_cuda and rowptr.is_cuda and col.is_cuda):
+        raise ValueError("subgraph_from_csr: tensors must be on the GPU")
+    node_set = node_set.to(torch.int64).contiguous()
+    rowptr = rowptr.to(torch.int64).contiguous()
+    col = col.to(torch.int64).contiguous()
+    n_nodes, n_set = int(rowptr.numel()) - 1, int(node_set.numel())
+    if n_nodes < 0:
+        raise ValueError("subgraph_from_csr: rowptr must have n_nodes + 1 entries")
+    return _run_subgraph(
+        lambda out, cap, res, ws, wb, st: lib.ngt_subgraph_csr(
+            rowptr.data_ptr(), col.data_ptr(), int(col.numel()), n_nodes, node_set.data_ptr(), n_set,
+            out, cap, res, ws, wb, st),
+        n_nodes, 0, n_set, node_set.device)
 
 
 def assemble_window_features(feature: torch.Tensor, cache: torch.Tensor, dup_index: torch.Tensor,

@@ -16,6 +16,7 @@ Every function returns plain numpy arrays and is bit-exact by construction
                             neighbour order fixed stable, see the docstring)
   subgraph_coo              torch_geometric.utils.subgraph(relabel_nodes=True)
                             semantics as used at window_state.py:127
+  subgraph_from_csr         NeutronGT/core/node_level_pipeline/window_state.py:92-119
 """
 from __future__ import annotations
 
@@ -189,3 +190,34 @@ def subgraph_coo(partition, edge_index, num_nodes: int):
     pos[part] = np.arange(part.shape[0])
     keep = (pos[ei[0]] >= 0) & (pos[ei[1]] >= 0)
     return np.stack([pos[ei[0][keep]], pos[ei[1][keep]]])
+
+
+def subgraph_from_csr(node_set, rowptr, col):
+    """_subgraph_from_csr (window_state.py:92-119), restated with numpy: the set
+    is sorted once; for each set node in set order, its CSR neighbours are
+    looked up by binary search in the sorted set and the matches emitted as
+    (position of the row node, original position of the neighbour)."""
+    node_set = np.asarray(node_set, np.int64)
+    rowptr = np.asarray(rowptr, np.int64)
+    col = np.asarray(col, np.int64)
+    if node_set.size == 0:
+        return np.zeros((2, 0), np.int64)
+    sort_order = np.argsort(node_set, kind="stable")
+    sorted_nodes = node_set[sort_order]
+    rows, cols = [], []
+    for local_src, g in enumerate(node_set.tolist()):
+        nbrs = col[rowptr[g]:rowptr[g + 1]]
+        if nbrs.size == 0:
+            continue
+        p = np.searchsorted(sorted_nodes, nbrs)
+        inb = p < sorted_nodes.size
+        matched = np.zeros(nbrs.size, bool)
+        matched[inb] = sorted_nodes[p[inb]] == nbrs[inb]
+        if not matched.any():
+            continue
+        local_dst = sort_order[p[matched]]
+        rows.append(np.full(local_dst.size, local_src, np.int64))
+        cols.append(local_dst.astype(np.int64))
+    if not rows:
+        return np.zeros((2, 0), np.int64)
+    return np.stack([np.concatenate(rows), np.concatenate(cols)])

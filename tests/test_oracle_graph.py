@@ -189,3 +189,50 @@ def test_subgraph_relabel_by_position():
     sub = OG.subgraph_coo(np.array([4, 3, 0]), ei, 10)
     # kept edges in global order: (0,3), (3,0), (4,3) -> positions (2,1), (1,2), (0,1)
     assert sub.tolist() == [[2, 1, 0], [1, 2, 1]]
+
+
+def _csr_of(ei, n):
+    """Row-major CSR of a COO (rows = edge_index[0]), neighbours in edge order,
+    and the COO listed in that CSR order (graph_data.py:28-35 convention)."""
+    order = np.argsort(ei[0], kind="stable")
+    rowptr = np.zeros(n + 1, np.int64)
+    rowptr[1:] = np.cumsum(np.bincount(ei[0], minlength=n))
+    return rowptr, ei[1][order], ei[:, order]
+
+
+def test_subgraph_from_csr_hand_derived():
+    # CSR of 6 nodes; set [4, 1, 3]: row 4 -> (1, 3), row 1 -> (4, 2, 4), row 3 -> (5)
+    rowptr = np.array([0, 1, 4, 5, 6, 8, 8])
+    col = np.array([1, 4, 2, 4, 0, 5, 1, 3])
+    out = OG.subgraph_from_csr(np.array([4, 1, 3]), rowptr, col)
+    assert out.tolist() == [[0, 0, 1, 1], [1, 2, 0, 0]]
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_subgraph_from_csr_matches_brute_force_and_coo_form(seed):
+    rng = np.random.default_rng(seed)
+    n = 300
+    ei = rng.integers(0, n, (2, 3000))
+    rowptr, col, ei_csr = _csr_of(ei, n)
+    node_set = rng.permutation(n)[:90]
+    got = OG.subgraph_from_csr(node_set, rowptr, col)
+    where = {int(g): i for i, g in enumerate(node_set)}
+    want = [(i, where[int(c)]) for i, g in enumerate(node_set)
+            for c in col[rowptr[g]:rowptr[g + 1]] if int(c) in where]
+    assert got.T.tolist() == [list(t) for t in want]
+    # sorted set: the CSR form lists edges in the same order as the COO form
+    # over the CSR-ordered edge list
+    s = np.sort(node_set)
+    np.testing.assert_array_equal(OG.subgraph_from_csr(s, rowptr, col),
+                                  OG.subgraph_coo(s, ei_csr, n))
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_subgraph_coo_matches_brute_force(seed):
+    rng = np.random.default_rng(seed + 10)
+    n = 200
+    ei = rng.integers(0, n, (2, 2500))
+    subset = rng.permutation(n)[:70]
+    where = {int(g): i for i, g in enumerate(subset)}
+    want = [(where[int(a)], where[int(b)]) for a, b in ei.T if int(a) in where and int(b) in where]
+    assert OG.subgraph_coo(subset, ei, n).T.tolist() == [list(t) for t in want]
