@@ -171,6 +171,117 @@ def cpu_baseline(cfg, ei_np, n_k, target_s: float = 3.0):
     }
 
 
+def prep_bench(args, cfg, dev) -> dict:
+    """Assembly of one window on the GPU, from the global graph to the
+    attention inputs: related-node selection (metisPartition.py:397-425), the
+    induced subgraph in both reference orders (window_state.py:92-127), the
+    window CSR and schedules, and the feature gather (train_eval.py:234-242).
+    The global graph is a Chung-Lu graph with cfg's node count and mean degree,
+    drawn on the GPU (duplicate pairs kept); the partition is a seeded random
+    set of cfg.n_q nodes, sorted.  The oracle's CPU restatement of the same
+    steps (the reference's host path) is timed once on the host beside it."""
+    import numpy as np
+    import torch
+
+    from neutrongt_amd import chunk_for_heads, small_for_heads
+    from neutrongt_amd import synthetic as S
+    from neutrongt_amd import window as W
+    from neutrongt_amd.csr import WindowAdjacency
+
+    n = cfg.n_global
+    g = torch.Generator(device=dev).manual_seed(S.SEED)
+    w = (torch.arange(n, device=dev, dtype=torch.float64) + 1.0) ** (-1.0 / (cfg.gamma - 1.0))
+    cdf = torch.cumsum(w / w.sum(), 0)
+    cdf[-1] = 1.0
+    m = int(n * cfg.mean_degree / 2)
+    a = torch.searchsorted(cdf, torch.rand(m, generator=g, device=dev, dtype=torch.float64),
+                           right=True)
+    b = torch.searchsorted(cdf, torch.rand(m, generator=g, device=dev, dtype=torch.float64),
+                           right=True)
+    keep = a != b
+    rows = torch.cat([a[keep], b[keep]])
+    cols = torch.cat([b[keep], a[keep]])
+    del a, b, keep, w, cdf
+    order = torch.argsort(rows, stable=True)
+    rows, col = rows[order], cols[order]
+    del cols, order
+    rowptr = torch.zeros(n + 1, dtype=torch.int64, device=dev)
+    rowptr[1:] = torch.cumsum(torch.bincount(rows, minlength=n), 0)
+    coo = torch.stack([rows, col])
+    del rows
+    xadj = rowptr.to(torch.int32)
+    adjncy = col.to(torch.int32)
+    eweights = torch.randint(1, 4, (col.numel(),), generator=g, device=dev, dtype=torch.int32)
+    part = torch.sort(torch.randperm(n, generator=g, device=dev)[: cfg.n_q]).values
+    feat_dim = cfg.feat_dim or 128
+    features = torch.randn(n, feat_dim, generator=g, device=dev)
+    pct = max(cfg.related_per_query, 1)
+    H = cfg.n_heads
+    E_glob = int(col.numel())
+    _log(f"[bench] prep: global graph n={n} directed entries={E_glob}, window {cfg.n_q} nodes, "
+         f"related {pct}%")
+
+    def timed(fn, reps=5):
+        out = fn()
+        ts = []
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            out = fn()
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t)
+        return out, 1e3 * statistics.median(ts)
+
+    win, t_rel = timed(lambda: W.merge_related_nodes(xadj, adjncy, eweights, part, pct))
+    sub_csr, t_csr = timed(lambda: W.subgraph_from_csr(win, rowptr, col))
+    sub_coo, t_coo = timed(lambda: W.subgraph(win, coo, n))
+    n_w = int(win.numel())
+    # attention edge_index: row 0 = key (the CSR row node), row 1 = query
+    adj, t_adj = timed(lambda: WindowAdjacency(sub_csr, n_w, n_w, chunk_for_heads(H),
+                                               small_for_heads(H)))
+    (x_i, _), t_gather = timed(lambda: W.gather_rows(features, win))
+    ops = {"merge_related_nodes_ms": t_rel, "subgraph_from_csr_ms": t_csr,
+           "subgraph_coo_ms": t_coo, "window_csr_build_ms": t_adj, "feature_gather_ms": t_gather}
+    total = t_rel + t_csr + t_adj + t_gather
+    _log("[bench] prep: " + ", ".join(f"{k} {v:.3f}" for k, v in ops.items())
+         + f"; window {n_w} nodes, {int(sub_csr.shape[1])} edges")
+
+    cpu = None
+    if not args.no_cpu:
+        from oracle import graph as OG
+
+        xadj_h, adj_h, ew_h = xadj.cpu().numpy(), adjncy.cpu().numpy(), eweights.cpu().numpy()
+        part_h, rowptr_h, col_h = part.cpu().numpy(), rowptr.cpu().numpy(), col.cpu().numpy()
+        feat_h = features.cpu().numpy()
+        t = time.perf_counter()
+        win_h, _ = OG.merge_related_nodes(xadj_h, adj_h, ew_h, part_h, pct)
+        sub_h = OG.subgraph_from_csr(win_h, rowptr_h, col_h)
+        OG.csr_from_coo(sub_h[0], sub_h[1], len(win_h), len(win_h))
+        feat_h[win_h]
+        t_cpu = time.perf_counter() - t
+        if not (np.array_equal(win_h, win.cpu().numpy())
+                and np.array_equal(sub_h, sub_csr.cpu().numpy())):
+            raise RuntimeError("window assembly differs from the oracle")
+        cpu = {"value": 1e3 * t_cpu, "unit": "ms", "cores": 1, "kind": "port",
+               "sample": "the same window once: the oracle's restatement of "
+                         "_merge_related_nodes (Python dict loop), _subgraph_from_csr (per-node "
+                         "searchsorted loop), the CSR build (numpy lexsort) and the feature gather"}
+        _log(f"[bench] prep cpu baseline {1e3 * t_cpu:.1f} ms")
+    return {
+        "metric": "window assembly time (related nodes, induced subgraph, window CSR, features)",
+        "value": total, "unit": "ms", "n_gpus": 1, "steps": 5, "warmup": 1, "ms_per_step": total,
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "int64",
+        "data": "synthetic",
+        "config": {"workload": (f"{cfg.name} window assembly: global Chung-Lu graph n={n}, "
+                                f"{E_glob} directed entries; window of {cfg.n_q} nodes + "
+                                f"{pct}% related -> {n_w} nodes, {int(sub_csr.shape[1])} edges; "
+                                f"features {feat_dim} fp32"),
+                   "window_nodes": n_w, "window_edges": int(sub_csr.shape[1])},
+        "ops": ops,
+        "cpu_baseline": cpu,
+    }
+
+
 def model_step_bench(args, cfg, layers: int, dev) -> dict:
     """The window training step of train_eval.py:255-300 on one GPU: the
     node-level Graphormer (cfg's hidden size, heads and layers; FFN width =
@@ -261,6 +372,9 @@ def main(argv=None) -> int:
                     help="run one 512 MiB device copy first (calibrates HBM byte counters)")
     ap.add_argument("--graph", action="store_true",
                     help="capture one step (all layers, fwd+bwd) in a HIP graph and time replays")
+    ap.add_argument("--prep", action="store_true",
+                    help="time the window assembly instead (related nodes, induced subgraph, "
+                         "window CSR, feature gather) on the config's global graph")
     ap.add_argument("--model", action="store_true",
                     help="time the whole window training step instead (encoder projections, "
                          "LayerNorm, FFN and attention, NLL, backward, AdamW) in bf16 autocast")
@@ -285,6 +399,13 @@ def main(argv=None) -> int:
     layers = args.layers or cfg.layers
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.prep:
+        if cfg.dense or not cfg.n_global:
+            print("--prep needs a sparse config with a global graph (gph_large, gt_arxiv, "
+                  "gt_highdeg)", file=sys.stderr)
+            return 2
+        print(json.dumps(prep_bench(args, cfg, dev)), flush=True)
+        return 0
     if args.model:
         if cfg.dense:
             print("--model runs the sparse window encoder; pick a sparse --config", file=sys.stderr)

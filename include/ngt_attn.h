@@ -245,8 +245,10 @@ int ngt_gather_rows(const void* src, int64_t n_src, const int64_t* idx, int64_t 
  *   1 set node out of range, 2 duplicate set node, 4 edge endpoint out of
  *   range, 8 CSR row outside col.  Entries past cap are not written; call once
  *   with out = NULL, read result, then again with cap = result[0].
- * Workspace from ngt_subgraph_workspace_bytes(n_nodes, n_edges (COO form, else
- * 0), n_set, ...); the map it holds is rebuilt by every call.
+ * Workspace from ngt_subgraph_workspace_bytes(n_nodes, n_edges, n_set, ...)
+ * with n_edges = edges of edge_index (COO form) or entries of col (CSR form);
+ * the map it holds is rebuilt by every call.  The CSR form spreads each row
+ * over waves of 2,048 entries, so hub rows do not serialise.
  */
 int ngt_subgraph_workspace_bytes(int64_t n_nodes, int64_t n_edges, int32_t n_set, size_t* bytes);
 int ngt_subgraph_coo(const int64_t* edge_index, int64_t n_edges, int64_t n_nodes,

@@ -39,12 +39,15 @@ constexpr unsigned long long kBadSetNode = 1, kDuplicateSetNode = 2, kBadEdge = 
 inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 struct SubLayout {
-  size_t pos, cnt, end, temp, temp_bytes, total;
+  size_t pos, cnt, end, nseg, seg_end, temp, temp_bytes, total;
 };
 
-int sub_layout(int64_t n_nodes, int64_t n_items, SubLayout* L) {
+// n_items: scan length (COO tiles or CSR segment waves); n_set: set size
+int sub_layout(int64_t n_nodes, int64_t n_items, int64_t n_set, SubLayout* L) {
   const size_t n = size_t(n_nodes > 0 ? n_nodes : 1);
+  if (n_set > n_items) n_items = n_set;
   const size_t m = size_t(n_items > 0 ? n_items : 1);
+  const size_t ns = size_t(n_set > 0 ? n_set : 1);
   size_t scan_bytes = 0;
   NGT_HIP_CHECK(rocprim::inclusive_scan(nullptr, scan_bytes, (int64_t*)nullptr, (int64_t*)nullptr,
                                         m, rocprim::plus<int64_t>(), hipStream_t(0)));
@@ -57,6 +60,8 @@ int sub_layout(int64_t n_nodes, int64_t n_items, SubLayout* L) {
   L->pos = take(n * 4);
   L->cnt = take(m * 8);
   L->end = take(m * 8);
+  L->nseg = take(ns * 8);
+  L->seg_end = take(ns * 8);
   L->temp_bytes = scan_bytes;
   L->temp = take(scan_bytes);
   L->total = off;
@@ -157,33 +162,79 @@ __global__ __launch_bounds__(kBlock) void k_coo_emit(const int64_t* ei, int64_t 
 }
 
 // ------------------------------------------------------------------ CSR form
+// A set node's CSR row is cut into segments of kSeg entries, one wave each, so
+// a hub row (hundreds of thousands of neighbours) is spread over many waves.
+// Segments are numbered in (set order, position in row) order, which is the
+// output order; a wave finds its segment by binary search over the inclusive
+// scan of the per-node segment counts.
+constexpr int64_t kSeg = 2048;
+
+__global__ void k_csr_segs(const int64_t* rowptr, int64_t n_col, int64_t n_nodes,
+                           const int64_t* set, int32_t n_set, int64_t* nseg,
+                           unsigned long long* result) {
+  const int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
+  if (i >= n_set) return;
+  const int64_t g = set[i];
+  int64_t ns = 0;
+  if (g >= 0 && g < n_nodes) {  // a bad set node is flagged by k_sub_mark
+    const int64_t b = rowptr[g], e = rowptr[g + 1];
+    if (b < 0 || e < b || e > n_col)
+      atomicOr(&result[1], kBadRowptr);
+    else
+      ns = (e - b + kSeg - 1) / kSeg;
+  }
+  nseg[i] = ns;
+}
+
+struct Segment {
+  int64_t row, b, e;  // set position; CSR range [b, e)
+};
+
+__device__ __forceinline__ bool find_segment(int64_t w, const int64_t* seg_end, const int64_t* nseg,
+                                             int32_t n_set, const int64_t* rowptr,
+                                             const int64_t* set, Segment& sg) {
+  if (n_set == 0 || w >= seg_end[n_set - 1]) return false;
+  int lo = 0, hi = n_set - 1;  // first i with seg_end[i] > w
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (seg_end[mid] > w)
+      hi = mid;
+    else
+      lo = mid + 1;
+  }
+  const int64_t k = w - (seg_end[lo] - nseg[lo]);
+  const int64_t g = set[lo];
+  const int64_t e0 = rowptr[g + 1];
+  sg.row = lo;
+  sg.b = rowptr[g] + k * kSeg;
+  sg.e = sg.b + kSeg < e0 ? sg.b + kSeg : e0;
+  return true;
+}
+
 __global__ __launch_bounds__(kBlock) void k_csr_count(const int64_t* rowptr, const int64_t* col,
-                                                      int64_t n_col, int64_t n_nodes,
-                                                      const int64_t* set, int32_t n_set,
-                                                      const int32_t* pos,
-                                                      int64_t* cnt, unsigned long long* result) {
+                                                      int64_t n_nodes, const int64_t* set,
+                                                      int32_t n_set, const int64_t* nseg,
+                                                      const int64_t* seg_end, int64_t n_waves,
+                                                      const int32_t* pos, int64_t* cnt,
+                                                      unsigned long long* result) {
   const int64_t w = blockIdx.x * int64_t(kWaves) + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  if (w >= n_set) return;
-  const int64_t g = set[w];
-  if (g < 0 || g >= n_nodes) {  // flagged by k_sub_mark; the row is skipped
+  if (w >= n_waves) return;
+  // rows that overlap (a non-monotone rowptr) could need more segments than
+  // the launch covers: refuse rather than drop edges
+  if (w == 0 && lane == 0 && n_set > 0 && seg_end[n_set - 1] > n_waves)
+    atomicOr(&result[1], kBadRowptr);
+  Segment sg;
+  if (!find_segment(w, seg_end, nseg, n_set, rowptr, set, sg)) {
     if (lane == 0) cnt[w] = 0;
-    return;
-  }
-  const int64_t b = rowptr[g], e = rowptr[g + 1];
-  if (b < 0 || e < b || e > n_col) {
-    if (lane == 0) {
-      cnt[w] = 0;
-      atomicOr(&result[1], kBadRowptr);
-    }
     return;
   }
   int64_t c = 0;
   bool bad = false;
-  for (int64_t p0 = b; p0 < e; p0 += 64) {
+  for (int64_t p0 = sg.b; p0 < sg.e; p0 += 64) {
     const int64_t p = p0 + lane;
     bool keep = false;
-    if (p < e) {
+    if (p < sg.e) {
       const int64_t nb = col[p];
       if (nb < 0 || nb >= n_nodes)
         bad = true;
@@ -197,23 +248,22 @@ __global__ __launch_bounds__(kBlock) void k_csr_count(const int64_t* rowptr, con
 }
 
 __global__ __launch_bounds__(kBlock) void k_csr_emit(const int64_t* rowptr, const int64_t* col,
-                                                     int64_t n_col, int64_t n_nodes,
-                                                     const int64_t* set, int32_t n_set,
-                                                     const int32_t* pos,
-                                                     const int64_t* cnt, const int64_t* end,
-                                                     int64_t* out, int64_t cap) {
+                                                     int64_t n_nodes, const int64_t* set,
+                                                     int32_t n_set, const int64_t* nseg,
+                                                     const int64_t* seg_end, int64_t n_waves,
+                                                     const int32_t* pos, const int64_t* cnt,
+                                                     const int64_t* end, int64_t* out,
+                                                     int64_t cap) {
   const int64_t w = blockIdx.x * int64_t(kWaves) + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  if (w >= n_set) return;
-  const int64_t g = set[w];
-  if (g < 0 || g >= n_nodes) return;
-  const int64_t b = rowptr[g], e = rowptr[g + 1];
-  if (b < 0 || e < b || e > n_col) return;
+  if (w >= n_waves) return;
+  Segment sg;
+  if (!find_segment(w, seg_end, nseg, n_set, rowptr, set, sg)) return;
   int64_t at = end[w] - cnt[w];
-  for (int64_t p0 = b; p0 < e; p0 += 64) {
+  for (int64_t p0 = sg.b; p0 < sg.e; p0 += 64) {
     const int64_t p = p0 + lane;
     int32_t pn = -1;
-    if (p < e) {
+    if (p < sg.e) {
       const int64_t nb = col[p];
       if (nb >= 0 && nb < n_nodes) pn = pos[nb];
     }
@@ -222,7 +272,7 @@ __global__ __launch_bounds__(kBlock) void k_csr_emit(const int64_t* rowptr, cons
     if (keep) {
       const int64_t k = at + lane_rank(m);
       if (k < cap) {
-        out[k] = w;
+        out[k] = sg.row;
         out[cap + k] = pn;
       }
     }
@@ -244,7 +294,7 @@ inline int grid_for(int64_t n) {
 
 int sub_prepare(int64_t n_nodes, int64_t n_items, const int64_t* set, int32_t n_set, void* ws,
                 size_t ws_bytes, hipStream_t s, int64_t* result, SubLayout* L, const char* who) {
-  NGT_CHECK_OK(sub_layout(n_nodes, n_items, L));
+  NGT_CHECK_OK(sub_layout(n_nodes, n_items, n_set, L));
   if (!ws || ws_bytes < L->total)
     return set_error(NGT_ERR_ARG, "%s: workspace too small (%zu < %zu)", who, ws_bytes, L->total);
   char* base = static_cast<char*>(ws);
@@ -279,9 +329,12 @@ extern "C" int ngt_subgraph_workspace_bytes(int64_t n_nodes, int64_t n_edges, in
                                             size_t* bytes) {
   if (!bytes || n_nodes < 0 || n_edges < 0 || n_set < 0)
     return set_error(NGT_ERR_ARG, "ngt_subgraph_workspace_bytes: bad arguments");
+  // COO form: n_edges edges in 2,048-edge tiles; CSR form: n_edges = entries of
+  // col, at most n_set + n_edges / kSeg segment waves
   const int64_t tiles = (n_edges + kTile - 1) / kTile;
+  const int64_t segs = int64_t(n_set) + (n_edges + kSeg - 1) / kSeg;
   SubLayout L;
-  NGT_CHECK_OK(sub_layout(n_nodes, tiles > n_set ? tiles : n_set, &L));
+  NGT_CHECK_OK(sub_layout(n_nodes, tiles > segs ? tiles : segs, n_set, &L));
   *bytes = L.total;
   return NGT_OK;
 }
@@ -326,23 +379,31 @@ extern "C" int ngt_subgraph_csr(const int64_t* rowptr, const int64_t* col, int64
   if (n_set > n_nodes)
     return set_error(NGT_ERR_ARG, "ngt_subgraph_csr: node set longer than the node count");
   const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t n_waves = int64_t(n_set) + (n_col + kSeg - 1) / kSeg;
   SubLayout L;
-  NGT_CHECK_OK(sub_prepare(n_nodes, n_set, node_set, n_set, ws, ws_bytes, s, result, &L,
+  NGT_CHECK_OK(sub_prepare(n_nodes, n_waves, node_set, n_set, ws, ws_bytes, s, result, &L,
                            "ngt_subgraph_csr"));
   if (n_set == 0) return NGT_OK;
   char* base = static_cast<char*>(ws);
   const int32_t* pos = reinterpret_cast<const int32_t*>(base + L.pos);
   int64_t* cnt = reinterpret_cast<int64_t*>(base + L.cnt);
   const int64_t* end = reinterpret_cast<const int64_t*>(base + L.end);
+  int64_t* nseg = reinterpret_cast<int64_t*>(base + L.nseg);
+  int64_t* seg_end = reinterpret_cast<int64_t*>(base + L.seg_end);
   auto* res = reinterpret_cast<unsigned long long*>(result);
-  const int grid = int((int64_t(n_set) + kWaves - 1) / kWaves);
   KernelTimer timer_("subgraph_csr", s);
-  hipLaunchKernelGGL(k_csr_count, dim3(grid), dim3(kBlock), 0, s, rowptr, col, n_col, n_nodes,
-                     node_set, n_set, pos, cnt, res);
-  NGT_CHECK_OK(sub_scan(L, base, n_set, result, s));
+  hipLaunchKernelGGL(k_csr_segs, dim3((n_set + kBlock - 1) / kBlock), dim3(kBlock), 0, s, rowptr,
+                     n_col, n_nodes, node_set, n_set, nseg, res);
+  size_t temp_bytes = L.temp_bytes;
+  NGT_HIP_CHECK(rocprim::inclusive_scan(base + L.temp, temp_bytes, nseg, seg_end, size_t(n_set),
+                                        rocprim::plus<int64_t>(), s));
+  const int64_t grid = (n_waves + kWaves - 1) / kWaves;
+  hipLaunchKernelGGL(k_csr_count, dim3(grid), dim3(kBlock), 0, s, rowptr, col, n_nodes, node_set,
+                     n_set, nseg, seg_end, n_waves, pos, cnt, res);
+  NGT_CHECK_OK(sub_scan(L, base, n_waves, result, s));
   if (out && cap > 0)
-    hipLaunchKernelGGL(k_csr_emit, dim3(grid), dim3(kBlock), 0, s, rowptr, col, n_col, n_nodes,
-                       node_set, n_set, pos, cnt, end, out, cap);
+    hipLaunchKernelGGL(k_csr_emit, dim3(grid), dim3(kBlock), 0, s, rowptr, col, n_nodes, node_set,
+                       n_set, nseg, seg_end, n_waves, pos, cnt, end, out, cap);
   NGT_HIP_CHECK(hipGetLastError());
   return NGT_OK;
 }

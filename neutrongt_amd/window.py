@@ -185,7 +185,7 @@ def subgraph_from_csr(node_set: torch.Tensor, rowptr: torch.Tensor, col: torch.T
         lambda out, cap, res, ws, wb, st: lib.ngt_subgraph_csr(
             rowptr.data_ptr(), col.data_ptr(), int(col.numel()), n_nodes, node_set.data_ptr(), n_set,
             out, cap, res, ws, wb, st),
-        n_nodes, 0, n_set, node_set.device)
+        n_nodes, int(col.numel()), n_set, node_set.device)
 
 
 def assemble_window_features(feature: torch.Tensor, cache: torch.Tensor, dup_index: torch.Tensor,

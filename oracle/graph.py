@@ -83,17 +83,17 @@ def merge_related_nodes(xadj, adjncy, eweights, partition, topk_percent: int):
     """weightMetis_keepParent._merge_related_nodes (metisPartition.py:397-425),
     restated with the same Python containers (dict insertion order, stable
     ``sorted``)."""
-    xadj = [int(x) for x in xadj]
-    adjncy = [int(x) for x in adjncy]
-    eweights = [int(x) for x in eweights]
+    xadj = np.asarray(xadj, np.int64)
+    adjncy = np.asarray(adjncy)
+    eweights = np.asarray(eweights)
     part = [int(x) for x in partition]
     partition_set = set(part)
     external = {}
     for node in part:
-        start, end = xadj[node], xadj[node + 1]
+        start, end = int(xadj[node]), int(xadj[node + 1])
         if end - start == 0:
             continue
-        for nb, w in zip(adjncy[start:end], eweights[start:end]):
+        for nb, w in zip(adjncy[start:end].tolist(), eweights[start:end].tolist()):
             if nb not in partition_set:
                 external[nb] = external.get(nb, 0) + w
     ranked = sorted(external.items(), key=lambda x: x[1], reverse=True)

@@ -91,6 +91,8 @@ def test_subgraph_rejects_bad_input():
     bad_rowptr = np.array([0, 1, 9, 3])  # row 1 runs past col
     with pytest.raises(IndexError, match="CSR row"):
         subgraph_from_csr(*_gpu(np.array([1, 0]), bad_rowptr, col))
+    with pytest.raises(IndexError, match="CSR row"):  # row 1 ends before it starts
+        subgraph_from_csr(*_gpu(np.array([1, 0]), np.array([0, 2, 1, 3]), col))
 
 
 def test_subgraph_full_size_window():
