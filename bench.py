@@ -240,8 +240,23 @@ def prep_bench(args, cfg, dev) -> dict:
     adj, t_adj = timed(lambda: WindowAdjacency(sub_csr, n_w, n_w, chunk_for_heads(H),
                                                small_for_heads(H)))
     (x_i, _), t_gather = timed(lambda: W.gather_rows(features, win))
+    # window refinement of this window: node_out with seeded node scores (30 %
+    # removed, the training loop's ratio), then node_in refilling it from the
+    # expired nodes by PPR mass (8 PPR entries per node of the global graph)
+    from neutrongt_amd import refine as RF
+
+    n_ppr = 8 * n
+    ppr = torch.stack([torch.randint(0, n, (n_ppr,), generator=g, device=dev),
+                       torch.randint(0, n, (n_ppr,), generator=g, device=dev)])
+    ppr_val = torch.rand(n_ppr, generator=g, device=dev) * 1e-3
+    scores = torch.rand(n_w, generator=g, device=dev)
+    (kept, kept_edges, expired), t_out = timed(
+        lambda: RF.node_out_window(win, sub_csr, scores, 0.3))
+    _, t_in = timed(lambda: RF.node_in_window(kept, expired, ppr, ppr_val, int(expired.numel()),
+                                              coo, n))
     ops = {"merge_related_nodes_ms": t_rel, "subgraph_from_csr_ms": t_csr,
-           "subgraph_coo_ms": t_coo, "window_csr_build_ms": t_adj, "feature_gather_ms": t_gather}
+           "subgraph_coo_ms": t_coo, "window_csr_build_ms": t_adj, "feature_gather_ms": t_gather,
+           "node_out_ms": t_out, "node_in_ms": t_in}
     total = t_rel + t_csr + t_adj + t_gather
     _log("[bench] prep: " + ", ".join(f"{k} {v:.3f}" for k, v in ops.items())
          + f"; window {n_w} nodes, {int(sub_csr.shape[1])} edges")
@@ -262,11 +277,20 @@ def prep_bench(args, cfg, dev) -> dict:
         if not (np.array_equal(win_h, win.cpu().numpy())
                 and np.array_equal(sub_h, sub_csr.cpu().numpy())):
             raise RuntimeError("window assembly differs from the oracle")
+        from oracle import refine as OR
+
+        t = time.perf_counter()
+        k_h, _, x_h = OR.node_out_window(win_h, sub_h, scores.cpu().numpy(), 0.3)
+        OR.node_in_window(k_h, x_h, ppr.cpu().numpy(), ppr_val.cpu().numpy(), x_h.size,
+                          coo.cpu().numpy(), n)
+        t_ref = time.perf_counter() - t
         cpu = {"value": 1e3 * t_cpu, "unit": "ms", "cores": 1, "kind": "port",
                "sample": "the same window once: the oracle's restatement of "
                          "_merge_related_nodes (Python dict loop), _subgraph_from_csr (per-node "
-                         "searchsorted loop), the CSR build (numpy lexsort) and the feature gather"}
-        _log(f"[bench] prep cpu baseline {1e3 * t_cpu:.1f} ms")
+                         "searchsorted loop), the CSR build (numpy lexsort) and the feature gather",
+               "refine_ms": 1e3 * t_ref}
+        _log(f"[bench] prep cpu baseline {1e3 * t_cpu:.1f} ms; node_out+node_in "
+             f"{1e3 * t_ref:.1f} ms")
     return {
         "metric": "window assembly time (related nodes, induced subgraph, window CSR, features)",
         "value": total, "unit": "ms", "n_gpus": 1, "steps": 5, "warmup": 1, "ms_per_step": total,

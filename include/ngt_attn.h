@@ -225,6 +225,17 @@ int ngt_gather_rows(const void* src, int64_t n_src, const int64_t* idx, int64_t 
                     int64_t row_bytes, void* dst, int32_t* bad, void* stream);
 
 /*
+ * Sequential segmented sum: out[s] = vals[seg[s]] + ... + vals[seg[s+1]-1],
+ * accumulated from 0.0f in index order, for s < n_seg (seg: int64 [n_seg+1]).
+ * This is the rounding of the fp32 scores.index_add_ in node_in
+ * (NeutronGT/core/metisPartition.py:197-201) once the contributions are
+ * grouped by candidate in their original order.  Segments outside
+ * [0, n_vals] are counted in *bad (device int32) and give 0.
+ */
+int ngt_segment_sum_f32(const float* vals, int64_t n_vals, const int64_t* seg, int64_t n_seg,
+                        float* out, int32_t* bad, void* stream);
+
+/*
  * Induced window subgraph with relabelling, on the GPU.
  *
  * ngt_subgraph_coo replaces torch_geometric.utils.subgraph(subset, edge_index,

@@ -97,6 +97,7 @@ SIGNATURES = {
     "ngt_related_workspace_bytes": [_i32, _i32, _psz],
     "ngt_merge_related_nodes": [_vp, _vp, _vp, _i32, _vp, _i32, _i32, _vp, _vp, _vp, _sz, _vp],
     "ngt_gather_rows": [_vp, _i64, _vp, _i64, _i64, _vp, _vp, _vp],
+    "ngt_segment_sum_f32": [_vp, _i64, _vp, _i64, _vp, _vp, _vp],
     "ngt_subgraph_workspace_bytes": [_i64, _i64, _i32, _vp],
     "ngt_subgraph_coo": [_vp, _i64, _i64, _vp, _i32, _vp, _i64, _vp, _vp, _sz, _vp],
     "ngt_subgraph_csr": [_vp, _vp, _i64, _i64, _vp, _i32, _vp, _i64, _vp, _vp, _sz, _vp],

@@ -191,6 +191,25 @@ __global__ void k_gather_rows(const uint32_t* __restrict__ src, int64_t n_src,
   }
 }
 
+// out[s] = vals[seg[s]] + vals[seg[s]+1] + ... + vals[seg[s+1]-1], summed from
+// 0.0f one element at a time in index order: the rounding of a sequential
+// index_add_ over the same elements in the same order.
+__global__ void k_segment_sum(const float* __restrict__ vals, int64_t n_vals,
+                              const int64_t* __restrict__ seg, int64_t n_seg,
+                              float* __restrict__ out, int32_t* bad) {
+  const int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
+  if (i >= n_seg) return;
+  const int64_t b = seg[i], e = seg[i + 1];
+  if (b < 0 || e < b || e > n_vals) {
+    atomicAdd(bad, 1);
+    out[i] = 0.f;
+    return;
+  }
+  float acc = 0.f;
+  for (int64_t p = b; p < e; ++p) acc += vals[p];
+  out[i] = acc;
+}
+
 }  // namespace
 }  // namespace ngt
 
@@ -280,6 +299,19 @@ extern "C" int ngt_gather_rows(const void* src, int64_t n_src, const int64_t* id
   hipLaunchKernelGGL(k_gather_rows, dim3(grid_for(n_rows * words)), dim3(kBlock), 0,
                      static_cast<hipStream_t>(stream), static_cast<const uint32_t*>(src), n_src,
                      idx, n_rows, words, static_cast<uint32_t*>(dst), bad);
+  NGT_HIP_CHECK(hipGetLastError());
+  return NGT_OK;
+}
+
+extern "C" int ngt_segment_sum_f32(const float* vals, int64_t n_vals, const int64_t* seg,
+                                   int64_t n_seg, float* out, int32_t* bad, void* stream) {
+  if (n_vals < 0 || n_seg < 0 || (n_seg > 0 && (!seg || !out || !bad)) || (n_vals > 0 && !vals))
+    return set_error(NGT_ERR_ARG, "ngt_segment_sum_f32: bad arguments");
+  if (n_seg == 0) return NGT_OK;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  KernelTimer timer_("segment_sum", st);
+  hipLaunchKernelGGL(k_segment_sum, dim3((n_seg + kBlock - 1) / kBlock),
+                     dim3(kBlock), 0, st, vals, n_vals, seg, n_seg, out, bad);
   NGT_HIP_CHECK(hipGetLastError());
   return NGT_OK;
 }
