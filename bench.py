@@ -205,8 +205,7 @@ def prep_bench(args, cfg, dev) -> dict:
     order = torch.argsort(rows, stable=True)
     rows, col = rows[order], cols[order]
     del cols, order
-    rowptr = torch.zeros(n + 1, dtype=torch.int64, device=dev)
-    rowptr[1:] = torch.cumsum(torch.bincount(rows, minlength=n), 0)
+    rowptr = torch.searchsorted(rows, torch.arange(n + 1, device=dev, dtype=torch.int64))
     coo = torch.stack([rows, col])
     del rows
     xadj = rowptr.to(torch.int32)

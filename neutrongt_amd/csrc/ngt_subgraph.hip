@@ -101,8 +101,9 @@ __device__ __forceinline__ bool coo_flag(const int64_t* src, const int64_t* dst,
     return false;
   }
   ps = pos[s];
+  if (ps < 0) return false;  // most edges leave here: no random read of pos[d]
   pd = pos[d];
-  return ps >= 0 && pd >= 0;
+  return pd >= 0;
 }
 
 __global__ __launch_bounds__(kBlock) void k_coo_count(const int64_t* ei, int64_t n_edges,

@@ -34,9 +34,14 @@ inline int grid_for(int64_t n) {
 }
 
 struct RelLayout {
-  size_t in_part, first_seen, wsum, deg, base, keys_a, keys_b, ids_a, ids_b, member, pos, temp,
-      total, temp_bytes;
+  size_t in_part, first_seen, wsum, deg, base, nseg, seg_end, keys_a, keys_b, ids_a, ids_b, member,
+      pos, temp, total, temp_bytes;
 };
+
+// A partition node's adjacency is walked in segments of kRelSeg entries, one
+// wave each, so a hub node (hundreds of thousands of neighbours) is spread
+// over many waves instead of serialising one.
+constexpr int32_t kRelSeg = 2048;
 
 int rel_layout(int32_t n_nodes, int32_t n_part, RelLayout* L) {
   const size_t n = size_t(n_nodes > 0 ? n_nodes : 1);
@@ -49,6 +54,10 @@ int rel_layout(int32_t n_nodes, int32_t n_part, RelLayout* L) {
                                         int32_t(0), n, rocprim::plus<int32_t>(), hipStream_t(0)));
   NGT_HIP_CHECK(rocprim::exclusive_scan(nullptr, scan2, (int32_t*)nullptr, (int32_t*)nullptr,
                                         int32_t(0), np, rocprim::plus<int32_t>(), hipStream_t(0)));
+  size_t scan3 = 0;
+  NGT_HIP_CHECK(rocprim::inclusive_scan(nullptr, scan3, (int32_t*)nullptr, (int32_t*)nullptr, np,
+                                        rocprim::plus<int32_t>(), hipStream_t(0)));
+  if (scan3 > scan2) scan2 = scan3;
   size_t off = 0;
   auto take = [&](size_t b) {
     const size_t at = off;
@@ -60,6 +69,8 @@ int rel_layout(int32_t n_nodes, int32_t n_part, RelLayout* L) {
   L->wsum = take(n * 8);
   L->deg = take(np * 4);
   L->base = take(np * 4);
+  L->nseg = take(np * 4);
+  L->seg_end = take(np * 4);
   L->keys_a = take(n * 8);
   L->keys_b = take(n * 8);
   L->ids_a = take(n * 4);
@@ -100,25 +111,47 @@ __global__ void k_rel_mark(const int64_t* __restrict__ part, int32_t n_part,
     }
     in_part[u] = 1;
     member[u] = 1;
-    deg[p] = xadj[u + 1] - xadj[u];
+    const int32_t d = xadj[u + 1] - xadj[u];
+    if (d < 0) atomicAdd(status + 2, 1);  // a decreasing row pointer: rejected, row skipped
+    deg[p] = d < 0 ? 0 : d;
   }
 }
 
-// One wave per partition position: lanes stride over the node's adjacency.
+__global__ void k_rel_segs(const int32_t* __restrict__ deg, int32_t n_part, int32_t* nseg) {
+  for (int64_t p = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; p < n_part;
+       p += int64_t(gridDim.x) * blockDim.x)
+    nseg[p] = (deg[p] + kRelSeg - 1) / kRelSeg;
+}
+
+// Waves stride over the segments (their count is read on the device, so every
+// wave ends); a wave finds its partition position by binary search over the
+// inclusive scan of the per-position segment counts.
 __global__ void k_rel_accumulate(const int64_t* __restrict__ part, int32_t n_part,
                                  const int32_t* __restrict__ xadj,
                                  const int32_t* __restrict__ adjncy,
                                  const int32_t* __restrict__ eweights, int32_t n_nodes,
                                  const int32_t* __restrict__ in_part,
-                                 const int32_t* __restrict__ base, int32_t* first_seen,
+                                 const int32_t* __restrict__ base,
+                                 const int32_t* __restrict__ nseg,
+                                 const int32_t* __restrict__ seg_end, int32_t* first_seen,
                                  unsigned long long* wsum, int32_t* status) {
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t waves = int64_t(gridDim.x) * (blockDim.x / kWave);
-  for (int64_t p = blockIdx.x * int64_t(blockDim.x / kWave) + (threadIdx.x / kWave); p < n_part;
-       p += waves) {
-    const int64_t u = part[p];
-    if (u < 0 || u >= n_nodes) continue;
-    const int32_t b = xadj[u], e = xadj[u + 1];
+  const int64_t n_segs = seg_end[n_part - 1];
+  for (int64_t w = blockIdx.x * int64_t(blockDim.x / kWave) + (threadIdx.x / kWave); w < n_segs;
+       w += waves) {
+    int lo = 0, hi = n_part - 1;  // first p with seg_end[p] > w
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (seg_end[mid] > w)
+        hi = mid;
+      else
+        lo = mid + 1;
+    }
+    const int64_t u = part[lo];  // in range: an invalid u has no segments
+    const int32_t row_b = xadj[u], row_e = xadj[u + 1];
+    const int32_t b = row_b + int32_t(w - (seg_end[lo] - nseg[lo])) * kRelSeg;
+    const int32_t e = b + kRelSeg < row_e ? b + kRelSeg : row_e;
     for (int32_t a = b + lane; a < e; a += kWave) {
       const int32_t nb = adjncy[a];
       if (nb < 0 || nb >= n_nodes) {
@@ -126,10 +159,10 @@ __global__ void k_rel_accumulate(const int64_t* __restrict__ part, int32_t n_par
         continue;
       }
       if (in_part[nb]) continue;
-      const int32_t w = eweights[a];
-      if (w < 0) atomicAdd(status + 2, 1);
-      atomicMin(first_seen + nb, base[p] + (a - b));
-      atomicAdd(wsum + nb, static_cast<unsigned long long>(w < 0 ? 0 : w));
+      const int32_t wt = eweights[a];
+      if (wt < 0) atomicAdd(status + 2, 1);
+      atomicMin(first_seen + nb, base[lo] + (a - row_b));
+      atomicAdd(wsum + nb, static_cast<unsigned long long>(wt < 0 ? 0 : wt));
     }
   }
 }
@@ -266,9 +299,15 @@ extern "C" int ngt_merge_related_nodes(const int32_t* xadj, const int32_t* adjnc
     size_t tb = L.temp_bytes;
     NGT_HIP_CHECK(rocprim::exclusive_scan(ws + L.temp, tb, deg, base, int32_t(0), size_t(n_part),
                                           rocprim::plus<int32_t>(), st));
+    int32_t* nseg = reinterpret_cast<int32_t*>(ws + L.nseg);
+    int32_t* seg_end = reinterpret_cast<int32_t*>(ws + L.seg_end);
+    hipLaunchKernelGGL(k_rel_segs, dim3(grid_for(n_part)), dim3(kBlock), 0, st, deg, n_part, nseg);
+    tb = L.temp_bytes;
+    NGT_HIP_CHECK(rocprim::inclusive_scan(ws + L.temp, tb, nseg, seg_end, size_t(n_part),
+                                          rocprim::plus<int32_t>(), st));
     hipLaunchKernelGGL(k_rel_accumulate, dim3(grid_for(int64_t(n_part) * kWave)), dim3(kBlock), 0,
-                       st, partition, n_part, xadj, adjncy, eweights, n_nodes, in_part, base,
-                       first_seen, wsum, out_len);
+                       st, partition, n_part, xadj, adjncy, eweights, n_nodes, in_part, base, nseg,
+                       seg_end, first_seen, wsum, out_len);
     NGT_HIP_CHECK(hipGetLastError());
   }
   hipLaunchKernelGGL(k_rel_keys, dim3(grid_for(n_nodes)), dim3(kBlock), 0, st, n_nodes,

@@ -40,6 +40,18 @@ def _segment_sum(vals: torch.Tensor, seg: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def _check_ids(num_nodes: int, *tensors):
+    """Node ids index device tables here: reject any outside [0, num_nodes)
+    on the host (one sync) instead of letting an index assert fire."""
+    parts = [t.reshape(-1) for t in tensors if t.numel()]
+    if not parts:
+        return
+    both = torch.stack([torch.stack([p.min(), p.max()]) for p in parts])
+    lo, hi = int(both[:, 0].min()), int(both[:, 1].max())
+    if lo < 0 or hi >= num_nodes:
+        raise IndexError(f"node id out of range [0, {num_nodes}): min {lo}, max {hi}")
+
+
 def node_out_window(nodes: torch.Tensor, edge_index: torch.Tensor, node_scores: torch.Tensor,
                     remove_ratio: float = 0.1):
     """One window of node_out (metisPartition.py:224-287).  Returns (kept
@@ -61,17 +73,23 @@ def node_in_window(nodes: torch.Tensor, buffer: torch.Tensor, ppr_edge_index: to
     """One window of node_in (metisPartition.py:160-222).  Returns None when no
     buffered node lies outside the window, else (new sorted nodes, their
     edge_index from the global graph, remaining buffer)."""
+    dev = nodes.device
+    _check_ids(num_nodes, nodes, buffer, ppr_edge_index)
+    in_window = torch.zeros(num_nodes, dtype=torch.bool, device=dev)
+    in_window[nodes] = True
     cand = torch.unique(buffer)
-    valid = cand[~torch.isin(cand, nodes)]
+    valid = cand[~in_window[cand]]
     if valid.numel() == 0:
         return None
     real_add = min(int(num_to_recover), int(valid.numel()))
-    mask_src = torch.isin(ppr_edge_index[0], nodes)
-    dest = ppr_edge_index[1][mask_src]
-    vals = ppr_val[mask_src]
-    mask_dst = torch.isin(dest, valid)
-    idx = torch.searchsorted(valid, dest[mask_dst])
-    contrib = vals[mask_dst].float()
+    # PPR entries from a window node to a candidate, in PPR-edge order; a
+    # position table replaces the reference's two isin passes
+    cand_pos = torch.full((num_nodes,), -1, dtype=torch.int64, device=dev)
+    cand_pos[valid] = torch.arange(valid.numel(), device=dev)
+    pos = cand_pos[ppr_edge_index[1]]
+    keep = in_window[ppr_edge_index[0]] & (pos >= 0)
+    idx = pos[keep]
+    contrib = ppr_val[keep].float()
     # group the contributions per candidate, keeping their PPR-edge order, and
     # add them one by one (the rounding of the reference's index_add_)
     grouped = contrib[torch.sort(idx, stable=True).indices]

@@ -74,3 +74,12 @@ def test_node_out_rejects_mismatched_scores():
     with pytest.raises(ValueError):
         node_out_window(_t(np.arange(5)), _t(np.zeros((2, 0), np.int64)),
                         torch.ones(4, device=DEV), 0.3)
+
+
+def test_node_in_rejects_out_of_range_ids():
+    from neutrongt_amd.refine import node_in_window
+
+    nodes, buf = _t(np.array([0, 1])), _t(np.array([2, 3]))
+    ppr = _t(np.array([[0, 1], [2, 9]]))
+    with pytest.raises(IndexError):
+        node_in_window(nodes, buf, ppr, torch.ones(2, device=DEV), 1, _t(np.zeros((2, 0))), 5)
