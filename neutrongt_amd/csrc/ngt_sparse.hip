@@ -105,7 +105,7 @@ __device__ __forceinline__ bool packed_work(int64_t pw, int n_pwaves, int n_grou
 }
 
 template <typename T, int DH>
-__device__ __forceinline__ void fwd_packed(const T* __restrict__ q, const T* __restrict__ k,
+__device__ __forceinline__ float fwd_packed(const T* __restrict__ q, const T* __restrict__ k,
                                            const T* __restrict__ v,
                                            const int32_t* __restrict__ rowptr,
                                            const int32_t* __restrict__ col, int64_t row, int h,
@@ -136,9 +136,15 @@ __device__ __forceinline__ void fwd_packed(const T* __restrict__ q, const T* __r
   store_row<T, DH>(out + (row * H + h) * DH, o);
   rinv[row * H + h] = 1.0f / den;
   zbuf[row * H + h] = z;
+  return z;
 }
 
 // ------------------------------------------------------------------ forward
+// With one head group (every head of a row in one wave) the node score
+// mean_h Z[i,h] of a row that is not split is reduced across the row's head
+// lanes and written here; split rows get theirs in the finalize.  ns is null
+// when no node scores are wanted or with several head groups (then
+// k_node_score reads zbuf).
 template <typename T, int DH>
 __global__ __launch_bounds__(kBlock) void k_fwd(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
@@ -146,15 +152,22 @@ __global__ __launch_bounds__(kBlock) void k_fwd(
     int32_t n_groups, int32_t hg, int32_t H, int32_t L, float inv_scale, float lo, float hi,
     float eps, T* __restrict__ out, float* __restrict__ rinv, float* __restrict__ zbuf,
     float* __restrict__ part_acc, float* __restrict__ part_z, const int32_t* __restrict__ rowptr,
-    const int32_t* __restrict__ packed, int32_t n_packed, int32_t n_pwaves) {
+    const int32_t* __restrict__ packed, int32_t n_packed, int32_t n_pwaves,
+    float* __restrict__ ns, int32_t ns_len) {
   const int64_t gw = int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
   if (gw >= int64_t(n_items) * n_groups) {
-    int64_t prow;
-    int ph;
-    if (packed_work(gw - int64_t(n_items) * n_groups, n_pwaves, n_groups, hg, L, H, packed,
-                    n_packed, prow, ph))
-      fwd_packed<T, DH>(q, k, v, rowptr, col, prow, ph, H, inv_scale, lo, hi, eps, out, rinv,
-                        zbuf);
+    int64_t prow = 0;
+    int ph = 0;
+    float z = 0.f;
+    const bool has = packed_work(gw - int64_t(n_items) * n_groups, n_pwaves, n_groups, hg, L, H,
+                                 packed, n_packed, prow, ph);
+    if (has)
+      z = fwd_packed<T, DH>(q, k, v, rowptr, col, prow, ph, H, inv_scale, lo, hi, eps, out, rinv,
+                            zbuf);
+    if (ns) {  // all lanes take part; lanes without a row add 0
+      const float zs = reduce_heads(z, L);
+      if (has && ph == 0 && prow < ns_len) ns[prow] = zs / float(H);
+    }
     return;
   }
   int item;
@@ -210,6 +223,7 @@ __global__ __launch_bounds__(kBlock) void k_fwd(
   }
 
   reduce_slots<DH>(acc, z, L);
+  const float zs = ns && it.w < 0 ? reduce_heads(z, L) : 0.f;  // inactive lanes hold 0
   if (ln.slot != 0 || !ln.active) return;
   if (it.w < 0) {
     const float den = z + eps;
@@ -219,6 +233,7 @@ __global__ __launch_bounds__(kBlock) void k_fwd(
     store_row<T, DH>(out + (row * H + h) * DH, o);
     rinv[row * H + h] = 1.0f / den;
     zbuf[row * H + h] = z;
+    if (ns && h == 0 && row < ns_len) ns[row] = zs / float(H);
   } else {
     const int64_t p = int64_t(it.w) * H + h;
     store_f32<DH>(part_acc + p * DH, acc);
@@ -233,11 +248,20 @@ template <typename T, int DH>
 __global__ __launch_bounds__(kBlock) void k_fwd_finalize(
     const int4* __restrict__ splits, int32_t H, float eps, const float* __restrict__ part_acc,
     const float* __restrict__ part_z, T* __restrict__ out, float* __restrict__ rinv,
-    float* __restrict__ zbuf) {
-  __shared__ float red[2][kWavesPerBlock][kColTile];
+    float* __restrict__ zbuf, float* __restrict__ ns, int32_t ns_len) {
+  __shared__ float red[3][kWavesPerBlock][kColTile];
   const int4 sp = splits[blockIdx.x];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
+  // node score of the split row (tile 0 only): lanes = heads (H <= 64), the 4
+  // waves take every 4th part, meet in LDS below
+  const bool want_ns = ns && blockIdx.y == 0 && sp.x < ns_len;
+  if (want_ns) {
+    float zh = 0.f;
+    if (lane < H)
+      for (int p = wave; p < sp.z; p += kWavesPerBlock) zh += part_z[int64_t(sp.y + p) * H + lane];
+    red[2][wave][lane] = zh;
+  }
   const int ncols = H * DH;
   const int col = blockIdx.y * kColTile + lane;
   const bool ok = col < ncols;
@@ -253,6 +277,13 @@ __global__ __launch_bounds__(kBlock) void k_fwd_finalize(
   red[0][wave][lane] = a;
   red[1][wave][lane] = z;
   __syncthreads();
+  if (want_ns && wave == kWavesPerBlock - 1) {
+    float zh = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWavesPerBlock; ++w) zh += red[2][w][lane];
+    for (int off = 1; off < kWave; off <<= 1) zh += shfl_xor(zh, off);
+    if (lane == 0) ns[sp.x] = zh / float(H);
+  }
   if (wave != 0 || !ok) return;
 #pragma unroll
   for (int w = 1; w < kWavesPerBlock; ++w) {
@@ -437,17 +468,17 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
 
 // Split key rows: columns are (h, [dk | dv]) = 2*H*DH per part.
 template <typename T, int DH>
-__global__ __launch_bounds__(kBlock) void k_bwd_kv_finalize(const int4* __restrict__ splits,
-                                                            int32_t H,
-                                                            const float* __restrict__ part_kv,
-                                                            T* __restrict__ grad_k,
-                                                            T* __restrict__ grad_v) {
+__device__ __forceinline__ void bwd_kv_finalize_tile(const int4* __restrict__ splits, int32_t H,
+                                                     const float* __restrict__ part_kv,
+                                                     T* __restrict__ grad_k,
+                                                     T* __restrict__ grad_v, int split,
+                                                     int tile) {
   __shared__ float red[kWavesPerBlock][kColTile];
-  const int4 sp = splits[blockIdx.x];
+  const int4 sp = splits[split];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
   const int ncols = 2 * H * DH;
-  const int col = blockIdx.y * kColTile + lane;
+  const int col = tile * kColTile + lane;
   const bool ok = col < ncols;
   float a = 0.f;
   if (ok)
@@ -498,7 +529,16 @@ __global__ __launch_bounds__(kBlock) void k_bwd_q(
     const float* __restrict__ ds, const int4* __restrict__ items, int32_t n_items,
     int32_t n_groups, int32_t hg, int32_t H, int32_t L, float inv_scale, T* __restrict__ grad_q,
     float* __restrict__ part_q, const int32_t* __restrict__ rowptr,
-    const int32_t* __restrict__ packed, int32_t n_packed, int32_t n_pwaves) {
+    const int32_t* __restrict__ packed, int32_t n_packed, int32_t n_pwaves, int32_t q_blocks,
+    const int4* __restrict__ splits_k, int32_t kv_tiles, const float* __restrict__ part_kv,
+    T* __restrict__ grad_k, T* __restrict__ grad_v) {
+  // Blocks past the dQ work finish the split key rows of bwd_kv (their dK/dV
+  // partials): that work is independent of dQ, so it rides in this launch.
+  if (int32_t(blockIdx.x) >= q_blocks) {
+    const int f = int(blockIdx.x) - q_blocks;
+    bwd_kv_finalize_tile<T, DH>(splits_k, H, part_kv, grad_k, grad_v, f / kv_tiles, f % kv_tiles);
+    return;
+  }
   const int64_t gw0 = int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
   if (gw0 >= int64_t(n_items) * n_groups) {
     int64_t prow;
@@ -681,6 +721,8 @@ int launch_fwd(const ngt_window_csr* c, const void* q, const void* k, const void
   float* zbuf = reinterpret_cast<float*>(ws + lay.zbuf);
   const int pw_q = packed_waves(c->n_packed_q, L);
   const int64_t waves_q = (int64_t(c->n_items_q) + pw_q) * groups;
+  // one head group: the forward kernels write the node scores themselves
+  float* ns_direct = groups == 1 && ns && ns_len > 0 ? ns : nullptr;
   if (waves_q > 0) {
     KernelTimer timer_("sparse_fwd", st);
     hipLaunchKernelGGL((k_fwd<T, DH>), dim3(blocks_for(waves_q)), dim3(kBlock), 0, st,
@@ -688,7 +730,7 @@ int launch_fwd(const ngt_window_csr* c, const void* q, const void* k, const void
                        static_cast<const T*>(v), c->col, reinterpret_cast<const int4*>(c->items_q),
                        c->n_items_q, groups, hg, H, L, inv_scale, lo, hi, eps,
                        static_cast<T*>(out), rinv, zbuf, part_acc, part_z, c->rowptr, c->packed_q,
-                       c->n_packed_q, pw_q);
+                       c->n_packed_q, pw_q, ns_direct, ns_len);
     NGT_HIP_CHECK(hipGetLastError());
   }
   if (c->n_splits_q > 0) {
@@ -696,10 +738,10 @@ int launch_fwd(const ngt_window_csr* c, const void* q, const void* k, const void
     dim3 grid(c->n_splits_q, (H * DH + kColTile - 1) / kColTile);
     hipLaunchKernelGGL((k_fwd_finalize<T, DH>), grid, dim3(kBlock), 0, st,
                        reinterpret_cast<const int4*>(c->splits_q), H, eps, part_acc, part_z,
-                       static_cast<T*>(out), rinv, zbuf);
+                       static_cast<T*>(out), rinv, zbuf, ns_direct, ns_len);
     NGT_HIP_CHECK(hipGetLastError());
   }
-  if (ns && ns_len > 0) {
+  if (ns && ns_len > 0 && !ns_direct) {
     KernelTimer timer_("sparse_node_score", st);
     hipLaunchKernelGGL(k_node_score, dim3((ns_len + kBlock - 1) / kBlock), dim3(kBlock), 0, st,
                        zbuf, ns_len, H, ns);
@@ -741,23 +783,20 @@ int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void
                        c->t_rowptr, c->packed_k, c->n_packed_k, pw_k);
     NGT_HIP_CHECK(hipGetLastError());
   }
-  if (c->n_splits_k > 0) {
-    KernelTimer timer_("sparse_bwd_kv_finalize", st);
-    dim3 grid(c->n_splits_k, (2 * H * DH + kColTile - 1) / kColTile);
-    hipLaunchKernelGGL((k_bwd_kv_finalize<T, DH>), grid, dim3(kBlock), 0, st,
-                       reinterpret_cast<const int4*>(c->splits_k), H, part_kv,
-                       static_cast<T*>(gk), static_cast<T*>(gv));
-    NGT_HIP_CHECK(hipGetLastError());
-  }
   const int pw_q = packed_waves(c->n_packed_q, L);
   const int64_t waves_q = (int64_t(c->n_items_q) + pw_q) * groups;
-  if (waves_q > 0) {
+  const int kv_tiles = (2 * H * DH + kColTile - 1) / kColTile;
+  const int64_t q_blocks = blocks_for(waves_q);
+  const int64_t fin_blocks = int64_t(c->n_splits_k) * kv_tiles;
+  if (q_blocks + fin_blocks > 0) {
     KernelTimer timer_("sparse_bwd_q", st);
-    hipLaunchKernelGGL((k_bwd_q<T, DH>), dim3(blocks_for(waves_q)), dim3(kBlock), 0, st,
-                       static_cast<const T*>(k), c->col, c->q2t, ds,
+    hipLaunchKernelGGL((k_bwd_q<T, DH>), dim3(unsigned(q_blocks + fin_blocks)), dim3(kBlock), 0,
+                       st, static_cast<const T*>(k), c->col, c->q2t, ds,
                        reinterpret_cast<const int4*>(c->items_q), c->n_items_q, groups, hg, H, L,
                        inv_scale, static_cast<T*>(gq), part_q, c->rowptr, c->packed_q,
-                       c->n_packed_q, pw_q);
+                       c->n_packed_q, pw_q, int32_t(q_blocks),
+                       reinterpret_cast<const int4*>(c->splits_k), kv_tiles, part_kv,
+                       static_cast<T*>(gk), static_cast<T*>(gv));
     NGT_HIP_CHECK(hipGetLastError());
   }
   if (c->n_splits_q > 0) {
