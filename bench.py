@@ -307,8 +307,8 @@ def prep_bench(args, cfg, dev) -> dict:
 
 def model_step_bench(args, cfg, layers: int, dev) -> dict:
     """The window training step of train_eval.py:255-300 on one GPU: the
-    node-level Graphormer (cfg's hidden size, heads and layers; FFN width =
-    hidden as in the GPH presets) over one synthetic window, bf16 autocast,
+    node-level Graphormer, or GT for the GT presets (cfg's hidden size, heads
+    and layers; FFN width = hidden as in the presets) over one synthetic window, bf16 autocast,
     NLL over the window's training nodes, backward, AdamW.  Related keys' K/V
     come from a per-layer cache.  The loss is read back every step, as the
     reference's loop does (loss.item())."""
@@ -317,7 +317,7 @@ def model_step_bench(args, cfg, layers: int, dev) -> dict:
 
     from neutrongt_amd import _lib
     from neutrongt_amd import synthetic as S
-    from neutrongt_amd.encoder import WindowGraphormer, window_step
+    from neutrongt_amd.encoder import WindowGraphormer, WindowGT, window_step
 
     H, d = cfg.n_heads, cfg.head_dim
     hidden = H * d
@@ -334,9 +334,11 @@ def model_step_bench(args, cfg, layers: int, dev) -> dict:
                    for _ in range(2)) for _ in range(layers)] if R else None
     ei = torch.from_numpy(ei_np).to(dev)
     torch.manual_seed(S.SEED)
-    model = WindowGraphormer(layers, H, feat, hidden, n_classes, dropout_rate=0.3,
-                             input_dropout_rate=0.1, attention_dropout_rate=0.5,
-                             ffn_dim=hidden).to(dev).train()
+    # GT presets run the GT twin (post-LN, MLP readout); the others Graphormer
+    family = WindowGT if cfg.name.startswith("gt") else WindowGraphormer
+    model = family(layers, H, feat, hidden, n_classes, dropout_rate=0.3,
+                   input_dropout_rate=0.1, attention_dropout_rate=0.5,
+                   ffn_dim=hidden).to(dev).train()
     n_params = sum(p.numel() for p in model.parameters())
     opt = torch.optim.AdamW(model.parameters(), lr=1e-4, weight_decay=0.01)
     _log(f"[bench] window step: {layers} layers, hidden {hidden}, {n_params} parameters, "
@@ -372,7 +374,7 @@ def model_step_bench(args, cfg, layers: int, dev) -> dict:
         "value": ms, "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": ms, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16", "data": "synthetic",
-        "config": {"workload": (f"{cfg.name} window step: {layers}-layer Graphormer, hidden "
+        "config": {"workload": (f"{cfg.name} window step: {layers}-layer {family.__name__}, hidden "
                                 f"{hidden}, {H} heads, ffn {hidden}, {n_params} parameters, "
                                 f"n_q={cfg.n_q}, n_k={n_k}, E={E}, bf16 autocast, AdamW"),
                    "layers": layers, "parameters": n_params, "edges": E},

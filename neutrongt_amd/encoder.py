@@ -1,26 +1,33 @@
-"""The window encoder around the HIP attention core: the caller side of the path.
+"""The window encoders around the HIP attention core: the caller side of the path.
 
-Mirrors NeutronGT's node-level Graphormer with its sparse attention
-(NeutronGT/models/graphormer_dist_node_level.py): ``FeedForwardNetwork``
-(:18-30), ``MultiHeadAttention`` (:128-173), ``EncoderLayer`` (:176-206) and
-``Graphormer.forward`` without the structural encodings (:242-381; the shipped
-scripts run with ``struct_enc`` False).  Sub-module and parameter names are the
-reference's, so a reference ``state_dict`` loads with ``strict=False`` (the
-unused centrality/attention-bias embeddings are the only extra keys).
+Two model families, as in NeutronGT's node-level pipeline (struct_enc False,
+the shipped setting):
 
-Projections, LayerNorm, GELU and the FFN are plain library GEMMs and
-elementwise ops (hipBLASLt through torch); run them under
-``torch.autocast("cuda", dtype=torch.bfloat16)`` for the bf16 window step.  The
-attention core is ``CoreAttention`` (HIP kernels only).
+  WindowGraphormer  NeutronGT/models/graphormer_dist_node_level.py: pre-LN
+                    ``EncoderLayer`` (:176-206) with ``MultiHeadAttention``
+                    (:128-173, output projection inside) and the GELU
+                    ``FeedForwardNetwork`` (:18-30); final LayerNorm and a
+                    linear readout (``Graphormer.forward``, :242-381).
+  WindowGT          NeutronGT/models/gt_dist_node_level_single_window.py:
+                    post-LN ``EncoderLayer`` (:305-353) whose attention block
+                    has no output projection (:230-302), ReLU FFN of width
+                    2*hidden, and the ``MLPReadout`` head (``GT_SW``, :505-680).
+
+Sub-module and parameter names are the reference's, so a reference
+``state_dict`` loads with ``strict=False`` (the unused structural-encoding
+embeddings are the only extra keys).  Projections, LayerNorm, activations and
+the FFN are plain library GEMMs and elementwise ops (hipBLASLt through torch);
+run them under ``torch.autocast("cuda", dtype=torch.bfloat16)`` for the bf16
+window step.  The attention core is ``CoreAttention`` (HIP kernels only).
 
 Related keys.  A window's queries may also attend to out-of-window related
 nodes whose K/V come from a cache (one ``(k, v)`` pair of ``[R, H, d]`` tensors
 per layer, detached).  They are appended after the window's own key rows, so
 edge_index key ids ``>= N`` address them; queries are the window's N nodes.
 The reference's ``dup_nodes_kv_cache`` (a detached K/V prefix replacing the
-first rows, :148-168) is the same mechanism placed in front of the window's
-rows; it is dead in the reference's training loop and is not offered here.
-``window_step`` mirrors one iteration of ``train_epoch``
+first rows, graphormer_dist_node_level.py:148-168) is the same mechanism placed
+in front of the window's rows; it is dead in the reference's training loop and
+is not offered here.  ``window_step`` mirrors one iteration of ``train_epoch``
 (NeutronGT/core/node_level_pipeline/train_eval.py:255-300) on one GPU.
 """
 from __future__ import annotations
@@ -36,7 +43,7 @@ from .attention import CoreAttention
 
 def init_params(module: nn.Module, n_layers: int) -> None:
     """Linear weights ~ N(0, 0.02/sqrt(n_layers)), zero bias; embeddings
-    N(0, 0.02) (graphormer_dist_node_level.py:10-15)."""
+    N(0, 0.02) (graphormer_dist_node_level.py:10-15; the GT twin's :22-28)."""
     if isinstance(module, nn.Linear):
         nn.init.normal_(module.weight, mean=0.0, std=0.02 / math.sqrt(n_layers))
         if module.bias is not None:
@@ -46,7 +53,7 @@ def init_params(module: nn.Module, n_layers: int) -> None:
 
 
 class FeedForwardNetwork(nn.Module):
-    """Linear -> GELU -> Linear (:18-30)."""
+    """Linear -> GELU -> Linear (graphormer_dist_node_level.py:18-30)."""
 
     def __init__(self, hidden_size: int, ffn_size: int, dropout_rate: float = 0.0):
         super().__init__()
@@ -58,10 +65,10 @@ class FeedForwardNetwork(nn.Module):
         return self.layer2(self.gelu(self.layer1(x)))
 
 
-class MultiHeadAttention(nn.Module):
-    """Q/K/V projections, the attention core, output projection (:128-173).
+class _Attention(nn.Module):
+    """Q/K/V projections and the attention core, shared by both families.
 
-    forward(x [1, N, hidden], edge_index, attn_type, kv_cache=None)
+    attend(x [1, N, hidden], edge_index, attn_type, kv_cache=None)
       -> (y [1, N, hidden], node_score, [k, v])
     ``kv_cache``: optional ``(k_r, v_r)``, each ``[R, H, d]``, appended after
     the window's own keys (related nodes; no gradient flows into them).
@@ -77,9 +84,8 @@ class MultiHeadAttention(nn.Module):
         self.linear_k = nn.Linear(hidden_size, num_heads * self.att_size)
         self.linear_v = nn.Linear(hidden_size, num_heads * self.att_size)
         self.local_attn = CoreAttention(hidden_size, attention_dropout_rate, num_heads)
-        self.output_layer = nn.Linear(num_heads * self.att_size, hidden_size)
 
-    def forward(self, x, edge_index=None, attn_type="sparse", kv_cache=None):
+    def attend(self, x, edge_index, attn_type, kv_cache):
         b, n, _ = x.shape
         H, d = self.num_heads, self.att_size
         q = self.linear_q(x).view(b, n, H, d)
@@ -94,14 +100,39 @@ class MultiHeadAttention(nn.Module):
             v_all = torch.cat([v, v_r.detach().to(v.dtype).unsqueeze(0)], dim=1)
         # the core needs one dtype for q, k, v (autocast gives bf16 for all three)
         y, score = self.local_attn(q, k_all, v_all, None, edge_index, attn_type)
-        y = self.output_layer(y)
-        if y.shape != x.shape:
-            raise RuntimeError(f"attention output {tuple(y.shape)} != input {tuple(x.shape)}")
         return y, score, [k, v]
 
 
+class MultiHeadAttention(_Attention):
+    """Graphormer attention block: projections, core, output projection
+    (graphormer_dist_node_level.py:128-173)."""
+
+    def __init__(self, hidden_size: int, attention_dropout_rate: float, num_heads: int):
+        super().__init__(hidden_size, attention_dropout_rate, num_heads)
+        self.output_layer = nn.Linear(num_heads * self.att_size, hidden_size)
+
+    def forward(self, x, edge_index=None, attn_type="sparse", kv_cache=None):
+        y, score, kv = self.attend(x, edge_index, attn_type, kv_cache)
+        y = self.output_layer(y)
+        if y.shape != x.shape:
+            raise RuntimeError(f"attention output {tuple(y.shape)} != input {tuple(x.shape)}")
+        return y, score, kv
+
+
+class GTMultiHeadAttention(_Attention):
+    """GT attention block: projections and core, no output projection (the
+    layer's ``O`` follows it; gt_dist_node_level_single_window.py:230-302)."""
+
+    def forward(self, x, edge_index=None, attn_type="sparse", kv_cache=None):
+        y, score, kv = self.attend(x, edge_index, attn_type, kv_cache)
+        if y.shape != x.shape:
+            raise RuntimeError(f"attention output {tuple(y.shape)} != input {tuple(x.shape)}")
+        return y, score, kv
+
+
 class EncoderLayer(nn.Module):
-    """Pre-LN block: x + Drop(MHA(LN(x))), then x + Drop(FFN(LN(x))) (:176-206)."""
+    """Pre-LN block: x + Drop(MHA(LN(x))), then x + Drop(FFN(LN(x)))
+    (graphormer_dist_node_level.py:176-206)."""
 
     def __init__(self, hidden_size: int, ffn_size: int, dropout_rate: float,
                  attention_dropout_rate: float, num_heads: int):
@@ -121,13 +152,73 @@ class EncoderLayer(nn.Module):
         return x, score, kv
 
 
-class WindowGraphormer(nn.Module):
-    """Node-level Graphormer over one window (:242-381, struct_enc False).
+class GTEncoderLayer(nn.Module):
+    """GT post-LN block (gt_dist_node_level_single_window.py:305-353):
+    y = O(Drop(MHA(x))); x = LN1(x + y); then the FFN (hidden -> 2*hidden ->
+    hidden, ReLU, dropout in between) is applied to y -- not to x -- and
+    x = LN2(x + FFN(y)).  The FFN input is the reference's as written (its own
+    comment questions it); kept so the layer computes the same function."""
+
+    def __init__(self, hidden_size: int, ffn_size: int, dropout_rate: float,
+                 attention_dropout_rate: float, num_heads: int):
+        super().__init__()
+        self.self_attention_norm = nn.LayerNorm(hidden_size)  # declared, unused (as in the reference)
+        self.self_attention = GTMultiHeadAttention(hidden_size, attention_dropout_rate, num_heads)
+        self.self_attention_dropout = nn.Dropout(dropout_rate)
+        self.O = nn.Linear(hidden_size, hidden_size)
+        self.layer_norm1 = nn.LayerNorm(hidden_size)
+        self.FFN_layer1 = nn.Linear(hidden_size, hidden_size * 2)
+        self.FFN_layer2 = nn.Linear(hidden_size * 2, hidden_size)
+        self.layer_norm2 = nn.LayerNorm(hidden_size)
+
+    def forward(self, x, edge_index=None, attn_type="sparse", kv_cache=None):
+        y, score, kv = self.self_attention(x, edge_index, attn_type, kv_cache)
+        y = self.O(self.self_attention_dropout(y))
+        x = self.layer_norm1(x + y)
+        y = self.FFN_layer2(self.self_attention_dropout(F.relu(self.FFN_layer1(y))))
+        x = self.layer_norm2(x + y)
+        return x, score, kv
+
+
+class MLPReadout(nn.Module):
+    """hidden -> hidden/2 -> hidden/4 -> output, ReLU between
+    (gt_dist_node_level_single_window.py:356-372)."""
+
+    def __init__(self, input_dim: int, output_dim: int, L: int = 2):
+        super().__init__()
+        dims = [input_dim // 2 ** i for i in range(L + 1)]
+        self.FC_layers = nn.ModuleList(
+            [nn.Linear(dims[i], dims[i + 1]) for i in range(L)] + [nn.Linear(dims[L], output_dim)])
+        self.L = L
+
+    def forward(self, x):
+        for i in range(self.L):
+            x = F.relu(self.FC_layers[i](x))
+        return self.FC_layers[self.L](x)
+
+
+class _WindowModel(nn.Module):
+    """node_encoder -> input dropout -> layers -> readout -> log_softmax.
 
     forward(x [N, input_dim], edge_index [2, E], attn_type="sparse",
             kv_cache=None (list of per-layer (k_r, v_r)))
       -> (log_probs [N, output_dim], per-layer node scores (detached))
     """
+
+    def forward(self, x, edge_index, attn_type="sparse", kv_cache=None):
+        if kv_cache is not None and len(kv_cache) != self.n_layers:
+            raise ValueError(f"kv_cache has {len(kv_cache)} entries for {self.n_layers} layers")
+        h = self.input_dropout(self.node_encoder(x.unsqueeze(0)))
+        scores = []
+        for i, layer in enumerate(self.layers):
+            h, score, _ = layer(h, edge_index, attn_type,
+                                kv_cache[i] if kv_cache is not None else None)
+            scores.append(score.detach() if score is not None else None)
+        return F.log_softmax(self.readout(h[0]).float(), dim=1), scores
+
+
+class WindowGraphormer(_WindowModel):
+    """Node-level Graphormer over one window (graphormer_dist_node_level.py:242-381)."""
 
     def __init__(self, n_layers: int, num_heads: int, input_dim: int, hidden_dim: int,
                  output_dim: int, dropout_rate: float = 0.0, input_dropout_rate: float = 0.0,
@@ -145,18 +236,31 @@ class WindowGraphormer(nn.Module):
         self.downstream_out_proj = nn.Linear(hidden_dim, output_dim)
         self.apply(lambda m: init_params(m, n_layers))
 
-    def forward(self, x, edge_index, attn_type="sparse", kv_cache=None):
-        if kv_cache is not None and len(kv_cache) != self.n_layers:
-            raise ValueError(f"kv_cache has {len(kv_cache)} entries for {self.n_layers} layers")
-        h = self.input_dropout(self.node_encoder(x.unsqueeze(0)))
-        scores = []
-        for i, layer in enumerate(self.layers):
-            h, score, _ = layer(h, edge_index, attn_type,
-                                kv_cache[i] if kv_cache is not None else None)
-            scores.append(score.detach() if score is not None else None)
-        h = self.final_ln(h)
-        out = self.downstream_out_proj(h[0])
-        return F.log_softmax(out.float(), dim=1), scores
+    def readout(self, h):
+        return self.downstream_out_proj(self.final_ln(h))
+
+
+class WindowGT(_WindowModel):
+    """Node-level GT over one window (GT_SW, gt_dist_node_level_single_window.py:505-680).
+    ``ffn_dim`` is accepted and unused: the GT layer's FFN is 2*hidden wide."""
+
+    def __init__(self, n_layers: int, num_heads: int, input_dim: int, hidden_dim: int,
+                 output_dim: int, dropout_rate: float = 0.0, input_dropout_rate: float = 0.0,
+                 attention_dropout_rate: float = 0.0, ffn_dim: int | None = None):
+        super().__init__()
+        self.num_heads = num_heads
+        self.n_layers = n_layers
+        self.node_encoder = nn.Linear(input_dim, hidden_dim)
+        self.input_dropout = nn.Dropout(input_dropout_rate)
+        self.layers = nn.ModuleList([
+            GTEncoderLayer(hidden_dim, ffn_dim or hidden_dim, dropout_rate,
+                           attention_dropout_rate, num_heads) for _ in range(n_layers)])
+        self.MLP_layer = MLPReadout(hidden_dim, output_dim)
+        self.downstream_out_proj = nn.Linear(hidden_dim, output_dim)  # declared, unused
+        self.apply(lambda m: init_params(m, n_layers))
+
+    def readout(self, h):
+        return self.MLP_layer(h)
 
 
 def window_step(model: nn.Module, optimizer, x, edge_index, labels, train_mask,

@@ -35,11 +35,16 @@ class OracleCore(nn.Module):
         return x[:n_q].reshape(1, n_q, -1).to(out_dtype), score
 
 
-def _build(dtype=torch.float32, seed=0):
-    from neutrongt_amd.encoder import WindowGraphormer
+def _family(name):
+    from neutrongt_amd.encoder import WindowGraphormer, WindowGT
 
+    return {"graphormer": WindowGraphormer, "gt": WindowGT}[name]
+
+
+def _build(dtype=torch.float32, seed=0, family="graphormer"):
+    cls = _family(family)
     torch.manual_seed(seed)
-    model = WindowGraphormer(2, H, FEAT, H * D_HEAD, CLASSES, ffn_dim=48)
+    model = cls(2, H, FEAT, H * D_HEAD, CLASSES, ffn_dim=48)
     # weights large enough that scores span the clamp range (the default init
     # is 0.02/sqrt(layers), which makes every score ~0)
     for m in model.modules():
@@ -52,7 +57,7 @@ def _build(dtype=torch.float32, seed=0):
     cache = [tuple(torch.randn(R, H, D_HEAD, generator=g) for _ in range(2)) for _ in range(2)]
     labels = torch.randint(0, CLASSES, (N_Q,), generator=g)
     mask = torch.rand(N_Q, generator=g) < 0.6
-    ref = WindowGraphormer(2, H, FEAT, H * D_HEAD, CLASSES, ffn_dim=48).to(dtype)
+    ref = cls(2, H, FEAT, H * D_HEAD, CLASSES, ffn_dim=48).to(dtype)
     ref.load_state_dict({k: v.to(dtype) for k, v in model.state_dict().items()})
     for layer in ref.layers:
         layer.self_attention.local_attn = OracleCore(H)
@@ -68,13 +73,16 @@ def _run(model, x, ei, cache, labels, mask, autocast=None):
         out, scores = model(x, ei, "sparse", cache)
     loss = F.nll_loss(out[mask], labels[mask])
     loss.backward()
-    grads = {n: p.grad.detach().double().cpu() for n, p in model.named_parameters()}
+    # (the GT model declares modules its forward never uses: no gradient)
+    grads = {n: p.grad.detach().double().cpu() for n, p in model.named_parameters()
+             if p.grad is not None}
     return out.detach(), [s.cpu() for s in scores], loss.detach(), grads
 
 
-def test_encoder_fp32_matches_oracle_encoder():
-    model, ref32, x, ei, cache, labels, mask = _build()
-    _, ref64, *_ = _build(torch.float64)
+@pytest.mark.parametrize("family", ["graphormer", "gt"])
+def test_encoder_fp32_matches_oracle_encoder(family):
+    model, ref32, x, ei, cache, labels, mask = _build(family=family)
+    _, ref64, *_ = _build(torch.float64, family=family)
     dev = torch.device("cuda")
     model = model.to(dev)
     gpu = _run(model, x.to(dev), ei.to(dev), [tuple(t.to(dev) for t in c) for c in cache],
@@ -90,15 +98,20 @@ def test_encoder_fp32_matches_oracle_encoder():
         assert_parity(gpu[3][n], c32[3][n], c64[3][n], torch.float32, f"grad {n}")
 
 
-def test_encoder_bf16_autocast_matches_oracle_encoder():
+@pytest.mark.parametrize("family", ["graphormer", "gt"])
+def test_encoder_bf16_autocast_matches_oracle_encoder(family):
     """bf16 autocast: the encoder with the HIP core against the same encoder,
     same GEMMs (bf16 autocast on the GPU), with the oracle as its attention
     core, at the bf16 tolerance.  Against the fp32 encoder on the CPU the
     difference is dominated by the bf16 GEMMs themselves (measured ~2.5e-2 on
-    LayerNorm-weight gradients), so that comparison is a 6e-2 sanity bound."""
-    model, ref32, x, ei, cache, labels, mask = _build(seed=3)
+    Graphormer's LayerNorm-weight gradients), so that comparison is a 6e-2
+    sanity bound -- on the log-probs for both families and on the gradients
+    for Graphormer only: in the post-LN GT layers the first layers' weight
+    gradients are small differences of large terms, and bf16 GEMM rounding
+    alone moves them by tens of percent (with either attention core)."""
+    model, ref32, x, ei, cache, labels, mask = _build(seed=3, family=family)
     dev = torch.device("cuda")
-    orc = _build(seed=3)[1].to(dev)  # fp32 weights, oracle core, on the GPU
+    orc = _build(seed=3, family=family)[1].to(dev)  # fp32 weights, oracle core, on the GPU
     model = model.to(dev)
     cache_bf = [tuple(t.to(torch.bfloat16) for t in c) for c in cache]
     args = (x.to(dev), ei.to(dev), [tuple(t.to(dev) for t in c) for c in cache_bf],
@@ -111,14 +124,16 @@ def test_encoder_bf16_autocast_matches_oracle_encoder():
         assert_close(gpu[3][n], ref[3][n], torch.bfloat16, f"grad {n}")
     cpu = _run(ref32, x, ei, [tuple(t.float() for t in c) for c in cache_bf], labels, mask)
     assert relerr(gpu[0], cpu[0]) <= 6e-2
-    for n in gpu[3]:
-        assert relerr(gpu[3][n], cpu[3][n]) <= 6e-2, n
+    if family == "graphormer":
+        for n in gpu[3]:
+            assert relerr(gpu[3][n], cpu[3][n]) <= 6e-2, n
 
 
-def test_window_step_trains_and_matches_the_first_loss():
+@pytest.mark.parametrize("family", ["graphormer", "gt"])
+def test_window_step_trains_and_matches_the_first_loss(family):
     from neutrongt_amd.encoder import window_step
 
-    model, ref32, x, ei, cache, labels, mask = _build(seed=5)
+    model, ref32, x, ei, cache, labels, mask = _build(seed=5, family=family)
     dev = torch.device("cuda")
     model = model.to(dev)
     opt = torch.optim.AdamW(model.parameters(), lr=3e-3, weight_decay=0.01)
@@ -146,3 +161,20 @@ def test_kv_cache_shape_is_checked():
         model(x, ei, "sparse", bad)
     with pytest.raises(ValueError):
         model(x, ei, "sparse", bad * 2)
+
+
+def test_state_dict_names_follow_the_reference():
+    """Parameter names of the reference modules (so their checkpoints load)."""
+    from neutrongt_amd.encoder import WindowGraphormer, WindowGT
+
+    g = set(WindowGraphormer(1, 2, 4, 8, 3).state_dict())
+    assert {"node_encoder.weight", "layers.0.self_attention_norm.weight",
+            "layers.0.self_attention.linear_q.weight", "layers.0.self_attention.output_layer.bias",
+            "layers.0.ffn_norm.bias", "layers.0.ffn.layer1.weight", "layers.0.ffn.layer2.bias",
+            "final_ln.weight", "downstream_out_proj.weight"} <= g
+    t = set(WindowGT(1, 2, 4, 8, 3).state_dict())
+    assert {"layers.0.self_attention.linear_v.bias", "layers.0.O.weight",
+            "layers.0.layer_norm1.weight", "layers.0.FFN_layer1.weight",
+            "layers.0.FFN_layer2.bias", "layers.0.layer_norm2.bias",
+            "MLP_layer.FC_layers.0.weight", "MLP_layer.FC_layers.2.bias"} <= t
+    assert WindowGT(1, 2, 4, 8, 3).layers[0].FFN_layer1.out_features == 16
