@@ -340,7 +340,8 @@ def model_step_bench(args, cfg, layers: int, dev) -> dict:
                    input_dropout_rate=0.1, attention_dropout_rate=0.5,
                    ffn_dim=hidden).to(dev).train()
     n_params = sum(p.numel() for p in model.parameters())
-    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, weight_decay=0.01)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, weight_decay=0.01,
+                            capturable=bool(args.graph))
     _log(f"[bench] window step: {layers} layers, hidden {hidden}, {n_params} parameters, "
          f"n_q={cfg.n_q} n_k={n_k} E={E}")
 
@@ -348,9 +349,40 @@ def model_step_bench(args, cfg, layers: int, dev) -> dict:
         loss, _ = window_step(model, opt, x, ei, labels, train_mask, cache, torch.bfloat16)
         return loss.item()
 
+    if args.tunable:
+        # GEMM kernel choice by measurement (hipBLASLt/rocBLAS candidates); a
+        # results file that already holds these shapes is only read
+        torch.cuda.tunable.enable(True)
+        torch.cuda.tunable.set_filename(args.tunable)
+        tuned = os.path.exists(args.tunable)
+        if tuned:
+            torch.cuda.tunable.read_file(args.tunable)
+        torch.cuda.tunable.tuning_enable(not tuned)
     for _ in range(max(args.warmup, 1)):
         step()
     torch.cuda.synchronize()
+    if args.tunable and not tuned:
+        torch.cuda.tunable.tuning_enable(False)  # the results file is written at exit
+    if args.graph:
+        # the whole step (forward, loss, backward, AdamW) as one HIP graph;
+        # warm-up on a side stream first, as graph capture requires
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                window_step(model, opt, x, ei, labels, train_mask, cache, torch.bfloat16)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            static_loss, _ = window_step(model, opt, x, ei, labels, train_mask, cache,
+                                         torch.bfloat16)
+
+        def step():  # noqa: F811
+            graph.replay()
+            return static_loss.item()
+
+        step()
+        torch.cuda.synchronize()
     times, losses = [], []
     for _ in range(args.steps):
         torch.cuda.synchronize()
@@ -377,7 +409,8 @@ def model_step_bench(args, cfg, layers: int, dev) -> dict:
         "config": {"workload": (f"{cfg.name} window step: {layers}-layer {family.__name__}, hidden "
                                 f"{hidden}, {H} heads, ffn {hidden}, {n_params} parameters, "
                                 f"n_q={cfg.n_q}, n_k={n_k}, E={E}, bf16 autocast, AdamW"),
-                   "layers": layers, "parameters": n_params, "edges": E},
+                   "layers": layers, "parameters": n_params, "edges": E,
+                   "hip_graph": bool(args.graph)},
         "attention_ms_per_step": attn_ms,
         "edges_per_s_in_step": layers * E / (ms * 1e-3),
         "losses": [losses[0], losses[-1]],
@@ -400,6 +433,9 @@ def main(argv=None) -> int:
     ap.add_argument("--prep", action="store_true",
                     help="time the window assembly instead (related nodes, induced subgraph, "
                          "window CSR, feature gather) on the config's global graph")
+    ap.add_argument("--tunable", default=None, metavar="CSV",
+                    help="with --model: let torch's TunableOp pick the GEMM kernels, reading "
+                         "(and, if missing, writing) this results file")
     ap.add_argument("--model", action="store_true",
                     help="time the whole window training step instead (encoder projections, "
                          "LayerNorm, FFN and attention, NLL, backward, AdamW) in bf16 autocast")

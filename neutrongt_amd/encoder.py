@@ -268,13 +268,20 @@ def window_step(model: nn.Module, optimizer, x, edge_index, labels, train_mask,
     """One window iteration of train_eval.py:255-300 on one GPU: forward, NLL
     over the window's training nodes, backward, optimizer step.  Returns
     (loss tensor, last layer's node scores).  ``autocast_dtype`` (e.g.
-    torch.bfloat16) runs the forward under torch.autocast."""
+    torch.bfloat16) runs the forward under torch.autocast.
+
+    Nothing here synchronises with the host, so the whole step can be captured
+    in a HIP graph (with a capturable optimizer): the masked mean is a
+    weighted sum, not a boolean selection (same value as the reference's
+    ``loss[mask_train].mean()``)."""
     if autocast_dtype is not None:
-        with torch.autocast("cuda", dtype=autocast_dtype):
+        capturing = torch.cuda.is_current_stream_capturing()
+        with torch.autocast("cuda", dtype=autocast_dtype, cache_enabled=not capturing):
             out, scores = model(x, edge_index, "sparse", kv_cache)
     else:
         out, scores = model(x, edge_index, "sparse", kv_cache)
-    loss = F.nll_loss(out[train_mask], labels[train_mask])
+    w = train_mask.to(out.dtype)
+    loss = (F.nll_loss(out, labels, reduction="none") * w).sum() / w.sum()
     optimizer.zero_grad(set_to_none=True)
     loss.backward()
     optimizer.step()
