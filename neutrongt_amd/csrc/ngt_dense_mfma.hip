@@ -74,11 +74,6 @@ __device__ __forceinline__ float sum4(s16x4 x) {
          (bf16_to_f32(static_cast<uint16_t>(x[2])) + bf16_to_f32(static_cast<uint16_t>(x[3])));
 }
 
-__device__ __forceinline__ s16x4 ones4() {
-  s16x4 r;
-  r[0] = r[1] = r[2] = r[3] = static_cast<short>(0x3f80);  // bf16 1.0
-  return r;
-}
 
 // ------------------------------------------------------------- LDS staging
 // A block stages kSB rows (keys or queries) of one head at a time: each thread
@@ -132,13 +127,32 @@ struct Stage {
 };
 
 __device__ __forceinline__ s16x4 lds4(const short* p) {
-  const uint2 w = *reinterpret_cast<const uint2*>(p);
-  s16x4 r;
-  r[0] = static_cast<short>(w.x & 0xffffu);
-  r[1] = static_cast<short>(w.x >> 16);
-  r[2] = static_cast<short>(w.y & 0xffffu);
-  r[3] = static_cast<short>(w.y >> 16);
-  return r;
+  return __builtin_bit_cast(s16x4, *reinterpret_cast<const uint2*>(p));
+}
+
+// Transposed stages are kT rows tall: rows DH .. kT-1 hold constants written
+// once (zeros, and for the forward with DH < 32 a row of ones at DH), so every
+// lane reads its B operand unconditionally -- no exec-masked LDS reads, whose
+// waits would serialise the K steps.
+template <int DH>
+__device__ __forceinline__ void fill_pad_rows(short (*t)[kSB + 8], bool ones_row) {
+  constexpr int kPadRows = kT - DH;
+  for (int e = threadIdx.x; e < kPadRows * (kSB + 8); e += kBlock) {
+    const int r = DH + e / (kSB + 8), c = e % (kSB + 8);
+    t[r][c] = (ones_row && r == DH) ? static_cast<short>(0x3f80) : static_cast<short>(0);
+  }
+}
+
+// max(x, x of lane ^ 32): v_permlane32_swap exchanges the two wave halves.
+__device__ __forceinline__ float max_halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 // ------------------------------------------------------------------ forward
@@ -152,7 +166,7 @@ __global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
                                                    float* __restrict__ lse) {
   constexpr int NC = DH / 8;  // K chunks of the QK^T contraction
   __shared__ __align__(16) short ks[kSB][DH + 8];  // K rows
-  __shared__ __align__(16) short vt[DH][kSB + 8];  // V^T: [c][key]
+  __shared__ __align__(16) short vt[kT][kSB + 8];  // V^T: [c][key], rows >= DH constant
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
   const int half = lane >> 5;
@@ -171,6 +185,7 @@ __global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
   float m = -INFINITY, l = 0.f;
   f32x16 acc = zero16();  // O^T[c][q]: c = 8*(i/4) + 4*half + i%4
 
+  fill_pad_rows<DH>(vt, true);
   Stage<DH> pk, pv;
   pk.load(k, 0, n_k, H, h);
   pv.load(v, 0, n_k, H, h);
@@ -200,7 +215,7 @@ __global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
           mx = fmaxf(mx, st[i]);
         }
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+      mx = max_halves(mx);
       const float m_new = fmaxf(m, mx * s2);  // scale > 0: max commutes with scaling
       const float alpha = __builtin_amdgcn_exp2f(m - m_new);
       if (__any(alpha != 1.f)) {
@@ -220,19 +235,18 @@ __global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
       }
       // O^T += V^T P^T, K steps of 8 keys.  For d < 32 row c = d of V^T is all
       // ones, so O^T row d accumulates the row sum of the (rounded) P.
+      s16x4 va[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const s16x4 va = l32 < DH ? lds4(&vt[l32][r0 + 8 * j + 4 * half])
-                                  : (l32 == DH ? ones4() : zero4());
-        acc = mfma(va, pb[j], acc);
-      }
+      for (int j = 0; j < 4; ++j) va[j] = lds4(&vt[l32][r0 + 8 * j + 4 * half]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc = mfma(va[j], pb[j], acc);
     }
   }
   if constexpr (DH < 32) {
     // O^T row d sits in acc[d/2] of the half-0 lanes (d is a multiple of 8).
     l = __shfl(acc[DH / 2], l32, kWave);
   } else {
-    l += __shfl_xor(l, 32, kWave);
+    l = sum_halves(l);
   }
   if (!q_ok) return;
   const float inv = n_k > 0 ? 1.0f / l : 0.f;
@@ -282,7 +296,7 @@ __global__ __launch_bounds__(kBlock) void k_mf_scores(const bf16_t* __restrict__
       for (int i = 0; i < 16; ++i) s += fabsf(st[i]);  // padded query rows are zero
     }
   }
-  s += __shfl_xor(s, 32, kWave);
+  s = sum_halves(s);
   if (k_ok && half == 0) part[int64_t(h) * n_k + kj] = s * scale;
 }
 
@@ -299,8 +313,8 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_kv(
   constexpr int NC = DH / 8;
   __shared__ __align__(16) short qs[kSB][DH + 8];
   __shared__ __align__(16) short gs[kSB][DH + 8];
-  __shared__ __align__(16) short qt[DH][kSB + 8];
-  __shared__ __align__(16) short gt[DH][kSB + 8];
+  __shared__ __align__(16) short qt[kT][kSB + 8];  // rows >= DH zero
+  __shared__ __align__(16) short gt[kT][kSB + 8];
   __shared__ __align__(16) float ls[kSB];
   __shared__ __align__(16) float dd[kSB];
   const int lane = threadIdx.x & (kWave - 1);
@@ -329,6 +343,8 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_kv(
       pd = ok ? dsum[int64_t(h) * n_q + qb + threadIdx.x] : 0.f;
     }
   };
+  fill_pad_rows<DH>(qt, false);
+  fill_pad_rows<DH>(gt, false);
   prefetch(0);
   for (int qb = 0; qb < n_q; qb += kSB) {
     __syncthreads();
@@ -366,13 +382,17 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_kv(
         dsa[j] = pack4(p0 * (dp[4 * j] - dv4.x), p1 * (dp[4 * j + 1] - dv4.y),
                        p2 * (dp[4 * j + 2] - dv4.z), p3 * (dp[4 * j + 3] - dv4.w));
       }
+      s16x4 gb[4], qbq[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int c0 = r0 + 8 * j + 4 * half;
-        const s16x4 gb = l32 < DH ? lds4(&gt[l32][c0]) : zero4();
-        const s16x4 qbq = l32 < DH ? lds4(&qt[l32][c0]) : zero4();
-        dv = mfma(pa[j], gb, dv);
-        dk = mfma(dsa[j], qbq, dk);
+        gb[j] = lds4(&gt[l32][c0]);
+        qbq[j] = lds4(&qt[l32][c0]);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        dv = mfma(pa[j], gb[j], dv);
+        dk = mfma(dsa[j], qbq[j], dk);
       }
     }
   }
@@ -399,7 +419,7 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_q(
   constexpr int NC = DH / 8;
   __shared__ __align__(16) short ks[kSB][DH + 8];
   __shared__ __align__(16) short vs[kSB][DH + 8];
-  __shared__ __align__(16) short kt[DH][kSB + 8];
+  __shared__ __align__(16) short kt[kT][kSB + 8];  // rows >= DH zero
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
   const int half = lane >> 5;
@@ -417,6 +437,7 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_q(
   const float Dq = q_ok ? dsum[int64_t(h) * n_q + qi] : 0.f;
   const float s2 = scale * kLog2e;
   f32x16 dq = zero16();  // D[q][c]: q = 8*(i/4)+4*half+i%4 (tile row), c = l32
+  fill_pad_rows<DH>(kt, false);
   Stage<DH> pk, pv;
   pk.load(k, 0, n_k, H, h);
   pv.load(v, 0, n_k, H, h);
@@ -452,11 +473,11 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_q(
       s16x4 dsa[4];  // dS as A operand: A[q][key step row] from the D[key][q] layout
 #pragma unroll
       for (int j = 0; j < 4; ++j) dsa[j] = pack4(ds[4 * j], ds[4 * j + 1], ds[4 * j + 2], ds[4 * j + 3]);
+      s16x4 kbk[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const s16x4 kbk = l32 < DH ? lds4(&kt[l32][r0 + 8 * j + 4 * half]) : zero4();
-        dq = mfma(dsa[j], kbk, dq);
-      }
+      for (int j = 0; j < 4; ++j) kbk[j] = lds4(&kt[l32][r0 + 8 * j + 4 * half]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) dq = mfma(dsa[j], kbk[j], dq);
     }
   }
   if (l32 >= DH) return;
