@@ -236,6 +236,41 @@ int ngt_segment_sum_f32(const float* vals, int64_t n_vals, const int64_t* seg, i
                         float* out, int32_t* bad, void* stream);
 
 /*
+ * Personalised PageRank by APPNP propagation with per-row top-k: one step of
+ * personal_pagerank_appnp (NeutronGT/core/ppr_backends/appnp_backend.py:
+ * 179-224, whose SpGEMM is cusparse_spgemm.cu:65-267) for n_rows seed rows.
+ *
+ * Graph: CSR rowptr [n_nodes+1], col (int64), inv_deg[c] = 1 / max(deg(c), 1)
+ * (fp32, the transition value of every edge c -> n).  State: fixed width K
+ * (1 <= K <= 64): row r holds st_cnt[r] entries st_col/st_val[r*K + j] in rank
+ * order (value descending, column ascending); seeds[r] is the row's seed.
+ *
+ * ngt_ppr_count writes row_off [n_rows+1] (int64): the exclusive scan of
+ *   sum_j deg(st_col[r, j]) + 1 per row; row_off[n_rows] is the product count
+ *   ngt_ppr_step needs (read it, then size the step's workspace).  Its
+ *   workspace is 8*(n_rows+1) rounded up to 256 bytes plus a scan buffer; ask
+ *   with ngt_ppr_count_workspace_bytes.
+ * ngt_ppr_step computes next = topK(keep * (state P) + alpha * e_seed) into
+ *   out_col/out_val/out_cnt (same layout as the state; must not alias it).
+ *   keep is 1 - alpha rounded to fp32 from double (the reference scales an
+ *   fp32 tensor by a Python float).  Products of one (row, column) are added
+ *   in the order (state rank, CSR position), so the result is deterministic.
+ * Bad ids (state columns, neighbours, seeds outside [0, n_nodes), negative
+ * degrees) are counted in *status (device int32) and skipped.
+ */
+int ngt_ppr_count_workspace_bytes(int32_t n_rows, size_t* bytes);
+int ngt_ppr_count(const int64_t* rowptr, int64_t n_nodes, const int32_t* st_col,
+                  const int32_t* st_cnt, int32_t n_rows, int32_t K, int64_t* row_off,
+                  int32_t* status, void* workspace, size_t workspace_bytes, void* stream);
+int ngt_ppr_step_workspace_bytes(int64_t total, int32_t n_rows, size_t* bytes);
+int ngt_ppr_step(const int64_t* rowptr, const int64_t* col, const float* inv_deg,
+                 int64_t n_nodes, const int32_t* st_col, const float* st_val,
+                 const int32_t* st_cnt, const int64_t* seeds, int32_t n_rows, int32_t K,
+                 float alpha, float keep, const int64_t* row_off, int64_t total,
+                 int32_t* out_col, float* out_val, int32_t* out_cnt, int32_t* status,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Induced window subgraph with relabelling, on the GPU.
  *
  * ngt_subgraph_coo replaces torch_geometric.utils.subgraph(subset, edge_index,

@@ -98,6 +98,11 @@ SIGNATURES = {
     "ngt_merge_related_nodes": [_vp, _vp, _vp, _i32, _vp, _i32, _i32, _vp, _vp, _vp, _sz, _vp],
     "ngt_gather_rows": [_vp, _i64, _vp, _i64, _i64, _vp, _vp, _vp],
     "ngt_segment_sum_f32": [_vp, _i64, _vp, _i64, _vp, _vp, _vp],
+    "ngt_ppr_count_workspace_bytes": [_i32, _vp],
+    "ngt_ppr_count": [_vp, _i64, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _sz, _vp],
+    "ngt_ppr_step_workspace_bytes": [_i64, _i32, _vp],
+    "ngt_ppr_step": [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i32, C.c_float, C.c_float,
+                     _vp, _i64, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
     "ngt_subgraph_workspace_bytes": [_i64, _i64, _i32, _vp],
     "ngt_subgraph_coo": [_vp, _i64, _i64, _vp, _i32, _vp, _i64, _vp, _vp, _sz, _vp],
     "ngt_subgraph_csr": [_vp, _vp, _i64, _i64, _vp, _i32, _vp, _i64, _vp, _vp, _sz, _vp],

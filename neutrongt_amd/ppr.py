@@ -1,0 +1,148 @@
+"""Personalised PageRank preprocessing on the GPU (APPNP propagation with
+per-row top-k), the step that feeds related-node selection and the METIS
+weights.
+
+``personal_pagerank_appnp`` keeps the signature and return value of the
+reference's backend (NeutronGT/core/ppr_backends/appnp_backend.py:227-310):
+batches of seed nodes start from their identity rows and are propagated
+``num_iterations`` times,
+
+    state <- topk_K( (1 - alpha) * state @ P + alpha * e_seed ),
+    P[c, n] = 1 / max(deg(c), 1) for every edge c -> n,
+
+with K = iter_topk (the shipped scripts run topk = iter_topk = 5, alpha 0.85,
+10 iterations, batch 8192); the result keeps min(topk, iter_topk) entries per
+seed and is returned as (edge_index [2, nnz] = (seed, node), values).  Each
+step is two HIP launches groups (ngt_ppr_count, then ngt_ppr_step: expansion,
+radix sort, ordered segment sums, per-row top-k) with one read-back of the
+product count in between.
+
+Differences from the reference, by design:
+  * iter_topk must be positive (1..64): without per-step pruning the state
+    grows with the reachable set, which the reference itself warns about;
+  * ties in the top-k go to the lower node id, and each (seed, node) sum is
+    taken in a fixed order, so the result is deterministic (cuSPARSE plus an
+    atomic scatter_add and torch.topk's tie order are not).
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import torch
+
+from . import _lib
+
+MAX_K = 64
+
+
+def transition_csr(edge_index: torch.Tensor | None = None, csr_data: dict | None = None,
+                   num_nodes: int | None = None, device="cuda"):
+    """(rowptr int64, col int64, inv_deg fp32, num_nodes) of the graph, as
+    _load_csr_graph / _build_csr_from_edge_index (appnp_backend.py:17-55) build
+    it: rows sorted by (src, dst), inv_deg = 1 / max(out-degree, 1) in fp32."""
+    dev = torch.device(device)
+    if csr_data is not None:
+        rowptr = torch.as_tensor(csr_data["rowptr"], dtype=torch.long, device=dev)
+        col = torch.as_tensor(csr_data["col"], dtype=torch.long, device=dev)
+        n = int(rowptr.numel() - 1)
+        if num_nodes is not None and n != int(num_nodes):
+            raise ValueError(f"CSR num_nodes mismatch: expected {num_nodes}, got {n}")
+        deg = (rowptr[1:] - rowptr[:-1]).clamp_min(1).to(torch.float32)
+        return rowptr, col, 1.0 / deg, n
+    if edge_index is None:
+        raise ValueError("edge_index must be provided when csr_data is None")
+    ei = edge_index.to(dev).long()
+    if ei.numel() == 0:
+        n = int(num_nodes or 0)
+        z = torch.zeros(n + 1, dtype=torch.long, device=dev)
+        return z, torch.empty(0, dtype=torch.long, device=dev), torch.ones(n, device=dev), n
+    n = int(num_nodes) if num_nodes is not None else int(ei.max().item()) + 1
+    order = torch.argsort(ei[0] * max(n, 1) + ei[1], stable=True)
+    src, dst = ei[0][order], ei[1][order]
+    counts = torch.bincount(src, minlength=n)
+    rowptr = torch.zeros(n + 1, dtype=torch.long, device=dev)
+    rowptr[1:] = torch.cumsum(counts, 0)
+    return rowptr, dst.contiguous(), 1.0 / counts.clamp_min(1).to(torch.float32), n
+
+
+def appnp_batch(rowptr, col, inv_deg, n_nodes: int, seeds: torch.Tensor, alpha: float, K: int,
+                num_iterations: int):
+    """Propagates one batch of seed rows.  Returns (cols [B, K] int32,
+    vals [B, K] fp32, cnt [B] int32), rows in rank order."""
+    lib = _lib.load()
+    dev = seeds.device
+    B = int(seeds.numel())
+    if not 1 <= K <= MAX_K:
+        raise ValueError(f"per-step top-k must be in 1..{MAX_K}, got {K}")
+    st_col = torch.zeros(B, K, dtype=torch.int32, device=dev)
+    st_val = torch.zeros(B, K, dtype=torch.float32, device=dev)
+    st_col[:, 0] = seeds.to(torch.int32)
+    st_val[:, 0] = 1.0
+    st_cnt = torch.ones(B, dtype=torch.int32, device=dev)
+    nx_col, nx_val, nx_cnt = torch.empty_like(st_col), torch.empty_like(st_val), torch.empty_like(st_cnt)
+    seeds = seeds.to(torch.int64).contiguous()
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    row_off = torch.empty(B + 1, dtype=torch.int64, device=dev)
+    cb = C.c_size_t()
+    _lib.check(lib.ngt_ppr_count_workspace_bytes(B, C.byref(cb)))
+    cws = torch.empty(cb.value, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    keep = float(1.0 - alpha)  # rounded to fp32 by ctypes, as fp32_tensor * (1 - alpha) is
+    for _ in range(num_iterations):
+        _lib.check(lib.ngt_ppr_count(rowptr.data_ptr(), n_nodes, st_col.data_ptr(),
+                                     st_cnt.data_ptr(), B, K, row_off.data_ptr(),
+                                     status.data_ptr(), cws.data_ptr(), cb.value, stream))
+        total = int(row_off[B].item())
+        sb = C.c_size_t()
+        _lib.check(lib.ngt_ppr_step_workspace_bytes(total, B, C.byref(sb)))
+        ws = torch.empty(sb.value, dtype=torch.uint8, device=dev)
+        _lib.check(lib.ngt_ppr_step(rowptr.data_ptr(), col.data_ptr(), inv_deg.data_ptr(),
+                                    n_nodes, st_col.data_ptr(), st_val.data_ptr(),
+                                    st_cnt.data_ptr(), seeds.data_ptr(), B, K, float(alpha), keep,
+                                    row_off.data_ptr(), total, nx_col.data_ptr(),
+                                    nx_val.data_ptr(), nx_cnt.data_ptr(), status.data_ptr(),
+                                    ws.data_ptr(), sb.value, stream))
+        st_col, nx_col = nx_col, st_col
+        st_val, nx_val = nx_val, st_val
+        st_cnt, nx_cnt = nx_cnt, st_cnt
+    if int(status.item()):
+        raise IndexError(f"personalised PageRank: {int(status.item())} node ids out of range")
+    return st_col, st_val, st_cnt
+
+
+def personal_pagerank_appnp(edge_index, alpha, topk=100, num_iterations: int = 10,
+                            batch_size: int = 8, device="cuda", csr_data=None,
+                            num_nodes: int | None = None, iter_topk: int | None = None,
+                            source_start: int | None = None, source_end: int | None = None):
+    """The reference's APPNP backend (appnp_backend.py:227-310) on the GPU.
+    Returns (edge_index [2, nnz] int64 = (seed, node), values fp32)."""
+    dev = torch.device(device)
+    if dev.type != "cuda":
+        raise RuntimeError("the APPNP backend runs on the GPU")
+    batch_size = max(1, int(batch_size))
+    num_iterations = max(1, int(num_iterations))
+    rowptr, col, inv_deg, n = transition_csr(edge_index, csr_data, num_nodes, dev)
+    empty = (torch.empty((2, 0), dtype=torch.long, device=dev),
+             torch.empty(0, dtype=torch.float32, device=dev))
+    if n == 0:
+        return empty
+    start = 0 if source_start is None else max(0, min(int(source_start), n))
+    end = n if source_end is None else max(start, min(int(source_end), n))
+    if start >= end:
+        return empty
+    topk = min(int(topk), n)
+    iter_topk = topk if iter_topk is None else int(iter_topk)
+    if iter_topk <= 0:
+        raise NotImplementedError("iter_topk <= 0 (no per-step pruning) is not supported: give a "
+                                  f"positive per-step top-k (1..{MAX_K})")
+    K = min(iter_topk, n)
+    final_keep = min(topk, K)
+    idx_out, val_out = [], []
+    for s0 in range(start, end, batch_size):
+        seeds = torch.arange(s0, min(s0 + batch_size, end), dtype=torch.long, device=dev)
+        cols, vals, cnt = appnp_batch(rowptr, col, inv_deg, n, seeds, alpha, K, num_iterations)
+        cnt = cnt.clamp(max=final_keep).long()
+        mask = torch.arange(K, device=dev)[None, :] < cnt[:, None]
+        idx_out.append(torch.stack([seeds.repeat_interleave(cnt), cols[mask].long()]))
+        val_out.append(vals[mask])
+    return torch.cat(idx_out, dim=1), torch.cat(val_out)
