@@ -171,6 +171,64 @@ def cpu_baseline(cfg, ei_np, n_k, target_s: float = 3.0):
     }
 
 
+def ppr_bench(args, cfg, dev) -> dict:
+    """Personalised-PageRank preprocessing (appnp_backend.py:227-310) with the
+    shipped settings (run_NeutronGT.sh: --ppr_topk 5 --ppr_iter_topk 5
+    --ppr_alpha 0.85 --ppr_num_iterations 10 --ppr_batch_size 8192) over a
+    Chung-Lu graph with cfg's global node count and mean degree.  The oracle's
+    restatement is timed on a seeded sample of seeds on one host core."""
+    import numpy as np
+    import torch
+
+    from neutrongt_amd import ppr as PPR
+    from neutrongt_amd import synthetic as S
+
+    n = cfg.n_global
+    u, v = S.chung_lu_edges(n, cfg.mean_degree, cfg.gamma, S.SEED)
+    ei = torch.from_numpy(np.stack([np.concatenate([u, v]), np.concatenate([v, u])]))
+    alpha, topk, iters, batch = 0.85, 5, 10, 8192
+    rowptr, col, inv_deg, _ = PPR.transition_csr(ei, num_nodes=n, device=dev)
+    csr = {"rowptr": rowptr, "col": col}
+    _log(f"[bench] ppr: graph n={n}, {int(col.numel())} directed edges; topk {topk}, "
+         f"{iters} iterations, batches of {batch}")
+    # one batch as warm-up, then the whole graph timed
+    PPR.personal_pagerank_appnp(None, alpha, topk=topk, num_iterations=iters, batch_size=batch,
+                                device=dev, csr_data=csr, iter_topk=topk, source_end=batch)
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    idx, val = PPR.personal_pagerank_appnp(None, alpha, topk=topk, num_iterations=iters,
+                                           batch_size=batch, device=dev, csr_data=csr,
+                                           iter_topk=topk)
+    torch.cuda.synchronize()
+    t_gpu = time.perf_counter() - t
+    _log(f"[bench] ppr: {t_gpu * 1e3:.1f} ms for {n} seeds ({int(idx.shape[1])} entries)")
+    cpu = None
+    if not args.no_cpu:
+        from oracle import ppr as OP
+
+        rp, cl, iv = rowptr.cpu().numpy(), col.cpu().numpy(), inv_deg.cpu().numpy()
+        sample = np.random.default_rng(S.SEED).choice(n, 200, replace=False)
+        t = time.perf_counter()
+        for sd in sample.tolist():
+            OP.appnp_row(rp, cl, iv, sd, alpha, topk, iters)
+        t_s = time.perf_counter() - t
+        cpu = {"value": t_s / sample.size * n * 1e3, "unit": "ms", "cores": 1, "kind": "port",
+               "sample": (f"the oracle's restatement on 200 seeded random seeds ({t_s:.1f} s), "
+                          f"scaled to all {n} seeds")}
+        _log(f"[bench] ppr cpu baseline {cpu['value'] / 1e3:.1f} s (extrapolated)")
+    return {
+        "metric": "personalised PageRank preprocessing time (APPNP, top-5, 10 iterations)",
+        "value": t_gpu * 1e3, "unit": "ms", "n_gpus": 1, "steps": 1, "warmup": 1,
+        "ms_per_step": t_gpu * 1e3, "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": (f"{cfg.name} global graph: Chung-Lu n={n}, "
+                                f"{int(col.numel())} directed edges, alpha {alpha}, top-{topk}, "
+                                f"{iters} iterations, batches of {batch} seeds"),
+                   "entries": int(idx.shape[1])},
+        "cpu_baseline": cpu,
+    }
+
+
 def prep_bench(args, cfg, dev) -> dict:
     """Assembly of one window on the GPU, from the global graph to the
     attention inputs: related-node selection (metisPartition.py:397-425), the
@@ -430,6 +488,9 @@ def main(argv=None) -> int:
                     help="run one 512 MiB device copy first (calibrates HBM byte counters)")
     ap.add_argument("--graph", action="store_true",
                     help="capture one step (all layers, fwd+bwd) in a HIP graph and time replays")
+    ap.add_argument("--ppr", action="store_true",
+                    help="time the personalised-PageRank preprocessing instead (APPNP, top-5, "
+                         "10 iterations, batches of 8192 seeds) on the config's global graph")
     ap.add_argument("--prep", action="store_true",
                     help="time the window assembly instead (related nodes, induced subgraph, "
                          "window CSR, feature gather) on the config's global graph")
@@ -460,6 +521,13 @@ def main(argv=None) -> int:
     layers = args.layers or cfg.layers
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.ppr:
+        if cfg.dense or not cfg.n_global:
+            print("--ppr needs a sparse config with a global graph (gt_arxiv, gt_highdeg, "
+                  "gph_large)", file=sys.stderr)
+            return 2
+        print(json.dumps(ppr_bench(args, cfg, dev)), flush=True)
+        return 0
     if args.prep:
         if cfg.dense or not cfg.n_global:
             print("--prep needs a sparse config with a global graph (gph_large, gt_arxiv, "

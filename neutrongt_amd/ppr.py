@@ -13,9 +13,9 @@ batches of seed nodes start from their identity rows and are propagated
 with K = iter_topk (the shipped scripts run topk = iter_topk = 5, alpha 0.85,
 10 iterations, batch 8192); the result keeps min(topk, iter_topk) entries per
 seed and is returned as (edge_index [2, nnz] = (seed, node), values).  Each
-step is two HIP launches groups (ngt_ppr_count, then ngt_ppr_step: expansion,
-radix sort, ordered segment sums, per-row top-k) with one read-back of the
-product count in between.
+step is ngt_ppr_count, one read-back of the product counts, then ngt_ppr_step
+(expansion, radix sort, ordered segment sums, per-row top-k) on the whole batch
+or on row chunks that bound the step's memory.
 
 Differences from the reference, by design:
   * iter_topk must be positive (1..64): without per-step pruning the state
@@ -66,9 +66,11 @@ def transition_csr(edge_index: torch.Tensor | None = None, csr_data: dict | None
 
 
 def appnp_batch(rowptr, col, inv_deg, n_nodes: int, seeds: torch.Tensor, alpha: float, K: int,
-                num_iterations: int):
+                num_iterations: int, max_products: int = 1 << 27):
     """Propagates one batch of seed rows.  Returns (cols [B, K] int32,
-    vals [B, K] fp32, cnt [B] int32), rows in rank order."""
+    vals [B, K] fp32, cnt [B] int32), rows in rank order.  A step whose
+    product count exceeds ``max_products`` runs on consecutive row chunks
+    (rows are independent), which bounds the step's workspace."""
     lib = _lib.load()
     dev = seeds.device
     B = int(seeds.numel())
@@ -88,20 +90,39 @@ def appnp_batch(rowptr, col, inv_deg, n_nodes: int, seeds: torch.Tensor, alpha: 
     cws = torch.empty(cb.value, dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream(dev).cuda_stream
     keep = float(1.0 - alpha)  # rounded to fp32 by ctypes, as fp32_tensor * (1 - alpha) is
-    for _ in range(num_iterations):
-        _lib.check(lib.ngt_ppr_count(rowptr.data_ptr(), n_nodes, st_col.data_ptr(),
-                                     st_cnt.data_ptr(), B, K, row_off.data_ptr(),
+
+    def count(r0, r1, off):
+        _lib.check(lib.ngt_ppr_count(rowptr.data_ptr(), n_nodes, st_col[r0:r1].data_ptr(),
+                                     st_cnt[r0:r1].data_ptr(), r1 - r0, K, off.data_ptr(),
                                      status.data_ptr(), cws.data_ptr(), cb.value, stream))
-        total = int(row_off[B].item())
+
+    def step(r0, r1, off, total):
         sb = C.c_size_t()
-        _lib.check(lib.ngt_ppr_step_workspace_bytes(total, B, C.byref(sb)))
+        _lib.check(lib.ngt_ppr_step_workspace_bytes(total, r1 - r0, C.byref(sb)))
         ws = torch.empty(sb.value, dtype=torch.uint8, device=dev)
         _lib.check(lib.ngt_ppr_step(rowptr.data_ptr(), col.data_ptr(), inv_deg.data_ptr(),
-                                    n_nodes, st_col.data_ptr(), st_val.data_ptr(),
-                                    st_cnt.data_ptr(), seeds.data_ptr(), B, K, float(alpha), keep,
-                                    row_off.data_ptr(), total, nx_col.data_ptr(),
-                                    nx_val.data_ptr(), nx_cnt.data_ptr(), status.data_ptr(),
-                                    ws.data_ptr(), sb.value, stream))
+                                    n_nodes, st_col[r0:r1].data_ptr(), st_val[r0:r1].data_ptr(),
+                                    st_cnt[r0:r1].data_ptr(), seeds[r0:r1].data_ptr(), r1 - r0,
+                                    K, float(alpha), keep, off.data_ptr(), total,
+                                    nx_col[r0:r1].data_ptr(), nx_val[r0:r1].data_ptr(),
+                                    nx_cnt[r0:r1].data_ptr(), status.data_ptr(), ws.data_ptr(),
+                                    sb.value, stream))
+
+    for _ in range(num_iterations):
+        count(0, B, row_off)
+        offs = row_off.cpu()
+        total = int(offs[B])
+        if total <= max_products:
+            step(0, B, row_off, total)
+        else:
+            r0 = 0
+            while r0 < B:
+                r1 = int(torch.searchsorted(offs, offs[r0] + max_products, right=True)) - 1
+                r1 = min(max(r1, r0 + 1), B)
+                part = torch.empty(r1 - r0 + 1, dtype=torch.int64, device=dev)
+                count(r0, r1, part)
+                step(r0, r1, part, int(offs[r1] - offs[r0]))
+                r0 = r1
         st_col, nx_col = nx_col, st_col
         st_val, nx_val = nx_val, st_val
         st_cnt, nx_cnt = nx_cnt, st_cnt

@@ -65,3 +65,24 @@ def test_appnp_rejects_unbounded_state_and_bad_ids():
     bad = {"rowptr": torch.tensor([0, 1, 2]), "col": torch.tensor([1, 7])}
     with pytest.raises(IndexError):
         personal_pagerank_appnp(None, 0.85, topk=2, device=DEV, csr_data=bad, iter_topk=2)
+
+
+def test_appnp_row_chunks_match_one_pass():
+    """A step split into row chunks (product budget far below the batch's)
+    gives the same rows as the oracle."""
+    from neutrongt_amd import ppr as PPR
+
+    n = 300
+    ei = _graph(n, 1500, 7, hub=True)
+    rowptr, col, inv, _ = OP.transition_csr(ei, n)
+    seeds = torch.arange(0, 120, device=DEV)
+    cols, vals, cnt = PPR.appnp_batch(torch.from_numpy(rowptr).to(DEV),
+                                      torch.from_numpy(col).to(DEV),
+                                      torch.from_numpy(inv).to(DEV), n, seeds, 0.85, 5, 4,
+                                      max_products=700)
+    cols, vals, cnt = cols.cpu().numpy(), vals.cpu().numpy(), cnt.cpu().numpy()
+    for r in range(120):
+        want = OP.appnp_row(rowptr, col, inv, r, 0.85, 5, 4)
+        assert cnt[r] == len(want)
+        assert cols[r, :cnt[r]].tolist() == [c for c, _ in want]
+        np.testing.assert_array_equal(vals[r, :cnt[r]], np.array([v for _, v in want], np.float32))
