@@ -57,6 +57,17 @@ __device__ __forceinline__ s16x4 load4(const bf16_t* p) {
   return r;
 }
 
+// Operands loaded from global memory before a stage loop go through an empty
+// asm that reads and rewrites their registers: the wait for those loads is
+// then placed before the loop.  Without it the wait lands on the first MFMA
+// inside the loop as vmcnt(0), which also waits for the next stage's prefetch
+// and serialises it with the compute.
+__device__ __forceinline__ s16x4 settle(s16x4 x) {
+  uint2 w = __builtin_bit_cast(uint2, x);
+  asm volatile("" : "+v"(w.x), "+v"(w.y));
+  return __builtin_bit_cast(s16x4, w);
+}
+
 __device__ __forceinline__ s16x4 zero4() {
   s16x4 r;
   r[0] = r[1] = r[2] = r[3] = 0;
@@ -179,7 +190,7 @@ __global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
   s16x4 qb[NC];
 #pragma unroll
   for (int j = 0; j < NC; ++j)
-    qb[j] = q_ok ? load4(q + (qi * H + h) * DH + 8 * j + 4 * half) : zero4();
+    qb[j] = settle(q_ok ? load4(q + (qi * H + h) * DH + 8 * j + 4 * half) : zero4());
 
   const float s2 = scale * kLog2e;  // scores in log2 units
   float m = -INFINITY, l = 0.f;
@@ -278,7 +289,7 @@ __global__ __launch_bounds__(kBlock) void k_mf_scores(const bf16_t* __restrict__
   s16x4 kbv[NC];  // K^T as B: lane holds K[kj][8j + 4*half .. +4]
 #pragma unroll
   for (int j = 0; j < NC; ++j)
-    kbv[j] = k_ok ? load4(k + (kj * H + h) * DH + 8 * j + 4 * half) : zero4();
+    kbv[j] = settle(k_ok ? load4(k + (kj * H + h) * DH + 8 * j + 4 * half) : zero4());
   float s = 0.f;
   Stage<DH> pq;
   pq.load(q, 0, n_q, H, h);
@@ -327,8 +338,8 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_kv(
   s16x4 kbv[NC], vbv[NC];  // K^T, V^T as B operands
 #pragma unroll
   for (int j = 0; j < NC; ++j) {
-    kbv[j] = k_ok ? load4(k + (kj * H + h) * DH + 8 * j + 4 * half) : zero4();
-    vbv[j] = k_ok ? load4(v + (kj * H + h) * DH + 8 * j + 4 * half) : zero4();
+    kbv[j] = settle(k_ok ? load4(k + (kj * H + h) * DH + 8 * j + 4 * half) : zero4());
+    vbv[j] = settle(k_ok ? load4(v + (kj * H + h) * DH + 8 * j + 4 * half) : zero4());
   }
   const float s2 = scale * kLog2e;
   f32x16 dk = zero16(), dv = zero16();  // D[key][c]: key = 8*(i/4)+4*half+i%4, c = l32
@@ -339,7 +350,9 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_kv(
     pg.load(g, qb, n_q, H, h);
     if (threadIdx.x < kSB) {
       const bool ok = qb + int(threadIdx.x) < n_q;
-      pl = ok ? lse[int64_t(h) * n_q + qb + threadIdx.x] * kLog2e : INFINITY;
+      // raw values here: scaling now would wait on this load (and on the
+      // stage's prefetch before it) at once
+      pl = ok ? lse[int64_t(h) * n_q + qb + threadIdx.x] : INFINITY;
       pd = ok ? dsum[int64_t(h) * n_q + qb + threadIdx.x] : 0.f;
     }
   };
@@ -353,7 +366,7 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_kv(
     pq.store_trans(qt);
     pg.store_trans(gt);
     if (threadIdx.x < kSB) {
-      ls[threadIdx.x] = pl;
+      ls[threadIdx.x] = pl * kLog2e;
       dd[threadIdx.x] = pd;
     }
     __syncthreads();
@@ -430,8 +443,8 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_q(
   s16x4 qbv[NC], gbv[NC];  // Q^T, G^T as B operands
 #pragma unroll
   for (int j = 0; j < NC; ++j) {
-    qbv[j] = q_ok ? load4(q + (qi * H + h) * DH + 8 * j + 4 * half) : zero4();
-    gbv[j] = q_ok ? load4(g + (qi * H + h) * DH + 8 * j + 4 * half) : zero4();
+    qbv[j] = settle(q_ok ? load4(q + (qi * H + h) * DH + 8 * j + 4 * half) : zero4());
+    gbv[j] = settle(q_ok ? load4(g + (qi * H + h) * DH + 8 * j + 4 * half) : zero4());
   }
   const float L2 = q_ok ? lse[int64_t(h) * n_q + qi] * kLog2e : INFINITY;
   const float Dq = q_ok ? dsum[int64_t(h) * n_q + qi] : 0.f;
