@@ -31,12 +31,16 @@ def chunk_for_heads(n_heads: int) -> int:
 
 
 def small_for_heads(n_heads: int) -> int:
-    """Rows with at most this many edges are packed one row per edge slot:
-    the kernels' slots per wave, 64 / next_pow2(H)."""
+    """Rows with at most this many edges are packed one row per edge slot
+    (no cross-slot reduction, no per-row work item): 64 / next_pow2(H), the
+    slots per wave of an all-heads pass, and 32 from H = 32 on.  On the
+    32,768-query window (H = 32, d = 24) raising it from 2 to 32 took the
+    layer from 1.45 to 1.40 ms; on the H = 8 windows 8 stays best (32 and 64
+    slowed the key-major pass)."""
     lanes = 1
     while lanes < n_heads:
         lanes <<= 1
-    return max(1, 64 // lanes)
+    return max(1, 64 // lanes, 32 if n_heads >= 32 else 1)
 
 
 class WindowAdjacency:

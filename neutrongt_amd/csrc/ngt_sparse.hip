@@ -15,10 +15,10 @@
 // edge and the d-element head slice of every gathered row, so the L lanes of a
 // slot read one contiguous segment of a K/V row per edge.
 //
-// Head groups: a launch can walk the work list once per group of `hg` heads
-// (all items of group 0, then group 1, ...), so that one pass gathers only
-// hg*d-element row slices.  The default is one group of all heads (see
-// heads_per_pass for the measurement behind that choice).
+// Head groups: a launch can walk the work list once per group of `hg` heads,
+// so that one pass gathers only hg*d-element row slices (heads_per_pass has
+// the per-kernel widths and the measurement behind them; virtual_wave the
+// order in which groups are dealt to the XCDs).
 #include "ngt_common.h"
 
 #include <stdlib.h>
@@ -71,10 +71,26 @@ struct Lane {
   bool active;  // lane maps to a real head
 };
 
-__device__ __forceinline__ bool wave_work(int n_items, int n_groups, int hg, int L, int H,
-                                          int& item, Lane& ln) {
+// Wave id of this wave in the launch's work order [items of group 0 | items of
+// group 1 | ... | packed waves of group 0 | ...], or -1 when it has none.
+// xcd != 0 (n_groups divides 8): block b serves head group b % n_groups.  The
+// dispatcher deals blocks to the eight XCDs round robin, so each XCD then
+// gathers the row slices of one head group only and its L2 holds 8/n_groups
+// times more rows of that slice.
+__device__ __forceinline__ int64_t virtual_wave(int32_t n_items, int32_t n_pwaves,
+                                                int32_t n_groups, int32_t xcd) {
+  const int wv = threadIdx.x >> 6;
+  if (!xcd) return int64_t(blockIdx.x) * kWavesPerBlock + wv;
+  const int g = static_cast<int>(blockIdx.x % unsigned(n_groups));
+  const int64_t w = int64_t(blockIdx.x / unsigned(n_groups)) * kWavesPerBlock + wv;
+  if (w < n_items) return int64_t(g) * n_items + w;
+  if (w - n_items < n_pwaves) return int64_t(n_items) * n_groups + int64_t(g) * n_pwaves + (w - n_items);
+  return -1;
+}
+
+__device__ __forceinline__ bool wave_work(int64_t gw, int n_items, int n_groups, int hg, int L,
+                                          int H, int& item, Lane& ln) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t gw = int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
   if (n_items <= 0) return false;
   const int64_t group = gw / n_items;
   if (group >= n_groups) return false;
@@ -93,6 +109,7 @@ __device__ __forceinline__ bool packed_work(int64_t pw, int n_pwaves, int n_grou
                                             int L, int H, const int32_t* __restrict__ packed,
                                             int n_packed, int64_t& row, int& h) {
   const int lane = threadIdx.x & (kWave - 1);
+  if (n_pwaves <= 0) return false;
   const int64_t group = pw / n_pwaves;
   if (group >= n_groups) return false;
   const int64_t idx = pw - group * n_pwaves;
@@ -118,16 +135,35 @@ __device__ __forceinline__ float fwd_packed(const T* __restrict__ q, const T* __
   load_words<T, DH>(q + (row * H + h) * DH, qw);
 #pragma unroll
   for (int c = 0; c < DH; ++c) acc[c] = 0.f;
+  // U edges per round: their K/V loads are in flight together, and the
+  // column indices of the next round are requested before this round's math.
+  constexpr int U = unroll_for(2 * RowWords<T, DH>::NV, NGT_FWD_WORDS);
   const int beg = rowptr[row], end = rowptr[row + 1];
-  for (int e = beg; e < end; ++e) {
-    const int64_t j = col[e];
-    RowWords<T, DH> kw, vw;
-    load_words<T, DH>(k + (j * H + h) * DH, kw);
-    load_words<T, DH>(v + (j * H + h) * DH, vw);
-    const float p = __expf(clampf(edge_dot<T, DH>(qw, kw) * inv_scale, lo, hi));
-    z += p;
+  int jn[U];
 #pragma unroll
-    for (int c = 0; c < DH; ++c) acc[c] = fmaf(p, word_elem<T, DH>(vw, c), acc[c]);
+  for (int u = 0; u < U; ++u) jn[u] = beg + u < end ? col[beg + u] : -1;
+  for (int e0 = beg; e0 < end; e0 += U) {
+    RowWords<T, DH> kw[U], vw[U];
+    int jc[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      jc[u] = jn[u];
+      if (jc[u] >= 0) {
+        load_words<T, DH>(k + (int64_t(jc[u]) * H + h) * DH, kw[u]);
+        load_words<T, DH>(v + (int64_t(jc[u]) * H + h) * DH, vw[u]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) jn[u] = e0 + U + u < end ? col[e0 + U + u] : -1;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (jc[u] >= 0) {
+        const float p = __expf(clampf(edge_dot<T, DH>(qw, kw[u]) * inv_scale, lo, hi));
+        z += p;
+#pragma unroll
+        for (int c = 0; c < DH; ++c) acc[c] = fmaf(p, word_elem<T, DH>(vw[u], c), acc[c]);
+      }
+    }
   }
   const float den = z + eps;
   float o[DH];
@@ -153,8 +189,9 @@ __global__ __launch_bounds__(kBlock) void k_fwd(
     float eps, T* __restrict__ out, float* __restrict__ rinv, float* __restrict__ zbuf,
     float* __restrict__ part_acc, float* __restrict__ part_z, const int32_t* __restrict__ rowptr,
     const int32_t* __restrict__ packed, int32_t n_packed, int32_t n_pwaves,
-    float* __restrict__ ns, int32_t ns_len) {
-  const int64_t gw = int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+    float* __restrict__ ns, int32_t ns_len, int32_t xcd) {
+  const int64_t gw = virtual_wave(n_items, n_pwaves, n_groups, xcd);
+  if (gw < 0) return;
   if (gw >= int64_t(n_items) * n_groups) {
     int64_t prow = 0;
     int ph = 0;
@@ -172,7 +209,7 @@ __global__ __launch_bounds__(kBlock) void k_fwd(
   }
   int item;
   Lane ln;
-  if (!wave_work(n_items, n_groups, hg, L, H, item, ln)) return;
+  if (!wave_work(gw, n_items, n_groups, hg, L, H, item, ln)) return;
   const int4 it = items[item];
   const int64_t row = it.x;
   const int h = ln.h;
@@ -344,24 +381,43 @@ __device__ __forceinline__ void bwd_kv_packed(
     dk[c] = 0.f;
     dv[c] = 0.f;
   }
+  constexpr int U = unroll_for(2 * RowWords<T, DH>::NV, NGT_BWD_KV_WORDS);
   const int beg = t_rowptr[row], end = t_rowptr[row + 1];
-  for (int e = beg; e < end; ++e) {
-    const int64_t i = t_col[e];
-    RowWords<T, DH> qw, gw;
-    load_words<T, DH>(q + (i * H + h) * DH, qw);
-    load_words<T, DH>(g + (i * H + h) * DH, gw);
-    const float2 r = rd[i * H + h];
-    const float a = edge_dot<T, DH>(qw, krw) * inv_scale;
-    const float p = __expf(clampf(a, lo, hi));
-    const float dp = r.x * edge_dot<T, DH>(gw, vrw) - r.y;
-    const float da = (a >= lo && a <= hi) ? dp * p : 0.f;
-    const float pr = p * r.x;
+  int in_[U];
 #pragma unroll
-    for (int c = 0; c < DH; ++c) {
-      dk[c] = fmaf(da, word_elem<T, DH>(qw, c), dk[c]);
-      dv[c] = fmaf(pr, word_elem<T, DH>(gw, c), dv[c]);
+  for (int u = 0; u < U; ++u) in_[u] = beg + u < end ? t_col[beg + u] : -1;
+  for (int e0 = beg; e0 < end; e0 += U) {
+    RowWords<T, DH> qw[U], gw[U];
+    float2 r[U];
+    int ic[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      ic[u] = in_[u];
+      if (ic[u] >= 0) {
+        const int64_t i = ic[u];
+        load_words<T, DH>(q + (i * H + h) * DH, qw[u]);
+        load_words<T, DH>(g + (i * H + h) * DH, gw[u]);
+        r[u] = rd[i * H + h];
+      }
     }
-    ds[int64_t(e) * H + h] = da;
+#pragma unroll
+    for (int u = 0; u < U; ++u) in_[u] = e0 + U + u < end ? t_col[e0 + U + u] : -1;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (ic[u] >= 0) {
+        const float a = edge_dot<T, DH>(qw[u], krw) * inv_scale;
+        const float p = __expf(clampf(a, lo, hi));
+        const float dp = r[u].x * edge_dot<T, DH>(gw[u], vrw) - r[u].y;
+        const float da = (a >= lo && a <= hi) ? dp * p : 0.f;
+        const float pr = p * r[u].x;
+#pragma unroll
+        for (int c = 0; c < DH; ++c) {
+          dk[c] = fmaf(da, word_elem<T, DH>(qw[u], c), dk[c]);
+          dv[c] = fmaf(pr, word_elem<T, DH>(gw[u], c), dv[c]);
+        }
+        ds[int64_t(e0 + u) * H + h] = da;
+      }
+    }
   }
 #pragma unroll
   for (int c = 0; c < DH; ++c) dk[c] *= inv_scale;
@@ -379,8 +435,9 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
     int32_t L, float inv_scale, float lo, float hi, T* __restrict__ grad_k,
     T* __restrict__ grad_v, float* __restrict__ ds, float* __restrict__ part_kv,
     const int32_t* __restrict__ t_rowptr, const int32_t* __restrict__ packed, int32_t n_packed,
-    int32_t n_pwaves) {
-  const int64_t gw0 = int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+    int32_t n_pwaves, int32_t xcd) {
+  const int64_t gw0 = virtual_wave(n_items, n_pwaves, n_groups, xcd);
+  if (gw0 < 0) return;
   if (gw0 >= int64_t(n_items) * n_groups) {
     int64_t prow;
     int ph;
@@ -392,7 +449,7 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
   }
   int item;
   Lane ln;
-  if (!wave_work(n_items, n_groups, hg, L, H, item, ln)) return;
+  if (!wave_work(gw0, n_items, n_groups, hg, L, H, item, ln)) return;
   const int4 it = items[item];
   const int64_t row = it.x;
   const int h = ln.h;
@@ -507,15 +564,37 @@ __device__ __forceinline__ void bwd_q_packed(const T* __restrict__ k,
   float dq[DH];
 #pragma unroll
   for (int c = 0; c < DH; ++c) dq[c] = 0.f;
+  constexpr int U = unroll_for(RowWords<T, DH>::NV, NGT_BWD_Q_WORDS);
   const int beg = rowptr[row], end = rowptr[row + 1];
-  for (int e = beg; e < end; ++e) {
-    const int64_t j = col[e];
-    const int64_t t = q2t[e];
-    RowWords<T, DH> kw;
-    load_words<T, DH>(k + (j * H + h) * DH, kw);
-    const float d = ds[t * H + h];
+  int jn[U], tn[U];
 #pragma unroll
-    for (int c = 0; c < DH; ++c) dq[c] = fmaf(d, word_elem<T, DH>(kw, c), dq[c]);
+  for (int u = 0; u < U; ++u) {
+    jn[u] = beg + u < end ? col[beg + u] : -1;
+    tn[u] = beg + u < end ? q2t[beg + u] : 0;
+  }
+  for (int e0 = beg; e0 < end; e0 += U) {
+    RowWords<T, DH> kw[U];
+    float d[U];
+    int jc[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      jc[u] = jn[u];
+      if (jc[u] >= 0) {
+        load_words<T, DH>(k + (int64_t(jc[u]) * H + h) * DH, kw[u]);
+        d[u] = ds[int64_t(tn[u]) * H + h];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      jn[u] = e0 + U + u < end ? col[e0 + U + u] : -1;
+      tn[u] = e0 + U + u < end ? q2t[e0 + U + u] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (jc[u] >= 0) {
+#pragma unroll
+        for (int c = 0; c < DH; ++c) dq[c] = fmaf(d[u], word_elem<T, DH>(kw[u], c), dq[c]);
+      }
   }
 #pragma unroll
   for (int c = 0; c < DH; ++c) dq[c] *= inv_scale;
@@ -531,7 +610,7 @@ __global__ __launch_bounds__(kBlock) void k_bwd_q(
     float* __restrict__ part_q, const int32_t* __restrict__ rowptr,
     const int32_t* __restrict__ packed, int32_t n_packed, int32_t n_pwaves, int32_t q_blocks,
     const int4* __restrict__ splits_k, int32_t kv_tiles, const float* __restrict__ part_kv,
-    T* __restrict__ grad_k, T* __restrict__ grad_v) {
+    T* __restrict__ grad_k, T* __restrict__ grad_v, int32_t xcd) {
   // Blocks past the dQ work finish the split key rows of bwd_kv (their dK/dV
   // partials): that work is independent of dQ, so it rides in this launch.
   if (int32_t(blockIdx.x) >= q_blocks) {
@@ -539,7 +618,8 @@ __global__ __launch_bounds__(kBlock) void k_bwd_q(
     bwd_kv_finalize_tile<T, DH>(splits_k, H, part_kv, grad_k, grad_v, f / kv_tiles, f % kv_tiles);
     return;
   }
-  const int64_t gw0 = int64_t(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+  const int64_t gw0 = virtual_wave(n_items, n_pwaves, n_groups, xcd);
+  if (gw0 < 0) return;
   if (gw0 >= int64_t(n_items) * n_groups) {
     int64_t prow;
     int ph;
@@ -550,7 +630,7 @@ __global__ __launch_bounds__(kBlock) void k_bwd_q(
   }
   int item;
   Lane ln;
-  if (!wave_work(n_items, n_groups, hg, L, H, item, ln)) return;
+  if (!wave_work(gw0, n_items, n_groups, hg, L, H, item, ln)) return;
   const int4 it = items[item];
   const int64_t row = it.x;
   const int h = ln.h;
@@ -632,16 +712,37 @@ inline int lanes_for(int n) {
 
 inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-// Heads per pass.  All heads in one pass (hg = H) measured fastest on the
-// 32,768-query / 105K-key window: splitting H=32 into 8-head groups costs more
-// in per-edge index/loop overhead than the smaller gathered working set saves
-// (bwd_kv 738 -> 1284 us).  NGT_HEAD_GROUP overrides for experiments.
-int heads_per_pass(int H) {
-  if (const char* env = getenv("NGT_HEAD_GROUP")) {
+// Heads per pass, per kernel (0 forward, 1 key-major backward, 2 query-major
+// backward).  Measured on the 32,768-query / 105K-key window (H = 32, d = 24,
+// bf16, us per launch at 32 / 16 / 8 / 4 heads per pass):
+//   forward        524 / 470 / 443 / 646
+//   key-major bwd  673 / 661 / 787 / 1250
+//   query-major    298 / 312 / 385 / 650
+// A narrower pass gathers smaller row slices, so more rows of them stay in
+// L2; it also runs more waves, each with a fixed cost (work item, q row,
+// cross-slot reductions that grow with the slot count 64 / heads).  The
+// backward kernels carry more per-wave reduction (dK and dV, or dQ, plus
+// per-edge ds) and more per-edge scalars, so they keep wider passes.
+// NGT_HEAD_GROUP (all kernels) or NGT_HEAD_GROUP_FWD / _KV / _Q override.
+int heads_per_pass(int H, int kind) {
+  static const char* const kEnv[3] = {"NGT_HEAD_GROUP_FWD", "NGT_HEAD_GROUP_KV",
+                                      "NGT_HEAD_GROUP_Q"};
+  const char* env = getenv(kEnv[kind]);
+  if (!env) env = getenv("NGT_HEAD_GROUP");
+  if (env) {
     const int v = atoi(env);
     if (v >= 1) return v < H ? v : H;
   }
-  return H;
+  const int cap = kind == 0 ? 8 : kind == 1 ? 16 : H;
+  return H > cap ? cap : H;
+}
+
+// Head groups are dealt to XCDs (virtual_wave) when their count divides 8;
+// NGT_XCD=0 turns that off for experiments.
+int xcd_mapping(int groups) {
+  if (groups <= 1 || 8 % groups != 0) return 0;
+  if (const char* env = getenv("NGT_XCD")) return atoi(env) != 0;
+  return 1;
 }
 
 struct FwdLayout {
@@ -708,29 +809,38 @@ inline unsigned blocks_for(int64_t waves) {
   return static_cast<unsigned>((waves + kWavesPerBlock - 1) / kWavesPerBlock);
 }
 
+// Blocks of an edge-kernel launch over n_items items and pw packed waves per
+// head group (see virtual_wave for the xcd order).
+inline unsigned edge_blocks(int n_items, int pw, int groups, int xcd) {
+  const int64_t per_group = int64_t(n_items) + pw;
+  if (per_group <= 0) return 0;
+  return xcd ? unsigned(groups) * blocks_for(per_group) : blocks_for(per_group * groups);
+}
+
 template <typename T, int DH>
 int launch_fwd(const ngt_window_csr* c, const void* q, const void* k, const void* v, int H,
                float inv_scale, float lo, float hi, float eps, void* out, float* rinv, float* ns,
                int ns_len, char* ws, hipStream_t st) {
-  const int hg = heads_per_pass(H);
+  const int hg = heads_per_pass(H, 0);
   const int groups = (H + hg - 1) / hg;
   const int L = lanes_for(hg);
   const FwdLayout lay = fwd_layout(c, H, DH);
   float* part_acc = reinterpret_cast<float*>(ws + lay.part_acc);
   float* part_z = reinterpret_cast<float*>(ws + lay.part_z);
   float* zbuf = reinterpret_cast<float*>(ws + lay.zbuf);
+  const int xcd = xcd_mapping(groups);
   const int pw_q = packed_waves(c->n_packed_q, L);
-  const int64_t waves_q = (int64_t(c->n_items_q) + pw_q) * groups;
+  const unsigned blocks_q = edge_blocks(c->n_items_q, pw_q, groups, xcd);
   // one head group: the forward kernels write the node scores themselves
   float* ns_direct = groups == 1 && ns && ns_len > 0 ? ns : nullptr;
-  if (waves_q > 0) {
+  if (blocks_q > 0) {
     KernelTimer timer_("sparse_fwd", st);
-    hipLaunchKernelGGL((k_fwd<T, DH>), dim3(blocks_for(waves_q)), dim3(kBlock), 0, st,
+    hipLaunchKernelGGL((k_fwd<T, DH>), dim3(blocks_q), dim3(kBlock), 0, st,
                        static_cast<const T*>(q), static_cast<const T*>(k),
                        static_cast<const T*>(v), c->col, reinterpret_cast<const int4*>(c->items_q),
                        c->n_items_q, groups, hg, H, L, inv_scale, lo, hi, eps,
                        static_cast<T*>(out), rinv, zbuf, part_acc, part_z, c->rowptr, c->packed_q,
-                       c->n_packed_q, pw_q, ns_direct, ns_len);
+                       c->n_packed_q, pw_q, ns_direct, ns_len, xcd);
     NGT_HIP_CHECK(hipGetLastError());
   }
   if (c->n_splits_q > 0) {
@@ -754,9 +864,6 @@ template <typename T, int DH>
 int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void* v,
                const void* out, const void* g, const float* rinv, int H, float inv_scale,
                float lo, float hi, void* gq, void* gk, void* gv, char* ws, hipStream_t st) {
-  const int hg = heads_per_pass(H);
-  const int groups = (H + hg - 1) / hg;
-  const int L = lanes_for(hg);
   const BwdLayout lay = bwd_layout(c, H, DH);
   float2* rd = reinterpret_cast<float2*>(ws + lay.rd);
   float* ds = reinterpret_cast<float*>(ws + lay.ds);
@@ -771,22 +878,29 @@ int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void
                        static_cast<const T*>(out), static_cast<const T*>(g), rinv, nrh, rd);
     NGT_HIP_CHECK(hipGetLastError());
   }
+  int hg = heads_per_pass(H, 1);
+  int groups = (H + hg - 1) / hg;
+  int L = lanes_for(hg);
+  int xcd = xcd_mapping(groups);
   const int pw_k = packed_waves(c->n_packed_k, L);
-  const int64_t waves_k = (int64_t(c->n_items_k) + pw_k) * groups;
-  if (waves_k > 0) {
+  const unsigned blocks_k = edge_blocks(c->n_items_k, pw_k, groups, xcd);
+  if (blocks_k > 0) {
     KernelTimer timer_("sparse_bwd_kv", st);
-    hipLaunchKernelGGL((k_bwd_kv<T, DH>), dim3(blocks_for(waves_k)), dim3(kBlock), 0, st,
+    hipLaunchKernelGGL((k_bwd_kv<T, DH>), dim3(blocks_k), dim3(kBlock), 0, st,
                        static_cast<const T*>(q), static_cast<const T*>(k),
                        static_cast<const T*>(v), static_cast<const T*>(g), rd, c->t_col,
                        reinterpret_cast<const int4*>(c->items_k), c->n_items_k, groups, hg, H, L,
                        inv_scale, lo, hi, static_cast<T*>(gk), static_cast<T*>(gv), ds, part_kv,
-                       c->t_rowptr, c->packed_k, c->n_packed_k, pw_k);
+                       c->t_rowptr, c->packed_k, c->n_packed_k, pw_k, xcd);
     NGT_HIP_CHECK(hipGetLastError());
   }
+  hg = heads_per_pass(H, 2);
+  groups = (H + hg - 1) / hg;
+  L = lanes_for(hg);
+  xcd = xcd_mapping(groups);
   const int pw_q = packed_waves(c->n_packed_q, L);
-  const int64_t waves_q = (int64_t(c->n_items_q) + pw_q) * groups;
   const int kv_tiles = (2 * H * DH + kColTile - 1) / kColTile;
-  const int64_t q_blocks = blocks_for(waves_q);
+  const int64_t q_blocks = edge_blocks(c->n_items_q, pw_q, groups, xcd);
   const int64_t fin_blocks = int64_t(c->n_splits_k) * kv_tiles;
   if (q_blocks + fin_blocks > 0) {
     KernelTimer timer_("sparse_bwd_q", st);
@@ -796,7 +910,7 @@ int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void
                        inv_scale, static_cast<T*>(gq), part_q, c->rowptr, c->packed_q,
                        c->n_packed_q, pw_q, int32_t(q_blocks),
                        reinterpret_cast<const int4*>(c->splits_k), kv_tiles, part_kv,
-                       static_cast<T*>(gk), static_cast<T*>(gv));
+                       static_cast<T*>(gk), static_cast<T*>(gv), xcd);
     NGT_HIP_CHECK(hipGetLastError());
   }
   if (c->n_splits_q > 0) {

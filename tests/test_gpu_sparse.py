@@ -91,6 +91,23 @@ def test_sparse_parity_hub_rows_split(H, d, dtype, chunk, small):
     _check(res, _oracle(q, k, v, ei, go, H), dtype, "hub")
 
 
+@pytest.mark.parametrize("H,hg,xcd,dtype", [(8, 2, "1", torch.float32), (8, 2, "0", torch.float32),
+                                           (8, 3, "1", torch.float32), (32, 4, "1", torch.bfloat16),
+                                           (6, 4, "1", torch.bfloat16)])
+def test_sparse_parity_head_groups(monkeypatch, H, hg, xcd, dtype):
+    """Every kernel walking the heads in groups of hg: groups dealt to the
+    XCDs (xcd on and the group count divides 8) or in launch order (xcd off,
+    or 3 groups); split, medium and packed rows in both orientations."""
+    _say(f"case head groups H={H} hg={hg} xcd={xcd} {dtype}")
+    monkeypatch.setenv("NGT_HEAD_GROUP", str(hg))
+    monkeypatch.setenv("NGT_XCD", xcd)
+    n = 150
+    ei = hub_coo(n, n, 700, seed=H + hg)
+    q, k, v, go = _qkv(n, n, H, 24, dtype, seed=11)
+    res = _run_kernel(q, k, v, ei, go, chunk=32, small=3)
+    _check(res, _oracle(q, k, v, ei, go, H), dtype, "head groups")
+
+
 def test_sparse_golden_fixtures():
     from pathlib import Path
 
