@@ -172,24 +172,38 @@ int ngt_sparse_bwd(int dtype, const void* q, const void* k, const void* v, const
                    size_t workspace_bytes, void* stream);
 
 /*
- * Dense full-window attention (all pairs, no mask/bias, dropout p = 0).
+ * Dense full-window attention (all pairs, no mask/bias).
  * Replaces CoreAttention.full_attention:
  *   NeutronGT/models/graphormer_dist_node_level.py:42-65
  *   NeutronGT/models/gt_dist_node_level_single_window.py:56-109
- *   S = (q * scale) k^T per head (the reference multiplies by sqrt(d));
- *   out = softmax(S) v;  lse[h,i] = logsumexp_j S[h,i,j] (fp32, for backward);
- *   node_score[j] = sum_i mean_h |S[h,i,j]| (may be NULL).
+ * and the "flash" branch's naive_attention (graphormer_dist_node_level.py:
+ * 100-105, 113-124; scale = 1/sqrt(d), dropout always on):
+ *   S = (q * scale) k^T per head (full_attention multiplies by sqrt(d));
+ *   P = softmax(S);  out = dropout(P) v;  lse[h,i] = logsumexp_j S[h,i,j]
+ *   (fp32, for backward); node_score[j] = sum_i mean_h |S[h,i,j]| (may be NULL).
+ * dropout_p in [0, 1] is the reference's att_dropout on P (training mode):
+ * element (h, i, j) is kept with probability 1 - round(p * 65536) / 65536 and
+ * scaled by 1 / (1 - p); the keep bit is a hash of (seed, h, i, j), so
+ * ngt_dense_bwd with the same seed and p reproduces the forward's mask.
+ * p > 0 needs n_q * ceil(n_k / 2) <= 2^32.
+ * out_f32 (bf16 only, may be NULL): the forward also writes out in fp32 there,
+ * and the backward then takes D_i = G_i . out_i from it instead of the
+ * bf16-rounded out (out may then be NULL in the backward).  For rows whose
+ * softmax is peaked, dS = P (dP - D) nearly cancels and the rounded out
+ * alone moves dQ by percents.
  */
 int ngt_dense_workspace_bytes(int32_t n_q, int32_t n_k, int32_t n_heads, int32_t head_dim,
                               size_t* fwd_bytes, size_t* bwd_bytes);
 int ngt_dense_fwd(int dtype, const void* q, const void* k, const void* v, int32_t n_q,
-                  int32_t n_k, int32_t n_heads, int32_t head_dim, float scale, void* out,
-                  float* lse, float* node_score, void* workspace, size_t workspace_bytes,
-                  void* stream);
+                  int32_t n_k, int32_t n_heads, int32_t head_dim, float scale, float dropout_p,
+                  uint64_t seed, void* out, float* out_f32, float* lse, float* node_score,
+                  void* workspace, size_t workspace_bytes, void* stream);
 int ngt_dense_bwd(int dtype, const void* q, const void* k, const void* v, const void* out,
-                  const void* grad_out, const float* lse, int32_t n_q, int32_t n_k,
-                  int32_t n_heads, int32_t head_dim, float scale, void* grad_q, void* grad_k,
-                  void* grad_v, void* workspace, size_t workspace_bytes, void* stream);
+                  const float* out_f32, const void* grad_out, const float* lse, int32_t n_q,
+                  int32_t n_k,
+                  int32_t n_heads, int32_t head_dim, float scale, float dropout_p, uint64_t seed,
+                  void* grad_q, void* grad_k, void* grad_v, void* workspace,
+                  size_t workspace_bytes, void* stream);
 
 /*
  * Related-node selection for one window.

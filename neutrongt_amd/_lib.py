@@ -73,6 +73,7 @@ class WindowCSR(C.Structure):
 
 
 _i32, _i64, _f32, _vp, _sz = C.c_int32, C.c_int64, C.c_float, C.c_void_p, C.c_size_t
+_u64 = C.c_uint64
 _pi32 = C.POINTER(C.c_int32)
 _psz = C.POINTER(C.c_size_t)
 _pcsr = C.POINTER(WindowCSR)
@@ -90,10 +91,10 @@ SIGNATURES = {
     "ngt_sparse_bwd": [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _pcsr, _i32, _i32, _f32, _f32, _f32,
                        _vp, _vp, _vp, _vp, _sz, _vp],
     "ngt_dense_workspace_bytes": [_i32, _i32, _i32, _i32, _psz, _psz],
-    "ngt_dense_fwd": [_i32, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _vp, _vp, _vp, _vp, _sz,
-                      _vp],
-    "ngt_dense_bwd": [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _vp, _vp,
-                      _vp, _vp, _sz, _vp],
+    "ngt_dense_fwd": [_i32, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _f32, _u64, _vp, _vp,
+                      _vp, _vp, _vp, _sz, _vp],
+    "ngt_dense_bwd": [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _f32,
+                      _u64, _vp, _vp, _vp, _vp, _sz, _vp],
     "ngt_related_workspace_bytes": [_i32, _i32, _psz],
     "ngt_merge_related_nodes": [_vp, _vp, _vp, _i32, _vp, _i32, _i32, _vp, _vp, _vp, _sz, _vp],
     "ngt_gather_rows": [_vp, _i64, _vp, _i64, _i64, _vp, _vp, _vp],

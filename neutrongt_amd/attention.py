@@ -132,26 +132,33 @@ def sparse_attention(q, k, v, edge_index, num_heads=None, scale=None, cache: Adj
 
 # -------------------------------------------------------------------- dense
 class DenseAttentionFunction(torch.autograd.Function):
-    """out = softmax((q*scale) k^T) v per head, node_score[j] = sum_i mean_h |S|."""
+    """out = dropout_p(softmax((q*scale) k^T)) v per head,
+    node_score[j] = sum_i mean_h |S|.  With dropout_p > 0 the keep mask is a
+    hash of (seed, head, query, key) (the C-ABI's ngt_dense_fwd documents it);
+    the backward regenerates it from the same seed."""
 
     @staticmethod
-    def forward(ctx, q, k, v, scale, want_scores):
+    def forward(ctx, q, k, v, scale, want_scores, dropout_p=0.0, seed=0):
         lib = _lib.load()
         n_q, H, d = q.shape
         n_k = k.shape[0]
         dev = q.device
         out = torch.empty_like(q)
+        # bf16: an fp32 copy of out feeds the backward's D = G . out
+        out32 = (torch.empty(n_q, H, d, dtype=torch.float32, device=dev)
+                 if q.dtype != torch.float32 else None)
         lse = torch.empty(H, n_q, dtype=torch.float32, device=dev)
         ns = torch.empty(n_k if want_scores else 0, dtype=torch.float32, device=dev)
         fb, bb = C.c_size_t(), C.c_size_t()
         _lib.check(lib.ngt_dense_workspace_bytes(n_q, n_k, H, d, C.byref(fb), C.byref(bb)))
         ws = _workspace(fb.value, dev)
         _lib.check(lib.ngt_dense_fwd(_dtype_code(q), q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                                     n_q, n_k, H, d, scale, out.data_ptr(), lse.data_ptr(),
-                                     ns.data_ptr() if want_scores and n_k else None,
+                                     n_q, n_k, H, d, scale, dropout_p, seed, out.data_ptr(),
+                                     out32.data_ptr() if out32 is not None else None,
+                                     lse.data_ptr(), ns.data_ptr() if want_scores and n_k else None,
                                      ws.data_ptr(), fb.value, _stream(dev)))
-        ctx.save_for_backward(q, k, v, out, lse)
-        ctx.scale, ctx.bwd_bytes = scale, bb.value
+        ctx.save_for_backward(q, k, v, out if out32 is None else out32, lse)
+        ctx.scale, ctx.bwd_bytes, ctx.dropout_p, ctx.seed = scale, bb.value, dropout_p, seed
         ctx.mark_non_differentiable(ns)
         return out, ns
 
@@ -169,16 +176,27 @@ class DenseAttentionFunction(torch.autograd.Function):
         gk = torch.empty_like(k)
         gv = torch.empty_like(v)
         ws = _workspace(ctx.bwd_bytes, dev)
+        f32_out = out.dtype != q.dtype  # the fp32 copy saved for a bf16 forward
         _lib.check(lib.ngt_dense_bwd(_dtype_code(q), q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                                     out.data_ptr(), g.data_ptr(), lse.data_ptr(), n_q, n_k, H, d,
-                                     ctx.scale, gq.data_ptr(), gk.data_ptr(), gv.data_ptr(),
-                                     ws.data_ptr(), ctx.bwd_bytes, _stream(dev)))
-        return gq, gk, gv, None, None
+                                     None if f32_out else out.data_ptr(),
+                                     out.data_ptr() if f32_out else None, g.data_ptr(),
+                                     lse.data_ptr(), n_q, n_k, H, d,
+                                     ctx.scale, ctx.dropout_p, ctx.seed, gq.data_ptr(),
+                                     gk.data_ptr(), gv.data_ptr(), ws.data_ptr(), ctx.bwd_bytes,
+                                     _stream(dev)))
+        return gq, gk, gv, None, None, None, None
 
 
-def dense_attention(q, k, v, scale=None, node_scores=True):
+def draw_seed() -> int:
+    """A 64-bit dropout seed from torch's default (CPU) generator, so that
+    torch.manual_seed makes dropout masks reproducible; no device sync."""
+    return int(torch.randint(0, 2**62, (1,), dtype=torch.int64).item())
+
+
+def dense_attention(q, k, v, scale=None, node_scores=True, dropout_p=0.0, seed=None):
     """Functional form of full_attention: q [.., N_q, H, d], k/v [.., N_k, H, d]
-    -> (x [N_q, H, d], node_scores [N_k] or empty)."""
+    -> (x [N_q, H, d], node_scores [N_k] or empty).  dropout_p > 0 applies
+    dropout to the attention probabilities (seed: None draws one)."""
     H, d = q.shape[-2], q.shape[-1]
     q = _prep(q.reshape(-1, H, d), "q")
     k = _prep(k.reshape(-1, H, d), "k")
@@ -190,7 +208,13 @@ def dense_attention(q, k, v, scale=None, node_scores=True):
         raise ValueError(f"shape mismatch q {tuple(q.shape)} k {tuple(k.shape)} v {tuple(v.shape)}")
     if scale is None:
         scale = math.sqrt(d)
-    return DenseAttentionFunction.apply(q, k, v, float(scale), bool(node_scores))
+    dropout_p = float(dropout_p)
+    if not 0.0 <= dropout_p <= 1.0:
+        raise ValueError(f"dropout probability has to be between 0 and 1, but got {dropout_p}")
+    if dropout_p > 0.0 and seed is None:
+        seed = draw_seed()
+    return DenseAttentionFunction.apply(q, k, v, float(scale), bool(node_scores), dropout_p,
+                                        int(seed or 0))
 
 
 # ---------------------------------------------------------------- the module
@@ -207,19 +231,29 @@ class CoreAttention(nn.Module):
         self.adjacency_cache = cache or default_cache
 
     def full_attention(self, k, q, v, attn_bias, mask=None, pruning_mask=None):
-        """graphormer_dist_node_level.py:42-65.  Returns (x [b, N, H, d], node_scores [N_k])."""
+        """graphormer_dist_node_level.py:42-65.  Returns (x [b, N, H, d], node_scores [N_k]).
+        In training mode the probabilities go through att_dropout (p of the
+        module's nn.Dropout), as the reference's self.att_dropout(x) does."""
         if attn_bias is not None or mask is not None or pruning_mask is not None:
             raise NotImplementedError(
                 "full attention with attn_bias/mask/pruning_mask is not implemented by the "
                 "dense kernel (all are None on NeutronGT's training path)")
-        if self.training and self.att_dropout.p > 0:
-            raise NotImplementedError(
-                "dropout on full-attention probabilities is not implemented by the dense kernel; "
-                "use attention_dropout_rate=0 or eval mode")
         if q.size(0) != 1:
             raise NotImplementedError("batch size must be 1 (as in NeutronGT's window step)")
-        x, ns = dense_attention(q, k, v, scale=self.scale)
+        p = self.att_dropout.p if self.training else 0.0
+        x, ns = dense_attention(q, k, v, scale=self.scale, dropout_p=p)
         return x.unsqueeze(0), ns
+
+    def naive_attention(self, q, k, v, dropout_p=0.0):
+        """graphormer_dist_node_level.py:100-105 on [b, N, H, d] inputs:
+        softmax(q k^T / sqrt(d)) with dropout always applied (F.dropout with
+        training=True), no node scores.  Returns (x [b, N, H, d], None)."""
+        if q.size(0) != 1:
+            raise NotImplementedError("batch size must be 1 (as in NeutronGT's window step)")
+        d = q.shape[-1]
+        x, _ = dense_attention(q, k, v, scale=1.0 / math.sqrt(d), node_scores=False,
+                               dropout_p=dropout_p)
+        return x.unsqueeze(0), None
 
     def sparse_attention_bias(self, q, k, v, edge_index, attn_bias):
         """graphormer_dist_node_level.py:67-98.  Returns (x [N_q, H, d], node_scores)."""
@@ -236,9 +270,10 @@ class CoreAttention(nn.Module):
         if attn_type == "sparse":
             x, score = self.sparse_attention_bias(q, k, v, edge_index, attn_bias)
         elif attn_type == "flash":
-            raise NotImplementedError(
-                "attn_type='flash' (the reference's fp16 naive attention with dropout always on) "
-                "is not provided; use 'sparse' or 'full'")
+            # The reference casts q/k/v to fp16 here and the result back to
+            # fp32; this runs the same math in the inputs' dtype (fp32 or bf16).
+            x, score = self.naive_attention(q, k, v, dropout_p=self.attention_dropout_rate)
+            x = x.float()
         else:
             x, score = self.full_attention(k, q, v, attn_bias, mask=mask, pruning_mask=pruning_mask)
         x = x.view(batch_size, s_len, -1)

@@ -265,6 +265,54 @@ __device__ __forceinline__ float reduce_heads(float v, int L) {
   return v;
 }
 
+// ------------------------------------------------------------ dropout masks
+// Dropout of attention probabilities (dense attention in training mode).
+// One 32-bit word serves two adjacent keys of a (head, query) row:
+//   word(h, i, j) = mix32((i * ceil(n_k / 2) + j / 2) ^ head_key(seed, h))
+//   keep(h, i, j) = (j odd ? word >> 16 : word & 0xffff) >= thr
+// with thr = round(p * 65536), so the keep probability is 1 - thr / 65536
+// (exactly 1 - p for p a multiple of 2^-16, e.g. 0.5).  Every kernel derives
+// the same bit for an element from its coordinates alone, so the backward
+// reproduces the forward's mask without storing it.  Kept probabilities are
+// scaled by 1 / (1 - p); p = 1 drops everything (scale 0).  mix32 is the
+// "lowbias32" integer hash (C. Wellons, hash-prospector, public domain).
+struct DropoutMask {
+  uint64_t seed;
+  uint32_t head_key;  // drop_head_key(seed, h): set by the kernel for its head
+  uint32_t n_kp;      // ceil(n_k / 2): words per query row
+  uint32_t thr;       // keep iff the 16-bit half >= thr
+  float scale;        // 1 / (1 - p), 0 for p = 1
+};
+
+__host__ __device__ __forceinline__ uint32_t mix32(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x7feb352dU;
+  x ^= x >> 15;
+  x *= 0x846ca68bU;
+  x ^= x >> 16;
+  return x;
+}
+
+__host__ __device__ __forceinline__ uint32_t drop_head_key(uint64_t seed, uint32_t h) {
+  return mix32(static_cast<uint32_t>(seed) ^
+               mix32(static_cast<uint32_t>(seed >> 32) + 0x9e3779b9U * (h + 1U)));
+}
+
+__device__ __forceinline__ DropoutMask drop_for_head(DropoutMask dm, int h) {
+  dm.head_key = drop_head_key(dm.seed, static_cast<uint32_t>(h));
+  return dm;
+}
+
+__device__ __forceinline__ uint32_t drop_word(const DropoutMask& dm, uint32_t i, uint32_t j) {
+  return mix32((i * dm.n_kp + (j >> 1)) ^ dm.head_key);
+}
+
+// Scale applied to element (.., j) given its pair's word: 1/(1-p) or 0.
+__device__ __forceinline__ float drop_scale(const DropoutMask& dm, uint32_t word, uint32_t j) {
+  const uint32_t half = (j & 1U) ? (word >> 16) : (word & 0xffffU);
+  return half >= dm.thr ? dm.scale : 0.f;
+}
+
 template <typename T>
 struct dtype_of;
 template <>

@@ -7,6 +7,10 @@
 // The backward is what autograd derives: dV = P^T G, dP = G V^T,
 // dS = P (dP - rowsum(dP P)) = P (dP - D) with D_i = G_i . out_i,
 // dQ = sqrt(d) dS K, dK = sqrt(d) dS^T Q.
+// With dropout (training mode, reference att_dropout on P): out = (P o M) v
+// with M = keep / (1 - p); dV = (P o M)^T G, dP = (G V^T) o M, and D_i = G_i .
+// out_i still equals rowsum(dP o P).  The mask is regenerated from
+// (seed, head, query, key) in every kernel (DropoutMask).
 //
 // Layout of one wave: 16 rows (lane % 16) x 4 column groups (lane / 16) of 8
 // columns each, i.e. a 16 x 32 tile of S per step.  The forward keeps an
@@ -26,10 +30,11 @@ namespace ngt {
 // Matrix-core kernels (ngt_dense_mfma.hip).
 bool mfma_dense_supported(int d);
 int mfma_dense_fwd(int d, const void* q, const void* k, const void* v, int n_q, int n_k, int H,
-                   float scale, void* out, float* lse, float* part, hipStream_t st);
+                   float scale, const DropoutMask* dm, void* out, float* out32, float* lse,
+                   float* part, hipStream_t st);
 int mfma_dense_bwd(int d, const void* q, const void* k, const void* v, const void* g,
                    const float* lse, const float* dsum, int n_q, int n_k, int H, float scale,
-                   void* gq, void* gk, void* gv, hipStream_t st);
+                   const DropoutMask* dm, void* gq, void* gk, void* gv, hipStream_t st);
 
 namespace {
 
@@ -65,11 +70,11 @@ __device__ __forceinline__ float row16_sum(float x) {
 // ------------------------------------------------------------------ forward
 // grid = (ceil(n_q / 64), H).  ns_part (optional) is [gridDim.x * H, n_k]:
 // per block and head, sum over the block's 64 query rows of |S[h, i, j]|.
-template <typename T, int DH>
+template <typename T, int DH, bool DROP>
 __global__ __launch_bounds__(kBlock) void k_dense_fwd(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, int32_t n_q,
-    int32_t n_k, int32_t H, float scale, T* __restrict__ out, float* __restrict__ lse,
-    float* __restrict__ ns_part) {
+    int32_t n_k, int32_t H, float scale, DropoutMask dm, T* __restrict__ out,
+    float* __restrict__ out32, float* __restrict__ lse, float* __restrict__ ns_part) {
   __shared__ float ns_lds[kScoreChunk];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
@@ -78,6 +83,7 @@ __global__ __launch_bounds__(kBlock) void k_dense_fwd(
   const int h = blockIdx.y;
   const int64_t qi = int64_t(blockIdx.x) * kRowsPerBlock + wave * kRows + r;
   const bool q_ok = qi < n_q;
+  if constexpr (DROP) dm = drop_for_head(dm, h);
 
   float qs[DH];
   if (q_ok) {
@@ -131,16 +137,24 @@ __global__ __launch_bounds__(kBlock) void k_dense_fwd(
       l *= alpha;
 #pragma unroll
       for (int c = 0; c < DH; ++c) acc[c] *= alpha;
+      uint32_t dw[kColsPerLane / 2];  // one dropout word per key pair
+      if constexpr (DROP) {
+#pragma unroll
+        for (int i = 0; i < kColsPerLane / 2; ++i)
+          dw[i] = drop_word(dm, uint32_t(qi), uint32_t(kb + g * kColsPerLane + 2 * i));
+      }
 #pragma unroll
       for (int i = 0; i < kColsPerLane; ++i) {
         const int64_t kj = kb + g * kColsPerLane + i;
         if (kj < kc_end) {
           const float p = __expf(s[i] - m_new);
-          l += p;
+          l += p;  // the softmax normaliser uses every key
+          float pv = p;
+          if constexpr (DROP) pv *= drop_scale(dm, dw[i / 2], uint32_t(kj));
           float vr[DH];
           load_row<T, DH>(v + (kj * H + h) * DH, vr);
 #pragma unroll
-          for (int c = 0; c < DH; ++c) acc[c] = fmaf(p, vr[c], acc[c]);
+          for (int c = 0; c < DH; ++c) acc[c] = fmaf(pv, vr[c], acc[c]);
         }
       }
       m = m_new;
@@ -164,6 +178,7 @@ __global__ __launch_bounds__(kBlock) void k_dense_fwd(
 #pragma unroll
     for (int c = 0; c < DH; ++c) o[c] = acc[c] * inv;
     store_row<T, DH>(out + (qi * H + h) * DH, o);
+    if (out32) store_f32<DH>(out32 + (qi * H + h) * DH, o);
     lse[int64_t(h) * n_q + qi] = n_k > 0 ? m + __logf(l) : -INFINITY;
   }
 }
@@ -180,16 +195,19 @@ __global__ void k_dense_scores(const float* __restrict__ part, int32_t rows, int
 }
 
 // ----------------------------------------------------------------- backward
-// Dq[h, i] = sum_c G[i,h,c] out[i,h,c]
-template <typename T, int DH>
-__global__ __launch_bounds__(kBlock) void k_dense_rowstat(const T* __restrict__ out,
+// Dq[h, i] = sum_c G[i,h,c] out[i,h,c].  For bf16 the forward's fp32 copy of
+// out (TO = float) is used when there is one: D enters dS = P (dP - D) where
+// the two terms nearly cancel for peaked rows, and the bf16-rounded out alone
+// moves dQ by a few percent there.
+template <typename TO, typename T, int DH>
+__global__ __launch_bounds__(kBlock) void k_dense_rowstat(const TO* __restrict__ out,
                                                           const T* __restrict__ g, int32_t n_q,
                                                           int32_t H, float* __restrict__ dq) {
   const int64_t n = int64_t(n_q) * H;
   for (int64_t t = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; t < n;
        t += int64_t(gridDim.x) * blockDim.x) {
     float o[DH], gg[DH];
-    load_row<T, DH>(out + t * DH, o);
+    load_row<TO, DH>(out + t * DH, o);
     load_row<T, DH>(g + t * DH, gg);
     const int64_t i = t / H, h = t % H;
     dq[h * n_q + i] = dotv<DH>(o, gg);
@@ -198,11 +216,11 @@ __global__ __launch_bounds__(kBlock) void k_dense_rowstat(const T* __restrict__ 
 
 // Key-major pass: lane owns key row (lane % 16) of the wave and 8 queries of
 // each 32-query tile.  grid = (ceil(n_k / 64), H).
-template <typename T, int DH>
+template <typename T, int DH, bool DROP>
 __global__ __launch_bounds__(kBlock) void k_dense_bwd_kv(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const T* __restrict__ g, const float* __restrict__ lse, const float* __restrict__ dsum,
-    int32_t n_q, int32_t n_k, int32_t H, float scale, T* __restrict__ grad_k,
+    int32_t n_q, int32_t n_k, int32_t H, float scale, DropoutMask dm, T* __restrict__ grad_k,
     T* __restrict__ grad_v) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
@@ -211,6 +229,7 @@ __global__ __launch_bounds__(kBlock) void k_dense_bwd_kv(
   const int h = blockIdx.y;
   const int64_t kj = int64_t(blockIdx.x) * kRowsPerBlock + wave * kRows + r;
   const bool k_ok = kj < n_k;
+  if constexpr (DROP) dm = drop_for_head(dm, h);
   float kr[DH], vr[DH], dk[DH], dv[DH];
   if (k_ok) {
     load_row<T, DH>(k + (kj * H + h) * DH, kr);
@@ -234,10 +253,14 @@ __global__ __launch_bounds__(kBlock) void k_dense_bwd_kv(
 #pragma unroll
         for (int c = 0; c < DH; ++c) qs[c] *= scale;
         const float p = __expf(dotv<DH>(qs, kr) - lse_h[qi]);
-        const float ds = p * (dotv<DH>(gi, vr) - ds_h[qi]);
+        float m = 1.f;
+        if constexpr (DROP)
+          m = drop_scale(dm, drop_word(dm, uint32_t(qi), uint32_t(kj)), uint32_t(kj));
+        const float ds = p * (m * dotv<DH>(gi, vr) - ds_h[qi]);
+        const float pm = p * m;
 #pragma unroll
         for (int c = 0; c < DH; ++c) {
-          dv[c] = fmaf(p, gi[c], dv[c]);
+          dv[c] = fmaf(pm, gi[c], dv[c]);
           dk[c] = fmaf(ds, qs[c], dk[c]);
         }
       }
@@ -257,11 +280,11 @@ __global__ __launch_bounds__(kBlock) void k_dense_bwd_kv(
 }
 
 // Query-major pass: lane owns query row (lane % 16) and 8 keys per tile.
-template <typename T, int DH>
+template <typename T, int DH, bool DROP>
 __global__ __launch_bounds__(kBlock) void k_dense_bwd_q(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const T* __restrict__ g, const float* __restrict__ lse, const float* __restrict__ dsum,
-    int32_t n_q, int32_t n_k, int32_t H, float scale, T* __restrict__ grad_q) {
+    int32_t n_q, int32_t n_k, int32_t H, float scale, DropoutMask dm, T* __restrict__ grad_q) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
   const int r = lane & 15;
@@ -269,6 +292,7 @@ __global__ __launch_bounds__(kBlock) void k_dense_bwd_q(
   const int h = blockIdx.y;
   const int64_t qi = int64_t(blockIdx.x) * kRowsPerBlock + wave * kRows + r;
   const bool q_ok = qi < n_q;
+  if constexpr (DROP) dm = drop_for_head(dm, h);
   float qs[DH], gi[DH], dq[DH];
   float L = 0.f, Dq = 0.f;
   if (q_ok) {
@@ -293,7 +317,10 @@ __global__ __launch_bounds__(kBlock) void k_dense_bwd_q(
         load_row<T, DH>(k + (kj * H + h) * DH, kr);
         load_row<T, DH>(v + (kj * H + h) * DH, vr);
         const float p = __expf(dotv<DH>(qs, kr) - L);
-        const float ds = p * (dotv<DH>(gi, vr) - Dq);
+        float m = 1.f;
+        if constexpr (DROP)
+          m = drop_scale(dm, drop_word(dm, uint32_t(qi), uint32_t(kj)), uint32_t(kj));
+        const float ds = p * (m * dotv<DH>(gi, vr) - Dq);
 #pragma unroll
         for (int c = 0; c < DH; ++c) dq[c] = fmaf(ds, kr[c], dq[c]);
       }
@@ -320,15 +347,24 @@ size_t bwd_ws(int32_t n_q, int32_t H) { return align256(size_t(n_q) * H * 4); }
 
 template <typename T, int DH>
 int launch_fwd(const void* q, const void* k, const void* v, int n_q, int n_k, int H, float scale,
-               void* out, float* lse, float* ns, char* ws, hipStream_t st) {
+               const DropoutMask* dm, void* out, float* out32, float* lse, float* ns, char* ws,
+               hipStream_t st) {
   if (n_q == 0) return NGT_OK;
   float* part = ns ? reinterpret_cast<float*>(ws) : nullptr;
   dim3 grid(static_cast<unsigned>(qblocks(n_q)), static_cast<unsigned>(H));
   {
     KernelTimer timer_("dense_fwd", st);
-    hipLaunchKernelGGL((k_dense_fwd<T, DH>), grid, dim3(kBlock), 0, st, static_cast<const T*>(q),
-                       static_cast<const T*>(k), static_cast<const T*>(v), n_q, n_k, H, scale,
-                       static_cast<T*>(out), lse, part);
+    const DropoutMask m = dm ? *dm : DropoutMask{};
+    if (dm)
+      hipLaunchKernelGGL((k_dense_fwd<T, DH, true>), grid, dim3(kBlock), 0, st,
+                         static_cast<const T*>(q), static_cast<const T*>(k),
+                         static_cast<const T*>(v), n_q, n_k, H, scale, m, static_cast<T*>(out),
+                         out32, lse, part);
+    else
+      hipLaunchKernelGGL((k_dense_fwd<T, DH, false>), grid, dim3(kBlock), 0, st,
+                         static_cast<const T*>(q), static_cast<const T*>(k),
+                         static_cast<const T*>(v), n_q, n_k, H, scale, m, static_cast<T*>(out),
+                         out32, lse, part);
     NGT_HIP_CHECK(hipGetLastError());
   }
   if (ns && n_k > 0) {
@@ -341,17 +377,22 @@ int launch_fwd(const void* q, const void* k, const void* v, int n_q, int n_k, in
 }
 
 template <typename T, int DH>
-int launch_bwd(const void* q, const void* k, const void* v, const void* out, const void* g,
-               const float* lse, int n_q, int n_k, int H, float scale, void* gq, void* gk,
-               void* gv, char* ws, hipStream_t st) {
+int launch_bwd(const void* q, const void* k, const void* v, const void* out, const float* out32,
+               const void* g, const float* lse, int n_q, int n_k, int H, float scale,
+               const DropoutMask* dm, void* gq, void* gk, void* gv, char* ws, hipStream_t st) {
+  const DropoutMask m = dm ? *dm : DropoutMask{};
   float* dsum = reinterpret_cast<float*>(ws);
   if (n_q > 0) {
     int64_t blocks = (int64_t(n_q) * H + kBlock - 1) / kBlock;
     if (blocks > 65536) blocks = 65536;
     {
       KernelTimer timer_("dense_rowstat", st);
-      hipLaunchKernelGGL((k_dense_rowstat<T, DH>), dim3(int(blocks)), dim3(kBlock), 0, st,
-                         static_cast<const T*>(out), static_cast<const T*>(g), n_q, H, dsum);
+      if (out32)
+        hipLaunchKernelGGL((k_dense_rowstat<float, T, DH>), dim3(int(blocks)), dim3(kBlock), 0, st,
+                           out32, static_cast<const T*>(g), n_q, H, dsum);
+      else
+        hipLaunchKernelGGL((k_dense_rowstat<T, T, DH>), dim3(int(blocks)), dim3(kBlock), 0, st,
+                           static_cast<const T*>(out), static_cast<const T*>(g), n_q, H, dsum);
       NGT_HIP_CHECK(hipGetLastError());
     }
   }
@@ -359,10 +400,16 @@ int launch_bwd(const void* q, const void* k, const void* v, const void* out, con
     dim3 grid(static_cast<unsigned>(qblocks(n_k)), static_cast<unsigned>(H));
     {
       KernelTimer timer_("dense_bwd_kv", st);
-      hipLaunchKernelGGL((k_dense_bwd_kv<T, DH>), grid, dim3(kBlock), 0, st,
-                         static_cast<const T*>(q), static_cast<const T*>(k),
-                         static_cast<const T*>(v), static_cast<const T*>(g), lse, dsum, n_q, n_k, H,
-                         scale, static_cast<T*>(gk), static_cast<T*>(gv));
+      if (dm)
+        hipLaunchKernelGGL((k_dense_bwd_kv<T, DH, true>), grid, dim3(kBlock), 0, st,
+                           static_cast<const T*>(q), static_cast<const T*>(k),
+                           static_cast<const T*>(v), static_cast<const T*>(g), lse, dsum, n_q,
+                           n_k, H, scale, m, static_cast<T*>(gk), static_cast<T*>(gv));
+      else
+        hipLaunchKernelGGL((k_dense_bwd_kv<T, DH, false>), grid, dim3(kBlock), 0, st,
+                           static_cast<const T*>(q), static_cast<const T*>(k),
+                           static_cast<const T*>(v), static_cast<const T*>(g), lse, dsum, n_q,
+                           n_k, H, scale, m, static_cast<T*>(gk), static_cast<T*>(gv));
       NGT_HIP_CHECK(hipGetLastError());
     }
   }
@@ -370,10 +417,16 @@ int launch_bwd(const void* q, const void* k, const void* v, const void* out, con
     dim3 grid(static_cast<unsigned>(qblocks(n_q)), static_cast<unsigned>(H));
     {
       KernelTimer timer_("dense_bwd_q", st);
-      hipLaunchKernelGGL((k_dense_bwd_q<T, DH>), grid, dim3(kBlock), 0, st,
-                         static_cast<const T*>(q), static_cast<const T*>(k),
-                         static_cast<const T*>(v), static_cast<const T*>(g), lse, dsum, n_q, n_k, H,
-                         scale, static_cast<T*>(gq));
+      if (dm)
+        hipLaunchKernelGGL((k_dense_bwd_q<T, DH, true>), grid, dim3(kBlock), 0, st,
+                           static_cast<const T*>(q), static_cast<const T*>(k),
+                           static_cast<const T*>(v), static_cast<const T*>(g), lse, dsum, n_q,
+                           n_k, H, scale, m, static_cast<T*>(gq));
+      else
+        hipLaunchKernelGGL((k_dense_bwd_q<T, DH, false>), grid, dim3(kBlock), 0, st,
+                           static_cast<const T*>(q), static_cast<const T*>(k),
+                           static_cast<const T*>(v), static_cast<const T*>(g), lse, dsum, n_q,
+                           n_k, H, scale, m, static_cast<T*>(gq));
       NGT_HIP_CHECK(hipGetLastError());
     }
   }
@@ -423,6 +476,31 @@ int check_args(const char* fn, int dtype, int n_q, int n_k, int H, int d) {
   return NGT_OK;
 }
 
+// Dropout parameters from p and the seed; *on = false for p = 0.
+int make_dropout(const char* fn, float p, uint64_t seed, int n_q, int n_k, DropoutMask* dm,
+                 bool* on) {
+  *on = false;
+  if (!(p >= 0.f && p <= 1.f))
+    return set_error(NGT_ERR_ARG, "%s: dropout_p=%g outside [0, 1]", fn, double(p));
+  if (p == 0.f) return NGT_OK;
+  const uint64_t words = uint64_t(n_q) * ((uint64_t(n_k) + 1) / 2);
+  if (words > (uint64_t(1) << 32))
+    return set_error(NGT_ERR_UNSUPPORTED,
+                     "%s: dropout needs n_q * ceil(n_k / 2) <= 2^32 (n_q=%d n_k=%d)", fn, n_q, n_k);
+  dm->seed = seed;
+  dm->head_key = 0;
+  dm->n_kp = static_cast<uint32_t>((uint64_t(n_k) + 1) / 2);
+  if (p >= 1.f) {  // everything dropped: keep-all mask with scale 0
+    dm->thr = 0;
+    dm->scale = 0.f;
+  } else {
+    dm->thr = static_cast<uint32_t>(lrint(double(p) * 65536.0));
+    dm->scale = static_cast<float>(1.0 / (1.0 - double(p)));
+  }
+  *on = true;
+  return NGT_OK;
+}
+
 // The bf16 path runs on the matrix cores (ngt_dense_mfma.hip) for d <= 32;
 // NGT_DENSE_VALU=1 selects the vector-ALU kernels instead (for comparison).
 bool use_mfma(int dtype, int d) {
@@ -430,16 +508,20 @@ bool use_mfma(int dtype, int d) {
   return dtype == NGT_BF16 && mfma_dense_supported(d) && !valu;
 }
 
-int rowstat_bf16(int d, const void* out, const void* g, int n_q, int H, float* dsum,
-                 hipStream_t st) {
+int rowstat_bf16(int d, const void* out, const float* out32, const void* g, int n_q, int H,
+                 float* dsum, hipStream_t st) {
   int64_t blocks = (int64_t(n_q) * H + kBlock - 1) / kBlock;
   if (blocks > 65536) blocks = 65536;
   KernelTimer timer_("dense_rowstat", st);
-#define NGT_RS(DH)                                                                              \
-  case DH:                                                                                      \
-    hipLaunchKernelGGL((k_dense_rowstat<bf16_t, DH>), dim3(int(blocks)), dim3(kBlock), 0, st,  \
-                       static_cast<const bf16_t*>(out), static_cast<const bf16_t*>(g), n_q, H,  \
-                       dsum);                                                                   \
+#define NGT_RS(DH)                                                                             \
+  case DH:                                                                                     \
+    if (out32)                                                                                 \
+      hipLaunchKernelGGL((k_dense_rowstat<float, bf16_t, DH>), dim3(int(blocks)), dim3(kBlock), \
+                         0, st, out32, static_cast<const bf16_t*>(g), n_q, H, dsum);           \
+    else                                                                                       \
+      hipLaunchKernelGGL((k_dense_rowstat<bf16_t, bf16_t, DH>), dim3(int(blocks)),              \
+                         dim3(kBlock), 0, st, static_cast<const bf16_t*>(out),                  \
+                         static_cast<const bf16_t*>(g), n_q, H, dsum);                          \
     break;
   switch (d) {
     NGT_RS(8)
@@ -469,11 +551,16 @@ extern "C" int ngt_dense_workspace_bytes(int32_t n_q, int32_t n_k, int32_t n_hea
 }
 
 extern "C" int ngt_dense_fwd(int dtype, const void* q, const void* k, const void* v, int32_t n_q,
-                             int32_t n_k, int32_t n_heads, int32_t head_dim, float scale, void* out,
+                             int32_t n_k, int32_t n_heads, int32_t head_dim, float scale,
+                             float dropout_p, uint64_t seed, void* out, float* out_f32,
                              float* lse, float* node_score, void* workspace,
                              size_t workspace_bytes, void* stream) {
   int rc = check_args("ngt_dense_fwd", dtype, n_q, n_k, n_heads, head_dim);
   if (rc != NGT_OK) return rc;
+  DropoutMask dmv{};
+  bool drop = false;
+  NGT_CHECK_OK(make_dropout("ngt_dense_fwd", dropout_p, seed, n_q, n_k, &dmv, &drop));
+  const DropoutMask* dm = drop ? &dmv : nullptr;
   if (n_q > 0 && (!q || !out || !lse)) return set_error(NGT_ERR_ARG, "ngt_dense_fwd: null q/out/lse");
   if (n_k > 0 && (!k || !v)) return set_error(NGT_ERR_ARG, "ngt_dense_fwd: null k/v");
   if (node_score && n_q > 0) {
@@ -488,25 +575,32 @@ extern "C" int ngt_dense_fwd(int dtype, const void* q, const void* k, const void
   if (use_mfma(dtype, head_dim)) {
     if (n_q == 0) return NGT_OK;
     float* part = node_score ? static_cast<float*>(workspace) : nullptr;
-    rc = mfma_dense_fwd(head_dim, q, k, v, n_q, n_k, n_heads, scale, out, lse, part, st);
+    rc = mfma_dense_fwd(head_dim, q, k, v, n_q, n_k, n_heads, scale, dm, out, out_f32, lse, part,
+                        st);
     if (rc != NGT_OK || !node_score || n_k == 0) return rc;
     hipLaunchKernelGGL(k_dense_scores, dim3((n_k + kBlock - 1) / kBlock), dim3(kBlock), 0, st,
                        part, n_heads, n_k, n_heads, node_score);
     NGT_HIP_CHECK(hipGetLastError());
     return NGT_OK;
   }
-  return dispatch<FwdOp>(dtype, head_dim, q, k, v, int(n_q), int(n_k), int(n_heads), scale, out,
-                         lse, node_score, static_cast<char*>(workspace), st);
+  return dispatch<FwdOp>(dtype, head_dim, q, k, v, int(n_q), int(n_k), int(n_heads), scale, dm,
+                         out, out_f32, lse, node_score, static_cast<char*>(workspace), st);
 }
 
 extern "C" int ngt_dense_bwd(int dtype, const void* q, const void* k, const void* v,
-                             const void* out, const void* grad_out, const float* lse, int32_t n_q,
+                             const void* out, const float* out_f32, const void* grad_out,
+                             const float* lse, int32_t n_q,
                              int32_t n_k, int32_t n_heads, int32_t head_dim, float scale,
-                             void* grad_q, void* grad_k, void* grad_v, void* workspace,
-                             size_t workspace_bytes, void* stream) {
+                             float dropout_p, uint64_t seed, void* grad_q, void* grad_k,
+                             void* grad_v, void* workspace, size_t workspace_bytes,
+                             void* stream) {
   int rc = check_args("ngt_dense_bwd", dtype, n_q, n_k, n_heads, head_dim);
   if (rc != NGT_OK) return rc;
-  if (n_q > 0 && (!q || !out || !grad_out || !lse || !grad_q))
+  DropoutMask dmv{};
+  bool drop = false;
+  NGT_CHECK_OK(make_dropout("ngt_dense_bwd", dropout_p, seed, n_q, n_k, &dmv, &drop));
+  const DropoutMask* dm = drop ? &dmv : nullptr;
+  if (n_q > 0 && (!q || (!out && !out_f32) || !grad_out || !lse || !grad_q))
     return set_error(NGT_ERR_ARG, "ngt_dense_bwd: null query-side pointer");
   if (n_k > 0 && (!k || !v || !grad_k || !grad_v))
     return set_error(NGT_ERR_ARG, "ngt_dense_bwd: null key-side pointer");
@@ -518,13 +612,13 @@ extern "C" int ngt_dense_bwd(int dtype, const void* q, const void* k, const void
   if (use_mfma(dtype, head_dim)) {
     float* dsum = static_cast<float*>(workspace);
     if (n_q > 0) {
-      rc = rowstat_bf16(head_dim, out, grad_out, n_q, n_heads, dsum, st);
+      rc = rowstat_bf16(head_dim, out, out_f32, grad_out, n_q, n_heads, dsum, st);
       if (rc != NGT_OK) return rc;
     }
-    return mfma_dense_bwd(head_dim, q, k, v, grad_out, lse, dsum, n_q, n_k, n_heads, scale,
+    return mfma_dense_bwd(head_dim, q, k, v, grad_out, lse, dsum, n_q, n_k, n_heads, scale, dm,
                           grad_q, grad_k, grad_v, st);
   }
-  return dispatch<BwdOp>(dtype, head_dim, q, k, v, out, grad_out, lse, int(n_q), int(n_k),
-                         int(n_heads), scale, grad_q, grad_k, grad_v,
+  return dispatch<BwdOp>(dtype, head_dim, q, k, v, out, out_f32, grad_out, lse, int(n_q), int(n_k),
+                         int(n_heads), scale, dm, grad_q, grad_k, grad_v,
                          static_cast<char*>(workspace), st);
 }

@@ -18,6 +18,10 @@
 // recomputed as D[q][key], dV += P^T G and dK += dS^T Q with Q/G tiles staged
 // in LDS) and query-major dQ (dQ += dS K with K staged in LDS).  Column scores
 // sum_i |S| come from a separate key-major pass (S tiles again on MFMA).
+// Dropout (DROP = true): the PV-class products take P o M, M = keep/(1-p)
+// from DropoutMask; the forward's row sums still come from the unmasked P
+// (an extra MFMA per K step against a constant ones row), and the backward
+// scales dP by M before dS = P o (dP - D).
 #include "ngt_common.h"
 
 #include <math.h>
@@ -168,12 +172,13 @@ __device__ __forceinline__ float sum_halves(float x) {
 
 // ------------------------------------------------------------------ forward
 // grid = (ceil(n_q / 128), H); wave w owns queries q0 .. q0+31.
-template <int DH>
+template <int DH, bool DROP>
 __global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
                                                    const bf16_t* __restrict__ k,
                                                    const bf16_t* __restrict__ v, int32_t n_q,
                                                    int32_t n_k, int32_t H, float scale,
-                                                   bf16_t* __restrict__ out,
+                                                   DropoutMask dm, bf16_t* __restrict__ out,
+                                                   float* __restrict__ out32,
                                                    float* __restrict__ lse) {
   constexpr int NC = DH / 8;  // K chunks of the QK^T contraction
   __shared__ __align__(16) short ks[kSB][DH + 8];  // K rows
@@ -185,6 +190,13 @@ __global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
   const int h = blockIdx.y;
   const int64_t qi = int64_t(blockIdx.x) * kRowsPerBlock + wave * kT + l32;
   const bool q_ok = qi < n_q;
+  if constexpr (DROP) dm = drop_for_head(dm, h);
+  // With dropout the ones row moves out of V^T into this constant A operand
+  // (row DH of A), multiplied with the unmasked P.
+  s16x4 ones_a = zero4();
+  if constexpr (DROP && DH < 32) {
+    if (l32 == DH) ones_a[0] = ones_a[1] = ones_a[2] = ones_a[3] = static_cast<short>(0x3f80);
+  }
 
   // Q^T as the B operand of S^T = K Q^T: lane holds Q[qi][8j + 4*half .. +4].
   s16x4 qb[NC];
@@ -196,7 +208,7 @@ __global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
   float m = -INFINITY, l = 0.f;
   f32x16 acc = zero16();  // O^T[c][q]: c = 8*(i/4) + 4*half + i%4
 
-  fill_pad_rows<DH>(vt, true);
+  fill_pad_rows<DH>(vt, !DROP);
   Stage<DH> pk, pv;
   pk.load(k, 0, n_k, H, h);
   pv.load(v, 0, n_k, H, h);
@@ -235,22 +247,42 @@ __global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
         for (int i = 0; i < 16; ++i) acc[i] *= alpha;
       }
       m = m_new;
-      s16x4 pb[4];
+      s16x4 pb[4], pm[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        pb[j] = pack4(__builtin_amdgcn_exp2f(fmaf(st[4 * j], s2, -m_new)), __builtin_amdgcn_exp2f(fmaf(st[4 * j + 1], s2, -m_new)),
-                      __builtin_amdgcn_exp2f(fmaf(st[4 * j + 2], s2, -m_new)), __builtin_amdgcn_exp2f(fmaf(st[4 * j + 3], s2, -m_new)));
+      for (int j = 0; j < 4; ++j) {
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(st[4 * j], s2, -m_new));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(st[4 * j + 1], s2, -m_new));
+        const float p2 = __builtin_amdgcn_exp2f(fmaf(st[4 * j + 2], s2, -m_new));
+        const float p3 = __builtin_amdgcn_exp2f(fmaf(st[4 * j + 3], s2, -m_new));
+        pb[j] = pack4(p0, p1, p2, p3);
+        if constexpr (DROP) {
+          // keys kb + r0 + 8j + 4*half + (0..3): two key pairs, one word each
+          const uint32_t key = uint32_t(kb + r0 + 8 * j + 4 * half);
+          const uint32_t w0 = drop_word(dm, uint32_t(qi), key);
+          const uint32_t w1 = drop_word(dm, uint32_t(qi), key + 2);
+          pm[j] = pack4(p0 * drop_scale(dm, w0, key), p1 * drop_scale(dm, w0, key + 1),
+                        p2 * drop_scale(dm, w1, key + 2), p3 * drop_scale(dm, w1, key + 3));
+        }
+      }
       if constexpr (DH == 32) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) l += sum4(pb[j]);
       }
       // O^T += V^T P^T, K steps of 8 keys.  For d < 32 row c = d of V^T is all
-      // ones, so O^T row d accumulates the row sum of the (rounded) P.
+      // ones, so O^T row d accumulates the row sum of the (rounded) P; with
+      // dropout that row comes from ones_a and the unmasked P instead.
       s16x4 va[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) va[j] = lds4(&vt[l32][r0 + 8 * j + 4 * half]);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc = mfma(va[j], pb[j], acc);
+      for (int j = 0; j < 4; ++j) {
+        if constexpr (DROP) {
+          acc = mfma(va[j], pm[j], acc);
+          if constexpr (DH < 32) acc = mfma(ones_a, pb[j], acc);
+        } else {
+          acc = mfma(va[j], pb[j], acc);
+        }
+      }
     }
   }
   if constexpr (DH < 32) {
@@ -264,7 +296,10 @@ __global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int c = 8 * (i / 4) + 4 * half + (i % 4);
-    if (c < DH) out[(qi * H + h) * DH + c].x = f32_to_bf16(acc[i] * inv);
+    if (c < DH) {
+      out[(qi * H + h) * DH + c].x = f32_to_bf16(acc[i] * inv);
+      if (out32) out32[(qi * H + h) * DH + c] = acc[i] * inv;
+    }
   }
   if (half == 0) lse[int64_t(h) * n_q + qi] = n_k > 0 ? (m + __log2f(l)) * kLn2 : -INFINITY;
 }
@@ -315,12 +350,12 @@ __global__ __launch_bounds__(kBlock) void k_mf_scores(const bf16_t* __restrict__
 // Key-major: dK, dV for keys k0 .. k0+31 of one head.  S, dP recomputed as
 // D[q][key]; Q and G stages of 128 queries in LDS, row-major (A operands of S
 // and dP) and transposed (B operands of dV += P^T G and dK += dS^T Q).
-template <int DH>
+template <int DH, bool DROP>
 __global__ __launch_bounds__(kBlock) void k_mf_bwd_kv(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
     const bf16_t* __restrict__ g, const float* __restrict__ lse, const float* __restrict__ dsum,
-    int32_t n_q, int32_t n_k, int32_t H, float scale, bf16_t* __restrict__ grad_k,
-    bf16_t* __restrict__ grad_v) {
+    int32_t n_q, int32_t n_k, int32_t H, float scale, DropoutMask dm,
+    bf16_t* __restrict__ grad_k, bf16_t* __restrict__ grad_v) {
   constexpr int NC = DH / 8;
   __shared__ __align__(16) short qs[kSB][DH + 8];
   __shared__ __align__(16) short gs[kSB][DH + 8];
@@ -335,6 +370,7 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_kv(
   const int h = blockIdx.y;
   const int64_t kj = int64_t(blockIdx.x) * kRowsPerBlock + wave * kT + l32;
   const bool k_ok = kj < n_k;
+  if constexpr (DROP) dm = drop_for_head(dm, h);
   s16x4 kbv[NC], vbv[NC];  // K^T, V^T as B operands
 #pragma unroll
   for (int j = 0; j < NC; ++j) {
@@ -391,9 +427,21 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_kv(
         const float p1 = __builtin_amdgcn_exp2f(fmaf(st[4 * j + 1], s2, -lv.y));
         const float p2 = __builtin_amdgcn_exp2f(fmaf(st[4 * j + 2], s2, -lv.z));
         const float p3 = __builtin_amdgcn_exp2f(fmaf(st[4 * j + 3], s2, -lv.w));
-        pa[j] = pack4(p0, p1, p2, p3);
-        dsa[j] = pack4(p0 * (dp[4 * j] - dv4.x), p1 * (dp[4 * j + 1] - dv4.y),
-                       p2 * (dp[4 * j + 2] - dv4.z), p3 * (dp[4 * j + 3] - dv4.w));
+        if constexpr (DROP) {
+          // this lane's key with queries qb + r .. +3: one word per element
+          const uint32_t qr = uint32_t(qb + r), kk = uint32_t(kj);
+          const float m0 = drop_scale(dm, drop_word(dm, qr, kk), kk);
+          const float m1 = drop_scale(dm, drop_word(dm, qr + 1, kk), kk);
+          const float m2 = drop_scale(dm, drop_word(dm, qr + 2, kk), kk);
+          const float m3 = drop_scale(dm, drop_word(dm, qr + 3, kk), kk);
+          pa[j] = pack4(p0 * m0, p1 * m1, p2 * m2, p3 * m3);
+          dsa[j] = pack4(p0 * (m0 * dp[4 * j] - dv4.x), p1 * (m1 * dp[4 * j + 1] - dv4.y),
+                         p2 * (m2 * dp[4 * j + 2] - dv4.z), p3 * (m3 * dp[4 * j + 3] - dv4.w));
+        } else {
+          pa[j] = pack4(p0, p1, p2, p3);
+          dsa[j] = pack4(p0 * (dp[4 * j] - dv4.x), p1 * (dp[4 * j + 1] - dv4.y),
+                         p2 * (dp[4 * j + 2] - dv4.z), p3 * (dp[4 * j + 3] - dv4.w));
+        }
       }
       s16x4 gb[4], qbq[4];
 #pragma unroll
@@ -424,11 +472,12 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_kv(
 
 // Query-major: dQ for queries q0 .. q0+31.  S^T, dP^T as D[key][q]; K and V
 // stages of 128 keys in LDS (row-major for the A operands, K^T for dQ += dS K).
-template <int DH>
+template <int DH, bool DROP>
 __global__ __launch_bounds__(kBlock) void k_mf_bwd_q(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
     const bf16_t* __restrict__ g, const float* __restrict__ lse, const float* __restrict__ dsum,
-    int32_t n_q, int32_t n_k, int32_t H, float scale, bf16_t* __restrict__ grad_q) {
+    int32_t n_q, int32_t n_k, int32_t H, float scale, DropoutMask dm,
+    bf16_t* __restrict__ grad_q) {
   constexpr int NC = DH / 8;
   __shared__ __align__(16) short ks[kSB][DH + 8];
   __shared__ __align__(16) short vs[kSB][DH + 8];
@@ -440,6 +489,7 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_q(
   const int h = blockIdx.y;
   const int64_t qi = int64_t(blockIdx.x) * kRowsPerBlock + wave * kT + l32;
   const bool q_ok = qi < n_q;
+  if constexpr (DROP) dm = drop_for_head(dm, h);
   s16x4 qbv[NC], gbv[NC];  // Q^T, G^T as B operands
 #pragma unroll
   for (int j = 0; j < NC; ++j) {
@@ -471,6 +521,15 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_q(
       for (int j = 0; j < NC; ++j) {
         st = mfma(lds4(&ks[r0 + l32][8 * j + 4 * half]), qbv[j], st);
         dp = mfma(lds4(&vs[r0 + l32][8 * j + 4 * half]), gbv[j], dp);
+      }
+      if constexpr (DROP) {  // dP o M: keys kb + r0 + 8*(i/4) + 4*half + i%4
+#pragma unroll
+        for (int i = 0; i < 16; i += 2) {
+          const uint32_t key = uint32_t(kb + r0 + 8 * (i / 4) + 4 * half + (i % 4));
+          const uint32_t w = drop_word(dm, uint32_t(qi), key);
+          dp[i] *= drop_scale(dm, w, key);
+          dp[i + 1] *= drop_scale(dm, w, key + 1);
+        }
       }
       float ds[16];
       if (kb + r0 + kT <= n_k) {
@@ -509,14 +568,22 @@ bool mfma_dense_supported(int d) { return d == 8 || d == 16 || d == 24 || d == 3
 
 template <int DH>
 static int mf_fwd(const void* q, const void* k, const void* v, int n_q, int n_k, int H,
-                  float scale, void* out, float* lse, float* part, hipStream_t st) {
+                  float scale, const DropoutMask* dm, void* out, float* out32, float* lse,
+                  float* part, hipStream_t st) {
   const dim3 grid((n_q + kRowsPerBlock - 1) / kRowsPerBlock, H);
   {
     KernelTimer timer_("dense_fwd", st);
-    hipLaunchKernelGGL((k_mf_fwd<DH>), grid, dim3(kBlock), 0, st,
-                       static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
-                       static_cast<const bf16_t*>(v), n_q, n_k, H, scale,
-                       static_cast<bf16_t*>(out), lse);
+    const DropoutMask m = dm ? *dm : DropoutMask{};
+    if (dm)
+      hipLaunchKernelGGL((k_mf_fwd<DH, true>), grid, dim3(kBlock), 0, st,
+                         static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
+                         static_cast<const bf16_t*>(v), n_q, n_k, H, scale, m,
+                         static_cast<bf16_t*>(out), out32, lse);
+    else
+      hipLaunchKernelGGL((k_mf_fwd<DH, false>), grid, dim3(kBlock), 0, st,
+                         static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
+                         static_cast<const bf16_t*>(v), n_q, n_k, H, scale, m,
+                         static_cast<bf16_t*>(out), out32, lse);
     NGT_HIP_CHECK(hipGetLastError());
   }
   if (part && n_k > 0) {
@@ -532,48 +599,64 @@ static int mf_fwd(const void* q, const void* k, const void* v, int n_q, int n_k,
 
 template <int DH>
 static int mf_bwd(const void* q, const void* k, const void* v, const void* g, const float* lse,
-                  const float* dsum, int n_q, int n_k, int H, float scale, void* gq, void* gk,
-                  void* gv, hipStream_t st) {
+                  const float* dsum, int n_q, int n_k, int H, float scale, const DropoutMask* dm,
+                  void* gq, void* gk, void* gv, hipStream_t st) {
+  const DropoutMask m = dm ? *dm : DropoutMask{};
   if (n_k > 0) {
     KernelTimer timer_("dense_bwd_kv", st);
     const dim3 grid((n_k + kRowsPerBlock - 1) / kRowsPerBlock, H);
-    hipLaunchKernelGGL((k_mf_bwd_kv<DH>), grid, dim3(kBlock), 0, st,
-                       static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
-                       static_cast<const bf16_t*>(v), static_cast<const bf16_t*>(g), lse, dsum,
-                       n_q, n_k, H, scale, static_cast<bf16_t*>(gk), static_cast<bf16_t*>(gv));
+    if (dm)
+      hipLaunchKernelGGL((k_mf_bwd_kv<DH, true>), grid, dim3(kBlock), 0, st,
+                         static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
+                         static_cast<const bf16_t*>(v), static_cast<const bf16_t*>(g), lse, dsum,
+                         n_q, n_k, H, scale, m, static_cast<bf16_t*>(gk),
+                         static_cast<bf16_t*>(gv));
+    else
+      hipLaunchKernelGGL((k_mf_bwd_kv<DH, false>), grid, dim3(kBlock), 0, st,
+                         static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
+                         static_cast<const bf16_t*>(v), static_cast<const bf16_t*>(g), lse, dsum,
+                         n_q, n_k, H, scale, m, static_cast<bf16_t*>(gk),
+                         static_cast<bf16_t*>(gv));
     NGT_HIP_CHECK(hipGetLastError());
   }
   if (n_q > 0) {
     KernelTimer timer_("dense_bwd_q", st);
     const dim3 grid((n_q + kRowsPerBlock - 1) / kRowsPerBlock, H);
-    hipLaunchKernelGGL((k_mf_bwd_q<DH>), grid, dim3(kBlock), 0, st,
-                       static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
-                       static_cast<const bf16_t*>(v), static_cast<const bf16_t*>(g), lse, dsum,
-                       n_q, n_k, H, scale, static_cast<bf16_t*>(gq));
+    if (dm)
+      hipLaunchKernelGGL((k_mf_bwd_q<DH, true>), grid, dim3(kBlock), 0, st,
+                         static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
+                         static_cast<const bf16_t*>(v), static_cast<const bf16_t*>(g), lse, dsum,
+                         n_q, n_k, H, scale, m, static_cast<bf16_t*>(gq));
+    else
+      hipLaunchKernelGGL((k_mf_bwd_q<DH, false>), grid, dim3(kBlock), 0, st,
+                         static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
+                         static_cast<const bf16_t*>(v), static_cast<const bf16_t*>(g), lse, dsum,
+                         n_q, n_k, H, scale, m, static_cast<bf16_t*>(gq));
     NGT_HIP_CHECK(hipGetLastError());
   }
   return NGT_OK;
 }
 
 int mfma_dense_fwd(int d, const void* q, const void* k, const void* v, int n_q, int n_k, int H,
-                   float scale, void* out, float* lse, float* part, hipStream_t st) {
+                   float scale, const DropoutMask* dm, void* out, float* out32, float* lse,
+                   float* part, hipStream_t st) {
   switch (d) {
-    case 8: return mf_fwd<8>(q, k, v, n_q, n_k, H, scale, out, lse, part, st);
-    case 16: return mf_fwd<16>(q, k, v, n_q, n_k, H, scale, out, lse, part, st);
-    case 24: return mf_fwd<24>(q, k, v, n_q, n_k, H, scale, out, lse, part, st);
-    case 32: return mf_fwd<32>(q, k, v, n_q, n_k, H, scale, out, lse, part, st);
+    case 8: return mf_fwd<8>(q, k, v, n_q, n_k, H, scale, dm, out, out32, lse, part, st);
+    case 16: return mf_fwd<16>(q, k, v, n_q, n_k, H, scale, dm, out, out32, lse, part, st);
+    case 24: return mf_fwd<24>(q, k, v, n_q, n_k, H, scale, dm, out, out32, lse, part, st);
+    case 32: return mf_fwd<32>(q, k, v, n_q, n_k, H, scale, dm, out, out32, lse, part, st);
     default: return set_error(NGT_ERR_UNSUPPORTED, "mfma dense: head_dim %d", d);
   }
 }
 
 int mfma_dense_bwd(int d, const void* q, const void* k, const void* v, const void* g,
                    const float* lse, const float* dsum, int n_q, int n_k, int H, float scale,
-                   void* gq, void* gk, void* gv, hipStream_t st) {
+                   const DropoutMask* dm, void* gq, void* gk, void* gv, hipStream_t st) {
   switch (d) {
-    case 8: return mf_bwd<8>(q, k, v, g, lse, dsum, n_q, n_k, H, scale, gq, gk, gv, st);
-    case 16: return mf_bwd<16>(q, k, v, g, lse, dsum, n_q, n_k, H, scale, gq, gk, gv, st);
-    case 24: return mf_bwd<24>(q, k, v, g, lse, dsum, n_q, n_k, H, scale, gq, gk, gv, st);
-    case 32: return mf_bwd<32>(q, k, v, g, lse, dsum, n_q, n_k, H, scale, gq, gk, gv, st);
+    case 8: return mf_bwd<8>(q, k, v, g, lse, dsum, n_q, n_k, H, scale, dm, gq, gk, gv, st);
+    case 16: return mf_bwd<16>(q, k, v, g, lse, dsum, n_q, n_k, H, scale, dm, gq, gk, gv, st);
+    case 24: return mf_bwd<24>(q, k, v, g, lse, dsum, n_q, n_k, H, scale, dm, gq, gk, gv, st);
+    case 32: return mf_bwd<32>(q, k, v, g, lse, dsum, n_q, n_k, H, scale, dm, gq, gk, gv, st);
     default: return set_error(NGT_ERR_UNSUPPORTED, "mfma dense: head_dim %d", d);
   }
 }

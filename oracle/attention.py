@@ -12,11 +12,20 @@ restated as its published algorithm: broadcast the index over ``src`` and call
 Also holds two independent formulations used to pin the restatement:
 ``sparse_bruteforce_fp64`` (dense masked matrix form, float64) and
 ``sparse_backward_closed_form`` (hand-derived gradients).
+
+Dropout of the dense path (the reference's ``self.att_dropout(x)`` after the
+softmax, and ``F.dropout(..., training=True)`` in the flash branch's
+naive_attention, graphormer_dist_node_level.py:100-105) draws torch's Philox
+stream, which no other implementation reproduces; the product replaces it by
+a hash of (seed, head, query, key).  ``dropout_multiplier`` restates that
+hash so a test can hand the same mask to this restatement; the mask's own
+statistics (keep rate, independence) are what ties it to the reference.
 """
 from __future__ import annotations
 
 import math
 
+import numpy as np
 import torch
 
 CLAMP_LO = -5.0
@@ -68,11 +77,58 @@ def sparse_attention_bias(q, k, v, edge_index, num_heads, attn_bias=None, scale=
     return x, node_scores
 
 
-def full_attention(q, k, v, scale=None, attn_bias=None, mask=None, pruning_mask=None):
-    """CoreAttention.full_attention (graphormer_dist_node_level.py:42-65), dropout p = 0.
+def _mix32(x):
+    """lowbias32 (C. Wellons, hash-prospector) on a uint32 array."""
+    x = x ^ (x >> np.uint32(16))
+    x = x * np.uint32(0x7FEB352D)
+    x = x ^ (x >> np.uint32(15))
+    x = x * np.uint32(0x846CA68B)
+    x = x ^ (x >> np.uint32(16))
+    return x
+
+
+def dropout_params(p):
+    """(threshold, scale) of the product's mask for probability p (passed to
+    the library as fp32): keep iff the 16-bit draw >= round(p * 65536), kept
+    values scaled by fp32(1 / (1 - p)); p = 1 keeps all with scale 0."""
+    p32 = float(np.float32(p))
+    if p32 >= 1.0:
+        return 0, np.float32(0.0)
+    return int(np.rint(p32 * 65536.0)), np.float32(1.0 / (1.0 - p32))
+
+
+def dropout_multiplier(seed, H, n_q, n_k, p):
+    """[H, n_q, n_k] float32: the multiplier (0 or 1/(1-p)) that the product's
+    dense kernels apply to P[h, i, j] for dropout probability p and a 64-bit
+    seed.  One 32-bit word per key pair of a (head, query) row:
+      word = mix32((i * ceil(n_k/2) + j // 2) ^ head_key),
+      head_key = mix32(lo32(seed) ^ mix32(hi32(seed) + 0x9e3779b9 * (h + 1))),
+    16-bit half j % 2 of the word compared with the threshold."""
+    thr, scale = dropout_params(p)
+    with np.errstate(over="ignore"):
+        s_lo = np.uint32(seed & 0xFFFFFFFF)
+        s_hi = np.uint32((seed >> 32) & 0xFFFFFFFF)
+        i = np.arange(n_q, dtype=np.uint32)[:, None]
+        j = np.arange(n_k, dtype=np.uint32)[None, :]
+        n_kp = np.uint32((n_k + 1) // 2)
+        out = np.empty((H, n_q, n_k), np.float32)
+        heads = np.arange(1, H + 1, dtype=np.uint32)
+        head_keys = _mix32(s_lo ^ _mix32(s_hi + np.uint32(0x9E3779B9) * heads))
+        for h in range(H):
+            w = _mix32((i * n_kp + (j >> np.uint32(1))) ^ head_keys[h])
+            half = np.where((j & np.uint32(1)) != 0, w >> np.uint32(16), w & np.uint32(0xFFFF))
+            out[h] = np.where(half >= thr, scale, np.float32(0.0))
+    return out
+
+
+def full_attention(q, k, v, scale=None, attn_bias=None, mask=None, pruning_mask=None,
+                   dropout_mult=None):
+    """CoreAttention.full_attention (graphormer_dist_node_level.py:42-65).
 
     q: [1, N_q, H, d]; k, v: [1, N_k, H, d].  Returns (x [1, N_q, H, d],
     node_scores [N_k]).  Note the reference MULTIPLIES q by sqrt(d).
+    ``dropout_mult`` ([H, N_q, N_k], from dropout_multiplier) stands for
+    self.att_dropout in training mode; None is eval mode / p = 0.
     """
     if scale is None:
         scale = math.sqrt(q.shape[-1])
@@ -91,10 +147,25 @@ def full_attention(q, k, v, scale=None, attn_bias=None, mask=None, pruning_mask=
         mask = mask.repeat(1, x.shape[1], 1, 1)
         x = x.masked_fill(mask, -1e9)
     x = torch.softmax(x, dim=3)
+    if dropout_mult is not None:
+        x = x * torch.as_tensor(dropout_mult, dtype=x.dtype).unsqueeze(0)
     x = x.matmul(v)
     x = x.transpose(1, 2).contiguous()
     node_scores = torch.abs(score).mean(dim=1).squeeze(0).sum(dim=0)
     return x, node_scores
+
+
+def naive_attention(q, k, v, dropout_mult=None):
+    """CoreAttention.naive_attention (graphormer_dist_node_level.py:100-105),
+    the "flash" branch, on [b, N, H, d] inputs: softmax(q k^T / sqrt(d)),
+    dropout (always applied there), times v.  Returns x [b, N_q, H, d]."""
+    d = q.shape[-1]
+    qt, kt, vt = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+    s = torch.matmul(qt, kt.transpose(-2, -1)) / (d ** 0.5)
+    p = torch.softmax(s, dim=-1)
+    if dropout_mult is not None:
+        p = p * torch.as_tensor(dropout_mult, dtype=p.dtype).unsqueeze(0)
+    return torch.matmul(p, vt).transpose(1, 2).contiguous()
 
 
 # --------------------------------------------------------------- pinning forms
@@ -150,8 +221,9 @@ def sparse_backward_closed_form(q, k, v, edge_index, grad_x, scale=None, lo=CLAM
     return dq, dk, dv
 
 
-def full_attention_fp64(q, k, v, scale=None):
-    """softmax((q*scale) k^T) v per head in float64; also returns sum_i mean_h |S|."""
+def full_attention_fp64(q, k, v, scale=None, dropout_mult=None):
+    """softmax((q*scale) k^T) [o dropout_mult] v per head in float64; also
+    returns sum_i mean_h |S|."""
     q = q.reshape(q.shape[-3], q.shape[-2], q.shape[-1]).double()
     k = k.reshape(k.shape[-3], k.shape[-2], k.shape[-1]).double()
     v = v.reshape(v.shape[-3], v.shape[-2], v.shape[-1]).double()
@@ -159,6 +231,8 @@ def full_attention_fp64(q, k, v, scale=None):
         scale = math.sqrt(q.shape[-1])
     s = torch.einsum("ihc,jhc->hij", q * scale, k)
     p = torch.softmax(s, dim=-1)
+    if dropout_mult is not None:
+        p = p * torch.as_tensor(dropout_mult, dtype=torch.float64)
     x = torch.einsum("hij,jhc->ihc", p, v)
     ns = s.abs().mean(0).sum(0)
     return x, ns
@@ -196,12 +270,16 @@ def sparse_fwd_bwd(q, k, v, edge_index, grad_x, num_heads, dtype=torch.float32):
     }
 
 
-def full_fwd_bwd(q, k, v, grad_x, dtype=torch.float32):
-    """full_attention forward + autograd backward on CPU; q [N_q,H,d], k/v [N_k,H,d]."""
+def full_fwd_bwd(q, k, v, grad_x, dtype=torch.float32, dropout_mult=None, flash=False):
+    """full_attention (or, flash=True, naive_attention) forward + autograd
+    backward on CPU; q [N_q,H,d], k/v [N_k,H,d]."""
     qf = q.to(dtype).clone().unsqueeze(0).requires_grad_(True)
     kf = k.to(dtype).clone().unsqueeze(0).requires_grad_(True)
     vf = v.to(dtype).clone().unsqueeze(0).requires_grad_(True)
-    x, ns = full_attention(qf, kf, vf)
+    if flash:
+        x, ns = naive_attention(qf, kf, vf, dropout_mult=dropout_mult), torch.empty(0)
+    else:
+        x, ns = full_attention(qf, kf, vf, dropout_mult=dropout_mult)
     x.backward(grad_x.to(dtype).unsqueeze(0))
     return {
         "x": x.detach()[0],

@@ -61,8 +61,18 @@ def test_argument_errors_are_reported_without_touching_the_gpu():
     rc = lib.ngt_sparse_fwd(0, None, None, None, C.byref(s), 8, 12, 1.0, -5.0, 5.0, 1e-6, None,
                             None, None, 0, None, 0, None)
     assert rc == 2 and b"head_dim" in lib.ngt_last_error()
-    rc = lib.ngt_dense_fwd(7, None, None, None, 1, 1, 1, 8, 1.0, None, None, None, None, 0, None)
+    rc = lib.ngt_dense_fwd(7, None, None, None, 1, 1, 1, 8, 1.0, 0.0, 0, None, None, None, None,
+                           None, 0, None)
     assert rc == 1
+    rc = lib.ngt_dense_fwd(0, None, None, None, 0, 0, 1, 8, 1.0, 1.5, 0, None, None, None, None,
+                           None, 0, None)
+    assert rc == 1 and b"dropout_p" in lib.ngt_last_error()
+    rc = lib.ngt_dense_fwd(0, None, None, None, 0, 0, 1, 8, 1.0, float("nan"), 0, None, None, None,
+                           None, None, 0, None)
+    assert rc == 1 and b"dropout_p" in lib.ngt_last_error()
+    rc = lib.ngt_dense_fwd(0, None, None, None, 65536, 131074, 1, 8, 1.0, 0.5, 0, None, None, None,
+                           None, None, 0, None)
+    assert rc == 2 and b"2^32" in lib.ngt_last_error()
     with pytest.raises(_lib.NGTError):
         _lib.check(1)
 

@@ -69,9 +69,6 @@ def test_dense_module_drop_in():
     ref = OA.full_fwd_bwd(q, k, v, go)
     assert_close(x[0].view(n, H, d).cpu(), ref["x"], torch.float32, "x")
     assert_close(score.cpu(), ref["node_scores"], torch.float32, "score")
-    mod.att_dropout.p = 0.5
-    with pytest.raises(NotImplementedError):
-        mod(q[None].cuda(), k[None].cuda(), v[None].cuda(), None, None, "full")
 
 
 def test_dense_full_size_sampled_rows_and_invariants():
@@ -105,3 +102,109 @@ def test_dense_full_size_sampled_rows_and_invariants():
     rhs = (res["dk"].double() * kd).sum().item()
     assert abs(lhs - rhs) / max(abs(lhs), abs(rhs)) < 10 * TOL[cfg.dtype]
     assert relerr(res["dv"].double().sum(0), gd.sum(0)) < 10 * TOL[cfg.dtype]
+
+
+def _run_drop(q, k, v, go, p, seed, flash=False):
+    qd, kd, vd = (t.cuda().requires_grad_(True) for t in (q, k, v))
+    d = q.shape[-1]
+    x, ns = dense_attention(qd, kd, vd, scale=1.0 / math.sqrt(d) if flash else None,
+                            node_scores=not flash, dropout_p=p, seed=seed)
+    x.backward(go.cuda())
+    torch.cuda.synchronize()
+    return {"x": x.detach().cpu(), "node_scores": ns.cpu(), "dq": qd.grad.cpu(),
+            "dk": kd.grad.cpu(), "dv": vd.grad.cpu()}
+
+
+@pytest.mark.parametrize("n_q,n_k,H,d,dtype,p", [
+    (70, 71, 2, 8, torch.float32, 0.5), (64, 130, 2, 16, torch.float32, 0.3),
+    (40, 40, 2, 64, torch.float32, 0.5), (100, 99, 4, 8, torch.bfloat16, 0.5),
+    (96, 150, 2, 16, torch.bfloat16, 0.2), (60, 61, 2, 24, torch.bfloat16, 0.5),
+    (70, 45, 3, 32, torch.bfloat16, 0.7), (33, 47, 2, 64, torch.bfloat16, 0.5),
+    (50, 50, 2, 8, torch.bfloat16, 1.0)])
+def test_dense_dropout_parity(n_q, n_k, H, d, dtype, p):
+    """Training-mode dropout on P: the kernels' mask equals the oracle's
+    (same seed), and out / dQ / dK / dV match the restatement with that mask."""
+    _say(f"case dense dropout n_q={n_q} n_k={n_k} H={H} d={d} {dtype} p={p}")
+    seed = 0x1234_5678_9ABC + n_q
+    q, k, v, go = _qkv(n_q, n_k, H, d, dtype, seed=n_q + 3 * d)
+    res = _run_drop(q, k, v, go, p, seed)
+    mult = OA.dropout_multiplier(seed, H, n_q, n_k, p)
+    ref = OA.full_fwd_bwd(q.float(), k.float(), v.float(), go.float(), dropout_mult=mult)
+    ref64 = OA.full_fwd_bwd(q.double(), k.double(), v.double(), go.double(),
+                            dtype=torch.float64, dropout_mult=mult)
+    for name in ("x", "node_scores", "dq", "dk", "dv"):
+        assert_parity(res[name].float(), ref[name], ref64[name], dtype, f"p={p} {name}")
+    again = _run_drop(q, k, v, go, p, seed)
+    for name in ("x", "dq", "dk", "dv"):
+        assert torch.equal(again[name], res[name]), f"{name} not reproducible"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_dense_dropout_mask_from_output(dtype):
+    """The kept set read off the output itself: with V = identity rows
+    (n_k = d) and P replaced by exact one-hot-free values, out[i, h, j] =
+    P[h,i,j] * mult[h,i,j], so the zero pattern of out is the mask."""
+    _say(f"case dense dropout mask {dtype}")
+    H, d, n_q = 2, 16, 64
+    n_k = d
+    g = torch.Generator().manual_seed(11)
+    q = torch.randn(n_q, H, d, generator=g).to(dtype) * 0.1
+    k = torch.randn(n_k, H, d, generator=g).to(dtype) * 0.1
+    v = torch.eye(d).unsqueeze(1).repeat(1, H, 1).to(dtype)  # v[j, h] = e_j
+    seed = 987654321
+    x, _ = dense_attention(q.cuda(), k.cuda(), v.cuda(), dropout_p=0.5, seed=seed)
+    mult = OA.dropout_multiplier(seed, H, n_q, n_k, 0.5)
+    kept = x.float().cpu().permute(1, 0, 2).numpy() != 0  # [H, n_q, n_k]
+    assert np.array_equal(kept, mult > 0)
+
+
+def test_dense_module_dropout_and_flash():
+    """CoreAttention in training mode draws a seed from torch's generator
+    (torch.manual_seed makes it repeatable), eval mode has no dropout, and the
+    flash branch (1/sqrt(d) scale, dropout always on) matches naive_attention."""
+    _say("case dense module dropout/flash")
+    H, d, n = 2, 8, 50
+    mod = CoreAttention(H * d, 0.5, H).cuda()
+    q, k, v, go = _qkv(n, n, H, d, torch.float32, seed=5)
+    args = (q[None].cuda(), k[None].cuda(), v[None].cuda(), None, None, "full")
+    mod.eval()
+    x_eval, _ = mod(*args)
+    ref = OA.full_fwd_bwd(q, k, v, go)
+    assert_close(x_eval[0].view(n, H, d).cpu(), ref["x"], torch.float32, "eval x")
+    mod.train()
+    torch.manual_seed(77)
+    x1, s1 = mod(*args)
+    torch.manual_seed(77)
+    seed = int(torch.randint(0, 2**62, (1,), dtype=torch.int64).item())
+    torch.manual_seed(77)
+    x2, _ = mod(*args)
+    assert torch.equal(x1, x2)
+    mult = OA.dropout_multiplier(seed, H, n, n, 0.5)
+    ref = OA.full_fwd_bwd(q, k, v, go, dropout_mult=mult)
+    assert_close(x1[0].view(n, H, d).cpu(), ref["x"], torch.float32, "train x")
+    assert_close(s1.cpu(), ref["node_scores"], torch.float32, "train score")
+    # flash branch
+    torch.manual_seed(78)
+    xf, sf = mod(q[None].cuda(), k[None].cuda(), v[None].cuda(), None, None, "flash")
+    assert sf is None and xf.dtype == torch.float32 and xf.shape == (1, n, H * d)
+    torch.manual_seed(78)
+    seed = int(torch.randint(0, 2**62, (1,), dtype=torch.int64).item())
+    mult = OA.dropout_multiplier(seed, H, n, n, 0.5)
+    ref = OA.full_fwd_bwd(q, k, v, go, dropout_mult=mult, flash=True)
+    assert_close(xf[0].view(n, H, d).cpu(), ref["x"], torch.float32, "flash x")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_dense_flash_backward(dtype):
+    _say(f"case dense flash backward {dtype}")
+    H, d, n_q, n_k = 2, 16, 45, 60
+    q, k, v, go = _qkv(n_q, n_k, H, d, dtype, seed=9)
+    seed = 555
+    res = _run_drop(q, k, v, go, 0.5, seed, flash=True)
+    mult = OA.dropout_multiplier(seed, H, n_q, n_k, 0.5)
+    ref = OA.full_fwd_bwd(q.float(), k.float(), v.float(), go.float(), dropout_mult=mult,
+                          flash=True)
+    ref64 = OA.full_fwd_bwd(q.double(), k.double(), v.double(), go.double(),
+                            dtype=torch.float64, dropout_mult=mult, flash=True)
+    for name in ("x", "dq", "dk", "dv"):
+        assert_parity(res[name].float(), ref[name], ref64[name], dtype, f"flash {name}")
