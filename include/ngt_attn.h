@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define NGT_ABI_VERSION 2
+#define NGT_ABI_VERSION 3
 
 #define NGT_F32 0
 #define NGT_BF16 1

@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libngt_attn.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 NGT_F32 = 0
 NGT_BF16 = 1
