@@ -456,7 +456,7 @@ def model_step_bench(args, cfg, layers: int, dev) -> dict:
     torch.cuda.synchronize()
     summ = _lib.timing_summary()
     _lib.timing_enable(False)
-    attn_ms = sum(v[1] for v in summ.values()) / args.steps
+    attn_ms = sum(v[1] for n, v in summ.items() if n.startswith(("sparse_", "dense_"))) / args.steps
     _log(f"[bench] window step {ms:.2f} ms (median of {args.steps}), attention kernels "
          f"{attn_ms:.2f} ms/step, loss {losses[0]:.4f} -> {losses[-1]:.4f}")
     return {

@@ -328,6 +328,17 @@ int ngt_subgraph_csr(const int64_t* rowptr, const int64_t* col, int64_t n_col, i
 int ngt_timing_enable(int on);
 int ngt_timing_summary(char* buf, size_t len);
 
+/*
+ * Column sums of a bf16 matrix in fp32: out[j] = sum_k dy[k][j], dy
+ * [n_rows, n_cols] row-major, 16-byte aligned, n_cols a multiple of 8; summed
+ * in a fixed order.  The bias gradient of the encoder's linear layers under
+ * bf16 autocast (the autograd of nn.Linear's bias in MultiHeadAttention and
+ * the FFN, NeutronGT/models/graphormer_dist_node_level.py:130-206).
+ */
+int ngt_colsum_workspace_bytes(int64_t n_rows, int32_t n_cols, size_t* bytes);
+int ngt_colsum_bf16(const void* dy, int64_t n_rows, int32_t n_cols, float* out, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

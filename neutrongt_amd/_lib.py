@@ -95,6 +95,8 @@ SIGNATURES = {
                       _vp, _vp, _vp, _sz, _vp],
     "ngt_dense_bwd": [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _f32,
                       _u64, _vp, _vp, _vp, _vp, _sz, _vp],
+    "ngt_colsum_workspace_bytes": [_i64, _i32, _psz],
+    "ngt_colsum_bf16": [_vp, _i64, _i32, _vp, _vp, _sz, _vp],
     "ngt_related_workspace_bytes": [_i32, _i32, _psz],
     "ngt_merge_related_nodes": [_vp, _vp, _vp, _i32, _vp, _i32, _i32, _vp, _vp, _vp, _sz, _vp],
     "ngt_gather_rows": [_vp, _i64, _vp, _i64, _i64, _vp, _vp, _vp],

@@ -16,9 +16,11 @@ the shipped setting):
 Sub-module and parameter names are the reference's, so a reference
 ``state_dict`` loads with ``strict=False`` (the unused structural-encoding
 embeddings are the only extra keys).  Projections, LayerNorm, activations and
-the FFN are plain library GEMMs and elementwise ops (hipBLASLt through torch);
-run them under ``torch.autocast("cuda", dtype=torch.bfloat16)`` for the bf16
-window step.  The attention core is ``CoreAttention`` (HIP kernels only).
+the FFN are library GEMMs and elementwise ops (hipBLASLt through torch) except
+for the linear layers' weight and bias gradients, which ``WgradLinear`` runs
+on the library's split-K kernel; run them under
+``torch.autocast("cuda", dtype=torch.bfloat16)`` for the bf16 window step.
+The attention core is ``CoreAttention`` (HIP kernels only).
 
 Related keys.  A window's queries may also attend to out-of-window related
 nodes whose K/V come from a cache (one ``(k, v)`` pair of ``[R, H, d]`` tensors
@@ -39,6 +41,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .attention import CoreAttention
+from .linear import WgradLinear
 
 
 def init_params(module: nn.Module, n_layers: int) -> None:
@@ -57,9 +60,9 @@ class FeedForwardNetwork(nn.Module):
 
     def __init__(self, hidden_size: int, ffn_size: int, dropout_rate: float = 0.0):
         super().__init__()
-        self.layer1 = nn.Linear(hidden_size, ffn_size)
+        self.layer1 = WgradLinear(hidden_size, ffn_size)
         self.gelu = nn.GELU()
-        self.layer2 = nn.Linear(ffn_size, hidden_size)
+        self.layer2 = WgradLinear(ffn_size, hidden_size)
 
     def forward(self, x):
         return self.layer2(self.gelu(self.layer1(x)))
@@ -80,9 +83,9 @@ class _Attention(nn.Module):
             raise ValueError(f"hidden size {hidden_size} is not a multiple of {num_heads} heads")
         self.num_heads = num_heads
         self.att_size = hidden_size // num_heads
-        self.linear_q = nn.Linear(hidden_size, num_heads * self.att_size)
-        self.linear_k = nn.Linear(hidden_size, num_heads * self.att_size)
-        self.linear_v = nn.Linear(hidden_size, num_heads * self.att_size)
+        self.linear_q = WgradLinear(hidden_size, num_heads * self.att_size)
+        self.linear_k = WgradLinear(hidden_size, num_heads * self.att_size)
+        self.linear_v = WgradLinear(hidden_size, num_heads * self.att_size)
         self.local_attn = CoreAttention(hidden_size, attention_dropout_rate, num_heads)
 
     def attend(self, x, edge_index, attn_type, kv_cache):
@@ -109,7 +112,7 @@ class MultiHeadAttention(_Attention):
 
     def __init__(self, hidden_size: int, attention_dropout_rate: float, num_heads: int):
         super().__init__(hidden_size, attention_dropout_rate, num_heads)
-        self.output_layer = nn.Linear(num_heads * self.att_size, hidden_size)
+        self.output_layer = WgradLinear(num_heads * self.att_size, hidden_size)
 
     def forward(self, x, edge_index=None, attn_type="sparse", kv_cache=None):
         y, score, kv = self.attend(x, edge_index, attn_type, kv_cache)
@@ -165,10 +168,10 @@ class GTEncoderLayer(nn.Module):
         self.self_attention_norm = nn.LayerNorm(hidden_size)  # declared, unused (as in the reference)
         self.self_attention = GTMultiHeadAttention(hidden_size, attention_dropout_rate, num_heads)
         self.self_attention_dropout = nn.Dropout(dropout_rate)
-        self.O = nn.Linear(hidden_size, hidden_size)
+        self.O = WgradLinear(hidden_size, hidden_size)
         self.layer_norm1 = nn.LayerNorm(hidden_size)
-        self.FFN_layer1 = nn.Linear(hidden_size, hidden_size * 2)
-        self.FFN_layer2 = nn.Linear(hidden_size * 2, hidden_size)
+        self.FFN_layer1 = WgradLinear(hidden_size, hidden_size * 2)
+        self.FFN_layer2 = WgradLinear(hidden_size * 2, hidden_size)
         self.layer_norm2 = nn.LayerNorm(hidden_size)
 
     def forward(self, x, edge_index=None, attn_type="sparse", kv_cache=None):
@@ -188,7 +191,7 @@ class MLPReadout(nn.Module):
         super().__init__()
         dims = [input_dim // 2 ** i for i in range(L + 1)]
         self.FC_layers = nn.ModuleList(
-            [nn.Linear(dims[i], dims[i + 1]) for i in range(L)] + [nn.Linear(dims[L], output_dim)])
+            [WgradLinear(dims[i], dims[i + 1]) for i in range(L)] + [WgradLinear(dims[L], output_dim)])
         self.L = L
 
     def forward(self, x):
@@ -227,13 +230,13 @@ class WindowGraphormer(_WindowModel):
         ffn_dim = ffn_dim or hidden_dim
         self.num_heads = num_heads
         self.n_layers = n_layers
-        self.node_encoder = nn.Linear(input_dim, hidden_dim)
+        self.node_encoder = WgradLinear(input_dim, hidden_dim)
         self.input_dropout = nn.Dropout(input_dropout_rate)
         self.layers = nn.ModuleList([
             EncoderLayer(hidden_dim, ffn_dim, dropout_rate, attention_dropout_rate, num_heads)
             for _ in range(n_layers)])
         self.final_ln = nn.LayerNorm(hidden_dim)
-        self.downstream_out_proj = nn.Linear(hidden_dim, output_dim)
+        self.downstream_out_proj = WgradLinear(hidden_dim, output_dim)
         self.apply(lambda m: init_params(m, n_layers))
 
     def readout(self, h):
@@ -250,13 +253,13 @@ class WindowGT(_WindowModel):
         super().__init__()
         self.num_heads = num_heads
         self.n_layers = n_layers
-        self.node_encoder = nn.Linear(input_dim, hidden_dim)
+        self.node_encoder = WgradLinear(input_dim, hidden_dim)
         self.input_dropout = nn.Dropout(input_dropout_rate)
         self.layers = nn.ModuleList([
             GTEncoderLayer(hidden_dim, ffn_dim or hidden_dim, dropout_rate,
                            attention_dropout_rate, num_heads) for _ in range(n_layers)])
         self.MLP_layer = MLPReadout(hidden_dim, output_dim)
-        self.downstream_out_proj = nn.Linear(hidden_dim, output_dim)  # declared, unused
+        self.downstream_out_proj = WgradLinear(hidden_dim, output_dim)  # declared, unused
         self.apply(lambda m: init_params(m, n_layers))
 
     def readout(self, h):

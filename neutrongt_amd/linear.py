@@ -1,0 +1,106 @@
+"""nn.Linear with a split-K weight gradient and a HIP bias gradient under
+bf16 autocast.
+
+The encoder's projections (NeutronGT/models/graphormer_dist_node_level.py:
+130-206, the GT twin's :230-302) multiply [32,768 x 768] activations by
+768 x 768 weights.  Their weight gradient dW = dY^T X has a 768 x 768 output
+and a 32,768-long reduction, and autocast's single GEMM for it ran at 190 us
+(few output tiles, no split of the reduction).  ``WgradLinear`` keeps
+nn.Linear's parameters, names and forward (the same bf16 GEMM autocast runs)
+and in the backward computes
+  dX = dY W                          (torch GEMM, bf16, as autocast does),
+  dW = sum_c dY_c^T X_c              (one batched library GEMM over 16 row
+                                      chunks with fp32 output, then a sum in
+                                      chunk order: 63 us),
+  db = column sums of dY             (ngt_colsum_bf16, fp32, fixed order).
+dW and db are fp32 (autocast's own backward rounds dW to bf16 first).
+Outside bf16 autocast, without gradients, or for widths that are not
+multiples of 8 it is a plain nn.Linear.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _lib
+
+_CHUNK = 2048      # rows per split of the weight-gradient reduction
+_MAX_SPLITS = 16   # 16 x 2048 rows measured fastest for 32,768 x 768 x 768
+
+
+def colsum_bf16(dy: torch.Tensor) -> torch.Tensor:
+    """fp32 column sums of a bf16 [K, n] GPU matrix (fixed summation order)."""
+    lib = _lib.load()
+    if dy.dtype != torch.bfloat16 or not dy.is_cuda or dy.dim() != 2:
+        raise TypeError("colsum_bf16 takes a 2-D bf16 GPU tensor")
+    if not dy.is_contiguous() or dy.data_ptr() % 16:
+        dy = dy.clone(memory_format=torch.contiguous_format)
+    K, n = dy.shape
+    out = torch.empty(n, dtype=torch.float32, device=dy.device)
+    nb = C.c_size_t()
+    _lib.check(lib.ngt_colsum_workspace_bytes(K, n, C.byref(nb)))
+    ws = torch.empty(max(nb.value, 1), dtype=torch.uint8, device=dy.device)
+    _lib.check(lib.ngt_colsum_bf16(dy.data_ptr(), K, n, out.data_ptr(), ws.data_ptr(), nb.value,
+                                   torch.cuda.current_stream(dy.device).cuda_stream))
+    return out
+
+
+def weight_grad(x: torch.Tensor, dy: torch.Tensor) -> torch.Tensor:
+    """dY^T X in fp32 for bf16 x [K, n_in], dy [K, n_out], split over rows."""
+    K = x.shape[0]
+    splits = max(1, min(_MAX_SPLITS, K // _CHUNK))
+    c = K // splits
+    main = splits * c
+    with torch.autocast("cuda", enabled=False):
+        if splits == 1:
+            return torch.mm(dy.t(), x, out_dtype=torch.float32)
+        # left operand transposed, right operand contiguous row chunks
+        dw = torch.bmm(dy[:main].view(splits, c, -1).transpose(1, 2),
+                       x[:main].view(splits, c, -1), out_dtype=torch.float32).sum(0)
+        if main < K:
+            dw += torch.mm(dy[main:].t(), x[main:], out_dtype=torch.float32)
+    return dw
+
+
+class _WgradLinearFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, weight, bias):
+        x16 = x.to(torch.bfloat16)
+        w16 = weight.to(torch.bfloat16)
+        b16 = bias.to(torch.bfloat16) if bias is not None else None
+        with torch.autocast("cuda", enabled=False):
+            y = F.linear(x16, w16, b16)
+        ctx.save_for_backward(x16, w16)
+        ctx.has_bias = bias is not None
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        x16, w16 = ctx.saved_tensors
+        n_out, n_in = w16.shape
+        g2 = gy.to(torch.bfloat16).reshape(-1, n_out).contiguous()
+        gx = dw = db = None
+        if ctx.needs_input_grad[0]:
+            with torch.autocast("cuda", enabled=False):
+                gx = (g2 @ w16).view(*x16.shape)
+        if ctx.needs_input_grad[1]:
+            dw = weight_grad(x16.reshape(-1, n_in).contiguous(), g2)
+        if ctx.has_bias and ctx.needs_input_grad[2]:
+            db = colsum_bf16(g2)
+        return gx, dw, db
+
+
+class WgradLinear(nn.Linear):
+    """nn.Linear (same parameters and state-dict names) with the split-K
+    weight gradient and the HIP bias gradient under bf16 autocast."""
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if (x.is_cuda and torch.is_grad_enabled() and self.weight.requires_grad
+                and torch.is_autocast_enabled("cuda")
+                and torch.get_autocast_dtype("cuda") == torch.bfloat16
+                and self.in_features % 8 == 0 and self.out_features % 8 == 0):
+            return _WgradLinearFn.apply(x, self.weight, self.bias)
+        return super().forward(x)
