@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define NGT_ABI_VERSION 3
+#define NGT_ABI_VERSION 4
 
 #define NGT_F32 0
 #define NGT_BF16 1
@@ -170,6 +170,27 @@ int ngt_sparse_bwd(int dtype, const void* q, const void* k, const void* v, const
                    int32_t n_heads, int32_t head_dim, float scale, float clamp_lo, float clamp_hi,
                    void* grad_q, void* grad_k, void* grad_v, void* workspace,
                    size_t workspace_bytes, void* stream);
+
+/*
+ * ngt_sparse_fwd / ngt_sparse_bwd with the key rows in two buffers: rows
+ * j < n_k_main come from k/v, rows j >= n_k_main (up to csr->n_k) from
+ * k_ext/v_ext row j - n_k_main.  Lets a caller append the detached K/V cache
+ * of related keys (the reference concatenates it,
+ * NeutronGT/models/graphormer_dist_node_level.py:162-168) without copying.
+ * grad_k/grad_v are [n_k_main, H, d]: rows of k_ext/v_ext get no gradient.
+ */
+int ngt_sparse_fwd_ext(int dtype, const void* q, const void* k, const void* v, const void* k_ext,
+                       const void* v_ext, int32_t n_k_main, const ngt_window_csr* csr,
+                       int32_t n_heads, int32_t head_dim, float scale, float clamp_lo,
+                       float clamp_hi, float eps, void* out, float* rinv, float* node_score,
+                       int32_t node_score_len, void* workspace, size_t workspace_bytes,
+                       void* stream);
+int ngt_sparse_bwd_ext(int dtype, const void* q, const void* k, const void* v, const void* k_ext,
+                       const void* v_ext, int32_t n_k_main, const void* out,
+                       const void* grad_out, const float* rinv, const ngt_window_csr* csr,
+                       int32_t n_heads, int32_t head_dim, float scale, float clamp_lo,
+                       float clamp_hi, void* grad_q, void* grad_k, void* grad_v, void* workspace,
+                       size_t workspace_bytes, void* stream);
 
 /*
  * Dense full-window attention (all pairs, no mask/bias).

@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libngt_attn.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 NGT_F32 = 0
 NGT_BF16 = 1
@@ -90,6 +90,10 @@ SIGNATURES = {
                        _vp, _i32, _vp, _sz, _vp],
     "ngt_sparse_bwd": [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _pcsr, _i32, _i32, _f32, _f32, _f32,
                        _vp, _vp, _vp, _vp, _sz, _vp],
+    "ngt_sparse_fwd_ext": [_i32, _vp, _vp, _vp, _vp, _vp, _i32, _pcsr, _i32, _i32, _f32, _f32,
+                           _f32, _f32, _vp, _vp, _vp, _i32, _vp, _sz, _vp],
+    "ngt_sparse_bwd_ext": [_i32, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _pcsr, _i32, _i32,
+                           _f32, _f32, _f32, _vp, _vp, _vp, _vp, _sz, _vp],
     "ngt_dense_workspace_bytes": [_i32, _i32, _i32, _i32, _psz, _psz],
     "ngt_dense_fwd": [_i32, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _f32, _u64, _vp, _vp,
                       _vp, _vp, _vp, _sz, _vp],

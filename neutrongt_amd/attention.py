@@ -57,11 +57,14 @@ class SparseAttentionFunction(torch.autograd.Function):
 
     q [N_q, H, d], k/v [N_k, H, d] (same dtype, fp32 or bf16).  node_score is
     returned without gradient (the reference's caller detaches it,
-    graphormer_dist_node_level.py:345).
+    graphormer_dist_node_level.py:345).  Optional k_ext/v_ext [R, H, d] are
+    further key rows N_k .. N_k+R-1 read from their own buffers (a detached
+    cache of related keys, so the caller need not concatenate); they receive
+    no gradient.
     """
 
     @staticmethod
-    def forward(ctx, q, k, v, adj, scale, lo, hi, eps):
+    def forward(ctx, q, k, v, adj, scale, lo, hi, eps, k_ext=None, v_ext=None):
         lib = _lib.load()
         n_q, H, d = q.shape
         dev = q.device
@@ -71,18 +74,26 @@ class SparseAttentionFunction(torch.autograd.Function):
         fb, bb = C.c_size_t(), C.c_size_t()
         _lib.check(lib.ngt_sparse_workspace_bytes(adj.ptr(), H, d, C.byref(fb), C.byref(bb)))
         ws = _workspace(fb.value, dev)
-        _lib.check(lib.ngt_sparse_fwd(_dtype_code(q), q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                                      adj.ptr(), H, d, scale, lo, hi, eps, out.data_ptr(),
-                                      rinv.data_ptr(), ns.data_ptr() if ns.numel() else None,
-                                      int(ns.numel()), ws.data_ptr(), fb.value, _stream(dev)))
-        ctx.save_for_backward(q, k, v, out, rinv)
+        ext = k_ext is not None
+        _lib.check(lib.ngt_sparse_fwd_ext(
+            _dtype_code(q), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+            k_ext.data_ptr() if ext else None, v_ext.data_ptr() if ext else None, k.shape[0],
+            adj.ptr(), H, d, scale, lo, hi, eps, out.data_ptr(), rinv.data_ptr(),
+            ns.data_ptr() if ns.numel() else None, int(ns.numel()), ws.data_ptr(), fb.value,
+            _stream(dev)))
+        if ext:
+            ctx.save_for_backward(q, k, v, out, rinv, k_ext, v_ext)
+        else:
+            ctx.save_for_backward(q, k, v, out, rinv)
         ctx.adj, ctx.scale, ctx.lo, ctx.hi, ctx.bwd_bytes = adj, scale, lo, hi, bb.value
         ctx.mark_non_differentiable(ns)
         return out, ns
 
     @staticmethod
     def backward(ctx, g_out, g_ns):
-        q, k, v, out, rinv = ctx.saved_tensors
+        saved = ctx.saved_tensors
+        q, k, v, out, rinv = saved[:5]
+        k_ext, v_ext = saved[5:] if len(saved) == 7 else (None, None)
         lib = _lib.load()
         n_q, H, d = q.shape
         dev = q.device
@@ -93,21 +104,25 @@ class SparseAttentionFunction(torch.autograd.Function):
         gk = torch.empty_like(k)
         gv = torch.empty_like(v)
         ws = _workspace(ctx.bwd_bytes, dev)
-        _lib.check(lib.ngt_sparse_bwd(_dtype_code(q), q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                                      out.data_ptr(), g.data_ptr(), rinv.data_ptr(),
-                                      ctx.adj.ptr(), H, d, ctx.scale, ctx.lo, ctx.hi,
-                                      gq.data_ptr(), gk.data_ptr(), gv.data_ptr(), ws.data_ptr(),
-                                      ctx.bwd_bytes, _stream(dev)))
-        return gq, gk, gv, None, None, None, None, None
+        ext = k_ext is not None
+        _lib.check(lib.ngt_sparse_bwd_ext(
+            _dtype_code(q), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+            k_ext.data_ptr() if ext else None, v_ext.data_ptr() if ext else None, k.shape[0],
+            out.data_ptr(), g.data_ptr(), rinv.data_ptr(), ctx.adj.ptr(), H, d, ctx.scale, ctx.lo,
+            ctx.hi, gq.data_ptr(), gk.data_ptr(), gv.data_ptr(), ws.data_ptr(), ctx.bwd_bytes,
+            _stream(dev)))
+        return gq, gk, gv, None, None, None, None, None, None, None
 
 
 def sparse_attention(q, k, v, edge_index, num_heads=None, scale=None, cache: AdjacencyCache = None,
-                     lo=CLAMP_LO, hi=CLAMP_HI, eps=EPS):
+                     lo=CLAMP_LO, hi=CLAMP_HI, eps=EPS, kv_ext=None):
     """Functional form.  q [.., N_q, H, d] -> (x [N_q, H, d], node_scores [max(dst)+1]).
 
     ``edge_index`` [2, E]: row 0 = key (src) index < N_k, row 1 = query (dst)
     index < N_q.  The reference requires N_q == N_k; N_q < N_k (extra key rows,
-    e.g. related nodes served from the cache) is also accepted.
+    e.g. related nodes served from the cache) is also accepted.  ``kv_ext``
+    = (k_r, v_r), each [R, H, d], supplies key rows N_k .. N_k+R-1 from their
+    own buffers without a concatenation; they get no gradient (a detached cache).
     """
     H, d = q.shape[-2], q.shape[-1]
     if num_heads is not None and num_heads != H:
@@ -120,14 +135,22 @@ def sparse_attention(q, k, v, edge_index, num_heads=None, scale=None, cache: Adj
     _dtype_code(q)
     if k.shape != v.shape or k.shape[1:] != q.shape[1:]:
         raise ValueError(f"shape mismatch q {tuple(q.shape)} k {tuple(k.shape)} v {tuple(v.shape)}")
-    if q.shape[0] > k.shape[0]:
-        raise ValueError(f"N_q={q.shape[0]} exceeds N_k={k.shape[0]}")
+    k_ext = v_ext = None
+    n_k = k.shape[0]
+    if kv_ext is not None:
+        k_ext = _prep(kv_ext[0].detach().reshape(-1, H, d), "k_ext")
+        v_ext = _prep(kv_ext[1].detach().reshape(-1, H, d), "v_ext")
+        if k_ext.shape != v_ext.shape or k_ext.dtype != q.dtype or v_ext.dtype != q.dtype:
+            raise ValueError(f"kv_ext must be two [R, {H}, {d}] tensors of dtype {q.dtype}")
+        n_k += k_ext.shape[0]
+    if q.shape[0] > n_k:
+        raise ValueError(f"N_q={q.shape[0]} exceeds N_k={n_k}")
     if scale is None:
         scale = math.sqrt(d)
     cache = cache or default_cache
-    adj = cache.get(edge_index, q.shape[0], k.shape[0], chunk_for_heads(H), small_for_heads(H))
+    adj = cache.get(edge_index, q.shape[0], n_k, chunk_for_heads(H), small_for_heads(H))
     return SparseAttentionFunction.apply(q, k, v, adj, float(scale), float(lo), float(hi),
-                                         float(eps))
+                                         float(eps), k_ext, v_ext)
 
 
 # -------------------------------------------------------------------- dense
@@ -255,20 +278,26 @@ class CoreAttention(nn.Module):
                                dropout_p=dropout_p)
         return x.unsqueeze(0), None
 
-    def sparse_attention_bias(self, q, k, v, edge_index, attn_bias):
-        """graphormer_dist_node_level.py:67-98.  Returns (x [N_q, H, d], node_scores)."""
+    def sparse_attention_bias(self, q, k, v, edge_index, attn_bias, kv_ext=None):
+        """graphormer_dist_node_level.py:67-98.  Returns (x [N_q, H, d], node_scores).
+        ``kv_ext`` (k_r, v_r): extra key rows after k/v, without gradient."""
         if attn_bias is not None:
             raise NotImplementedError(
                 "sparse attention with a dense attn_bias is not implemented (struct_enc is "
                 "False on NeutronGT's training path)")
         return sparse_attention(q, k, v, edge_index, num_heads=self.num_heads, scale=self.scale,
-                                cache=self.adjacency_cache)
+                                cache=self.adjacency_cache, kv_ext=kv_ext)
 
     def forward(self, q, k, v, attn_bias=None, edge_index=None, attn_type=None, mask=None,
-                pruning_mask=None):
+                pruning_mask=None, kv_ext=None):
+        """The reference's dispatch; ``kv_ext`` (an addition: (k_r, v_r), each
+        [R, H, d], no gradient) appends key rows without a concatenation."""
         batch_size, s_len = q.size(0), q.size(1)
+        if kv_ext is not None and attn_type != "sparse":
+            k = torch.cat([k, kv_ext[0].detach().to(k.dtype).reshape(1, -1, *k.shape[2:])], dim=1)
+            v = torch.cat([v, kv_ext[1].detach().to(v.dtype).reshape(1, -1, *v.shape[2:])], dim=1)
         if attn_type == "sparse":
-            x, score = self.sparse_attention_bias(q, k, v, edge_index, attn_bias)
+            x, score = self.sparse_attention_bias(q, k, v, edge_index, attn_bias, kv_ext=kv_ext)
         elif attn_type == "flash":
             # The reference casts q/k/v to fp16 here and the result back to
             # fp32; this runs the same math in the inputs' dtype (fp32 or bf16).

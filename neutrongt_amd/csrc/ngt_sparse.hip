@@ -23,6 +23,7 @@
 
 #include <stdlib.h>
 
+#include <type_traits>
 #include <utility>
 
 namespace ngt {
@@ -46,6 +47,32 @@ __device__ __forceinline__ float dot(const float (&a)[DH], const float (&b)[DH])
 __device__ __forceinline__ float clampf(float a, float lo, float hi) {
   return fminf(fmaxf(a, lo), hi);
 }
+
+// Key rows: rows j < n_main of k/v, then rows j - n_main of k_ext/v_ext (a
+// second buffer, e.g. the detached cache of related keys, so the caller need
+// not concatenate it).  With one buffer k_ext = k, v_ext = v and n_main = n_k.
+// Gradients exist only for the rows of k/v (the second buffer is constant).
+// The per-edge gathers of the query-major kernels are instantiated with and
+// without the second buffer (EXT): the select costs 2-5 % of the forward.
+template <typename T, bool EXT = true>
+struct Keys {
+  const T* k;
+  const T* v;
+  const T* k_ext;
+  const T* v_ext;
+  int64_t n_main;
+
+  template <int DH>
+  __device__ __forceinline__ const T* krow(int64_t j, int H, int h) const {
+    if (!EXT) return k + (j * H + h) * DH;
+    return j < n_main ? k + (j * H + h) * DH : k_ext + ((j - n_main) * H + h) * DH;
+  }
+  template <int DH>
+  __device__ __forceinline__ const T* vrow(int64_t j, int H, int h) const {
+    if (!EXT) return v + (j * H + h) * DH;
+    return j < n_main ? v + (j * H + h) * DH : v_ext + ((j - n_main) * H + h) * DH;
+  }
+};
 
 // Edges per slot whose row loads are issued together before any is used:
 // as many as fit a budget of raw 16-byte words per lane (at most 4).
@@ -121,9 +148,8 @@ __device__ __forceinline__ bool packed_work(int64_t pw, int n_pwaves, int n_grou
   return true;
 }
 
-template <typename T, int DH>
-__device__ __forceinline__ float fwd_packed(const T* __restrict__ q, const T* __restrict__ k,
-                                           const T* __restrict__ v,
+template <typename T, int DH, bool EXT>
+__device__ __forceinline__ float fwd_packed(const T* __restrict__ q, const Keys<T, EXT>& kv,
                                            const int32_t* __restrict__ rowptr,
                                            const int32_t* __restrict__ col, int64_t row, int h,
                                            int H, float inv_scale, float lo, float hi, float eps,
@@ -149,8 +175,8 @@ __device__ __forceinline__ float fwd_packed(const T* __restrict__ q, const T* __
     for (int u = 0; u < U; ++u) {
       jc[u] = jn[u];
       if (jc[u] >= 0) {
-        load_words<T, DH>(k + (int64_t(jc[u]) * H + h) * DH, kw[u]);
-        load_words<T, DH>(v + (int64_t(jc[u]) * H + h) * DH, vw[u]);
+        load_words<T, DH>(kv.template krow<DH>(jc[u], H, h), kw[u]);
+        load_words<T, DH>(kv.template vrow<DH>(jc[u], H, h), vw[u]);
       }
     }
 #pragma unroll
@@ -181,9 +207,9 @@ __device__ __forceinline__ float fwd_packed(const T* __restrict__ q, const T* __
 // lanes and written here; split rows get theirs in the finalize.  ns is null
 // when no node scores are wanted or with several head groups (then
 // k_node_score reads zbuf).
-template <typename T, int DH>
+template <typename T, int DH, bool EXT>
 __global__ __launch_bounds__(kBlock) void k_fwd(
-    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    const T* __restrict__ q, const Keys<T, EXT> kv,
     const int32_t* __restrict__ col, const int4* __restrict__ items, int32_t n_items,
     int32_t n_groups, int32_t hg, int32_t H, int32_t L, float inv_scale, float lo, float hi,
     float eps, T* __restrict__ out, float* __restrict__ rinv, float* __restrict__ zbuf,
@@ -199,7 +225,7 @@ __global__ __launch_bounds__(kBlock) void k_fwd(
     const bool has = packed_work(gw - int64_t(n_items) * n_groups, n_pwaves, n_groups, hg, L, H,
                                  packed, n_packed, prow, ph);
     if (has)
-      z = fwd_packed<T, DH>(q, k, v, rowptr, col, prow, ph, H, inv_scale, lo, hi, eps, out, rinv,
+      z = fwd_packed<T, DH, EXT>(q, kv, rowptr, col, prow, ph, H, inv_scale, lo, hi, eps, out, rinv,
                             zbuf);
     if (ns) {  // all lanes take part; lanes without a row add 0
       const float zs = reduce_heads(z, L);
@@ -243,8 +269,8 @@ __global__ __launch_bounds__(kBlock) void k_fwd(
         ok[u] = t < nb && ln.active;
         const int64_t j = __shfl(my_j, t < nb ? t : 0, kWave);
         if (ok[u]) {
-          load_words<T, DH>(k + (j * H + h) * DH, kw[u]);
-          load_words<T, DH>(v + (j * H + h) * DH, vw[u]);
+          load_words<T, DH>(kv.template krow<DH>(j, H, h), kw[u]);
+          load_words<T, DH>(kv.template vrow<DH>(j, H, h), vw[u]);
         }
       }
 #pragma unroll
@@ -368,14 +394,14 @@ __global__ __launch_bounds__(kBlock) void k_rowstat(const T* __restrict__ out,
 
 template <typename T, int DH>
 __device__ __forceinline__ void bwd_kv_packed(
-    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    const T* __restrict__ q, const Keys<T>& kv,
     const T* __restrict__ g, const float2* __restrict__ rd, const int32_t* __restrict__ t_rowptr,
     const int32_t* __restrict__ t_col, int64_t row, int h, int H, float inv_scale, float lo,
     float hi, T* __restrict__ grad_k, T* __restrict__ grad_v, float* __restrict__ ds) {
   RowWords<T, DH> krw, vrw;
   float dk[DH], dv[DH];
-  load_words<T, DH>(k + (row * H + h) * DH, krw);
-  load_words<T, DH>(v + (row * H + h) * DH, vrw);
+  load_words<T, DH>(kv.template krow<DH>(row, H, h), krw);
+  load_words<T, DH>(kv.template vrow<DH>(row, H, h), vrw);
 #pragma unroll
   for (int c = 0; c < DH; ++c) {
     dk[c] = 0.f;
@@ -421,6 +447,7 @@ __device__ __forceinline__ void bwd_kv_packed(
   }
 #pragma unroll
   for (int c = 0; c < DH; ++c) dk[c] *= inv_scale;
+  if (row >= kv.n_main) return;  // constant key rows: no gradient
   store_row<T, DH>(grad_k + (row * H + h) * DH, dk);
   store_row<T, DH>(grad_v + (row * H + h) * DH, dv);
 }
@@ -429,7 +456,7 @@ __device__ __forceinline__ void bwd_kv_packed(
 // (stored at the key-major edge position for the query-major pass).
 template <typename T, int DH>
 __global__ __launch_bounds__(kBlock) void k_bwd_kv(
-    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    const T* __restrict__ q, const Keys<T> kv,
     const T* __restrict__ g, const float2* __restrict__ rd, const int32_t* __restrict__ t_col,
     const int4* __restrict__ items, int32_t n_items, int32_t n_groups, int32_t hg, int32_t H,
     int32_t L, float inv_scale, float lo, float hi, T* __restrict__ grad_k,
@@ -443,7 +470,7 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
     int ph;
     if (packed_work(gw0 - int64_t(n_items) * n_groups, n_pwaves, n_groups, hg, L, H, packed,
                     n_packed, prow, ph))
-      bwd_kv_packed<T, DH>(q, k, v, g, rd, t_rowptr, t_col, prow, ph, H, inv_scale, lo, hi,
+      bwd_kv_packed<T, DH>(q, kv, g, rd, t_rowptr, t_col, prow, ph, H, inv_scale, lo, hi,
                            grad_k, grad_v, ds);
     return;
   }
@@ -463,8 +490,8 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
     dv[c] = 0.f;
   }
   if (ln.active) {
-    load_words<T, DH>(k + (row * H + h) * DH, krw);
-    load_words<T, DH>(v + (row * H + h) * DH, vrw);
+    load_words<T, DH>(kv.template krow<DH>(row, H, h), krw);
+    load_words<T, DH>(kv.template vrow<DH>(row, H, h), vrw);
   } else {
     zero_words<T, DH>(krw);
     zero_words<T, DH>(vrw);
@@ -514,6 +541,7 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
 #pragma unroll
   for (int c = 0; c < DH; ++c) dk[c] *= inv_scale;
   if (it.w < 0) {
+    if (row >= kv.n_main) return;  // constant key rows: no gradient
     store_row<T, DH>(grad_k + (row * H + h) * DH, dk);
     store_row<T, DH>(grad_v + (row * H + h) * DH, dv);
   } else {
@@ -528,10 +556,11 @@ template <typename T, int DH>
 __device__ __forceinline__ void bwd_kv_finalize_tile(const int4* __restrict__ splits, int32_t H,
                                                      const float* __restrict__ part_kv,
                                                      T* __restrict__ grad_k,
-                                                     T* __restrict__ grad_v, int split,
-                                                     int tile) {
+                                                     T* __restrict__ grad_v, int64_t n_main,
+                                                     int split, int tile) {
   __shared__ float red[kWavesPerBlock][kColTile];
   const int4 sp = splits[split];
+  if (sp.x >= n_main) return;  // constant key row: no gradient (uniform per block)
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
   const int ncols = 2 * H * DH;
@@ -554,8 +583,8 @@ __device__ __forceinline__ void bwd_kv_finalize_tile(const int4* __restrict__ sp
     elem<T>::store(grad_v + at + (c - DH), a);
 }
 
-template <typename T, int DH>
-__device__ __forceinline__ void bwd_q_packed(const T* __restrict__ k,
+template <typename T, int DH, bool EXT>
+__device__ __forceinline__ void bwd_q_packed(const Keys<T, EXT>& kv,
                                              const int32_t* __restrict__ rowptr,
                                              const int32_t* __restrict__ col,
                                              const int32_t* __restrict__ q2t,
@@ -580,7 +609,7 @@ __device__ __forceinline__ void bwd_q_packed(const T* __restrict__ k,
     for (int u = 0; u < U; ++u) {
       jc[u] = jn[u];
       if (jc[u] >= 0) {
-        load_words<T, DH>(k + (int64_t(jc[u]) * H + h) * DH, kw[u]);
+        load_words<T, DH>(kv.template krow<DH>(jc[u], H, h), kw[u]);
         d[u] = ds[int64_t(tn[u]) * H + h];
       }
     }
@@ -602,9 +631,9 @@ __device__ __forceinline__ void bwd_q_packed(const T* __restrict__ k,
 }
 
 // Query-major pass: grad_q[i] = sum_e da_e k_j / scale.
-template <typename T, int DH>
+template <typename T, int DH, bool EXT>
 __global__ __launch_bounds__(kBlock) void k_bwd_q(
-    const T* __restrict__ k, const int32_t* __restrict__ col, const int32_t* __restrict__ q2t,
+    const Keys<T, EXT> kv, const int32_t* __restrict__ col, const int32_t* __restrict__ q2t,
     const float* __restrict__ ds, const int4* __restrict__ items, int32_t n_items,
     int32_t n_groups, int32_t hg, int32_t H, int32_t L, float inv_scale, T* __restrict__ grad_q,
     float* __restrict__ part_q, const int32_t* __restrict__ rowptr,
@@ -615,7 +644,8 @@ __global__ __launch_bounds__(kBlock) void k_bwd_q(
   // partials): that work is independent of dQ, so it rides in this launch.
   if (int32_t(blockIdx.x) >= q_blocks) {
     const int f = int(blockIdx.x) - q_blocks;
-    bwd_kv_finalize_tile<T, DH>(splits_k, H, part_kv, grad_k, grad_v, f / kv_tiles, f % kv_tiles);
+    bwd_kv_finalize_tile<T, DH>(splits_k, H, part_kv, grad_k, grad_v, kv.n_main, f / kv_tiles,
+                                f % kv_tiles);
     return;
   }
   const int64_t gw0 = virtual_wave(n_items, n_pwaves, n_groups, xcd);
@@ -625,7 +655,7 @@ __global__ __launch_bounds__(kBlock) void k_bwd_q(
     int ph;
     if (packed_work(gw0 - int64_t(n_items) * n_groups, n_pwaves, n_groups, hg, L, H, packed,
                     n_packed, prow, ph))
-      bwd_q_packed<T, DH>(k, rowptr, col, q2t, ds, prow, ph, H, inv_scale, grad_q);
+      bwd_q_packed<T, DH, EXT>(kv, rowptr, col, q2t, ds, prow, ph, H, inv_scale, grad_q);
     return;
   }
   int item;
@@ -657,7 +687,7 @@ __global__ __launch_bounds__(kBlock) void k_bwd_q(
         const int64_t j = __shfl(my_j, src, kWave);
         const int64_t tp = __shfl(my_t, src, kWave);
         if (ok[u]) {
-          load_words<T, DH>(k + (j * H + h) * DH, kw[u]);
+          load_words<T, DH>(kv.template krow<DH>(j, H, h), kw[u]);
           dsv[u] = ds[tp * H + h];
         }
       }
@@ -817,10 +847,20 @@ inline unsigned edge_blocks(int n_items, int pw, int groups, int xcd) {
   return xcd ? unsigned(groups) * blocks_for(per_group) : blocks_for(per_group * groups);
 }
 
+template <typename T, bool EXT = true>
+Keys<T, EXT> make_keys(const void* k, const void* v, const void* k_ext, const void* v_ext,
+                       int64_t n_main) {
+  const T* kk = static_cast<const T*>(k);
+  const T* vv = static_cast<const T*>(v);
+  return Keys<T, EXT>{kk, vv, k_ext ? static_cast<const T*>(k_ext) : kk,
+                      v_ext ? static_cast<const T*>(v_ext) : vv, n_main};
+}
+
 template <typename T, int DH>
-int launch_fwd(const ngt_window_csr* c, const void* q, const void* k, const void* v, int H,
-               float inv_scale, float lo, float hi, float eps, void* out, float* rinv, float* ns,
-               int ns_len, char* ws, hipStream_t st) {
+int launch_fwd(const ngt_window_csr* c, const void* q, const void* k, const void* v,
+               const void* k_ext, const void* v_ext, int64_t n_main, int H, float inv_scale,
+               float lo, float hi, float eps, void* out, float* rinv, float* ns, int ns_len,
+               char* ws, hipStream_t st) {
   const int hg = heads_per_pass(H, 0);
   const int groups = (H + hg - 1) / hg;
   const int L = lanes_for(hg);
@@ -835,12 +875,19 @@ int launch_fwd(const ngt_window_csr* c, const void* q, const void* k, const void
   float* ns_direct = groups == 1 && ns && ns_len > 0 ? ns : nullptr;
   if (blocks_q > 0) {
     KernelTimer timer_("sparse_fwd", st);
-    hipLaunchKernelGGL((k_fwd<T, DH>), dim3(blocks_q), dim3(kBlock), 0, st,
-                       static_cast<const T*>(q), static_cast<const T*>(k),
-                       static_cast<const T*>(v), c->col, reinterpret_cast<const int4*>(c->items_q),
-                       c->n_items_q, groups, hg, H, L, inv_scale, lo, hi, eps,
-                       static_cast<T*>(out), rinv, zbuf, part_acc, part_z, c->rowptr, c->packed_q,
-                       c->n_packed_q, pw_q, ns_direct, ns_len, xcd);
+    auto launch = [&](auto ext) {
+      constexpr bool E = decltype(ext)::value;
+      hipLaunchKernelGGL((k_fwd<T, DH, E>), dim3(blocks_q), dim3(kBlock), 0, st,
+                         static_cast<const T*>(q), make_keys<T, E>(k, v, k_ext, v_ext, n_main),
+                         c->col, reinterpret_cast<const int4*>(c->items_q), c->n_items_q, groups,
+                         hg, H, L, inv_scale, lo, hi, eps, static_cast<T*>(out), rinv, zbuf,
+                         part_acc, part_z, c->rowptr, c->packed_q, c->n_packed_q, pw_q,
+                         ns_direct, ns_len, xcd);
+    };
+    if (n_main < c->n_k)
+      launch(std::true_type{});
+    else
+      launch(std::false_type{});
     NGT_HIP_CHECK(hipGetLastError());
   }
   if (c->n_splits_q > 0) {
@@ -862,8 +909,9 @@ int launch_fwd(const ngt_window_csr* c, const void* q, const void* k, const void
 
 template <typename T, int DH>
 int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void* v,
-               const void* out, const void* g, const float* rinv, int H, float inv_scale,
-               float lo, float hi, void* gq, void* gk, void* gv, char* ws, hipStream_t st) {
+               const void* k_ext, const void* v_ext, int64_t n_main, const void* out,
+               const void* g, const float* rinv, int H, float inv_scale, float lo, float hi,
+               void* gq, void* gk, void* gv, char* ws, hipStream_t st) {
   const BwdLayout lay = bwd_layout(c, H, DH);
   float2* rd = reinterpret_cast<float2*>(ws + lay.rd);
   float* ds = reinterpret_cast<float*>(ws + lay.ds);
@@ -887,8 +935,8 @@ int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void
   if (blocks_k > 0) {
     KernelTimer timer_("sparse_bwd_kv", st);
     hipLaunchKernelGGL((k_bwd_kv<T, DH>), dim3(blocks_k), dim3(kBlock), 0, st,
-                       static_cast<const T*>(q), static_cast<const T*>(k),
-                       static_cast<const T*>(v), static_cast<const T*>(g), rd, c->t_col,
+                       static_cast<const T*>(q), make_keys<T>(k, v, k_ext, v_ext, n_main),
+                       static_cast<const T*>(g), rd, c->t_col,
                        reinterpret_cast<const int4*>(c->items_k), c->n_items_k, groups, hg, H, L,
                        inv_scale, lo, hi, static_cast<T*>(gk), static_cast<T*>(gv), ds, part_kv,
                        c->t_rowptr, c->packed_k, c->n_packed_k, pw_k, xcd);
@@ -904,13 +952,20 @@ int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void
   const int64_t fin_blocks = int64_t(c->n_splits_k) * kv_tiles;
   if (q_blocks + fin_blocks > 0) {
     KernelTimer timer_("sparse_bwd_q", st);
-    hipLaunchKernelGGL((k_bwd_q<T, DH>), dim3(unsigned(q_blocks + fin_blocks)), dim3(kBlock), 0,
-                       st, static_cast<const T*>(k), c->col, c->q2t, ds,
-                       reinterpret_cast<const int4*>(c->items_q), c->n_items_q, groups, hg, H, L,
-                       inv_scale, static_cast<T*>(gq), part_q, c->rowptr, c->packed_q,
-                       c->n_packed_q, pw_q, int32_t(q_blocks),
-                       reinterpret_cast<const int4*>(c->splits_k), kv_tiles, part_kv,
-                       static_cast<T*>(gk), static_cast<T*>(gv), xcd);
+    auto launch = [&](auto ext) {
+      constexpr bool E = decltype(ext)::value;
+      hipLaunchKernelGGL((k_bwd_q<T, DH, E>), dim3(unsigned(q_blocks + fin_blocks)), dim3(kBlock),
+                         0, st, make_keys<T, E>(k, v, k_ext, v_ext, n_main), c->col, c->q2t, ds,
+                         reinterpret_cast<const int4*>(c->items_q), c->n_items_q, groups, hg, H,
+                         L, inv_scale, static_cast<T*>(gq), part_q, c->rowptr, c->packed_q,
+                         c->n_packed_q, pw_q, int32_t(q_blocks),
+                         reinterpret_cast<const int4*>(c->splits_k), kv_tiles, part_kv,
+                         static_cast<T*>(gk), static_cast<T*>(gv), xcd);
+    };
+    if (n_main < c->n_k)
+      launch(std::true_type{});
+    else
+      launch(std::false_type{});
     NGT_HIP_CHECK(hipGetLastError());
   }
   if (c->n_splits_q > 0) {
@@ -972,26 +1027,73 @@ extern "C" int ngt_sparse_workspace_bytes(const ngt_window_csr* csr, int32_t n_h
   return NGT_OK;
 }
 
-extern "C" int ngt_sparse_fwd(int dtype, const void* q, const void* k, const void* v,
-                              const ngt_window_csr* csr, int32_t n_heads, int32_t head_dim,
-                              float scale, float clamp_lo, float clamp_hi, float eps, void* out,
-                              float* rinv, float* node_score, int32_t node_score_len,
-                              void* workspace, size_t workspace_bytes, void* stream) {
+extern "C" int ngt_sparse_fwd_ext(int dtype, const void* q, const void* k, const void* v,
+                                  const void* k_ext, const void* v_ext, int32_t n_k_main,
+                                  const ngt_window_csr* csr, int32_t n_heads, int32_t head_dim,
+                                  float scale, float clamp_lo, float clamp_hi, float eps,
+                                  void* out, float* rinv, float* node_score,
+                                  int32_t node_score_len, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
   int rc = check_common("ngt_sparse_fwd", dtype, csr, n_heads, head_dim);
   if (rc != NGT_OK) return rc;
   if (!(scale > 0.f)) return set_error(NGT_ERR_ARG, "ngt_sparse_fwd: scale must be > 0");
   if (csr->n_q > 0 && (!q || !out || !rinv))
     return set_error(NGT_ERR_ARG, "ngt_sparse_fwd: null q/out/rinv");
-  if (csr->n_edges > 0 && (!k || !v)) return set_error(NGT_ERR_ARG, "ngt_sparse_fwd: null k/v");
+  if (n_k_main < 0 || n_k_main > csr->n_k)
+    return set_error(NGT_ERR_ARG, "ngt_sparse_fwd: n_k_main=%d outside [0, n_k=%d]", n_k_main,
+                     csr->n_k);
+  if (csr->n_edges > 0 && ((n_k_main > 0 && (!k || !v)) ||
+                           (n_k_main < csr->n_k && (!k_ext || !v_ext))))
+    return set_error(NGT_ERR_ARG, "ngt_sparse_fwd: null k/v");
   if (node_score_len < 0 || node_score_len > csr->n_q)
     return set_error(NGT_ERR_ARG, "ngt_sparse_fwd: node_score_len out of range");
   const size_t need = fwd_layout(csr, n_heads, head_dim).total;
   if (need > 0 && (!workspace || workspace_bytes < need))
     return set_error(NGT_ERR_WORKSPACE, "ngt_sparse_fwd: workspace %zu < %zu", workspace_bytes,
                      need);
-  return dispatch<FwdOp>(dtype, head_dim, csr, q, k, v, int(n_heads), 1.0f / scale, clamp_lo,
-                         clamp_hi, eps, out, rinv, node_score, int(node_score_len),
-                         static_cast<char*>(workspace), static_cast<hipStream_t>(stream));
+  return dispatch<FwdOp>(dtype, head_dim, csr, q, k, v, k_ext, v_ext, int64_t(n_k_main),
+                         int(n_heads), 1.0f / scale, clamp_lo, clamp_hi, eps, out, rinv,
+                         node_score, int(node_score_len), static_cast<char*>(workspace),
+                         static_cast<hipStream_t>(stream));
+}
+
+extern "C" int ngt_sparse_fwd(int dtype, const void* q, const void* k, const void* v,
+                              const ngt_window_csr* csr, int32_t n_heads, int32_t head_dim,
+                              float scale, float clamp_lo, float clamp_hi, float eps, void* out,
+                              float* rinv, float* node_score, int32_t node_score_len,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+  if (!csr) return set_error(NGT_ERR_ARG, "ngt_sparse_fwd: null csr");
+  return ngt_sparse_fwd_ext(dtype, q, k, v, nullptr, nullptr, csr->n_k, csr, n_heads, head_dim,
+                            scale, clamp_lo, clamp_hi, eps, out, rinv, node_score,
+                            node_score_len, workspace, workspace_bytes, stream);
+}
+
+extern "C" int ngt_sparse_bwd_ext(int dtype, const void* q, const void* k, const void* v,
+                                  const void* k_ext, const void* v_ext, int32_t n_k_main,
+                                  const void* out, const void* grad_out, const float* rinv,
+                                  const ngt_window_csr* csr, int32_t n_heads, int32_t head_dim,
+                                  float scale, float clamp_lo, float clamp_hi, void* grad_q,
+                                  void* grad_k, void* grad_v, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  int rc = check_common("ngt_sparse_bwd", dtype, csr, n_heads, head_dim);
+  if (rc != NGT_OK) return rc;
+  if (!(scale > 0.f)) return set_error(NGT_ERR_ARG, "ngt_sparse_bwd: scale must be > 0");
+  if (csr->n_q > 0 && (!q || !out || !grad_out || !rinv || !grad_q))
+    return set_error(NGT_ERR_ARG, "ngt_sparse_bwd: null query-side pointer");
+  if (n_k_main < 0 || n_k_main > csr->n_k)
+    return set_error(NGT_ERR_ARG, "ngt_sparse_bwd: n_k_main=%d outside [0, n_k=%d]", n_k_main,
+                     csr->n_k);
+  if ((n_k_main > 0 && (!k || !v || !grad_k || !grad_v)) ||
+      (n_k_main < csr->n_k && (!k_ext || !v_ext)))
+    return set_error(NGT_ERR_ARG, "ngt_sparse_bwd: null key-side pointer");
+  const size_t need = bwd_layout(csr, n_heads, head_dim).total;
+  if (need > 0 && (!workspace || workspace_bytes < need))
+    return set_error(NGT_ERR_WORKSPACE, "ngt_sparse_bwd: workspace %zu < %zu", workspace_bytes,
+                     need);
+  return dispatch<BwdOp>(dtype, head_dim, csr, q, k, v, k_ext, v_ext, int64_t(n_k_main), out,
+                         grad_out, rinv, int(n_heads), 1.0f / scale, clamp_lo, clamp_hi, grad_q,
+                         grad_k, grad_v, static_cast<char*>(workspace),
+                         static_cast<hipStream_t>(stream));
 }
 
 extern "C" int ngt_sparse_bwd(int dtype, const void* q, const void* k, const void* v,
@@ -1000,18 +1102,8 @@ extern "C" int ngt_sparse_bwd(int dtype, const void* q, const void* k, const voi
                               float scale, float clamp_lo, float clamp_hi, void* grad_q,
                               void* grad_k, void* grad_v, void* workspace, size_t workspace_bytes,
                               void* stream) {
-  int rc = check_common("ngt_sparse_bwd", dtype, csr, n_heads, head_dim);
-  if (rc != NGT_OK) return rc;
-  if (!(scale > 0.f)) return set_error(NGT_ERR_ARG, "ngt_sparse_bwd: scale must be > 0");
-  if (csr->n_q > 0 && (!q || !out || !grad_out || !rinv || !grad_q))
-    return set_error(NGT_ERR_ARG, "ngt_sparse_bwd: null query-side pointer");
-  if (csr->n_k > 0 && (!k || !v || !grad_k || !grad_v))
-    return set_error(NGT_ERR_ARG, "ngt_sparse_bwd: null key-side pointer");
-  const size_t need = bwd_layout(csr, n_heads, head_dim).total;
-  if (need > 0 && (!workspace || workspace_bytes < need))
-    return set_error(NGT_ERR_WORKSPACE, "ngt_sparse_bwd: workspace %zu < %zu", workspace_bytes,
-                     need);
-  return dispatch<BwdOp>(dtype, head_dim, csr, q, k, v, out, grad_out, rinv, int(n_heads),
-                         1.0f / scale, clamp_lo, clamp_hi, grad_q, grad_k, grad_v,
-                         static_cast<char*>(workspace), static_cast<hipStream_t>(stream));
+  if (!csr) return set_error(NGT_ERR_ARG, "ngt_sparse_bwd: null csr");
+  return ngt_sparse_bwd_ext(dtype, q, k, v, nullptr, nullptr, csr->n_k, out, grad_out, rinv, csr,
+                            n_heads, head_dim, scale, clamp_lo, clamp_hi, grad_q, grad_k, grad_v,
+                            workspace, workspace_bytes, stream);
 }

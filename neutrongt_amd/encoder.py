@@ -94,15 +94,21 @@ class _Attention(nn.Module):
         q = self.linear_q(x).view(b, n, H, d)
         k = self.linear_k(x).view(b, n, H, d)
         v = self.linear_v(x).view(b, n, H, d)
-        k_all, v_all = k, v
-        if kv_cache is not None:
-            k_r, v_r = kv_cache
-            if k_r.shape != v_r.shape or tuple(k_r.shape[1:]) != (H, d):
-                raise ValueError(f"kv_cache rows must be [R, {H}, {d}], got {tuple(k_r.shape)}")
-            k_all = torch.cat([k, k_r.detach().to(k.dtype).unsqueeze(0)], dim=1)
-            v_all = torch.cat([v, v_r.detach().to(v.dtype).unsqueeze(0)], dim=1)
+        if kv_cache is None:
+            y, score = self.local_attn(q, k, v, None, edge_index, attn_type)
+            return y, score, [k, v]
+        k_r, v_r = kv_cache
+        if k_r.shape != v_r.shape or tuple(k_r.shape[1:]) != (H, d):
+            raise ValueError(f"kv_cache rows must be [R, {H}, {d}], got {tuple(k_r.shape)}")
         # the core needs one dtype for q, k, v (autocast gives bf16 for all three)
-        y, score = self.local_attn(q, k_all, v_all, None, edge_index, attn_type)
+        k_r, v_r = k_r.detach().to(k.dtype), v_r.detach().to(v.dtype)
+        if isinstance(self.local_attn, CoreAttention):
+            # read from the cache's own buffers: no concatenation, no gradient
+            y, score = self.local_attn(q, k, v, None, edge_index, attn_type, kv_ext=(k_r, v_r))
+        else:  # another core (e.g. the reference's) takes the concatenated keys
+            y, score = self.local_attn(q, torch.cat([k, k_r.unsqueeze(0)], dim=1),
+                                       torch.cat([v, v_r.unsqueeze(0)], dim=1), None,
+                                       edge_index, attn_type)
         return y, score, [k, v]
 
 

@@ -256,3 +256,44 @@ def test_full_size_window_sampled_rows_and_invariants(name):
     sv = res["dv"].double().sum(0)
     sg = go.double()[has].sum(0)
     assert relerr(sv, sg) < max(1e-3, 10 * TOL[cfg.dtype])
+
+
+@pytest.mark.parametrize("H,d,dtype,chunk,small,hg", [(8, 16, torch.float32, 16, 3, None),
+                                                      (32, 24, torch.bfloat16, 32, 2, None),
+                                                      (8, 8, torch.float32, 0, 0, "2")])
+def test_sparse_external_key_rows(monkeypatch, H, d, dtype, chunk, small, hg):
+    """Key rows split over two buffers (window rows + a detached cache of related
+    keys, ngt_sparse_fwd_ext/bwd_ext): same output, node scores and dQ as the
+    oracle over the concatenated keys, dK/dV for the window rows only, with hub
+    rows (split chunks) on both sides of the boundary."""
+    _say(f"case external keys H={H} d={d} {dtype} chunk={chunk} hg={hg}")
+    if hg:
+        monkeypatch.setenv("NGT_HEAD_GROUP", hg)
+    n_q, n_main, n_ext = 150, 170, 90
+    n_k = n_main + n_ext
+    rng = np.random.default_rng(H + d)
+    src = np.concatenate([rng.integers(0, n_k, 1500), np.full(300, 5), np.full(260, n_main + 7),
+                          rng.integers(n_main, n_k, 200)])
+    dst = np.concatenate([rng.integers(0, n_q, 1500), rng.integers(0, n_q, 300),
+                          rng.integers(0, n_q, 260), np.zeros(200, np.int64)])
+    ei = np.stack([src, dst]).astype(np.int64)
+    q, k, v, go = _qkv(n_q, n_k, H, d, dtype, seed=21)
+    ref = _oracle(q, k, v, ei, go, H)
+    qd = q.cuda().requires_grad_(True)
+    kd = k[:n_main].cuda().requires_grad_(True)
+    vd = v[:n_main].cuda().requires_grad_(True)
+    kx, vx = k[n_main:].cuda(), v[n_main:].cuda()
+    eid = torch.from_numpy(ei).cuda()
+    if chunk:
+        adj = WindowAdjacency(eid, n_q, n_k, chunk, small)
+        x, ns = SparseAttentionFunction.apply(qd, kd, vd, adj, float(d) ** 0.5, -5.0, 5.0, 1e-6,
+                                              kx, vx)
+    else:
+        x, ns = sparse_attention(qd, kd, vd, eid, kv_ext=(kx, vx))
+    x.backward(go.cuda())
+    torch.cuda.synchronize()
+    res = {"x": x.detach().cpu(), "node_scores": ns.cpu(), "dq": qd.grad.cpu(),
+           "dk": kd.grad.cpu(), "dv": vd.grad.cpu()}
+    ref["dk"], ref["dv"] = ref["dk"][:n_main], ref["dv"][:n_main]
+    _check(res, ref, dtype, "external keys")
+    assert kx.grad is None and vx.grad is None
