@@ -54,6 +54,9 @@ __device__ __forceinline__ float clampf(float a, float lo, float hi) {
 // Gradients exist only for the rows of k/v (the second buffer is constant).
 // The per-edge gathers of the query-major kernels are instantiated with and
 // without the second buffer (EXT): the select costs 2-5 % of the forward.
+// With two buffers the forward takes 132 VGPRs against 108 (one wave less per
+// SIMD; about 5 % of its time in the window step), whether the gathers select
+// a base or branch; capping it at 128 spills.
 template <typename T, bool EXT = true>
 struct Keys {
   const T* k;
@@ -64,13 +67,32 @@ struct Keys {
 
   template <int DH>
   __device__ __forceinline__ const T* krow(int64_t j, int H, int h) const {
-    if (!EXT) return k + (j * H + h) * DH;
-    return j < n_main ? k + (j * H + h) * DH : k_ext + ((j - n_main) * H + h) * DH;
+    if (!EXT || j < n_main) return k + (j * H + h) * DH;
+    return k_ext + ((j - n_main) * H + h) * DH;
   }
   template <int DH>
   __device__ __forceinline__ const T* vrow(int64_t j, int H, int h) const {
-    if (!EXT) return v + (j * H + h) * DH;
-    return j < n_main ? v + (j * H + h) * DH : v_ext + ((j - n_main) * H + h) * DH;
+    if (!EXT || j < n_main) return v + (j * H + h) * DH;
+    return v_ext + ((j - n_main) * H + h) * DH;
+  }
+  // K and V words of key row j for head h
+  template <int DH>
+  __device__ __forceinline__ void load_kv(int64_t j, int H, int h, RowWords<T, DH>& kw,
+                                          RowWords<T, DH>& vw) const {
+    if (!EXT || j < n_main) {
+      load_words<T, DH>(k + (j * H + h) * DH, kw);
+      load_words<T, DH>(v + (j * H + h) * DH, vw);
+    } else {
+      load_words<T, DH>(k_ext + ((j - n_main) * H + h) * DH, kw);
+      load_words<T, DH>(v_ext + ((j - n_main) * H + h) * DH, vw);
+    }
+  }
+  template <int DH>
+  __device__ __forceinline__ void load_k(int64_t j, int H, int h, RowWords<T, DH>& kw) const {
+    if (!EXT || j < n_main)
+      load_words<T, DH>(k + (j * H + h) * DH, kw);
+    else
+      load_words<T, DH>(k_ext + ((j - n_main) * H + h) * DH, kw);
   }
 };
 
@@ -175,8 +197,7 @@ __device__ __forceinline__ float fwd_packed(const T* __restrict__ q, const Keys<
     for (int u = 0; u < U; ++u) {
       jc[u] = jn[u];
       if (jc[u] >= 0) {
-        load_words<T, DH>(kv.template krow<DH>(jc[u], H, h), kw[u]);
-        load_words<T, DH>(kv.template vrow<DH>(jc[u], H, h), vw[u]);
+        kv.template load_kv<DH>(jc[u], H, h, kw[u], vw[u]);
       }
     }
 #pragma unroll
@@ -269,8 +290,7 @@ __global__ __launch_bounds__(kBlock) void k_fwd(
         ok[u] = t < nb && ln.active;
         const int64_t j = __shfl(my_j, t < nb ? t : 0, kWave);
         if (ok[u]) {
-          load_words<T, DH>(kv.template krow<DH>(j, H, h), kw[u]);
-          load_words<T, DH>(kv.template vrow<DH>(j, H, h), vw[u]);
+          kv.template load_kv<DH>(j, H, h, kw[u], vw[u]);
         }
       }
 #pragma unroll
@@ -609,7 +629,7 @@ __device__ __forceinline__ void bwd_q_packed(const Keys<T, EXT>& kv,
     for (int u = 0; u < U; ++u) {
       jc[u] = jn[u];
       if (jc[u] >= 0) {
-        load_words<T, DH>(kv.template krow<DH>(jc[u], H, h), kw[u]);
+        kv.template load_k<DH>(jc[u], H, h, kw[u]);
         d[u] = ds[int64_t(tn[u]) * H + h];
       }
     }
@@ -687,7 +707,7 @@ __global__ __launch_bounds__(kBlock) void k_bwd_q(
         const int64_t j = __shfl(my_j, src, kWave);
         const int64_t tp = __shfl(my_t, src, kWave);
         if (ok[u]) {
-          load_words<T, DH>(kv.template krow<DH>(j, H, h), kw[u]);
+          kv.template load_k<DH>(j, H, h, kw[u]);
           dsv[u] = ds[tp * H + h];
         }
       }
@@ -847,9 +867,10 @@ inline unsigned edge_blocks(int n_items, int pw, int groups, int xcd) {
   return xcd ? unsigned(groups) * blocks_for(per_group) : blocks_for(per_group * groups);
 }
 
-template <typename T, bool EXT = true>
+template <typename T, int DH, bool EXT = true>
 Keys<T, EXT> make_keys(const void* k, const void* v, const void* k_ext, const void* v_ext,
-                       int64_t n_main) {
+                       int64_t n_main, int H) {
+  (void)H;
   const T* kk = static_cast<const T*>(k);
   const T* vv = static_cast<const T*>(v);
   return Keys<T, EXT>{kk, vv, k_ext ? static_cast<const T*>(k_ext) : kk,
@@ -878,7 +899,7 @@ int launch_fwd(const ngt_window_csr* c, const void* q, const void* k, const void
     auto launch = [&](auto ext) {
       constexpr bool E = decltype(ext)::value;
       hipLaunchKernelGGL((k_fwd<T, DH, E>), dim3(blocks_q), dim3(kBlock), 0, st,
-                         static_cast<const T*>(q), make_keys<T, E>(k, v, k_ext, v_ext, n_main),
+                         static_cast<const T*>(q), make_keys<T, DH, E>(k, v, k_ext, v_ext, n_main, H),
                          c->col, reinterpret_cast<const int4*>(c->items_q), c->n_items_q, groups,
                          hg, H, L, inv_scale, lo, hi, eps, static_cast<T*>(out), rinv, zbuf,
                          part_acc, part_z, c->rowptr, c->packed_q, c->n_packed_q, pw_q,
@@ -935,7 +956,7 @@ int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void
   if (blocks_k > 0) {
     KernelTimer timer_("sparse_bwd_kv", st);
     hipLaunchKernelGGL((k_bwd_kv<T, DH>), dim3(blocks_k), dim3(kBlock), 0, st,
-                       static_cast<const T*>(q), make_keys<T>(k, v, k_ext, v_ext, n_main),
+                       static_cast<const T*>(q), make_keys<T, DH>(k, v, k_ext, v_ext, n_main, H),
                        static_cast<const T*>(g), rd, c->t_col,
                        reinterpret_cast<const int4*>(c->items_k), c->n_items_k, groups, hg, H, L,
                        inv_scale, lo, hi, static_cast<T*>(gk), static_cast<T*>(gv), ds, part_kv,
@@ -955,7 +976,7 @@ int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void
     auto launch = [&](auto ext) {
       constexpr bool E = decltype(ext)::value;
       hipLaunchKernelGGL((k_bwd_q<T, DH, E>), dim3(unsigned(q_blocks + fin_blocks)), dim3(kBlock),
-                         0, st, make_keys<T, E>(k, v, k_ext, v_ext, n_main), c->col, c->q2t, ds,
+                         0, st, make_keys<T, DH, E>(k, v, k_ext, v_ext, n_main, H), c->col, c->q2t, ds,
                          reinterpret_cast<const int4*>(c->items_q), c->n_items_q, groups, hg, H,
                          L, inv_scale, static_cast<T*>(gq), part_q, c->rowptr, c->packed_q,
                          c->n_packed_q, pw_q, int32_t(q_blocks),
