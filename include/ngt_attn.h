@@ -350,6 +350,26 @@ int ngt_timing_enable(int on);
 int ngt_timing_summary(char* buf, size_t len);
 
 /*
+ * LayerNorm over the last dimension (n_cols, a multiple of 4, at most 2048):
+ *   y = (x - mean) / sqrt(var + eps) * gamma + beta per row, fp32 math,
+ *   x in in_dtype, y in out_dtype (NGT_F32 or NGT_BF16), mean/rstd [n_rows]
+ *   fp32 saved for the backward; gamma/beta fp32.  The backward writes dx in
+ *   in_dtype from dy in grad_dtype, and dgamma/dbeta (fp32, either may be
+ *   NULL) as column sums added in a fixed order.  Rows 8-byte aligned.
+ * Replaces the encoder's nn.LayerNorm under bf16 autocast
+ * (NeutronGT/models/graphormer_dist_node_level.py:176-206, final_ln at
+ * :242-381; NeutronGT/models/gt_dist_node_level_single_window.py:305-353).
+ */
+int ngt_layernorm_fwd(int in_dtype, const void* x, int64_t n_rows, int32_t n_cols,
+                      const float* gamma, const float* beta, float eps, int out_dtype, void* y,
+                      float* mean, float* rstd, void* stream);
+int ngt_layernorm_bwd_workspace_bytes(int64_t n_rows, int32_t n_cols, size_t* bytes);
+int ngt_layernorm_bwd(int in_dtype, const void* x, int grad_dtype, const void* dy, int64_t n_rows,
+                      int32_t n_cols, const float* gamma, const float* mean, const float* rstd,
+                      void* dx, float* dgamma, float* dbeta, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/*
  * Column sums of a bf16 matrix in fp32: out[j] = sum_k dy[k][j], dy
  * [n_rows, n_cols] row-major, 16-byte aligned, n_cols a multiple of 8; summed
  * in a fixed order.  The bias gradient of the encoder's linear layers under

@@ -15,10 +15,11 @@ the shipped setting):
 
 Sub-module and parameter names are the reference's, so a reference
 ``state_dict`` loads with ``strict=False`` (the unused structural-encoding
-embeddings are the only extra keys).  Projections, LayerNorm, activations and
-the FFN are library GEMMs and elementwise ops (hipBLASLt through torch) except
-for the linear layers' weight and bias gradients, which ``WgradLinear`` runs
-on the library's split-K kernel; run them under
+embeddings are the only extra keys).  Projections, activations and the FFN are
+library GEMMs and elementwise ops (hipBLASLt through torch); the linear layers'
+weight and bias gradients run through ``WgradLinear`` (a row-split GEMM and the
+library's column sums) and the LayerNorms through ``FusedLayerNorm`` (the
+library's fused kernels).  Run them under
 ``torch.autocast("cuda", dtype=torch.bfloat16)`` for the bf16 window step.
 The attention core is ``CoreAttention`` (HIP kernels only).
 
@@ -41,6 +42,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .attention import CoreAttention
+from .layernorm import FusedLayerNorm
 from .linear import WgradLinear
 
 
@@ -146,10 +148,11 @@ class EncoderLayer(nn.Module):
     def __init__(self, hidden_size: int, ffn_size: int, dropout_rate: float,
                  attention_dropout_rate: float, num_heads: int):
         super().__init__()
-        self.self_attention_norm = nn.LayerNorm(hidden_size)
+        # pre-LN: both norms feed only bf16 linear layers (bf16 output under autocast)
+        self.self_attention_norm = FusedLayerNorm(hidden_size, out_bf16=True)
         self.self_attention = MultiHeadAttention(hidden_size, attention_dropout_rate, num_heads)
         self.self_attention_dropout = nn.Dropout(dropout_rate)
-        self.ffn_norm = nn.LayerNorm(hidden_size)
+        self.ffn_norm = FusedLayerNorm(hidden_size, out_bf16=True)
         self.ffn = FeedForwardNetwork(hidden_size, ffn_size, dropout_rate)
         self.ffn_dropout = nn.Dropout(dropout_rate)
 
@@ -175,10 +178,10 @@ class GTEncoderLayer(nn.Module):
         self.self_attention = GTMultiHeadAttention(hidden_size, attention_dropout_rate, num_heads)
         self.self_attention_dropout = nn.Dropout(dropout_rate)
         self.O = WgradLinear(hidden_size, hidden_size)
-        self.layer_norm1 = nn.LayerNorm(hidden_size)
+        self.layer_norm1 = FusedLayerNorm(hidden_size)  # the residual stream: fp32 as autocast
         self.FFN_layer1 = WgradLinear(hidden_size, hidden_size * 2)
         self.FFN_layer2 = WgradLinear(hidden_size * 2, hidden_size)
-        self.layer_norm2 = nn.LayerNorm(hidden_size)
+        self.layer_norm2 = FusedLayerNorm(hidden_size)
 
     def forward(self, x, edge_index=None, attn_type="sparse", kv_cache=None):
         y, score, kv = self.self_attention(x, edge_index, attn_type, kv_cache)
@@ -241,7 +244,7 @@ class WindowGraphormer(_WindowModel):
         self.layers = nn.ModuleList([
             EncoderLayer(hidden_dim, ffn_dim, dropout_rate, attention_dropout_rate, num_heads)
             for _ in range(n_layers)])
-        self.final_ln = nn.LayerNorm(hidden_dim)
+        self.final_ln = FusedLayerNorm(hidden_dim, out_bf16=True)  # feeds the readout linear
         self.downstream_out_proj = WgradLinear(hidden_dim, output_dim)
         self.apply(lambda m: init_params(m, n_layers))
 

@@ -1,0 +1,97 @@
+"""nn.LayerNorm on the library's fused kernels under bf16 autocast.
+
+The encoder's LayerNorms (graphormer_dist_node_level.py:176-206 pre-LN
+``self_attention_norm`` / ``ffn_norm`` and ``final_ln``; the GT twin's post-LN
+``layer_norm1/2``, gt_dist_node_level_single_window.py:305-353).  Under bf16
+autocast torch computes each as: cast the bf16 input to fp32, LayerNorm in
+fp32 (fp32 output), and, where a linear layer consumes it, a cast back to
+bf16; the backward takes three more kernels.  ``FusedLayerNorm`` keeps
+nn.LayerNorm's parameters and state-dict names and runs ``ngt_layernorm_fwd``
+/ ``ngt_layernorm_bwd``: one wave per row, fp32 math on the fp32 or bf16
+input, the output written in fp32 (autocast's type) or, with
+``out_bf16=True`` for a norm whose only consumers are bf16 linear layers,
+directly in bf16 (the rounding the consumer's cast would apply).  dgamma and
+dbeta are fp32 column sums added in a fixed order.  Outside bf16 autocast or
+for unsupported shapes it is a plain nn.LayerNorm.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import torch
+import torch.nn as nn
+
+from . import _lib
+
+_CODES = {torch.float32: _lib.NGT_F32, torch.bfloat16: _lib.NGT_BF16}
+
+
+def _rows(t: torch.Tensor, n_cols: int) -> torch.Tensor:
+    t = t.reshape(-1, n_cols)
+    if not t.is_contiguous() or t.data_ptr() % 8:
+        t = t.clone(memory_format=torch.contiguous_format)
+    return t
+
+
+class _LayerNormFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, weight, bias, eps, out_bf16):
+        lib = _lib.load()
+        n_cols = weight.numel()
+        x2 = _rows(x, n_cols)
+        n = x2.shape[0]
+        dev = x.device
+        y = torch.empty(n, n_cols, device=dev,
+                        dtype=torch.bfloat16 if out_bf16 else torch.float32)
+        mean = torch.empty(n, device=dev, dtype=torch.float32)
+        rstd = torch.empty(n, device=dev, dtype=torch.float32)
+        w = weight.detach().float().contiguous()
+        b = bias.detach().float().contiguous()
+        _lib.check(lib.ngt_layernorm_fwd(_CODES[x2.dtype], x2.data_ptr(), n, n_cols, w.data_ptr(),
+                                         b.data_ptr(), float(eps), _CODES[y.dtype], y.data_ptr(),
+                                         mean.data_ptr(), rstd.data_ptr(),
+                                         torch.cuda.current_stream(dev).cuda_stream))
+        ctx.save_for_backward(x2, w, mean, rstd)
+        ctx.in_shape = x.shape
+        return y.view(*x.shape)
+
+    @staticmethod
+    def backward(ctx, gy):
+        x2, w, mean, rstd = ctx.saved_tensors
+        lib = _lib.load()
+        n, n_cols = x2.shape
+        dev = x2.device
+        if gy.dtype not in _CODES:
+            gy = gy.float()
+        g2 = _rows(gy, n_cols)
+        dx = torch.empty_like(x2)
+        dw = torch.empty(n_cols, device=dev, dtype=torch.float32)
+        db = torch.empty(n_cols, device=dev, dtype=torch.float32)
+        nb = C.c_size_t()
+        _lib.check(lib.ngt_layernorm_bwd_workspace_bytes(n, n_cols, C.byref(nb)))
+        ws = torch.empty(max(nb.value, 1), dtype=torch.uint8, device=dev)
+        _lib.check(lib.ngt_layernorm_bwd(_CODES[x2.dtype], x2.data_ptr(), _CODES[g2.dtype],
+                                         g2.data_ptr(), n, n_cols, w.data_ptr(),
+                                         mean.data_ptr(), rstd.data_ptr(), dx.data_ptr(),
+                                         dw.data_ptr(), db.data_ptr(), ws.data_ptr(), nb.value,
+                                         torch.cuda.current_stream(dev).cuda_stream))
+        return dx.view(*ctx.in_shape), dw, db, None, None
+
+
+class FusedLayerNorm(nn.LayerNorm):
+    """nn.LayerNorm (same parameters and names) on the fused kernels under
+    bf16 autocast; ``out_bf16`` writes the output in bf16 for bf16 consumers."""
+
+    def __init__(self, normalized_shape, eps: float = 1e-5, out_bf16: bool = False, **kw):
+        super().__init__(normalized_shape, eps=eps, **kw)
+        self.out_bf16 = bool(out_bf16)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        n_cols = self.normalized_shape[-1]
+        if (x.is_cuda and len(self.normalized_shape) == 1 and self.elementwise_affine
+                and self.bias is not None and x.dtype in _CODES
+                and torch.is_autocast_enabled("cuda")
+                and torch.get_autocast_dtype("cuda") == torch.bfloat16
+                and n_cols % 4 == 0 and 4 <= n_cols <= 2048):
+            return _LayerNormFn.apply(x, self.weight, self.bias, self.eps, self.out_bf16)
+        return super().forward(x)
