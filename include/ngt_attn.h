@@ -370,6 +370,28 @@ int ngt_layernorm_bwd(int in_dtype, const void* x, int grad_dtype, const void* d
                       size_t workspace_bytes, void* stream);
 
 /*
+ * Residual add, dropout and LayerNorm in one pass (the pre-LN sub-layer
+ * boundary of the Graphormer layer, NeutronGT/models/graphormer_dist_node_level.py:196-206):
+ *   sum = x + dropout_p(y)  (x, y, sum in dtype; sum may be NULL),
+ *   out = LayerNorm(sum)    (out_dtype; mean/rstd fp32 [n_rows]).
+ * sum is rounded to dtype before the LayerNorm reads it.  Element (r, c) is
+ * kept as the dense-attention mask keeps (head 0, query r, key c) for the same
+ * seed, scaled by 1/(1-p); 0 <= p < 1.  The backward takes the saved sum, the
+ * gradients of out and (may be NULL) of sum, and writes dx = g_sum + LN
+ * backward, dy = dx * mask (both in dtype), dgamma/dbeta fp32 (fixed order).
+ * Workspace: ngt_layernorm_bwd_workspace_bytes.
+ */
+int ngt_add_layernorm_fwd(int dtype, const void* x, const void* y, int64_t n_rows, int32_t n_cols,
+                          float dropout_p, uint64_t seed, const float* gamma, const float* beta,
+                          float eps, void* sum, int out_dtype, void* out, float* mean, float* rstd,
+                          void* stream);
+int ngt_add_layernorm_bwd(int dtype, const void* sum, int grad_dtype, const void* g_out,
+                          const void* g_sum, int64_t n_rows, int32_t n_cols, float dropout_p,
+                          uint64_t seed, const float* gamma, const float* mean, const float* rstd,
+                          void* dx, void* dy, float* dgamma, float* dbeta, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/*
  * Column sums of a bf16 matrix in fp32: out[j] = sum_k dy[k][j], dy
  * [n_rows, n_cols] row-major, 16-byte aligned, n_cols a multiple of 8; summed
  * in a fixed order.  The bias gradient of the encoder's linear layers under

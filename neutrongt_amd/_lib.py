@@ -103,6 +103,10 @@ SIGNATURES = {
     "ngt_layernorm_bwd_workspace_bytes": [_i64, _i32, _psz],
     "ngt_layernorm_bwd": [_i32, _vp, _i32, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
                           _vp],
+    "ngt_add_layernorm_fwd": [_i32, _vp, _vp, _i64, _i32, _f32, _u64, _vp, _vp, _f32, _vp, _i32,
+                              _vp, _vp, _vp, _vp],
+    "ngt_add_layernorm_bwd": [_i32, _vp, _i32, _vp, _vp, _i64, _i32, _f32, _u64, _vp, _vp, _vp,
+                              _vp, _vp, _vp, _vp, _vp, _sz, _vp],
     "ngt_colsum_workspace_bytes": [_i64, _i32, _psz],
     "ngt_colsum_bf16": [_vp, _i64, _i32, _vp, _vp, _sz, _vp],
     "ngt_related_workspace_bytes": [_i32, _i32, _psz],

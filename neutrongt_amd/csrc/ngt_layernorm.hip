@@ -15,6 +15,10 @@
 // column partials added in block order by a second pass (deterministic).
 #include "ngt_common.h"
 
+#include <math.h>
+
+#include <type_traits>
+
 namespace ngt {
 namespace {
 
@@ -244,6 +248,199 @@ inline int64_t bwd_blocks(int64_t n_rows) {
   return (n_rows + kRowsPerBwdBlock - 1) / kRowsPerBwdBlock;
 }
 
+
+// ----------------------------------------------- residual add + dropout + LN
+// The pre-LN sub-layer boundary of the Graphormer layer
+// (graphormer_dist_node_level.py:196-206):  s = x + dropout_p(y), out = LN(s),
+// both kept (s is the residual stream).  s is rounded to T before the
+// LayerNorm reads it, as the unfused sequence does.  The dropout bit of
+// element (row, col) is the DropoutMask hash with head 0, query row, key col.
+template <typename T>
+__device__ __forceinline__ float round_to(float v);
+template <>
+__device__ __forceinline__ float round_to<float>(float v) {
+  return v;
+}
+template <>
+__device__ __forceinline__ float round_to<bf16_t>(float v) {
+  return bf16_to_f32(f32_to_bf16(v));
+}
+
+template <bool DROP>
+__device__ __forceinline__ void drop4(const DropoutMask& dm, int64_t row, int col, float (&m)[4]) {
+  if (!DROP) {
+    m[0] = m[1] = m[2] = m[3] = 1.f;
+    return;
+  }
+  const uint32_t w0 = drop_word(dm, uint32_t(row), uint32_t(col));
+  const uint32_t w1 = drop_word(dm, uint32_t(row), uint32_t(col + 2));
+  m[0] = drop_scale(dm, w0, col);
+  m[1] = drop_scale(dm, w0, col + 1);
+  m[2] = drop_scale(dm, w1, col + 2);
+  m[3] = drop_scale(dm, w1, col + 3);
+}
+
+template <typename T, typename TO, int Q, bool DROP>
+__global__ __launch_bounds__(kBlock) void k_add_ln_fwd(
+    const T* __restrict__ x, const T* __restrict__ y, int64_t n_rows, int32_t n_cols,
+    DropoutMask dm, const float* __restrict__ gamma, const float* __restrict__ beta, float eps,
+    T* __restrict__ sum, TO* __restrict__ out, float* __restrict__ mean,
+    float* __restrict__ rstd) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = int64_t(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+  if (row >= n_rows) return;  // whole wave; no block barrier follows
+  const int nq = n_cols / 4;
+  float v[Q][4];
+  float sacc = 0.f;
+#pragma unroll
+  for (int j = 0; j < Q; ++j) {
+    const int qd = lane + j * kWave;
+    if (qd < nq) {
+      float xv[4], yv[4], m[4];
+      load4f<T>(x + row * n_cols + 4 * qd, xv);
+      load4f<T>(y + row * n_cols + 4 * qd, yv);
+      drop4<DROP>(dm, row, 4 * qd, m);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        v[j][c] = round_to<T>(xv[c] + yv[c] * m[c]);
+        sacc += v[j][c];
+      }
+      if (sum) store4f<T>(sum + row * n_cols + 4 * qd, v[j]);
+    }
+  }
+  const float mu = wave_sum(sacc) / float(n_cols);
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < Q; ++j) {
+    const int qd = lane + j * kWave;
+    if (qd < nq) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float dlt = v[j][c] - mu;
+        ss = fmaf(dlt, dlt, ss);
+      }
+    }
+  }
+  const float rs = 1.0f / sqrtf(wave_sum(ss) / float(n_cols) + eps);
+#pragma unroll
+  for (int j = 0; j < Q; ++j) {
+    const int qd = lane + j * kWave;
+    if (qd < nq) {
+      float o[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int col = 4 * qd + c;
+        o[c] = fmaf((v[j][c] - mu) * rs, gamma[col], beta[col]);
+      }
+      store4f<TO>(out + row * n_cols + 4 * qd, o);
+    }
+  }
+  if (lane == 0) {
+    mean[row] = mu;
+    rstd[row] = rs;
+  }
+}
+
+// ds = g_sum + LN backward of g_out (at s); dx = ds, dy = ds * mask; block
+// partials of dgamma / dbeta as in k_ln_bwd.
+template <typename T, typename TG, int Q, bool DROP>
+__global__ __launch_bounds__(kBlock) void k_add_ln_bwd(
+    const T* __restrict__ sum, const TG* __restrict__ g_out, const T* __restrict__ g_sum,
+    int64_t n_rows, int32_t n_cols, DropoutMask dm, const float* __restrict__ gamma,
+    const float* __restrict__ mean, const float* __restrict__ rstd, T* __restrict__ dx,
+    T* __restrict__ dy, float* __restrict__ part) {
+  extern __shared__ float red[];  // [kWaves][2 * n_cols]
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x >> 6;
+  const int nq = n_cols / 4;
+  float dg[Q][4], db[Q][4];
+#pragma unroll
+  for (int j = 0; j < Q; ++j)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) dg[j][c] = db[j][c] = 0.f;
+  const int64_t r0 = int64_t(blockIdx.x) * kRowsPerBwdBlock;
+  for (int rr = wave; rr < kRowsPerBwdBlock; rr += kWaves) {
+    const int64_t row = r0 + rr;
+    if (row >= n_rows) break;
+    const float mu = mean[row], rs = rstd[row];
+    float xh[Q][4], g[Q][4];
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int j = 0; j < Q; ++j) {
+      const int qd = lane + j * kWave;
+      if (qd < nq) {
+        float sv[4], dv[4];
+        load4f<T>(sum + row * n_cols + 4 * qd, sv);
+        load4f<TG>(g_out + row * n_cols + 4 * qd, dv);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          xh[j][c] = (sv[c] - mu) * rs;
+          g[j][c] = dv[c] * gamma[4 * qd + c];
+          s1 += g[j][c];
+          s2 = fmaf(g[j][c], xh[j][c], s2);
+          dg[j][c] = fmaf(dv[c], xh[j][c], dg[j][c]);
+          db[j][c] += dv[c];
+        }
+      }
+    }
+    const float c1 = wave_sum(s1) / float(n_cols);
+    const float c2 = wave_sum(s2) / float(n_cols);
+#pragma unroll
+    for (int j = 0; j < Q; ++j) {
+      const int qd = lane + j * kWave;
+      if (qd < nq) {
+        float gs[4] = {0.f, 0.f, 0.f, 0.f}, m[4], o[4], oy[4];
+        if (g_sum) load4f<T>(g_sum + row * n_cols + 4 * qd, gs);
+        drop4<DROP>(dm, row, 4 * qd, m);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          o[c] = gs[c] + rs * (g[j][c] - c1 - xh[j][c] * c2);
+          oy[c] = o[c] * m[c];
+        }
+        store4f<T>(dx + row * n_cols + 4 * qd, o);
+        store4f<T>(dy + row * n_cols + 4 * qd, oy);
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < Q; ++j) {
+    const int qd = lane + j * kWave;
+    if (qd < nq) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        red[wave * 2 * n_cols + 4 * qd + c] = dg[j][c];
+        red[wave * 2 * n_cols + n_cols + 4 * qd + c] = db[j][c];
+      }
+    }
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < 2 * n_cols; t += kBlock) {
+    float a = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) a += red[w * 2 * n_cols + t];
+    part[int64_t(blockIdx.x) * 2 * n_cols + t] = a;
+  }
+}
+
+// Dropout parameters of the fused op (p in [0, 1)); *on = false for p = 0.
+int add_ln_dropout(const char* fn, float p, uint64_t seed, int64_t n_rows, int n_cols,
+                   DropoutMask* dm, bool* on) {
+  *on = false;
+  if (!(p >= 0.f && p < 1.f))
+    return set_error(NGT_ERR_ARG, "%s: dropout_p=%g outside [0, 1)", fn, double(p));
+  if (p == 0.f) return NGT_OK;
+  const uint64_t n_kp = (uint64_t(n_cols) + 1) / 2;
+  if (uint64_t(n_rows) * n_kp > (uint64_t(1) << 32))
+    return set_error(NGT_ERR_UNSUPPORTED, "%s: dropout needs n_rows * n_cols / 2 <= 2^32", fn);
+  dm->seed = seed;
+  dm->head_key = drop_head_key(seed, 0);
+  dm->n_kp = static_cast<uint32_t>(n_kp);
+  dm->thr = static_cast<uint32_t>(lrint(double(p) * 65536.0));
+  dm->scale = static_cast<float>(1.0 / (1.0 - double(p)));
+  *on = true;
+  return NGT_OK;
+}
+
 }  // namespace
 }  // namespace ngt
 
@@ -351,6 +548,131 @@ extern "C" int ngt_layernorm_bwd(int in_dtype, const void* x, int grad_dtype, co
     hipLaunchKernelGGL(k_ln_bwd_reduce, dim3((2 * n_cols + kRedCols - 1) / kRedCols), dim3(kBlock), 0,
                        st, static_cast<const float*>(workspace), static_cast<int32_t>(nb), n_cols,
                        dgamma, dbeta);
+    NGT_HIP_CHECK(hipGetLastError());
+  }
+  return NGT_OK;
+}
+
+extern "C" int ngt_add_layernorm_fwd(int dtype, const void* x, const void* y, int64_t n_rows,
+                                     int32_t n_cols, float dropout_p, uint64_t seed,
+                                     const float* gamma, const float* beta, float eps, void* sum,
+                                     int out_dtype, void* out, float* mean, float* rstd,
+                                     void* stream) {
+  NGT_CHECK_OK(check("ngt_add_layernorm_fwd", dtype, n_rows, n_cols));
+  NGT_CHECK_OK(check("ngt_add_layernorm_fwd", out_dtype, n_rows, n_cols));
+  DropoutMask dm{};
+  bool drop = false;
+  NGT_CHECK_OK(add_ln_dropout("ngt_add_layernorm_fwd", dropout_p, seed, n_rows, n_cols, &dm, &drop));
+  if (n_rows == 0) return NGT_OK;
+  if (!x || !y || !gamma || !beta || !out || !mean || !rstd)
+    return set_error(NGT_ERR_ARG, "ngt_add_layernorm_fwd: null pointer");
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y) |
+       reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(sum)) & 7)
+    return set_error(NGT_ERR_ARG, "ngt_add_layernorm_fwd: rows must be 8-byte aligned");
+  if (!(eps >= 0.f)) return set_error(NGT_ERR_ARG, "ngt_add_layernorm_fwd: eps must be >= 0");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t blocks = (n_rows + kWaves - 1) / kWaves;
+  if (blocks > 0x7fffffff)
+    return set_error(NGT_ERR_UNSUPPORTED, "ngt_add_layernorm_fwd: too many rows");
+  const int nq = quads_for(n_cols);
+  KernelTimer timer_("add_layernorm_fwd", st);
+  auto launch = [&](auto t, auto to, auto dr) {
+    using T = decltype(t);
+    using TO = decltype(to);
+    constexpr bool D = decltype(dr)::value;
+    const dim3 g(static_cast<unsigned>(blocks)), b(kBlock);
+    const T* xx = static_cast<const T*>(x);
+    const T* yy = static_cast<const T*>(y);
+    T* ss = static_cast<T*>(sum);
+    TO* oo = static_cast<TO*>(out);
+    switch (nq) {
+      case 1: hipLaunchKernelGGL((k_add_ln_fwd<T, TO, 1, D>), g, b, 0, st, xx, yy, n_rows, n_cols, dm, gamma, beta, eps, ss, oo, mean, rstd); break;
+      case 2: hipLaunchKernelGGL((k_add_ln_fwd<T, TO, 2, D>), g, b, 0, st, xx, yy, n_rows, n_cols, dm, gamma, beta, eps, ss, oo, mean, rstd); break;
+      case 3: hipLaunchKernelGGL((k_add_ln_fwd<T, TO, 3, D>), g, b, 0, st, xx, yy, n_rows, n_cols, dm, gamma, beta, eps, ss, oo, mean, rstd); break;
+      case 4: hipLaunchKernelGGL((k_add_ln_fwd<T, TO, 4, D>), g, b, 0, st, xx, yy, n_rows, n_cols, dm, gamma, beta, eps, ss, oo, mean, rstd); break;
+      case 6: hipLaunchKernelGGL((k_add_ln_fwd<T, TO, 6, D>), g, b, 0, st, xx, yy, n_rows, n_cols, dm, gamma, beta, eps, ss, oo, mean, rstd); break;
+      default: hipLaunchKernelGGL((k_add_ln_fwd<T, TO, 8, D>), g, b, 0, st, xx, yy, n_rows, n_cols, dm, gamma, beta, eps, ss, oo, mean, rstd); break;
+    }
+  };
+  auto with_drop = [&](auto t, auto to) {
+    if (drop)
+      launch(t, to, std::true_type{});
+    else
+      launch(t, to, std::false_type{});
+  };
+  if (dtype == NGT_F32)
+    out_dtype == NGT_F32 ? with_drop(float{}, float{}) : with_drop(float{}, bf16_t{});
+  else
+    out_dtype == NGT_F32 ? with_drop(bf16_t{}, float{}) : with_drop(bf16_t{}, bf16_t{});
+  NGT_HIP_CHECK(hipGetLastError());
+  return NGT_OK;
+}
+
+extern "C" int ngt_add_layernorm_bwd(int dtype, const void* sum, int grad_dtype,
+                                     const void* g_out, const void* g_sum, int64_t n_rows,
+                                     int32_t n_cols, float dropout_p, uint64_t seed,
+                                     const float* gamma, const float* mean, const float* rstd,
+                                     void* dx, void* dy, float* dgamma, float* dbeta,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+  NGT_CHECK_OK(check("ngt_add_layernorm_bwd", dtype, n_rows, n_cols));
+  NGT_CHECK_OK(check("ngt_add_layernorm_bwd", grad_dtype, n_rows, n_cols));
+  DropoutMask dm{};
+  bool drop = false;
+  NGT_CHECK_OK(add_ln_dropout("ngt_add_layernorm_bwd", dropout_p, seed, n_rows, n_cols, &dm, &drop));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t nb = bwd_blocks(n_rows);
+  if (nb > 0) {
+    if (!sum || !g_out || !gamma || !mean || !rstd || !dx || !dy)
+      return set_error(NGT_ERR_ARG, "ngt_add_layernorm_bwd: null pointer");
+    if ((reinterpret_cast<uintptr_t>(sum) | reinterpret_cast<uintptr_t>(g_out) |
+         reinterpret_cast<uintptr_t>(g_sum) | reinterpret_cast<uintptr_t>(dx) |
+         reinterpret_cast<uintptr_t>(dy)) & 7)
+      return set_error(NGT_ERR_ARG, "ngt_add_layernorm_bwd: rows must be 8-byte aligned");
+    const size_t need = size_t(nb) * 2 * n_cols * 4;
+    if (!workspace || workspace_bytes < need)
+      return set_error(NGT_ERR_WORKSPACE, "ngt_add_layernorm_bwd: workspace %zu < %zu",
+                       workspace_bytes, need);
+    if (nb > 0x7fffffff)
+      return set_error(NGT_ERR_UNSUPPORTED, "ngt_add_layernorm_bwd: too many rows");
+    KernelTimer timer_("add_layernorm_bwd", st);
+    const size_t lds = size_t(kWaves) * 2 * n_cols * 4;
+    float* part = static_cast<float*>(workspace);
+    const int nq = quads_for(n_cols);
+    auto launch = [&](auto t, auto tg, auto dr) {
+      using T = decltype(t);
+      using TG = decltype(tg);
+      constexpr bool D = decltype(dr)::value;
+      const dim3 g(static_cast<unsigned>(nb)), b(kBlock);
+      const T* ss = static_cast<const T*>(sum);
+      const TG* go = static_cast<const TG*>(g_out);
+      const T* gs = static_cast<const T*>(g_sum);
+      T* ox = static_cast<T*>(dx);
+      T* oy = static_cast<T*>(dy);
+      switch (nq) {
+        case 1: hipLaunchKernelGGL((k_add_ln_bwd<T, TG, 1, D>), g, b, lds, st, ss, go, gs, n_rows, n_cols, dm, gamma, mean, rstd, ox, oy, part); break;
+        case 2: hipLaunchKernelGGL((k_add_ln_bwd<T, TG, 2, D>), g, b, lds, st, ss, go, gs, n_rows, n_cols, dm, gamma, mean, rstd, ox, oy, part); break;
+        case 3: hipLaunchKernelGGL((k_add_ln_bwd<T, TG, 3, D>), g, b, lds, st, ss, go, gs, n_rows, n_cols, dm, gamma, mean, rstd, ox, oy, part); break;
+        case 4: hipLaunchKernelGGL((k_add_ln_bwd<T, TG, 4, D>), g, b, lds, st, ss, go, gs, n_rows, n_cols, dm, gamma, mean, rstd, ox, oy, part); break;
+        case 6: hipLaunchKernelGGL((k_add_ln_bwd<T, TG, 6, D>), g, b, lds, st, ss, go, gs, n_rows, n_cols, dm, gamma, mean, rstd, ox, oy, part); break;
+        default: hipLaunchKernelGGL((k_add_ln_bwd<T, TG, 8, D>), g, b, lds, st, ss, go, gs, n_rows, n_cols, dm, gamma, mean, rstd, ox, oy, part); break;
+      }
+    };
+    auto with_drop = [&](auto t, auto tg) {
+      if (drop)
+        launch(t, tg, std::true_type{});
+      else
+        launch(t, tg, std::false_type{});
+    };
+    if (dtype == NGT_F32)
+      grad_dtype == NGT_F32 ? with_drop(float{}, float{}) : with_drop(float{}, bf16_t{});
+    else
+      grad_dtype == NGT_F32 ? with_drop(bf16_t{}, float{}) : with_drop(bf16_t{}, bf16_t{});
+    NGT_HIP_CHECK(hipGetLastError());
+  }
+  if (dgamma || dbeta) {
+    hipLaunchKernelGGL(k_ln_bwd_reduce, dim3((2 * n_cols + kRedCols - 1) / kRedCols), dim3(kBlock),
+                       0, st, static_cast<const float*>(workspace), static_cast<int32_t>(nb),
+                       n_cols, dgamma, dbeta);
     NGT_HIP_CHECK(hipGetLastError());
   }
   return NGT_OK;

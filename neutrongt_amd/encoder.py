@@ -42,7 +42,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .attention import CoreAttention
-from .layernorm import FusedLayerNorm
+from .layernorm import FusedLayerNorm, add_dropout_layernorm
 from .linear import WgradLinear
 
 
@@ -159,8 +159,9 @@ class EncoderLayer(nn.Module):
     def forward(self, x, edge_index=None, attn_type="sparse", kv_cache=None):
         y, score, kv = self.self_attention(self.self_attention_norm(x), edge_index, attn_type,
                                            kv_cache)
-        x = x + self.self_attention_dropout(y)
-        x = x + self.ffn_dropout(self.ffn(self.ffn_norm(x)))
+        # x + Drop(y) and the FFN's LayerNorm of it: one fused pass under bf16 autocast
+        x, h = add_dropout_layernorm(x, y, self.ffn_norm, self.self_attention_dropout)
+        x = x + self.ffn_dropout(self.ffn(h))
         return x, score, kv
 
 

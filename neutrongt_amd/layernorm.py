@@ -20,6 +20,7 @@ import ctypes as C
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 from . import _lib
 
@@ -95,3 +96,77 @@ class FusedLayerNorm(nn.LayerNorm):
                 and n_cols % 4 == 0 and 4 <= n_cols <= 2048):
             return _LayerNormFn.apply(x, self.weight, self.bias, self.eps, self.out_bf16)
         return super().forward(x)
+
+
+def _fused_ok(x: torch.Tensor, ln: nn.LayerNorm) -> bool:
+    n_cols = ln.normalized_shape[-1]
+    return (isinstance(ln, FusedLayerNorm) and x.is_cuda and len(ln.normalized_shape) == 1
+            and ln.elementwise_affine and ln.bias is not None and x.dtype in _CODES
+            and torch.is_autocast_enabled("cuda")
+            and torch.get_autocast_dtype("cuda") == torch.bfloat16
+            and n_cols % 4 == 0 and 4 <= n_cols <= 2048)
+
+
+class _AddLayerNormFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, y, weight, bias, eps, p, seed, out_bf16):
+        lib = _lib.load()
+        n_cols = weight.numel()
+        x2, y2 = _rows(x, n_cols), _rows(y, n_cols)
+        n = x2.shape[0]
+        dev = x.device
+        s = torch.empty_like(x2)
+        out = torch.empty(n, n_cols, device=dev,
+                          dtype=torch.bfloat16 if out_bf16 else torch.float32)
+        mean = torch.empty(n, device=dev, dtype=torch.float32)
+        rstd = torch.empty(n, device=dev, dtype=torch.float32)
+        w = weight.detach().float().contiguous()
+        b = bias.detach().float().contiguous()
+        _lib.check(lib.ngt_add_layernorm_fwd(
+            _CODES[x2.dtype], x2.data_ptr(), y2.data_ptr(), n, n_cols, float(p), int(seed),
+            w.data_ptr(), b.data_ptr(), float(eps), s.data_ptr(), _CODES[out.dtype],
+            out.data_ptr(), mean.data_ptr(), rstd.data_ptr(),
+            torch.cuda.current_stream(dev).cuda_stream))
+        ctx.save_for_backward(s, w, mean, rstd)
+        ctx.p, ctx.seed, ctx.shape = float(p), int(seed), x.shape
+        return s.view(*x.shape), out.view(*x.shape)
+
+    @staticmethod
+    def backward(ctx, g_s, g_out):
+        s, w, mean, rstd = ctx.saved_tensors
+        lib = _lib.load()
+        n, n_cols = s.shape
+        dev = s.device
+        if g_out is None:
+            g_out = torch.zeros(n, n_cols, device=dev, dtype=torch.float32)
+        g_out2 = _rows(g_out if g_out.dtype in _CODES else g_out.float(), n_cols)
+        g_s2 = _rows(g_s.to(s.dtype), n_cols) if g_s is not None else None
+        dx = torch.empty_like(s)
+        dy = torch.empty_like(s)
+        dw = torch.empty(n_cols, device=dev, dtype=torch.float32)
+        db = torch.empty(n_cols, device=dev, dtype=torch.float32)
+        nb = C.c_size_t()
+        _lib.check(lib.ngt_layernorm_bwd_workspace_bytes(n, n_cols, C.byref(nb)))
+        ws = torch.empty(max(nb.value, 1), dtype=torch.uint8, device=dev)
+        _lib.check(lib.ngt_add_layernorm_bwd(
+            _CODES[s.dtype], s.data_ptr(), _CODES[g_out2.dtype], g_out2.data_ptr(),
+            g_s2.data_ptr() if g_s2 is not None else None, n, n_cols, ctx.p, ctx.seed,
+            w.data_ptr(), mean.data_ptr(), rstd.data_ptr(), dx.data_ptr(), dy.data_ptr(),
+            dw.data_ptr(), db.data_ptr(), ws.data_ptr(), nb.value,
+            torch.cuda.current_stream(dev).cuda_stream))
+        return dx.view(*ctx.shape), dy.view(*ctx.shape), dw, db, None, None, None, None
+
+
+def add_dropout_layernorm(x: torch.Tensor, y: torch.Tensor, ln: nn.LayerNorm,
+                          dropout: nn.Dropout):
+    """(s, ln(s)) with s = x + dropout(y): the residual add and the LayerNorm
+    that follows it, as one pass of ``ngt_add_layernorm_fwd`` under bf16
+    autocast (the dropout mask then comes from this library's hash, seeded
+    from torch's generator); otherwise the unfused torch ops."""
+    p = dropout.p if dropout.training else 0.0
+    if (_fused_ok(x, ln) and y.dtype == x.dtype and y.shape == x.shape and p < 1.0
+            and torch.is_grad_enabled()):
+        seed = int(torch.randint(0, 2**62, (1,), dtype=torch.int64).item()) if p > 0 else 0
+        return _AddLayerNormFn.apply(x, y, ln.weight, ln.bias, ln.eps, p, seed, ln.out_bf16)
+    s = x + F.dropout(y, p, dropout.training) if p > 0 else x + y
+    return s, ln(s)

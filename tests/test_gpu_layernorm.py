@@ -80,3 +80,43 @@ def test_fused_layernorm_module_under_autocast():
         ref.weight.grad = ref.bias.grad = None
     # outside autocast: nn.LayerNorm itself
     assert torch.equal(mod(x.detach().float()), ref(x.detach().float()))
+
+
+@pytest.mark.parametrize("n,c,dt,p", [(32768, 768, torch.bfloat16, 0.3), (1000, 128, torch.float32, 0.5),
+                                      (513, 64, torch.bfloat16, 0.0), (7, 2048, torch.float32, 0.1)])
+def test_add_dropout_layernorm_matches_fp64(n, c, dt, p):
+    """s = x + dropout(y), out = LN(s) in one pass, against the same formula
+    in float64 with the oracle's mask; dx = dS + LN backward, dy = dx * mask."""
+    from neutrongt_amd.layernorm import _AddLayerNormFn
+    from oracle import attention as OA
+    _say(f"case add+dropout+LN n={n} c={c} {dt} p={p}")
+    g = torch.Generator(device="cuda").manual_seed(n + c)
+    x = torch.randn(n, c, device="cuda", generator=g).to(dt)
+    y = torch.randn(n, c, device="cuda", generator=g).to(dt)
+    w = torch.randn(c, device="cuda", generator=g)
+    b = torch.randn(c, device="cuda", generator=g)
+    g_s = torch.randn(n, c, device="cuda", generator=g).to(dt)
+    g_o = torch.randn(n, c, device="cuda", generator=g).to(dt)
+    seed = 1234 + n
+    xr, yr = x.clone().requires_grad_(True), y.clone().requires_grad_(True)
+    wr, br = w.clone().requires_grad_(True), b.clone().requires_grad_(True)
+    s, out = _AddLayerNormFn.apply(xr, yr, wr, br, 1e-5, p, seed, dt == torch.bfloat16)
+    (s.float() * g_s.float()).sum().add_((out.float() * g_o.float()).sum()).backward()
+    mult = torch.from_numpy(OA.dropout_multiplier(seed, 1, n, c, p)[0]).cuda().double()
+    s_ref = (x.double() + y.double() * mult).to(dt)  # the stored sum is in the input dtype
+    if p == 0.0:
+        assert torch.equal(s, s_ref)
+    assert relerr(s, s_ref) < (5e-3 if dt == torch.bfloat16 else 1e-6)
+    s64 = s.detach().double().requires_grad_(True)
+    w64, b64 = w.double().requires_grad_(True), b.double().requires_grad_(True)
+    o64 = F.layer_norm(s64, (c,), w64, b64, 1e-5)
+    (o64 * g_o.double()).sum().backward()
+    assert relerr(out, o64) < (5e-3 if dt == torch.bfloat16 else 1e-5)
+    dx64 = s64.grad + g_s.double()
+    tol = 5e-3 if dt == torch.bfloat16 else 1e-5
+    assert relerr(xr.grad, dx64) < tol
+    assert relerr(yr.grad, dx64 * mult) < tol
+    assert relerr(wr.grad, w64.grad) < 1e-5 and relerr(br.grad, b64.grad) < 1e-5
+    if p > 0:
+        kept = (mult > 0).float().mean().item()
+        assert abs(kept - (1 - p)) < 0.02
