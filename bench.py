@@ -101,6 +101,58 @@ def measured_traffic(config: str, kernel: str):
     return float(rec["read_bytes"]) + float(rec["write_bytes"])
 
 
+# Rows each sparse kernel gathers per edge, as (table rows, row bytes factor):
+# the forward K and V rows of all keys, the key-major pass Q and dO rows of the
+# queries, the query-major pass K rows.
+GATHER_TABLES = {"sparse_fwd": lambda n_q, n_k: 2 * n_k,
+                 "sparse_bwd_kv": lambda n_q, n_k: 2 * n_q,
+                 "sparse_bwd_q": lambda n_q, n_k: n_k}
+
+
+def gather_ceiling(kernel: str, cfg, n_k: int, dev, n_idx: int = 1 << 22, reps: int = 5):
+    """Measured ceiling for the dominant sparse kernel's access pattern:
+    ngt_probe_gather over a table as large as the rows that kernel gathers
+    (e.g. Q and dO of every query for the key-major pass), with uniform random
+    indices, so nearly every row misses L2.  Returns GB/s of gathered rows,
+    timed by the library's hipEvents like the kernels."""
+    import ctypes as C
+
+    import torch
+
+    from neutrongt_amd import _lib
+
+    rows_fn = GATHER_TABLES.get(kernel)
+    if rows_fn is None:
+        return None
+    row_bytes = _elem_bytes(cfg.dtype) * cfg.n_heads * cfg.head_dim
+    n_rows = rows_fn(cfg.n_q, n_k)
+    table = torch.ones(n_rows * row_bytes // 4, dtype=torch.int32, device=dev)
+    g = torch.Generator(device="cpu").manual_seed(7)
+    idx = torch.randint(0, n_rows, (n_idx,), generator=g, dtype=torch.int32).to(dev)
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    lib = _lib.load()
+    st = C.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+    def launch():
+        _lib.check(lib.ngt_probe_gather(C.c_void_p(table.data_ptr()), n_rows, row_bytes,
+                                        C.c_void_p(idx.data_ptr()), n_idx,
+                                        C.c_void_p(sink.data_ptr()), st))
+    launch()
+    torch.cuda.synchronize()
+    _lib.timing_enable(True)
+    _lib.timing_summary()
+    for _ in range(reps):
+        launch()
+    torch.cuda.synchronize()
+    summ = _lib.timing_summary()
+    _lib.timing_enable(False)
+    cnt, ms = summ["probe_gather"]
+    gbs = n_idx * row_bytes / (ms / cnt * 1e-3) / 1e9
+    del table, idx, sink
+    return {"row_bytes": row_bytes, "table_MB": n_rows * row_bytes / 1e6, "indices": n_idx,
+            "distribution": "uniform", "gather_GBs": gbs}
+
+
 def cpu_baseline(cfg, ei_np, n_k, target_s: float = 3.0):
     """The reference's op sequence (CPU oracle, fp32) on the in-edges of a
     seeded random subset of the window's query rows, sized so one fwd+bwd takes
@@ -653,6 +705,18 @@ def main(argv=None) -> int:
         roof = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": ach / HBM_PEAK_GBS, "traffic": traffic, "kernel": dom,
                 "bytes_per_launch": kb, "avg_launch_us": dom_avg_s * 1e6}
+        # The kernel's measured HBM/fabric bytes per second against the rate a
+        # pure random-row gather of the same table reaches on this GPU.
+        ceil = gather_ceiling(dom, cfg, n_k, dev)
+        if ceil is not None:
+            if traffic is not None:
+                ceil["kernel_traffic_GBs"] = traffic / dom_avg_s / 1e9
+                ceil["kernel_traffic_frac"] = ceil["kernel_traffic_GBs"] / ceil["gather_GBs"]
+            roof["gather_ceiling"] = ceil
+            _log(f"[bench] uniform random {ceil['row_bytes']}-byte row gathers from a "
+                 f"{ceil['table_MB']:.0f} MB table: {ceil['gather_GBs']:.0f} GB/s"
+                 + (f"; {dom} moves {ceil['kernel_traffic_GBs']:.0f} GB/s of measured traffic"
+                    if traffic is not None else ""))
         pb = path_bytes(cfg, n_k, E)
         path = {"algorithmic_bytes_per_layer": pb,
                 "achieved_GBs": pb * layers / (ms_step * 1e-3) / 1e9,

@@ -350,6 +350,18 @@ int ngt_timing_enable(int on);
 int ngt_timing_summary(char* buf, size_t len);
 
 /*
+ * Random row-gather probe (no counterpart in the reference: a measured
+ * ceiling for the benchmark's roofline).  Gathers row idx[e] (int32, rows
+ * outside [0, n_rows) are skipped) of a table of n_rows rows of row_bytes
+ * bytes for e < n_idx, whole rows by 16-byte loads in the wave layout of the
+ * sparse kernels, and discards the data (sink: device uint32, written only in
+ * a case that does not occur with real data).  row_bytes must be 16 x (1..4)
+ * x a power of two <= 64.  Timed as "probe_gather" while timing is enabled.
+ */
+int ngt_probe_gather(const void* table, int64_t n_rows, int64_t row_bytes, const int32_t* idx,
+                     int64_t n_idx, uint32_t* sink, void* stream);
+
+/*
  * LayerNorm over the last dimension (n_cols, a multiple of 4, at most 2048):
  *   y = (x - mean) / sqrt(var + eps) * gamma + beta per row, fp32 math,
  *   x in in_dtype, y in out_dtype (NGT_F32 or NGT_BF16), mean/rstd [n_rows]

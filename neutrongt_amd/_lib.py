@@ -123,6 +123,7 @@ SIGNATURES = {
     "ngt_subgraph_csr": [_vp, _vp, _i64, _i64, _vp, _i32, _vp, _i64, _vp, _vp, _sz, _vp],
     "ngt_timing_enable": [_i32],
     "ngt_timing_summary": [C.c_char_p, _sz],
+    "ngt_probe_gather": [_vp, _i64, _i64, _vp, _i64, _vp, _vp],
 }
 _RESTYPES = {"ngt_last_error": C.c_char_p}
 

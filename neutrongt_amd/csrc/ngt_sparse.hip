@@ -48,6 +48,28 @@ __device__ __forceinline__ float clampf(float a, float lo, float hi) {
   return fminf(fmaxf(a, lo), hi);
 }
 
+// Sum of x[p * stride] for p = first, first + step, ... < n, added in that
+// order.  The loads go out in batches of 8, so a split row's many partials
+// are not one chain of dependent loads; the additions keep the plain loop's
+// order (the same bits).
+__device__ __forceinline__ float strided_sum(const float* __restrict__ x, int first, int n,
+                                             int step, int64_t stride) {
+  constexpr int B = 8;
+  float a = 0.f;
+  for (int p0 = first; p0 < n; p0 += B * step) {
+    float v[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      const int p = p0 + u * step;
+      v[u] = p < n ? x[int64_t(p) * stride] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < B; ++u)
+      if (p0 + u * step < n) a += v[u];
+  }
+  return a;
+}
+
 // Key rows: rows j < n_main of k/v, then rows j - n_main of k_ext/v_ext (a
 // second buffer, e.g. the detached cache of related keys, so the caller need
 // not concatenate it).  With one buffer k_ext = k, v_ext = v and n_main = n_k.
@@ -226,8 +248,8 @@ __device__ __forceinline__ float fwd_packed(const T* __restrict__ q, const Keys<
 // With one head group (every head of a row in one wave) the node score
 // mean_h Z[i,h] of a row that is not split is reduced across the row's head
 // lanes and written here; split rows get theirs in the finalize.  ns is null
-// when no node scores are wanted or with several head groups (then
-// k_node_score reads zbuf).
+// when no node scores are wanted or with several head groups (then the
+// finalize launch computes them from zbuf).
 template <typename T, int DH, bool EXT>
 __global__ __launch_bounds__(kBlock) void k_fwd(
     const T* __restrict__ q, const Keys<T, EXT> kv,
@@ -325,37 +347,49 @@ __global__ __launch_bounds__(kBlock) void k_fwd(
 }
 
 // Split rows: column c of the H*DH output columns of row sp.x is the sum of
-// that column over the row's partial slots.  grid = (n_splits, col tiles);
-// the 4 waves of a block take every 4th part and meet in LDS.
+// that column over the row's partial slots.  Blocks [0, n_splits * tiles) take
+// (split row, 64-column tile); the 4 waves of a block take every 4th part and
+// meet in LDS.  Tile 0 of a split row also writes its node score from the
+// parts' Z.  The launch's first ns_blocks blocks (dispatched first, so they
+// overlap the tiles) write the node scores of the rows that are not split
+// (degree <= chunk) from zbuf, which the forward kernel has completed; split
+// rows are left to their tile 0.
 template <typename T, int DH>
 __global__ __launch_bounds__(kBlock) void k_fwd_finalize(
-    const int4* __restrict__ splits, int32_t H, float eps, const float* __restrict__ part_acc,
-    const float* __restrict__ part_z, T* __restrict__ out, float* __restrict__ rinv,
-    float* __restrict__ zbuf, float* __restrict__ ns, int32_t ns_len) {
+    const int4* __restrict__ splits, int32_t tiles, int32_t H, float eps,
+    const float* __restrict__ part_acc, const float* __restrict__ part_z, T* __restrict__ out,
+    float* __restrict__ rinv, float* __restrict__ zbuf, float* __restrict__ ns, int32_t ns_len,
+    const int32_t* __restrict__ rowptr, int32_t chunk, int32_t ns_blocks) {
   __shared__ float red[3][kWavesPerBlock][kColTile];
-  const int4 sp = splits[blockIdx.x];
+  if (int32_t(blockIdx.x) < ns_blocks) {
+    const int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+    if (i >= ns_len || rowptr[i + 1] - rowptr[i] > chunk) return;
+    ns[i] = strided_sum(zbuf + i * H, 0, H, 1, 1) / float(H);
+    return;
+  }
+  const unsigned fb = blockIdx.x - unsigned(ns_blocks);
+  const int split = int(fb / unsigned(tiles));
+  const int tile = int(fb % unsigned(tiles));
+  const int4 sp = splits[split];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
   // node score of the split row (tile 0 only): lanes = heads (H <= 64), the 4
   // waves take every 4th part, meet in LDS below
-  const bool want_ns = ns && blockIdx.y == 0 && sp.x < ns_len;
+  const bool want_ns = ns && tile == 0 && sp.x < ns_len;
   if (want_ns) {
-    float zh = 0.f;
-    if (lane < H)
-      for (int p = wave; p < sp.z; p += kWavesPerBlock) zh += part_z[int64_t(sp.y + p) * H + lane];
+    const float zh = lane < H ? strided_sum(part_z + int64_t(sp.y) * H + lane, wave, sp.z,
+                                            kWavesPerBlock, H)
+                              : 0.f;
     red[2][wave][lane] = zh;
   }
   const int ncols = H * DH;
-  const int col = blockIdx.y * kColTile + lane;
+  const int col = tile * kColTile + lane;
   const bool ok = col < ncols;
   const int h = ok ? col / DH : 0;
   float a = 0.f, z = 0.f;
   if (ok) {
-    for (int p = wave; p < sp.z; p += kWavesPerBlock) {
-      const int64_t base = int64_t(sp.y + p);
-      a += part_acc[base * ncols + col];
-      z += part_z[base * H + h];
-    }
+    a = strided_sum(part_acc + int64_t(sp.y) * ncols + col, wave, sp.z, kWavesPerBlock, ncols);
+    z = strided_sum(part_z + int64_t(sp.y) * H + h, wave, sp.z, kWavesPerBlock, H);
   }
   red[0][wave][lane] = a;
   red[1][wave][lane] = z;
@@ -379,18 +413,6 @@ __global__ __launch_bounds__(kBlock) void k_fwd_finalize(
   if (col % DH == 0) {
     rinv[row * H + h] = 1.0f / den;
     zbuf[row * H + h] = z;
-  }
-}
-
-// node_score[i] = sum_h Z[i,h] / H  (the reference: per-edge mean over heads,
-// summed over the row's edges).
-__global__ void k_node_score(const float* __restrict__ zbuf, int32_t ns_len, int32_t H,
-                             float* __restrict__ ns) {
-  for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < ns_len;
-       i += int64_t(gridDim.x) * blockDim.x) {
-    float s = 0.f;
-    for (int h = 0; h < H; ++h) s += zbuf[i * H + h];
-    ns[i] = s / float(H);
   }
 }
 
@@ -586,9 +608,10 @@ __device__ __forceinline__ void bwd_kv_finalize_tile(const int4* __restrict__ sp
   const int ncols = 2 * H * DH;
   const int col = tile * kColTile + lane;
   const bool ok = col < ncols;
-  float a = 0.f;
-  if (ok)
-    for (int p = wave; p < sp.z; p += kWavesPerBlock) a += part_kv[int64_t(sp.y + p) * ncols + col];
+  const float a0 =
+      ok ? strided_sum(part_kv + int64_t(sp.y) * ncols + col, wave, sp.z, kWavesPerBlock, ncols)
+         : 0.f;
+  float a = a0;
   red[wave][lane] = a;
   __syncthreads();
   if (wave != 0 || !ok) return;
@@ -742,9 +765,9 @@ __global__ __launch_bounds__(kBlock) void k_bwd_q_finalize(const int4* __restric
   const int ncols = H * DH;
   const int col = blockIdx.y * kColTile + lane;
   const bool ok = col < ncols;
-  float a = 0.f;
-  if (ok)
-    for (int p = wave; p < sp.z; p += kWavesPerBlock) a += part_q[int64_t(sp.y + p) * ncols + col];
+  float a = ok ? strided_sum(part_q + int64_t(sp.y) * ncols + col, wave, sp.z, kWavesPerBlock,
+                            ncols)
+               : 0.f;
   red[wave][lane] = a;
   __syncthreads();
   if (wave != 0 || !ok) return;
@@ -911,18 +934,19 @@ int launch_fwd(const ngt_window_csr* c, const void* q, const void* k, const void
       launch(std::false_type{});
     NGT_HIP_CHECK(hipGetLastError());
   }
-  if (c->n_splits_q > 0) {
+  // Split rows' finalize; with several head groups the node scores of the
+  // other rows ride in the same launch as extra blocks.
+  const int tiles = (H * DH + kColTile - 1) / kColTile;
+  const int64_t fin_blocks = int64_t(c->n_splits_q) * tiles;
+  const bool ns_late = ns && ns_len > 0 && !ns_direct;
+  const int64_t ns_blocks = ns_late ? (ns_len + kBlock - 1) / kBlock : 0;
+  if (fin_blocks + ns_blocks > 0) {
     KernelTimer timer_("sparse_fwd_finalize", st);
-    dim3 grid(c->n_splits_q, (H * DH + kColTile - 1) / kColTile);
-    hipLaunchKernelGGL((k_fwd_finalize<T, DH>), grid, dim3(kBlock), 0, st,
-                       reinterpret_cast<const int4*>(c->splits_q), H, eps, part_acc, part_z,
-                       static_cast<T*>(out), rinv, zbuf, ns_direct, ns_len);
-    NGT_HIP_CHECK(hipGetLastError());
-  }
-  if (ns && ns_len > 0 && !ns_direct) {
-    KernelTimer timer_("sparse_node_score", st);
-    hipLaunchKernelGGL(k_node_score, dim3((ns_len + kBlock - 1) / kBlock), dim3(kBlock), 0, st,
-                       zbuf, ns_len, H, ns);
+    hipLaunchKernelGGL((k_fwd_finalize<T, DH>), dim3(unsigned(fin_blocks + ns_blocks)),
+                       dim3(kBlock), 0, st, reinterpret_cast<const int4*>(c->splits_q), tiles, H,
+                       eps, part_acc, part_z, static_cast<T*>(out), rinv, zbuf,
+                       ns_direct ? ns_direct : (ns_late ? ns : nullptr), ns_len, c->rowptr,
+                       c->chunk_q, int32_t(ns_blocks));
     NGT_HIP_CHECK(hipGetLastError());
   }
   return NGT_OK;
