@@ -1,10 +1,11 @@
 // Dense full-window attention on the matrix cores (bf16 inputs, fp32
 // accumulation), head_dim d in {8, 16, 24, 32}.
 //
-// Every product runs on v_mfma_f32_32x32x8_bf16: its K = 8 equals the smallest
-// head dim, so the QK^T and dP = G V^T contractions over d have no padding,
-// and the PV-class contractions over keys/queries take 8-row K steps.  Lane
-// layouts of the 32x32x8 instruction (checked on gfx950):
+// Products run on v_mfma_f32_32x32x8_bf16 and, two K steps at a time, on
+// v_mfma_f32_32x32x16_bf16 (mfma2): K = 8 equals the smallest head dim, so the
+// QK^T and dP = G V^T contractions over d have no padding, and the PV-class
+// contractions over keys/queries take 16-row K steps.  Lane layouts of the
+// 32x32x8 instruction (checked on gfx950):
 //   A (32 x 8):  lane l holds A[l % 32][4*(l/32) + i], i < 4
 //   B (8 x 32):  lane l holds B[4*(l/32) + i][l % 32], i < 4
 //   D (32 x 32): lane l holds D[8*(i/4) + 4*(l/32) + i%4][l % 32], i < 16
@@ -41,6 +42,21 @@ constexpr float kLn2 = 0.6931471805599453f;
 
 __device__ __forceinline__ f32x16 mfma(s16x4 a, s16x4 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(a, b, c, 0, 0, 0);
+}
+
+// Two K = 8 steps as one v_mfma_f32_32x32x16_bf16 (which the chip runs at
+// twice the rate of the K = 8 form): the lane's A operand is a0 ++ a1 and its
+// B operand b0 ++ b1.  Element r of a lane's A and of its B carry the same
+// contraction index, so pairing a0 with b0 and a1 with b1 slot by slot gives
+// exactly mfma(a1, b1, mfma(a0, b0, c)) up to the fp32 accumulation order,
+// whatever order the instruction assigns to the 16 indices.
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ f32x16 mfma2(s16x4 a0, s16x4 a1, s16x4 b0, s16x4 b1, f32x16 c) {
+  const s16x8 a = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+  const s16x8 b = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
 __device__ __forceinline__ f32x16 zero16() {
@@ -226,7 +242,10 @@ __global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
       // S^T tile: rows = keys kb + r0 + (8*(i/4) + 4*half + i%4), col = this lane's query.
       f32x16 st = zero16();
 #pragma unroll
-      for (int j = 0; j < NC; ++j) st = mfma(lds4(&ks[r0 + l32][8 * j + 4 * half]), qb[j], st);
+      for (int j = 0; j + 1 < NC; j += 2)
+        st = mfma2(lds4(&ks[r0 + l32][8 * j + 4 * half]), lds4(&ks[r0 + l32][8 * j + 8 + 4 * half]),
+                   qb[j], qb[j + 1], st);
+      if constexpr (NC % 2) st = mfma(lds4(&ks[r0 + l32][8 * (NC - 1) + 4 * half]), qb[NC - 1], st);
       float mx = -INFINITY;
       if (kb + r0 + kT <= n_k) {
 #pragma unroll
@@ -275,12 +294,12 @@ __global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
 #pragma unroll
       for (int j = 0; j < 4; ++j) va[j] = lds4(&vt[l32][r0 + 8 * j + 4 * half]);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < 4; j += 2) {
         if constexpr (DROP) {
-          acc = mfma(va[j], pm[j], acc);
-          if constexpr (DH < 32) acc = mfma(ones_a, pb[j], acc);
+          acc = mfma2(va[j], va[j + 1], pm[j], pm[j + 1], acc);
+          if constexpr (DH < 32) acc = mfma2(ones_a, ones_a, pb[j], pb[j + 1], acc);
         } else {
-          acc = mfma(va[j], pb[j], acc);
+          acc = mfma2(va[j], va[j + 1], pb[j], pb[j + 1], acc);
         }
       }
     }
@@ -336,8 +355,11 @@ __global__ __launch_bounds__(kBlock) void k_mf_scores(const bf16_t* __restrict__
     for (int sub = 0; sub < kSB / kT && qb + sub * kT < n_q; ++sub) {
       f32x16 st = zero16();
 #pragma unroll
-      for (int j = 0; j < NC; ++j)
-        st = mfma(lds4(&qs[sub * kT + l32][8 * j + 4 * half]), kbv[j], st);
+      for (int j = 0; j + 1 < NC; j += 2)
+        st = mfma2(lds4(&qs[sub * kT + l32][8 * j + 4 * half]),
+                   lds4(&qs[sub * kT + l32][8 * j + 8 + 4 * half]), kbv[j], kbv[j + 1], st);
+      if constexpr (NC % 2)
+        st = mfma(lds4(&qs[sub * kT + l32][8 * (NC - 1) + 4 * half]), kbv[NC - 1], st);
 #pragma unroll
       for (int i = 0; i < 16; ++i) s += fabsf(st[i]);  // padded query rows are zero
     }
@@ -412,9 +434,15 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_kv(
       // S and dP tiles, rows = queries qb + r0 + 8*(i/4) + 4*half + i%4, col = this lane's key.
       f32x16 st = zero16(), dp = zero16();
 #pragma unroll
-      for (int j = 0; j < NC; ++j) {
-        st = mfma(lds4(&qs[r0 + l32][8 * j + 4 * half]), kbv[j], st);
-        dp = mfma(lds4(&gs[r0 + l32][8 * j + 4 * half]), vbv[j], dp);
+      for (int j = 0; j + 1 < NC; j += 2) {
+        st = mfma2(lds4(&qs[r0 + l32][8 * j + 4 * half]), lds4(&qs[r0 + l32][8 * j + 8 + 4 * half]),
+                   kbv[j], kbv[j + 1], st);
+        dp = mfma2(lds4(&gs[r0 + l32][8 * j + 4 * half]), lds4(&gs[r0 + l32][8 * j + 8 + 4 * half]),
+                   vbv[j], vbv[j + 1], dp);
+      }
+      if constexpr (NC % 2) {
+        st = mfma(lds4(&qs[r0 + l32][8 * (NC - 1) + 4 * half]), kbv[NC - 1], st);
+        dp = mfma(lds4(&gs[r0 + l32][8 * (NC - 1) + 4 * half]), vbv[NC - 1], dp);
       }
       s16x4 pa[4], dsa[4];  // P^T and dS^T as A operands: A[key][query step row]
 #pragma unroll
@@ -451,9 +479,9 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_kv(
         qbq[j] = lds4(&qt[l32][c0]);
       }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        dv = mfma(pa[j], gb[j], dv);
-        dk = mfma(dsa[j], qbq[j], dk);
+      for (int j = 0; j < 4; j += 2) {
+        dv = mfma2(pa[j], pa[j + 1], gb[j], gb[j + 1], dv);
+        dk = mfma2(dsa[j], dsa[j + 1], qbq[j], qbq[j + 1], dk);
       }
     }
   }
@@ -518,9 +546,15 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_q(
       const int r0 = sub * kT;
       f32x16 st = zero16(), dp = zero16();
 #pragma unroll
-      for (int j = 0; j < NC; ++j) {
-        st = mfma(lds4(&ks[r0 + l32][8 * j + 4 * half]), qbv[j], st);
-        dp = mfma(lds4(&vs[r0 + l32][8 * j + 4 * half]), gbv[j], dp);
+      for (int j = 0; j + 1 < NC; j += 2) {
+        st = mfma2(lds4(&ks[r0 + l32][8 * j + 4 * half]), lds4(&ks[r0 + l32][8 * j + 8 + 4 * half]),
+                   qbv[j], qbv[j + 1], st);
+        dp = mfma2(lds4(&vs[r0 + l32][8 * j + 4 * half]), lds4(&vs[r0 + l32][8 * j + 8 + 4 * half]),
+                   gbv[j], gbv[j + 1], dp);
+      }
+      if constexpr (NC % 2) {
+        st = mfma(lds4(&ks[r0 + l32][8 * (NC - 1) + 4 * half]), qbv[NC - 1], st);
+        dp = mfma(lds4(&vs[r0 + l32][8 * (NC - 1) + 4 * half]), gbv[NC - 1], dp);
       }
       if constexpr (DROP) {  // dP o M: keys kb + r0 + 8*(i/4) + 4*half + i%4
 #pragma unroll
@@ -549,7 +583,7 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_q(
 #pragma unroll
       for (int j = 0; j < 4; ++j) kbk[j] = lds4(&kt[l32][r0 + 8 * j + 4 * half]);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) dq = mfma(dsa[j], kbk[j], dq);
+      for (int j = 0; j < 4; j += 2) dq = mfma2(dsa[j], dsa[j + 1], kbk[j], kbk[j + 1], dq);
     }
   }
   if (l32 >= DH) return;
