@@ -77,6 +77,19 @@ def test_argument_errors_are_reported_without_touching_the_gpu():
         _lib.check(1)
 
 
+def test_gather_probe_rejects_bad_rows_without_touching_the_gpu():
+    lib = _lib.load()
+    assert lib.ngt_probe_gather(None, 10, 1536, None, 5, None, None) == 1
+    assert b"null pointer" in lib.ngt_last_error()
+    fake = C.c_void_p(256)  # never dereferenced: the checks fail before any launch
+    assert lib.ngt_probe_gather(fake, 10, 100, fake, 5, fake, None) == 1
+    assert b"multiple of 16" in lib.ngt_last_error()
+    # 5 words per row: neither 1..4 words per lane times a power of two
+    assert lib.ngt_probe_gather(fake, 10, 80, fake, 5, fake, None) == 2
+    assert lib.ngt_probe_gather(fake, -1, 1536, fake, 5, fake, None) == 1
+    assert lib.ngt_probe_gather(None, 10, 1536, None, 0, None, None) == 0  # nothing to do
+
+
 def test_product_never_imports_the_oracle():
     pkg = ROOT / "neutrongt_amd"
     for f in list(pkg.rglob("*.py")) + list(pkg.rglob("*.hip")):
