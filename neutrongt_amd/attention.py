@@ -44,7 +44,7 @@ def _prep(t: torch.Tensor, name: str) -> torch.Tensor:
 
 
 def _stream(dev) -> int:
-    return torch.cuda.current_stream(dev).cuda_stream
+    return _lib.stream_ptr(dev)
 
 
 def _workspace(nbytes: int, dev) -> torch.Tensor:

@@ -90,7 +90,7 @@ class WindowAdjacency:
         with torch.cuda.device(dev):
             _lib.check(lib.ngt_csr_workspace_bytes(E, n_q, n_k, C.byref(ws_bytes)))
             ws = torch.empty(max(ws_bytes.value, 1), dtype=torch.uint8, device=dev)
-            stream = torch.cuda.current_stream(dev).cuda_stream
+            stream = _lib.stream_ptr(dev)
             _lib.check(lib.ngt_csr_build(ei.data_ptr() if E else None, C.byref(s), ws.data_ptr(),
                                          ws_bytes.value, stream))
             info = self.info_dev.cpu()  # one sync per window build

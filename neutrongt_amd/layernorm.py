@@ -51,7 +51,7 @@ class _LayerNormFn(torch.autograd.Function):
         _lib.check(lib.ngt_layernorm_fwd(_CODES[x2.dtype], x2.data_ptr(), n, n_cols, w.data_ptr(),
                                          b.data_ptr(), float(eps), _CODES[y.dtype], y.data_ptr(),
                                          mean.data_ptr(), rstd.data_ptr(),
-                                         torch.cuda.current_stream(dev).cuda_stream))
+                                         _lib.stream_ptr(dev)))
         ctx.save_for_backward(x2, w, mean, rstd)
         ctx.in_shape = x.shape
         return y.view(*x.shape)
@@ -75,7 +75,7 @@ class _LayerNormFn(torch.autograd.Function):
                                          g2.data_ptr(), n, n_cols, w.data_ptr(),
                                          mean.data_ptr(), rstd.data_ptr(), dx.data_ptr(),
                                          dw.data_ptr(), db.data_ptr(), ws.data_ptr(), nb.value,
-                                         torch.cuda.current_stream(dev).cuda_stream))
+                                         _lib.stream_ptr(dev)))
         return dx.view(*ctx.in_shape), dw, db, None, None
 
 
@@ -126,7 +126,7 @@ class _AddLayerNormFn(torch.autograd.Function):
             _CODES[x2.dtype], x2.data_ptr(), y2.data_ptr(), n, n_cols, float(p), int(seed),
             w.data_ptr(), b.data_ptr(), float(eps), s.data_ptr(), _CODES[out.dtype],
             out.data_ptr(), mean.data_ptr(), rstd.data_ptr(),
-            torch.cuda.current_stream(dev).cuda_stream))
+            _lib.stream_ptr(dev)))
         ctx.save_for_backward(s, w, mean, rstd)
         ctx.p, ctx.seed, ctx.shape = float(p), int(seed), x.shape
         return s.view(*x.shape), out.view(*x.shape)
@@ -153,7 +153,7 @@ class _AddLayerNormFn(torch.autograd.Function):
             g_s2.data_ptr() if g_s2 is not None else None, n, n_cols, ctx.p, ctx.seed,
             w.data_ptr(), mean.data_ptr(), rstd.data_ptr(), dx.data_ptr(), dy.data_ptr(),
             dw.data_ptr(), db.data_ptr(), ws.data_ptr(), nb.value,
-            torch.cuda.current_stream(dev).cuda_stream))
+            _lib.stream_ptr(dev)))
         return dx.view(*ctx.shape), dy.view(*ctx.shape), dw, db, None, None, None, None
 
 

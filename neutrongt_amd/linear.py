@@ -44,7 +44,7 @@ def colsum_bf16(dy: torch.Tensor) -> torch.Tensor:
     _lib.check(lib.ngt_colsum_workspace_bytes(K, n, C.byref(nb)))
     ws = torch.empty(max(nb.value, 1), dtype=torch.uint8, device=dy.device)
     _lib.check(lib.ngt_colsum_bf16(dy.data_ptr(), K, n, out.data_ptr(), ws.data_ptr(), nb.value,
-                                   torch.cuda.current_stream(dy.device).cuda_stream))
+                                   _lib.stream_ptr(dy.device)))
     return out
 
 

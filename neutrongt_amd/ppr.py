@@ -88,7 +88,7 @@ def appnp_batch(rowptr, col, inv_deg, n_nodes: int, seeds: torch.Tensor, alpha: 
     cb = C.c_size_t()
     _lib.check(lib.ngt_ppr_count_workspace_bytes(B, C.byref(cb)))
     cws = torch.empty(cb.value, dtype=torch.uint8, device=dev)
-    stream = torch.cuda.current_stream(dev).cuda_stream
+    stream = _lib.stream_ptr(dev)
     keep = float(1.0 - alpha)  # rounded to fp32 by ctypes, as fp32_tensor * (1 - alpha) is
 
     def count(r0, r1, off):

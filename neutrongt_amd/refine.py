@@ -36,7 +36,7 @@ def _segment_sum(vals: torch.Tensor, seg: torch.Tensor) -> torch.Tensor:
     if n_seg > 0:
         _lib.check(lib.ngt_segment_sum_f32(vals.data_ptr(), int(vals.numel()), seg.data_ptr(),
                                            n_seg, out.data_ptr(), bad.data_ptr(),
-                                           torch.cuda.current_stream(vals.device).cuda_stream))
+                                           _lib.stream_ptr(vals.device)))
     return out
 
 

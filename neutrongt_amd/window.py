@@ -56,7 +56,7 @@ def merge_related_nodes(xadj: torch.Tensor, adjncy: torch.Tensor, eweights: torc
     nb = C.c_size_t()
     _lib.check(lib.ngt_related_workspace_bytes(n_nodes, int(part.numel()), C.byref(nb)))
     ws = torch.empty(max(nb.value, 1), dtype=torch.uint8, device=dev)
-    stream = torch.cuda.current_stream(dev).cuda_stream
+    stream = _lib.stream_ptr(dev)
     _lib.check(lib.ngt_merge_related_nodes(xadj.data_ptr(), adjncy.data_ptr(),
                                            eweights.data_ptr(), n_nodes, part.data_ptr(),
                                            int(part.numel()), int(topk_percent), out.data_ptr(),
@@ -118,7 +118,7 @@ def gather_rows(src: torch.Tensor, idx: torch.Tensor, out: torch.Tensor | None =
     bad = torch.zeros(1, dtype=torch.int32, device=src.device)
     if row_bytes % 4:
         raise ValueError("gather_rows: row size must be a multiple of 4 bytes")
-    stream = torch.cuda.current_stream(src.device).cuda_stream
+    stream = _lib.stream_ptr(src.device)
     _lib.check(lib.ngt_gather_rows(src.data_ptr(), int(src.shape[0]), idx.data_ptr(),
                                    int(idx.numel()), int(row_bytes), out.data_ptr(),
                                    bad.data_ptr(), stream))
@@ -136,7 +136,7 @@ def _run_subgraph(call, n_nodes: int, n_edges: int, n_set: int, device):
     _lib.check(lib.ngt_subgraph_workspace_bytes(n_nodes, n_edges, n_set, C.byref(nb)))
     ws = torch.empty(max(nb.value, 1), dtype=torch.uint8, device=device)
     result = torch.zeros(2, dtype=torch.int64, device=device)
-    stream = torch.cuda.current_stream(device).cuda_stream
+    stream = _lib.stream_ptr(device)
     _lib.check(call(None, 0, result.data_ptr(), ws.data_ptr(), nb.value, stream))
     n, err = (int(v) for v in result.tolist())
     if err:
