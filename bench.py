@@ -11,9 +11,11 @@ reused by every layer and step, as in the training loop).
 
 Prints ONE JSON line: value = masked edges/s (layers x E / step time), the
 roofline of the dominant kernel (algorithmic bytes / its mean launch time,
-from hipEvents recorded around each launch on its own stream) and the CPU
-baseline: the reference's op sequence (the CPU oracle, fp32 torch) timed on a
-bounded sample of the same window.
+from hipEvents recorded around each launch on its own stream; its measured
+traffic from profiles/traffic.json; and the rate a pure random-row gather of
+the same table reaches, roofline.gather_ceiling) and the CPU baseline: the
+reference's op sequence (the CPU oracle, fp32 torch) timed on a bounded sample
+of the same window.
 """
 from __future__ import annotations
 
