@@ -348,7 +348,8 @@ def prep_bench(args, cfg, dev) -> dict:
     sub_coo, t_coo = timed(lambda: W.subgraph(win, coo, n))
     n_w = int(win.numel())
     # attention edge_index: row 0 = key (the CSR row node), row 1 = query
-    adj, t_adj = timed(lambda: WindowAdjacency(sub_csr, n_w, n_w, chunk_for_heads(H),
+    adj, t_adj = timed(lambda: WindowAdjacency(sub_csr, n_w, n_w,
+                                               chunk_for_heads(H, int(sub_csr.shape[1])),
                                                small_for_heads(H)))
     (x_i, _), t_gather = timed(lambda: W.gather_rows(features, win))
     # window refinement of this window: node_out with seeded node scores (30 %
@@ -620,7 +621,7 @@ def main(argv=None) -> int:
         for _ in range(2):
             torch.cuda.synchronize()
             t1 = time.perf_counter()
-            adj = WindowAdjacency(ei, cfg.n_q, n_k, chunk_for_heads(H), small_for_heads(H))
+            adj = WindowAdjacency(ei, cfg.n_q, n_k, chunk_for_heads(H, E), small_for_heads(H))
             csr_ms = (time.perf_counter() - t1) * 1e3
             cold = csr_ms if cold is None else cold
         _log(f"[bench] csr built in {csr_ms:.2f} ms (first build {cold:.1f} ms; incl. one info "

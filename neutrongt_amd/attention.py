@@ -148,7 +148,8 @@ def sparse_attention(q, k, v, edge_index, num_heads=None, scale=None, cache: Adj
     if scale is None:
         scale = math.sqrt(d)
     cache = cache or default_cache
-    adj = cache.get(edge_index, q.shape[0], n_k, chunk_for_heads(H), small_for_heads(H))
+    adj = cache.get(edge_index, q.shape[0], n_k, chunk_for_heads(H, int(edge_index.shape[-1])),
+                    small_for_heads(H))
     return SparseAttentionFunction.apply(q, k, v, adj, float(scale), float(lo), float(hi),
                                          float(eps), k_ext, v_ext)
 

@@ -11,6 +11,7 @@ layer of a window step and across epochs.
 from __future__ import annotations
 
 import ctypes as C
+import os
 from collections import OrderedDict
 
 import torch
@@ -19,15 +20,30 @@ from . import _lib
 
 # A work item covers at most this many edges of one row; longer rows are cut
 # into chunks whose partial sums a finalize pass adds.  With the kernels'
-# 8 edge slots per wave (8 heads per pass) a chunk is 32 rounds of a wave.
+# 8 edge slots per wave (8 heads per pass) a 256-edge chunk is 32 rounds of a
+# wave.
 CHUNK_EDGES = 256
+CHUNK_EDGES_MAX = 1024
 
 
-def chunk_for_heads(n_heads: int) -> int:
-    """Edges per work item (the same for every head count; the argument is
-    kept so callers can pass the layer's head count)."""
+def chunk_for_heads(n_heads: int, n_edges: int = 0) -> int:
+    """Edges per work item: 2^floor(log2(n_edges / 2048)) within [256, 1024]
+    (256 when n_edges is not given).  Longer chunks mean fewer partials and
+    smaller finalize passes, but a hub row's chunk is one wave's serial work,
+    which must stay short next to the whole kernel.  Measured per layer
+    fwd+bwd at 256 / 512 / 1024: the high-degree window (3.65 M edges)
+    374 / 346 / 341 us; GPH_Large (1.79 M) 1.394 / 1.385 / 1.414 ms; GPH_Slim
+    and the GT arxiv window (0.25 M) 67 / 95 / 153 and 80 / 110 / 175 us.
+    The head count does not enter; the argument keeps the callers' form.
+    NGT_CHUNK_EDGES overrides the choice."""
     del n_heads
-    return CHUNK_EDGES
+    env = os.environ.get("NGT_CHUNK_EDGES")
+    if env and int(env) > 0:
+        return int(env)
+    chunk = CHUNK_EDGES
+    while chunk < CHUNK_EDGES_MAX and 2 * chunk * 2048 <= n_edges:
+        chunk *= 2
+    return chunk
 
 
 def small_for_heads(n_heads: int) -> int:
