@@ -68,8 +68,11 @@ def chung_lu_edges(n: int, mean_degree: float, gamma: float = 2.1, seed: int = S
     w = (np.arange(n, dtype=np.float64) + 1.0) ** (-1.0 / (gamma - 1.0))
     cdf = np.cumsum(w / w.sum())
     cdf[-1] = 1.0
-    target = n * mean_degree / 2.0
-    m = int(target)
+    # at most half of the n(n-1)/2 possible pairs: beyond that the dedup
+    # saturates and the recalibration below would grow m without bound
+    target = min(n * mean_degree / 2.0, n * (n - 1) / 4.0)
+    m = max(int(target), 1)
+    m_cap = 64 * m + 1024
     best = None
     for _ in range(max_iter):
         a = np.searchsorted(cdf, rng.random(m), side="right")
@@ -84,7 +87,7 @@ def chung_lu_edges(n: int, mean_degree: float, gamma: float = 2.1, seed: int = S
         if abs(got - target) <= tol * target:
             break
         m = int(m * target / max(got, 1) * 1.02) if got < target else int(m * target / got)
-        m = max(m, 1)
+        m = min(max(m, 1), m_cap)
     return best // n, best % n
 
 

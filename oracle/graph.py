@@ -56,7 +56,8 @@ def work_items(rowptr, chunk: int, small: int = 0):
     order, part slot = item index).  Rows with small < degree <= chunk are one
     item each (part -1) and rows with degree <= small go to the packed list;
     both follow the order of a stable ascending sort by degree, reversed
-    (longest first; equal degrees by descending row id).
+    (longest first; equal degrees by descending row id).  Requires
+    small < chunk (the host clamps it), so no row is both split and packed.
     Returns (items [n,4], splits [m,4], packed [p])."""
     rowptr = np.asarray(rowptr, dtype=np.int64)
     deg = np.diff(rowptr)
