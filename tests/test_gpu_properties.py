@@ -113,3 +113,61 @@ def _assert_grad_close(ours, ref64, term_scale, dtype, what):
         atol = 10 * tol * max(ref64.abs().max().item(), term_scale.abs().max().item())
         worst = (ours - ref64).abs().max().item()
         assert worst <= atol, f"{what}: max abs diff {worst:.3e} > {atol:.3e}"
+
+
+@settings(max_examples=40, deadline=None, database=None, derandomize=True,
+          suppress_health_check=[HealthCheck.too_slow])
+@given(n_q=st.integers(1, 400), n_k=st.integers(1, 400), H=st.sampled_from([1, 2, 5]),
+       d=st.sampled_from([8, 16, 24, 32, 64]),
+       dtype=st.sampled_from([torch.float32, torch.bfloat16]),
+       p=st.sampled_from([0.0, 0.0, 0.3]), seed=st.integers(0, 2**40))
+def test_dense_random_sizes_match_the_oracle(n_q, n_k, H, d, dtype, p, seed):
+    """Dense all-pairs attention at random sizes (tails of the 32-row tiles
+    and 128-row stages on both sides), with and without dropout."""
+    from neutrongt_amd import DenseAttentionFunction
+    from tests._util import assert_parity
+
+    print(f"case dense n_q={n_q} n_k={n_k} H={H} d={d} {dtype} p={p} seed={seed}", flush=True)
+    g = torch.Generator().manual_seed(seed % (2**31))
+    q, k, v = (torch.randn(n, H, d, generator=g).to(dtype) for n in (n_q, n_k, n_k))
+    go = torch.randn(n_q, H, d, generator=g).to(dtype)
+    qd, kd, vd = (t.cuda().requires_grad_(True) for t in (q, k, v))
+    x, ns = DenseAttentionFunction.apply(qd, kd, vd, float(d) ** 0.5, True, p, seed)
+    x.backward(go.cuda())
+    torch.cuda.synchronize()
+    mult = OA.dropout_multiplier(seed, H, n_q, n_k, p) if p > 0 else None
+    ref = OA.full_fwd_bwd(q.float(), k.float(), v.float(), go.float(), dropout_mult=mult)
+    ref64 = OA.full_fwd_bwd(q.double(), k.double(), v.double(), go.double(),
+                            dtype=torch.float64, dropout_mult=mult)
+    got = {"x": x.detach(), "node_scores": ns, "dq": qd.grad, "dk": kd.grad, "dv": vd.grad}
+    for name in ("x", "node_scores"):
+        assert got[name].shape == ref[name].shape, name
+        assert_parity(got[name].float().cpu(), ref[name], ref64[name], dtype, name)
+    scale = _dense_term_scales(q.float(), k.float(), v.float(), go.float(), float(d) ** 0.5,
+                               mult)
+    for name in ("dq", "dk", "dv"):
+        assert got[name].shape == ref[name].shape, name
+        _assert_grad_close(got[name].double().cpu(), ref64[name].double(), scale[name], dtype,
+                           f"dense {name}")
+
+
+def _dense_term_scales(q, k, v, go, scale, mult):
+    """The size of the terms each dense gradient sums (float64): with
+    dP = (G V^T) o M, D_i = sum_j P_ij dP_ij and t = P o (|dP| + |D|),
+    dQ ~ scale t |K|, dK ~ scale t^T |Q|, dV ~ (P o M)^T |G|.  One key (or one
+    dominant key) makes dS = P (dP - D) cancel to about zero: the kernels
+    recompute P from the saved log-sum-exp and leave rounding noise of the
+    terms' size there, where the restatement's exact P = 1 may cancel exactly."""
+    q, k, v, g = (t.double() for t in (q, k, v, go))
+    m = torch.ones(q.shape[1], q.shape[0], k.shape[0], dtype=torch.float64) if mult is None \
+        else torch.as_tensor(mult, dtype=torch.float64)
+    s = torch.einsum("ihc,jhc->hij", q * scale, k)
+    p = torch.softmax(s, dim=-1)
+    dp = torch.einsum("ihc,jhc->hij", g, v) * m
+    dd = (p * dp).sum(-1, keepdim=True)
+    t = p * (dp.abs() + dd.abs())
+    return {
+        "dq": scale * torch.einsum("hij,jhc->ihc", t, k.abs()),
+        "dk": scale * torch.einsum("hij,ihc->jhc", t, q.abs()),
+        "dv": torch.einsum("hij,ihc->jhc", p * m, g.abs()),
+    }
