@@ -608,10 +608,9 @@ __device__ __forceinline__ void bwd_kv_finalize_tile(const int4* __restrict__ sp
   const int ncols = 2 * H * DH;
   const int col = tile * kColTile + lane;
   const bool ok = col < ncols;
-  const float a0 =
+  float a =
       ok ? strided_sum(part_kv + int64_t(sp.y) * ncols + col, wave, sp.z, kWavesPerBlock, ncols)
          : 0.f;
-  float a = a0;
   red[wave][lane] = a;
   __syncthreads();
   if (wave != 0 || !ok) return;
