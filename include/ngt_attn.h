@@ -212,6 +212,10 @@ int ngt_sparse_bwd_ext(int dtype, const void* q, const void* k, const void* v, c
  * bf16-rounded out (out may then be NULL in the backward).  For rows whose
  * softmax is peaked, dS = P (dP - D) nearly cancels and the rounded out
  * alone moves dQ by percents.
+ * workspace: fwd_bytes / bwd_bytes from ngt_dense_workspace_bytes.  The
+ * forward uses it for node-score partials and, on its vector-ALU kernels
+ * (fp32; bf16 at head_dim 64), for per-split softmax states when it splits
+ * the keys of a large window over several blocks; pass it on every call.
  */
 int ngt_dense_workspace_bytes(int32_t n_q, int32_t n_k, int32_t n_heads, int32_t head_dim,
                               size_t* fwd_bytes, size_t* bwd_bytes);

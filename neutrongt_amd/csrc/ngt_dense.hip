@@ -12,17 +12,19 @@
 // out_i still equals rowsum(dP o P).  The mask is regenerated from
 // (seed, head, query, key) in every kernel (DropoutMask).
 //
-// Layout of one wave: 16 rows (lane % 16) x 4 column groups (lane / 16) of 8
-// columns each, i.e. a 16 x 32 tile of S per step.  The forward keeps an
-// online softmax per row (running max m, running sum l); every lane owns the
-// partial sums of its own 8 columns and the four column groups of a row are
-// combined once at the end.  Key/query tiles are read straight from global
-// memory: a head's K/V (or Q/G) slice is a few hundred KB and stays in L2.
+// Vector-ALU kernels (fp32, and bf16 at d = 64): one row per lane (query
+// rows in the forward and dQ pass, key rows in the dK/dV pass), the other
+// side streamed at wave-uniform addresses, so its rows arrive through scalar
+// loads and feed the lane's FMAs from scalar registers.  The forward keeps an
+// online softmax per row (running max m, running sum l); a block's 4 waves
+// split the streamed rows and add their partial results in a fixed order at
+// the end.
 #include "ngt_common.h"
 
 #include <math.h>
 #include <stdlib.h>
 
+#include <type_traits>
 #include <utility>
 
 namespace ngt {
@@ -40,11 +42,25 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / kWave;
-constexpr int kRows = 16;        // rows per wave
-constexpr int kColsPerLane = 8;  // columns per lane per tile
-constexpr int kTile = 4 * kColsPerLane;
-constexpr int kRowsPerBlock = kWaves * kRows;
-constexpr int kScoreChunk = 8192;  // keys per LDS node-score accumulator pass
+constexpr int kRowsPerBlock = kWave;  // one row per lane; the block's waves split the other side
+constexpr int kKeyTile = 32;          // forward: keys per online-softmax step of a wave
+constexpr int kStreamTile = 16;       // backward: streamed rows per step of a wave
+constexpr int kNsKeys = 16;           // keys per node-score transpose
+constexpr int kNsStride = kNsKeys + 4;
+constexpr int kSumChunk = 16;  // values per lane per round of the cross-wave sum
+constexpr int kLdsFloats = kWaves * kWave * kNsStride;
+static_assert((kWaves - 1) * kSumChunk * kWave <= kLdsFloats, "cross-wave sum buffer");
+static_assert(kKeyTile % kNsKeys == 0 && kStreamTile % 2 == 0, "tiles cover whole key pairs");
+
+// One dependent FMA chain: the kernels keep several rows' dot products in
+// flight, so a second partial sum would only add an addition.
+template <int DH>
+__device__ __forceinline__ float dot1(const float (&a)[DH], const float (&b)[DH]) {
+  float s = a[0] * b[0];
+#pragma unroll
+  for (int c = 1; c < DH; ++c) s = fmaf(a[c], b[c], s);
+  return s;
+}
 
 template <int DH>
 __device__ __forceinline__ float dotv(const float (&a)[DH], const float (&b)[DH]) {
@@ -57,31 +73,80 @@ __device__ __forceinline__ float dotv(const float (&a)[DH], const float (&b)[DH]
   return s0 + s1;
 }
 
-// Sum over the 16 lanes of a DPP row (lanes 16g .. 16g+15); every lane of the
-// row receives the total.
-__device__ __forceinline__ float row16_sum(float x) {
-  x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x128, 0xf, 0xf, false));
-  x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x124, 0xf, 0xf, false));
-  x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x122, 0xf, 0xf, false));
-  x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x121, 0xf, 0xf, false));
+// An opaque copy of a wave-uniform integer, pinned to a scalar register.
+// Addresses of streamed rows built from it stay in scalar registers (and
+// their loads scalar) even where the compiler has already copied the
+// original into a vector register for a per-lane address.
+__device__ __forceinline__ int uniform_int(int x) {
+  asm volatile("" : "+s"(x));
   return x;
 }
 
+// Marks x as read and rewritten here.  Volatile asm statements keep their
+// order, so a group of arithmetic followed by pins of its results completes
+// before the next statement (and the loads whose addresses come from a later
+// uniform_int); without it the scheduler is free to hoist every scalar load
+// of a tile ahead of all arithmetic.
+__device__ __forceinline__ void pin(float& x) { asm volatile("" : "+v"(x)); }
+
+// x summed lane by lane over the block's waves, in wave order, into wave 0's
+// registers (the other waves' copies are left as they were).  buf holds
+// (kWaves - 1) * kSumChunk * kWave floats and may be reused by the caller
+// before the call: every round starts with a barrier.
+template <int N>
+__device__ __forceinline__ void waves_sum(float (&x)[N], float* buf, int w, int lane) {
+#pragma unroll
+  for (int c0 = 0; c0 < N; c0 += kSumChunk) {
+    __syncthreads();
+    if (w > 0) {
+#pragma unroll
+      for (int c = 0; c < kSumChunk && c0 + c < N; ++c)
+        buf[((w - 1) * kSumChunk + c) * kWave + lane] = x[c0 + c];
+    }
+    __syncthreads();
+    if (w == 0) {
+#pragma unroll
+      for (int c = 0; c < kSumChunk && c0 + c < N; ++c) {
+        float s = x[c0 + c];
+#pragma unroll
+        for (int u = 0; u < kWaves - 1; ++u) s += buf[(u * kSumChunk + c) * kWave + lane];
+        x[c0 + c] = s;
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------------ forward
-// grid = (ceil(n_q / 64), H).  ns_part (optional) is [gridDim.x * H, n_k]:
-// per block and head, sum over the block's 64 query rows of |S[h, i, j]|.
+// One block = 64 query rows (one per lane) of one head; its 4 waves take the
+// 32-key tiles in turn (wave w: tiles w, w + 4, ...) and meet at the end.
+// Block b serves rows 64 (b / H) .. of head b % H: consecutive blocks take
+// consecutive heads, so the round-robin of blocks over the 8 XCDs gives each
+// XCD's L2 the K/V slices of its own heads.  The keys' rows are read at
+// wave-uniform addresses (scalar loads), so a lane's arithmetic takes them
+// straight from scalar registers.  Per tile a lane keeps its row's online
+// softmax (running max m, running sum l, rescale once per tile).
+// ns_part (optional) is [n_blocks, n_k]: per block (64 rows of one head),
+// sum over its rows of |S[h, i, j]|, one writer per key.
 template <typename T, int DH, bool DROP>
 __global__ __launch_bounds__(kBlock) void k_dense_fwd(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, int32_t n_q,
-    int32_t n_k, int32_t H, float scale, DropoutMask dm, T* __restrict__ out,
-    float* __restrict__ out32, float* __restrict__ lse, float* __restrict__ ns_part) {
-  __shared__ float ns_lds[kScoreChunk];
+    int32_t n_k, int32_t H, float scale, DropoutMask dm, int32_t n_split, int32_t split_keys,
+    T* __restrict__ out, float* __restrict__ out32, float* __restrict__ lse,
+    float* __restrict__ ns_part, float* __restrict__ part_ml, float* __restrict__ part_acc) {
+  __shared__ float lds[kLdsFloats];
+  __shared__ float m_lds[kWaves * kWave];
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x >> 6;
-  const int r = lane & 15;
-  const int g = lane >> 4;
-  const int h = blockIdx.y;
-  const int64_t qi = int64_t(blockIdx.x) * kRowsPerBlock + wave * kRows + r;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // block -> (rows, key split, head) in scalar registers: the division runs
+  // on the vector ALU, and addresses built from a vector register would turn
+  // the streamed rows' scalar loads into vector loads
+  const int h = __builtin_amdgcn_readfirstlane(blockIdx.x % H);
+  const int rs = __builtin_amdgcn_readfirstlane(blockIdx.x / H);
+  const int sp = __builtin_amdgcn_readfirstlane(rs % n_split);
+  const int rb = __builtin_amdgcn_readfirstlane(rs / n_split);
+  const int k0 = sp * split_keys;                 // this block's keys: [k0, k1)
+  const int k1 = min(n_k, k0 + split_keys);
+  const int64_t qi = int64_t(rb) * kRowsPerBlock + lane;
   const bool q_ok = qi < n_q;
   if constexpr (DROP) dm = drop_for_head(dm, h);
 
@@ -92,94 +157,178 @@ __global__ __launch_bounds__(kBlock) void k_dense_fwd(
     for (int c = 0; c < DH; ++c) qs[c] *= scale;
   } else {
 #pragma unroll
-    for (int c = 0; c < DH; ++c) qs[c] = 0.f;
+    for (int c = 0; c < DH; ++c) qs[c] = 0.f;  // S = 0 exactly: no node-score share
   }
   float acc[DH];
 #pragma unroll
   for (int c = 0; c < DH; ++c) acc[c] = 0.f;
   float m = -INFINITY, l = 0.f;
-  const bool scores = ns_part != nullptr;
+  const int64_t HD = int64_t(H) * DH;  // row stride of q, k, v
+  const T* k_h = k + int64_t(uniform_int(h)) * DH;  // streamed rows of this head
+  const T* v_h = v + int64_t(uniform_int(h)) * DH;
+  float* ns_w = lds + w * kWave * kNsStride;
+  float* ns_dst = ns_part ? ns_part + (int64_t(rb) * H + h) * n_k : nullptr;
 
-  for (int kc = 0; kc < n_k; kc += kScoreChunk) {
-    const int kc_end = min(n_k, kc + kScoreChunk);
-    if (scores) {
-      __syncthreads();
-      for (int t = threadIdx.x; t < kScoreChunk; t += kBlock) ns_lds[t] = 0.f;
-      __syncthreads();
+  // keys per scalar-load group: up to 64 scalar registers of K (or V) rows in
+  // flight; unbounded, the scheduler hoists a whole tile's loads and spills
+  constexpr int kLoadGroup = DH >= 64 ? 1 : 64 / DH;
+  static_assert(kKeyTile % kLoadGroup == 0, "load groups tile the key tile");
+  const int n_tiles = (k1 - k0 + kKeyTile - 1) / kKeyTile;
+  for (int t = w; t < n_tiles; t += kWaves) {
+    // One body for every tile: key indices past k1 load row k1 - 1 (in
+    // bounds) and get S = -inf, hence p = 0; their node-score columns are
+    // never stored.
+    const int kb = k0 + t * kKeyTile;
+    const int k_last = k1 - 1;
+    float s[kKeyTile];
+#pragma unroll
+    for (int g0 = 0; g0 < kKeyTile; g0 += kLoadGroup) {
+      const int kg = uniform_int(kb + g0);
+      float kr[kLoadGroup][DH];
+#pragma unroll
+      for (int i = 0; i < kLoadGroup; ++i)
+        load_row<T, DH>(k_h + int64_t(min(kg + i, k_last)) * HD, kr[i]);
+#pragma unroll
+      for (int i = 0; i < kLoadGroup; ++i) {
+        s[g0 + i] = dot1<DH>(qs, kr[i]);
+        pin(s[g0 + i]);
+      }
     }
-    for (int kb = kc; kb < kc_end; kb += kTile) {
-      float s[kColsPerLane];
-      float tmax = -INFINITY;
+    if (kb + kKeyTile > k1) {
 #pragma unroll
-      for (int i = 0; i < kColsPerLane; ++i) {
-        const int64_t kj = kb + g * kColsPerLane + i;
-        if (kj < kc_end) {
-          float kr[DH];
-          load_row<T, DH>(k + (kj * H + h) * DH, kr);
-          s[i] = dotv<DH>(qs, kr);
-          tmax = fmaxf(tmax, s[i]);
-        } else {
-          s[i] = -INFINITY;
-        }
-      }
-      if (scores) {
-#pragma unroll
-        for (int i = 0; i < kColsPerLane; ++i) {
-          const float a = row16_sum(q_ok && s[i] != -INFINITY ? fabsf(s[i]) : 0.f);
-          const int kj = kb + g * kColsPerLane + i;
-          if (r == 0 && kj < kc_end) atomicAdd(&ns_lds[kj - kc], a);
-        }
-      }
-      tmax = fmaxf(tmax, shfl_xor(tmax, 16));
-      tmax = fmaxf(tmax, shfl_xor(tmax, 32));
-      const float m_new = fmaxf(m, tmax);
-      const float alpha = __expf(m - m_new);
-      l *= alpha;
-#pragma unroll
-      for (int c = 0; c < DH; ++c) acc[c] *= alpha;
-      uint32_t dw[kColsPerLane / 2];  // one dropout word per key pair
-      if constexpr (DROP) {
-#pragma unroll
-        for (int i = 0; i < kColsPerLane / 2; ++i)
-          dw[i] = drop_word(dm, uint32_t(qi), uint32_t(kb + g * kColsPerLane + 2 * i));
-      }
-#pragma unroll
-      for (int i = 0; i < kColsPerLane; ++i) {
-        const int64_t kj = kb + g * kColsPerLane + i;
-        if (kj < kc_end) {
-          const float p = __expf(s[i] - m_new);
-          l += p;  // the softmax normaliser uses every key
-          float pv = p;
-          if constexpr (DROP) pv *= drop_scale(dm, dw[i / 2], uint32_t(kj));
-          float vr[DH];
-          load_row<T, DH>(v + (kj * H + h) * DH, vr);
-#pragma unroll
-          for (int c = 0; c < DH; ++c) acc[c] = fmaf(pv, vr[c], acc[c]);
-        }
-      }
-      m = m_new;
+      for (int i = 0; i < kKeyTile; ++i)
+        if (kb + i > k_last) s[i] = -INFINITY;
     }
-    if (scores) {
-      __syncthreads();
-      float* dst = ns_part + (int64_t(blockIdx.x) * H + h) * n_k + kc;
-      for (int t = threadIdx.x; t < kc_end - kc; t += kBlock) dst[t] = ns_lds[t];
+    float tmax = s[0];
+#pragma unroll
+    for (int i = 1; i < kKeyTile; ++i) tmax = fmaxf(tmax, s[i]);
+    const float m_new = fmaxf(m, tmax);
+    const float alpha = __expf(m - m_new);
+    l *= alpha;
+#pragma unroll
+    for (int c = 0; c < DH; ++c) acc[c] *= alpha;
+    uint32_t dw[kKeyTile / 2];  // one dropout word per key pair
+    if constexpr (DROP) {
+#pragma unroll
+      for (int i = 0; i < kKeyTile / 2; ++i) dw[i] = drop_word(dm, uint32_t(qi), uint32_t(kb + 2 * i));
+    }
+    // (the V rows' addresses come from new opaque copies of the tile base:
+    // left to itself the compiler keeps the K loop's 32 row offsets live)
+#pragma unroll
+    for (int g0 = 0; g0 < kKeyTile; g0 += kLoadGroup) {
+      const int kg = uniform_int(kb + g0);
+      float vr[kLoadGroup][DH];
+#pragma unroll
+      for (int i = 0; i < kLoadGroup; ++i)
+        load_row<T, DH>(v_h + int64_t(min(kg + i, k_last)) * HD, vr[i]);
+#pragma unroll
+      for (int i = 0; i < kLoadGroup; ++i) {
+        const float p = __expf(s[g0 + i] - m_new);
+        l += p;  // the softmax normaliser uses every key
+        float pv = p;
+        if constexpr (DROP) pv *= drop_scale(dm, dw[(g0 + i) / 2], uint32_t(kb + g0 + i));
+#pragma unroll
+        for (int c = 0; c < DH; ++c) acc[c] = fmaf(pv, vr[i][c], acc[c]);
+      }
+      pin(l);
+#pragma unroll
+      for (int c = 0; c < DH; ++c) pin(acc[c]);
+    }
+    m = m_new;
+    if (ns_dst) {
+      // |S| of 16 keys x 64 rows through this wave's LDS patch: lane = row
+      // writes its 16 values, then lane = (key, quarter of the rows) adds 16
+      // rows and the four quarters meet by shuffles (fixed order).
+#pragma unroll
+      for (int h0 = 0; h0 < kKeyTile; h0 += kNsKeys) {
+#pragma unroll
+        for (int c = 0; c < kNsKeys; c += 4) {
+          const float4 a = {fabsf(s[h0 + c]), fabsf(s[h0 + c + 1]), fabsf(s[h0 + c + 2]),
+                            fabsf(s[h0 + c + 3])};
+          *reinterpret_cast<float4*>(ns_w + lane * kNsStride + c) = a;
+        }
+        __builtin_amdgcn_wave_barrier();
+        const int key = lane & (kNsKeys - 1);
+        const int rq = lane >> 4;
+        float x = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) x += ns_w[(rq * 16 + r) * kNsStride + key];
+        x += shfl_xor(x, 16);
+        x += shfl_xor(x, 32);
+        const int kj = kb + h0 + key;
+        if (lane < kNsKeys && kj < k1) ns_dst[kj] = x;
+        __builtin_amdgcn_wave_barrier();
+      }
     }
   }
-  l += shfl_xor(l, 16);
-  l += shfl_xor(l, 32);
+
+  // the waves' partial softmax states: common maximum, then sums in wave order
+  m_lds[w * kWave + lane] = m;
+  __syncthreads();
+  float M = m_lds[lane];
 #pragma unroll
-  for (int c = 0; c < DH; ++c) {
-    acc[c] += shfl_xor(acc[c], 16);
-    acc[c] += shfl_xor(acc[c], 32);
+  for (int u = 1; u < kWaves; ++u) M = fmaxf(M, m_lds[u * kWave + lane]);
+  const float alpha = m == -INFINITY ? 0.f : __expf(m - M);
+  float x[DH + 1];
+#pragma unroll
+  for (int c = 0; c < DH; ++c) x[c] = acc[c] * alpha;
+  x[DH] = l * alpha;
+  waves_sum<DH + 1>(x, lds, w, lane);
+  if (n_split > 1) {
+    // the split's softmax state (max M, sum l, unnormalised acc) for the combine
+    if (w == 0 && q_ok) {
+      const int64_t r = (int64_t(sp) * H + h) * n_q + qi;
+      part_ml[2 * r] = M;
+      part_ml[2 * r + 1] = x[DH];
+      float a[DH];
+#pragma unroll
+      for (int c = 0; c < DH; ++c) a[c] = x[c];
+      store_f32<DH>(part_acc + ((int64_t(sp) * n_q + qi) * H + h) * DH, a);
+    }
+    return;
   }
-  if (q_ok && g == 0) {
+  if (w == 0 && q_ok) {
     float o[DH];
-    const float inv = n_k > 0 ? 1.0f / l : 0.f;
+    const float inv = n_k > 0 ? 1.0f / x[DH] : 0.f;
 #pragma unroll
-    for (int c = 0; c < DH; ++c) o[c] = acc[c] * inv;
+    for (int c = 0; c < DH; ++c) o[c] = x[c] * inv;
     store_row<T, DH>(out + (qi * H + h) * DH, o);
     if (out32) store_f32<DH>(out32 + (qi * H + h) * DH, o);
-    lse[int64_t(h) * n_q + qi] = n_k > 0 ? m + __logf(l) : -INFINITY;
+    lse[int64_t(h) * n_q + qi] = n_k > 0 ? M + __logf(x[DH]) : -INFINITY;
+  }
+}
+
+// The key splits' softmax states of one (query, head) per thread, in split
+// order: M = max M_s, l = sum l_s e^(M_s - M), out = sum acc_s e^(M_s - M) / l.
+template <typename T, int DH>
+__global__ __launch_bounds__(kBlock) void k_dense_combine(
+    const float* __restrict__ part_ml, const float* __restrict__ part_acc, int32_t n_split,
+    int32_t n_q, int32_t H, T* __restrict__ out, float* __restrict__ out32,
+    float* __restrict__ lse) {
+  const int64_t n = int64_t(n_q) * H;
+  for (int64_t t = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; t < n;
+       t += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t qi = t / H, h = t % H;
+    float M = -INFINITY;
+    for (int s = 0; s < n_split; ++s) M = fmaxf(M, part_ml[2 * ((s * H + h) * n_q + qi)]);
+    float l = 0.f, acc[DH];
+#pragma unroll
+    for (int c = 0; c < DH; ++c) acc[c] = 0.f;
+    for (int s = 0; s < n_split; ++s) {
+      const int64_t r = (s * H + h) * n_q + qi;
+      const float a = __expf(part_ml[2 * r] - M);
+      l = fmaf(a, part_ml[2 * r + 1], l);
+      float pa[DH];
+      load_row<float, DH>(part_acc + (s * n_q + qi) * H * DH + h * DH, pa);
+#pragma unroll
+      for (int c = 0; c < DH; ++c) acc[c] = fmaf(a, pa[c], acc[c]);
+    }
+    const float inv = 1.0f / l;
+#pragma unroll
+    for (int c = 0; c < DH; ++c) acc[c] *= inv;
+    store_row<T, DH>(out + t * DH, acc);
+    if (out32) store_f32<DH>(out32 + t * DH, acc);
+    lse[h * n_q + qi] = M + __logf(l);
   }
 }
 
@@ -214,83 +363,128 @@ __global__ __launch_bounds__(kBlock) void k_dense_rowstat(const TO* __restrict__
   }
 }
 
-// Key-major pass: lane owns key row (lane % 16) of the wave and 8 queries of
-// each 32-query tile.  grid = (ceil(n_k / 64), H).
+// Key-major pass: one block = 64 key rows (one per lane) of one head, in the
+// forward's block order; its waves take the 16-query tiles in turn.  Each
+// lane keeps K_j * scale and V_j; the query rows (Q, dO, lse, D) are read at
+// wave-uniform addresses.  dK = scale sum_i dS_ij Q_i is summed unscaled and
+// scaled once.
 template <typename T, int DH, bool DROP>
 __global__ __launch_bounds__(kBlock) void k_dense_bwd_kv(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const T* __restrict__ g, const float* __restrict__ lse, const float* __restrict__ dsum,
     int32_t n_q, int32_t n_k, int32_t H, float scale, DropoutMask dm, T* __restrict__ grad_k,
     T* __restrict__ grad_v) {
+  __shared__ float lds[kLdsFloats];
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x >> 6;
-  const int r = lane & 15;
-  const int grp = lane >> 4;
-  const int h = blockIdx.y;
-  const int64_t kj = int64_t(blockIdx.x) * kRowsPerBlock + wave * kRows + r;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int h = __builtin_amdgcn_readfirstlane(blockIdx.x % H);
+  const int rb = __builtin_amdgcn_readfirstlane(blockIdx.x / H);
+  const int64_t kj = int64_t(rb) * kRowsPerBlock + lane;
   const bool k_ok = kj < n_k;
   if constexpr (DROP) dm = drop_for_head(dm, h);
-  float kr[DH], vr[DH], dk[DH], dv[DH];
+  float ks[DH], vr[DH], dk[DH], dv[DH];
   if (k_ok) {
-    load_row<T, DH>(k + (kj * H + h) * DH, kr);
+    load_row<T, DH>(k + (kj * H + h) * DH, ks);
     load_row<T, DH>(v + (kj * H + h) * DH, vr);
+#pragma unroll
+    for (int c = 0; c < DH; ++c) ks[c] *= scale;
   } else {
 #pragma unroll
-    for (int c = 0; c < DH; ++c) kr[c] = vr[c] = 0.f;
+    for (int c = 0; c < DH; ++c) ks[c] = vr[c] = 0.f;
   }
 #pragma unroll
   for (int c = 0; c < DH; ++c) dk[c] = dv[c] = 0.f;
-  const float* lse_h = lse + int64_t(h) * n_q;
-  const float* ds_h = dsum + int64_t(h) * n_q;
-  for (int qb = grp * kColsPerLane; qb < n_q; qb += kTile) {
-#pragma unroll 2
-    for (int i = 0; i < kColsPerLane; ++i) {
-      const int64_t qi = qb + i;
-      if (qi < n_q) {
-        float qs[DH], gi[DH];
-        load_row<T, DH>(q + (qi * H + h) * DH, qs);
-        load_row<T, DH>(g + (qi * H + h) * DH, gi);
+  const int hs = uniform_int(h);
+  const int64_t HD = int64_t(H) * DH;
+  const T* q_h = q + int64_t(hs) * DH;  // streamed rows of this head
+  const T* g_h = g + int64_t(hs) * DH;
+  const float* lse_h = lse + int64_t(hs) * n_q;
+  const float* ds_h = dsum + int64_t(hs) * n_q;
+  // one query's contribution, from its streamed rows
+  auto contrib = [&](int qi, const float (&qr)[DH], const float (&gr)[DH], float L, float D) {
+    const float p = __expf(dot1<DH>(qr, ks) - L);
+    float mm = 1.f;
+    if constexpr (DROP)
+      mm = drop_scale(dm, drop_word(dm, uint32_t(qi), uint32_t(kj)), uint32_t(kj));
+    const float ds = p * (mm * dot1<DH>(gr, vr) - D);
+    const float pm = p * mm;
 #pragma unroll
-        for (int c = 0; c < DH; ++c) qs[c] *= scale;
-        const float p = __expf(dotv<DH>(qs, kr) - lse_h[qi]);
-        float m = 1.f;
-        if constexpr (DROP)
-          m = drop_scale(dm, drop_word(dm, uint32_t(qi), uint32_t(kj)), uint32_t(kj));
-        const float ds = p * (m * dotv<DH>(gi, vr) - ds_h[qi]);
-        const float pm = p * m;
+    for (int c = 0; c < DH; ++c) {
+      dv[c] = fmaf(pm, gr[c], dv[c]);
+      dk[c] = fmaf(ds, qr[c], dk[c]);
+    }
+  };
+  auto step = [&](int qi) {
+    float qr[DH], gr[DH];
+    load_row<T, DH>(q_h + int64_t(qi) * HD, qr);
+    load_row<T, DH>(g_h + int64_t(qi) * HD, gr);
+    contrib(qi, qr, gr, lse_h[qi], ds_h[qi]);
+  };
+  // Full tiles in groups of kGroup queries: a group's scalar loads are issued
+  // together from an opaque copy of its first index and its results pinned
+  // before the next group (else each load waits on its own).  At d = 64 the
+  // lane's own K, V, dK, dV rows already take 256 registers.
+  constexpr int kGroup = DH >= 16 ? 1 : 16 / DH;
+  constexpr int kUnroll = DH >= 64 ? 2 : kStreamTile / kGroup;
+  const int n_tiles = (n_q + kStreamTile - 1) / kStreamTile;
+  for (int t = w; t < n_tiles; t += kWaves) {
+    const int qb = t * kStreamTile;
+    if (qb + kStreamTile <= n_q) {
+#pragma unroll kUnroll
+      for (int g0 = 0; g0 < kStreamTile; g0 += kGroup) {
+        const int qg = uniform_int(qb + g0);
+        float qr[kGroup][DH], gr[kGroup][DH], L[kGroup], D[kGroup];
+#pragma unroll
+        for (int i = 0; i < kGroup; ++i) {
+          load_row<T, DH>(q_h + int64_t(qg + i) * HD, qr[i]);
+          load_row<T, DH>(g_h + int64_t(qg + i) * HD, gr[i]);
+          L[i] = lse_h[qg + i];
+          D[i] = ds_h[qg + i];
+        }
+#pragma unroll
+        for (int i = 0; i < kGroup; ++i) contrib(qg + i, qr[i], gr[i], L[i], D[i]);
 #pragma unroll
         for (int c = 0; c < DH; ++c) {
-          dv[c] = fmaf(pm, gi[c], dv[c]);
-          dk[c] = fmaf(ds, qs[c], dk[c]);
+          pin(dk[c]);
+          pin(dv[c]);
         }
       }
+    } else {
+      for (int i = 0; qb + i < n_q; ++i) step(qb + i);
     }
   }
+  float x[2 * DH];
 #pragma unroll
   for (int c = 0; c < DH; ++c) {
-    dk[c] += shfl_xor(dk[c], 16);
-    dk[c] += shfl_xor(dk[c], 32);
-    dv[c] += shfl_xor(dv[c], 16);
-    dv[c] += shfl_xor(dv[c], 32);
+    x[c] = dk[c];
+    x[DH + c] = dv[c];
   }
-  if (k_ok && grp == 0) {
+  waves_sum<2 * DH>(x, lds, w, lane);
+  if (w == 0 && k_ok) {
+#pragma unroll
+    for (int c = 0; c < DH; ++c) {
+      dk[c] = x[c] * scale;
+      dv[c] = x[DH + c];
+    }
     store_row<T, DH>(grad_k + (kj * H + h) * DH, dk);
     store_row<T, DH>(grad_v + (kj * H + h) * DH, dv);
   }
 }
 
-// Query-major pass: lane owns query row (lane % 16) and 8 keys per tile.
+// Query-major pass: one block = 64 query rows (one per lane) of one head; its
+// waves take the 16-key tiles in turn, reading K/V rows at wave-uniform
+// addresses.
 template <typename T, int DH, bool DROP>
 __global__ __launch_bounds__(kBlock) void k_dense_bwd_q(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const T* __restrict__ g, const float* __restrict__ lse, const float* __restrict__ dsum,
     int32_t n_q, int32_t n_k, int32_t H, float scale, DropoutMask dm, T* __restrict__ grad_q) {
+  __shared__ float lds[kLdsFloats];
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x >> 6;
-  const int r = lane & 15;
-  const int grp = lane >> 4;
-  const int h = blockIdx.y;
-  const int64_t qi = int64_t(blockIdx.x) * kRowsPerBlock + wave * kRows + r;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int h = __builtin_amdgcn_readfirstlane(blockIdx.x % H);
+  const int rb = __builtin_amdgcn_readfirstlane(blockIdx.x / H);
+  const int64_t qi = int64_t(rb) * kRowsPerBlock + lane;
   const bool q_ok = qi < n_q;
   if constexpr (DROP) dm = drop_for_head(dm, h);
   float qs[DH], gi[DH], dq[DH];
@@ -308,31 +502,68 @@ __global__ __launch_bounds__(kBlock) void k_dense_bwd_q(
   }
 #pragma unroll
   for (int c = 0; c < DH; ++c) dq[c] = 0.f;
-  for (int kb = grp * kColsPerLane; kb < n_k; kb += kTile) {
-#pragma unroll 2
-    for (int i = 0; i < kColsPerLane; ++i) {
-      const int64_t kj = kb + i;
-      if (kj < n_k) {
-        float kr[DH], vr[DH];
-        load_row<T, DH>(k + (kj * H + h) * DH, kr);
-        load_row<T, DH>(v + (kj * H + h) * DH, vr);
-        const float p = __expf(dotv<DH>(qs, kr) - L);
-        float m = 1.f;
-        if constexpr (DROP)
-          m = drop_scale(dm, drop_word(dm, uint32_t(qi), uint32_t(kj)), uint32_t(kj));
-        const float ds = p * (m * dotv<DH>(gi, vr) - Dq);
+  const int hs = uniform_int(h);
+  const int64_t HD = int64_t(H) * DH;
+  const T* k_h = k + int64_t(hs) * DH;  // streamed rows of this head
+  const T* v_h = v + int64_t(hs) * DH;
+  // one key's contribution, from its streamed rows
+  auto contrib = [&](int kj, const float (&kr)[DH], const float (&vr)[DH], uint32_t word) {
+    const float p = __expf(dot1<DH>(qs, kr) - L);
+    float mm = 1.f;
+    if constexpr (DROP) mm = drop_scale(dm, word, uint32_t(kj));
+    const float ds = p * (mm * dot1<DH>(gi, vr) - Dq);
 #pragma unroll
-        for (int c = 0; c < DH; ++c) dq[c] = fmaf(ds, kr[c], dq[c]);
+    for (int c = 0; c < DH; ++c) dq[c] = fmaf(ds, kr[c], dq[c]);
+  };
+  auto step = [&](int kj, uint32_t word) {
+    float kr[DH], vr[DH];
+    load_row<T, DH>(k_h + int64_t(kj) * HD, kr);
+    load_row<T, DH>(v_h + int64_t(kj) * HD, vr);
+    contrib(kj, kr, vr, word);
+  };
+  // full tiles in groups of kGroup keys (a key pair at least), loads issued
+  // together and results pinned per group as in the dK/dV pass (at d = 8,
+  // pairs: 1.72 ms at 16,000 x 16,000 x 8 heads, against 2.14 ms for groups
+  // of 4, whose 64 scalar registers of rows stall the wave longer)
+#ifndef NGT_DENSE_Q_GROUP
+#define NGT_DENSE_Q_GROUP 2
+#endif
+  constexpr int kGroup = DH >= 16 ? 2 : NGT_DENSE_Q_GROUP;
+  const int n_tiles = (n_k + kStreamTile - 1) / kStreamTile;
+  for (int t = w; t < n_tiles; t += kWaves) {
+    const int kb = t * kStreamTile;
+    if (kb + kStreamTile <= n_k) {
+#pragma unroll
+      for (int g0 = 0; g0 < kStreamTile; g0 += kGroup) {
+        const int kg = uniform_int(kb + g0);
+        float kr[kGroup][DH], vr[kGroup][DH];
+#pragma unroll
+        for (int i = 0; i < kGroup; ++i) {
+          load_row<T, DH>(k_h + int64_t(kg + i) * HD, kr[i]);
+          load_row<T, DH>(v_h + int64_t(kg + i) * HD, vr[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < kGroup; i += 2) {
+          const uint32_t word = DROP ? drop_word(dm, uint32_t(qi), uint32_t(kb + g0 + i)) : 0U;
+          contrib(kb + g0 + i, kr[i], vr[i], word);
+          contrib(kb + g0 + i + 1, kr[i + 1], vr[i + 1], word);
+        }
+#pragma unroll
+        for (int c = 0; c < DH; ++c) pin(dq[c]);
+      }
+    } else {
+      for (int i = 0; kb + i < n_k; ++i) {
+        const uint32_t word = DROP ? drop_word(dm, uint32_t(qi), uint32_t(kb + i)) : 0U;
+        step(kb + i, word);
       }
     }
   }
+  waves_sum<DH>(dq, lds, w, lane);
+  if (w == 0 && q_ok) {
 #pragma unroll
-  for (int c = 0; c < DH; ++c) {
-    dq[c] += shfl_xor(dq[c], 16);
-    dq[c] += shfl_xor(dq[c], 32);
-    dq[c] *= scale;
+    for (int c = 0; c < DH; ++c) dq[c] *= scale;
+    store_row<T, DH>(grad_q + (qi * H + h) * DH, dq);
   }
-  if (q_ok && grp == 0) store_row<T, DH>(grad_q + (qi * H + h) * DH, dq);
 }
 
 // ------------------------------------------------------------------ host side
@@ -340,8 +571,34 @@ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 inline int64_t qblocks(int32_t n) { return (int64_t(n) + kRowsPerBlock - 1) / kRowsPerBlock; }
 
-size_t fwd_ws(int32_t n_q, int32_t n_k, int32_t H) {
+// Key splits of the vector-ALU forward: about kSplitTarget blocks in all
+// (several rounds of resident blocks, so the last round's idle tail stays
+// small), at least kMinSplitKeys keys per split, splits whole key tiles.
+constexpr int64_t kSplitTarget = 8192;
+constexpr int kMinSplitKeys = 512;
+struct KeySplit {
+  int n_split, split_keys;
+};
+KeySplit key_split(int32_t n_q, int32_t n_k, int32_t H) {
+  const int64_t units = qblocks(n_q) * H;
+  int64_t want = units > 0 ? (kSplitTarget + units - 1) / units : 1;
+  want = std::min<int64_t>(want, std::max<int64_t>(1, n_k / kMinSplitKeys));
+  if (want <= 1 || n_k <= 0) return {1, std::max(n_k, 1)};
+  int keys = static_cast<int>((n_k + want - 1) / want);
+  keys = (keys + kKeyTile - 1) / kKeyTile * kKeyTile;
+  return {static_cast<int>((n_k + keys - 1) / keys), keys};
+}
+
+size_t ns_part_bytes(int32_t n_q, int32_t n_k, int32_t H) {
   return align256(size_t(qblocks(n_q)) * H * size_t(n_k) * 4);
+}
+size_t split_bytes(int32_t n_q, int32_t n_k, int32_t H, int32_t d) {
+  const KeySplit ks = key_split(n_q, n_k, H);
+  if (ks.n_split <= 1) return 0;
+  return align256(size_t(ks.n_split) * n_q * H * 8) + align256(size_t(ks.n_split) * n_q * H * d * 4);
+}
+size_t fwd_ws(int32_t n_q, int32_t n_k, int32_t H, int32_t d) {
+  return ns_part_bytes(n_q, n_k, H) + split_bytes(n_q, n_k, H, d);
 }
 size_t bwd_ws(int32_t n_q, int32_t H) { return align256(size_t(n_q) * H * 4); }
 
@@ -351,20 +608,33 @@ int launch_fwd(const void* q, const void* k, const void* v, int n_q, int n_k, in
                hipStream_t st) {
   if (n_q == 0) return NGT_OK;
   float* part = ns ? reinterpret_cast<float*>(ws) : nullptr;
-  dim3 grid(static_cast<unsigned>(qblocks(n_q)), static_cast<unsigned>(H));
+  const KeySplit ks = key_split(n_q, n_k, H);
+  float* part_ml = ks.n_split > 1 ? reinterpret_cast<float*>(ws + ns_part_bytes(n_q, n_k, H))
+                                  : nullptr;
+  float* part_acc =
+      ks.n_split > 1 ? part_ml + align256(size_t(ks.n_split) * n_q * H * 8) / 4 : nullptr;
+  const dim3 grid(static_cast<unsigned>(qblocks(n_q) * H * ks.n_split));
   {
     KernelTimer timer_("dense_fwd", st);
     const DropoutMask m = dm ? *dm : DropoutMask{};
     if (dm)
       hipLaunchKernelGGL((k_dense_fwd<T, DH, true>), grid, dim3(kBlock), 0, st,
                          static_cast<const T*>(q), static_cast<const T*>(k),
-                         static_cast<const T*>(v), n_q, n_k, H, scale, m, static_cast<T*>(out),
-                         out32, lse, part);
+                         static_cast<const T*>(v), n_q, n_k, H, scale, m, ks.n_split,
+                         ks.split_keys, static_cast<T*>(out), out32, lse, part, part_ml, part_acc);
     else
       hipLaunchKernelGGL((k_dense_fwd<T, DH, false>), grid, dim3(kBlock), 0, st,
                          static_cast<const T*>(q), static_cast<const T*>(k),
-                         static_cast<const T*>(v), n_q, n_k, H, scale, m, static_cast<T*>(out),
-                         out32, lse, part);
+                         static_cast<const T*>(v), n_q, n_k, H, scale, m, ks.n_split,
+                         ks.split_keys, static_cast<T*>(out), out32, lse, part, part_ml, part_acc);
+    NGT_HIP_CHECK(hipGetLastError());
+  }
+  if (ks.n_split > 1) {
+    KernelTimer timer_("dense_combine", st);
+    int64_t blocks = (int64_t(n_q) * H + kBlock - 1) / kBlock;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL((k_dense_combine<T, DH>), dim3(int(blocks)), dim3(kBlock), 0, st, part_ml,
+                       part_acc, ks.n_split, n_q, H, static_cast<T*>(out), out32, lse);
     NGT_HIP_CHECK(hipGetLastError());
   }
   if (ns && n_k > 0) {
@@ -397,7 +667,7 @@ int launch_bwd(const void* q, const void* k, const void* v, const void* out, con
     }
   }
   if (n_k > 0) {
-    dim3 grid(static_cast<unsigned>(qblocks(n_k)), static_cast<unsigned>(H));
+    const dim3 grid(static_cast<unsigned>(qblocks(n_k) * H));
     {
       KernelTimer timer_("dense_bwd_kv", st);
       if (dm)
@@ -414,7 +684,7 @@ int launch_bwd(const void* q, const void* k, const void* v, const void* out, con
     }
   }
   if (n_q > 0) {
-    dim3 grid(static_cast<unsigned>(qblocks(n_q)), static_cast<unsigned>(H));
+    const dim3 grid(static_cast<unsigned>(qblocks(n_q) * H));
     {
       KernelTimer timer_("dense_bwd_q", st);
       if (dm)
@@ -545,7 +815,7 @@ extern "C" int ngt_dense_workspace_bytes(int32_t n_q, int32_t n_k, int32_t n_hea
                                          int32_t head_dim, size_t* fwd_bytes, size_t* bwd_bytes) {
   const int rc = check_args("ngt_dense_workspace_bytes", NGT_F32, n_q, n_k, n_heads, head_dim);
   if (rc != NGT_OK) return rc;
-  if (fwd_bytes) *fwd_bytes = fwd_ws(n_q, n_k, n_heads);
+  if (fwd_bytes) *fwd_bytes = fwd_ws(n_q, n_k, n_heads, head_dim);
   if (bwd_bytes) *bwd_bytes = bwd_ws(n_q, n_heads);
   return NGT_OK;
 }
@@ -563,9 +833,16 @@ extern "C" int ngt_dense_fwd(int dtype, const void* q, const void* k, const void
   const DropoutMask* dm = drop ? &dmv : nullptr;
   if (n_q > 0 && (!q || !out || !lse)) return set_error(NGT_ERR_ARG, "ngt_dense_fwd: null q/out/lse");
   if (n_k > 0 && (!k || !v)) return set_error(NGT_ERR_ARG, "ngt_dense_fwd: null k/v");
-  if (node_score && n_q > 0) {
-    const size_t need = fwd_ws(n_q, n_k, n_heads);
-    if (!workspace || workspace_bytes < need)
+  if (n_q > 0) {
+    // node-score partials; the vector-ALU kernels' key-split states after them
+    size_t need = 0;
+    if (!use_mfma(dtype, head_dim))
+      need = node_score || key_split(n_q, n_k, n_heads).n_split > 1
+                 ? fwd_ws(n_q, n_k, n_heads, head_dim)
+                 : 0;
+    else if (node_score)
+      need = ns_part_bytes(n_q, n_k, n_heads);
+    if (need && (!workspace || workspace_bytes < need))
       return set_error(NGT_ERR_WORKSPACE, "ngt_dense_fwd: workspace %zu < %zu", workspace_bytes,
                        need);
   }

@@ -37,7 +37,11 @@ def _qkv(n_q, n_k, H, d, dtype, seed):
     (50, 77, 1, 32, torch.float32), (40, 40, 2, 64, torch.float32),
     (100, 100, 8, 8, torch.bfloat16), (96, 150, 4, 16, torch.bfloat16),
     (60, 61, 2, 24, torch.bfloat16), (70, 45, 3, 32, torch.bfloat16),
-    (33, 47, 2, 64, torch.bfloat16), (1, 1, 1, 8, torch.bfloat16), (130, 33, 2, 8, torch.bfloat16)])
+    (33, 47, 2, 64, torch.bfloat16), (1, 1, 1, 8, torch.bfloat16), (130, 33, 2, 8, torch.bfloat16),
+    # long key ranges: the vector-ALU forward splits the keys over blocks
+    # (5, 4, 2 and 3 splits, last one ragged) and combines the splits
+    (100, 3000, 2, 8, torch.float32), (37, 2100, 1, 24, torch.float32),
+    (64, 1300, 3, 64, torch.float32), (50, 1800, 2, 64, torch.bfloat16)])
 def test_dense_parity(n_q, n_k, H, d, dtype):
     _say(f"case dense n_q={n_q} n_k={n_k} H={H} d={d} {dtype}")
     q, k, v, go = _qkv(n_q, n_k, H, d, dtype, seed=n_q + d)
@@ -120,7 +124,7 @@ def _run_drop(q, k, v, go, p, seed, flash=False):
     (40, 40, 2, 64, torch.float32, 0.5), (100, 99, 4, 8, torch.bfloat16, 0.5),
     (96, 150, 2, 16, torch.bfloat16, 0.2), (60, 61, 2, 24, torch.bfloat16, 0.5),
     (70, 45, 3, 32, torch.bfloat16, 0.7), (33, 47, 2, 64, torch.bfloat16, 0.5),
-    (50, 50, 2, 8, torch.bfloat16, 1.0)])
+    (50, 50, 2, 8, torch.bfloat16, 1.0), (70, 2500, 2, 16, torch.float32, 0.5)])
 def test_dense_dropout_parity(n_q, n_k, H, d, dtype, p):
     """Training-mode dropout on P: the kernels' mask equals the oracle's
     (same seed), and out / dQ / dK / dV match the restatement with that mask."""
