@@ -48,6 +48,9 @@ CONFIGS = {
     "gt_arxiv": WindowConfig("gt_arxiv", 10584, 13.8, 8, 16, torch.bfloat16, related_per_query=8,
                              n_global=169343, feat_dim=128),
     "dense_slim": WindowConfig("dense_slim", 16000, 0.0, 8, 8, torch.bfloat16, dense=True),
+    # the same all-pairs window in fp32, the dtype the reference's ablation trains in
+    "dense_slim_f32": WindowConfig("dense_slim_f32", 16000, 0.0, 8, 8, torch.float32,
+                                   dense=True),
     "gph_large": WindowConfig("gph_large", 32768, 50.5, 32, 24, torch.bfloat16,
                               related_per_query=4, n_global=2449029, feat_dim=100, layers=12),
     "gt_highdeg": WindowConfig("gt_highdeg", 7280, 490.0, 8, 16, torch.bfloat16,
