@@ -53,6 +53,21 @@ def test_dense_parity(n_q, n_k, H, d, dtype):
         assert_parity(res[name].float(), ref[name], ref64[name], dtype, name)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("n_q,n_k", [(0, 37), (45, 0)])
+def test_dense_empty_side(n_q, n_k, dtype):
+    """A window without queries or without keys: the empty softmax axis and
+    P @ V give zeros (the oracle's torch ops, as the reference's): node scores
+    0 over the keys and dK = dV = 0, or out = 0 and dQ = 0."""
+    _say(f"case dense empty n_q={n_q} n_k={n_k} {dtype}")
+    q, k, v, go = _qkv(n_q, n_k, 2, 8, dtype, seed=5)
+    res = _run(q, k, v, go)
+    ref = OA.full_fwd_bwd(q.float(), k.float(), v.float(), go.float())
+    for name in ("x", "node_scores", "dq", "dk", "dv"):
+        assert res[name].shape == ref[name].shape, name
+        assert torch.equal(res[name].float(), ref[name]), name
+
+
 def test_dense_golden():
     for f in sorted((Path(__file__).parent / "golden").glob("attn_dense_*.npz")):
         _say(f"case golden {f.name}")
