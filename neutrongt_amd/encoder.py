@@ -157,12 +157,19 @@ class EncoderLayer(nn.Module):
         self.ffn_dropout = nn.Dropout(dropout_rate)
 
     def forward(self, x, edge_index=None, attn_type="sparse", kv_cache=None):
-        y, score, kv = self.self_attention(self.self_attention_norm(x), edge_index, attn_type,
-                                           kv_cache)
+        x, f, score, kv = self.forward_open(x, self.self_attention_norm(x), edge_index,
+                                            attn_type, kv_cache)
+        return x + self.ffn_dropout(f), score, kv
+
+    def forward_open(self, x, x_norm, edge_index=None, attn_type="sparse", kv_cache=None):
+        """The block from x and its LayerNorm x_norm = self_attention_norm(x)
+        on, with the FFN's residual add left open: returns (x', f, score, kv),
+        the block's output being x' + ffn_dropout(f).  A stack closes it
+        together with the next LayerNorm (add_dropout_layernorm)."""
+        y, score, kv = self.self_attention(x_norm, edge_index, attn_type, kv_cache)
         # x + Drop(y) and the FFN's LayerNorm of it: one fused pass under bf16 autocast
         x, h = add_dropout_layernorm(x, y, self.ffn_norm, self.self_attention_dropout)
-        x = x + self.ffn_dropout(self.ffn(h))
-        return x, score, kv
+        return x, self.ffn(h), score, kv
 
 
 class GTEncoderLayer(nn.Module):
@@ -223,6 +230,20 @@ class _WindowModel(nn.Module):
             raise ValueError(f"kv_cache has {len(kv_cache)} entries for {self.n_layers} layers")
         h = self.input_dropout(self.node_encoder(x.unsqueeze(0)))
         scores = []
+        if isinstance(self, WindowGraphormer) and self.n_layers > 0:
+            # pre-LN stack: each block's FFN residual add + dropout and the
+            # LayerNorm after it (the next block's, or final_ln) are one pass
+            h_norm = self.layers[0].self_attention_norm(h)
+            for i, layer in enumerate(self.layers):
+                x_res, f, score, _ = layer.forward_open(
+                    h, h_norm, edge_index, attn_type,
+                    kv_cache[i] if kv_cache is not None else None)
+                scores.append(score.detach() if score is not None else None)
+                ln = (self.layers[i + 1].self_attention_norm if i + 1 < self.n_layers
+                      else self.final_ln)
+                h, h_norm = add_dropout_layernorm(x_res, f, ln, layer.ffn_dropout)
+            logits = self.downstream_out_proj(h_norm[0])
+            return F.log_softmax(logits.float(), dim=1), scores
         for i, layer in enumerate(self.layers):
             h, score, _ = layer(h, edge_index, attn_type,
                                 kv_cache[i] if kv_cache is not None else None)
