@@ -58,11 +58,15 @@ def test_sparse_graph_replay_matches_eager(H, d, dtype):
     _capture_and_check(step, (q, k, v))
 
 
-def test_dense_graph_replay_matches_eager():
-    print("case graph dense", flush=True)
-    n, H, d = 500, 4, 8
+@pytest.mark.parametrize("n_q,n_k,H,d,dtype", [
+    (500, 500, 4, 8, torch.bfloat16),   # matrix-core kernels
+    (300, 2100, 2, 8, torch.float32),   # vector-ALU kernels, keys split over 4 blocks + combine
+])
+def test_dense_graph_replay_matches_eager(n_q, n_k, H, d, dtype):
+    print(f"case graph dense n_q={n_q} n_k={n_k} H={H} d={d} {dtype}", flush=True)
     g = torch.Generator().manual_seed(2)
-    q, k, v, go = (torch.randn(n, H, d, generator=g).to(torch.bfloat16).cuda() for _ in range(4))
+    q, k, v, go = (torch.randn(n, H, d, generator=g).to(dtype).cuda()
+                   for n in (n_q, n_k, n_k, n_q))
     for t in (q, k, v):
         t.requires_grad_(True)
 
