@@ -417,12 +417,13 @@ __global__ __launch_bounds__(kBlock) void k_dense_bwd_kv(
   const T* g_h = g + int64_t(hs) * DH;
   const float* lse_h = lse + int64_t(hs) * n_q;
   const float* ds_h = dsum + int64_t(hs) * n_q;
-  // one query's contribution, from its streamed rows
-  auto contrib = [&](int qi, const float (&qr)[DH], const float (&gr)[DH], float L, float D) {
+  // one query's contribution, from its streamed rows (word: the dropout word
+  // of (qi, this lane's key pair))
+  auto contrib = [&](const float (&qr)[DH], const float (&gr)[DH], float L, float D,
+                     uint32_t word) {
     const float p = __expf(dot1<DH>(qr, ks) - L);
     float mm = 1.f;
-    if constexpr (DROP)
-      mm = drop_scale(dm, drop_word(dm, uint32_t(qi), uint32_t(kj)), uint32_t(kj));
+    if constexpr (DROP) mm = drop_scale(dm, word, uint32_t(kj));
     const float ds = p * (mm * dot1<DH>(gr, vr) - D);
     const float pm = p * mm;
 #pragma unroll
@@ -435,7 +436,7 @@ __global__ __launch_bounds__(kBlock) void k_dense_bwd_kv(
     float qr[DH], gr[DH];
     load_row<T, DH>(q_h + int64_t(qi) * HD, qr);
     load_row<T, DH>(g_h + int64_t(qi) * HD, gr);
-    contrib(qi, qr, gr, lse_h[qi], ds_h[qi]);
+    contrib(qr, gr, lse_h[qi], ds_h[qi], DROP ? drop_word(dm, uint32_t(qi), uint32_t(kj)) : 0U);
   };
   // Full tiles in groups of kGroup queries: a group's scalar loads are issued
   // together from an opaque copy of its first index and its results pinned
@@ -458,8 +459,26 @@ __global__ __launch_bounds__(kBlock) void k_dense_bwd_kv(
           L[i] = lse_h[qg + i];
           D[i] = ds_h[qg + i];
         }
+        uint32_t wd[kGroup] = {};
+        if constexpr (DROP && kGroup % 2 == 0) {
+          // Lanes 2m and 2m + 1 hold one key pair, hence one dropout word per
+          // query: the even lane hashes query i's, the odd lane query i + 1's,
+          // and they swap (DPP quad_perm [1, 0, 3, 2]).
+          const bool odd = lane & 1;
 #pragma unroll
-        for (int i = 0; i < kGroup; ++i) contrib(qg + i, qr[i], gr[i], L[i], D[i]);
+          for (int i = 0; i < kGroup; i += 2) {
+            const uint32_t mine = drop_word(dm, uint32_t(qg + i + odd), uint32_t(kj));
+            const uint32_t other = static_cast<uint32_t>(
+                __builtin_amdgcn_mov_dpp(static_cast<int>(mine), 0xB1, 0xf, 0xf, false));
+            wd[i] = odd ? other : mine;
+            wd[i + 1] = odd ? mine : other;
+          }
+        } else if constexpr (DROP) {
+#pragma unroll
+          for (int i = 0; i < kGroup; ++i) wd[i] = drop_word(dm, uint32_t(qg + i), uint32_t(kj));
+        }
+#pragma unroll
+        for (int i = 0; i < kGroup; ++i) contrib(qr[i], gr[i], L[i], D[i], wd[i]);
 #pragma unroll
         for (int c = 0; c < DH; ++c) {
           pin(dk[c]);
