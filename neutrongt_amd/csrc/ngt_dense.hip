@@ -53,7 +53,9 @@ static_assert((kWaves - 1) * kSumChunk * kWave <= kLdsFloats, "cross-wave sum bu
 static_assert(kKeyTile % kNsKeys == 0 && kStreamTile % 2 == 0, "tiles cover whole key pairs");
 
 // One dependent FMA chain: the kernels keep several rows' dot products in
-// flight, so a second partial sum would only add an addition.
+// flight, so a second partial sum would only add an addition.  (Four partial
+// sums from d = 32 on were measured: the d = 32 forward slowed 2.25 -> 2.53 ms
+// and the d = 64 dK/dV pass spilled, 13.7 -> 18.0 ms.)
 template <int DH>
 __device__ __forceinline__ float dot1(const float (&a)[DH], const float (&b)[DH]) {
   float s = a[0] * b[0];
@@ -438,6 +440,49 @@ __global__ __launch_bounds__(kBlock) void k_dense_bwd_kv(
     load_row<T, DH>(g_h + int64_t(qi) * HD, gr);
     contrib(qr, gr, lse_h[qi], ds_h[qi], DROP ? drop_word(dm, uint32_t(qi), uint32_t(kj)) : 0U);
   };
+  // d = 64: a query's Q and dO rows (128 scalar registers together) do not
+  // fit beside the kernel's other scalars; each is read in halves for the two
+  // dot products and read again, through an opaque index (so the compiler
+  // reloads from the scalar cache instead of keeping the rows), for the dV
+  // and dK updates.
+  auto step_halves = [&](int qi) {
+    constexpr int HF = DH / 2;
+    float s_ = 0.f, dp = 0.f;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      float r[HF];
+      load_row<T, HF>(q_h + int64_t(uniform_int(qi)) * HD + hh * HF, r);
+#pragma unroll
+      for (int c = 0; c < HF; ++c) s_ = fmaf(r[c], ks[hh * HF + c], s_);
+    }
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      float r[HF];
+      load_row<T, HF>(g_h + int64_t(uniform_int(qi)) * HD + hh * HF, r);
+#pragma unroll
+      for (int c = 0; c < HF; ++c) dp = fmaf(r[c], vr[hh * HF + c], dp);
+    }
+    const float p = __expf(s_ - lse_h[qi]);
+    float mm = 1.f;
+    if constexpr (DROP)
+      mm = drop_scale(dm, drop_word(dm, uint32_t(qi), uint32_t(kj)), uint32_t(kj));
+    const float ds = p * (mm * dp - ds_h[qi]);
+    const float pm = p * mm;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      float r[HF];
+      load_row<T, HF>(g_h + int64_t(uniform_int(qi)) * HD + hh * HF, r);
+#pragma unroll
+      for (int c = 0; c < HF; ++c) dv[hh * HF + c] = fmaf(pm, r[c], dv[hh * HF + c]);
+    }
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      float r[HF];
+      load_row<T, HF>(q_h + int64_t(uniform_int(qi)) * HD + hh * HF, r);
+#pragma unroll
+      for (int c = 0; c < HF; ++c) dk[hh * HF + c] = fmaf(ds, r[c], dk[hh * HF + c]);
+    }
+  };
   // Full tiles in groups of kGroup queries: a group's scalar loads are issued
   // together from an opaque copy of its first index and its results pinned
   // before the next group (else each load waits on its own).  At d = 64 the
@@ -447,7 +492,9 @@ __global__ __launch_bounds__(kBlock) void k_dense_bwd_kv(
   const int n_tiles = (n_q + kStreamTile - 1) / kStreamTile;
   for (int t = w; t < n_tiles; t += kWaves) {
     const int qb = t * kStreamTile;
-    if (qb + kStreamTile <= n_q) {
+    if constexpr (DH >= 64) {
+      for (int i = 0; i < kStreamTile && qb + i < n_q; ++i) step_halves(qb + i);
+    } else if (qb + kStreamTile <= n_q) {
 #pragma unroll kUnroll
       for (int g0 = 0; g0 < kStreamTile; g0 += kGroup) {
         const int qg = uniform_int(qb + g0);
@@ -557,6 +604,37 @@ __global__ __launch_bounds__(kBlock) void k_dense_bwd_q(
     load_row<T, DH>(v_h + int64_t(kj) * HD, vr);
     contrib(kj, kr, vr, word);
   };
+  // d = 64: a key's K and V rows are read in halves, and K again through an
+  // opaque index for the dQ update (as in the dK/dV pass)
+  auto step_halves = [&](int kj, uint32_t word) {
+    constexpr int HF = DH / 2;
+    float s_ = 0.f, dp = 0.f;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      float r[HF];
+      load_row<T, HF>(k_h + int64_t(uniform_int(kj)) * HD + hh * HF, r);
+#pragma unroll
+      for (int c = 0; c < HF; ++c) s_ = fmaf(qs[hh * HF + c], r[c], s_);
+    }
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      float r[HF];
+      load_row<T, HF>(v_h + int64_t(uniform_int(kj)) * HD + hh * HF, r);
+#pragma unroll
+      for (int c = 0; c < HF; ++c) dp = fmaf(gi[hh * HF + c], r[c], dp);
+    }
+    const float p = __expf(s_ - L);
+    float mm = 1.f;
+    if constexpr (DROP) mm = drop_scale(dm, word, uint32_t(kj));
+    const float ds = p * (mm * dp - Dq);
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      float r[HF];
+      load_row<T, HF>(k_h + int64_t(uniform_int(kj)) * HD + hh * HF, r);
+#pragma unroll
+      for (int c = 0; c < HF; ++c) dq[hh * HF + c] = fmaf(ds, r[c], dq[hh * HF + c]);
+    }
+  };
   // full tiles in groups of kGroup keys (a key pair at least), loads issued
   // together and results pinned per group as in the dK/dV pass (at d = 8,
   // pairs: 1.72 ms at 16,000 x 16,000 x 8 heads, against 2.14 ms for groups
@@ -568,7 +646,12 @@ __global__ __launch_bounds__(kBlock) void k_dense_bwd_q(
   const int n_tiles = (n_k + kStreamTile - 1) / kStreamTile;
   for (int t = w; t < n_tiles; t += kWaves) {
     const int kb = t * kStreamTile;
-    if (kb + kStreamTile <= n_k) {
+    if constexpr (DH >= 64) {
+      for (int i = 0; i < kStreamTile && kb + i < n_k; ++i) {
+        const uint32_t word = DROP ? drop_word(dm, uint32_t(qi), uint32_t(kb + i)) : 0U;
+        step_halves(kb + i, word);
+      }
+    } else if (kb + kStreamTile <= n_k) {
 #pragma unroll
       for (int g0 = 0; g0 < kStreamTile; g0 += kGroup) {
         const int kg = uniform_int(kb + g0);
