@@ -10,12 +10,13 @@ are resident in HBM before timing starts (the CSR is built once per window and
 reused by every layer and step, as in the training loop).
 
 Prints ONE JSON line: value = masked edges/s (layers x E / step time), the
-roofline of the dominant kernel (algorithmic bytes / its mean launch time,
-from hipEvents recorded around each launch on its own stream; its measured
-traffic from profiles/traffic.json; and the rate a pure random-row gather of
-the same table reaches, roofline.gather_ceiling) and the CPU baseline: the
-reference's op sequence (the CPU oracle, fp32 torch) timed on a bounded sample
-of the same window.
+roofline of the dominant kernel (its share of the layer's compulsory bytes /
+its mean launch time, from hipEvents recorded around each launch on its own
+stream; its measured L2-to-fabric traffic per launch from
+profiles/traffic.json, rocprofv3 FETCH_SIZE and WRITE_SIZE scaled by a device
+copy), the whole path's compulsory bytes per second (path_roofline) and the
+CPU baseline: the reference's op sequence (the CPU oracle, fp32 torch) timed
+on a bounded sample of the same window, on all host threads and on one.
 """
 from __future__ import annotations
 
@@ -48,21 +49,25 @@ def _elem_bytes(dtype) -> int:
 
 
 def sparse_kernel_bytes(name: str, cfg, n_k: int, E: int, adj) -> float:
-    """Algorithmic (compulsory) HBM bytes of one launch of a sparse kernel:
-    every tensor the kernel must touch, counted once."""
+    """Compulsory HBM bytes of one launch of a sparse kernel: its share of the
+    layer's compulsory bytes (every input, output and index array of the path
+    that the kernel must touch, counted once).  Intermediates the library
+    writes for its own later passes (the per-edge dS, split-row partials,
+    work lists) are not counted: a different kernel split would not need them.
+    The shares of the forward, rowstat, key-major and query-major passes add
+    up to path_bytes."""
     b = _elem_bytes(cfg.dtype)
     H = cfg.n_heads
     D = H * cfg.head_dim
     n_q = cfg.n_q
-    iq, ik = adj.struct.n_items_q, adj.struct.n_items_k
-    if name == "sparse_fwd":  # Q, K, V, O, col, items, rinv, node_score
-        return b * D * (2 * n_q + 2 * n_k) + 4 * E + 16 * iq + 4 * n_q * H + 4 * adj.dst_end
-    if name == "sparse_bwd_kv":  # Q, G, K, V, dK, dV, {r, rD}, t_col, items, dS (write)
-        return b * D * (2 * n_q + 4 * n_k) + 8 * n_q * H + 4 * E + 16 * ik + 4 * E * H
-    if name == "sparse_bwd_q":  # K, dQ, col, q2t, dS (read), items
-        return b * D * (n_k + n_q) + 8 * E + 4 * E * H + 16 * iq
-    if name == "sparse_rowstat":  # O, G, rinv, {r, rD}
-        return b * D * 2 * n_q + 12 * n_q * H
+    if name == "sparse_fwd":  # Q, K, V, O, rowptr, col, rinv, node_score
+        return b * D * (2 * n_q + 2 * n_k) + 4 * (n_q + 1) + 4 * E + 4 * n_q * H + 4 * adj.dst_end
+    if name == "sparse_rowstat":  # O (dO is counted in the key-major pass)
+        return b * D * n_q
+    if name == "sparse_bwd_kv":  # Q, dO, K, V, dK, dV, {r, D}, t_rowptr, t_col
+        return b * D * (2 * n_q + 4 * n_k) + 8 * n_q * H + 4 * (n_k + 1) + 4 * E
+    if name == "sparse_bwd_q":  # dQ, rowptr, col, q2t (K is counted in the key-major pass)
+        return b * D * n_q + 4 * (n_q + 1) + 8 * E
     return float("nan")
 
 
@@ -104,63 +109,42 @@ def measured_traffic(config: str, kernel: str):
     return float(rec["read_bytes"]) + float(rec["write_bytes"])
 
 
-# Rows each sparse kernel gathers per edge, as (table rows, row bytes factor):
-# the forward K and V rows of all keys, the key-major pass Q and dO rows of the
-# queries, the query-major pass K rows.
-GATHER_TABLES = {"sparse_fwd": lambda n_q, n_k: 2 * n_k,
-                 "sparse_bwd_kv": lambda n_q, n_k: 2 * n_q,
-                 "sparse_bwd_q": lambda n_q, n_k: n_k}
+def _cpu_model() -> tuple[str, int | None]:
+    """(model name, sockets) of the host CPU from lscpu (or /proc/cpuinfo)."""
+    import subprocess
+
+    model, sockets = "", None
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            key, _, val = line.partition(":")
+            if key.strip() == "Model name" and not model:
+                model = val.strip()
+            elif key.strip() == "Socket(s)":
+                try:
+                    sockets = int(val.strip())
+                except ValueError:
+                    pass
+    except (OSError, subprocess.SubprocessError):
+        pass
+    if not model:
+        try:
+            with open("/proc/cpuinfo") as f:
+                for line in f:
+                    if line.startswith("model name"):
+                        model = line.split(":", 1)[1].strip()
+                        break
+        except OSError:
+            pass
+    return model, sockets
 
 
-def gather_ceiling(kernel: str, cfg, n_k: int, dev, n_idx: int = 1 << 22, reps: int = 5):
-    """Measured ceiling for the dominant sparse kernel's access pattern:
-    ngt_probe_gather over a table as large as the rows that kernel gathers
-    (e.g. Q and dO of every query for the key-major pass), with uniform random
-    indices, so nearly every row misses L2.  Returns GB/s of gathered rows,
-    timed by the library's hipEvents like the kernels."""
-    import ctypes as C
-
-    import torch
-
-    from neutrongt_amd import _lib
-
-    rows_fn = GATHER_TABLES.get(kernel)
-    if rows_fn is None:
-        return None
-    row_bytes = _elem_bytes(cfg.dtype) * cfg.n_heads * cfg.head_dim
-    n_rows = rows_fn(cfg.n_q, n_k)
-    table = torch.ones(n_rows * row_bytes // 4, dtype=torch.int32, device=dev)
-    g = torch.Generator(device="cpu").manual_seed(7)
-    idx = torch.randint(0, n_rows, (n_idx,), generator=g, dtype=torch.int32).to(dev)
-    sink = torch.zeros(4, dtype=torch.int32, device=dev)
-    lib = _lib.load()
-    st = C.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
-
-    def launch():
-        _lib.check(lib.ngt_probe_gather(C.c_void_p(table.data_ptr()), n_rows, row_bytes,
-                                        C.c_void_p(idx.data_ptr()), n_idx,
-                                        C.c_void_p(sink.data_ptr()), st))
-    launch()
-    torch.cuda.synchronize()
-    _lib.timing_enable(True)
-    _lib.timing_summary()
-    for _ in range(reps):
-        launch()
-    torch.cuda.synchronize()
-    summ = _lib.timing_summary()
-    _lib.timing_enable(False)
-    cnt, ms = summ["probe_gather"]
-    gbs = n_idx * row_bytes / (ms / cnt * 1e-3) / 1e9
-    del table, idx, sink
-    return {"row_bytes": row_bytes, "table_MB": n_rows * row_bytes / 1e6, "indices": n_idx,
-            "distribution": "uniform", "gather_GBs": gbs}
-
-
-def cpu_baseline(cfg, ei_np, n_k, target_s: float = 3.0):
+def cpu_baseline(cfg, ei_np, n_k, target_s: float = 2.0, reps: int = 5):
     """The reference's op sequence (CPU oracle, fp32) on the in-edges of a
-    seeded random subset of the window's query rows, sized so one fwd+bwd takes
-    ~target_s.
-    1 warm-up + median of 3.  Returns the cpu_baseline JSON object."""
+    seeded random subset of the window's query rows, sized so one fwd+bwd
+    takes ~target_s: on every host thread this process may use, then on one
+    thread (its own, smaller sample).  1 warm-up + median of ``reps`` each.
+    Returns the cpu_baseline JSON object (value = the all-threads figure)."""
     import numpy as np
     import torch
 
@@ -171,7 +155,6 @@ def cpu_baseline(cfg, ei_np, n_k, target_s: float = 3.0):
     env = os.environ.get("OMP_NUM_THREADS")
     if env and env.isdigit():
         threads = min(threads, int(env))
-    torch.set_num_threads(max(1, threads))
     H = cfg.n_heads
     q, k, v, go = S.make_qkv(cfg, n_k, layer=0, device="cpu")
     # query rows in a seeded random order, so any prefix has the window's
@@ -194,35 +177,43 @@ def cpu_baseline(cfg, ei_np, n_k, target_s: float = 3.0):
         OA.sparse_fwd_bwd(args[0], args[1], args[2], args[4], args[3], H, dtype=torch.float32)
         return time.perf_counter() - t
 
-    n_rows = min(cfg.n_q, 64)
-    args = sample(n_rows)
-    t = run(args)
-    while t < target_s / 3 and n_rows < cfg.n_q:
-        n_rows = min(cfg.n_q, int(n_rows * min(8.0, max(1.5, target_s / max(t, 1e-3)))))
+    def measure(n_threads):
+        torch.set_num_threads(max(1, n_threads))
+        n_rows = min(cfg.n_q, 64)
         args = sample(n_rows)
-        t = run(args)  # doubles as the warm-up of the final size
-    times = [run(args) for _ in range(3)]
-    t_med = statistics.median(times)
-    e_s = int(args[4].shape[1])
-    model = ""
+        run(args)  # first call pays torch's one-time set-up
+        t = run(args)
+        while t < target_s / 3 and n_rows < cfg.n_q:
+            n_rows = min(cfg.n_q, int(n_rows * min(8.0, max(1.5, target_s / max(t, 1e-3)))))
+            args = sample(n_rows)
+            t = run(args)  # doubles as the warm-up of the final size
+        t_med = statistics.median(run(args) for _ in range(reps))
+        return int(args[4].shape[1]) / t_med, n_rows, int(args[4].shape[1]), t_med
+
+    prev = torch.get_num_threads()
     try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
+        v_all, rows_all, e_all, t_all = measure(threads)
+        used = torch.get_num_threads()
+        v_one, rows_one, e_one, t_one = measure(1)
+    finally:
+        torch.set_num_threads(prev)
+    model, sockets = _cpu_model()
+    kind = "bf16-rounded" if cfg.dtype != torch.float32 else "fp32"
     return {
-        "value": e_s / t_med,
+        "value": v_all,
         "unit": "edges/s",
-        "cores": torch.get_num_threads(),
+        "cores": used,
         "kind": "port",
         "sample": (f"one layer fwd+bwd of the reference op sequence (torch CPU oracle in fp32 on "
-                   f"{'bf16-rounded' if cfg.dtype != torch.float32 else 'fp32'} inputs) on the "
-                   f"in-edges of {n_rows} of {cfg.n_q} query rows "
-                   f"(seeded random choice): {e_s} edges, all {H} heads; median of 3 after 1 warm-up, "
-                   f"{t_med:.2f} s each; cpu: {model}"),
+                   f"{kind} inputs, all {H} heads) on the in-edges of a seeded random choice of "
+                   f"query rows: {rows_all} of {cfg.n_q} rows ({e_all} edges) on {used} threads, "
+                   f"{t_all:.2f} s per run; median of {reps} after 1 warm-up"),
+        "single_thread": {"value": v_one, "unit": "edges/s", "cores": 1,
+                          "sample": f"{rows_one} rows ({e_one} edges), {t_one:.2f} s per run, "
+                                    f"median of {reps} after 1 warm-up"},
+        "cpu_model": model,
+        "sockets": sockets,
+        "affinity_threads": len(os.sched_getaffinity(0)),
     }
 
 
@@ -711,18 +702,6 @@ def main(argv=None) -> int:
         roof = {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": ach / HBM_PEAK_GBS, "traffic": traffic, "kernel": dom,
                 "bytes_per_launch": kb, "avg_launch_us": dom_avg_s * 1e6}
-        # The kernel's measured HBM/fabric bytes per second against the rate a
-        # pure random-row gather of the same table reaches on this GPU.
-        ceil = gather_ceiling(dom, cfg, n_k, dev)
-        if ceil is not None:
-            if traffic is not None:
-                ceil["kernel_traffic_GBs"] = traffic / dom_avg_s / 1e9
-                ceil["kernel_traffic_frac"] = ceil["kernel_traffic_GBs"] / ceil["gather_GBs"]
-            roof["gather_ceiling"] = ceil
-            _log(f"[bench] uniform random {ceil['row_bytes']}-byte row gathers from a "
-                 f"{ceil['table_MB']:.0f} MB table: {ceil['gather_GBs']:.0f} GB/s"
-                 + (f"; {dom} moves {ceil['kernel_traffic_GBs']:.0f} GB/s of measured traffic"
-                    if traffic is not None else ""))
         pb = path_bytes(cfg, n_k, E)
         path = {"algorithmic_bytes_per_layer": pb,
                 "achieved_GBs": pb * layers / (ms_step * 1e-3) / 1e9,
@@ -734,7 +713,9 @@ def main(argv=None) -> int:
     if not args.no_cpu and not cfg.dense:
         _log("[bench] timing the CPU baseline ...")
         cpu = cpu_baseline(cfg, ei_np, n_k)
-        _log(f"[bench] cpu baseline {cpu['value'] / 1e6:.3f} M edges/s on {cpu['cores']} threads")
+        _log(f"[bench] cpu baseline {cpu['value'] / 1e6:.3f} M edges/s on {cpu['cores']} threads, "
+             f"{cpu['single_thread']['value'] / 1e6:.3f} M edges/s on 1 ({cpu['cpu_model']}, "
+             f"{cpu['sockets']} sockets)")
 
     dtype = "f32" if cfg.dtype == torch.float32 else "bf16"
     out = {

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define NGT_ABI_VERSION 4
+#define NGT_ABI_VERSION 5
 
 #define NGT_F32 0
 #define NGT_BF16 1
@@ -212,23 +212,31 @@ int ngt_sparse_bwd_ext(int dtype, const void* q, const void* k, const void* v, c
  * bf16-rounded out (out may then be NULL in the backward).  For rows whose
  * softmax is peaked, dS = P (dP - D) nearly cancels and the rounded out
  * alone moves dQ by percents.
- * workspace: fwd_bytes / bwd_bytes from ngt_dense_workspace_bytes.  The
- * forward uses it for node-score partials and, on its vector-ALU kernels
- * (fp32; bf16 at head_dim 64), for per-split softmax states when it splits
- * the keys of a large window over several blocks; pass it on every call.
+ * workspace: fwd_bytes / bwd_bytes from ngt_dense_workspace_bytes for the
+ * same dtype, sizes and node_scores (non-zero when node_score will be passed).
+ * The forward uses it for node-score partials (H * n_k floats on the bf16
+ * matrix-core path, d <= 32; per-block partials on the vector-ALU kernels)
+ * and, on the vector-ALU kernels (fp32; bf16 at head_dim 64), for per-split
+ * softmax states when it splits the keys of a large window over several
+ * blocks; a size of 0 means none is needed.
+ * seed_dev (may be NULL): a device uint64 the kernels read the seed from when
+ * they start, instead of `seed`; a captured HIP graph that rewrites it before
+ * each replay draws a new mask per replay.  Forward and backward must see the
+ * same value.
+ * scale must be > 0 (NGT_ERR_ARG otherwise).
  */
-int ngt_dense_workspace_bytes(int32_t n_q, int32_t n_k, int32_t n_heads, int32_t head_dim,
-                              size_t* fwd_bytes, size_t* bwd_bytes);
+int ngt_dense_workspace_bytes(int dtype, int32_t n_q, int32_t n_k, int32_t n_heads,
+                              int32_t head_dim, int32_t node_scores, size_t* fwd_bytes,
+                              size_t* bwd_bytes);
 int ngt_dense_fwd(int dtype, const void* q, const void* k, const void* v, int32_t n_q,
                   int32_t n_k, int32_t n_heads, int32_t head_dim, float scale, float dropout_p,
-                  uint64_t seed, void* out, float* out_f32, float* lse, float* node_score,
-                  void* workspace, size_t workspace_bytes, void* stream);
+                  uint64_t seed, const uint64_t* seed_dev, void* out, float* out_f32, float* lse,
+                  float* node_score, void* workspace, size_t workspace_bytes, void* stream);
 int ngt_dense_bwd(int dtype, const void* q, const void* k, const void* v, const void* out,
                   const float* out_f32, const void* grad_out, const float* lse, int32_t n_q,
-                  int32_t n_k,
-                  int32_t n_heads, int32_t head_dim, float scale, float dropout_p, uint64_t seed,
-                  void* grad_q, void* grad_k, void* grad_v, void* workspace,
-                  size_t workspace_bytes, void* stream);
+                  int32_t n_k, int32_t n_heads, int32_t head_dim, float scale, float dropout_p,
+                  uint64_t seed, const uint64_t* seed_dev, void* grad_q, void* grad_k,
+                  void* grad_v, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Related-node selection for one window.
@@ -354,24 +362,13 @@ int ngt_timing_enable(int on);
 int ngt_timing_summary(char* buf, size_t len);
 
 /*
- * Random row-gather probe (no counterpart in the reference: a measured
- * ceiling for the benchmark's roofline).  Gathers row idx[e] (int32, rows
- * outside [0, n_rows) are skipped) of a table of n_rows rows of row_bytes
- * bytes for e < n_idx, whole rows by 16-byte loads in the wave layout of the
- * sparse kernels, and discards the data (sink: device uint32, written only in
- * a case that does not occur with real data).  row_bytes must be 16 x (1..4)
- * x a power of two <= 64.  Timed as "probe_gather" while timing is enabled.
- */
-int ngt_probe_gather(const void* table, int64_t n_rows, int64_t row_bytes, const int32_t* idx,
-                     int64_t n_idx, uint32_t* sink, void* stream);
-
-/*
  * LayerNorm over the last dimension (n_cols, a multiple of 4, at most 2048):
  *   y = (x - mean) / sqrt(var + eps) * gamma + beta per row, fp32 math,
  *   x in in_dtype, y in out_dtype (NGT_F32 or NGT_BF16), mean/rstd [n_rows]
  *   fp32 saved for the backward; gamma/beta fp32.  The backward writes dx in
  *   in_dtype from dy in grad_dtype, and dgamma/dbeta (fp32, either may be
- *   NULL) as column sums added in a fixed order.  Rows 8-byte aligned.
+ *   NULL) as column sums added in a fixed order.  Row bases 16-byte aligned
+ *   for fp32, 8-byte for bf16 (each lane moves 4 elements per access).
  * Replaces the encoder's nn.LayerNorm under bf16 autocast
  * (NeutronGT/models/graphormer_dist_node_level.py:176-206, final_ln at
  * :242-381; NeutronGT/models/gt_dist_node_level_single_window.py:305-353).
@@ -395,17 +392,20 @@ int ngt_layernorm_bwd(int in_dtype, const void* x, int grad_dtype, const void* d
  * seed, scaled by 1/(1-p); 0 <= p < 1.  The backward takes the saved sum, the
  * gradients of out and (may be NULL) of sum, and writes dx = g_sum + LN
  * backward, dy = dx * mask (both in dtype), dgamma/dbeta fp32 (fixed order).
- * Workspace: ngt_layernorm_bwd_workspace_bytes.
+ * Workspace: ngt_layernorm_bwd_workspace_bytes.  seed_dev (may be NULL) as
+ * for ngt_dense_fwd: the seed is read from device memory at launch.  Row
+ * alignment as for ngt_layernorm_fwd.
  */
 int ngt_add_layernorm_fwd(int dtype, const void* x, const void* y, int64_t n_rows, int32_t n_cols,
-                          float dropout_p, uint64_t seed, const float* gamma, const float* beta,
-                          float eps, void* sum, int out_dtype, void* out, float* mean, float* rstd,
-                          void* stream);
+                          float dropout_p, uint64_t seed, const uint64_t* seed_dev,
+                          const float* gamma, const float* beta, float eps, void* sum,
+                          int out_dtype, void* out, float* mean, float* rstd, void* stream);
 int ngt_add_layernorm_bwd(int dtype, const void* sum, int grad_dtype, const void* g_out,
                           const void* g_sum, int64_t n_rows, int32_t n_cols, float dropout_p,
-                          uint64_t seed, const float* gamma, const float* mean, const float* rstd,
-                          void* dx, void* dy, float* dgamma, float* dbeta, void* workspace,
-                          size_t workspace_bytes, void* stream);
+                          uint64_t seed, const uint64_t* seed_dev, const float* gamma,
+                          const float* mean, const float* rstd, void* dx, void* dy,
+                          float* dgamma, float* dbeta, void* workspace, size_t workspace_bytes,
+                          void* stream);
 
 /*
  * Column sums of a bf16 matrix in fp32: out[j] = sum_k dy[k][j], dy

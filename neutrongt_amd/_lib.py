@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libngt_attn.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 NGT_F32 = 0
 NGT_BF16 = 1
@@ -96,19 +96,19 @@ SIGNATURES = {
                            _f32, _f32, _vp, _vp, _vp, _i32, _vp, _sz, _vp],
     "ngt_sparse_bwd_ext": [_i32, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _pcsr, _i32, _i32,
                            _f32, _f32, _f32, _vp, _vp, _vp, _vp, _sz, _vp],
-    "ngt_dense_workspace_bytes": [_i32, _i32, _i32, _i32, _psz, _psz],
+    "ngt_dense_workspace_bytes": [_i32, _i32, _i32, _i32, _i32, _i32, _psz, _psz],
     "ngt_dense_fwd": [_i32, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _f32, _u64, _vp, _vp,
-                      _vp, _vp, _vp, _sz, _vp],
+                      _vp, _vp, _vp, _vp, _sz, _vp],
     "ngt_dense_bwd": [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _f32,
-                      _u64, _vp, _vp, _vp, _vp, _sz, _vp],
+                      _u64, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
     "ngt_layernorm_fwd": [_i32, _vp, _i64, _i32, _vp, _vp, _f32, _i32, _vp, _vp, _vp, _vp],
     "ngt_layernorm_bwd_workspace_bytes": [_i64, _i32, _psz],
     "ngt_layernorm_bwd": [_i32, _vp, _i32, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
                           _vp],
-    "ngt_add_layernorm_fwd": [_i32, _vp, _vp, _i64, _i32, _f32, _u64, _vp, _vp, _f32, _vp, _i32,
-                              _vp, _vp, _vp, _vp],
+    "ngt_add_layernorm_fwd": [_i32, _vp, _vp, _i64, _i32, _f32, _u64, _vp, _vp, _vp, _f32, _vp,
+                              _i32, _vp, _vp, _vp, _vp],
     "ngt_add_layernorm_bwd": [_i32, _vp, _i32, _vp, _vp, _i64, _i32, _f32, _u64, _vp, _vp, _vp,
-                              _vp, _vp, _vp, _vp, _vp, _sz, _vp],
+                              _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
     "ngt_colsum_workspace_bytes": [_i64, _i32, _psz],
     "ngt_colsum_bf16": [_vp, _i64, _i32, _vp, _vp, _sz, _vp],
     "ngt_related_workspace_bytes": [_i32, _i32, _psz],
@@ -125,7 +125,6 @@ SIGNATURES = {
     "ngt_subgraph_csr": [_vp, _vp, _i64, _i64, _vp, _i32, _vp, _i64, _vp, _vp, _sz, _vp],
     "ngt_timing_enable": [_i32],
     "ngt_timing_summary": [C.c_char_p, _sz],
-    "ngt_probe_gather": [_vp, _i64, _i64, _vp, _i64, _vp, _vp],
 }
 _RESTYPES = {"ngt_last_error": C.c_char_p}
 

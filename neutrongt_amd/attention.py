@@ -159,36 +159,48 @@ class DenseAttentionFunction(torch.autograd.Function):
     """out = dropout_p(softmax((q*scale) k^T)) v per head,
     node_score[j] = sum_i mean_h |S|.  With dropout_p > 0 the keep mask is a
     hash of (seed, head, query, key) (the C-ABI's ngt_dense_fwd documents it);
-    the backward regenerates it from the same seed."""
+    the backward regenerates it from the same seed.  ``seed_t`` (an int64
+    device tensor of one element, or None) supplies the seed from device
+    memory instead of the host integer ``seed``."""
 
     @staticmethod
-    def forward(ctx, q, k, v, scale, want_scores, dropout_p=0.0, seed=0):
+    def forward(ctx, q, k, v, scale, want_scores, dropout_p=0.0, seed=0, seed_t=None):
         lib = _lib.load()
         n_q, H, d = q.shape
         n_k = k.shape[0]
         dev = q.device
+        dt = _dtype_code(q)
         out = torch.empty_like(q)
         # bf16: an fp32 copy of out feeds the backward's D = G . out
         out32 = (torch.empty(n_q, H, d, dtype=torch.float32, device=dev)
                  if q.dtype != torch.float32 else None)
         lse = torch.empty(H, n_q, dtype=torch.float32, device=dev)
+        want = bool(want_scores and n_k)
         ns = torch.empty(n_k if want_scores else 0, dtype=torch.float32, device=dev)
         fb, bb = C.c_size_t(), C.c_size_t()
-        _lib.check(lib.ngt_dense_workspace_bytes(n_q, n_k, H, d, C.byref(fb), C.byref(bb)))
-        ws = _workspace(fb.value, dev)
-        _lib.check(lib.ngt_dense_fwd(_dtype_code(q), q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                                     n_q, n_k, H, d, scale, dropout_p, seed, out.data_ptr(),
+        _lib.check(lib.ngt_dense_workspace_bytes(dt, n_q, n_k, H, d, int(want), C.byref(fb),
+                                                 C.byref(bb)))
+        ws = _workspace(fb.value, dev) if fb.value else None
+        sp = seed_t.data_ptr() if seed_t is not None else None
+        _lib.check(lib.ngt_dense_fwd(dt, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                     n_q, n_k, H, d, scale, dropout_p, seed, sp, out.data_ptr(),
                                      out32.data_ptr() if out32 is not None else None,
-                                     lse.data_ptr(), ns.data_ptr() if want_scores and n_k else None,
-                                     ws.data_ptr(), fb.value, _stream(dev)))
-        ctx.save_for_backward(q, k, v, out if out32 is None else out32, lse)
+                                     lse.data_ptr(), ns.data_ptr() if want else None,
+                                     ws.data_ptr() if ws is not None else None, fb.value,
+                                     _stream(dev)))
+        if seed_t is not None:
+            ctx.save_for_backward(q, k, v, out if out32 is None else out32, lse, seed_t)
+        else:
+            ctx.save_for_backward(q, k, v, out if out32 is None else out32, lse)
         ctx.scale, ctx.bwd_bytes, ctx.dropout_p, ctx.seed = scale, bb.value, dropout_p, seed
         ctx.mark_non_differentiable(ns)
         return out, ns
 
     @staticmethod
     def backward(ctx, g_out, g_ns):
-        q, k, v, out, lse = ctx.saved_tensors
+        saved = ctx.saved_tensors
+        q, k, v, out, lse = saved[:5]
+        seed_t = saved[5] if len(saved) == 6 else None
         lib = _lib.load()
         n_q, H, d = q.shape
         n_k = k.shape[0]
@@ -205,22 +217,29 @@ class DenseAttentionFunction(torch.autograd.Function):
                                      None if f32_out else out.data_ptr(),
                                      out.data_ptr() if f32_out else None, g.data_ptr(),
                                      lse.data_ptr(), n_q, n_k, H, d,
-                                     ctx.scale, ctx.dropout_p, ctx.seed, gq.data_ptr(),
-                                     gk.data_ptr(), gv.data_ptr(), ws.data_ptr(), ctx.bwd_bytes,
-                                     _stream(dev)))
-        return gq, gk, gv, None, None, None, None
+                                     ctx.scale, ctx.dropout_p, ctx.seed,
+                                     seed_t.data_ptr() if seed_t is not None else None,
+                                     gq.data_ptr(), gk.data_ptr(), gv.data_ptr(), ws.data_ptr(),
+                                     ctx.bwd_bytes, _stream(dev)))
+        return gq, gk, gv, None, None, None, None, None
 
 
-def draw_seed() -> int:
-    """A 64-bit dropout seed from torch's default (CPU) generator, so that
-    torch.manual_seed makes dropout masks reproducible; no device sync."""
-    return int(torch.randint(0, 2**62, (1,), dtype=torch.int64).item())
+def draw_seed(device) -> torch.Tensor:
+    """A 64-bit dropout seed drawn on ``device`` from torch's device generator,
+    as an int64 tensor of one element that the kernels read when they run.
+    torch.manual_seed / torch.cuda.manual_seed make it reproducible, no host
+    sync is needed, and inside a captured HIP graph each replay draws a new
+    seed (torch advances the generator's offset per replay), so dropout masks
+    differ between replays as they do between eager steps."""
+    return torch.randint(0, 2**62, (1,), dtype=torch.int64, device=device)
 
 
 def dense_attention(q, k, v, scale=None, node_scores=True, dropout_p=0.0, seed=None):
     """Functional form of full_attention: q [.., N_q, H, d], k/v [.., N_k, H, d]
     -> (x [N_q, H, d], node_scores [N_k] or empty).  dropout_p > 0 applies
-    dropout to the attention probabilities (seed: None draws one)."""
+    dropout to the attention probabilities.  seed: an int (a fixed mask), an
+    int64 device tensor of one element (read by the kernels when they run), or
+    None to draw one on the device with draw_seed."""
     H, d = q.shape[-2], q.shape[-1]
     q = _prep(q.reshape(-1, H, d), "q")
     k = _prep(k.reshape(-1, H, d), "k")
@@ -235,10 +254,15 @@ def dense_attention(q, k, v, scale=None, node_scores=True, dropout_p=0.0, seed=N
     dropout_p = float(dropout_p)
     if not 0.0 <= dropout_p <= 1.0:
         raise ValueError(f"dropout probability has to be between 0 and 1, but got {dropout_p}")
+    if not float(scale) > 0.0:
+        raise ValueError(f"scale must be > 0, got {scale}")
+    seed_t = None
     if dropout_p > 0.0 and seed is None:
-        seed = draw_seed()
+        seed_t = draw_seed(q.device)
+    elif isinstance(seed, torch.Tensor):
+        seed_t, seed = seed, None
     return DenseAttentionFunction.apply(q, k, v, float(scale), bool(node_scores), dropout_p,
-                                        int(seed or 0))
+                                        int(seed or 0), seed_t)
 
 
 # ---------------------------------------------------------------- the module

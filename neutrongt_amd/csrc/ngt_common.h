@@ -276,8 +276,13 @@ __device__ __forceinline__ float reduce_heads(float v, int L) {
 // reproduces the forward's mask without storing it.  Kept probabilities are
 // scaled by 1 / (1 - p); p = 1 drops everything (scale 0).  mix32 is the
 // "lowbias32" integer hash (C. Wellons, hash-prospector, public domain).
+// The seed is either a value fixed at launch or, with seed_dev set, read from
+// device memory when the kernel starts: a captured HIP graph whose replays
+// refresh that word (e.g. from torch's graph-safe generator) then draws a new
+// mask per replay instead of replaying the captured one.
 struct DropoutMask {
   uint64_t seed;
+  const uint64_t* seed_dev;  // null: use seed
   uint32_t head_key;  // drop_head_key(seed, h): set by the kernel for its head
   uint32_t n_kp;      // ceil(n_k / 2): words per query row
   uint32_t thr;       // keep iff the 16-bit half >= thr
@@ -298,7 +303,12 @@ __host__ __device__ __forceinline__ uint32_t drop_head_key(uint64_t seed, uint32
                mix32(static_cast<uint32_t>(seed >> 32) + 0x9e3779b9U * (h + 1U)));
 }
 
+__device__ __forceinline__ uint64_t drop_seed(const DropoutMask& dm) {
+  return dm.seed_dev ? *dm.seed_dev : dm.seed;
+}
+
 __device__ __forceinline__ DropoutMask drop_for_head(DropoutMask dm, int h) {
+  dm.seed = drop_seed(dm);
   dm.head_key = drop_head_key(dm.seed, static_cast<uint32_t>(h));
   return dm;
 }

@@ -882,8 +882,8 @@ int check_args(const char* fn, int dtype, int n_q, int n_k, int H, int d) {
 }
 
 // Dropout parameters from p and the seed; *on = false for p = 0.
-int make_dropout(const char* fn, float p, uint64_t seed, int n_q, int n_k, DropoutMask* dm,
-                 bool* on) {
+int make_dropout(const char* fn, float p, uint64_t seed, const uint64_t* seed_dev, int n_q,
+                 int n_k, DropoutMask* dm, bool* on) {
   *on = false;
   if (!(p >= 0.f && p <= 1.f))
     return set_error(NGT_ERR_ARG, "%s: dropout_p=%g outside [0, 1]", fn, double(p));
@@ -893,6 +893,7 @@ int make_dropout(const char* fn, float p, uint64_t seed, int n_q, int n_k, Dropo
     return set_error(NGT_ERR_UNSUPPORTED,
                      "%s: dropout needs n_q * ceil(n_k / 2) <= 2^32 (n_q=%d n_k=%d)", fn, n_q, n_k);
   dm->seed = seed;
+  dm->seed_dev = seed_dev;
   dm->head_key = 0;
   dm->n_kp = static_cast<uint32_t>((uint64_t(n_k) + 1) / 2);
   if (p >= 1.f) {  // everything dropped: keep-all mask with scale 0
@@ -941,49 +942,61 @@ int rowstat_bf16(int d, const void* out, const float* out32, const void* g, int 
   return NGT_OK;
 }
 
+// Forward workspace: the matrix-core path needs H * n_k floats of node-score
+// partials (only with node scores); the vector-ALU path needs per-block
+// node-score partials (only with node scores) and, when it splits the keys,
+// the split states behind them.
+size_t fwd_need(int dtype, int32_t n_q, int32_t n_k, int32_t H, int32_t d, bool node_scores) {
+  if (use_mfma(dtype, d)) return node_scores ? align256(size_t(H) * n_k * 4) : 0;
+  return node_scores || key_split(n_q, n_k, H).n_split > 1 ? fwd_ws(n_q, n_k, H, d) : 0;
+}
+
+__global__ void k_fill_zero(float* __restrict__ p, int64_t n) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.f;
+}
+
 }  // namespace
 }  // namespace ngt
 
 using namespace ngt;
 
-extern "C" int ngt_dense_workspace_bytes(int32_t n_q, int32_t n_k, int32_t n_heads,
-                                         int32_t head_dim, size_t* fwd_bytes, size_t* bwd_bytes) {
-  const int rc = check_args("ngt_dense_workspace_bytes", NGT_F32, n_q, n_k, n_heads, head_dim);
+extern "C" int ngt_dense_workspace_bytes(int dtype, int32_t n_q, int32_t n_k, int32_t n_heads,
+                                         int32_t head_dim, int32_t node_scores,
+                                         size_t* fwd_bytes, size_t* bwd_bytes) {
+  const int rc = check_args("ngt_dense_workspace_bytes", dtype, n_q, n_k, n_heads, head_dim);
   if (rc != NGT_OK) return rc;
-  if (fwd_bytes) *fwd_bytes = fwd_ws(n_q, n_k, n_heads, head_dim);
+  if (fwd_bytes) *fwd_bytes = n_q > 0 ? fwd_need(dtype, n_q, n_k, n_heads, head_dim, node_scores != 0) : 0;
   if (bwd_bytes) *bwd_bytes = bwd_ws(n_q, n_heads);
   return NGT_OK;
 }
 
 extern "C" int ngt_dense_fwd(int dtype, const void* q, const void* k, const void* v, int32_t n_q,
                              int32_t n_k, int32_t n_heads, int32_t head_dim, float scale,
-                             float dropout_p, uint64_t seed, void* out, float* out_f32,
-                             float* lse, float* node_score, void* workspace,
-                             size_t workspace_bytes, void* stream) {
+                             float dropout_p, uint64_t seed, const uint64_t* seed_dev,
+                             void* out, float* out_f32, float* lse, float* node_score,
+                             void* workspace, size_t workspace_bytes, void* stream) {
   int rc = check_args("ngt_dense_fwd", dtype, n_q, n_k, n_heads, head_dim);
   if (rc != NGT_OK) return rc;
+  if (!(scale > 0.f)) return set_error(NGT_ERR_ARG, "ngt_dense_fwd: scale must be > 0");
   DropoutMask dmv{};
   bool drop = false;
-  NGT_CHECK_OK(make_dropout("ngt_dense_fwd", dropout_p, seed, n_q, n_k, &dmv, &drop));
+  NGT_CHECK_OK(make_dropout("ngt_dense_fwd", dropout_p, seed, seed_dev, n_q, n_k, &dmv, &drop));
   const DropoutMask* dm = drop ? &dmv : nullptr;
   if (n_q > 0 && (!q || !out || !lse)) return set_error(NGT_ERR_ARG, "ngt_dense_fwd: null q/out/lse");
   if (n_k > 0 && (!k || !v)) return set_error(NGT_ERR_ARG, "ngt_dense_fwd: null k/v");
   if (n_q > 0) {
-    // node-score partials; the vector-ALU kernels' key-split states after them
-    size_t need = 0;
-    if (!use_mfma(dtype, head_dim))
-      need = node_score || key_split(n_q, n_k, n_heads).n_split > 1
-                 ? fwd_ws(n_q, n_k, n_heads, head_dim)
-                 : 0;
-    else if (node_score)
-      need = ns_part_bytes(n_q, n_k, n_heads);
+    const size_t need = fwd_need(dtype, n_q, n_k, n_heads, head_dim, node_score != nullptr);
     if (need && (!workspace || workspace_bytes < need))
       return set_error(NGT_ERR_WORKSPACE, "ngt_dense_fwd: workspace %zu < %zu", workspace_bytes,
                        need);
   }
-  if (node_score && n_q == 0 && n_k > 0)
-    NGT_HIP_CHECK(hipMemsetAsync(node_score, 0, size_t(n_k) * 4, static_cast<hipStream_t>(stream)));
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (node_score && n_q == 0 && n_k > 0) {  // no queries: every column score is 0
+    hipLaunchKernelGGL(k_fill_zero, dim3(unsigned((n_k + kBlock - 1) / kBlock)), dim3(kBlock), 0,
+                       st, node_score, int64_t(n_k));
+    NGT_HIP_CHECK(hipGetLastError());
+  }
   if (use_mfma(dtype, head_dim)) {
     if (n_q == 0) return NGT_OK;
     float* part = node_score ? static_cast<float*>(workspace) : nullptr;
@@ -1003,14 +1016,15 @@ extern "C" int ngt_dense_bwd(int dtype, const void* q, const void* k, const void
                              const void* out, const float* out_f32, const void* grad_out,
                              const float* lse, int32_t n_q,
                              int32_t n_k, int32_t n_heads, int32_t head_dim, float scale,
-                             float dropout_p, uint64_t seed, void* grad_q, void* grad_k,
-                             void* grad_v, void* workspace, size_t workspace_bytes,
-                             void* stream) {
+                             float dropout_p, uint64_t seed, const uint64_t* seed_dev,
+                             void* grad_q, void* grad_k, void* grad_v, void* workspace,
+                             size_t workspace_bytes, void* stream) {
   int rc = check_args("ngt_dense_bwd", dtype, n_q, n_k, n_heads, head_dim);
   if (rc != NGT_OK) return rc;
+  if (!(scale > 0.f)) return set_error(NGT_ERR_ARG, "ngt_dense_bwd: scale must be > 0");
   DropoutMask dmv{};
   bool drop = false;
-  NGT_CHECK_OK(make_dropout("ngt_dense_bwd", dropout_p, seed, n_q, n_k, &dmv, &drop));
+  NGT_CHECK_OK(make_dropout("ngt_dense_bwd", dropout_p, seed, seed_dev, n_q, n_k, &dmv, &drop));
   const DropoutMask* dm = drop ? &dmv : nullptr;
   if (n_q > 0 && (!q || (!out && !out_f32) || !grad_out || !lse || !grad_q))
     return set_error(NGT_ERR_ARG, "ngt_dense_bwd: null query-side pointer");

@@ -238,6 +238,14 @@ int check(const char* fn, int dt, int64_t n_rows, int n_cols) {
   return NGT_OK;
 }
 
+// Address bits that must be clear in a row base: each lane moves 4 elements
+// per access (16 bytes for fp32, 8 for bf16); n_cols % 4 == 0 keeps every row
+// at that alignment once the base is.
+inline uintptr_t row_align(int dt) { return dt == NGT_F32 ? 15 : 7; }
+inline bool misaligned(const void* p, int dt) {
+  return (reinterpret_cast<uintptr_t>(p) & row_align(dt)) != 0;
+}
+
 // Smallest supported Q with 64 * 4 * Q >= n_cols.
 inline int quads_for(int n_cols) {
   const int q = (n_cols + 255) / 256;
@@ -286,6 +294,7 @@ __global__ __launch_bounds__(kBlock) void k_add_ln_fwd(
     DropoutMask dm, const float* __restrict__ gamma, const float* __restrict__ beta, float eps,
     T* __restrict__ sum, TO* __restrict__ out, float* __restrict__ mean,
     float* __restrict__ rstd) {
+  if constexpr (DROP) dm = drop_for_head(dm, 0);
   const int lane = threadIdx.x & (kWave - 1);
   const int64_t row = int64_t(blockIdx.x) * kWaves + (threadIdx.x >> 6);
   if (row >= n_rows) return;  // whole wave; no block barrier follows
@@ -349,6 +358,7 @@ __global__ __launch_bounds__(kBlock) void k_add_ln_bwd(
     int64_t n_rows, int32_t n_cols, DropoutMask dm, const float* __restrict__ gamma,
     const float* __restrict__ mean, const float* __restrict__ rstd, T* __restrict__ dx,
     T* __restrict__ dy, float* __restrict__ part) {
+  if constexpr (DROP) dm = drop_for_head(dm, 0);
   extern __shared__ float red[];  // [kWaves][2 * n_cols]
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
@@ -423,8 +433,8 @@ __global__ __launch_bounds__(kBlock) void k_add_ln_bwd(
 }
 
 // Dropout parameters of the fused op (p in [0, 1)); *on = false for p = 0.
-int add_ln_dropout(const char* fn, float p, uint64_t seed, int64_t n_rows, int n_cols,
-                   DropoutMask* dm, bool* on) {
+int add_ln_dropout(const char* fn, float p, uint64_t seed, const uint64_t* seed_dev,
+                   int64_t n_rows, int n_cols, DropoutMask* dm, bool* on) {
   *on = false;
   if (!(p >= 0.f && p < 1.f))
     return set_error(NGT_ERR_ARG, "%s: dropout_p=%g outside [0, 1)", fn, double(p));
@@ -433,6 +443,7 @@ int add_ln_dropout(const char* fn, float p, uint64_t seed, int64_t n_rows, int n
   if (uint64_t(n_rows) * n_kp > (uint64_t(1) << 32))
     return set_error(NGT_ERR_UNSUPPORTED, "%s: dropout needs n_rows * n_cols / 2 <= 2^32", fn);
   dm->seed = seed;
+  dm->seed_dev = seed_dev;
   dm->head_key = drop_head_key(seed, 0);
   dm->n_kp = static_cast<uint32_t>(n_kp);
   dm->thr = static_cast<uint32_t>(lrint(double(p) * 65536.0));
@@ -454,8 +465,9 @@ extern "C" int ngt_layernorm_fwd(int in_dtype, const void* x, int64_t n_rows, in
   if (n_rows == 0) return NGT_OK;
   if (!x || !gamma || !beta || !y || !mean || !rstd)
     return set_error(NGT_ERR_ARG, "ngt_layernorm_fwd: null pointer");
-  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 7)
-    return set_error(NGT_ERR_ARG, "ngt_layernorm_fwd: x and y must be 8-byte aligned");
+  if (misaligned(x, in_dtype) || misaligned(y, out_dtype))
+    return set_error(NGT_ERR_ARG,
+                     "ngt_layernorm_fwd: rows must be 16-byte (fp32) / 8-byte (bf16) aligned");
   if (!(eps >= 0.f)) return set_error(NGT_ERR_ARG, "ngt_layernorm_fwd: eps must be >= 0");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t blocks = (n_rows + kWaves - 1) / kWaves;
@@ -507,9 +519,9 @@ extern "C" int ngt_layernorm_bwd(int in_dtype, const void* x, int grad_dtype, co
   if (nb > 0) {
     if (!x || !dy || !gamma || !mean || !rstd || !dx)
       return set_error(NGT_ERR_ARG, "ngt_layernorm_bwd: null pointer");
-    if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(dy) |
-         reinterpret_cast<uintptr_t>(dx)) & 7)
-      return set_error(NGT_ERR_ARG, "ngt_layernorm_bwd: x, dy, dx must be 8-byte aligned");
+    if (misaligned(x, in_dtype) || misaligned(dy, grad_dtype) || misaligned(dx, in_dtype))
+      return set_error(NGT_ERR_ARG,
+                       "ngt_layernorm_bwd: rows must be 16-byte (fp32) / 8-byte (bf16) aligned");
     const size_t need = size_t(nb) * 2 * n_cols * 4;
     if (!workspace || workspace_bytes < need)
       return set_error(NGT_ERR_WORKSPACE, "ngt_layernorm_bwd: workspace %zu < %zu",
@@ -555,20 +567,22 @@ extern "C" int ngt_layernorm_bwd(int in_dtype, const void* x, int grad_dtype, co
 
 extern "C" int ngt_add_layernorm_fwd(int dtype, const void* x, const void* y, int64_t n_rows,
                                      int32_t n_cols, float dropout_p, uint64_t seed,
-                                     const float* gamma, const float* beta, float eps, void* sum,
-                                     int out_dtype, void* out, float* mean, float* rstd,
-                                     void* stream) {
+                                     const uint64_t* seed_dev, const float* gamma,
+                                     const float* beta, float eps, void* sum, int out_dtype,
+                                     void* out, float* mean, float* rstd, void* stream) {
   NGT_CHECK_OK(check("ngt_add_layernorm_fwd", dtype, n_rows, n_cols));
   NGT_CHECK_OK(check("ngt_add_layernorm_fwd", out_dtype, n_rows, n_cols));
   DropoutMask dm{};
   bool drop = false;
-  NGT_CHECK_OK(add_ln_dropout("ngt_add_layernorm_fwd", dropout_p, seed, n_rows, n_cols, &dm, &drop));
+  NGT_CHECK_OK(add_ln_dropout("ngt_add_layernorm_fwd", dropout_p, seed, seed_dev, n_rows, n_cols,
+                              &dm, &drop));
   if (n_rows == 0) return NGT_OK;
   if (!x || !y || !gamma || !beta || !out || !mean || !rstd)
     return set_error(NGT_ERR_ARG, "ngt_add_layernorm_fwd: null pointer");
-  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y) |
-       reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(sum)) & 7)
-    return set_error(NGT_ERR_ARG, "ngt_add_layernorm_fwd: rows must be 8-byte aligned");
+  if (misaligned(x, dtype) || misaligned(y, dtype) || misaligned(sum, dtype) ||
+      misaligned(out, out_dtype))
+    return set_error(NGT_ERR_ARG,
+                     "ngt_add_layernorm_fwd: rows must be 16-byte (fp32) / 8-byte (bf16) aligned");
   if (!(eps >= 0.f)) return set_error(NGT_ERR_ARG, "ngt_add_layernorm_fwd: eps must be >= 0");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t blocks = (n_rows + kWaves - 1) / kWaves;
@@ -611,23 +625,25 @@ extern "C" int ngt_add_layernorm_fwd(int dtype, const void* x, const void* y, in
 extern "C" int ngt_add_layernorm_bwd(int dtype, const void* sum, int grad_dtype,
                                      const void* g_out, const void* g_sum, int64_t n_rows,
                                      int32_t n_cols, float dropout_p, uint64_t seed,
-                                     const float* gamma, const float* mean, const float* rstd,
-                                     void* dx, void* dy, float* dgamma, float* dbeta,
-                                     void* workspace, size_t workspace_bytes, void* stream) {
+                                     const uint64_t* seed_dev, const float* gamma,
+                                     const float* mean, const float* rstd, void* dx, void* dy,
+                                     float* dgamma, float* dbeta, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
   NGT_CHECK_OK(check("ngt_add_layernorm_bwd", dtype, n_rows, n_cols));
   NGT_CHECK_OK(check("ngt_add_layernorm_bwd", grad_dtype, n_rows, n_cols));
   DropoutMask dm{};
   bool drop = false;
-  NGT_CHECK_OK(add_ln_dropout("ngt_add_layernorm_bwd", dropout_p, seed, n_rows, n_cols, &dm, &drop));
+  NGT_CHECK_OK(add_ln_dropout("ngt_add_layernorm_bwd", dropout_p, seed, seed_dev, n_rows, n_cols,
+                              &dm, &drop));
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t nb = bwd_blocks(n_rows);
   if (nb > 0) {
     if (!sum || !g_out || !gamma || !mean || !rstd || !dx || !dy)
       return set_error(NGT_ERR_ARG, "ngt_add_layernorm_bwd: null pointer");
-    if ((reinterpret_cast<uintptr_t>(sum) | reinterpret_cast<uintptr_t>(g_out) |
-         reinterpret_cast<uintptr_t>(g_sum) | reinterpret_cast<uintptr_t>(dx) |
-         reinterpret_cast<uintptr_t>(dy)) & 7)
-      return set_error(NGT_ERR_ARG, "ngt_add_layernorm_bwd: rows must be 8-byte aligned");
+    if (misaligned(sum, dtype) || misaligned(g_out, grad_dtype) || misaligned(g_sum, dtype) ||
+        misaligned(dx, dtype) || misaligned(dy, dtype))
+      return set_error(NGT_ERR_ARG,
+                       "ngt_add_layernorm_bwd: rows must be 16-byte (fp32) / 8-byte (bf16) aligned");
     const size_t need = size_t(nb) * 2 * n_cols * 4;
     if (!workspace || workspace_bytes < need)
       return set_error(NGT_ERR_WORKSPACE, "ngt_add_layernorm_bwd: workspace %zu < %zu",

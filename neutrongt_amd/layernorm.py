@@ -23,13 +23,16 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import _lib
+from .attention import draw_seed
 
 _CODES = {torch.float32: _lib.NGT_F32, torch.bfloat16: _lib.NGT_BF16}
 
 
 def _rows(t: torch.Tensor, n_cols: int) -> torch.Tensor:
+    """[n, n_cols] contiguous view (or copy) whose base meets the kernels'
+    alignment: 16 bytes for fp32 rows, 8 for bf16 (4 elements per access)."""
     t = t.reshape(-1, n_cols)
-    if not t.is_contiguous() or t.data_ptr() % 8:
+    if not t.is_contiguous() or t.data_ptr() % (16 if t.dtype == torch.float32 else 8):
         t = t.clone(memory_format=torch.contiguous_format)
     return t
 
@@ -109,7 +112,7 @@ def _fused_ok(x: torch.Tensor, ln: nn.LayerNorm) -> bool:
 
 class _AddLayerNormFn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, y, weight, bias, eps, p, seed, out_bf16):
+    def forward(ctx, x, y, weight, bias, eps, p, seed, out_bf16, seed_t=None):
         lib = _lib.load()
         n_cols = weight.numel()
         x2, y2 = _rows(x, n_cols), _rows(y, n_cols)
@@ -124,16 +127,20 @@ class _AddLayerNormFn(torch.autograd.Function):
         b = bias.detach().float().contiguous()
         _lib.check(lib.ngt_add_layernorm_fwd(
             _CODES[x2.dtype], x2.data_ptr(), y2.data_ptr(), n, n_cols, float(p), int(seed),
-            w.data_ptr(), b.data_ptr(), float(eps), s.data_ptr(), _CODES[out.dtype],
-            out.data_ptr(), mean.data_ptr(), rstd.data_ptr(),
-            _lib.stream_ptr(dev)))
-        ctx.save_for_backward(s, w, mean, rstd)
+            seed_t.data_ptr() if seed_t is not None else None, w.data_ptr(), b.data_ptr(),
+            float(eps), s.data_ptr(), _CODES[out.dtype], out.data_ptr(), mean.data_ptr(),
+            rstd.data_ptr(), _lib.stream_ptr(dev)))
+        if seed_t is not None:
+            ctx.save_for_backward(s, w, mean, rstd, seed_t)
+        else:
+            ctx.save_for_backward(s, w, mean, rstd)
         ctx.p, ctx.seed, ctx.shape = float(p), int(seed), x.shape
         return s.view(*x.shape), out.view(*x.shape)
 
     @staticmethod
     def backward(ctx, g_s, g_out):
-        s, w, mean, rstd = ctx.saved_tensors
+        s, w, mean, rstd = ctx.saved_tensors[:4]
+        seed_t = ctx.saved_tensors[4] if len(ctx.saved_tensors) == 5 else None
         lib = _lib.load()
         n, n_cols = s.shape
         dev = s.device
@@ -151,22 +158,24 @@ class _AddLayerNormFn(torch.autograd.Function):
         _lib.check(lib.ngt_add_layernorm_bwd(
             _CODES[s.dtype], s.data_ptr(), _CODES[g_out2.dtype], g_out2.data_ptr(),
             g_s2.data_ptr() if g_s2 is not None else None, n, n_cols, ctx.p, ctx.seed,
-            w.data_ptr(), mean.data_ptr(), rstd.data_ptr(), dx.data_ptr(), dy.data_ptr(),
+            seed_t.data_ptr() if seed_t is not None else None, w.data_ptr(), mean.data_ptr(),
+            rstd.data_ptr(), dx.data_ptr(), dy.data_ptr(),
             dw.data_ptr(), db.data_ptr(), ws.data_ptr(), nb.value,
             _lib.stream_ptr(dev)))
-        return dx.view(*ctx.shape), dy.view(*ctx.shape), dw, db, None, None, None, None
+        return dx.view(*ctx.shape), dy.view(*ctx.shape), dw, db, None, None, None, None, None
 
 
 def add_dropout_layernorm(x: torch.Tensor, y: torch.Tensor, ln: nn.LayerNorm,
                           dropout: nn.Dropout):
     """(s, ln(s)) with s = x + dropout(y): the residual add and the LayerNorm
     that follows it, as one pass of ``ngt_add_layernorm_fwd`` under bf16
-    autocast (the dropout mask then comes from this library's hash, seeded
-    from torch's generator); otherwise the unfused torch ops."""
+    autocast (the dropout mask then comes from this library's hash, with a
+    seed drawn on the device from torch's generator, so that every replay of a
+    captured graph draws a new mask); otherwise the unfused torch ops."""
     p = dropout.p if dropout.training else 0.0
     if (_fused_ok(x, ln) and y.dtype == x.dtype and y.shape == x.shape and p < 1.0
             and torch.is_grad_enabled()):
-        seed = int(torch.randint(0, 2**62, (1,), dtype=torch.int64).item()) if p > 0 else 0
-        return _AddLayerNormFn.apply(x, y, ln.weight, ln.bias, ln.eps, p, seed, ln.out_bf16)
+        seed_t = draw_seed(x.device) if p > 0 else None
+        return _AddLayerNormFn.apply(x, y, ln.weight, ln.bias, ln.eps, p, 0, ln.out_bf16, seed_t)
     s = x + F.dropout(y, p, dropout.training) if p > 0 else x + y
     return s, ln(s)

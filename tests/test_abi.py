@@ -62,32 +62,60 @@ def test_argument_errors_are_reported_without_touching_the_gpu():
                             None, None, 0, None, 0, None)
     assert rc == 2 and b"head_dim" in lib.ngt_last_error()
     rc = lib.ngt_dense_fwd(7, None, None, None, 1, 1, 1, 8, 1.0, 0.0, 0, None, None, None, None,
-                           None, 0, None)
+                           None, None, 0, None)
     assert rc == 1
     rc = lib.ngt_dense_fwd(0, None, None, None, 0, 0, 1, 8, 1.0, 1.5, 0, None, None, None, None,
-                           None, 0, None)
+                           None, None, 0, None)
     assert rc == 1 and b"dropout_p" in lib.ngt_last_error()
     rc = lib.ngt_dense_fwd(0, None, None, None, 0, 0, 1, 8, 1.0, float("nan"), 0, None, None, None,
-                           None, None, 0, None)
+                           None, None, None, 0, None)
     assert rc == 1 and b"dropout_p" in lib.ngt_last_error()
     rc = lib.ngt_dense_fwd(0, None, None, None, 65536, 131074, 1, 8, 1.0, 0.5, 0, None, None, None,
-                           None, None, 0, None)
+                           None, None, None, 0, None)
     assert rc == 2 and b"2^32" in lib.ngt_last_error()
+    # the dense kernels need scale > 0 (the matrix-core forward scales its running maximum)
+    for sc in (0.0, -2.0, float("nan")):
+        rc = lib.ngt_dense_fwd(1, None, None, None, 0, 0, 1, 8, sc, 0.0, 0, None, None, None,
+                               None, None, None, 0, None)
+        assert rc == 1 and b"scale" in lib.ngt_last_error()
+        rc = lib.ngt_dense_bwd(1, None, None, None, None, None, None, None, 0, 0, 1, 8, sc, 0.0,
+                               0, None, None, None, None, None, 0, None)
+        assert rc == 1 and b"scale" in lib.ngt_last_error()
     with pytest.raises(_lib.NGTError):
         _lib.check(1)
 
 
-def test_gather_probe_rejects_bad_rows_without_touching_the_gpu():
+def test_dense_workspace_query_depends_on_path_and_scores():
+    """The matrix-core path (bf16, d <= 32) needs H * n_k floats of node-score
+    partials and nothing without node scores; the vector-ALU path sizes its
+    per-block partials only when node scores are wanted."""
     lib = _lib.load()
-    assert lib.ngt_probe_gather(None, 10, 1536, None, 5, None, None) == 1
-    assert b"null pointer" in lib.ngt_last_error()
-    fake = C.c_void_p(256)  # never dereferenced: the checks fail before any launch
-    assert lib.ngt_probe_gather(fake, 10, 100, fake, 5, fake, None) == 1
-    assert b"multiple of 16" in lib.ngt_last_error()
-    # 5 words per row: neither 1..4 words per lane times a power of two
-    assert lib.ngt_probe_gather(fake, 10, 80, fake, 5, fake, None) == 2
-    assert lib.ngt_probe_gather(fake, -1, 1536, fake, 5, fake, None) == 1
-    assert lib.ngt_probe_gather(None, 10, 1536, None, 0, None, None) == 0  # nothing to do
+    fb, bb = C.c_size_t(), C.c_size_t()
+    assert lib.ngt_dense_workspace_bytes(1, 16000, 16000, 8, 8, 1, C.byref(fb), C.byref(bb)) == 0
+    assert fb.value == 8 * 16000 * 4 and bb.value >= 16000 * 8 * 4
+    assert lib.ngt_dense_workspace_bytes(1, 16000, 16000, 8, 8, 0, C.byref(fb), C.byref(bb)) == 0
+    assert fb.value == 0
+    assert lib.ngt_dense_workspace_bytes(0, 500, 300, 2, 8, 1, C.byref(fb), C.byref(bb)) == 0
+    with_ns = fb.value
+    assert lib.ngt_dense_workspace_bytes(0, 500, 300, 2, 8, 0, C.byref(fb), C.byref(bb)) == 0
+    assert with_ns >= 2 * 300 * 4 and fb.value < with_ns
+
+
+def test_layernorm_rejects_misaligned_rows_without_touching_the_gpu():
+    """fp32 rows move 16 bytes per lane access, bf16 rows 8: bases off that
+    alignment are an argument error, before any launch."""
+    lib = _lib.load()
+    p16, p8 = C.c_void_p(4096), C.c_void_p(4096 + 8)
+    m = C.c_void_p(8192)
+    rc = lib.ngt_layernorm_fwd(0, p8, 4, 64, m, m, 1e-5, 0, p16, m, m, None)
+    assert rc == 1 and b"aligned" in lib.ngt_last_error()
+    rc = lib.ngt_layernorm_fwd(0, p16, 4, 64, m, m, 1e-5, 0, p8, m, m, None)
+    assert rc == 1 and b"aligned" in lib.ngt_last_error()
+    rc = lib.ngt_add_layernorm_fwd(0, p16, p8, 4, 64, 0.0, 0, None, m, m, 1e-5, None, 0, p16, m,
+                                   m, None)
+    assert rc == 1 and b"aligned" in lib.ngt_last_error()
+    rc = lib.ngt_layernorm_bwd(0, p16, 0, p8, 4, 64, m, m, m, p16, None, None, m, 1 << 20, None)
+    assert rc == 1 and b"aligned" in lib.ngt_last_error()
 
 
 def test_product_never_imports_the_oracle():

@@ -91,9 +91,10 @@ def test_dense_module_drop_in():
 
 
 def test_dense_full_size_sampled_rows_and_invariants():
-    """16,000-node all-pairs window (H=8, d=8, bf16): sampled query rows against
-    the float64 row formula, column scores against a chunked CPU sum, and the
-    size-independent identities <dQ,Q> = <dK,K>, sum_j dV_j = sum_i G_i."""
+    """16,000-node all-pairs window (H=8, d=8, bf16): sampled query rows and
+    sampled key rows (dK, dV) against float64 formulas, column scores against a
+    chunked CPU sum, and the size-independent identities <dQ,Q> = <dK,K>,
+    sum_j dV_j = sum_i G_i."""
     cfg = S.CONFIGS["dense_slim"]
     _say(f"case dense full-size n={cfg.n_q}")
     q, k, v, go = S.make_qkv(cfg, cfg.n_q)
@@ -111,12 +112,31 @@ def test_dense_full_size_sampled_rows_and_invariants():
         dq = sc * (p * (dp - dd)) @ kd[:, h]
         assert relerr(res["x"][rows, h], x) < TOL[cfg.dtype]
         assert relerr(res["dq"][rows, h], dq) < TOL[cfg.dtype]
+    # dK / dV of sampled key rows (and the first and last key), elementwise:
+    # a key column sums over every query, so each query row's softmax and
+    # D_i = G_i . X_i are formed in float64, 2,000 rows at a time; the same
+    # pass accumulates the column scores.
+    keys = np.unique(np.concatenate([np.random.default_rng(2).choice(n, 48, replace=False),
+                                     [0, n - 1]]))
+    kt = torch.from_numpy(keys)
     ns = torch.zeros(n, dtype=torch.float64)
+    dk = torch.zeros(keys.size, H, d, dtype=torch.float64)
+    dv = torch.zeros(keys.size, H, d, dtype=torch.float64)
     for h in range(H):
         for c in range(0, n, 2000):
-            ns += ((qd[c:c + 2000, h] * sc) @ kd[:, h].T).abs().sum(0)
+            s = (qd[c:c + 2000, h] * sc) @ kd[:, h].T  # [2000, n]
+            ns += s.abs().sum(0)
+            p = torch.softmax(s, -1)
+            x = p @ vd[:, h]
+            dd = (gd[c:c + 2000, h] * x).sum(-1, keepdim=True)
+            pc = p[:, kt]
+            ds = pc * (gd[c:c + 2000, h] @ vd[kt, h].T - dd)
+            dk[:, h] += sc * ds.T @ qd[c:c + 2000, h]
+            dv[:, h] += pc.T @ gd[c:c + 2000, h]
     ns /= H
     assert relerr(res["node_scores"], ns) < TOL[cfg.dtype]
+    assert_close(res["dk"][kt].float(), dk, cfg.dtype, "dense dk keys")
+    assert_close(res["dv"][kt].float(), dv, cfg.dtype, "dense dv keys")
     lhs = (res["dq"].double() * qd).sum().item()
     rhs = (res["dk"].double() * kd).sum().item()
     assert abs(lhs - rhs) / max(abs(lhs), abs(rhs)) < 10 * TOL[cfg.dtype]
@@ -178,9 +198,10 @@ def test_dense_dropout_mask_from_output(dtype):
 
 
 def test_dense_module_dropout_and_flash():
-    """CoreAttention in training mode draws a seed from torch's generator
-    (torch.manual_seed makes it repeatable), eval mode has no dropout, and the
-    flash branch (1/sqrt(d) scale, dropout always on) matches naive_attention."""
+    """CoreAttention in training mode draws its seed on the device from torch's
+    generator (torch.manual_seed makes it repeatable), eval mode has no
+    dropout, and the flash branch (1/sqrt(d) scale, dropout always on) matches
+    naive_attention."""
     _say("case dense module dropout/flash")
     H, d, n = 2, 8, 50
     mod = CoreAttention(H * d, 0.5, H).cuda()
@@ -194,7 +215,7 @@ def test_dense_module_dropout_and_flash():
     torch.manual_seed(77)
     x1, s1 = mod(*args)
     torch.manual_seed(77)
-    seed = int(torch.randint(0, 2**62, (1,), dtype=torch.int64).item())
+    seed = int(torch.randint(0, 2**62, (1,), dtype=torch.int64, device="cuda").item())
     torch.manual_seed(77)
     x2, _ = mod(*args)
     assert torch.equal(x1, x2)
@@ -207,7 +228,7 @@ def test_dense_module_dropout_and_flash():
     xf, sf = mod(q[None].cuda(), k[None].cuda(), v[None].cuda(), None, None, "flash")
     assert sf is None and xf.dtype == torch.float32 and xf.shape == (1, n, H * d)
     torch.manual_seed(78)
-    seed = int(torch.randint(0, 2**62, (1,), dtype=torch.int64).item())
+    seed = int(torch.randint(0, 2**62, (1,), dtype=torch.int64, device="cuda").item())
     mult = OA.dropout_multiplier(seed, H, n, n, 0.5)
     ref = OA.full_fwd_bwd(q, k, v, go, dropout_mult=mult, flash=True)
     assert_close(xf[0].view(n, H, d).cpu(), ref["x"], torch.float32, "flash x")

@@ -231,6 +231,60 @@ def _sampled_rows_oracle(q, k, v, ei, go, rows, H):
                              gs.float(), H, dtype=torch.float32)
 
 
+def _sampled_keys_fp64(q, k, v, ei, go, keys, scale, lo=-5.0, hi=5.0, eps=1e-6,
+                       chunk=100_000):
+    """dK and dV of the key rows ``keys`` in float64 from the closed form
+    (oracle.attention.sparse_backward_closed_form, restricted): a key's
+    gradient sums over its out-edges (j -> i), and each term needs query i's
+    whole row (Z_i, X_i), so the rows of every query adjacent to a sampled key
+    are computed in full first.  Exact for the sampled keys; edges are walked in
+    chunks so a hub's sub-window stays small in memory."""
+    src, dst = ei[0], ei[1]
+    n_q, H, d = q.shape
+    qd, kd, vd, gd = (t.double() for t in (q, k, v, go))
+    sel = np.isin(src, keys)
+    adj_q = np.unique(dst[sel])
+    m = np.isin(dst, adj_q)
+    sub_src, sub_dst = torch.from_numpy(src[m]), torch.from_numpy(dst[m])
+    z = torch.zeros(n_q, H, dtype=torch.float64)
+    wv = torch.zeros(n_q, H, d, dtype=torch.float64)
+    for c in range(0, sub_src.numel(), chunk):
+        j, i = sub_src[c:c + chunk], sub_dst[c:c + chunk]
+        p = torch.exp(((kd[j] * qd[i]).sum(-1) / scale).clamp(lo, hi))
+        z.index_add_(0, i, p)
+        wv.index_add_(0, i, p.unsqueeze(-1) * vd[j])
+    r = 1.0 / (z + eps)
+    dd = (gd * wv * r.unsqueeze(-1)).sum(-1)  # D_i = G_i . X_i
+    pos = -np.ones(kd.shape[0], np.int64)
+    pos[keys] = np.arange(len(keys))
+    e_src, e_dst = torch.from_numpy(src[sel]), torch.from_numpy(dst[sel])
+    dk = torch.zeros(len(keys), H, d, dtype=torch.float64)
+    dv = torch.zeros(len(keys), H, d, dtype=torch.float64)
+    for c in range(0, e_src.numel(), chunk):
+        j, i = e_src[c:c + chunk], e_dst[c:c + chunk]
+        a = (kd[j] * qd[i]).sum(-1) / scale
+        p = torch.exp(a.clamp(lo, hi))
+        dp = r[i] * ((gd[i] * vd[j]).sum(-1) - dd[i])
+        da = dp * p * ((a >= lo) & (a <= hi)).double()
+        at = torch.from_numpy(pos[j.numpy()])
+        dk.index_add_(0, at, da.unsqueeze(-1) * qd[i] / scale)
+        dv.index_add_(0, at, (p * r[i]).unsqueeze(-1) * gd[i])
+    return dk, dv
+
+
+def _sample_keys(ei, n_q, n_k, rng, n=64):
+    """64 random keys with out-edges, the key with the most out-edges (the
+    key-major hub, split over many chunks) and one related key (rows past the
+    window's queries), if the window has any."""
+    deg = np.bincount(ei[0], minlength=n_k)
+    live = np.flatnonzero(deg)
+    picks = [rng.choice(live, min(n, live.size), replace=False), [int(deg.argmax())]]
+    rel = live[live >= n_q]
+    if rel.size:
+        picks.append([int(rel[rng.integers(rel.size)])])
+    return np.unique(np.concatenate(picks)), deg
+
+
 @pytest.mark.parametrize("name", ["gph_slim", "gt_arxiv", "gph_large", "gt_highdeg"])
 def test_full_size_window_sampled_rows_and_invariants(name):
     cfg = S.CONFIGS[name]
@@ -246,6 +300,16 @@ def test_full_size_window_sampled_rows_and_invariants(name):
     assert_close(res["x"][rows].float(), ref["x"], cfg.dtype, f"{name}:x rows")
     assert_close(res["dq"][rows].float(), ref["dq"], cfg.dtype, f"{name}:dq rows")
     assert_close(res["node_scores"][rows].float(), ref["node_scores"], cfg.dtype, f"{name}:ns")
+    # dK / dV of sampled key rows, elementwise, against the float64 closed form
+    keys, kdeg = _sample_keys(ei, cfg.n_q, n_k, rng)
+    _say(f"  {name}: {keys.size} sampled keys, max key degree {int(kdeg.max())}")
+    dk, dv = _sampled_keys_fp64(q, k, v, ei, go, keys, float(cfg.head_dim) ** 0.5)
+    assert_close(res["dk"][keys].float(), dk, cfg.dtype, f"{name}:dk keys")
+    assert_close(res["dv"][keys].float(), dv, cfg.dtype, f"{name}:dv keys")
+    hub = int(kdeg.argmax())
+    at = int(np.searchsorted(keys, hub))
+    assert_close(res["dk"][hub].float(), dk[at], cfg.dtype, f"{name}:dk hub")
+    assert_close(res["dv"][hub].float(), dv[at], cfg.dtype, f"{name}:dv hub")
     # <dQ, Q> = <dK, K> = sum_e da_e a_e  (a is bilinear in q and k)
     lhs = (res["dq"].double() * q.double()).sum().item()
     rhs = (res["dk"].double() * k.double()).sum().item()

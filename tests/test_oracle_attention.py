@@ -149,6 +149,50 @@ def test_full_attention_gradcheck_fp64():
     assert torch.autograd.gradcheck(f, (q, k, v), eps=1e-6, atol=1e-7)
 
 
+def test_naive_attention_hand_row():
+    """The flash branch (graphormer_dist_node_level.py:100-105): softmax of
+    q k^T / sqrt(d), the dropout multiplier applied to the probabilities with
+    no renormalisation, then v.  One query row worked by hand: d = 4, so
+    1/sqrt(d) = 1/2, and keys whose scores are 0, 1, 2, 3; key 1 dropped at
+    p = 0.5 (kept keys scaled by 2)."""
+    H, d = 1, 4
+    q = torch.zeros(1, 1, H, d, dtype=torch.float64)
+    q[0, 0, 0, 0] = 2.0
+    k = torch.zeros(1, 4, H, d, dtype=torch.float64)
+    v = torch.zeros(1, 4, H, d, dtype=torch.float64)
+    for j in range(4):
+        k[0, j, 0, 0] = float(j)       # s_j = 2 * j / 2 = j
+        v[0, j, 0, :] = torch.tensor([1.0, float(j), float(j * j), -1.0])
+    mult = np.array([[[2.0, 0.0, 2.0, 2.0]]])  # [H, n_q, n_k]
+    x = OA.naive_attention(q, k, v, dropout_mult=mult)[0, 0, 0]
+    z = sum(math.exp(j) for j in range(4))
+    w = [math.exp(j) / z * m for j, m in zip(range(4), (2.0, 0.0, 2.0, 2.0))]
+    want = [sum(w), sum(wj * j for j, wj in enumerate(w)), sum(wj * j * j for j, wj in enumerate(w)),
+            -sum(w)]
+    torch.testing.assert_close(x, torch.tensor(want, dtype=torch.float64), rtol=1e-13, atol=0)
+    # a x sqrt(d) scale (full_attention's) gives scores 0, 4, 8, 12: far from the row above
+    xs, _ = OA.full_attention(q, k, v, dropout_mult=mult)
+    assert relerr(xs[0, 0, 0], torch.tensor(want)) > 0.1
+    # without dropout the weights sum to one: x[0] == 1, x[3] == -1
+    x0 = OA.naive_attention(q, k, v)[0, 0, 0]
+    assert abs(x0[0].item() - 1.0) < 1e-15 and abs(x0[3].item() + 1.0) < 1e-15
+
+
+@pytest.mark.parametrize("n_q,n_k,H,d,p", [(9, 13, 2, 8, 0.0), (12, 7, 3, 16, 0.5)])
+def test_naive_attention_matches_fp64_form_and_gradcheck(n_q, n_k, H, d, p):
+    """naive_attention equals the einsum form softmax((q / sqrt(d)) k^T) v with
+    the same multiplier; its autograd backward passes gradcheck."""
+    q, k, v, _ = _inputs(n_q, n_k, H, d, seed=n_q + d)
+    mult = OA.dropout_multiplier(123, H, n_q, n_k, p) if p else None
+    x = OA.naive_attention(q[None], k[None], v[None], dropout_mult=mult)[0]
+    xb, _ = OA.full_attention_fp64(q, k, v, scale=1.0 / math.sqrt(d), dropout_mult=mult)
+    assert relerr(x, xb) < 1e-12
+    qs, ks, vs = (t[:5, :, :4].clone().requires_grad_(True) for t in (q, k, v))
+    m = OA.dropout_multiplier(5, H, 5, 5, p) if p else None
+    f = lambda a, b, c: OA.naive_attention(a[None], b[None], c[None], dropout_mult=m)
+    assert torch.autograd.gradcheck(f, (qs, ks, vs), eps=1e-6, atol=1e-7)
+
+
 def test_golden_fixtures_reproduce():
     files = sorted(GOLDEN.glob("attn_*.npz"))
     assert files, "golden fixtures missing (tests/golden/make_golden.py)"
