@@ -158,6 +158,22 @@ int ngt_sparse_fwd(int dtype, const void* q, const void* k, const void* v,
                    size_t workspace_bytes, void* stream);
 
 /*
+ * ngt_sparse_fwd without a workspace argument, allocating nothing.  No
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops, harnesses that
+ * forbid hipMalloc).  Its scratch is a static device array of 32 MiB that
+ * each device using the library holds until the process ends; a window whose
+ * forward workspace (ngt_sparse_workspace_bytes' fwd_bytes) exceeds it is
+ * rejected with NGT_ERR_UNSUPPORTED.  Same results as ngt_sparse_fwd, bit for
+ * bit.  Every call on a device shares that device's array: calls that overlap
+ * on one device (several streams or threads) race.
+ */
+int ngt_sparse_fwd_noalloc(int dtype, const void* q, const void* k, const void* v,
+                           const ngt_window_csr* csr, int32_t n_heads, int32_t head_dim,
+                           float scale, float clamp_lo, float clamp_hi, float eps, void* out,
+                           float* rinv, float* node_score, int32_t node_score_len, void* stream);
+
+/*
  * Sparse attention backward (what autograd derives from the same lines).
  * With G = grad_out, r = rinv, D_i = sum_c G[i,h,c] out[i,h,c]:
  *   dp_e = r_i (G_i . v_j - D_i);  da_e = dp_e p_e [lo <= a_e <= hi]

@@ -90,6 +90,8 @@ SIGNATURES = {
     "ngt_sparse_workspace_bytes": [_pcsr, _i32, _i32, _psz, _psz],
     "ngt_sparse_fwd": [_i32, _vp, _vp, _vp, _pcsr, _i32, _i32, _f32, _f32, _f32, _f32, _vp, _vp,
                        _vp, _i32, _vp, _sz, _vp],
+    "ngt_sparse_fwd_noalloc": [_i32, _vp, _vp, _vp, _pcsr, _i32, _i32, _f32, _f32, _f32, _f32,
+                               _vp, _vp, _vp, _i32, _vp],
     "ngt_sparse_bwd": [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _pcsr, _i32, _i32, _f32, _f32, _f32,
                        _vp, _vp, _vp, _vp, _sz, _vp],
     "ngt_sparse_fwd_ext": [_i32, _vp, _vp, _vp, _vp, _vp, _i32, _pcsr, _i32, _i32, _f32, _f32,

@@ -1151,3 +1151,64 @@ extern "C" int ngt_sparse_bwd(int dtype, const void* q, const void* k, const voi
                             n_heads, head_dim, scale, clamp_lo, clamp_hi, grad_q, grad_k, grad_v,
                             workspace, workspace_bytes, stream);
 }
+
+// ------------------------------------------------ allocation-free forward
+// ngt_sparse_fwd for callers that cannot allocate (code under HIP graph
+// capture, serving loops, harnesses that forbid hipMalloc): its scratch (the
+// split rows' fp32 partials and the per-(row, head) Z buffer, the forward's
+// workspace) lives in a static device array of kNoAllocScratchBytes that every
+// device holds until the process ends.  Host code never passes the array's
+// name to a kernel (on the host it is only a stand-in for the symbol): the
+// device address comes from hipGetSymbolAddress, once per device, with that
+// device current, and is kept per device.  Nothing in the scratch has to start
+// at zero: every word a kernel reads was written earlier in the same call
+// (each split item writes its partial slot, every row -- empty rows included,
+// through the packed list -- writes its Z), so the last call's contents are
+// never read.  Calls that overlap on one device share the array and race.
+#include <mutex>
+
+constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;  // 32 MiB per device
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Device address of `scratch` on the current device (looked up on the first
+// call there).
+int scratch_ptr(void** out) {
+  int dev = -1;
+  NGT_HIP_CHECK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return set_error(NGT_ERR_UNSUPPORTED, "ngt_sparse_fwd_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    NGT_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return set_error(NGT_ERR_HIP, "ngt_sparse_fwd_noalloc: no address for scratch");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return NGT_OK;
+}
+}  // namespace
+
+extern "C" int ngt_sparse_fwd_noalloc(int dtype, const void* q, const void* k, const void* v,
+                                      const ngt_window_csr* csr, int32_t n_heads,
+                                      int32_t head_dim, float scale, float clamp_lo,
+                                      float clamp_hi, float eps, void* out, float* rinv,
+                                      float* node_score, int32_t node_score_len, void* stream) {
+  const int rc = check_common("ngt_sparse_fwd_noalloc", dtype, csr, n_heads, head_dim);
+  if (rc != NGT_OK) return rc;
+  const size_t need = fwd_layout(csr, n_heads, head_dim).total;
+  if (need > kNoAllocScratchBytes)
+    return set_error(NGT_ERR_UNSUPPORTED,
+                     "ngt_sparse_fwd_noalloc: the window needs %zu bytes of scratch; the static "
+                     "buffer holds %zu (use ngt_sparse_fwd with a workspace)",
+                     need, kNoAllocScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) NGT_CHECK_OK(scratch_ptr(&ws));
+  return ngt_sparse_fwd(dtype, q, k, v, csr, n_heads, head_dim, scale, clamp_lo, clamp_hi, eps,
+                        out, rinv, node_score, node_score_len, ws, need, stream);
+}

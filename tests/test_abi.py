@@ -118,6 +118,21 @@ def test_layernorm_rejects_misaligned_rows_without_touching_the_gpu():
     assert rc == 1 and b"aligned" in lib.ngt_last_error()
 
 
+def test_noalloc_forward_rejects_windows_beyond_its_scratch_without_touching_the_gpu():
+    """The allocation-free forward holds 32 MiB of static scratch: a window
+    whose forward workspace is larger is refused before anything runs."""
+    lib = _lib.load()
+    s = _lib.WindowCSR()
+    s.n_q = s.n_k = 200_000
+    s.n_packed_q = s.n_packed_k = 200_000  # counters consistent with an edgeless window
+    fb, bb = C.c_size_t(), C.c_size_t()
+    assert lib.ngt_sparse_workspace_bytes(C.byref(s), 64, 8, C.byref(fb), C.byref(bb)) == 0
+    assert fb.value > 32 << 20
+    rc = lib.ngt_sparse_fwd_noalloc(1, None, None, None, C.byref(s), 64, 8, 8.0 ** 0.5, -5.0, 5.0,
+                                    1e-6, None, None, None, 0, None)
+    assert rc == 2 and b"static" in lib.ngt_last_error()
+
+
 def test_product_never_imports_the_oracle():
     pkg = ROOT / "neutrongt_amd"
     for f in list(pkg.rglob("*.py")) + list(pkg.rglob("*.hip")):
