@@ -277,6 +277,26 @@ int ngt_merge_related_nodes(const int32_t* xadj, const int32_t* adjncy, const in
                             void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * METIS adjacency and edge weights from a PPR edge list, on the GPU.
+ * Replaces build_adj_fromat, NeutronGT/core/ppr_preprocess.py:30-71.
+ * edge_index: int64 [2, n_entries] (row 1 at edge_index + n_entries);
+ * ppr_val: fp32 [n_entries].  Entry e is the undirected key (min, max) of its
+ * endpoints; the values of one key are added in fp32 in entry order starting
+ * from 0 (a fixed order: the reference's scatter_add_ run sequentially), and
+ * w = int32(clamp_min(sum * 1000, 1)) with truncation.  Out: the symmetric
+ * CSR xadj int32 [n_nodes + 1], adjncy / eweights int32 [2U] (capacity
+ * 2 * n_entries suffices) over the U unique keys: rows in ascending node id,
+ * inside row u the keys (u, v > u) in ascending v, then the keys (v < u, u)
+ * in ascending v.  info (device int64[3]) = {U, entries with an id outside
+ * [0, n_nodes), weights >= 2^31}; the caller must reject the result when
+ * either count is non-zero.  Workspace: ngt_adj_weights_workspace_bytes.
+ */
+int ngt_adj_weights_workspace_bytes(int64_t n_entries, int64_t n_nodes, size_t* bytes);
+int ngt_adj_weights(const int64_t* edge_index, const float* ppr_val, int64_t n_entries,
+                    int64_t n_nodes, int32_t* xadj, int32_t* adjncy, int32_t* eweights,
+                    int64_t* info, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Row gather dst[r, :] = src[idx[r], :] for r < n_rows (row_bytes a multiple
  * of 4).  Assembles a window's feature block from the feature table and the
  * duplicate-node cache, as in

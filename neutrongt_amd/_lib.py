@@ -115,6 +115,8 @@ SIGNATURES = {
     "ngt_colsum_bf16": [_vp, _i64, _i32, _vp, _vp, _sz, _vp],
     "ngt_related_workspace_bytes": [_i32, _i32, _psz],
     "ngt_merge_related_nodes": [_vp, _vp, _vp, _i32, _vp, _i32, _i32, _vp, _vp, _vp, _sz, _vp],
+    "ngt_adj_weights_workspace_bytes": [_i64, _i64, _psz],
+    "ngt_adj_weights": [_vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
     "ngt_gather_rows": [_vp, _i64, _vp, _i64, _i64, _vp, _vp, _vp],
     "ngt_segment_sum_f32": [_vp, _i64, _vp, _i64, _vp, _vp, _vp],
     "ngt_ppr_count_workspace_bytes": [_i32, _vp],

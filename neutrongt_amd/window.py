@@ -209,33 +209,41 @@ def assemble_window_features(feature: torch.Tensor, cache: torch.Tensor, dup_ind
 
 
 def adj_weights(edge_index: torch.Tensor, ppr_val: torch.Tensor):
-    """Symmetric int32 METIS adjacency + weights from a PPR edge list.
+    """Symmetric int32 METIS adjacency + weights from a PPR edge list
+    (build_adj_fromat, NeutronGT/core/ppr_preprocess.py:30-71), on the GPU
+    (``ngt_adj_weights``).
 
-    w = int32(clamp_min(fp32 sum of the PPR values of {u,v} * 1000, 1)); rows in
-    ascending node order; inside row u the (u, v>u) keys come first in ascending
-    v, then the (v<u, u) keys in ascending v (stable order).  Returns
-    (xadj, adjncy, eweights) int32 on edge_index's device.
+    w = int32(clamp_min(fp32 sum of the PPR values of {u,v} * 1000, 1)), the
+    values of a key added in entry order from 0 (fixed, not atomic); rows in
+    ascending node order; inside row u the (u, v>u) keys come first in
+    ascending v, then the (v<u, u) keys in ascending v (stable order).  The
+    node count is max(edge_index) + 1 (one device-to-host read, as in the
+    reference).  Returns (xadj, adjncy, eweights) int32 on edge_index's device.
     """
     dev = edge_index.device
+    if not edge_index.is_cuda:
+        raise ValueError("adj_weights runs on the GPU (edge_index is on the CPU)")
     if edge_index.numel() == 0:
         z = torch.zeros(0, dtype=torch.int32, device=dev)
         return torch.zeros(1, dtype=torch.int32, device=dev), z, z
-    n = int(edge_index.max().item()) + 1
-    src, dst = edge_index[0].long(), edge_index[1].long()
-    u = torch.minimum(src, dst)
-    v = torch.maximum(src, dst)
-    key = u * n + v
-    uniq, inv = torch.unique(key, sorted=True, return_inverse=True)
-    summed = torch.zeros(uniq.numel(), dtype=torch.float32, device=dev)
-    summed.scatter_add_(0, inv, ppr_val.to(torch.float32))
-    uu = torch.div(uniq, n, rounding_mode="floor")
-    vv = uniq % n
-    w = (summed * 1000).clamp_min(1).to(torch.int32)
-    u_all = torch.cat([uu, vv])
-    v_all = torch.cat([vv, uu])
-    w_all = torch.cat([w, w])
-    order = torch.sort(u_all, stable=True).indices
-    deg = torch.bincount(u_all, minlength=n)
-    xadj = torch.zeros(n + 1, dtype=torch.int64, device=dev)
-    xadj[1:] = torch.cumsum(deg, 0)
-    return xadj.to(torch.int32), v_all[order].to(torch.int32), w_all[order]
+    ei = edge_index.to(torch.int64).contiguous()
+    val = ppr_val.to(device=dev, dtype=torch.float32).contiguous()
+    E = int(ei.shape[1])
+    if val.numel() != E:
+        raise ValueError(f"{val.numel()} PPR values for {E} entries")
+    n = int(ei.max().item()) + 1
+    lib = _lib.load()
+    nb = C.c_size_t()
+    _lib.check(lib.ngt_adj_weights_workspace_bytes(E, n, C.byref(nb)))
+    ws = torch.empty(max(nb.value, 1), dtype=torch.uint8, device=dev)
+    xadj = torch.empty(n + 1, dtype=torch.int32, device=dev)
+    adjncy = torch.empty(2 * E, dtype=torch.int32, device=dev)
+    ew = torch.empty(2 * E, dtype=torch.int32, device=dev)
+    info = torch.empty(3, dtype=torch.int64, device=dev)
+    _lib.check(lib.ngt_adj_weights(ei.data_ptr(), val.data_ptr(), E, n, xadj.data_ptr(),
+                                   adjncy.data_ptr(), ew.data_ptr(), info.data_ptr(),
+                                   ws.data_ptr(), nb.value, _lib.stream_ptr(dev)))
+    u, bad, big = (int(x) for x in info.tolist())
+    if bad or big:
+        raise ValueError(f"adj_weights: {bad} entries with a negative id, {big} weights >= 2^31")
+    return xadj, adjncy[: 2 * u], ew[: 2 * u]

@@ -1,12 +1,17 @@
-"""The window encoder (projections, LayerNorm, FFN and the HIP attention core)
-against the same encoder on the CPU whose attention is the oracle: log-probs,
-per-layer node scores and every parameter gradient."""
+"""The window encoders (projections, LayerNorm, FFN and the HIP attention core)
+against the oracle's restatement of the reference encoders (oracle/encoder.py,
+square windows, eval mode), and -- with related-key caches, bf16 autocast and
+gradients -- against the same encoder whose attention core is the oracle:
+log-probs, per-layer node scores and every parameter gradient.  Also the
+reference-side install() of the HIP core into a module shaped like the
+reference's MultiHeadAttention."""
 import pytest
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
 from oracle import attention as OA
+from oracle import encoder as OE
 from tests._util import TOL, assert_close, assert_parity, random_coo, relerr
 
 pytestmark = pytest.mark.gpu
@@ -77,6 +82,118 @@ def _run(model, x, ei, cache, labels, mask, autocast=None):
     grads = {n: p.grad.detach().double().cpu() for n, p in model.named_parameters()
              if p.grad is not None}
     return out.detach(), [s.cpu() for s in scores], loss.detach(), grads
+
+
+@pytest.mark.parametrize("family", ["graphormer", "gt"])
+@pytest.mark.parametrize("attn_type", ["sparse", "full"])
+def test_encoder_matches_the_reference_encoder_restatement(family, attn_type):
+    """fp32, eval mode, square window (every node a query and a key, no
+    cache): the product's encoder on the GPU against oracle/encoder.py's
+    functional restatement of Graphormer.forward / GT_SW.forward on the CPU,
+    loaded with the same state_dict -- log-probs and per-layer node scores at
+    1e-5 (against the fp32 and float64 restatements)."""
+    print(f"case encoder vs reference restatement {family} {attn_type}", flush=True)
+    model, _, x, _, _, _, _ = _build(seed=11, family=family)
+    ei = torch.from_numpy(random_coo(N_Q, N_Q, 900, seed=11))
+    n_layers = len(model.layers)
+    fwd = OE.graphormer_forward if family == "graphormer" else OE.gt_forward
+    sd = model.state_dict()
+    ref32 = fwd({k: v.float() for k, v in sd.items()}, x.float(), ei, n_layers, H, attn_type)
+    ref64 = fwd({k: v.double() for k, v in sd.items()}, x.double(), ei, n_layers, H, attn_type)
+    dev = torch.device("cuda")
+    model = model.to(dev).eval()
+    with torch.no_grad():
+        out, scores = model(x.to(dev), ei.to(dev), attn_type, None)
+    assert_parity(out.cpu(), ref32[0], ref64[0], torch.float32, "log_probs")
+    assert len(scores) == n_layers
+    for i, (a, b, c) in enumerate(zip(scores, ref32[1], ref64[1])):
+        assert a.shape == b.shape, (a.shape, b.shape)
+        assert_parity(a.cpu(), b, c, torch.float32, f"node_score layer {i}")
+
+
+class _RefCoreAttention(nn.Module):
+    """A module with the reference CoreAttention's attributes
+    (graphormer_dist_node_level.py:33-40) whose forward runs the oracle's
+    sparse restatement on the CPU -- what install() must find and replace."""
+
+    def __init__(self, hidden_size, attention_dropout_rate, num_heads):
+        super().__init__()
+        self.hidden_size_per_attention_head = hidden_size // num_heads
+        self.scale = (hidden_size // num_heads) ** 0.5
+        self.num_heads = num_heads
+        self.attention_dropout_rate = attention_dropout_rate
+        self.att_dropout = nn.Dropout(attention_dropout_rate)
+
+    def forward(self, q, k, v, attn_bias=None, edge_index=None, attn_type=None, mask=None,
+                pruning_mask=None):
+        b, n = q.shape[0], q.shape[1]
+        x, score = OA.sparse_attention_bias(q.cpu(), k.cpu(), v.cpu(), edge_index.cpu(),
+                                            self.num_heads)
+        return x.reshape(b, n, -1).to(q.device), score.to(q.device)
+
+
+class _RefMHA(nn.Module):
+    """Shaped like the reference's MultiHeadAttention
+    (graphormer_dist_node_level.py:128-173, dup_nodes_kv_cache None): projections,
+    local_attn(q, k, v, attn_bias, edge_index, attn_type), output_layer."""
+
+    def __init__(self, hidden_size, attention_dropout_rate, num_heads):
+        super().__init__()
+        self.num_heads = num_heads
+        self.att_size = hidden_size // num_heads
+        self.linear_q = nn.Linear(hidden_size, hidden_size)
+        self.linear_k = nn.Linear(hidden_size, hidden_size)
+        self.linear_v = nn.Linear(hidden_size, hidden_size)
+        self.local_attn = _RefCoreAttention(hidden_size, attention_dropout_rate, num_heads)
+        self.output_layer = nn.Linear(hidden_size, hidden_size)
+
+    def forward(self, x, attn_bias=None, edge_index=None, attn_type=None):
+        b = x.shape[0]
+        q = self.linear_q(x).view(b, -1, self.num_heads, self.att_size)
+        k = self.linear_k(x).view(b, -1, self.num_heads, self.att_size)
+        v = self.linear_v(x).view(b, -1, self.num_heads, self.att_size)
+        y, score = self.local_attn(q, k, v, attn_bias, edge_index, attn_type)
+        return self.output_layer(y), score
+
+
+def test_install_replaces_the_reference_core_in_place():
+    """install() swaps every reference-shaped local_attn of a model for the HIP
+    CoreAttention (hidden size, heads and dropout kept, training mode kept);
+    the model's output is unchanged within 1e-5 (the oracle core before, the
+    HIP core after) and the core now runs on the GPU."""
+    from neutrongt_amd import CoreAttention, install
+
+    print("case install", flush=True)
+    torch.manual_seed(4)
+    hidden = H * D_HEAD
+    model = nn.ModuleList([_RefMHA(hidden, 0.25, H) for _ in range(2)]).cuda().eval()
+    for m in model.modules():
+        if isinstance(m, nn.Linear):
+            nn.init.normal_(m.weight, std=1.5 / m.in_features ** 0.5)
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(1, N_Q, hidden, generator=g).cuda()
+    ei = torch.from_numpy(random_coo(N_Q, N_Q, 900, seed=4)).cuda()
+
+    def run():
+        y, scores = x, []
+        with torch.no_grad():
+            for mha in model:
+                y, s = mha(y, None, ei, "sparse")
+                scores.append(s)
+        return y, scores
+
+    before = run()
+    assert install(model) == 2
+    for mha in model:
+        core = mha.local_attn
+        assert isinstance(core, CoreAttention)
+        assert core.num_heads == H and core.hidden_size_per_attention_head == D_HEAD
+        assert core.attention_dropout_rate == 0.25 and not core.training
+    assert install(model) == 0  # already installed
+    after = run()
+    assert_close(after[0].cpu(), before[0].cpu(), torch.float32, "install: output")
+    for a, b in zip(after[1], before[1]):
+        assert_close(a.cpu(), b.cpu(), torch.float32, "install: node scores")
 
 
 @pytest.mark.parametrize("family", ["graphormer", "gt"])

@@ -46,16 +46,50 @@ def test_related_nodes_match_oracle(n, E, n_part, seed):
         np.testing.assert_array_equal(got, want)
 
 
-def test_adj_weights_on_gpu_match_oracle():
-    _say("case adj weights")
-    rng = np.random.default_rng(4)
-    ei = rng.integers(0, 500, (2, 5000))
-    val = rng.random(5000).astype(np.float32) / 50
+@pytest.mark.parametrize("n,E,dup", [(500, 5000, 1), (60, 400, 1), (300, 20000, 8), (1, 3, 1),
+                                     (2000, 30000, 40)])
+def test_adj_weights_on_gpu_match_oracle(n, E, dup):
+    """ngt_adj_weights bit for bit against the oracle, including keys with
+    many PPR entries (dup > 1: each (u, v) pair drawn from a small pool, in
+    both directions), whose fp32 sums depend on the order of the adds."""
+    _say(f"case adj weights n={n} E={E} dup={dup}")
+    rng = np.random.default_rng(n + E)
+    if dup > 1:
+        pool = rng.integers(0, n, (2, E // dup))
+        pick = rng.integers(0, pool.shape[1], E)
+        ei = pool[:, pick]
+        flip = rng.random(E) < 0.5
+        ei = np.where(flip, ei[::-1], ei)
+    else:
+        ei = rng.integers(0, n, (2, E))
+    val = (rng.random(E).astype(np.float32) / 50).astype(np.float32)
+    keys = np.minimum(ei[0], ei[1]) * n + np.maximum(ei[0], ei[1])
+    if dup > 1:
+        assert np.bincount(np.unique(keys, return_inverse=True)[1]).max() >= 3
     x, a, w = W.adj_weights(torch.from_numpy(ei).cuda(), torch.from_numpy(val).cuda())
     xo, ao, wo = OG.adj_weights(ei, val)
     np.testing.assert_array_equal(x.cpu().numpy(), xo)
     np.testing.assert_array_equal(a.cpu().numpy(), ao)
     np.testing.assert_array_equal(w.cpu().numpy(), wo)
+
+
+def test_adj_weights_on_gpu_sum_in_entry_order():
+    """A key whose three values truncate to 2 summed in entry order and to 3 in
+    reverse: the GPU path adds in entry order (no atomics), both ways round."""
+    _say("case adj weights order")
+    a, b, c = 0.0005994238, 0.0004226872, 0.0019778889
+    for ei, vals, want in (([[4, 1, 4], [1, 4, 1]], [a, b, c], 2),
+                           ([[1, 4, 1], [4, 1, 4]], [c, b, a], 3)):
+        x, adj, w = W.adj_weights(torch.tensor(ei).cuda(),
+                                  torch.tensor(vals, dtype=torch.float32).cuda())
+        assert w.tolist() == [want, want] and adj.tolist() == [4, 1]
+        assert x.tolist() == [0, 0, 1, 1, 1, 2]
+
+
+def test_adj_weights_rejects_negative_ids():
+    _say("case adj weights bad id")
+    with pytest.raises(ValueError):
+        W.adj_weights(torch.tensor([[0, -1], [1, 2]]).cuda(), torch.tensor([0.1, 0.2]).cuda())
 
 
 def test_window_feature_assembly_bit_exact():

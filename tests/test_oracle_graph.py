@@ -171,17 +171,27 @@ def test_adj_weights_hand_derived():
     assert ew.tolist() == [3, 1, 3, 1]
 
 
-def test_host_adj_weights_matches_oracle():
+def test_adj_weights_sums_each_key_in_entry_order():
+    """Three PPR entries of one undirected key whose fp32 sum truncates to 2 in
+    entry order ((0 + a) + b) + c and to 3 in the reverse order: the oracle
+    follows the reference's sequential scatter_add_ (entry order)."""
+    a, b, c = np.float32(0.0005994238), np.float32(0.0004226872), np.float32(0.0019778889)
+    f = np.float32
+    assert int(f(f(f(f(0) + a) + b) + c) * f(1000)) == 2
+    assert int(f(f(f(f(0) + c) + b) + a) * f(1000)) == 3
+    ei = np.array([[4, 1, 4], [1, 4, 1]])
+    xadj, adjncy, ew = OG.adj_weights(ei, np.array([a, b, c], np.float32))
+    assert ew.tolist() == [2, 2] and adjncy.tolist() == [4, 1]
+    xadj, adjncy, ew = OG.adj_weights(ei[:, ::-1], np.array([c, b, a], np.float32))
+    assert ew.tolist() == [3, 3]
+
+
+def test_host_adj_weights_has_no_cpu_path():
     from neutrongt_amd import window as W
 
-    rng = np.random.default_rng(9)
-    ei = rng.integers(0, 60, (2, 400))
-    val = rng.random(400).astype(np.float32) / 100
-    x, a, w = W.adj_weights(torch.from_numpy(ei), torch.from_numpy(val))
-    xo, ao, wo = OG.adj_weights(ei, val)
-    np.testing.assert_array_equal(x.numpy(), xo)
-    np.testing.assert_array_equal(a.numpy(), ao)
-    np.testing.assert_array_equal(w.numpy(), wo)
+    ei = torch.tensor([[0, 1], [1, 0]])
+    with pytest.raises(ValueError):
+        W.adj_weights(ei, torch.tensor([0.1, 0.2]))
 
 
 def test_subgraph_relabel_by_position():
