@@ -334,6 +334,13 @@ struct dtype_of<bf16_t> {
   static constexpr int value = NGT_BF16;
 };
 
+// Key split of a dense matrix-core pass: n_split blocks along grid z, each
+// over split_keys consecutive keys (a multiple of the 128-key stage).
+struct MfSplit {
+  int n_split;
+  int split_keys;
+};
+
 // Records a message for ngt_last_error() (thread-local) and returns the code.
 int set_error(int code, const char* fmt, ...);
 

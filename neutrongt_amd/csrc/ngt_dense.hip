@@ -31,12 +31,15 @@ namespace ngt {
 
 // Matrix-core kernels (ngt_dense_mfma.hip).
 bool mfma_dense_supported(int d);
+MfSplit mfma_fwd_split(int n_q, int n_k, int H);
+MfSplit mfma_dq_split(int n_q, int n_k, int H);
 int mfma_dense_fwd(int d, const void* q, const void* k, const void* v, int n_q, int n_k, int H,
                    float scale, const DropoutMask* dm, void* out, float* out32, float* lse,
-                   float* part, hipStream_t st);
+                   float* part, MfSplit sp, float* part_ml, float* part_acc, hipStream_t st);
 int mfma_dense_bwd(int d, const void* q, const void* k, const void* v, const void* g,
                    const float* lse, const float* dsum, int n_q, int n_k, int H, float scale,
-                   const DropoutMask* dm, void* gq, void* gk, void* gv, hipStream_t st);
+                   const DropoutMask* dm, void* gq, void* gk, void* gv, MfSplit sq,
+                   float* part_dq, hipStream_t st);
 
 namespace {
 
@@ -946,9 +949,49 @@ int rowstat_bf16(int d, const void* out, const float* out32, const void* g, int 
 // partials (only with node scores); the vector-ALU path needs per-block
 // node-score partials (only with node scores) and, when it splits the keys,
 // the split states behind them.
+// The matrix-core path: [node-score partials H * n_k (with node scores)]
+// [split states (m, l) and unnormalised outputs (with a key split)].
+struct MfFwdLayout {
+  size_t ml, acc, total;
+  MfSplit sp;
+};
+MfFwdLayout mf_fwd_layout(int32_t n_q, int32_t n_k, int32_t H, int32_t d, bool node_scores) {
+  MfFwdLayout L{};
+  L.sp = mfma_fwd_split(n_q, n_k, H);
+  size_t off = node_scores ? align256(size_t(H) * n_k * 4) : 0;
+  if (L.sp.n_split > 1) {
+    L.ml = off;
+    off += align256(size_t(L.sp.n_split) * n_q * H * 8);
+    L.acc = off;
+    off += align256(size_t(L.sp.n_split) * n_q * H * d * 4);
+  }
+  L.total = off;
+  return L;
+}
+
 size_t fwd_need(int dtype, int32_t n_q, int32_t n_k, int32_t H, int32_t d, bool node_scores) {
-  if (use_mfma(dtype, d)) return node_scores ? align256(size_t(H) * n_k * 4) : 0;
+  if (use_mfma(dtype, d)) return mf_fwd_layout(n_q, n_k, H, d, node_scores).total;
   return node_scores || key_split(n_q, n_k, H).n_split > 1 ? fwd_ws(n_q, n_k, H, d) : 0;
+}
+
+// Backward workspace: D_i [n_q, H] fp32, and on the matrix-core path the key
+// splits' partial dQ after it.
+size_t bwd_need(int dtype, int32_t n_q, int32_t n_k, int32_t H, int32_t d) {
+  size_t need = bwd_ws(n_q, H);
+  if (use_mfma(dtype, d) && n_q > 0) {
+    const MfSplit sq = mfma_dq_split(n_q, n_k, H);
+    if (sq.n_split > 1) need += align256(size_t(sq.n_split) * n_q * H * d * 4);
+  }
+  return need;
+}
+
+template <int DH>
+void launch_mf_combine(const float* part_ml, const float* part_acc, int n_split, int n_q, int H,
+                       void* out, float* out32, float* lse, hipStream_t st) {
+  int64_t blocks = (int64_t(n_q) * H + kBlock - 1) / kBlock;
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL((k_dense_combine<bf16_t, DH>), dim3(int(blocks)), dim3(kBlock), 0, st,
+                     part_ml, part_acc, n_split, n_q, H, static_cast<bf16_t*>(out), out32, lse);
 }
 
 __global__ void k_fill_zero(float* __restrict__ p, int64_t n) {
@@ -967,7 +1010,7 @@ extern "C" int ngt_dense_workspace_bytes(int dtype, int32_t n_q, int32_t n_k, in
   const int rc = check_args("ngt_dense_workspace_bytes", dtype, n_q, n_k, n_heads, head_dim);
   if (rc != NGT_OK) return rc;
   if (fwd_bytes) *fwd_bytes = n_q > 0 ? fwd_need(dtype, n_q, n_k, n_heads, head_dim, node_scores != 0) : 0;
-  if (bwd_bytes) *bwd_bytes = bwd_ws(n_q, n_heads);
+  if (bwd_bytes) *bwd_bytes = bwd_need(dtype, n_q, n_k, n_heads, head_dim);
   return NGT_OK;
 }
 
@@ -1000,9 +1043,24 @@ extern "C" int ngt_dense_fwd(int dtype, const void* q, const void* k, const void
   if (use_mfma(dtype, head_dim)) {
     if (n_q == 0) return NGT_OK;
     float* part = node_score ? static_cast<float*>(workspace) : nullptr;
+    const MfFwdLayout L = mf_fwd_layout(n_q, n_k, n_heads, head_dim, node_score != nullptr);
+    char* ws = static_cast<char*>(workspace);
+    float* part_ml = L.sp.n_split > 1 ? reinterpret_cast<float*>(ws + L.ml) : nullptr;
+    float* part_acc = L.sp.n_split > 1 ? reinterpret_cast<float*>(ws + L.acc) : nullptr;
     rc = mfma_dense_fwd(head_dim, q, k, v, n_q, n_k, n_heads, scale, dm, out, out_f32, lse, part,
-                        st);
-    if (rc != NGT_OK || !node_score || n_k == 0) return rc;
+                        L.sp, part_ml, part_acc, st);
+    if (rc != NGT_OK) return rc;
+    if (L.sp.n_split > 1) {
+      KernelTimer timer_("dense_combine", st);
+      switch (head_dim) {
+        case 8: launch_mf_combine<8>(part_ml, part_acc, L.sp.n_split, n_q, n_heads, out, out_f32, lse, st); break;
+        case 16: launch_mf_combine<16>(part_ml, part_acc, L.sp.n_split, n_q, n_heads, out, out_f32, lse, st); break;
+        case 24: launch_mf_combine<24>(part_ml, part_acc, L.sp.n_split, n_q, n_heads, out, out_f32, lse, st); break;
+        default: launch_mf_combine<32>(part_ml, part_acc, L.sp.n_split, n_q, n_heads, out, out_f32, lse, st); break;
+      }
+      NGT_HIP_CHECK(hipGetLastError());
+    }
+    if (!node_score || n_k == 0) return NGT_OK;
     hipLaunchKernelGGL(k_dense_scores, dim3((n_k + kWave - 1) / kWave), dim3(kScoreThreads), 0, st,
                        part, n_heads, n_k, n_heads, node_score);
     NGT_HIP_CHECK(hipGetLastError());
@@ -1030,7 +1088,7 @@ extern "C" int ngt_dense_bwd(int dtype, const void* q, const void* k, const void
     return set_error(NGT_ERR_ARG, "ngt_dense_bwd: null query-side pointer");
   if (n_k > 0 && (!k || !v || !grad_k || !grad_v))
     return set_error(NGT_ERR_ARG, "ngt_dense_bwd: null key-side pointer");
-  const size_t need = bwd_ws(n_q, n_heads);
+  const size_t need = bwd_need(dtype, n_q, n_k, n_heads, head_dim);
   if (need > 0 && (!workspace || workspace_bytes < need))
     return set_error(NGT_ERR_WORKSPACE, "ngt_dense_bwd: workspace %zu < %zu", workspace_bytes,
                      need);
@@ -1041,8 +1099,12 @@ extern "C" int ngt_dense_bwd(int dtype, const void* q, const void* k, const void
       rc = rowstat_bf16(head_dim, out, out_f32, grad_out, n_q, n_heads, dsum, st);
       if (rc != NGT_OK) return rc;
     }
+    const MfSplit sq = n_q > 0 ? mfma_dq_split(n_q, n_k, n_heads) : MfSplit{1, 1};
+    float* part_dq = sq.n_split > 1
+                         ? reinterpret_cast<float*>(static_cast<char*>(workspace) + bwd_ws(n_q, n_heads))
+                         : nullptr;
     return mfma_dense_bwd(head_dim, q, k, v, grad_out, lse, dsum, n_q, n_k, n_heads, scale, dm,
-                          grad_q, grad_k, grad_v, st);
+                          grad_q, grad_k, grad_v, sq, part_dq, st);
   }
   return dispatch<BwdOp>(dtype, head_dim, q, k, v, out, out_f32, grad_out, lse, int(n_q), int(n_k),
                          int(n_heads), scale, dm, grad_q, grad_k, grad_v,

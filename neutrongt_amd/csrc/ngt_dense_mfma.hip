@@ -26,6 +26,9 @@
 #include "ngt_common.h"
 
 #include <math.h>
+#include <stdlib.h>
+
+#include <algorithm>
 
 namespace ngt {
 namespace {
@@ -217,7 +220,9 @@ __global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
                                                    int32_t n_k, int32_t H, float scale,
                                                    DropoutMask dm, bf16_t* __restrict__ out,
                                                    float* __restrict__ out32,
-                                                   float* __restrict__ lse) {
+                                                   float* __restrict__ lse, int32_t split_keys,
+                                                   float* __restrict__ part_ml,
+                                                   float* __restrict__ part_acc) {
   constexpr int NC = DH / 8;  // K chunks of the QK^T contraction
   __shared__ __align__(16) short ks[kSB][DH + kRowPad];  // K rows
   __shared__ __align__(16) short vt[kT][kSB + kColPad];  // V^T: [c][key], rows >= DH constant
@@ -246,20 +251,24 @@ __global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
   float m = -INFINITY, l = 0.f;
   f32x16 acc = zero16();  // O^T[c][q]: c = 8*(i/4) + 4*half + i%4
 
+  // keys [k_begin, k_end) of this block's split (blockIdx.z; split_keys a
+  // multiple of kSB); one split covers all keys
+  const int k_begin = int(blockIdx.z) * split_keys;
+  const int k_end = min(n_k, k_begin + split_keys);
   fill_pad_rows<DH>(vt, !DROP);
   Stage<DH> pk, pv;
-  pk.load(k, 0, n_k, H, h);
-  pv.load(v, 0, n_k, H, h);
-  for (int kb = 0; kb < n_k; kb += kSB) {
+  pk.load(k, k_begin, k_end, H, h);
+  pv.load(v, k_begin, k_end, H, h);
+  for (int kb = k_begin; kb < k_end; kb += kSB) {
     __syncthreads();
     pk.store_rows(ks);
     pv.store_trans(vt);
     __syncthreads();
-    if (kb + kSB < n_k) {
-      pk.load(k, kb + kSB, n_k, H, h);
-      pv.load(v, kb + kSB, n_k, H, h);
+    if (kb + kSB < k_end) {
+      pk.load(k, kb + kSB, k_end, H, h);
+      pv.load(v, kb + kSB, k_end, H, h);
     }
-    for (int sub = 0; sub < kSB / kT && kb + sub * kT < n_k; ++sub) {
+    for (int sub = 0; sub < kSB / kT && kb + sub * kT < k_end; ++sub) {
       const int r0 = sub * kT;
       // S^T tile: rows = keys kb + r0 + (8*(i/4) + 4*half + i%4), col = this lane's query.
       f32x16 st = zero16();
@@ -269,13 +278,13 @@ __global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
                    qb[j], qb[j + 1], st);
       if constexpr (NC % 2) st = mfma(lds4(&ks[r0 + l32][8 * (NC - 1) + 4 * half]), qb[NC - 1], st);
       float mx = -INFINITY;
-      if (kb + r0 + kT <= n_k) {
+      if (kb + r0 + kT <= k_end) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) mx = fmaxf(mx, st[i]);
-      } else {  // tail tile: keys past n_k drop out
+      } else {  // tail tile: keys past the split's end drop out
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          if (kb + r0 + 8 * (i / 4) + 4 * half + (i % 4) >= n_k) st[i] = -INFINITY;
+          if (kb + r0 + 8 * (i / 4) + 4 * half + (i % 4) >= k_end) st[i] = -INFINITY;
           mx = fmaxf(mx, st[i]);
         }
       }
@@ -333,6 +342,21 @@ __global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
     l = sum_halves(l);
   }
   if (!q_ok) return;
+  if (part_ml) {
+    // this split's softmax state in natural-log units (m ln 2, l) and its
+    // unnormalised O, merged in split order by k_dense_combine
+    const int64_t z = blockIdx.z;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int c = 8 * (i / 4) + 4 * half + (i % 4);
+      if (c < DH) part_acc[((z * n_q + qi) * H + h) * DH + c] = acc[i];
+    }
+    if (half == 0) {
+      part_ml[2 * ((z * H + h) * n_q + qi)] = m * kLn2;
+      part_ml[2 * ((z * H + h) * n_q + qi) + 1] = l;
+    }
+    return;
+  }
   const float inv = n_k > 0 ? 1.0f / l : 0.f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
@@ -527,7 +551,7 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_q(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
     const bf16_t* __restrict__ g, const float* __restrict__ lse, const float* __restrict__ dsum,
     int32_t n_q, int32_t n_k, int32_t H, float scale, DropoutMask dm,
-    bf16_t* __restrict__ grad_q) {
+    bf16_t* __restrict__ grad_q, int32_t split_keys, float* __restrict__ part_dq) {
   constexpr int NC = DH / 8;
   __shared__ __align__(16) short ks[kSB][DH + kRowPad];
   __shared__ __align__(16) short vs[kSB][DH + kRowPad];
@@ -550,21 +574,23 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_q(
   const float Dq = q_ok ? dsum[int64_t(h) * n_q + qi] : 0.f;
   const float s2 = scale * kLog2e;
   f32x16 dq = zero16();  // D[q][c]: q = 8*(i/4)+4*half+i%4 (tile row), c = l32
+  const int k_begin = int(blockIdx.z) * split_keys;  // this block's key split
+  const int k_end = min(n_k, k_begin + split_keys);
   fill_pad_rows<DH>(kt, false);
   Stage<DH> pk, pv;
-  pk.load(k, 0, n_k, H, h);
-  pv.load(v, 0, n_k, H, h);
-  for (int kb = 0; kb < n_k; kb += kSB) {
+  pk.load(k, k_begin, k_end, H, h);
+  pv.load(v, k_begin, k_end, H, h);
+  for (int kb = k_begin; kb < k_end; kb += kSB) {
     __syncthreads();
     pk.store_rows(ks);
     pv.store_rows(vs);
     pk.store_trans(kt);
     __syncthreads();
-    if (kb + kSB < n_k) {
-      pk.load(k, kb + kSB, n_k, H, h);
-      pv.load(v, kb + kSB, n_k, H, h);
+    if (kb + kSB < k_end) {
+      pk.load(k, kb + kSB, k_end, H, h);
+      pv.load(v, kb + kSB, k_end, H, h);
     }
-    for (int sub = 0; sub < kSB / kT && kb + sub * kT < n_k; ++sub) {
+    for (int sub = 0; sub < kSB / kT && kb + sub * kT < k_end; ++sub) {
       const int r0 = sub * kT;
       f32x16 st = zero16(), dp = zero16();
 #pragma unroll
@@ -588,14 +614,14 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_q(
         }
       }
       float ds[16];
-      if (kb + r0 + kT <= n_k) {
+      if (kb + r0 + kT <= k_end) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) ds[i] = __builtin_amdgcn_exp2f(fmaf(st[i], s2, -L2)) * (dp[i] - Dq);
-      } else {  // tail tile: keys past n_k drop out
+      } else {  // tail tile: keys past the split's end drop out
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int key = kb + r0 + 8 * (i / 4) + 4 * half + (i % 4);
-          ds[i] = key < n_k ? __builtin_amdgcn_exp2f(fmaf(st[i], s2, -L2)) * (dp[i] - Dq) : 0.f;
+          ds[i] = key < k_end ? __builtin_amdgcn_exp2f(fmaf(st[i], s2, -L2)) * (dp[i] - Dq) : 0.f;
         }
       }
       s16x4 dsa[4];  // dS as A operand: A[q][key step row] from the D[key][q] layout
@@ -610,10 +636,32 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_q(
   }
   if (l32 >= DH) return;
   const int64_t q0 = int64_t(blockIdx.x) * kRowsPerBlock + wave * kT;
+  if (part_dq) {  // this split's dQ, unscaled fp32; k_mf_dq_combine adds the splits in order
+    float* pz = part_dq + int64_t(blockIdx.z) * n_q * H * DH;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int64_t qq = q0 + 8 * (i / 4) + 4 * half + (i % 4);
+      if (qq < n_q) pz[(qq * H + h) * DH + l32] = dq[i];
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int64_t qq = q0 + 8 * (i / 4) + 4 * half + (i % 4);
     if (qq < n_q) grad_q[(qq * H + h) * DH + l32].x = f32_to_bf16(dq[i] * scale);
+  }
+}
+
+// grad_q = scale * sum of the key splits' partial dQ, added in split order.
+__global__ __launch_bounds__(kBlock) void k_mf_dq_combine(const float* __restrict__ part,
+                                                          int32_t n_split, int64_t n,
+                                                          float scale,
+                                                          bf16_t* __restrict__ grad_q) {
+  for (int64_t t = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; t < n;
+       t += int64_t(gridDim.x) * blockDim.x) {
+    float a = part[t];
+    for (int s = 1; s < n_split; ++s) a += part[int64_t(s) * n + t];
+    grad_q[t].x = f32_to_bf16(a * scale);
   }
 }
 
@@ -622,11 +670,42 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_q(
 // Launchers used by ngt_dense.hip for bf16 and d in {8, 16, 24, 32}.
 bool mfma_dense_supported(int d) { return d == 8 || d == 16 || d == 24 || d == 32; }
 
+// Key splits: the forward (one wave per 32 queries and head, all keys) and
+// the dQ pass have grids of ceil(n_q / 32) * H waves, about 4 per SIMD at
+// 16,000 queries and 8 heads, while their registers leave room for more.
+// Splitting the keys over blockIdx.z raises the waves per SIMD; each split's
+// state is merged afterwards in split order.  Measured at 16,000 nodes, 8
+// heads, d = 8 (us per launch, splits 1 / 2 / 3 / 4): forward 406 / 375 /
+// 372 / 364 plus a 7-9 us combine; dQ 427 / 404 / 396 plus 7 us.  The gains
+// are small because the kernels are bound by vector-ALU issue (16
+// exponentials and about 40 other vector instructions per 32 x 32 tile and
+// wave), not by latency: issuing the next tile's S product ahead of the
+// current tile's softmax chain made the forward slower (406 -> 432 us).
+// NGT_MF_FWD_SPLIT / NGT_MF_DQ_SPLIT override the count.
+static MfSplit plan_split(int n_q, int n_k, int H, int target_waves, const char* env) {
+  const int64_t base = int64_t((n_q + kRowsPerBlock - 1) / kRowsPerBlock) * H * kWaves;
+  int want = base > 0 ? int((target_waves + base / 2) / base) : 1;
+  if (const char* e = getenv(env)) want = atoi(e);
+  want = std::max(1, std::min({want, 8, std::max(1, n_k / 512)}));
+  if (want <= 1 || n_k <= 0) return {1, std::max(n_k, 1)};
+  int keys = (n_k + want - 1) / want;
+  keys = (keys + kSB - 1) / kSB * kSB;
+  return {(n_k + keys - 1) / keys, keys};
+}
+MfSplit mfma_fwd_split(int n_q, int n_k, int H) {
+  return plan_split(n_q, n_k, H, 6144, "NGT_MF_FWD_SPLIT");
+}
+MfSplit mfma_dq_split(int n_q, int n_k, int H) {
+  return plan_split(n_q, n_k, H, 12288, "NGT_MF_DQ_SPLIT");
+}
+
 template <int DH>
 static int mf_fwd(const void* q, const void* k, const void* v, int n_q, int n_k, int H,
                   float scale, const DropoutMask* dm, void* out, float* out32, float* lse,
-                  float* part, hipStream_t st) {
-  const dim3 grid((n_q + kRowsPerBlock - 1) / kRowsPerBlock, H);
+                  float* part, MfSplit sp, float* part_ml, float* part_acc, hipStream_t st) {
+  const dim3 grid((n_q + kRowsPerBlock - 1) / kRowsPerBlock, H, sp.n_split);
+  float* pml = sp.n_split > 1 ? part_ml : nullptr;
+  float* pacc = sp.n_split > 1 ? part_acc : nullptr;
   {
     KernelTimer timer_("dense_fwd", st);
     const DropoutMask m = dm ? *dm : DropoutMask{};
@@ -634,12 +713,12 @@ static int mf_fwd(const void* q, const void* k, const void* v, int n_q, int n_k,
       hipLaunchKernelGGL((k_mf_fwd<DH, true>), grid, dim3(kBlock), 0, st,
                          static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
                          static_cast<const bf16_t*>(v), n_q, n_k, H, scale, m,
-                         static_cast<bf16_t*>(out), out32, lse);
+                         static_cast<bf16_t*>(out), out32, lse, sp.split_keys, pml, pacc);
     else
       hipLaunchKernelGGL((k_mf_fwd<DH, false>), grid, dim3(kBlock), 0, st,
                          static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
                          static_cast<const bf16_t*>(v), n_q, n_k, H, scale, m,
-                         static_cast<bf16_t*>(out), out32, lse);
+                         static_cast<bf16_t*>(out), out32, lse, sp.split_keys, pml, pacc);
     NGT_HIP_CHECK(hipGetLastError());
   }
   if (part && n_k > 0) {
@@ -656,7 +735,7 @@ static int mf_fwd(const void* q, const void* k, const void* v, int n_q, int n_k,
 template <int DH>
 static int mf_bwd(const void* q, const void* k, const void* v, const void* g, const float* lse,
                   const float* dsum, int n_q, int n_k, int H, float scale, const DropoutMask* dm,
-                  void* gq, void* gk, void* gv, hipStream_t st) {
+                  void* gq, void* gk, void* gv, MfSplit sq, float* part_dq, hipStream_t st) {
   const DropoutMask m = dm ? *dm : DropoutMask{};
   if (n_k > 0) {
     KernelTimer timer_("dense_bwd_kv", st);
@@ -676,43 +755,55 @@ static int mf_bwd(const void* q, const void* k, const void* v, const void* g, co
     NGT_HIP_CHECK(hipGetLastError());
   }
   if (n_q > 0) {
-    KernelTimer timer_("dense_bwd_q", st);
-    const dim3 grid((n_q + kRowsPerBlock - 1) / kRowsPerBlock, H);
-    if (dm)
-      hipLaunchKernelGGL((k_mf_bwd_q<DH, true>), grid, dim3(kBlock), 0, st,
-                         static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
-                         static_cast<const bf16_t*>(v), static_cast<const bf16_t*>(g), lse, dsum,
-                         n_q, n_k, H, scale, m, static_cast<bf16_t*>(gq));
-    else
-      hipLaunchKernelGGL((k_mf_bwd_q<DH, false>), grid, dim3(kBlock), 0, st,
-                         static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
-                         static_cast<const bf16_t*>(v), static_cast<const bf16_t*>(g), lse, dsum,
-                         n_q, n_k, H, scale, m, static_cast<bf16_t*>(gq));
-    NGT_HIP_CHECK(hipGetLastError());
+    float* pdq = sq.n_split > 1 ? part_dq : nullptr;
+    {
+      KernelTimer timer_("dense_bwd_q", st);
+      const dim3 grid((n_q + kRowsPerBlock - 1) / kRowsPerBlock, H, sq.n_split);
+      if (dm)
+        hipLaunchKernelGGL((k_mf_bwd_q<DH, true>), grid, dim3(kBlock), 0, st,
+                           static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
+                           static_cast<const bf16_t*>(v), static_cast<const bf16_t*>(g), lse, dsum,
+                           n_q, n_k, H, scale, m, static_cast<bf16_t*>(gq), sq.split_keys, pdq);
+      else
+        hipLaunchKernelGGL((k_mf_bwd_q<DH, false>), grid, dim3(kBlock), 0, st,
+                           static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
+                           static_cast<const bf16_t*>(v), static_cast<const bf16_t*>(g), lse, dsum,
+                           n_q, n_k, H, scale, m, static_cast<bf16_t*>(gq), sq.split_keys, pdq);
+      NGT_HIP_CHECK(hipGetLastError());
+    }
+    if (pdq) {
+      KernelTimer timer_("dense_dq_combine", st);
+      const int64_t n = int64_t(n_q) * H * DH;
+      const unsigned blocks = unsigned(std::min<int64_t>((n + kBlock - 1) / kBlock, 65536));
+      hipLaunchKernelGGL(k_mf_dq_combine, dim3(blocks), dim3(kBlock), 0, st, pdq, sq.n_split, n,
+                         scale, static_cast<bf16_t*>(gq));
+      NGT_HIP_CHECK(hipGetLastError());
+    }
   }
   return NGT_OK;
 }
 
 int mfma_dense_fwd(int d, const void* q, const void* k, const void* v, int n_q, int n_k, int H,
                    float scale, const DropoutMask* dm, void* out, float* out32, float* lse,
-                   float* part, hipStream_t st) {
+                   float* part, MfSplit sp, float* part_ml, float* part_acc, hipStream_t st) {
   switch (d) {
-    case 8: return mf_fwd<8>(q, k, v, n_q, n_k, H, scale, dm, out, out32, lse, part, st);
-    case 16: return mf_fwd<16>(q, k, v, n_q, n_k, H, scale, dm, out, out32, lse, part, st);
-    case 24: return mf_fwd<24>(q, k, v, n_q, n_k, H, scale, dm, out, out32, lse, part, st);
-    case 32: return mf_fwd<32>(q, k, v, n_q, n_k, H, scale, dm, out, out32, lse, part, st);
+    case 8: return mf_fwd<8>(q, k, v, n_q, n_k, H, scale, dm, out, out32, lse, part, sp, part_ml, part_acc, st);
+    case 16: return mf_fwd<16>(q, k, v, n_q, n_k, H, scale, dm, out, out32, lse, part, sp, part_ml, part_acc, st);
+    case 24: return mf_fwd<24>(q, k, v, n_q, n_k, H, scale, dm, out, out32, lse, part, sp, part_ml, part_acc, st);
+    case 32: return mf_fwd<32>(q, k, v, n_q, n_k, H, scale, dm, out, out32, lse, part, sp, part_ml, part_acc, st);
     default: return set_error(NGT_ERR_UNSUPPORTED, "mfma dense: head_dim %d", d);
   }
 }
 
 int mfma_dense_bwd(int d, const void* q, const void* k, const void* v, const void* g,
                    const float* lse, const float* dsum, int n_q, int n_k, int H, float scale,
-                   const DropoutMask* dm, void* gq, void* gk, void* gv, hipStream_t st) {
+                   const DropoutMask* dm, void* gq, void* gk, void* gv, MfSplit sq,
+                   float* part_dq, hipStream_t st) {
   switch (d) {
-    case 8: return mf_bwd<8>(q, k, v, g, lse, dsum, n_q, n_k, H, scale, dm, gq, gk, gv, st);
-    case 16: return mf_bwd<16>(q, k, v, g, lse, dsum, n_q, n_k, H, scale, dm, gq, gk, gv, st);
-    case 24: return mf_bwd<24>(q, k, v, g, lse, dsum, n_q, n_k, H, scale, dm, gq, gk, gv, st);
-    case 32: return mf_bwd<32>(q, k, v, g, lse, dsum, n_q, n_k, H, scale, dm, gq, gk, gv, st);
+    case 8: return mf_bwd<8>(q, k, v, g, lse, dsum, n_q, n_k, H, scale, dm, gq, gk, gv, sq, part_dq, st);
+    case 16: return mf_bwd<16>(q, k, v, g, lse, dsum, n_q, n_k, H, scale, dm, gq, gk, gv, sq, part_dq, st);
+    case 24: return mf_bwd<24>(q, k, v, g, lse, dsum, n_q, n_k, H, scale, dm, gq, gk, gv, sq, part_dq, st);
+    case 32: return mf_bwd<32>(q, k, v, g, lse, dsum, n_q, n_k, H, scale, dm, gq, gk, gv, sq, part_dq, st);
     default: return set_error(NGT_ERR_UNSUPPORTED, "mfma dense: head_dim %d", d);
   }
 }

@@ -91,10 +91,16 @@ def test_dense_workspace_query_depends_on_path_and_scores():
     per-block partials only when node scores are wanted."""
     lib = _lib.load()
     fb, bb = C.c_size_t(), C.c_size_t()
-    assert lib.ngt_dense_workspace_bytes(1, 16000, 16000, 8, 8, 1, C.byref(fb), C.byref(bb)) == 0
-    assert fb.value == 8 * 16000 * 4 and bb.value >= 16000 * 8 * 4
-    assert lib.ngt_dense_workspace_bytes(1, 16000, 16000, 8, 8, 0, C.byref(fb), C.byref(bb)) == 0
+    assert lib.ngt_dense_workspace_bytes(1, 300, 300, 8, 8, 1, C.byref(fb), C.byref(bb)) == 0
+    a256 = lambda x: (x + 255) // 256 * 256
+    assert fb.value == a256(8 * 300 * 4) and bb.value >= 300 * 8 * 4
+    assert lib.ngt_dense_workspace_bytes(1, 300, 300, 8, 8, 0, C.byref(fb), C.byref(bb)) == 0
     assert fb.value == 0
+    # a large window splits its keys over blocks: the split states come on top
+    assert lib.ngt_dense_workspace_bytes(1, 16000, 16000, 8, 8, 0, C.byref(fb), C.byref(bb)) == 0
+    no_ns = fb.value
+    assert lib.ngt_dense_workspace_bytes(1, 16000, 16000, 8, 8, 1, C.byref(fb), C.byref(bb)) == 0
+    assert fb.value == no_ns + a256(8 * 16000 * 4)
     assert lib.ngt_dense_workspace_bytes(0, 500, 300, 2, 8, 1, C.byref(fb), C.byref(bb)) == 0
     with_ns = fb.value
     assert lib.ngt_dense_workspace_bytes(0, 500, 300, 2, 8, 0, C.byref(fb), C.byref(bb)) == 0

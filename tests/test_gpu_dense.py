@@ -53,6 +53,27 @@ def test_dense_parity(n_q, n_k, H, d, dtype):
         assert_parity(res[name].float(), ref[name], ref64[name], dtype, name)
 
 
+@pytest.mark.parametrize("d", [8, 16, 24, 32])
+@pytest.mark.parametrize("fwd_split,dq_split,p", [(2, 3, 0.0), (3, 2, 0.5), (4, 4, 0.0)])
+def test_dense_mfma_key_splits(monkeypatch, d, fwd_split, dq_split, p):
+    """bf16 matrix-core kernels with the keys split over blocks (forward states
+    merged by the combine, dQ partials added in split order), a ragged last
+    split, with and without dropout, against the restatement."""
+    _say(f"case dense mfma splits d={d} fwd={fwd_split} dq={dq_split} p={p}")
+    monkeypatch.setenv("NGT_MF_FWD_SPLIT", str(fwd_split))
+    monkeypatch.setenv("NGT_MF_DQ_SPLIT", str(dq_split))
+    n_q, n_k, H = 200, 2100, 2
+    q, k, v, go = _qkv(n_q, n_k, H, d, torch.bfloat16, seed=d + fwd_split)
+    seed = 0xABCD + d
+    res = _run_drop(q, k, v, go, p, seed) if p else _run(q, k, v, go)
+    mult = OA.dropout_multiplier(seed, H, n_q, n_k, p) if p else None
+    ref = OA.full_fwd_bwd(q.float(), k.float(), v.float(), go.float(), dropout_mult=mult)
+    ref64 = OA.full_fwd_bwd(q.double(), k.double(), v.double(), go.double(), dtype=torch.float64,
+                            dropout_mult=mult)
+    for name in ("x", "dq", "dk", "dv") + (("node_scores",) if not p else ()):
+        assert_parity(res[name].float(), ref[name], ref64[name], torch.bfloat16, f"split {name}")
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("n_q,n_k", [(0, 37), (45, 0)])
 def test_dense_empty_side(n_q, n_k, dtype):
