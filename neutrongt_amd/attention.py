@@ -71,22 +71,24 @@ class SparseAttentionFunction(torch.autograd.Function):
         out = torch.empty_like(q)
         rinv = torch.empty(n_q, H, dtype=torch.float32, device=dev)
         ns = torch.empty(adj.dst_end, dtype=torch.float32, device=dev)
-        fb, bb = C.c_size_t(), C.c_size_t()
-        _lib.check(lib.ngt_sparse_workspace_bytes(adj.ptr(), H, d, C.byref(fb), C.byref(bb)))
-        ws = _workspace(fb.value, dev)
+        fwd_bytes, bwd_bytes = adj.workspace_bytes(H, d)
+        ws = _workspace(fwd_bytes, dev)
         ext = k_ext is not None
         _lib.check(lib.ngt_sparse_fwd_ext(
             _dtype_code(q), q.data_ptr(), k.data_ptr(), v.data_ptr(),
             k_ext.data_ptr() if ext else None, v_ext.data_ptr() if ext else None, k.shape[0],
             adj.ptr(), H, d, scale, lo, hi, eps, out.data_ptr(), rinv.data_ptr(),
-            ns.data_ptr() if ns.numel() else None, int(ns.numel()), ws.data_ptr(), fb.value,
+            ns.data_ptr() if ns.numel() else None, int(ns.numel()), ws.data_ptr(), fwd_bytes,
             _stream(dev)))
         if ext:
             ctx.save_for_backward(q, k, v, out, rinv, k_ext, v_ext)
         else:
             ctx.save_for_backward(q, k, v, out, rinv)
-        ctx.adj, ctx.scale, ctx.lo, ctx.hi, ctx.bwd_bytes = adj, scale, lo, hi, bb.value
+        ctx.adj, ctx.scale, ctx.lo, ctx.hi, ctx.bwd_bytes = adj, scale, lo, hi, bwd_bytes
         ctx.mark_non_differentiable(ns)
+        # the node scores have no gradient: let the engine pass None for them
+        # instead of filling a zero tensor (a kernel launch per layer)
+        ctx.set_materialize_grads(False)
         return out, ns
 
     @staticmethod
@@ -94,6 +96,8 @@ class SparseAttentionFunction(torch.autograd.Function):
         saved = ctx.saved_tensors
         q, k, v, out, rinv = saved[:5]
         k_ext, v_ext = saved[5:] if len(saved) == 7 else (None, None)
+        if g_out is None:  # the output was not used by the loss
+            return None, None, None, None, None, None, None, None, None, None
         lib = _lib.load()
         n_q, H, d = q.shape
         dev = q.device
@@ -194,6 +198,7 @@ class DenseAttentionFunction(torch.autograd.Function):
             ctx.save_for_backward(q, k, v, out if out32 is None else out32, lse)
         ctx.scale, ctx.bwd_bytes, ctx.dropout_p, ctx.seed = scale, bb.value, dropout_p, seed
         ctx.mark_non_differentiable(ns)
+        ctx.set_materialize_grads(False)  # no zero tensor for the node scores' gradient
         return out, ns
 
     @staticmethod
@@ -201,6 +206,8 @@ class DenseAttentionFunction(torch.autograd.Function):
         saved = ctx.saved_tensors
         q, k, v, out, lse = saved[:5]
         seed_t = saved[5] if len(saved) == 6 else None
+        if g_out is None:
+            return None, None, None, None, None, None, None, None
         lib = _lib.load()
         n_q, H, d = q.shape
         n_k = k.shape[0]

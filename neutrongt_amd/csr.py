@@ -127,9 +127,23 @@ class WindowAdjacency:
         self.dst_end = self.info[_lib.INFO_DST_END]
         self.max_deg_q = self.info[_lib.INFO_MAX_DEG_Q]
         self.max_deg_k = self.info[_lib.INFO_MAX_DEG_K]
+        self._ptr = C.byref(self.struct)
+        self._ws_bytes = {}
 
     def ptr(self):
-        return C.byref(self.struct)
+        return self._ptr
+
+    def workspace_bytes(self, n_heads: int, head_dim: int):
+        """(forward, backward) workspace bytes of ngt_sparse_fwd/bwd for this
+        window and head shape, asked once and kept."""
+        key = (int(n_heads), int(head_dim))
+        hit = self._ws_bytes.get(key)
+        if hit is None:
+            fb, bb = C.c_size_t(), C.c_size_t()
+            _lib.check(_lib.load().ngt_sparse_workspace_bytes(self._ptr, key[0], key[1],
+                                                             C.byref(fb), C.byref(bb)))
+            hit = self._ws_bytes[key] = (fb.value, bb.value)
+        return hit
 
 
 class AdjacencyCache:

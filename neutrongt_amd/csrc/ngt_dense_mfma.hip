@@ -103,6 +103,48 @@ __device__ __forceinline__ s16x4 pack4(float a, float b, float c, float d) {
   return __builtin_bit_cast(s16x4, w);
 }
 
+// x * s as two bf16 operands hi = RNE(x s), lo = RNE(x s - hi) (the
+// difference is exact in fp32): contracting a bf16 row r against hi ++ lo
+// gives r . (x s) with products exact and a relative error of at most 2^-18
+// per term, so the softmax scale rides inside the MFMA instead of costing a
+// VALU multiply per score.
+__device__ __forceinline__ void split_scaled(s16x4 x, float s, s16x4& hi, s16x4& lo) {
+  float f[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) f[i] = bf16_to_f32(static_cast<uint16_t>(x[i])) * s;
+  hi = pack4(f[0], f[1], f[2], f[3]);
+  lo = pack4(f[0] - bf16_to_f32(static_cast<uint16_t>(hi[0])),
+             f[1] - bf16_to_f32(static_cast<uint16_t>(hi[1])),
+             f[2] - bf16_to_f32(static_cast<uint16_t>(hi[2])),
+             f[3] - bf16_to_f32(static_cast<uint16_t>(hi[3])));
+}
+
+// x as three bf16 pieces {hi, mid, lo, 0} (each the RNE of the exact fp32
+// remainder), so that hi + mid + lo carries x to fp32 precision: a per-row
+// term folded into a tile as one more MFMA K step costs no accuracy.
+__device__ __forceinline__ uint2 split3(float x) {
+  const uint16_t hi = f32_to_bf16(x);
+  const float r1 = x - bf16_to_f32(hi);
+  const uint16_t mid = f32_to_bf16(r1);
+  const float r2 = r1 - bf16_to_f32(mid);
+  return make_uint2(uint32_t(hi) | (uint32_t(mid) << 16), uint32_t(f32_to_bf16(r2)));
+}
+
+// Constant MFMA operand with ones in slots 0-2 of the lanes of half `which`:
+// against split3 pieces held by those lanes it adds hi + mid + lo.
+__device__ __forceinline__ s16x4 ones3(int half, int which) {
+  s16x4 r = zero4();
+  if (half == which) r[0] = r[1] = r[2] = static_cast<short>(0x3f80);
+  return r;
+}
+
+__device__ __forceinline__ f32x16 fill16(float v) {
+  f32x16 r;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) r[i] = v;
+  return r;
+}
+
 __device__ __forceinline__ float sum4(s16x4 x) {
   return (bf16_to_f32(static_cast<uint16_t>(x[0])) + bf16_to_f32(static_cast<uint16_t>(x[1]))) +
          (bf16_to_f32(static_cast<uint16_t>(x[2])) + bf16_to_f32(static_cast<uint16_t>(x[3])));
@@ -248,7 +290,15 @@ __global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
     qb[j] = settle(q_ok ? load4(q + (qi * H + h) * DH + 8 * j + 4 * half) : zero4());
 
   const float s2 = scale * kLog2e;  // scores in log2 units
+  // Q^T s2 as hi ++ lo operands: the MFMA yields scores already scaled, and
+  // with the accumulator input -m (m the running maximum, once one is set) it
+  // yields S s2 - m, so a tile that does not raise any column's maximum -- all
+  // but the first few -- goes straight to exp2.
+  s16x4 qhi[NC], qlo[NC];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) split_scaled(qb[j], s2, qhi[j], qlo[j]);
   float m = -INFINITY, l = 0.f;
+  f32x16 base = zero16();  // -m once m is finite
   f32x16 acc = zero16();  // O^T[c][q]: c = 8*(i/4) + 4*half + i%4
 
   // keys [k_begin, k_end) of this block's split (blockIdx.z; split_keys a
@@ -270,13 +320,14 @@ __global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
     }
     for (int sub = 0; sub < kSB / kT && kb + sub * kT < k_end; ++sub) {
       const int r0 = sub * kT;
-      // S^T tile: rows = keys kb + r0 + (8*(i/4) + 4*half + i%4), col = this lane's query.
-      f32x16 st = zero16();
+      // S^T s2 - m tile (S^T s2 before the first maximum): rows = keys
+      // kb + r0 + (8*(i/4) + 4*half + i%4), col = this lane's query.
+      f32x16 st = base;
 #pragma unroll
-      for (int j = 0; j + 1 < NC; j += 2)
-        st = mfma2(lds4(&ks[r0 + l32][8 * j + 4 * half]), lds4(&ks[r0 + l32][8 * j + 8 + 4 * half]),
-                   qb[j], qb[j + 1], st);
-      if constexpr (NC % 2) st = mfma(lds4(&ks[r0 + l32][8 * (NC - 1) + 4 * half]), qb[NC - 1], st);
+      for (int j = 0; j < NC; ++j) {
+        const s16x4 ka = lds4(&ks[r0 + l32][8 * j + 4 * half]);
+        st = mfma2(ka, ka, qhi[j], qlo[j], st);
+      }
       float mx = -INFINITY;
       if (kb + r0 + kT <= k_end) {
 #pragma unroll
@@ -288,22 +339,30 @@ __global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
           mx = fmaxf(mx, st[i]);
         }
       }
-      mx = max_halves(mx);
-      const float m_new = fmaxf(m, mx * s2);  // scale > 0: max commutes with scaling
-      const float alpha = __builtin_amdgcn_exp2f(m - m_new);
-      if (__any(alpha != 1.f)) {
+      mx = max_halves(mx);  // finite: the tile holds at least one key
+      // how far this column's maximum moves: the whole tile maximum for the
+      // first tile (m unset, base 0), else its excess over m
+      const bool first = m == -INFINITY;
+      const float up = first ? mx : fmaxf(mx, 0.f);
+      if (__any(first || up > 0.f)) {
+        const float m_new = first ? mx : m + up;
+        const float alpha = __builtin_amdgcn_exp2f(m - m_new);  // 0 for the first tile
         l *= alpha;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) acc[i] *= alpha;
+        for (int i = 0; i < 16; ++i) {
+          acc[i] *= alpha;
+          st[i] -= up;
+        }
+        m = m_new;
+        base = fill16(-m);
       }
-      m = m_new;
       s16x4 pb[4], pm[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float p0 = __builtin_amdgcn_exp2f(fmaf(st[4 * j], s2, -m_new));
-        const float p1 = __builtin_amdgcn_exp2f(fmaf(st[4 * j + 1], s2, -m_new));
-        const float p2 = __builtin_amdgcn_exp2f(fmaf(st[4 * j + 2], s2, -m_new));
-        const float p3 = __builtin_amdgcn_exp2f(fmaf(st[4 * j + 3], s2, -m_new));
+        const float p0 = __builtin_amdgcn_exp2f(st[4 * j]);
+        const float p1 = __builtin_amdgcn_exp2f(st[4 * j + 1]);
+        const float p2 = __builtin_amdgcn_exp2f(st[4 * j + 2]);
+        const float p3 = __builtin_amdgcn_exp2f(st[4 * j + 3]);
         pb[j] = pack4(p0, p1, p2, p3);
         if constexpr (DROP) {
           // keys kb + r0 + 8j + 4*half + (0..3): two key pairs, one word each
@@ -429,8 +488,9 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_kv(
   __shared__ __align__(16) short gs[kSB][DH + kRowPad];
   __shared__ __align__(16) short qt[kT][kSB + kColPad];  // rows >= DH zero
   __shared__ __align__(16) short gt[kT][kSB + kColPad];
-  __shared__ __align__(16) float ls[kSB];
-  __shared__ __align__(16) float dd[kSB];
+  // per query row: the split3 pieces of -L (log2 units), then of -D
+  __shared__ __align__(16) uint2 xr[kSB][2];
+  __shared__ __align__(16) float dd[kSB];  // -D, with dropout only
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
   const int half = lane >> 5;
@@ -446,6 +506,14 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_kv(
     vbv[j] = settle(k_ok ? load4(v + (kj * H + h) * DH + 8 * j + 4 * half) : zero4());
   }
   const float s2 = scale * kLog2e;
+  // S s2 - L and dP - D come straight out of the MFMAs: K^T s2 as hi ++ lo
+  // operands (each Q row read once, fed twice), and the query's -L and -D
+  // pieces from its LDS record as one more K step each: -L held by the lower
+  // lanes, -D by the upper ones, against constant ones on the matching half.
+  s16x4 khi[NC], klo[NC];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) split_scaled(kbv[j], s2, khi[j], klo[j]);
+  const s16x4 ones_l = ones3(half, 0), ones_d = ones3(half, 1);
   f32x16 dk = zero16(), dv = zero16();  // D[key][c]: key = 8*(i/4)+4*half+i%4, c = l32
   Stage<DH> pq, pg;
   float pl = 0.f, pd = 0.f;
@@ -470,51 +538,60 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_kv(
     pq.store_trans(qt);
     pg.store_trans(gt);
     if (threadIdx.x < kSB) {
-      ls[threadIdx.x] = pl * kLog2e;
-      dd[threadIdx.x] = pd;
+      // padded rows: -L = -1e30 (finite, so the zero slots of the D step
+      // stay 0; exp2 of the score is 0), D = 0 with zero G rows
+      const float nl = pl == INFINITY ? -1e30f : -pl * kLog2e;
+      xr[threadIdx.x][0] = split3(nl);
+      xr[threadIdx.x][1] = split3(-pd);
+      if constexpr (DROP) dd[threadIdx.x] = -pd;
     }
     __syncthreads();
     if (qb + kSB < n_q) prefetch(qb + kSB);
     for (int sub = 0; sub < kSB / kT && qb + sub * kT < n_q; ++sub) {
       const int r0 = sub * kT;
-      // S and dP tiles, rows = queries qb + r0 + 8*(i/4) + 4*half + i%4, col = this lane's key.
+      // S s2 - L and dP - D tiles (dP alone with dropout), rows = queries
+      // qb + r0 + 8*(i/4) + 4*half + i%4, col = this lane's key.
+      const s16x4 xa = __builtin_bit_cast(s16x4, xr[r0 + l32][half]);
       f32x16 st = zero16(), dp = zero16();
 #pragma unroll
-      for (int j = 0; j + 1 < NC; j += 2) {
-        st = mfma2(lds4(&qs[r0 + l32][8 * j + 4 * half]), lds4(&qs[r0 + l32][8 * j + 8 + 4 * half]),
-                   kbv[j], kbv[j + 1], st);
+      for (int j = 0; j < NC; ++j) {
+        const s16x4 qa = lds4(&qs[r0 + l32][8 * j + 4 * half]);
+        st = mfma2(qa, qa, khi[j], klo[j], st);
+      }
+      st = mfma(xa, ones_l, st);
+#pragma unroll
+      for (int j = 0; j + 1 < NC; j += 2)
         dp = mfma2(lds4(&gs[r0 + l32][8 * j + 4 * half]), lds4(&gs[r0 + l32][8 * j + 8 + 4 * half]),
                    vbv[j], vbv[j + 1], dp);
-      }
-      if constexpr (NC % 2) {
-        st = mfma(lds4(&qs[r0 + l32][8 * (NC - 1) + 4 * half]), kbv[NC - 1], st);
-        dp = mfma(lds4(&gs[r0 + l32][8 * (NC - 1) + 4 * half]), vbv[NC - 1], dp);
+      if constexpr (DROP) {
+        if constexpr (NC % 2) dp = mfma(lds4(&gs[r0 + l32][8 * (NC - 1) + 4 * half]), vbv[NC - 1], dp);
+      } else if constexpr (NC % 2) {
+        dp = mfma2(lds4(&gs[r0 + l32][8 * (NC - 1) + 4 * half]), xa, vbv[NC - 1], ones_d, dp);
+      } else {
+        dp = mfma(xa, ones_d, dp);
       }
       s16x4 pa[4], dsa[4];  // P^T and dS^T as A operands: A[key][query step row]
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int r = r0 + 8 * j + 4 * half;  // rows r .. r+3 of this K step
-        const float4 lv = *reinterpret_cast<const float4*>(&ls[r]);
-        const float4 dv4 = *reinterpret_cast<const float4*>(&dd[r]);
-        // padded rows carry ls = +inf: exp2(-inf) = 0
-        const float p0 = __builtin_amdgcn_exp2f(fmaf(st[4 * j], s2, -lv.x));
-        const float p1 = __builtin_amdgcn_exp2f(fmaf(st[4 * j + 1], s2, -lv.y));
-        const float p2 = __builtin_amdgcn_exp2f(fmaf(st[4 * j + 2], s2, -lv.z));
-        const float p3 = __builtin_amdgcn_exp2f(fmaf(st[4 * j + 3], s2, -lv.w));
+        const float p0 = __builtin_amdgcn_exp2f(st[4 * j]);
+        const float p1 = __builtin_amdgcn_exp2f(st[4 * j + 1]);
+        const float p2 = __builtin_amdgcn_exp2f(st[4 * j + 2]);
+        const float p3 = __builtin_amdgcn_exp2f(st[4 * j + 3]);
         if constexpr (DROP) {
           // this lane's key with queries qb + r .. +3: one word per element
+          const float4 dv4 = *reinterpret_cast<const float4*>(&dd[r]);  // -D
           const uint32_t qr = uint32_t(qb + r), kk = uint32_t(kj);
           const float m0 = drop_scale(dm, drop_word(dm, qr, kk), kk);
           const float m1 = drop_scale(dm, drop_word(dm, qr + 1, kk), kk);
           const float m2 = drop_scale(dm, drop_word(dm, qr + 2, kk), kk);
           const float m3 = drop_scale(dm, drop_word(dm, qr + 3, kk), kk);
           pa[j] = pack4(p0 * m0, p1 * m1, p2 * m2, p3 * m3);
-          dsa[j] = pack4(p0 * (m0 * dp[4 * j] - dv4.x), p1 * (m1 * dp[4 * j + 1] - dv4.y),
-                         p2 * (m2 * dp[4 * j + 2] - dv4.z), p3 * (m3 * dp[4 * j + 3] - dv4.w));
+          dsa[j] = pack4(p0 * fmaf(m0, dp[4 * j], dv4.x), p1 * fmaf(m1, dp[4 * j + 1], dv4.y),
+                         p2 * fmaf(m2, dp[4 * j + 2], dv4.z), p3 * fmaf(m3, dp[4 * j + 3], dv4.w));
         } else {
           pa[j] = pack4(p0, p1, p2, p3);
-          dsa[j] = pack4(p0 * (dp[4 * j] - dv4.x), p1 * (dp[4 * j + 1] - dv4.y),
-                         p2 * (dp[4 * j + 2] - dv4.z), p3 * (dp[4 * j + 3] - dv4.w));
+          dsa[j] = pack4(p0 * dp[4 * j], p1 * dp[4 * j + 1], p2 * dp[4 * j + 2], p3 * dp[4 * j + 3]);
         }
       }
       s16x4 gb[4], qbq[4];
@@ -573,6 +650,17 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_q(
   const float L2 = q_ok ? lse[int64_t(h) * n_q + qi] * kLog2e : INFINITY;
   const float Dq = q_ok ? dsum[int64_t(h) * n_q + qi] : 0.f;
   const float s2 = scale * kLog2e;
+  // S^T s2 - L and dP^T - D come straight out of the MFMAs: Q^T s2 as hi ++ lo
+  // operands (the K rows read once, fed twice), the lane's -L as the
+  // accumulator input of every S tile, and its -D pieces as one more K step
+  // of dP against constant ones.  Padded queries: -L = -inf (p = 0) and D = 0
+  // with zero G rows (dP = 0).
+  s16x4 qhi[NC], qlo[NC];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) split_scaled(qbv[j], s2, qhi[j], qlo[j]);
+  const f32x16 st0 = fill16(-L2);
+  const s16x4 ones_a = ones3(half, 0);
+  const s16x4 db = half == 0 ? __builtin_bit_cast(s16x4, split3(-Dq)) : zero4();
   f32x16 dq = zero16();  // D[q][c]: q = 8*(i/4)+4*half+i%4 (tile row), c = l32
   const int k_begin = int(blockIdx.z) * split_keys;  // this block's key split
   const int k_end = min(n_k, k_begin + split_keys);
@@ -592,36 +680,41 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_q(
     }
     for (int sub = 0; sub < kSB / kT && kb + sub * kT < k_end; ++sub) {
       const int r0 = sub * kT;
-      f32x16 st = zero16(), dp = zero16();
+      f32x16 st = st0, dp = zero16();  // -> S^T s2 - L, dP^T - D (dP^T with dropout)
 #pragma unroll
-      for (int j = 0; j + 1 < NC; j += 2) {
-        st = mfma2(lds4(&ks[r0 + l32][8 * j + 4 * half]), lds4(&ks[r0 + l32][8 * j + 8 + 4 * half]),
-                   qbv[j], qbv[j + 1], st);
+      for (int j = 0; j < NC; ++j) {
+        const s16x4 ka = lds4(&ks[r0 + l32][8 * j + 4 * half]);
+        st = mfma2(ka, ka, qhi[j], qlo[j], st);
+      }
+#pragma unroll
+      for (int j = 0; j + 1 < NC; j += 2)
         dp = mfma2(lds4(&vs[r0 + l32][8 * j + 4 * half]), lds4(&vs[r0 + l32][8 * j + 8 + 4 * half]),
                    gbv[j], gbv[j + 1], dp);
+      if constexpr (DROP) {
+        if constexpr (NC % 2) dp = mfma(lds4(&vs[r0 + l32][8 * (NC - 1) + 4 * half]), gbv[NC - 1], dp);
+      } else if constexpr (NC % 2) {
+        dp = mfma2(lds4(&vs[r0 + l32][8 * (NC - 1) + 4 * half]), ones_a, gbv[NC - 1], db, dp);
+      } else {
+        dp = mfma(ones_a, db, dp);
       }
-      if constexpr (NC % 2) {
-        st = mfma(lds4(&ks[r0 + l32][8 * (NC - 1) + 4 * half]), qbv[NC - 1], st);
-        dp = mfma(lds4(&vs[r0 + l32][8 * (NC - 1) + 4 * half]), gbv[NC - 1], dp);
-      }
-      if constexpr (DROP) {  // dP o M: keys kb + r0 + 8*(i/4) + 4*half + i%4
+      if constexpr (DROP) {  // dP o M - D: keys kb + r0 + 8*(i/4) + 4*half + i%4
 #pragma unroll
         for (int i = 0; i < 16; i += 2) {
           const uint32_t key = uint32_t(kb + r0 + 8 * (i / 4) + 4 * half + (i % 4));
           const uint32_t w = drop_word(dm, uint32_t(qi), key);
-          dp[i] *= drop_scale(dm, w, key);
-          dp[i + 1] *= drop_scale(dm, w, key + 1);
+          dp[i] = fmaf(dp[i], drop_scale(dm, w, key), -Dq);
+          dp[i + 1] = fmaf(dp[i + 1], drop_scale(dm, w, key + 1), -Dq);
         }
       }
       float ds[16];
       if (kb + r0 + kT <= k_end) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) ds[i] = __builtin_amdgcn_exp2f(fmaf(st[i], s2, -L2)) * (dp[i] - Dq);
+        for (int i = 0; i < 16; ++i) ds[i] = __builtin_amdgcn_exp2f(st[i]) * dp[i];
       } else {  // tail tile: keys past the split's end drop out
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int key = kb + r0 + 8 * (i / 4) + 4 * half + (i % 4);
-          ds[i] = key < k_end ? __builtin_amdgcn_exp2f(fmaf(st[i], s2, -L2)) * (dp[i] - Dq) : 0.f;
+          ds[i] = key < k_end ? __builtin_amdgcn_exp2f(st[i]) * dp[i] : 0.f;
         }
       }
       s16x4 dsa[4];  // dS as A operand: A[q][key step row] from the D[key][q] layout
