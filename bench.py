@@ -5,7 +5,7 @@ A step is one pass of the attention path over one synthetic window: for the
 default workload (GPH_Large: 32,768-query window + 4 related keys per query,
 H=32, d=24, bf16, 12 layers) the forward of all 12 attention layers followed by
 their backward, each layer with its own q/k/v, through the drop-in autograd
-path (SparseAttentionFunction -> libngt_attn.so).  Inputs and the window CSR
+path (window_attention: C++ autograd node -> libngt_attn.so).  Inputs and the window CSR
 are resident in HBM before timing starts (the CSR is built once per window and
 reused by every layer and step, as in the training loop).
 
@@ -562,7 +562,7 @@ def main(argv=None) -> int:
 
     from neutrongt_amd import _lib, chunk_for_heads, small_for_heads
     from neutrongt_amd import synthetic as S
-    from neutrongt_amd.attention import DenseAttentionFunction, SparseAttentionFunction
+    from neutrongt_amd.attention import DenseAttentionFunction, window_attention
     from neutrongt_amd.csr import WindowAdjacency
 
     cfg = S.CONFIGS[args.config]
@@ -631,7 +631,7 @@ def main(argv=None) -> int:
             if cfg.dense:
                 x, _ = DenseAttentionFunction.apply(q, k, v, scale, True)
             else:
-                x, _ = SparseAttentionFunction.apply(q, k, v, adj, scale, -5.0, 5.0, 1e-6)
+                x, _ = window_attention(q, k, v, adj, scale, -5.0, 5.0, 1e-6)
             outs.append(x)
             grads.append(go)
         torch.autograd.backward(outs, grads)

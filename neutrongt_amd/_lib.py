@@ -166,6 +166,39 @@ def load(path: str | os.PathLike | None = None):
         return lib
 
 
+_ext = None
+EXT_PATH = Path(__file__).resolve().parent / "ngt_autograd.so"
+
+
+def autograd_ext():
+    """The C++ autograd node of the sparse attention (ngt_autograd.so, built
+    beside the library), bound to the loaded library's entry points; None when
+    it is not built -- the Python autograd.Function then drives the same
+    library calls."""
+    global _ext
+    if _ext is not None:
+        return _ext or None
+    lib = load()
+    with _lock:
+        if _ext is None:
+            if not EXT_PATH.exists():
+                _ext = False
+            else:
+                import importlib.util
+
+                spec = importlib.util.spec_from_file_location("ngt_autograd", EXT_PATH)
+                mod = importlib.util.module_from_spec(spec)
+                spec.loader.exec_module(mod)
+                if mod.csr_struct_bytes() != C.sizeof(WindowCSR):
+                    raise RuntimeError(f"{EXT_PATH.name} was built against another "
+                                       "ngt_window_csr; rebuild it")
+                addr = lambda fn: C.cast(fn, C.c_void_p).value
+                mod.init(addr(lib.ngt_sparse_fwd_ext), addr(lib.ngt_sparse_bwd_ext),
+                         addr(lib.ngt_last_error))
+                _ext = mod
+    return _ext or None
+
+
 def stream_ptr(device) -> int:
     """hipStream_t (as an int) of torch's current stream on ``device``.
 

@@ -118,6 +118,24 @@ class SparseAttentionFunction(torch.autograd.Function):
         return gq, gk, gv, None, None, None, None, None, None, None
 
 
+def window_attention(q, k, v, adj, scale, lo=CLAMP_LO, hi=CLAMP_HI, eps=EPS, k_ext=None,
+                     v_ext=None):
+    """SparseAttentionFunction's operation over a built WindowAdjacency, run by
+    the C++ autograd node (ngt_autograd.so) when it is built -- the same
+    library calls without a Python frame or ctypes conversion per layer and
+    without the GIL on the autograd engine's device thread -- else by
+    SparseAttentionFunction.  q/k/v (and k_ext/v_ext) as that function takes
+    them: contiguous, 16-byte aligned, on the GPU."""
+    ext = _lib.autograd_ext()
+    if ext is None:
+        return SparseAttentionFunction.apply(q, k, v, adj, scale, lo, hi, eps, k_ext, v_ext)
+    H, d = q.shape[1], q.shape[2]
+    fwd_bytes, bwd_bytes = adj.workspace_bytes(H, d)
+    return ext.sparse_attention(q, k, v, k_ext, v_ext, adj.csr_bytes, adj.mem, adj.dst_end,
+                                float(scale), float(lo), float(hi), float(eps), fwd_bytes,
+                                bwd_bytes)
+
+
 def sparse_attention(q, k, v, edge_index, num_heads=None, scale=None, cache: AdjacencyCache = None,
                      lo=CLAMP_LO, hi=CLAMP_HI, eps=EPS, kv_ext=None):
     """Functional form.  q [.., N_q, H, d] -> (x [N_q, H, d], node_scores [max(dst)+1]).
@@ -154,8 +172,8 @@ def sparse_attention(q, k, v, edge_index, num_heads=None, scale=None, cache: Adj
     cache = cache or default_cache
     adj = cache.get(edge_index, q.shape[0], n_k, chunk_for_heads(H, int(edge_index.shape[-1])),
                     small_for_heads(H))
-    return SparseAttentionFunction.apply(q, k, v, adj, float(scale), float(lo), float(hi),
-                                         float(eps), k_ext, v_ext)
+    return window_attention(q, k, v, adj, float(scale), float(lo), float(hi), float(eps), k_ext,
+                            v_ext)
 
 
 # -------------------------------------------------------------------- dense

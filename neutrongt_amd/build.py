@@ -96,6 +96,31 @@ def build_library(verbose: bool = False, jobs: int | None = None, out: Path | No
     return out
 
 
+def build_autograd_ext(verbose: bool = False) -> Path:
+    """Compiles csrc/ngt_autograd.cpp (host C++: the sparse attention's
+    autograd node, see that file) as a torch extension with g++ and puts
+    ngt_autograd.so beside the library; returns its path."""
+    import torch
+    from torch.utils import cpp_extension
+
+    build_dir = BUILD / "autograd"
+    build_dir.mkdir(parents=True, exist_ok=True)
+    torch_lib = Path(torch.__file__).resolve().parent / "lib"
+    rocm = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+    cpp_extension.load(
+        name="ngt_autograd", sources=[str(CSRC / "ngt_autograd.cpp")],
+        extra_include_paths=[str(INCLUDE), str(rocm / "include")],
+        extra_cflags=["-O2", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1"],
+        extra_ldflags=[f"-L{torch_lib}", "-lc10_hip", f"-L{rocm / 'lib'}", "-lamdhip64"],
+        build_directory=str(build_dir), verbose=verbose, with_cuda=False, is_python_module=True)
+    out = PKG / "ngt_autograd.so"
+    tmp = out.with_name(out.name + ".tmp")
+    shutil.copyfile(build_dir / "ngt_autograd.so", tmp)
+    os.replace(tmp, out)
+    return out
+
+
 if __name__ == "__main__":
     path = build_library(verbose="-v" in sys.argv)
     print(path)
+    print(build_autograd_ext(verbose="-v" in sys.argv))

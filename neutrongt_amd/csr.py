@@ -11,6 +11,7 @@ layer of a window step and across epochs.
 from __future__ import annotations
 
 import ctypes as C
+import math
 import os
 from collections import OrderedDict
 
@@ -78,21 +79,24 @@ class WindowAdjacency:
         miq, msq, mik, msk = (C.c_int32() for _ in range(4))
         _lib.check(lib.ngt_csr_sizes(E, n_q, n_k, chunk, chunk, C.byref(miq), C.byref(msq),
                                      C.byref(mik), C.byref(msk)))
-        i32 = dict(dtype=torch.int32, device=dev)
-        self.rowptr = torch.empty(n_q + 1, **i32)
-        self.col = torch.empty(max(E, 1), **i32)
-        self.perm = torch.empty(max(E, 1), **i32)
-        self.t_rowptr = torch.empty(n_k + 1, **i32)
-        self.t_col = torch.empty(max(E, 1), **i32)
-        self.t_perm = torch.empty(max(E, 1), **i32)
-        self.q2t = torch.empty(max(E, 1), **i32)
-        self.items_q = torch.empty(miq.value, 4, **i32)
-        self.splits_q = torch.empty(msq.value, 4, **i32)
-        self.items_k = torch.empty(mik.value, 4, **i32)
-        self.splits_k = torch.empty(msk.value, 4, **i32)
-        self.packed_q = torch.empty(max(n_q, 1), **i32)
-        self.packed_k = torch.empty(max(n_k, 1), **i32)
-        self.info_dev = torch.zeros(_lib.INFO_LEN, **i32)
+        # every device array of the window lives in one int32 allocation
+        # (self.mem, 256-byte aligned slices), so that holding self.mem keeps
+        # all memory the ngt_window_csr points into alive
+        e1 = max(E, 1)
+        layout = (("rowptr", (n_q + 1,)), ("col", (e1,)), ("perm", (e1,)),
+                  ("t_rowptr", (n_k + 1,)), ("t_col", (e1,)), ("t_perm", (e1,)), ("q2t", (e1,)),
+                  ("items_q", (miq.value, 4)), ("splits_q", (msq.value, 4)),
+                  ("items_k", (mik.value, 4)), ("splits_k", (msk.value, 4)),
+                  ("packed_q", (max(n_q, 1),)), ("packed_k", (max(n_k, 1),)),
+                  ("info_dev", (_lib.INFO_LEN,)))
+        offs, total = [], 0
+        for _, shape in layout:
+            offs.append(total)
+            total += -(-math.prod(shape) // 64) * 64
+        self.mem = torch.empty(total, dtype=torch.int32, device=dev)
+        for (name, shape), o in zip(layout, offs):
+            setattr(self, name, self.mem[o:o + math.prod(shape)].view(shape))
+        self.info_dev.zero_()
         s = _lib.WindowCSR()
         s.n_q, s.n_k, s.n_edges, s.chunk_q, s.chunk_k = n_q, n_k, E, chunk, chunk
         s.small_q = s.small_k = small
@@ -129,6 +133,9 @@ class WindowAdjacency:
         self.max_deg_k = self.info[_lib.INFO_MAX_DEG_K]
         self._ptr = C.byref(self.struct)
         self._ws_bytes = {}
+        # the struct's bytes as a CPU tensor, for callers that keep a copy
+        # (the C++ autograd node holds it with self.mem until its backward)
+        self.csr_bytes = torch.frombuffer(bytearray(bytes(s)), dtype=torch.uint8)
 
     def ptr(self):
         return self._ptr

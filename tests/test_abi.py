@@ -153,3 +153,13 @@ def test_build_entry_compiles(tmp_path):
 
     flags = " ".join(build.HIPCC_FLAGS)
     assert "-packed-fp32-ops" in flags and "--offload-arch=gfx950" in flags
+
+
+def test_autograd_node_loads_and_matches_the_struct_without_touching_the_gpu():
+    """ngt_autograd.so (the sparse attention's C++ autograd node) loads, binds
+    to the library's entry points and was built against this header's
+    ngt_window_csr."""
+    ext = _lib.autograd_ext()
+    assert ext is not None, "ngt_autograd.so is not built"
+    assert ext.csr_struct_bytes() == C.sizeof(_lib.WindowCSR)
+    assert callable(ext.sparse_attention)
