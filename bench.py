@@ -96,8 +96,9 @@ def path_bytes(cfg, n_k: int, E: int) -> float:
 
 
 def measured_traffic(config: str, kernel: str):
-    """HBM bytes per launch of `kernel` measured with rocprofv3 counters
-    (profiles/traffic.json, calibrated against a plain device copy), or None."""
+    """Bytes per launch of `kernel` between its L2 and the fabric (MALL or
+    HBM), measured with rocprofv3 FETCH_SIZE and WRITE_SIZE (profiles/traffic.json,
+    scaled by what the same counters read for a plain device copy), or None."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(path) as f:

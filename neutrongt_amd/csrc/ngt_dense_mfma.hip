@@ -42,6 +42,7 @@ constexpr int kT = 32;                  // tile edge (rows/cols of one MFMA)
 constexpr int kRowsPerBlock = kWaves * kT;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kRebase = 8.f;  // forward: P entries stay below 2^8 (fp32 sums, bf16 operands)
 
 __device__ __forceinline__ f32x16 mfma(s16x4 a, s16x4 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(a, b, c, 0, 0, 0);
@@ -340,11 +341,15 @@ __global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
         }
       }
       mx = max_halves(mx);  // finite: the tile holds at least one key
-      // how far this column's maximum moves: the whole tile maximum for the
-      // first tile (m unset, base 0), else its excess over m
+      // The base m moves only when a column's maximum exceeds it by more
+      // than kRebase (log2 units), so scores up to 2^kRebase times the base
+      // enter P and the row sum as they are -- exact, since both share the
+      // base -- and after the first tile (m unset, base 0) a wave rebases
+      // only on a rare large jump instead of whenever any of its 32 columns
+      // finds a new maximum (most tiles).
       const bool first = m == -INFINITY;
       const float up = first ? mx : fmaxf(mx, 0.f);
-      if (__any(first || up > 0.f)) {
+      if (__any(first || up > kRebase)) {
         const float m_new = first ? mx : m + up;
         const float alpha = __builtin_amdgcn_exp2f(m - m_new);  // 0 for the first tile
         l *= alpha;
@@ -488,8 +493,9 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_kv(
   __shared__ __align__(16) short gs[kSB][DH + kRowPad];
   __shared__ __align__(16) short qt[kT][kSB + kColPad];  // rows >= DH zero
   __shared__ __align__(16) short gt[kT][kSB + kColPad];
-  // per query row: the split3 pieces of -L (log2 units), then of -D
-  __shared__ __align__(16) uint2 xr[kSB][2];
+  // per query row: the split3 pieces of -L (log2 units) in xr[0], of -D in
+  // xr[1] (half-major: a half-wave reads 32 consecutive records)
+  __shared__ __align__(16) uint2 xr[2][kSB];
   __shared__ __align__(16) float dd[kSB];  // -D, with dropout only
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
@@ -541,8 +547,8 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_kv(
       // padded rows: -L = -1e30 (finite, so the zero slots of the D step
       // stay 0; exp2 of the score is 0), D = 0 with zero G rows
       const float nl = pl == INFINITY ? -1e30f : -pl * kLog2e;
-      xr[threadIdx.x][0] = split3(nl);
-      xr[threadIdx.x][1] = split3(-pd);
+      xr[0][threadIdx.x] = split3(nl);
+      xr[1][threadIdx.x] = split3(-pd);
       if constexpr (DROP) dd[threadIdx.x] = -pd;
     }
     __syncthreads();
@@ -551,7 +557,7 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_kv(
       const int r0 = sub * kT;
       // S s2 - L and dP - D tiles (dP alone with dropout), rows = queries
       // qb + r0 + 8*(i/4) + 4*half + i%4, col = this lane's key.
-      const s16x4 xa = __builtin_bit_cast(s16x4, xr[r0 + l32][half]);
+      const s16x4 xa = __builtin_bit_cast(s16x4, xr[half][r0 + l32]);
       f32x16 st = zero16(), dp = zero16();
 #pragma unroll
       for (int j = 0; j < NC; ++j) {

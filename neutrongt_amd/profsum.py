@@ -67,8 +67,8 @@ def pmc_table(fetch_dir: str, write_dir: str, tcc_dir: str | None = None) -> str
         note = (f"calibration: 512 MiB device copy read FETCH_SIZE={f_max:.0f} KiB, "
                 f"WRITE_SIZE={w_max:.0f} KiB -> factors read x{cf:.3f}, write x{cw:.3f}")
     out = [note, "",
-           "| kernel | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM read MB (scaled) | "
-           "HBM write MB (scaled) | L2 hit |",
+           "| kernel | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | L2->fabric read MB (scaled) | "
+           "L2->fabric write MB (scaled) | L2 hit |",
            "|---|---|---|---|---|---|---|"]
     for k, c in fe.items():
         if "ngt::" not in k:
