@@ -19,10 +19,14 @@
 // recomputed as D[q][key], dV += P^T G and dK += dS^T Q with Q/G tiles staged
 // in LDS) and query-major dQ (dQ += dS K with K staged in LDS).  Column scores
 // sum_i |S| come from a separate key-major pass (S tiles again on MFMA).
+// Per-score arithmetic rides in the MFMAs: the softmax scale as a hi/lo bf16
+// pair of the per-lane operand (split_scaled), the per-query -lse, -D and the
+// forward's running maximum as accumulator inputs or as one more K step of
+// three bf16 pieces (split3), so a score costs an exponential and a pack.
 // Dropout (DROP = true): the PV-class products take P o M, M = keep/(1-p)
 // from DropoutMask; the forward's row sums still come from the unmasked P
 // (an extra MFMA per K step against a constant ones row), and the backward
-// scales dP by M before dS = P o (dP - D).
+// forms dS = P o (M dP - D) on the VALU.
 #include "ngt_common.h"
 
 #include <math.h>
