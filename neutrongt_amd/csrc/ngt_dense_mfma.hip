@@ -259,17 +259,17 @@ __device__ __forceinline__ float sum_halves(float x) {
 }
 
 // ------------------------------------------------------------------ forward
-// grid = (ceil(n_q / 128), H); wave w owns queries q0 .. q0+31.
+// One block: queries bx*128 .. +127 of head h, keys of split z; wave w owns
+// queries q0 .. q0+31.
 template <int DH, bool DROP>
-__global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
-                                                   const bf16_t* __restrict__ k,
-                                                   const bf16_t* __restrict__ v, int32_t n_q,
-                                                   int32_t n_k, int32_t H, float scale,
-                                                   DropoutMask dm, bf16_t* __restrict__ out,
-                                                   float* __restrict__ out32,
-                                                   float* __restrict__ lse, int32_t split_keys,
-                                                   float* __restrict__ part_ml,
-                                                   float* __restrict__ part_acc) {
+__device__ __forceinline__ void mf_fwd_block(int bx, int h, int z, const bf16_t* __restrict__ q,
+                                             const bf16_t* __restrict__ k,
+                                             const bf16_t* __restrict__ v, int32_t n_q,
+                                             int32_t n_k, int32_t H, float scale, DropoutMask dm,
+                                             bf16_t* __restrict__ out, float* __restrict__ out32,
+                                             float* __restrict__ lse, int32_t split_keys,
+                                             float* __restrict__ part_ml,
+                                             float* __restrict__ part_acc) {
   constexpr int NC = DH / 8;  // K chunks of the QK^T contraction
   __shared__ __align__(16) short ks[kSB][DH + kRowPad];  // K rows
   __shared__ __align__(16) short vt[kT][kSB + kColPad];  // V^T: [c][key], rows >= DH constant
@@ -277,8 +277,7 @@ __global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
   const int wave = threadIdx.x >> 6;
   const int half = lane >> 5;
   const int l32 = lane & 31;
-  const int h = blockIdx.y;
-  const int64_t qi = int64_t(blockIdx.x) * kRowsPerBlock + wave * kT + l32;
+  const int64_t qi = int64_t(bx) * kRowsPerBlock + wave * kT + l32;
   const bool q_ok = qi < n_q;
   if constexpr (DROP) dm = drop_for_head(dm, h);
   // With dropout the ones row moves out of V^T into this constant A operand
@@ -306,9 +305,9 @@ __global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
   f32x16 base = zero16();  // -m once m is finite
   f32x16 acc = zero16();  // O^T[c][q]: c = 8*(i/4) + 4*half + i%4
 
-  // keys [k_begin, k_end) of this block's split (blockIdx.z; split_keys a
+  // keys [k_begin, k_end) of this block's split (z; split_keys a
   // multiple of kSB); one split covers all keys
-  const int k_begin = int(blockIdx.z) * split_keys;
+  const int k_begin = z * split_keys;
   const int k_end = min(n_k, k_begin + split_keys);
   fill_pad_rows<DH>(vt, !DROP);
   Stage<DH> pk, pv;
@@ -413,7 +412,6 @@ __global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
   if (part_ml) {
     // this split's softmax state in natural-log units (m ln 2, l) and its
     // unnormalised O, merged in split order by k_dense_combine
-    const int64_t z = blockIdx.z;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int c = 8 * (i / 4) + 4 * half + (i % 4);
@@ -437,22 +435,22 @@ __global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
   if (half == 0) lse[int64_t(h) * n_q + qi] = n_k > 0 ? (m + __log2f(l)) * kLn2 : -INFINITY;
 }
 
-// Column scores: part[h][j] = sum_i |S[h, i, j]|.  grid = (ceil(n_k/128), H);
-// wave w owns keys k0 .. k0+31; S = Q K^T tiles with rows = queries, Q staged
-// 128 rows at a time in LDS (prefetched while the previous stage computes).
+// Column scores: part[h][j] = sum_i |S[h, i, j]|.  One block: keys
+// bx*128 .. +127 of head h; wave w owns keys k0 .. k0+31; S = Q K^T tiles
+// with rows = queries, Q staged 128 rows at a time in LDS (prefetched while
+// the previous stage computes).
 template <int DH>
-__global__ __launch_bounds__(kBlock) void k_mf_scores(const bf16_t* __restrict__ q,
-                                                      const bf16_t* __restrict__ k, int32_t n_q,
-                                                      int32_t n_k, int32_t H, float scale,
-                                                      float* __restrict__ part) {
+__device__ __forceinline__ void mf_scores_block(int bx, int h, const bf16_t* __restrict__ q,
+                                                const bf16_t* __restrict__ k, int32_t n_q,
+                                                int32_t n_k, int32_t H, float scale,
+                                                float* __restrict__ part) {
   constexpr int NC = DH / 8;
   __shared__ __align__(16) short qs[kSB][DH + kRowPad];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
   const int half = lane >> 5;
   const int l32 = lane & 31;
-  const int h = blockIdx.y;
-  const int64_t kj = int64_t(blockIdx.x) * kRowsPerBlock + wave * kT + l32;
+  const int64_t kj = int64_t(bx) * kRowsPerBlock + wave * kT + l32;
   const bool k_ok = kj < n_k;
   s16x4 kbv[NC];  // K^T as B: lane holds K[kj][8j + 4*half .. +4]
 #pragma unroll
@@ -480,6 +478,36 @@ __global__ __launch_bounds__(kBlock) void k_mf_scores(const bf16_t* __restrict__
   }
   s = sum_halves(s);
   if (k_ok && half == 0) part[int64_t(h) * n_k + kj] = s * scale;
+}
+
+// The forward and the column scores in one launch.  grid = (max(fwd_bx,
+// score_bx), H, n_split + (part ? 1 : 0)): slices z < n_split are forward
+// blocks (fwd_bx = ceil(n_q / 128)); the last slice, dispatched last, holds
+// the score blocks (score_bx = ceil(n_k / 128)).  The scores need neither the
+// softmax nor the output, so their blocks fill the CUs that the forward's
+// last, partial round of blocks leaves idle, instead of running as a launch
+// of their own after it.
+template <int DH, bool DROP>
+__global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
+                                                   const bf16_t* __restrict__ k,
+                                                   const bf16_t* __restrict__ v, int32_t n_q,
+                                                   int32_t n_k, int32_t H, float scale,
+                                                   DropoutMask dm, bf16_t* __restrict__ out,
+                                                   float* __restrict__ out32,
+                                                   float* __restrict__ lse, int32_t split_keys,
+                                                   float* __restrict__ part_ml,
+                                                   float* __restrict__ part_acc,
+                                                   int32_t n_split, int32_t fwd_bx,
+                                                   int32_t score_bx, float* __restrict__ part) {
+  const int bx = static_cast<int>(blockIdx.x), h = static_cast<int>(blockIdx.y);
+  const int z = static_cast<int>(blockIdx.z);
+  if (z == n_split) {  // block-uniform
+    if (bx < score_bx) mf_scores_block<DH>(bx, h, q, k, n_q, n_k, H, scale, part);
+    return;
+  }
+  if (bx < fwd_bx)
+    mf_fwd_block<DH, DROP>(bx, h, z, q, k, v, n_q, n_k, H, scale, dm, out, out32, lse,
+                           split_keys, part_ml, part_acc);
 }
 
 // ----------------------------------------------------------------- backward
@@ -778,12 +806,13 @@ bool mfma_dense_supported(int d) { return d == 8 || d == 16 || d == 24 || d == 3
 // 16,000 queries and 8 heads, while their registers leave room for more.
 // Splitting the keys over blockIdx.z raises the waves per SIMD; each split's
 // state is merged afterwards in split order.  Measured at 16,000 nodes, 8
-// heads, d = 8 (us per launch, splits 1 / 2 / 3 / 4): forward 406 / 375 /
-// 372 / 364 plus a 7-9 us combine; dQ 427 / 404 / 396 plus 7 us.  The gains
-// are small because the kernels are bound by vector-ALU issue (16
-// exponentials and about 40 other vector instructions per 32 x 32 tile and
-// wave), not by latency: issuing the next tile's S product ahead of the
-// current tile's softmax chain made the forward slower (406 -> 432 us).
+// heads, d = 8 with the per-score arithmetic in the MFMAs (us per launch):
+// forward 331 / 325 / 324 / 329 / 334 at 2 / 3 / 4 / 6 / 8 splits plus a
+// 7-13 us combine; dQ 348 / 337 / 334 / 332 / 335 at 1 / 2 / 3 / 4 / 6.
+// What bounds these kernels is each wave's chain MFMA -> exp -> pack -> MFMA
+// per tile with 4-5 waves per SIMD; issuing the next tile's products ahead of
+// the current tile's softmax work costs registers (one wave less per SIMD)
+// and measured slower: forward 406 -> 432 us, dK/dV 479 -> 585 us.
 // NGT_MF_FWD_SPLIT / NGT_MF_DQ_SPLIT override the count.
 static MfSplit plan_split(int n_q, int n_k, int H, int target_waves, const char* env) {
   const int64_t base = int64_t((n_q + kRowsPerBlock - 1) / kRowsPerBlock) * H * kWaves;
@@ -806,32 +835,27 @@ template <int DH>
 static int mf_fwd(const void* q, const void* k, const void* v, int n_q, int n_k, int H,
                   float scale, const DropoutMask* dm, void* out, float* out32, float* lse,
                   float* part, MfSplit sp, float* part_ml, float* part_acc, hipStream_t st) {
-  const dim3 grid((n_q + kRowsPerBlock - 1) / kRowsPerBlock, H, sp.n_split);
+  const int fwd_bx = (n_q + kRowsPerBlock - 1) / kRowsPerBlock;
+  const int score_bx = part && n_k > 0 ? (n_k + kRowsPerBlock - 1) / kRowsPerBlock : 0;
+  const dim3 grid(std::max(fwd_bx, score_bx), H, sp.n_split + (score_bx > 0 ? 1 : 0));
   float* pml = sp.n_split > 1 ? part_ml : nullptr;
   float* pacc = sp.n_split > 1 ? part_acc : nullptr;
-  {
-    KernelTimer timer_("dense_fwd", st);
-    const DropoutMask m = dm ? *dm : DropoutMask{};
-    if (dm)
-      hipLaunchKernelGGL((k_mf_fwd<DH, true>), grid, dim3(kBlock), 0, st,
-                         static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
-                         static_cast<const bf16_t*>(v), n_q, n_k, H, scale, m,
-                         static_cast<bf16_t*>(out), out32, lse, sp.split_keys, pml, pacc);
-    else
-      hipLaunchKernelGGL((k_mf_fwd<DH, false>), grid, dim3(kBlock), 0, st,
-                         static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
-                         static_cast<const bf16_t*>(v), n_q, n_k, H, scale, m,
-                         static_cast<bf16_t*>(out), out32, lse, sp.split_keys, pml, pacc);
-    NGT_HIP_CHECK(hipGetLastError());
-  }
-  if (part && n_k > 0) {
-    KernelTimer timer_("dense_scores", st);
-    const dim3 g2((n_k + kRowsPerBlock - 1) / kRowsPerBlock, H);
-    hipLaunchKernelGGL((k_mf_scores<DH>), g2, dim3(kBlock), 0, st,
-                       static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k), n_q, n_k, H,
-                       scale, part);
-    NGT_HIP_CHECK(hipGetLastError());
-  }
+  // one launch: the forward and, when wanted, the column scores
+  KernelTimer timer_("dense_fwd", st);
+  const DropoutMask m = dm ? *dm : DropoutMask{};
+  if (dm)
+    hipLaunchKernelGGL((k_mf_fwd<DH, true>), grid, dim3(kBlock), 0, st,
+                       static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
+                       static_cast<const bf16_t*>(v), n_q, n_k, H, scale, m,
+                       static_cast<bf16_t*>(out), out32, lse, sp.split_keys, pml, pacc,
+                       sp.n_split, fwd_bx, score_bx, part);
+  else
+    hipLaunchKernelGGL((k_mf_fwd<DH, false>), grid, dim3(kBlock), 0, st,
+                       static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
+                       static_cast<const bf16_t*>(v), n_q, n_k, H, scale, m,
+                       static_cast<bf16_t*>(out), out32, lse, sp.split_keys, pml, pacc,
+                       sp.n_split, fwd_bx, score_bx, part);
+  NGT_HIP_CHECK(hipGetLastError());
   return NGT_OK;
 }
 
