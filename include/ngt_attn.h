@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define NGT_ABI_VERSION 5
+#define NGT_ABI_VERSION 6
 
 #define NGT_F32 0
 #define NGT_BF16 1
@@ -207,6 +207,47 @@ int ngt_sparse_bwd_ext(int dtype, const void* q, const void* k, const void* v, c
                        int32_t n_heads, int32_t head_dim, float scale, float clamp_lo,
                        float clamp_hi, void* grad_q, void* grad_k, void* grad_v, void* workspace,
                        size_t workspace_bytes, void* stream);
+
+/*
+ * The optional per-pair bias of the sparse path.  Replaces the attn_bias term
+ * of CoreAttention.sparse_attention_bias:
+ *   NeutronGT/models/graphormer_dist_node_level.py:81-84
+ *   (twin NeutronGT/models/gt_dist_node_level_single_window.py:151-157)
+ * where a dense [1, H, N, N] bias, indexed [h, src, dst], is added to each
+ * edge's clamped score:  p_e = exp(clamp(a_e, lo, hi) + bias[h, j, i]).
+ *
+ * ngt_edge_bias_gather copies bias[h][src][dst] (fp32, element strides
+ * stride_h / stride_src / stride_dst; src < csr->n_k, dst < csr->n_q) into
+ * per-edge arrays [E, H] in both CSR orders: edge_bias_q for the query-major
+ * positions, edge_bias_t for the key-major ones.
+ * ngt_sparse_fwd_bias / ngt_sparse_bwd_bias are ngt_sparse_fwd_ext /
+ * ngt_sparse_bwd_ext with that term (edge_bias_q in the forward, edge_bias_t
+ * in the backward).  The backward also writes, when grad_edge_bias_t is not
+ * null, the score gradient of every edge in key-major order [E, H]:
+ * dp_e p_e, the bias's gradient (the clamp mask does not apply to it).
+ * ngt_edge_bias_grad adds those per pair, in key-major edge order (duplicate
+ * edges are adjacent there), and stores the sums into grad_bias[h][src][dst];
+ * entries of pairs without an edge are not written (zero them first).
+ */
+int ngt_edge_bias_gather(const ngt_window_csr* csr, int32_t n_heads, const float* bias,
+                         int64_t stride_h, int64_t stride_src, int64_t stride_dst,
+                         float* edge_bias_q, float* edge_bias_t, void* stream);
+int ngt_sparse_fwd_bias(int dtype, const void* q, const void* k, const void* v,
+                        const void* k_ext, const void* v_ext, int32_t n_k_main,
+                        const ngt_window_csr* csr, int32_t n_heads, int32_t head_dim, float scale,
+                        float clamp_lo, float clamp_hi, float eps, const float* edge_bias_q,
+                        void* out, float* rinv, float* node_score, int32_t node_score_len,
+                        void* workspace, size_t workspace_bytes, void* stream);
+int ngt_sparse_bwd_bias(int dtype, const void* q, const void* k, const void* v,
+                        const void* k_ext, const void* v_ext, int32_t n_k_main, const void* out,
+                        const void* grad_out, const float* rinv, const ngt_window_csr* csr,
+                        int32_t n_heads, int32_t head_dim, float scale, float clamp_lo,
+                        float clamp_hi, const float* edge_bias_t, float* grad_edge_bias_t,
+                        void* grad_q, void* grad_k, void* grad_v, void* workspace,
+                        size_t workspace_bytes, void* stream);
+int ngt_edge_bias_grad(const ngt_window_csr* csr, int32_t n_heads, const float* grad_edge_bias_t,
+                       float* grad_bias, int64_t stride_h, int64_t stride_src,
+                       int64_t stride_dst, void* stream);
 
 /*
  * Dense full-window attention (all pairs, no mask/bias).

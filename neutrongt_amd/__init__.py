@@ -9,8 +9,9 @@ window_attention(...)    the same over a built WindowAdjacency (C++ autograd nod
 dense_attention(...)     functional full-window attention
 WindowAdjacency          device CSR/transposed CSR/work lists of one window
 """
-from .attention import (CoreAttention, DenseAttentionFunction, SparseAttentionFunction,
-                        dense_attention, install, sparse_attention, window_attention)
+from .attention import (CoreAttention, DenseAttentionFunction, SparseAttentionBiasFunction,
+                        SparseAttentionFunction, dense_attention, install, sparse_attention,
+                        window_attention)
 from .csr import AdjacencyCache, WindowAdjacency, chunk_for_heads, default_cache, small_for_heads
 
 __all__ = [
@@ -20,6 +21,7 @@ __all__ = [
     "window_attention",
     "dense_attention",
     "SparseAttentionFunction",
+    "SparseAttentionBiasFunction",
     "DenseAttentionFunction",
     "WindowAdjacency",
     "AdjacencyCache",

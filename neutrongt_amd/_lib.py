@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libngt_attn.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 NGT_F32 = 0
 NGT_BF16 = 1
@@ -98,6 +98,12 @@ SIGNATURES = {
                            _f32, _f32, _vp, _vp, _vp, _i32, _vp, _sz, _vp],
     "ngt_sparse_bwd_ext": [_i32, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _pcsr, _i32, _i32,
                            _f32, _f32, _f32, _vp, _vp, _vp, _vp, _sz, _vp],
+    "ngt_edge_bias_gather": [_pcsr, _i32, _vp, _i64, _i64, _i64, _vp, _vp, _vp],
+    "ngt_sparse_fwd_bias": [_i32, _vp, _vp, _vp, _vp, _vp, _i32, _pcsr, _i32, _i32, _f32, _f32,
+                            _f32, _f32, _vp, _vp, _vp, _vp, _i32, _vp, _sz, _vp],
+    "ngt_sparse_bwd_bias": [_i32, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _pcsr, _i32, _i32,
+                            _f32, _f32, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
+    "ngt_edge_bias_grad": [_pcsr, _i32, _vp, _vp, _i64, _i64, _i64, _vp],
     "ngt_dense_workspace_bytes": [_i32, _i32, _i32, _i32, _i32, _i32, _psz, _psz],
     "ngt_dense_fwd": [_i32, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _f32, _u64, _vp, _vp,
                       _vp, _vp, _vp, _vp, _sz, _vp],

@@ -118,6 +118,84 @@ class SparseAttentionFunction(torch.autograd.Function):
         return gq, gk, gv, None, None, None, None, None, None, None
 
 
+class SparseAttentionBiasFunction(torch.autograd.Function):
+    """SparseAttentionFunction with the reference's optional per-pair bias
+    (attn_bias, graphormer_dist_node_level.py:81-84): ``bias`` [H, Ns, Nd]
+    fp32 on the GPU, any strides, indexed [h, src, dst] (Ns >= N_k, Nd >= N_q),
+    added to each edge's clamped score: p_e = exp(clamp(a_e) + bias[h, j, i]).
+    The bias gets a gradient when it requires one: the score gradient of each
+    edge (no clamp mask), summed over duplicate edges in a fixed order."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, bias, adj, scale, lo, hi, eps, k_ext=None, v_ext=None):
+        lib = _lib.load()
+        n_q, H, d = q.shape
+        dev = q.device
+        if (bias.dim() != 3 or bias.dtype != torch.float32 or not bias.is_cuda
+                or bias.shape[0] != H or bias.shape[1] < adj.n_k or bias.shape[2] < adj.n_q):
+            raise ValueError(f"bias must be an fp32 GPU tensor [{H}, >= {adj.n_k}, >= {adj.n_q}] "
+                             f"(indexed [h, src, dst]), got {tuple(bias.shape)} {bias.dtype}")
+        st = _stream(dev)
+        E = adj.n_edges
+        eb_q = torch.empty(max(E, 1), H, dtype=torch.float32, device=dev)
+        eb_t = torch.empty(max(E, 1), H, dtype=torch.float32, device=dev)
+        _lib.check(lib.ngt_edge_bias_gather(adj.ptr(), H, bias.data_ptr(), *bias.stride(),
+                                            eb_q.data_ptr(), eb_t.data_ptr(), st))
+        out = torch.empty_like(q)
+        rinv = torch.empty(n_q, H, dtype=torch.float32, device=dev)
+        ns = torch.empty(adj.dst_end, dtype=torch.float32, device=dev)
+        fwd_bytes, bwd_bytes = adj.workspace_bytes(H, d)
+        ws = _workspace(fwd_bytes, dev)
+        ext = k_ext is not None
+        _lib.check(lib.ngt_sparse_fwd_bias(
+            _dtype_code(q), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+            k_ext.data_ptr() if ext else None, v_ext.data_ptr() if ext else None, k.shape[0],
+            adj.ptr(), H, d, scale, lo, hi, eps, eb_q.data_ptr(), out.data_ptr(),
+            rinv.data_ptr(), ns.data_ptr() if ns.numel() else None, int(ns.numel()),
+            ws.data_ptr(), fwd_bytes, st))
+        saved = [q, k, v, out, rinv, eb_t] + ([k_ext, v_ext] if ext else [])
+        ctx.save_for_backward(*saved)
+        ctx.adj, ctx.scale, ctx.lo, ctx.hi, ctx.bwd_bytes = adj, scale, lo, hi, bwd_bytes
+        ctx.bias_shape = tuple(bias.shape)
+        ctx.mark_non_differentiable(ns)
+        ctx.set_materialize_grads(False)
+        return out, ns
+
+    @staticmethod
+    def backward(ctx, g_out, g_ns):
+        saved = ctx.saved_tensors
+        q, k, v, out, rinv, eb_t = saved[:6]
+        k_ext, v_ext = saved[6:] if len(saved) == 8 else (None, None)
+        if g_out is None:
+            return (None,) * 11
+        lib = _lib.load()
+        n_q, H, d = q.shape
+        dev = q.device
+        st = _stream(dev)
+        g = g_out.to(q.dtype)
+        if not g.is_contiguous() or g.data_ptr() % 16:
+            g = g.contiguous() if not g.is_contiguous() else g.clone()
+        gq = torch.empty_like(q)
+        gk = torch.empty_like(k)
+        gv = torch.empty_like(v)
+        want_bias = ctx.needs_input_grad[3]
+        deb = torch.empty_like(eb_t) if want_bias else None
+        ws = _workspace(ctx.bwd_bytes, dev)
+        ext = k_ext is not None
+        _lib.check(lib.ngt_sparse_bwd_bias(
+            _dtype_code(q), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+            k_ext.data_ptr() if ext else None, v_ext.data_ptr() if ext else None, k.shape[0],
+            out.data_ptr(), g.data_ptr(), rinv.data_ptr(), ctx.adj.ptr(), H, d, ctx.scale,
+            ctx.lo, ctx.hi, eb_t.data_ptr(), deb.data_ptr() if want_bias else None,
+            gq.data_ptr(), gk.data_ptr(), gv.data_ptr(), ws.data_ptr(), ctx.bwd_bytes, st))
+        gb = None
+        if want_bias:
+            gb = torch.zeros(ctx.bias_shape, dtype=torch.float32, device=dev)
+            _lib.check(lib.ngt_edge_bias_grad(ctx.adj.ptr(), H, deb.data_ptr(), gb.data_ptr(),
+                                              *gb.stride(), st))
+        return gq, gk, gv, gb, None, None, None, None, None, None, None
+
+
 def window_attention(q, k, v, adj, scale, lo=CLAMP_LO, hi=CLAMP_HI, eps=EPS, k_ext=None,
                      v_ext=None):
     """SparseAttentionFunction's operation over a built WindowAdjacency, run by
@@ -137,7 +215,7 @@ def window_attention(q, k, v, adj, scale, lo=CLAMP_LO, hi=CLAMP_HI, eps=EPS, k_e
 
 
 def sparse_attention(q, k, v, edge_index, num_heads=None, scale=None, cache: AdjacencyCache = None,
-                     lo=CLAMP_LO, hi=CLAMP_HI, eps=EPS, kv_ext=None):
+                     lo=CLAMP_LO, hi=CLAMP_HI, eps=EPS, kv_ext=None, attn_bias=None):
     """Functional form.  q [.., N_q, H, d] -> (x [N_q, H, d], node_scores [max(dst)+1]).
 
     ``edge_index`` [2, E]: row 0 = key (src) index < N_k, row 1 = query (dst)
@@ -145,6 +223,9 @@ def sparse_attention(q, k, v, edge_index, num_heads=None, scale=None, cache: Adj
     e.g. related nodes served from the cache) is also accepted.  ``kv_ext``
     = (k_r, v_r), each [R, H, d], supplies key rows N_k .. N_k+R-1 from their
     own buffers without a concatenation; they get no gradient (a detached cache).
+    ``attn_bias`` [1, H, Ns, Nd] (the reference's dense per-pair bias, indexed
+    [0, h, src, dst], Ns >= N_k and Nd >= N_q) is added to each edge's clamped
+    score and receives a gradient when it requires one.
     """
     H, d = q.shape[-2], q.shape[-1]
     if num_heads is not None and num_heads != H:
@@ -172,6 +253,16 @@ def sparse_attention(q, k, v, edge_index, num_heads=None, scale=None, cache: Adj
     cache = cache or default_cache
     adj = cache.get(edge_index, q.shape[0], n_k, chunk_for_heads(H, int(edge_index.shape[-1])),
                     small_for_heads(H))
+    if attn_bias is not None:
+        if (attn_bias.dim() != 4 or attn_bias.shape[0] != 1 or attn_bias.shape[1] != H
+                or attn_bias.shape[2] < n_k or attn_bias.shape[3] < q.shape[0]):
+            raise ValueError(f"attn_bias must be [1, {H}, >= {n_k}, >= {q.shape[0]}] "
+                             f"(indexed [0, h, src, dst]), got {tuple(attn_bias.shape)}")
+        if not attn_bias.is_cuda:
+            raise ValueError("attn_bias must be a GPU tensor")
+        bias = attn_bias[0].to(torch.float32)
+        return SparseAttentionBiasFunction.apply(q, k, v, bias, adj, float(scale), float(lo),
+                                                 float(hi), float(eps), k_ext, v_ext)
     return window_attention(q, k, v, adj, float(scale), float(lo), float(hi), float(eps), k_ext,
                             v_ext)
 
@@ -330,13 +421,11 @@ class CoreAttention(nn.Module):
 
     def sparse_attention_bias(self, q, k, v, edge_index, attn_bias, kv_ext=None):
         """graphormer_dist_node_level.py:67-98.  Returns (x [N_q, H, d], node_scores).
-        ``kv_ext`` (k_r, v_r): extra key rows after k/v, without gradient."""
-        if attn_bias is not None:
-            raise NotImplementedError(
-                "sparse attention with a dense attn_bias is not implemented (struct_enc is "
-                "False on NeutronGT's training path)")
+        ``kv_ext`` (k_r, v_r): extra key rows after k/v, without gradient.
+        ``attn_bias`` [1, H, N, N] (optional): added to each edge's clamped
+        score at [0, h, src, dst], as the reference's :81-84 does."""
         return sparse_attention(q, k, v, edge_index, num_heads=self.num_heads, scale=self.scale,
-                                cache=self.adjacency_cache, kv_ext=kv_ext)
+                                cache=self.adjacency_cache, kv_ext=kv_ext, attn_bias=attn_bias)
 
     def forward(self, q, k, v, attn_bias=None, edge_index=None, attn_type=None, mask=None,
                 pruning_mask=None, kv_ext=None):

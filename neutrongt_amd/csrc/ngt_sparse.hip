@@ -192,13 +192,13 @@ __device__ __forceinline__ bool packed_work(int64_t pw, int n_pwaves, int n_grou
   return true;
 }
 
-template <typename T, int DH, bool EXT>
+template <typename T, int DH, bool EXT, bool BIAS>
 __device__ __forceinline__ float fwd_packed(const T* __restrict__ q, const Keys<T, EXT>& kv,
                                            const int32_t* __restrict__ rowptr,
                                            const int32_t* __restrict__ col, int64_t row, int h,
                                            int H, float inv_scale, float lo, float hi, float eps,
                                            T* __restrict__ out, float* __restrict__ rinv,
-                                           float* __restrict__ zbuf) {
+                                           float* __restrict__ zbuf, const float* __restrict__ eb) {
   RowWords<T, DH> qw;
   float acc[DH];
   float z = 0.f;
@@ -215,11 +215,13 @@ __device__ __forceinline__ float fwd_packed(const T* __restrict__ q, const Keys<
   for (int e0 = beg; e0 < end; e0 += U) {
     RowWords<T, DH> kw[U], vw[U];
     int jc[U];
+    float bu[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       jc[u] = jn[u];
       if (jc[u] >= 0) {
         kv.template load_kv<DH>(jc[u], H, h, kw[u], vw[u]);
+        if constexpr (BIAS) bu[u] = eb[int64_t(e0 + u) * H + h];
       }
     }
 #pragma unroll
@@ -227,7 +229,9 @@ __device__ __forceinline__ float fwd_packed(const T* __restrict__ q, const Keys<
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (jc[u] >= 0) {
-        const float p = __expf(clampf(edge_dot<T, DH>(qw, kw[u]) * inv_scale, lo, hi));
+        float s = clampf(edge_dot<T, DH>(qw, kw[u]) * inv_scale, lo, hi);
+        if constexpr (BIAS) s += bu[u];  // the bias is added after the clamp
+        const float p = __expf(s);
         z += p;
 #pragma unroll
         for (int c = 0; c < DH; ++c) acc[c] = fmaf(p, word_elem<T, DH>(vw[u], c), acc[c]);
@@ -250,7 +254,7 @@ __device__ __forceinline__ float fwd_packed(const T* __restrict__ q, const Keys<
 // lanes and written here; split rows get theirs in the finalize.  ns is null
 // when no node scores are wanted or with several head groups (then the
 // finalize launch computes them from zbuf).
-template <typename T, int DH, bool EXT>
+template <typename T, int DH, bool EXT, bool BIAS>
 __global__ __launch_bounds__(kBlock) void k_fwd(
     const T* __restrict__ q, const Keys<T, EXT> kv,
     const int32_t* __restrict__ col, const int4* __restrict__ items, int32_t n_items,
@@ -258,7 +262,7 @@ __global__ __launch_bounds__(kBlock) void k_fwd(
     float eps, T* __restrict__ out, float* __restrict__ rinv, float* __restrict__ zbuf,
     float* __restrict__ part_acc, float* __restrict__ part_z, const int32_t* __restrict__ rowptr,
     const int32_t* __restrict__ packed, int32_t n_packed, int32_t n_pwaves,
-    float* __restrict__ ns, int32_t ns_len, int32_t xcd) {
+    float* __restrict__ ns, int32_t ns_len, int32_t xcd, const float* __restrict__ eb) {
   const int64_t gw = virtual_wave(n_items, n_pwaves, n_groups, xcd);
   if (gw < 0) return;
   if (gw >= int64_t(n_items) * n_groups) {
@@ -268,8 +272,8 @@ __global__ __launch_bounds__(kBlock) void k_fwd(
     const bool has = packed_work(gw - int64_t(n_items) * n_groups, n_pwaves, n_groups, hg, L, H,
                                  packed, n_packed, prow, ph);
     if (has)
-      z = fwd_packed<T, DH, EXT>(q, kv, rowptr, col, prow, ph, H, inv_scale, lo, hi, eps, out, rinv,
-                            zbuf);
+      z = fwd_packed<T, DH, EXT, BIAS>(q, kv, rowptr, col, prow, ph, H, inv_scale, lo, hi, eps,
+                                       out, rinv, zbuf, eb);
     if (ns) {  // all lanes take part; lanes without a row add 0
       const float zs = reduce_heads(z, L);
       if (has && ph == 0 && prow < ns_len) ns[prow] = zs / float(H);
@@ -306,6 +310,7 @@ __global__ __launch_bounds__(kBlock) void k_fwd(
     for (int t0 = 0; t0 < nb; t0 += S * U) {
       RowWords<T, DH> kw[U], vw[U];
       bool ok[U];
+      float bu[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int t = t0 + u * S + ln.slot;
@@ -313,12 +318,15 @@ __global__ __launch_bounds__(kBlock) void k_fwd(
         const int64_t j = __shfl(my_j, t < nb ? t : 0, kWave);
         if (ok[u]) {
           kv.template load_kv<DH>(j, H, h, kw[u], vw[u]);
+          if constexpr (BIAS) bu[u] = eb[int64_t(blk + t) * H + h];
         }
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         if (ok[u]) {
-          const float p = __expf(clampf(edge_dot<T, DH>(qw, kw[u]) * inv_scale, lo, hi));
+          float s = clampf(edge_dot<T, DH>(qw, kw[u]) * inv_scale, lo, hi);
+          if constexpr (BIAS) s += bu[u];  // the bias is added after the clamp
+          const float p = __expf(s);
           z += p;
 #pragma unroll
           for (int c = 0; c < DH; ++c) acc[c] = fmaf(p, word_elem<T, DH>(vw[u], c), acc[c]);
@@ -434,12 +442,13 @@ __global__ __launch_bounds__(kBlock) void k_rowstat(const T* __restrict__ out,
   }
 }
 
-template <typename T, int DH>
+template <typename T, int DH, bool BIAS>
 __device__ __forceinline__ void bwd_kv_packed(
     const T* __restrict__ q, const Keys<T>& kv,
     const T* __restrict__ g, const float2* __restrict__ rd, const int32_t* __restrict__ t_rowptr,
     const int32_t* __restrict__ t_col, int64_t row, int h, int H, float inv_scale, float lo,
-    float hi, T* __restrict__ grad_k, T* __restrict__ grad_v, float* __restrict__ ds) {
+    float hi, T* __restrict__ grad_k, T* __restrict__ grad_v, float* __restrict__ ds,
+    const float* __restrict__ eb, float* __restrict__ deb) {
   RowWords<T, DH> krw, vrw;
   float dk[DH], dv[DH];
   load_words<T, DH>(kv.template krow<DH>(row, H, h), krw);
@@ -458,6 +467,7 @@ __device__ __forceinline__ void bwd_kv_packed(
     RowWords<T, DH> qw[U], gw[U];
     float2 r[U];
     int ic[U];
+    float bu[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       ic[u] = in_[u];
@@ -466,6 +476,7 @@ __device__ __forceinline__ void bwd_kv_packed(
         load_words<T, DH>(q + (i * H + h) * DH, qw[u]);
         load_words<T, DH>(g + (i * H + h) * DH, gw[u]);
         r[u] = rd[i * H + h];
+        if constexpr (BIAS) bu[u] = eb[int64_t(e0 + u) * H + h];
       }
     }
 #pragma unroll
@@ -474,9 +485,14 @@ __device__ __forceinline__ void bwd_kv_packed(
     for (int u = 0; u < U; ++u) {
       if (ic[u] >= 0) {
         const float a = edge_dot<T, DH>(qw[u], krw) * inv_scale;
-        const float p = __expf(clampf(a, lo, hi));
+        float s = clampf(a, lo, hi);
+        if constexpr (BIAS) s += bu[u];
+        const float p = __expf(s);
         const float dp = r[u].x * edge_dot<T, DH>(gw[u], vrw) - r[u].y;
         const float da = (a >= lo && a <= hi) ? dp * p : 0.f;
+        if constexpr (BIAS) {  // the bias's gradient: the score's, without the clamp mask
+          if (deb) deb[int64_t(e0 + u) * H + h] = dp * p;
+        }
         const float pr = p * r[u].x;
 #pragma unroll
         for (int c = 0; c < DH; ++c) {
@@ -496,7 +512,7 @@ __device__ __forceinline__ void bwd_kv_packed(
 
 // Key-major pass: grad_k, grad_v of key row j and da_e for every edge of j
 // (stored at the key-major edge position for the query-major pass).
-template <typename T, int DH>
+template <typename T, int DH, bool BIAS>
 __global__ __launch_bounds__(kBlock) void k_bwd_kv(
     const T* __restrict__ q, const Keys<T> kv,
     const T* __restrict__ g, const float2* __restrict__ rd, const int32_t* __restrict__ t_col,
@@ -504,7 +520,7 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
     int32_t L, float inv_scale, float lo, float hi, T* __restrict__ grad_k,
     T* __restrict__ grad_v, float* __restrict__ ds, float* __restrict__ part_kv,
     const int32_t* __restrict__ t_rowptr, const int32_t* __restrict__ packed, int32_t n_packed,
-    int32_t n_pwaves, int32_t xcd) {
+    int32_t n_pwaves, int32_t xcd, const float* __restrict__ eb, float* __restrict__ deb) {
   const int64_t gw0 = virtual_wave(n_items, n_pwaves, n_groups, xcd);
   if (gw0 < 0) return;
   if (gw0 >= int64_t(n_items) * n_groups) {
@@ -512,8 +528,8 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
     int ph;
     if (packed_work(gw0 - int64_t(n_items) * n_groups, n_pwaves, n_groups, hg, L, H, packed,
                     n_packed, prow, ph))
-      bwd_kv_packed<T, DH>(q, kv, g, rd, t_rowptr, t_col, prow, ph, H, inv_scale, lo, hi,
-                           grad_k, grad_v, ds);
+      bwd_kv_packed<T, DH, BIAS>(q, kv, g, rd, t_rowptr, t_col, prow, ph, H, inv_scale, lo, hi,
+                                 grad_k, grad_v, ds, eb, deb);
     return;
   }
   int item;
@@ -548,6 +564,7 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
       RowWords<T, DH> qw[U], gw[U];
       float2 r[U];
       bool ok[U];
+      float bu[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int t = t0 + u * S + ln.slot;
@@ -557,6 +574,7 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
           load_words<T, DH>(q + (i * H + h) * DH, qw[u]);
           load_words<T, DH>(g + (i * H + h) * DH, gw[u]);
           r[u] = rd[i * H + h];
+          if constexpr (BIAS) bu[u] = eb[int64_t(blk + t) * H + h];
         }
       }
 #pragma unroll
@@ -564,9 +582,14 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
         if (ok[u]) {
           // rows stay packed; elements are unpacked at each use
           const float a = edge_dot<T, DH>(qw[u], krw) * inv_scale;
-          const float p = __expf(clampf(a, lo, hi));
+          float s = clampf(a, lo, hi);
+          if constexpr (BIAS) s += bu[u];
+          const float p = __expf(s);
           const float dp = r[u].x * edge_dot<T, DH>(gw[u], vrw) - r[u].y;
           const float da = (a >= lo && a <= hi) ? dp * p : 0.f;
+          if constexpr (BIAS) {  // the bias's gradient: the score's, without the clamp mask
+            if (deb) deb[int64_t(blk + t0 + u * S + ln.slot) * H + h] = dp * p;
+          }
           const float pr = p * r[u].x;
 #pragma unroll
           for (int c = 0; c < DH; ++c) {
@@ -903,7 +926,7 @@ template <typename T, int DH>
 int launch_fwd(const ngt_window_csr* c, const void* q, const void* k, const void* v,
                const void* k_ext, const void* v_ext, int64_t n_main, int H, float inv_scale,
                float lo, float hi, float eps, void* out, float* rinv, float* ns, int ns_len,
-               char* ws, hipStream_t st) {
+               char* ws, hipStream_t st, const float* eb) {
   const int hg = heads_per_pass(H, 0);
   const int groups = (H + hg - 1) / hg;
   const int L = lanes_for(hg);
@@ -918,19 +941,24 @@ int launch_fwd(const ngt_window_csr* c, const void* q, const void* k, const void
   float* ns_direct = groups == 1 && ns && ns_len > 0 ? ns : nullptr;
   if (blocks_q > 0) {
     KernelTimer timer_("sparse_fwd", st);
-    auto launch = [&](auto ext) {
+    auto launch = [&](auto ext, auto bias) {
       constexpr bool E = decltype(ext)::value;
-      hipLaunchKernelGGL((k_fwd<T, DH, E>), dim3(blocks_q), dim3(kBlock), 0, st,
+      constexpr bool B = decltype(bias)::value;
+      hipLaunchKernelGGL((k_fwd<T, DH, E, B>), dim3(blocks_q), dim3(kBlock), 0, st,
                          static_cast<const T*>(q), make_keys<T, DH, E>(k, v, k_ext, v_ext, n_main, H),
                          c->col, reinterpret_cast<const int4*>(c->items_q), c->n_items_q, groups,
                          hg, H, L, inv_scale, lo, hi, eps, static_cast<T*>(out), rinv, zbuf,
                          part_acc, part_z, c->rowptr, c->packed_q, c->n_packed_q, pw_q,
-                         ns_direct, ns_len, xcd);
+                         ns_direct, ns_len, xcd, eb);
     };
-    if (n_main < c->n_k)
-      launch(std::true_type{});
-    else
-      launch(std::false_type{});
+    const bool ext = n_main < c->n_k;
+    if (eb) {
+      if (ext) launch(std::true_type{}, std::true_type{});
+      else launch(std::false_type{}, std::true_type{});
+    } else {
+      if (ext) launch(std::true_type{}, std::false_type{});
+      else launch(std::false_type{}, std::false_type{});
+    }
     NGT_HIP_CHECK(hipGetLastError());
   }
   // Split rows' finalize; with several head groups the node scores of the
@@ -955,7 +983,8 @@ template <typename T, int DH>
 int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void* v,
                const void* k_ext, const void* v_ext, int64_t n_main, const void* out,
                const void* g, const float* rinv, int H, float inv_scale, float lo, float hi,
-               void* gq, void* gk, void* gv, char* ws, hipStream_t st) {
+               void* gq, void* gk, void* gv, char* ws, hipStream_t st, const float* eb,
+               float* deb) {
   const BwdLayout lay = bwd_layout(c, H, DH);
   float2* rd = reinterpret_cast<float2*>(ws + lay.rd);
   float* ds = reinterpret_cast<float*>(ws + lay.ds);
@@ -978,12 +1007,19 @@ int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void
   const unsigned blocks_k = edge_blocks(c->n_items_k, pw_k, groups, xcd);
   if (blocks_k > 0) {
     KernelTimer timer_("sparse_bwd_kv", st);
-    hipLaunchKernelGGL((k_bwd_kv<T, DH>), dim3(blocks_k), dim3(kBlock), 0, st,
-                       static_cast<const T*>(q), make_keys<T, DH>(k, v, k_ext, v_ext, n_main, H),
-                       static_cast<const T*>(g), rd, c->t_col,
-                       reinterpret_cast<const int4*>(c->items_k), c->n_items_k, groups, hg, H, L,
-                       inv_scale, lo, hi, static_cast<T*>(gk), static_cast<T*>(gv), ds, part_kv,
-                       c->t_rowptr, c->packed_k, c->n_packed_k, pw_k, xcd);
+    auto launch = [&](auto bias) {
+      constexpr bool B = decltype(bias)::value;
+      hipLaunchKernelGGL((k_bwd_kv<T, DH, B>), dim3(blocks_k), dim3(kBlock), 0, st,
+                         static_cast<const T*>(q), make_keys<T, DH>(k, v, k_ext, v_ext, n_main, H),
+                         static_cast<const T*>(g), rd, c->t_col,
+                         reinterpret_cast<const int4*>(c->items_k), c->n_items_k, groups, hg, H,
+                         L, inv_scale, lo, hi, static_cast<T*>(gk), static_cast<T*>(gv), ds,
+                         part_kv, c->t_rowptr, c->packed_k, c->n_packed_k, pw_k, xcd, eb, deb);
+    };
+    if (eb)
+      launch(std::true_type{});
+    else
+      launch(std::false_type{});
     NGT_HIP_CHECK(hipGetLastError());
   }
   hg = heads_per_pass(H, 2);
@@ -1021,6 +1057,67 @@ int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void
     NGT_HIP_CHECK(hipGetLastError());
   }
   return NGT_OK;
+}
+
+// ------------------------------------- dense per-pair bias <-> per-edge bias
+// The reference's optional attn_bias is a dense [H, N, N] term indexed
+// [h, src, dst] and added to each edge's clamped score
+// (graphormer_dist_node_level.py:81-84).  The kernels read it per edge in CSR
+// order: eb_q[pos][h] for the query-major edge at pos and eb_t[q2t[pos]][h]
+// for its key-major position.  One thread per query-major edge; its row
+// (query) is the largest r with rowptr[r] <= pos.
+__device__ __forceinline__ int32_t row_of(const int32_t* __restrict__ rowptr, int32_t n_rows,
+                                          int64_t pos) {
+  int32_t lo = 0, hi = n_rows;  // rowptr[lo] <= pos < rowptr[hi]
+  while (hi - lo > 1) {
+    const int32_t mid = lo + (hi - lo) / 2;
+    if (rowptr[mid] <= pos)
+      lo = mid;
+    else
+      hi = mid;
+  }
+  return lo;
+}
+
+__global__ __launch_bounds__(kBlock) void k_edge_bias_gather(
+    const int32_t* __restrict__ rowptr, int32_t n_q, const int32_t* __restrict__ col,
+    const int32_t* __restrict__ q2t, int64_t n_edges, int32_t H, const float* __restrict__ bias,
+    int64_t sh, int64_t ss, int64_t sd, float* __restrict__ eb_q, float* __restrict__ eb_t) {
+  for (int64_t pos = int64_t(blockIdx.x) * kBlock + threadIdx.x; pos < n_edges;
+       pos += int64_t(gridDim.x) * kBlock) {
+    const int64_t dst = row_of(rowptr, n_q, pos);
+    const int64_t src = col[pos];
+    const int64_t tp = q2t[pos];
+    for (int h = 0; h < H; ++h) {
+      const float b = bias[h * sh + src * ss + dst * sd];
+      eb_q[pos * H + h] = b;
+      eb_t[tp * H + h] = b;
+    }
+  }
+}
+
+// Gradient of the dense bias: grad[h, src, dst] = the sum of deb_t over the
+// edges (src -> dst), added in key-major order (edges with the same pair are
+// adjacent there); pairs without an edge are left as they are.  One thread
+// per key-major edge; the first edge of each pair's run writes the sum.
+__global__ __launch_bounds__(kBlock) void k_edge_bias_grad(
+    const int32_t* __restrict__ t_rowptr, int32_t n_k, const int32_t* __restrict__ t_col,
+    int64_t n_edges, int32_t H, const float* __restrict__ deb_t, float* __restrict__ grad,
+    int64_t sh, int64_t ss, int64_t sd) {
+  for (int64_t t = int64_t(blockIdx.x) * kBlock + threadIdx.x; t < n_edges;
+       t += int64_t(gridDim.x) * kBlock) {
+    const int32_t key = row_of(t_rowptr, n_k, t);
+    const int32_t qi = t_col[t];
+    const int64_t beg = t_rowptr[key], end = t_rowptr[key + 1];
+    if (t > beg && t_col[t - 1] == qi) continue;  // not the first edge of its pair
+    int64_t last = t + 1;
+    while (last < end && t_col[last] == qi) ++last;
+    for (int h = 0; h < H; ++h) {
+      float a = 0.f;
+      for (int64_t u = t; u < last; ++u) a += deb_t[u * H + h];
+      grad[h * sh + int64_t(key) * ss + int64_t(qi) * sd] = a;
+    }
+  }
 }
 
 template <template <typename, int> class F, typename... Args>
@@ -1071,13 +1168,12 @@ extern "C" int ngt_sparse_workspace_bytes(const ngt_window_csr* csr, int32_t n_h
   return NGT_OK;
 }
 
-extern "C" int ngt_sparse_fwd_ext(int dtype, const void* q, const void* k, const void* v,
-                                  const void* k_ext, const void* v_ext, int32_t n_k_main,
-                                  const ngt_window_csr* csr, int32_t n_heads, int32_t head_dim,
-                                  float scale, float clamp_lo, float clamp_hi, float eps,
-                                  void* out, float* rinv, float* node_score,
-                                  int32_t node_score_len, void* workspace,
-                                  size_t workspace_bytes, void* stream) {
+static int sparse_fwd(int dtype, const void* q, const void* k, const void* v, const void* k_ext,
+                      const void* v_ext, int32_t n_k_main, const ngt_window_csr* csr,
+                      int32_t n_heads, int32_t head_dim, float scale, float clamp_lo,
+                      float clamp_hi, float eps, const float* edge_bias, void* out, float* rinv,
+                      float* node_score, int32_t node_score_len, void* workspace,
+                      size_t workspace_bytes, void* stream) {
   int rc = check_common("ngt_sparse_fwd", dtype, csr, n_heads, head_dim);
   if (rc != NGT_OK) return rc;
   if (!(scale > 0.f)) return set_error(NGT_ERR_ARG, "ngt_sparse_fwd: scale must be > 0");
@@ -1098,7 +1194,33 @@ extern "C" int ngt_sparse_fwd_ext(int dtype, const void* q, const void* k, const
   return dispatch<FwdOp>(dtype, head_dim, csr, q, k, v, k_ext, v_ext, int64_t(n_k_main),
                          int(n_heads), 1.0f / scale, clamp_lo, clamp_hi, eps, out, rinv,
                          node_score, int(node_score_len), static_cast<char*>(workspace),
-                         static_cast<hipStream_t>(stream));
+                         static_cast<hipStream_t>(stream), edge_bias);
+}
+
+extern "C" int ngt_sparse_fwd_ext(int dtype, const void* q, const void* k, const void* v,
+                                  const void* k_ext, const void* v_ext, int32_t n_k_main,
+                                  const ngt_window_csr* csr, int32_t n_heads, int32_t head_dim,
+                                  float scale, float clamp_lo, float clamp_hi, float eps,
+                                  void* out, float* rinv, float* node_score,
+                                  int32_t node_score_len, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  return sparse_fwd(dtype, q, k, v, k_ext, v_ext, n_k_main, csr, n_heads, head_dim, scale,
+                    clamp_lo, clamp_hi, eps, nullptr, out, rinv, node_score, node_score_len,
+                    workspace, workspace_bytes, stream);
+}
+
+extern "C" int ngt_sparse_fwd_bias(int dtype, const void* q, const void* k, const void* v,
+                                   const void* k_ext, const void* v_ext, int32_t n_k_main,
+                                   const ngt_window_csr* csr, int32_t n_heads, int32_t head_dim,
+                                   float scale, float clamp_lo, float clamp_hi, float eps,
+                                   const float* edge_bias, void* out, float* rinv,
+                                   float* node_score, int32_t node_score_len, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+  if (csr && csr->n_edges > 0 && !edge_bias)
+    return set_error(NGT_ERR_ARG, "ngt_sparse_fwd_bias: null edge_bias");
+  return sparse_fwd(dtype, q, k, v, k_ext, v_ext, n_k_main, csr, n_heads, head_dim, scale,
+                    clamp_lo, clamp_hi, eps, csr && csr->n_edges > 0 ? edge_bias : nullptr, out,
+                    rinv, node_score, node_score_len, workspace, workspace_bytes, stream);
 }
 
 extern "C" int ngt_sparse_fwd(int dtype, const void* q, const void* k, const void* v,
@@ -1112,13 +1234,13 @@ extern "C" int ngt_sparse_fwd(int dtype, const void* q, const void* k, const voi
                             node_score_len, workspace, workspace_bytes, stream);
 }
 
-extern "C" int ngt_sparse_bwd_ext(int dtype, const void* q, const void* k, const void* v,
-                                  const void* k_ext, const void* v_ext, int32_t n_k_main,
-                                  const void* out, const void* grad_out, const float* rinv,
-                                  const ngt_window_csr* csr, int32_t n_heads, int32_t head_dim,
-                                  float scale, float clamp_lo, float clamp_hi, void* grad_q,
-                                  void* grad_k, void* grad_v, void* workspace,
-                                  size_t workspace_bytes, void* stream) {
+static int sparse_bwd(int dtype, const void* q, const void* k, const void* v, const void* k_ext,
+                      const void* v_ext, int32_t n_k_main, const void* out, const void* grad_out,
+                      const float* rinv, const ngt_window_csr* csr, int32_t n_heads,
+                      int32_t head_dim, float scale, float clamp_lo, float clamp_hi,
+                      const float* edge_bias_t, float* grad_edge_bias_t, void* grad_q,
+                      void* grad_k, void* grad_v, void* workspace, size_t workspace_bytes,
+                      void* stream) {
   int rc = check_common("ngt_sparse_bwd", dtype, csr, n_heads, head_dim);
   if (rc != NGT_OK) return rc;
   if (!(scale > 0.f)) return set_error(NGT_ERR_ARG, "ngt_sparse_bwd: scale must be > 0");
@@ -1137,7 +1259,77 @@ extern "C" int ngt_sparse_bwd_ext(int dtype, const void* q, const void* k, const
   return dispatch<BwdOp>(dtype, head_dim, csr, q, k, v, k_ext, v_ext, int64_t(n_k_main), out,
                          grad_out, rinv, int(n_heads), 1.0f / scale, clamp_lo, clamp_hi, grad_q,
                          grad_k, grad_v, static_cast<char*>(workspace),
-                         static_cast<hipStream_t>(stream));
+                         static_cast<hipStream_t>(stream), edge_bias_t, grad_edge_bias_t);
+}
+
+extern "C" int ngt_sparse_bwd_ext(int dtype, const void* q, const void* k, const void* v,
+                                  const void* k_ext, const void* v_ext, int32_t n_k_main,
+                                  const void* out, const void* grad_out, const float* rinv,
+                                  const ngt_window_csr* csr, int32_t n_heads, int32_t head_dim,
+                                  float scale, float clamp_lo, float clamp_hi, void* grad_q,
+                                  void* grad_k, void* grad_v, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
+  return sparse_bwd(dtype, q, k, v, k_ext, v_ext, n_k_main, out, grad_out, rinv, csr, n_heads,
+                    head_dim, scale, clamp_lo, clamp_hi, nullptr, nullptr, grad_q, grad_k,
+                    grad_v, workspace, workspace_bytes, stream);
+}
+
+extern "C" int ngt_sparse_bwd_bias(int dtype, const void* q, const void* k, const void* v,
+                                   const void* k_ext, const void* v_ext, int32_t n_k_main,
+                                   const void* out, const void* grad_out, const float* rinv,
+                                   const ngt_window_csr* csr, int32_t n_heads, int32_t head_dim,
+                                   float scale, float clamp_lo, float clamp_hi,
+                                   const float* edge_bias_t, float* grad_edge_bias_t,
+                                   void* grad_q, void* grad_k, void* grad_v, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+  if (csr && csr->n_edges > 0 && !edge_bias_t)
+    return set_error(NGT_ERR_ARG, "ngt_sparse_bwd_bias: null edge_bias_t");
+  const bool any = csr && csr->n_edges > 0;
+  return sparse_bwd(dtype, q, k, v, k_ext, v_ext, n_k_main, out, grad_out, rinv, csr, n_heads,
+                    head_dim, scale, clamp_lo, clamp_hi, any ? edge_bias_t : nullptr,
+                    any ? grad_edge_bias_t : nullptr, grad_q, grad_k, grad_v, workspace,
+                    workspace_bytes, stream);
+}
+
+static unsigned edge_grid(int64_t n) {
+  return unsigned(std::min<int64_t>((n + kBlock - 1) / kBlock, 1 << 16));
+}
+
+extern "C" int ngt_edge_bias_gather(const ngt_window_csr* csr, int32_t n_heads, const float* bias,
+                                    int64_t stride_h, int64_t stride_src, int64_t stride_dst,
+                                    float* edge_bias_q, float* edge_bias_t, void* stream) {
+  int rc = check_common("ngt_edge_bias_gather", NGT_F32, csr, n_heads, 8);
+  if (rc != NGT_OK) return rc;
+  if (csr->n_edges == 0) return NGT_OK;
+  if (!bias || !edge_bias_q || !edge_bias_t)
+    return set_error(NGT_ERR_ARG, "ngt_edge_bias_gather: null pointer");
+  if (stride_h < 0 || stride_src < 0 || stride_dst < 0)
+    return set_error(NGT_ERR_ARG, "ngt_edge_bias_gather: negative stride");
+  hipLaunchKernelGGL(k_edge_bias_gather, dim3(edge_grid(csr->n_edges)), dim3(kBlock), 0,
+                     static_cast<hipStream_t>(stream), csr->rowptr, csr->n_q, csr->col, csr->q2t,
+                     csr->n_edges, n_heads, bias, stride_h, stride_src, stride_dst, edge_bias_q,
+                     edge_bias_t);
+  NGT_HIP_CHECK(hipGetLastError());
+  return NGT_OK;
+}
+
+extern "C" int ngt_edge_bias_grad(const ngt_window_csr* csr, int32_t n_heads,
+                                  const float* grad_edge_bias_t, float* grad_bias,
+                                  int64_t stride_h, int64_t stride_src, int64_t stride_dst,
+                                  void* stream) {
+  int rc = check_common("ngt_edge_bias_grad", NGT_F32, csr, n_heads, 8);
+  if (rc != NGT_OK) return rc;
+  if (csr->n_edges == 0) return NGT_OK;
+  if (!grad_edge_bias_t || !grad_bias)
+    return set_error(NGT_ERR_ARG, "ngt_edge_bias_grad: null pointer");
+  if (stride_h < 0 || stride_src < 0 || stride_dst < 0)
+    return set_error(NGT_ERR_ARG, "ngt_edge_bias_grad: negative stride");
+  hipLaunchKernelGGL(k_edge_bias_grad, dim3(edge_grid(csr->n_edges)), dim3(kBlock), 0,
+                     static_cast<hipStream_t>(stream), csr->t_rowptr, csr->n_k, csr->t_col,
+                     csr->n_edges, n_heads, grad_edge_bias_t, grad_bias, stride_h, stride_src,
+                     stride_dst);
+  NGT_HIP_CHECK(hipGetLastError());
+  return NGT_OK;
 }
 
 extern "C" int ngt_sparse_bwd(int dtype, const void* q, const void* k, const void* v,

@@ -239,11 +239,14 @@ def full_attention_fp64(q, k, v, scale=None, dropout_mult=None):
 
 
 # --------------------------------------------------------- autograd wrappers
-def sparse_fwd_bwd(q, k, v, edge_index, grad_x, num_heads, dtype=torch.float32):
+def sparse_fwd_bwd(q, k, v, edge_index, grad_x, num_heads, dtype=torch.float32, attn_bias=None):
     """Runs the restatement forward + autograd backward on CPU in ``dtype``.
 
     q [N_q,H,d], k/v [N_k,H,d] (any float dtype; cast to ``dtype``), grad_x
-    [N_q,H,d].  Returns dict(x [N_q,H,d], node_scores, dq, dk, dv).
+    [N_q,H,d].  Returns dict(x [N_q,H,d], node_scores, dq, dk, dv).  With
+    ``attn_bias`` [H, N_k, N_q] (indexed [h, src, dst]) the reference's square
+    [1, H, N, N] bias is that block zero-padded, and the dict also holds
+    dbias [H, N_k, N_q].
     """
     n_q = q.shape[0]
     n_k = k.shape[0]
@@ -256,18 +259,26 @@ def sparse_fwd_bwd(q, k, v, edge_index, grad_x, num_heads, dtype=torch.float32):
     vf[:n_k] = v.to(dtype)
     for t in (qf, kf, vf):
         t.requires_grad_(True)
+    ab = None
+    if attn_bias is not None:
+        ab = torch.zeros(1, num_heads, n, n, dtype=dtype)
+        ab[0, :, :n_k, :n_q] = attn_bias.to(dtype)
+        ab.requires_grad_(True)
     x, ns = sparse_attention_bias(qf.unsqueeze(0), kf.unsqueeze(0), vf.unsqueeze(0), edge_index,
-                                  num_heads)
+                                  num_heads, attn_bias=ab)
     g = torch.zeros_like(x)
     g[:n_q] = grad_x.to(dtype)
     x.backward(g)
-    return {
+    res = {
         "x": x.detach()[:n_q],
         "node_scores": ns.detach(),
         "dq": qf.grad[:n_q],
         "dk": kf.grad[:n_k],
         "dv": vf.grad[:n_k],
     }
+    if ab is not None:
+        res["dbias"] = ab.grad[0, :, :n_k, :n_q]
+    return res
 
 
 def full_fwd_bwd(q, k, v, grad_x, dtype=torch.float32, dropout_mult=None, flash=False):

@@ -286,3 +286,54 @@ def test_dropout_is_unbiased_and_matches_fp64():
     # gives mean 0.095, so the bounds separate the two
     assert (mean - base).abs().max().item() < 0.3
     assert (mean - base).abs().mean().item() < 0.06
+
+
+def test_sparse_bias_added_after_clamp_and_its_gradient():
+    """The optional per-pair bias (graphormer_dist_node_level.py:81-84): a
+    dense [1, H, N, N] tensor indexed [0, h, src, dst] and added to each
+    edge's score after the clamp.  Worked with explicit float64 loops on a
+    3-node window with a duplicate edge and a clamped edge: the output, the
+    bias's gradient (the score gradient of every edge, not masked by the
+    clamp, summed over the duplicate pair) and dQ (masked by the clamp).
+    bias[0, 1, 0] != bias[0, 0, 1], so a transposed index fails."""
+    H, d, n = 1, 2, 3
+    src = np.array([0, 1, 1, 2, 0])
+    dst = np.array([0, 0, 0, 0, 1])
+    q = np.array([[[1.0, 0.5]], [[0.25, -1.0]], [[0.0, 0.0]]])           # [n, H, d]
+    k = np.array([[[0.5, 1.0]], [[8.0, 6.0]], [[-1.0, 0.5]]])            # key 1: a > 5 at query 0
+    v = np.array([[[1.0, 2.0]], [[-1.0, 0.5]], [[0.25, -2.0]]])
+    g = np.array([[[0.5, -1.0]], [[2.0, 1.0]], [[0.0, 0.0]]])
+    bias = np.zeros((H, n, n))
+    bias[0, 1, 0], bias[0, 0, 1], bias[0, 0, 0], bias[0, 2, 0] = 0.3, -0.7, 0.1, -0.2
+    sq = math.sqrt(d)
+    a = np.array([k[j, 0] @ q[i, 0] / sq for j, i in zip(src, dst)])
+    assert a[1] > 5 and a[2] > 5
+    s = np.clip(a, -5.0, 5.0) + np.array([bias[0, j, i] for j, i in zip(src, dst)])
+    p = np.exp(s)
+    Z = np.zeros(n)
+    x = np.zeros((n, d))
+    for e, (j, i) in enumerate(zip(src, dst)):
+        Z[i] += p[e]
+        x[i] += p[e] * v[j, 0]
+    x = x / (Z + 1e-6)[:, None]
+    r = 1.0 / (Z + 1e-6)
+    D = np.array([g[i, 0] @ x[i] for i in range(n)])
+    dscore = np.array([p[e] * r[i] * (g[i, 0] @ v[j, 0] - D[i]) for e, (j, i) in enumerate(zip(src, dst))])
+    dbias = np.zeros((H, n, n))
+    for e, (j, i) in enumerate(zip(src, dst)):
+        dbias[0, j, i] += dscore[e]
+    da = np.where((a >= -5) & (a <= 5), dscore, 0.0)
+    dq = np.zeros((n, d))
+    for e, (j, i) in enumerate(zip(src, dst)):
+        dq[i] += da[e] * k[j, 0] / sq
+    ei = torch.from_numpy(np.stack([src, dst]))
+    T = lambda t: torch.from_numpy(t)
+    ref = OA.sparse_fwd_bwd(T(q), T(k), T(v), ei, T(g), H, dtype=torch.float64, attn_bias=T(bias))
+    np.testing.assert_allclose(ref["x"][:, 0].numpy(), x, rtol=1e-12, atol=1e-14)
+    np.testing.assert_allclose(ref["dbias"].numpy(), dbias, rtol=1e-12, atol=1e-14)
+    np.testing.assert_allclose(ref["dq"][:, 0].numpy(), dq, rtol=1e-12, atol=1e-14)
+    assert dbias[0, 1, 0] != 0.0  # the clamped duplicate pair still passes gradient to its bias
+    # the same with the bias transposed differs
+    bad = OA.sparse_fwd_bwd(T(q), T(k), T(v), ei, T(g), H, dtype=torch.float64,
+                            attn_bias=T(bias.transpose(0, 2, 1).copy()))
+    assert np.abs(bad["x"][:, 0].numpy() - x).max() > 1e-3
