@@ -250,6 +250,38 @@ int ngt_edge_bias_grad(const ngt_window_csr* csr, int32_t n_heads, const float* 
                        int64_t stride_dst, void* stream);
 
 /*
+ * Dense attention with the reference's optional terms, in its materialized
+ * form.  Replaces the attn_bias / pruning_mask / mask lines of
+ * CoreAttention.full_attention:
+ *   NeutronGT/models/graphormer_dist_node_level.py:51-58
+ *   (twin NeutronGT/models/gt_dist_node_level_single_window.py:80-97)
+ * with the products S = Q K^T, O = (P o M) V, G V^T, (P o M)^T G, dS K and
+ * dS^T Q left to library GEMMs; all arrays fp32 and contiguous, [H, n_q, n_k]
+ * unless stated.
+ * ngt_dense_bias_softmax_fwd: z = mask[i][j] ? -1e9 : s * scale + bias
+ *   (bias nullable: the sum of attn_bias and pruning_mask; mask nullable,
+ *   uint8 [n_q, n_k], nonzero = filled); p = softmax_j(z); pd = p o M with
+ *   the dropout multiplier of ngt_dense_fwd (same seed, same mask; pd only
+ *   with dropout_p > 0); lse [H, n_q] = max + log(sum).
+ * ngt_dense_bias_softmax_bwd: with dpd = dL/d(p o M): dP = M o dpd,
+ *   D_i = sum_j p dP, ds = p o (dP - D), 0 where masked.  ds is also the
+ *   gradient of bias (and so of attn_bias and pruning_mask).
+ * ngt_dense_abs_colsum: node_score[j] = sum_i mean_h |s * scale| (the
+ *   reference's abs(score).mean(dim=1).sum(dim=0)), in a fixed order, with a
+ *   caller workspace of ngt_dense_abs_colsum_workspace_bytes(n_k).
+ */
+int ngt_dense_bias_softmax_fwd(int32_t n_heads, int32_t n_q, int32_t n_k, const float* s,
+                               float scale, const float* bias, const uint8_t* mask,
+                               float dropout_p, uint64_t seed, const uint64_t* seed_dev, float* p,
+                               float* pd, float* lse, void* stream);
+int ngt_dense_bias_softmax_bwd(int32_t n_heads, int32_t n_q, int32_t n_k, const float* p,
+                               const float* dpd, const uint8_t* mask, float dropout_p,
+                               uint64_t seed, const uint64_t* seed_dev, float* ds, void* stream);
+int ngt_dense_abs_colsum_workspace_bytes(int32_t n_k, size_t* bytes);
+int ngt_dense_abs_colsum(int32_t n_heads, int32_t n_q, int32_t n_k, const float* s, float scale,
+                         float* node_score, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Dense full-window attention (all pairs, no mask/bias).
  * Replaces CoreAttention.full_attention:
  *   NeutronGT/models/graphormer_dist_node_level.py:42-65

@@ -9,9 +9,9 @@ window_attention(...)    the same over a built WindowAdjacency (C++ autograd nod
 dense_attention(...)     functional full-window attention
 WindowAdjacency          device CSR/transposed CSR/work lists of one window
 """
-from .attention import (CoreAttention, DenseAttentionFunction, SparseAttentionBiasFunction,
-                        SparseAttentionFunction, dense_attention, install, sparse_attention,
-                        window_attention)
+from .attention import (CoreAttention, DenseAttentionBiasFunction, DenseAttentionFunction,
+                        SparseAttentionBiasFunction, SparseAttentionFunction, dense_attention,
+                        dense_attention_bias, install, sparse_attention, window_attention)
 from .csr import AdjacencyCache, WindowAdjacency, chunk_for_heads, default_cache, small_for_heads
 
 __all__ = [
@@ -23,6 +23,8 @@ __all__ = [
     "SparseAttentionFunction",
     "SparseAttentionBiasFunction",
     "DenseAttentionFunction",
+    "DenseAttentionBiasFunction",
+    "dense_attention_bias",
     "WindowAdjacency",
     "AdjacencyCache",
     "chunk_for_heads",

@@ -104,6 +104,11 @@ SIGNATURES = {
     "ngt_sparse_bwd_bias": [_i32, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _pcsr, _i32, _i32,
                             _f32, _f32, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
     "ngt_edge_bias_grad": [_pcsr, _i32, _vp, _vp, _i64, _i64, _i64, _vp],
+    "ngt_dense_bias_softmax_fwd": [_i32, _i32, _i32, _vp, _f32, _vp, _vp, _f32, _u64, _vp, _vp,
+                                   _vp, _vp, _vp],
+    "ngt_dense_bias_softmax_bwd": [_i32, _i32, _i32, _vp, _vp, _vp, _f32, _u64, _vp, _vp, _vp],
+    "ngt_dense_abs_colsum_workspace_bytes": [_i32, _psz],
+    "ngt_dense_abs_colsum": [_i32, _i32, _i32, _vp, _f32, _vp, _vp, _sz, _vp],
     "ngt_dense_workspace_bytes": [_i32, _i32, _i32, _i32, _i32, _i32, _psz, _psz],
     "ngt_dense_fwd": [_i32, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _f32, _u64, _vp, _vp,
                       _vp, _vp, _vp, _vp, _sz, _vp],

@@ -340,6 +340,126 @@ class DenseAttentionFunction(torch.autograd.Function):
         return gq, gk, gv, None, None, None, None, None
 
 
+class DenseAttentionBiasFunction(torch.autograd.Function):
+    """full_attention with the reference's optional terms
+    (graphormer_dist_node_level.py:51-58): out = dropout_p(softmax(z)) v with
+    z = mask ? -1e9 : (q*scale) k^T + bias per head, node_score[j] =
+    sum_i mean_h |(q*scale) k^T|.  ``bias`` [H, N_q, N_k] fp32 (attn_bias +
+    pruning_mask, or None), ``mask`` [N_q, N_k] uint8 (nonzero = filled, or
+    None).  The products run as library GEMMs in fp32 (the reference's own
+    materialized form: a dense bias is O(N_q N_k H) whatever the kernel);
+    logits, mask, softmax, dropout (the fused kernels' hash mask for the same
+    seed), the softmax backward and the node scores are the library's
+    ngt_dense_bias_* / ngt_dense_abs_colsum kernels.  ``bias`` gets dS as
+    its gradient (zero where masked)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, bias, mask, scale, want_scores, dropout_p=0.0, seed=0, seed_t=None):
+        lib = _lib.load()
+        n_q, H, d = q.shape
+        n_k = k.shape[0]
+        dev = q.device
+        st = _stream(dev)
+        qh = q.permute(1, 0, 2).float().contiguous()
+        kh = k.permute(1, 0, 2).float().contiguous()
+        vh = v.permute(1, 0, 2).float().contiguous()
+        s = torch.bmm(qh, kh.transpose(1, 2).contiguous())  # [H, n_q, n_k]
+        ns = torch.zeros(n_k if want_scores else 0, dtype=torch.float32, device=dev)
+        if want_scores and n_k and n_q:
+            wb = C.c_size_t()
+            _lib.check(lib.ngt_dense_abs_colsum_workspace_bytes(n_k, C.byref(wb)))
+            ws = _workspace(wb.value, dev)
+            _lib.check(lib.ngt_dense_abs_colsum(H, n_q, n_k, s.data_ptr(), scale, ns.data_ptr(),
+                                                ws.data_ptr(), wb.value, st))
+        drop = dropout_p > 0.0
+        p = torch.empty_like(s)
+        pd = torch.empty_like(s) if drop else None
+        lse = torch.empty(H, n_q, dtype=torch.float32, device=dev)
+        sp = seed_t.data_ptr() if seed_t is not None else None
+        _lib.check(lib.ngt_dense_bias_softmax_fwd(
+            H, n_q, n_k, s.data_ptr(), scale, bias.data_ptr() if bias is not None else None,
+            mask.data_ptr() if mask is not None else None, dropout_p, seed, sp, p.data_ptr(),
+            pd.data_ptr() if drop else None, lse.data_ptr(), st))
+        del s
+        o = torch.bmm(pd if drop else p, vh)  # [H, n_q, d]
+        out = o.permute(1, 0, 2).to(q.dtype).contiguous()
+        ctx.save_for_backward(qh, kh, vh, p, pd, mask, seed_t)
+        ctx.scale, ctx.dropout_p, ctx.seed = scale, dropout_p, seed
+        ctx.dtypes = (q.dtype, k.dtype, v.dtype)
+        ctx.mark_non_differentiable(ns)
+        ctx.set_materialize_grads(False)
+        return out, ns
+
+    @staticmethod
+    def backward(ctx, g_out, g_ns):
+        qh, kh, vh, p, pd, mask, seed_t = ctx.saved_tensors
+        if g_out is None:
+            return (None,) * 10
+        lib = _lib.load()
+        H, n_q, n_k = p.shape
+        dev = p.device
+        st = _stream(dev)
+        gh = g_out.permute(1, 0, 2).float().contiguous()
+        pm = pd if pd is not None else p
+        dpd = torch.bmm(gh, vh.transpose(1, 2).contiguous())  # [H, n_q, n_k]
+        dv = torch.bmm(pm.transpose(1, 2).contiguous(), gh)  # [H, n_k, d]
+        ds = torch.empty_like(p)
+        _lib.check(lib.ngt_dense_bias_softmax_bwd(
+            H, n_q, n_k, p.data_ptr(), dpd.data_ptr(),
+            mask.data_ptr() if mask is not None else None, ctx.dropout_p, ctx.seed,
+            seed_t.data_ptr() if seed_t is not None else None, ds.data_ptr(), st))
+        del dpd
+        dq = torch.bmm(ds, kh) * ctx.scale
+        dk = torch.bmm(ds.transpose(1, 2).contiguous(), qh) * ctx.scale
+        tq, tk, tv = ctx.dtypes
+        return (dq.permute(1, 0, 2).to(tq), dk.permute(1, 0, 2).to(tk), dv.permute(1, 0, 2).to(tv),
+                ds if ctx.needs_input_grad[3] else None, None, None, None, None, None, None)
+
+
+def dense_attention_bias(q, k, v, scale, attn_bias=None, pruning_mask=None, mask=None,
+                         node_scores=True, dropout_p=0.0, seed=None):
+    """full_attention with attn_bias / pruning_mask / mask as the reference
+    applies them (graphormer_dist_node_level.py:51-58): q [1, N_q, H, d],
+    k/v [1, N_k, H, d]; attn_bias and pruning_mask broadcast to
+    [1, H, N_q, N_k] and added after the scaling; mask (bool, [N_q, N_k])
+    fills with -1e9.  Returns (x [N_q, H, d], node_scores [N_k])."""
+    H, d = q.shape[-2], q.shape[-1]
+    q = _prep(q.reshape(-1, H, d), "q")
+    k = _prep(k.reshape(-1, H, d), "k")
+    v = _prep(v.reshape(-1, H, d), "v")
+    n_q, n_k = q.shape[0], k.shape[0]
+    bias = None
+    if attn_bias is not None or pruning_mask is not None:
+        for t in (attn_bias, pruning_mask):
+            try:
+                ok = t is None or torch.broadcast_shapes(t.shape, (1, H, n_q, n_k)) == (1, H, n_q, n_k)
+            except RuntimeError:
+                ok = False
+            if not ok:
+                raise ValueError(f"attn_bias/pruning_mask must broadcast to [1, {H}, {n_q}, {n_k}], "
+                                 f"got {tuple(t.shape)}")
+        bias = torch.zeros(1, H, n_q, n_k, dtype=torch.float32, device=q.device)
+        for t in (attn_bias, pruning_mask):
+            if t is not None:
+                bias = bias + t.to(device=q.device, dtype=torch.float32)
+        bias = bias[0]
+        if not bias.is_contiguous():
+            bias = bias.contiguous()
+    mk = None
+    if mask is not None:
+        mk = mask.to(device=q.device).expand(n_q, n_k).to(torch.uint8).contiguous()
+    dropout_p = float(dropout_p)
+    if not 0.0 <= dropout_p <= 1.0:
+        raise ValueError(f"dropout probability has to be between 0 and 1, but got {dropout_p}")
+    seed_t = None
+    if dropout_p > 0.0 and seed is None:
+        seed_t = draw_seed(q.device)
+    elif isinstance(seed, torch.Tensor):
+        seed_t, seed = seed, None
+    return DenseAttentionBiasFunction.apply(q, k, v, bias, mk, float(scale), bool(node_scores),
+                                            dropout_p, int(seed or 0), seed_t)
+
+
 def draw_seed(device) -> torch.Tensor:
     """A 64-bit dropout seed drawn on ``device`` from torch's device generator,
     as an int64 tensor of one element that the kernels read when they run.
@@ -383,10 +503,23 @@ def dense_attention(q, k, v, scale=None, node_scores=True, dropout_p=0.0, seed=N
 
 # ---------------------------------------------------------------- the module
 class CoreAttention(nn.Module):
-    """Same constructor/attributes/forward as the reference's CoreAttention."""
+    """Same constructor/attributes/forward as the reference's CoreAttention.
 
-    def __init__(self, hidden_size, attention_dropout_rate, num_heads, cache: AdjacencyCache = None):
+    ``flash_layout`` (an addition) picks the flash branch's output layout:
+    "graphormer" (default) as graphormer_dist_node_level.py:111-122 returns it
+    (the [b, H, N, d] result transposed back to [b, N, H*d]); "gt_twin" as
+    gt_dist_node_level_single_window.py:212-225 does, viewing the [b, H, N, d]
+    result as [b, N, H*d] without the transpose (heads and nodes interleave).
+    install() picks "gt_twin" for the GT twin's modules."""
+
+    FLASH_LAYOUTS = ("graphormer", "gt_twin")
+
+    def __init__(self, hidden_size, attention_dropout_rate, num_heads, cache: AdjacencyCache = None,
+                 flash_layout: str = "graphormer"):
         super().__init__()
+        if flash_layout not in self.FLASH_LAYOUTS:
+            raise ValueError(f"flash_layout must be one of {self.FLASH_LAYOUTS}, got {flash_layout!r}")
+        self.flash_layout = flash_layout
         self.hidden_size_per_attention_head = hidden_size // num_heads
         self.scale = math.sqrt(self.hidden_size_per_attention_head)
         self.num_heads = num_heads
@@ -397,15 +530,17 @@ class CoreAttention(nn.Module):
     def full_attention(self, k, q, v, attn_bias, mask=None, pruning_mask=None):
         """graphormer_dist_node_level.py:42-65.  Returns (x [b, N, H, d], node_scores [N_k]).
         In training mode the probabilities go through att_dropout (p of the
-        module's nn.Dropout), as the reference's self.att_dropout(x) does."""
-        if attn_bias is not None or mask is not None or pruning_mask is not None:
-            raise NotImplementedError(
-                "full attention with attn_bias/mask/pruning_mask is not implemented by the "
-                "dense kernel (all are None on NeutronGT's training path)")
+        module's nn.Dropout), as the reference's self.att_dropout(x) does.
+        With attn_bias, pruning_mask or mask the materialized path runs
+        (dense_attention_bias); without them the fused kernels."""
         if q.size(0) != 1:
             raise NotImplementedError("batch size must be 1 (as in NeutronGT's window step)")
         p = self.att_dropout.p if self.training else 0.0
-        x, ns = dense_attention(q, k, v, scale=self.scale, dropout_p=p)
+        if attn_bias is not None or mask is not None or pruning_mask is not None:
+            x, ns = dense_attention_bias(q, k, v, self.scale, attn_bias=attn_bias,
+                                         pruning_mask=pruning_mask, mask=mask, dropout_p=p)
+        else:
+            x, ns = dense_attention(q, k, v, scale=self.scale, dropout_p=p)
         return x.unsqueeze(0), ns
 
     def naive_attention(self, q, k, v, dropout_p=0.0):
@@ -442,6 +577,8 @@ class CoreAttention(nn.Module):
             # fp32; this runs the same math in the inputs' dtype (fp32 or bf16).
             x, score = self.naive_attention(q, k, v, dropout_p=self.attention_dropout_rate)
             x = x.float()
+            if self.flash_layout == "gt_twin":  # [b, H, N, d] memory, viewed as [b, N, H*d] below
+                x = x.transpose(1, 2).contiguous()
         else:
             x, score = self.full_attention(k, q, v, attn_bias, mask=mask, pruning_mask=pruning_mask)
         x = x.view(batch_size, s_len, -1)
@@ -451,14 +588,18 @@ class CoreAttention(nn.Module):
 def install(model: nn.Module, cache: AdjacencyCache = None) -> int:
     """Replaces every ``local_attn`` CoreAttention-like submodule of ``model``
     (NeutronGT's MultiHeadAttention / DistributedAttentionNodeLevel) with this
-    module, keeping hidden size, heads and dropout.  Returns the count."""
+    module, keeping hidden size, heads and dropout, and for modules of the GT
+    twin (gt_dist_node_level_single_window) its flash-branch output layout.
+    Returns the count."""
     n = 0
     for mod in list(model.modules()):
         old = getattr(mod, "local_attn", None)
         if isinstance(old, nn.Module) and hasattr(old, "hidden_size_per_attention_head") \
                 and not isinstance(old, CoreAttention):
+            twin = type(old).__module__.rsplit(".", 1)[-1] == "gt_dist_node_level_single_window"
             new = CoreAttention(old.hidden_size_per_attention_head * old.num_heads,
-                                old.attention_dropout_rate, old.num_heads, cache=cache)
+                                old.attention_dropout_rate, old.num_heads, cache=cache,
+                                flash_layout="gt_twin" if twin else "graphormer")
             new.train(old.training)
             mod.local_attn = new
             n += 1

@@ -5,6 +5,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <math.h>
 #include <stdint.h>
 
 #include "../../include/ngt_attn.h"
@@ -323,6 +324,7 @@ __device__ __forceinline__ float drop_scale(const DropoutMask& dm, uint32_t word
   return half >= dm.thr ? dm.scale : 0.f;
 }
 
+
 template <typename T>
 struct dtype_of;
 template <>
@@ -361,6 +363,33 @@ struct KernelTimer {
     if (on) timing_record(name, st, false);
   }
 };
+
+// Host: the DropoutMask of keep probability 1 - p for an n_q x n_k score
+// matrix (one word per query and key pair); *on is false for p = 0.
+inline int make_dropout(const char* fn, float p, uint64_t seed, const uint64_t* seed_dev, int n_q,
+                 int n_k, DropoutMask* dm, bool* on) {
+  *on = false;
+  if (!(p >= 0.f && p <= 1.f))
+    return set_error(NGT_ERR_ARG, "%s: dropout_p=%g outside [0, 1]", fn, double(p));
+  if (p == 0.f) return NGT_OK;
+  const uint64_t words = uint64_t(n_q) * ((uint64_t(n_k) + 1) / 2);
+  if (words > (uint64_t(1) << 32))
+    return set_error(NGT_ERR_UNSUPPORTED,
+                     "%s: dropout needs n_q * ceil(n_k / 2) <= 2^32 (n_q=%d n_k=%d)", fn, n_q, n_k);
+  dm->seed = seed;
+  dm->seed_dev = seed_dev;
+  dm->head_key = 0;
+  dm->n_kp = static_cast<uint32_t>((uint64_t(n_k) + 1) / 2);
+  if (p >= 1.f) {  // everything dropped: keep-all mask with scale 0
+    dm->thr = 0;
+    dm->scale = 0.f;
+  } else {
+    dm->thr = static_cast<uint32_t>(lrint(double(p) * 65536.0));
+    dm->scale = static_cast<float>(1.0 / (1.0 - double(p)));
+  }
+  *on = true;
+  return NGT_OK;
+}
 
 }  // namespace ngt
 

@@ -885,30 +885,6 @@ int check_args(const char* fn, int dtype, int n_q, int n_k, int H, int d) {
 }
 
 // Dropout parameters from p and the seed; *on = false for p = 0.
-int make_dropout(const char* fn, float p, uint64_t seed, const uint64_t* seed_dev, int n_q,
-                 int n_k, DropoutMask* dm, bool* on) {
-  *on = false;
-  if (!(p >= 0.f && p <= 1.f))
-    return set_error(NGT_ERR_ARG, "%s: dropout_p=%g outside [0, 1]", fn, double(p));
-  if (p == 0.f) return NGT_OK;
-  const uint64_t words = uint64_t(n_q) * ((uint64_t(n_k) + 1) / 2);
-  if (words > (uint64_t(1) << 32))
-    return set_error(NGT_ERR_UNSUPPORTED,
-                     "%s: dropout needs n_q * ceil(n_k / 2) <= 2^32 (n_q=%d n_k=%d)", fn, n_q, n_k);
-  dm->seed = seed;
-  dm->seed_dev = seed_dev;
-  dm->head_key = 0;
-  dm->n_kp = static_cast<uint32_t>((uint64_t(n_k) + 1) / 2);
-  if (p >= 1.f) {  // everything dropped: keep-all mask with scale 0
-    dm->thr = 0;
-    dm->scale = 0.f;
-  } else {
-    dm->thr = static_cast<uint32_t>(lrint(double(p) * 65536.0));
-    dm->scale = static_cast<float>(1.0 / (1.0 - double(p)));
-  }
-  *on = true;
-  return NGT_OK;
-}
 
 // The bf16 path runs on the matrix cores (ngt_dense_mfma.hip) for d <= 32;
 // NGT_DENSE_VALU=1 selects the vector-ALU kernels instead (for comparison).

@@ -281,21 +281,32 @@ def sparse_fwd_bwd(q, k, v, edge_index, grad_x, num_heads, dtype=torch.float32, 
     return res
 
 
-def full_fwd_bwd(q, k, v, grad_x, dtype=torch.float32, dropout_mult=None, flash=False):
+def full_fwd_bwd(q, k, v, grad_x, dtype=torch.float32, dropout_mult=None, flash=False,
+                 attn_bias=None, pruning_mask=None, mask=None):
     """full_attention (or, flash=True, naive_attention) forward + autograd
-    backward on CPU; q [N_q,H,d], k/v [N_k,H,d]."""
+    backward on CPU; q [N_q,H,d], k/v [N_k,H,d].  attn_bias / pruning_mask
+    ([1, H, N_q, N_k] or broadcastable) get their gradients in the dict as
+    "dbias" / "dpruning"; mask is a bool [N_q, N_k]."""
     qf = q.to(dtype).clone().unsqueeze(0).requires_grad_(True)
     kf = k.to(dtype).clone().unsqueeze(0).requires_grad_(True)
     vf = v.to(dtype).clone().unsqueeze(0).requires_grad_(True)
+    ab = attn_bias.to(dtype).clone().requires_grad_(True) if attn_bias is not None else None
+    pm = pruning_mask.to(dtype).clone().requires_grad_(True) if pruning_mask is not None else None
     if flash:
         x, ns = naive_attention(qf, kf, vf, dropout_mult=dropout_mult), torch.empty(0)
     else:
-        x, ns = full_attention(qf, kf, vf, dropout_mult=dropout_mult)
+        x, ns = full_attention(qf, kf, vf, attn_bias=ab, pruning_mask=pm, mask=mask,
+                               dropout_mult=dropout_mult)
     x.backward(grad_x.to(dtype).unsqueeze(0))
-    return {
+    res = {
         "x": x.detach()[0],
         "node_scores": ns.detach(),
         "dq": qf.grad[0],
         "dk": kf.grad[0],
         "dv": vf.grad[0],
     }
+    if ab is not None:
+        res["dbias"] = ab.grad
+    if pm is not None:
+        res["dpruning"] = pm.grad
+    return res

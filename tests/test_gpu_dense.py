@@ -269,3 +269,39 @@ def test_dense_flash_backward(dtype):
                             dtype=torch.float64, dropout_mult=mult, flash=True)
     for name in ("x", "dq", "dk", "dv"):
         assert_parity(res[name].float(), ref[name], ref64[name], dtype, f"flash {name}")
+
+
+def test_flash_branch_gt_twin_layout():
+    """flash_layout='gt_twin' views the [b, H, N, d] result as [b, N, H*d]
+    without transposing back (gt_dist_node_level_single_window.py:212-225);
+    install() picks it for a module of that file."""
+    _say("case flash gt twin layout")
+    H, d, n = 2, 8, 40
+    q, k, v, go = _qkv(n, n, H, d, torch.float32, seed=11)
+    args = (q[None].cuda(), k[None].cuda(), v[None].cuda(), None, None, "flash")
+    torch.manual_seed(79)
+    xg, _ = CoreAttention(H * d, 0.5, H).cuda()(*args)
+    torch.manual_seed(79)
+    xt, _ = CoreAttention(H * d, 0.5, H, flash_layout="gt_twin").cuda()(*args)
+    # the same numbers in the reference twin's memory order
+    want = xg.view(1, n, H, d).transpose(1, 2).contiguous().view(1, n, H * d)
+    assert torch.equal(xt, want) and not torch.equal(xt, xg)
+    with pytest.raises(ValueError):
+        CoreAttention(H * d, 0.5, H, flash_layout="other")
+
+    class TwinCore(torch.nn.Module):  # shaped like the twin's CoreAttention
+        def __init__(self):
+            super().__init__()
+            self.hidden_size_per_attention_head, self.num_heads = d, H
+            self.attention_dropout_rate = 0.5
+
+    TwinCore.__module__ = "NeutronGT.models.gt_dist_node_level_single_window"
+
+    class Holder(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.local_attn = TwinCore()
+
+    from neutrongt_amd import install
+    h = Holder()
+    assert install(h) == 1 and h.local_attn.flash_layout == "gt_twin"

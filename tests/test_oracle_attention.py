@@ -337,3 +337,39 @@ def test_sparse_bias_added_after_clamp_and_its_gradient():
     bad = OA.sparse_fwd_bwd(T(q), T(k), T(v), ei, T(g), H, dtype=torch.float64,
                             attn_bias=T(bias.transpose(0, 2, 1).copy()))
     assert np.abs(bad["x"][:, 0].numpy() - x).max() > 1e-3
+
+
+def test_full_attention_bias_pruning_mask_by_hand():
+    """full_attention's optional terms (graphormer_dist_node_level.py:51-58):
+    z = (q sqrt(d)) k^T + attn_bias + pruning_mask, then masked_fill(mask,
+    -1e9), softmax over keys.  One head, 2 queries, 3 keys worked in float64:
+    query 0 has key 2 masked; query 1 has every key masked (the reference then
+    weighs all keys equally).  The biases' gradient is dS, zero where masked;
+    the node scores ignore both terms."""
+    H, d = 1, 2
+    q = torch.tensor([[[0.5, -1.0]], [[1.0, 0.25]]], dtype=torch.float64)      # [2, H, d]
+    k = torch.tensor([[[1.0, 0.5]], [[-0.5, 1.0]], [[2.0, 0.0]]], dtype=torch.float64)
+    v = torch.tensor([[[1.0, 0.0]], [[0.0, 2.0]], [[-1.0, 1.0]]], dtype=torch.float64)
+    g = torch.tensor([[[1.0, -0.5]], [[0.5, 2.0]]], dtype=torch.float64)
+    ab = torch.tensor([[[[0.1, -0.2, 0.3], [0.0, 0.4, -0.1]]]], dtype=torch.float64)
+    pm = torch.tensor([[[[-1.0, 0.0, 0.5], [0.2, 0.0, 0.0]]]], dtype=torch.float64)
+    mask = torch.tensor([[False, False, True], [True, True, True]])
+    sq = math.sqrt(d)
+    Q, K, V, G = q[:, 0].numpy(), k[:, 0].numpy(), v[:, 0].numpy(), g[:, 0].numpy()
+    S = (Q * sq) @ K.T
+    Z = S + ab[0, 0].numpy() + pm[0, 0].numpy()
+    Z = np.where(mask.numpy(), -1e9, Z)
+    P = np.exp(Z - Z.max(1, keepdims=True))
+    P /= P.sum(1, keepdims=True)
+    X = P @ V
+    dP = G @ V.T
+    dS = P * (dP - (P * dP).sum(1, keepdims=True))
+    dZ = np.where(mask.numpy(), 0.0, dS)
+    ref = OA.full_fwd_bwd(q, k, v, g, dtype=torch.float64, attn_bias=ab, pruning_mask=pm,
+                          mask=mask)
+    np.testing.assert_allclose(ref["x"][:, 0].numpy(), X, rtol=1e-12, atol=1e-14)
+    np.testing.assert_allclose(X[1], V.mean(0), rtol=1e-12)  # all keys masked: equal weights
+    np.testing.assert_allclose(ref["dbias"][0, 0].numpy(), dZ, rtol=1e-12, atol=1e-14)
+    np.testing.assert_allclose(ref["dpruning"][0, 0].numpy(), dZ, rtol=1e-12, atol=1e-14)
+    np.testing.assert_allclose(ref["node_scores"].numpy(), np.abs(S).sum(0), rtol=1e-12)
+    np.testing.assert_allclose(ref["dq"][:, 0].numpy(), sq * (dZ @ K), rtol=1e-12, atol=1e-14)
