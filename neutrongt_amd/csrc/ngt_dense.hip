@@ -31,15 +31,15 @@ namespace ngt {
 
 // Matrix-core kernels (ngt_dense_mfma.hip).
 bool mfma_dense_supported(int d);
-MfSplit mfma_fwd_split(int n_q, int n_k, int H);
+MfSplit mfma_fwd_split(int n_q, int n_k, int H, bool node_scores);
 MfSplit mfma_dq_split(int n_q, int n_k, int H);
 int mfma_dense_fwd(int d, const void* q, const void* k, const void* v, int n_q, int n_k, int H,
                    float scale, const DropoutMask* dm, void* out, float* out32, float* lse,
                    float* part, MfSplit sp, float* part_ml, float* part_acc, hipStream_t st);
 int mfma_dense_bwd(int d, const void* q, const void* k, const void* v, const void* g,
-                   const float* lse, const float* dsum, int n_q, int n_k, int H, float scale,
-                   const DropoutMask* dm, void* gq, void* gk, void* gv, MfSplit sq,
-                   float* part_dq, hipStream_t st);
+                   const void* out, const float* out32, const float* lse, float* dsum, int n_q,
+                   int n_k, int H, float scale, const DropoutMask* dm, void* gq, void* gk, void* gv,
+                   MfSplit sq, float* part_dq, hipStream_t st);
 
 namespace {
 
@@ -884,41 +884,11 @@ int check_args(const char* fn, int dtype, int n_q, int n_k, int H, int d) {
   return NGT_OK;
 }
 
-// Dropout parameters from p and the seed; *on = false for p = 0.
-
 // The bf16 path runs on the matrix cores (ngt_dense_mfma.hip) for d <= 32;
 // NGT_DENSE_VALU=1 selects the vector-ALU kernels instead (for comparison).
 bool use_mfma(int dtype, int d) {
   static const bool valu = getenv("NGT_DENSE_VALU") != nullptr;
   return dtype == NGT_BF16 && mfma_dense_supported(d) && !valu;
-}
-
-int rowstat_bf16(int d, const void* out, const float* out32, const void* g, int n_q, int H,
-                 float* dsum, hipStream_t st) {
-  int64_t blocks = (int64_t(n_q) * H + kBlock - 1) / kBlock;
-  if (blocks > 65536) blocks = 65536;
-  KernelTimer timer_("dense_rowstat", st);
-#define NGT_RS(DH)                                                                             \
-  case DH:                                                                                     \
-    if (out32)                                                                                 \
-      hipLaunchKernelGGL((k_dense_rowstat<float, bf16_t, DH>), dim3(int(blocks)), dim3(kBlock), \
-                         0, st, out32, static_cast<const bf16_t*>(g), n_q, H, dsum);           \
-    else                                                                                       \
-      hipLaunchKernelGGL((k_dense_rowstat<bf16_t, bf16_t, DH>), dim3(int(blocks)),              \
-                         dim3(kBlock), 0, st, static_cast<const bf16_t*>(out),                  \
-                         static_cast<const bf16_t*>(g), n_q, H, dsum);                          \
-    break;
-  switch (d) {
-    NGT_RS(8)
-    NGT_RS(16)
-    NGT_RS(24)
-    NGT_RS(32)
-    default:
-      return set_error(NGT_ERR_UNSUPPORTED, "rowstat: head_dim %d", d);
-  }
-#undef NGT_RS
-  NGT_HIP_CHECK(hipGetLastError());
-  return NGT_OK;
 }
 
 // Forward workspace: the matrix-core path needs H * n_k floats of node-score
@@ -933,7 +903,7 @@ struct MfFwdLayout {
 };
 MfFwdLayout mf_fwd_layout(int32_t n_q, int32_t n_k, int32_t H, int32_t d, bool node_scores) {
   MfFwdLayout L{};
-  L.sp = mfma_fwd_split(n_q, n_k, H);
+  L.sp = mfma_fwd_split(n_q, n_k, H, node_scores);
   size_t off = node_scores ? align256(size_t(H) * n_k * 4) : 0;
   if (L.sp.n_split > 1) {
     L.ml = off;
@@ -1070,17 +1040,13 @@ extern "C" int ngt_dense_bwd(int dtype, const void* q, const void* k, const void
                      need);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (use_mfma(dtype, head_dim)) {
-    float* dsum = static_cast<float*>(workspace);
-    if (n_q > 0) {
-      rc = rowstat_bf16(head_dim, out, out_f32, grad_out, n_q, n_heads, dsum, st);
-      if (rc != NGT_OK) return rc;
-    }
+    float* dsum = static_cast<float*>(workspace);  // written by the dQ pass
     const MfSplit sq = n_q > 0 ? mfma_dq_split(n_q, n_k, n_heads) : MfSplit{1, 1};
     float* part_dq = sq.n_split > 1
                          ? reinterpret_cast<float*>(static_cast<char*>(workspace) + bwd_ws(n_q, n_heads))
                          : nullptr;
-    return mfma_dense_bwd(head_dim, q, k, v, grad_out, lse, dsum, n_q, n_k, n_heads, scale, dm,
-                          grad_q, grad_k, grad_v, sq, part_dq, st);
+    return mfma_dense_bwd(head_dim, q, k, v, grad_out, out, out_f32, lse, dsum, n_q, n_k,
+                          n_heads, scale, dm, grad_q, grad_k, grad_v, sq, part_dq, st);
   }
   return dispatch<BwdOp>(dtype, head_dim, q, k, v, out, out_f32, grad_out, lse, int(n_q), int(n_k),
                          int(n_heads), scale, dm, grad_q, grad_k, grad_v,

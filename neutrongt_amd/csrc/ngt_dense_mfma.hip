@@ -40,6 +40,17 @@ namespace {
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
+// Work-item and work-group ids as register reads.  The kernels of this file
+// are built with the IEEE mode bit off, which the device library's functions
+// behind threadIdx / blockIdx / gridDim are not, and the compiler does not
+// inline across that difference: each use would be a call whose result it
+// treats as a per-lane value, so loop bounds derived from a block index would
+// be compared on the VALU in every tile.
+__device__ __forceinline__ int tid_x() { return static_cast<int>(__builtin_amdgcn_workitem_id_x()); }
+__device__ __forceinline__ int wg_x() { return static_cast<int>(__builtin_amdgcn_workgroup_id_x()); }
+__device__ __forceinline__ int wg_y() { return static_cast<int>(__builtin_amdgcn_workgroup_id_y()); }
+__device__ __forceinline__ int wg_z() { return static_cast<int>(__builtin_amdgcn_workgroup_id_z()); }
+
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / kWave;
 constexpr int kT = 32;                  // tile edge (rows/cols of one MFMA)
@@ -190,7 +201,7 @@ struct Stage {
                                        int H, int h) {
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-      const int e = threadIdx.x + i * kBlock;
+      const int e = tid_x() + i * kBlock;
       const int r = e / VPR, cv = e - r * VPR;
       w[i] = make_uint4(0u, 0u, 0u, 0u);
       if (e < kSB * VPR && row0 + r < n_rows)
@@ -200,7 +211,7 @@ struct Stage {
   __device__ __forceinline__ void store_rows(short (*lds)[DH + kRowPad]) const {
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-      const int e = threadIdx.x + i * kBlock;
+      const int e = tid_x() + i * kBlock;
       if (e < kSB * VPR) {
         const int r = e / VPR, cv = e - r * VPR;
         if constexpr ((DH + kRowPad) % 8 == 0) {
@@ -215,7 +226,7 @@ struct Stage {
   __device__ __forceinline__ void store_trans(short (*lds)[kSB + kColPad]) const {
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-      const int e = threadIdx.x + i * kBlock;
+      const int e = tid_x() + i * kBlock;
       if (e < kSB * VPR) {
         const int r = e / VPR, cv = e - r * VPR;
         const uint32_t u[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
@@ -240,7 +251,7 @@ __device__ __forceinline__ s16x4 lds4(const short* p) {
 template <int DH>
 __device__ __forceinline__ void fill_pad_rows(short (*t)[kSB + kColPad], bool ones_row) {
   constexpr int kPadRows = kT - DH;
-  for (int e = threadIdx.x; e < kPadRows * (kSB + kColPad); e += kBlock) {
+  for (int e = tid_x(); e < kPadRows * (kSB + kColPad); e += kBlock) {
     const int r = DH + e / (kSB + kColPad), c = e % (kSB + kColPad);
     t[r][c] = (ones_row && r == DH) ? static_cast<short>(0x3f80) : static_cast<short>(0);
   }
@@ -273,8 +284,8 @@ __device__ __forceinline__ void mf_fwd_block(int bx, int h, int z, const bf16_t*
   constexpr int NC = DH / 8;  // K chunks of the QK^T contraction
   __shared__ __align__(16) short ks[kSB][DH + kRowPad];  // K rows
   __shared__ __align__(16) short vt[kT][kSB + kColPad];  // V^T: [c][key], rows >= DH constant
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x >> 6;
+  const int lane = tid_x() & (kWave - 1);
+  const int wave = tid_x() >> 6;
   const int half = lane >> 5;
   const int l32 = lane & 31;
   const int64_t qi = int64_t(bx) * kRowsPerBlock + wave * kT + l32;
@@ -446,8 +457,8 @@ __device__ __forceinline__ void mf_scores_block(int bx, int h, const bf16_t* __r
                                                 float* __restrict__ part) {
   constexpr int NC = DH / 8;
   __shared__ __align__(16) short qs[kSB][DH + kRowPad];
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x >> 6;
+  const int lane = tid_x() & (kWave - 1);
+  const int wave = tid_x() >> 6;
   const int half = lane >> 5;
   const int l32 = lane & 31;
   const int64_t kj = int64_t(bx) * kRowsPerBlock + wave * kT + l32;
@@ -499,8 +510,8 @@ __global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
                                                    float* __restrict__ part_acc,
                                                    int32_t n_split, int32_t fwd_bx,
                                                    int32_t score_bx, float* __restrict__ part) {
-  const int bx = static_cast<int>(blockIdx.x), h = static_cast<int>(blockIdx.y);
-  const int z = static_cast<int>(blockIdx.z);
+  const int bx = wg_x(), h = wg_y();
+  const int z = wg_z();
   if (z == n_split) {  // block-uniform
     if (bx < score_bx) mf_scores_block<DH>(bx, h, q, k, n_q, n_k, H, scale, part);
     return;
@@ -510,16 +521,38 @@ __global__ __launch_bounds__(kBlock) void k_mf_fwd(const bf16_t* __restrict__ q,
                            split_keys, part_ml, part_acc);
 }
 
+// grad_q = scale * sum of the key splits' partial dQ, added in split order;
+// block b of nb takes elements b * kBlock + tid_x(), stepping nb * kBlock.
+__device__ __forceinline__ void dq_combine(const float* __restrict__ part, int n_split, int64_t n,
+                                           float scale, bf16_t* __restrict__ grad_q, int64_t b,
+                                           int64_t nb) {
+  for (int64_t t = b * kBlock + tid_x(); t < n; t += nb * kBlock) {
+    float a = part[t];
+    for (int s = 1; s < n_split; ++s) a += part[int64_t(s) * n + t];
+    grad_q[t].x = f32_to_bf16(a * scale);
+  }
+}
+
 // ----------------------------------------------------------------- backward
 // Key-major: dK, dV for keys k0 .. k0+31 of one head.  S, dP recomputed as
 // D[q][key]; Q and G stages of 128 queries in LDS, row-major (A operands of S
 // and dP) and transposed (B operands of dV += P^T G and dK += dS^T Q).
+//
+// Blocks with wg_x() >= kv_bx do not take keys: with a split dQ pass
+// (part_dq set) they add its partial dQ in split order into grad_q, so that
+// merge rides in this launch instead of a launch of its own.
 template <int DH, bool DROP>
 __global__ __launch_bounds__(kBlock) void k_mf_bwd_kv(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
     const bf16_t* __restrict__ g, const float* __restrict__ lse, const float* __restrict__ dsum,
     int32_t n_q, int32_t n_k, int32_t H, float scale, DropoutMask dm,
-    bf16_t* __restrict__ grad_k, bf16_t* __restrict__ grad_v) {
+    bf16_t* __restrict__ grad_k, bf16_t* __restrict__ grad_v, int32_t kv_bx, int32_t comb_bx,
+    const float* __restrict__ part_dq, int32_t n_split_q, bf16_t* __restrict__ grad_q) {
+  if (wg_x() >= kv_bx) {  // block-uniform: a merge block (grid.y = H)
+    dq_combine(part_dq, n_split_q, int64_t(n_q) * H * DH, scale, grad_q,
+               int64_t(wg_x() - kv_bx) * H + wg_y(), int64_t(comb_bx) * H);
+    return;
+  }
   constexpr int NC = DH / 8;
   __shared__ __align__(16) short qs[kSB][DH + kRowPad];
   __shared__ __align__(16) short gs[kSB][DH + kRowPad];
@@ -529,12 +562,12 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_kv(
   // xr[1] (half-major: a half-wave reads 32 consecutive records)
   __shared__ __align__(16) uint2 xr[2][kSB];
   __shared__ __align__(16) float dd[kSB];  // -D, with dropout only
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x >> 6;
+  const int lane = tid_x() & (kWave - 1);
+  const int wave = tid_x() >> 6;
   const int half = lane >> 5;
   const int l32 = lane & 31;
-  const int h = blockIdx.y;
-  const int64_t kj = int64_t(blockIdx.x) * kRowsPerBlock + wave * kT + l32;
+  const int h = wg_y();
+  const int64_t kj = int64_t(wg_x()) * kRowsPerBlock + wave * kT + l32;
   const bool k_ok = kj < n_k;
   if constexpr (DROP) dm = drop_for_head(dm, h);
   s16x4 kbv[NC], vbv[NC];  // K^T, V^T as B operands
@@ -558,12 +591,12 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_kv(
   auto prefetch = [&](int qb) {
     pq.load(q, qb, n_q, H, h);
     pg.load(g, qb, n_q, H, h);
-    if (threadIdx.x < kSB) {
-      const bool ok = qb + int(threadIdx.x) < n_q;
+    if (tid_x() < kSB) {
+      const bool ok = qb + int(tid_x()) < n_q;
       // raw values here: scaling now would wait on this load (and on the
       // stage's prefetch before it) at once
-      pl = ok ? lse[int64_t(h) * n_q + qb + threadIdx.x] : INFINITY;
-      pd = ok ? dsum[int64_t(h) * n_q + qb + threadIdx.x] : 0.f;
+      pl = ok ? lse[int64_t(h) * n_q + qb + tid_x()] : INFINITY;
+      pd = ok ? dsum[int64_t(h) * n_q + qb + tid_x()] : 0.f;
     }
   };
   fill_pad_rows<DH>(qt, false);
@@ -575,13 +608,13 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_kv(
     pg.store_rows(gs);
     pq.store_trans(qt);
     pg.store_trans(gt);
-    if (threadIdx.x < kSB) {
+    if (tid_x() < kSB) {
       // padded rows: -L = -1e30 (finite, so the zero slots of the D step
       // stay 0; exp2 of the score is 0), D = 0 with zero G rows
       const float nl = pl == INFINITY ? -1e30f : -pl * kLog2e;
-      xr[0][threadIdx.x] = split3(nl);
-      xr[1][threadIdx.x] = split3(-pd);
-      if constexpr (DROP) dd[threadIdx.x] = -pd;
+      xr[0][tid_x()] = split3(nl);
+      xr[1][tid_x()] = split3(-pd);
+      if constexpr (DROP) dd[tid_x()] = -pd;
     }
     __syncthreads();
     if (qb + kSB < n_q) prefetch(qb + kSB);
@@ -648,7 +681,7 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_kv(
   }
   // D[key][c] -> grad rows; lane holds column c = l32 of 16 key rows.
   if (l32 >= DH) return;
-  const int64_t k0 = int64_t(blockIdx.x) * kRowsPerBlock + wave * kT;
+  const int64_t k0 = int64_t(wg_x()) * kRowsPerBlock + wave * kT;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int64_t key = k0 + 8 * (i / 4) + 4 * half + (i % 4);
@@ -661,22 +694,28 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_kv(
 
 // Query-major: dQ for queries q0 .. q0+31.  S^T, dP^T as D[key][q]; K and V
 // stages of 128 keys in LDS (row-major for the A operands, K^T for dQ += dS K).
+// This pass runs first in the backward and forms each query's
+// D = sum_c G o itself (o the forward's fp32 output when it kept one, else the
+// bf16 output: D enters dS = P (dP - D) where the two terms nearly cancel for
+// peaked rows, and the rounded output alone moves dQ by a few percent there);
+// the blocks of key split 0 store it in dsum for the key-major pass.
 template <int DH, bool DROP>
 __global__ __launch_bounds__(kBlock) void k_mf_bwd_q(
     const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
-    const bf16_t* __restrict__ g, const float* __restrict__ lse, const float* __restrict__ dsum,
-    int32_t n_q, int32_t n_k, int32_t H, float scale, DropoutMask dm,
-    bf16_t* __restrict__ grad_q, int32_t split_keys, float* __restrict__ part_dq) {
+    const bf16_t* __restrict__ g, const bf16_t* __restrict__ out, const float* __restrict__ out32,
+    const float* __restrict__ lse, float* __restrict__ dsum, int32_t n_q, int32_t n_k, int32_t H,
+    float scale, DropoutMask dm, bf16_t* __restrict__ grad_q, int32_t split_keys,
+    float* __restrict__ part_dq) {
   constexpr int NC = DH / 8;
   __shared__ __align__(16) short ks[kSB][DH + kRowPad];
   __shared__ __align__(16) short vs[kSB][DH + kRowPad];
   __shared__ __align__(16) short kt[kT][kSB + kColPad];  // rows >= DH zero
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x >> 6;
+  const int lane = tid_x() & (kWave - 1);
+  const int wave = tid_x() >> 6;
   const int half = lane >> 5;
   const int l32 = lane & 31;
-  const int h = blockIdx.y;
-  const int64_t qi = int64_t(blockIdx.x) * kRowsPerBlock + wave * kT + l32;
+  const int h = wg_y();
+  const int64_t qi = int64_t(wg_x()) * kRowsPerBlock + wave * kT + l32;
   const bool q_ok = qi < n_q;
   if constexpr (DROP) dm = drop_for_head(dm, h);
   s16x4 qbv[NC], gbv[NC];  // Q^T, G^T as B operands
@@ -686,7 +725,28 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_q(
     gbv[j] = settle(q_ok ? load4(g + (qi * H + h) * DH + 8 * j + 4 * half) : zero4());
   }
   const float L2 = q_ok ? lse[int64_t(h) * n_q + qi] * kLog2e : INFINITY;
-  const float Dq = q_ok ? dsum[int64_t(h) * n_q + qi] : 0.f;
+  // D: this lane's 4 * NC columns in order, then the other half's
+  float dpart = 0.f;
+  if (q_ok) {
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      const int64_t o = (qi * H + h) * DH + 8 * j + 4 * half;
+      float ov[4];
+      if (out32) {
+        const float4 f = *reinterpret_cast<const float4*>(out32 + o);
+        ov[0] = f.x, ov[1] = f.y, ov[2] = f.z, ov[3] = f.w;
+      } else {
+        const s16x4 ob = load4(out + o);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ov[i] = bf16_to_f32(static_cast<uint16_t>(ob[i]));
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        dpart = fmaf(bf16_to_f32(static_cast<uint16_t>(gbv[j][i])), ov[i], dpart);
+    }
+  }
+  const float Dq = sum_halves(dpart);
+  if (wg_z() == 0 && half == 0 && q_ok) dsum[int64_t(h) * n_q + qi] = Dq;
   const float s2 = scale * kLog2e;
   // S^T s2 - L and dP^T - D come straight out of the MFMAs: Q^T s2 as hi ++ lo
   // operands (the K rows read once, fed twice), the lane's -L as the
@@ -700,7 +760,7 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_q(
   const s16x4 ones_a = ones3(half, 0);
   const s16x4 db = half == 0 ? __builtin_bit_cast(s16x4, split3(-Dq)) : zero4();
   f32x16 dq = zero16();  // D[q][c]: q = 8*(i/4)+4*half+i%4 (tile row), c = l32
-  const int k_begin = int(blockIdx.z) * split_keys;  // this block's key split
+  const int k_begin = wg_z() * split_keys;  // this block's key split
   const int k_end = min(n_k, k_begin + split_keys);
   fill_pad_rows<DH>(kt, false);
   Stage<DH> pk, pv;
@@ -766,9 +826,9 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_q(
     }
   }
   if (l32 >= DH) return;
-  const int64_t q0 = int64_t(blockIdx.x) * kRowsPerBlock + wave * kT;
-  if (part_dq) {  // this split's dQ, unscaled fp32; k_mf_dq_combine adds the splits in order
-    float* pz = part_dq + int64_t(blockIdx.z) * n_q * H * DH;
+  const int64_t q0 = int64_t(wg_x()) * kRowsPerBlock + wave * kT;
+  if (part_dq) {  // this split's dQ, unscaled fp32; the splits are added in order afterwards
+    float* pz = part_dq + int64_t(wg_z()) * n_q * H * DH;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int64_t qq = q0 + 8 * (i / 4) + 4 * half + (i % 4);
@@ -783,17 +843,14 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_q(
   }
 }
 
-// grad_q = scale * sum of the key splits' partial dQ, added in split order.
+// grad_q = scale * sum of the key splits' partial dQ, added in split order
+// (kernel: a grid of its own, used when no dK/dV launch follows).
 __global__ __launch_bounds__(kBlock) void k_mf_dq_combine(const float* __restrict__ part,
                                                           int32_t n_split, int64_t n,
                                                           float scale,
-                                                          bf16_t* __restrict__ grad_q) {
-  for (int64_t t = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; t < n;
-       t += int64_t(gridDim.x) * blockDim.x) {
-    float a = part[t];
-    for (int s = 1; s < n_split; ++s) a += part[int64_t(s) * n + t];
-    grad_q[t].x = f32_to_bf16(a * scale);
-  }
+                                                          bf16_t* __restrict__ grad_q,
+                                                          int32_t n_blocks) {
+  dq_combine(part, n_split, n, scale, grad_q, wg_x(), n_blocks);
 }
 
 }  // namespace
@@ -804,19 +861,24 @@ bool mfma_dense_supported(int d) { return d == 8 || d == 16 || d == 24 || d == 3
 // Key splits: the forward (one wave per 32 queries and head, all keys) and
 // the dQ pass have grids of ceil(n_q / 32) * H waves, about 4 per SIMD at
 // 16,000 queries and 8 heads, while their registers leave room for more.
-// Splitting the keys over blockIdx.z raises the waves per SIMD; each split's
+// Splitting the keys over wg_z() raises the waves per SIMD; each split's
 // state is merged afterwards in split order.  Measured at 16,000 nodes, 8
 // heads, d = 8 with the per-score arithmetic in the MFMAs (us per launch):
-// forward 331 / 325 / 324 / 329 / 334 at 2 / 3 / 4 / 6 / 8 splits plus a
-// 7-13 us combine; dQ 348 / 337 / 334 / 332 / 335 at 1 / 2 / 3 / 4 / 6.
+// forward alone 331 / 325 / 324 / 329 / 334 at 2 / 3 / 4 / 6 / 8 splits plus a
+// 7-13 us combine; dQ 348 / 337 / 334 / 332 / 335 at 1 / 2 / 3 / 4 / 6.  When
+// the column-score blocks share the forward's launch they bring as many waves
+// again, and one split is best: 384 us for forward and scores against 392 us
+// plus the combine at 2 splits.  `shared_waves` counts such other waves.
 // What bounds these kernels is each wave's chain MFMA -> exp -> pack -> MFMA
 // per tile with 4-5 waves per SIMD; issuing the next tile's products ahead of
 // the current tile's softmax work costs registers (one wave less per SIMD)
 // and measured slower: forward 406 -> 432 us, dK/dV 479 -> 585 us.
 // NGT_MF_FWD_SPLIT / NGT_MF_DQ_SPLIT override the count.
-static MfSplit plan_split(int n_q, int n_k, int H, int target_waves, const char* env) {
+static MfSplit plan_split(int n_q, int n_k, int H, int target_waves, int64_t shared_waves,
+                          const char* env) {
   const int64_t base = int64_t((n_q + kRowsPerBlock - 1) / kRowsPerBlock) * H * kWaves;
-  int want = base > 0 ? int((target_waves + base / 2) / base) : 1;
+  const int64_t room = std::max<int64_t>(target_waves - shared_waves, 0);
+  int want = base > 0 ? int((room + base / 2) / base) : 1;
   if (const char* e = getenv(env)) want = atoi(e);
   want = std::max(1, std::min({want, 8, std::max(1, n_k / 512)}));
   if (want <= 1 || n_k <= 0) return {1, std::max(n_k, 1)};
@@ -824,11 +886,13 @@ static MfSplit plan_split(int n_q, int n_k, int H, int target_waves, const char*
   keys = (keys + kSB - 1) / kSB * kSB;
   return {(n_k + keys - 1) / keys, keys};
 }
-MfSplit mfma_fwd_split(int n_q, int n_k, int H) {
-  return plan_split(n_q, n_k, H, 6144, "NGT_MF_FWD_SPLIT");
+MfSplit mfma_fwd_split(int n_q, int n_k, int H, bool node_scores) {
+  const int64_t score_waves =
+      node_scores ? int64_t((n_k + kRowsPerBlock - 1) / kRowsPerBlock) * H * kWaves : 0;
+  return plan_split(n_q, n_k, H, 6144, score_waves, "NGT_MF_FWD_SPLIT");
 }
 MfSplit mfma_dq_split(int n_q, int n_k, int H) {
-  return plan_split(n_q, n_k, H, 12288, "NGT_MF_DQ_SPLIT");
+  return plan_split(n_q, n_k, H, 12288, 0, "NGT_MF_DQ_SPLIT");
 }
 
 template <int DH>
@@ -859,53 +923,58 @@ static int mf_fwd(const void* q, const void* k, const void* v, int n_q, int n_k,
   return NGT_OK;
 }
 
+// The backward in two launches: the dQ pass (which also stores D), then the
+// dK/dV pass (which reads it), carrying the dQ splits' merge in extra blocks.
 template <int DH>
-static int mf_bwd(const void* q, const void* k, const void* v, const void* g, const float* lse,
-                  const float* dsum, int n_q, int n_k, int H, float scale, const DropoutMask* dm,
-                  void* gq, void* gk, void* gv, MfSplit sq, float* part_dq, hipStream_t st) {
+static int mf_bwd(const void* q, const void* k, const void* v, const void* g, const void* out,
+                  const float* out32, const float* lse, float* dsum, int n_q, int n_k, int H,
+                  float scale, const DropoutMask* dm, void* gq, void* gk, void* gv, MfSplit sq,
+                  float* part_dq, hipStream_t st) {
   const DropoutMask m = dm ? *dm : DropoutMask{};
+  float* pdq = n_q > 0 && sq.n_split > 1 ? part_dq : nullptr;
+  if (n_q > 0) {
+    KernelTimer timer_("dense_bwd_q", st);
+    const dim3 grid((n_q + kRowsPerBlock - 1) / kRowsPerBlock, H, sq.n_split);
+    if (dm)
+      hipLaunchKernelGGL((k_mf_bwd_q<DH, true>), grid, dim3(kBlock), 0, st,
+                         static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
+                         static_cast<const bf16_t*>(v), static_cast<const bf16_t*>(g),
+                         static_cast<const bf16_t*>(out), out32, lse, dsum, n_q, n_k, H, scale, m,
+                         static_cast<bf16_t*>(gq), sq.split_keys, pdq);
+    else
+      hipLaunchKernelGGL((k_mf_bwd_q<DH, false>), grid, dim3(kBlock), 0, st,
+                         static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
+                         static_cast<const bf16_t*>(v), static_cast<const bf16_t*>(g),
+                         static_cast<const bf16_t*>(out), out32, lse, dsum, n_q, n_k, H, scale, m,
+                         static_cast<bf16_t*>(gq), sq.split_keys, pdq);
+    NGT_HIP_CHECK(hipGetLastError());
+  }
+  const int64_t n_dq = int64_t(n_q) * H * DH;
   if (n_k > 0) {
     KernelTimer timer_("dense_bwd_kv", st);
-    const dim3 grid((n_k + kRowsPerBlock - 1) / kRowsPerBlock, H);
+    const int kv_bx = (n_k + kRowsPerBlock - 1) / kRowsPerBlock;
+    // merge blocks per head: about 4 elements per thread
+    const int cbx = pdq ? int((n_dq + int64_t(4) * kBlock * H - 1) / (int64_t(4) * kBlock * H)) : 0;
+    const dim3 grid(kv_bx + cbx, H);
     if (dm)
       hipLaunchKernelGGL((k_mf_bwd_kv<DH, true>), grid, dim3(kBlock), 0, st,
                          static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
                          static_cast<const bf16_t*>(v), static_cast<const bf16_t*>(g), lse, dsum,
-                         n_q, n_k, H, scale, m, static_cast<bf16_t*>(gk),
-                         static_cast<bf16_t*>(gv));
+                         n_q, n_k, H, scale, m, static_cast<bf16_t*>(gk), static_cast<bf16_t*>(gv),
+                         kv_bx, cbx, pdq, sq.n_split, static_cast<bf16_t*>(gq));
     else
       hipLaunchKernelGGL((k_mf_bwd_kv<DH, false>), grid, dim3(kBlock), 0, st,
                          static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
                          static_cast<const bf16_t*>(v), static_cast<const bf16_t*>(g), lse, dsum,
-                         n_q, n_k, H, scale, m, static_cast<bf16_t*>(gk),
-                         static_cast<bf16_t*>(gv));
+                         n_q, n_k, H, scale, m, static_cast<bf16_t*>(gk), static_cast<bf16_t*>(gv),
+                         kv_bx, cbx, pdq, sq.n_split, static_cast<bf16_t*>(gq));
     NGT_HIP_CHECK(hipGetLastError());
-  }
-  if (n_q > 0) {
-    float* pdq = sq.n_split > 1 ? part_dq : nullptr;
-    {
-      KernelTimer timer_("dense_bwd_q", st);
-      const dim3 grid((n_q + kRowsPerBlock - 1) / kRowsPerBlock, H, sq.n_split);
-      if (dm)
-        hipLaunchKernelGGL((k_mf_bwd_q<DH, true>), grid, dim3(kBlock), 0, st,
-                           static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
-                           static_cast<const bf16_t*>(v), static_cast<const bf16_t*>(g), lse, dsum,
-                           n_q, n_k, H, scale, m, static_cast<bf16_t*>(gq), sq.split_keys, pdq);
-      else
-        hipLaunchKernelGGL((k_mf_bwd_q<DH, false>), grid, dim3(kBlock), 0, st,
-                           static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
-                           static_cast<const bf16_t*>(v), static_cast<const bf16_t*>(g), lse, dsum,
-                           n_q, n_k, H, scale, m, static_cast<bf16_t*>(gq), sq.split_keys, pdq);
-      NGT_HIP_CHECK(hipGetLastError());
-    }
-    if (pdq) {
-      KernelTimer timer_("dense_dq_combine", st);
-      const int64_t n = int64_t(n_q) * H * DH;
-      const unsigned blocks = unsigned(std::min<int64_t>((n + kBlock - 1) / kBlock, 65536));
-      hipLaunchKernelGGL(k_mf_dq_combine, dim3(blocks), dim3(kBlock), 0, st, pdq, sq.n_split, n,
-                         scale, static_cast<bf16_t*>(gq));
-      NGT_HIP_CHECK(hipGetLastError());
-    }
+  } else if (pdq) {  // no dK/dV launch to carry the merge
+    KernelTimer timer_("dense_dq_combine", st);
+    const unsigned blocks = unsigned(std::min<int64_t>((n_dq + kBlock - 1) / kBlock, 65536));
+    hipLaunchKernelGGL(k_mf_dq_combine, dim3(blocks), dim3(kBlock), 0, st, pdq, sq.n_split, n_dq,
+                       scale, static_cast<bf16_t*>(gq), int32_t(blocks));
+    NGT_HIP_CHECK(hipGetLastError());
   }
   return NGT_OK;
 }
@@ -923,16 +992,21 @@ int mfma_dense_fwd(int d, const void* q, const void* k, const void* v, int n_q, 
 }
 
 int mfma_dense_bwd(int d, const void* q, const void* k, const void* v, const void* g,
-                   const float* lse, const float* dsum, int n_q, int n_k, int H, float scale,
-                   const DropoutMask* dm, void* gq, void* gk, void* gv, MfSplit sq,
-                   float* part_dq, hipStream_t st) {
+                   const void* out, const float* out32, const float* lse, float* dsum, int n_q,
+                   int n_k, int H, float scale, const DropoutMask* dm, void* gq, void* gk, void* gv,
+                   MfSplit sq, float* part_dq, hipStream_t st) {
+#define NGT_MF_BWD(DH)                                                                      \
+  case DH:                                                                                  \
+    return mf_bwd<DH>(q, k, v, g, out, out32, lse, dsum, n_q, n_k, H, scale, dm, gq, gk, gv, \
+                      sq, part_dq, st);
   switch (d) {
-    case 8: return mf_bwd<8>(q, k, v, g, lse, dsum, n_q, n_k, H, scale, dm, gq, gk, gv, sq, part_dq, st);
-    case 16: return mf_bwd<16>(q, k, v, g, lse, dsum, n_q, n_k, H, scale, dm, gq, gk, gv, sq, part_dq, st);
-    case 24: return mf_bwd<24>(q, k, v, g, lse, dsum, n_q, n_k, H, scale, dm, gq, gk, gv, sq, part_dq, st);
-    case 32: return mf_bwd<32>(q, k, v, g, lse, dsum, n_q, n_k, H, scale, dm, gq, gk, gv, sq, part_dq, st);
+    NGT_MF_BWD(8)
+    NGT_MF_BWD(16)
+    NGT_MF_BWD(24)
+    NGT_MF_BWD(32)
     default: return set_error(NGT_ERR_UNSUPPORTED, "mfma dense: head_dim %d", d);
   }
+#undef NGT_MF_BWD
 }
 
 }  // namespace ngt
