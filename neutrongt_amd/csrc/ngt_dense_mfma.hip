@@ -313,6 +313,7 @@ __device__ __forceinline__ void mf_fwd_block(int bx, int h, int z, const bf16_t*
 #pragma unroll
   for (int j = 0; j < NC; ++j) split_scaled(qb[j], s2, qhi[j], qlo[j]);
   float m = -INFINITY, l = 0.f;
+  float thr = -INFINITY;   // rebase threshold on S s2 - m
   f32x16 base = zero16();  // -m once m is finite
   f32x16 acc = zero16();  // O^T[c][q]: c = 8*(i/4) + 4*half + i%4
 
@@ -354,16 +355,18 @@ __device__ __forceinline__ void mf_fwd_block(int bx, int h, int z, const bf16_t*
           mx = fmaxf(mx, st[i]);
         }
       }
-      mx = max_halves(mx);  // finite: the tile holds at least one key
       // The base m moves only when a column's maximum exceeds it by more
       // than kRebase (log2 units), so scores up to 2^kRebase times the base
       // enter P and the row sum as they are -- exact, since both share the
       // base -- and after the first tile (m unset, base 0) a wave rebases
       // only on a rare large jump instead of whenever any of its 32 columns
-      // finds a new maximum (most tiles).
-      const bool first = m == -INFINITY;
-      const float up = first ? mx : fmaxf(mx, 0.f);
-      if (__any(first || up > kRebase)) {
+      // finds a new maximum (most tiles).  The test needs no column maximum:
+      // some lane's own 16 scores exceed thr (-inf before the first tile,
+      // kRebase after it) exactly when some column's maximum does.
+      if (__any(mx > thr)) {
+        mx = max_halves(mx);  // the column's maximum; finite: the tile holds a key
+        const bool first = m == -INFINITY;
+        const float up = first ? mx : fmaxf(mx, 0.f);
         const float m_new = first ? mx : m + up;
         const float alpha = __builtin_amdgcn_exp2f(m - m_new);  // 0 for the first tile
         l *= alpha;
@@ -374,6 +377,7 @@ __device__ __forceinline__ void mf_fwd_block(int bx, int h, int z, const bf16_t*
         }
         m = m_new;
         base = fill16(-m);
+        thr = kRebase;
       }
       s16x4 pb[4], pm[4];
 #pragma unroll
