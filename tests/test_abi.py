@@ -96,11 +96,16 @@ def test_dense_workspace_query_depends_on_path_and_scores():
     assert fb.value == a256(8 * 300 * 4) and bb.value >= 300 * 8 * 4
     assert lib.ngt_dense_workspace_bytes(1, 300, 300, 8, 8, 0, C.byref(fb), C.byref(bb)) == 0
     assert fb.value == 0
-    # a large window splits its keys over blocks: the split states come on top
+    # a large window without node scores splits its keys over blocks (the split
+    # states: (m, l) and unnormalised O per split, query and head); with node
+    # scores their blocks share the launch and the forward takes one split
     assert lib.ngt_dense_workspace_bytes(1, 16000, 16000, 8, 8, 0, C.byref(fb), C.byref(bb)) == 0
-    no_ns = fb.value
+    n_split = 2
+    assert fb.value == a256(n_split * 16000 * 8 * 8) + a256(n_split * 16000 * 8 * 8 * 4)
     assert lib.ngt_dense_workspace_bytes(1, 16000, 16000, 8, 8, 1, C.byref(fb), C.byref(bb)) == 0
-    assert fb.value == no_ns + a256(8 * 16000 * 4)
+    assert fb.value == a256(8 * 16000 * 4)
+    # the backward: D per query and head, then three key splits' partial dQ
+    assert bb.value == a256(16000 * 8 * 4) + a256(3 * 16000 * 8 * 8 * 4)
     assert lib.ngt_dense_workspace_bytes(0, 500, 300, 2, 8, 1, C.byref(fb), C.byref(bb)) == 0
     with_ns = fb.value
     assert lib.ngt_dense_workspace_bytes(0, 500, 300, 2, 8, 0, C.byref(fb), C.byref(bb)) == 0
