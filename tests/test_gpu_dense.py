@@ -305,3 +305,57 @@ def test_flash_branch_gt_twin_layout():
     from neutrongt_amd import install
     h = Holder()
     assert install(h) == 1 and h.local_attn.flash_layout == "gt_twin"
+
+
+def _abi_fwd_bwd(q, k, v, go, keep_f32):
+    """ngt_dense_fwd / ngt_dense_bwd through the C ABI, bf16, no node scores.
+    keep_f32: the forward writes an fp32 copy of the output and the backward
+    takes D = G . o from it; otherwise the backward gets the bf16 output only."""
+    import ctypes as C
+
+    from neutrongt_amd import _lib
+    lib = _lib.load()
+    qd, kd, vd, gd = (t.cuda().contiguous() for t in (q, k, v, go))
+    n_q, H, d = q.shape
+    n_k = k.shape[0]
+    scale = float(d) ** 0.5
+    st = _lib.stream_ptr(qd.device)
+    out = torch.empty_like(qd)
+    out32 = torch.empty(n_q, H, d, dtype=torch.float32, device="cuda") if keep_f32 else None
+    lse = torch.empty(H, n_q, dtype=torch.float32, device="cuda")
+    fb, bb = C.c_size_t(), C.c_size_t()
+    _lib.check(lib.ngt_dense_workspace_bytes(_lib.NGT_BF16, n_q, n_k, H, d, 0, C.byref(fb),
+                                             C.byref(bb)))
+    wf = torch.empty(max(fb.value, 1), dtype=torch.uint8, device="cuda")
+    wb = torch.empty(max(bb.value, 1), dtype=torch.uint8, device="cuda")
+    _lib.check(lib.ngt_dense_fwd(_lib.NGT_BF16, qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), n_q,
+                                 n_k, H, d, scale, 0.0, 0, None, out.data_ptr(),
+                                 out32.data_ptr() if keep_f32 else None, lse.data_ptr(), None,
+                                 wf.data_ptr(), fb.value, st))
+    gq, gk, gv = torch.empty_like(qd), torch.empty_like(kd), torch.empty_like(vd)
+    _lib.check(lib.ngt_dense_bwd(_lib.NGT_BF16, qd.data_ptr(), kd.data_ptr(), vd.data_ptr(),
+                                 None if keep_f32 else out.data_ptr(),
+                                 out32.data_ptr() if keep_f32 else None, gd.data_ptr(),
+                                 lse.data_ptr(), n_q, n_k, H, d, scale, 0.0, 0, None,
+                                 gq.data_ptr(), gk.data_ptr(), gv.data_ptr(), wb.data_ptr(),
+                                 bb.value, st))
+    torch.cuda.synchronize()
+    return {"x": out.cpu(), "dq": gq.cpu(), "dk": gk.cpu(), "dv": gv.cpu()}
+
+
+@pytest.mark.parametrize("n_q,n_k,H,d", [(300, 2100, 4, 16), (130, 97, 2, 8), (64, 1500, 3, 32)])
+def test_dense_bf16_backward_from_the_bf16_output(n_q, n_k, H, d):
+    """The matrix-core dQ pass forms D = G . o itself: from the forward's fp32
+    copy of the output when the caller kept one, else from the bf16 output
+    (the C ABI allows either).  Both against the restatement; the long key
+    ranges run the forward's and the dQ pass's key splits, the latter merged
+    by extra blocks of the dK/dV launch."""
+    _say(f"case dense bf16 D from bf16 out n_q={n_q} n_k={n_k} H={H} d={d}")
+    q, k, v, go = _qkv(n_q, n_k, H, d, torch.bfloat16, seed=n_k + d)
+    ref = OA.full_fwd_bwd(q.float(), k.float(), v.float(), go.float())
+    ref64 = OA.full_fwd_bwd(q.double(), k.double(), v.double(), go.double(), dtype=torch.float64)
+    for keep in (True, False):
+        res = _abi_fwd_bwd(q, k, v, go, keep)
+        for name in ("x", "dq", "dk", "dv"):
+            assert_parity(res[name].float(), ref[name], ref64[name], torch.bfloat16,
+                          f"{name} keep_f32={keep}")
