@@ -14,11 +14,14 @@
 // its rows feeds the next MFMA as B without any data movement.
 //
 // Forward, per (head, 32 queries): S^T = K Q^T (rows = keys, cols = queries),
-// online softmax per query column (in-lane over 16 keys + one lane^32 swap),
-// O^T += V^T P^T with V^T staged in LDS.  Backward: key-major dK/dV (S and dP
-// recomputed as D[q][key], dV += P^T G and dK += dS^T Q with Q/G tiles staged
-// in LDS) and query-major dQ (dQ += dS K with K staged in LDS).  Column scores
-// sum_i |S| come from a separate key-major pass (S tiles again on MFMA).
+// online softmax per query column (in-lane over 16 keys; the column maximum
+// over both wave halves only when the base moves), O^T += V^T P^T with V^T
+// staged in LDS.  Column scores sum_i |S| come from key-major blocks in the
+// same launch (S tiles again on MFMA).  Backward, in this order: query-major
+// dQ (dQ += dS K with K staged in LDS; it also forms each query's D = G . o)
+// and key-major dK/dV (S and dP recomputed as D[q][key], dV += P^T G and
+// dK += dS^T Q with Q/G tiles staged in LDS; extra blocks merge the dQ key
+// splits).
 // Per-score arithmetic rides in the MFMAs: the softmax scale as a hi/lo bf16
 // pair of the per-lane operand (split_scaled), the per-query -lse, -D and the
 // forward's running maximum as accumulator inputs or as one more K step of
