@@ -545,7 +545,7 @@ __device__ __forceinline__ void dq_combine(const float* __restrict__ part, int n
 // D[q][key]; Q and G stages of 128 queries in LDS, row-major (A operands of S
 // and dP) and transposed (B operands of dV += P^T G and dK += dS^T Q).
 //
-// Blocks with wg_x() >= kv_bx do not take keys: with a split dQ pass
+// Blocks at grid x >= kv_bx do not take keys: with a split dQ pass
 // (part_dq set) they add its partial dQ in split order into grad_q, so that
 // merge rides in this launch instead of a launch of its own.
 template <int DH, bool DROP>
@@ -868,7 +868,7 @@ bool mfma_dense_supported(int d) { return d == 8 || d == 16 || d == 24 || d == 3
 // Key splits: the forward (one wave per 32 queries and head, all keys) and
 // the dQ pass have grids of ceil(n_q / 32) * H waves, about 4 per SIMD at
 // 16,000 queries and 8 heads, while their registers leave room for more.
-// Splitting the keys over wg_z() raises the waves per SIMD; each split's
+// Splitting the keys over the grid's z dimension raises the waves per SIMD; each split's
 // state is merged afterwards in split order.  Measured at 16,000 nodes, 8
 // heads, d = 8 with the per-score arithmetic in the MFMAs (us per launch):
 // forward alone 331 / 325 / 324 / 329 / 334 at 2 / 3 / 4 / 6 / 8 splits plus a
@@ -876,10 +876,11 @@ bool mfma_dense_supported(int d) { return d == 8 || d == 16 || d == 24 || d == 3
 // the column-score blocks share the forward's launch they bring as many waves
 // again, and one split is best: 384 us for forward and scores against 392 us
 // plus the combine at 2 splits.  `shared_waves` counts such other waves.
-// What bounds these kernels is each wave's chain MFMA -> exp -> pack -> MFMA
-// per tile with 4-5 waves per SIMD; issuing the next tile's products ahead of
-// the current tile's softmax work costs registers (one wave less per SIMD)
-// and measured slower: forward 406 -> 432 us, dK/dV 479 -> 585 us.
+// What bounds these kernels is the per-score VALU work (an exponential, a
+// pack and, in the backward, a product per score) at 4-5 waves per SIMD;
+// issuing the next tile's products ahead of the current tile's softmax work
+// costs registers (one wave less per SIMD) and measured slower: forward
+// 406 -> 432 us, dK/dV 479 -> 585 us.
 // NGT_MF_FWD_SPLIT / NGT_MF_DQ_SPLIT override the count.
 static MfSplit plan_split(int n_q, int n_k, int H, int target_waves, int64_t shared_waves,
                           const char* env) {
