@@ -305,9 +305,11 @@ int ngt_dense_abs_colsum(int32_t n_heads, int32_t n_q, int32_t n_k, const float*
  * same dtype, sizes and node_scores (non-zero when node_score will be passed).
  * The forward uses it for node-score partials (H * n_k floats on the bf16
  * matrix-core path, d <= 32; per-block partials on the vector-ALU kernels)
- * and, on the vector-ALU kernels (fp32; bf16 at head_dim 64), for per-split
- * softmax states when it splits the keys of a large window over several
- * blocks; a size of 0 means none is needed.
+ * and for per-split softmax states when it splits the keys of a large window
+ * over several blocks (the vector-ALU kernels, fp32 and bf16 at head_dim 64;
+ * the matrix-core path when no node scores are asked for); a size of 0 means
+ * none is needed.  The backward uses it for D per query and head and, on the
+ * matrix-core path, for the partial dQ of its key splits.
  * seed_dev (may be NULL): a device uint64 the kernels read the seed from when
  * they start, instead of `seed`; a captured HIP graph that rewrites it before
  * each replay draws a new mask per replay.  Forward and backward must see the
