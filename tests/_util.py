@@ -52,16 +52,18 @@ def hub_coo(n_q: int, n_k: int, hub_deg: int, seed: int = 0):
 
 
 def assert_parity(ours, ref32, ref64, dtype, what=""):
-    """Parity with the fp32 oracle at the stated tolerance -- or, where the fp32
-    oracle itself is farther than that from the float64 truth (ill-conditioned
-    cases, e.g. the dense path's x sqrt(d) logits at d = 64), at most 3x the
-    oracle's own fp32 error, and no farther from the truth than that."""
+    """Parity with the fp32 oracle at the stated tolerance.  Where the fp32
+    oracle is itself more than a third of that tolerance from the float64 truth
+    (ill-conditioned cases, e.g. the dense path's x sqrt(d) logits at d >= 24),
+    the result is measured against the float64 truth instead, at the same
+    tolerance -- unless even the fp32 oracle misses it there, and then at 1.25x
+    the oracle's own error."""
     tol = TOL[dtype]
     own = relerr(ref32, ref64) if ref64 is not None else 0.0
     if own * 3 <= tol or ref64 is None:
         assert_close(ours, ref32, dtype, what)
         return
-    e32 = relerr(ours, ref32)
     e64 = relerr(ours, ref64)
-    assert e32 <= 3 * own and e64 <= 3 * own, (
-        f"{what}: err vs fp32 oracle {e32:.3e}, vs fp64 {e64:.3e}, oracle's own {own:.3e}")
+    bar = max(tol, 1.25 * own)
+    assert e64 <= bar, (
+        f"{what}: err vs fp64 {e64:.3e} > {bar:.3e} (fp32 oracle's own {own:.3e})")
