@@ -231,10 +231,20 @@ def ppr_bench(args, cfg, dev) -> dict:
     from neutrongt_amd import synthetic as S
 
     n = cfg.n_global
-    u, v = S.chung_lu_edges(n, cfg.mean_degree, cfg.gamma, S.SEED)
+    cap = args.ppr_degree_cap
+    t0 = time.perf_counter()
+    u, v = S.chung_lu_edges(n, cfg.mean_degree, cfg.gamma, S.SEED, degree_cap=cap)
+    if args.ppr_relabel:
+        # the same graph under a seeded random node numbering: the generator
+        # numbers nodes by decreasing weight, so the top-k's ties (lowest id
+        # first) would otherwise always land on the largest hubs
+        perm = np.random.default_rng(S.SEED + 1).permutation(n).astype(np.int64)
+        u, v = perm[u], perm[v]
     ei = torch.from_numpy(np.stack([np.concatenate([u, v]), np.concatenate([v, u])]))
+    _log(f"[bench] ppr: graph drawn in {time.perf_counter() - t0:.1f} s")
     alpha, topk, iters, batch = 0.85, 5, 10, 8192
     rowptr, col, inv_deg, _ = PPR.transition_csr(ei, num_nodes=n, device=dev)
+    deg_max = int((rowptr[1:] - rowptr[:-1]).max().item()) if n else 0
     csr = {"rowptr": rowptr, "col": col}
     _log(f"[bench] ppr: graph n={n}, {int(col.numel())} directed edges; topk {topk}, "
          f"{iters} iterations, batches of {batch}")
@@ -242,12 +252,22 @@ def ppr_bench(args, cfg, dev) -> dict:
     PPR.personal_pagerank_appnp(None, alpha, topk=topk, num_iterations=iters, batch_size=batch,
                                 device=dev, csr_data=csr, iter_topk=topk, source_end=batch)
     torch.cuda.synchronize()
+    # all seeds, in chunks of 32 batches with a progress line after each (the
+    # rows are independent, so chunking changes nothing but the logging)
+    chunk = 32 * batch
+    idx_parts, val_parts = [], []
     t = time.perf_counter()
-    idx, val = PPR.personal_pagerank_appnp(None, alpha, topk=topk, num_iterations=iters,
-                                           batch_size=batch, device=dev, csr_data=csr,
-                                           iter_topk=topk)
-    torch.cuda.synchronize()
+    for s0 in range(0, n, chunk):
+        i_c, v_c = PPR.personal_pagerank_appnp(None, alpha, topk=topk, num_iterations=iters,
+                                               batch_size=batch, device=dev, csr_data=csr,
+                                               iter_topk=topk, source_start=s0,
+                                               source_end=min(s0 + chunk, n))
+        idx_parts.append(i_c)
+        val_parts.append(v_c)
+        torch.cuda.synchronize()
+        _log(f"[bench] ppr: seeds {min(s0 + chunk, n)}/{n} after {time.perf_counter() - t:.1f} s")
     t_gpu = time.perf_counter() - t
+    idx, val = torch.cat(idx_parts, dim=1), torch.cat(val_parts)
     _log(f"[bench] ppr: {t_gpu * 1e3:.1f} ms for {n} seeds ({int(idx.shape[1])} entries)")
     cpu = None
     if not args.no_cpu:
@@ -256,22 +276,37 @@ def ppr_bench(args, cfg, dev) -> dict:
         rp, cl, iv = rowptr.cpu().numpy(), col.cpu().numpy(), inv_deg.cpu().numpy()
         sample = np.random.default_rng(S.SEED).choice(n, 200, replace=False)
         t = time.perf_counter()
-        for sd in sample.tolist():
-            OP.appnp_row(rp, cl, iv, sd, alpha, topk, iters)
+        rows = [OP.appnp_row(rp, cl, iv, sd, alpha, topk, iters) for sd in sample.tolist()]
         t_s = time.perf_counter() - t
+        # the same seeds' rows of the GPU result, checked against the oracle's
+        # (entries in rank order; nodes and fp32 values bit for bit)
+        src, dst, vv = idx[0].cpu().numpy(), idx[1].cpu().numpy(), val.cpu().numpy()
+        starts = np.searchsorted(src, sample, side="left")
+        ends = np.searchsorted(src, sample, side="right")
+        exact = sum(
+            [int(c) for c, _ in row] == dst[a:b].tolist()
+            and np.array([w for _, w in row], np.float32).tobytes() == vv[a:b].tobytes()
+            for row, a, b in zip(rows, starts, ends))
         cpu = {"value": t_s / sample.size * n * 1e3, "unit": "ms", "cores": 1, "kind": "port",
                "sample": (f"the oracle's restatement on 200 seeded random seeds ({t_s:.1f} s), "
-                          f"scaled to all {n} seeds")}
-        _log(f"[bench] ppr cpu baseline {cpu['value'] / 1e3:.1f} s (extrapolated)")
+                          f"scaled to all {n} seeds"),
+               "rows_bit_exact": f"{exact}/{sample.size}"}
+        _log(f"[bench] ppr cpu baseline {cpu['value'] / 1e3:.1f} s (extrapolated); "
+             f"{exact}/{sample.size} sampled rows bit-exact against the oracle")
     return {
         "metric": "personalised PageRank preprocessing time (APPNP, top-5, 10 iterations)",
         "value": t_gpu * 1e3, "unit": "ms", "n_gpus": 1, "steps": 1, "warmup": 1,
         "ms_per_step": t_gpu * 1e3, "higher_is_better": False, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": (f"{cfg.name} global graph: Chung-Lu n={n}, "
-                                f"{int(col.numel())} directed edges, alpha {alpha}, top-{topk}, "
-                                f"{iters} iterations, batches of {batch} seeds"),
-                   "entries": int(idx.shape[1])},
+                                f"{int(col.numel())} directed edges"
+                                + (f" (expected degrees capped at {cap:g})" if cap else "")
+                                + (", nodes randomly relabelled" if args.ppr_relabel else "")
+                                + f", alpha {alpha}, top-{topk}, {iters} iterations, "
+                                f"batches of {batch} seeds"),
+                   "entries": int(idx.shape[1]), "degree_cap": cap,
+                   "relabelled": bool(args.ppr_relabel),
+                   "max_degree": int(deg_max)},
         "cpu_baseline": cpu,
     }
 
@@ -543,6 +578,12 @@ def main(argv=None) -> int:
     ap.add_argument("--ppr", action="store_true",
                     help="time the personalised-PageRank preprocessing instead (APPNP, top-5, "
                          "10 iterations, batches of 8192 seeds) on the config's global graph")
+    ap.add_argument("--ppr-degree-cap", type=float, default=None,
+                    help="with --ppr: cap the global graph's expected node degrees (e.g. 17481, "
+                         "ogbn-products' largest degree); default uncapped")
+    ap.add_argument("--ppr-relabel", action="store_true",
+                    help="with --ppr: number the global graph's nodes by a seeded random "
+                         "permutation (the generator numbers them by decreasing degree)")
     ap.add_argument("--prep", action="store_true",
                     help="time the window assembly instead (related nodes, induced subgraph, "
                          "window CSR, feature gather) on the config's global graph")

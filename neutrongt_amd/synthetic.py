@@ -59,21 +59,34 @@ CONFIGS = {
 
 
 def chung_lu_edges(n: int, mean_degree: float, gamma: float = 2.1, seed: int = SEED,
-                   tol: float = 0.02, max_iter: int = 12):
+                   tol: float = 0.02, max_iter: int = 12, degree_cap: float | None = None):
     """Undirected Chung-Lu graph: weights (i+1)^(-1/(gamma-1)); m endpoint pairs
     drawn i.i.d. proportional to weight, self pairs dropped, deduplicated; m is
     recalibrated until the realised mean degree is within ``tol`` of the target
-    (or max_iter).  Returns (u, v) int64 arrays with u < v, sorted."""
+    (or max_iter).  ``degree_cap`` flattens the largest weights so that no node
+    expects more than about that many neighbours (None: uncapped, the default).
+    Returns (u, v) int64 arrays with u < v, sorted."""
     if n <= 1 or mean_degree <= 0:
         z = np.zeros(0, np.int64)
         return z, z
     rng = np.random.default_rng(seed)
     w = (np.arange(n, dtype=np.float64) + 1.0) ** (-1.0 / (gamma - 1.0))
-    cdf = np.cumsum(w / w.sum())
-    cdf[-1] = 1.0
     # at most half of the n(n-1)/2 possible pairs: beyond that the dedup
     # saturates and the recalibration below would grow m without bound
     target = min(n * mean_degree / 2.0, n * (n - 1) / 4.0)
+    if degree_cap is not None and 2.0 * target * w[0] / w.sum() > degree_cap:
+        # node i expects about 2 m w_i / sum(w) endpoints: find the weight
+        # ceiling c that gives the heaviest node degree_cap (monotone in c)
+        lo, hi = 0.0, float(w[0])
+        for _ in range(100):
+            c = 0.5 * (lo + hi)
+            if 2.0 * target * c / np.minimum(w, c).sum() > degree_cap:
+                hi = c
+            else:
+                lo = c
+        w = np.minimum(w, lo)
+    cdf = np.cumsum(w / w.sum())
+    cdf[-1] = 1.0
     m = max(int(target), 1)
     m_cap = 64 * m + 1024
     best = None
