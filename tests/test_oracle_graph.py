@@ -246,3 +246,23 @@ def test_subgraph_coo_matches_brute_force(seed):
     where = {int(g): i for i, g in enumerate(subset)}
     want = [(where[int(a)], where[int(b)]) for a, b in ei.T if int(a) in where and int(b) in where]
     assert OG.subgraph_coo(subset, ei, n).T.tolist() == [list(t) for t in want]
+
+
+def test_chung_lu_degree_cap():
+    """The generator's degree cap flattens only the heaviest weights: without
+    it the draw is unchanged (the benchmark windows depend on that), with it
+    the largest degree drops to about the cap while the mean degree holds."""
+    from neutrongt_amd import synthetic as S
+    n, mean = 20000, 14.0
+    u0, v0 = S.chung_lu_edges(n, mean, 2.1, S.SEED)
+    u1, v1 = S.chung_lu_edges(n, mean, 2.1, S.SEED, degree_cap=None)
+    assert np.array_equal(u0, u1) and np.array_equal(v0, v1)
+    d0 = np.bincount(np.concatenate([u0, v0]), minlength=n)
+    u2, v2 = S.chung_lu_edges(n, mean, 2.1, S.SEED, degree_cap=200)
+    d2 = np.bincount(np.concatenate([u2, v2]), minlength=n)
+    assert d0.max() > 1000 and d2.max() < 1.3 * 200
+    assert abs(d2.mean() - mean) < 0.05 * mean
+    assert np.all(u2 < v2)
+    # a cap above the heaviest expected degree changes nothing
+    u3, v3 = S.chung_lu_edges(n, mean, 2.1, S.SEED, degree_cap=1e9)
+    assert np.array_equal(u0, u3) and np.array_equal(v0, v3)
