@@ -304,9 +304,12 @@ __global__ __launch_bounds__(kBlock) void k_fwd(
   constexpr int NV = RowWords<T, DH>::NV;
   constexpr int U = unroll_for(2 * NV, NGT_FWD_WORDS);
   const int lane = threadIdx.x & (kWave - 1);
+  // each 64-edge block's column indices are requested one block ahead
+  int nx_j = lane < it.z - it.y ? col[it.y + lane] : 0;
   for (int blk = it.y; blk < it.z; blk += kWave) {
     const int nb = min(kWave, it.z - blk);
-    const int my_j = lane < nb ? col[blk + lane] : 0;
+    const int my_j = nx_j;
+    nx_j = lane < it.z - blk - kWave ? col[blk + kWave + lane] : 0;
     for (int t0 = 0; t0 < nb; t0 += S * U) {
       RowWords<T, DH> kw[U], vw[U];
       bool ok[U];
@@ -557,9 +560,12 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
   constexpr int NV = RowWords<T, DH>::NV;
   constexpr int U = unroll_for(2 * NV, NGT_BWD_KV_WORDS);
   const int lane = threadIdx.x & (kWave - 1);
+  // each 64-edge block's row indices are requested one block ahead
+  int nx_i = lane < it.z - it.y ? t_col[it.y + lane] : 0;
   for (int blk = it.y; blk < it.z; blk += kWave) {
     const int nb = min(kWave, it.z - blk);
-    const int my_i = lane < nb ? t_col[blk + lane] : 0;
+    const int my_i = nx_i;
+    nx_i = lane < it.z - blk - kWave ? t_col[blk + kWave + lane] : 0;
     for (int t0 = 0; t0 < nb; t0 += S * U) {
       RowWords<T, DH> qw[U], gw[U];
       float2 r[U];
@@ -736,10 +742,14 @@ __global__ __launch_bounds__(kBlock) void k_bwd_q(
   constexpr int NV = RowWords<T, DH>::NV;
   constexpr int U = unroll_for(NV, NGT_BWD_Q_WORDS);
   const int lane = threadIdx.x & (kWave - 1);
+  // each 64-edge block's column and key-major indices are requested one block ahead
+  int nx_j = lane < it.z - it.y ? col[it.y + lane] : 0;
+  int nx_t = lane < it.z - it.y ? q2t[it.y + lane] : 0;
   for (int blk = it.y; blk < it.z; blk += kWave) {
     const int nb = min(kWave, it.z - blk);
-    const int my_j = lane < nb ? col[blk + lane] : 0;
-    const int my_t = lane < nb ? q2t[blk + lane] : 0;
+    const int my_j = nx_j, my_t = nx_t;
+    nx_j = lane < it.z - blk - kWave ? col[blk + kWave + lane] : 0;
+    nx_t = lane < it.z - blk - kWave ? q2t[blk + kWave + lane] : 0;
     for (int t0 = 0; t0 < nb; t0 += S * U) {
       RowWords<T, DH> kw[U];
       float dsv[U];
