@@ -262,7 +262,8 @@ int ngt_edge_bias_grad(const ngt_window_csr* csr, int32_t n_heads, const float* 
  *   (bias nullable: the sum of attn_bias and pruning_mask; mask nullable,
  *   uint8 [n_q, n_k], nonzero = filled); p = softmax_j(z); pd = p o M with
  *   the dropout multiplier of ngt_dense_fwd (same seed, same mask; pd only
- *   with dropout_p > 0); lse [H, n_q] = max + log(sum).
+ *   with dropout_p > 0); lse [H, n_q] = max + log(sum).  n_heads * n_q must
+ *   not exceed 2^24 (NGT_ERR_ARG), here and in the backward.
  * ngt_dense_bias_softmax_bwd: with dpd = dL/d(p o M): dP = M o dpd,
  *   D_i = sum_j p dP, ds = p o (dP - D), 0 where masked.  ds is also the
  *   gradient of bias (and so of attn_bias and pruning_mask).

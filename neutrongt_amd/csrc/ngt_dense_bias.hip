@@ -16,6 +16,9 @@ namespace {
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / kWave;
 constexpr float kMasked = -1e9f;  // masked_fill value of the reference
+// Rows (head, query) of the softmax kernels: one block each, and a dispatch
+// holds fewer than 2^32 work-items.
+constexpr int64_t kMaxRows = int64_t(1) << 24;
 constexpr int kColChunks = 64;    // row chunks of the column sums
 
 __device__ __forceinline__ float wave_max(float x) {
@@ -163,6 +166,9 @@ extern "C" int ngt_dense_bias_softmax_fwd(int32_t n_heads, int32_t n_q, int32_t 
                                           float* lse, void* stream) {
   if (n_heads < 1 || n_q < 0 || n_k < 0)
     return set_error(NGT_ERR_ARG, "ngt_dense_bias_softmax_fwd: bad sizes");
+  if (int64_t(n_heads) * n_q > kMaxRows)  // one block of kBlock work-items per row
+    return set_error(NGT_ERR_ARG, "ngt_dense_bias_softmax_fwd: n_heads * n_q > %lld",
+                     static_cast<long long>(kMaxRows));
   DropoutMask dm{};
   bool drop = false;
   NGT_CHECK_OK(make_dropout("ngt_dense_bias_softmax_fwd", dropout_p, seed, seed_dev, n_q, n_k, &dm,
@@ -188,6 +194,9 @@ extern "C" int ngt_dense_bias_softmax_bwd(int32_t n_heads, int32_t n_q, int32_t 
                                           const uint64_t* seed_dev, float* ds, void* stream) {
   if (n_heads < 1 || n_q < 0 || n_k < 0)
     return set_error(NGT_ERR_ARG, "ngt_dense_bias_softmax_bwd: bad sizes");
+  if (int64_t(n_heads) * n_q > kMaxRows)  // one block of kBlock work-items per row
+    return set_error(NGT_ERR_ARG, "ngt_dense_bias_softmax_bwd: n_heads * n_q > %lld",
+                     static_cast<long long>(kMaxRows));
   DropoutMask dm{};
   bool drop = false;
   NGT_CHECK_OK(make_dropout("ngt_dense_bias_softmax_bwd", dropout_p, seed, seed_dev, n_q, n_k, &dm,

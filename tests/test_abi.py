@@ -81,6 +81,13 @@ def test_argument_errors_are_reported_without_touching_the_gpu():
         rc = lib.ngt_dense_bwd(1, None, None, None, None, None, None, None, 0, 0, 1, 8, sc, 0.0,
                                0, None, None, None, None, None, 0, None)
         assert rc == 1 and b"scale" in lib.ngt_last_error()
+    # the optional-terms softmax runs one block per (head, query) row: more
+    # than 2^24 rows are refused before anything launches
+    rc = lib.ngt_dense_bias_softmax_fwd(256, 65537, 8, None, 1.0, None, None, 0.0, 0, None, None,
+                                        None, None, None)
+    assert rc == 1 and b"n_heads * n_q" in lib.ngt_last_error()
+    rc = lib.ngt_dense_bias_softmax_bwd(256, 65537, 8, None, None, None, 0.0, 0, None, None, None)
+    assert rc == 1 and b"n_heads * n_q" in lib.ngt_last_error()
     with pytest.raises(_lib.NGTError):
         _lib.check(1)
 
