@@ -308,6 +308,7 @@ def ppr_bench(args, cfg, dev) -> dict:
                    "relabelled": bool(args.ppr_relabel),
                    "max_degree": int(deg_max)},
         "cpu_baseline": cpu,
+        "also": also,
     }
 
 
@@ -443,6 +444,7 @@ def prep_bench(args, cfg, dev) -> dict:
                    "window_nodes": n_w, "window_edges": int(sub_csr.shape[1])},
         "ops": ops,
         "cpu_baseline": cpu,
+        "also": also,
     }
 
 
@@ -558,51 +560,11 @@ def model_step_bench(args, cfg, layers: int, dev) -> dict:
     }
 
 
-def main(argv=None) -> int:
-    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--min-warmup-ms", type=float, default=300.0,
-                    help="keep taking untimed warm-up steps past --warmup until this much time "
-                         "has passed (0: exactly --warmup)")
-    ap.add_argument("--config", default="gph_large",
-                    help="gph_large (default), gph_slim, gt_arxiv, gt_highdeg, dense_slim, "
-                         "dense_slim_f32")
-    ap.add_argument("--layers", type=int, default=None, help="override the layer count")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--calib-copy", action="store_true",
-                    help="run one 512 MiB device copy first (calibrates HBM byte counters)")
-    ap.add_argument("--graph", action="store_true",
-                    help="capture one step (all layers, fwd+bwd) in a HIP graph and time replays")
-    ap.add_argument("--ppr", action="store_true",
-                    help="time the personalised-PageRank preprocessing instead (APPNP, top-5, "
-                         "10 iterations, batches of 8192 seeds) on the config's global graph")
-    ap.add_argument("--ppr-degree-cap", type=float, default=None,
-                    help="with --ppr: cap the global graph's expected node degrees (e.g. 17481, "
-                         "ogbn-products' largest degree); default uncapped")
-    ap.add_argument("--ppr-relabel", action="store_true",
-                    help="with --ppr: number the global graph's nodes by a seeded random "
-                         "permutation (the generator numbers them by decreasing degree)")
-    ap.add_argument("--prep", action="store_true",
-                    help="time the window assembly instead (related nodes, induced subgraph, "
-                         "window CSR, feature gather) on the config's global graph")
-    ap.add_argument("--tunable", default=None, metavar="CSV",
-                    help="with --model: let torch's TunableOp pick the GEMM kernels, reading "
-                         "(and, if missing, writing) this results file")
-    ap.add_argument("--model", action="store_true",
-                    help="time the whole window training step instead (encoder projections, "
-                         "LayerNorm, FFN and attention, NLL, backward, AdamW) in bf16 autocast")
-    args = ap.parse_args(argv)
-
-    world = int(os.environ.get("WORLD_SIZE", "1"))
-    if args.gpus != 1 or world != 1:
-        print("bench.py measures one GPU only: this build runs the attention path on a single "
-              "MI355X (window sharding across GPUs is not part of it); use --gpus 1.",
-              file=sys.stderr)
-        return 2
-
-    import numpy as np
+def measure_window(args, cfg, layers: int, dev, graph: bool, calib_copy: bool) -> dict:
+    """Time `layers` layers of the window attention fwd+bwd on `cfg` (W warm-up
+    steps, then exactly K timed steps between events on the current stream),
+    then the same steps again with the library's per-launch hipEvents; returns
+    the step time, edges/s, per-kernel times and the dominant kernel's roofline."""
     import torch
 
     from neutrongt_amd import _lib, chunk_for_heads, small_for_heads
@@ -610,30 +572,6 @@ def main(argv=None) -> int:
     from neutrongt_amd.attention import DenseAttentionFunction, window_attention
     from neutrongt_amd.csr import WindowAdjacency
 
-    cfg = S.CONFIGS[args.config]
-    layers = args.layers or cfg.layers
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    if args.ppr:
-        if cfg.dense or not cfg.n_global:
-            print("--ppr needs a sparse config with a global graph (gt_arxiv, gt_highdeg, "
-                  "gph_large)", file=sys.stderr)
-            return 2
-        print(json.dumps(ppr_bench(args, cfg, dev)), flush=True)
-        return 0
-    if args.prep:
-        if cfg.dense or not cfg.n_global:
-            print("--prep needs a sparse config with a global graph (gph_large, gt_arxiv, "
-                  "gt_highdeg)", file=sys.stderr)
-            return 2
-        print(json.dumps(prep_bench(args, cfg, dev)), flush=True)
-        return 0
-    if args.model:
-        if cfg.dense:
-            print("--model runs the sparse window encoder; pick a sparse --config", file=sys.stderr)
-            return 2
-        print(json.dumps(model_step_bench(args, cfg, layers, dev)), flush=True)
-        return 0
     H, d = cfg.n_heads, cfg.head_dim
     scale = math.sqrt(d)
 
@@ -681,7 +619,7 @@ def main(argv=None) -> int:
             grads.append(go)
         torch.autograd.backward(outs, grads)
 
-    if args.calib_copy:
+    if calib_copy:
         src = torch.empty(256 << 20, dtype=torch.int16, device=dev).fill_(1)
         dst = torch.empty_like(src)
         torch.cuda.synchronize()
@@ -702,7 +640,7 @@ def main(argv=None) -> int:
     torch.cuda.synchronize()
     warm_ms = (time.perf_counter() - t_w) * 1e3
     run = step
-    if args.graph:
+    if graph:
         # Same kernels, launched from one captured graph (no per-launch host work).
         side = torch.cuda.Stream(dev)
         side.wait_stream(torch.cuda.current_stream(dev))
@@ -763,6 +701,109 @@ def main(argv=None) -> int:
                 "frac": pb * layers / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS}
     _log(f"[bench] kernels: " + ", ".join(f"{n} {v['avg_us']:.1f}us x{v['launches']}"
                                           for n, v in sorted(kernels.items())))
+    return {"ms_step": ms_step, "value": value, "kernels": kernels, "roof": roof, "path": path,
+            "n_k": n_k, "E": E, "csr_ms": csr_ms, "warm_steps": warm_steps,
+            "warm_ms": warm_ms, "ei_np": ei_np}
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--min-warmup-ms", type=float, default=300.0,
+                    help="keep taking untimed warm-up steps past --warmup until this much time "
+                         "has passed (0: exactly --warmup)")
+    ap.add_argument("--config", default="gph_large",
+                    help="gph_large (default), gph_slim, gt_arxiv, gt_highdeg, dense_slim, "
+                         "dense_slim_f32")
+    ap.add_argument("--layers", type=int, default=None, help="override the layer count")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--also", default=None,
+                    help="a second window timed the same way and reported under 'also' "
+                         "(default: gph_slim when the config is gph_large, the metric's other "
+                         "workload; 'none' for no second window)")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="run one 512 MiB device copy first (calibrates HBM byte counters)")
+    ap.add_argument("--graph", action="store_true",
+                    help="capture one step (all layers, fwd+bwd) in a HIP graph and time replays")
+    ap.add_argument("--ppr", action="store_true",
+                    help="time the personalised-PageRank preprocessing instead (APPNP, top-5, "
+                         "10 iterations, batches of 8192 seeds) on the config's global graph")
+    ap.add_argument("--ppr-degree-cap", type=float, default=None,
+                    help="with --ppr: cap the global graph's expected node degrees (e.g. 17481, "
+                         "ogbn-products' largest degree); default uncapped")
+    ap.add_argument("--ppr-relabel", action="store_true",
+                    help="with --ppr: number the global graph's nodes by a seeded random "
+                         "permutation (the generator numbers them by decreasing degree)")
+    ap.add_argument("--prep", action="store_true",
+                    help="time the window assembly instead (related nodes, induced subgraph, "
+                         "window CSR, feature gather) on the config's global graph")
+    ap.add_argument("--tunable", default=None, metavar="CSV",
+                    help="with --model: let torch's TunableOp pick the GEMM kernels, reading "
+                         "(and, if missing, writing) this results file")
+    ap.add_argument("--model", action="store_true",
+                    help="time the whole window training step instead (encoder projections, "
+                         "LayerNorm, FFN and attention, NLL, backward, AdamW) in bf16 autocast")
+    args = ap.parse_args(argv)
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this build runs the attention path on a single "
+              "MI355X (window sharding across GPUs is not part of it); use --gpus 1.",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    from neutrongt_amd import synthetic as S
+
+    cfg = S.CONFIGS[args.config]
+    layers = args.layers or cfg.layers
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    if args.ppr:
+        if cfg.dense or not cfg.n_global:
+            print("--ppr needs a sparse config with a global graph (gt_arxiv, gt_highdeg, "
+                  "gph_large)", file=sys.stderr)
+            return 2
+        print(json.dumps(ppr_bench(args, cfg, dev)), flush=True)
+        return 0
+    if args.prep:
+        if cfg.dense or not cfg.n_global:
+            print("--prep needs a sparse config with a global graph (gph_large, gt_arxiv, "
+                  "gt_highdeg)", file=sys.stderr)
+            return 2
+        print(json.dumps(prep_bench(args, cfg, dev)), flush=True)
+        return 0
+    if args.model:
+        if cfg.dense:
+            print("--model runs the sparse window encoder; pick a sparse --config", file=sys.stderr)
+            return 2
+        print(json.dumps(model_step_bench(args, cfg, layers, dev)), flush=True)
+        return 0
+    r = measure_window(args, cfg, layers, dev, args.graph, args.calib_copy)
+    ms_step, value, kernels, roof, path = (r["ms_step"], r["value"], r["kernels"], r["roof"],
+                                           r["path"])
+    n_k, E, ei_np, H, d = r["n_k"], r["E"], r["ei_np"], cfg.n_heads, cfg.head_dim
+    csr_ms, warm_steps, warm_ms = r["csr_ms"], r["warm_steps"], r["warm_ms"]
+
+    also = None
+    second = args.also if args.also is not None else ("gph_slim" if args.config == "gph_large"
+                                                       and args.layers is None else "none")
+    if second != "none":
+        cfg2 = S.CONFIGS[second]
+        _log(f"[bench] second window: {second}")
+        r2 = measure_window(args, cfg2, cfg2.layers, dev, False, False)
+        also = {second: {
+            "value": r2["value"], "unit": "edges/s", "ms_per_step": r2["ms_step"],
+            "dtype": "f32" if cfg2.dtype == torch.float32 else "bf16",
+            "workload": (f"{cfg2.name}: {cfg2.layers}-layer sparse attention fwd+bwd, window "
+                         f"n_q={cfg2.n_q}, n_k={r2['n_k']}, E={r2['E']}, H={cfg2.n_heads}, "
+                         f"d={cfg2.head_dim}"),
+            "roofline": r2["roof"], "path_roofline": r2["path"],
+            "kernels_avg_us": {n: round(v["avg_us"], 2) for n, v in r2["kernels"].items()},
+        }}
 
     cpu = None
     if not args.no_cpu and not cfg.dense:
@@ -798,6 +839,7 @@ def main(argv=None) -> int:
         "path_roofline": path,
         "kernels": kernels,
         "cpu_baseline": cpu,
+        "also": also,
     }
     print(json.dumps(out), flush=True)
     return 0
