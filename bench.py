@@ -798,7 +798,8 @@ def main(argv=None) -> int:
         also = {second: {
             "value": r2["value"], "unit": "edges/s", "ms_per_step": r2["ms_step"],
             "dtype": "f32" if cfg2.dtype == torch.float32 else "bf16",
-            "workload": (f"{cfg2.name}: {cfg2.layers}-layer sparse attention fwd+bwd, window "
+            "workload": (f"{cfg2.name}: {cfg2.layers}-layer "
+                         f"{'dense' if cfg2.dense else 'sparse'} attention fwd+bwd, window "
                          f"n_q={cfg2.n_q}, n_k={r2['n_k']}, E={r2['E']}, H={cfg2.n_heads}, "
                          f"d={cfg2.head_dim}"),
             "roofline": r2["roof"], "path_roofline": r2["path"],
