@@ -24,24 +24,29 @@ from . import _lib
 # 8 edge slots per wave (8 heads per pass) a 256-edge chunk is 32 rounds of a
 # wave.
 CHUNK_EDGES = 256
+CHUNK_EDGES_MIN = 128
 CHUNK_EDGES_MAX = 1024
 
 
 def chunk_for_heads(n_heads: int, n_edges: int = 0) -> int:
-    """Edges per work item: 2^floor(log2(n_edges / 2048)) within [256, 1024]
+    """Edges per work item: 2^floor(log2(n_edges / 2048)) within [128, 1024]
     (256 when n_edges is not given).  Longer chunks mean fewer partials and
     smaller finalize passes, but a hub row's chunk is one wave's serial work,
     which must stay short next to the whole kernel.  Measured per layer
     fwd+bwd at 256 / 512 / 1024: the high-degree window (3.65 M edges)
     374 / 346 / 341 us; GPH_Large (1.79 M) 1.394 / 1.385 / 1.414 ms; GPH_Slim
-    and the GT arxiv window (0.25 M) 67 / 95 / 153 and 80 / 110 / 175 us.
-    The head count does not enter; the argument keeps the callers' form.
-    NGT_CHUNK_EDGES overrides the choice."""
+    and the GT arxiv window (0.25 M) 67 / 95 / 153 and 80 / 110 / 175 us, and
+    at 128 / 256 as HIP-graph replays 62.3 / 63.9 and 71.8 / 75.8 us (their
+    key-major pass is one round of waves, as long as its longest chunk; 64
+    gave no more).  The head count does not enter; the argument keeps the
+    callers' form.  NGT_CHUNK_EDGES overrides the choice."""
     del n_heads
     env = os.environ.get("NGT_CHUNK_EDGES")
     if env and int(env) > 0:
         return int(env)
-    chunk = CHUNK_EDGES
+    if n_edges <= 0:
+        return CHUNK_EDGES
+    chunk = CHUNK_EDGES_MIN
     while chunk < CHUNK_EDGES_MAX and 2 * chunk * 2048 <= n_edges:
         chunk *= 2
     return chunk
