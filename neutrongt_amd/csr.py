@@ -55,14 +55,20 @@ def chunk_for_heads(n_heads: int, n_edges: int = 0) -> int:
 def small_for_heads(n_heads: int) -> int:
     """Rows with at most this many edges are packed one row per edge slot
     (no cross-slot reduction, no per-row work item): 64 / next_pow2(H), the
-    slots per wave of an all-heads pass, and 32 from H = 32 on.  On the
-    32,768-query window (H = 32, d = 24) raising it from 2 to 32 took the
-    layer from 1.45 to 1.40 ms; on the H = 8 windows 8 stays best (32 and 64
-    slowed the key-major pass)."""
+    slots per wave of an all-heads pass, except 16 at 5-8 heads and 32 from
+    H = 32 on.  On the 32,768-query window (H = 32, d = 24) raising it from 2
+    to 32 took the layer from 1.45 to 1.40 ms.  At H = 8 with 128-edge chunks
+    (HIP-graph replays, us per layer at 8 / 12 / 16 / 24 / 32): GPH_Slim
+    61.9 / 58.6 / 56.5 / 60.5 / 68.1, the GT arxiv window 72.0 / 69.7 / 66.0 /
+    64.4 / 72.7, the high-degree window 312-314 throughout."""
     lanes = 1
     while lanes < n_heads:
         lanes <<= 1
-    return max(1, 64 // lanes, 32 if n_heads >= 32 else 1)
+    if n_heads >= 32:
+        return 32
+    if lanes == 8:
+        return 16
+    return max(1, 64 // lanes)
 
 
 class WindowAdjacency:
