@@ -795,6 +795,10 @@ def main(argv=None) -> int:
         cfg2 = S.CONFIGS[second]
         _log(f"[bench] second window: {second}")
         r2 = measure_window(args, cfg2, cfg2.layers, dev, False, False)
+        # the same steps replayed from one captured HIP graph: a one-layer step
+        # of this size is bound by the host's per-layer autograd cost in eager
+        # mode, and the replay shows the kernels' own rate
+        r2g = measure_window(args, cfg2, cfg2.layers, dev, True, False)
         also = {second: {
             "value": r2["value"], "unit": "edges/s", "ms_per_step": r2["ms_step"],
             "dtype": "f32" if cfg2.dtype == torch.float32 else "bf16",
@@ -802,6 +806,7 @@ def main(argv=None) -> int:
                          f"{'dense' if cfg2.dense else 'sparse'} attention fwd+bwd, window "
                          f"n_q={cfg2.n_q}, n_k={r2['n_k']}, E={r2['E']}, H={cfg2.n_heads}, "
                          f"d={cfg2.head_dim}"),
+            "hip_graph_value": r2g["value"], "hip_graph_ms_per_step": r2g["ms_step"],
             "roofline": r2["roof"], "path_roofline": r2["path"],
             "kernels_avg_us": {n: round(v["avg_us"], 2) for n, v in r2["kernels"].items()},
         }}
