@@ -180,6 +180,10 @@ int ngt_sparse_fwd_noalloc(int dtype, const void* q, const void* k, const void* 
  *   grad_q[i] = sum_e da_e k_j / scale      (query-major pass)
  *   grad_k[j] = sum_e da_e q_i / scale      (key-major pass, no atomics)
  *   grad_v[j] = sum_e p_e r_i G_i           (key-major pass, no atomics)
+ * da_e reaches the query-major pass through the workspace, or, on windows
+ * with at least 32 edges per key row (csr->n_edges >= 32 csr->n_k) and no
+ * per-edge bias, is recomputed there from the edge's K and V rows; both give
+ * the same bits.  The workspace size does not depend on that choice.
  */
 int ngt_sparse_bwd(int dtype, const void* q, const void* k, const void* v, const void* out,
                    const void* grad_out, const float* rinv, const ngt_window_csr* csr,

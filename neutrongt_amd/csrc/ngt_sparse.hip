@@ -502,7 +502,7 @@ __device__ __forceinline__ void bwd_kv_packed(
           dk[c] = fmaf(da, word_elem<T, DH>(qw[u], c), dk[c]);
           dv[c] = fmaf(pr, word_elem<T, DH>(gw[u], c), dv[c]);
         }
-        ds[int64_t(e0 + u) * H + h] = da;
+        if (ds) ds[int64_t(e0 + u) * H + h] = da;
       }
     }
   }
@@ -514,7 +514,8 @@ __device__ __forceinline__ void bwd_kv_packed(
 }
 
 // Key-major pass: grad_k, grad_v of key row j and da_e for every edge of j
-// (stored at the key-major edge position for the query-major pass).
+// (stored at the key-major edge position for the query-major pass; ds is null
+// when that pass recomputes da_e itself).
 template <typename T, int DH, bool BIAS>
 __global__ __launch_bounds__(kBlock) void k_bwd_kv(
     const T* __restrict__ q, const Keys<T> kv,
@@ -602,7 +603,7 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
             dk[c] = fmaf(da, word_elem<T, DH>(qw[u], c), dk[c]);
             dv[c] = fmaf(pr, word_elem<T, DH>(gw[u], c), dv[c]);
           }
-          ds[int64_t(blk + t0 + u * S + ln.slot) * H + h] = da;
+          if (ds) ds[int64_t(blk + t0 + u * S + ln.slot) * H + h] = da;
         }
       }
     }
@@ -654,17 +655,48 @@ __device__ __forceinline__ void bwd_kv_finalize_tile(const int4* __restrict__ sp
     elem<T>::store(grad_v + at + (c - DH), a);
 }
 
-template <typename T, int DH, bool EXT>
+// The query-major pass either reads each edge's da from ds (written by the
+// key-major pass) or, with RC, recomputes it from the row's q, dO and {r, rD}
+// and the edge's K and V rows.  The recomputation repeats the key-major
+// pass's operations on the same operands in the same order (edge_dot, clamp,
+// exp, the clamp mask), so da and hence dQ come out bit for bit the same.
+struct RecomputeArgs {
+  const void* q;        // [N_q, H, d] of the element type
+  const void* g;        // dO, same layout
+  const float2* rd;     // {r, r (dO . O)} per (query, head)
+  float lo, hi;         // the score clamp
+};
+
+template <typename T, int DH>
+__device__ __forceinline__ float recompute_da(const RowWords<T, DH>& qw, const RowWords<T, DH>& gw,
+                                              float2 rr, const RowWords<T, DH>& kw,
+                                              const RowWords<T, DH>& vw, float inv_scale,
+                                              float lo, float hi) {
+  const float a = edge_dot<T, DH>(qw, kw) * inv_scale;
+  const float p = __expf(clampf(a, lo, hi));
+  const float dp = rr.x * edge_dot<T, DH>(gw, vw) - rr.y;
+  return (a >= lo && a <= hi) ? dp * p : 0.f;
+}
+
+template <typename T, int DH, bool EXT, bool RC>
 __device__ __forceinline__ void bwd_q_packed(const Keys<T, EXT>& kv,
                                              const int32_t* __restrict__ rowptr,
                                              const int32_t* __restrict__ col,
                                              const int32_t* __restrict__ q2t,
                                              const float* __restrict__ ds, int64_t row, int h,
-                                             int H, float inv_scale, T* __restrict__ grad_q) {
+                                             int H, float inv_scale, T* __restrict__ grad_q,
+                                             const RecomputeArgs& rc) {
   float dq[DH];
 #pragma unroll
   for (int c = 0; c < DH; ++c) dq[c] = 0.f;
-  constexpr int U = unroll_for(RowWords<T, DH>::NV, NGT_BWD_Q_WORDS);
+  RowWords<T, DH> qw, gw;
+  float2 rr = make_float2(0.f, 0.f);
+  if constexpr (RC) {
+    load_words<T, DH>(static_cast<const T*>(rc.q) + (row * H + h) * DH, qw);
+    load_words<T, DH>(static_cast<const T*>(rc.g) + (row * H + h) * DH, gw);
+    rr = rc.rd[row * H + h];
+  }
+  constexpr int U = unroll_for((RC ? 2 : 1) * RowWords<T, DH>::NV, NGT_BWD_Q_WORDS);
   const int beg = rowptr[row], end = rowptr[row + 1];
   int jn[U], tn[U];
 #pragma unroll
@@ -673,15 +705,19 @@ __device__ __forceinline__ void bwd_q_packed(const Keys<T, EXT>& kv,
     tn[u] = beg + u < end ? q2t[beg + u] : 0;
   }
   for (int e0 = beg; e0 < end; e0 += U) {
-    RowWords<T, DH> kw[U];
+    RowWords<T, DH> kw[U], vw[RC ? U : 1];
     float d[U];
     int jc[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       jc[u] = jn[u];
       if (jc[u] >= 0) {
-        kv.template load_k<DH>(jc[u], H, h, kw[u]);
-        d[u] = ds[int64_t(tn[u]) * H + h];
+        if constexpr (RC) {
+          kv.template load_kv<DH>(jc[u], H, h, kw[u], vw[u]);
+        } else {
+          kv.template load_k<DH>(jc[u], H, h, kw[u]);
+          d[u] = ds[int64_t(tn[u]) * H + h];
+        }
       }
     }
 #pragma unroll
@@ -692,6 +728,7 @@ __device__ __forceinline__ void bwd_q_packed(const Keys<T, EXT>& kv,
 #pragma unroll
     for (int u = 0; u < U; ++u)
       if (jc[u] >= 0) {
+        if constexpr (RC) d[u] = recompute_da<T, DH>(qw, gw, rr, kw[u], vw[u], inv_scale, rc.lo, rc.hi);
 #pragma unroll
         for (int c = 0; c < DH; ++c) dq[c] = fmaf(d[u], word_elem<T, DH>(kw[u], c), dq[c]);
       }
@@ -702,7 +739,7 @@ __device__ __forceinline__ void bwd_q_packed(const Keys<T, EXT>& kv,
 }
 
 // Query-major pass: grad_q[i] = sum_e da_e k_j / scale.
-template <typename T, int DH, bool EXT>
+template <typename T, int DH, bool EXT, bool RC>
 __global__ __launch_bounds__(kBlock) void k_bwd_q(
     const Keys<T, EXT> kv, const int32_t* __restrict__ col, const int32_t* __restrict__ q2t,
     const float* __restrict__ ds, const int4* __restrict__ items, int32_t n_items,
@@ -710,7 +747,7 @@ __global__ __launch_bounds__(kBlock) void k_bwd_q(
     float* __restrict__ part_q, const int32_t* __restrict__ rowptr,
     const int32_t* __restrict__ packed, int32_t n_packed, int32_t n_pwaves, int32_t q_blocks,
     const int4* __restrict__ splits_k, int32_t kv_tiles, const float* __restrict__ part_kv,
-    T* __restrict__ grad_k, T* __restrict__ grad_v, int32_t xcd) {
+    T* __restrict__ grad_k, T* __restrict__ grad_v, int32_t xcd, const RecomputeArgs rc) {
   // Blocks past the dQ work finish the split key rows of bwd_kv (their dK/dV
   // partials): that work is independent of dQ, so it rides in this launch.
   if (int32_t(blockIdx.x) >= q_blocks) {
@@ -726,7 +763,7 @@ __global__ __launch_bounds__(kBlock) void k_bwd_q(
     int ph;
     if (packed_work(gw0 - int64_t(n_items) * n_groups, n_pwaves, n_groups, hg, L, H, packed,
                     n_packed, prow, ph))
-      bwd_q_packed<T, DH, EXT>(kv, rowptr, col, q2t, ds, prow, ph, H, inv_scale, grad_q);
+      bwd_q_packed<T, DH, EXT, RC>(kv, rowptr, col, q2t, ds, prow, ph, H, inv_scale, grad_q, rc);
     return;
   }
   int item;
@@ -739,8 +776,20 @@ __global__ __launch_bounds__(kBlock) void k_bwd_q(
   float dq[DH];
 #pragma unroll
   for (int c = 0; c < DH; ++c) dq[c] = 0.f;
+  RowWords<T, DH> qw, gw;
+  float2 rr = make_float2(0.f, 0.f);
+  if constexpr (RC) {
+    if (ln.active) {
+      load_words<T, DH>(static_cast<const T*>(rc.q) + (row * H + h) * DH, qw);
+      load_words<T, DH>(static_cast<const T*>(rc.g) + (row * H + h) * DH, gw);
+      rr = rc.rd[row * H + h];
+    } else {
+      zero_words<T, DH>(qw);
+      zero_words<T, DH>(gw);
+    }
+  }
   constexpr int NV = RowWords<T, DH>::NV;
-  constexpr int U = unroll_for(NV, NGT_BWD_Q_WORDS);
+  constexpr int U = unroll_for((RC ? 2 : 1) * NV, NGT_BWD_Q_WORDS);
   const int lane = threadIdx.x & (kWave - 1);
   // each 64-edge block's column and key-major indices are requested one block ahead
   int nx_j = lane < it.z - it.y ? col[it.y + lane] : 0;
@@ -751,7 +800,7 @@ __global__ __launch_bounds__(kBlock) void k_bwd_q(
     nx_j = lane < it.z - blk - kWave ? col[blk + kWave + lane] : 0;
     nx_t = lane < it.z - blk - kWave ? q2t[blk + kWave + lane] : 0;
     for (int t0 = 0; t0 < nb; t0 += S * U) {
-      RowWords<T, DH> kw[U];
+      RowWords<T, DH> kw[U], vw[RC ? U : 1];
       float dsv[U];
       bool ok[U];
 #pragma unroll
@@ -760,15 +809,21 @@ __global__ __launch_bounds__(kBlock) void k_bwd_q(
         ok[u] = t < nb && ln.active;
         const int src = t < nb ? t : 0;
         const int64_t j = __shfl(my_j, src, kWave);
-        const int64_t tp = __shfl(my_t, src, kWave);
+        const int64_t tp = RC ? 0 : __shfl(my_t, src, kWave);
         if (ok[u]) {
-          kv.template load_k<DH>(j, H, h, kw[u]);
-          dsv[u] = ds[tp * H + h];
+          if constexpr (RC) {
+            kv.template load_kv<DH>(j, H, h, kw[u], vw[u]);
+          } else {
+            kv.template load_k<DH>(j, H, h, kw[u]);
+            dsv[u] = ds[tp * H + h];
+          }
         }
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         if (ok[u]) {
+          if constexpr (RC)
+            dsv[u] = recompute_da<T, DH>(qw, gw, rr, kw[u], vw[u], inv_scale, rc.lo, rc.hi);
 #pragma unroll
           for (int c = 0; c < DH; ++c) dq[c] = fmaf(dsv[u], word_elem<T, DH>(kw[u], c), dq[c]);
         }
@@ -840,6 +895,23 @@ int heads_per_pass(int H, int kind) {
   }
   const int cap = kind == 0 ? 8 : kind == 1 ? 16 : H;
   return H > cap ? cap : H;
+}
+
+// dQ from recomputed da (RC) instead of the ds written by the key-major pass:
+// the query-major pass then gathers each edge's V row next to its K row, and
+// the key-major pass skips its ds writes.  That pays where the key rows are
+// reused enough to stay in L2.  Measured, the two passes' time per layer (us,
+// dS read -> recompute): the high-degree GT window (95 edges per key row)
+// 222.6 -> 188.2 (the layer 303 -> 267), GPH_Slim (15) 33.7 -> 31.9, the GT
+// arxiv window (5) 38.5 -> 40.2, GPH_Large (17; its K/V rows do not fit the
+// L2s) 940 -> 1,148.  So it is chosen from 32 edges per key row on; the bias
+// path keeps ds (its da carries the per-edge bias).
+// NGT_DQ_RECOMPUTE=0/1 overrides the choice (not with a bias).
+constexpr int64_t kRecomputeEdgesPerKey = 32;
+bool dq_recompute(const ngt_window_csr* c, const float* eb) {
+  if (eb) return false;
+  if (const char* env = getenv("NGT_DQ_RECOMPUTE")) return atoi(env) != 0;
+  return c->n_k > 0 && c->n_edges >= kRecomputeEdgesPerKey * c->n_k;
 }
 
 // Head groups are dealt to XCDs (virtual_wave) when their count divides 8;
@@ -1000,6 +1072,7 @@ int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void
   float* ds = reinterpret_cast<float*>(ws + lay.ds);
   float* part_kv = reinterpret_cast<float*>(ws + lay.part_kv);
   float* part_q = reinterpret_cast<float*>(ws + lay.part_q);
+  const bool rc = dq_recompute(c, eb);
   const int64_t nrh = int64_t(c->n_q) * H;
   if (nrh > 0) {
     int64_t blocks = (nrh + kBlock - 1) / kBlock;
@@ -1023,8 +1096,9 @@ int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void
                          static_cast<const T*>(q), make_keys<T, DH>(k, v, k_ext, v_ext, n_main, H),
                          static_cast<const T*>(g), rd, c->t_col,
                          reinterpret_cast<const int4*>(c->items_k), c->n_items_k, groups, hg, H,
-                         L, inv_scale, lo, hi, static_cast<T*>(gk), static_cast<T*>(gv), ds,
-                         part_kv, c->t_rowptr, c->packed_k, c->n_packed_k, pw_k, xcd, eb, deb);
+                         L, inv_scale, lo, hi, static_cast<T*>(gk), static_cast<T*>(gv),
+                         rc ? nullptr : ds, part_kv, c->t_rowptr, c->packed_k, c->n_packed_k,
+                         pw_k, xcd, eb, deb);
     };
     if (eb)
       launch(std::true_type{});
@@ -1042,20 +1116,26 @@ int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void
   const int64_t fin_blocks = int64_t(c->n_splits_k) * kv_tiles;
   if (q_blocks + fin_blocks > 0) {
     KernelTimer timer_("sparse_bwd_q", st);
-    auto launch = [&](auto ext) {
+    const RecomputeArgs rca{q, g, rd, lo, hi};
+    auto launch = [&](auto ext, auto recomp) {
       constexpr bool E = decltype(ext)::value;
-      hipLaunchKernelGGL((k_bwd_q<T, DH, E>), dim3(unsigned(q_blocks + fin_blocks)), dim3(kBlock),
+      constexpr bool R = decltype(recomp)::value;
+      hipLaunchKernelGGL((k_bwd_q<T, DH, E, R>), dim3(unsigned(q_blocks + fin_blocks)), dim3(kBlock),
                          0, st, make_keys<T, DH, E>(k, v, k_ext, v_ext, n_main, H), c->col, c->q2t, ds,
                          reinterpret_cast<const int4*>(c->items_q), c->n_items_q, groups, hg, H,
                          L, inv_scale, static_cast<T*>(gq), part_q, c->rowptr, c->packed_q,
                          c->n_packed_q, pw_q, int32_t(q_blocks),
                          reinterpret_cast<const int4*>(c->splits_k), kv_tiles, part_kv,
-                         static_cast<T*>(gk), static_cast<T*>(gv), xcd);
+                         static_cast<T*>(gk), static_cast<T*>(gv), xcd, rca);
     };
-    if (n_main < c->n_k)
-      launch(std::true_type{});
-    else
-      launch(std::false_type{});
+    const bool ext = n_main < c->n_k;
+    if (rc) {
+      if (ext) launch(std::true_type{}, std::true_type{});
+      else launch(std::false_type{}, std::true_type{});
+    } else {
+      if (ext) launch(std::true_type{}, std::false_type{});
+      else launch(std::false_type{}, std::false_type{});
+    }
     NGT_HIP_CHECK(hipGetLastError());
   }
   if (c->n_splits_q > 0) {
