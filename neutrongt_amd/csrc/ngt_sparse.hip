@@ -445,7 +445,18 @@ __global__ __launch_bounds__(kBlock) void k_rowstat(const T* __restrict__ out,
   }
 }
 
-template <typename T, int DH, bool BIAS>
+// da_e into ds.  NT: as a non-temporal store, which keeps a large ds from
+// streaming through the L2 and evicting the Q / dO rows the pass gathers (a
+// template flag: chosen at run time, the two stores fold into one plain store).
+template <bool NT>
+__device__ __forceinline__ void store_da(float* __restrict__ ds, int64_t i, float da) {
+  if constexpr (NT)
+    __builtin_nontemporal_store(da, ds + i);
+  else
+    ds[i] = da;
+}
+
+template <typename T, int DH, bool BIAS, bool NT>
 __device__ __forceinline__ void bwd_kv_packed(
     const T* __restrict__ q, const Keys<T>& kv,
     const T* __restrict__ g, const float2* __restrict__ rd, const int32_t* __restrict__ t_rowptr,
@@ -502,7 +513,7 @@ __device__ __forceinline__ void bwd_kv_packed(
           dk[c] = fmaf(da, word_elem<T, DH>(qw[u], c), dk[c]);
           dv[c] = fmaf(pr, word_elem<T, DH>(gw[u], c), dv[c]);
         }
-        if (ds) ds[int64_t(e0 + u) * H + h] = da;
+        if (ds) store_da<NT>(ds, int64_t(e0 + u) * H + h, da);
       }
     }
   }
@@ -516,7 +527,7 @@ __device__ __forceinline__ void bwd_kv_packed(
 // Key-major pass: grad_k, grad_v of key row j and da_e for every edge of j
 // (stored at the key-major edge position for the query-major pass; ds is null
 // when that pass recomputes da_e itself).
-template <typename T, int DH, bool BIAS>
+template <typename T, int DH, bool BIAS, bool NT>
 __global__ __launch_bounds__(kBlock) void k_bwd_kv(
     const T* __restrict__ q, const Keys<T> kv,
     const T* __restrict__ g, const float2* __restrict__ rd, const int32_t* __restrict__ t_col,
@@ -532,8 +543,8 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
     int ph;
     if (packed_work(gw0 - int64_t(n_items) * n_groups, n_pwaves, n_groups, hg, L, H, packed,
                     n_packed, prow, ph))
-      bwd_kv_packed<T, DH, BIAS>(q, kv, g, rd, t_rowptr, t_col, prow, ph, H, inv_scale, lo, hi,
-                                 grad_k, grad_v, ds, eb, deb);
+      bwd_kv_packed<T, DH, BIAS, NT>(q, kv, g, rd, t_rowptr, t_col, prow, ph, H, inv_scale, lo,
+                                     hi, grad_k, grad_v, ds, eb, deb);
     return;
   }
   int item;
@@ -603,7 +614,7 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
             dk[c] = fmaf(da, word_elem<T, DH>(qw[u], c), dk[c]);
             dv[c] = fmaf(pr, word_elem<T, DH>(gw[u], c), dv[c]);
           }
-          if (ds) ds[int64_t(blk + t0 + u * S + ln.slot) * H + h] = da;
+          if (ds) store_da<NT>(ds, int64_t(blk + t0 + u * S + ln.slot) * H + h, da);
         }
       }
     }
@@ -914,6 +925,16 @@ bool dq_recompute(const ngt_window_csr* c, const float* eb) {
   return c->n_k > 0 && c->n_edges >= kRecomputeEdgesPerKey * c->n_k;
 }
 
+// ds written with non-temporal stores when it is too large to stay cached for
+// the query-major pass anyway (E * H * 4 bytes above 64 MB): GPH_Large's
+// 228 MB, bwd_kv 640 -> 630 us per layer, bwd_q 296 -> 295.  On windows whose
+// ds stays in the MALL the query-major pass loses more than the key-major one
+// gains (GT arxiv, 7.7 MB: bwd_q 14.7 -> 15.2 us).  NGT_DS_NT=0/1 overrides.
+bool ds_nontemporal(const ngt_window_csr* c, int H) {
+  if (const char* env = getenv("NGT_DS_NT")) return atoi(env) != 0;
+  return size_t(c->n_edges) * size_t(H) * 4 > (size_t(64) << 20);
+}
+
 // Head groups are dealt to XCDs (virtual_wave) when their count divides 8;
 // NGT_XCD=0 turns that off for experiments.
 int xcd_mapping(int groups) {
@@ -1090,9 +1111,10 @@ int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void
   const unsigned blocks_k = edge_blocks(c->n_items_k, pw_k, groups, xcd);
   if (blocks_k > 0) {
     KernelTimer timer_("sparse_bwd_kv", st);
-    auto launch = [&](auto bias) {
+    auto launch = [&](auto bias, auto nt) {
       constexpr bool B = decltype(bias)::value;
-      hipLaunchKernelGGL((k_bwd_kv<T, DH, B>), dim3(blocks_k), dim3(kBlock), 0, st,
+      constexpr bool N = decltype(nt)::value;
+      hipLaunchKernelGGL((k_bwd_kv<T, DH, B, N>), dim3(blocks_k), dim3(kBlock), 0, st,
                          static_cast<const T*>(q), make_keys<T, DH>(k, v, k_ext, v_ext, n_main, H),
                          static_cast<const T*>(g), rd, c->t_col,
                          reinterpret_cast<const int4*>(c->items_k), c->n_items_k, groups, hg, H,
@@ -1100,10 +1122,14 @@ int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void
                          rc ? nullptr : ds, part_kv, c->t_rowptr, c->packed_k, c->n_packed_k,
                          pw_k, xcd, eb, deb);
     };
-    if (eb)
-      launch(std::true_type{});
-    else
-      launch(std::false_type{});
+    const bool nt = !rc && ds_nontemporal(c, H);
+    if (eb) {
+      if (nt) launch(std::true_type{}, std::true_type{});
+      else launch(std::true_type{}, std::false_type{});
+    } else {
+      if (nt) launch(std::false_type{}, std::true_type{});
+      else launch(std::false_type{}, std::false_type{});
+    }
     NGT_HIP_CHECK(hipGetLastError());
   }
   hg = heads_per_pass(H, 2);

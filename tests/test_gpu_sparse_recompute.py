@@ -101,3 +101,25 @@ def test_recompute_forced_on_a_low_reuse_window_gives_the_same_bits(monkeypatch)
     b = _run(q, k, v, ei, go, 64, 8)
     for name in ("x", "node_scores", "dq", "dk", "dv"):
         assert torch.equal(a[name], b[name]), name
+
+
+def test_nontemporal_score_gradient_stores_give_the_same_bits(monkeypatch):
+    """The key-major pass writes the score gradients with non-temporal stores
+    when they are too large to stay cached (GPH_Large); forcing either store
+    kind on a small window changes no bit, and both match the oracle."""
+    n_q, n_k, H, d = 400, 450, 8, 16
+    rng = np.random.default_rng(11)
+    src = np.concatenate([rng.integers(0, n_k, 5000), np.full(700, 3)])
+    dst = np.concatenate([rng.integers(0, n_q, 5000), rng.integers(0, n_q, 700)])
+    ei = np.stack([src, dst]).astype(np.int64)
+    q, k, v, go = _qkv(n_q, n_k, H, d, torch.bfloat16, seed=12)
+    monkeypatch.setenv("NGT_DQ_RECOMPUTE", "0")
+    monkeypatch.setenv("NGT_DS_NT", "0")
+    a = _run(q, k, v, ei, go, 64, 16)
+    monkeypatch.setenv("NGT_DS_NT", "1")
+    b = _run(q, k, v, ei, go, 64, 16)
+    ref = OA.sparse_fwd_bwd(q.float(), k.float(), v.float(), torch.from_numpy(ei), go.float(), H,
+                            dtype=torch.float32)
+    for name in ("x", "node_scores", "dq", "dk", "dv"):
+        assert torch.equal(a[name], b[name]), name
+        assert_close(b[name].float(), ref[name].float(), torch.bfloat16, f"nt:{name}")
