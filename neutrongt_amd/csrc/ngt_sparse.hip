@@ -134,6 +134,14 @@ constexpr int unroll_for(int words_per_edge, int budget) {
                                   : (budget / words_per_edge >= 4 ? 4 : budget / words_per_edge);
 }
 
+// The key-major pass keeps at most 2 edges per slot in flight: on the
+// high-degree window (bf16, d = 16, 4 words per edge) 4 took bwd_kv 100 ->
+// 108 us per layer, GPH_Slim and the GT arxiv window read the same either way,
+// and GPH_Large's 6-word edges already fit only 2.
+constexpr int kv_unroll(int words_per_edge) {
+  return unroll_for(words_per_edge, NGT_BWD_KV_WORDS) < 2 ? 1 : 2;
+}
+
 // Work decomposition shared by the edge kernels.
 struct Lane {
   int slot;     // edge slot of this lane
@@ -472,7 +480,7 @@ __device__ __forceinline__ void bwd_kv_packed(
     dk[c] = 0.f;
     dv[c] = 0.f;
   }
-  constexpr int U = unroll_for(2 * RowWords<T, DH>::NV, NGT_BWD_KV_WORDS);
+  constexpr int U = kv_unroll(2 * RowWords<T, DH>::NV);
   const int beg = t_rowptr[row], end = t_rowptr[row + 1];
   int in_[U];
 #pragma unroll
@@ -570,7 +578,7 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
     zero_words<T, DH>(vrw);
   }
   constexpr int NV = RowWords<T, DH>::NV;
-  constexpr int U = unroll_for(2 * NV, NGT_BWD_KV_WORDS);
+  constexpr int U = kv_unroll(2 * NV);
   const int lane = threadIdx.x & (kWave - 1);
   // each 64-edge block's row indices are requested one block ahead
   int nx_i = lane < it.z - it.y ? t_col[it.y + lane] : 0;
