@@ -308,7 +308,6 @@ def ppr_bench(args, cfg, dev) -> dict:
                    "relabelled": bool(args.ppr_relabel),
                    "max_degree": int(deg_max)},
         "cpu_baseline": cpu,
-        "also": also,
     }
 
 
@@ -324,7 +323,7 @@ def prep_bench(args, cfg, dev) -> dict:
     import numpy as np
     import torch
 
-    from neutrongt_amd import chunk_for_heads, small_for_heads
+    from neutrongt_amd import chunk_for_heads, pack_q_adaptive, small_for_heads
     from neutrongt_amd import synthetic as S
     from neutrongt_amd import window as W
     from neutrongt_amd.csr import WindowAdjacency
@@ -379,7 +378,7 @@ def prep_bench(args, cfg, dev) -> dict:
     # attention edge_index: row 0 = key (the CSR row node), row 1 = query
     adj, t_adj = timed(lambda: WindowAdjacency(sub_csr, n_w, n_w,
                                                chunk_for_heads(H, int(sub_csr.shape[1])),
-                                               small_for_heads(H)))
+                                               small_for_heads(H), pack_q_adaptive(H)))
     (x_i, _), t_gather = timed(lambda: W.gather_rows(features, win))
     # window refinement of this window: node_out with seeded node scores (30 %
     # removed, the training loop's ratio), then node_in refilling it from the
@@ -444,7 +443,6 @@ def prep_bench(args, cfg, dev) -> dict:
                    "window_nodes": n_w, "window_edges": int(sub_csr.shape[1])},
         "ops": ops,
         "cpu_baseline": cpu,
-        "also": also,
     }
 
 
@@ -567,7 +565,7 @@ def measure_window(args, cfg, layers: int, dev, graph: bool, calib_copy: bool) -
     the step time, edges/s, per-kernel times and the dominant kernel's roofline."""
     import torch
 
-    from neutrongt_amd import _lib, chunk_for_heads, small_for_heads
+    from neutrongt_amd import _lib, chunk_for_heads, pack_q_adaptive, small_for_heads
     from neutrongt_amd import synthetic as S
     from neutrongt_amd.attention import DenseAttentionFunction, window_attention
     from neutrongt_amd.csr import WindowAdjacency
@@ -597,7 +595,8 @@ def measure_window(args, cfg, layers: int, dev, graph: bool, calib_copy: bool) -
         for _ in range(2):
             torch.cuda.synchronize()
             t1 = time.perf_counter()
-            adj = WindowAdjacency(ei, cfg.n_q, n_k, chunk_for_heads(H, E), small_for_heads(H))
+            adj = WindowAdjacency(ei, cfg.n_q, n_k, chunk_for_heads(H, E), small_for_heads(H),
+                                  pack_q_adaptive(H))
             csr_ms = (time.perf_counter() - t1) * 1e3
             cold = csr_ms if cold is None else cold
         _log(f"[bench] csr built in {csr_ms:.2f} ms (first build {cold:.1f} ms; incl. one info "

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define NGT_ABI_VERSION 6
+#define NGT_ABI_VERSION 7
 
 #define NGT_F32 0
 #define NGT_BF16 1
@@ -51,6 +51,8 @@ extern "C" {
 #define NGT_INFO_MAX_DEG_K 10
 #define NGT_INFO_PACKED_Q 11  /* rows in the packed small-row list, query-major */
 #define NGT_INFO_PACKED_K 12
+#define NGT_INFO_SMALL_Q 13   /* packing threshold the build used, query-major */
+#define NGT_INFO_SMALL_K 14
 #define NGT_INFO_LEN 16
 
 /*
@@ -73,13 +75,22 @@ extern "C" {
  *   item covers the whole row; part >= 0 is the partial slot of one chunk.
  * Splits are int32x4 {row, part_begin, n_parts, 0}.
  */
+/* small_q / small_k value asking ngt_csr_build to choose the packing
+ * threshold from the rows' degrees: the first of 8, 16, 24, 32 (each capped
+ * at chunk - 1) that packs at least 78 % of the rows, else the last; the
+ * threshold used is reported in info[NGT_INFO_SMALL_Q / _K].  Measured as the
+ * best or within 1 % of it on seven windows with 8 heads (GT arxiv windows
+ * with 0-16 related keys per query, GPH_Slim windows of mean degree 8-28). */
+#define NGT_SMALL_FROM_DEGREES (-1)
+
 typedef struct ngt_window_csr {
   int32_t n_q;
   int32_t n_k;
   int64_t n_edges;
   int32_t chunk_q;   /* max edges per work item */
   int32_t chunk_k;
-  int32_t small_q;   /* rows with <= small edges go to the packed list (0 <= small < chunk) */
+  int32_t small_q;   /* rows with <= small edges go to the packed list (0 <= small < chunk),
+                        or NGT_SMALL_FROM_DEGREES */
   int32_t small_k;
   int32_t* rowptr;   /* [n_q + 1] */
   int32_t* col;      /* [E] */

@@ -12,7 +12,8 @@ WindowAdjacency          device CSR/transposed CSR/work lists of one window
 from .attention import (CoreAttention, DenseAttentionBiasFunction, DenseAttentionFunction,
                         SparseAttentionBiasFunction, SparseAttentionFunction, dense_attention,
                         dense_attention_bias, install, sparse_attention, window_attention)
-from .csr import AdjacencyCache, WindowAdjacency, chunk_for_heads, default_cache, small_for_heads
+from .csr import (AdjacencyCache, WindowAdjacency, chunk_for_heads, default_cache, pack_q_adaptive,
+                  small_for_heads)
 
 __all__ = [
     "CoreAttention",
@@ -28,6 +29,7 @@ __all__ = [
     "WindowAdjacency",
     "AdjacencyCache",
     "chunk_for_heads",
+    "pack_q_adaptive",
     "small_for_heads",
     "default_cache",
 ]

@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libngt_attn.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 NGT_F32 = 0
 NGT_BF16 = 1
@@ -31,6 +31,9 @@ INFO_MAX_DEG_Q = 9
 INFO_MAX_DEG_K = 10
 INFO_PACKED_Q = 11
 INFO_PACKED_K = 12
+INFO_SMALL_Q = 13
+INFO_SMALL_K = 14
+SMALL_FROM_DEGREES = -1  # ngt_csr_build picks the packing threshold from the degrees
 INFO_LEN = 16
 
 

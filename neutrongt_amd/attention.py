@@ -19,7 +19,7 @@ import torch
 import torch.nn as nn
 
 from . import _lib
-from .csr import AdjacencyCache, chunk_for_heads, default_cache, small_for_heads
+from .csr import AdjacencyCache, chunk_for_heads, default_cache, pack_q_adaptive, small_for_heads
 
 CLAMP_LO = -5.0
 CLAMP_HI = 5.0
@@ -252,7 +252,7 @@ def sparse_attention(q, k, v, edge_index, num_heads=None, scale=None, cache: Adj
         scale = math.sqrt(d)
     cache = cache or default_cache
     adj = cache.get(edge_index, q.shape[0], n_k, chunk_for_heads(H, int(edge_index.shape[-1])),
-                    small_for_heads(H))
+                    small_for_heads(H), pack_q_adaptive(H))
     if attn_bias is not None:
         if (attn_bias.dim() != 4 or attn_bias.shape[0] != 1 or attn_bias.shape[1] != H
                 or attn_bias.shape[2] < n_k or attn_bias.shape[3] < q.shape[0]):

@@ -56,7 +56,8 @@ def small_for_heads(n_heads: int) -> int:
     """Rows with at most this many edges are packed one row per edge slot
     (no cross-slot reduction, no per-row work item): 64 / next_pow2(H), the
     slots per wave of an all-heads pass, except 16 at 5-8 heads and 32 from
-    H = 32 on.  On the 32,768-query window (H = 32, d = 24) raising it from 2
+    H = 32 on.  At 5-8 heads this is the key-major list's threshold, and the
+    query-major list's comes from the window's degrees (pack_q_adaptive).  On the 32,768-query window (H = 32, d = 24) raising it from 2
     to 32 took the layer from 1.45 to 1.40 ms.  At H = 8 with 128-edge chunks
     (HIP-graph replays, us per layer at 8 / 12 / 16 / 24 / 32): GPH_Slim
     61.9 / 58.6 / 56.5 / 60.5 / 68.1, the GT arxiv window 72.0 / 69.7 / 66.0 /
@@ -71,10 +72,32 @@ def small_for_heads(n_heads: int) -> int:
     return max(1, 64 // lanes)
 
 
+def pack_q_adaptive(n_heads: int) -> bool:
+    """Whether the query-major packing threshold is read from the window's
+    degrees (5-8 heads).  A packed row is walked serially by one edge slot, a
+    longer row by a whole wave, and the best threshold follows the degree
+    distribution rather than the head count.  HIP-graph replays, us per layer
+    at thresholds 8 / 16 / 24 / 32 / 48 (in brackets the share of query rows
+    that the chosen threshold packs):
+      GT arxiv window,  0 related keys: 51.3 / 49.5 / 53.4 / 54.0 / 62.3 (16: 0.85)
+                        4 related keys: 60.5 / 55.9 / 58.7 / 63.6 / 68.4 (16: 0.79)
+                        8 related keys: 68.1 / 64.9 / 62.2 / 67.9 / 73.1 (24: 0.85)
+                       16 related keys: 78.5 / 78.2 / 81.2 / 75.8 / 81.7 (32: 0.85)
+      GPH_Slim, mean degree  8:         47.7 / 48.6 / 52.5 / 54.9 / 63.8 ( 8: 0.82)
+                mean degree 14:         58.8 / 56.6 / 60.0 / 64.0 / 72.5 (16: 0.86)
+                mean degree 28:         85.1 / 85.3 / 85.9 / 87.8 / 91.1 (24: 0.80)
+    The first step that packs at least 78 % of the rows is within 1 % of the
+    best threshold on all seven windows; ngt_csr_build applies that rule on
+    the device (small_q = NGT_SMALL_FROM_DEGREES) from the degrees it sorts
+    anyway, so the choice costs no extra host round trip."""
+    return 4 < n_heads <= 8
+
+
 class WindowAdjacency:
     """Both CSR orientations of one window plus its work lists (int32, on device)."""
 
-    def __init__(self, edge_index: torch.Tensor, n_q: int, n_k: int, chunk: int, small: int = 0):
+    def __init__(self, edge_index: torch.Tensor, n_q: int, n_k: int, chunk: int, small: int = 0,
+                 pack_q: bool = False):
         if edge_index.dim() != 2 or edge_index.shape[0] != 2:
             raise ValueError(f"edge_index must be [2, E], got {tuple(edge_index.shape)}")
         if not edge_index.is_cuda:
@@ -86,7 +109,8 @@ class WindowAdjacency:
         self.edge_index = edge_index  # pins the cache key's storage
         self.n_q, self.n_k, self.n_edges, self.chunk = int(n_q), int(n_k), E, int(chunk)
         small = int(min(max(small, 0), chunk - 1))
-        self.small = small
+        self.small = small  # key-major threshold (and query-major unless pack_q)
+        small_q = _lib.SMALL_FROM_DEGREES if pack_q else small
         miq, msq, mik, msk = (C.c_int32() for _ in range(4))
         _lib.check(lib.ngt_csr_sizes(E, n_q, n_k, chunk, chunk, C.byref(miq), C.byref(msq),
                                      C.byref(mik), C.byref(msk)))
@@ -110,7 +134,7 @@ class WindowAdjacency:
         self.info_dev.zero_()
         s = _lib.WindowCSR()
         s.n_q, s.n_k, s.n_edges, s.chunk_q, s.chunk_k = n_q, n_k, E, chunk, chunk
-        s.small_q = s.small_k = small
+        s.small_q, s.small_k = small_q, small
         for name in ("rowptr", "col", "perm", "t_rowptr", "t_col", "t_perm", "q2t", "items_q",
                      "splits_q", "packed_q", "items_k", "splits_k", "packed_k"):
             setattr(s, name, getattr(self, name).data_ptr())
@@ -127,6 +151,7 @@ class WindowAdjacency:
             info = self.info_dev.cpu()  # one sync per window build
         del ws
         self.info = [int(x) for x in info.tolist()]
+        self.small_q = self.info[_lib.INFO_SMALL_Q]  # the threshold the build used
         if self.info[_lib.INFO_BAD_EDGES]:
             raise IndexError(f"edge_index has {self.info[_lib.INFO_BAD_EDGES]} entries outside "
                              f"[0, {n_k}) x [0, {n_q}) (src x dst)")
@@ -172,14 +197,14 @@ class AdjacencyCache:
         self._d: OrderedDict = OrderedDict()
 
     def get(self, edge_index: torch.Tensor, n_q: int, n_k: int, chunk: int,
-            small: int = 0) -> WindowAdjacency:
+            small: int = 0, pack_q: bool = False) -> WindowAdjacency:
         key = (edge_index.data_ptr(), edge_index._version, tuple(edge_index.shape),
-               str(edge_index.device), edge_index.dtype, n_q, n_k, chunk, small)
+               str(edge_index.device), edge_index.dtype, n_q, n_k, chunk, small, pack_q)
         adj = self._d.get(key)
         if adj is not None and adj.edge_index is edge_index:
             self._d.move_to_end(key)
             return adj
-        adj = WindowAdjacency(edge_index, n_q, n_k, chunk, small)
+        adj = WindowAdjacency(edge_index, n_q, n_k, chunk, small, pack_q)
         self._d[key] = adj
         while len(self._d) > self.capacity:
             self._d.popitem(last=False)

@@ -157,13 +157,32 @@ __device__ __forceinline__ int32_t upper_bound_u32(const uint32_t* __restrict__ 
   return lo;
 }
 
+// Packing threshold read from the degrees (small = NGT_SMALL_FROM_DEGREES):
+// the first step that packs at least kPackSharePct % of the rows.
+constexpr int32_t kPackSteps[4] = {8, 16, 24, 32};
+constexpr int64_t kPackSharePct = 78;
+
+__device__ __forceinline__ int32_t packing_threshold(const uint32_t* __restrict__ sdeg,
+                                                     int32_t n_rows, int32_t chunk) {
+  int32_t t = 0;
+  for (int i = 0; i < 4; ++i) {
+    t = min(kPackSteps[i], chunk - 1);
+    const int32_t packed = upper_bound_u32(sdeg, n_rows, static_cast<uint32_t>(t));
+    if (int64_t(packed) * 100 >= int64_t(n_rows) * kPackSharePct) break;
+  }
+  return t;
+}
+
 // From the rows sorted by ascending degree: the packed small rows and the
-// single-item medium rows, both longest first.  info gets the totals.
+// single-item medium rows, both longest first.  info gets the totals and the
+// packing threshold used.
 __global__ void k_emit_sorted(const int32_t* __restrict__ rowptr, int32_t n_rows, int32_t chunk,
-                              int32_t small, const uint32_t* __restrict__ sdeg,
+                              int32_t small_in, const uint32_t* __restrict__ sdeg,
                               const int32_t* __restrict__ srow, const Count3* __restrict__ scan,
                               int4* __restrict__ items, int32_t* __restrict__ packed,
-                              int32_t* __restrict__ info, int info_base, int packed_slot) {
+                              int32_t* __restrict__ info, int info_base, int packed_slot,
+                              int small_slot) {
+  const int32_t small = small_in < 0 ? packing_threshold(sdeg, n_rows, chunk) : small_in;
   const int32_t n_small = upper_bound_u32(sdeg, n_rows, static_cast<uint32_t>(small));
   const int32_t n_le_chunk = upper_bound_u32(sdeg, n_rows, static_cast<uint32_t>(chunk));
   const int32_t n_medium = n_le_chunk - n_small;
@@ -179,6 +198,7 @@ __global__ void k_emit_sorted(const int32_t* __restrict__ rowptr, int32_t n_rows
     info[info_base + 1] = tot.split_items;             // partial slots
     info[info_base + 2] = tot.split_rows;              // split rows
     info[packed_slot] = n_small;                       // packed rows
+    info[small_slot] = small;                          // their threshold
   }
   for (int32_t p = blockIdx.x * blockDim.x + threadIdx.x; p < n_le_chunk;
        p += gridDim.x * blockDim.x) {
@@ -258,8 +278,8 @@ int csr_layout(int64_t E, int32_t n_q, int32_t n_k, CsrLayout* L) {
 
 int build_worklist(const int32_t* rowptr, int32_t n_rows, int32_t chunk, int32_t small,
                    int4* items, int4* splits, int32_t* packed, int32_t* info, int info_base,
-                   int packed_slot, int max_deg_slot, char* ws, const CsrLayout& L,
-                   hipStream_t st) {
+                   int packed_slot, int small_slot, int max_deg_slot, char* ws,
+                   const CsrLayout& L, hipStream_t st) {
   Count3* cnt = reinterpret_cast<Count3*>(ws + L.cnt);
   Count3* scan = reinterpret_cast<Count3*>(ws + L.cnt_scan);
   uint32_t* deg_a = reinterpret_cast<uint32_t*>(ws + L.deg_a);
@@ -268,7 +288,8 @@ int build_worklist(const int32_t* rowptr, int32_t n_rows, int32_t chunk, int32_t
   int32_t* row_b = reinterpret_cast<int32_t*>(ws + L.row_b);
   if (n_rows == 0) {
     hipLaunchKernelGGL(k_emit_sorted, dim3(1), dim3(kBlock), 0, st, rowptr, n_rows, chunk, small,
-                       deg_b, row_b, scan, items, packed, info, info_base, packed_slot);
+                       deg_b, row_b, scan, items, packed, info, info_base, packed_slot,
+                       small_slot);
     NGT_HIP_CHECK(hipGetLastError());
     return NGT_OK;
   }
@@ -286,7 +307,7 @@ int build_worklist(const int32_t* rowptr, int32_t n_rows, int32_t chunk, int32_t
                                           size_t(n_rows), 0u, 32u, st));
   hipLaunchKernelGGL(k_emit_sorted, dim3(grid_for(n_rows)), dim3(kBlock), 0, st, rowptr, n_rows,
                      chunk, small, deg_b, row_b, scan, items, packed, info, info_base,
-                     packed_slot);
+                     packed_slot, small_slot);
   NGT_HIP_CHECK(hipGetLastError());
   return NGT_OK;
 }
@@ -332,9 +353,11 @@ extern "C" int ngt_csr_build(const int64_t* edge_index, ngt_window_csr* csr, voi
   const int64_t E = csr->n_edges;
   const int32_t n_q = csr->n_q, n_k = csr->n_k;
   if (E < 0 || n_q < 0 || n_k < 0 || csr->chunk_q <= 0 || csr->chunk_k <= 0 ||
-      csr->small_q < 0 || csr->small_k < 0 || csr->small_q >= csr->chunk_q ||
-      csr->small_k >= csr->chunk_k)
-    return set_error(NGT_ERR_ARG, "ngt_csr_build: bad sizes (need 0 <= small < chunk)");
+      csr->small_q < NGT_SMALL_FROM_DEGREES || csr->small_k < NGT_SMALL_FROM_DEGREES ||
+      csr->small_q >= csr->chunk_q || csr->small_k >= csr->chunk_k)
+    return set_error(NGT_ERR_ARG,
+                     "ngt_csr_build: bad sizes (need 0 <= small < chunk, or small = "
+                     "NGT_SMALL_FROM_DEGREES)");
   if (E > 0 && (!edge_index || n_q == 0 || n_k == 0))
     return set_error(NGT_ERR_ARG, "ngt_csr_build: edges given for an empty window");
   if (!csr->rowptr || !csr->t_rowptr || !csr->info || !csr->items_q || !csr->items_k ||
@@ -400,11 +423,11 @@ extern "C" int ngt_csr_build(const int64_t* edge_index, ngt_window_csr* csr, voi
   rc = build_worklist(csr->rowptr, n_q, csr->chunk_q, csr->small_q,
                       reinterpret_cast<int4*>(csr->items_q), reinterpret_cast<int4*>(csr->splits_q),
                       csr->packed_q, csr->info, NGT_INFO_ITEMS_Q, NGT_INFO_PACKED_Q,
-                      NGT_INFO_MAX_DEG_Q, ws, L, st);
+                      NGT_INFO_SMALL_Q, NGT_INFO_MAX_DEG_Q, ws, L, st);
   if (rc != NGT_OK) return rc;
   rc = build_worklist(csr->t_rowptr, n_k, csr->chunk_k, csr->small_k,
                       reinterpret_cast<int4*>(csr->items_k), reinterpret_cast<int4*>(csr->splits_k),
                       csr->packed_k, csr->info, NGT_INFO_ITEMS_K, NGT_INFO_PACKED_K,
-                      NGT_INFO_MAX_DEG_K, ws, L, st);
+                      NGT_INFO_SMALL_K, NGT_INFO_MAX_DEG_K, ws, L, st);
   return rc;
 }

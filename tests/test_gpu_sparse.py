@@ -376,3 +376,40 @@ def test_sparse_bitwise_reproducible(H, d, dtype):
     b = _run_kernel(q, k, v, ei, go, chunk=64, small=2)
     for name in a:
         assert torch.equal(a[name], b[name]), name
+
+
+@pytest.mark.parametrize("related", [0, 8, 16])  # thresholds 16, 24 and 32
+def test_query_packing_from_degrees(related):
+    """At 5-8 heads the query-major packing threshold comes from the window's
+    degrees (the first of 8/16/24/32 that packs >= 78 % of the rows) while the
+    key-major list keeps its own: both work lists bit for bit against the
+    oracle with their own thresholds, and the attention within tolerance."""
+    _say(f"case pack_q related={related}")
+    n_q, n_k, H, d = 400, 400, 8, 16
+    rng = np.random.default_rng(related + 1)
+    src = rng.integers(0, n_k, 12 * n_q)
+    dst = rng.integers(0, n_q, 12 * n_q)
+    if related:  # every query also attends `related` extra keys (as the cache's related rows)
+        src = np.concatenate([src, rng.integers(0, n_k, related * n_q)])
+        dst = np.concatenate([dst, np.repeat(np.arange(n_q), related)])
+    ei = np.stack([src, dst]).astype(np.int64)
+    deg = np.bincount(ei[1], minlength=n_q)
+    want = next((t for t in (8, 16, 24, 32) if (deg <= t).sum() >= 0.78 * n_q), 32)
+    small_k = 16
+    adj = WindowAdjacency(torch.from_numpy(ei).cuda(), n_q, n_k, 128, small_k, pack_q=True)
+    assert adj.small_q == want and adj.small == small_k
+    ref = OG.csr_from_coo(ei[0], ei[1], n_q, n_k)
+    for side, rp, small in (("q", ref["rowptr"], want), ("k", ref["t_rowptr"], small_k)):
+        items, splits, packed = OG.work_items(rp, 128, small)
+        np.testing.assert_array_equal(getattr(adj, "items_" + side).cpu().numpy()[: items.shape[0]],
+                                      items, err_msg="items_" + side)
+        np.testing.assert_array_equal(getattr(adj, "packed_" + side).cpu().numpy()[: packed.shape[0]],
+                                      packed, err_msg="packed_" + side)
+    q, k, v, go = _qkv(n_q, n_k, H, d, torch.bfloat16, seed=related + 5)
+    qd, kd, vd = (t.cuda().requires_grad_(True) for t in (q, k, v))
+    x, ns = SparseAttentionFunction.apply(qd, kd, vd, adj, float(d) ** 0.5, -5.0, 5.0, 1e-6)
+    x.backward(go.cuda())
+    torch.cuda.synchronize()
+    res = {"x": x.detach().cpu(), "node_scores": ns.cpu(), "dq": qd.grad.cpu(),
+           "dk": kd.grad.cpu(), "dv": vd.grad.cpu()}
+    _check(res, _oracle(q, k, v, ei, go, H), torch.bfloat16, f"pack_q related={related}")
