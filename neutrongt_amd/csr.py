@@ -32,13 +32,14 @@ def chunk_for_heads(n_heads: int, n_edges: int = 0) -> int:
     """Edges per work item: 2^floor(log2(n_edges / 2048)) within [128, 1024]
     (256 when n_edges is not given).  Longer chunks mean fewer partials and
     smaller finalize passes, but a hub row's chunk is one wave's serial work,
-    which must stay short next to the whole kernel.  Measured per layer
-    fwd+bwd at 256 / 512 / 1024: the high-degree window (3.65 M edges)
-    374 / 346 / 341 us; GPH_Large (1.79 M) 1.394 / 1.385 / 1.414 ms; GPH_Slim
-    and the GT arxiv window (0.25 M) 67 / 95 / 153 and 80 / 110 / 175 us, and
-    at 128 / 256 as HIP-graph replays 62.3 / 63.9 and 71.8 / 75.8 us (their
-    key-major pass is one round of waves, as long as its longest chunk; 64
-    gave no more).  The head count does not enter; the argument keeps the
+    which must stay short next to the whole kernel.  Measured on the current
+    kernels: the high-degree window (3.67 M edges) 272 / 264 / 322 us per layer
+    at 512 / 1024 / 2048; GPH_Large (1.79 M) 16.47 / 16.35 / 16.72 ms per
+    12-layer step at 256 / 512 / 1024 (at 256 its key-major pass gains 6 us and
+    the query-major pass and the finalizes lose 19); GPH_Slim and the GT arxiv
+    window (0.25 M) at 128 / 256 as HIP-graph replays 62.3 / 63.9 and 71.8 /
+    75.8 us (their key-major pass is one round of waves, as long as its
+    longest chunk; 64 gave no more; 512 and 1024 had cost them 40-120 %).  The head count does not enter; the argument keeps the
     callers' form.  NGT_CHUNK_EDGES overrides the choice."""
     del n_heads
     env = os.environ.get("NGT_CHUNK_EDGES")
