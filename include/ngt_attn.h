@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define NGT_ABI_VERSION 7
+#define NGT_ABI_VERSION 8
 
 #define NGT_F32 0
 #define NGT_BF16 1
@@ -176,8 +176,11 @@ int ngt_sparse_fwd(int dtype, const void* q, const void* k, const void* v,
  * each device using the library holds until the process ends; a window whose
  * forward workspace (ngt_sparse_workspace_bytes' fwd_bytes) exceeds it is
  * rejected with NGT_ERR_UNSUPPORTED.  Same results as ngt_sparse_fwd, bit for
- * bit.  Every call on a device shares that device's array: calls that overlap
- * on one device (several streams or threads) race.
+ * bit.  The scratch used is the current device's copy: `stream` must belong
+ * to the current device (NGT_ERR_ARG otherwise; the null stream is the
+ * current device's).  Every call on a device shares that device's array:
+ * calls that overlap on one device (several streams or threads) race, so a
+ * caller issues them on one stream at a time per device.
  */
 int ngt_sparse_fwd_noalloc(int dtype, const void* q, const void* k, const void* v,
                            const ngt_window_csr* csr, int32_t n_heads, int32_t head_dim,
@@ -271,30 +274,43 @@ int ngt_edge_bias_grad(const ngt_window_csr* csr, int32_t n_heads, const float* 
  *   NeutronGT/models/graphormer_dist_node_level.py:51-58
  *   (twin NeutronGT/models/gt_dist_node_level_single_window.py:80-97)
  * with the products S = Q K^T, O = (P o M) V, G V^T, (P o M)^T G, dS K and
- * dS^T Q left to library GEMMs; all arrays fp32 and contiguous, [H, n_q, n_k]
- * unless stated.
+ * dS^T Q left to library GEMMs; all arrays fp32 and contiguous.  The softmax
+ * calls cover the n_heads consecutive heads head0 .. head0 + n_heads - 1 of
+ * the window, so a caller can run the window a few heads at a time: their
+ * arrays are [n_heads, n_q, n_k] and hold just those heads (head0 places the
+ * dropout mask).
  * ngt_dense_bias_softmax_fwd: z = mask[i][j] ? -1e9 : s * scale + bias
  *   (bias nullable: the sum of attn_bias and pruning_mask; mask nullable,
  *   uint8 [n_q, n_k], nonzero = filled); p = softmax_j(z); pd = p o M with
  *   the dropout multiplier of ngt_dense_fwd (same seed, same mask; pd only
- *   with dropout_p > 0); lse [H, n_q] = max + log(sum).  n_heads * n_q must
- *   not exceed 2^24 (NGT_ERR_ARG), here and in the backward.
+ *   with dropout_p > 0); lse [n_heads, n_q] = max + log(sum) (nullable).
+ *   n_heads * n_q must not exceed 2^24 (NGT_ERR_ARG), here and in the
+ *   backward.
  * ngt_dense_bias_softmax_bwd: with dpd = dL/d(p o M): dP = M o dpd,
  *   D_i = sum_j p dP, ds = p o (dP - D), 0 where masked.  ds is also the
  *   gradient of bias (and so of attn_bias and pruning_mask).
- * ngt_dense_abs_colsum: node_score[j] = sum_i mean_h |s * scale| (the
- *   reference's abs(score).mean(dim=1).sum(dim=0)), in a fixed order, with a
+ * ngt_dense_abs_head_sum: m [n_q, n_k] = (accumulate ? m : 0) + the sum over
+ *   the call's n_heads heads of s [n_heads, n_q, n_k], in head order, of
+ *   |s * scale|; calls over consecutive head ranges give the bits of one
+ *   call over all heads.
+ * ngt_dense_abs_colsum: node_score[j] = sum_i m[i][j] / n_heads (the
+ *   reference's abs(score).mean(dim=1).sum(dim=0), with m from
+ *   ngt_dense_abs_head_sum over all n_heads heads), in a fixed order, with a
  *   caller workspace of ngt_dense_abs_colsum_workspace_bytes(n_k).
  */
-int ngt_dense_bias_softmax_fwd(int32_t n_heads, int32_t n_q, int32_t n_k, const float* s,
-                               float scale, const float* bias, const uint8_t* mask,
-                               float dropout_p, uint64_t seed, const uint64_t* seed_dev, float* p,
-                               float* pd, float* lse, void* stream);
-int ngt_dense_bias_softmax_bwd(int32_t n_heads, int32_t n_q, int32_t n_k, const float* p,
-                               const float* dpd, const uint8_t* mask, float dropout_p,
-                               uint64_t seed, const uint64_t* seed_dev, float* ds, void* stream);
+int ngt_dense_bias_softmax_fwd(int32_t n_heads, int32_t head0, int32_t n_q, int32_t n_k,
+                               const float* s, float scale, const float* bias,
+                               const uint8_t* mask, float dropout_p, uint64_t seed,
+                               const uint64_t* seed_dev, float* p, float* pd, float* lse,
+                               void* stream);
+int ngt_dense_bias_softmax_bwd(int32_t n_heads, int32_t head0, int32_t n_q, int32_t n_k,
+                               const float* p, const float* dpd, const uint8_t* mask,
+                               float dropout_p, uint64_t seed, const uint64_t* seed_dev,
+                               float* ds, void* stream);
+int ngt_dense_abs_head_sum(int32_t n_heads, int32_t n_q, int32_t n_k, const float* s, float scale,
+                           int32_t accumulate, float* m, void* stream);
 int ngt_dense_abs_colsum_workspace_bytes(int32_t n_k, size_t* bytes);
-int ngt_dense_abs_colsum(int32_t n_heads, int32_t n_q, int32_t n_k, const float* s, float scale,
+int ngt_dense_abs_colsum(int32_t n_heads, int32_t n_q, int32_t n_k, const float* m,
                          float* node_score, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
@@ -397,6 +413,37 @@ int ngt_adj_weights(const int64_t* edge_index, const float* ppr_val, int64_t n_e
  */
 int ngt_gather_rows(const void* src, int64_t n_src, const int64_t* idx, int64_t n_rows,
                     int64_t row_bytes, void* dst, int32_t* bad, void* stream);
+
+/*
+ * Duplicate-node layout of a rank's windows.
+ * Replaces _compute_local_duplicate_nodes and build_dup_cache_metadata,
+ *   NeutronGT/core/node_level_pipeline/window_state.py:52-73 and :181-205.
+ * nodes: int64 [n_nodes], the rank's n_windows windows back to back; window
+ * w is nodes[win_ptr[w] .. win_ptr[w+1]) (win_ptr: device int64
+ * [n_windows + 1], non-decreasing, win_ptr[0] = 0, win_ptr[n_windows] =
+ * n_nodes).  A node id is a duplicate when it occurs at least min_count
+ * times in nodes (min_count 2: the rerange; 1: every id, the cache metadata
+ * of given duplicate lists; 1 <= min_count <= 65536).  Out:
+ *   reranged [n_nodes]: each window's duplicates in their original order,
+ *     then its other nodes in their original order (torch.cat of
+ *     part[isin(part, dups)] and part[~isin(part, dups)]);
+ *   cache_ids [capacity n_nodes]: the sorted unique duplicate ids
+ *     (torch.unique(..., sorted=True));
+ *   dup_index [capacity n_nodes]: for every window in order, the cache
+ *     position of each of its duplicates (torch.searchsorted(cache_ids, .));
+ *     window w's entries are dup_index[dup_ptr[w] .. dup_ptr[w+1]), and its
+ *     duplicate count is dup_ptr[w+1] - dup_ptr[w];
+ *   dup_ptr [n_windows + 1] (int64);
+ *   info (device int64[3]) = {cache entries, total duplicates, elements
+ *     outside the windows win_ptr describes}; the caller must reject the
+ *     result when the third is non-zero.
+ * Workspace: ngt_window_dup_workspace_bytes(n_nodes).
+ */
+int ngt_window_dup_workspace_bytes(int64_t n_nodes, size_t* bytes);
+int ngt_window_dup_layout(const int64_t* nodes, int64_t n_nodes, const int64_t* win_ptr,
+                          int32_t n_windows, int32_t min_count, int64_t* reranged,
+                          int64_t* dup_ptr, int64_t* cache_ids, int64_t* dup_index,
+                          int64_t* info, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Sequential segmented sum: out[s] = vals[seg[s]] + ... + vals[seg[s+1]-1],

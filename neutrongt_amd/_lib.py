@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libngt_attn.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 NGT_F32 = 0
 NGT_BF16 = 1
@@ -107,11 +107,13 @@ SIGNATURES = {
     "ngt_sparse_bwd_bias": [_i32, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _pcsr, _i32, _i32,
                             _f32, _f32, _f32, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
     "ngt_edge_bias_grad": [_pcsr, _i32, _vp, _vp, _i64, _i64, _i64, _vp],
-    "ngt_dense_bias_softmax_fwd": [_i32, _i32, _i32, _vp, _f32, _vp, _vp, _f32, _u64, _vp, _vp,
-                                   _vp, _vp, _vp],
-    "ngt_dense_bias_softmax_bwd": [_i32, _i32, _i32, _vp, _vp, _vp, _f32, _u64, _vp, _vp, _vp],
+    "ngt_dense_bias_softmax_fwd": [_i32, _i32, _i32, _i32, _vp, _f32, _vp, _vp, _f32, _u64, _vp,
+                                   _vp, _vp, _vp, _vp],
+    "ngt_dense_bias_softmax_bwd": [_i32, _i32, _i32, _i32, _vp, _vp, _vp, _f32, _u64, _vp, _vp,
+                                   _vp],
+    "ngt_dense_abs_head_sum": [_i32, _i32, _i32, _vp, _f32, _i32, _vp, _vp],
     "ngt_dense_abs_colsum_workspace_bytes": [_i32, _psz],
-    "ngt_dense_abs_colsum": [_i32, _i32, _i32, _vp, _f32, _vp, _vp, _sz, _vp],
+    "ngt_dense_abs_colsum": [_i32, _i32, _i32, _vp, _vp, _vp, _sz, _vp],
     "ngt_dense_workspace_bytes": [_i32, _i32, _i32, _i32, _i32, _i32, _psz, _psz],
     "ngt_dense_fwd": [_i32, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32, _f32, _u64, _vp, _vp,
                       _vp, _vp, _vp, _vp, _sz, _vp],
@@ -132,6 +134,8 @@ SIGNATURES = {
     "ngt_adj_weights_workspace_bytes": [_i64, _i64, _psz],
     "ngt_adj_weights": [_vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
     "ngt_gather_rows": [_vp, _i64, _vp, _i64, _i64, _vp, _vp, _vp],
+    "ngt_window_dup_workspace_bytes": [_i64, _psz],
+    "ngt_window_dup_layout": [_vp, _i64, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
     "ngt_segment_sum_f32": [_vp, _i64, _vp, _i64, _vp, _vp, _vp],
     "ngt_ppr_count_workspace_bytes": [_i32, _vp],
     "ngt_ppr_count": [_vp, _i64, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _sz, _vp],
@@ -203,6 +207,12 @@ def autograd_ext():
                 spec = importlib.util.spec_from_file_location("ngt_autograd", EXT_PATH)
                 mod = importlib.util.module_from_spec(spec)
                 spec.loader.exec_module(mod)
+                ext_abi = mod.abi_version() if hasattr(mod, "abi_version") else None
+                if ext_abi != lib.ngt_abi_version():
+                    # the entry points handed over below are cast to the
+                    # prototypes the extension was compiled with
+                    raise RuntimeError(f"{EXT_PATH.name} was built against ABI version {ext_abi}, "
+                                       f"the library is {lib.ngt_abi_version()}; rebuild it")
                 if mod.csr_struct_bytes() != C.sizeof(WindowCSR):
                     raise RuntimeError(f"{EXT_PATH.name} was built against another "
                                        "ngt_window_csr; rebuild it")

@@ -340,51 +340,112 @@ class DenseAttentionFunction(torch.autograd.Function):
         return gq, gk, gv, None, None, None, None, None
 
 
+# Bytes of [n_q, n_k] fp32 matrices that the materialized dense path may hold
+# at once for its head chunks (S, P, P o M, dL/d(P o M) and dS per head); a
+# window runs as many heads per chunk as fit, at least one.
+DENSE_BIAS_BUDGET_BYTES = 4 << 30
+_DENSE_BIAS_MATS_PER_HEAD = 5
+
+
+def dense_bias_head_chunk(H: int, n_q: int, n_k: int, budget: int = None) -> int:
+    """Heads per chunk of the materialized dense path: as many as keep
+    5 [n_q, n_k] fp32 matrices per head within ``budget`` bytes (default
+    DENSE_BIAS_BUDGET_BYTES) and the softmax launches within 2^24 rows, at
+    least one and at most H."""
+    budget = DENSE_BIAS_BUDGET_BYTES if budget is None else int(budget)
+    per_head = _DENSE_BIAS_MATS_PER_HEAD * 4 * max(n_q, 1) * max(n_k, 1)
+    c = max(1, min(H, budget // per_head))
+    return max(1, min(c, (1 << 24) // max(n_q, 1)))
+
+
+def _f32_contig(*ts):
+    for t in ts:
+        if t is not None and (t.dtype != torch.float32 or not t.is_contiguous()):
+            raise RuntimeError(f"internal: dense-bias operand is {t.dtype}, contiguous="
+                               f"{t.is_contiguous()} (needs contiguous float32)")
+
+
 class DenseAttentionBiasFunction(torch.autograd.Function):
     """full_attention with the reference's optional terms
     (graphormer_dist_node_level.py:51-58): out = dropout_p(softmax(z)) v with
     z = mask ? -1e9 : (q*scale) k^T + bias per head, node_score[j] =
     sum_i mean_h |(q*scale) k^T|.  ``bias`` [H, N_q, N_k] fp32 (attn_bias +
     pruning_mask, or None), ``mask`` [N_q, N_k] uint8 (nonzero = filled, or
-    None).  The products run as library GEMMs in fp32 (the reference's own
-    materialized form: a dense bias is O(N_q N_k H) whatever the kernel);
-    logits, mask, softmax, dropout (the fused kernels' hash mask for the same
-    seed), the softmax backward and the node scores are the library's
-    ngt_dense_bias_* / ngt_dense_abs_colsum kernels.  ``bias`` gets dS as
-    its gradient (zero where masked)."""
+    None).  The products run as library GEMMs in fp32, one head at a time
+    (the reference's own materialized form: a dense bias is O(N_q N_k H)
+    whatever the kernel); logits, mask, softmax, dropout (the fused kernels'
+    hash mask for the same seed), the softmax backward and the node scores
+    are the library's ngt_dense_bias_* / ngt_dense_abs_* kernels.  The heads
+    run ``head_chunk`` at a time and the backward recomputes S and P per
+    chunk, so no [H, N_q, N_k] intermediate is kept; each head's arithmetic
+    is the same whatever the chunk, so every chunk size gives the same bits.
+    Autocast is off inside (every operand is fp32).  ``bias`` gets dS as its
+    gradient (zero where masked)."""
 
     @staticmethod
-    def forward(ctx, q, k, v, bias, mask, scale, want_scores, dropout_p=0.0, seed=0, seed_t=None):
-        lib = _lib.load()
-        n_q, H, d = q.shape
-        n_k = k.shape[0]
-        dev = q.device
-        st = _stream(dev)
-        qh = q.permute(1, 0, 2).float().contiguous()
-        kh = k.permute(1, 0, 2).float().contiguous()
-        vh = v.permute(1, 0, 2).float().contiguous()
-        s = torch.bmm(qh, kh.transpose(1, 2).contiguous())  # [H, n_q, n_k]
-        ns = torch.zeros(n_k if want_scores else 0, dtype=torch.float32, device=dev)
-        if want_scores and n_k and n_q:
-            wb = C.c_size_t()
-            _lib.check(lib.ngt_dense_abs_colsum_workspace_bytes(n_k, C.byref(wb)))
-            ws = _workspace(wb.value, dev)
-            _lib.check(lib.ngt_dense_abs_colsum(H, n_q, n_k, s.data_ptr(), scale, ns.data_ptr(),
-                                                ws.data_ptr(), wb.value, st))
-        drop = dropout_p > 0.0
+    def _chunk_softmax(lib, st, qh, khT, bias, mask, scale, h0, h1, dropout_p, seed, seed_t,
+                       lse=None):
+        """S, P and P o M (or None) of heads h0 .. h1-1."""
+        n_q, n_k = qh.shape[1], khT.shape[2]
+        hc = h1 - h0
+        s = torch.empty(hc, n_q, n_k, dtype=torch.float32, device=qh.device)
+        for h in range(h0, h1):
+            torch.mm(qh[h], khT[h], out=s[h - h0])
         p = torch.empty_like(s)
-        pd = torch.empty_like(s) if drop else None
-        lse = torch.empty(H, n_q, dtype=torch.float32, device=dev)
-        sp = seed_t.data_ptr() if seed_t is not None else None
+        pd = torch.empty_like(s) if dropout_p > 0.0 else None
+        b = bias[h0:h1] if bias is not None else None
+        _f32_contig(s, b)
         _lib.check(lib.ngt_dense_bias_softmax_fwd(
-            H, n_q, n_k, s.data_ptr(), scale, bias.data_ptr() if bias is not None else None,
-            mask.data_ptr() if mask is not None else None, dropout_p, seed, sp, p.data_ptr(),
-            pd.data_ptr() if drop else None, lse.data_ptr(), st))
-        del s
-        o = torch.bmm(pd if drop else p, vh)  # [H, n_q, d]
-        out = o.permute(1, 0, 2).to(q.dtype).contiguous()
-        ctx.save_for_backward(qh, kh, vh, p, pd, mask, seed_t)
-        ctx.scale, ctx.dropout_p, ctx.seed = scale, dropout_p, seed
+            hc, h0, n_q, n_k, s.data_ptr(), scale, b.data_ptr() if b is not None else None,
+            mask.data_ptr() if mask is not None else None, dropout_p, seed,
+            seed_t.data_ptr() if seed_t is not None else None, p.data_ptr(),
+            pd.data_ptr() if pd is not None else None,
+            lse[h0:h1].data_ptr() if lse is not None else None, st))
+        return s, p, pd
+
+    @staticmethod
+    def forward(ctx, q, k, v, bias, mask, scale, want_scores, dropout_p=0.0, seed=0, seed_t=None,
+                head_chunk=None):
+        with torch.autocast("cuda", enabled=False):
+            lib = _lib.load()
+            n_q, H, d = q.shape
+            n_k = k.shape[0]
+            dev = q.device
+            st = _stream(dev)
+            c = int(head_chunk) if head_chunk else dense_bias_head_chunk(H, n_q, n_k)
+            c = max(1, min(c, H))
+            qh = q.permute(1, 0, 2).float().contiguous()  # [H, n_q, d]
+            kh = k.permute(1, 0, 2).float().contiguous()
+            vh = v.permute(1, 0, 2).float().contiguous()
+            khT = kh.transpose(1, 2).contiguous()  # [H, d, n_k]
+            _f32_contig(qh, kh, vh, khT, bias)
+            ns = torch.zeros(n_k if want_scores else 0, dtype=torch.float32, device=dev)
+            scores = bool(want_scores and n_k and n_q)
+            m = torch.empty(n_q, n_k, dtype=torch.float32, device=dev) if scores else None
+            o = torch.empty(H, n_q, d, dtype=torch.float32, device=dev)
+            lse = torch.empty(H, n_q, dtype=torch.float32, device=dev)
+            for h0 in range(0, H, c):
+                h1 = min(H, h0 + c)
+                s, p, pd = DenseAttentionBiasFunction._chunk_softmax(
+                    lib, st, qh, khT, bias, mask, scale, h0, h1, dropout_p, seed, seed_t, lse)
+                if scores:
+                    _lib.check(lib.ngt_dense_abs_head_sum(h1 - h0, n_q, n_k, s.data_ptr(), scale,
+                                                          int(h0 > 0), m.data_ptr(), st))
+                del s
+                pm = pd if pd is not None else p
+                for h in range(h0, h1):
+                    torch.mm(pm[h - h0], vh[h], out=o[h])
+                del p, pd, pm
+            if scores:
+                wb = C.c_size_t()
+                _lib.check(lib.ngt_dense_abs_colsum_workspace_bytes(n_k, C.byref(wb)))
+                ws = _workspace(wb.value, dev)
+                _lib.check(lib.ngt_dense_abs_colsum(H, n_q, n_k, m.data_ptr(), ns.data_ptr(),
+                                                    ws.data_ptr(), wb.value, st))
+                del m
+            out = o.permute(1, 0, 2).to(q.dtype).contiguous()
+        ctx.save_for_backward(qh, khT, vh, bias, mask, seed_t)
+        ctx.scale, ctx.dropout_p, ctx.seed, ctx.chunk = scale, dropout_p, seed, c
         ctx.dtypes = (q.dtype, k.dtype, v.dtype)
         ctx.mark_non_differentiable(ns)
         ctx.set_materialize_grads(False)
@@ -392,37 +453,63 @@ class DenseAttentionBiasFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, g_out, g_ns):
-        qh, kh, vh, p, pd, mask, seed_t = ctx.saved_tensors
+        qh, khT, vh, bias, mask, seed_t = ctx.saved_tensors
         if g_out is None:
-            return (None,) * 10
-        lib = _lib.load()
-        H, n_q, n_k = p.shape
-        dev = p.device
-        st = _stream(dev)
-        gh = g_out.permute(1, 0, 2).float().contiguous()
-        pm = pd if pd is not None else p
-        dpd = torch.bmm(gh, vh.transpose(1, 2).contiguous())  # [H, n_q, n_k]
-        dv = torch.bmm(pm.transpose(1, 2).contiguous(), gh)  # [H, n_k, d]
-        ds = torch.empty_like(p)
-        _lib.check(lib.ngt_dense_bias_softmax_bwd(
-            H, n_q, n_k, p.data_ptr(), dpd.data_ptr(),
-            mask.data_ptr() if mask is not None else None, ctx.dropout_p, ctx.seed,
-            seed_t.data_ptr() if seed_t is not None else None, ds.data_ptr(), st))
-        del dpd
-        dq = torch.bmm(ds, kh) * ctx.scale
-        dk = torch.bmm(ds.transpose(1, 2).contiguous(), qh) * ctx.scale
-        tq, tk, tv = ctx.dtypes
-        return (dq.permute(1, 0, 2).to(tq), dk.permute(1, 0, 2).to(tk), dv.permute(1, 0, 2).to(tv),
-                ds if ctx.needs_input_grad[3] else None, None, None, None, None, None, None)
+            return (None,) * 11
+        with torch.autocast("cuda", enabled=False):
+            lib = _lib.load()
+            H, n_q, d = qh.shape
+            n_k = khT.shape[2]
+            dev = qh.device
+            st = _stream(dev)
+            c = ctx.chunk
+            gh = g_out.permute(1, 0, 2).float().contiguous()  # [H, n_q, d]
+            _f32_contig(gh)
+            dq = torch.empty(H, n_q, d, dtype=torch.float32, device=dev)
+            dk = torch.empty(H, n_k, d, dtype=torch.float32, device=dev)
+            dv = torch.empty(H, n_k, d, dtype=torch.float32, device=dev)
+            want_bias = ctx.needs_input_grad[3]
+            dbias = torch.empty(H, n_q, n_k, dtype=torch.float32, device=dev) if want_bias else None
+            for h0 in range(0, H, c):
+                h1 = min(H, h0 + c)
+                # S and P again, with the forward's calls (the same bits)
+                s, p, pd = DenseAttentionBiasFunction._chunk_softmax(
+                    lib, st, qh, khT, bias, mask, ctx.scale, h0, h1, ctx.dropout_p, ctx.seed,
+                    seed_t)
+                del s
+                pm = pd if pd is not None else p
+                dpd = torch.empty(h1 - h0, n_q, n_k, dtype=torch.float32, device=dev)
+                for h in range(h0, h1):
+                    torch.mm(gh[h], vh[h].t(), out=dpd[h - h0])
+                    torch.mm(pm[h - h0].t(), gh[h], out=dv[h])
+                del pd, pm
+                ds = dbias[h0:h1] if want_bias else torch.empty_like(dpd)
+                _f32_contig(p, dpd, ds)
+                _lib.check(lib.ngt_dense_bias_softmax_bwd(
+                    h1 - h0, h0, n_q, n_k, p.data_ptr(), dpd.data_ptr(),
+                    mask.data_ptr() if mask is not None else None, ctx.dropout_p, ctx.seed,
+                    seed_t.data_ptr() if seed_t is not None else None, ds.data_ptr(), st))
+                del p, dpd
+                for h in range(h0, h1):
+                    torch.mm(ds[h - h0], khT[h].t(), out=dq[h])
+                    torch.mm(ds[h - h0].t(), qh[h], out=dk[h])
+                del ds
+            dq.mul_(ctx.scale)
+            dk.mul_(ctx.scale)
+            tq, tk, tv = ctx.dtypes
+            return (dq.permute(1, 0, 2).to(tq), dk.permute(1, 0, 2).to(tk),
+                    dv.permute(1, 0, 2).to(tv), dbias, None, None, None, None, None, None, None)
 
 
 def dense_attention_bias(q, k, v, scale, attn_bias=None, pruning_mask=None, mask=None,
-                         node_scores=True, dropout_p=0.0, seed=None):
+                         node_scores=True, dropout_p=0.0, seed=None, head_chunk=None):
     """full_attention with attn_bias / pruning_mask / mask as the reference
     applies them (graphormer_dist_node_level.py:51-58): q [1, N_q, H, d],
     k/v [1, N_k, H, d]; attn_bias and pruning_mask broadcast to
     [1, H, N_q, N_k] and added after the scaling; mask (bool, [N_q, N_k])
-    fills with -1e9.  Returns (x [N_q, H, d], node_scores [N_k])."""
+    fills with -1e9.  Returns (x [N_q, H, d], node_scores [N_k]).
+    ``head_chunk``: heads per chunk (default: dense_bias_head_chunk, from
+    DENSE_BIAS_BUDGET_BYTES); the result does not depend on it."""
     H, d = q.shape[-2], q.shape[-1]
     q = _prep(q.reshape(-1, H, d), "q")
     k = _prep(k.reshape(-1, H, d), "k")
@@ -457,7 +544,7 @@ def dense_attention_bias(q, k, v, scale, attn_bias=None, pruning_mask=None, mask
     elif isinstance(seed, torch.Tensor):
         seed_t, seed = seed, None
     return DenseAttentionBiasFunction.apply(q, k, v, bias, mk, float(scale), bool(node_scores),
-                                            dropout_p, int(seed or 0), seed_t)
+                                            dropout_p, int(seed or 0), seed_t, head_chunk)
 
 
 def draw_seed(device) -> torch.Tensor:

@@ -5,14 +5,16 @@ key/src, row 1 = query/dst; NeutronGT/core/node_level_pipeline/
 window_state.py:122-140) and re-derives the grouping with gathers and scatter
 adds on every call (NeutronGT/models/graphormer_dist_node_level.py:75-97).
 Here the window's edge_index is converted once on the GPU
-(``ngt_csr_build``) and cached: the same edge_index object is reused by every
-layer of a window step and across epochs.
+(``ngt_csr_build``) and cached (AdjacencyCache): found again by the same
+edge_index object (every layer of a window step) or by equal contents (a
+fresh device copy of the window's edges each step).
 """
 from __future__ import annotations
 
 import ctypes as C
 import math
 import os
+import weakref
 from collections import OrderedDict
 
 import torch
@@ -108,6 +110,8 @@ class WindowAdjacency:
         ei = edge_index.to(torch.int64).contiguous()
         E = int(ei.shape[1])
         self.edge_index = edge_index  # pins the cache key's storage
+        # a later tensor with the same contents (AdjacencyCache): weak reference, version
+        self.alias, self.alias_version = None, None
         self.n_q, self.n_k, self.n_edges, self.chunk = int(n_q), int(n_k), E, int(chunk)
         small = int(min(max(small, 0), chunk - 1))
         self.small = small  # key-major threshold (and query-major unless pack_q)
@@ -191,24 +195,71 @@ class WindowAdjacency:
 
 
 class AdjacencyCache:
-    """LRU of WindowAdjacency keyed by the edge_index tensor's storage/version."""
+    """LRU of WindowAdjacency, found by the edge_index tensor or by its contents.
 
-    def __init__(self, capacity: int = 64):
+    The same edge_index object (every layer of a window step) is a hit with no
+    device work.  A new tensor with the same contents -- the reference's loop
+    copies the window's edge_index to the device afresh every step
+    (NeutronGT/core/node_level_pipeline/train_eval.py:244) -- is matched by a
+    device-side comparison against the cached windows of the same shape (one
+    host sync), and is remembered through a weak reference, so the other layers
+    of its step hit without comparing again.  An entry whose own edge_index was
+    modified in place is dropped.  The cache holds at most ``capacity``
+    windows and ``max_bytes`` of device memory (their arenas and the
+    edge_index tensors they keep), least recently used first out."""
+
+    def __init__(self, capacity: int = 64, max_bytes: int = 2 << 30):
         self.capacity = capacity
-        self._d: OrderedDict = OrderedDict()
+        self.max_bytes = int(max_bytes)
+        self._d: OrderedDict = OrderedDict()  # id -> (shape key, adjacency, version)
+        self._next = 0
+        self.builds = 0  # windows built (a test and bench counter)
+        self.content_hits = 0
+
+    @staticmethod
+    def _nbytes(adj: WindowAdjacency) -> int:
+        return adj.mem.numel() * 4 + adj.edge_index.numel() * adj.edge_index.element_size()
+
+    def nbytes(self) -> int:
+        return sum(self._nbytes(a) for _, a, _ in self._d.values())
 
     def get(self, edge_index: torch.Tensor, n_q: int, n_k: int, chunk: int,
             small: int = 0, pack_q: bool = False) -> WindowAdjacency:
-        key = (edge_index.data_ptr(), edge_index._version, tuple(edge_index.shape),
-               str(edge_index.device), edge_index.dtype, n_q, n_k, chunk, small, pack_q)
-        adj = self._d.get(key)
-        if adj is not None and adj.edge_index is edge_index:
-            self._d.move_to_end(key)
-            return adj
+        shape_key = (tuple(edge_index.shape), str(edge_index.device), edge_index.dtype, n_q, n_k,
+                     chunk, small, pack_q)
+        same_shape = []
+        for eid in reversed(self._d):  # most recent first
+            key, adj, ver = self._d[eid]
+            if key != shape_key:
+                continue
+            if adj.edge_index._version != ver:
+                continue  # stale: dropped below
+            if adj.edge_index is edge_index:
+                self._d.move_to_end(eid)
+                return adj
+            alias = adj.alias() if adj.alias is not None else None
+            if alias is edge_index and adj.alias_version == edge_index._version:
+                self._d.move_to_end(eid)
+                return adj
+            same_shape.append(eid)
+        for eid in [e for e, (_, a, v) in self._d.items() if a.edge_index._version != v]:
+            del self._d[eid]
+        for eid in same_shape:
+            adj = self._d[eid][1]
+            if torch.equal(adj.edge_index, edge_index):  # one device compare + sync
+                adj.alias = weakref.ref(edge_index)
+                adj.alias_version = edge_index._version
+                self._d.move_to_end(eid)
+                self.content_hits += 1
+                return adj
         adj = WindowAdjacency(edge_index, n_q, n_k, chunk, small, pack_q)
-        self._d[key] = adj
-        while len(self._d) > self.capacity:
-            self._d.popitem(last=False)
+        self.builds += 1
+        self._d[self._next] = (shape_key, adj, edge_index._version)
+        self._next += 1
+        total = self.nbytes()
+        while len(self._d) > 1 and (len(self._d) > self.capacity or total > self.max_bytes):
+            _, (_, old, _) = self._d.popitem(last=False)
+            total -= self._nbytes(old)
         return adj
 
     def clear(self):

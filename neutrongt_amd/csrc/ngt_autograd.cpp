@@ -60,6 +60,21 @@ Tensor rows16(const Tensor& t) {
   return t;
 }
 
+// The library reads rows [n, H, d] of one dtype from 16-byte aligned,
+// contiguous GPU memory on q's device; anything else is an error here rather
+// than wrong reads in the kernels.
+void check_rows(const char* name, const Tensor& t, const Tensor& q) {
+  TORCH_CHECK(t.is_cuda(), name, " must be a GPU tensor");
+  TORCH_CHECK(t.device() == q.device(), name, " is on ", t.device(), ", q on ", q.device());
+  TORCH_CHECK(t.scalar_type() == q.scalar_type(), name, " has dtype ", t.scalar_type(),
+              ", q has ", q.scalar_type());
+  TORCH_CHECK(t.dim() == 3 && t.size(1) == q.size(1) && t.size(2) == q.size(2), name,
+              " must be [n, ", q.size(1), ", ", q.size(2), "], got ", t.sizes());
+  TORCH_CHECK(t.is_contiguous(), name, " must be contiguous");
+  TORCH_CHECK(reinterpret_cast<uintptr_t>(t.data_ptr()) % 16 == 0, name,
+              " must be 16-byte aligned");
+}
+
 Tensor workspace(int64_t bytes, const Tensor& like) {
   return at::empty({std::max<int64_t>(bytes, 1)}, like.options().dtype(at::kByte));
 }
@@ -73,16 +88,26 @@ struct SparseAttention : public torch::autograd::Function<SparseAttention> {
                              double scale, double lo, double hi, double eps, int64_t fwd_bytes,
                              int64_t bwd_bytes) {
     TORCH_CHECK(g_fwd && g_bwd, "ngt_autograd.init() was not called");
+    // an absent argument is an empty optional: autograd inputs may not be
+    // undefined tensors
+    const Tensor k_ext = k_ext_opt.value_or(Tensor()), v_ext = v_ext_opt.value_or(Tensor());
+    const bool ext = k_ext.defined();
+    TORCH_CHECK(ext == v_ext.defined(), "k_ext and v_ext must be given together");
+    check_rows("q", q, q);
+    check_rows("k", k, q);
+    check_rows("v", v, q);
+    TORCH_CHECK(k.sizes() == v.sizes(), "k and v differ in shape: ", k.sizes(), " vs ", v.sizes());
+    if (ext) {
+      check_rows("k_ext", k_ext, q);
+      check_rows("v_ext", v_ext, q);
+      TORCH_CHECK(k_ext.sizes() == v_ext.sizes(), "k_ext and v_ext differ in shape");
+    }
     const int64_t n_q = q.size(0), H = q.size(1), d = q.size(2);
     Tensor out = at::empty_like(q);
     const auto f32 = q.options().dtype(at::kFloat);
     Tensor rinv = at::empty({n_q, H}, f32);
     Tensor ns = at::empty({dst_end}, f32);
     Tensor ws = workspace(fwd_bytes, q);
-    // an absent argument is an empty optional: autograd inputs may not be
-    // undefined tensors
-    const Tensor k_ext = k_ext_opt.value_or(Tensor()), v_ext = v_ext_opt.value_or(Tensor());
-    const bool ext = k_ext.defined();
     check(g_fwd(dtype_code(q), q.data_ptr(), k.data_ptr(), v.data_ptr(),
                 ext ? k_ext.data_ptr() : nullptr, ext ? v_ext.data_ptr() : nullptr,
                 static_cast<int32_t>(k.size(0)), csr_of(csr), static_cast<int32_t>(H),
@@ -161,6 +186,8 @@ void init(int64_t fwd, int64_t bwd, int64_t err) {
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("init", &init, "entry points of libngt_attn.so: fwd, bwd, last_error (addresses)");
   m.def("csr_struct_bytes", []() { return static_cast<int64_t>(sizeof(ngt_window_csr)); });
+  m.def("abi_version", []() { return static_cast<int64_t>(NGT_ABI_VERSION); },
+        "NGT_ABI_VERSION of the header this extension was compiled against");
   m.def("sparse_attention", &sparse_attention,
         "(q, k, v, k_ext, v_ext, csr, csr_mem, dst_end, scale, lo, hi, eps, fwd_bytes, "
         "bwd_bytes) -> (out, node_scores)");

@@ -1492,10 +1492,18 @@ std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxScratchDevices] = {};
 
 // Device address of `scratch` on the current device (looked up on the first
-// call there).
-int scratch_ptr(void** out) {
+// call there).  hipGetSymbolAddress answers for the current device, so a
+// stream of another device is refused: its kernels would be handed this
+// device's copy of the array.
+int scratch_ptr(hipStream_t stream, void** out) {
   int dev = -1;
   NGT_HIP_CHECK(hipGetDevice(&dev));
+  hipDevice_t sdev = -1;
+  NGT_HIP_CHECK(hipStreamGetDevice(stream, &sdev));
+  if (sdev != dev)
+    return set_error(NGT_ERR_ARG,
+                     "ngt_sparse_fwd_noalloc: the stream belongs to device %d, the current device "
+                     "is %d (make the stream's device current)", int(sdev), dev);
   if (dev < 0 || dev >= kMaxScratchDevices)
     return set_error(NGT_ERR_UNSUPPORTED, "ngt_sparse_fwd_noalloc: device %d out of range", dev);
   std::lock_guard<std::mutex> lk(g_scratch_mu);
@@ -1524,7 +1532,7 @@ extern "C" int ngt_sparse_fwd_noalloc(int dtype, const void* q, const void* k, c
                      "buffer holds %zu (use ngt_sparse_fwd with a workspace)",
                      need, kNoAllocScratchBytes);
   void* ws = nullptr;
-  if (need > 0) NGT_CHECK_OK(scratch_ptr(&ws));
+  if (need > 0) NGT_CHECK_OK(scratch_ptr(static_cast<hipStream_t>(stream), &ws));
   return ngt_sparse_fwd(dtype, q, k, v, csr, n_heads, head_dim, scale, clamp_lo, clamp_hi, eps,
                         out, rinv, node_score, node_score_len, ws, need, stream);
 }

@@ -3,8 +3,11 @@
   merge_related_nodes       GPU (ngt_merge_related_nodes); mirrors
                             weightMetis_keepParent._merge_related_nodes,
                             NeutronGT/core/metisPartition.py:397-425
-  duplicate_rerange         NeutronGT/core/node_level_pipeline/window_state.py:52-73
-  dup_cache_metadata        NeutronGT/core/node_level_pipeline/window_state.py:181-205
+  window_dup_layout         GPU (ngt_window_dup_layout); the two functions below
+                            in one pass
+  duplicate_rerange         GPU; NeutronGT/core/node_level_pipeline/window_state.py:52-73
+  dup_cache_metadata        GPU; NeutronGT/core/node_level_pipeline/window_state.py:181-205
+  dup_feature_cache         GPU row gather; window_state.py:204
   assemble_window_features  GPU row gather (ngt_gather_rows); mirrors
                             NeutronGT/core/node_level_pipeline/train_eval.py:234-242
   adj_weights               NeutronGT/core/ppr_preprocess.py:30-71 weight rule,
@@ -15,9 +18,8 @@
                             and metisPartition.py:280,290
   subgraph_from_csr         GPU (ngt_subgraph_csr); window_state.py:92-119
 
-The duplicate bookkeeping is host logic in the reference (torch unique/isin on
-CPU tensors) and stays torch code here; the per-element work (related-node
-ranking, induced subgraphs, feature gathers) runs as HIP kernels.
+Every step runs as HIP kernels; Python only sizes buffers and reads back
+counts.
 """
 from __future__ import annotations
 
@@ -67,42 +69,92 @@ def merge_related_nodes(xadj: torch.Tensor, adjncy: torch.Tensor, eweights: torc
     return out[:length]
 
 
-def duplicate_rerange(local_partitions):
-    """Nodes present in >= 2 of a rank's windows move to the front of each
-    window (original order kept).  Returns (reranged, dup_nodes_per_partition)."""
-    if not local_partitions:
-        return [], []
-    all_nodes = torch.cat([p.to(torch.long).cpu() for p in local_partitions])
-    if all_nodes.numel() == 0:
-        return ([p.clone() for p in local_partitions],
-                [torch.empty((0,), dtype=torch.long) for _ in local_partitions])
-    uniq, counts = torch.unique(all_nodes, return_counts=True, sorted=True)
-    dups = uniq[counts >= 2]
-    if dups.numel() == 0:
-        return ([p.clone() for p in local_partitions],
-                [torch.empty((0,), dtype=torch.long) for _ in local_partitions])
-    reranged, dup_lists = [], []
-    for p in local_partitions:
-        pc = p.to(torch.long).cpu()
-        m = torch.isin(pc, dups)
-        reranged.append(torch.cat([pc[m], pc[~m]]))
-        dup_lists.append(pc[m])
-    return reranged, dup_lists
+def window_dup_layout(local_partitions, device=None, min_count: int = 2):
+    """The duplicate-node layout of a rank's windows in one GPU pass
+    (``ngt_window_dup_layout``): _compute_local_duplicate_nodes
+    (NeutronGT/core/node_level_pipeline/window_state.py:52-73) followed by
+    build_dup_cache_metadata (:181-205).
+
+    ``local_partitions``: the rank's windows, 1-D integer tensors (CPU or GPU).
+    A node is a duplicate when it occurs ``min_count`` or more times over all
+    of them.  Returns (reranged, dup_nodes_per_partition, cache_ids,
+    dup_indices), int64 on ``device`` (default: the current GPU):
+    ``reranged[w]`` is window w with its duplicates first, both parts in their
+    original order; ``dup_nodes_per_partition[w]`` its leading duplicates;
+    ``cache_ids`` the sorted unique duplicates (the rows the feature cache
+    holds); ``dup_indices[w]`` the cache position of each of window w's
+    duplicates.  One device-to-host read (the counts)."""
+    parts = list(local_partitions)
+    dev = torch.device(device) if device is not None else torch.device(
+        "cuda", torch.cuda.current_device())
+    if dev.type != "cuda":
+        raise ValueError("window_dup_layout runs on the GPU")
+    empty = lambda: torch.empty((0,), dtype=torch.long, device=dev)  # noqa: E731
+    if not parts:
+        return [], [], empty(), []
+    lens = [int(p.numel()) for p in parts]
+    T, W = sum(lens), len(parts)
+    nodes = (torch.cat([p.reshape(-1).to(device=dev, dtype=torch.long) for p in parts])
+             if T else empty())
+    ptr = [0]
+    for n in lens:
+        ptr.append(ptr[-1] + n)
+    win_ptr = torch.tensor(ptr, dtype=torch.long).to(dev)
+    lib = _lib.load()
+    nb = C.c_size_t()
+    _lib.check(lib.ngt_window_dup_workspace_bytes(T, C.byref(nb)))
+    ws = torch.empty(max(nb.value, 1), dtype=torch.uint8, device=dev)
+    reranged = torch.empty(max(T, 1), dtype=torch.long, device=dev)
+    cache_ids = torch.empty(max(T, 1), dtype=torch.long, device=dev)
+    dup_index = torch.empty(max(T, 1), dtype=torch.long, device=dev)
+    # the counts come back in one copy: info[3] then dup_ptr[W + 1]
+    counts = torch.empty(3 + W + 1, dtype=torch.long, device=dev)
+    info, dup_ptr = counts[:3], counts[3:]
+    _lib.check(lib.ngt_window_dup_layout(
+        nodes.data_ptr() if T else None, T, win_ptr.data_ptr(), W, int(min_count),
+        reranged.data_ptr(), dup_ptr.data_ptr(), cache_ids.data_ptr(), dup_index.data_ptr(),
+        info.data_ptr(), ws.data_ptr(), nb.value, _lib.stream_ptr(dev)))
+    host = counts.tolist()
+    n_cache, _total, bad = host[:3]
+    dptr = host[3:]
+    if bad:
+        raise ValueError(f"window_dup_layout: {bad} nodes outside the windows (internal error)")
+    rer = list(torch.split(reranged[:T], lens)) if T else [empty() for _ in parts]
+    dups = [r[: dptr[w + 1] - dptr[w]] for w, r in enumerate(rer)]
+    idx = [dup_index[dptr[w]: dptr[w + 1]] for w in range(W)]
+    return rer, dups, cache_ids[:n_cache], idx
+
+
+def duplicate_rerange(local_partitions, device=None):
+    """_compute_local_duplicate_nodes (window_state.py:52-73) on the GPU:
+    nodes present in >= 2 of a rank's windows move to the front of each
+    window (original order kept).  Returns (reranged, dup_nodes_per_partition)
+    as int64 GPU tensors."""
+    rer, dups, _, _ = window_dup_layout(local_partitions, device=device, min_count=2)
+    return rer, dups
 
 
 def dup_cache_metadata(dup_lists, device=None):
-    """(cache_ids sorted unique, per-window indices into the cache)."""
-    non_empty = [d.to(torch.long).cpu() for d in dup_lists if d.numel() > 0]
-    if not non_empty:
-        return (torch.empty((0,), dtype=torch.long),
-                [torch.empty((0,), dtype=torch.long, device=device) for _ in dup_lists])
-    uniq = torch.unique(torch.cat(non_empty), sorted=True)
-    idx = []
-    for d in dup_lists:
-        dc = d.to(torch.long).cpu()
-        t = torch.searchsorted(uniq, dc) if dc.numel() else torch.empty((0,), dtype=torch.long)
-        idx.append(t.to(device=device, dtype=torch.long) if device is not None else t)
-    return uniq, idx
+    """build_dup_cache_metadata (window_state.py:181-205) on the GPU:
+    (cache_ids = the sorted unique ids of ``dup_lists``, per-window indices
+    into it).  Empty ``dup_lists`` give an empty cache and an empty list, as
+    the reference's early return does."""
+    if not list(dup_lists):
+        dev = torch.device(device) if device is not None else torch.device(
+            "cuda", torch.cuda.current_device())
+        return torch.empty((0,), dtype=torch.long, device=dev), []
+    _, _, cache_ids, idx = window_dup_layout(dup_lists, device=device, min_count=1)
+    return cache_ids, idx
+
+
+def dup_feature_cache(feature: torch.Tensor, cache_ids: torch.Tensor) -> torch.Tensor:
+    """feature[cache_ids] on the GPU (the reference's
+    local_dup_nodes_per_partition_feature, window_state.py:204): the cache of
+    duplicate nodes' feature rows that assemble_window_features reads."""
+    out, bad = gather_rows(feature, cache_ids.to(feature.device))
+    if cache_ids.numel() and int(bad.item()):
+        raise IndexError("dup_feature_cache: cache id outside the feature table")
+    return out
 
 
 def gather_rows(src: torch.Tensor, idx: torch.Tensor, out: torch.Tensor | None = None):

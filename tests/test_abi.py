@@ -83,11 +83,15 @@ def test_argument_errors_are_reported_without_touching_the_gpu():
         assert rc == 1 and b"scale" in lib.ngt_last_error()
     # the optional-terms softmax runs one block per (head, query) row: more
     # than 2^24 rows are refused before anything launches
-    rc = lib.ngt_dense_bias_softmax_fwd(256, 65537, 8, None, 1.0, None, None, 0.0, 0, None, None,
+    rc = lib.ngt_dense_bias_softmax_fwd(256, 0, 65537, 8, None, 1.0, None, None, 0.0, 0, None,
+                                        None, None, None, None)
+    assert rc == 1 and b"n_heads * n_q" in lib.ngt_last_error()
+    rc = lib.ngt_dense_bias_softmax_bwd(256, 0, 65537, 8, None, None, None, 0.0, 0, None, None,
+                                        None)
+    assert rc == 1 and b"n_heads * n_q" in lib.ngt_last_error()
+    rc = lib.ngt_dense_bias_softmax_fwd(2, -1, 4, 8, None, 1.0, None, None, 0.0, 0, None, None,
                                         None, None, None)
-    assert rc == 1 and b"n_heads * n_q" in lib.ngt_last_error()
-    rc = lib.ngt_dense_bias_softmax_bwd(256, 65537, 8, None, None, None, 0.0, 0, None, None, None)
-    assert rc == 1 and b"n_heads * n_q" in lib.ngt_last_error()
+    assert rc == 1 and b"bad sizes" in lib.ngt_last_error()
     with pytest.raises(_lib.NGTError):
         _lib.check(1)
 
@@ -175,3 +179,36 @@ def test_autograd_node_loads_and_matches_the_struct_without_touching_the_gpu():
     assert ext is not None, "ngt_autograd.so is not built"
     assert ext.csr_struct_bytes() == C.sizeof(_lib.WindowCSR)
     assert callable(ext.sparse_attention)
+
+
+def test_noalloc_forward_refuses_a_window_beyond_its_static_scratch():
+    # A window whose forward workspace (Z and the split rows' partials) exceeds
+    # the 32 MiB static array is refused before any launch or device query.
+    lib = _lib.load()
+    s = _lib.WindowCSR()
+    s.n_q = s.n_k = 300_000
+    s.n_packed_q = s.n_packed_k = 300_000  # every row packed: the counters are consistent
+    H, d = 32, 24
+    fb, bb = C.c_size_t(), C.c_size_t()
+    assert lib.ngt_sparse_workspace_bytes(C.byref(s), H, d, C.byref(fb), C.byref(bb)) == 0
+    assert fb.value > 32 << 20
+    rc = lib.ngt_sparse_fwd_noalloc(1, None, None, None, C.byref(s), H, d, 4.9, -5.0, 5.0, 1e-6,
+                                    None, None, None, 0, None)
+    assert rc == 2
+    msg = lib.ngt_last_error()
+    assert b"scratch" in msg and b"ngt_sparse_fwd with a workspace" in msg
+    # and the usual argument checks come first
+    rc = lib.ngt_sparse_fwd_noalloc(1, None, None, None, None, H, d, 4.9, -5.0, 5.0, 1e-6, None,
+                                    None, None, 0, None)
+    assert rc == 1 and b"null csr" in lib.ngt_last_error()
+
+
+def test_dense_bias_head_chunk_follows_the_budget():
+    from neutrongt_amd import attention as A
+
+    # 16,000 x 16,000 fp32 is 1.02 GB per matrix: 5 per head exceed 4 GiB
+    assert A.dense_bias_head_chunk(8, 16000, 16000) == 1
+    assert A.dense_bias_head_chunk(8, 1000, 1000) == 8
+    assert A.dense_bias_head_chunk(32, 4000, 4000, budget=1 << 30) == 3
+    # and the softmax launches stay within 2^24 (head, query) rows
+    assert A.dense_bias_head_chunk(64, 1 << 20, 1, budget=1 << 60) == 16

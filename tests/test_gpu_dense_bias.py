@@ -114,3 +114,53 @@ def test_dense_bias_shape_is_checked():
     q = torch.randn(1, 10, 2, 8, device="cuda")
     with pytest.raises(ValueError):
         dense_attention_bias(q, q, q, 8 ** 0.5, attn_bias=torch.zeros(1, 3, 10, 10, device="cuda"))
+
+
+def test_dense_bias_under_bf16_autocast():
+    """The reference's struct_enc path under torch.autocast(bfloat16), as the
+    bf16 window step runs it: the Function computes in fp32 inside (autocast
+    off there), so q/k/v in bf16 give the oracle's result on the same
+    bf16-rounded inputs."""
+    _say("case dense bias under bf16 autocast")
+    n, H, d = 40, 4, 16
+    q, k, v, go, ab, pm, mask = _inputs(n, n, H, d, torch.bfloat16, seed=6)
+    qd, kd, vd = (t.cuda().unsqueeze(0).requires_grad_(True) for t in (q, k, v))
+    abd = ab.cuda().requires_grad_(True)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        x, ns = dense_attention_bias(qd, kd, vd, d ** 0.5, attn_bias=abd, pruning_mask=pm.cuda(),
+                                     mask=mask.cuda())
+    assert x.dtype == torch.bfloat16 and ns.dtype == torch.float32
+    x.backward(go.cuda())
+    torch.cuda.synchronize()
+    res = {"x": x.detach().cpu(), "node_scores": ns.cpu(), "dq": qd.grad[0].cpu(),
+           "dk": kd.grad[0].cpu(), "dv": vd.grad[0].cpu(), "dbias": abd.grad.cpu()}
+    assert abd.grad.dtype == torch.float32
+    _check(res, q, k, v, go, ab, pm, None if mask is None else mask, torch.bfloat16)
+
+
+@pytest.mark.parametrize("p", [0.0, 0.4])
+def test_dense_bias_head_chunks_give_the_one_shot_bits(p):
+    """The materialized path run one head at a time, two at a time and all at
+    once: every output and gradient is bit-identical."""
+    _say(f"case dense bias head chunks p={p}")
+    n_q, n_k, H, d = 70, 90, 5, 8
+    q, k, v, go, ab, pm, mask = _inputs(n_q, n_k, H, d, torch.float32, seed=7)
+    runs = []
+    for chunk in (H, 1, 2):
+        qd, kd, vd = (t.cuda().unsqueeze(0).requires_grad_(True) for t in (q, k, v))
+        abd = ab.cuda().requires_grad_(True)
+        x, ns = dense_attention_bias(qd, kd, vd, d ** 0.5, attn_bias=abd, pruning_mask=pm.cuda(),
+                                     mask=mask.cuda(), dropout_p=p, seed=99, head_chunk=chunk)
+        x.backward(go.cuda())
+        torch.cuda.synchronize()
+        runs.append([x.detach().cpu(), ns.cpu(), qd.grad.cpu(), kd.grad.cpu(), vd.grad.cpu(),
+                     abd.grad.cpu()])
+    for other in runs[1:]:
+        for a, b, name in zip(runs[0], other, ("x", "ns", "dq", "dk", "dv", "dbias")):
+            assert torch.equal(a, b), f"{name} differs between head chunks"
+    mult = OA.dropout_multiplier(99, H, n_q, n_k, p) if p else None
+    res = dict(zip(("x", "node_scores", "dq", "dk", "dv", "dbias"),
+                   [runs[0][0], runs[0][1], runs[0][2][0], runs[0][3][0], runs[0][4][0],
+                    runs[0][5]]))
+    _check(res, q, k, v, go, ab, pm, mask, torch.float32, mult=mult)
+

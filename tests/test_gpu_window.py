@@ -100,13 +100,13 @@ def test_window_feature_assembly_bit_exact():
     rer, dups = W.duplicate_rerange([torch.from_numpy(p) for p in parts])
     cache_ids, idx = W.dup_cache_metadata(dups, device="cuda")
     fd = feat.cuda()
-    cache = fd[cache_ids.cuda()]
+    cache = W.dup_feature_cache(fd, cache_ids)
     for r, i in zip(rer, idx):
-        x = W.assemble_window_features(fd, cache, i, r.cuda())
-        want = OG.assemble_window_features(feat.numpy(), cache_ids.numpy(), i.cpu().numpy(),
-                                           r.numpy())
+        x = W.assemble_window_features(fd, cache, i, r)
+        want = OG.assemble_window_features(feat.numpy(), cache_ids.cpu().numpy(), i.cpu().numpy(),
+                                           r.cpu().numpy())
         assert torch.equal(x.cpu(), torch.from_numpy(want))
-        assert torch.equal(x.cpu(), feat[r])
+        assert torch.equal(x.cpu(), feat[r.cpu()])
 
 
 def test_gather_rows_flags_bad_index():

@@ -142,22 +142,56 @@ def test_duplicate_rerange_and_cache_hand_derived():
         np.testing.assert_array_equal(OG.assemble_window_features(feat, cache_ids, i, r), feat[r])
 
 
-def test_host_dup_logic_matches_oracle():
-    from neutrongt_amd import window as W
+def _dup_alt(parts):
+    """Duplicate layout by counting with a dict and list scans (no unique,
+    isin or searchsorted): the independent form the oracle is checked against."""
+    count = {}
+    for p in parts:
+        for x in p.tolist():
+            count[x] = count.get(x, 0) + 1
+    rer, dups = [], []
+    for p in parts:
+        xs = p.tolist()
+        d = [x for x in xs if count[x] >= 2]
+        rer.append(d + [x for x in xs if count[x] < 2])
+        dups.append(d)
+    cache = sorted({x for x, c in count.items() if c >= 2})
+    idx = [[cache.index(x) for x in d] for d in dups]
+    return rer, dups, cache, idx
 
-    rng = np.random.default_rng(2)
-    parts = [rng.choice(100, 30, replace=False) for _ in range(4)]
-    rer, dups = W.duplicate_rerange([torch.from_numpy(p) for p in parts])
-    rer_o, dups_o = OG.duplicate_rerange(parts)
-    for a, b in zip(rer, rer_o):
-        np.testing.assert_array_equal(a.numpy(), b)
-    for a, b in zip(dups, dups_o):
-        np.testing.assert_array_equal(a.numpy(), b)
-    cache_ids, idx = W.dup_cache_metadata(dups)
-    cache_o, idx_o = OG.dup_cache_metadata(dups_o)
-    np.testing.assert_array_equal(cache_ids.numpy(), cache_o)
-    for a, b in zip(idx, idx_o):
-        np.testing.assert_array_equal(a.numpy(), b)
+
+def dup_cases():
+    """Hand-made windows: none duplicated, all duplicated, a node in 3+
+    windows, an empty window, a node twice in one window, negative and large
+    ids; plus random sets."""
+    cases = [
+        [np.array([4, 2, 9]), np.array([1, 7]), np.array([3])],
+        [np.array([5, 6]), np.array([6, 5]), np.array([5, 6])],
+        [np.array([0, 11, 3]), np.array([11, 4]), np.array([8, 11, 0]), np.array([11])],
+        [np.array([], dtype=np.int64), np.array([2, 3]), np.array([3, 9])],
+        [np.array([7, 7, 1]), np.array([2])],
+        [np.array([-3, 2**40, 5]), np.array([5, -3]), np.array([2**40 + 1])],
+        [np.array([], dtype=np.int64), np.array([], dtype=np.int64)],
+        [np.array([12])],
+    ]
+    rng = np.random.default_rng(11)
+    for t in range(6):
+        W = int(rng.integers(2, 9))
+        n = int(rng.integers(20, 4000))
+        cases.append([rng.choice(n, int(rng.integers(0, min(n, 600))), replace=False)
+                      for _ in range(W)])
+    return cases
+
+
+def test_dup_oracle_matches_counting_form():
+    for parts in dup_cases():
+        rer, dups = OG.duplicate_rerange(parts)
+        cache, idx = OG.dup_cache_metadata(dups)
+        rer_a, dups_a, cache_a, idx_a = _dup_alt(parts)
+        assert [r.tolist() for r in rer] == rer_a
+        assert [d.tolist() for d in dups] == dups_a
+        assert cache.tolist() == cache_a
+        assert [i.tolist() for i in idx] == idx_a
 
 
 # -------------------------------------------------------------- adj weights
