@@ -540,6 +540,38 @@ def model_step_bench(args, cfg, layers: int, dev) -> dict:
     summ = _lib.timing_summary()
     _lib.timing_enable(False)
     attn_ms = sum(v[1] for n, v in summ.items() if n.startswith(("sparse_", "dense_"))) / args.steps
+    copies = {}
+    if not args.graph:
+        # the reference's loop copies the window's edge_index to the device
+        # every step (train_eval.py:244): timed with the cache matching the
+        # copy by contents, and with the cache emptied first (a CSR rebuild
+        # every step, what an identity-keyed cache would do)
+        from neutrongt_amd.csr import default_cache
+
+        ei_host = ei.cpu()
+
+        def step_copy():
+            loss, _ = window_step(model, opt, x, ei_host.to(dev), labels, train_mask, cache,
+                                  torch.bfloat16)
+            return loss.item()
+
+        def step_rebuild():
+            default_cache.clear()
+            return step_copy()
+
+        for name, fn in (("per_step_copy_ms", step_copy), ("per_step_rebuild_ms", step_rebuild)):
+            fn()
+            ts = []
+            for _ in range(args.steps):
+                torch.cuda.synchronize()
+                t = time.perf_counter()
+                fn()
+                torch.cuda.synchronize()
+                ts.append(time.perf_counter() - t)
+            copies[name] = 1e3 * statistics.median(ts)
+        _log(f"[bench] window step with a fresh edge_index copy per step: "
+             f"{copies['per_step_copy_ms']:.2f} ms (CSR found by contents), "
+             f"{copies['per_step_rebuild_ms']:.2f} ms (CSR rebuilt)")
     _log(f"[bench] window step {ms:.2f} ms (median of {args.steps}), attention kernels "
          f"{attn_ms:.2f} ms/step, loss {losses[0]:.4f} -> {losses[-1]:.4f}")
     return {
@@ -553,6 +585,7 @@ def model_step_bench(args, cfg, layers: int, dev) -> dict:
                    "layers": layers, "parameters": n_params, "edges": E,
                    "hip_graph": bool(args.graph)},
         "attention_ms_per_step": attn_ms,
+        **copies,
         "edges_per_s_in_step": layers * E / (ms * 1e-3),
         "losses": [losses[0], losses[-1]],
     }

@@ -121,6 +121,13 @@ typedef struct ngt_window_csr {
   int32_t n_parts_k;
   int32_t n_splits_k;
   int32_t n_packed_k;
+  /* Optional (NULL: not built): rows in descending degree order, ties by
+   * descending row id -- every query row, and the key rows j < min(n_q, n_k)
+   * (the window's own nodes).  The tiled kernels of dense windows schedule
+   * blocks of rows of similar degree from them; without them every window
+   * runs the work-list kernels. */
+  int32_t* order_q;  /* [n_q] */
+  int32_t* order_k;  /* [min(n_q, n_k)] */
 } ngt_window_csr;
 
 int ngt_abi_version(void);

@@ -74,6 +74,8 @@ class WindowCSR(C.Structure):
         ("n_parts_k", C.c_int32),
         ("n_splits_k", C.c_int32),
         ("n_packed_k", C.c_int32),
+        ("order_q", C.c_void_p),
+        ("order_k", C.c_void_p),
     ]
 
 

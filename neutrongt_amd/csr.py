@@ -100,7 +100,10 @@ class WindowAdjacency:
     """Both CSR orientations of one window plus its work lists (int32, on device)."""
 
     def __init__(self, edge_index: torch.Tensor, n_q: int, n_k: int, chunk: int, small: int = 0,
-                 pack_q: bool = False):
+                 pack_q: bool = False, tiled: bool = True):
+        """``tiled``: also build the rows' degree orders (order_q, order_k), which
+        let the library run its tiled kernels on dense windows; without them
+        every window runs the work-list kernels."""
         if edge_index.dim() != 2 or edge_index.shape[0] != 2:
             raise ValueError(f"edge_index must be [2, E], got {tuple(edge_index.shape)}")
         if not edge_index.is_cuda:
@@ -129,6 +132,9 @@ class WindowAdjacency:
                   ("items_k", (mik.value, 4)), ("splits_k", (msk.value, 4)),
                   ("packed_q", (max(n_q, 1),)), ("packed_k", (max(n_k, 1),)),
                   ("info_dev", (_lib.INFO_LEN,)))
+        if tiled:
+            layout = layout + (("order_q", (max(n_q, 1),)),
+                               ("order_k", (max(min(n_q, n_k), 1),)))
         offs, total = [], 0
         for _, shape in layout:
             offs.append(total)
@@ -141,8 +147,10 @@ class WindowAdjacency:
         s.n_q, s.n_k, s.n_edges, s.chunk_q, s.chunk_k = n_q, n_k, E, chunk, chunk
         s.small_q, s.small_k = small_q, small
         for name in ("rowptr", "col", "perm", "t_rowptr", "t_col", "t_perm", "q2t", "items_q",
-                     "splits_q", "packed_q", "items_k", "splits_k", "packed_k"):
+                     "splits_q", "packed_q", "items_k", "splits_k", "packed_k") + (
+                         ("order_q", "order_k") if tiled else ()):
             setattr(s, name, getattr(self, name).data_ptr())
+        self.tiled = tiled
         s.info = self.info_dev.data_ptr()
         s.max_items_q, s.max_splits_q = miq.value, msq.value
         s.max_items_k, s.max_splits_k = mik.value, msk.value

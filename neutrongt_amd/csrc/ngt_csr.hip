@@ -5,7 +5,9 @@
 //   rows with small < degree <= chunk -> one work item per row, longest first,
 //   rows with degree <= small         -> packed list, longest first; the
 //                                        kernels give each such row one edge
-//                                        slot (several rows per wave).
+//                                        slot (several rows per wave);
+// and, when asked for, the rows longest first (the tiled kernels' order): all
+// query rows, and the key rows j < min(n_q, n_k) (the window's own nodes).
 //
 // The reference keeps the window mask as a COO edge_index
 // (NeutronGT/core/node_level_pipeline/window_state.py:122-140) and consumes it
@@ -180,8 +182,8 @@ __global__ void k_emit_sorted(const int32_t* __restrict__ rowptr, int32_t n_rows
                               int32_t small_in, const uint32_t* __restrict__ sdeg,
                               const int32_t* __restrict__ srow, const Count3* __restrict__ scan,
                               int4* __restrict__ items, int32_t* __restrict__ packed,
-                              int32_t* __restrict__ info, int info_base, int packed_slot,
-                              int small_slot) {
+                              int32_t* __restrict__ order, int32_t* __restrict__ info,
+                              int info_base, int packed_slot, int small_slot) {
   const int32_t small = small_in < 0 ? packing_threshold(sdeg, n_rows, chunk) : small_in;
   const int32_t n_small = upper_bound_u32(sdeg, n_rows, static_cast<uint32_t>(small));
   const int32_t n_le_chunk = upper_bound_u32(sdeg, n_rows, static_cast<uint32_t>(chunk));
@@ -209,6 +211,18 @@ __global__ void k_emit_sorted(const int32_t* __restrict__ rowptr, int32_t n_rows
       items[tot.split_items + (n_le_chunk - 1 - p)] = make_int4(r, rowptr[r], rowptr[r + 1], -1);
     }
   }
+  // every row, longest first (when the order covers all rows)
+  if (order)
+    for (int32_t p = blockIdx.x * blockDim.x + threadIdx.x; p < n_rows;
+         p += gridDim.x * blockDim.x)
+      order[n_rows - 1 - p] = srow[p];
+}
+
+// order[n - 1 - p] = srow[p]: rows sorted by ascending degree, reversed.
+__global__ void k_emit_order(const int32_t* __restrict__ srow, int32_t n,
+                             int32_t* __restrict__ order) {
+  for (int32_t p = blockIdx.x * blockDim.x + threadIdx.x; p < n; p += gridDim.x * blockDim.x)
+    order[n - 1 - p] = srow[p];
 }
 
 __global__ void k_ends(const uint64_t* __restrict__ key_q, const uint64_t* __restrict__ key_k,
@@ -233,7 +247,8 @@ inline int grid_for(int64_t n) {
 }
 
 struct CsrLayout {
-  size_t key_a, key_b, key_c, eid, tpos, cnt, cnt_scan, deg_a, deg_b, row_a, row_b, temp, total;
+  size_t key_a, key_b, key_c, eid, tpos, cnt, cnt_scan, deg_a, deg_b, row_a, row_b, deg_c, row_c,
+      temp, total;
   size_t temp_bytes;
 };
 
@@ -264,6 +279,8 @@ int csr_layout(int64_t E, int32_t n_q, int32_t n_k, CsrLayout* L) {
   L->deg_b = take(size_t(n_rows + 1) * 4);
   L->row_a = take(size_t(n_rows + 1) * 4);
   L->row_b = take(size_t(n_rows + 1) * 4);
+  L->deg_c = take(size_t(n_rows + 1) * 4);
+  L->row_c = take(size_t(n_rows + 1) * 4);
   size_t deg_sort_bytes = 0;
   NGT_HIP_CHECK(rocprim::radix_sort_pairs(nullptr, deg_sort_bytes, (uint32_t*)nullptr,
                                           (uint32_t*)nullptr, (int32_t*)nullptr,
@@ -276,8 +293,11 @@ int csr_layout(int64_t E, int32_t n_q, int32_t n_k, CsrLayout* L) {
   return NGT_OK;
 }
 
+// order (optional): the first n_order rows (all rows when n_order == n_rows),
+// longest first.
 int build_worklist(const int32_t* rowptr, int32_t n_rows, int32_t chunk, int32_t small,
-                   int4* items, int4* splits, int32_t* packed, int32_t* info, int info_base,
+                   int4* items, int4* splits, int32_t* packed, int32_t* order, int32_t n_order,
+                   int32_t* info, int info_base,
                    int packed_slot, int small_slot, int max_deg_slot, char* ws,
                    const CsrLayout& L, hipStream_t st) {
   Count3* cnt = reinterpret_cast<Count3*>(ws + L.cnt);
@@ -288,7 +308,7 @@ int build_worklist(const int32_t* rowptr, int32_t n_rows, int32_t chunk, int32_t
   int32_t* row_b = reinterpret_cast<int32_t*>(ws + L.row_b);
   if (n_rows == 0) {
     hipLaunchKernelGGL(k_emit_sorted, dim3(1), dim3(kBlock), 0, st, rowptr, n_rows, chunk, small,
-                       deg_b, row_b, scan, items, packed, info, info_base, packed_slot,
+                       deg_b, row_b, scan, items, packed, order, info, info_base, packed_slot,
                        small_slot);
     NGT_HIP_CHECK(hipGetLastError());
     return NGT_OK;
@@ -305,10 +325,23 @@ int build_worklist(const int32_t* rowptr, int32_t n_rows, int32_t chunk, int32_t
   temp_bytes = L.temp_bytes;
   NGT_HIP_CHECK(rocprim::radix_sort_pairs(ws + L.temp, temp_bytes, deg_a, deg_b, row_a, row_b,
                                           size_t(n_rows), 0u, 32u, st));
+  const bool full_order = order && n_order >= n_rows;
   hipLaunchKernelGGL(k_emit_sorted, dim3(grid_for(n_rows)), dim3(kBlock), 0, st, rowptr, n_rows,
-                     chunk, small, deg_b, row_b, scan, items, packed, info, info_base,
-                     packed_slot, small_slot);
+                     chunk, small, deg_b, row_b, scan, items, packed,
+                     full_order ? order : nullptr, info, info_base, packed_slot, small_slot);
   NGT_HIP_CHECK(hipGetLastError());
+  if (order && !full_order && n_order > 0) {
+    // the leading rows alone: (degree, row) of rows [0, n_order) are the
+    // first n_order entries of deg_a / row_a (row order)
+    uint32_t* deg_c = reinterpret_cast<uint32_t*>(ws + L.deg_c);
+    int32_t* row_c = reinterpret_cast<int32_t*>(ws + L.row_c);
+    temp_bytes = L.temp_bytes;
+    NGT_HIP_CHECK(rocprim::radix_sort_pairs(ws + L.temp, temp_bytes, deg_a, deg_c, row_a, row_c,
+                                            size_t(n_order), 0u, 32u, st));
+    hipLaunchKernelGGL(k_emit_order, dim3(grid_for(n_order)), dim3(kBlock), 0, st, row_c, n_order,
+                       order);
+    NGT_HIP_CHECK(hipGetLastError());
+  }
   return NGT_OK;
 }
 
@@ -422,12 +455,14 @@ extern "C" int ngt_csr_build(const int64_t* edge_index, ngt_window_csr* csr, voi
   }
   rc = build_worklist(csr->rowptr, n_q, csr->chunk_q, csr->small_q,
                       reinterpret_cast<int4*>(csr->items_q), reinterpret_cast<int4*>(csr->splits_q),
-                      csr->packed_q, csr->info, NGT_INFO_ITEMS_Q, NGT_INFO_PACKED_Q,
+                      csr->packed_q, csr->order_q, n_q, csr->info, NGT_INFO_ITEMS_Q,
+                      NGT_INFO_PACKED_Q,
                       NGT_INFO_SMALL_Q, NGT_INFO_MAX_DEG_Q, ws, L, st);
   if (rc != NGT_OK) return rc;
   rc = build_worklist(csr->t_rowptr, n_k, csr->chunk_k, csr->small_k,
                       reinterpret_cast<int4*>(csr->items_k), reinterpret_cast<int4*>(csr->splits_k),
-                      csr->packed_k, csr->info, NGT_INFO_ITEMS_K, NGT_INFO_PACKED_K,
+                      csr->packed_k, csr->order_k, n_q < n_k ? n_q : n_k, csr->info,
+                      NGT_INFO_ITEMS_K, NGT_INFO_PACKED_K,
                       NGT_INFO_SMALL_K, NGT_INFO_MAX_DEG_K, ws, L, st);
   return rc;
 }

@@ -543,14 +543,16 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
     int32_t L, float inv_scale, float lo, float hi, T* __restrict__ grad_k,
     T* __restrict__ grad_v, float* __restrict__ ds, float* __restrict__ part_kv,
     const int32_t* __restrict__ t_rowptr, const int32_t* __restrict__ packed, int32_t n_packed,
-    int32_t n_pwaves, int32_t xcd, const float* __restrict__ eb, float* __restrict__ deb) {
+    int32_t n_pwaves, int32_t xcd, const float* __restrict__ eb, float* __restrict__ deb,
+    int32_t row_min) {
+  // key rows < row_min are left to another pass (the tiled one)
   const int64_t gw0 = virtual_wave(n_items, n_pwaves, n_groups, xcd);
   if (gw0 < 0) return;
   if (gw0 >= int64_t(n_items) * n_groups) {
     int64_t prow;
     int ph;
     if (packed_work(gw0 - int64_t(n_items) * n_groups, n_pwaves, n_groups, hg, L, H, packed,
-                    n_packed, prow, ph))
+                    n_packed, prow, ph) && prow >= row_min)
       bwd_kv_packed<T, DH, BIAS, NT>(q, kv, g, rd, t_rowptr, t_col, prow, ph, H, inv_scale, lo,
                                      hi, grad_k, grad_v, ds, eb, deb);
     return;
@@ -560,6 +562,7 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
   if (!wave_work(gw0, n_items, n_groups, hg, L, H, item, ln)) return;
   const int4 it = items[item];
   const int64_t row = it.x;
+  if (row < row_min) return;  // uniform per wave
   const int h = ln.h;
   const int S = ln.S;
 
@@ -648,10 +651,11 @@ __device__ __forceinline__ void bwd_kv_finalize_tile(const int4* __restrict__ sp
                                                      const float* __restrict__ part_kv,
                                                      T* __restrict__ grad_k,
                                                      T* __restrict__ grad_v, int64_t n_main,
-                                                     int split, int tile) {
+                                                     int split, int tile, int32_t row_min) {
   __shared__ float red[kWavesPerBlock][kColTile];
   const int4 sp = splits[split];
   if (sp.x >= n_main) return;  // constant key row: no gradient (uniform per block)
+  if (sp.x < row_min) return;  // a row another pass handles (uniform per block)
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x >> 6;
   const int ncols = 2 * H * DH;
@@ -766,13 +770,15 @@ __global__ __launch_bounds__(kBlock) void k_bwd_q(
     float* __restrict__ part_q, const int32_t* __restrict__ rowptr,
     const int32_t* __restrict__ packed, int32_t n_packed, int32_t n_pwaves, int32_t q_blocks,
     const int4* __restrict__ splits_k, int32_t kv_tiles, const float* __restrict__ part_kv,
-    T* __restrict__ grad_k, T* __restrict__ grad_v, int32_t xcd, const RecomputeArgs rc) {
+    T* __restrict__ grad_k, T* __restrict__ grad_v, int32_t xcd, const RecomputeArgs rc,
+    int32_t kv_row_min) {
   // Blocks past the dQ work finish the split key rows of bwd_kv (their dK/dV
-  // partials): that work is independent of dQ, so it rides in this launch.
+  // partials; rows >= kv_row_min): that work is independent of dQ, so it
+  // rides in this launch.
   if (int32_t(blockIdx.x) >= q_blocks) {
     const int f = int(blockIdx.x) - q_blocks;
     bwd_kv_finalize_tile<T, DH>(splits_k, H, part_kv, grad_k, grad_v, kv.n_main, f / kv_tiles,
-                                f % kv_tiles);
+                                f % kv_tiles, kv_row_min);
     return;
   }
   const int64_t gw0 = virtual_wave(n_items, n_pwaves, n_groups, xcd);
@@ -882,6 +888,480 @@ __global__ __launch_bounds__(kBlock) void k_bwd_q_finalize(const int4* __restric
   elem<T>::store(grad_q + int64_t(sp.x) * ncols + col, a);
 }
 
+// ------------------------------------------------------ tiled (dense windows)
+// On windows where a large share of the possible (query, key) pairs are edges
+// (the high-degree GT windows: about 7 % of the in-window pairs), the
+// work-list kernels' row gathers nearly all hit the L2 and run at its request
+// rate.  The tiled kernels read each row slice once per block of rows
+// instead.  A block owns QB = 4 * S rows (taken in descending degree order,
+// so that its rows have similar degrees), one head group of hg heads and one
+// part of the swept column range.  It walks the part in column blocks: the
+// block first copies the column block's row slices into LDS with coalesced
+// loads, then every edge slot walks its own row's edges into the column block
+// (columns are sorted within a row) and reads the other side's slices from
+// LDS.  A row's accumulators stay in registers for the whole part; the
+// parts' sums are added in part order by a finalize kernel, so the result is
+// deterministic and no atomics are used.  The number of parts of a row block
+// follows the degree of its first (longest) row, about e_slot edges per slot
+// and part, so that blocks of hub rows are cut finer than the rest.
+//
+// Query-major (k_q_tiled): rows are queries, columns keys, the swept columns
+// [0, n_sweep) with n_sweep = min(n_q, n_k) (the window's own nodes); K and V
+// slices are staged.  The sparse columns >= n_sweep (related keys) are
+// gathered from global memory by the last part.  MODE 0 is the forward
+// (partials of sum p v and Z), MODE 1 the dQ pass with each edge's da
+// recomputed from K and V (partials of sum da k).
+// Key-major (k_kv_tiled): rows are the keys j < n_sweep, columns every query;
+// Q and dO slices and {r, rD} are staged.  Partials are indexed by the row's
+// position in the degree order.
+
+// First position p in [lo, hi) with col[p] >= x (hi if none); col sorted.
+__device__ __forceinline__ int lower_bound_col(const int32_t* __restrict__ col, int lo, int hi,
+                                               int x) {
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (col[mid] < x) lo = mid + 1; else hi = mid;
+  }
+  return lo;
+}
+
+// Parts of the row block whose first (longest) row sits at order position
+// `first`: ceil(degree / e_slot), at least 1, at most p_max and the number
+// of column blocks.
+__device__ __forceinline__ int tile_row_parts(const int32_t* __restrict__ rowptr,
+                                              const int32_t* __restrict__ order, int64_t first,
+                                              int e_slot, int p_max, int n_cols, int kb) {
+  const int64_t r0 = order[first];
+  const int deg = rowptr[r0 + 1] - rowptr[r0];
+  const int nb = (n_cols + kb - 1) / kb;
+  int p = (deg + e_slot - 1) / e_slot;
+  p = min(p, min(p_max, nb));
+  return p < 1 ? 1 : p;
+}
+
+// Slot geometry of a tiled block: lane -> (slot, head); block -> (row block,
+// part, head group) with the head group fastest.  Blocks past their row
+// block's part count are empty (live false: they leave before any barrier).
+struct TileTask {
+  int g, part, n_parts, hl, h, slot, c0, c1;
+  int64_t ridx;
+  bool act, live;
+};
+
+__device__ __forceinline__ TileTask tile_task(const int32_t* __restrict__ rowptr,
+                                              const int32_t* __restrict__ order, int n_rows,
+                                              int n_cols, int n_groups, int p_max, int e_slot,
+                                              int hg, int L, int kb) {
+  TileTask t;
+  const unsigned per_rb = unsigned(n_groups * p_max);
+  const int gp = int(blockIdx.x % per_rb);
+  const int64_t rb = int64_t(blockIdx.x / per_rb);
+  t.g = gp % n_groups;
+  t.part = gp / n_groups;
+  const int S = kWave / L;
+  const int64_t rows_per_block = int64_t(kWavesPerBlock) * S;
+  t.n_parts = tile_row_parts(rowptr, order, rb * rows_per_block, e_slot, p_max, n_cols, kb);
+  t.live = t.part < t.n_parts;
+  int cols = (n_cols + t.n_parts - 1) / t.n_parts;
+  cols = (cols + kb - 1) / kb * kb;
+  t.c0 = min(n_cols, t.part * cols);
+  t.c1 = min(n_cols, t.c0 + cols);
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+  t.hl = lane & (L - 1);
+  t.slot = lane / L;
+  t.h = t.g * hg + t.hl;
+  t.act = t.hl < hg;
+  t.ridx = rb * rows_per_block + int64_t(wave) * S + t.slot;
+  (void)n_rows;
+  return t;
+}
+
+template <typename T, int DH>
+__device__ __forceinline__ void lds_words(const uint4* __restrict__ p, RowWords<T, DH>& r) {
+#pragma unroll
+  for (int i = 0; i < RowWords<T, DH>::NV; ++i) r.w[i] = p[i];
+}
+
+// Loads per thread (of each staged tensor) in flight before the stores to LDS.
+constexpr int kStageBatch = 4;
+
+// Copies words t = threadIdx.x, + kBlock, ... < n of two tensors to LDS in
+// batches of B per thread: load(t, a, b) reads them, store(t, a, b) writes
+// them; the B loads of a batch are issued before its first store.
+template <int B, typename Load, typename Store>
+__device__ __forceinline__ void stage_words(int n, Load load, Store store) {
+  for (int t0 = threadIdx.x; t0 < n; t0 += B * kBlock) {
+    uint4 a0, b0, a1, b1, a2, b2, a3, b3;
+    static_assert(B == 4, "four words per batch");
+    const int t1 = t0 + kBlock, t2 = t0 + 2 * kBlock, t3 = t0 + 3 * kBlock;
+    if (t0 < n) load(t0, a0, b0);
+    if (t1 < n) load(t1, a1, b1);
+    if (t2 < n) load(t2, a2, b2);
+    if (t3 < n) load(t3, a3, b3);
+    if (t0 < n) store(t0, a0, b0);
+    if (t1 < n) store(t1, a1, b1);
+    if (t2 < n) store(t2, a2, b2);
+    if (t3 < n) store(t3, a3, b3);
+  }
+}
+
+// Staged slices are padded by one 16-byte word per column, so that the
+// slices of consecutive columns start in different LDS banks.
+template <typename T, int DH>
+__host__ __device__ constexpr int tile_stride(int hg) {
+  return hg * RowWords<T, DH>::NV + 1;
+}
+
+template <typename T, int DH, bool EXT, int MODE>
+__global__ __launch_bounds__(kBlock) void k_q_tiled(
+    const T* __restrict__ q, const Keys<T, EXT> kv, const int32_t* __restrict__ rowptr,
+    const int32_t* __restrict__ col, const int32_t* __restrict__ order, int32_t n_q,
+    int32_t n_sweep, int32_t H, int32_t hg, int32_t L, int32_t n_groups, int32_t p_max,
+    int32_t e_slot, int32_t kb, float inv_scale, float lo, float hi, const RecomputeArgs rc,
+    float* __restrict__ part_acc, float* __restrict__ part_z) {
+  extern __shared__ uint4 stage[];
+  constexpr int NV = RowWords<T, DH>::NV;
+  constexpr int U = unroll_for(2 * NV, NGT_FWD_WORDS);
+  const TileTask tk = tile_task(rowptr, order, n_q, n_sweep, n_groups, p_max, e_slot, hg, L, kb);
+  if (!tk.live) return;  // uniform over the block
+  const bool work = tk.ridx < n_q && tk.act;
+  const int64_t row = work ? order[tk.ridx] : 0;
+  const int h = tk.h;
+  int pos = 0, pend = 0, tail_end = 0;
+  if (work) {
+    const int beg = rowptr[row], end = rowptr[row + 1];
+    pos = lower_bound_col(col, beg, end, tk.c0);
+    pend = lower_bound_col(col, pos, end, tk.c1);
+    tail_end = tk.part == tk.n_parts - 1 ? end : pend;  // the last part: columns >= n_sweep
+  }
+  RowWords<T, DH> qw, gw;
+  float2 rr = make_float2(0.f, 0.f);
+  if (work) {
+    load_words<T, DH>((MODE == 0 ? q : static_cast<const T*>(rc.q)) + (row * H + h) * DH, qw);
+    if constexpr (MODE == 1) {
+      load_words<T, DH>(static_cast<const T*>(rc.g) + (row * H + h) * DH, gw);
+      rr = rc.rd[row * H + h];
+    }
+  } else {
+    zero_words<T, DH>(qw);
+    zero_words<T, DH>(gw);
+  }
+  float acc[DH];
+  float z = 0.f;
+#pragma unroll
+  for (int c = 0; c < DH; ++c) acc[c] = 0.f;
+  auto edge = [&](const RowWords<T, DH>& kw, const RowWords<T, DH>& vw) {
+    if constexpr (MODE == 0) {
+      const float p = __expf(clampf(edge_dot<T, DH>(qw, kw) * inv_scale, lo, hi));
+      z += p;
+#pragma unroll
+      for (int c = 0; c < DH; ++c) acc[c] = fmaf(p, word_elem<T, DH>(vw, c), acc[c]);
+    } else {
+      const float d = recompute_da<T, DH>(qw, gw, rr, kw, vw, inv_scale, lo, hi);
+#pragma unroll
+      for (int c = 0; c < DH; ++c) acc[c] = fmaf(d, word_elem<T, DH>(kw, c), acc[c]);
+    }
+  };
+  const int slice = hg * NV;                  // 16-byte words of one column's K (or V) slice
+  const int stride = tile_stride<T, DH>(hg);  // padded
+  uint4* ks = stage;
+  uint4* vs = stage + int64_t(kb) * stride;
+  for (int cb = tk.c0; cb < tk.c1; cb += kb) {
+    const int nc = min(kb, tk.c1 - cb);
+    __syncthreads();  // the previous column block's readers are done
+    // kStageBatch words of K and of V per thread in flight before any is stored
+    stage_words<kStageBatch>(nc * slice, [&](int t, uint4& a, uint4& b) {
+      const int jl = t / slice, w = t - jl * slice;
+      a = reinterpret_cast<const uint4*>(kv.template krow<DH>(cb + jl, H, tk.g * hg))[w];
+      b = reinterpret_cast<const uint4*>(kv.template vrow<DH>(cb + jl, H, tk.g * hg))[w];
+    }, [&](int t, const uint4& a, const uint4& b) {
+      const int jl = t / slice, w = t - jl * slice;
+      ks[jl * stride + w] = a;
+      vs[jl * stride + w] = b;
+    });
+    __syncthreads();
+    if (!work) continue;
+    const int cend = cb + nc;
+    // this round's and the next round's columns are in registers; the
+    // round after that is requested while this one runs
+    int cur[U], nxt[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      cur[u] = pos + u < pend ? col[pos + u] : INT32_MAX;
+      nxt[u] = pos + U + u < pend ? col[pos + U + u] : INT32_MAX;
+    }
+    for (;;) {
+      int nn[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) nn[u] = pos + 2 * U + u < pend ? col[pos + 2 * U + u] : INT32_MAX;
+      RowWords<T, DH> kw[U], vw[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (cur[u] < cend) {
+          const int o = (cur[u] - cb) * stride + tk.hl * NV;
+          lds_words<T, DH>(ks + o, kw[u]);
+          lds_words<T, DH>(vs + o, vw[u]);
+        }
+      int took = 0;
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (cur[u] < cend) {
+          edge(kw[u], vw[u]);
+          ++took;
+        }
+      pos += took;
+      if (took < U) break;  // the row's next edge is in a later column block
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        cur[u] = nxt[u];
+        nxt[u] = nn[u];
+      }
+    }
+  }
+  if (!work) return;
+  // columns >= n_sweep: gathered from global memory (the last part)
+  for (int e0 = pend; e0 < tail_end; e0 += U) {
+    RowWords<T, DH> kw[U], vw[U];
+    bool ok[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      ok[u] = e0 + u < tail_end;
+      if (ok[u]) kv.template load_kv<DH>(col[e0 + u], H, h, kw[u], vw[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (ok[u]) edge(kw[u], vw[u]);
+  }
+  const int64_t pr = (int64_t(tk.part) * n_q + tk.ridx) * H + h;
+  store_f32<DH>(part_acc + pr * DH, acc);
+  if constexpr (MODE == 0) part_z[pr] = z;
+}
+
+// Forward finalize: one thread per (order position, head); the parts in order.
+template <typename T, int DH>
+__global__ __launch_bounds__(kBlock) void k_fwd_tiled_finalize(
+    const float* __restrict__ part_acc, const float* __restrict__ part_z,
+    const int32_t* __restrict__ rowptr, const int32_t* __restrict__ order, int32_t n_q,
+    int32_t n_sweep, int32_t H, int32_t rows_per_block, int32_t p_max, int32_t e_slot, int32_t kb,
+    float eps, T* __restrict__ out, float* __restrict__ rinv, float* __restrict__ zbuf,
+    float* __restrict__ ns, int32_t ns_len) {
+  const int64_t t = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+  const int64_t nrh = int64_t(n_q) * H;
+  if (t >= nrh) return;
+  const int64_t ridx = t / H;
+  const int h = int(t - ridx * H);
+  const int P = tile_row_parts(rowptr, order, ridx / rows_per_block * rows_per_block, e_slot,
+                               p_max, n_sweep, kb);
+  float acc[DH], z = 0.f;
+#pragma unroll
+  for (int c = 0; c < DH; ++c) acc[c] = 0.f;
+  for (int p = 0; p < P; ++p) {
+    float a[DH];
+    load_f32<DH>(part_acc + (p * nrh + t) * DH, a);
+#pragma unroll
+    for (int c = 0; c < DH; ++c) acc[c] += a[c];
+    z += part_z[p * nrh + t];
+  }
+  const int64_t row = order[ridx];
+  const int64_t o = row * H + h;
+  const float den = z + eps;
+  float ov[DH];
+#pragma unroll
+  for (int c = 0; c < DH; ++c) ov[c] = acc[c] / den;
+  store_row<T, DH>(out + o * DH, ov);
+  rinv[o] = 1.0f / den;
+  zbuf[o] = z;
+  if (ns && h == 0 && row < ns_len) {
+    float zs = 0.f;
+    for (int hh = 0; hh < H; ++hh) {
+      float zh = 0.f;
+      for (int p = 0; p < P; ++p) zh += part_z[p * nrh + t + hh];
+      zs += zh;
+    }
+    ns[row] = zs / float(H);
+  }
+}
+
+// Key-major tiled pass: dK, dV partials of the keys j < n_sweep.
+template <typename T, int DH>
+__global__ __launch_bounds__(kBlock) void k_kv_tiled(
+    const T* __restrict__ q, const Keys<T> kv, const T* __restrict__ g,
+    const float2* __restrict__ rd, const int32_t* __restrict__ t_rowptr,
+    const int32_t* __restrict__ t_col, const int32_t* __restrict__ order, int32_t n_rows,
+    int32_t n_q, int32_t H, int32_t hg, int32_t L, int32_t n_groups, int32_t p_max,
+    int32_t e_slot, int32_t kb, float inv_scale, float lo, float hi,
+    float* __restrict__ part_kv) {
+  extern __shared__ uint4 stage[];
+  constexpr int NV = RowWords<T, DH>::NV;
+  constexpr int U = unroll_for(2 * NV, NGT_BWD_KV_WORDS);
+  const TileTask tk = tile_task(t_rowptr, order, n_rows, n_q, n_groups, p_max, e_slot, hg, L, kb);
+  if (!tk.live) return;
+  const bool work = tk.ridx < n_rows && tk.act;
+  const int64_t row = work ? order[tk.ridx] : 0;
+  const int h = tk.h;
+  int pos = 0, pend = 0;
+  if (work) {
+    const int beg = t_rowptr[row], end = t_rowptr[row + 1];
+    pos = lower_bound_col(t_col, beg, end, tk.c0);
+    pend = lower_bound_col(t_col, pos, end, tk.c1);
+  }
+  RowWords<T, DH> krw, vrw;
+  if (work) {
+    load_words<T, DH>(kv.template krow<DH>(row, H, h), krw);
+    load_words<T, DH>(kv.template vrow<DH>(row, H, h), vrw);
+  } else {
+    zero_words<T, DH>(krw);
+    zero_words<T, DH>(vrw);
+  }
+  float dk[DH], dv[DH];
+#pragma unroll
+  for (int c = 0; c < DH; ++c) {
+    dk[c] = 0.f;
+    dv[c] = 0.f;
+  }
+  const int slice = hg * NV;
+  const int stride = tile_stride<T, DH>(hg);
+  uint4* qs = stage;
+  uint4* gs = stage + int64_t(kb) * stride;
+  float2* rs = reinterpret_cast<float2*>(stage + 2 * int64_t(kb) * stride);
+  for (int cb = tk.c0; cb < tk.c1; cb += kb) {
+    const int nc = min(kb, tk.c1 - cb);
+    __syncthreads();
+    stage_words<kStageBatch>(nc * slice, [&](int t, uint4& a, uint4& b) {
+      const int il = t / slice, w = t - il * slice;
+      const int64_t base = (int64_t(cb + il) * H + tk.g * hg) * DH;
+      a = reinterpret_cast<const uint4*>(q + base)[w];
+      b = reinterpret_cast<const uint4*>(g + base)[w];
+    }, [&](int t, const uint4& a, const uint4& b) {
+      const int il = t / slice, w = t - il * slice;
+      qs[il * stride + w] = a;
+      gs[il * stride + w] = b;
+    });
+    for (int t = threadIdx.x; t < nc * hg; t += kBlock) {
+      const int il = t / hg, hh = t - il * hg;
+      rs[t] = rd[int64_t(cb + il) * H + tk.g * hg + hh];
+    }
+    __syncthreads();
+    if (!work) continue;
+    const int cend = cb + nc;
+    int cur[U], nxt[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      cur[u] = pos + u < pend ? t_col[pos + u] : INT32_MAX;
+      nxt[u] = pos + U + u < pend ? t_col[pos + U + u] : INT32_MAX;
+    }
+    for (;;) {
+      int nn[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        nn[u] = pos + 2 * U + u < pend ? t_col[pos + 2 * U + u] : INT32_MAX;
+      RowWords<T, DH> qw[U], gw[U];
+      float2 r[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (cur[u] < cend) {
+          const int il = cur[u] - cb;
+          const int o = il * stride + tk.hl * NV;
+          lds_words<T, DH>(qs + o, qw[u]);
+          lds_words<T, DH>(gs + o, gw[u]);
+          r[u] = rs[il * hg + tk.hl];
+        }
+      int took = 0;
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (cur[u] < cend) {
+          const float a = edge_dot<T, DH>(qw[u], krw) * inv_scale;
+          const float p = __expf(clampf(a, lo, hi));
+          const float dp = r[u].x * edge_dot<T, DH>(gw[u], vrw) - r[u].y;
+          const float da = (a >= lo && a <= hi) ? dp * p : 0.f;
+          const float pr = p * r[u].x;
+#pragma unroll
+          for (int c = 0; c < DH; ++c) {
+            dk[c] = fmaf(da, word_elem<T, DH>(qw[u], c), dk[c]);
+            dv[c] = fmaf(pr, word_elem<T, DH>(gw[u], c), dv[c]);
+          }
+          ++took;
+        }
+      pos += took;
+      if (took < U) break;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        cur[u] = nxt[u];
+        nxt[u] = nn[u];
+      }
+    }
+  }
+  if (!work) return;
+  float* pp = part_kv + ((int64_t(tk.part) * n_rows + tk.ridx) * H + h) * (2 * DH);
+  store_f32<DH>(pp, dk);
+  store_f32<DH>(pp + DH, dv);
+}
+
+// Backward finalize of the tiled passes: threads [0, n_q * H) add the dQ
+// parts (query order positions), threads past them the dK/dV parts of the
+// keys j < n_rows_k (key order positions; keys >= n_main have no gradient);
+// each in part order.
+template <typename T, int DH>
+__global__ __launch_bounds__(kBlock) void k_bwd_tiled_finalize(
+    const float* __restrict__ part_q, const int32_t* __restrict__ rowptr,
+    const int32_t* __restrict__ order_q, int32_t n_q, const float* __restrict__ part_kv,
+    const int32_t* __restrict__ t_rowptr, const int32_t* __restrict__ order_k, int32_t n_rows_k,
+    int64_t n_main, int32_t n_sweep, int32_t H, int32_t rows_per_block, int32_t p_max,
+    int32_t e_slot, int32_t kb_q, int32_t kb_k, float inv_scale, T* __restrict__ grad_q,
+    T* __restrict__ grad_k, T* __restrict__ grad_v) {
+  const int64_t t = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+  const int64_t nq = int64_t(n_q) * H;
+  if (t < nq) {
+    const int64_t ridx = t / H;
+    const int h = int(t - ridx * H);
+    const int P = tile_row_parts(rowptr, order_q, ridx / rows_per_block * rows_per_block, e_slot,
+                                 p_max, n_sweep, kb_q);
+    float a[DH];
+#pragma unroll
+    for (int c = 0; c < DH; ++c) a[c] = 0.f;
+    for (int p = 0; p < P; ++p) {
+      float b[DH];
+      load_f32<DH>(part_q + (p * nq + t) * DH, b);
+#pragma unroll
+      for (int c = 0; c < DH; ++c) a[c] += b[c];
+    }
+#pragma unroll
+    for (int c = 0; c < DH; ++c) a[c] *= inv_scale;
+    store_row<T, DH>(grad_q + (int64_t(order_q[ridx]) * H + h) * DH, a);
+    return;
+  }
+  const int64_t u = t - nq;
+  const int64_t nk = int64_t(n_rows_k) * H;
+  if (u >= nk) return;
+  const int64_t ridx = u / H;
+  const int h = int(u - ridx * H);
+  const int64_t key = order_k[ridx];
+  if (key >= n_main) return;  // constant key row: no gradient
+  const int P = tile_row_parts(t_rowptr, order_k, ridx / rows_per_block * rows_per_block, e_slot,
+                               p_max, n_q, kb_k);
+  float dk[DH], dv[DH];
+#pragma unroll
+  for (int c = 0; c < DH; ++c) {
+    dk[c] = 0.f;
+    dv[c] = 0.f;
+  }
+  for (int p = 0; p < P; ++p) {
+    float b[DH], e[DH];
+    load_f32<DH>(part_kv + (p * nk + u) * (2 * DH), b);
+    load_f32<DH>(part_kv + (p * nk + u) * (2 * DH) + DH, e);
+#pragma unroll
+    for (int c = 0; c < DH; ++c) {
+      dk[c] += b[c];
+      dv[c] += e[c];
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < DH; ++c) dk[c] *= inv_scale;
+  const int64_t o = (key * H + h) * DH;
+  store_row<T, DH>(grad_k + o, dk);
+  store_row<T, DH>(grad_v + o, dv);
+}
+
 // ------------------------------------------------------------------ host side
 inline int lanes_for(int n) {
   int L = 1;
@@ -951,20 +1431,106 @@ int xcd_mapping(int groups) {
   return 1;
 }
 
+// Tiled kernels (dense windows): run only when asked for (NGT_TILED=1), where
+// the row orders are built, the head count splits into groups of 4 (or fits
+// one group of at most 8) and the staged slices fit kTileLds bytes for at
+// least 16 columns.  Measured on the high-degree GT window (7,280 queries,
+// 3.67 M edges, H = 8, d = 16, bf16), µs per launch, work lists -> tiled at
+// 64 / 128 / 256 edges per slot and part: forward 75 -> 674 / 884 / 1,200,
+// key-major 100 -> 1,085 / 1,400 / 1,973, dQ 80 -> 814 / 1,058 / 1,484.  The
+// counters show why: an LDS block of 64 KiB leaves 2 blocks (8 waves) per CU
+// where the work-list kernels keep about 3 times as many waves in flight, and
+// each block's column blocks run as a chain of stage -> barrier -> walk ->
+// barrier episodes whose load latency nothing overlaps, with 8.2 M LDS bank
+// conflict cycles and 1.6 x the VALU instructions of the work-list forward.
+// They stay as a tested option; overlapping the staging of the next column
+// block with the walk of the current one is what they would need.
+// NGT_TILE_HEADS, NGT_TILE_EDGES, NGT_TILE_PARTS and NGT_TILE_LDS override
+// the heads per group, the edges per slot and part, the most parts per row
+// block and the LDS bytes per block.
+constexpr size_t kTileLds = 65536;
+
+struct TilePlan {
+  bool on;
+  int hg, groups, L, rows_per_block;
+  int n_sweep;  // swept columns of the query-major passes: min(n_q, n_k)
+  int p_max;    // most column parts of one row block
+  int e_slot;   // edges per slot and part that a row block's parts aim at
+};
+
+int tiled_heads(int H) {
+  if (const char* env = getenv("NGT_TILE_HEADS")) {
+    const int v = atoi(env);
+    if (v >= 1 && H % v == 0 && v <= 8) return v;
+  }
+  if (H % 4 == 0) return 4;
+  return H <= 8 ? H : 0;
+}
+
+inline int env_int(const char* name, int dflt, int lo, int hi) {
+  if (const char* env = getenv(name)) {
+    const int v = atoi(env);
+    if (v >= lo && v <= hi) return v;
+  }
+  return dflt;
+}
+
+TilePlan tile_plan(const ngt_window_csr* c, int H, int d) {
+  TilePlan t{};
+  t.on = false;
+  t.n_sweep = c->n_q < c->n_k ? c->n_q : c->n_k;
+  if (!c->order_q || !c->order_k || t.n_sweep < 1) return t;
+  t.hg = tiled_heads(H);
+  if (t.hg < 1) return t;
+  // the largest staged slice per column (key-major: Q, dO and {r, rD}, fp32, padded)
+  if ((size_t(t.hg) * (2 * size_t(d) * 4 + 8) + 32) * 16 > kTileLds) return t;
+  const char* env = getenv("NGT_TILED");
+  if (!env || atoi(env) == 0) return t;
+  t.groups = H / t.hg;
+  t.L = lanes_for(t.hg);
+  t.rows_per_block = kWavesPerBlock * (kWave / t.L);
+  t.p_max = env_int("NGT_TILE_PARTS", 16, 1, 64);
+  t.e_slot = env_int("NGT_TILE_EDGES", 256, 1, 1 << 20);
+  t.on = true;
+  return t;
+}
+
+// Columns per staged block for a slice of bytes_per_col bytes per column, in
+// kTileLds bytes of LDS (NGT_TILE_LDS overrides, 8-64 KiB).
+inline int tile_cols(size_t bytes_per_col) {
+  const size_t lds = size_t(env_int("NGT_TILE_LDS", int(kTileLds), 8192, int(kTileLds)));
+  int kb = int(lds / bytes_per_col);
+  if (kb > 512) kb = 512;
+  return kb & ~15;
+}
+
+template <typename T, int DH>
+size_t tile_q_col_bytes(int hg) {
+  return 2 * size_t(tile_stride<T, DH>(hg)) * 16;
+}
+template <typename T, int DH>
+size_t tile_kv_col_bytes(int hg) {
+  return 2 * size_t(tile_stride<T, DH>(hg)) * 16 + size_t(hg) * 8;
+}
+
 struct FwdLayout {
   size_t part_acc, part_z, zbuf, total;
 };
 struct BwdLayout {
-  size_t rd, ds, part_kv, part_q, total;
+  size_t rd, ds, part_kv, part_q, part_tk, total;
 };
 
 FwdLayout fwd_layout(const ngt_window_csr* c, int H, int d) {
   FwdLayout L{};
+  const TilePlan tp = tile_plan(c, H, d);
+  const size_t parts = tp.on ? size_t(tp.p_max) * c->n_q : size_t(c->n_parts_q);
+  const size_t split = size_t(c->n_parts_q);
+  const size_t n = parts > split ? parts : split;  // (partial rows) x H, either kernel family
   size_t off = 0;
   L.part_acc = off;
-  off += align256(size_t(c->n_parts_q) * H * d * 4);
+  off += align256(n * H * d * 4);
   L.part_z = off;
-  off += align256(size_t(c->n_parts_q) * H * 4);
+  off += align256(n * H * 4);
   L.zbuf = off;
   off += align256(size_t(c->n_q) * H * 4);
   L.total = off;
@@ -973,6 +1539,13 @@ FwdLayout fwd_layout(const ngt_window_csr* c, int H, int d) {
 
 BwdLayout bwd_layout(const ngt_window_csr* c, int H, int d) {
   BwdLayout L{};
+  const TilePlan tp = tile_plan(c, H, d);
+  size_t nq = size_t(c->n_parts_q), ntk = 0;
+  if (tp.on) {
+    const size_t tq = size_t(tp.p_max) * c->n_q;  // the tiled dQ parts share part_q
+    nq = tq > nq ? tq : nq;
+    ntk = size_t(tp.p_max) * tp.n_sweep;
+  }
   size_t off = 0;
   L.rd = off;
   off += align256(size_t(c->n_q) * H * 8);
@@ -981,7 +1554,9 @@ BwdLayout bwd_layout(const ngt_window_csr* c, int H, int d) {
   L.part_kv = off;
   off += align256(size_t(c->n_parts_k) * H * 2 * d * 4);
   L.part_q = off;
-  off += align256(size_t(c->n_parts_q) * H * d * 4);
+  off += align256(nq * H * d * 4);
+  L.part_tk = off;
+  off += align256(ntk * H * 2 * d * 4);
   L.total = off;
   return L;
 }
@@ -1033,11 +1608,59 @@ Keys<T, EXT> make_keys(const void* k, const void* v, const void* k_ext, const vo
                       v_ext ? static_cast<const T*>(v_ext) : vv, n_main};
 }
 
+// Tiled forward: k_q_tiled<MODE 0> over (row block, part, head group), then
+// the finalize over (query, head).
+template <typename T, int DH>
+int launch_fwd_tiled(const ngt_window_csr* c, const TilePlan& tp, const void* q, const void* k,
+                     const void* v, const void* k_ext, const void* v_ext, int64_t n_main, int H,
+                     float inv_scale, float lo, float hi, float eps, void* out, float* rinv,
+                     float* ns, int ns_len, char* ws, hipStream_t st) {
+  const FwdLayout lay = fwd_layout(c, H, DH);
+  float* part_acc = reinterpret_cast<float*>(ws + lay.part_acc);
+  float* part_z = reinterpret_cast<float*>(ws + lay.part_z);
+  float* zbuf = reinterpret_cast<float*>(ws + lay.zbuf);
+  const size_t per_col = tile_q_col_bytes<T, DH>(tp.hg);
+  const int kb = tile_cols(per_col);
+  const int64_t rblocks = (int64_t(c->n_q) + tp.rows_per_block - 1) / tp.rows_per_block;
+  const int64_t blocks = rblocks * tp.groups * tp.p_max;
+  if (blocks > 0) {
+    KernelTimer timer_("sparse_fwd", st);
+    const RecomputeArgs none{nullptr, nullptr, nullptr, lo, hi};
+    auto launch = [&](auto ext) {
+      constexpr bool E = decltype(ext)::value;
+      hipLaunchKernelGGL((k_q_tiled<T, DH, E, 0>), dim3(unsigned(blocks)), dim3(kBlock),
+                         size_t(kb) * per_col, st, static_cast<const T*>(q),
+                         make_keys<T, DH, E>(k, v, k_ext, v_ext, n_main, H), c->rowptr, c->col,
+                         c->order_q, c->n_q, tp.n_sweep, H, tp.hg, tp.L, tp.groups, tp.p_max,
+                         tp.e_slot, kb, inv_scale, lo, hi, none, part_acc, part_z);
+    };
+    if (n_main < c->n_k) launch(std::true_type{});
+    else launch(std::false_type{});
+    NGT_HIP_CHECK(hipGetLastError());
+  }
+  const int64_t nrh = int64_t(c->n_q) * H;
+  if (nrh > 0) {
+    KernelTimer timer_("sparse_fwd_finalize", st);
+    hipLaunchKernelGGL((k_fwd_tiled_finalize<T, DH>), dim3(unsigned((nrh + kBlock - 1) / kBlock)),
+                       dim3(kBlock), 0, st, part_acc, part_z, c->rowptr, c->order_q, c->n_q,
+                       tp.n_sweep, H, tp.rows_per_block, tp.p_max, tp.e_slot, kb, eps,
+                       static_cast<T*>(out), rinv, zbuf, ns_len > 0 ? ns : nullptr, ns_len);
+    NGT_HIP_CHECK(hipGetLastError());
+  }
+  return NGT_OK;
+}
+
 template <typename T, int DH>
 int launch_fwd(const ngt_window_csr* c, const void* q, const void* k, const void* v,
                const void* k_ext, const void* v_ext, int64_t n_main, int H, float inv_scale,
                float lo, float hi, float eps, void* out, float* rinv, float* ns, int ns_len,
                char* ws, hipStream_t st, const float* eb) {
+  if (!eb) {
+    const TilePlan tp = tile_plan(c, H, DH);
+    if (tp.on)
+      return launch_fwd_tiled<T, DH>(c, tp, q, k, v, k_ext, v_ext, n_main, H, inv_scale, lo, hi,
+                                     eps, out, rinv, ns, ns_len, ws, st);
+  }
   const int hg = heads_per_pass(H, 0);
   const int groups = (H + hg - 1) / hg;
   const int L = lanes_for(hg);
@@ -1090,6 +1713,101 @@ int launch_fwd(const ngt_window_csr* c, const void* q, const void* k, const void
   return NGT_OK;
 }
 
+// Tiled backward (after k_rowstat, with each edge's da recomputed in the dQ
+// pass): k_kv_tiled over the key rows j < n_sweep, the work-list key-major
+// pass over the key rows j >= n_sweep that have a gradient (with the finalize
+// of its split rows), k_q_tiled<MODE 1> over the queries, then one finalize
+// for the tiled parts.
+template <typename T, int DH>
+int launch_bwd_tiled(const ngt_window_csr* c, const TilePlan& tp, const void* q, const void* k,
+                     const void* v, const void* k_ext, const void* v_ext, int64_t n_main,
+                     const void* g, const float2* rd, int H, float inv_scale, float lo, float hi,
+                     void* gq, void* gk, void* gv, const BwdLayout& lay, char* ws,
+                     hipStream_t st) {
+  float* part_q = reinterpret_cast<float*>(ws + lay.part_q);
+  float* part_kv = reinterpret_cast<float*>(ws + lay.part_kv);
+  float* part_tk = reinterpret_cast<float*>(ws + lay.part_tk);
+  const int rows_k = tp.n_sweep;
+  const size_t kv_col = tile_kv_col_bytes<T, DH>(tp.hg);
+  const int kb_k = tile_cols(kv_col);
+  const int64_t blocks_k =
+      (int64_t(rows_k) + tp.rows_per_block - 1) / tp.rows_per_block * tp.groups * tp.p_max;
+  if (blocks_k > 0) {
+    KernelTimer timer_("sparse_bwd_kv", st);
+    hipLaunchKernelGGL((k_kv_tiled<T, DH>), dim3(unsigned(blocks_k)), dim3(kBlock),
+                       size_t(kb_k) * kv_col, st, static_cast<const T*>(q),
+                       make_keys<T, DH>(k, v, k_ext, v_ext, n_main, H), static_cast<const T*>(g),
+                       rd, c->t_rowptr, c->t_col, c->order_k, rows_k, c->n_q, H, tp.hg, tp.L,
+                       tp.groups, tp.p_max, tp.e_slot, kb_k, inv_scale, lo, hi, part_tk);
+    NGT_HIP_CHECK(hipGetLastError());
+  }
+  const bool rest = n_main > rows_k;  // key rows past the sweep with a gradient
+  if (rest) {
+    const int hg = heads_per_pass(H, 1);
+    const int groups = (H + hg - 1) / hg;
+    const int L = lanes_for(hg);
+    const int xcd = xcd_mapping(groups);
+    const int pw_k = packed_waves(c->n_packed_k, L);
+    const unsigned blocks = edge_blocks(c->n_items_k, pw_k, groups, xcd);
+    if (blocks > 0) {
+      KernelTimer timer_("sparse_bwd_kv_rest", st);
+      hipLaunchKernelGGL((k_bwd_kv<T, DH, false, false>), dim3(blocks), dim3(kBlock), 0, st,
+                         static_cast<const T*>(q), make_keys<T, DH>(k, v, k_ext, v_ext, n_main, H),
+                         static_cast<const T*>(g), rd, c->t_col,
+                         reinterpret_cast<const int4*>(c->items_k), c->n_items_k, groups, hg, H,
+                         L, inv_scale, lo, hi, static_cast<T*>(gk), static_cast<T*>(gv), nullptr,
+                         part_kv, c->t_rowptr, c->packed_k, c->n_packed_k, pw_k, xcd, nullptr,
+                         nullptr, rows_k);
+      NGT_HIP_CHECK(hipGetLastError());
+    }
+  }
+  const size_t q_col = tile_q_col_bytes<T, DH>(tp.hg);
+  const int kb_q = tile_cols(q_col);
+  const int64_t blocks_q =
+      (int64_t(c->n_q) + tp.rows_per_block - 1) / tp.rows_per_block * tp.groups * tp.p_max;
+  const int kv_tiles = (2 * H * DH + kColTile - 1) / kColTile;
+  const int64_t fin_rest = rest ? int64_t(c->n_splits_k) * kv_tiles : 0;
+  if (blocks_q > 0) {
+    KernelTimer timer_("sparse_bwd_q", st);
+    const RecomputeArgs rca{q, g, rd, lo, hi};
+    auto launch = [&](auto ext) {
+      constexpr bool E = decltype(ext)::value;
+      hipLaunchKernelGGL((k_q_tiled<T, DH, E, 1>), dim3(unsigned(blocks_q)), dim3(kBlock),
+                         size_t(kb_q) * q_col, st, static_cast<const T*>(q),
+                         make_keys<T, DH, E>(k, v, k_ext, v_ext, n_main, H), c->rowptr, c->col,
+                         c->order_q, c->n_q, tp.n_sweep, H, tp.hg, tp.L, tp.groups, tp.p_max,
+                         tp.e_slot, kb_q, inv_scale, lo, hi, rca, part_q, nullptr);
+    };
+    if (n_main < c->n_k) launch(std::true_type{});
+    else launch(std::false_type{});
+    NGT_HIP_CHECK(hipGetLastError());
+  }
+  if (fin_rest > 0) {
+    // split key rows past the sweep: k_bwd_q's finalize blocks alone (no dQ blocks)
+    KernelTimer timer_("sparse_bwd_kv_rest_finalize", st);
+    const RecomputeArgs none{nullptr, nullptr, nullptr, lo, hi};
+    hipLaunchKernelGGL((k_bwd_q<T, DH, false, false>), dim3(unsigned(fin_rest)), dim3(kBlock), 0,
+                       st, make_keys<T, DH, false>(k, v, k_ext, v_ext, n_main, H), c->col, c->q2t,
+                       nullptr, reinterpret_cast<const int4*>(c->items_q), 0, 1, H, H, 1, inv_scale,
+                       static_cast<T*>(gq), nullptr, c->rowptr, c->packed_q, 0, 0, 0,
+                       reinterpret_cast<const int4*>(c->splits_k), kv_tiles, part_kv,
+                       static_cast<T*>(gk), static_cast<T*>(gv), 0, none, rows_k);
+    NGT_HIP_CHECK(hipGetLastError());
+  }
+  const int64_t threads = int64_t(c->n_q) * H + int64_t(rows_k) * H;
+  if (threads > 0) {
+    KernelTimer timer_("sparse_bwd_q_finalize", st);
+    hipLaunchKernelGGL((k_bwd_tiled_finalize<T, DH>),
+                       dim3(unsigned((threads + kBlock - 1) / kBlock)), dim3(kBlock), 0, st,
+                       part_q, c->rowptr, c->order_q, c->n_q, part_tk, c->t_rowptr, c->order_k,
+                       rows_k, n_main, tp.n_sweep, H, tp.rows_per_block, tp.p_max, tp.e_slot,
+                       kb_q, kb_k, inv_scale, static_cast<T*>(gq), static_cast<T*>(gk),
+                       static_cast<T*>(gv));
+    NGT_HIP_CHECK(hipGetLastError());
+  }
+  return NGT_OK;
+}
+
 template <typename T, int DH>
 int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void* v,
                const void* k_ext, const void* v_ext, int64_t n_main, const void* out,
@@ -1111,6 +1829,12 @@ int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void
                        static_cast<const T*>(out), static_cast<const T*>(g), rinv, nrh, rd);
     NGT_HIP_CHECK(hipGetLastError());
   }
+  if (rc) {  // the tiled passes recompute each edge's da in the dQ pass
+    const TilePlan tp = tile_plan(c, H, DH);
+    if (tp.on)
+      return launch_bwd_tiled<T, DH>(c, tp, q, k, v, k_ext, v_ext, n_main, g, rd, H, inv_scale,
+                                     lo, hi, gq, gk, gv, lay, ws, st);
+  }
   int hg = heads_per_pass(H, 1);
   int groups = (H + hg - 1) / hg;
   int L = lanes_for(hg);
@@ -1128,7 +1852,7 @@ int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void
                          reinterpret_cast<const int4*>(c->items_k), c->n_items_k, groups, hg, H,
                          L, inv_scale, lo, hi, static_cast<T*>(gk), static_cast<T*>(gv),
                          rc ? nullptr : ds, part_kv, c->t_rowptr, c->packed_k, c->n_packed_k,
-                         pw_k, xcd, eb, deb);
+                         pw_k, xcd, eb, deb, 0);
     };
     const bool nt = !rc && ds_nontemporal(c, H);
     if (eb) {
@@ -1160,7 +1884,7 @@ int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void
                          L, inv_scale, static_cast<T*>(gq), part_q, c->rowptr, c->packed_q,
                          c->n_packed_q, pw_q, int32_t(q_blocks),
                          reinterpret_cast<const int4*>(c->splits_k), kv_tiles, part_kv,
-                         static_cast<T*>(gk), static_cast<T*>(gv), xcd, rca);
+                         static_cast<T*>(gk), static_cast<T*>(gv), xcd, rca, 0);
     };
     const bool ext = n_main < c->n_k;
     if (rc) {

@@ -104,6 +104,17 @@ def merge_related_nodes(xadj, adjncy, eweights, partition, topk_percent: int):
     return np.array(out, dtype=np.int64), len(external)
 
 
+def row_orders(rowptr, t_rowptr, n_q, n_k):
+    """The rows longest first, ties by descending row id (a stable ascending
+    sort by degree, reversed): every query row, and the key rows j <
+    min(n_q, n_k).  The schedule order of the library's tiled kernels; it
+    changes no result, only which rows share a block."""
+    dq = np.diff(np.asarray(rowptr, np.int64))
+    dk = np.diff(np.asarray(t_rowptr, np.int64))[: min(n_q, n_k)]
+    return (np.argsort(dq, kind="stable")[::-1].astype(np.int32),
+            np.argsort(dk, kind="stable")[::-1].astype(np.int32))
+
+
 def duplicate_rerange(local_partitions):
     """_compute_local_duplicate_nodes (window_state.py:52-73): nodes present in
     >= 2 of the rank's windows go first in each window (original order kept)."""

@@ -35,10 +35,11 @@ def test_every_declared_symbol_is_exported_and_bound():
 
 def test_struct_layout_matches_header():
     # int32 n_q, n_k; int64 n_edges; int32 chunk_q, chunk_k, small_q, small_k;
-    # 14 pointers; 12 int32
-    assert C.sizeof(_lib.WindowCSR) == 8 + 8 + 16 + 14 * 8 + 12 * 4
+    # 14 pointers; 12 int32; 2 pointers (the row orders)
+    assert C.sizeof(_lib.WindowCSR) == 8 + 8 + 16 + 14 * 8 + 12 * 4 + 2 * 8
     assert _lib.WindowCSR.rowptr.offset == 32
     assert _lib.WindowCSR.max_items_q.offset == 32 + 14 * 8
+    assert _lib.WindowCSR.order_q.offset == 32 + 14 * 8 + 12 * 4
 
 
 def test_csr_sizes_arithmetic():

@@ -18,13 +18,14 @@ def _say(*a):
 
 
 def _run_kernel(q, k, v, ei, go, chunk=None, small=0):
-    """fwd + bwd through the HIP path; returns dict of CPU tensors."""
+    """fwd + bwd through the HIP path; returns dict of CPU tensors.  With an
+    explicit chunk the work-list kernels run (no row orders: no tiled path)."""
     qd, kd, vd = (t.cuda().requires_grad_(True) for t in (q, k, v))
     eid = torch.from_numpy(ei).cuda()
     if chunk is None:
         x, ns = sparse_attention(qd, kd, vd, eid)
     else:
-        adj = WindowAdjacency(eid, q.shape[0], k.shape[0], chunk, small)
+        adj = WindowAdjacency(eid, q.shape[0], k.shape[0], chunk, small, tiled=False)
         x, ns = SparseAttentionFunction.apply(qd, kd, vd, adj, float(q.shape[-1]) ** 0.5, -5.0,
                                               5.0, 1e-6)
     x.backward(go.cuda())
@@ -178,6 +179,9 @@ def test_csr_bit_exact(n_q, n_k, E, chunk, small):
     got = {n: getattr(adj, n).cpu().numpy() for n in ref}
     for n in ref:
         np.testing.assert_array_equal(got[n][: ref[n].shape[0]], ref[n], err_msg=n)
+    oq, ok = OG.row_orders(ref["rowptr"], ref["t_rowptr"], n_q, n_k)
+    np.testing.assert_array_equal(adj.order_q.cpu().numpy()[: oq.shape[0]], oq, err_msg="order_q")
+    np.testing.assert_array_equal(adj.order_k.cpu().numpy()[: ok.shape[0]], ok, err_msg="order_k")
     for side, rp in (("q", ref["rowptr"]), ("k", ref["t_rowptr"])):
         items, splits, packed = OG.work_items(rp, chunk, small)
         gi = getattr(adj, "items_" + side).cpu().numpy()[: items.shape[0]]
@@ -349,7 +353,7 @@ def test_sparse_external_key_rows(monkeypatch, H, d, dtype, chunk, small, hg):
     kx, vx = k[n_main:].cuda(), v[n_main:].cuda()
     eid = torch.from_numpy(ei).cuda()
     if chunk:
-        adj = WindowAdjacency(eid, n_q, n_k, chunk, small)
+        adj = WindowAdjacency(eid, n_q, n_k, chunk, small, tiled=False)
         x, ns = SparseAttentionFunction.apply(qd, kd, vd, adj, float(d) ** 0.5, -5.0, 5.0, 1e-6,
                                               kx, vx)
     else:
@@ -396,7 +400,8 @@ def test_query_packing_from_degrees(related):
     deg = np.bincount(ei[1], minlength=n_q)
     want = next((t for t in (8, 16, 24, 32) if (deg <= t).sum() >= 0.78 * n_q), 32)
     small_k = 16
-    adj = WindowAdjacency(torch.from_numpy(ei).cuda(), n_q, n_k, 128, small_k, pack_q=True)
+    adj = WindowAdjacency(torch.from_numpy(ei).cuda(), n_q, n_k, 128, small_k, pack_q=True,
+                          tiled=False)
     assert adj.small_q == want and adj.small == small_k
     ref = OG.csr_from_coo(ei[0], ei[1], n_q, n_k)
     for side, rp, small in (("q", ref["rowptr"], want), ("k", ref["t_rowptr"], small_k)):

@@ -45,7 +45,7 @@ def _run(q, k, v, ei, go, chunk, small, n_main=None):
     vd = v[:n_main].cuda().requires_grad_(True)
     kx = k[n_main:].cuda() if n_main < n_k else None
     vx = v[n_main:].cuda() if n_main < n_k else None
-    adj = WindowAdjacency(torch.from_numpy(ei).cuda(), n_q, n_k, chunk, small)
+    adj = WindowAdjacency(torch.from_numpy(ei).cuda(), n_q, n_k, chunk, small, tiled=False)
     x, ns = SparseAttentionFunction.apply(qd, kd, vd, adj, float(q.shape[-1]) ** 0.5, -5.0, 5.0,
                                           1e-6, kx, vx)
     x.backward(go.cuda())

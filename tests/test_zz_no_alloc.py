@@ -57,7 +57,7 @@ def test_noalloc_forward_matches_workspace_forward(H, d, dtype):
     for n, hub, chunk, seed in ((900, 2500, 64, 1), (300, 700, 32, 2)):
         print(f"case noalloc n={n} hub={hub} H={H} d={d} {dtype}", flush=True)
         ei, q, k, v = _window(n, hub, H, d, dtype, seed)
-        adj = WindowAdjacency(torch.from_numpy(ei).cuda(), n, n, chunk, 2)
+        adj = WindowAdjacency(torch.from_numpy(ei).cuda(), n, n, chunk, 2, tiled=False)
         assert adj.struct.n_splits_q > 0  # split rows: the partials live in the scratch
         qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
         ref = _fwd(lib, adj, qd, kd, vd, noalloc=False)
