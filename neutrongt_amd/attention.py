@@ -660,10 +660,15 @@ class CoreAttention(nn.Module):
         if attn_type == "sparse":
             x, score = self.sparse_attention_bias(q, k, v, edge_index, attn_bias, kv_ext=kv_ext)
         elif attn_type == "flash":
-            # The reference casts q/k/v to fp16 here and the result back to
-            # fp32; this runs the same math in the inputs' dtype (fp32 or bf16).
-            x, score = self.naive_attention(q, k, v, dropout_p=self.attention_dropout_rate)
-            x = x.float()
+            # The reference casts q/k/v to fp16 and the result back to fp32
+            # (graphormer_dist_node_level.py:111-122).  Here the inputs are
+            # rounded to fp16 as well (held in fp32, where fp16 values are
+            # exact), the attention runs on the fp32 kernels, and the output is
+            # rounded to fp16 before it is returned as fp32.  The gradients
+            # pass through the same two casts, so they too are fp16-rounded.
+            q16, k16, v16 = (t.half().float() for t in (q, k, v))
+            x, score = self.naive_attention(q16, k16, v16, dropout_p=self.attention_dropout_rate)
+            x = x.half().float()
             if self.flash_layout == "gt_twin":  # [b, H, N, d] memory, viewed as [b, N, H*d] below
                 x = x.transpose(1, 2).contiguous()
         else:

@@ -464,13 +464,49 @@ __device__ __forceinline__ void store_da(float* __restrict__ ds, int64_t i, floa
     ds[i] = da;
 }
 
-template <typename T, int DH, bool BIAS, bool NT>
+// The per-row statistics {r, r D} of a query, D = dO . out per head: read
+// from rd (k_rowstat's output), or with FOLD formed at the edge from the
+// query's out row and rinv with k_rowstat's own arithmetic (the same bits),
+// which saves the k_rowstat launch where a window's key-major pass is one
+// round of waves and its time a launch's fixed cost.
+struct FoldArgs {
+  const void* out;     // [N_q, H, d] of the element type
+  const float* rinv;   // 1 / (Z + eps) per (query, head)
+};
+
+template <typename T, int DH, bool FOLD>
+struct RowStat {
+  RowWords<T, DH> ow;
+  float2 r;
+  __device__ __forceinline__ void load(const float2* __restrict__ rd, const FoldArgs& fa,
+                                       int64_t i, int H, int h) {
+    if constexpr (FOLD) {
+      load_words<T, DH>(static_cast<const T*>(fa.out) + (i * H + h) * DH, ow);
+      r.x = fa.rinv[i * H + h];
+    } else {
+      r = rd[i * H + h];
+    }
+  }
+  // {r, r D} once the row's dO words gw have arrived
+  __device__ __forceinline__ float2 get(const RowWords<T, DH>& gw) const {
+    if constexpr (FOLD) {
+      float o[DH], gg[DH];
+      words_to_f32<T, DH>(ow, o);
+      words_to_f32<T, DH>(gw, gg);
+      return make_float2(r.x, r.x * dot<DH>(o, gg));
+    } else {
+      return r;
+    }
+  }
+};
+
+template <typename T, int DH, bool BIAS, bool NT, bool FOLD>
 __device__ __forceinline__ void bwd_kv_packed(
     const T* __restrict__ q, const Keys<T>& kv,
     const T* __restrict__ g, const float2* __restrict__ rd, const int32_t* __restrict__ t_rowptr,
     const int32_t* __restrict__ t_col, int64_t row, int h, int H, float inv_scale, float lo,
     float hi, T* __restrict__ grad_k, T* __restrict__ grad_v, float* __restrict__ ds,
-    const float* __restrict__ eb, float* __restrict__ deb) {
+    const float* __restrict__ eb, float* __restrict__ deb, const FoldArgs& fa) {
   RowWords<T, DH> krw, vrw;
   float dk[DH], dv[DH];
   load_words<T, DH>(kv.template krow<DH>(row, H, h), krw);
@@ -487,7 +523,7 @@ __device__ __forceinline__ void bwd_kv_packed(
   for (int u = 0; u < U; ++u) in_[u] = beg + u < end ? t_col[beg + u] : -1;
   for (int e0 = beg; e0 < end; e0 += U) {
     RowWords<T, DH> qw[U], gw[U];
-    float2 r[U];
+    RowStat<T, DH, FOLD> rs[U];
     int ic[U];
     float bu[U];
 #pragma unroll
@@ -497,7 +533,7 @@ __device__ __forceinline__ void bwd_kv_packed(
         const int64_t i = ic[u];
         load_words<T, DH>(q + (i * H + h) * DH, qw[u]);
         load_words<T, DH>(g + (i * H + h) * DH, gw[u]);
-        r[u] = rd[i * H + h];
+        rs[u].load(rd, fa, i, H, h);
         if constexpr (BIAS) bu[u] = eb[int64_t(e0 + u) * H + h];
       }
     }
@@ -506,16 +542,17 @@ __device__ __forceinline__ void bwd_kv_packed(
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (ic[u] >= 0) {
+        const float2 r = rs[u].get(gw[u]);
         const float a = edge_dot<T, DH>(qw[u], krw) * inv_scale;
         float s = clampf(a, lo, hi);
         if constexpr (BIAS) s += bu[u];
         const float p = __expf(s);
-        const float dp = r[u].x * edge_dot<T, DH>(gw[u], vrw) - r[u].y;
+        const float dp = r.x * edge_dot<T, DH>(gw[u], vrw) - r.y;
         const float da = (a >= lo && a <= hi) ? dp * p : 0.f;
         if constexpr (BIAS) {  // the bias's gradient: the score's, without the clamp mask
           if (deb) deb[int64_t(e0 + u) * H + h] = dp * p;
         }
-        const float pr = p * r[u].x;
+        const float pr = p * r.x;
 #pragma unroll
         for (int c = 0; c < DH; ++c) {
           dk[c] = fmaf(da, word_elem<T, DH>(qw[u], c), dk[c]);
@@ -535,7 +572,7 @@ __device__ __forceinline__ void bwd_kv_packed(
 // Key-major pass: grad_k, grad_v of key row j and da_e for every edge of j
 // (stored at the key-major edge position for the query-major pass; ds is null
 // when that pass recomputes da_e itself).
-template <typename T, int DH, bool BIAS, bool NT>
+template <typename T, int DH, bool BIAS, bool NT, bool FOLD>
 __global__ __launch_bounds__(kBlock) void k_bwd_kv(
     const T* __restrict__ q, const Keys<T> kv,
     const T* __restrict__ g, const float2* __restrict__ rd, const int32_t* __restrict__ t_col,
@@ -544,7 +581,7 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
     T* __restrict__ grad_v, float* __restrict__ ds, float* __restrict__ part_kv,
     const int32_t* __restrict__ t_rowptr, const int32_t* __restrict__ packed, int32_t n_packed,
     int32_t n_pwaves, int32_t xcd, const float* __restrict__ eb, float* __restrict__ deb,
-    int32_t row_min) {
+    int32_t row_min, const FoldArgs fa) {
   // key rows < row_min are left to another pass (the tiled one)
   const int64_t gw0 = virtual_wave(n_items, n_pwaves, n_groups, xcd);
   if (gw0 < 0) return;
@@ -553,8 +590,8 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
     int ph;
     if (packed_work(gw0 - int64_t(n_items) * n_groups, n_pwaves, n_groups, hg, L, H, packed,
                     n_packed, prow, ph) && prow >= row_min)
-      bwd_kv_packed<T, DH, BIAS, NT>(q, kv, g, rd, t_rowptr, t_col, prow, ph, H, inv_scale, lo,
-                                     hi, grad_k, grad_v, ds, eb, deb);
+      bwd_kv_packed<T, DH, BIAS, NT, FOLD>(q, kv, g, rd, t_rowptr, t_col, prow, ph, H, inv_scale,
+                                           lo, hi, grad_k, grad_v, ds, eb, deb, fa);
     return;
   }
   int item;
@@ -591,7 +628,7 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
     nx_i = lane < it.z - blk - kWave ? t_col[blk + kWave + lane] : 0;
     for (int t0 = 0; t0 < nb; t0 += S * U) {
       RowWords<T, DH> qw[U], gw[U];
-      float2 r[U];
+      RowStat<T, DH, FOLD> rs[U];
       bool ok[U];
       float bu[U];
 #pragma unroll
@@ -602,7 +639,7 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
         if (ok[u]) {
           load_words<T, DH>(q + (i * H + h) * DH, qw[u]);
           load_words<T, DH>(g + (i * H + h) * DH, gw[u]);
-          r[u] = rd[i * H + h];
+          rs[u].load(rd, fa, i, H, h);
           if constexpr (BIAS) bu[u] = eb[int64_t(blk + t) * H + h];
         }
       }
@@ -610,16 +647,17 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
       for (int u = 0; u < U; ++u) {
         if (ok[u]) {
           // rows stay packed; elements are unpacked at each use
+          const float2 r = rs[u].get(gw[u]);
           const float a = edge_dot<T, DH>(qw[u], krw) * inv_scale;
           float s = clampf(a, lo, hi);
           if constexpr (BIAS) s += bu[u];
           const float p = __expf(s);
-          const float dp = r[u].x * edge_dot<T, DH>(gw[u], vrw) - r[u].y;
+          const float dp = r.x * edge_dot<T, DH>(gw[u], vrw) - r.y;
           const float da = (a >= lo && a <= hi) ? dp * p : 0.f;
           if constexpr (BIAS) {  // the bias's gradient: the score's, without the clamp mask
             if (deb) deb[int64_t(blk + t0 + u * S + ln.slot) * H + h] = dp * p;
           }
-          const float pr = p * r[u].x;
+          const float pr = p * r.x;
 #pragma unroll
           for (int c = 0; c < DH; ++c) {
             dk[c] = fmaf(da, word_elem<T, DH>(qw[u], c), dk[c]);
@@ -1413,6 +1451,19 @@ bool dq_recompute(const ngt_window_csr* c, const float* eb) {
   return c->n_k > 0 && c->n_edges >= kRecomputeEdgesPerKey * c->n_k;
 }
 
+// k_rowstat folded into the key-major pass (RowStat<.., true>) on windows of
+// at most kFoldEdges edges without a bias or a recomputed dQ: there the pass
+// is one round of waves bound by its longest chain, so the extra out-row
+// load per edge rides with the Q and dO loads, and the launch (with its gap)
+// goes.  The dQ pass then reads ds and needs no statistics.
+// NGT_FOLD_ROWSTAT=0/1 overrides the choice.
+constexpr int64_t kFoldEdges = int64_t(1) << 19;
+bool rowstat_fold(const ngt_window_csr* c, const float* eb, bool rc) {
+  if (eb || rc) return false;
+  if (const char* env = getenv("NGT_FOLD_ROWSTAT")) return atoi(env) != 0;
+  return c->n_edges <= kFoldEdges;
+}
+
 // ds written with non-temporal stores when it is too large to stay cached for
 // the query-major pass anyway (E * H * 4 bytes above 64 MB): GPH_Large's
 // 228 MB, bwd_kv 640 -> 630 us per layer, bwd_q 296 -> 295.  On windows whose
@@ -1751,13 +1802,13 @@ int launch_bwd_tiled(const ngt_window_csr* c, const TilePlan& tp, const void* q,
     const unsigned blocks = edge_blocks(c->n_items_k, pw_k, groups, xcd);
     if (blocks > 0) {
       KernelTimer timer_("sparse_bwd_kv_rest", st);
-      hipLaunchKernelGGL((k_bwd_kv<T, DH, false, false>), dim3(blocks), dim3(kBlock), 0, st,
+      hipLaunchKernelGGL((k_bwd_kv<T, DH, false, false, false>), dim3(blocks), dim3(kBlock), 0, st,
                          static_cast<const T*>(q), make_keys<T, DH>(k, v, k_ext, v_ext, n_main, H),
                          static_cast<const T*>(g), rd, c->t_col,
                          reinterpret_cast<const int4*>(c->items_k), c->n_items_k, groups, hg, H,
                          L, inv_scale, lo, hi, static_cast<T*>(gk), static_cast<T*>(gv), nullptr,
                          part_kv, c->t_rowptr, c->packed_k, c->n_packed_k, pw_k, xcd, nullptr,
-                         nullptr, rows_k);
+                         nullptr, rows_k, FoldArgs{nullptr, nullptr});
       NGT_HIP_CHECK(hipGetLastError());
     }
   }
@@ -1820,8 +1871,9 @@ int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void
   float* part_kv = reinterpret_cast<float*>(ws + lay.part_kv);
   float* part_q = reinterpret_cast<float*>(ws + lay.part_q);
   const bool rc = dq_recompute(c, eb);
+  const bool fold = rowstat_fold(c, eb, rc);
   const int64_t nrh = int64_t(c->n_q) * H;
-  if (nrh > 0) {
+  if (nrh > 0 && !fold) {
     int64_t blocks = (nrh + kBlock - 1) / kBlock;
     if (blocks > 65536) blocks = 65536;
     KernelTimer timer_("sparse_rowstat", st);
@@ -1843,24 +1895,29 @@ int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void
   const unsigned blocks_k = edge_blocks(c->n_items_k, pw_k, groups, xcd);
   if (blocks_k > 0) {
     KernelTimer timer_("sparse_bwd_kv", st);
-    auto launch = [&](auto bias, auto nt) {
+    const FoldArgs fa{out, rinv};
+    auto launch = [&](auto bias, auto nt, auto fold_t) {
       constexpr bool B = decltype(bias)::value;
       constexpr bool N = decltype(nt)::value;
-      hipLaunchKernelGGL((k_bwd_kv<T, DH, B, N>), dim3(blocks_k), dim3(kBlock), 0, st,
+      constexpr bool F = decltype(fold_t)::value;
+      hipLaunchKernelGGL((k_bwd_kv<T, DH, B, N, F>), dim3(blocks_k), dim3(kBlock), 0, st,
                          static_cast<const T*>(q), make_keys<T, DH>(k, v, k_ext, v_ext, n_main, H),
                          static_cast<const T*>(g), rd, c->t_col,
                          reinterpret_cast<const int4*>(c->items_k), c->n_items_k, groups, hg, H,
                          L, inv_scale, lo, hi, static_cast<T*>(gk), static_cast<T*>(gv),
                          rc ? nullptr : ds, part_kv, c->t_rowptr, c->packed_k, c->n_packed_k,
-                         pw_k, xcd, eb, deb, 0);
+                         pw_k, xcd, eb, deb, 0, fa);
     };
     const bool nt = !rc && ds_nontemporal(c, H);
-    if (eb) {
-      if (nt) launch(std::true_type{}, std::true_type{});
-      else launch(std::true_type{}, std::false_type{});
+    if (fold) {  // no bias and no recomputed dQ
+      if (nt) launch(std::false_type{}, std::true_type{}, std::true_type{});
+      else launch(std::false_type{}, std::false_type{}, std::true_type{});
+    } else if (eb) {
+      if (nt) launch(std::true_type{}, std::true_type{}, std::false_type{});
+      else launch(std::true_type{}, std::false_type{}, std::false_type{});
     } else {
-      if (nt) launch(std::false_type{}, std::true_type{});
-      else launch(std::false_type{}, std::false_type{});
+      if (nt) launch(std::false_type{}, std::true_type{}, std::false_type{});
+      else launch(std::false_type{}, std::false_type{}, std::false_type{});
     }
     NGT_HIP_CHECK(hipGetLastError());
   }

@@ -282,17 +282,23 @@ def sparse_fwd_bwd(q, k, v, edge_index, grad_x, num_heads, dtype=torch.float32, 
 
 
 def full_fwd_bwd(q, k, v, grad_x, dtype=torch.float32, dropout_mult=None, flash=False,
-                 attn_bias=None, pruning_mask=None, mask=None):
+                 attn_bias=None, pruning_mask=None, mask=None, flash_half=False):
     """full_attention (or, flash=True, naive_attention) forward + autograd
     backward on CPU; q [N_q,H,d], k/v [N_k,H,d].  attn_bias / pruning_mask
     ([1, H, N_q, N_k] or broadcastable) get their gradients in the dict as
-    "dbias" / "dpruning"; mask is a bool [N_q, N_k]."""
+    "dbias" / "dpruning"; mask is a bool [N_q, N_k].  flash_half=True runs
+    the flash branch as the reference's forward does (graphormer_dist_node_
+    level.py:111-122): q, k, v cast to fp16, naive_attention in fp16, the
+    result cast back to ``dtype``."""
     qf = q.to(dtype).clone().unsqueeze(0).requires_grad_(True)
     kf = k.to(dtype).clone().unsqueeze(0).requires_grad_(True)
     vf = v.to(dtype).clone().unsqueeze(0).requires_grad_(True)
     ab = attn_bias.to(dtype).clone().requires_grad_(True) if attn_bias is not None else None
     pm = pruning_mask.to(dtype).clone().requires_grad_(True) if pruning_mask is not None else None
-    if flash:
+    if flash and flash_half:
+        x = naive_attention(qf.half(), kf.half(), vf.half(), dropout_mult=dropout_mult).to(dtype)
+        ns = torch.empty(0)
+    elif flash:
         x, ns = naive_attention(qf, kf, vf, dropout_mult=dropout_mult), torch.empty(0)
     else:
         x, ns = full_attention(qf, kf, vf, attn_bias=ab, pruning_mask=pm, mask=mask,

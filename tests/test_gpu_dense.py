@@ -244,15 +244,54 @@ def test_dense_module_dropout_and_flash():
     ref = OA.full_fwd_bwd(q, k, v, go, dropout_mult=mult)
     assert_close(x1[0].view(n, H, d).cpu(), ref["x"], torch.float32, "train x")
     assert_close(s1.cpu(), ref["node_scores"], torch.float32, "train score")
-    # flash branch
+    # flash branch: the reference's fp16 casts (graphormer_dist_node_level.py:111-122)
     torch.manual_seed(78)
     xf, sf = mod(q[None].cuda(), k[None].cuda(), v[None].cuda(), None, None, "flash")
     assert sf is None and xf.dtype == torch.float32 and xf.shape == (1, n, H * d)
     torch.manual_seed(78)
     seed = int(torch.randint(0, 2**62, (1,), dtype=torch.int64, device="cuda").item())
     mult = OA.dropout_multiplier(seed, H, n, n, 0.5)
-    ref = OA.full_fwd_bwd(q, k, v, go, dropout_mult=mult, flash=True)
-    assert_close(xf[0].view(n, H, d).cpu(), ref["x"], torch.float32, "flash x")
+    ref = OA.full_fwd_bwd(q, k, v, go, dropout_mult=mult, flash=True, flash_half=True)
+    # fp16 arithmetic in the reference: every intermediate is rounded to fp16
+    # (unit roundoff 2^-11 = 4.9e-4); the kernels keep them in fp32
+    assert relerr(xf[0].view(n, H, d).cpu(), ref["x"]) < 2e-3
+    assert torch.equal(xf, xf.half().float())  # the output is fp16-rounded
+
+
+def test_flash_branch_rounds_inputs_and_gradients_to_fp16():
+    """The flash branch casts q/k/v to fp16 as the reference does: inputs
+    that differ below fp16's precision give the same bits, the output is
+    fp16-valued, and forward and gradients stay within fp16 rounding of the
+    reference's fp16 arithmetic (restated on the CPU in fp16)."""
+    _say("case flash fp16")
+    H, d, n_q, n_k = 2, 16, 45, 60
+    q, k, v, go = _qkv(n_q, n_k, H, d, torch.float32, seed=19)
+    q, k, v = (t.half().float() for t in (q, k, v))  # fp16 values
+    mod = CoreAttention(H * d, 0.5, H).cuda().train()
+    # (1 + 2^-14) times an fp16 value is no fp16 value but rounds back to it:
+    # 2^-14 is below half of fp16's relative spacing (2^-11 at least)
+    outs = []
+    for bump in (0.0, 2.0 ** -14):
+        qd, kd, vd = ((t * (1 + bump)).cuda()[None].requires_grad_(True) for t in (q, k, v))
+        torch.manual_seed(81)
+        x, _ = mod(qd, kd, vd, None, None, "flash")
+        x.backward(go.reshape(1, n_q, H * d).cuda())
+        torch.cuda.synchronize()
+        outs.append([x.detach().cpu(), qd.grad.cpu(), kd.grad.cpu(), vd.grad.cpu()])
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    x, dq, dk, dv = outs[0]
+    assert torch.equal(x, x.half().float())
+    for gr in (dq, dk, dv):  # the gradients pass through the fp16 cast too
+        assert torch.equal(gr, gr.half().float())
+    torch.manual_seed(81)
+    seed = int(torch.randint(0, 2**62, (1,), dtype=torch.int64, device="cuda").item())
+    mult = OA.dropout_multiplier(seed, H, n_q, n_k, 0.5)
+    ref = OA.full_fwd_bwd(q, k, v, go, dropout_mult=mult, flash=True, flash_half=True)
+    got = {"x": x[0].view(n_q, H, d), "dq": dq[0], "dk": dk[0], "dv": dv[0]}
+    for name, t in got.items():
+        e = relerr(t, ref[name])
+        assert e < 2e-3, (name, e)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])

@@ -123,3 +123,35 @@ def test_nontemporal_score_gradient_stores_give_the_same_bits(monkeypatch):
     for name in ("x", "node_scores", "dq", "dk", "dv"):
         assert torch.equal(a[name], b[name]), name
         assert_close(b[name].float(), ref[name].float(), torch.bfloat16, f"nt:{name}")
+
+
+@pytest.mark.parametrize("H,d,dtype,n_main", [(8, 8, torch.float32, None),
+                                              (8, 16, torch.bfloat16, 380),
+                                              (32, 24, torch.bfloat16, None),
+                                              (2, 64, torch.float32, None)])
+def test_rowstat_folded_into_the_key_major_pass_gives_the_same_bits(monkeypatch, H, d, dtype,
+                                                                    n_main):
+    """On small windows the key-major pass forms each query's {r, r D} from
+    its out row and rinv itself (no k_rowstat launch), with k_rowstat's
+    arithmetic: forcing the fold on and off changes no bit; split, medium and
+    packed key rows; keys in one or two buffers."""
+    _say(f"case rowstat fold H={H} d={d} {dtype} n_main={n_main}")
+    n_q, n_k = 420, 450
+    rng = np.random.default_rng(H + d)
+    src = np.concatenate([rng.integers(0, n_k, 5000), np.full(700, 3), np.full(300, n_k - 2)])
+    dst = np.concatenate([rng.integers(0, n_q, 5000), rng.integers(0, n_q, 700),
+                          rng.integers(0, n_q, 300)])
+    ei = np.stack([src, dst]).astype(np.int64)
+    q, k, v, go = _qkv(n_q, n_k, H, d, dtype, seed=13)
+    monkeypatch.setenv("NGT_DQ_RECOMPUTE", "0")
+    monkeypatch.setenv("NGT_FOLD_ROWSTAT", "0")
+    a = _run(q, k, v, ei, go, 64, 8, n_main=n_main)
+    monkeypatch.setenv("NGT_FOLD_ROWSTAT", "1")
+    b = _run(q, k, v, ei, go, 64, 8, n_main=n_main)
+    ref = OA.sparse_fwd_bwd(q.float(), k.float(), v.float(), torch.from_numpy(ei), go.float(), H,
+                            dtype=torch.float32)
+    if n_main is not None:
+        ref["dk"], ref["dv"] = ref["dk"][:n_main], ref["dv"][:n_main]
+    for name in ("x", "node_scores", "dq", "dk", "dv"):
+        assert torch.equal(a[name], b[name]), name
+        assert_close(b[name].float(), ref[name].float(), dtype, f"fold:{name}")
