@@ -394,11 +394,25 @@ def prep_bench(args, cfg, dev) -> dict:
         lambda: RF.node_out_window(win, sub_csr, scores, 0.3))
     _, t_in = timed(lambda: RF.node_in_window(kept, expired, ppr, ppr_val, int(expired.numel()),
                                               coo, n))
+    # a rank's eight windows (disjoint partitions, each widened by its related
+    # nodes, so that they overlap) rebuilt as _rebuild_local_window_structures
+    # does: duplicate layout, feature cache, induced subgraphs from the CSR
+    perm = torch.randperm(n, generator=g, device=dev)
+    n_win = 8 if 8 * cfg.n_q <= n else max(1, n // cfg.n_q)
+    rank_wins = [W.merge_related_nodes(xadj, adjncy, eweights,
+                                       torch.sort(perm[i * cfg.n_q:(i + 1) * cfg.n_q]).values, pct)
+                 for i in range(n_win)]
+    lw, t_rank = timed(lambda: W.rebuild_local_windows(rank_wins, features, rowptr=rowptr,
+                                                       col=col), reps=3)
+    n_dup = int(lw.feature_cache.shape[0])
+    del lw, rank_wins, perm
     ops = {"merge_related_nodes_ms": t_rel, "subgraph_from_csr_ms": t_csr,
            "subgraph_coo_ms": t_coo, "window_csr_build_ms": t_adj, "feature_gather_ms": t_gather,
-           "node_out_ms": t_out, "node_in_ms": t_in}
+           "node_out_ms": t_out, "node_in_ms": t_in, "rank_windows": n_win,
+           "rank_rebuild_ms": t_rank, "rank_cached_nodes": n_dup}
     total = t_rel + t_csr + t_adj + t_gather
-    _log("[bench] prep: " + ", ".join(f"{k} {v:.3f}" for k, v in ops.items())
+    _log("[bench] prep: " + ", ".join(f"{k} {v:.3f}" if isinstance(v, float) else f"{k} {v}"
+                                      for k, v in ops.items())
          + f"; window {n_w} nodes, {int(sub_csr.shape[1])} edges")
 
     cpu = None

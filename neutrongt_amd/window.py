@@ -17,6 +17,8 @@
                             relabel_nodes=True as called at window_state.py:82,127
                             and metisPartition.py:280,290
   subgraph_from_csr         GPU (ngt_subgraph_csr); window_state.py:92-119
+  rebuild_local_windows     a rank's windows: duplicate layout, feature cache and
+                            induced subgraphs in one call; window_state.py:223-260
 
 Every step runs as HIP kernels; Python only sizes buffers and reads back
 counts.
@@ -299,3 +301,72 @@ def adj_weights(edge_index: torch.Tensor, ppr_val: torch.Tensor):
     if bad or big:
         raise ValueError(f"adj_weights: {bad} entries with a negative id, {big} weights >= 2^31")
     return xadj, adjncy[: 2 * u], ew[: 2 * u]
+
+
+class LocalWindows:
+    """A rank's window structures as _rebuild_local_window_structures keeps
+    them (NeutronGT/core/node_level_pipeline/window_state.py:223-260), on the
+    GPU: ``partitions`` (duplicates first when the cache is used),
+    ``dup_nodes`` and ``dup_indices`` per window, ``feature_cache`` (the
+    duplicate nodes' feature rows), ``sub_edge_index`` per window (the
+    induced subgraph relabelled by position in its partition) and ``timings``
+    (seconds, the reference's timing_stats keys; each step synchronised)."""
+
+    def __init__(self, partitions, dup_nodes, dup_indices, feature_cache, sub_edge_index,
+                 timings):
+        self.partitions = partitions
+        self.dup_nodes = dup_nodes
+        self.dup_indices = dup_indices
+        self.feature_cache = feature_cache
+        self.sub_edge_index = sub_edge_index
+        self.timings = timings
+
+    def features(self, i: int, feature: torch.Tensor) -> torch.Tensor:
+        """x_i of window i (train_eval.py:234-242): its duplicates' rows from
+        the cache, the rest from ``feature``; bitwise feature[partition]."""
+        idx = self.dup_indices[i] if self.dup_indices else torch.empty(
+            (0,), dtype=torch.long, device=feature.device)
+        return assemble_window_features(feature, self.feature_cache, idx, self.partitions[i])
+
+
+def rebuild_local_windows(local_partitions, feature: torch.Tensor, use_cache: bool = True,
+                          edge_index: torch.Tensor | None = None, num_nodes: int | None = None,
+                          rowptr: torch.Tensor | None = None, col: torch.Tensor | None = None):
+    """_rebuild_local_window_structures (window_state.py:223-260) for one rank,
+    every step on the GPU: with ``use_cache`` the duplicate layout and its
+    feature cache (:52-73, :181-205; window_dup_layout), then each window's
+    induced subgraph, from the global COO ``edge_index`` (PyG subgraph,
+    :122-133) or, without it, from the global CSR ``rowptr``/``col``
+    (_subgraph_from_csr, :92-119, 134-140).  ``feature`` [num_nodes, F] on
+    the GPU.  The struct_enc spatial positions (:247-256) are not built.
+    Returns a LocalWindows."""
+    import time
+
+    dev = feature.device
+    if not feature.is_cuda:
+        raise ValueError("rebuild_local_windows: feature must be on the GPU")
+    if edge_index is None and (rowptr is None or col is None):
+        raise ValueError("rebuild_local_windows: give edge_index (+ num_nodes) or rowptr and col")
+    parts = [p.reshape(-1).to(device=dev, dtype=torch.long) for p in local_partitions]
+    timings = {"local_dup_cache_rebuild_time": 0.0, "local_subgraph_rebuild_time": 0.0,
+               "local_spatial_rebuild_time": 0.0}
+    torch.cuda.synchronize(dev)
+    t = time.perf_counter()
+    if use_cache and parts:
+        parts, dups, cache_ids, idx = window_dup_layout(parts, device=dev)
+        cache = dup_feature_cache(feature, cache_ids)
+    else:
+        dups = [torch.empty((0,), dtype=torch.long, device=dev) for _ in parts]
+        idx = []
+        cache = torch.empty((0,) + tuple(feature.shape[1:]), dtype=feature.dtype, device=dev)
+    torch.cuda.synchronize(dev)
+    timings["local_dup_cache_rebuild_time"] = time.perf_counter() - t
+    t = time.perf_counter()
+    if edge_index is not None:
+        n = int(num_nodes) if num_nodes is not None else int(feature.shape[0])
+        subs = [subgraph(p, edge_index, n) for p in parts]
+    else:
+        subs = [subgraph_from_csr(p, rowptr, col) for p in parts]
+    torch.cuda.synchronize(dev)
+    timings["local_subgraph_rebuild_time"] = time.perf_counter() - t
+    return LocalWindows(parts, dups, idx, cache, subs, timings)

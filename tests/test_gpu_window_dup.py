@@ -96,3 +96,45 @@ def test_dup_layout_rank_scale_and_feature_assembly():
     for w in (0, 7, 15):
         x = W.assemble_window_features(fd, fcache, idx[w], rer[w])
         assert torch.equal(x.cpu(), feat[torch.from_numpy(rer_o[w])])
+
+
+@pytest.mark.parametrize("use_cache,route", [(True, "coo"), (True, "csr"), (False, "coo")])
+def test_rebuild_local_windows_matches_oracle(use_cache, route):
+    """A rank's windows rebuilt as _rebuild_local_window_structures does
+    (window_state.py:223-260): duplicate layout and feature cache, then each
+    window's induced subgraph over its (reranged) partition, from the global
+    COO or CSR; x_i from the cache equals feature[partition]."""
+    _say(f"case rebuild local windows cache={use_cache} route={route}")
+    rng = np.random.default_rng(17)
+    n, E = 3000, 40000
+    src = rng.integers(0, n, E)
+    dst = rng.integers(0, n, E)
+    order = np.lexsort((dst, src))  # CSR order for the csr route
+    ei = np.stack([src[order], dst[order]]).astype(np.int64)
+    rowptr = np.searchsorted(ei[0], np.arange(n + 1)).astype(np.int64)
+    parts = [np.sort(rng.choice(n, 700, replace=False)) for _ in range(5)]  # overlapping windows
+    feat = torch.randn(n, 24, generator=torch.Generator().manual_seed(3))
+    fd = feat.cuda()
+    kw = (dict(edge_index=torch.from_numpy(ei).cuda(), num_nodes=n) if route == "coo" else
+          dict(rowptr=torch.from_numpy(rowptr).cuda(), col=torch.from_numpy(ei[1]).cuda()))
+    lw = W.rebuild_local_windows([torch.from_numpy(p) for p in parts], fd, use_cache=use_cache, **kw)
+    if use_cache:
+        rer_o, dups_o, cache_o, idx_o = _oracle(parts)
+    else:
+        rer_o, dups_o = parts, [np.zeros(0, np.int64)] * len(parts)
+        cache_o, idx_o = np.zeros(0, np.int64), []
+    assert len(lw.partitions) == len(parts) and len(lw.sub_edge_index) == len(parts)
+    assert lw.feature_cache.shape == (len(cache_o), 24)
+    assert torch.equal(lw.feature_cache.cpu(), feat[torch.from_numpy(np.asarray(cache_o, np.int64))])
+    for w in range(len(parts)):
+        _same(lw.partitions[w], rer_o[w], f"partition[{w}]")
+        _same(lw.dup_nodes[w], dups_o[w], f"dups[{w}]")
+        if use_cache:
+            _same(lw.dup_indices[w], idx_o[w], f"dup_index[{w}]")
+        want = (OG.subgraph_coo(rer_o[w], ei, n) if route == "coo"
+                else OG.subgraph_from_csr(rer_o[w], rowptr, ei[1]))
+        _same(lw.sub_edge_index[w], want, f"sub_edge_index[{w}]")
+        x = lw.features(w, fd)
+        assert torch.equal(x.cpu(), feat[torch.from_numpy(np.asarray(rer_o[w], np.int64))])
+    assert set(lw.timings) == {"local_dup_cache_rebuild_time", "local_subgraph_rebuild_time",
+                               "local_spatial_rebuild_time"}
