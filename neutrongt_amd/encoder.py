@@ -43,7 +43,7 @@ import torch.nn.functional as F
 
 from .attention import CoreAttention
 from .layernorm import FusedLayerNorm, add_dropout_layernorm
-from .linear import WgradLinear
+from .linear import WgradLinear, project
 
 
 def init_params(module: nn.Module, n_layers: int) -> None:
@@ -93,9 +93,8 @@ class _Attention(nn.Module):
     def attend(self, x, edge_index, attn_type, kv_cache):
         b, n, _ = x.shape
         H, d = self.num_heads, self.att_size
-        q = self.linear_q(x).view(b, n, H, d)
-        k = self.linear_k(x).view(b, n, H, d)
-        v = self.linear_v(x).view(b, n, H, d)
+        q, k, v = project(x, self.linear_q, self.linear_k, self.linear_v)
+        q, k, v = q.view(b, n, H, d), k.view(b, n, H, d), v.view(b, n, H, d)
         if kv_cache is None:
             y, score = self.local_attn(q, k, v, None, edge_index, attn_type)
             return y, score, [k, v]

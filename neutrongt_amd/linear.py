@@ -15,7 +15,9 @@ and in the backward computes
   db = column sums of dY             (ngt_colsum_bf16, fp32, fixed order).
 dW and db are fp32 (autocast's own backward rounds dW to bf16 first).
 Outside bf16 autocast, without gradients, or for widths that are not
-multiples of 8 it is a plain nn.Linear.
+multiples of 8 it is a plain nn.Linear.  ``project(x, lin_q, lin_k, lin_v)``
+runs several such layers on one input as one autograd node whose backward
+sums dX inside the GEMMs.
 """
 from __future__ import annotations
 
@@ -93,14 +95,85 @@ class _WgradLinearFn(torch.autograd.Function):
         return gx, dw, db
 
 
+class _ProjectionGroupFn(torch.autograd.Function):
+    """Several projections of one input, y_i = x W_i^T + b_i, as one node.
+
+    Forward: one GEMM per projection, as ``_WgradLinearFn``.  Backward: dX is
+    accumulated by the GEMMs themselves (dX = dY_0 W_0, then dX += dY_i W_i
+    with the library's beta = 1), where separate nodes would leave autograd to
+    add their bf16 dX tensors with elementwise kernels (two extra passes over
+    a [32,768 x 768] tensor for Q/K/V).  dW and db as ``_WgradLinearFn``."""
+
+    @staticmethod
+    def forward(ctx, x, *params):
+        x16 = x.to(torch.bfloat16)
+        n = len(params) // 2
+        ws = [params[2 * i].to(torch.bfloat16) for i in range(n)]
+        bs = [params[2 * i + 1] for i in range(n)]
+        ys = []
+        with torch.autocast("cuda", enabled=False):
+            for w16, b in zip(ws, bs):
+                ys.append(F.linear(x16, w16, b.to(torch.bfloat16) if b is not None else None))
+        ctx.save_for_backward(x16, *ws)
+        ctx.has_bias = [b is not None for b in bs]
+        ctx.set_materialize_grads(False)  # an unused output: no GEMMs, no weight gradient
+        return tuple(ys)
+
+    @staticmethod
+    def backward(ctx, *gys):
+        x16, *ws = ctx.saved_tensors
+        n_in = x16.shape[-1]
+        x2 = None
+        gx = None
+        grads = []
+        for i, (gy, w16) in enumerate(zip(gys, ws)):
+            if gy is None:
+                grads += [None, None]
+                continue
+            g2 = gy.to(torch.bfloat16).reshape(-1, w16.shape[0]).contiguous()
+            if ctx.needs_input_grad[0]:
+                with torch.autocast("cuda", enabled=False):
+                    if gx is None:
+                        gx = g2 @ w16
+                    else:
+                        gx.addmm_(g2, w16)
+            dw = db = None
+            if ctx.needs_input_grad[1 + 2 * i]:
+                if x2 is None:
+                    x2 = x16.reshape(-1, n_in).contiguous()
+                dw = weight_grad(x2, g2)
+            if ctx.has_bias[i] and ctx.needs_input_grad[2 + 2 * i]:
+                db = colsum_bf16(g2)
+            grads += [dw, db]
+        if gx is not None:
+            gx = gx.view(*x16.shape)
+        return (gx, *grads)
+
+
+def _fast_path(lin: nn.Linear, x: torch.Tensor) -> bool:
+    return (x.is_cuda and torch.is_grad_enabled() and lin.weight.requires_grad
+            and torch.is_autocast_enabled("cuda")
+            and torch.get_autocast_dtype("cuda") == torch.bfloat16
+            and lin.in_features % 8 == 0 and lin.out_features % 8 == 0)
+
+
+def project(x: torch.Tensor, *lins: nn.Linear):
+    """(lin(x) for lin in lins), with the backward's dX summed inside the
+    GEMMs when all of them take the bf16 autocast path; otherwise each
+    module's own forward."""
+    if len(lins) > 1 and all(isinstance(l, WgradLinear) and _fast_path(l, x) for l in lins):
+        params = []
+        for l in lins:
+            params += [l.weight, l.bias]
+        return _ProjectionGroupFn.apply(x, *params)
+    return tuple(l(x) for l in lins)
+
+
 class WgradLinear(nn.Linear):
     """nn.Linear (same parameters and state-dict names) with the split-K
     weight gradient and the HIP bias gradient under bf16 autocast."""
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if (x.is_cuda and torch.is_grad_enabled() and self.weight.requires_grad
-                and torch.is_autocast_enabled("cuda")
-                and torch.get_autocast_dtype("cuda") == torch.bfloat16
-                and self.in_features % 8 == 0 and self.out_features % 8 == 0):
+        if _fast_path(self, x):
             return _WgradLinearFn.apply(x, self.weight, self.bias)
         return super().forward(x)

@@ -71,3 +71,56 @@ def test_wgrad_linear_module_under_autocast():
     # outside autocast it is nn.Linear
     y32 = mod(x.detach())
     assert y32.dtype == torch.float32
+
+
+@pytest.mark.parametrize("use", ["qkv", "qv", "k"])
+def test_projection_group_matches_separate_layers(use):
+    """project(x, q, k, v): forward bit-equal to the separate layers; dX (summed
+    inside the GEMMs) as close to the float64 sum of the bf16 products as
+    autograd's sum of the separate layers' bf16 dX; dW/db as float64.  Outputs
+    left out of the loss get no weight gradient."""
+    from neutrongt_amd.linear import project
+    _say(f"case projection group use={use}")
+    torch.manual_seed(1)
+    n_in, n_out = 128, 96
+    refs = [nn.Linear(n_in, n_out).cuda() for _ in range(3)]
+    mods = [WgradLinear(n_in, n_out).cuda() for _ in range(3)]
+    for m, r in zip(mods, refs):
+        m.load_state_dict(r.state_dict())
+    x = torch.randn(2, 3000, n_in, device="cuda", requires_grad=True)
+    x2 = x.detach().clone().requires_grad_(True)
+    gys = [torch.randn(2, 3000, n_out, device="cuda") for _ in range(3)]
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        ys = project(x, *mods)
+        ys_ref = [r(x2) for r in refs]
+    for y, yr in zip(ys, ys_ref):
+        assert y.dtype == torch.bfloat16 and torch.equal(y, yr)
+    picked = [i for i, c in enumerate("qkv") if c in use]
+    sum(((ys[i].float() * gys[i]).sum() for i in picked)).backward()
+    sum(((ys_ref[i].float() * gys[i]).sum() for i in picked)).backward()
+    x16 = x.detach().to(torch.bfloat16).reshape(-1, n_in).double()
+    exact = sum(gys[i].to(torch.bfloat16).reshape(-1, n_out).double()
+                @ mods[i].weight.detach().to(torch.bfloat16).double() for i in picked)
+    err = relerr(x.grad.reshape(-1, n_in), exact)
+    err_ref = relerr(x2.grad.reshape(-1, n_in), exact)
+    assert err < 8e-3 and err <= 1.5 * err_ref + 1e-4, (err, err_ref)
+    for i in range(3):
+        if i not in picked:
+            assert mods[i].weight.grad is None and mods[i].bias.grad is None
+            continue
+        g16 = gys[i].to(torch.bfloat16).reshape(-1, n_out).double()
+        assert relerr(mods[i].weight.grad, g16.T @ x16) < 1e-5
+        assert relerr(mods[i].bias.grad, g16.sum(0)) < 1e-5
+
+
+def test_projection_group_without_input_grad():
+    from neutrongt_amd.linear import project
+    _say("case projection group, input without grad")
+    mods = [WgradLinear(64, 64).cuda() for _ in range(3)]
+    x = torch.randn(700, 64, device="cuda")
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        ys = project(x, *mods)
+    sum(y.float().sum() for y in ys).backward()
+    x16 = x.to(torch.bfloat16).double()
+    for m in mods:
+        assert relerr(m.weight.grad, torch.ones(700, 64, dtype=torch.float64, device="cuda").T @ x16) < 1e-5
