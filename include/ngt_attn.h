@@ -590,10 +590,12 @@ int ngt_add_layernorm_bwd(int dtype, const void* sum, int grad_dtype, const void
 
 /*
  * Column sums of a bf16 matrix in fp32: out[j] = sum_k dy[k][j], dy
- * [n_rows, n_cols] row-major, 16-byte aligned, n_cols a multiple of 8; summed
- * in a fixed order.  The bias gradient of the encoder's linear layers under
- * bf16 autocast (the autograd of nn.Linear's bias in MultiHeadAttention and
- * the FFN, NeutronGT/models/graphormer_dist_node_level.py:130-206).
+ * [n_rows, n_cols] row-major (any n_cols >= 1; 16-byte loads when n_cols is
+ * a multiple of 8 and dy 16-byte aligned); summed in a fixed order, the same
+ * for either load width.  The bias gradient of the encoder's linear layers
+ * under bf16 autocast (the autograd of nn.Linear's bias in
+ * MultiHeadAttention, the FFN and the readout,
+ * NeutronGT/models/graphormer_dist_node_level.py:130-206, :242-381).
  */
 int ngt_colsum_workspace_bytes(int64_t n_rows, int32_t n_cols, size_t* bytes);
 int ngt_colsum_bf16(const void* dy, int64_t n_rows, int32_t n_cols, float* out, void* workspace,

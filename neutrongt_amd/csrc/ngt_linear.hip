@@ -6,7 +6,7 @@
 // under bf16 autocast, where dy is [32,768 x 768]; the weight gradient itself
 // is a library GEMM (neutrongt_amd/linear.py).  A column reduction of a tall
 // matrix: blocks own 256 columns (a thread 8 adjacent columns, one 16-byte
-// load per row) of a chunk of rows, and a second pass adds the chunks'
+// load per row when the width allows) of a chunk of rows, and a second pass adds the chunks'
 // partials in chunk order.  HBM-bound: K * n * 2 bytes read once.
 #include "ngt_common.h"
 
@@ -19,7 +19,11 @@ constexpr int kRowLanes = kBlock / 32;  // threads per column group
 constexpr int kRowsPerChunk = 256;
 
 // part[chunk][j] = sum over the chunk's rows of dy[k][j].
-// grid = (ceil(n / 256), n_chunks).
+// grid = (ceil(n / 256), n_chunks).  VEC: n a multiple of 8 and dy 16-byte
+// aligned, one 16-byte load per row and thread; otherwise (e.g. a 47-class
+// readout) the thread's 8 columns are read one bf16 at a time, those past n
+// skipped.  Both add each column's rows in the same order.
+template <bool VEC>
 __global__ __launch_bounds__(kBlock) void k_colsum(const bf16_t* __restrict__ dy, int64_t K,
                                                    int32_t n, float* __restrict__ part) {
   __shared__ float red[kRowLanes][kColsPerBlock];
@@ -33,12 +37,18 @@ __global__ __launch_bounds__(kBlock) void k_colsum(const bf16_t* __restrict__ dy
   for (int c = 0; c < 8; ++c) s[c] = 0.f;
   if (col < n) {
     for (int64_t r = r0 + rl; r < r1; r += kRowLanes) {
-      const uint4 w = *reinterpret_cast<const uint4*>(dy + r * n + col);
-      const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+      if constexpr (VEC) {
+        const uint4 w = *reinterpret_cast<const uint4*>(dy + r * n + col);
+        const uint32_t u[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        s[2 * c] += bf16_to_f32(static_cast<uint16_t>(u[c] & 0xffffu));
-        s[2 * c + 1] += bf16_to_f32(static_cast<uint16_t>(u[c] >> 16));
+        for (int c = 0; c < 4; ++c) {
+          s[2 * c] += bf16_to_f32(static_cast<uint16_t>(u[c] & 0xffffu));
+          s[2 * c + 1] += bf16_to_f32(static_cast<uint16_t>(u[c] >> 16));
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+          if (col + c < n) s[c] += bf16_to_f32(dy[r * n + col + c].x);
       }
     }
   }
@@ -85,7 +95,6 @@ int check(const char* fn, int64_t K, int n) {
   if (K < 0 || n < 1)
     return set_error(NGT_ERR_ARG, "%s: bad sizes n_rows=%lld n_cols=%d", fn,
                      static_cast<long long>(K), n);
-  if (n % 8) return set_error(NGT_ERR_UNSUPPORTED, "%s: n_cols=%d is not a multiple of 8", fn, n);
   if (chunks_for(K) > 65535)
     return set_error(NGT_ERR_UNSUPPORTED, "%s: n_rows=%lld exceeds %lld", fn,
                      static_cast<long long>(K), 65535LL * kRowsPerChunk);
@@ -112,16 +121,22 @@ extern "C" int ngt_colsum_bf16(const void* dy, int64_t n_rows, int32_t n_cols, f
   const int64_t nc = chunks_for(n_rows);
   if (nc > 0) {
     if (!dy) return set_error(NGT_ERR_ARG, "ngt_colsum_bf16: null dy");
-    if (reinterpret_cast<uintptr_t>(dy) & 15)
-      return set_error(NGT_ERR_ARG, "ngt_colsum_bf16: dy must be 16-byte aligned");
+    if (reinterpret_cast<uintptr_t>(dy) & 1)
+      return set_error(NGT_ERR_ARG, "ngt_colsum_bf16: dy must be 2-byte aligned");
+    const bool vec = n_cols % 8 == 0 && !(reinterpret_cast<uintptr_t>(dy) & 15);
     const size_t need = size_t(nc) * n_cols * 4;
     if (!workspace || workspace_bytes < need)
       return set_error(NGT_ERR_WORKSPACE, "ngt_colsum_bf16: workspace %zu < %zu", workspace_bytes,
                        need);
     KernelTimer timer_("colsum", st);
     const dim3 grid((n_cols + kColsPerBlock - 1) / kColsPerBlock, static_cast<unsigned>(nc));
-    hipLaunchKernelGGL(k_colsum, grid, dim3(kBlock), 0, st, static_cast<const bf16_t*>(dy),
-                       n_rows, n_cols, static_cast<float*>(workspace));
+    if (vec)
+      hipLaunchKernelGGL(k_colsum<true>, grid, dim3(kBlock), 0, st, static_cast<const bf16_t*>(dy),
+                         n_rows, n_cols, static_cast<float*>(workspace));
+    else
+      hipLaunchKernelGGL(k_colsum<false>, grid, dim3(kBlock), 0, st,
+                         static_cast<const bf16_t*>(dy), n_rows, n_cols,
+                         static_cast<float*>(workspace));
     NGT_HIP_CHECK(hipGetLastError());
   }
   // no rows: the reduce adds no chunks and writes zeros

@@ -97,6 +97,18 @@ def test_argument_errors_are_reported_without_touching_the_gpu():
         _lib.check(1)
 
 
+def test_colsum_takes_any_width():
+    """Column sums of any width (a 47-class readout's bias gradient): one fp32
+    partial per 256-row chunk and column; zero columns refused."""
+    lib = _lib.load()
+    nb = C.c_size_t()
+    for n in (1, 7, 47, 768):
+        assert lib.ngt_colsum_workspace_bytes(1000, n, C.byref(nb)) == 0
+        assert nb.value == 4 * n * 4  # ceil(1000 / 256) chunks
+    assert lib.ngt_colsum_workspace_bytes(1000, 0, C.byref(nb)) == 1
+    assert b"bad sizes" in lib.ngt_last_error()
+
+
 def test_dense_workspace_query_depends_on_path_and_scores():
     """The matrix-core path (bf16, d <= 32) needs H * n_k floats of node-score
     partials and nothing without node scores; the vector-ALU path sizes its

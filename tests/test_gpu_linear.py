@@ -20,7 +20,8 @@ def _say(*a):
 
 @pytest.mark.parametrize("K,n_out,n_in", [(32768, 768, 768), (1000, 64, 128), (37, 24, 40),
                                           (5000, 1536, 768), (300, 136, 8), (1, 8, 8),
-                                          (70001, 128, 256)])
+                                          (70001, 128, 256), (32768, 47, 768), (32768, 768, 100),
+                                          (513, 9, 13), (300, 1, 8)])
 def test_weight_and_bias_grad_match_fp64(K, n_out, n_in):
     _say(f"case wgrad K={K} n_out={n_out} n_in={n_in}")
     g = torch.Generator(device="cuda").manual_seed(K + n_out)
@@ -39,8 +40,36 @@ def test_colsum_edge_cases():
     empty = torch.empty(0, 16, device="cuda", dtype=torch.bfloat16)
     assert colsum_bf16(empty).abs().sum().item() == 0
     base = torch.randn(513, 40, device="cuda").to(torch.bfloat16)
-    view = base[1:]  # rows start 80 bytes in: not 16-byte aligned -> copied
+    view = base[1:]  # rows start 80 bytes in: not 16-byte aligned -> 2-byte loads
     assert relerr(colsum_bf16(view), view.double().sum(0)) < 1e-5
+    # the two load widths add each column's rows in the same order: same bits
+    assert torch.equal(colsum_bf16(view), colsum_bf16(view.clone()))
+    for n in (1, 7, 47, 100, 263):
+        dy = torch.randn(1000, n, device="cuda").to(torch.bfloat16)
+        assert relerr(colsum_bf16(dy), dy.double().sum(0)) < 1e-5, n
+
+
+@pytest.mark.parametrize("n_in,n_out", [(100, 768), (768, 47)])
+def test_wgrad_linear_any_width(n_in, n_out):
+    """The node encoder (100 -> 768) and a 47-class readout take the split-K
+    dW and the HIP db too: dW/db as float64 products, forward as nn.Linear."""
+    _say(f"case WgradLinear width {n_in} -> {n_out}")
+    torch.manual_seed(2)
+    ref = nn.Linear(n_in, n_out).cuda()
+    mod = WgradLinear(n_in, n_out).cuda()
+    mod.load_state_dict(ref.state_dict())
+    x = torch.randn(32768, n_in, device="cuda")
+    gy = torch.randn(32768, n_out, device="cuda")
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y = mod(x)
+        y_ref = ref(x)
+    assert torch.equal(y, y_ref)
+    y.backward(gy)
+    x16 = x.to(torch.bfloat16).double()
+    g16 = gy.to(torch.bfloat16).double()
+    assert mod.weight.grad.dtype == torch.float32
+    assert relerr(mod.weight.grad, g16.T @ x16) < 1e-5
+    assert relerr(mod.bias.grad, g16.sum(0)) < 1e-5
 
 
 def test_wgrad_linear_module_under_autocast():
