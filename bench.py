@@ -495,8 +495,10 @@ def model_step_bench(args, cfg, layers: int, dev) -> dict:
                    input_dropout_rate=0.1, attention_dropout_rate=0.5,
                    ffn_dim=hidden).to(dev).train()
     n_params = sum(p.numel() for p in model.parameters())
+    # torch's single-kernel AdamW (the reference builds the foreach default,
+    # main_sp_node_level_ppr.py:164; same update rule)
     opt = torch.optim.AdamW(model.parameters(), lr=1e-4, weight_decay=0.01,
-                            capturable=bool(args.graph))
+                            capturable=bool(args.graph), fused=True)
     _log(f"[bench] window step: {layers} layers, hidden {hidden}, {n_params} parameters, "
          f"n_q={cfg.n_q} n_k={n_k} E={E}")
 
