@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define NGT_ABI_VERSION 8
+#define NGT_ABI_VERSION 9
 
 #define NGT_F32 0
 #define NGT_BF16 1
@@ -232,6 +232,25 @@ int ngt_sparse_bwd_ext(int dtype, const void* q, const void* k, const void* v, c
                        int32_t n_heads, int32_t head_dim, float scale, float clamp_lo,
                        float clamp_hi, void* grad_q, void* grad_k, void* grad_v, void* workspace,
                        size_t workspace_bytes, void* stream);
+
+/*
+ * ngt_sparse_bwd_ext writing grad_q, grad_k and grad_v with a row stride of
+ * grad_row_stride elements (0: n_heads * head_dim, contiguous rows; else at
+ * least that and a multiple of 16 bytes; the gradients 16-byte aligned).
+ * Lets the caller of the Q/K/V projections (NeutronGT/models/
+ * graphormer_dist_node_level.py:130-147: three nn.Linear of one input) take
+ * the three gradients as one [N, 3 * H * d] matrix -- grad_q at column 0,
+ * grad_k at H * d, grad_v at 2 * H * d, stride 3 * H * d -- and run the
+ * projections' backward as one GEMM per operand.  Same values as
+ * ngt_sparse_bwd_ext, bit for bit.
+ */
+int ngt_sparse_bwd_strided(int dtype, const void* q, const void* k, const void* v,
+                           const void* k_ext, const void* v_ext, int32_t n_k_main,
+                           const void* out, const void* grad_out, const float* rinv,
+                           const ngt_window_csr* csr, int32_t n_heads, int32_t head_dim,
+                           float scale, float clamp_lo, float clamp_hi, void* grad_q,
+                           void* grad_k, void* grad_v, int64_t grad_row_stride, void* workspace,
+                           size_t workspace_bytes, void* stream);
 
 /*
  * The optional per-pair bias of the sparse path.  Replaces the attn_bias term

@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libngt_attn.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 NGT_F32 = 0
 NGT_BF16 = 1
@@ -103,6 +103,8 @@ SIGNATURES = {
                            _f32, _f32, _vp, _vp, _vp, _i32, _vp, _sz, _vp],
     "ngt_sparse_bwd_ext": [_i32, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _pcsr, _i32, _i32,
                            _f32, _f32, _f32, _vp, _vp, _vp, _vp, _sz, _vp],
+    "ngt_sparse_bwd_strided": [_i32, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _pcsr, _i32,
+                               _i32, _f32, _f32, _f32, _vp, _vp, _vp, _i64, _vp, _sz, _vp],
     "ngt_edge_bias_gather": [_pcsr, _i32, _vp, _i64, _i64, _i64, _vp, _vp, _vp],
     "ngt_sparse_fwd_bias": [_i32, _vp, _vp, _vp, _vp, _vp, _i32, _pcsr, _i32, _i32, _f32, _f32,
                             _f32, _f32, _vp, _vp, _vp, _vp, _i32, _vp, _sz, _vp],
@@ -219,7 +221,7 @@ def autograd_ext():
                     raise RuntimeError(f"{EXT_PATH.name} was built against another "
                                        "ngt_window_csr; rebuild it")
                 addr = lambda fn: C.cast(fn, C.c_void_p).value
-                mod.init(addr(lib.ngt_sparse_fwd_ext), addr(lib.ngt_sparse_bwd_ext),
+                mod.init(addr(lib.ngt_sparse_fwd_ext), addr(lib.ngt_sparse_bwd_strided),
                          addr(lib.ngt_last_error))
                 _ext = mod
     return _ext or None

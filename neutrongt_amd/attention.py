@@ -60,11 +60,14 @@ class SparseAttentionFunction(torch.autograd.Function):
     graphormer_dist_node_level.py:345).  Optional k_ext/v_ext [R, H, d] are
     further key rows N_k .. N_k+R-1 read from their own buffers (a detached
     cache of related keys, so the caller need not concatenate); they receive
-    no gradient.
+    no gradient.  ``interleave_grads`` (with N_q == N_k): dQ, dK and dV come
+    back as views of one [N, 3, H, d] buffer (ngt_sparse_bwd_strided), which a
+    caller of three projections of one input can multiply as one matrix.
     """
 
     @staticmethod
-    def forward(ctx, q, k, v, adj, scale, lo, hi, eps, k_ext=None, v_ext=None):
+    def forward(ctx, q, k, v, adj, scale, lo, hi, eps, k_ext=None, v_ext=None,
+                interleave_grads=False):
         lib = _lib.load()
         n_q, H, d = q.shape
         dev = q.device
@@ -85,6 +88,7 @@ class SparseAttentionFunction(torch.autograd.Function):
         else:
             ctx.save_for_backward(q, k, v, out, rinv)
         ctx.adj, ctx.scale, ctx.lo, ctx.hi, ctx.bwd_bytes = adj, scale, lo, hi, bwd_bytes
+        ctx.interleave = bool(interleave_grads) and q.shape[0] == k.shape[0]
         ctx.mark_non_differentiable(ns)
         # the node scores have no gradient: let the engine pass None for them
         # instead of filling a zero tensor (a kernel launch per layer)
@@ -97,25 +101,31 @@ class SparseAttentionFunction(torch.autograd.Function):
         q, k, v, out, rinv = saved[:5]
         k_ext, v_ext = saved[5:] if len(saved) == 7 else (None, None)
         if g_out is None:  # the output was not used by the loss
-            return None, None, None, None, None, None, None, None, None, None
+            return (None,) * 11
         lib = _lib.load()
         n_q, H, d = q.shape
         dev = q.device
         g = g_out.to(q.dtype)
         if not g.is_contiguous() or g.data_ptr() % 16:
             g = g.contiguous() if not g.is_contiguous() else g.clone()
-        gq = torch.empty_like(q)
-        gk = torch.empty_like(k)
-        gv = torch.empty_like(v)
+        if ctx.interleave:  # one [N, 3, H, d] buffer: dQ, dK, dV of a row side by side
+            buf = torch.empty(n_q, 3, H, d, dtype=q.dtype, device=dev)
+            gq, gk, gv = buf.unbind(1)
+            ldg = 3 * H * d
+        else:
+            gq = torch.empty_like(q)
+            gk = torch.empty_like(k)
+            gv = torch.empty_like(v)
+            ldg = 0
         ws = _workspace(ctx.bwd_bytes, dev)
         ext = k_ext is not None
-        _lib.check(lib.ngt_sparse_bwd_ext(
+        _lib.check(lib.ngt_sparse_bwd_strided(
             _dtype_code(q), q.data_ptr(), k.data_ptr(), v.data_ptr(),
             k_ext.data_ptr() if ext else None, v_ext.data_ptr() if ext else None, k.shape[0],
             out.data_ptr(), g.data_ptr(), rinv.data_ptr(), ctx.adj.ptr(), H, d, ctx.scale, ctx.lo,
-            ctx.hi, gq.data_ptr(), gk.data_ptr(), gv.data_ptr(), ws.data_ptr(), ctx.bwd_bytes,
-            _stream(dev)))
-        return gq, gk, gv, None, None, None, None, None, None, None
+            ctx.hi, gq.data_ptr(), gk.data_ptr(), gv.data_ptr(), ldg, ws.data_ptr(),
+            ctx.bwd_bytes, _stream(dev)))
+        return gq, gk, gv, None, None, None, None, None, None, None, None
 
 
 class SparseAttentionBiasFunction(torch.autograd.Function):
@@ -197,25 +207,28 @@ class SparseAttentionBiasFunction(torch.autograd.Function):
 
 
 def window_attention(q, k, v, adj, scale, lo=CLAMP_LO, hi=CLAMP_HI, eps=EPS, k_ext=None,
-                     v_ext=None):
+                     v_ext=None, interleave_grads=False):
     """SparseAttentionFunction's operation over a built WindowAdjacency, run by
     the C++ autograd node (ngt_autograd.so) when it is built -- the same
     library calls without a Python frame or ctypes conversion per layer and
     without the GIL on the autograd engine's device thread -- else by
     SparseAttentionFunction.  q/k/v (and k_ext/v_ext) as that function takes
-    them: contiguous, 16-byte aligned, on the GPU."""
+    them: contiguous, 16-byte aligned, on the GPU.  ``interleave_grads``: see
+    SparseAttentionFunction."""
     ext = _lib.autograd_ext()
     if ext is None:
-        return SparseAttentionFunction.apply(q, k, v, adj, scale, lo, hi, eps, k_ext, v_ext)
+        return SparseAttentionFunction.apply(q, k, v, adj, scale, lo, hi, eps, k_ext, v_ext,
+                                             interleave_grads)
     H, d = q.shape[1], q.shape[2]
     fwd_bytes, bwd_bytes = adj.workspace_bytes(H, d)
     return ext.sparse_attention(q, k, v, k_ext, v_ext, adj.csr_bytes, adj.mem, adj.dst_end,
                                 float(scale), float(lo), float(hi), float(eps), fwd_bytes,
-                                bwd_bytes)
+                                bwd_bytes, bool(interleave_grads))
 
 
 def sparse_attention(q, k, v, edge_index, num_heads=None, scale=None, cache: AdjacencyCache = None,
-                     lo=CLAMP_LO, hi=CLAMP_HI, eps=EPS, kv_ext=None, attn_bias=None):
+                     lo=CLAMP_LO, hi=CLAMP_HI, eps=EPS, kv_ext=None, attn_bias=None,
+                     interleave_grads=False):
     """Functional form.  q [.., N_q, H, d] -> (x [N_q, H, d], node_scores [max(dst)+1]).
 
     ``edge_index`` [2, E]: row 0 = key (src) index < N_k, row 1 = query (dst)
@@ -225,7 +238,8 @@ def sparse_attention(q, k, v, edge_index, num_heads=None, scale=None, cache: Adj
     own buffers without a concatenation; they get no gradient (a detached cache).
     ``attn_bias`` [1, H, Ns, Nd] (the reference's dense per-pair bias, indexed
     [0, h, src, dst], Ns >= N_k and Nd >= N_q) is added to each edge's clamped
-    score and receives a gradient when it requires one.
+    score and receives a gradient when it requires one.  ``interleave_grads``
+    (N_q == N_k, no bias): dQ, dK, dV as views of one [N, 3, H, d] buffer.
     """
     H, d = q.shape[-2], q.shape[-1]
     if num_heads is not None and num_heads != H:
@@ -264,7 +278,7 @@ def sparse_attention(q, k, v, edge_index, num_heads=None, scale=None, cache: Adj
         return SparseAttentionBiasFunction.apply(q, k, v, bias, adj, float(scale), float(lo),
                                                  float(hi), float(eps), k_ext, v_ext)
     return window_attention(q, k, v, adj, float(scale), float(lo), float(hi), float(eps), k_ext,
-                            v_ext)
+                            v_ext, interleave_grads)
 
 
 # -------------------------------------------------------------------- dense
@@ -641,24 +655,30 @@ class CoreAttention(nn.Module):
                                dropout_p=dropout_p)
         return x.unsqueeze(0), None
 
-    def sparse_attention_bias(self, q, k, v, edge_index, attn_bias, kv_ext=None):
+    def sparse_attention_bias(self, q, k, v, edge_index, attn_bias, kv_ext=None,
+                              interleave_grads=False):
         """graphormer_dist_node_level.py:67-98.  Returns (x [N_q, H, d], node_scores).
         ``kv_ext`` (k_r, v_r): extra key rows after k/v, without gradient.
         ``attn_bias`` [1, H, N, N] (optional): added to each edge's clamped
         score at [0, h, src, dst], as the reference's :81-84 does."""
         return sparse_attention(q, k, v, edge_index, num_heads=self.num_heads, scale=self.scale,
-                                cache=self.adjacency_cache, kv_ext=kv_ext, attn_bias=attn_bias)
+                                cache=self.adjacency_cache, kv_ext=kv_ext, attn_bias=attn_bias,
+                                interleave_grads=interleave_grads)
 
     def forward(self, q, k, v, attn_bias=None, edge_index=None, attn_type=None, mask=None,
-                pruning_mask=None, kv_ext=None):
+                pruning_mask=None, kv_ext=None, interleave_grads=False):
         """The reference's dispatch; ``kv_ext`` (an addition: (k_r, v_r), each
-        [R, H, d], no gradient) appends key rows without a concatenation."""
+        [R, H, d], no gradient) appends key rows without a concatenation;
+        ``interleave_grads`` (an addition, sparse path): dQ, dK, dV as views of
+        one [N, 3, H, d] buffer, for a caller that projects q, k, v from one
+        input (the other paths ignore it)."""
         batch_size, s_len = q.size(0), q.size(1)
         if kv_ext is not None and attn_type != "sparse":
             k = torch.cat([k, kv_ext[0].detach().to(k.dtype).reshape(1, -1, *k.shape[2:])], dim=1)
             v = torch.cat([v, kv_ext[1].detach().to(v.dtype).reshape(1, -1, *v.shape[2:])], dim=1)
         if attn_type == "sparse":
-            x, score = self.sparse_attention_bias(q, k, v, edge_index, attn_bias, kv_ext=kv_ext)
+            x, score = self.sparse_attention_bias(q, k, v, edge_index, attn_bias, kv_ext=kv_ext,
+                                                  interleave_grads=interleave_grads)
         elif attn_type == "flash":
             # The reference casts q/k/v to fp16 and the result back to fp32
             # (graphormer_dist_node_level.py:111-122).  Here the inputs are

@@ -5,7 +5,7 @@
 // NeutronGT/models/graphormer_dist_node_level.py:67-98): (q, k, v) ->
 // (out, node_scores), node scores without gradient, optional detached extra
 // key rows (k_ext, v_ext).  Forward and backward call the library's C ABI
-// (ngt_sparse_fwd_ext / ngt_sparse_bwd_ext) through function pointers that the
+// (ngt_sparse_fwd_ext / ngt_sparse_bwd_strided) through function pointers that the
 // Python side hands over once from the loaded libngt_attn.so, so a layer's
 // forward and backward run no Python frame, take no GIL on the autograd
 // engine's device thread and convert no ctypes arguments.  Host code only:
@@ -27,7 +27,7 @@ using torch::autograd::AutogradContext;
 using torch::autograd::tensor_list;
 
 decltype(&ngt_sparse_fwd_ext) g_fwd = nullptr;
-decltype(&ngt_sparse_bwd_ext) g_bwd = nullptr;
+decltype(&ngt_sparse_bwd_strided) g_bwd = nullptr;
 decltype(&ngt_last_error) g_err = nullptr;
 
 void check(int rc) {
@@ -79,14 +79,14 @@ Tensor workspace(int64_t bytes, const Tensor& like) {
   return at::empty({std::max<int64_t>(bytes, 1)}, like.options().dtype(at::kByte));
 }
 
-constexpr int kInputs = 14;  // forward arguments after ctx
+constexpr int kInputs = 15;  // forward arguments after ctx
 
 struct SparseAttention : public torch::autograd::Function<SparseAttention> {
   static tensor_list forward(AutogradContext* ctx, Tensor q, Tensor k, Tensor v,
                              std::optional<Tensor> k_ext_opt, std::optional<Tensor> v_ext_opt,
                              Tensor csr, Tensor csr_mem, int64_t dst_end,
                              double scale, double lo, double hi, double eps, int64_t fwd_bytes,
-                             int64_t bwd_bytes) {
+                             int64_t bwd_bytes, bool interleave_grads) {
     TORCH_CHECK(g_fwd && g_bwd, "ngt_autograd.init() was not called");
     // an absent argument is an empty optional: autograd inputs may not be
     // undefined tensors
@@ -125,6 +125,7 @@ struct SparseAttention : public torch::autograd::Function<SparseAttention> {
     ctx->saved_data["lo"] = lo;
     ctx->saved_data["hi"] = hi;
     ctx->saved_data["bwd_bytes"] = bwd_bytes;
+    ctx->saved_data["interleave"] = interleave_grads && n_q == k.size(0);
     ctx->mark_non_differentiable({ns});
     // the node scores have no gradient: no zero tensor is made for them
     ctx->set_materialize_grads(false);
@@ -141,7 +142,20 @@ struct SparseAttention : public torch::autograd::Function<SparseAttention> {
     const Tensor csr = ctx->saved_data["csr"].toTensor();
     const int64_t bwd_bytes = ctx->saved_data["bwd_bytes"].toInt();
     const Tensor g = rows16(grads[0].to(q.scalar_type()));
-    Tensor gq = at::empty_like(q), gk = at::empty_like(k), gv = at::empty_like(v);
+    Tensor gq, gk, gv;
+    int64_t ldg = 0;
+    if (ctx->saved_data["interleave"].toBool()) {
+      // one [N, 3, H, d] buffer: row i holds dQ, dK, dV of row i side by side
+      const Tensor buf = at::empty({q.size(0), 3, q.size(1), q.size(2)}, q.options());
+      gq = buf.select(1, 0);
+      gk = buf.select(1, 1);
+      gv = buf.select(1, 2);
+      ldg = 3 * q.size(1) * q.size(2);
+    } else {
+      gq = at::empty_like(q);
+      gk = at::empty_like(k);
+      gv = at::empty_like(v);
+    }
     Tensor ws = workspace(bwd_bytes, q);
     const bool ext = k_ext.defined();
     check(g_bwd(dtype_code(q), q.data_ptr(), k.data_ptr(), v.data_ptr(),
@@ -152,7 +166,7 @@ struct SparseAttention : public torch::autograd::Function<SparseAttention> {
                 static_cast<float>(ctx->saved_data["scale"].toDouble()),
                 static_cast<float>(ctx->saved_data["lo"].toDouble()),
                 static_cast<float>(ctx->saved_data["hi"].toDouble()), gq.data_ptr(),
-                gk.data_ptr(), gv.data_ptr(), ws.data_ptr(), static_cast<size_t>(bwd_bytes),
+                gk.data_ptr(), gv.data_ptr(), ldg, ws.data_ptr(), static_cast<size_t>(bwd_bytes),
                 stream_of(q)));
     res[0] = gq;
     res[1] = gk;
@@ -166,18 +180,18 @@ std::tuple<Tensor, Tensor> sparse_attention(Tensor q, Tensor k, Tensor v,
                                             std::optional<Tensor> v_ext, Tensor csr,
                                             Tensor csr_mem, int64_t dst_end, double scale,
                                             double lo, double hi, double eps, int64_t fwd_bytes,
-                                            int64_t bwd_bytes) {
+                                            int64_t bwd_bytes, bool interleave_grads) {
   TORCH_CHECK(csr.device().is_cpu() && csr.scalar_type() == at::kByte &&
                   csr.numel() == static_cast<int64_t>(sizeof(ngt_window_csr)),
               "csr must hold the bytes of one ngt_window_csr (", sizeof(ngt_window_csr), ")");
   auto r = SparseAttention::apply(q, k, v, k_ext, v_ext, csr, csr_mem, dst_end, scale, lo, hi, eps,
-                                  fwd_bytes, bwd_bytes);
+                                  fwd_bytes, bwd_bytes, interleave_grads);
   return {r[0], r[1]};
 }
 
 void init(int64_t fwd, int64_t bwd, int64_t err) {
   g_fwd = reinterpret_cast<decltype(&ngt_sparse_fwd_ext)>(fwd);
-  g_bwd = reinterpret_cast<decltype(&ngt_sparse_bwd_ext)>(bwd);
+  g_bwd = reinterpret_cast<decltype(&ngt_sparse_bwd_strided)>(bwd);
   g_err = reinterpret_cast<decltype(&ngt_last_error)>(err);
 }
 
@@ -190,5 +204,6 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "NGT_ABI_VERSION of the header this extension was compiled against");
   m.def("sparse_attention", &sparse_attention,
         "(q, k, v, k_ext, v_ext, csr, csr_mem, dst_end, scale, lo, hi, eps, fwd_bytes, "
-        "bwd_bytes) -> (out, node_scores)");
+        "bwd_bytes, interleave_grads) -> (out, node_scores); interleave_grads: dQ, dK, dV as "
+        "views of one [N, 3, H, d] buffer (when q and k have the same rows)");
 }

@@ -505,8 +505,9 @@ __device__ __forceinline__ void bwd_kv_packed(
     const T* __restrict__ q, const Keys<T>& kv,
     const T* __restrict__ g, const float2* __restrict__ rd, const int32_t* __restrict__ t_rowptr,
     const int32_t* __restrict__ t_col, int64_t row, int h, int H, float inv_scale, float lo,
-    float hi, T* __restrict__ grad_k, T* __restrict__ grad_v, float* __restrict__ ds,
-    const float* __restrict__ eb, float* __restrict__ deb, const FoldArgs& fa) {
+    float hi, T* __restrict__ grad_k, T* __restrict__ grad_v, int64_t ldg,
+    float* __restrict__ ds, const float* __restrict__ eb, float* __restrict__ deb,
+    const FoldArgs& fa) {
   RowWords<T, DH> krw, vrw;
   float dk[DH], dv[DH];
   load_words<T, DH>(kv.template krow<DH>(row, H, h), krw);
@@ -565,8 +566,8 @@ __device__ __forceinline__ void bwd_kv_packed(
 #pragma unroll
   for (int c = 0; c < DH; ++c) dk[c] *= inv_scale;
   if (row >= kv.n_main) return;  // constant key rows: no gradient
-  store_row<T, DH>(grad_k + (row * H + h) * DH, dk);
-  store_row<T, DH>(grad_v + (row * H + h) * DH, dv);
+  store_row<T, DH>(grad_k + row * ldg + h * DH, dk);
+  store_row<T, DH>(grad_v + row * ldg + h * DH, dv);
 }
 
 // Key-major pass: grad_k, grad_v of key row j and da_e for every edge of j
@@ -578,7 +579,7 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
     const T* __restrict__ g, const float2* __restrict__ rd, const int32_t* __restrict__ t_col,
     const int4* __restrict__ items, int32_t n_items, int32_t n_groups, int32_t hg, int32_t H,
     int32_t L, float inv_scale, float lo, float hi, T* __restrict__ grad_k,
-    T* __restrict__ grad_v, float* __restrict__ ds, float* __restrict__ part_kv,
+    T* __restrict__ grad_v, int64_t ldg, float* __restrict__ ds, float* __restrict__ part_kv,
     const int32_t* __restrict__ t_rowptr, const int32_t* __restrict__ packed, int32_t n_packed,
     int32_t n_pwaves, int32_t xcd, const float* __restrict__ eb, float* __restrict__ deb,
     int32_t row_min, const FoldArgs fa) {
@@ -591,7 +592,7 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
     if (packed_work(gw0 - int64_t(n_items) * n_groups, n_pwaves, n_groups, hg, L, H, packed,
                     n_packed, prow, ph) && prow >= row_min)
       bwd_kv_packed<T, DH, BIAS, NT, FOLD>(q, kv, g, rd, t_rowptr, t_col, prow, ph, H, inv_scale,
-                                           lo, hi, grad_k, grad_v, ds, eb, deb, fa);
+                                           lo, hi, grad_k, grad_v, ldg, ds, eb, deb, fa);
     return;
   }
   int item;
@@ -674,8 +675,8 @@ __global__ __launch_bounds__(kBlock) void k_bwd_kv(
   for (int c = 0; c < DH; ++c) dk[c] *= inv_scale;
   if (it.w < 0) {
     if (row >= kv.n_main) return;  // constant key rows: no gradient
-    store_row<T, DH>(grad_k + (row * H + h) * DH, dk);
-    store_row<T, DH>(grad_v + (row * H + h) * DH, dv);
+    store_row<T, DH>(grad_k + row * ldg + h * DH, dk);
+    store_row<T, DH>(grad_v + row * ldg + h * DH, dv);
   } else {
     float* p = part_kv + (int64_t(it.w) * H + h) * (2 * DH);
     store_f32<DH>(p, dk);
@@ -688,8 +689,9 @@ template <typename T, int DH>
 __device__ __forceinline__ void bwd_kv_finalize_tile(const int4* __restrict__ splits, int32_t H,
                                                      const float* __restrict__ part_kv,
                                                      T* __restrict__ grad_k,
-                                                     T* __restrict__ grad_v, int64_t n_main,
-                                                     int split, int tile, int32_t row_min) {
+                                                     T* __restrict__ grad_v, int64_t ldg,
+                                                     int64_t n_main, int split, int tile,
+                                                     int32_t row_min) {
   __shared__ float red[kWavesPerBlock][kColTile];
   const int4 sp = splits[split];
   if (sp.x >= n_main) return;  // constant key row: no gradient (uniform per block)
@@ -709,7 +711,7 @@ __device__ __forceinline__ void bwd_kv_finalize_tile(const int4* __restrict__ sp
   for (int w = 1; w < kWavesPerBlock; ++w) a += red[w][lane];
   const int h = col / (2 * DH);
   const int c = col - h * 2 * DH;
-  const int64_t at = (int64_t(sp.x) * H + h) * DH;
+  const int64_t at = int64_t(sp.x) * ldg + h * DH;
   if (c < DH)
     elem<T>::store(grad_k + at + c, a);
   else
@@ -746,7 +748,7 @@ __device__ __forceinline__ void bwd_q_packed(const Keys<T, EXT>& kv,
                                              const int32_t* __restrict__ q2t,
                                              const float* __restrict__ ds, int64_t row, int h,
                                              int H, float inv_scale, T* __restrict__ grad_q,
-                                             const RecomputeArgs& rc) {
+                                             int64_t ldg, const RecomputeArgs& rc) {
   float dq[DH];
 #pragma unroll
   for (int c = 0; c < DH; ++c) dq[c] = 0.f;
@@ -796,7 +798,7 @@ __device__ __forceinline__ void bwd_q_packed(const Keys<T, EXT>& kv,
   }
 #pragma unroll
   for (int c = 0; c < DH; ++c) dq[c] *= inv_scale;
-  store_row<T, DH>(grad_q + (row * H + h) * DH, dq);
+  store_row<T, DH>(grad_q + row * ldg + h * DH, dq);
 }
 
 // Query-major pass: grad_q[i] = sum_e da_e k_j / scale.
@@ -805,7 +807,7 @@ __global__ __launch_bounds__(kBlock) void k_bwd_q(
     const Keys<T, EXT> kv, const int32_t* __restrict__ col, const int32_t* __restrict__ q2t,
     const float* __restrict__ ds, const int4* __restrict__ items, int32_t n_items,
     int32_t n_groups, int32_t hg, int32_t H, int32_t L, float inv_scale, T* __restrict__ grad_q,
-    float* __restrict__ part_q, const int32_t* __restrict__ rowptr,
+    int64_t ldg, float* __restrict__ part_q, const int32_t* __restrict__ rowptr,
     const int32_t* __restrict__ packed, int32_t n_packed, int32_t n_pwaves, int32_t q_blocks,
     const int4* __restrict__ splits_k, int32_t kv_tiles, const float* __restrict__ part_kv,
     T* __restrict__ grad_k, T* __restrict__ grad_v, int32_t xcd, const RecomputeArgs rc,
@@ -815,8 +817,8 @@ __global__ __launch_bounds__(kBlock) void k_bwd_q(
   // rides in this launch.
   if (int32_t(blockIdx.x) >= q_blocks) {
     const int f = int(blockIdx.x) - q_blocks;
-    bwd_kv_finalize_tile<T, DH>(splits_k, H, part_kv, grad_k, grad_v, kv.n_main, f / kv_tiles,
-                                f % kv_tiles, kv_row_min);
+    bwd_kv_finalize_tile<T, DH>(splits_k, H, part_kv, grad_k, grad_v, ldg, kv.n_main,
+                                f / kv_tiles, f % kv_tiles, kv_row_min);
     return;
   }
   const int64_t gw0 = virtual_wave(n_items, n_pwaves, n_groups, xcd);
@@ -826,7 +828,8 @@ __global__ __launch_bounds__(kBlock) void k_bwd_q(
     int ph;
     if (packed_work(gw0 - int64_t(n_items) * n_groups, n_pwaves, n_groups, hg, L, H, packed,
                     n_packed, prow, ph))
-      bwd_q_packed<T, DH, EXT, RC>(kv, rowptr, col, q2t, ds, prow, ph, H, inv_scale, grad_q, rc);
+      bwd_q_packed<T, DH, EXT, RC>(kv, rowptr, col, q2t, ds, prow, ph, H, inv_scale, grad_q, ldg,
+                                   rc);
     return;
   }
   int item;
@@ -898,7 +901,7 @@ __global__ __launch_bounds__(kBlock) void k_bwd_q(
 #pragma unroll
   for (int c = 0; c < DH; ++c) dq[c] *= inv_scale;
   if (it.w < 0)
-    store_row<T, DH>(grad_q + (row * H + h) * DH, dq);
+    store_row<T, DH>(grad_q + row * ldg + h * DH, dq);
   else
     store_f32<DH>(part_q + (int64_t(it.w) * H + h) * DH, dq);
 }
@@ -907,7 +910,7 @@ template <typename T, int DH>
 __global__ __launch_bounds__(kBlock) void k_bwd_q_finalize(const int4* __restrict__ splits,
                                                            int32_t H,
                                                            const float* __restrict__ part_q,
-                                                           T* __restrict__ grad_q) {
+                                                           T* __restrict__ grad_q, int64_t ldg) {
   __shared__ float red[kWavesPerBlock][kColTile];
   const int4 sp = splits[blockIdx.x];
   const int lane = threadIdx.x & (kWave - 1);
@@ -923,7 +926,7 @@ __global__ __launch_bounds__(kBlock) void k_bwd_q_finalize(const int4* __restric
   if (wave != 0 || !ok) return;
 #pragma unroll
   for (int w = 1; w < kWavesPerBlock; ++w) a += red[w][lane];
-  elem<T>::store(grad_q + int64_t(sp.x) * ncols + col, a);
+  elem<T>::store(grad_q + int64_t(sp.x) * ldg + col, a);
 }
 
 // ------------------------------------------------------ tiled (dense windows)
@@ -1806,9 +1809,10 @@ int launch_bwd_tiled(const ngt_window_csr* c, const TilePlan& tp, const void* q,
                          static_cast<const T*>(q), make_keys<T, DH>(k, v, k_ext, v_ext, n_main, H),
                          static_cast<const T*>(g), rd, c->t_col,
                          reinterpret_cast<const int4*>(c->items_k), c->n_items_k, groups, hg, H,
-                         L, inv_scale, lo, hi, static_cast<T*>(gk), static_cast<T*>(gv), nullptr,
-                         part_kv, c->t_rowptr, c->packed_k, c->n_packed_k, pw_k, xcd, nullptr,
-                         nullptr, rows_k, FoldArgs{nullptr, nullptr});
+                         L, inv_scale, lo, hi, static_cast<T*>(gk), static_cast<T*>(gv),
+                         int64_t(H) * DH, nullptr, part_kv, c->t_rowptr, c->packed_k,
+                         c->n_packed_k, pw_k, xcd, nullptr, nullptr, rows_k,
+                         FoldArgs{nullptr, nullptr});
       NGT_HIP_CHECK(hipGetLastError());
     }
   }
@@ -1840,7 +1844,8 @@ int launch_bwd_tiled(const ngt_window_csr* c, const TilePlan& tp, const void* q,
     hipLaunchKernelGGL((k_bwd_q<T, DH, false, false>), dim3(unsigned(fin_rest)), dim3(kBlock), 0,
                        st, make_keys<T, DH, false>(k, v, k_ext, v_ext, n_main, H), c->col, c->q2t,
                        nullptr, reinterpret_cast<const int4*>(c->items_q), 0, 1, H, H, 1, inv_scale,
-                       static_cast<T*>(gq), nullptr, c->rowptr, c->packed_q, 0, 0, 0,
+                       static_cast<T*>(gq), int64_t(H) * DH, nullptr, c->rowptr, c->packed_q, 0, 0,
+                       0,
                        reinterpret_cast<const int4*>(c->splits_k), kv_tiles, part_kv,
                        static_cast<T*>(gk), static_cast<T*>(gv), 0, none, rows_k);
     NGT_HIP_CHECK(hipGetLastError());
@@ -1863,8 +1868,8 @@ template <typename T, int DH>
 int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void* v,
                const void* k_ext, const void* v_ext, int64_t n_main, const void* out,
                const void* g, const float* rinv, int H, float inv_scale, float lo, float hi,
-               void* gq, void* gk, void* gv, char* ws, hipStream_t st, const float* eb,
-               float* deb) {
+               void* gq, void* gk, void* gv, int64_t ldg, char* ws, hipStream_t st,
+               const float* eb, float* deb) {
   const BwdLayout lay = bwd_layout(c, H, DH);
   float2* rd = reinterpret_cast<float2*>(ws + lay.rd);
   float* ds = reinterpret_cast<float*>(ws + lay.ds);
@@ -1881,7 +1886,7 @@ int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void
                        static_cast<const T*>(out), static_cast<const T*>(g), rinv, nrh, rd);
     NGT_HIP_CHECK(hipGetLastError());
   }
-  if (rc) {  // the tiled passes recompute each edge's da in the dQ pass
+  if (rc && ldg == int64_t(H) * DH) {  // the tiled passes recompute each edge's da in the dQ pass
     const TilePlan tp = tile_plan(c, H, DH);
     if (tp.on)
       return launch_bwd_tiled<T, DH>(c, tp, q, k, v, k_ext, v_ext, n_main, g, rd, H, inv_scale,
@@ -1904,7 +1909,7 @@ int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void
                          static_cast<const T*>(q), make_keys<T, DH>(k, v, k_ext, v_ext, n_main, H),
                          static_cast<const T*>(g), rd, c->t_col,
                          reinterpret_cast<const int4*>(c->items_k), c->n_items_k, groups, hg, H,
-                         L, inv_scale, lo, hi, static_cast<T*>(gk), static_cast<T*>(gv),
+                         L, inv_scale, lo, hi, static_cast<T*>(gk), static_cast<T*>(gv), ldg,
                          rc ? nullptr : ds, part_kv, c->t_rowptr, c->packed_k, c->n_packed_k,
                          pw_k, xcd, eb, deb, 0, fa);
     };
@@ -1938,7 +1943,7 @@ int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void
       hipLaunchKernelGGL((k_bwd_q<T, DH, E, R>), dim3(unsigned(q_blocks + fin_blocks)), dim3(kBlock),
                          0, st, make_keys<T, DH, E>(k, v, k_ext, v_ext, n_main, H), c->col, c->q2t, ds,
                          reinterpret_cast<const int4*>(c->items_q), c->n_items_q, groups, hg, H,
-                         L, inv_scale, static_cast<T*>(gq), part_q, c->rowptr, c->packed_q,
+                         L, inv_scale, static_cast<T*>(gq), ldg, part_q, c->rowptr, c->packed_q,
                          c->n_packed_q, pw_q, int32_t(q_blocks),
                          reinterpret_cast<const int4*>(c->splits_k), kv_tiles, part_kv,
                          static_cast<T*>(gk), static_cast<T*>(gv), xcd, rca, 0);
@@ -1958,7 +1963,7 @@ int launch_bwd(const ngt_window_csr* c, const void* q, const void* k, const void
     dim3 grid(c->n_splits_q, (H * DH + kColTile - 1) / kColTile);
     hipLaunchKernelGGL((k_bwd_q_finalize<T, DH>), grid, dim3(kBlock), 0, st,
                        reinterpret_cast<const int4*>(c->splits_q), H, part_q,
-                       static_cast<T*>(gq));
+                       static_cast<T*>(gq), ldg);
     NGT_HIP_CHECK(hipGetLastError());
   }
   return NGT_OK;
@@ -2144,10 +2149,21 @@ static int sparse_bwd(int dtype, const void* q, const void* k, const void* v, co
                       const float* rinv, const ngt_window_csr* csr, int32_t n_heads,
                       int32_t head_dim, float scale, float clamp_lo, float clamp_hi,
                       const float* edge_bias_t, float* grad_edge_bias_t, void* grad_q,
-                      void* grad_k, void* grad_v, void* workspace, size_t workspace_bytes,
-                      void* stream) {
+                      void* grad_k, void* grad_v, int64_t grad_row_stride, void* workspace,
+                      size_t workspace_bytes, void* stream) {
   int rc = check_common("ngt_sparse_bwd", dtype, csr, n_heads, head_dim);
   if (rc != NGT_OK) return rc;
+  const int64_t row_elems = int64_t(n_heads) * head_dim;
+  const int64_t ldg = grad_row_stride == 0 ? row_elems : grad_row_stride;
+  const int64_t esize = dtype == NGT_F32 ? 4 : 2;
+  if (ldg < row_elems || (ldg * esize) % 16)
+    return set_error(NGT_ERR_ARG,
+                     "ngt_sparse_bwd: gradient row stride %lld elements (at least %lld, a "
+                     "multiple of 16 bytes)",
+                     static_cast<long long>(ldg), static_cast<long long>(row_elems));
+  if ((reinterpret_cast<uintptr_t>(grad_q) | reinterpret_cast<uintptr_t>(grad_k) |
+       reinterpret_cast<uintptr_t>(grad_v)) & 15)
+    return set_error(NGT_ERR_ARG, "ngt_sparse_bwd: gradients must be 16-byte aligned");
   if (!(scale > 0.f)) return set_error(NGT_ERR_ARG, "ngt_sparse_bwd: scale must be > 0");
   if (csr->n_q > 0 && (!q || !out || !grad_out || !rinv || !grad_q))
     return set_error(NGT_ERR_ARG, "ngt_sparse_bwd: null query-side pointer");
@@ -2163,7 +2179,7 @@ static int sparse_bwd(int dtype, const void* q, const void* k, const void* v, co
                      need);
   return dispatch<BwdOp>(dtype, head_dim, csr, q, k, v, k_ext, v_ext, int64_t(n_k_main), out,
                          grad_out, rinv, int(n_heads), 1.0f / scale, clamp_lo, clamp_hi, grad_q,
-                         grad_k, grad_v, static_cast<char*>(workspace),
+                         grad_k, grad_v, ldg, static_cast<char*>(workspace),
                          static_cast<hipStream_t>(stream), edge_bias_t, grad_edge_bias_t);
 }
 
@@ -2176,7 +2192,20 @@ extern "C" int ngt_sparse_bwd_ext(int dtype, const void* q, const void* k, const
                                   size_t workspace_bytes, void* stream) {
   return sparse_bwd(dtype, q, k, v, k_ext, v_ext, n_k_main, out, grad_out, rinv, csr, n_heads,
                     head_dim, scale, clamp_lo, clamp_hi, nullptr, nullptr, grad_q, grad_k,
-                    grad_v, workspace, workspace_bytes, stream);
+                    grad_v, 0, workspace, workspace_bytes, stream);
+}
+
+extern "C" int ngt_sparse_bwd_strided(int dtype, const void* q, const void* k, const void* v,
+                                      const void* k_ext, const void* v_ext, int32_t n_k_main,
+                                      const void* out, const void* grad_out, const float* rinv,
+                                      const ngt_window_csr* csr, int32_t n_heads,
+                                      int32_t head_dim, float scale, float clamp_lo,
+                                      float clamp_hi, void* grad_q, void* grad_k, void* grad_v,
+                                      int64_t grad_row_stride, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+  return sparse_bwd(dtype, q, k, v, k_ext, v_ext, n_k_main, out, grad_out, rinv, csr, n_heads,
+                    head_dim, scale, clamp_lo, clamp_hi, nullptr, nullptr, grad_q, grad_k,
+                    grad_v, grad_row_stride, workspace, workspace_bytes, stream);
 }
 
 extern "C" int ngt_sparse_bwd_bias(int dtype, const void* q, const void* k, const void* v,
@@ -2192,7 +2221,7 @@ extern "C" int ngt_sparse_bwd_bias(int dtype, const void* q, const void* k, cons
   const bool any = csr && csr->n_edges > 0;
   return sparse_bwd(dtype, q, k, v, k_ext, v_ext, n_k_main, out, grad_out, rinv, csr, n_heads,
                     head_dim, scale, clamp_lo, clamp_hi, any ? edge_bias_t : nullptr,
-                    any ? grad_edge_bias_t : nullptr, grad_q, grad_k, grad_v, workspace,
+                    any ? grad_edge_bias_t : nullptr, grad_q, grad_k, grad_v, 0, workspace,
                     workspace_bytes, stream);
 }
 

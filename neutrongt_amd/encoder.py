@@ -43,7 +43,7 @@ import torch.nn.functional as F
 
 from .attention import CoreAttention
 from .layernorm import FusedLayerNorm, add_dropout_layernorm
-from .linear import WgradLinear, project
+from .linear import WgradLinear, groupable, project
 
 
 def init_params(module: nn.Module, n_layers: int) -> None:
@@ -93,10 +93,16 @@ class _Attention(nn.Module):
     def attend(self, x, edge_index, attn_type, kv_cache):
         b, n, _ = x.shape
         H, d = self.num_heads, self.att_size
-        q, k, v = project(x, self.linear_q, self.linear_k, self.linear_v)
+        lins = (self.linear_q, self.linear_k, self.linear_v)
+        # one projection node, and the sparse core hands back dQ, dK, dV as
+        # column blocks of one matrix for its backward
+        interleave = (groupable(x, *lins) and attn_type == "sparse"
+                      and isinstance(self.local_attn, CoreAttention))
+        extra = {"interleave_grads": True} if interleave else {}
+        q, k, v = project(x, *lins)
         q, k, v = q.view(b, n, H, d), k.view(b, n, H, d), v.view(b, n, H, d)
         if kv_cache is None:
-            y, score = self.local_attn(q, k, v, None, edge_index, attn_type)
+            y, score = self.local_attn(q, k, v, None, edge_index, attn_type, **extra)
             return y, score, [k, v]
         k_r, v_r = kv_cache
         if k_r.shape != v_r.shape or tuple(k_r.shape[1:]) != (H, d):
@@ -105,7 +111,8 @@ class _Attention(nn.Module):
         k_r, v_r = k_r.detach().to(k.dtype), v_r.detach().to(v.dtype)
         if isinstance(self.local_attn, CoreAttention):
             # read from the cache's own buffers: no concatenation, no gradient
-            y, score = self.local_attn(q, k, v, None, edge_index, attn_type, kv_ext=(k_r, v_r))
+            y, score = self.local_attn(q, k, v, None, edge_index, attn_type, kv_ext=(k_r, v_r),
+                                       **extra)
         else:  # another core (e.g. the reference's) takes the concatenated keys
             y, score = self.local_attn(q, torch.cat([k, k_r.unsqueeze(0)], dim=1),
                                        torch.cat([v, v_r.unsqueeze(0)], dim=1), None,

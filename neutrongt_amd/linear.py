@@ -97,14 +97,44 @@ class _WgradLinearFn(torch.autograd.Function):
         return gx, dw, db
 
 
+def _joint_rows(gys, n_out: int):
+    """The [M, len(gys) * n_out] bf16 matrix whose column blocks are the
+    gradients gys, when they are views of one buffer laid out that way (the
+    attention core's interleaved dQ/dK/dV); else None."""
+    if len(gys) < 2 or any(g is None for g in gys):
+        return None
+    g0 = gys[0]
+    if g0.dtype != torch.bfloat16 or any(g.shape != g0.shape or g.dtype != g0.dtype for g in gys):
+        return None
+    width = n_out * len(gys)
+    try:
+        rows = [g.view(-1, n_out) for g in gys]
+    except RuntimeError:
+        return None
+    es = g0.element_size()
+    base = g0.untyped_storage().data_ptr()
+    for i, r in enumerate(rows):
+        if (r.stride() != (width, 1) or r.data_ptr() != g0.data_ptr() + i * n_out * es
+                or r.untyped_storage().data_ptr() != base):
+            return None
+    m = rows[0].shape[0]
+    if (g0.storage_offset() + m * width) * es > g0.untyped_storage().nbytes():
+        return None
+    return torch.as_strided(g0, (m, width), (width, 1))
+
+
 class _ProjectionGroupFn(torch.autograd.Function):
     """Several projections of one input, y_i = x W_i^T + b_i, as one node.
 
-    Forward: one GEMM per projection, as ``_WgradLinearFn``.  Backward: dX is
-    accumulated by the GEMMs themselves (dX = dY_0 W_0, then dX += dY_i W_i
-    with the library's beta = 1), where separate nodes would leave autograd to
-    add their bf16 dX tensors with elementwise kernels (two extra passes over
-    a [32,768 x 768] tensor for Q/K/V).  dW and db as ``_WgradLinearFn``."""
+    Forward: one GEMM per projection, as ``_WgradLinearFn``.  Backward: when
+    the output gradients are column blocks of one [M, k * n_out] matrix (the
+    attention core's interleaved dQ/dK/dV), one GEMM each for dX (against the
+    stacked weights), dW (split-K, fp32) and db (one column sum).  Otherwise
+    dX is accumulated by the GEMMs themselves (dX = dY_0 W_0, then dX +=
+    dY_i W_i with the library's beta = 1), where separate nodes would leave
+    autograd to add their bf16 dX tensors with elementwise kernels (two extra
+    passes over a [32,768 x 768] tensor for Q/K/V); dW and db per projection
+    as ``_WgradLinearFn``."""
 
     @staticmethod
     def forward(ctx, x, *params):
@@ -125,6 +155,24 @@ class _ProjectionGroupFn(torch.autograd.Function):
     def backward(ctx, *gys):
         x16, *ws = ctx.saved_tensors
         n_in = x16.shape[-1]
+        n_out = ws[0].shape[0]
+        joint = None
+        if (all(w.shape[0] == n_out for w in ws) and all(ctx.needs_input_grad[1::2])
+                and (all(ctx.has_bias) and all(ctx.needs_input_grad[2::2])
+                     or not any(ctx.has_bias))):
+            joint = _joint_rows(gys, n_out)
+        if joint is not None:
+            gx = None
+            if ctx.needs_input_grad[0]:
+                with torch.autocast("cuda", enabled=False):
+                    gx = (joint @ torch.cat(ws, 0)).view(*x16.shape)
+            dw = weight_grad(x16.reshape(-1, n_in).contiguous(), joint)
+            db = colsum_bf16(joint) if ctx.has_bias[0] else None
+            grads = []
+            for i in range(len(ws)):
+                grads += [dw[i * n_out:(i + 1) * n_out],
+                          db[i * n_out:(i + 1) * n_out] if db is not None else None]
+            return (gx, *grads)
         x2 = None
         gx = None
         grads = []
@@ -158,11 +206,17 @@ def _fast_path(lin: nn.Linear, x: torch.Tensor) -> bool:
             and torch.get_autocast_dtype("cuda") == torch.bfloat16)
 
 
+def groupable(x: torch.Tensor, *lins: nn.Linear) -> bool:
+    """Whether project(x, *lins) runs them as one node."""
+    return len(lins) > 1 and all(isinstance(l, WgradLinear) and _fast_path(l, x) for l in lins)
+
+
 def project(x: torch.Tensor, *lins: nn.Linear):
     """(lin(x) for lin in lins), with the backward's dX summed inside the
-    GEMMs when all of them take the bf16 autocast path; otherwise each
-    module's own forward."""
-    if len(lins) > 1 and all(isinstance(l, WgradLinear) and _fast_path(l, x) for l in lins):
+    GEMMs (and, for gradients that arrive as column blocks of one matrix, dW
+    and db as one GEMM and one column sum) when all of them take the bf16
+    autocast path; otherwise each module's own forward."""
+    if groupable(x, *lins):
         params = []
         for l in lins:
             params += [l.weight, l.bias]

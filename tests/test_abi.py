@@ -97,6 +97,25 @@ def test_argument_errors_are_reported_without_touching_the_gpu():
         _lib.check(1)
 
 
+def test_strided_backward_validates_its_row_stride_without_touching_the_gpu():
+    """ngt_sparse_bwd_strided: the gradients' row stride is at least H * d and
+    a multiple of 16 bytes, and the gradients 16-byte aligned; anything else
+    is refused before a launch."""
+    lib = _lib.load()
+    s = _lib.WindowCSR()  # empty window: nothing would launch anyway
+    args = lambda dtype, ld, gq=None: (dtype, None, None, None, None, None, 0, None, None, None,
+                                       C.byref(s), 8, 16, 4.0, -5.0, 5.0, gq, None, None, ld,
+                                       None, 0, None)
+    assert lib.ngt_sparse_bwd_strided(*args(1, 127)) == 1  # below H * d = 128
+    assert b"row stride" in lib.ngt_last_error()
+    assert lib.ngt_sparse_bwd_strided(*args(1, 132)) == 1  # 264 bytes: not a multiple of 16
+    assert lib.ngt_sparse_bwd_strided(*args(0, 132)) == 0  # 528 bytes in fp32
+    assert lib.ngt_sparse_bwd_strided(*args(1, 0)) == 0    # 0: contiguous rows
+    assert lib.ngt_sparse_bwd_strided(*args(1, 384)) == 0  # [N, 3, H, d]
+    assert lib.ngt_sparse_bwd_strided(*args(1, 384, 8)) == 1
+    assert b"16-byte aligned" in lib.ngt_last_error()
+
+
 def test_colsum_takes_any_width():
     """Column sums of any width (a 47-class readout's bias gradient): one fp32
     partial per 256-row chunk and column; zero columns refused."""

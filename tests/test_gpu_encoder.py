@@ -295,3 +295,49 @@ def test_state_dict_names_follow_the_reference():
             "layers.0.FFN_layer2.bias", "layers.0.layer_norm2.bias",
             "MLP_layer.FC_layers.0.weight", "MLP_layer.FC_layers.2.bias"} <= t
     assert WindowGT(1, 2, 4, 8, 3).layers[0].FFN_layer1.out_features == 16
+
+
+@pytest.mark.parametrize("family", ["graphormer", "gt"])
+def test_qkv_backward_takes_the_interleaved_gradients(monkeypatch, family):
+    """Under bf16 autocast each layer's Q/K/V projections run as one node and
+    the sparse core hands back dQ, dK, dV as column blocks of one matrix, so
+    the projections' backward runs on it (one dX GEMM, one dW GEMM, one
+    column sum per layer); the gradients match the same model with that hand
+    over turned off (the projections then sum dX with addmm): the last
+    layer's Q/K/V weight and bias gradients within fp32 accumulation (same
+    bf16 products), the rest within the bf16 tolerance."""
+    import neutrongt_amd.linear as L
+    from neutrongt_amd.attention import CoreAttention
+    model, _, x, ei, cache, labels, mask = _build(seed=5, family=family)
+    dev = torch.device("cuda")
+    model = model.to(dev)
+    cache_bf = [tuple(t.to(torch.bfloat16).to(dev) for t in c) for c in cache]
+    args = (x.to(dev), ei.to(dev), cache_bf, labels.to(dev), mask.to(dev))
+    seen = []
+    orig = L._joint_rows
+
+    def spy(gys, n_out):
+        r = orig(gys, n_out)
+        seen.append(r is not None)
+        return r
+
+    monkeypatch.setattr(L, "_joint_rows", spy)
+    joint = _run(model, *args, autocast=torch.bfloat16)
+    assert seen == [True, True], seen  # both layers
+    fwd = CoreAttention.forward
+
+    def no_interleave(self, *a, **kw):
+        kw.pop("interleave_grads", None)
+        return fwd(self, *a, **kw)
+
+    monkeypatch.setattr(CoreAttention, "forward", no_interleave)
+    seen.clear()
+    sep = _run(model, *args, autocast=torch.bfloat16)
+    assert seen == [False, False], seen
+    assert torch.equal(joint[0], sep[0])  # same forward
+    last = f"layers.{len(model.layers) - 1}.self_attention.linear_"
+    for n in joint[3]:
+        if n.startswith(last):
+            assert relerr(joint[3][n], sep[3][n]) < 1e-5, n
+        else:
+            assert_close(joint[3][n], sep[3][n], torch.bfloat16, f"grad {n}")

@@ -153,3 +153,36 @@ def test_projection_group_without_input_grad():
     x16 = x.to(torch.bfloat16).double()
     for m in mods:
         assert relerr(m.weight.grad, torch.ones(700, 64, dtype=torch.float64, device="cuda").T @ x16) < 1e-5
+
+
+@pytest.mark.parametrize("bias", [True, False])
+def test_projection_group_with_interleaved_gradients(bias):
+    """Output gradients that are column blocks of one [M, 3 n] matrix (the
+    sparse core's interleaved dQ/dK/dV) take the stacked path: dX one GEMM
+    against the stacked weights, dW one split-K GEMM, db one column sum --
+    dW/db as float64 products, dX as close to the float64 sum as the
+    separate path, and both paths' dW/db within fp32 accumulation."""
+    from neutrongt_amd.linear import _joint_rows, project
+    _say(f"case projection group, interleaved gradients bias={bias}")
+    torch.manual_seed(3)
+    n_in, n_out, m = 128, 96, 6000
+    mods = [WgradLinear(n_in, n_out, bias=bias).cuda() for _ in range(3)]
+    x = torch.randn(1, m, n_in, device="cuda", requires_grad=True)
+    buf = torch.randn(m, 3, n_out, device="cuda").to(torch.bfloat16)
+    gys = [buf[:, i].view(1, m, n_out) for i in range(3)]
+    assert _joint_rows(gys, n_out) is not None
+    assert _joint_rows([g.clone() for g in gys], n_out) is None  # separate buffers
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        ys = project(x, *mods)
+    torch.autograd.backward(ys, gys)
+    x16 = x.detach().to(torch.bfloat16).reshape(-1, n_in).double()
+    g64 = [buf[:, i].double() for i in range(3)]
+    exact = sum(g @ mod.weight.detach().to(torch.bfloat16).double() for g, mod in zip(g64, mods))
+    assert relerr(x.grad.reshape(-1, n_in), exact) < 8e-3
+    for g, mod in zip(g64, mods):
+        assert mod.weight.grad.shape == (n_out, n_in) and mod.weight.grad.is_contiguous()
+        assert relerr(mod.weight.grad, g.T @ x16) < 1e-5
+        if bias:
+            assert relerr(mod.bias.grad, g.sum(0)) < 1e-5
+        else:
+            assert mod.bias is None
