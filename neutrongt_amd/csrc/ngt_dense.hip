@@ -33,13 +33,14 @@ namespace ngt {
 bool mfma_dense_supported(int d);
 MfSplit mfma_fwd_split(int n_q, int n_k, int H, bool node_scores);
 MfSplit mfma_dq_split(int n_q, int n_k, int H);
+int mfma_fused_blocks(int n_q, int n_k, int H, int d);
 int mfma_dense_fwd(int d, const void* q, const void* k, const void* v, int n_q, int n_k, int H,
                    float scale, const DropoutMask* dm, void* out, float* out32, float* lse,
                    float* part, MfSplit sp, float* part_ml, float* part_acc, hipStream_t st);
 int mfma_dense_bwd(int d, const void* q, const void* k, const void* v, const void* g,
                    const void* out, const float* out32, const float* lse, float* dsum, int n_q,
                    int n_k, int H, float scale, const DropoutMask* dm, void* gq, void* gk, void* gv,
-                   MfSplit sq, float* part_dq, hipStream_t st);
+                   MfSplit sq, float* part_dq, int fused_blocks, hipStream_t st);
 
 namespace {
 
@@ -920,13 +921,16 @@ size_t fwd_need(int dtype, int32_t n_q, int32_t n_k, int32_t H, int32_t d, bool 
   return node_scores || key_split(n_q, n_k, H).n_split > 1 ? fwd_ws(n_q, n_k, H, d) : 0;
 }
 
-// Backward workspace: D_i [n_q, H] fp32, and on the matrix-core path the key
-// splits' partial dQ after it.
+// Backward workspace: D_i [n_q, H] fp32, and on the matrix-core path after it
+// the key splits' partial dQ (two passes) or the key blocks' partial dQ
+// (single pass).
 size_t bwd_need(int dtype, int32_t n_q, int32_t n_k, int32_t H, int32_t d) {
   size_t need = bwd_ws(n_q, H);
   if (use_mfma(dtype, d) && n_q > 0) {
+    const int fb = mfma_fused_blocks(n_q, n_k, H, d);
     const MfSplit sq = mfma_dq_split(n_q, n_k, H);
-    if (sq.n_split > 1) need += align256(size_t(sq.n_split) * n_q * H * d * 4);
+    const int parts = fb > 0 ? fb : (sq.n_split > 1 ? sq.n_split : 0);
+    if (parts > 0) need += align256(size_t(parts) * n_q * H * d * 4);
   }
   return need;
 }
@@ -1042,11 +1046,12 @@ extern "C" int ngt_dense_bwd(int dtype, const void* q, const void* k, const void
   if (use_mfma(dtype, head_dim)) {
     float* dsum = static_cast<float*>(workspace);  // written by the dQ pass
     const MfSplit sq = n_q > 0 ? mfma_dq_split(n_q, n_k, n_heads) : MfSplit{1, 1};
-    float* part_dq = sq.n_split > 1
+    const int fb = mfma_fused_blocks(n_q, n_k, n_heads, head_dim);
+    float* part_dq = sq.n_split > 1 || fb > 0
                          ? reinterpret_cast<float*>(static_cast<char*>(workspace) + bwd_ws(n_q, n_heads))
                          : nullptr;
     return mfma_dense_bwd(head_dim, q, k, v, grad_out, out, out_f32, lse, dsum, n_q, n_k,
-                          n_heads, scale, dm, grad_q, grad_k, grad_v, sq, part_dq, st);
+                          n_heads, scale, dm, grad_q, grad_k, grad_v, sq, part_dq, fb, st);
   }
   return dispatch<BwdOp>(dtype, head_dim, q, k, v, out, out_f32, grad_out, lse, int(n_q), int(n_k),
                          int(n_heads), scale, dm, grad_q, grad_k, grad_v,

@@ -699,6 +699,256 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_kv(
   }
 }
 
+// D[h][q] = sum_c G[q][h][c] o[q][h][c] (o the forward's fp32 output when
+// it kept one, else the bf16 output), one thread per (query, head), with
+// k_mf_bwd_q's arithmetic: each half's 4-column groups j = 0 .. NC-1 as one
+// fmaf chain, then the two halves' sums added.  The single-pass backward
+// reads it as k_mf_bwd_kv does.
+template <int DH>
+__global__ __launch_bounds__(kBlock) void k_mf_dsum(const bf16_t* __restrict__ g,
+                                                    const bf16_t* __restrict__ out,
+                                                    const float* __restrict__ out32, int32_t n_q,
+                                                    int32_t H, float* __restrict__ dsum) {
+  constexpr int NC = DH / 8;
+  const int64_t t = int64_t(wg_x()) * kBlock + tid_x();
+  if (t >= int64_t(n_q) * H) return;
+  const int64_t qi = t / H;
+  const int h = int(t - qi * H);
+  const int64_t row = (qi * H + h) * DH;
+  float part[2];
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    float a = 0.f;
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      const int64_t o = row + 8 * j + 4 * half;
+      const s16x4 gb = load4(g + o);
+      float ov[4];
+      if (out32) {
+        const float4 f = *reinterpret_cast<const float4*>(out32 + o);
+        ov[0] = f.x, ov[1] = f.y, ov[2] = f.z, ov[3] = f.w;
+      } else {
+        const s16x4 ob = load4(out + o);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ov[i] = bf16_to_f32(static_cast<uint16_t>(ob[i]));
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a = fmaf(bf16_to_f32(static_cast<uint16_t>(gb[i])), ov[i], a);
+    }
+    part[half] = a;
+  }
+  dsum[int64_t(h) * n_q + qi] = part[0] + part[1];
+}
+
+// Single-pass backward, key-major: dK and dV as k_mf_bwd_kv, and each score
+// tile's dS, already packed to bf16 for dK, is also contracted with the
+// wave's own K rows into a partial dQ, so the exponentials are computed once
+// instead of once per pass.  dS crosses lanes through a wave-private LDS tile
+// (written one key per lane, read one query per lane as the MFMA's A
+// operand).  Within a block the 4 waves' partials of a query sub-tile are
+// added in a fixed order: in step t of a stage, wave w takes sub-tile
+// (w + t) mod 4, so each step's waves touch distinct sub-tiles, and sub-tile
+// s collects waves s, s-1, s-2, s-3 (mod 4) in that order as the accumulator
+// input of their MFMAs, a block barrier between steps.  At the end of a stage
+// the block's partial dQ over its 128 keys goes to part_dq[block][q][h][c];
+// k_mf_dq_combine adds the blocks' partials in block order.
+constexpr int kTrPad = 4;  // shorts: rows of 72 bytes
+template <int DH, bool DROP>
+__global__ __launch_bounds__(kBlock) void k_mf_bwd_fused(
+    const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
+    const bf16_t* __restrict__ g, const float* __restrict__ lse, const float* __restrict__ dsum,
+    int32_t n_q, int32_t n_k, int32_t H, float scale, DropoutMask dm,
+    bf16_t* __restrict__ grad_k, bf16_t* __restrict__ grad_v, float* __restrict__ part_dq) {
+  constexpr int NC = DH / 8;
+  constexpr int kSubs = kSB / kT;  // query sub-tiles per stage (= waves per block)
+  static_assert(kSubs == kWaves, "one sub-tile per wave and step");
+  __shared__ __align__(16) short qs[kSB][DH + kRowPad];
+  __shared__ __align__(16) short gs[kSB][DH + kRowPad];
+  __shared__ __align__(16) short qt[kT][kSB + kColPad];  // rows >= DH zero
+  __shared__ __align__(16) short gt[kT][kSB + kColPad];
+  __shared__ __align__(16) uint2 xr[2][kSB];
+  __shared__ __align__(16) float dd[kSB];               // -D, with dropout only
+  __shared__ __align__(16) short tr[kWaves][kT][kT + kTrPad];  // a wave's dS tile, [q][key]
+  // the stage's partial dQ per sub-tile in the MFMA's D layout of the lanes
+  // that hold columns c < DH: [sub][half][c][16 rows]
+  __shared__ __align__(16) float red[kSubs][2][DH][16];
+  const int lane = tid_x() & (kWave - 1);
+  const int wave = tid_x() >> 6;
+  const int half = lane >> 5;
+  const int l32 = lane & 31;
+  const int h = wg_y();
+  const int64_t k0 = int64_t(wg_x()) * kRowsPerBlock + wave * kT;
+  const int64_t kj = k0 + l32;
+  const bool k_ok = kj < n_k;
+  if constexpr (DROP) dm = drop_for_head(dm, h);
+  s16x4 kbv[NC], vbv[NC];  // K^T, V^T as B operands
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    kbv[j] = settle(k_ok ? load4(k + (kj * H + h) * DH + 8 * j + 4 * half) : zero4());
+    vbv[j] = settle(k_ok ? load4(v + (kj * H + h) * DH + 8 * j + 4 * half) : zero4());
+  }
+  // this wave's K rows as the B operand of dQ += dS K: lane (c = l32, half)
+  // holds K[k0 + 8j + 4 half + i][c] (zero for c >= DH and keys past n_k)
+  s16x4 kq[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t key = k0 + 8 * j + 4 * half + i;
+      kq[j][i] = (l32 < DH && key < n_k) ? static_cast<short>(k[(key * H + h) * DH + l32].x)
+                                         : static_cast<short>(0);
+    }
+    kq[j] = settle(kq[j]);
+  }
+  const float s2 = scale * kLog2e;
+  s16x4 khi[NC], klo[NC];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) split_scaled(kbv[j], s2, khi[j], klo[j]);
+  const s16x4 ones_l = ones3(half, 0), ones_d = ones3(half, 1);
+  f32x16 dk = zero16(), dv = zero16();
+  Stage<DH> pq, pg;
+  float pl = 0.f, pd = 0.f;
+  auto prefetch = [&](int qb) {
+    pq.load(q, qb, n_q, H, h);
+    pg.load(g, qb, n_q, H, h);
+    if (tid_x() < kSB) {
+      const bool ok = qb + int(tid_x()) < n_q;
+      pl = ok ? lse[int64_t(h) * n_q + qb + tid_x()] : INFINITY;
+      pd = ok ? dsum[int64_t(h) * n_q + qb + tid_x()] : 0.f;
+    }
+  };
+  fill_pad_rows<DH>(qt, false);
+  fill_pad_rows<DH>(gt, false);
+  short (*T)[kT + kTrPad] = tr[wave];
+  prefetch(0);
+  for (int qb = 0; qb < n_q; qb += kSB) {
+    __syncthreads();
+    pq.store_rows(qs);
+    pg.store_rows(gs);
+    pq.store_trans(qt);
+    pg.store_trans(gt);
+    if (tid_x() < kSB) {
+      const float nl = pl == INFINITY ? -1e30f : -pl * kLog2e;
+      xr[0][tid_x()] = split3(nl);
+      xr[1][tid_x()] = split3(-pd);
+      if constexpr (DROP) dd[tid_x()] = -pd;
+    }
+    __syncthreads();
+    if (qb + kSB < n_q) prefetch(qb + kSB);
+    // not unrolled: unrolled, the steps' operands stay live across them (162 -> 180 VGPRs)
+#pragma unroll 1
+    for (int step = 0; step < kSubs; ++step) {
+      const int sub = (wave + step) & (kSubs - 1);
+      if (qb + sub * kT < n_q) {  // uniform per wave; every wave meets the barrier below
+        const int r0 = sub * kT;
+        const s16x4 xa = __builtin_bit_cast(s16x4, xr[half][r0 + l32]);
+        f32x16 st = zero16(), dp = zero16();
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+          const s16x4 qa = lds4(&qs[r0 + l32][8 * j + 4 * half]);
+          st = mfma2(qa, qa, khi[j], klo[j], st);
+        }
+        st = mfma(xa, ones_l, st);
+#pragma unroll
+        for (int j = 0; j + 1 < NC; j += 2)
+          dp = mfma2(lds4(&gs[r0 + l32][8 * j + 4 * half]),
+                     lds4(&gs[r0 + l32][8 * j + 8 + 4 * half]), vbv[j], vbv[j + 1], dp);
+        if constexpr (DROP) {
+          if constexpr (NC % 2)
+            dp = mfma(lds4(&gs[r0 + l32][8 * (NC - 1) + 4 * half]), vbv[NC - 1], dp);
+        } else if constexpr (NC % 2) {
+          dp = mfma2(lds4(&gs[r0 + l32][8 * (NC - 1) + 4 * half]), xa, vbv[NC - 1], ones_d, dp);
+        } else {
+          dp = mfma(xa, ones_d, dp);
+        }
+        s16x4 pa[4], dsa[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int r = r0 + 8 * j + 4 * half;
+          const float p0 = __builtin_amdgcn_exp2f(st[4 * j]);
+          const float p1 = __builtin_amdgcn_exp2f(st[4 * j + 1]);
+          const float p2 = __builtin_amdgcn_exp2f(st[4 * j + 2]);
+          const float p3 = __builtin_amdgcn_exp2f(st[4 * j + 3]);
+          if constexpr (DROP) {
+            const float4 dv4 = *reinterpret_cast<const float4*>(&dd[r]);  // -D
+            const uint32_t qr = uint32_t(qb + r), kk = uint32_t(kj);
+            const float m0 = drop_scale(dm, drop_word(dm, qr, kk), kk);
+            const float m1 = drop_scale(dm, drop_word(dm, qr + 1, kk), kk);
+            const float m2 = drop_scale(dm, drop_word(dm, qr + 2, kk), kk);
+            const float m3 = drop_scale(dm, drop_word(dm, qr + 3, kk), kk);
+            pa[j] = pack4(p0 * m0, p1 * m1, p2 * m2, p3 * m3);
+            dsa[j] = pack4(p0 * fmaf(m0, dp[4 * j], dv4.x), p1 * fmaf(m1, dp[4 * j + 1], dv4.y),
+                           p2 * fmaf(m2, dp[4 * j + 2], dv4.z), p3 * fmaf(m3, dp[4 * j + 3], dv4.w));
+          } else {
+            pa[j] = pack4(p0, p1, p2, p3);
+            dsa[j] = pack4(p0 * dp[4 * j], p1 * dp[4 * j + 1], p2 * dp[4 * j + 2],
+                           p3 * dp[4 * j + 3]);
+          }
+        }
+        // dS (queries r0 + 8j + 4 half + i, this lane's key) -> T[query][key]
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) T[8 * j + 4 * half + i][l32] = dsa[j][i];
+        s16x4 gb[4], qbq[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int c0 = r0 + 8 * j + 4 * half;
+          gb[j] = lds4(&gt[l32][c0]);
+          qbq[j] = lds4(&qt[l32][c0]);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j += 2) {
+          dv = mfma2(pa[j], pa[j + 1], gb[j], gb[j + 1], dv);
+          dk = mfma2(dsa[j], dsa[j + 1], qbq[j], qbq[j + 1], dk);
+        }
+        // partial dQ of this sub-tile over the wave's keys, on top of the
+        // waves before it: A = dS[query][key] read back from T (a wave's own
+        // LDS writes and reads complete in order), B = kq
+        f32x16 acc = zero16();
+        if (step > 0 && l32 < DH) {
+          const float4* rp = reinterpret_cast<const float4*>(&red[sub][half][l32][0]);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const float4 f = rp[u];
+            acc[4 * u] = f.x, acc[4 * u + 1] = f.y, acc[4 * u + 2] = f.z, acc[4 * u + 3] = f.w;
+          }
+        }
+        s16x4 ta[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ta[j] = lds4(&T[l32][8 * j + 4 * half]);
+        acc = mfma2(ta[0], ta[1], kq[0], kq[1], acc);
+        acc = mfma2(ta[2], ta[3], kq[2], kq[3], acc);
+        if (l32 < DH) {
+          float4* wp = reinterpret_cast<float4*>(&red[sub][half][l32][0]);
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            wp[u] = make_float4(acc[4 * u], acc[4 * u + 1], acc[4 * u + 2], acc[4 * u + 3]);
+        }
+      }
+      __syncthreads();
+    }
+    // the block's partial dQ over its keys for this stage's queries
+    const int nvalid = min(kSB, n_q - qb);
+    float* pz = part_dq + int64_t(wg_x()) * n_q * H * DH;
+    for (int e = tid_x(); e < nvalid * DH; e += kBlock) {
+      const int r = e / DH, c = e - (e / DH) * DH;
+      const int sb = r / kT, rr = r - sb * kT;  // D row rr = 8 (i / 4) + 4 half + i % 4
+      const int hf = (rr >> 2) & 1, i = ((rr >> 3) << 2) | (rr & 3);
+      pz[(int64_t(qb + r) * H + h) * DH + c] = red[sb][hf][c][i];
+    }
+  }
+  if (l32 >= DH) return;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t key = k0 + 8 * (i / 4) + 4 * half + (i % 4);
+    if (key < n_k) {
+      grad_k[(key * H + h) * DH + l32].x = f32_to_bf16(dk[i] * scale);
+      grad_v[(key * H + h) * DH + l32].x = f32_to_bf16(dv[i]);
+    }
+  }
+}
+
 // Query-major: dQ for queries q0 .. q0+31.  S^T, dP^T as D[key][q]; K and V
 // stages of 128 keys in LDS (row-major for the A operands, K^T for dQ += dS K).
 // This pass runs first in the backward and forms each query's
@@ -903,6 +1153,22 @@ MfSplit mfma_dq_split(int n_q, int n_k, int H) {
   return plan_split(n_q, n_k, H, 12288, 0, "NGT_MF_DQ_SPLIT");
 }
 
+// The single-pass backward (k_mf_bwd_fused) or the two passes: the number of
+// 128-key blocks whose partial dQ the backward workspace holds, 0 for the two
+// passes.  Two passes by default: at 16,000 nodes, 8 heads, d = 8 the single
+// pass measured 1,069 us plus a 136 us combine of its 512 MB of partials
+// against 470 + 324 us (162 VGPRs, 3 waves per SIMD, against 114 and 4; four
+// block barriers per stage for the fixed summation order).
+// NGT_DENSE_FUSED=1 turns it on.
+int mfma_fused_blocks(int n_q, int n_k, int H, int d) {
+  (void)H;
+  (void)d;
+  if (n_q <= 0 || n_k < kSB) return 0;
+  bool on = false;
+  if (const char* e = getenv("NGT_DENSE_FUSED")) on = atoi(e) != 0;
+  return on ? (n_k + kRowsPerBlock - 1) / kRowsPerBlock : 0;
+}
+
 template <int DH>
 static int mf_fwd(const void* q, const void* k, const void* v, int n_q, int n_k, int H,
                   float scale, const DropoutMask* dm, void* out, float* out32, float* lse,
@@ -928,6 +1194,50 @@ static int mf_fwd(const void* q, const void* k, const void* v, int n_q, int n_k,
                        static_cast<bf16_t*>(out), out32, lse, sp.split_keys, pml, pacc,
                        sp.n_split, fwd_bx, score_bx, part);
   NGT_HIP_CHECK(hipGetLastError());
+  return NGT_OK;
+}
+
+// The single-pass backward: D, then dK/dV with the blocks' partial dQ, then
+// dQ as the partials' sum in block order.
+template <int DH>
+static int mf_bwd_fused(const void* q, const void* k, const void* v, const void* g,
+                        const void* out, const float* out32, const float* lse, float* dsum,
+                        int n_q, int n_k, int H, float scale, const DropoutMask* dm, void* gq,
+                        void* gk, void* gv, int kv_bx, float* part, hipStream_t st) {
+  {
+    KernelTimer timer_("dense_dsum", st);
+    const int64_t nrh = int64_t(n_q) * H;
+    hipLaunchKernelGGL((k_mf_dsum<DH>), dim3(unsigned((nrh + kBlock - 1) / kBlock)), dim3(kBlock),
+                       0, st, static_cast<const bf16_t*>(g), static_cast<const bf16_t*>(out), out32,
+                       n_q, H, dsum);
+    NGT_HIP_CHECK(hipGetLastError());
+  }
+  {
+    KernelTimer timer_("dense_bwd_fused", st);
+    const DropoutMask m = dm ? *dm : DropoutMask{};
+    const dim3 grid(kv_bx, H);
+    if (dm)
+      hipLaunchKernelGGL((k_mf_bwd_fused<DH, true>), grid, dim3(kBlock), 0, st,
+                         static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
+                         static_cast<const bf16_t*>(v), static_cast<const bf16_t*>(g), lse, dsum,
+                         n_q, n_k, H, scale, m, static_cast<bf16_t*>(gk), static_cast<bf16_t*>(gv),
+                         part);
+    else
+      hipLaunchKernelGGL((k_mf_bwd_fused<DH, false>), grid, dim3(kBlock), 0, st,
+                         static_cast<const bf16_t*>(q), static_cast<const bf16_t*>(k),
+                         static_cast<const bf16_t*>(v), static_cast<const bf16_t*>(g), lse, dsum,
+                         n_q, n_k, H, scale, m, static_cast<bf16_t*>(gk), static_cast<bf16_t*>(gv),
+                         part);
+    NGT_HIP_CHECK(hipGetLastError());
+  }
+  {
+    KernelTimer timer_("dense_dq_combine", st);
+    const int64_t n_dq = int64_t(n_q) * H * DH;
+    const unsigned blocks = unsigned(std::min<int64_t>((n_dq + kBlock - 1) / kBlock, 65536));
+    hipLaunchKernelGGL(k_mf_dq_combine, dim3(blocks), dim3(kBlock), 0, st, part, kv_bx, n_dq,
+                       scale, static_cast<bf16_t*>(gq), int32_t(blocks));
+    NGT_HIP_CHECK(hipGetLastError());
+  }
   return NGT_OK;
 }
 
@@ -1002,9 +1312,12 @@ int mfma_dense_fwd(int d, const void* q, const void* k, const void* v, int n_q, 
 int mfma_dense_bwd(int d, const void* q, const void* k, const void* v, const void* g,
                    const void* out, const float* out32, const float* lse, float* dsum, int n_q,
                    int n_k, int H, float scale, const DropoutMask* dm, void* gq, void* gk, void* gv,
-                   MfSplit sq, float* part_dq, hipStream_t st) {
+                   MfSplit sq, float* part_dq, int fused_blocks, hipStream_t st) {
 #define NGT_MF_BWD(DH)                                                                      \
   case DH:                                                                                  \
+    if (fused_blocks > 0)                                                                   \
+      return mf_bwd_fused<DH>(q, k, v, g, out, out32, lse, dsum, n_q, n_k, H, scale, dm, gq, \
+                              gk, gv, fused_blocks, part_dq, st);                           \
     return mf_bwd<DH>(q, k, v, g, out, out32, lse, dsum, n_q, n_k, H, scale, dm, gq, gk, gv, \
                       sq, part_dq, st);
   switch (d) {

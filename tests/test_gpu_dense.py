@@ -74,6 +74,31 @@ def test_dense_mfma_key_splits(monkeypatch, d, fwd_split, dq_split, p):
         assert_parity(res[name].float(), ref[name], ref64[name], torch.bfloat16, f"split {name}")
 
 
+@pytest.mark.parametrize("d", [8, 16, 24, 32])
+@pytest.mark.parametrize("n_q,n_k,H,p", [(300, 300, 2, 0.0), (77, 1000, 3, 0.0),
+                                         (200, 129, 1, 0.5), (1030, 260, 2, 0.3)])
+def test_dense_single_pass_backward(monkeypatch, d, n_q, n_k, H, p):
+    """The single-pass backward (NGT_DENSE_FUSED=1: dK/dV key-major with each
+    tile's dS also contracted into per-block partial dQ, summed over the key
+    blocks in order): ragged query stages and key blocks, with and without
+    dropout, against the restatement; and bitwise reproducible."""
+    _say(f"case dense single pass d={d} n_q={n_q} n_k={n_k} H={H} p={p}")
+    monkeypatch.setenv("NGT_DENSE_FUSED", "1")
+    q, k, v, go = _qkv(n_q, n_k, H, d, torch.bfloat16, seed=d + n_q)
+    seed = 0x5EED + d
+    run = (lambda: _run_drop(q, k, v, go, p, seed)) if p else (lambda: _run(q, k, v, go))
+    res = run()
+    mult = OA.dropout_multiplier(seed, H, n_q, n_k, p) if p else None
+    ref = OA.full_fwd_bwd(q.float(), k.float(), v.float(), go.float(), dropout_mult=mult)
+    ref64 = OA.full_fwd_bwd(q.double(), k.double(), v.double(), go.double(), dtype=torch.float64,
+                            dropout_mult=mult)
+    for name in ("x", "dq", "dk", "dv"):
+        assert_parity(res[name].float(), ref[name], ref64[name], torch.bfloat16, f"fused {name}")
+    again = run()
+    for name in ("dq", "dk", "dv"):
+        assert torch.equal(res[name], again[name]), name
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("n_q,n_k", [(0, 37), (45, 0)])
 def test_dense_empty_side(n_q, n_k, dtype):
@@ -111,13 +136,15 @@ def test_dense_module_drop_in():
     assert_close(score.cpu(), ref["node_scores"], torch.float32, "score")
 
 
-def test_dense_full_size_sampled_rows_and_invariants():
+@pytest.mark.parametrize("fused", ["0", "1"])
+def test_dense_full_size_sampled_rows_and_invariants(monkeypatch, fused):
     """16,000-node all-pairs window (H=8, d=8, bf16): sampled query rows and
     sampled key rows (dK, dV) against float64 formulas, column scores against a
     chunked CPU sum, and the size-independent identities <dQ,Q> = <dK,K>,
-    sum_j dV_j = sum_i G_i."""
+    sum_j dV_j = sum_i G_i; with the two-pass and the single-pass backward."""
+    monkeypatch.setenv("NGT_DENSE_FUSED", fused)
     cfg = S.CONFIGS["dense_slim"]
-    _say(f"case dense full-size n={cfg.n_q}")
+    _say(f"case dense full-size n={cfg.n_q} fused={fused}")
     q, k, v, go = S.make_qkv(cfg, cfg.n_q)
     res = _run(q, k, v, go)
     n, H, d = cfg.n_q, cfg.n_heads, cfg.head_dim
