@@ -341,3 +341,45 @@ def test_qkv_backward_takes_the_interleaved_gradients(monkeypatch, family):
             assert relerr(joint[3][n], sep[3][n]) < 1e-5, n
         else:
             assert_close(joint[3][n], sep[3][n], torch.bfloat16, f"grad {n}")
+
+
+@pytest.mark.parametrize("family", ["graphormer", "gt"])
+def test_window_step_graph_replays_follow_the_weights(family):
+    """The whole window step (forward, loss, backward, AdamW) captured in one
+    HIP graph (as bench.py --model --graph runs it): each replay reads the
+    weights the previous replay's optimizer step wrote, so replays and eager
+    steps of an identical model give the same losses and parameters, bit for
+    bit."""
+    from neutrongt_amd.encoder import window_step
+    dev = torch.device("cuda")
+    models = []
+    for _ in range(2):
+        m, _, x, ei, cache, labels, mask = _build(seed=9, family=family)
+        for mod in m.modules():  # no dropout: the two runs draw no random numbers
+            if isinstance(mod, nn.Dropout):
+                mod.p = 0.0
+        models.append(m.to(dev))
+    xs, eis, ls, ms = x.to(dev), ei.to(dev), labels.to(dev), mask.to(dev)
+    cs = [tuple(t.to(torch.bfloat16).to(dev) for t in c) for c in cache]
+    opts = [torch.optim.AdamW(m.parameters(), lr=3e-3, weight_decay=0.01, capturable=True)
+            for m in models]
+    eager = [window_step(models[0], opts[0], xs, eis, ls, ms, cs, torch.bfloat16)[0].item()
+             for _ in range(5)]
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):  # warm-up (also the first two of the five steps)
+        warm = [window_step(models[1], opts[1], xs, eis, ls, ms, cs, torch.bfloat16)[0].item()
+                for _ in range(2)]
+    torch.cuda.current_stream(dev).wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_loss, _ = window_step(models[1], opts[1], xs, eis, ls, ms, cs, torch.bfloat16)
+    replayed = []
+    for _ in range(3):
+        graph.replay()
+        replayed.append(static_loss.item())
+    torch.cuda.synchronize()
+    assert warm == eager[:2]
+    assert replayed == eager[2:], (replayed, eager)
+    for (n, p), (_, q) in zip(models[0].named_parameters(), models[1].named_parameters()):
+        assert torch.equal(p, q), n
