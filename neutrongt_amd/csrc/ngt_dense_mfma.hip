@@ -769,9 +769,10 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_fused(
   __shared__ __align__(16) uint2 xr[2][kSB];
   __shared__ __align__(16) float dd[kSB];               // -D, with dropout only
   __shared__ __align__(16) short tr[kWaves][kT][kT + kTrPad];  // a wave's dS tile, [q][key]
-  // the stage's partial dQ per sub-tile in the MFMA's D layout of the lanes
-  // that hold columns c < DH: [sub][half][c][16 rows]
-  __shared__ __align__(16) float red[kSubs][2][DH][16];
+  // the stage's partial dQ per sub-tile in the MFMA's D layout, every lane
+  // (columns c >= DH hold zeros): [sub][row group u][half][c][4 rows], so a
+  // lane's 16-byte accesses of one u are 16 bytes apart
+  __shared__ __align__(16) float red[kSubs][4][2][kT][4];
   const int lane = tid_x() & (kWave - 1);
   const int wave = tid_x() >> 6;
   const int half = lane >> 5;
@@ -905,26 +906,25 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_fused(
         // partial dQ of this sub-tile over the wave's keys, on top of the
         // waves before it: A = dS[query][key] read back from T (a wave's own
         // LDS writes and reads complete in order), B = kq
-        f32x16 acc = zero16();
-        if (step > 0 && l32 < DH) {
-          const float4* rp = reinterpret_cast<const float4*>(&red[sub][half][l32][0]);
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const float4 f = rp[u];
-            acc[4 * u] = f.x, acc[4 * u + 1] = f.y, acc[4 * u + 2] = f.z, acc[4 * u + 3] = f.w;
-          }
-        }
         s16x4 ta[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) ta[j] = lds4(&T[l32][8 * j + 4 * half]);
-        acc = mfma2(ta[0], ta[1], kq[0], kq[1], acc);
-        acc = mfma2(ta[2], ta[3], kq[2], kq[3], acc);
-        if (l32 < DH) {
-          float4* wp = reinterpret_cast<float4*>(&red[sub][half][l32][0]);
+        f32x16 acc;
+        if (step == 0) {  // uniform: the first wave of this sub-tile starts the sum
+          acc = mfma2(ta[0], ta[1], kq[0], kq[1], zero16());
+        } else {
 #pragma unroll
-          for (int u = 0; u < 4; ++u)
-            wp[u] = make_float4(acc[4 * u], acc[4 * u + 1], acc[4 * u + 2], acc[4 * u + 3]);
+          for (int u = 0; u < 4; ++u) {
+            const float4 f = *reinterpret_cast<const float4*>(&red[sub][u][half][l32][0]);
+            acc[4 * u] = f.x, acc[4 * u + 1] = f.y, acc[4 * u + 2] = f.z, acc[4 * u + 3] = f.w;
+          }
+          acc = mfma2(ta[0], ta[1], kq[0], kq[1], acc);
         }
+        acc = mfma2(ta[2], ta[3], kq[2], kq[3], acc);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          *reinterpret_cast<float4*>(&red[sub][u][half][l32][0]) =
+              make_float4(acc[4 * u], acc[4 * u + 1], acc[4 * u + 2], acc[4 * u + 3]);
       }
       __syncthreads();
     }
@@ -933,9 +933,8 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_fused(
     float* pz = part_dq + int64_t(wg_x()) * n_q * H * DH;
     for (int e = tid_x(); e < nvalid * DH; e += kBlock) {
       const int r = e / DH, c = e - (e / DH) * DH;
-      const int sb = r / kT, rr = r - sb * kT;  // D row rr = 8 (i / 4) + 4 half + i % 4
-      const int hf = (rr >> 2) & 1, i = ((rr >> 3) << 2) | (rr & 3);
-      pz[(int64_t(qb + r) * H + h) * DH + c] = red[sb][hf][c][i];
+      const int sb = r / kT, rr = r - sb * kT;  // D row rr = 8 u + 4 half + i, i < 4
+      pz[(int64_t(qb + r) * H + h) * DH + c] = red[sb][rr >> 3][(rr >> 2) & 1][c][rr & 3];
     }
   }
   if (l32 >= DH) return;
@@ -1156,9 +1155,10 @@ MfSplit mfma_dq_split(int n_q, int n_k, int H) {
 // The single-pass backward (k_mf_bwd_fused) or the two passes: the number of
 // 128-key blocks whose partial dQ the backward workspace holds, 0 for the two
 // passes.  Two passes by default: at 16,000 nodes, 8 heads, d = 8 the single
-// pass measured 1,069 us plus a 136 us combine of its 512 MB of partials
-// against 470 + 324 us (162 VGPRs, 3 waves per SIMD, against 114 and 4; four
-// block barriers per stage for the fixed summation order).
+// pass measured 1,009 us plus a 136 us combine of its 512 MB of partials
+// against 470 + 324 us (162 VGPRs, 3 waves per SIMD, against 114 and 4, so
+// its 4,000 waves take 1.3 rounds; four block barriers per stage for the
+// fixed summation order).
 // NGT_DENSE_FUSED=1 turns it on.
 int mfma_fused_blocks(int n_q, int n_k, int H, int d) {
   (void)H;
