@@ -769,10 +769,11 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_fused(
   __shared__ __align__(16) uint2 xr[2][kSB];
   __shared__ __align__(16) float dd[kSB];               // -D, with dropout only
   __shared__ __align__(16) short tr[kWaves][kT][kT + kTrPad];  // a wave's dS tile, [q][key]
-  // the stage's partial dQ per sub-tile in the MFMA's D layout, every lane
-  // (columns c >= DH hold zeros): [sub][row group u][half][c][4 rows], so a
-  // lane's 16-byte accesses of one u are 16 bytes apart
-  __shared__ __align__(16) float red[kSubs][4][2][kT][4];
+  // the stage's partial dQ per sub-tile in the MFMA's D layout:
+  // [sub][row group u][half][c][4 rows], so a lane's 16-byte accesses of one u
+  // are 16 bytes apart.  Lanes of columns c >= DH (zeros, never stored) all
+  // use the spare column DH, so every lane takes the same path.
+  __shared__ __align__(16) float red[kSubs][4][2][DH + 1][4];
   const int lane = tid_x() & (kWave - 1);
   const int wave = tid_x() >> 6;
   const int half = lane >> 5;
@@ -821,6 +822,7 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_fused(
   fill_pad_rows<DH>(qt, false);
   fill_pad_rows<DH>(gt, false);
   short (*T)[kT + kTrPad] = tr[wave];
+  const int rc = l32 < DH ? l32 : DH;  // this lane's column of red
   prefetch(0);
   for (int qb = 0; qb < n_q; qb += kSB) {
     __syncthreads();
@@ -915,7 +917,7 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_fused(
         } else {
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
-            const float4 f = *reinterpret_cast<const float4*>(&red[sub][u][half][l32][0]);
+            const float4 f = *reinterpret_cast<const float4*>(&red[sub][u][half][rc][0]);
             acc[4 * u] = f.x, acc[4 * u + 1] = f.y, acc[4 * u + 2] = f.z, acc[4 * u + 3] = f.w;
           }
           acc = mfma2(ta[0], ta[1], kq[0], kq[1], acc);
@@ -923,7 +925,7 @@ __global__ __launch_bounds__(kBlock) void k_mf_bwd_fused(
         acc = mfma2(ta[2], ta[3], kq[2], kq[3], acc);
 #pragma unroll
         for (int u = 0; u < 4; ++u)
-          *reinterpret_cast<float4*>(&red[sub][u][half][l32][0]) =
+          *reinterpret_cast<float4*>(&red[sub][u][half][rc][0]) =
               make_float4(acc[4 * u], acc[4 * u + 1], acc[4 * u + 2], acc[4 * u + 3]);
       }
       __syncthreads();
@@ -1155,10 +1157,10 @@ MfSplit mfma_dq_split(int n_q, int n_k, int H) {
 // The single-pass backward (k_mf_bwd_fused) or the two passes: the number of
 // 128-key blocks whose partial dQ the backward workspace holds, 0 for the two
 // passes.  Two passes by default: at 16,000 nodes, 8 heads, d = 8 the single
-// pass measured 1,009 us plus a 136 us combine of its 512 MB of partials
-// against 470 + 324 us (162 VGPRs, 3 waves per SIMD, against 114 and 4, so
-// its 4,000 waves take 1.3 rounds; four block barriers per stage for the
-// fixed summation order).
+// pass measured 991 us plus a 136 us combine of its 512 MB of partials
+// against 470 + 324 us (162 VGPRs, 3 waves per SIMD, against 114 and 4;
+// forced to 4 waves per SIMD, 30 VGPRs spilled, 923 us: the block's
+// lockstep steps and each step's LDS round trips lengthen a tile's chain).
 // NGT_DENSE_FUSED=1 turns it on.
 int mfma_fused_blocks(int n_q, int n_k, int H, int d) {
   (void)H;
