@@ -249,8 +249,10 @@ def ppr_bench(args, cfg, dev) -> dict:
     _log(f"[bench] ppr: graph n={n}, {int(col.numel())} directed edges; topk {topk}, "
          f"{iters} iterations, batches of {batch}")
     # one batch as warm-up, then the whole graph timed
+    method = args.ppr_method
     PPR.personal_pagerank_appnp(None, alpha, topk=topk, num_iterations=iters, batch_size=batch,
-                                device=dev, csr_data=csr, iter_topk=topk, source_end=batch)
+                                device=dev, csr_data=csr, iter_topk=topk, source_end=batch,
+                                method=method)
     torch.cuda.synchronize()
     # all seeds, in chunks of 32 batches with a progress line after each (the
     # rows are independent, so chunking changes nothing but the logging)
@@ -261,7 +263,7 @@ def ppr_bench(args, cfg, dev) -> dict:
         i_c, v_c = PPR.personal_pagerank_appnp(None, alpha, topk=topk, num_iterations=iters,
                                                batch_size=batch, device=dev, csr_data=csr,
                                                iter_topk=topk, source_start=s0,
-                                               source_end=min(s0 + chunk, n))
+                                               source_end=min(s0 + chunk, n), method=method)
         idx_parts.append(i_c)
         val_parts.append(v_c)
         torch.cuda.synchronize()
@@ -305,7 +307,7 @@ def ppr_bench(args, cfg, dev) -> dict:
                                 + f", alpha {alpha}, top-{topk}, {iters} iterations, "
                                 f"batches of {batch} seeds"),
                    "entries": int(idx.shape[1]), "degree_cap": cap,
-                   "relabelled": bool(args.ppr_relabel),
+                   "relabelled": bool(args.ppr_relabel), "step": method,
                    "max_degree": int(deg_max)},
         "cpu_baseline": cpu,
     }
@@ -789,6 +791,9 @@ def main(argv=None) -> int:
     ap.add_argument("--ppr-relabel", action="store_true",
                     help="with --ppr: number the global graph's nodes by a seeded random "
                          "permutation (the generator numbers them by decreasing degree)")
+    ap.add_argument("--ppr-method", choices=("direct", "sort"), default="direct",
+                    help="with --ppr: the propagation step's form (direct evaluation, or the "
+                         "sorted product list); both give the same bits")
     ap.add_argument("--prep", action="store_true",
                     help="time the window assembly instead (related nodes, induced subgraph, "
                          "window CSR, feature gather) on the config's global graph")

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define NGT_ABI_VERSION 9
+#define NGT_ABI_VERSION 10
 
 #define NGT_F32 0
 #define NGT_BF16 1
@@ -503,7 +503,22 @@ int ngt_segment_sum_f32(const float* vals, int64_t n_vals, const int64_t* seg, i
  *   fp32 tensor by a Python float).  Products of one (row, column) are added
  *   in the order (state rank, CSR position), so the result is deterministic.
  * Bad ids (state columns, neighbours, seeds outside [0, n_nodes), negative
- * degrees) are counted in *status (device int32) and skipped.
+ * degrees) are counted in *status (device int32) and skipped; so is a total
+ * below row_off[n_rows] (then nothing is expanded).
+ * ngt_ppr_step_direct computes the same step, bit for bit, without the
+ *   product list: each (row, column) sum is evaluated where the column first
+ *   occurs, from searches in the row's other state lists, and each chunk of
+ *   512 entries of one list keeps its best K before a per-row merge.  total
+ *   is row_off[n_rows] from ngt_ppr_count (or any upper bound of the product
+ *   count): the workspace, O(n_rows * (K + 1) + total / 512) * K * 8 bytes,
+ *   is sized from it; no sort.  Needs every CSR row's columns in ascending
+ *   order (transition_csr's order).  max_mult >= 1, the
+ *   most times one column repeats within a CSR row (1 for a graph without
+ *   duplicate edges), lets it skip columns whose value is shown to fall
+ *   below the row's K-th best (0: no skipping; the result is the same).
+ *   status points to two int32: [0] bad ids as above, [1] CSR rows met out of
+ *   order, a column repeated more than max_mult times, or a total too small
+ *   for the state's lists (the output is then invalid).
  */
 int ngt_ppr_count_workspace_bytes(int32_t n_rows, size_t* bytes);
 int ngt_ppr_count(const int64_t* rowptr, int64_t n_nodes, const int32_t* st_col,
@@ -516,6 +531,13 @@ int ngt_ppr_step(const int64_t* rowptr, const int64_t* col, const float* inv_deg
                  float alpha, float keep, const int64_t* row_off, int64_t total,
                  int32_t* out_col, float* out_val, int32_t* out_cnt, int32_t* status,
                  void* workspace, size_t workspace_bytes, void* stream);
+int ngt_ppr_step_direct_workspace_bytes(int64_t total, int32_t n_rows, int32_t K, size_t* bytes);
+int ngt_ppr_step_direct(const int64_t* rowptr, const int64_t* col, const float* inv_deg,
+                        int64_t n_nodes, const int32_t* st_col, const float* st_val,
+                        const int32_t* st_cnt, const int64_t* seeds, int32_t n_rows, int32_t K,
+                        float alpha, float keep, int32_t max_mult, int64_t total,
+                        int32_t* out_col, float* out_val, int32_t* out_cnt, int32_t* status,
+                        void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Induced window subgraph with relabelling, on the GPU.

@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libngt_attn.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 NGT_F32 = 0
 NGT_BF16 = 1
@@ -146,6 +146,9 @@ SIGNATURES = {
     "ngt_ppr_step_workspace_bytes": [_i64, _i32, _vp],
     "ngt_ppr_step": [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i32, C.c_float, C.c_float,
                      _vp, _i64, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
+    "ngt_ppr_step_direct_workspace_bytes": [_i64, _i32, _i32, _vp],
+    "ngt_ppr_step_direct": [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i32, C.c_float,
+                            C.c_float, _i32, _i64, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
     "ngt_subgraph_workspace_bytes": [_i64, _i64, _i32, _vp],
     "ngt_subgraph_coo": [_vp, _i64, _i64, _vp, _i32, _vp, _i64, _vp, _vp, _sz, _vp],
     "ngt_subgraph_csr": [_vp, _vp, _i64, _i64, _vp, _i32, _vp, _i64, _vp, _vp, _sz, _vp],

@@ -97,11 +97,15 @@ __global__ __launch_bounds__(kBlock) void k_ppr_expand(
     const float* __restrict__ inv_deg, int64_t n_nodes, const int32_t* __restrict__ st_col,
     const float* __restrict__ st_val, const int32_t* __restrict__ st_cnt,
     const int64_t* __restrict__ seeds, int32_t n_rows, int32_t K,
-    const int64_t* __restrict__ row_off, KeyFmt f, KeyT* __restrict__ keys,
+    const int64_t* __restrict__ row_off, int64_t total, KeyFmt f, KeyT* __restrict__ keys,
     float* __restrict__ vals, int32_t* status) {
   const int64_t r = blockIdx.x * int64_t(kWaves) + (threadIdx.x >> 6);
   const int lane = threadIdx.x & (kWave - 1);
   if (r >= n_rows) return;
+  if (row_off[n_rows] > total) {  // the product list would overrun the workspace
+    if (r == 0 && lane == 0) atomicAdd(status, 1);
+    return;
+  }
   int64_t at = row_off[r];
   const KeyT rk = KeyT(r) << f.rs;
   const KeyT dead = rk | (KeyT(f.deadcol) << 1);
@@ -352,7 +356,7 @@ int ppr_sort_reduce(const int64_t* rowptr, const int64_t* col, const float* inv_
   int32_t* flag = reinterpret_cast<int32_t*>(ws + L.flag);
   int32_t* pos = reinterpret_cast<int32_t*>(ws + L.pos);
   hipLaunchKernelGGL(k_ppr_expand<KeyT>, dim3(grid_waves(n_rows)), dim3(kBlock), 0, s, rowptr,
-                     col, inv_deg, n_nodes, st_col, st_val, st_cnt, seeds, n_rows, K, row_off, f,
+                     col, inv_deg, n_nodes, st_col, st_val, st_cnt, seeds, n_rows, K, row_off, total, f,
                      keys_a, vals_a, status);
   NGT_HIP_CHECK(hipGetLastError());
   size_t tb = L.temp_bytes;
@@ -370,6 +374,476 @@ int ppr_sort_reduce(const int64_t* rowptr, const int64_t* col, const float* inv_
                      reinterpret_cast<int32_t*>(ws + L.seg_col),
                      reinterpret_cast<float*>(ws + L.seg_val));
   NGT_HIP_CHECK(hipGetLastError());
+  return NGT_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Direct evaluation: no product list, no sort.  For row r with state lists
+// L_j = the CSR row of st_col[r, j] (columns ascending) and weights
+// w_j = st_val[r, j] * inv_deg[st_col[r, j]], the sum of column n is
+//   s = 0; for j in rank order: for every occurrence of n in L_j: s += w_j,
+// which is exactly the additions, in the same order, that the stable sort of
+// the product list (j, CSR position) gives one (row, n) segment.  Position p
+// of list j is evaluated by the lane that owns it: the first occurrence of n
+// in the first list holding it (searches in the other lists decide).
+//
+// Work: one wave per chunk of kDirChunk consecutive entries of one list (a
+// row's chunks are its lists' chunks in rank order, at least one per row for
+// the teleport entry).  A chunk's columns lie in [vmin, vmax], its first and
+// last entry, so each other list is searched once per chunk for the slice of
+// entries in that interval (one lane per list, all lists at once); the slices
+// are staged in LDS as int32 and the per-column searches run there (slices
+// that do not fit search their part of global memory).  Each chunk keeps its
+// best K (value descending, column ascending); a per-row merge takes the best
+// K of its chunks', which is the best K of the row whatever the chunking.
+//
+// Pruning, which changes no result.  With nonnegative weights, keep and
+// alpha, a column's value is at least fl(w_j * keep) for every list j that
+// holds it (fp32 sums of nonnegative terms only grow), and a list of at least
+// K * M entries, M the most repeats of one column within a CSR row, holds K
+// distinct columns: so the row's K-th best value is at least tau, the largest
+// fl(w_j * keep) over such lists.  A column whose value is shown to lie below
+// tau cannot be among the row's best K.  Its upper bound is keep times the
+// sum of M * w over the lists whose slice may hold it, less the lists a
+// search has ruled out, heaviest first, with fp32's rounding of the exact sum
+// (at most K * M + 1 roundings) covered by a factor 1 + 2^-10.
+
+constexpr int kDirU = 8;                                 // entries per lane
+constexpr int64_t kDirChunk = int64_t(kWave) * kDirU;    // entries per chunk
+constexpr int kDirStage = 2048;                          // staged slice entries per wave
+
+__device__ __forceinline__ int64_t lane_i64(int64_t v, int src) {  // src wave-uniform
+  const uint64_t u = uint64_t(v);
+  const uint32_t lo = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(u)), src));
+  const uint32_t hi = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(u >> 32)), src));
+  return int64_t((uint64_t(hi) << 32) | lo);
+}
+
+__device__ __forceinline__ float lane_f32(float v, int src) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
+}
+
+// first index in [b, e) whose column is >= x (strict: > x), e if none
+template <bool kStrict>
+__device__ __forceinline__ int64_t col_bound(const int64_t* __restrict__ col, int64_t b, int64_t e,
+                                             int64_t x) {
+  while (b < e) {
+    const int64_t mid = b + ((e - b) >> 1);
+    const bool left = kStrict ? col[mid] <= x : col[mid] < x;
+    if (left) b = mid + 1; else e = mid;
+  }
+  return b;
+}
+
+__device__ __forceinline__ int32_t clamp_i32(int64_t v) {
+  return v < INT32_MIN ? INT32_MIN : (v > INT32_MAX ? INT32_MAX : int32_t(v));
+}
+
+// chunks per row: the sum over its state lists of ceil(length / kDirChunk),
+// at least 1 (the teleport entry)
+__global__ void k_ppr_chunks(const int64_t* __restrict__ rowptr, int64_t n_nodes,
+                             const int32_t* __restrict__ st_col, const int32_t* __restrict__ st_cnt,
+                             int32_t n_rows, int32_t K, int32_t* __restrict__ nch) {
+  const int64_t r = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
+  if (r > n_rows) return;
+  if (r == n_rows) {
+    nch[r] = 0;
+    return;
+  }
+  int64_t c = 0;
+  const int n = st_cnt[r];
+  if (n >= 0 && n <= K) {
+    for (int j = 0; j < n; ++j) {
+      const int32_t cl = st_col[r * K + j];
+      if (cl < 0 || cl >= n_nodes) continue;
+      const int64_t d = rowptr[cl + 1] - rowptr[cl];
+      if (d > 0) c += (d + kDirChunk - 1) / kDirChunk;
+    }
+  }
+  nch[r] = c > 0 ? int32_t(c) : 1;
+}
+
+// status[0]: bad neighbour ids and seeds; status[1]: CSR rows out of order,
+// a column repeated more than max_mult times, or chunk counts past the bound
+__global__ __launch_bounds__(kBlock) void k_ppr_direct(
+    const int64_t* __restrict__ rowptr, const int64_t* __restrict__ col,
+    const float* __restrict__ inv_deg, int64_t n_nodes, const int32_t* __restrict__ st_col,
+    const float* __restrict__ st_val, const int32_t* __restrict__ st_cnt,
+    const int64_t* __restrict__ seeds, int32_t n_rows, int32_t K, float alpha, float keep,
+    int32_t max_mult, const int32_t* __restrict__ chunk_off, int32_t max_chunks,
+    float* __restrict__ part_val, int32_t* __restrict__ part_col, int32_t* __restrict__ part_cnt,
+    int32_t* status) {
+#pragma clang fp contract(off)
+  __shared__ int32_t stage_all[kWaves][kDirStage];
+  const int32_t w = __builtin_amdgcn_readfirstlane(int(blockIdx.x * kWaves + (threadIdx.x >> 6)));
+  const int lane = threadIdx.x & (kWave - 1);
+  int32_t* stage = stage_all[threadIdx.x >> 6];
+  const int32_t n_chunks = __builtin_amdgcn_readfirstlane(chunk_off[n_rows]);
+  if (n_chunks > max_chunks) {
+    if (w == 0 && lane == 0) atomicAdd(status + 1, 1);
+    return;
+  }
+  if (w >= n_chunks) return;
+  // the row: chunk_off[r] <= w < chunk_off[r + 1] (every row has a chunk)
+  int32_t lo = 0, hi = n_rows;
+  while (hi - lo > 1) {
+    const int32_t mid = (lo + hi) >> 1;
+    if (chunk_off[mid] <= w) lo = mid; else hi = mid;
+  }
+  const int32_t r = __builtin_amdgcn_readfirstlane(lo);
+  const int32_t ci = w - __builtin_amdgcn_readfirstlane(chunk_off[r]);
+  int n = __builtin_amdgcn_readfirstlane(st_cnt[r]);
+  if (n < 0 || n > K) n = 0;
+  // lane j < n holds list j: begin, length, weight, first and last column
+  int64_t lb = 0, ll = 0, lfirst = 0, llast = -1;
+  float lw = 0.f;
+  if (lane < n) {
+    const int32_t c = st_col[int64_t(r) * K + lane];
+    if (c >= 0 && c < n_nodes) {
+      const int64_t b = rowptr[c], e = rowptr[c + 1];
+      if (e > b) {
+        lb = b;
+        ll = e - b;
+        lw = st_val[int64_t(r) * K + lane] * inv_deg[c];
+        lfirst = col[b];
+        llast = col[e - 1];
+      }
+    }
+  }
+  // this chunk's list j: the last nonempty list whose first chunk is <= ci
+  const int32_t cj = int32_t((ll + kDirChunk - 1) / kDirChunk);
+  int32_t cinc = cj;
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int32_t v = __shfl_up(cinc, off, kWave);
+    if (lane >= off) cinc += v;
+  }
+  const uint64_t jm = __ballot(cj > 0 && cinc - cj <= ci);
+  const int j = jm ? 63 - __clzll(jm) : -1;  // -1: no list (the teleport chunk of an empty row)
+  int64_t p0 = 0, ej = 0, vmin = 0, vmax = -1;
+  if (j >= 0) {
+    const int32_t sub = ci - (__builtin_amdgcn_readlane(cinc, j) - __builtin_amdgcn_readlane(cj, j));
+    const int64_t bj = lane_i64(lb, j);
+    p0 = bj + int64_t(sub) * kDirChunk;
+    ej = bj + lane_i64(ll, j);
+    const int64_t pe = p0 + kDirChunk < ej ? p0 + kDirChunk : ej;
+    vmin = col[p0];
+    vmax = col[pe - 1];
+  }
+  const float wj_own = j >= 0 ? lane_f32(lw, j) : 0.f;
+  const int64_t sd = seeds[r];
+  const bool seed_ok = sd >= 0 && sd < n_nodes;
+
+  // every other list's slice [slo, shi) of columns in [vmin, vmax], and where
+  // it is staged: at soff in the wave's LDS when the slices up to it fit
+  int64_t slo = 0, shi = 0;
+  if (j >= 0 && lane < n && lane != j && ll > 0 && vmax >= lfirst && vmin <= llast) {
+    slo = col_bound<false>(col, lb, lb + ll, vmin);
+    shi = col_bound<true>(col, slo, lb + ll, vmax);
+  }
+  const int64_t sm = shi - slo;
+  int64_t sinc = sm;
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int64_t v = __shfl_up(sinc, off, kWave);
+    if (lane >= off) sinc += v;
+  }
+  const int64_t soff64 = sinc - sm;
+  const bool staged = sm > 0 && sinc <= kDirStage;  // the slices up to this one fit
+  const int32_t soff = staged ? int32_t(soff64) : 0;
+  const uint64_t stm = __ballot(staged);
+  const int32_t n_stage = stm ? int32_t(lane_i64(sinc, 63 - __clzll(stm))) : 0;
+  for (int32_t f0 = 0; f0 < n_stage; f0 += kWave) {  // uniform trips: every lane shuffles
+    const int32_t f = f0 + lane;
+    // the slice holding entry f: the last lane whose slice starts at or before f
+    int sl = 0;
+#pragma unroll
+    for (int h = kWave / 2; h > 0; h >>= 1)
+      if (__shfl(soff64, sl + h, kWave) <= f) sl += h;
+    const int64_t src = __shfl(slo, sl, kWave) + (f - __shfl(soff64, sl, kWave));
+    if (f < n_stage) stage[f] = clamp_i32(col[src]);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // this chunk's entries: column, owner, repeats within its own list
+  int32_t nv[kDirU];
+  bool own[kDirU];
+  int32_t rep[kDirU];
+  float s[kDirU];
+#pragma unroll
+  for (int u = 0; u < kDirU; ++u) {
+    const int64_t p = p0 + lane + u * kWave;
+    own[u] = false;
+    nv[u] = 0;
+    rep[u] = 0;
+    s[u] = 0.f;
+    if (j < 0 || p >= ej) continue;
+    const int64_t x = col[p];
+    bool o = x >= 0 && x < n_nodes;
+    if (!o) atomicAdd(status, 1);
+    const int64_t bj = ej - lane_i64(ll, j);
+    if (p > bj) {
+      const int64_t prev = col[p - 1];
+      if (prev > x) atomicAdd(status + 1, 1);
+      if (prev == x) o = false;  // a repeat: its first occurrence owns it
+    }
+    if (max_mult > 0 && p - max_mult >= bj && col[p - max_mult] == x) atomicAdd(status + 1, 1);
+    if (o) {
+      int32_t c = 1;
+      for (int64_t q = p + 1; q < ej && col[q] == x; ++q) ++c;
+      rep[u] = c;
+      nv[u] = int32_t(x);
+    }
+    own[u] = o;
+  }
+
+  // find column x in list jj's slice: count of its entries (0: absent)
+  auto slice_count = [&](bool st, int32_t so, int64_t lo_, int64_t hi_, int32_t x) -> int32_t {
+    int32_t c = 0;
+    if (st) {
+      int32_t a = so, len = int32_t(hi_ - lo_);
+      while (len > 0) {
+        const int32_t half = len >> 1;
+        if (stage[a + half] < x) { a += half + 1; len -= half + 1; } else len = half;
+      }
+      for (const int32_t e = so + int32_t(hi_ - lo_); a < e && stage[a] == x; ++a) ++c;
+    } else {
+      int64_t a = col_bound<false>(col, lo_, hi_, x);
+      for (; a < hi_ && col[a] == x; ++a) ++c;
+    }
+    return c;
+  };
+
+  bool prune = j >= 0 && max_mult > 0 && int64_t(max_mult) * K <= 4096 && keep >= 0.f &&
+               alpha >= 0.f;
+  if (__ballot(lane < n && !(lw >= 0.f && lw <= __FLT_MAX__))) prune = false;  // < 0, inf, NaN
+  float tau = (lane < n && ll >= int64_t(K) * max_mult) ? lw * keep : -INFINITY;
+  for (int off = 32; off > 0; off >>= 1) tau = fmaxf(tau, __shfl_xor(tau, off, kWave));
+  if (prune && tau > 0.f) {
+    // lists by weight, heaviest first: lane i of `order` names the list of rank i
+    int rank = lane;
+    if (lane < n) {
+      rank = 0;
+      for (int i = 0; i < n; ++i) {
+        const float wi = lane_f32(lw, i);
+        rank += (wi > lw || (wi == lw && i < lane)) ? 1 : 0;
+      }
+    }
+    const int order = __builtin_amdgcn_ds_permute(rank * 4, lane);
+    // sum of M * w over the own list and the other lists whose slice is not empty
+    double base_bnd = double(max_mult) * double(wj_own);
+    for (int jj = 0; jj < n; ++jj)
+      if (jj != j && lane_i64(sm, jj) > 0) base_bnd += double(max_mult) * double(lane_f32(lw, jj));
+    const double err = base_bnd * 0x1p-40;
+    // a column survives while keep * (bound + rounding of the double sums)
+    // * (1 + 2^-10) reaches tau; the seed always survives (alpha)
+    const double cut = double(tau) / (double(keep) * (1.0 + 1.0 / 1024.0));
+    double bnd[kDirU];
+    bool alive[kDirU];
+#pragma unroll
+    for (int u = 0; u < kDirU; ++u) {
+      bnd[u] = base_bnd;
+      alive[u] = own[u] && (base_bnd + err >= cut || (seed_ok && nv[u] == sd));
+    }
+    for (int i = 0; i < n; ++i) {
+      bool any = false;
+#pragma unroll
+      for (int u = 0; u < kDirU; ++u) any |= alive[u] && !(seed_ok && nv[u] == sd);
+      if (__ballot(any) == 0) break;
+      const int jj = __builtin_amdgcn_readlane(order, i);
+      if (jj == j) continue;
+      const int64_t m = lane_i64(sm, jj);
+      if (m == 0) continue;
+      const bool st = __builtin_amdgcn_readlane(int(staged), jj) != 0;
+      const int32_t so = __builtin_amdgcn_readlane(soff, jj);
+      const int64_t lo_ = lane_i64(slo, jj), hi_ = lo_ + m;
+      const double mwj = double(max_mult) * double(lane_f32(lw, jj));
+#pragma unroll
+      for (int u = 0; u < kDirU; ++u) {
+        if (!alive[u] || (seed_ok && nv[u] == sd)) continue;
+        if (slice_count(st, so, lo_, hi_, nv[u]) > 0) continue;  // held: the bound stays
+        bnd[u] -= mwj;
+        if (bnd[u] + err < cut) alive[u] = false;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kDirU; ++u) own[u] = own[u] && alive[u];
+  }
+
+  // sums in list order; a column found in an earlier list belongs to it
+  for (int jj = 0; jj < n; ++jj) {
+    if (jj == j) {
+#pragma unroll
+      for (int u = 0; u < kDirU; ++u)
+        if (own[u])
+          for (int32_t c = 0; c < rep[u]; ++c) s[u] += wj_own;
+      continue;
+    }
+    const int64_t m = lane_i64(sm, jj);
+    if (m == 0) continue;
+    const bool st = __builtin_amdgcn_readlane(int(staged), jj) != 0;
+    const int32_t so = __builtin_amdgcn_readlane(soff, jj);
+    const int64_t lo_ = lane_i64(slo, jj), hi_ = lo_ + m;
+    const float wj = lane_f32(lw, jj);
+#pragma unroll
+    for (int u = 0; u < kDirU; ++u) {
+      if (!own[u]) continue;
+      const int32_t c = slice_count(st, so, lo_, hi_, nv[u]);
+      if (c == 0) continue;
+      if (jj < j) {
+        own[u] = false;  // an earlier list holds it
+        continue;
+      }
+      for (int32_t k = 0; k < c; ++k) s[u] += wj;
+    }
+  }
+  float cv[kDirU + 1];
+  int32_t cc[kDirU + 1];
+#pragma unroll
+  for (int u = 0; u < kDirU; ++u) {
+    cv[u] = own[u] ? scale_then_add(s[u], keep, alpha, seed_ok && nv[u] == sd) : -INFINITY;
+    cc[u] = own[u] ? nv[u] : INT32_MAX;
+  }
+  cv[kDirU] = -INFINITY;
+  cc[kDirU] = INT32_MAX;
+  bool extra = false;
+  if (ci == 0) {  // the teleport entry alone when no list holds the seed
+    if (!seed_ok) {
+      if (lane == 0) atomicAdd(status, 1);
+    } else {
+      bool found = false;
+      if (ll > 0 && sd >= lfirst && sd <= llast) {
+        const int64_t a = col_bound<false>(col, lb, lb + ll, sd);
+        found = a < lb + ll && col[a] == sd;
+      }
+      if (__ballot(found) == 0 && lane == 0) {
+        cv[kDirU] = scale_then_add(0.f, keep, alpha, true);
+        cc[kDirU] = int32_t(sd);
+        extra = true;
+      }
+    }
+  }
+  int real = 0;
+#pragma unroll
+  for (int u = 0; u < kDirU; ++u) real += __popcll(__ballot(own[u]));
+  real += __popcll(__ballot(extra));
+  const int n_out = real < K ? real : K;
+  float pv = INFINITY;
+  int32_t pc = -1;  // the last pick: everything ranks after (+inf, -1)
+  for (int t = 0; t < n_out; ++t) {
+    float bv = -INFINITY;
+    int32_t bc = INT32_MAX;
+#pragma unroll
+    for (int u = 0; u <= kDirU; ++u) {
+      if (better(pv, pc, cv[u], cc[u]) && better(cv[u], cc[u], bv, bc)) {
+        bv = cv[u];
+        bc = cc[u];
+      }
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+      const float ov = __shfl_xor(bv, off, kWave);
+      const int32_t oc = __shfl_xor(bc, off, kWave);
+      if (better(ov, oc, bv, bc)) {
+        bv = ov;
+        bc = oc;
+      }
+    }
+    if (lane == 0) {
+      part_val[int64_t(w) * K + t] = bv;
+      part_col[int64_t(w) * K + t] = bc;
+    }
+    pv = bv;
+    pc = bc;
+  }
+  if (lane == 0) part_cnt[w] = n_out;
+}
+
+// One wave per row: the best K of its chunks' best K.
+__global__ __launch_bounds__(kBlock) void k_ppr_merge(
+    const int32_t* __restrict__ chunk_off, int32_t max_chunks, const float* __restrict__ part_val,
+    const int32_t* __restrict__ part_col, const int32_t* __restrict__ part_cnt, int32_t n_rows,
+    int32_t K, int32_t* __restrict__ out_col, float* __restrict__ out_val,
+    int32_t* __restrict__ out_cnt) {
+  const int32_t r = __builtin_amdgcn_readfirstlane(int(blockIdx.x * kWaves + (threadIdx.x >> 6)));
+  const int lane = threadIdx.x & (kWave - 1);
+  if (r >= n_rows || chunk_off[n_rows] > max_chunks) return;  // the latter flagged above
+  const int32_t c0 = chunk_off[r], c1 = chunk_off[r + 1];
+  if (c1 - c0 == 1) {
+    const int32_t cnt = part_cnt[c0];
+    if (lane < cnt) {
+      out_col[int64_t(r) * K + lane] = part_col[int64_t(c0) * K + lane];
+      out_val[int64_t(r) * K + lane] = part_val[int64_t(c0) * K + lane];
+    }
+    if (lane == 0) out_cnt[r] = cnt;
+    return;
+  }
+  int32_t have = 0;
+  for (int32_t c = c0 + lane; c < c1; c += kWave) have += part_cnt[c];
+  for (int off = 32; off > 0; off >>= 1) have += __shfl_xor(have, off, kWave);
+  const int n_out = have < K ? have : K;
+  const int64_t m = int64_t(c1 - c0) * K;
+  float pv = INFINITY;
+  int32_t pc = -1;
+  for (int t = 0; t < n_out; ++t) {
+    float bv = -INFINITY;
+    int32_t bc = INT32_MAX;
+    for (int64_t i = lane; i < m; i += kWave) {
+      const int32_t c = c0 + int32_t(i / K);
+      const int32_t k = int32_t(i % K);
+      if (k >= part_cnt[c]) continue;
+      const float v = part_val[int64_t(c) * K + k];
+      const int32_t cl = part_col[int64_t(c) * K + k];
+      if (better(pv, pc, v, cl) && better(v, cl, bv, bc)) {
+        bv = v;
+        bc = cl;
+      }
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+      const float ov = __shfl_xor(bv, off, kWave);
+      const int32_t oc = __shfl_xor(bc, off, kWave);
+      if (better(ov, oc, bv, bc)) {
+        bv = ov;
+        bc = oc;
+      }
+    }
+    if (lane == 0) {
+      out_col[int64_t(r) * K + t] = bc;
+      out_val[int64_t(r) * K + t] = bv;
+    }
+    pv = bv;
+    pc = bc;
+  }
+  if (lane == 0) out_cnt[r] = n_out;
+}
+
+struct DirectLayout {
+  size_t nch, chunk_off, temp, temp_bytes, part_val, part_col, part_cnt, total;
+  int64_t max_chunks;
+};
+
+int direct_layout(int64_t total, int32_t n_rows, int32_t K, DirectLayout* L) {
+  const size_t m = size_t(n_rows > 0 ? n_rows : 1);
+  // a row's chunks: at most 1 + sum over its <= K lists of (length / kDirChunk + 1)
+  L->max_chunks = int64_t(m) * (K + 1) + (total > 0 ? total : 0) / kDirChunk + 1;
+  const size_t c = size_t(L->max_chunks);
+  size_t scan_bytes = 0;
+  NGT_HIP_CHECK(rocprim::exclusive_scan(nullptr, scan_bytes, (int32_t*)nullptr, (int32_t*)nullptr,
+                                        int32_t(0), m + 1, rocprim::plus<int32_t>(),
+                                        hipStream_t(0)));
+  size_t off = 0;
+  auto take = [&](size_t b) {
+    const size_t at = off;
+    off += align256(b);
+    return at;
+  };
+  L->nch = take((m + 1) * 4);
+  L->chunk_off = take((m + 1) * 4);
+  L->temp_bytes = scan_bytes;
+  L->temp = take(scan_bytes);
+  L->part_val = take(c * size_t(K) * 4);
+  L->part_col = take(c * size_t(K) * 4);
+  L->part_cnt = take(c * 4);
+  L->total = off;
   return NGT_OK;
 }
 
@@ -471,6 +945,64 @@ extern "C" int ngt_ppr_step(const int64_t* rowptr, const int64_t* col, const flo
                                            end_bit, status, ws, L, s));
   hipLaunchKernelGGL(k_ppr_topk, dim3(grid_waves(n_rows)), dim3(kBlock), 0, s, seg_row, seg_col,
                      seg_val, n_seg, n_rows, K, out_col, out_val, out_cnt);
+  NGT_HIP_CHECK(hipGetLastError());
+  return NGT_OK;
+}
+
+extern "C" int ngt_ppr_step_direct_workspace_bytes(int64_t total, int32_t n_rows, int32_t K,
+                                                   size_t* bytes) {
+  if (!bytes || total < 0 || n_rows < 0 || K < 1 || K > kMaxK)
+    return set_error(NGT_ERR_ARG, "ngt_ppr_step_direct_workspace_bytes: bad arguments");
+  DirectLayout L;
+  NGT_CHECK_OK(direct_layout(total, n_rows, K, &L));
+  *bytes = L.total;
+  return NGT_OK;
+}
+
+extern "C" int ngt_ppr_step_direct(const int64_t* rowptr, const int64_t* col,
+                                   const float* inv_deg, int64_t n_nodes, const int32_t* st_col,
+                                   const float* st_val, const int32_t* st_cnt,
+                                   const int64_t* seeds, int32_t n_rows, int32_t K, float alpha,
+                                   float keep, int32_t max_mult, int64_t total,
+                                   int32_t* out_col, float* out_val,
+                                   int32_t* out_cnt, int32_t* status, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+  if (n_nodes < 0 || n_rows < 0 || K < 1 || K > kMaxK || total < n_rows || max_mult < 0 ||
+      (n_rows > 0 && (!rowptr || !col || !inv_deg || !st_col || !st_val || !st_cnt || !seeds ||
+                      !out_col || !out_val || !out_cnt || !status)))
+    return set_error(NGT_ERR_ARG, "ngt_ppr_step_direct: bad arguments");
+  if (n_nodes >= (int64_t(1) << 31) || n_rows >= (1 << 30) ||
+      total / kDirChunk + int64_t(n_rows) * (K + 1) >= (int64_t(1) << 31) - 1)
+    return set_error(NGT_ERR_UNSUPPORTED,
+                     "ngt_ppr_step_direct: node, row or product count too large (split the batch)");
+  if (n_rows == 0) return NGT_OK;
+  DirectLayout L;
+  NGT_CHECK_OK(direct_layout(total, n_rows, K, &L));
+  if (!workspace || workspace_bytes < L.total)
+    return set_error(NGT_ERR_WORKSPACE, "ngt_ppr_step_direct: workspace %zu < %zu",
+                     workspace_bytes, L.total);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  int32_t* nch = reinterpret_cast<int32_t*>(ws + L.nch);
+  int32_t* chunk_off = reinterpret_cast<int32_t*>(ws + L.chunk_off);
+  float* part_val = reinterpret_cast<float*>(ws + L.part_val);
+  int32_t* part_col = reinterpret_cast<int32_t*>(ws + L.part_col);
+  int32_t* part_cnt = reinterpret_cast<int32_t*>(ws + L.part_cnt);
+  KernelTimer timer_("ppr_step", s);
+  hipLaunchKernelGGL(k_ppr_chunks, dim3((n_rows + kBlock) / kBlock), dim3(kBlock), 0, s, rowptr,
+                     n_nodes, st_col, st_cnt, n_rows, K, nch);
+  NGT_HIP_CHECK(hipGetLastError());
+  size_t tb = L.temp_bytes;
+  NGT_HIP_CHECK(rocprim::exclusive_scan(ws + L.temp, tb, nch, chunk_off, int32_t(0),
+                                        size_t(n_rows) + 1, rocprim::plus<int32_t>(), s));
+  hipLaunchKernelGGL(k_ppr_direct, dim3(grid_waves(L.max_chunks)), dim3(kBlock), 0, s, rowptr,
+                     col, inv_deg, n_nodes, st_col, st_val, st_cnt, seeds, n_rows, K, alpha, keep,
+                     max_mult, chunk_off, int32_t(L.max_chunks), part_val, part_col, part_cnt,
+                     status);
+  NGT_HIP_CHECK(hipGetLastError());
+  hipLaunchKernelGGL(k_ppr_merge, dim3(grid_waves(n_rows)), dim3(kBlock), 0, s, chunk_off,
+                     int32_t(L.max_chunks), part_val, part_col, part_cnt, n_rows, K, out_col,
+                     out_val, out_cnt);
   NGT_HIP_CHECK(hipGetLastError());
   return NGT_OK;
 }

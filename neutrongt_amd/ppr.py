@@ -13,9 +13,14 @@ batches of seed nodes start from their identity rows and are propagated
 with K = iter_topk (the shipped scripts run topk = iter_topk = 5, alpha 0.85,
 10 iterations, batch 8192); the result keeps min(topk, iter_topk) entries per
 seed and is returned as (edge_index [2, nnz] = (seed, node), values).  Each
-step is ngt_ppr_count, one read-back of the product counts, then ngt_ppr_step
-(expansion, radix sort, ordered segment sums, per-row top-k) on the whole batch
-or on row chunks that bound the step's memory.
+step is ngt_ppr_count, one read-back of the product counts, then
+ngt_ppr_step_direct: every (seed, node) sum evaluated where the node first
+occurs in the seed's state lists (binary searches in the others, the products
+added in the same order), the best K kept per chunk of a row and merged per
+row; no product list is written or sorted.  ``method="sort"`` runs the
+product-list form instead (ngt_ppr_step: expansion, radix sort, ordered
+segment sums, per-row top-k, on row chunks that bound the step's memory); the
+two give the same bits.
 
 Differences from the reference, by design:
   * iter_topk must be positive (1..64): without per-step pruning the state
@@ -48,7 +53,7 @@ def transition_csr(edge_index: torch.Tensor | None = None, csr_data: dict | None
         if num_nodes is not None and n != int(num_nodes):
             raise ValueError(f"CSR num_nodes mismatch: expected {num_nodes}, got {n}")
         deg = (rowptr[1:] - rowptr[:-1]).clamp_min(1).to(torch.float32)
-        return rowptr, col, 1.0 / deg, n
+        return rowptr, _sorted_rows(rowptr, col), 1.0 / deg, n
     if edge_index is None:
         raise ValueError("edge_index must be provided when csr_data is None")
     ei = edge_index.to(dev).long()
@@ -65,17 +70,63 @@ def transition_csr(edge_index: torch.Tensor | None = None, csr_data: dict | None
     return rowptr, dst.contiguous(), 1.0 / counts.clamp_min(1).to(torch.float32), n
 
 
+def _sorted_rows(rowptr: torch.Tensor, col: torch.Tensor) -> torch.Tensor:
+    """col with every CSR row's columns in ascending order (a stable sort by
+    (row, column) when some row is not).  Sums do not depend on the order
+    within a row: repeats of a column in one row carry the same product."""
+    if col.numel() < 2:
+        return col
+    n = rowptr.numel() - 1
+    deg = (rowptr[1:] - rowptr[:-1]).clamp_min(0)
+    if int(rowptr[0]) != 0 or int(deg.sum()) != col.numel():
+        return col  # malformed rows: left to the kernels' own checks
+    desc = col[1:] < col[:-1]  # entry i: col[i + 1] below col[i]
+    last = rowptr[1:-1] - 1    # a row's last entry may exceed the next row's first
+    desc[last[(last >= 0) & (last < desc.numel())]] = False
+    if not bool(desc.any()):
+        return col
+    row = torch.repeat_interleave(torch.arange(n, device=col.device), deg)
+    lo = int(col.min())
+    span = int(col.max()) - lo + 1
+    order = torch.argsort(row * span + (col - lo), stable=True)
+    return col[order].contiguous()
+
+
+def max_repeats(rowptr: torch.Tensor, col: torch.Tensor) -> int:
+    """The most times one column repeats within a CSR row whose columns are
+    in ascending order (1 without duplicate edges)."""
+    if col.numel() < 2:
+        return 1
+    same = col[1:] == col[:-1]  # entry i: col[i + 1] repeats col[i]
+    last = rowptr[1:-1] - 1
+    same[last[(last >= 0) & (last < same.numel())]] = False
+    if not bool(same.any()):
+        return 1
+    idx = torch.arange(same.numel(), device=col.device)
+    brk = torch.cummax(torch.where(same, torch.full_like(idx, -1), idx), 0).values
+    return int((idx - brk).max()) + 1
+
+
 def appnp_batch(rowptr, col, inv_deg, n_nodes: int, seeds: torch.Tensor, alpha: float, K: int,
-                num_iterations: int, max_products: int = 1 << 27):
+                num_iterations: int, max_products: int = 1 << 27, method: str = "direct",
+                max_mult: int | None = None):
     """Propagates one batch of seed rows.  Returns (cols [B, K] int32,
-    vals [B, K] fp32, cnt [B] int32), rows in rank order.  A step whose
-    product count exceeds ``max_products`` runs on consecutive row chunks
-    (rows are independent), which bounds the step's workspace."""
+    vals [B, K] fp32, cnt [B] int32), rows in rank order.  ``method``
+    "direct" (ngt_ppr_step_direct; CSR rows must be in ascending column order,
+    as transition_csr returns them; ``max_mult`` is max_repeats(rowptr, col),
+    found here when None, and 0 turns its pruning off, with the same result)
+    or "sort" (ngt_ppr_step), where a step whose product count exceeds
+    ``max_products`` runs on consecutive row chunks (rows are independent),
+    which bounds the step's workspace."""
     lib = _lib.load()
     dev = seeds.device
     B = int(seeds.numel())
     if not 1 <= K <= MAX_K:
         raise ValueError(f"per-step top-k must be in 1..{MAX_K}, got {K}")
+    if method not in ("direct", "sort"):
+        raise ValueError(f"method must be 'direct' or 'sort', got {method!r}")
+    if method == "direct" and max_mult is None:
+        max_mult = max_repeats(rowptr, col)
     st_col = torch.zeros(B, K, dtype=torch.int32, device=dev)
     st_val = torch.zeros(B, K, dtype=torch.float32, device=dev)
     st_col[:, 0] = seeds.to(torch.int32)
@@ -83,7 +134,7 @@ def appnp_batch(rowptr, col, inv_deg, n_nodes: int, seeds: torch.Tensor, alpha: 
     st_cnt = torch.ones(B, dtype=torch.int32, device=dev)
     nx_col, nx_val, nx_cnt = torch.empty_like(st_col), torch.empty_like(st_val), torch.empty_like(st_cnt)
     seeds = seeds.to(torch.int64).contiguous()
-    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    status = torch.zeros(2, dtype=torch.int32, device=dev)
     row_off = torch.empty(B + 1, dtype=torch.int64, device=dev)
     cb = C.c_size_t()
     _lib.check(lib.ngt_ppr_count_workspace_bytes(B, C.byref(cb)))
@@ -108,13 +159,27 @@ def appnp_batch(rowptr, col, inv_deg, n_nodes: int, seeds: torch.Tensor, alpha: 
                                     nx_cnt[r0:r1].data_ptr(), status.data_ptr(), ws.data_ptr(),
                                     sb.value, stream))
 
+    def step_direct(total):
+        sb = C.c_size_t()
+        _lib.check(lib.ngt_ppr_step_direct_workspace_bytes(total, B, K, C.byref(sb)))
+        ws = torch.empty(sb.value, dtype=torch.uint8, device=dev)
+        _lib.check(lib.ngt_ppr_step_direct(rowptr.data_ptr(), col.data_ptr(), inv_deg.data_ptr(),
+                                           n_nodes, st_col.data_ptr(), st_val.data_ptr(),
+                                           st_cnt.data_ptr(), seeds.data_ptr(), B, K,
+                                           float(alpha), keep, int(max_mult), total,
+                                           nx_col.data_ptr(), nx_val.data_ptr(),
+                                           nx_cnt.data_ptr(), status.data_ptr(), ws.data_ptr(),
+                                           sb.value, stream))
+
     for _ in range(num_iterations):
         count(0, B, row_off)
-        offs = row_off.cpu()
-        total = int(offs[B])
-        if total <= max_products:
+        total = int(row_off[B])
+        if method == "direct":
+            step_direct(total)
+        elif total <= max_products:
             step(0, B, row_off, total)
         else:
+            offs = row_off.cpu()
             r0 = 0
             while r0 < B:
                 r1 = int(torch.searchsorted(offs, offs[r0] + max_products, right=True)) - 1
@@ -126,17 +191,24 @@ def appnp_batch(rowptr, col, inv_deg, n_nodes: int, seeds: torch.Tensor, alpha: 
         st_col, nx_col = nx_col, st_col
         st_val, nx_val = nx_val, st_val
         st_cnt, nx_cnt = nx_cnt, st_cnt
-    if int(status.item()):
-        raise IndexError(f"personalised PageRank: {int(status.item())} node ids out of range")
+    bad, disorder = status.tolist()
+    if bad:
+        raise IndexError(f"personalised PageRank: {bad} node ids out of range")
+    if disorder:
+        raise ValueError("personalised PageRank: CSR rows must list their columns in ascending "
+                         "order for the direct step (transition_csr sorts them), with no column "
+                         "repeated more than max_mult times")
     return st_col, st_val, st_cnt
 
 
 def personal_pagerank_appnp(edge_index, alpha, topk=100, num_iterations: int = 10,
                             batch_size: int = 8, device="cuda", csr_data=None,
                             num_nodes: int | None = None, iter_topk: int | None = None,
-                            source_start: int | None = None, source_end: int | None = None):
+                            source_start: int | None = None, source_end: int | None = None,
+                            method: str = "direct"):
     """The reference's APPNP backend (appnp_backend.py:227-310) on the GPU.
-    Returns (edge_index [2, nnz] int64 = (seed, node), values fp32)."""
+    Returns (edge_index [2, nnz] int64 = (seed, node), values fp32).
+    ``method``: the step's form, "direct" or "sort" (see appnp_batch)."""
     dev = torch.device(device)
     if dev.type != "cuda":
         raise RuntimeError("the APPNP backend runs on the GPU")
@@ -159,9 +231,11 @@ def personal_pagerank_appnp(edge_index, alpha, topk=100, num_iterations: int = 1
     K = min(iter_topk, n)
     final_keep = min(topk, K)
     idx_out, val_out = [], []
+    mult = max_repeats(rowptr, col) if method == "direct" else None
     for s0 in range(start, end, batch_size):
         seeds = torch.arange(s0, min(s0 + batch_size, end), dtype=torch.long, device=dev)
-        cols, vals, cnt = appnp_batch(rowptr, col, inv_deg, n, seeds, alpha, K, num_iterations)
+        cols, vals, cnt = appnp_batch(rowptr, col, inv_deg, n, seeds, alpha, K, num_iterations,
+                                      method=method, max_mult=mult)
         cnt = cnt.clamp(max=final_keep).long()
         mask = torch.arange(K, device=dev)[None, :] < cnt[:, None]
         idx_out.append(torch.stack([seeds.repeat_interleave(cnt), cols[mask].long()]))

@@ -93,6 +93,18 @@ def test_argument_errors_are_reported_without_touching_the_gpu():
     rc = lib.ngt_dense_bias_softmax_fwd(2, -1, 4, 8, None, 1.0, None, None, 0.0, 0, None, None,
                                         None, None, None)
     assert rc == 1 and b"bad sizes" in lib.ngt_last_error()
+    # the direct PPR step: K range, a total below one entry per row, and
+    # counts past its int32 chunk ids are refused before anything launches
+    for K, total, n_rows in ((0, 4, 4), (65, 4, 4), (5, 3, 4)):
+        rc = lib.ngt_ppr_step_direct(None, None, None, 10, None, None, None, None, n_rows, K,
+                                     0.85, 0.15, 1, total, None, None, None, None, None, 0, None)
+        assert rc == 1 and b"ngt_ppr_step_direct" in lib.ngt_last_error()
+    rc = lib.ngt_ppr_step_direct(1, 1, 1, 10, 1, 1, 1, 1, 4, 5, 0.85, 0.15, -1, 8, 1, 1, 1, 1,
+                                 None, 0, None)
+    assert rc == 1
+    rc = lib.ngt_ppr_step_direct(1, 1, 1, 10, 1, 1, 1, 1, 4, 5, 0.85, 0.15, 1, 1 << 41, 1, 1, 1,
+                                 1, None, 0, None)
+    assert rc == 2 and b"too large" in lib.ngt_last_error()
     with pytest.raises(_lib.NGTError):
         _lib.check(1)
 
