@@ -439,62 +439,132 @@ __device__ __forceinline__ int32_t clamp_i32(int64_t v) {
   return v < INT32_MIN ? INT32_MIN : (v > INT32_MAX ? INT32_MAX : int32_t(v));
 }
 
-// chunks per row: the sum over its state lists of ceil(length / kDirChunk),
-// at least 1 (the teleport entry)
-__global__ void k_ppr_chunks(const int64_t* __restrict__ rowptr, int64_t n_nodes,
-                             const int32_t* __restrict__ st_col, const int32_t* __restrict__ st_cnt,
-                             int32_t n_rows, int32_t K, int32_t* __restrict__ nch) {
-  const int64_t r = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
-  if (r > n_rows) return;
-  if (r == n_rows) {
-    nch[r] = 0;
-    return;
-  }
-  int64_t c = 0;
-  const int n = st_cnt[r];
-  if (n >= 0 && n <= K) {
-    for (int j = 0; j < n; ++j) {
-      const int32_t cl = st_col[r * K + j];
-      if (cl < 0 || cl >= n_nodes) continue;
-      const int64_t d = rowptr[cl + 1] - rowptr[cl];
-      if (d > 0) c += (d + kDirChunk - 1) / kDirChunk;
+// cnt[u] = the number of entries equal to x[u] in a slice of m >= 1 sorted
+// columns, for every u with act[u]: at stage[so ..] (staged, int32) or at
+// col[lo ..].  Branchless lower bounds with one trip count for all u, so the
+// U searches' loads are in flight together.
+template <int U>
+__device__ __forceinline__ void slice_counts(const int32_t* stage, const int64_t* __restrict__ col,
+                                             bool staged, int32_t so, int64_t lo, int64_t m,
+                                             const int32_t (&x)[U], const bool (&act)[U],
+                                             int32_t (&cnt)[U]) {
+  if (staged) {
+    int32_t a[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) a[u] = so;
+    for (int32_t len = int32_t(m); len > 1;) {
+      const int32_t half = len >> 1;
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (act[u]) a[u] = stage[a[u] + half] < x[u] ? a[u] + half : a[u];
+      len -= half;
+    }
+    const int32_t e = so + int32_t(m);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      cnt[u] = 0;
+      if (!act[u]) continue;
+      int32_t q = a[u] + (stage[a[u]] < x[u] ? 1 : 0);
+      for (; q < e && stage[q] == x[u]; ++q) ++cnt[u];
+    }
+  } else {
+    int64_t a[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) a[u] = lo;
+    for (int64_t len = m; len > 1;) {
+      const int64_t half = len >> 1;
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (act[u]) a[u] = col[a[u] + half] < x[u] ? a[u] + half : a[u];
+      len -= half;
+    }
+    const int64_t e = lo + m;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      cnt[u] = 0;
+      if (!act[u]) continue;
+      int64_t q = a[u] + (col[a[u]] < x[u] ? 1 : 0);
+      for (; q < e && col[q] == x[u]; ++q) ++cnt[u];
     }
   }
-  nch[r] = c > 0 ? int32_t(c) : 1;
 }
 
-// status[0]: bad neighbour ids and seeds; status[1]: CSR rows out of order,
-// a column repeated more than max_mult times, or chunk counts past the bound
-__global__ __launch_bounds__(kBlock) void k_ppr_direct(
+// For every list l < n whose lane sets `need`: slo and shi on lane l become
+// the first entry of list l (col[lb, lb + ll), ascending) >= vlo and > vhi;
+// 0 on the other lanes.  With n <= 32, G lanes per (list, bound) run a
+// (G+1)-way search together, each round testing G pivots of the open range;
+// above that, each lane runs both binary searches itself.  Every lane takes
+// part in every shuffle.
+__device__ __forceinline__ void coop_slices(const int64_t* __restrict__ col, int n, bool need,
+                                            int64_t lb, int64_t ll, int64_t vlo, int64_t vhi,
+                                            int lane, int64_t& slo, int64_t& shi) {
+  slo = shi = 0;
+  if (n <= kWave / 2) {
+    const int G = kWave / (2 * (n > 0 ? n : 1));
+    const int g = lane / G, k = lane % G;
+    const int jj = g >> 1, bnd = g & 1;  // group 2 jj + b: list jj, bound b (0: >= vlo, 1: > vhi)
+    const bool mine = g < 2 * n;
+    const int src = mine ? jj : 0;
+    const bool nd = __shfl(int(need), src, kWave) != 0 && mine;
+    int64_t L = __shfl(lb, src, kWave);
+    const int64_t len = __shfl(ll, src, kWave);
+    int64_t R = nd ? L + len : L;
+    const int64_t x = bnd ? vhi : vlo;
+    const uint64_t gmask = mine ? (((1ull << G) - 1ull) << (g * G)) : 0ull;
+    while (__ballot(R > L)) {
+      const int64_t piv = L + ((R - L) * (k + 1)) / (G + 1);  // in [L, R) when R > L
+      bool right = false;  // the answer lies after piv
+      if (R > L) {
+        const int64_t v = col[piv];
+        right = bnd ? v <= x : v < x;
+      }
+      const uint64_t bal = __ballot(right) & gmask;
+      const int cnt = __popcll(bal);  // the group's pivots ascend: a prefix goes right
+      const int64_t lo_p = __shfl(piv, g * G + (cnt > 0 ? cnt - 1 : 0), kWave);
+      const int64_t hi_p = __shfl(piv, g * G + (cnt < G ? cnt : G - 1), kWave);
+      if (R > L) {
+        if (cnt > 0) L = lo_p + 1;
+        if (cnt < G) R = hi_p;
+      }
+    }
+    slo = __shfl(L, (2 * lane) * G < kWave ? (2 * lane) * G : 0, kWave);
+    shi = __shfl(L, (2 * lane + 1) * G < kWave ? (2 * lane + 1) * G : 0, kWave);
+    if (!need) slo = shi = 0;
+  } else if (need) {
+    int64_t a = lb, c = lb;
+    for (int64_t len = ll; len > 1;) {
+      const int64_t half = len >> 1;
+      a = col[a + half] < vlo ? a + half : a;
+      c = col[c + half] <= vhi ? c + half : c;
+      len -= half;
+    }
+    slo = a + (col[a] < vlo ? 1 : 0);
+    shi = c + (col[c] <= vhi ? 1 : 0);
+  }
+}
+
+// Per row, one wave: the table of its state lists (begin, length, first and
+// last column, weight w_j = st_val * inv_deg, the same fp32 product the chunks
+// would form), its chunk count (the sum over its lists of ceil(length /
+// kDirChunk), at least 1 for the teleport entry) and whether a list holds the
+// seed.  Wave n_rows writes the count slot the scan turns into the total.
+__global__ __launch_bounds__(kBlock) void k_ppr_rows(
     const int64_t* __restrict__ rowptr, const int64_t* __restrict__ col,
     const float* __restrict__ inv_deg, int64_t n_nodes, const int32_t* __restrict__ st_col,
     const float* __restrict__ st_val, const int32_t* __restrict__ st_cnt,
-    const int64_t* __restrict__ seeds, int32_t n_rows, int32_t K, float alpha, float keep,
-    int32_t max_mult, const int32_t* __restrict__ chunk_off, int32_t max_chunks,
-    float* __restrict__ part_val, int32_t* __restrict__ part_col, int32_t* __restrict__ part_cnt,
+    const int64_t* __restrict__ seeds, int32_t n_rows, int32_t K, int64_t* __restrict__ tl_b,
+    int64_t* __restrict__ tl_len, int64_t* __restrict__ tl_first, int64_t* __restrict__ tl_last,
+    float* __restrict__ tl_w, int32_t* __restrict__ nch, int32_t* __restrict__ seed_in,
     int32_t* status) {
-#pragma clang fp contract(off)
-  __shared__ int32_t stage_all[kWaves][kDirStage];
-  const int32_t w = __builtin_amdgcn_readfirstlane(int(blockIdx.x * kWaves + (threadIdx.x >> 6)));
+  const int32_t r = __builtin_amdgcn_readfirstlane(int(blockIdx.x * kWaves + (threadIdx.x >> 6)));
   const int lane = threadIdx.x & (kWave - 1);
-  int32_t* stage = stage_all[threadIdx.x >> 6];
-  const int32_t n_chunks = __builtin_amdgcn_readfirstlane(chunk_off[n_rows]);
-  if (n_chunks > max_chunks) {
-    if (w == 0 && lane == 0) atomicAdd(status + 1, 1);
+  if (r > n_rows) return;
+  if (r == n_rows) {
+    if (lane == 0) nch[r] = 0;
     return;
   }
-  if (w >= n_chunks) return;
-  // the row: chunk_off[r] <= w < chunk_off[r + 1] (every row has a chunk)
-  int32_t lo = 0, hi = n_rows;
-  while (hi - lo > 1) {
-    const int32_t mid = (lo + hi) >> 1;
-    if (chunk_off[mid] <= w) lo = mid; else hi = mid;
-  }
-  const int32_t r = __builtin_amdgcn_readfirstlane(lo);
-  const int32_t ci = w - __builtin_amdgcn_readfirstlane(chunk_off[r]);
   int n = __builtin_amdgcn_readfirstlane(st_cnt[r]);
   if (n < 0 || n > K) n = 0;
-  // lane j < n holds list j: begin, length, weight, first and last column
   int64_t lb = 0, ll = 0, lfirst = 0, llast = -1;
   float lw = 0.f;
   if (lane < n) {
@@ -509,6 +579,66 @@ __global__ __launch_bounds__(kBlock) void k_ppr_direct(
         llast = col[e - 1];
       }
     }
+    const int64_t at = int64_t(r) * K + lane;
+    tl_b[at] = lb;
+    tl_len[at] = ll;
+    tl_first[at] = lfirst;
+    tl_last[at] = llast;
+    tl_w[at] = lw;
+  }
+  int64_t c = (ll + kDirChunk - 1) / kDirChunk;
+  for (int off = 32; off > 0; off >>= 1) c += __shfl_xor(c, off, kWave);
+  const int64_t sd = seeds[r];
+  const bool seed_ok = sd >= 0 && sd < n_nodes;
+  int64_t slo, shi;
+  coop_slices(col, n, seed_ok && lane < n && ll > 0 && sd >= lfirst && sd <= llast, lb, ll, sd,
+              sd, lane, slo, shi);
+  const bool found = __ballot(shi > slo) != 0;
+  if (lane == 0) {
+    nch[r] = c > 0 ? int32_t(c) : 1;
+    seed_in[r] = found ? 1 : 0;
+    if (!seed_ok) atomicAdd(status, 1);
+  }
+}
+
+// row_of[c] = the row of chunk c (c < max_chunks), one thread per row
+__global__ void k_ppr_chunk_rows(const int32_t* __restrict__ chunk_off, int32_t n_rows,
+                                 int32_t max_chunks, int32_t* __restrict__ row_of) {
+  const int64_t r = blockIdx.x * int64_t(blockDim.x) + threadIdx.x;
+  if (r >= n_rows) return;
+  const int32_t e = chunk_off[r + 1] < max_chunks ? chunk_off[r + 1] : max_chunks;
+  for (int32_t c = chunk_off[r]; c < e; ++c) row_of[c] = int32_t(r);
+}
+
+// One chunk w (uniform) of the direct step, on one wave whose LDS slice
+// buffer is `stage`.  status[0]: bad neighbour ids and seeds; status[1]: CSR
+// rows out of order or a column repeated more than max_mult times.
+__device__ __forceinline__ void ppr_chunk(
+    const int64_t* __restrict__ rowptr, const int64_t* __restrict__ col,
+    const float* __restrict__ inv_deg, int64_t n_nodes, const int32_t* __restrict__ st_col,
+    const float* __restrict__ st_val, const int32_t* __restrict__ st_cnt,
+    const int64_t* __restrict__ seeds, int32_t n_rows, int32_t K, float alpha, float keep,
+    int32_t max_mult, const int32_t* __restrict__ chunk_off, const int32_t* __restrict__ row_of,
+    const int64_t* __restrict__ tl_b, const int64_t* __restrict__ tl_len,
+    const int64_t* __restrict__ tl_first, const int64_t* __restrict__ tl_last,
+    const float* __restrict__ tl_w, const int32_t* __restrict__ seed_in,
+    float* __restrict__ part_val, int32_t* __restrict__ part_col, int32_t* __restrict__ part_cnt,
+    int32_t* status, const int32_t w, const int lane, int32_t* stage) {
+#pragma clang fp contract(off)
+  const int32_t r = __builtin_amdgcn_readfirstlane(row_of[w]);
+  const int32_t ci = w - __builtin_amdgcn_readfirstlane(chunk_off[r]);
+  int n = __builtin_amdgcn_readfirstlane(st_cnt[r]);
+  if (n < 0 || n > K) n = 0;
+  // lane j < n holds list j: begin, length, weight, first and last column
+  int64_t lb = 0, ll = 0, lfirst = 0, llast = -1;
+  float lw = 0.f;
+  if (lane < n) {
+    const int64_t at = int64_t(r) * K + lane;
+    lb = tl_b[at];
+    ll = tl_len[at];
+    lfirst = tl_first[at];
+    llast = tl_last[at];
+    lw = tl_w[at];
   }
   // this chunk's list j: the last nonempty list whose first chunk is <= ci
   const int32_t cj = int32_t((ll + kDirChunk - 1) / kDirChunk);
@@ -536,10 +666,9 @@ __global__ __launch_bounds__(kBlock) void k_ppr_direct(
   // every other list's slice [slo, shi) of columns in [vmin, vmax], and where
   // it is staged: at soff in the wave's LDS when the slices up to it fit
   int64_t slo = 0, shi = 0;
-  if (j >= 0 && lane < n && lane != j && ll > 0 && vmax >= lfirst && vmin <= llast) {
-    slo = col_bound<false>(col, lb, lb + ll, vmin);
-    shi = col_bound<true>(col, slo, lb + ll, vmax);
-  }
+  const bool need = j >= 0 && lane < n && lane != j && ll > 0 && vmax >= lfirst && vmin <= llast;
+  coop_slices(col, n, need, lb, ll, vmin, vmax, lane, slo, shi);
+  if (shi < slo) shi = slo;  // rows out of order (flagged where they are read)
   const int64_t sm = shi - slo;
   int64_t sinc = sm;
   for (int off = 1; off < kWave; off <<= 1) {
@@ -551,15 +680,26 @@ __global__ __launch_bounds__(kBlock) void k_ppr_direct(
   const int32_t soff = staged ? int32_t(soff64) : 0;
   const uint64_t stm = __ballot(staged);
   const int32_t n_stage = stm ? int32_t(lane_i64(sinc, 63 - __clzll(stm))) : 0;
-  for (int32_t f0 = 0; f0 < n_stage; f0 += kWave) {  // uniform trips: every lane shuffles
-    const int32_t f = f0 + lane;
-    // the slice holding entry f: the last lane whose slice starts at or before f
-    int sl = 0;
+  constexpr int kStageU = 8;  // entries per lane in flight
+  for (int32_t f0 = 0; f0 < n_stage; f0 += kWave * kStageU) {  // uniform: every lane shuffles
+    int64_t src[kStageU];
 #pragma unroll
-    for (int h = kWave / 2; h > 0; h >>= 1)
-      if (__shfl(soff64, sl + h, kWave) <= f) sl += h;
-    const int64_t src = __shfl(slo, sl, kWave) + (f - __shfl(soff64, sl, kWave));
-    if (f < n_stage) stage[f] = clamp_i32(col[src]);
+    for (int k = 0; k < kStageU; ++k) {
+      const int32_t f = f0 + k * kWave + lane;
+      // the slice holding entry f: the last lane whose slice starts at or before f
+      int sl = 0;
+#pragma unroll
+      for (int h = kWave / 2; h > 0; h >>= 1)
+        if (__shfl(soff64, sl + h, kWave) <= f) sl += h;
+      src[k] = __shfl(slo, sl, kWave) + (f - __shfl(soff64, sl, kWave));
+    }
+    int64_t v[kStageU];
+#pragma unroll
+    for (int k = 0; k < kStageU; ++k)
+      if (f0 + k * kWave + lane < n_stage) v[k] = col[src[k]];
+#pragma unroll
+    for (int k = 0; k < kStageU; ++k)
+      if (f0 + k * kWave + lane < n_stage) stage[f0 + k * kWave + lane] = clamp_i32(v[k]);
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -596,23 +736,6 @@ __global__ __launch_bounds__(kBlock) void k_ppr_direct(
     }
     own[u] = o;
   }
-
-  // find column x in list jj's slice: count of its entries (0: absent)
-  auto slice_count = [&](bool st, int32_t so, int64_t lo_, int64_t hi_, int32_t x) -> int32_t {
-    int32_t c = 0;
-    if (st) {
-      int32_t a = so, len = int32_t(hi_ - lo_);
-      while (len > 0) {
-        const int32_t half = len >> 1;
-        if (stage[a + half] < x) { a += half + 1; len -= half + 1; } else len = half;
-      }
-      for (const int32_t e = so + int32_t(hi_ - lo_); a < e && stage[a] == x; ++a) ++c;
-    } else {
-      int64_t a = col_bound<false>(col, lo_, hi_, x);
-      for (; a < hi_ && col[a] == x; ++a) ++c;
-    }
-    return c;
-  };
 
   bool prune = j >= 0 && max_mult > 0 && int64_t(max_mult) * K <= 4096 && keep >= 0.f &&
                alpha >= 0.f;
@@ -656,12 +779,16 @@ __global__ __launch_bounds__(kBlock) void k_ppr_direct(
       if (m == 0) continue;
       const bool st = __builtin_amdgcn_readlane(int(staged), jj) != 0;
       const int32_t so = __builtin_amdgcn_readlane(soff, jj);
-      const int64_t lo_ = lane_i64(slo, jj), hi_ = lo_ + m;
+      const int64_t lo_ = lane_i64(slo, jj);
       const double mwj = double(max_mult) * double(lane_f32(lw, jj));
+      bool act[kDirU];
+      int32_t cnt[kDirU];
+#pragma unroll
+      for (int u = 0; u < kDirU; ++u) act[u] = alive[u] && !(seed_ok && nv[u] == sd);
+      slice_counts<kDirU>(stage, col, st, so, lo_, m, nv, act, cnt);
 #pragma unroll
       for (int u = 0; u < kDirU; ++u) {
-        if (!alive[u] || (seed_ok && nv[u] == sd)) continue;
-        if (slice_count(st, so, lo_, hi_, nv[u]) > 0) continue;  // held: the bound stays
+        if (!act[u] || cnt[u] > 0) continue;  // held: the bound stays
         bnd[u] -= mwj;
         if (bnd[u] + err < cut) alive[u] = false;
       }
@@ -683,12 +810,14 @@ __global__ __launch_bounds__(kBlock) void k_ppr_direct(
     if (m == 0) continue;
     const bool st = __builtin_amdgcn_readlane(int(staged), jj) != 0;
     const int32_t so = __builtin_amdgcn_readlane(soff, jj);
-    const int64_t lo_ = lane_i64(slo, jj), hi_ = lo_ + m;
+    const int64_t lo_ = lane_i64(slo, jj);
     const float wj = lane_f32(lw, jj);
+    int32_t cnt[kDirU];
+    slice_counts<kDirU>(stage, col, st, so, lo_, m, nv, own, cnt);
 #pragma unroll
     for (int u = 0; u < kDirU; ++u) {
       if (!own[u]) continue;
-      const int32_t c = slice_count(st, so, lo_, hi_, nv[u]);
+      const int32_t c = cnt[u];
       if (c == 0) continue;
       if (jj < j) {
         own[u] = false;  // an earlier list holds it
@@ -707,21 +836,10 @@ __global__ __launch_bounds__(kBlock) void k_ppr_direct(
   cv[kDirU] = -INFINITY;
   cc[kDirU] = INT32_MAX;
   bool extra = false;
-  if (ci == 0) {  // the teleport entry alone when no list holds the seed
-    if (!seed_ok) {
-      if (lane == 0) atomicAdd(status, 1);
-    } else {
-      bool found = false;
-      if (ll > 0 && sd >= lfirst && sd <= llast) {
-        const int64_t a = col_bound<false>(col, lb, lb + ll, sd);
-        found = a < lb + ll && col[a] == sd;
-      }
-      if (__ballot(found) == 0 && lane == 0) {
-        cv[kDirU] = scale_then_add(0.f, keep, alpha, true);
-        cc[kDirU] = int32_t(sd);
-        extra = true;
-      }
-    }
+  if (ci == 0 && seed_ok && !seed_in[r] && lane == 0) {  // the teleport entry alone
+    cv[kDirU] = scale_then_add(0.f, keep, alpha, true);
+    cc[kDirU] = int32_t(sd);
+    extra = true;
   }
   int real = 0;
 #pragma unroll
@@ -756,6 +874,33 @@ __global__ __launch_bounds__(kBlock) void k_ppr_direct(
     pc = bc;
   }
   if (lane == 0) part_cnt[w] = n_out;
+}
+
+// One wave per chunk.  status[1] also flags chunk counts past the bound the
+// workspace was sized for (nothing is then written).
+__global__ __launch_bounds__(kBlock) void k_ppr_direct(
+    const int64_t* __restrict__ rowptr, const int64_t* __restrict__ col,
+    const float* __restrict__ inv_deg, int64_t n_nodes, const int32_t* __restrict__ st_col,
+    const float* __restrict__ st_val, const int32_t* __restrict__ st_cnt,
+    const int64_t* __restrict__ seeds, int32_t n_rows, int32_t K, float alpha, float keep,
+    int32_t max_mult, const int32_t* __restrict__ chunk_off, int32_t max_chunks,
+    const int32_t* __restrict__ row_of, const int64_t* __restrict__ tl_b,
+    const int64_t* __restrict__ tl_len, const int64_t* __restrict__ tl_first,
+    const int64_t* __restrict__ tl_last, const float* __restrict__ tl_w,
+    const int32_t* __restrict__ seed_in, float* __restrict__ part_val,
+    int32_t* __restrict__ part_col, int32_t* __restrict__ part_cnt, int32_t* status) {
+  __shared__ int32_t stage_all[kWaves][kDirStage];
+  const int32_t w = __builtin_amdgcn_readfirstlane(int(blockIdx.x * kWaves + (threadIdx.x >> 6)));
+  const int lane = threadIdx.x & (kWave - 1);
+  const int32_t n_chunks = __builtin_amdgcn_readfirstlane(chunk_off[n_rows]);
+  if (n_chunks > max_chunks) {
+    if (w == 0 && lane == 0) atomicAdd(status + 1, 1);
+    return;
+  }
+  if (w >= n_chunks) return;
+  ppr_chunk(rowptr, col, inv_deg, n_nodes, st_col, st_val, st_cnt, seeds, n_rows, K, alpha, keep,
+            max_mult, chunk_off, row_of, tl_b, tl_len, tl_first, tl_last, tl_w, seed_in, part_val,
+            part_col, part_cnt, status, w, lane, stage_all[threadIdx.x >> 6]);
 }
 
 // One wave per row: the best K of its chunks' best K.
@@ -817,7 +962,8 @@ __global__ __launch_bounds__(kBlock) void k_ppr_merge(
 }
 
 struct DirectLayout {
-  size_t nch, chunk_off, temp, temp_bytes, part_val, part_col, part_cnt, total;
+  size_t nch, chunk_off, temp, temp_bytes, row_of, tl_b, tl_len, tl_first, tl_last, tl_w, seed_in,
+      part_val, part_col, part_cnt, total;
   int64_t max_chunks;
 };
 
@@ -840,6 +986,13 @@ int direct_layout(int64_t total, int32_t n_rows, int32_t K, DirectLayout* L) {
   L->chunk_off = take((m + 1) * 4);
   L->temp_bytes = scan_bytes;
   L->temp = take(scan_bytes);
+  L->row_of = take(c * 4);
+  L->tl_b = take(m * size_t(K) * 8);
+  L->tl_len = take(m * size_t(K) * 8);
+  L->tl_first = take(m * size_t(K) * 8);
+  L->tl_last = take(m * size_t(K) * 8);
+  L->tl_w = take(m * size_t(K) * 4);
+  L->seed_in = take(m * 4);
   L->part_val = take(c * size_t(K) * 4);
   L->part_col = take(c * size_t(K) * 4);
   L->part_cnt = take(c * 4);
@@ -989,16 +1142,28 @@ extern "C" int ngt_ppr_step_direct(const int64_t* rowptr, const int64_t* col,
   int32_t* part_col = reinterpret_cast<int32_t*>(ws + L.part_col);
   int32_t* part_cnt = reinterpret_cast<int32_t*>(ws + L.part_cnt);
   KernelTimer timer_("ppr_step", s);
-  hipLaunchKernelGGL(k_ppr_chunks, dim3((n_rows + kBlock) / kBlock), dim3(kBlock), 0, s, rowptr,
-                     n_nodes, st_col, st_cnt, n_rows, K, nch);
+  int64_t* tl_b = reinterpret_cast<int64_t*>(ws + L.tl_b);
+  int64_t* tl_len = reinterpret_cast<int64_t*>(ws + L.tl_len);
+  int64_t* tl_first = reinterpret_cast<int64_t*>(ws + L.tl_first);
+  int64_t* tl_last = reinterpret_cast<int64_t*>(ws + L.tl_last);
+  float* tl_w = reinterpret_cast<float*>(ws + L.tl_w);
+  int32_t* seed_in = reinterpret_cast<int32_t*>(ws + L.seed_in);
+  int32_t* row_of = reinterpret_cast<int32_t*>(ws + L.row_of);
+  const int32_t max_chunks = int32_t(L.max_chunks);
+  hipLaunchKernelGGL(k_ppr_rows, dim3(grid_waves(int64_t(n_rows) + 1)), dim3(kBlock), 0, s,
+                     rowptr, col, inv_deg, n_nodes, st_col, st_val, st_cnt, seeds, n_rows, K,
+                     tl_b, tl_len, tl_first, tl_last, tl_w, nch, seed_in, status);
   NGT_HIP_CHECK(hipGetLastError());
   size_t tb = L.temp_bytes;
   NGT_HIP_CHECK(rocprim::exclusive_scan(ws + L.temp, tb, nch, chunk_off, int32_t(0),
                                         size_t(n_rows) + 1, rocprim::plus<int32_t>(), s));
+  hipLaunchKernelGGL(k_ppr_chunk_rows, dim3((n_rows + kBlock - 1) / kBlock), dim3(kBlock), 0, s,
+                     chunk_off, n_rows, max_chunks, row_of);
+  NGT_HIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL(k_ppr_direct, dim3(grid_waves(L.max_chunks)), dim3(kBlock), 0, s, rowptr,
                      col, inv_deg, n_nodes, st_col, st_val, st_cnt, seeds, n_rows, K, alpha, keep,
-                     max_mult, chunk_off, int32_t(L.max_chunks), part_val, part_col, part_cnt,
-                     status);
+                     max_mult, chunk_off, max_chunks, row_of, tl_b, tl_len, tl_first, tl_last,
+                     tl_w, seed_in, part_val, part_col, part_cnt, status);
   NGT_HIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL(k_ppr_merge, dim3(grid_waves(n_rows)), dim3(kBlock), 0, s, chunk_off,
                      int32_t(L.max_chunks), part_val, part_col, part_cnt, n_rows, K, out_col,
