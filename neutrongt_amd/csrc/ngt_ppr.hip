@@ -7,7 +7,10 @@
 // with P[c, n] = 1 / max(deg(c), 1) for every edge c -> n of the graph CSR.
 //
 // The state is fixed-width: row r holds cnt[r] <= K entries (col, val) in
-// rank order (value descending, then column ascending).  A step is
+// rank order (value descending, then column ascending).  Two forms of the
+// step give the same bits: the direct evaluation further down
+// (ngt_ppr_step_direct, no product list) and the sorted product list
+// (ngt_ppr_step), which is
 //   1. count:   per row, the number of products sum_j deg(col_j) plus one
 //               teleport entry; an exclusive scan gives each row's range;
 //   2. expand:  one wave per row writes, in order j = 0 .. cnt-1 and CSR order
