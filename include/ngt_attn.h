@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define NGT_ABI_VERSION 10
+#define NGT_ABI_VERSION 11
 
 #define NGT_F32 0
 #define NGT_BF16 1
@@ -641,6 +641,17 @@ int ngt_add_layernorm_bwd(int dtype, const void* sum, int grad_dtype, const void
 int ngt_colsum_workspace_bytes(int64_t n_rows, int32_t n_cols, size_t* bytes);
 int ngt_colsum_bf16(const void* dy, int64_t n_rows, int32_t n_cols, float* out, void* workspace,
                     size_t workspace_bytes, void* stream);
+
+/*
+ * out[i] = sum over c = 0 .. n_chunks-1, in that order, of in[c * n + i]
+ * (fp32; in is [n_chunks, n] row-major, out [n]; n_chunks >= 1).  The sum of
+ * the row-chunk partials of the encoder's split-K weight gradient dW = dY^T X
+ * (the autograd of nn.Linear's weight, NeutronGT/models/
+ * graphormer_dist_node_level.py:130-206): a batched GEMM leaves one partial
+ * dW per chunk of rows.  16-byte loads when n is a multiple of 4 and both
+ * pointers are 16-byte aligned; the same order either way.
+ */
+int ngt_chunk_sum_f32(const float* in, int32_t n_chunks, int64_t n, float* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libngt_attn.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 NGT_F32 = 0
 NGT_BF16 = 1
@@ -133,6 +133,7 @@ SIGNATURES = {
                               _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
     "ngt_colsum_workspace_bytes": [_i64, _i32, _psz],
     "ngt_colsum_bf16": [_vp, _i64, _i32, _vp, _vp, _sz, _vp],
+    "ngt_chunk_sum_f32": [_vp, _i32, _i64, _vp, _vp],
     "ngt_related_workspace_bytes": [_i32, _i32, _psz],
     "ngt_merge_related_nodes": [_vp, _vp, _vp, _i32, _vp, _i32, _i32, _vp, _vp, _vp, _sz, _vp],
     "ngt_adj_weights_workspace_bytes": [_i64, _i64, _psz],

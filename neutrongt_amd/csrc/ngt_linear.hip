@@ -119,10 +119,75 @@ int check(const char* fn, int64_t K, int n) {
   return NGT_OK;
 }
 
+// out[i] = sum over c = 0 .. n_chunks-1, in that order, of in[c * n + i]: the
+// row-chunk partials of the split-K weight gradient added up.  4 elements a
+// thread (one 16-byte load per chunk when n is a multiple of 4 and the
+// pointers 16-byte aligned), the loads of 4 chunks in flight at once.
+// HBM-bound: n_chunks * n * 4 bytes read, n * 4 written.
+template <bool VEC>
+__global__ __launch_bounds__(kBlock) void k_chunk_sum(const float* __restrict__ in,
+                                                       int32_t n_chunks, int64_t n,
+                                                       float* __restrict__ out) {
+  const int64_t stride = int64_t(gridDim.x) * kBlock * 4;
+  for (int64_t i = (blockIdx.x * int64_t(kBlock) + threadIdx.x) * 4; i < n; i += stride) {
+    if (VEC) {
+      float4 acc = *reinterpret_cast<const float4*>(in + i);
+      int32_t c = 1;
+      for (; c + 4 <= n_chunks; c += 4) {
+        float4 v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = *reinterpret_cast<const float4*>(in + (c + k) * n + i);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          acc.x += v[k].x;
+          acc.y += v[k].y;
+          acc.z += v[k].z;
+          acc.w += v[k].w;
+        }
+      }
+      for (; c < n_chunks; ++c) {
+        const float4 v = *reinterpret_cast<const float4*>(in + c * n + i);
+        acc.x += v.x;
+        acc.y += v.y;
+        acc.z += v.z;
+        acc.w += v.w;
+      }
+      *reinterpret_cast<float4*>(out + i) = acc;
+    } else {
+      for (int64_t e = i; e < i + 4 && e < n; ++e) {
+        float acc = in[e];
+        for (int32_t c = 1; c < n_chunks; ++c) acc += in[c * n + e];
+        out[e] = acc;
+      }
+    }
+  }
+}
+
 }  // namespace
 }  // namespace ngt
 
 using namespace ngt;
+
+extern "C" int ngt_chunk_sum_f32(const float* in, int32_t n_chunks, int64_t n, float* out,
+                                 void* stream) {
+  if (n_chunks < 1 || n < 0 || (n > 0 && (!in || !out)))
+    return set_error(NGT_ERR_ARG, "ngt_chunk_sum_f32: bad arguments");
+  if (n == 0) return NGT_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool vec = n % 4 == 0 && !(reinterpret_cast<uintptr_t>(in) & 15) &&
+                   !(reinterpret_cast<uintptr_t>(out) & 15);
+  int64_t blocks = (n + kBlock * 4 - 1) / (kBlock * 4);
+  if (blocks > 65536) blocks = 65536;
+  KernelTimer timer_("chunk_sum", st);
+  if (vec)
+    hipLaunchKernelGGL(k_chunk_sum<true>, dim3(unsigned(blocks)), dim3(kBlock), 0, st, in, n_chunks,
+                       n, out);
+  else
+    hipLaunchKernelGGL(k_chunk_sum<false>, dim3(unsigned(blocks)), dim3(kBlock), 0, st, in,
+                       n_chunks, n, out);
+  NGT_HIP_CHECK(hipGetLastError());
+  return NGT_OK;
+}
 
 extern "C" int ngt_colsum_workspace_bytes(int64_t n_rows, int32_t n_cols, size_t* bytes) {
   NGT_CHECK_OK(check("ngt_colsum_workspace_bytes", n_rows, n_cols));

@@ -11,7 +11,7 @@ and in the backward computes
   dX = dY W                          (torch GEMM, bf16, as autocast does),
   dW = sum_c dY_c^T X_c              (one batched library GEMM over 16 row
                                       chunks with fp32 output, then a sum in
-                                      chunk order: 63 us),
+                                      chunk order, ngt_chunk_sum_f32),
   db = column sums of dY             (ngt_colsum_bf16, fp32, fixed order).
 dW and db are fp32 (autocast's own backward rounds dW to bf16 first).
 Outside bf16 autocast or without gradients it is a plain nn.Linear.  Any
@@ -52,6 +52,19 @@ def colsum_bf16(dy: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def chunk_sum(parts: torch.Tensor) -> torch.Tensor:
+    """Sum over dim 0 of an fp32 GPU tensor, the slices added in order
+    (ngt_chunk_sum_f32)."""
+    lib = _lib.load()
+    if parts.dtype != torch.float32 or not parts.is_cuda or parts.dim() < 2:
+        raise TypeError("chunk_sum takes an fp32 GPU tensor with a leading chunk dimension")
+    parts = parts.contiguous()
+    out = torch.empty(parts.shape[1:], dtype=torch.float32, device=parts.device)
+    _lib.check(lib.ngt_chunk_sum_f32(parts.data_ptr(), parts.shape[0], out.numel(),
+                                     out.data_ptr(), _lib.stream_ptr(parts.device)))
+    return out
+
+
 def weight_grad(x: torch.Tensor, dy: torch.Tensor) -> torch.Tensor:
     """dY^T X in fp32 for bf16 x [K, n_in], dy [K, n_out], split over rows.
     Outputs of 1.5 M elements or more (the stacked Q/K/V gradient, 2,304 x
@@ -66,8 +79,8 @@ def weight_grad(x: torch.Tensor, dy: torch.Tensor) -> torch.Tensor:
         if splits == 1:
             return torch.mm(dy.t(), x, out_dtype=torch.float32)
         # left operand transposed, right operand contiguous row chunks
-        dw = torch.bmm(dy[:main].view(splits, c, -1).transpose(1, 2),
-                       x[:main].view(splits, c, -1), out_dtype=torch.float32).sum(0)
+        dw = chunk_sum(torch.bmm(dy[:main].view(splits, c, -1).transpose(1, 2),
+                                 x[:main].view(splits, c, -1), out_dtype=torch.float32))
         if main < K:
             dw += torch.mm(dy[main:].t(), x[main:], out_dtype=torch.float32)
     return dw

@@ -8,7 +8,7 @@ import pytest
 import torch
 import torch.nn as nn
 
-from neutrongt_amd.linear import WgradLinear, colsum_bf16, weight_grad
+from neutrongt_amd.linear import WgradLinear, chunk_sum, colsum_bf16, weight_grad
 from tests._util import relerr
 
 pytestmark = pytest.mark.gpu
@@ -47,6 +47,26 @@ def test_colsum_edge_cases():
     for n in (1, 7, 47, 100, 263):
         dy = torch.randn(1000, n, device="cuda").to(torch.bfloat16)
         assert relerr(colsum_bf16(dy), dy.double().sum(0)) < 1e-5, n
+
+
+@pytest.mark.parametrize("chunks,n", [(1, 12), (3, 10), (4, 589824), (5, 7), (16, 589824),
+                                      (17, 1001), (8, 2304 * 768)])
+def test_chunk_sum_adds_the_chunks_in_order(chunks, n):
+    """ngt_chunk_sum_f32 equals a sequential fp32 sum over the chunks, chunk 0
+    first, bit for bit, with 16-byte and with scalar loads."""
+    _say(f"case chunk_sum chunks={chunks} n={n}")
+    g = torch.Generator(device="cuda").manual_seed(chunks * 7 + n)
+    parts = torch.randn(chunks, n, device="cuda", generator=g) * torch.logspace(
+        -3, 3, chunks, device="cuda")[:, None]
+    want = parts[0].clone()
+    for c in range(1, chunks):
+        want = want + parts[c]  # one fp32 rounding per chunk, in order
+    got = chunk_sum(parts)
+    assert torch.equal(got, want)
+    buf = torch.empty(chunks * n + 1, device="cuda")
+    odd = buf[1:].view(chunks, n)  # 4 bytes in: scalar loads
+    odd.copy_(parts)
+    assert torch.equal(chunk_sum(odd), want)
 
 
 @pytest.mark.parametrize("n_in,n_out", [(100, 768), (768, 47)])
