@@ -394,26 +394,30 @@ int ppr_sort_reduce(const int64_t* rowptr, const int64_t* col, const float* inv_
 // row's chunks are its lists' chunks in rank order, at least one per row for
 // the teleport entry).  A chunk's columns lie in [vmin, vmax], its first and
 // last entry, so each other list is searched once per chunk for the slice of
-// entries in that interval (one lane per list, all lists at once); the slices
-// are staged in LDS as int32 and the per-column searches run there (slices
-// that do not fit search their part of global memory).  Each chunk keeps its
-// best K (value descending, column ascending); a per-row merge takes the best
-// K of its chunks', which is the best K of the row whatever the chunking.
+// entries in that interval (a cooperative search, all lists at once); the
+// per-column lookups then run inside those slices.  The columns a bound does
+// not rule out are compacted and summed exactly.  Each chunk keeps its best K
+// (value descending, column ascending); a per-row merge takes the best K of
+// its chunks', which is the best K of the row whatever the chunking.
 //
 // Pruning, which changes no result.  With nonnegative weights, keep and
 // alpha, a column's value is at least fl(w_j * keep) for every list j that
-// holds it (fp32 sums of nonnegative terms only grow), and a list of at least
-// K * M entries, M the most repeats of one column within a CSR row, holds K
-// distinct columns: so the row's K-th best value is at least tau, the largest
-// fl(w_j * keep) over such lists.  A column whose value is shown to lie below
-// tau cannot be among the row's best K.  Its upper bound is keep times the
-// sum of M * w over the lists whose slice may hold it, less the lists a
-// search has ruled out, heaviest first, with fp32's rounding of the exact sum
-// (at most K * M + 1 roundings) covered by a factor 1 + 2^-10.
+// holds it (fp32 sums of nonnegative terms only grow), and a list of L
+// entries holds at least ceil(L / M) distinct columns, M the most repeats of
+// one column within a CSR row.  So if the i heaviest lists together are sure
+// to hold K distinct columns (the most of their ceil(L / M), plus the seed
+// when no list holds it and alpha is at least the bound), the row's K-th best
+// value is at least tau = fl(w_(i) * keep) for the first such i.  A column
+// whose value is shown to lie below tau cannot be among the row's best K.
+// A column's upper bound is keep times: its own list's repeats times w_j,
+// plus the exact share of the lists whose slice holds at most kDirRev entries
+// (each slice entry looked up among the chunk's columns adds its w), plus
+// M * w for every larger non-empty slice; fp32's rounding of the exact sum
+// (at most K * M + 1 roundings) is covered by a factor 1 + 2^-10.
 
 constexpr int kDirU = 8;                                 // entries per lane
 constexpr int64_t kDirChunk = int64_t(kWave) * kDirU;    // entries per chunk
-constexpr int kDirStage = 2048;                          // staged slice entries per wave
+constexpr int kDirRev = 256;  // slices up to this size are looked up from the slice's side
 
 __device__ __forceinline__ int64_t lane_i64(int64_t v, int src) {  // src wave-uniform
   const uint64_t u = uint64_t(v);
@@ -442,53 +446,31 @@ __device__ __forceinline__ int32_t clamp_i32(int64_t v) {
   return v < INT32_MIN ? INT32_MIN : (v > INT32_MAX ? INT32_MAX : int32_t(v));
 }
 
-// cnt[u] = the number of entries equal to x[u] in a slice of m >= 1 sorted
-// columns, for every u with act[u]: at stage[so ..] (staged, int32) or at
-// col[lo ..].  Branchless lower bounds with one trip count for all u, so the
-// U searches' loads are in flight together.
+// cnt[u] = the number of entries equal to x[u] in the m >= 1 sorted columns
+// col[lo ..], for every u with act[u].  Branchless lower bounds with one trip
+// count for all u, so the U searches' loads are in flight together (the
+// slices stay in L2 and L1; staging them in LDS first measured slower).
 template <int U>
-__device__ __forceinline__ void slice_counts(const int32_t* stage, const int64_t* __restrict__ col,
-                                             bool staged, int32_t so, int64_t lo, int64_t m,
-                                             const int32_t (&x)[U], const bool (&act)[U],
-                                             int32_t (&cnt)[U]) {
-  if (staged) {
-    int32_t a[U];
+__device__ __forceinline__ void slice_counts(const int64_t* __restrict__ col, int64_t lo,
+                                             int64_t m, const int32_t (&x)[U],
+                                             const bool (&act)[U], int32_t (&cnt)[U]) {
+  int64_t a[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) a[u] = so;
-    for (int32_t len = int32_t(m); len > 1;) {
-      const int32_t half = len >> 1;
+  for (int u = 0; u < U; ++u) a[u] = lo;
+  for (int64_t len = m; len > 1;) {
+    const int64_t half = len >> 1;
 #pragma unroll
-      for (int u = 0; u < U; ++u)
-        if (act[u]) a[u] = stage[a[u] + half] < x[u] ? a[u] + half : a[u];
-      len -= half;
-    }
-    const int32_t e = so + int32_t(m);
+    for (int u = 0; u < U; ++u)
+      if (act[u]) a[u] = col[a[u] + half] < x[u] ? a[u] + half : a[u];
+    len -= half;
+  }
+  const int64_t e = lo + m;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      cnt[u] = 0;
-      if (!act[u]) continue;
-      int32_t q = a[u] + (stage[a[u]] < x[u] ? 1 : 0);
-      for (; q < e && stage[q] == x[u]; ++q) ++cnt[u];
-    }
-  } else {
-    int64_t a[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) a[u] = lo;
-    for (int64_t len = m; len > 1;) {
-      const int64_t half = len >> 1;
-#pragma unroll
-      for (int u = 0; u < U; ++u)
-        if (act[u]) a[u] = col[a[u] + half] < x[u] ? a[u] + half : a[u];
-      len -= half;
-    }
-    const int64_t e = lo + m;
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      cnt[u] = 0;
-      if (!act[u]) continue;
-      int64_t q = a[u] + (col[a[u]] < x[u] ? 1 : 0);
-      for (; q < e && col[q] == x[u]; ++q) ++cnt[u];
-    }
+  for (int u = 0; u < U; ++u) {
+    cnt[u] = 0;
+    if (!act[u]) continue;
+    int64_t q = a[u] + (col[a[u]] < x[u] ? 1 : 0);
+    for (; q < e && col[q] == x[u]; ++q) ++cnt[u];
   }
 }
 
@@ -613,9 +595,125 @@ __global__ void k_ppr_chunk_rows(const int32_t* __restrict__ chunk_off, int32_t 
   for (int32_t c = chunk_off[r]; c < e; ++c) row_of[c] = int32_t(r);
 }
 
-// One chunk w (uniform) of the direct step, on one wave whose LDS slice
-// buffer is `stage`.  status[0]: bad neighbour ids and seeds; status[1]: CSR
-// rows out of order or a column repeated more than max_mult times.
+// What a chunk's survivors need: the per-list values every lane holds for
+// list `lane` (slice begin/size, staging, weight) and the chunk's context.
+struct ChunkCtx {
+  const int64_t* col;
+  const int32_t* own_lds;  // the chunk's columns, position t at [t]
+  const int32_t* surv;     // the surviving positions, S of them
+  int32_t S;
+  int n, j, lane;
+  int64_t p0, ej;
+  float wj_own, keep, alpha;
+  bool seed_ok, extra;  // extra: this lane adds the seed's teleport entry
+  int64_t sd;
+  int32_t K, w;
+  int64_t sm, slo;
+  float lw;
+};
+
+// The exact sums of the chunk's surviving positions (UB per lane, in the order
+// of the lists; a column an earlier list holds belongs to that list), then the
+// chunk's best K of them and the teleport entry into part_*.
+template <int UB>
+__device__ __forceinline__ void chunk_survivors(const ChunkCtx& x, float* __restrict__ part_val,
+                                                int32_t* __restrict__ part_col,
+                                                int32_t* __restrict__ part_cnt) {
+#pragma clang fp contract(off)
+  int32_t nv[UB];
+  bool own[UB];
+  int32_t rep[UB];
+  float s[UB];
+#pragma unroll
+  for (int u = 0; u < UB; ++u) {
+    const int32_t idx = x.lane + u * kWave;
+    own[u] = idx < x.S;
+    const int32_t t = own[u] ? x.surv[idx] : 0;
+    nv[u] = own[u] ? x.own_lds[t] : 0;
+    s[u] = 0.f;
+    rep[u] = 0;
+    if (own[u]) {
+      int32_t c = 1;
+      for (int64_t q = x.p0 + t + 1; q < x.ej && x.col[q] == nv[u]; ++q) ++c;
+      rep[u] = c;
+    }
+  }
+  for (int jj = 0; jj < x.n; ++jj) {
+    if (jj == x.j) {
+#pragma unroll
+      for (int u = 0; u < UB; ++u)
+        if (own[u])
+          for (int32_t c = 0; c < rep[u]; ++c) s[u] += x.wj_own;
+      continue;
+    }
+    const int64_t m = lane_i64(x.sm, jj);
+    if (m == 0) continue;
+    const int64_t lo_ = lane_i64(x.slo, jj);
+    const float wj = lane_f32(x.lw, jj);
+    int32_t cnt[UB];
+    slice_counts<UB>(x.col, lo_, m, nv, own, cnt);
+#pragma unroll
+    for (int u = 0; u < UB; ++u) {
+      if (!own[u]) continue;
+      const int32_t c = cnt[u];
+      if (c == 0) continue;
+      if (jj < x.j) {
+        own[u] = false;  // an earlier list holds it
+        continue;
+      }
+      for (int32_t k = 0; k < c; ++k) s[u] += wj;
+    }
+  }
+  float cv[UB + 1];
+  int32_t cc[UB + 1];
+#pragma unroll
+  for (int u = 0; u < UB; ++u) {
+    cv[u] = own[u] ? scale_then_add(s[u], x.keep, x.alpha, x.seed_ok && nv[u] == x.sd)
+                   : -INFINITY;
+    cc[u] = own[u] ? nv[u] : INT32_MAX;
+  }
+  cv[UB] = x.extra ? scale_then_add(0.f, x.keep, x.alpha, true) : -INFINITY;
+  cc[UB] = x.extra ? int32_t(x.sd) : INT32_MAX;
+  int real = 0;
+#pragma unroll
+  for (int u = 0; u < UB; ++u) real += __popcll(__ballot(own[u]));
+  real += __popcll(__ballot(x.extra));
+  const int n_out = real < x.K ? real : x.K;
+  float pv = INFINITY;
+  int32_t pc = -1;  // the last pick: everything ranks after (+inf, -1)
+  for (int t = 0; t < n_out; ++t) {
+    float bv = -INFINITY;
+    int32_t bc = INT32_MAX;
+#pragma unroll
+    for (int u = 0; u <= UB; ++u) {
+      if (better(pv, pc, cv[u], cc[u]) && better(cv[u], cc[u], bv, bc)) {
+        bv = cv[u];
+        bc = cc[u];
+      }
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+      const float ov = __shfl_xor(bv, off, kWave);
+      const int32_t oc = __shfl_xor(bc, off, kWave);
+      if (better(ov, oc, bv, bc)) {
+        bv = ov;
+        bc = oc;
+      }
+    }
+    if (x.lane == 0) {
+      part_val[int64_t(x.w) * x.K + t] = bv;
+      part_col[int64_t(x.w) * x.K + t] = bc;
+    }
+    pv = bv;
+    pc = bc;
+  }
+  if (x.lane == 0) part_cnt[x.w] = n_out;
+}
+
+// One chunk w (uniform) of the direct step, on one wave with two LDS arrays
+// of kDirChunk slots (the chunk's columns; the pruning bound's small-slice
+// sums, then the compacted survivors).  status[0]: bad neighbour ids and
+// seeds; status[1]: CSR rows out of order or a column repeated more than
+// max_mult times.
 __device__ __forceinline__ void ppr_chunk(
     const int64_t* __restrict__ rowptr, const int64_t* __restrict__ col,
     const float* __restrict__ inv_deg, int64_t n_nodes, const int32_t* __restrict__ st_col,
@@ -626,7 +724,7 @@ __device__ __forceinline__ void ppr_chunk(
     const int64_t* __restrict__ tl_first, const int64_t* __restrict__ tl_last,
     const float* __restrict__ tl_w, const int32_t* __restrict__ seed_in,
     float* __restrict__ part_val, int32_t* __restrict__ part_col, int32_t* __restrict__ part_cnt,
-    int32_t* status, const int32_t w, const int lane, int32_t* stage) {
+    int32_t* status, const int32_t w, const int lane, int32_t* own_lds, float* small_sum) {
 #pragma clang fp contract(off)
   const int32_t r = __builtin_amdgcn_readfirstlane(row_of[w]);
   const int32_t ci = w - __builtin_amdgcn_readfirstlane(chunk_off[r]);
@@ -666,62 +764,28 @@ __device__ __forceinline__ void ppr_chunk(
   const int64_t sd = seeds[r];
   const bool seed_ok = sd >= 0 && sd < n_nodes;
 
-  // every other list's slice [slo, shi) of columns in [vmin, vmax], and where
-  // it is staged: at soff in the wave's LDS when the slices up to it fit
+  // every other list's slice [slo, shi) of columns in [vmin, vmax]
   int64_t slo = 0, shi = 0;
   const bool need = j >= 0 && lane < n && lane != j && ll > 0 && vmax >= lfirst && vmin <= llast;
   coop_slices(col, n, need, lb, ll, vmin, vmax, lane, slo, shi);
   if (shi < slo) shi = slo;  // rows out of order (flagged where they are read)
   const int64_t sm = shi - slo;
-  int64_t sinc = sm;
-  for (int off = 1; off < kWave; off <<= 1) {
-    const int64_t v = __shfl_up(sinc, off, kWave);
-    if (lane >= off) sinc += v;
-  }
-  const int64_t soff64 = sinc - sm;
-  const bool staged = sm > 0 && sinc <= kDirStage;  // the slices up to this one fit
-  const int32_t soff = staged ? int32_t(soff64) : 0;
-  const uint64_t stm = __ballot(staged);
-  const int32_t n_stage = stm ? int32_t(lane_i64(sinc, 63 - __clzll(stm))) : 0;
-  constexpr int kStageU = 8;  // entries per lane in flight
-  for (int32_t f0 = 0; f0 < n_stage; f0 += kWave * kStageU) {  // uniform: every lane shuffles
-    int64_t src[kStageU];
-#pragma unroll
-    for (int k = 0; k < kStageU; ++k) {
-      const int32_t f = f0 + k * kWave + lane;
-      // the slice holding entry f: the last lane whose slice starts at or before f
-      int sl = 0;
-#pragma unroll
-      for (int h = kWave / 2; h > 0; h >>= 1)
-        if (__shfl(soff64, sl + h, kWave) <= f) sl += h;
-      src[k] = __shfl(slo, sl, kWave) + (f - __shfl(soff64, sl, kWave));
-    }
-    int64_t v[kStageU];
-#pragma unroll
-    for (int k = 0; k < kStageU; ++k)
-      if (f0 + k * kWave + lane < n_stage) v[k] = col[src[k]];
-#pragma unroll
-    for (int k = 0; k < kStageU; ++k)
-      if (f0 + k * kWave + lane < n_stage) stage[f0 + k * kWave + lane] = clamp_i32(v[k]);
-  }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
   // this chunk's entries: column, owner, repeats within its own list
   int32_t nv[kDirU];
   bool own[kDirU];
   int32_t rep[kDirU];
-  float s[kDirU];
 #pragma unroll
   for (int u = 0; u < kDirU; ++u) {
     const int64_t p = p0 + lane + u * kWave;
     own[u] = false;
     nv[u] = 0;
     rep[u] = 0;
-    s[u] = 0.f;
+    own_lds[lane + u * kWave] = INT32_MAX;  // past the list: above every column
+    small_sum[lane + u * kWave] = 0.f;
     if (j < 0 || p >= ej) continue;
     const int64_t x = col[p];
+    own_lds[lane + u * kWave] = clamp_i32(x);
     bool o = x >= 0 && x < n_nodes;
     if (!o) atomicAdd(status, 1);
     const int64_t bj = ej - lane_i64(ll, j);
@@ -743,9 +807,9 @@ __device__ __forceinline__ void ppr_chunk(
   bool prune = j >= 0 && max_mult > 0 && int64_t(max_mult) * K <= 4096 && keep >= 0.f &&
                alpha >= 0.f;
   if (__ballot(lane < n && !(lw >= 0.f && lw <= __FLT_MAX__))) prune = false;  // < 0, inf, NaN
-  float tau = (lane < n && ll >= int64_t(K) * max_mult) ? lw * keep : -INFINITY;
-  for (int off = 32; off > 0; off >>= 1) tau = fmaxf(tau, __shfl_xor(tau, off, kWave));
-  if (prune && tau > 0.f) {
+  float tau = -INFINITY;
+  int order = 0;
+  if (prune) {
     // lists by weight, heaviest first: lane i of `order` names the list of rank i
     int rank = lane;
     if (lane < n) {
@@ -755,128 +819,120 @@ __device__ __forceinline__ void ppr_chunk(
         rank += (wi > lw || (wi == lw && i < lane)) ? 1 : 0;
       }
     }
-    const int order = __builtin_amdgcn_ds_permute(rank * 4, lane);
-    // sum of M * w over the own list and the other lists whose slice is not empty
-    double base_bnd = double(max_mult) * double(wj_own);
-    for (int jj = 0; jj < n; ++jj)
-      if (jj != j && lane_i64(sm, jj) > 0) base_bnd += double(max_mult) * double(lane_f32(lw, jj));
-    const double err = base_bnd * 0x1p-40;
+    order = __builtin_amdgcn_ds_permute(rank * 4, lane);
+    // tau: the union of the i heaviest lists holds at least max ceil(length / M)
+    // distinct columns, each worth at least fl(w_(i) * keep); a seed that no
+    // list holds is one more, worth alpha
+    const bool seed_alone = seed_ok && !seed_in[r];
+    int64_t dmax = 0;
+    for (int i = 0; i < n; ++i) {
+      const int jj = __builtin_amdgcn_readlane(order, i);
+      const int64_t d = (lane_i64(ll, jj) + max_mult - 1) / max_mult;
+      dmax = d > dmax ? d : dmax;
+      const float v = lane_f32(lw, jj) * keep;
+      if (dmax + ((seed_alone && alpha >= v) ? 1 : 0) >= K) {
+        tau = v;
+        break;
+      }
+    }
+  }
+  if (prune && tau > 0.f) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // slices of at most kDirRev entries: each entry is looked up among the
+    // chunk's own (ascending) columns and adds its list's w to the slot of the
+    // column's first occurrence, so small_sum holds those lists' exact share
+    // of each column's sum (fp32 adds in any order: a bound, not the value);
+    // larger slices count M * w until a lookup rules them out
+    double big = 0.0, all = double(max_mult) * double(wj_own);
+    for (int jj = 0; jj < n; ++jj) {
+      const int64_t m = lane_i64(sm, jj);
+      if (jj == j || m == 0) continue;
+      const float wjj = lane_f32(lw, jj);
+      all += double(max_mult) * double(wjj);
+      if (m > kDirRev) {
+        big += double(max_mult) * double(wjj);
+        continue;
+      }
+      const int64_t lo_ = lane_i64(slo, jj);
+      for (int32_t k0 = 0; k0 < int32_t(m); k0 += kWave) {
+        const int32_t k = k0 + lane;
+        if (k >= int32_t(m)) continue;
+        const int32_t x = clamp_i32(col[lo_ + k]);
+        int32_t a = 0;
+        for (int32_t len = int32_t(kDirChunk); len > 1;) {
+          const int32_t half = len >> 1;
+          a = own_lds[a + half - 1] < x ? a + half : a;
+          len -= half;
+        }
+        if (own_lds[a] < x) ++a;
+        if (a < int32_t(kDirChunk) && own_lds[a] == x) atomicAdd(small_sum + a, wjj);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const double err = all * 0x1p-40;
     // a column survives while keep * (bound + rounding of the double sums)
-    // * (1 + 2^-10) reaches tau; the seed always survives (alpha)
+    // * (1 + 2^-10) reaches tau; the seed always survives (alpha).  The fp32
+    // share of the small slices is raised by 2^-16 to cover its roundings.
     const double cut = double(tau) / (double(keep) * (1.0 + 1.0 / 1024.0));
     double bnd[kDirU];
     bool alive[kDirU];
 #pragma unroll
     for (int u = 0; u < kDirU; ++u) {
-      bnd[u] = base_bnd;
-      alive[u] = own[u] && (base_bnd + err >= cut || (seed_ok && nv[u] == sd));
-    }
-    for (int i = 0; i < n; ++i) {
-      bool any = false;
-#pragma unroll
-      for (int u = 0; u < kDirU; ++u) any |= alive[u] && !(seed_ok && nv[u] == sd);
-      if (__ballot(any) == 0) break;
-      const int jj = __builtin_amdgcn_readlane(order, i);
-      if (jj == j) continue;
-      const int64_t m = lane_i64(sm, jj);
-      if (m == 0) continue;
-      const bool st = __builtin_amdgcn_readlane(int(staged), jj) != 0;
-      const int32_t so = __builtin_amdgcn_readlane(soff, jj);
-      const int64_t lo_ = lane_i64(slo, jj);
-      const double mwj = double(max_mult) * double(lane_f32(lw, jj));
-      bool act[kDirU];
-      int32_t cnt[kDirU];
-#pragma unroll
-      for (int u = 0; u < kDirU; ++u) act[u] = alive[u] && !(seed_ok && nv[u] == sd);
-      slice_counts<kDirU>(stage, col, st, so, lo_, m, nv, act, cnt);
-#pragma unroll
-      for (int u = 0; u < kDirU; ++u) {
-        if (!act[u] || cnt[u] > 0) continue;  // held: the bound stays
-        bnd[u] -= mwj;
-        if (bnd[u] + err < cut) alive[u] = false;
-      }
+      bnd[u] = double(rep[u]) * double(wj_own) +
+               double(small_sum[lane + u * kWave]) * (1.0 + 0x1p-16) + big;
+      alive[u] = own[u] && (bnd[u] + err >= cut || (seed_ok && nv[u] == sd));
     }
 #pragma unroll
     for (int u = 0; u < kDirU; ++u) own[u] = own[u] && alive[u];
   }
 
-  // sums in list order; a column found in an earlier list belongs to it
-  for (int jj = 0; jj < n; ++jj) {
-    if (jj == j) {
-#pragma unroll
-      for (int u = 0; u < kDirU; ++u)
-        if (own[u])
-          for (int32_t c = 0; c < rep[u]; ++c) s[u] += wj_own;
-      continue;
-    }
-    const int64_t m = lane_i64(sm, jj);
-    if (m == 0) continue;
-    const bool st = __builtin_amdgcn_readlane(int(staged), jj) != 0;
-    const int32_t so = __builtin_amdgcn_readlane(soff, jj);
-    const int64_t lo_ = lane_i64(slo, jj);
-    const float wj = lane_f32(lw, jj);
-    int32_t cnt[kDirU];
-    slice_counts<kDirU>(stage, col, st, so, lo_, m, nv, own, cnt);
-#pragma unroll
-    for (int u = 0; u < kDirU; ++u) {
-      if (!own[u]) continue;
-      const int32_t c = cnt[u];
-      if (c == 0) continue;
-      if (jj < j) {
-        own[u] = false;  // an earlier list holds it
-        continue;
-      }
-      for (int32_t k = 0; k < c; ++k) s[u] += wj;
-    }
-  }
-  float cv[kDirU + 1];
-  int32_t cc[kDirU + 1];
+  // the surviving positions, compacted (small_sum's slots are free again)
+  int32_t* surv = reinterpret_cast<int32_t*>(small_sum);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
+  int32_t S = 0;
 #pragma unroll
   for (int u = 0; u < kDirU; ++u) {
-    cv[u] = own[u] ? scale_then_add(s[u], keep, alpha, seed_ok && nv[u] == sd) : -INFINITY;
-    cc[u] = own[u] ? nv[u] : INT32_MAX;
+    const uint64_t mk = __ballot(own[u]);
+    if (own[u]) surv[S + __popcll(mk & below)] = lane + u * kWave;
+    S += __popcll(mk);
   }
-  cv[kDirU] = -INFINITY;
-  cc[kDirU] = INT32_MAX;
-  bool extra = false;
-  if (ci == 0 && seed_ok && !seed_in[r] && lane == 0) {  // the teleport entry alone
-    cv[kDirU] = scale_then_add(0.f, keep, alpha, true);
-    cc[kDirU] = int32_t(sd);
-    extra = true;
-  }
-  int real = 0;
-#pragma unroll
-  for (int u = 0; u < kDirU; ++u) real += __popcll(__ballot(own[u]));
-  real += __popcll(__ballot(extra));
-  const int n_out = real < K ? real : K;
-  float pv = INFINITY;
-  int32_t pc = -1;  // the last pick: everything ranks after (+inf, -1)
-  for (int t = 0; t < n_out; ++t) {
-    float bv = -INFINITY;
-    int32_t bc = INT32_MAX;
-#pragma unroll
-    for (int u = 0; u <= kDirU; ++u) {
-      if (better(pv, pc, cv[u], cc[u]) && better(cv[u], cc[u], bv, bc)) {
-        bv = cv[u];
-        bc = cc[u];
-      }
-    }
-    for (int off = 32; off > 0; off >>= 1) {
-      const float ov = __shfl_xor(bv, off, kWave);
-      const int32_t oc = __shfl_xor(bc, off, kWave);
-      if (better(ov, oc, bv, bc)) {
-        bv = ov;
-        bc = oc;
-      }
-    }
-    if (lane == 0) {
-      part_val[int64_t(w) * K + t] = bv;
-      part_col[int64_t(w) * K + t] = bc;
-    }
-    pv = bv;
-    pc = bc;
-  }
-  if (lane == 0) part_cnt[w] = n_out;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  ChunkCtx x;
+  x.col = col;
+  x.own_lds = own_lds;
+  x.surv = surv;
+  x.S = S;
+  x.n = n;
+  x.j = j;
+  x.lane = lane;
+  x.p0 = p0;
+  x.ej = ej;
+  x.wj_own = wj_own;
+  x.keep = keep;
+  x.alpha = alpha;
+  x.seed_ok = seed_ok;
+  x.extra = ci == 0 && seed_ok && !seed_in[r] && lane == 0;  // the teleport entry alone
+  x.sd = sd;
+  x.K = K;
+  x.w = w;
+  x.sm = sm;
+  x.slo = slo;
+  x.lw = lw;
+  if (S <= kWave)
+    chunk_survivors<1>(x, part_val, part_col, part_cnt);
+  else if (S <= 2 * kWave)
+    chunk_survivors<2>(x, part_val, part_col, part_cnt);
+  else
+    chunk_survivors<kDirU>(x, part_val, part_col, part_cnt);
 }
 
 // One wave per chunk.  status[1] also flags chunk counts past the bound the
@@ -892,7 +948,8 @@ __global__ __launch_bounds__(kBlock) void k_ppr_direct(
     const int64_t* __restrict__ tl_last, const float* __restrict__ tl_w,
     const int32_t* __restrict__ seed_in, float* __restrict__ part_val,
     int32_t* __restrict__ part_col, int32_t* __restrict__ part_cnt, int32_t* status) {
-  __shared__ int32_t stage_all[kWaves][kDirStage];
+  __shared__ int32_t own_all[kWaves][kDirChunk];
+  __shared__ float small_all[kWaves][kDirChunk];
   const int32_t w = __builtin_amdgcn_readfirstlane(int(blockIdx.x * kWaves + (threadIdx.x >> 6)));
   const int lane = threadIdx.x & (kWave - 1);
   const int32_t n_chunks = __builtin_amdgcn_readfirstlane(chunk_off[n_rows]);
@@ -903,7 +960,8 @@ __global__ __launch_bounds__(kBlock) void k_ppr_direct(
   if (w >= n_chunks) return;
   ppr_chunk(rowptr, col, inv_deg, n_nodes, st_col, st_val, st_cnt, seeds, n_rows, K, alpha, keep,
             max_mult, chunk_off, row_of, tl_b, tl_len, tl_first, tl_last, tl_w, seed_in, part_val,
-            part_col, part_cnt, status, w, lane, stage_all[threadIdx.x >> 6]);
+            part_col, part_cnt, status, w, lane, own_all[threadIdx.x >> 6],
+            small_all[threadIdx.x >> 6]);
 }
 
 // One wave per row: the best K of its chunks' best K.
