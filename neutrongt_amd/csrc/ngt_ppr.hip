@@ -409,8 +409,8 @@ int ppr_sort_reduce(const int64_t* rowptr, const int64_t* col, const float* inv_
 // when no list holds it and alpha is at least the bound), the row's K-th best
 // value is at least tau = fl(w_(i) * keep) for the first such i.  A column
 // whose value is shown to lie below tau cannot be among the row's best K.
-// A column's upper bound is keep times: its own list's repeats times w_j,
-// plus the exact share of the lists whose slice holds at most kDirRev entries
+// A column's upper bound is keep times: M * w_j for its own list, plus the
+// exact share of the lists whose slice holds at most kDirRev entries
 // (each slice entry looked up among the chunk's columns adds its w), plus
 // M * w for every larger non-empty slice; fp32's rounding of the exact sum
 // (at most K * M + 1 roundings) is covered by a factor 1 + 2^-10.
@@ -612,71 +612,60 @@ struct ChunkCtx {
   float lw;
 };
 
-// The exact sums of the chunk's surviving positions (UB per lane, in the order
-// of the lists; a column an earlier list holds belongs to that list), then the
-// chunk's best K of them and the teleport entry into part_*.
-template <int UB>
-__device__ __forceinline__ void chunk_survivors(const ChunkCtx& x, float* __restrict__ part_val,
+// The exact sums of the chunk's surviving positions, 64 at a time (one per
+// lane; lists in order, a column an earlier list holds belongs to that list),
+// kept in LDS: the column in surv[i] (-1: another list's) and the value's
+// bits in own_lds[i], whose column survivor i has read by then (survivors
+// ascend, so survivor i's position is at least i).  Then the chunk's best K of
+// them and the teleport entry into part_*.
+__device__ __forceinline__ void chunk_survivors(const ChunkCtx& x, int32_t* surv, int32_t* vals,
+                                                float* __restrict__ part_val,
                                                 int32_t* __restrict__ part_col,
                                                 int32_t* __restrict__ part_cnt) {
 #pragma clang fp contract(off)
-  int32_t nv[UB];
-  bool own[UB];
-  int32_t rep[UB];
-  float s[UB];
-#pragma unroll
-  for (int u = 0; u < UB; ++u) {
-    const int32_t idx = x.lane + u * kWave;
-    own[u] = idx < x.S;
-    const int32_t t = own[u] ? x.surv[idx] : 0;
-    nv[u] = own[u] ? x.own_lds[t] : 0;
-    s[u] = 0.f;
-    rep[u] = 0;
-    if (own[u]) {
-      int32_t c = 1;
-      for (int64_t q = x.p0 + t + 1; q < x.ej && x.col[q] == nv[u]; ++q) ++c;
-      rep[u] = c;
+  int real = 0;
+  for (int32_t base = 0; base < x.S; base += kWave) {  // uniform
+    const int32_t idx = base + x.lane;
+    bool own[1] = {idx < x.S};
+    const int32_t t = own[0] ? surv[idx] : 0;
+    const int32_t nv[1] = {own[0] ? x.own_lds[t] : 0};
+    int32_t rep = 0;
+    if (own[0]) {
+      rep = 1;
+      for (int64_t q = x.p0 + t + 1; q < x.ej && x.col[q] == nv[0]; ++q) ++rep;
     }
-  }
-  for (int jj = 0; jj < x.n; ++jj) {
-    if (jj == x.j) {
-#pragma unroll
-      for (int u = 0; u < UB; ++u)
-        if (own[u])
-          for (int32_t c = 0; c < rep[u]; ++c) s[u] += x.wj_own;
-      continue;
-    }
-    const int64_t m = lane_i64(x.sm, jj);
-    if (m == 0) continue;
-    const int64_t lo_ = lane_i64(x.slo, jj);
-    const float wj = lane_f32(x.lw, jj);
-    int32_t cnt[UB];
-    slice_counts<UB>(x.col, lo_, m, nv, own, cnt);
-#pragma unroll
-    for (int u = 0; u < UB; ++u) {
-      if (!own[u]) continue;
-      const int32_t c = cnt[u];
-      if (c == 0) continue;
-      if (jj < x.j) {
-        own[u] = false;  // an earlier list holds it
+    float s = 0.f;
+    for (int jj = 0; jj < x.n; ++jj) {
+      if (jj == x.j) {
+        if (own[0])
+          for (int32_t c = 0; c < rep; ++c) s += x.wj_own;
         continue;
       }
-      for (int32_t k = 0; k < c; ++k) s[u] += wj;
+      const int64_t m = lane_i64(x.sm, jj);
+      if (m == 0) continue;
+      const int64_t lo_ = lane_i64(x.slo, jj);
+      const float wj = lane_f32(x.lw, jj);
+      int32_t cnt[1];
+      slice_counts<1>(x.col, lo_, m, nv, own, cnt);
+      if (!own[0] || cnt[0] == 0) continue;
+      if (jj < x.j) {
+        own[0] = false;  // an earlier list holds it
+        continue;
+      }
+      for (int32_t k = 0; k < cnt[0]; ++k) s += wj;
+    }
+    real += __popcll(__ballot(own[0]));
+    if (idx < x.S) {
+      vals[idx] = __float_as_int(
+          own[0] ? scale_then_add(s, x.keep, x.alpha, x.seed_ok && nv[0] == x.sd) : 0.f);
+      surv[idx] = own[0] ? nv[0] : -1;
     }
   }
-  float cv[UB + 1];
-  int32_t cc[UB + 1];
-#pragma unroll
-  for (int u = 0; u < UB; ++u) {
-    cv[u] = own[u] ? scale_then_add(s[u], x.keep, x.alpha, x.seed_ok && nv[u] == x.sd)
-                   : -INFINITY;
-    cc[u] = own[u] ? nv[u] : INT32_MAX;
-  }
-  cv[UB] = x.extra ? scale_then_add(0.f, x.keep, x.alpha, true) : -INFINITY;
-  cc[UB] = x.extra ? int32_t(x.sd) : INT32_MAX;
-  int real = 0;
-#pragma unroll
-  for (int u = 0; u < UB; ++u) real += __popcll(__ballot(own[u]));
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const float ev = x.extra ? scale_then_add(0.f, x.keep, x.alpha, true) : -INFINITY;
+  const int32_t ec = x.extra ? int32_t(x.sd) : INT32_MAX;
   real += __popcll(__ballot(x.extra));
   const int n_out = real < x.K ? real : x.K;
   float pv = INFINITY;
@@ -684,11 +673,17 @@ __device__ __forceinline__ void chunk_survivors(const ChunkCtx& x, float* __rest
   for (int t = 0; t < n_out; ++t) {
     float bv = -INFINITY;
     int32_t bc = INT32_MAX;
-#pragma unroll
-    for (int u = 0; u <= UB; ++u) {
-      if (better(pv, pc, cv[u], cc[u]) && better(cv[u], cc[u], bv, bc)) {
-        bv = cv[u];
-        bc = cc[u];
+    if (better(pv, pc, ev, ec) && better(ev, ec, bv, bc)) {
+      bv = ev;
+      bc = ec;
+    }
+    for (int32_t i = x.lane; i < x.S; i += kWave) {
+      const int32_t c = surv[i];
+      if (c < 0) continue;
+      const float v = __int_as_float(vals[i]);
+      if (better(pv, pc, v, c) && better(v, c, bv, bc)) {
+        bv = v;
+        bc = c;
       }
     }
     for (int off = 32; off > 0; off >>= 1) {
@@ -710,8 +705,8 @@ __device__ __forceinline__ void chunk_survivors(const ChunkCtx& x, float* __rest
 }
 
 // One chunk w (uniform) of the direct step, on one wave with two LDS arrays
-// of kDirChunk slots (the chunk's columns; the pruning bound's small-slice
-// sums, then the compacted survivors).  status[0]: bad neighbour ids and
+// of kDirChunk slots (the chunk's columns, then the survivors' values; the
+// pruning bound's small-slice sums, then the compacted survivors).  status[0]: bad neighbour ids and
 // seeds; status[1]: CSR rows out of order or a column repeated more than
 // max_mult times.
 __device__ __forceinline__ void ppr_chunk(
@@ -774,13 +769,11 @@ __device__ __forceinline__ void ppr_chunk(
   // this chunk's entries: column, owner, repeats within its own list
   int32_t nv[kDirU];
   bool own[kDirU];
-  int32_t rep[kDirU];
 #pragma unroll
   for (int u = 0; u < kDirU; ++u) {
     const int64_t p = p0 + lane + u * kWave;
     own[u] = false;
     nv[u] = 0;
-    rep[u] = 0;
     own_lds[lane + u * kWave] = INT32_MAX;  // past the list: above every column
     small_sum[lane + u * kWave] = 0.f;
     if (j < 0 || p >= ej) continue;
@@ -795,12 +788,7 @@ __device__ __forceinline__ void ppr_chunk(
       if (prev == x) o = false;  // a repeat: its first occurrence owns it
     }
     if (max_mult > 0 && p - max_mult >= bj && col[p - max_mult] == x) atomicAdd(status + 1, 1);
-    if (o) {
-      int32_t c = 1;
-      for (int64_t q = p + 1; q < ej && col[q] == x; ++q) ++c;
-      rep[u] = c;
-      nv[u] = int32_t(x);
-    }
+    if (o) nv[u] = int32_t(x);
     own[u] = o;
   }
 
@@ -878,16 +866,12 @@ __device__ __forceinline__ void ppr_chunk(
     // * (1 + 2^-10) reaches tau; the seed always survives (alpha).  The fp32
     // share of the small slices is raised by 2^-16 to cover its roundings.
     const double cut = double(tau) / (double(keep) * (1.0 + 1.0 / 1024.0));
-    double bnd[kDirU];
-    bool alive[kDirU];
+    const double fixed = double(max_mult) * double(wj_own) + big + err;  // own list: <= M repeats
 #pragma unroll
     for (int u = 0; u < kDirU; ++u) {
-      bnd[u] = double(rep[u]) * double(wj_own) +
-               double(small_sum[lane + u * kWave]) * (1.0 + 0x1p-16) + big;
-      alive[u] = own[u] && (bnd[u] + err >= cut || (seed_ok && nv[u] == sd));
+      const double bnd = fixed + double(small_sum[lane + u * kWave]) * (1.0 + 0x1p-16);
+      own[u] = own[u] && (bnd >= cut || (seed_ok && nv[u] == sd));
     }
-#pragma unroll
-    for (int u = 0; u < kDirU; ++u) own[u] = own[u] && alive[u];
   }
 
   // the surviving positions, compacted (small_sum's slots are free again)
@@ -927,12 +911,7 @@ __device__ __forceinline__ void ppr_chunk(
   x.sm = sm;
   x.slo = slo;
   x.lw = lw;
-  if (S <= kWave)
-    chunk_survivors<1>(x, part_val, part_col, part_cnt);
-  else if (S <= 2 * kWave)
-    chunk_survivors<2>(x, part_val, part_col, part_cnt);
-  else
-    chunk_survivors<kDirU>(x, part_val, part_col, part_cnt);
+  chunk_survivors(x, surv, own_lds, part_val, part_col, part_cnt);
 }
 
 // One wave per chunk.  status[1] also flags chunk counts past the bound the
