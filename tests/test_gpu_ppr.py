@@ -194,9 +194,10 @@ def test_direct_and_sorted_steps_agree_on_a_large_graph(K, hub_deg):
     seeds = torch.arange(n, device=DEV)
     got = [PPR.appnp_batch(rowptr, col, inv, n, seeds, 0.85, K, 10, method=m, max_mult=mm)
            for m, mm in (("direct", mult), ("direct", 0), ("sort", None))]
+    live = torch.arange(K, device=DEV)[None, :] < got[0][2][:, None]  # slots past cnt: unset
     for c, v, k in got[1:]:
-        assert torch.equal(c, got[0][0]) and torch.equal(k, got[0][2])
-        assert torch.equal(v.view(torch.int32), got[0][1].view(torch.int32))
+        assert torch.equal(k, got[0][2]) and torch.equal(c[live], got[0][0][live])
+        assert torch.equal(v[live].view(torch.int32), got[0][1][live].view(torch.int32))
     full = _simple_graph(n, 12 * n, 4, hub_deg, 12)
     got = [PPR.personal_pagerank_appnp(torch.from_numpy(full), 0.85, topk=K, num_iterations=10,
                                        batch_size=8192, device=DEV, num_nodes=n, iter_topk=K,
@@ -238,3 +239,47 @@ def test_appnp_row_chunks_match_one_pass():
         assert cnt[r] == len(want)
         assert cols[r, :cnt[r]].tolist() == [c for c, _ in want]
         np.testing.assert_array_equal(vals[r, :cnt[r]], np.array([v for _, v in want], np.float32))
+
+
+def _random_case(seed):
+    rng = np.random.default_rng(1000 + seed)
+    n = int(rng.integers(20, 3000))
+    E = int(rng.integers(n, 12 * n))
+    ei = rng.integers(0, n, (2, E))
+    if rng.random() < 0.5:  # hubs
+        h = int(rng.integers(1, 4))
+        deg = int(rng.integers(n // 4, n))
+        ei = np.concatenate([ei, np.stack([rng.integers(0, n, h * deg) % h,
+                                           rng.integers(0, n, h * deg)])], axis=1)
+    if rng.random() < 0.7:
+        ei = np.concatenate([ei, ei[::-1]], axis=1)
+    if rng.random() < 0.5:  # simple graph: max_repeats 1
+        ei = np.unique(ei[:, ei[0] != ei[1]], axis=1)
+    K = int(rng.choice([1, 2, 5, 8, 33, 64]))
+    alpha = float(rng.choice([0.0, 0.15, 0.5, 0.85, 1.0]))
+    iters = int(rng.integers(2, 7))
+    return n, torch.from_numpy(ei), K, alpha, iters
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_direct_and_sorted_steps_agree_on_random_graphs(seed):
+    """Random graphs (duplicate edges or none, hubs, isolated nodes), K from 1
+    to 64 (states past 32 lists take the direct step's per-lane slice
+    search), alpha from 0 (keep 1) to 1 (keep 0: no pruning bound): the
+    direct step with and without its bound and the sorted products give the
+    same bits for every seed."""
+    from neutrongt_amd import ppr as PPR
+
+    n, ei, K, alpha, iters = _random_case(seed)
+    print(f"case ppr random seed={seed} n={n} E={ei.shape[1]} K={K} alpha={alpha}", flush=True)
+    rowptr, col, inv, _ = PPR.transition_csr(ei, num_nodes=n, device=DEV)
+    mult = PPR.max_repeats(rowptr, col)
+    seeds = torch.arange(n, device=DEV)
+    got = [PPR.appnp_batch(rowptr, col, inv, n, seeds, alpha, min(K, n), iters, method=m,
+                           max_mult=mm)
+           for m, mm in (("direct", mult), ("direct", 0), ("sort", None))]
+    live = torch.arange(min(K, n), device=DEV)[None, :] < got[0][2][:, None]  # slots past cnt: unset
+    for c, v, k in got[1:]:
+        assert torch.equal(k, got[0][2])
+        assert torch.equal(c[live], got[0][0][live])
+        assert torch.equal(v[live].view(torch.int32), got[0][1][live].view(torch.int32))
