@@ -530,17 +530,25 @@ __device__ __forceinline__ void coop_slices(const int64_t* __restrict__ col, int
 
 // Per row, one wave: the table of its state lists (begin, length, first and
 // last column, weight w_j = st_val * inv_deg, the same fp32 product the chunks
-// would form), its chunk count (the sum over its lists of ceil(length /
-// kDirChunk), at least 1 for the teleport entry) and whether a list holds the
-// seed.  Wave n_rows writes the count slot the scan turns into the total.
+// would form), the lower bound tau of its K-th best value (-inf: no bound),
+// the lists it skips, its chunk count (the sum over the other lists of
+// ceil(length / kDirChunk), at least 1 for the teleport entry), whether a
+// list it keeps holds the seed, and the seed's exact value.  A list is
+// skipped when it is among the lightest whose keep * sum of M * w stays below
+// tau: a column that only skipped lists hold is worth less than tau, so its
+// entries need no chunk; columns a kept list holds are still summed over
+// every list.  Wave n_rows writes the count slot the scan turns into the
+// total.
 __global__ __launch_bounds__(kBlock) void k_ppr_rows(
     const int64_t* __restrict__ rowptr, const int64_t* __restrict__ col,
     const float* __restrict__ inv_deg, int64_t n_nodes, const int32_t* __restrict__ st_col,
     const float* __restrict__ st_val, const int32_t* __restrict__ st_cnt,
-    const int64_t* __restrict__ seeds, int32_t n_rows, int32_t K, int64_t* __restrict__ tl_b,
-    int64_t* __restrict__ tl_len, int64_t* __restrict__ tl_first, int64_t* __restrict__ tl_last,
-    float* __restrict__ tl_w, int32_t* __restrict__ nch, int32_t* __restrict__ seed_in,
-    int32_t* status) {
+    const int64_t* __restrict__ seeds, int32_t n_rows, int32_t K, float alpha, float keep,
+    int32_t max_mult, int64_t* __restrict__ tl_b, int64_t* __restrict__ tl_len,
+    int64_t* __restrict__ tl_first, int64_t* __restrict__ tl_last, float* __restrict__ tl_w,
+    int32_t* __restrict__ tl_skip, int32_t* __restrict__ nch, int32_t* __restrict__ seed_in,
+    float* __restrict__ seed_val, float* __restrict__ row_tau, int32_t* status) {
+#pragma clang fp contract(off)
   const int32_t r = __builtin_amdgcn_readfirstlane(int(blockIdx.x * kWaves + (threadIdx.x >> 6)));
   const int lane = threadIdx.x & (kWave - 1);
   if (r > n_rows) return;
@@ -571,17 +579,73 @@ __global__ __launch_bounds__(kBlock) void k_ppr_rows(
     tl_last[at] = llast;
     tl_w[at] = lw;
   }
-  int64_t c = (ll + kDirChunk - 1) / kDirChunk;
-  for (int off = 32; off > 0; off >>= 1) c += __shfl_xor(c, off, kWave);
   const int64_t sd = seeds[r];
   const bool seed_ok = sd >= 0 && sd < n_nodes;
-  int64_t slo, shi;
+  int64_t slo, shi;  // the seed's entries in list `lane`
   coop_slices(col, n, seed_ok && lane < n && ll > 0 && sd >= lfirst && sd <= llast, lb, ll, sd,
               sd, lane, slo, shi);
-  const bool found = __ballot(shi > slo) != 0;
+  const bool held_any = __ballot(shi > slo) != 0;
+
+  bool prune = max_mult > 0 && int64_t(max_mult) * K <= 4096 && keep >= 0.f && alpha >= 0.f;
+  if (__ballot(lane < n && !(lw >= 0.f && lw <= __FLT_MAX__))) prune = false;  // < 0, inf, NaN
+  float tau = -INFINITY;
+  bool skip = false;
+  if (prune) {
+    // lists by weight, heaviest first: lane i of `order` names the list of rank i
+    int rank = lane;
+    if (lane < n) {
+      rank = 0;
+      for (int i = 0; i < n; ++i) {
+        const float wi = lane_f32(lw, i);
+        rank += (wi > lw || (wi == lw && i < lane)) ? 1 : 0;
+      }
+    }
+    const int order = __builtin_amdgcn_ds_permute(rank * 4, lane);
+    // tau: the union of the i heaviest lists holds at least max ceil(length / M)
+    // distinct columns, each worth at least fl(w_(i) * keep); a seed that no
+    // list holds is one more, worth alpha
+    const bool seed_alone = seed_ok && !held_any;
+    int64_t dmax = 0;
+    for (int i = 0; i < n; ++i) {
+      const int jj = __builtin_amdgcn_readlane(order, i);
+      const int64_t d = (lane_i64(ll, jj) + max_mult - 1) / max_mult;
+      dmax = d > dmax ? d : dmax;
+      const float v = lane_f32(lw, jj) * keep;
+      if (dmax + ((seed_alone && alpha >= v) ? 1 : 0) >= K) {
+        tau = v;
+        break;
+      }
+    }
+    if (tau > 0.f) {
+      // the lightest lists whose keep * sum of M * w, rounding covered as in the
+      // chunks, stays below tau
+      const double cut = double(tau) / (double(keep) * (1.0 + 1.0 / 1024.0));
+      double acc = 0.0;
+      int nskip = 0;
+      for (int i = n - 1; i >= 0; --i) {
+        acc += double(max_mult) * double(lane_f32(lw, __builtin_amdgcn_readlane(order, i)));
+        if (acc * (1.0 + 0x1p-40) >= cut) break;
+        ++nskip;
+      }
+      skip = lane < n && rank >= n - nskip;
+    }
+  }
+  int64_t c = skip ? 0 : (ll + kDirChunk - 1) / kDirChunk;
+  for (int off = 32; off > 0; off >>= 1) c += __shfl_xor(c, off, kWave);
+  const bool held_live = __ballot(shi > slo && !skip) != 0;
+  // the seed's value: its entries' products in list order, scaled, plus alpha
+  float sv = 0.f;
+  for (int jj = 0; jj < n; ++jj) {
+    const int32_t cnt = __builtin_amdgcn_readlane(int(shi - slo), jj);
+    const float wj = lane_f32(lw, jj);
+    for (int32_t k = 0; k < cnt; ++k) sv += wj;
+  }
+  if (lane < n) tl_skip[int64_t(r) * K + lane] = skip ? 1 : 0;
   if (lane == 0) {
     nch[r] = c > 0 ? int32_t(c) : 1;
-    seed_in[r] = found ? 1 : 0;
+    seed_in[r] = held_live ? 1 : 0;
+    seed_val[r] = scale_then_add(sv, keep, alpha, true);
+    row_tau[r] = prune ? tau : -INFINITY;
     if (!seed_ok) atomicAdd(status, 1);
   }
 }
@@ -610,6 +674,8 @@ struct ChunkCtx {
   int32_t K, w;
   int64_t sm, slo;
   float lw;
+  bool lsk;      // list `lane` is skipped: it owns no column
+  float seed_v;  // the seed's value, for the teleport entry
 };
 
 // The exact sums of the chunk's surviving positions, 64 at a time (one per
@@ -648,8 +714,8 @@ __device__ __forceinline__ void chunk_survivors(const ChunkCtx& x, int32_t* surv
       int32_t cnt[1];
       slice_counts<1>(x.col, lo_, m, nv, own, cnt);
       if (!own[0] || cnt[0] == 0) continue;
-      if (jj < x.j) {
-        own[0] = false;  // an earlier list holds it
+      if (jj < x.j && !__builtin_amdgcn_readlane(int(x.lsk), jj)) {
+        own[0] = false;  // an earlier list that is not skipped holds it
         continue;
       }
       for (int32_t k = 0; k < cnt[0]; ++k) s += wj;
@@ -664,7 +730,7 @@ __device__ __forceinline__ void chunk_survivors(const ChunkCtx& x, int32_t* surv
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  const float ev = x.extra ? scale_then_add(0.f, x.keep, x.alpha, true) : -INFINITY;
+  const float ev = x.extra ? x.seed_v : -INFINITY;
   const int32_t ec = x.extra ? int32_t(x.sd) : INT32_MAX;
   real += __popcll(__ballot(x.extra));
   const int n_out = real < x.K ? real : x.K;
@@ -717,9 +783,11 @@ __device__ __forceinline__ void ppr_chunk(
     int32_t max_mult, const int32_t* __restrict__ chunk_off, const int32_t* __restrict__ row_of,
     const int64_t* __restrict__ tl_b, const int64_t* __restrict__ tl_len,
     const int64_t* __restrict__ tl_first, const int64_t* __restrict__ tl_last,
-    const float* __restrict__ tl_w, const int32_t* __restrict__ seed_in,
-    float* __restrict__ part_val, int32_t* __restrict__ part_col, int32_t* __restrict__ part_cnt,
-    int32_t* status, const int32_t w, const int lane, int32_t* own_lds, float* small_sum) {
+    const float* __restrict__ tl_w, const int32_t* __restrict__ tl_skip,
+    const int32_t* __restrict__ seed_in, const float* __restrict__ seed_val,
+    const float* __restrict__ row_tau, float* __restrict__ part_val,
+    int32_t* __restrict__ part_col, int32_t* __restrict__ part_cnt, int32_t* status,
+    const int32_t w, const int lane, int32_t* own_lds, float* small_sum) {
 #pragma clang fp contract(off)
   const int32_t r = __builtin_amdgcn_readfirstlane(row_of[w]);
   const int32_t ci = w - __builtin_amdgcn_readfirstlane(chunk_off[r]);
@@ -728,6 +796,7 @@ __device__ __forceinline__ void ppr_chunk(
   // lane j < n holds list j: begin, length, weight, first and last column
   int64_t lb = 0, ll = 0, lfirst = 0, llast = -1;
   float lw = 0.f;
+  bool lsk = false;  // skipped: no chunks of its own, and it owns no column
   if (lane < n) {
     const int64_t at = int64_t(r) * K + lane;
     lb = tl_b[at];
@@ -735,9 +804,10 @@ __device__ __forceinline__ void ppr_chunk(
     lfirst = tl_first[at];
     llast = tl_last[at];
     lw = tl_w[at];
+    lsk = tl_skip[at] != 0;
   }
-  // this chunk's list j: the last nonempty list whose first chunk is <= ci
-  const int32_t cj = int32_t((ll + kDirChunk - 1) / kDirChunk);
+  // this chunk's list j: the last list with chunks whose first chunk is <= ci
+  const int32_t cj = lsk ? 0 : int32_t((ll + kDirChunk - 1) / kDirChunk);
   int32_t cinc = cj;
   for (int off = 1; off < kWave; off <<= 1) {
     const int32_t v = __shfl_up(cinc, off, kWave);
@@ -792,38 +862,8 @@ __device__ __forceinline__ void ppr_chunk(
     own[u] = o;
   }
 
-  bool prune = j >= 0 && max_mult > 0 && int64_t(max_mult) * K <= 4096 && keep >= 0.f &&
-               alpha >= 0.f;
-  if (__ballot(lane < n && !(lw >= 0.f && lw <= __FLT_MAX__))) prune = false;  // < 0, inf, NaN
-  float tau = -INFINITY;
-  int order = 0;
-  if (prune) {
-    // lists by weight, heaviest first: lane i of `order` names the list of rank i
-    int rank = lane;
-    if (lane < n) {
-      rank = 0;
-      for (int i = 0; i < n; ++i) {
-        const float wi = lane_f32(lw, i);
-        rank += (wi > lw || (wi == lw && i < lane)) ? 1 : 0;
-      }
-    }
-    order = __builtin_amdgcn_ds_permute(rank * 4, lane);
-    // tau: the union of the i heaviest lists holds at least max ceil(length / M)
-    // distinct columns, each worth at least fl(w_(i) * keep); a seed that no
-    // list holds is one more, worth alpha
-    const bool seed_alone = seed_ok && !seed_in[r];
-    int64_t dmax = 0;
-    for (int i = 0; i < n; ++i) {
-      const int jj = __builtin_amdgcn_readlane(order, i);
-      const int64_t d = (lane_i64(ll, jj) + max_mult - 1) / max_mult;
-      dmax = d > dmax ? d : dmax;
-      const float v = lane_f32(lw, jj) * keep;
-      if (dmax + ((seed_alone && alpha >= v) ? 1 : 0) >= K) {
-        tau = v;
-        break;
-      }
-    }
-  }
+  const float tau = row_tau[r];  // -inf: no bound for this row
+  const bool prune = j >= 0;
   if (prune && tau > 0.f) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -904,7 +944,10 @@ __device__ __forceinline__ void ppr_chunk(
   x.keep = keep;
   x.alpha = alpha;
   x.seed_ok = seed_ok;
-  x.extra = ci == 0 && seed_ok && !seed_in[r] && lane == 0;  // the teleport entry alone
+  // the seed, when no list with chunks holds it, with its exact value
+  x.extra = ci == 0 && seed_ok && !seed_in[r] && lane == 0;
+  x.seed_v = seed_val[r];
+  x.lsk = lsk;
   x.sd = sd;
   x.K = K;
   x.w = w;
@@ -925,8 +968,10 @@ __global__ __launch_bounds__(kBlock) void k_ppr_direct(
     const int32_t* __restrict__ row_of, const int64_t* __restrict__ tl_b,
     const int64_t* __restrict__ tl_len, const int64_t* __restrict__ tl_first,
     const int64_t* __restrict__ tl_last, const float* __restrict__ tl_w,
-    const int32_t* __restrict__ seed_in, float* __restrict__ part_val,
-    int32_t* __restrict__ part_col, int32_t* __restrict__ part_cnt, int32_t* status) {
+    const int32_t* __restrict__ tl_skip, const int32_t* __restrict__ seed_in,
+    const float* __restrict__ seed_val, const float* __restrict__ row_tau,
+    float* __restrict__ part_val, int32_t* __restrict__ part_col, int32_t* __restrict__ part_cnt,
+    int32_t* status) {
   __shared__ int32_t own_all[kWaves][kDirChunk];
   __shared__ float small_all[kWaves][kDirChunk];
   const int32_t w = __builtin_amdgcn_readfirstlane(int(blockIdx.x * kWaves + (threadIdx.x >> 6)));
@@ -938,9 +983,9 @@ __global__ __launch_bounds__(kBlock) void k_ppr_direct(
   }
   if (w >= n_chunks) return;
   ppr_chunk(rowptr, col, inv_deg, n_nodes, st_col, st_val, st_cnt, seeds, n_rows, K, alpha, keep,
-            max_mult, chunk_off, row_of, tl_b, tl_len, tl_first, tl_last, tl_w, seed_in, part_val,
-            part_col, part_cnt, status, w, lane, own_all[threadIdx.x >> 6],
-            small_all[threadIdx.x >> 6]);
+            max_mult, chunk_off, row_of, tl_b, tl_len, tl_first, tl_last, tl_w, tl_skip, seed_in,
+            seed_val, row_tau, part_val, part_col, part_cnt, status, w, lane,
+            own_all[threadIdx.x >> 6], small_all[threadIdx.x >> 6]);
 }
 
 // One wave per row: the best K of its chunks' best K.
@@ -1002,8 +1047,8 @@ __global__ __launch_bounds__(kBlock) void k_ppr_merge(
 }
 
 struct DirectLayout {
-  size_t nch, chunk_off, temp, temp_bytes, row_of, tl_b, tl_len, tl_first, tl_last, tl_w, seed_in,
-      part_val, part_col, part_cnt, total;
+  size_t nch, chunk_off, temp, temp_bytes, row_of, tl_b, tl_len, tl_first, tl_last, tl_w, tl_skip,
+      seed_in, seed_val, row_tau, part_val, part_col, part_cnt, total;
   int64_t max_chunks;
 };
 
@@ -1032,7 +1077,10 @@ int direct_layout(int64_t total, int32_t n_rows, int32_t K, DirectLayout* L) {
   L->tl_first = take(m * size_t(K) * 8);
   L->tl_last = take(m * size_t(K) * 8);
   L->tl_w = take(m * size_t(K) * 4);
+  L->tl_skip = take(m * size_t(K) * 4);
   L->seed_in = take(m * 4);
+  L->seed_val = take(m * 4);
+  L->row_tau = take(m * 4);
   L->part_val = take(c * size_t(K) * 4);
   L->part_col = take(c * size_t(K) * 4);
   L->part_cnt = take(c * 4);
@@ -1188,11 +1236,15 @@ extern "C" int ngt_ppr_step_direct(const int64_t* rowptr, const int64_t* col,
   int64_t* tl_last = reinterpret_cast<int64_t*>(ws + L.tl_last);
   float* tl_w = reinterpret_cast<float*>(ws + L.tl_w);
   int32_t* seed_in = reinterpret_cast<int32_t*>(ws + L.seed_in);
+  int32_t* tl_skip = reinterpret_cast<int32_t*>(ws + L.tl_skip);
+  float* seed_val = reinterpret_cast<float*>(ws + L.seed_val);
+  float* row_tau = reinterpret_cast<float*>(ws + L.row_tau);
   int32_t* row_of = reinterpret_cast<int32_t*>(ws + L.row_of);
   const int32_t max_chunks = int32_t(L.max_chunks);
   hipLaunchKernelGGL(k_ppr_rows, dim3(grid_waves(int64_t(n_rows) + 1)), dim3(kBlock), 0, s,
                      rowptr, col, inv_deg, n_nodes, st_col, st_val, st_cnt, seeds, n_rows, K,
-                     tl_b, tl_len, tl_first, tl_last, tl_w, nch, seed_in, status);
+                     alpha, keep, max_mult, tl_b, tl_len, tl_first, tl_last, tl_w, tl_skip, nch,
+                     seed_in, seed_val, row_tau, status);
   NGT_HIP_CHECK(hipGetLastError());
   size_t tb = L.temp_bytes;
   NGT_HIP_CHECK(rocprim::exclusive_scan(ws + L.temp, tb, nch, chunk_off, int32_t(0),
@@ -1203,7 +1255,8 @@ extern "C" int ngt_ppr_step_direct(const int64_t* rowptr, const int64_t* col,
   hipLaunchKernelGGL(k_ppr_direct, dim3(grid_waves(L.max_chunks)), dim3(kBlock), 0, s, rowptr,
                      col, inv_deg, n_nodes, st_col, st_val, st_cnt, seeds, n_rows, K, alpha, keep,
                      max_mult, chunk_off, max_chunks, row_of, tl_b, tl_len, tl_first, tl_last,
-                     tl_w, seed_in, part_val, part_col, part_cnt, status);
+                     tl_w, tl_skip, seed_in, seed_val, row_tau, part_val, part_col, part_cnt,
+                     status);
   NGT_HIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL(k_ppr_merge, dim3(grid_waves(n_rows)), dim3(kBlock), 0, s, chunk_off,
                      int32_t(L.max_chunks), part_val, part_col, part_cnt, n_rows, K, out_col,
