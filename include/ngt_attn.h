@@ -514,8 +514,9 @@ int ngt_segment_sum_f32(const float* vals, int64_t n_vals, const int64_t* seg, i
  *   is sized from it; no sort.  Needs every CSR row's columns in ascending
  *   order (transition_csr's order).  max_mult >= 1, the
  *   most times one column repeats within a CSR row (1 for a graph without
- *   duplicate edges), lets it skip columns whose value is shown to fall
- *   below the row's K-th best (0: no skipping; the result is the same).
+ *   duplicate edges), lets it skip columns, and whole lists, whose values
+ *   are shown to fall below the row's K-th best (0: no skipping; the result
+ *   is the same).
  *   status points to two int32: [0] bad ids as above, [1] CSR rows met out of
  *   order, a column repeated more than max_mult times, or a total too small
  *   for the state's lists (the output is then invalid).
