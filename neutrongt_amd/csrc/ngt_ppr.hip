@@ -430,18 +430,6 @@ __device__ __forceinline__ float lane_f32(float v, int src) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
 }
 
-// first index in [b, e) whose column is >= x (strict: > x), e if none
-template <bool kStrict>
-__device__ __forceinline__ int64_t col_bound(const int64_t* __restrict__ col, int64_t b, int64_t e,
-                                             int64_t x) {
-  while (b < e) {
-    const int64_t mid = b + ((e - b) >> 1);
-    const bool left = kStrict ? col[mid] <= x : col[mid] < x;
-    if (left) b = mid + 1; else e = mid;
-  }
-  return b;
-}
-
 __device__ __forceinline__ int32_t clamp_i32(int64_t v) {
   return v < INT32_MIN ? INT32_MIN : (v > INT32_MAX ? INT32_MAX : int32_t(v));
 }
@@ -660,7 +648,7 @@ __global__ void k_ppr_chunk_rows(const int32_t* __restrict__ chunk_off, int32_t 
 }
 
 // What a chunk's survivors need: the per-list values every lane holds for
-// list `lane` (slice begin/size, staging, weight) and the chunk's context.
+// list `lane` (slice begin and size, weight, skipped) and the chunk's context.
 struct ChunkCtx {
   const int64_t* col;
   const int32_t* own_lds;  // the chunk's columns, position t at [t]
@@ -772,15 +760,13 @@ __device__ __forceinline__ void chunk_survivors(const ChunkCtx& x, int32_t* surv
 
 // One chunk w (uniform) of the direct step, on one wave with two LDS arrays
 // of kDirChunk slots (the chunk's columns, then the survivors' values; the
-// pruning bound's small-slice sums, then the compacted survivors).  status[0]: bad neighbour ids and
-// seeds; status[1]: CSR rows out of order or a column repeated more than
-// max_mult times.
+// pruning bound's small-slice sums, then the compacted survivors).
+// status[0]: bad neighbour ids; status[1]: CSR rows out of order or a column
+// repeated more than max_mult times.
 __device__ __forceinline__ void ppr_chunk(
-    const int64_t* __restrict__ rowptr, const int64_t* __restrict__ col,
-    const float* __restrict__ inv_deg, int64_t n_nodes, const int32_t* __restrict__ st_col,
-    const float* __restrict__ st_val, const int32_t* __restrict__ st_cnt,
-    const int64_t* __restrict__ seeds, int32_t n_rows, int32_t K, float alpha, float keep,
-    int32_t max_mult, const int32_t* __restrict__ chunk_off, const int32_t* __restrict__ row_of,
+    const int64_t* __restrict__ col, int64_t n_nodes, const int32_t* __restrict__ st_cnt,
+    const int64_t* __restrict__ seeds, int32_t K, float alpha, float keep, int32_t max_mult,
+    const int32_t* __restrict__ chunk_off, const int32_t* __restrict__ row_of,
     const int64_t* __restrict__ tl_b, const int64_t* __restrict__ tl_len,
     const int64_t* __restrict__ tl_first, const int64_t* __restrict__ tl_last,
     const float* __restrict__ tl_w, const int32_t* __restrict__ tl_skip,
@@ -836,7 +822,7 @@ __device__ __forceinline__ void ppr_chunk(
   if (shi < slo) shi = slo;  // rows out of order (flagged where they are read)
   const int64_t sm = shi - slo;
 
-  // this chunk's entries: column, owner, repeats within its own list
+  // this chunk's entries: column (also into LDS) and whether this entry owns it
   int32_t nv[kDirU];
   bool own[kDirU];
 #pragma unroll
@@ -863,8 +849,7 @@ __device__ __forceinline__ void ppr_chunk(
   }
 
   const float tau = row_tau[r];  // -inf: no bound for this row
-  const bool prune = j >= 0;
-  if (prune && tau > 0.f) {
+  if (j >= 0 && tau > 0.f) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -960,9 +945,7 @@ __device__ __forceinline__ void ppr_chunk(
 // One wave per chunk.  status[1] also flags chunk counts past the bound the
 // workspace was sized for (nothing is then written).
 __global__ __launch_bounds__(kBlock) void k_ppr_direct(
-    const int64_t* __restrict__ rowptr, const int64_t* __restrict__ col,
-    const float* __restrict__ inv_deg, int64_t n_nodes, const int32_t* __restrict__ st_col,
-    const float* __restrict__ st_val, const int32_t* __restrict__ st_cnt,
+    const int64_t* __restrict__ col, int64_t n_nodes, const int32_t* __restrict__ st_cnt,
     const int64_t* __restrict__ seeds, int32_t n_rows, int32_t K, float alpha, float keep,
     int32_t max_mult, const int32_t* __restrict__ chunk_off, int32_t max_chunks,
     const int32_t* __restrict__ row_of, const int64_t* __restrict__ tl_b,
@@ -982,10 +965,9 @@ __global__ __launch_bounds__(kBlock) void k_ppr_direct(
     return;
   }
   if (w >= n_chunks) return;
-  ppr_chunk(rowptr, col, inv_deg, n_nodes, st_col, st_val, st_cnt, seeds, n_rows, K, alpha, keep,
-            max_mult, chunk_off, row_of, tl_b, tl_len, tl_first, tl_last, tl_w, tl_skip, seed_in,
-            seed_val, row_tau, part_val, part_col, part_cnt, status, w, lane,
-            own_all[threadIdx.x >> 6], small_all[threadIdx.x >> 6]);
+  ppr_chunk(col, n_nodes, st_cnt, seeds, K, alpha, keep, max_mult, chunk_off, row_of, tl_b, tl_len,
+            tl_first, tl_last, tl_w, tl_skip, seed_in, seed_val, row_tau, part_val, part_col,
+            part_cnt, status, w, lane, own_all[threadIdx.x >> 6], small_all[threadIdx.x >> 6]);
 }
 
 // One wave per row: the best K of its chunks' best K.
@@ -1252,8 +1234,8 @@ extern "C" int ngt_ppr_step_direct(const int64_t* rowptr, const int64_t* col,
   hipLaunchKernelGGL(k_ppr_chunk_rows, dim3((n_rows + kBlock - 1) / kBlock), dim3(kBlock), 0, s,
                      chunk_off, n_rows, max_chunks, row_of);
   NGT_HIP_CHECK(hipGetLastError());
-  hipLaunchKernelGGL(k_ppr_direct, dim3(grid_waves(L.max_chunks)), dim3(kBlock), 0, s, rowptr,
-                     col, inv_deg, n_nodes, st_col, st_val, st_cnt, seeds, n_rows, K, alpha, keep,
+  hipLaunchKernelGGL(k_ppr_direct, dim3(grid_waves(L.max_chunks)), dim3(kBlock), 0, s, col,
+                     n_nodes, st_cnt, seeds, n_rows, K, alpha, keep,
                      max_mult, chunk_off, max_chunks, row_of, tl_b, tl_len, tl_first, tl_last,
                      tl_w, tl_skip, seed_in, seed_val, row_tau, part_val, part_col, part_cnt,
                      status);
