@@ -42,3 +42,6 @@ def test_window_preparation_bench(capsys):
 def test_ppr_bench(capsys):
     out = _run(capsys, ["--ppr", "--config", "gt_arxiv", "--no-cpu"])
     assert out["unit"] == "ms" and out["config"]["entries"] > 0
+    assert out["config"]["step"] == "direct"
+    srt = _run(capsys, ["--ppr", "--config", "gt_arxiv", "--no-cpu", "--ppr-method", "sort"])
+    assert srt["config"]["step"] == "sort" and srt["config"]["entries"] == out["config"]["entries"]
