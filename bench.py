@@ -248,10 +248,11 @@ def ppr_bench(args, cfg, dev) -> dict:
     csr = {"rowptr": rowptr, "col": col}
     _log(f"[bench] ppr: graph n={n}, {int(col.numel())} directed edges; topk {topk}, "
          f"{iters} iterations, batches of {batch}")
-    # one batch as warm-up, then the whole graph timed
+    # eight batches as warm-up (as many as run at once, so the streams exist),
+    # then the whole graph timed
     method = args.ppr_method
     PPR.personal_pagerank_appnp(None, alpha, topk=topk, num_iterations=iters, batch_size=batch,
-                                device=dev, csr_data=csr, iter_topk=topk, source_end=batch,
+                                device=dev, csr_data=csr, iter_topk=topk, source_end=8 * batch,
                                 method=method)
     torch.cuda.synchronize()
     # all seeds, in chunks of 32 batches with a progress line after each (the

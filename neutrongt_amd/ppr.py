@@ -17,7 +17,9 @@ step is ngt_ppr_count, one read-back of the product counts, then
 ngt_ppr_step_direct: every (seed, node) sum evaluated where the node first
 occurs in the seed's state lists (binary searches in the others, the products
 added in the same order), the best K kept per chunk of a row and merged per
-row; no product list is written or sorted.  ``method="sort"`` runs the
+row; no product list is written or sorted.  Several batches are in flight at
+once, each on a stream of its own, so that one batch's read-back overlaps the
+others' kernels.  ``method="sort"`` runs the
 product-list form instead (ngt_ppr_step: expansion, radix sort, ordered
 segment sums, per-row top-k, on row chunks that bound the step's memory); the
 two give the same bits.
@@ -31,6 +33,7 @@ Differences from the reference, by design:
 """
 from __future__ import annotations
 
+import collections
 import ctypes as C
 
 import torch
@@ -107,6 +110,133 @@ def max_repeats(rowptr: torch.Tensor, col: torch.Tensor) -> int:
     return int((idx - brk).max()) + 1
 
 
+def _check_status(status: torch.Tensor) -> None:
+    bad, disorder = status.tolist()
+    if bad:
+        raise IndexError(f"personalised PageRank: {bad} node ids out of range")
+    if disorder:
+        raise ValueError("personalised PageRank: CSR rows must list their columns in ascending "
+                         "order for the direct step (transition_csr sorts them), with no column "
+                         "repeated more than max_mult times")
+
+
+def _direct_batch(lib, rowptr, col, inv_deg, n_nodes: int, seeds: torch.Tensor, alpha: float,
+                  K: int, num_iterations: int, max_mult: int, stream, host_total: torch.Tensor):
+    """One batch through ngt_ppr_count + ngt_ppr_step_direct, all on
+    ``stream``, as a generator: after each step's count it enqueues an
+    asynchronous copy of the product total into ``host_total`` (pinned host
+    memory) and yields, so that the caller can enqueue other batches' work on
+    other streams while the copy lands; resumed, it waits for the copy and
+    enqueues the step.  Returns (cols, vals, cnt, status) on ``stream``."""
+    dev = seeds.device
+    B = int(seeds.numel())
+    sp = stream.cuda_stream
+    with torch.cuda.stream(stream):
+        st_col = torch.zeros(B, K, dtype=torch.int32, device=dev)
+        st_val = torch.zeros(B, K, dtype=torch.float32, device=dev)
+        st_col[:, 0] = seeds.to(torch.int32)
+        st_val[:, 0] = 1.0
+        st_cnt = torch.ones(B, dtype=torch.int32, device=dev)
+        nx_col, nx_val, nx_cnt = (torch.empty_like(st_col), torch.empty_like(st_val),
+                                  torch.empty_like(st_cnt))
+        seeds = seeds.to(torch.int64).contiguous()
+        status = torch.zeros(2, dtype=torch.int32, device=dev)
+        row_off = torch.empty(B + 1, dtype=torch.int64, device=dev)
+        cb = C.c_size_t()
+        _lib.check(lib.ngt_ppr_count_workspace_bytes(B, C.byref(cb)))
+        cws = torch.empty(cb.value, dtype=torch.uint8, device=dev)
+    keep = float(1.0 - alpha)  # rounded to fp32 by ctypes, as fp32_tensor * (1 - alpha) is
+    landed = torch.cuda.Event()
+    for _ in range(num_iterations):
+        _lib.check(lib.ngt_ppr_count(rowptr.data_ptr(), n_nodes, st_col.data_ptr(),
+                                     st_cnt.data_ptr(), B, K, row_off.data_ptr(),
+                                     status.data_ptr(), cws.data_ptr(), cb.value, sp))
+        with torch.cuda.stream(stream):
+            host_total.copy_(row_off[B:], non_blocking=True)
+        landed.record(stream)
+        yield
+        landed.synchronize()
+        total = int(host_total[0])
+        sb = C.c_size_t()
+        _lib.check(lib.ngt_ppr_step_direct_workspace_bytes(total, B, K, C.byref(sb)))
+        with torch.cuda.stream(stream):
+            ws = torch.empty(sb.value, dtype=torch.uint8, device=dev)
+        _lib.check(lib.ngt_ppr_step_direct(rowptr.data_ptr(), col.data_ptr(), inv_deg.data_ptr(),
+                                           n_nodes, st_col.data_ptr(), st_val.data_ptr(),
+                                           st_cnt.data_ptr(), seeds.data_ptr(), B, K,
+                                           float(alpha), keep, int(max_mult), total,
+                                           nx_col.data_ptr(), nx_val.data_ptr(),
+                                           nx_cnt.data_ptr(), status.data_ptr(), ws.data_ptr(),
+                                           sb.value, sp))
+        st_col, nx_col = nx_col, st_col
+        st_val, nx_val = nx_val, st_val
+        st_cnt, nx_cnt = nx_cnt, st_cnt
+    return st_col, st_val, st_cnt, status
+
+
+_STREAMS: dict = {}
+
+
+def _side_streams(dev: torch.device, n: int) -> list:
+    """n streams of default priority on ``dev``, created once per process and
+    reused by every call."""
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    have = _STREAMS.setdefault(idx, [])
+    while len(have) < n:
+        have.append(torch.cuda.Stream(torch.device("cuda", idx)))
+    return have[:n]
+
+
+def _run_direct(rowptr, col, inv_deg, n_nodes: int, seed_batches, alpha: float, K: int,
+                num_iterations: int, max_mult: int, streams: int):
+    """Propagates the seed batches through the direct step with up to
+    ``streams`` batches in flight, each on a stream of its own (default
+    priority; 1 = torch's current stream), and returns per batch (cols, vals,
+    cnt), ready on the current stream.  Rows are independent, so the results
+    do not depend on ``streams``: it lets the host's wait for one batch's
+    product total overlap the other batches' kernels, and small steps of
+    different batches share the GPU.  Raises after the last batch if any
+    batch flagged an id out of range or a CSR row out of order."""
+    lib = _lib.load()
+    if not seed_batches:
+        return []
+    dev = seed_batches[0].device
+    cur = torch.cuda.current_stream(dev)
+    n_str = max(1, min(int(streams), len(seed_batches)))
+    pool = [cur] if n_str == 1 else _side_streams(dev, n_str)
+    hosts = [torch.empty(1, dtype=torch.int64, pin_memory=True) for _ in pool]
+    results = [None] * len(seed_batches)
+    queue = iter(enumerate(seed_batches))
+
+    def start(slot):
+        nxt = next(queue, None)
+        if nxt is None:
+            return None
+        i, seeds = nxt
+        pool[slot].wait_stream(cur)  # the graph and the seeds come from the current stream
+        return (_direct_batch(lib, rowptr, col, inv_deg, n_nodes, seeds, alpha, K,
+                              num_iterations, max_mult, pool[slot], hosts[slot]), i, slot)
+
+    active = collections.deque(e for e in map(start, range(n_str)) if e is not None)
+    while active:
+        entry = active.popleft()
+        try:
+            next(entry[0])
+            active.append(entry)
+        except StopIteration as stop:
+            results[entry[1]] = stop.value
+            nxt = start(entry[2])
+            if nxt is not None:
+                active.append(nxt)
+    for s in pool:
+        cur.wait_stream(s)
+    for r in results:
+        for t in r:
+            t.record_stream(cur)
+    _check_status(torch.stack([r[3] for r in results]).sum(0))
+    return [r[:3] for r in results]
+
+
 def appnp_batch(rowptr, col, inv_deg, n_nodes: int, seeds: torch.Tensor, alpha: float, K: int,
                 num_iterations: int, max_products: int = 1 << 27, method: str = "direct",
                 max_mult: int | None = None):
@@ -118,15 +248,18 @@ def appnp_batch(rowptr, col, inv_deg, n_nodes: int, seeds: torch.Tensor, alpha: 
     or "sort" (ngt_ppr_step), where a step whose product count exceeds
     ``max_products`` runs on consecutive row chunks (rows are independent),
     which bounds the step's workspace."""
-    lib = _lib.load()
-    dev = seeds.device
-    B = int(seeds.numel())
     if not 1 <= K <= MAX_K:
         raise ValueError(f"per-step top-k must be in 1..{MAX_K}, got {K}")
     if method not in ("direct", "sort"):
         raise ValueError(f"method must be 'direct' or 'sort', got {method!r}")
-    if method == "direct" and max_mult is None:
-        max_mult = max_repeats(rowptr, col)
+    if method == "direct":
+        if max_mult is None:
+            max_mult = max_repeats(rowptr, col)
+        return _run_direct(rowptr, col, inv_deg, n_nodes, [seeds], alpha, K, num_iterations,
+                           max_mult, 1)[0]
+    lib = _lib.load()
+    dev = seeds.device
+    B = int(seeds.numel())
     st_col = torch.zeros(B, K, dtype=torch.int32, device=dev)
     st_val = torch.zeros(B, K, dtype=torch.float32, device=dev)
     st_col[:, 0] = seeds.to(torch.int32)
@@ -159,24 +292,10 @@ def appnp_batch(rowptr, col, inv_deg, n_nodes: int, seeds: torch.Tensor, alpha: 
                                     nx_cnt[r0:r1].data_ptr(), status.data_ptr(), ws.data_ptr(),
                                     sb.value, stream))
 
-    def step_direct(total):
-        sb = C.c_size_t()
-        _lib.check(lib.ngt_ppr_step_direct_workspace_bytes(total, B, K, C.byref(sb)))
-        ws = torch.empty(sb.value, dtype=torch.uint8, device=dev)
-        _lib.check(lib.ngt_ppr_step_direct(rowptr.data_ptr(), col.data_ptr(), inv_deg.data_ptr(),
-                                           n_nodes, st_col.data_ptr(), st_val.data_ptr(),
-                                           st_cnt.data_ptr(), seeds.data_ptr(), B, K,
-                                           float(alpha), keep, int(max_mult), total,
-                                           nx_col.data_ptr(), nx_val.data_ptr(),
-                                           nx_cnt.data_ptr(), status.data_ptr(), ws.data_ptr(),
-                                           sb.value, stream))
-
     for _ in range(num_iterations):
         count(0, B, row_off)
         total = int(row_off[B])
-        if method == "direct":
-            step_direct(total)
-        elif total <= max_products:
+        if total <= max_products:
             step(0, B, row_off, total)
         else:
             offs = row_off.cpu()
@@ -191,13 +310,7 @@ def appnp_batch(rowptr, col, inv_deg, n_nodes: int, seeds: torch.Tensor, alpha: 
         st_col, nx_col = nx_col, st_col
         st_val, nx_val = nx_val, st_val
         st_cnt, nx_cnt = nx_cnt, st_cnt
-    bad, disorder = status.tolist()
-    if bad:
-        raise IndexError(f"personalised PageRank: {bad} node ids out of range")
-    if disorder:
-        raise ValueError("personalised PageRank: CSR rows must list their columns in ascending "
-                         "order for the direct step (transition_csr sorts them), with no column "
-                         "repeated more than max_mult times")
+    _check_status(status)
     return st_col, st_val, st_cnt
 
 
@@ -205,10 +318,12 @@ def personal_pagerank_appnp(edge_index, alpha, topk=100, num_iterations: int = 1
                             batch_size: int = 8, device="cuda", csr_data=None,
                             num_nodes: int | None = None, iter_topk: int | None = None,
                             source_start: int | None = None, source_end: int | None = None,
-                            method: str = "direct"):
+                            method: str = "direct", streams: int = 8):
     """The reference's APPNP backend (appnp_backend.py:227-310) on the GPU.
     Returns (edge_index [2, nnz] int64 = (seed, node), values fp32).
-    ``method``: the step's form, "direct" or "sort" (see appnp_batch)."""
+    ``method``: the step's form, "direct" or "sort" (see appnp_batch);
+    ``streams``: batches in flight at once with the direct step (each on a
+    stream of its own; the result does not depend on it)."""
     dev = torch.device(device)
     if dev.type != "cuda":
         raise RuntimeError("the APPNP backend runs on the GPU")
@@ -230,14 +345,22 @@ def personal_pagerank_appnp(edge_index, alpha, topk=100, num_iterations: int = 1
                                   f"positive per-step top-k (1..{MAX_K})")
     K = min(iter_topk, n)
     final_keep = min(topk, K)
-    idx_out, val_out = [], []
-    mult = max_repeats(rowptr, col) if method == "direct" else None
-    for s0 in range(start, end, batch_size):
-        seeds = torch.arange(s0, min(s0 + batch_size, end), dtype=torch.long, device=dev)
-        cols, vals, cnt = appnp_batch(rowptr, col, inv_deg, n, seeds, alpha, K, num_iterations,
-                                      method=method, max_mult=mult)
-        cnt = cnt.clamp(max=final_keep).long()
-        mask = torch.arange(K, device=dev)[None, :] < cnt[:, None]
-        idx_out.append(torch.stack([seeds.repeat_interleave(cnt), cols[mask].long()]))
-        val_out.append(vals[mask])
-    return torch.cat(idx_out, dim=1), torch.cat(val_out)
+    if not 1 <= K <= MAX_K:
+        raise ValueError(f"per-step top-k must be in 1..{MAX_K}, got {K}")
+    if method not in ("direct", "sort"):
+        raise ValueError(f"method must be 'direct' or 'sort', got {method!r}")
+    batches = [torch.arange(s0, min(s0 + batch_size, end), dtype=torch.long, device=dev)
+               for s0 in range(start, end, batch_size)]
+    if method == "direct":
+        outs = _run_direct(rowptr, col, inv_deg, n, batches, alpha, K, num_iterations,
+                           max_repeats(rowptr, col), streams)
+    else:
+        outs = [appnp_batch(rowptr, col, inv_deg, n, seeds, alpha, K, num_iterations,
+                            method=method) for seeds in batches]
+    # every row's first min(cnt, topk) entries, seeds in order
+    cols = torch.cat([o[0] for o in outs])
+    vals = torch.cat([o[1] for o in outs])
+    cnt = torch.cat([o[2] for o in outs]).clamp(max=final_keep).long()
+    mask = torch.arange(K, device=dev)[None, :] < cnt[:, None]
+    seeds = torch.arange(start, end, dtype=torch.long, device=dev)
+    return torch.stack([seeds.repeat_interleave(cnt), cols[mask].long()]), vals[mask]

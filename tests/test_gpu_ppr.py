@@ -220,6 +220,32 @@ def test_appnp_rejects_unbounded_state_and_bad_ids():
                                     method=method)
 
 
+def test_appnp_batches_in_flight_give_the_same_bits():
+    """Batches run with 1, 2, 3 or 8 in flight (a stream each) give the same
+    bits as the oracle, with more batches than streams and a short last
+    batch; an id out of range in a later batch still raises."""
+    from neutrongt_amd.ppr import personal_pagerank_appnp
+
+    n = 700
+    ei = _graph(n, 3000, 13, hub=True)
+    want_i, want_v = OP.personal_pagerank_appnp(ei, 0.85, topk=5, num_iterations=6, num_nodes=n,
+                                                iter_topk=5)
+    for streams in (1, 2, 3, 8):
+        got_i, got_v = personal_pagerank_appnp(torch.from_numpy(ei), 0.85, topk=5,
+                                               num_iterations=6, batch_size=45, device=DEV,
+                                               num_nodes=n, iter_topk=5, streams=streams)
+        np.testing.assert_array_equal(got_i.cpu().numpy(), want_i)
+        np.testing.assert_array_equal(got_v.cpu().numpy(), want_v)
+    rowptr = torch.arange(0, 41, device=DEV)
+    col = (torch.arange(40, device=DEV) + 1) % 40
+    col[37] = 99  # only the last batch's seeds reach it
+    for streams in (1, 3):
+        with pytest.raises(IndexError):
+            personal_pagerank_appnp(None, 0.85, topk=2, batch_size=8, device=DEV,
+                                    csr_data={"rowptr": rowptr, "col": col}, iter_topk=2,
+                                    num_iterations=2, streams=streams)
+
+
 def test_appnp_row_chunks_match_one_pass():
     """A step split into row chunks (product budget far below the batch's)
     gives the same rows as the oracle."""
