@@ -217,19 +217,23 @@ def _run_direct(rowptr, col, inv_deg, n_nodes: int, seed_batches, alpha: float, 
         return (_direct_batch(lib, rowptr, col, inv_deg, n_nodes, seeds, alpha, K,
                               num_iterations, max_mult, pool[slot], hosts[slot]), i, slot)
 
-    active = collections.deque(e for e in map(start, range(n_str)) if e is not None)
-    while active:
-        entry = active.popleft()
-        try:
-            next(entry[0])
-            active.append(entry)
-        except StopIteration as stop:
-            results[entry[1]] = stop.value
-            nxt = start(entry[2])
-            if nxt is not None:
-                active.append(nxt)
-    for s in pool:
-        cur.wait_stream(s)
+    try:
+        active = collections.deque(e for e in map(start, range(n_str)) if e is not None)
+        while active:
+            entry = active.popleft()
+            try:
+                next(entry[0])
+                active.append(entry)
+            except StopIteration as stop:
+                results[entry[1]] = stop.value
+                nxt = start(entry[2])
+                if nxt is not None:
+                    active.append(nxt)
+    finally:
+        # also on an error: later work on the current stream (which may reuse
+        # the seeds' memory) waits for what the batches already enqueued
+        for s in pool:
+            cur.wait_stream(s)
     for r in results:
         for t in r:
             t.record_stream(cur)
