@@ -236,6 +236,17 @@ def test_appnp_batches_in_flight_give_the_same_bits():
                                                num_nodes=n, iter_topk=5, streams=streams)
         np.testing.assert_array_equal(got_i.cpu().numpy(), want_i)
         np.testing.assert_array_equal(got_v.cpu().numpy(), want_v)
+    # called on a stream of the caller's: the graph is made on it, and the
+    # result is read there without a device-wide sync
+    user = torch.cuda.Stream(DEV)
+    with torch.cuda.stream(user):
+        ei_dev = torch.from_numpy(ei).to(DEV, non_blocking=False)
+        got_i, got_v = personal_pagerank_appnp(ei_dev, 0.85, topk=5, num_iterations=6,
+                                               batch_size=45, device=DEV, num_nodes=n,
+                                               iter_topk=5, streams=4)
+        host_i, host_v = got_i.cpu(), got_v.cpu()
+    np.testing.assert_array_equal(host_i.numpy(), want_i)
+    np.testing.assert_array_equal(host_v.numpy(), want_v)
     rowptr = torch.arange(0, 41, device=DEV)
     col = (torch.arange(40, device=DEV) + 1) % 40
     col[37] = 99  # only the last batch's seeds reach it
