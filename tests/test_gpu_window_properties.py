@@ -1,7 +1,7 @@
 """Property tests of the window preparation on the GPU (hypothesis,
 derandomized): random power-law global graphs of varying size and density
-with duplicate edges and (optionally) many tied PPR values; a random
-partition; the related-node expansion, the induced subgraph in global edge
+with duplicate edges and (optionally) many tied PPR values; the METIS
+weights built from them; a random partition; the related-node expansion, the induced subgraph in global edge
 order and the CSR-walk subgraph in set order -- each bit for bit against the
 oracle."""
 import numpy as np
@@ -39,6 +39,10 @@ def test_window_preparation_matches_the_oracle(n, mean_degree, gamma, seed, part
     E = ei.shape[1]
     val = (rng.integers(1, 5, E) / 1000 if ties else rng.random(E) / 100).astype(np.float32)
     xadj, adjncy, ew = OG.adj_weights(ei, val)
+    # the METIS weights themselves (keys summed in entry order, truncated)
+    gx, ga, gw = W.adj_weights(_d(ei), _d(val, torch.float32))
+    for g, w in ((gx, xadj), (ga, adjncy), (gw, ew)):
+        np.testing.assert_array_equal(g.cpu().numpy(), w)
     n_nodes = int(xadj.shape[0]) - 1
     part = rng.permutation(n_nodes)[: int(part_frac * n_nodes)].astype(np.int64)
     print(f"case window n={n} E={E} nodes={n_nodes} part={part.shape[0]} pct={pct} ties={ties} "
