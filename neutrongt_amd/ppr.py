@@ -33,12 +33,12 @@ Differences from the reference, by design:
 """
 from __future__ import annotations
 
-import collections
 import ctypes as C
+import functools
 
 import torch
 
-from . import _lib
+from . import _lib, _streams
 
 MAX_K = 64
 
@@ -121,13 +121,12 @@ def _check_status(status: torch.Tensor) -> None:
 
 
 def _direct_batch(lib, rowptr, col, inv_deg, n_nodes: int, seeds: torch.Tensor, alpha: float,
-                  K: int, num_iterations: int, max_mult: int, stream, host_total: torch.Tensor):
+                  K: int, num_iterations: int, max_mult: int, stream, host: torch.Tensor):
     """One batch through ngt_ppr_count + ngt_ppr_step_direct, all on
-    ``stream``, as a generator: after each step's count it enqueues an
-    asynchronous copy of the product total into ``host_total`` (pinned host
-    memory) and yields, so that the caller can enqueue other batches' work on
-    other streams while the copy lands; resumed, it waits for the copy and
-    enqueues the step.  Returns (cols, vals, cnt, status) on ``stream``."""
+    ``stream``, as a job of _streams.run_in_flight: after each step's count it
+    copies the product total into ``host[0]`` (pinned) asynchronously and
+    yields; resumed, it waits for the copy and enqueues the step.  Returns
+    (cols, vals, cnt, status)."""
     dev = seeds.device
     B = int(seeds.numel())
     sp = stream.cuda_stream
@@ -152,11 +151,11 @@ def _direct_batch(lib, rowptr, col, inv_deg, n_nodes: int, seeds: torch.Tensor, 
                                      st_cnt.data_ptr(), B, K, row_off.data_ptr(),
                                      status.data_ptr(), cws.data_ptr(), cb.value, sp))
         with torch.cuda.stream(stream):
-            host_total.copy_(row_off[B:], non_blocking=True)
+            host[:1].copy_(row_off[B:], non_blocking=True)
         landed.record(stream)
         yield
         landed.synchronize()
-        total = int(host_total[0])
+        total = int(host[0])
         sb = C.c_size_t()
         _lib.check(lib.ngt_ppr_step_direct_workspace_bytes(total, B, K, C.byref(sb)))
         with torch.cuda.stream(stream):
@@ -174,19 +173,6 @@ def _direct_batch(lib, rowptr, col, inv_deg, n_nodes: int, seeds: torch.Tensor, 
     return st_col, st_val, st_cnt, status
 
 
-_STREAMS: dict = {}
-
-
-def _side_streams(dev: torch.device, n: int) -> list:
-    """n streams of default priority on ``dev``, created once per process and
-    reused by every call."""
-    idx = dev.index if dev.index is not None else torch.cuda.current_device()
-    have = _STREAMS.setdefault(idx, [])
-    while len(have) < n:
-        have.append(torch.cuda.Stream(torch.device("cuda", idx)))
-    return have[:n]
-
-
 def _run_direct(rowptr, col, inv_deg, n_nodes: int, seed_batches, alpha: float, K: int,
                 num_iterations: int, max_mult: int, streams: int):
     """Propagates the seed batches through the direct step with up to
@@ -200,43 +186,9 @@ def _run_direct(rowptr, col, inv_deg, n_nodes: int, seed_batches, alpha: float, 
     lib = _lib.load()
     if not seed_batches:
         return []
-    dev = seed_batches[0].device
-    cur = torch.cuda.current_stream(dev)
-    n_str = max(1, min(int(streams), len(seed_batches)))
-    pool = [cur] if n_str == 1 else _side_streams(dev, n_str)
-    hosts = [torch.empty(1, dtype=torch.int64, pin_memory=True) for _ in pool]
-    results = [None] * len(seed_batches)
-    queue = iter(enumerate(seed_batches))
-
-    def start(slot):
-        nxt = next(queue, None)
-        if nxt is None:
-            return None
-        i, seeds = nxt
-        pool[slot].wait_stream(cur)  # the graph and the seeds come from the current stream
-        return (_direct_batch(lib, rowptr, col, inv_deg, n_nodes, seeds, alpha, K,
-                              num_iterations, max_mult, pool[slot], hosts[slot]), i, slot)
-
-    try:
-        active = collections.deque(e for e in map(start, range(n_str)) if e is not None)
-        while active:
-            entry = active.popleft()
-            try:
-                next(entry[0])
-                active.append(entry)
-            except StopIteration as stop:
-                results[entry[1]] = stop.value
-                nxt = start(entry[2])
-                if nxt is not None:
-                    active.append(nxt)
-    finally:
-        # also on an error: later work on the current stream (which may reuse
-        # the seeds' memory) waits for what the batches already enqueued
-        for s in pool:
-            cur.wait_stream(s)
-    for r in results:
-        for t in r:
-            t.record_stream(cur)
+    jobs = [functools.partial(_direct_batch, lib, rowptr, col, inv_deg, n_nodes, seeds, alpha, K,
+                              num_iterations, max_mult) for seeds in seed_batches]
+    results = _streams.run_in_flight(jobs, seed_batches[0].device, streams)
     _check_status(torch.stack([r[3] for r in results]).sum(0))
     return [r[:3] for r in results]
 

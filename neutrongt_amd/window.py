@@ -26,10 +26,11 @@ counts.
 from __future__ import annotations
 
 import ctypes as C
+import functools
 
 import torch
 
-from . import _lib
+from . import _lib, _streams
 
 
 def merge_related_nodes(xadj: torch.Tensor, adjncy: torch.Tensor, eweights: torch.Tensor,
@@ -183,31 +184,36 @@ _SUBGRAPH_ERRORS = {1: "node id out of range in the node set", 2: "duplicate nod
                     4: "edge endpoint out of range", 8: "CSR row outside col"}
 
 
-def _run_subgraph(call, n_nodes: int, n_edges: int, n_set: int, device):
-    """Count pass, one read-back, then the emit pass into an exact [2, n] tensor."""
+def _subgraph_job(call, n_nodes: int, n_edges: int, n_set: int, device, stream, host):
+    """Count pass, the count copied into ``host`` (pinned) asynchronously, a
+    yield, then the emit pass into an exact [2, n] tensor: a job of
+    _streams.run_in_flight."""
     lib = _lib.load()
     nb = C.c_size_t()
     _lib.check(lib.ngt_subgraph_workspace_bytes(n_nodes, n_edges, n_set, C.byref(nb)))
-    ws = torch.empty(max(nb.value, 1), dtype=torch.uint8, device=device)
-    result = torch.zeros(2, dtype=torch.int64, device=device)
-    stream = _lib.stream_ptr(device)
-    _lib.check(call(None, 0, result.data_ptr(), ws.data_ptr(), nb.value, stream))
-    n, err = (int(v) for v in result.tolist())
+    with torch.cuda.stream(stream):
+        ws = torch.empty(max(nb.value, 1), dtype=torch.uint8, device=device)
+        result = torch.zeros(2, dtype=torch.int64, device=device)
+    sp = stream.cuda_stream
+    _lib.check(call(None, 0, result.data_ptr(), ws.data_ptr(), nb.value, sp))
+    with torch.cuda.stream(stream):
+        host[:2].copy_(result, non_blocking=True)
+    landed = torch.cuda.Event()
+    landed.record(stream)
+    yield
+    landed.synchronize()
+    n, err = int(host[0]), int(host[1])
     if err:
         why = ", ".join(m for b, m in _SUBGRAPH_ERRORS.items() if err & b)
         raise IndexError(f"subgraph: {why}")
-    out = torch.empty(2, n, dtype=torch.int64, device=device)
+    with torch.cuda.stream(stream):
+        out = torch.empty(2, n, dtype=torch.int64, device=device)
     if n:
-        _lib.check(call(out.data_ptr(), n, result.data_ptr(), ws.data_ptr(), nb.value, stream))
+        _lib.check(call(out.data_ptr(), n, result.data_ptr(), ws.data_ptr(), nb.value, sp))
     return out
 
 
-def subgraph(subset: torch.Tensor, edge_index: torch.Tensor, num_nodes: int) -> torch.Tensor:
-    """torch_geometric.utils.subgraph(subset, edge_index, relabel_nodes=True,
-    num_nodes)[0] on the GPU (window_state.py:82,127; metisPartition.py:280,290):
-    the edges with both endpoints in ``subset``, in their original order, each
-    node renamed to its position in ``subset``.  int64 [2, E_sub].  Raises
-    IndexError on ids outside [0, num_nodes) or a repeated subset node."""
+def _coo_call(subset: torch.Tensor, edge_index: torch.Tensor, num_nodes: int):
     lib = _lib.load()
     if not (subset.is_cuda and edge_index.is_cuda):
         raise ValueError("subgraph: tensors must be on the GPU")
@@ -216,16 +222,12 @@ def subgraph(subset: torch.Tensor, edge_index: torch.Tensor, num_nodes: int) -> 
     subset = subset.to(torch.int64).contiguous()
     ei = edge_index.to(torch.int64).contiguous()
     E, n_set = int(ei.shape[1]), int(subset.numel())
-    return _run_subgraph(
-        lambda out, cap, res, ws, wb, st: lib.ngt_subgraph_coo(
-            ei.data_ptr(), E, int(num_nodes), subset.data_ptr(), n_set, out, cap, res, ws, wb, st),
-        int(num_nodes), E, n_set, subset.device)
+    call = lambda out, cap, res, ws, wb, st: lib.ngt_subgraph_coo(  # noqa: E731
+        ei.data_ptr(), E, int(num_nodes), subset.data_ptr(), n_set, out, cap, res, ws, wb, st)
+    return functools.partial(_subgraph_job, call, int(num_nodes), E, n_set, subset.device)
 
 
-def subgraph_from_csr(node_set: torch.Tensor, rowptr: torch.Tensor, col: torch.Tensor) -> torch.Tensor:
-    """_subgraph_from_csr (window_state.py:92-119) on the GPU: for each node of
-    ``node_set`` in order, its CSR neighbours (CSR order) inside the set, as
-    (position of the row node, position of the neighbour).  int64 [2, E_sub]."""
+def _csr_call(node_set: torch.Tensor, rowptr: torch.Tensor, col: torch.Tensor):
     lib = _lib.load()
     if not (node_set.is_cuda and rowptr.is_cuda and col.is_cuda):
         raise ValueError("subgraph_from_csr: tensors must be on the GPU")
@@ -235,11 +237,40 @@ def subgraph_from_csr(node_set: torch.Tensor, rowptr: torch.Tensor, col: torch.T
     n_nodes, n_set = int(rowptr.numel()) - 1, int(node_set.numel())
     if n_nodes < 0:
         raise ValueError("subgraph_from_csr: rowptr must have n_nodes + 1 entries")
-    return _run_subgraph(
-        lambda out, cap, res, ws, wb, st: lib.ngt_subgraph_csr(
-            rowptr.data_ptr(), col.data_ptr(), int(col.numel()), n_nodes, node_set.data_ptr(), n_set,
-            out, cap, res, ws, wb, st),
-        n_nodes, int(col.numel()), n_set, node_set.device)
+    call = lambda out, cap, res, ws, wb, st: lib.ngt_subgraph_csr(  # noqa: E731
+        rowptr.data_ptr(), col.data_ptr(), int(col.numel()), n_nodes, node_set.data_ptr(), n_set,
+        out, cap, res, ws, wb, st)
+    return functools.partial(_subgraph_job, call, n_nodes, int(col.numel()), n_set,
+                             node_set.device)
+
+
+def subgraph(subset: torch.Tensor, edge_index: torch.Tensor, num_nodes: int) -> torch.Tensor:
+    """torch_geometric.utils.subgraph(subset, edge_index, relabel_nodes=True,
+    num_nodes)[0] on the GPU (window_state.py:82,127; metisPartition.py:280,290):
+    the edges with both endpoints in ``subset``, in their original order, each
+    node renamed to its position in ``subset``.  int64 [2, E_sub].  Raises
+    IndexError on ids outside [0, num_nodes) or a repeated subset node."""
+    job = _coo_call(subset, edge_index, num_nodes)
+    return _streams.run_in_flight([job], subset.device, 1)[0]
+
+
+def subgraph_from_csr(node_set: torch.Tensor, rowptr: torch.Tensor, col: torch.Tensor) -> torch.Tensor:
+    """_subgraph_from_csr (window_state.py:92-119) on the GPU: for each node of
+    ``node_set`` in order, its CSR neighbours (CSR order) inside the set, as
+    (position of the row node, position of the neighbour).  int64 [2, E_sub]."""
+    job = _csr_call(node_set, rowptr, col)
+    return _streams.run_in_flight([job], node_set.device, 1)[0]
+
+
+def subgraphs_from_csr(node_sets, rowptr: torch.Tensor, col: torch.Tensor,
+                       streams: int = 4) -> list:
+    """subgraph_from_csr for each of ``node_sets``, up to ``streams`` windows
+    in flight (each on a stream of its own; same results).  Each window's
+    walk touches only its own rows, so on a large graph the windows' count
+    read-backs and small passes overlap (the COO form streams the whole edge
+    list per window and fills the GPU alone, so it has no such variant)."""
+    jobs = [_csr_call(s, rowptr, col) for s in node_sets]
+    return _streams.run_in_flight(jobs, rowptr.device, streams) if jobs else []
 
 
 def assemble_window_features(feature: torch.Tensor, cache: torch.Tensor, dup_index: torch.Tensor,
@@ -331,7 +362,8 @@ class LocalWindows:
 
 def rebuild_local_windows(local_partitions, feature: torch.Tensor, use_cache: bool = True,
                           edge_index: torch.Tensor | None = None, num_nodes: int | None = None,
-                          rowptr: torch.Tensor | None = None, col: torch.Tensor | None = None):
+                          rowptr: torch.Tensor | None = None, col: torch.Tensor | None = None,
+                          streams: int = 4):
     """_rebuild_local_window_structures (window_state.py:223-260) for one rank,
     every step on the GPU: with ``use_cache`` the duplicate layout and its
     feature cache (:52-73, :181-205; window_dup_layout), then each window's
@@ -339,7 +371,8 @@ def rebuild_local_windows(local_partitions, feature: torch.Tensor, use_cache: bo
     :122-133) or, without it, from the global CSR ``rowptr``/``col``
     (_subgraph_from_csr, :92-119, 134-140).  ``feature`` [num_nodes, F] on
     the GPU.  The struct_enc spatial positions (:247-256) are not built.
-    Returns a LocalWindows."""
+    ``streams``: windows whose CSR-walk subgraphs are built at once, each on
+    a stream of its own (same result).  Returns a LocalWindows."""
     import time
 
     dev = feature.device
@@ -366,7 +399,7 @@ def rebuild_local_windows(local_partitions, feature: torch.Tensor, use_cache: bo
         n = int(num_nodes) if num_nodes is not None else int(feature.shape[0])
         subs = [subgraph(p, edge_index, n) for p in parts]
     else:
-        subs = [subgraph_from_csr(p, rowptr, col) for p in parts]
+        subs = subgraphs_from_csr(parts, rowptr, col, streams=streams)
     torch.cuda.synchronize(dev)
     timings["local_subgraph_rebuild_time"] = time.perf_counter() - t
     return LocalWindows(parts, dups, idx, cache, subs, timings)

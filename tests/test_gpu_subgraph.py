@@ -95,6 +95,27 @@ def test_subgraph_rejects_bad_input():
         subgraph_from_csr(*_gpu(np.array([1, 0]), np.array([0, 2, 1, 3]), col))
 
 
+def test_subgraphs_from_csr_in_flight_match_one_at_a_time():
+    """Several windows' CSR-walk subgraphs with 1, 2 or 4 in flight (a stream
+    each): the oracle's edges for every window, an empty window among them; a
+    repeated node in a later window still raises."""
+    from neutrongt_amd.window import subgraphs_from_csr
+
+    n = 800
+    ei = _graph(n, 12000, 7, hub=2000)
+    rowptr, col = _csr_of(ei, n)
+    rng = np.random.default_rng(77)
+    sets = [rng.permutation(n)[:k] for k in (150, 0, 400, 37, 800, 260)]
+    want = [OG.subgraph_from_csr(s, rowptr, col) for s in sets]
+    rp_d, col_d = _gpu(rowptr, col)
+    sets_d = _gpu(*sets)
+    for streams in (1, 2, 4):
+        for got, w in zip(subgraphs_from_csr(sets_d, rp_d, col_d, streams=streams), want):
+            np.testing.assert_array_equal(got.cpu().numpy(), w)
+    with pytest.raises(IndexError, match="duplicate"):
+        subgraphs_from_csr(sets_d[:3] + _gpu(np.array([5, 9, 5])), rp_d, col_d, streams=2)
+
+
 def test_subgraph_full_size_window():
     """A 32,768-node window of a 2,000,000-node, 24M-edge graph (both forms)."""
     from neutrongt_amd.window import subgraph, subgraph_from_csr
