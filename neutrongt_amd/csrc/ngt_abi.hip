@@ -52,22 +52,29 @@ bool timing_enabled() { return g_timing.load(std::memory_order_relaxed); }
 
 void timing_record(const char* name, hipStream_t st, bool start) {
   std::lock_guard<std::mutex> lk(g_mu);
+  // A record that fails leaves no half pair behind: the kernel goes untimed.
   if (start) {
     hipEvent_t e = take_event();
     if (!e) return;
-    hipEventRecord(e, st);
+    if (hipEventRecord(e, st) != hipSuccess) {
+      g_pool.push_back(e);
+      return;
+    }
     g_open.push_back(Pending{name, e, nullptr});
     return;
   }
   for (size_t i = g_open.size(); i-- > 0;) {
     if (g_open[i].name == name) {
-      hipEvent_t e = take_event();
-      if (!e) return;
-      hipEventRecord(e, st);
       Pending p = g_open[i];
-      p.stop = e;
-      g_pending.push_back(p);
       g_open.erase(g_open.begin() + static_cast<long>(i));
+      hipEvent_t e = take_event();
+      if (e && hipEventRecord(e, st) == hipSuccess) {
+        p.stop = e;
+        g_pending.push_back(p);
+        return;
+      }
+      if (e) g_pool.push_back(e);
+      g_pool.push_back(p.start);
       return;
     }
   }
