@@ -248,12 +248,12 @@ def ppr_bench(args, cfg, dev) -> dict:
     csr = {"rowptr": rowptr, "col": col}
     _log(f"[bench] ppr: graph n={n}, {int(col.numel())} directed edges; topk {topk}, "
          f"{iters} iterations, batches of {batch}")
-    # eight batches as warm-up (as many as run at once, so the streams exist),
-    # then the whole graph timed
-    method = args.ppr_method
+    # as many batches as run at once as warm-up (so the streams exist), then
+    # the whole graph timed
+    method, streams = args.ppr_method, max(1, args.ppr_streams)
     PPR.personal_pagerank_appnp(None, alpha, topk=topk, num_iterations=iters, batch_size=batch,
-                                device=dev, csr_data=csr, iter_topk=topk, source_end=8 * batch,
-                                method=method)
+                                device=dev, csr_data=csr, iter_topk=topk,
+                                source_end=streams * batch, method=method, streams=streams)
     torch.cuda.synchronize()
     # all seeds, in chunks of 32 batches with a progress line after each (the
     # rows are independent, so chunking changes nothing but the logging)
@@ -264,7 +264,8 @@ def ppr_bench(args, cfg, dev) -> dict:
         i_c, v_c = PPR.personal_pagerank_appnp(None, alpha, topk=topk, num_iterations=iters,
                                                batch_size=batch, device=dev, csr_data=csr,
                                                iter_topk=topk, source_start=s0,
-                                               source_end=min(s0 + chunk, n), method=method)
+                                               source_end=min(s0 + chunk, n), method=method,
+                                               streams=streams)
         idx_parts.append(i_c)
         val_parts.append(v_c)
         torch.cuda.synchronize()
@@ -308,7 +309,7 @@ def ppr_bench(args, cfg, dev) -> dict:
                                 + f", alpha {alpha}, top-{topk}, {iters} iterations, "
                                 f"batches of {batch} seeds"),
                    "entries": int(idx.shape[1]), "degree_cap": cap,
-                   "relabelled": bool(args.ppr_relabel), "step": method,
+                   "relabelled": bool(args.ppr_relabel), "step": method, "streams": streams,
                    "max_degree": int(deg_max)},
         "cpu_baseline": cpu,
     }
@@ -795,6 +796,9 @@ def main(argv=None) -> int:
     ap.add_argument("--ppr-method", choices=("direct", "sort"), default="direct",
                     help="with --ppr: the propagation step's form (direct evaluation, or the "
                          "sorted product list); both give the same bits")
+    ap.add_argument("--ppr-streams", type=int, default=8,
+                    help="with --ppr: seed batches in flight at once, each on a stream of its "
+                         "own (the result does not depend on it)")
     ap.add_argument("--prep", action="store_true",
                     help="time the window assembly instead (related nodes, induced subgraph, "
                          "window CSR, feature gather) on the config's global graph")
