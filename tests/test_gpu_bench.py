@@ -45,3 +45,6 @@ def test_ppr_bench(capsys):
     assert out["config"]["step"] == "direct"
     srt = _run(capsys, ["--ppr", "--config", "gt_arxiv", "--no-cpu", "--ppr-method", "sort"])
     assert srt["config"]["step"] == "sort" and srt["config"]["entries"] == out["config"]["entries"]
+    one = _run(capsys, ["--ppr", "--config", "gt_arxiv", "--no-cpu", "--ppr-streams", "1"])
+    assert out["config"]["streams"] == 8 and one["config"]["streams"] == 1
+    assert one["config"]["entries"] == out["config"]["entries"]
