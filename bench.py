@@ -250,7 +250,8 @@ def ppr_bench(args, cfg, dev) -> dict:
          f"{iters} iterations, batches of {batch}")
     # as many batches as run at once as warm-up (so the streams exist), then
     # the whole graph timed
-    method, streams = args.ppr_method, max(1, args.ppr_streams)
+    method = args.ppr_method
+    streams = max(1, args.ppr_streams) if method == "direct" else 1  # the sort form: one at a time
     PPR.personal_pagerank_appnp(None, alpha, topk=topk, num_iterations=iters, batch_size=batch,
                                 device=dev, csr_data=csr, iter_topk=topk,
                                 source_end=streams * batch, method=method, streams=streams)
