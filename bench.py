@@ -743,7 +743,8 @@ def measure_window(args, cfg, layers: int, dev, graph: bool, calib_copy: bool) -
         peak = FP32_TFLOPS if cfg.dtype == torch.float32 else MFMA_BF16_TFLOPS
         roof = {"bound": "mfma", "achieved": flops / dom_avg_s / 1e12, "peak": peak,
                 "unit": "TFLOP/s", "frac": flops / dom_avg_s / 1e12 / peak,
-                "traffic": None, "kernel": dom, "flops_per_launch": flops,
+                "traffic": measured_traffic(cfg.name, dom) if layers == cfg.layers else None,
+                "kernel": dom, "flops_per_launch": flops,
                 "avg_launch_us": dom_avg_s * 1e6}
         path = None
     else:
