@@ -410,11 +410,16 @@ def prep_bench(args, cfg, dev) -> dict:
     lw, t_rank = timed(lambda: W.rebuild_local_windows(rank_wins, features, rowptr=rowptr,
                                                        col=col), reps=3)
     n_dup = int(lw.feature_cache.shape[0])
+    # the last run's two phases (each ends in a device sync): the duplicate
+    # layout with its feature cache, and the windows' subgraphs
+    t_dup = 1e3 * lw.timings["local_dup_cache_rebuild_time"]
+    t_subs = 1e3 * lw.timings["local_subgraph_rebuild_time"]
     del lw, rank_wins, perm
     ops = {"merge_related_nodes_ms": t_rel, "subgraph_from_csr_ms": t_csr,
            "subgraph_coo_ms": t_coo, "window_csr_build_ms": t_adj, "feature_gather_ms": t_gather,
            "node_out_ms": t_out, "node_in_ms": t_in, "rank_windows": n_win,
-           "rank_rebuild_ms": t_rank, "rank_cached_nodes": n_dup}
+           "rank_rebuild_ms": t_rank, "rank_dup_cache_ms": t_dup, "rank_subgraphs_ms": t_subs,
+           "rank_cached_nodes": n_dup}
     total = t_rel + t_csr + t_adj + t_gather
     _log("[bench] prep: " + ", ".join(f"{k} {v:.3f}" if isinstance(v, float) else f"{k} {v}"
                                       for k, v in ops.items())
