@@ -414,6 +414,8 @@ def prep_bench(args, cfg, dev) -> dict:
     # layout with its feature cache, and the windows' subgraphs
     t_dup = 1e3 * lw.timings["local_dup_cache_rebuild_time"]
     t_subs = 1e3 * lw.timings["local_subgraph_rebuild_time"]
+    rank_h = [w.cpu().numpy() for w in rank_wins]
+    rank_out = ([w.cpu().numpy() for w in lw.partitions], lw.feature_cache.cpu().numpy())
     del lw, rank_wins, perm
     ops = {"merge_related_nodes_ms": t_rel, "subgraph_from_csr_ms": t_csr,
            "subgraph_coo_ms": t_coo, "window_csr_build_ms": t_adj, "feature_gather_ms": t_gather,
@@ -448,13 +450,23 @@ def prep_bench(args, cfg, dev) -> dict:
         OR.node_in_window(k_h, x_h, ppr.cpu().numpy(), ppr_val.cpu().numpy(), x_h.size,
                           coo.cpu().numpy(), n)
         t_ref = time.perf_counter() - t
+        # the rank's duplicate layout and feature cache (_compute_local_duplicate_nodes,
+        # build_dup_cache_metadata and the cache gather: the reference's host path)
+        t = time.perf_counter()
+        rer_h, dups_h = OG.duplicate_rerange(rank_h)
+        cache_h, _ = OG.dup_cache_metadata(dups_h)
+        cache_feat_h = feat_h[cache_h]
+        t_dup_cpu = time.perf_counter() - t
+        if not (all(np.array_equal(a, b) for a, b in zip(rer_h, rank_out[0]))
+                and np.array_equal(cache_feat_h, rank_out[1])):
+            raise RuntimeError("rank duplicate layout differs from the oracle")
         cpu = {"value": 1e3 * t_cpu, "unit": "ms", "cores": 1, "kind": "port",
                "sample": "the same window once: the oracle's restatement of "
                          "_merge_related_nodes (Python dict loop), _subgraph_from_csr (per-node "
                          "searchsorted loop), the CSR build (numpy lexsort) and the feature gather",
-               "refine_ms": 1e3 * t_ref}
+               "refine_ms": 1e3 * t_ref, "rank_dup_cache_ms": 1e3 * t_dup_cpu}
         _log(f"[bench] prep cpu baseline {1e3 * t_cpu:.1f} ms; node_out+node_in "
-             f"{1e3 * t_ref:.1f} ms")
+             f"{1e3 * t_ref:.1f} ms; rank duplicate layout + cache {1e3 * t_dup_cpu:.1f} ms")
     return {
         "metric": "window assembly time (related nodes, induced subgraph, window CSR, features)",
         "value": total, "unit": "ms", "n_gpus": 1, "steps": 5, "warmup": 1, "ms_per_step": total,
