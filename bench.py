@@ -395,6 +395,8 @@ def prep_bench(args, cfg, dev) -> dict:
                        torch.randint(0, n, (n_ppr,), generator=g, device=dev)])
     ppr_val = torch.rand(n_ppr, generator=g, device=dev) * 1e-3
     scores = torch.rand(n_w, generator=g, device=dev)
+    # the METIS weights built from that PPR list (build_adj_fromat)
+    (_, _, ew_g), t_adjw = timed(lambda: W.adj_weights(ppr, ppr_val))
     (kept, kept_edges, expired), t_out = timed(
         lambda: RF.node_out_window(win, sub_csr, scores, 0.3))
     _, t_in = timed(lambda: RF.node_in_window(kept, expired, ppr, ppr_val, int(expired.numel()),
@@ -419,7 +421,8 @@ def prep_bench(args, cfg, dev) -> dict:
     del lw, rank_wins, perm
     ops = {"merge_related_nodes_ms": t_rel, "subgraph_from_csr_ms": t_csr,
            "subgraph_coo_ms": t_coo, "window_csr_build_ms": t_adj, "feature_gather_ms": t_gather,
-           "node_out_ms": t_out, "node_in_ms": t_in, "rank_windows": n_win,
+           "node_out_ms": t_out, "node_in_ms": t_in, "adj_weights_ms": t_adjw,
+           "rank_windows": n_win,
            "rank_rebuild_ms": t_rank, "rank_dup_cache_ms": t_dup, "rank_subgraphs_ms": t_subs,
            "rank_cached_nodes": n_dup}
     total = t_rel + t_csr + t_adj + t_gather
@@ -460,13 +463,22 @@ def prep_bench(args, cfg, dev) -> dict:
         if not (all(np.array_equal(a, b) for a, b in zip(rer_h, rank_out[0]))
                 and np.array_equal(cache_feat_h, rank_out[1])):
             raise RuntimeError("rank duplicate layout differs from the oracle")
+        # the METIS weights of the same PPR list (numpy unique + ordered adds)
+        ppr_h, pv_h = ppr.cpu().numpy(), ppr_val.cpu().numpy()
+        t = time.perf_counter()
+        _, _, ew_h = OG.adj_weights(ppr_h, pv_h)
+        t_adjw_cpu = time.perf_counter() - t
+        if not np.array_equal(ew_h, ew_g.cpu().numpy()):
+            raise RuntimeError("METIS weights differ from the oracle")
         cpu = {"value": 1e3 * t_cpu, "unit": "ms", "cores": 1, "kind": "port",
                "sample": "the same window once: the oracle's restatement of "
                          "_merge_related_nodes (Python dict loop), _subgraph_from_csr (per-node "
                          "searchsorted loop), the CSR build (numpy lexsort) and the feature gather",
-               "refine_ms": 1e3 * t_ref, "rank_dup_cache_ms": 1e3 * t_dup_cpu}
+               "refine_ms": 1e3 * t_ref, "rank_dup_cache_ms": 1e3 * t_dup_cpu,
+               "adj_weights_ms": 1e3 * t_adjw_cpu}
         _log(f"[bench] prep cpu baseline {1e3 * t_cpu:.1f} ms; node_out+node_in "
-             f"{1e3 * t_ref:.1f} ms; rank duplicate layout + cache {1e3 * t_dup_cpu:.1f} ms")
+             f"{1e3 * t_ref:.1f} ms; rank duplicate layout + cache {1e3 * t_dup_cpu:.1f} ms; "
+             f"METIS weights {1e3 * t_adjw_cpu:.1f} ms")
     return {
         "metric": "window assembly time (related nodes, induced subgraph, window CSR, features)",
         "value": total, "unit": "ms", "n_gpus": 1, "steps": 5, "warmup": 1, "ms_per_step": total,
