@@ -89,7 +89,10 @@ def pmc_table(fetch_dir: str, write_dir: str, tcc_dir: str | None = None) -> str
 # kernel symbol -> the timer name the library records for its launches
 TIMER_NAMES = {"k_fwd": "sparse_fwd", "k_bwd_kv": "sparse_bwd_kv", "k_bwd_q": "sparse_bwd_q",
                "k_rowstat": "sparse_rowstat", "k_mf_fwd": "dense_fwd",
-               "k_mf_bwd_kv": "dense_bwd_kv", "k_mf_bwd_q": "dense_bwd_q"}
+               "k_mf_bwd_kv": "dense_bwd_kv", "k_mf_bwd_q": "dense_bwd_q",
+               "k_dense_fwd": "dense_fwd", "k_dense_bwd_kv": "dense_bwd_kv",
+               "k_dense_bwd_q": "dense_bwd_q", "k_dense_rowstat": "dense_rowstat",
+               "k_dense_combine": "dense_combine", "k_dense_scores": "dense_scores"}
 
 
 def _calibration(fe, wr):
